@@ -1,0 +1,268 @@
+#!/usr/bin/env python3
+"""Benchmark of the FlyHigh conv hot path on one MI355X.
+
+Workload (one step): every conv layer of one FlyHighFG pair() and one mid() at 1080p (network 856x480, padded to
+864x480), batch 1, NHWC f16, random He-normal weights and seeded uniform inputs resident in HBM. The pair stage
+(17 convs) and the mid stage (8 convs) are each captured once as a HIP graph; a step replays both. The value is
+conv-only 1080p frames/s = 1000 / ms per step (the non-conv ops of pair()/mid() are not part of this path).
+
+Alongside: per-layer time and roofline fraction (each layer's R launches captured in a graph, median of G replays
+over R; "cold" rotates buffer sets larger than the 256 MB MALL, "warm" reuses one), the layers of the single-layer
+configurations (3x3 32->32 at 1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1), and the CPU
+baseline: the oracle (a C restatement of the reference's conv arithmetic) over the same conv layers on the host's
+cores.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flyhigh-engine_amd"))
+
+METRIC = "1080p frames/s (pair+mid); per-conv-layer % of MFMA or HBM roofline"
+HBM_PEAK = 8.0e12       # B/s
+MFMA_F16_PEAK = 2.5e15  # FLOP/s, dense
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def roof(flops, nbytes):
+    t_hbm, t_mfma = nbytes / HBM_PEAK, flops / MFMA_F16_PEAK
+    return ("hbm", t_hbm) if t_hbm >= t_mfma else ("mfma", t_mfma)
+
+
+class Net:
+    """Plans and resident buffers of a list of conv layers, chained as the graph chains them."""
+
+    def __init__(self, layers, seed, torch, np, fhconv):
+        self.layers = layers
+        self.plans, self.bufs = {}, {}
+        dev = torch.device("cuda", 0)
+        rng = np.random.default_rng(seed)
+        f16 = lambda a: torch.from_numpy(np.asarray(a, np.float32).astype(np.float16))  # noqa: E731
+        for L in layers:
+            wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
+            b = f16(rng.normal(0, 0.01, L.cout))
+            s = f16(rng.uniform(0.05, 0.3, L.cout)) if L.act == 1 else None
+            d = fhconv.make_desc(1, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
+                                 residual=L.residual)
+            p = fhconv.ConvPlan(d, wt, b, s)
+            x = self.bufs[L.chain][1] if L.chain else \
+                f16(rng.uniform(-1, 1, (1, L.h, L.w, L.cin))).to(dev)
+            y = torch.zeros((1, L.hout, L.wout, L.cout), dtype=torch.float16, device=dev)
+            if L.residual:
+                r = self.bufs[L.res_from][1] if L.res_from else \
+                    f16(rng.uniform(-1, 1, (1, L.hout, L.wout, L.cout))).to(dev)
+            else:
+                r = None
+            ws = torch.empty(p.workspace_bytes // 4 + 4, dtype=torch.float32, device=dev) \
+                if p.workspace_bytes else None
+            self.plans[L.name] = p
+            self.bufs[L.name] = (x, y, r, ws)
+
+    def run(self, names=None):
+        for L in self.layers:
+            if names is None or L.name in names:
+                x, y, r, ws = self.bufs[L.name]
+                self.plans[L.name].run(x, y, r, ws)
+
+
+def time_graph(torch, fn, reps, graphs, stream):
+    """Median over `graphs` replays of a graph holding `reps` calls of fn, per call, in microseconds."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()  # warm the path outside the capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(reps):
+                fn(i)
+    ts = []
+    for _ in range(graphs):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3 / reps)
+    return statistics.median(ts)
+
+
+def layer_timing(torch, np, fhconv, net, L, reps, graphs, cold_bytes, stream):
+    """Warm and cold per-launch time of one layer (graph of `reps` launches)."""
+    p = net.plans[L.name]
+    x, y, r, ws = net.bufs[L.name]
+    warm = time_graph(torch, lambda i=0: p.run(x, y, r, ws), reps, graphs, stream)
+    # cold: rotate through enough distinct x / y / res sets to exceed the MALL
+    per = x.numel() * 2 + y.numel() * 2 + (r.numel() * 2 if r is not None else 0)
+    nsets = max(2, min(4096, -(-cold_bytes // per)))
+    creps = -(-max(reps, nsets) // nsets) * nsets
+    sets = [(torch.empty_like(x).uniform_(-1, 1), torch.empty_like(y),
+             torch.empty_like(r).uniform_(-1, 1) if r is not None else None) for _ in range(nsets)]
+    cold = time_graph(torch, lambda i=0: p.run(sets[i % nsets][0], sets[i % nsets][1], sets[i % nsets][2], ws),
+                      creps, graphs, stream)
+    del sets
+    bound, t_roof = roof(L.flops, L.bytes)
+    d = p.describe()
+    return dict(name=L.name, variant=d["name"], cin=L.cin, cout=L.cout, h=L.h, w=L.w, stride=L.stride, k=L.k,
+                us_warm=round(warm, 3), us_cold=round(cold, 3), flops=L.flops, bytes=L.bytes, bound=bound,
+                roof_us=round(t_roof * 1e6, 3), frac_cold=round(t_roof * 1e6 / cold, 4),
+                frac_warm=round(t_roof * 1e6 / warm, 4),
+                tflops_cold=round(L.flops / cold / 1e6, 2), gbs_cold=round(L.bytes / cold / 1e3, 1),
+                cold_sets=nsets)
+
+
+def cpu_baseline(np, layers, threads):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    rng = np.random.default_rng(5)
+    f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).view(np.uint16)  # noqa: E731
+    total = 0.0
+    for L in layers:
+        x = f16(rng.uniform(-1, 1, (1, L.h, L.w, L.cin)))
+        wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
+        b = f16(rng.normal(0, 0.01, L.cout))
+        s = f16(rng.uniform(0.05, 0.3, L.cout))
+        r = f16(rng.uniform(-1, 1, (1, L.hout, L.wout, L.cout)))
+        d = oracle.make_desc(1, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
+                             residual=L.residual)
+        t0 = time.perf_counter()
+        oracle.conv(d, x, wt, b, s, r, threads=threads)
+        total += time.perf_counter() - t0
+    return total
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--reps", type=int, default=100, help="launches per timing graph (per-layer timing)")
+    ap.add_argument("--graphs", type=int, default=20, help="graph replays per per-layer timing (median)")
+    ap.add_argument("--cold-mb", type=int, default=600, help="buffer bytes rotated by the cold timing")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-configs", action="store_true", help="skip the single-layer configurations")
+    ap.add_argument("--no-layers", action="store_true", help="skip the per-layer timing of the frame workload")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the conv path shards "
+              "by frame pair, one independent pipeline per GPU, so N GPUs run N of these)", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    import fhconv
+    import flyhighfg
+
+    torch.cuda.init()
+    dev = torch.device("cuda", 0)
+    stream = torch.cuda.Stream(device=dev)
+    net_w, net_h = 864, 480  # default_internal(1920, 1080) = (856, 480), padded to a multiple of 32
+    assert flyhighfg.default_internal(1920, 1080) == (856, 480)
+    layers = flyhighfg.flyhighfg_layers(net_w, net_h, k=1)
+    pair = [L for L in layers if L.stage == "pair"]
+    mid = [L for L in layers if L.stage == "mid"]
+    log(f"bench: FlyHighFG conv layers at {net_w}x{net_h}: {len(pair)} pair + {len(mid)} mid")
+    net = Net(layers, 1, torch, np, fhconv)
+    torch.cuda.synchronize()
+
+    gp, gm = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        net.run()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(gp, stream=stream):
+            net.run({L.name for L in pair})
+        with torch.cuda.graph(gm, stream=stream):
+            net.run({L.name for L in mid})
+    for _ in range(args.warmup):
+        gp.replay()
+        gm.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(args.steps):
+        gp.replay()
+        gm.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    ev_ms = e0.elapsed_time(e1) / args.steps
+    log(f"bench: {ms_per_step * 1e3:.2f} us per pair+mid (wall), {ev_ms * 1e3:.2f} us (events)")
+
+    # pair and mid separately (events on the replay stream)
+    def stage_us(g, n=200):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(n):
+            g.replay()
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) * 1e3 / n
+
+    pair_us, mid_us = stage_us(gp), stage_us(gm)
+
+    per_layer = []
+    if not args.no_layers:
+        for L in layers:
+            per_layer.append(layer_timing(torch, np, fhconv, net, L, args.reps, args.graphs,
+                                          args.cold_mb << 20, stream))
+            log("layer", json.dumps(per_layer[-1]))
+    cfg_layers = []
+    if not args.no_configs:
+        for c in (1, 2, 3):
+            cl = flyhighfg.config_layers(c)
+            cnet = Net(cl, 100 + c, torch, np, fhconv)
+            for L in cl:
+                cfg_layers.append(dict(config=c, **layer_timing(torch, np, fhconv, cnet, L, args.reps,
+                                                                args.graphs, args.cold_mb << 20, stream)))
+                log("config layer", json.dumps(cfg_layers[-1]))
+            del cnet
+            torch.cuda.empty_cache()
+
+    # the dominant kernel of the step: the layer with the largest time (warm, as inside the frame graphs)
+    roofline = None
+    if per_layer:
+        dom = max(per_layer, key=lambda r: r["us_warm"])
+        unit = "GB/s" if dom["bound"] == "hbm" else "TFLOP/s"
+        achieved = dom["gbs_cold"] if dom["bound"] == "hbm" else dom["tflops_cold"]
+        peak = HBM_PEAK / 1e9 if dom["bound"] == "hbm" else MFMA_F16_PEAK / 1e12
+        roofline = dict(bound=dom["bound"], achieved=achieved, peak=peak, unit=unit,
+                        frac=round(achieved / peak, 4), traffic=None, kernel=dom["name"], variant=dom["variant"],
+                        us_cold=dom["us_cold"], us_warm=dom["us_warm"],
+                        per_launch_bytes=dom["bytes"], per_launch_flops=dom["flops"])
+
+    cpu = None
+    if not args.no_cpu:
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        secs = cpu_baseline(np, layers, threads)
+        cpu = dict(value=round(1.0 / secs, 4), unit="frames/s", cores=threads, kind="port",
+                   sample=f"all {len(layers)} conv layers of one pair()+mid() at {net_w}x{net_h} once through the "
+                          "C oracle (restatement of the reference WGSL conv arithmetic), not lavapipe",
+                   seconds=round(secs, 3))
+        log(f"bench: CPU baseline {secs:.3f} s per pair+mid on {threads} threads")
+
+    out = dict(
+        metric=METRIC, value=round(1000.0 / ms_per_step, 2), unit="frames/s", n_gpus=1, steps=args.steps,
+        warmup=args.warmup, ms_per_step=round(ms_per_step, 6), higher_is_better=True, scaling="weak",
+        vs_baseline=None, dtype="f16", data="synthetic",
+        config=dict(workload="FlyHighFG conv layers of one pair()+mid() at 1080p (network 856x480 padded to "
+                             "864x480), batch 1, NHWC f16, conv-only",
+                    frame="1920x1080", network=f"{net_w}x{net_h}", conv_layers=len(layers), k=1,
+                    parallelism="single GPU"),
+        pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), event_ms_per_step=round(ev_ms, 6),
+        roofline=roofline, cpu_baseline=cpu, layers=per_layer, config_layers=cfg_layers,
+    )
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,575 @@
+// The C ABI of the conv hot path (include/fhc_conv.h): plans, the MI355X planner and its choice table, weight
+// packing into MFMA fragment order, and the launch of the kernels in conv_kernels.hip.
+#include <algorithm>
+#include <cmath>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "common.h"
+#include "conv_kernels.h"
+#include "fhc_conv.h"
+
+namespace fhc {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const char* msg) { g_last_error = msg ? msg : ""; }
+void clear_error() { g_last_error.clear(); }
+
+namespace {
+
+constexpr size_t kLdsBudget = 64 * 1024;  // dynamic LDS per workgroup the planner stays within
+
+uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// ---- the choice table (TuneTable, ops/conv/tune_cache.rs:6-9) ----------------------------------------------
+using TuneKey = std::tuple<uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>;
+std::mutex g_tune_mu;
+std::map<TuneKey, uint32_t> g_tune;
+
+// ---- variant codes -------------------------------------------------------------------------------------------
+// code = tile configuration id (bits 0-4, 1..kNumCfg) | global split-K code (bits 5-6: 0 -> 1, 1 -> 2, 2 -> 4,
+// 3 -> 8 splits). Fits the reference table's u8 value (tune_cache.rs:82).
+constexpr uint32_t kSplitCodes[4] = {1, 2, 4, 8};
+uint32_t make_code(int cfg, uint32_t ksplit) {
+    uint32_t sc = 0;
+    for (uint32_t i = 0; i < 4; i++)
+        if (kSplitCodes[i] == ksplit) sc = i;
+    return (uint32_t)cfg | (sc << 5);
+}
+bool decode_code(uint32_t code, int* cfg, uint32_t* ksplit) {
+    const int c = (int)(code & 31u);
+    if (c < 1 || c > kNumCfg || code > 127u) return false;
+    *cfg = c;
+    *ksplit = kSplitCodes[(code >> 5) & 3u];
+    return true;
+}
+std::string code_name(uint32_t code) {
+    int cfg;
+    uint32_t ks;
+    if (!decode_code(code, &cfg, &ks)) return "";
+    const TileCfg& t = kTileCfgs[cfg];
+    std::ostringstream o;
+    o << "igemm.t" << t.fm * t.wm << "x16.n" << t.fn * 16 * t.wn << ".w" << t.wm << "x" << t.wn << "x" << t.wk;
+    if (ks > 1) o << "/k" << ks;
+    return o.str();
+}
+
+struct Geometry {
+    uint32_t hout, wout, taps, cin8;
+};
+
+bool valid_desc(const fhc_conv_desc& d, std::string* why) {
+    char b[256];
+    auto bad = [&](const char* m) {
+        snprintf(b, sizeof b, "%s (n=%u h=%u w=%u cin=%u cout=%u k=%ux%u stride=%u pad=%u)", m, d.n, d.h, d.w, d.cin,
+                 d.cout, d.kh, d.kw, d.stride, d.pad);
+        *why = b;
+        return false;
+    };
+    if (d.n == 0 || d.h == 0 || d.w == 0 || d.cin == 0 || d.cout == 0) return bad("empty tensor");
+    if (!((d.kh == 3 && d.kw == 3 && d.pad == 1 && (d.stride == 1 || d.stride == 2)) ||
+          (d.kh == 1 && d.kw == 1 && d.pad == 0 && d.stride == 1)))
+        return bad("unsupported conv: 3x3 pad 1 stride 1/2 or 1x1 pad 0 stride 1");
+    if (d.cin > 4096 || d.cout > 4096) return bad("channel count above 4096");
+    if (d.h > 16384 || d.w > 16384 || d.n > 4096) return bad("tensor dimension too large");
+    if (d.x_cstride < d.x_c0 + d.cin) return bad("input view: x_cstride < x_c0 + cin");
+    if (d.y_cstride < d.y_c0 + d.cout) return bad("output view: y_cstride < y_c0 + cout");
+    if (d.residual > 1) return bad("residual must be 0 or 1");
+    if (d.residual && d.r_cstride < d.r_c0 + d.cout) return bad("residual view: r_cstride < r_c0 + cout");
+    if (d.act > 2) return bad("unknown activation");
+    if (d.act == FHC_ACT_LEAKY && !std::isfinite(d.alpha)) return bad("LeakyReLU alpha is not finite");
+    const uint64_t pix_in = (uint64_t)d.n * d.h * d.w, pix_out = (uint64_t)d.n * d.h * d.w;  // hout <= h
+    if (pix_in > (1ull << 31) || pix_out * d.y_cstride > (1ull << 40)) return bad("tensor too large");
+    if (d.ksplit != 0 && d.ksplit != 1 && d.ksplit != 2 && d.ksplit != 4 && d.ksplit != 8)
+        return bad("ksplit must be 0, 1, 2, 4 or 8");
+    return true;
+}
+
+}  // namespace
+
+}  // namespace fhc
+
+using namespace fhc;
+
+struct fhc_conv_plan {
+    fhc_conv_desc d;
+    Geometry g;
+    uint32_t code;
+    int cfg;
+    uint32_t ksplit;  // effective global split count (1 = none)
+    ConvKArgs args;   // kernel arguments with the tensor pointers left null
+    dim3 grid;
+    uint32_t threads;
+    size_t lds;
+    size_t ws_bytes;
+    size_t packed_bytes;
+    int device;
+    void* dmem;  // packed weights | bias | slope
+    LaunchFn launch;
+};
+
+namespace fhc {
+namespace {
+
+// Fill the launch geometry of `p` for configuration `cfg` and global split `ks`; false if it does not fit.
+bool configure(fhc_conv_plan& p, int cfg, uint32_t ks, std::string* why) {
+    const fhc_conv_desc& d = p.d;
+    const TileCfg& t = kTileCfgs[cfg];
+    const int KS = (int)d.kh, S = (int)d.stride;
+    const int TH = t.fm * t.wm, BN = t.fn * 16 * t.wn;
+    const int IH = (TH - 1) * S + KS, IW = 15 * S + KS;
+    LaunchFn fn = conv_launcher(KS, S, cfg);
+    if (!fn) {
+        *why = "no kernel instantiated for this kernel size / stride / configuration";
+        return false;
+    }
+    // channel chunk: everything at once when it fits the LDS budget, else equal chunks of a multiple of 8;
+    // a global split needs at least `ks` chunks
+    const uint32_t cin8 = p.g.cin8;
+    const size_t per_ch = (size_t)IH * IW * 2;               // LDS bytes per staged channel
+    const size_t table_max = (size_t)KS * KS * 512 / 8 * 4;  // offset table for cc <= 512
+    long ccmax = (long)((kLdsBudget - table_max - 16) / per_ch) - 8;
+    ccmax = ccmax / 8 * 8;
+    if (ccmax > 512) ccmax = 512;
+    if (ccmax < 8) {
+        *why = "halo tile does not fit in LDS";
+        return false;
+    }
+    uint32_t nchunks = div_ceil(cin8, (uint32_t)ccmax);
+    if (ks > 1 && nchunks < ks) nchunks = std::min<uint32_t>(ks, cin8 / 8);
+    uint32_t cc = div_ceil(div_ceil(cin8, nchunks), 8) * 8;
+    nchunks = div_ceil(cin8, cc);
+    const uint32_t cps = ks > 1 ? div_ceil(nchunks, ks) : nchunks;
+    const uint32_t zcount = div_ceil(nchunks, cps);
+    const uint32_t taps = p.g.taps;
+    const uint32_t tapgroups = taps * cc / 8;
+    const uint32_t ksteps = div_ceil(tapgroups, 4);
+    size_t lds = (((size_t)tapgroups * 4 + 15) & ~(size_t)15) + (size_t)IH * IW * (cc + 8) * 2;
+    if (t.wk > 1) {
+        const size_t red = (size_t)(t.wk - 1) * t.wm * t.wn * t.fm * t.fn * 64 * 16;
+        lds = std::max(lds, red);
+    }
+    if (lds > kLdsBudget) {
+        *why = "LDS budget exceeded";
+        return false;
+    }
+    const uint32_t tiles_x = div_ceil(p.g.wout, 16), tiles_y = div_ceil(p.g.hout, TH);
+    const uint32_t ntn = div_ceil(d.cout, BN);
+    const uint64_t blocks = (uint64_t)d.n * tiles_y * tiles_x * ntn;
+    if (blocks > 0x7fffffffull) {
+        *why = "grid too large";
+        return false;
+    }
+    ConvKArgs& a = p.args;
+    a = ConvKArgs{};
+    a.n = (int)d.n;
+    a.h = (int)d.h;
+    a.w = (int)d.w;
+    a.cin = (int)d.cin;
+    a.cout = (int)d.cout;
+    a.hout = (int)p.g.hout;
+    a.wout = (int)p.g.wout;
+    a.pad = (int)d.pad;
+    a.xcs = (int)d.x_cstride;
+    a.xc0 = (int)d.x_c0;
+    a.ycs = (int)d.y_cstride;
+    a.yc0 = (int)d.y_c0;
+    a.rcs = (int)d.r_cstride;
+    a.rc0 = (int)d.r_c0;
+    a.act = (int)d.act;
+    a.alpha = d.alpha;
+    a.residual = (int)d.residual;
+    a.cc = (int)cc;
+    a.nchunks = (int)nchunks;
+    a.ksteps = (int)ksteps;
+    a.tapgroups = (int)tapgroups;
+    a.tiles_x = (int)tiles_x;
+    a.tiles_y = (int)tiles_y;
+    a.ntn = (int)ntn;
+    a.chunks_per_split = (int)cps;
+    a.np = (int)(ntn * BN);
+    p.cfg = cfg;
+    p.ksplit = zcount;
+    p.code = make_code(cfg, zcount);
+    p.grid = dim3((unsigned)blocks, zcount, 1);
+    p.threads = 64u * t.wm * t.wn * t.wk;
+    p.lds = lds;
+    p.ws_bytes = zcount > 1 ? (size_t)zcount * d.n * p.g.hout * p.g.wout * a.np * sizeof(float) : 0;
+    p.launch = fn;
+    return true;
+}
+
+// The MI355X planner's default when neither the caller nor the table chose: the widest channel tile that
+// pads cout by at most a quarter, 8-row tiles (4 for stride 2 when the halo would not fit), and the 4-wave K split
+// for deep layers whose tile grid cannot fill the 256 CUs.
+int heuristic_cfg(const fhc_conv_desc& d, const Geometry& g) {
+    struct Opt {
+        int bn, cfg8, cfg4;
+    };
+    const Opt opts[] = {{128, 6, 0}, {64, 1, 4}, {48, 9, 0}, {32, 2, 5}, {16, 3, 10}};
+    int cfg8 = 3, cfg4 = 10;
+    for (const Opt& o : opts) {
+        const uint32_t padded = div_ceil(d.cout, o.bn) * o.bn;
+        if ((padded - d.cout) * 4 <= d.cout) {
+            cfg8 = o.cfg8;
+            cfg4 = o.cfg4 ? o.cfg4 : o.cfg8;
+            break;
+        }
+    }
+    const uint32_t tiles8 = d.n * div_ceil(g.hout, 8) * div_ceil(g.wout, 16) * div_ceil(d.cout, 64);
+    if (g.taps * g.cin8 >= 1024 && tiles8 < 128 && d.cout > 32) return 7;
+    return d.stride == 2 ? cfg4 : cfg8;
+}
+
+void pack_weights(const fhc_conv_plan& p, const uint16_t* w, std::vector<uint16_t>& out) {
+    const fhc_conv_desc& d = p.d;
+    const ConvKArgs& a = p.args;
+    const int nb16 = a.np / 16, gpt = a.cc / 8;
+    out.assign((size_t)nb16 * a.nchunks * a.ksteps * 64 * 8, 0);
+    size_t o = 0;
+    for (int nb = 0; nb < nb16; nb++)
+        for (int c = 0; c < a.nchunks; c++)
+            for (int s = 0; s < a.ksteps; s++)
+                for (int l = 0; l < 64; l++)
+                    for (int i = 0; i < 8; i++, o++) {
+                        const int j = 4 * s + (l >> 4);  // 8-channel group of this K position
+                        if (j >= a.tapgroups) continue;
+                        const int tap = j / gpt, g = j % gpt;
+                        const uint32_t ci = (uint32_t)(c * a.cc + g * 8 + i), co = (uint32_t)(nb * 16 + (l & 15));
+                        if (ci >= d.cin || co >= d.cout) continue;
+                        const uint32_t ky = (uint32_t)tap / d.kw, kx = (uint32_t)tap % d.kw;
+                        out[o] = w[(((size_t)co * d.cin + ci) * d.kh + ky) * d.kw + kx];
+                    }
+}
+
+hipError_t upload(fhc_conv_plan& p, const std::vector<uint16_t>& packed, const uint16_t* bias, const uint16_t* slope) {
+    const size_t np = (size_t)p.args.np;
+    const size_t wbytes = (packed.size() * 2 + 255) & ~(size_t)255;
+    const size_t total = wbytes + 2 * np * 2 + 256;
+    std::vector<uint16_t> host(total / 2, 0);
+    memcpy(host.data(), packed.data(), packed.size() * 2);
+    uint16_t* hb = host.data() + wbytes / 2;
+    uint16_t* hs = hb + np;
+    for (uint32_t i = 0; i < p.d.cout; i++) {
+        hb[i] = bias[i];
+        hs[i] = slope ? slope[i] : (uint16_t)0x3c00;  // f16 1.0
+    }
+    hipError_t e = hipMalloc(&p.dmem, total);
+    if (e != hipSuccess) {
+        p.dmem = nullptr;
+        return e;
+    }
+    e = hipMemcpy(p.dmem, host.data(), total, hipMemcpyHostToDevice);
+    if (e != hipSuccess) return e;
+    p.args.wpk = p.dmem;
+    p.args.bias = reinterpret_cast<const uint16_t*>(static_cast<char*>(p.dmem) + wbytes);
+    p.args.slope = p.args.bias + np;
+    p.packed_bytes = packed.size() * 2;
+    return hipSuccess;
+}
+
+// The planner's choice for `d` (conv_pick, autotune.rs:186-233): a forced variant, else the table, else the
+// heuristic; the caller's forced split-K (or the reference code's split nibble) applies on top.
+bool plan_choose(const fhc_conv_desc& d, fhc_conv_plan& p, std::string* why) {
+    p.d = d;
+    p.dmem = nullptr;
+    p.g.hout = (d.h + 2 * d.pad - d.kh) / d.stride + 1;
+    p.g.wout = (d.w + 2 * d.pad - d.kw) / d.stride + 1;
+    p.g.taps = d.kh * d.kw;
+    p.g.cin8 = div_ceil(d.cin, 8) * 8;
+    // the choice: forced variant, then the table, then the heuristic (conv_pick, autotune.rs:186-233)
+    int cfg = 0;
+    uint32_t ks = 1;
+    if (d.variant != 0) {
+        if (!decode_code(d.variant, &cfg, &ks)) {
+            *why = "unknown variant " + std::to_string(d.variant);
+            return false;
+        }
+    } else {
+        const int hit = fhc_tune_get(d.cin, d.cout, d.h, d.w, d.stride);
+        if (hit < 0 || !decode_code((uint32_t)hit, &cfg, &ks)) {
+            cfg = heuristic_cfg(d, p.g);
+            ks = 1;
+        }
+    }
+    if (d.ksplit != 0)
+        ks = d.ksplit;
+    else if (d.ref_cand != 0xFFu && d.ref_cand != 0 && (d.ref_cand >> 4) != 0 && d.variant == 0) {
+        const uint32_t rk = d.ref_cand >> 4;  // candidates.rs:4: forced split-K 1 / 2 / 4
+        if (rk == 1 || rk == 2 || rk == 4) ks = rk;
+    }
+    if (!configure(p, cfg, ks, why)) {
+        // a table entry or heuristic that does not fit this shape falls back to the 4-row tile
+        if (d.variant != 0 || !configure(p, d.cout <= 32 ? 5 : 4, ks, why)) {
+            *why += " (variant " + code_name(make_code(cfg, ks)) + ")";
+            return false;
+        }
+    }
+    return true;
+}
+
+std::string describe_json(const fhc_conv_plan* p) {
+    const fhc_conv_desc& d = p->d;
+    const TileCfg& t = kTileCfgs[p->cfg];
+    const double flops = 2.0 * d.n * p->g.hout * p->g.wout * d.cout * d.cin * d.kh * d.kw;
+    const double out_el = (double)d.n * p->g.hout * p->g.wout * d.cout;
+    const double bytes = 2.0 * ((double)d.n * d.h * d.w * d.cin + out_el + (double)d.cout * d.cin * d.kh * d.kw +
+                                d.cout + (d.act == FHC_ACT_PRELU ? d.cout : 0) + (d.residual ? out_el : 0));
+    const size_t packed = (size_t)(p->args.np / 16) * p->args.nchunks * p->args.ksteps * 64 * 16;
+    char b[1024];
+    snprintf(b, sizeof b,
+             "{\"variant\":%u,\"name\":\"%s\",\"cfg\":%d,\"tile_rows\":%d,\"tile_cols\":16,\"tile_channels\":%d,"
+             "\"waves\":[%d,%d,%d],\"ksplit\":%u,\"cc\":%d,\"nchunks\":%d,\"ksteps\":%d,\"grid\":[%u,%u],"
+             "\"threads\":%u,\"lds\":%zu,\"packed_weight_bytes\":%zu,\"workspace_bytes\":%zu,\"hout\":%u,"
+             "\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
+             p->code, code_name(p->code).c_str(), p->cfg, t.fm * t.wm, t.fn * 16 * t.wn, t.wm, t.wn, t.wk, p->ksplit,
+             p->args.cc, p->args.nchunks, p->args.ksteps, p->grid.x, p->grid.y, p->threads, p->lds, packed,
+             p->ws_bytes, p->g.hout, p->g.wout, flops, bytes);
+    return b;
+}
+
+}  // namespace
+}  // namespace fhc
+
+extern "C" const char* fhc_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" int fhc_conv_plan_create(const fhc_conv_desc* desc, const uint16_t* w_oihw, const uint16_t* bias,
+                                    const uint16_t* slope, fhc_conv_plan** out) {
+    return guard(-1, [&]() -> int {
+        if (!out) return fail(-1, "fhc_conv_plan_create: NULL output handle");
+        *out = nullptr;
+        if (!desc) return fail(-1, "fhc_conv_plan_create: NULL descriptor");
+        if (!w_oihw || !bias) return fail(-1, "fhc_conv_plan_create: NULL weights or bias");
+        fhc_conv_desc d = *desc;
+        if (d.x_cstride == 0) d.x_cstride = d.cin;
+        if (d.y_cstride == 0) d.y_cstride = d.cout;
+        if (d.r_cstride == 0) d.r_cstride = d.cout;
+        std::string why;
+        if (!valid_desc(d, &why)) return fail(-1, "fhc_conv_plan_create: %s", why.c_str());
+        if (d.act == FHC_ACT_PRELU && !slope) return fail(-1, "fhc_conv_plan_create: PReLU needs a slope");
+        auto p = std::make_unique<fhc_conv_plan>();
+        if (!plan_choose(d, *p, &why)) return fail(-1, "fhc_conv_plan_create: %s", why.c_str());
+        hipError_t e = hipGetDevice(&p->device);
+        if (e != hipSuccess) return fail(-1, "fhc_conv_plan_create: hipGetDevice: %s", hipGetErrorString(e));
+        std::vector<uint16_t> packed;
+        pack_weights(*p, w_oihw, packed);
+        e = upload(*p, packed, bias, slope);
+        if (e != hipSuccess) {
+            if (p->dmem) (void)hipFree(p->dmem);
+            return fail(-1, "fhc_conv_plan_create: device upload: %s", hipGetErrorString(e));
+        }
+        *out = p.release();
+        clear_error();
+        return 0;
+    });
+}
+
+extern "C" size_t fhc_conv_workspace_bytes(const fhc_conv_plan* p) { return p ? p->ws_bytes : 0; }
+
+extern "C" int fhc_conv_out_shape(const fhc_conv_plan* p, uint32_t* hout, uint32_t* wout) {
+    if (!p) return fail(-1, "fhc_conv_out_shape: NULL plan");
+    if (hout) *hout = p->g.hout;
+    if (wout) *wout = p->g.wout;
+    return 0;
+}
+
+extern "C" int fhc_conv_run(const fhc_conv_plan* p, const void* x, void* y, const void* res, void* workspace,
+                            void* stream) {
+    return guard(-1, [&]() -> int {
+        if (!p) return fail(-1, "fhc_conv_run: NULL plan");
+        if (!x || !y) return fail(-1, "fhc_conv_run: NULL input or output");
+        if (p->d.residual && !res) return fail(-1, "fhc_conv_run: the plan has a residual but res is NULL");
+        if (p->ws_bytes && !workspace)
+            return fail(-1, "fhc_conv_run: the plan needs %zu bytes of workspace", p->ws_bytes);
+        if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)res) & 1u)
+            return fail(-1, "fhc_conv_run: f16 tensors must be 2-byte aligned");
+        if ((uintptr_t)workspace & 15u) return fail(-1, "fhc_conv_run: workspace must be 16-byte aligned");
+        int dev = -1;
+        if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
+            return fail(-1, "fhc_conv_run: the plan belongs to device %d, the current device is %d", p->device, dev);
+        ConvKArgs a = p->args;
+        a.x = static_cast<const uint16_t*>(x);
+        a.y = static_cast<uint16_t*>(y);
+        a.res = static_cast<const uint16_t*>(res);
+        a.part = static_cast<float*>(workspace);
+        a.xvec = ((uintptr_t)x % 16 == 0) && a.xcs % 8 == 0 && a.xc0 % 8 == 0;
+        a.yvec = ((uintptr_t)y % 8 == 0) && a.ycs % 4 == 0 && a.yc0 % 4 == 0;
+        a.rvec = a.residual && ((uintptr_t)res % 8 == 0) && a.rcs % 4 == 0 && a.rc0 % 4 == 0;
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        hipError_t e = p->launch(a, p->grid, p->lds, s);
+        if (e != hipSuccess) return fail(-1, "fhc_conv_run: launch: %s", hipGetErrorString(e));
+        if (p->ksplit > 1) {
+            e = splitk_reduce_launch(a, (int)p->ksplit, s);
+            if (e != hipSuccess) return fail(-1, "fhc_conv_run: split-K reduce launch: %s", hipGetErrorString(e));
+        }
+        return 0;
+    });
+}
+
+extern "C" int fhc_conv_describe(const fhc_conv_plan* p, char* json, size_t cap) {
+    return guard(-1, [&]() -> int {
+        if (!p) return fail(-1, "fhc_conv_describe: NULL plan");
+        return write_string(describe_json(p), json, cap);
+    });
+}
+
+extern "C" int fhc_conv_plan_dry(const fhc_conv_desc* desc, char* json, size_t cap) {
+    return guard(-1, [&]() -> int {
+        if (!desc) return fail(-1, "fhc_conv_plan_dry: NULL descriptor");
+        fhc_conv_desc d = *desc;
+        if (d.x_cstride == 0) d.x_cstride = d.cin;
+        if (d.y_cstride == 0) d.y_cstride = d.cout;
+        if (d.r_cstride == 0) d.r_cstride = d.cout;
+        std::string why;
+        if (!valid_desc(d, &why)) return fail(-1, "fhc_conv_plan_dry: %s", why.c_str());
+        fhc_conv_plan p{};
+        if (!plan_choose(d, p, &why)) return fail(-1, "fhc_conv_plan_dry: %s", why.c_str());
+        p.device = -1;
+        return write_string(describe_json(&p), json, cap);
+    });
+}
+
+extern "C" void fhc_conv_plan_destroy(fhc_conv_plan* p) {
+    if (!p) return;
+    if (p->dmem) (void)hipFree(p->dmem);
+    delete p;
+}
+
+// ---- choice table -------------------------------------------------------------------------------------------
+
+extern "C" int fhc_tune_parse(const char* text) {
+    return guard(-1, [&]() -> int {
+        if (!text) return fail(-1, "fhc_tune_parse: NULL text");
+        // parse_tune (tune_cache.rs:71-87): "cin,cout,h,w,stride=code" per line, malformed lines skipped
+        std::istringstream in(text);
+        std::string line;
+        int n = 0;
+        std::lock_guard<std::mutex> lk(g_tune_mu);
+        while (std::getline(in, line)) {
+            const size_t eq = line.find('=');
+            if (eq == std::string::npos) continue;
+            std::vector<uint32_t> f;
+            std::istringstream ks(line.substr(0, eq));
+            std::string part;
+            bool ok = true;
+            while (std::getline(ks, part, ',')) {
+                const size_t a = part.find_first_not_of(" \t\r"), b = part.find_last_not_of(" \t\r");
+                if (a == std::string::npos) {
+                    ok = false;
+                    break;
+                }
+                const std::string v = part.substr(a, b - a + 1);
+                if (v.find_first_not_of("0123456789") != std::string::npos || v.size() > 9) {
+                    ok = false;
+                    break;
+                }
+                f.push_back((uint32_t)std::stoul(v));
+            }
+            if (!ok || f.size() != 5) continue;
+            std::string v = line.substr(eq + 1);
+            const size_t a = v.find_first_not_of(" \t\r"), b = v.find_last_not_of(" \t\r");
+            if (a == std::string::npos) continue;
+            v = v.substr(a, b - a + 1);
+            if (v.empty() || v.size() > 3 || v.find_first_not_of("0123456789") != std::string::npos) continue;
+            const unsigned long code = std::stoul(v);
+            if (code > 255) continue;
+            g_tune[TuneKey(f[0], f[1], f[2], f[3], f[4])] = (uint32_t)code;
+            n++;
+        }
+        return n;
+    });
+}
+
+extern "C" int fhc_tune_format(char* text, size_t cap) {
+    return guard(-1, [&]() -> int {
+        // format_tune (tune_cache.rs:88-94): lines sorted as strings, joined by newlines
+        std::vector<std::string> lines;
+        {
+            std::lock_guard<std::mutex> lk(g_tune_mu);
+            for (const auto& kv : g_tune) {
+                const TuneKey& k = kv.first;
+                lines.push_back(std::to_string(std::get<0>(k)) + "," + std::to_string(std::get<1>(k)) + "," +
+                                std::to_string(std::get<2>(k)) + "," + std::to_string(std::get<3>(k)) + "," +
+                                std::to_string(std::get<4>(k)) + "=" + std::to_string(kv.second));
+            }
+        }
+        std::sort(lines.begin(), lines.end());
+        std::string s;
+        for (size_t i = 0; i < lines.size(); i++) s += (i ? "\n" : "") + lines[i];
+        return write_string(s, text, cap);
+    });
+}
+
+extern "C" int fhc_tune_clear(void) {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    g_tune.clear();
+    return 0;
+}
+
+extern "C" int fhc_tune_get(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride) {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    auto it = g_tune.find(TuneKey(cin, cout, h, w, stride));
+    return it == g_tune.end() ? -1 : (int)it->second;
+}
+
+extern "C" int fhc_variant_name(uint32_t code, char* buf, size_t cap) {
+    return guard(-1, [&]() -> int {
+        const std::string s = code_name(code);
+        if (s.empty()) return fail(-1, "fhc_variant_name: unknown variant %u", code);
+        return write_string(s, buf, cap);
+    });
+}
+
+extern "C" int fhc_variant_list(const fhc_conv_desc* desc, uint32_t* codes, size_t cap) {
+    return guard(-1, [&]() -> int {
+        if (!desc) return fail(-1, "fhc_variant_list: NULL descriptor");
+        fhc_conv_desc d = *desc;
+        if (d.x_cstride == 0) d.x_cstride = d.cin;
+        if (d.y_cstride == 0) d.y_cstride = d.cout;
+        if (d.r_cstride == 0) d.r_cstride = d.cout;
+        std::string why;
+        if (!valid_desc(d, &why)) return fail(-1, "fhc_variant_list: %s", why.c_str());
+        fhc_conv_plan p{};
+        p.d = d;
+        p.g.hout = (d.h + 2 * d.pad - d.kh) / d.stride + 1;
+        p.g.wout = (d.w + 2 * d.pad - d.kw) / d.stride + 1;
+        p.g.taps = d.kh * d.kw;
+        p.g.cin8 = div_ceil(d.cin, 8) * 8;
+        // every configuration that fits, without split; with global splits where the tile grid is small
+        // (the counterpart of cand_list's split-K variants, candidates.rs:52-57)
+        std::vector<uint32_t> out;
+        for (int cfg = 1; cfg <= kNumCfg; cfg++) {
+            const TileCfg& t = kTileCfgs[cfg];
+            const uint32_t bn = (uint32_t)(t.fn * 16 * t.wn);
+            if (bn >= 2 * div_ceil(d.cout, 16) * 16 && bn > 16) continue;  // mostly padding
+            for (uint32_t ks : {1u, 2u, 4u, 8u}) {
+                if (!configure(p, cfg, ks, &why)) continue;
+                if (p.ksplit != ks) continue;
+                if (ks > 1 && p.grid.x >= 512) continue;
+                out.push_back(p.code);
+            }
+        }
+        if (!codes && cap) return fail(-1, "fhc_variant_list: NULL output");
+        if (out.size() > cap) return fail(-1, "fhc_variant_list: %zu variants do not fit in %zu", out.size(), cap);
+        for (size_t i = 0; i < out.size(); i++) codes[i] = out[i];
+        return (int)out.size();
+    });
+}
+
+extern "C" int fhc_probe_mfma_layout(const void* a, const void* b, void* d, void* stream) {
+    return guard(-1, [&]() -> int {
+        if (!a || !b || !d) return fail(-1, "fhc_probe_mfma_layout: NULL pointer");
+        hipError_t e = mfma_probe_launch(static_cast<const uint16_t*>(a), static_cast<const uint16_t*>(b),
+                                         static_cast<float*>(d), static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return fail(-1, "fhc_probe_mfma_layout: %s", hipGetErrorString(e));
+        return 0;
+    });
+}

@@ -1,0 +1,67 @@
+// Device-side contract of the conv kernels: the argument block every launch takes, the tile configurations the
+// planner can choose from, and the launcher table. Shared by conv_kernels.hip (kernels) and api.cpp (host).
+#pragma once
+#include <cstddef>
+#include <cstdint>
+
+#include <hip/hip_runtime.h>
+
+namespace fhc {
+
+// One conv launch. Activations NHWC f16: element (img, y, x, c) of a view at ((img*H + y)*W + x)*cs + c0 + c.
+struct ConvKArgs {
+    const uint16_t* x;
+    uint16_t* y;
+    const uint16_t* res;
+    const void* wpk;        // packed weights, MFMA A-fragment order: [nb16][chunk][kstep][lane 64][8 halves]
+    const uint16_t* bias;   // f16, padded to np
+    const uint16_t* slope;  // f16, padded to np (PReLU only)
+    float* part;            // split-K partials [z][n*hout*wout][np] f32 (global split only)
+    int n, h, w, cin, cout, hout, wout, pad;
+    int xcs, xc0, ycs, yc0, rcs, rc0;
+    int act;
+    float alpha;
+    int residual;
+    int cc;         // input channels staged per chunk (multiple of 8)
+    int nchunks;    // ceil(cin8 / cc)
+    int ksteps;     // MFMA K-steps (of 32) per chunk = ceil(taps * cc / 32)
+    int tapgroups;  // 8-channel groups per chunk = taps * cc / 8
+    int tiles_x, tiles_y, ntn;  // output tiles: columns of 16, rows of TH, channel tiles of BN
+    int chunks_per_split;       // global split-K: chunks handled by one z
+    int np;                     // output channels padded to ntn * BN
+    int xvec, yvec, rvec;       // vector paths: 16-byte input loads, 8-byte output stores / residual loads
+};
+
+// A tile configuration: wave grid WM x WN x WK (WK > 1 splits K inside the workgroup), each wave FM output rows
+// of 16 pixels by FN blocks of 16 channels. TH = FM * WM output rows per tile, BN = FN * 16 * WN channels.
+struct TileCfg {
+    int fm, fn, wm, wn, wk;
+};
+
+// Configuration ids 1..kNumCfg (0 is "none"); the table is the same on host and device side.
+constexpr int kNumCfg = 10;
+inline constexpr TileCfg kTileCfgs[kNumCfg + 1] = {
+    {0, 0, 0, 0, 0},
+    {2, 4, 4, 1, 1},  // 1: TH 8, BN 64
+    {2, 2, 4, 1, 1},  // 2: TH 8, BN 32
+    {2, 1, 4, 1, 1},  // 3: TH 8, BN 16
+    {1, 4, 4, 1, 1},  // 4: TH 4, BN 64
+    {1, 2, 4, 1, 1},  // 5: TH 4, BN 32
+    {4, 4, 2, 2, 1},  // 6: TH 8, BN 128
+    {4, 4, 1, 1, 4},  // 7: TH 4, BN 64, K split over 4 waves
+    {2, 4, 2, 1, 2},  // 8: TH 4, BN 64, K split over 2 waves
+    {2, 3, 4, 1, 1},  // 9: TH 8, BN 48
+    {1, 1, 4, 1, 1},  // 10: TH 4, BN 16
+};
+
+using LaunchFn = hipError_t (*)(const ConvKArgs&, dim3 grid, size_t lds, hipStream_t);
+
+// The launcher of configuration `cfg` for a (kernel size, stride) pair, or nullptr if not instantiated.
+LaunchFn conv_launcher(int ks, int stride, int cfg);
+hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s);
+
+// Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the
+// operand layouts the conv kernels assume. Device pointers.
+hipError_t mfma_probe_launch(const uint16_t* a, const uint16_t* b, float* d, hipStream_t s);
+
+}  // namespace fhc

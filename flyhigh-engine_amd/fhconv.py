@@ -1,0 +1,302 @@
+"""Python host driver of libfhconv.so, the FlyHigh conv hot path on MI355X (ctypes over include/fhc_conv.h).
+
+It mirrors the reference's conv-op interface at plan and run time (crates/flyhigh-engine/src/ops/conv/):
+
+- ``ConvOp`` / ``conv_pick`` / ``conv`` : BuildCtx::conv_pick + the recorded Steps (autotune.rs:100-109, :159-235);
+  here a plan is created once and run on a HIP stream;
+- ``cand_list`` / ``cand_name`` / ``ref_conv_steps``: the reference planner restated (candidates.rs:17-85,
+  kernels.rs:99-279), for planner parity;
+- ``parse_tune`` / ``format_tune``: the choice table text (tune_cache.rs:71-94);
+- errors raise ``FhcError`` with the library's ``fhc_last_error`` message (the reference's C ABI returns -1 and sets
+  fh_last_error, crates/flyhigh-capi/src/lib.rs:27-48).
+
+Tensors are torch f16 (or int16/uint16 bit patterns) on the GPU in NHWC layout; the module only passes their device
+pointers and never computes a conv itself: when the library is missing, loading it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfhconv.so")
+
+ACT_NONE, ACT_PRELU, ACT_LEAKY = 0, 1, 2
+
+# reference candidate codes (ops/conv/candidates.rs:5-14)
+CAND_DIRECT, CAND_TC, CAND_TILED, CAND_TILED8, CAND_DIRECT64 = 0, 1, 2, 3, 4
+CAND_TILED16, CAND_TILEDN8, CAND_TILED88, CAND_TILEDM32, CAND_TILED8P = 5, 6, 7, 8, 9
+
+
+class FhcError(RuntimeError):
+    pass
+
+
+class ConvDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "n", "h", "w", "cin", "cout", "kh", "kw", "stride", "pad",
+        "x_cstride", "x_c0", "y_cstride", "y_c0", "r_cstride", "r_c0", "act")] + [
+        ("alpha", ctypes.c_float)] + [(n, ctypes.c_uint32) for n in ("residual", "variant", "ksplit", "ref_cand")]
+
+
+class RefConv(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "cin", "cout", "h", "w", "stride", "residual", "coop", "cand", "ksplit_env", "f32_mode")]
+
+
+_lib = None
+
+
+def load():
+    """The library handle; raises if libfhconv.so has not been built (no fallback exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FhcError(f"{LIB_PATH} is missing: build it first (__graft_entry__.build() or make -C {HERE})")
+    L = ctypes.CDLL(LIB_PATH)
+    P, U32, SZ = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_size_t
+    sig = {
+        "fhc_last_error": ([], ctypes.c_char_p),
+        "fhc_conv_plan_create": ([ctypes.POINTER(ConvDesc), P, P, P, ctypes.POINTER(P)], ctypes.c_int),
+        "fhc_conv_workspace_bytes": ([P], SZ),
+        "fhc_conv_out_shape": ([P, ctypes.POINTER(U32), ctypes.POINTER(U32)], ctypes.c_int),
+        "fhc_conv_run": ([P, P, P, P, P, P], ctypes.c_int),
+        "fhc_conv_describe": ([P, ctypes.c_char_p, SZ], ctypes.c_int),
+        "fhc_conv_plan_destroy": ([P], None),
+        "fhc_conv_plan_dry": ([ctypes.POINTER(ConvDesc), ctypes.c_char_p, SZ], ctypes.c_int),
+        "fhc_tune_parse": ([ctypes.c_char_p], ctypes.c_int),
+        "fhc_tune_format": ([ctypes.c_char_p, SZ], ctypes.c_int),
+        "fhc_tune_clear": ([], ctypes.c_int),
+        "fhc_tune_get": ([U32] * 5, ctypes.c_int),
+        "fhc_variant_name": ([U32, ctypes.c_char_p, SZ], ctypes.c_int),
+        "fhc_variant_list": ([ctypes.POINTER(ConvDesc), ctypes.POINTER(U32), SZ], ctypes.c_int),
+        "fhc_ref_cand_list": ([ctypes.c_int, U32, U32, U32, ctypes.c_int, ctypes.c_int,
+                               ctypes.POINTER(ctypes.c_uint8), SZ], ctypes.c_int),
+        "fhc_ref_cand_name": ([ctypes.c_uint8, ctypes.c_char_p, SZ], ctypes.c_int),
+        "fhc_ref_conv_steps": ([ctypes.POINTER(RefConv), ctypes.c_char_p, SZ], ctypes.c_int),
+        "fhc_probe_mfma_layout": ([P, P, P, P], ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    return load().fhc_last_error().decode()
+
+
+def _check(rc, what):
+    if rc < 0:
+        raise FhcError(f"{what}: {last_error()}")
+    return rc
+
+
+def _ptr(t):
+    """Device pointer of a torch tensor (or an int), None for None."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream_handle(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def make_desc(n, h, w, cin, cout, k=3, stride=1, pad=None, act=ACT_PRELU, alpha=0.0, residual=False,
+              x_cstride=0, x_c0=0, y_cstride=0, y_c0=0, r_cstride=0, r_c0=0, variant=0, ksplit=0,
+              ref_cand=0xFF) -> ConvDesc:
+    if pad is None:
+        pad = 1 if k == 3 else 0
+    d = ConvDesc()
+    for name, v in dict(n=n, h=h, w=w, cin=cin, cout=cout, kh=k, kw=k, stride=stride, pad=pad,
+                        x_cstride=x_cstride, x_c0=x_c0, y_cstride=y_cstride, y_c0=y_c0, r_cstride=r_cstride,
+                        r_c0=r_c0, act=act, alpha=alpha, residual=int(bool(residual)), variant=variant,
+                        ksplit=ksplit, ref_cand=ref_cand).items():
+        setattr(d, name, v)
+    return d
+
+
+def _host_u16(a):
+    """A host buffer of f16 bit patterns (numpy uint16/float16 or a CPU torch tensor) and its pointer."""
+    import numpy as np
+    if a is None:
+        return None, None
+    if hasattr(a, "detach"):  # torch tensor
+        a = a.detach().cpu().contiguous().view(-1)
+        import torch
+        if a.dtype == torch.float16:
+            a = a.view(torch.int16)
+        a = a.numpy()
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.float16:
+        a = a.view(np.uint16)
+    if a.dtype not in (np.uint16, np.int16):
+        raise FhcError(f"weights must be f16 bit patterns, got {a.dtype}")
+    return a, a.ctypes.data_as(ctypes.c_void_p)
+
+
+class ConvPlan:
+    """A planned conv: fhc_conv_plan_create (conv_pick + buildb/buildb_tap), then run() per frame."""
+
+    def __init__(self, desc: ConvDesc, w_oihw, bias, slope=None):
+        L = load()
+        self.desc = desc
+        wa, wp = _host_u16(w_oihw)
+        ba, bp = _host_u16(bias)
+        sa, sp = _host_u16(slope)
+        if wa is None or wa.size != desc.cout * desc.cin * desc.kh * desc.kw:
+            raise FhcError("weights must hold cout*cin*kh*kw f16 values (OIHW)")
+        if ba is None or ba.size != desc.cout or (sa is not None and sa.size != desc.cout):
+            raise FhcError("bias and slope must hold cout f16 values")
+        h = ctypes.c_void_p()
+        _check(L.fhc_conv_plan_create(ctypes.byref(desc), wp, bp, sp, ctypes.byref(h)), "fhc_conv_plan_create")
+        self._h = h
+        ho, wo = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(L.fhc_conv_out_shape(h, ctypes.byref(ho), ctypes.byref(wo)), "fhc_conv_out_shape")
+        self.hout, self.wout = ho.value, wo.value
+        self.workspace_bytes = L.fhc_conv_workspace_bytes(h)
+
+    @property
+    def handle(self):
+        return self._h.value
+
+    def describe(self) -> dict:
+        buf = ctypes.create_string_buffer(2048)
+        _check(load().fhc_conv_describe(self._h, buf, len(buf)), "fhc_conv_describe")
+        return json.loads(buf.value.decode())
+
+    def run(self, x, y, res=None, workspace=None, stream=None):
+        _check(load().fhc_conv_run(self._h, _ptr(x), _ptr(y), _ptr(res), _ptr(workspace),
+                                   _stream_handle(stream)), "fhc_conv_run")
+
+    def out_elems(self):
+        d = self.desc
+        return d.n * self.hout * self.wout * (d.y_cstride or d.cout)
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            load().fhc_conv_plan_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+@dataclass
+class ConvOp:
+    """One conv of the graph as the planner sees it (ConvOp, ops/conv/autotune.rs:100-109), NHWC."""
+    weight: object          # OIHW f16 [cout][cin][k][k]
+    bias: object            # f16 [cout]
+    slope: object = None    # f16 [cout] (PReLU) or None (identity: the reference's `ones`)
+    cin: int = 0
+    cout: int = 0
+    stride: int = 1
+    k: int = 3
+
+
+def conv_pick(op: ConvOp, n: int, h: int, w: int, residual: bool = False, **kw) -> ConvPlan:
+    """Plan a conv of `op` over an NHWC input of n x h x w (BuildCtx::conv_pick, autotune.rs:159-235)."""
+    act = ACT_PRELU if op.slope is not None else ACT_NONE
+    d = make_desc(n, h, w, op.cin, op.cout, k=op.k, stride=op.stride, act=act, residual=residual, **kw)
+    return ConvPlan(d, op.weight, op.bias, op.slope)
+
+
+def conv(plan: ConvPlan, x, res=None, stream=None):
+    """Run `plan` on NHWC f16 input x (torch, on the GPU); returns a new NHWC f16 output."""
+    import torch
+    d = plan.desc
+    y = torch.empty((d.n, plan.hout, plan.wout, d.y_cstride or d.cout), dtype=torch.float16, device=x.device)
+    ws = None
+    if plan.workspace_bytes:
+        ws = torch.empty(plan.workspace_bytes // 4 + 4, dtype=torch.float32, device=x.device)
+    plan.run(x, y, res, ws, stream)
+    return y
+
+
+def plan_dry(desc: ConvDesc) -> dict:
+    """The planner's choice for `desc` without a device (fhc_conv_plan_dry)."""
+    buf = ctypes.create_string_buffer(2048)
+    _check(load().fhc_conv_plan_dry(ctypes.byref(desc), buf, len(buf)), "fhc_conv_plan_dry")
+    return json.loads(buf.value.decode())
+
+
+# ---- the reference planner restated, and the choice table ----------------------------------------------------
+
+def cand_list(coop: bool, cout: int, hout: int, wout: int, direct_ok: bool, try_all: bool = False):
+    buf = (ctypes.c_uint8 * 64)()
+    n = _check(load().fhc_ref_cand_list(int(coop), cout, hout, wout, int(direct_ok), int(try_all), buf, 64),
+               "fhc_ref_cand_list")
+    return list(buf[:n])
+
+
+def cand_name(code: int) -> str:
+    buf = ctypes.create_string_buffer(64)
+    _check(load().fhc_ref_cand_name(code, buf, 64), "fhc_ref_cand_name")
+    return buf.value.decode()
+
+
+def ref_conv_steps(cin, cout, h, w, stride, residual=False, coop=True, cand=0xFF, ksplit_env=0, f32_mode=False):
+    """The reference's dispatches for one conv: list of (pipeline, (gx,gy,gz), weight_bytes, [param words])."""
+    c = RefConv(cin=cin, cout=cout, h=h, w=w, stride=stride, residual=int(residual), coop=int(coop), cand=cand,
+                ksplit_env=ksplit_env, f32_mode=int(f32_mode))
+    buf = ctypes.create_string_buffer(4096)
+    _check(load().fhc_ref_conv_steps(ctypes.byref(c), buf, len(buf)), "fhc_ref_conv_steps")
+    out = []
+    for line in buf.value.decode().splitlines():
+        name, grid, wb, params = line.split(" ", 3)
+        g = tuple(int(v) for v in grid.strip("()").split(","))
+        words = [int(v, 16) for v in params[1:].split()]
+        out.append((name, g, int(wb[1:]), words))
+    return out
+
+
+def parse_tune(text: str) -> int:
+    return _check(load().fhc_tune_parse(text.encode()), "fhc_tune_parse")
+
+
+def format_tune() -> str:
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(load().fhc_tune_format(buf, len(buf)), "fhc_tune_format")
+    return buf.value.decode()
+
+
+def tune_clear():
+    load().fhc_tune_clear()
+
+
+def tune_get(cin, cout, h, w, stride) -> Optional[int]:
+    v = load().fhc_tune_get(cin, cout, h, w, stride)
+    return None if v < 0 else v
+
+
+def variant_name(code: int) -> str:
+    buf = ctypes.create_string_buffer(128)
+    _check(load().fhc_variant_name(code, buf, len(buf)), "fhc_variant_name")
+    return buf.value.decode()
+
+
+def variant_list(desc: ConvDesc) -> Sequence[int]:
+    arr = (ctypes.c_uint32 * 256)()
+    n = _check(load().fhc_variant_list(ctypes.byref(desc), arr, 256), "fhc_variant_list")
+    return list(arr[:n])
+
+
+def probe_mfma_layout(a, b, d, stream=None):
+    _check(load().fhc_probe_mfma_layout(_ptr(a), _ptr(b), _ptr(d), _stream_handle(stream)), "fhc_probe_mfma_layout")

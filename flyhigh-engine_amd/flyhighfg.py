@@ -1,0 +1,135 @@
+"""The conv layers of the FlyHighFG graph and of the benchmark configurations, as the planner walks them.
+
+The FlyHighFG table restates the conv ops of the reference graph (models/graph.json:68-1244, the weight shapes of
+models/flyhighfg.json) as the planner's conv arm sees them (crates/flyhigh-engine/src/net/build.rs:209-278):
+``conv`` ops carry a PReLU slope, ``conv2d`` ops and the convex-upsample conv (build.rs:379-416) have none, and a
+following ``add`` of a plain same-shape tensor is fused as the residual (build.rs:222-237). The pair / mid split
+is the graph's mid_start (crates/flyhigh-engine/src/model/graph.rs:182). Layer input sizes follow from the
+network size: the encoder reads the quarter-resolution image and halves it twice (stride-2 e1 and e3); the
+coarse block works at 1/16, the fine block and FiLM at 1/8, the refine block at 1/4.
+"""
+from __future__ import annotations
+
+import math
+
+from dataclasses import dataclass
+from typing import List, Optional
+
+
+@dataclass(frozen=True)
+class ConvLayer:
+    name: str
+    stage: str            # "pair" or "mid"
+    cin: int
+    cout: int
+    h: int                # input height / width
+    w: int
+    stride: int = 1
+    k: int = 3
+    act: int = 1          # 1 PReLU (graph op conv), 0 identity (conv2d), 2 LeakyReLU(alpha)
+    alpha: float = 0.0
+    residual: bool = False
+    chain: Optional[str] = None  # the conv whose output is this conv's input (None: a non-conv op feeds it)
+    res_from: Optional[str] = None  # the conv whose output is the fused residual (None: another op's output)
+    weight: str = ""      # weight tensor name in the model manifest
+
+    @property
+    def hout(self):
+        pad = 1 if self.k == 3 else 0
+        return (self.h + 2 * pad - self.k) // self.stride + 1
+
+    @property
+    def wout(self):
+        pad = 1 if self.k == 3 else 0
+        return (self.w + 2 * pad - self.k) // self.stride + 1
+
+    @property
+    def flops(self):
+        return 2 * self.hout * self.wout * self.cout * self.cin * self.k * self.k
+
+    @property
+    def bytes(self):
+        """Algorithmic bytes: f16 input + output + weights + bias + slope (+ residual), each touched once."""
+        out = self.hout * self.wout * self.cout
+        return 2 * (self.h * self.w * self.cin + out + self.cout * self.cin * self.k * self.k + self.cout
+                    + (self.cout if self.act == 1 else 0) + (out if self.residual else 0))
+
+
+def default_internal(w: int, h: int):
+    """The network resolution of a frame size: the frame itself up to 960 px on the long side, above that the
+    480-line rung, aspect kept, multiples of 8 (crates/flyhigh-engine/src/options.rs:347-356)."""
+    if max(w, h) <= 960:
+        return (w, h)
+    s = min(480.0 / h, 1.0)
+    rw = max(int(math.floor(w * s / 8.0 + 0.5)) * 8, 64)  # f64::round: half away from zero
+    rh = max(int(math.floor(h * s / 8.0 + 0.5)) * 8, 64)
+    return (min(rw, w), min(rh, h))
+
+
+def pad32(v: int) -> int:
+    return (v + 31) // 32 * 32
+
+
+def flyhighfg_layers(net_w: int = 864, net_h: int = 480, k: int = 1) -> List[ConvLayer]:
+    """Conv layers of one pair() and one mid() at a padded network size (default: 1080p's 856x480 -> 864x480)."""
+    qw, qh = net_w // 4, net_h // 4
+    e8w, e8h = (qw + 2 - 3) // 2 + 1, (qh + 2 - 3) // 2 + 1
+    e16w, e16h = (e8w + 2 - 3) // 2 + 1, (e8h + 2 - 3) // 2 + 1
+    L = []
+    for side in ("a", "b"):
+        L += [
+            ConvLayer(f"enc.e1.{side}", "pair", 3, 36, qh, qw, 2, weight="enc.e1.0.weight"),
+            ConvLayer(f"enc.e2.{side}", "pair", 36, 36, e8h, e8w, residual=True, chain=f"enc.e1.{side}",
+                      res_from=f"enc.e1.{side}", weight="enc.e2.0.weight"),
+            ConvLayer(f"enc.e3.{side}", "pair", 36, 72, e8h, e8w, 2, chain=f"enc.e2.{side}", weight="enc.e3.0.weight"),
+            ConvLayer(f"enc.e4.{side}", "pair", 72, 72, e16h, e16w, residual=True, chain=f"enc.e3.{side}",
+                      res_from=f"enc.e3.{side}", weight="enc.e4.0.weight"),
+        ]
+    L += [
+        ConvLayer("coarse.c1", "pair", 279, 96, e16h, e16w, weight="coarse.c1.0.weight"),
+        ConvLayer("coarse.c2", "pair", 96, 96, e16h, e16w, chain="coarse.c1", weight="coarse.c2.0.weight"),
+        ConvLayer("coarse.c3", "pair", 96, 96, e16h, e16w, residual=True, chain="coarse.c2",
+                  res_from="coarse.c1", weight="coarse.c3.0.weight"),
+        ConvLayer("coarse.c4", "pair", 96, 96, e16h, e16w, chain="coarse.c3", weight="coarse.c4.0.weight"),
+        ConvLayer("coarse.head", "pair", 96, 12, e16h, e16w, act=0, chain="coarse.c4",
+                  weight="coarse.head.weight"),
+    ]
+    for i in range(k):
+        sfx = f".{i}" if k > 1 else ""
+        L += [
+            ConvLayer(f"fine.r1{sfx}", "pair", 155, 48, e8h, e8w, weight="fine.r1.0.weight"),
+            ConvLayer(f"fine.r2{sfx}", "pair", 48, 48, e8h, e8w, chain=f"fine.r1{sfx}", weight="fine.r2.0.weight"),
+            ConvLayer(f"fine.r3{sfx}", "pair", 48, 48, e8h, e8w, chain=f"fine.r2{sfx}", weight="fine.r3.0.weight"),
+            ConvLayer(f"fine.out{sfx}", "pair", 48, 7, e8h, e8w, act=0, chain=f"fine.r3{sfx}",
+                      weight="fine.out.weight"),
+        ]
+    L += [
+        ConvLayer("film.h1", "mid", 48, 48, e8h, e8w, weight="film.h1.0.weight"),
+        ConvLayer("film.h2", "mid", 48, 48, e8h, e8w, chain="film.h1", weight="film.h2.0.weight"),
+        ConvLayer("film.out", "mid", 48, 5, e8h, e8w, act=0, chain="film.h2", weight="film.out.weight"),
+        ConvLayer("up.w", "mid", 48, 36, e8h, e8w, act=0, weight="up.w.weight"),
+        ConvLayer("refine.q1", "mid", 14, 24, qh, qw, weight="refine.q1.0.weight"),
+        ConvLayer("refine.q2", "mid", 24, 24, qh, qw, chain="refine.q1", weight="refine.q2.0.weight"),
+        ConvLayer("refine.q3", "mid", 24, 24, qh, qw, chain="refine.q2", weight="refine.q3.0.weight"),
+        ConvLayer("refine.q4", "mid", 24, 3, qh, qw, act=0, chain="refine.q3", weight="refine.q4.weight"),
+    ]
+    return L
+
+
+def config_layers(cfg: int) -> List[ConvLayer]:
+    """The single-layer / ladder benchmark configurations C1-C3 (batch 1, NHWC f16)."""
+    if cfg == 1:  # 3x3 32->32 at 1080p/8, LeakyReLU(0.1)
+        return [ConvLayer("c1.conv", "pair", 32, 32, 136, 240, act=2, alpha=0.1)]
+    if cfg == 2:  # 1080p/4 ladder: s2 32->64 from 544x960, three 64->64, residual (the s2 output) on the last
+        return [
+            ConvLayer("c2.down", "pair", 32, 64, 544, 960, 2),
+            ConvLayer("c2.b1", "pair", 64, 64, 272, 480, chain="c2.down"),
+            ConvLayer("c2.b2", "pair", 64, 64, 272, 480, chain="c2.b1"),
+            ConvLayer("c2.b3", "pair", 64, 64, 272, 480, residual=True, chain="c2.b2", res_from="c2.down"),
+        ]
+    if cfg == 3:  # deep small-spatial 1080p/16: 128->128 (split-K) and 1x1 128->64 on the same input
+        return [
+            ConvLayer("c3.deep", "pair", 128, 128, 68, 120),
+            ConvLayer("c3.pw", "pair", 128, 64, 68, 120, k=1, act=0),
+        ]
+    raise ValueError(f"unknown configuration {cfg}")

@@ -1,0 +1,145 @@
+/* fhc_conv: the FlyHigh convolution hot path on MI355X (gfx950), as a C ABI.
+ *
+ * A drop-in for the reference engine's conv op. The reference has no FFI at conv level: its conv boundary is the
+ * Rust-internal record/replay pair
+ *   plan time  BuildCtx::conv_pick(&ConvOp, Option<&Tensor>)  crates/flyhigh-engine/src/ops/conv/autotune.rs:159
+ *              -> Gpu::conv_tc / conv_tiled_with / conv_direct crates/flyhigh-engine/src/ops/conv/kernels.rs:100-279
+ *   run time   replay of the recorded Steps                   crates/flyhigh-engine/src/gpu/exec.rs:62-87
+ * This ABI keeps that split: fhc_conv_plan_create is conv_pick + the weight packing (buildb/buildb_tap), and
+ * fhc_conv_run is the replay of the plan's dispatches onto a HIP stream.
+ *
+ * Conventions (those of the reference's C ABI, crates/flyhigh-capi/src/lib.rs:27-48 and include/flyhigh.h:12):
+ *  - every call returns 0 (or a size / count) on success and a negative value on error; the message is then in
+ *    fhc_last_error(), which is thread-local; nothing aborts and nothing throws across this boundary;
+ *  - handles are opaque; a plan is immutable after create; single-threaded use per handle for create/destroy,
+ *    fhc_conv_run may be called from any thread on a stream of the device the plan was created on;
+ *  - tensors are caller-owned device buffers (the reference's arena, gpu/alloc.rs:85); the library never
+ *    allocates during fhc_conv_run and never assumes zeroed memory.
+ *
+ * Tensors are NHWC f16 (IEEE binary16 bit patterns in uint16_t), batch-major: element (img, y, x, c) of a view
+ * lives at ((img * H + y) * W + x) * cstride + c0 + c. The reference stores planar [C][H][W] f16 with batch 1
+ * (crates/flyhigh-engine/src/ops/tensor.rs:6-17); a channel view there (c0) is a channel offset here, and a
+ * concat slice is written in place by giving the producer the slice's cstride/c0.
+ */
+#ifndef FHC_CONV_H
+#define FHC_CONV_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FHC_ACT_NONE 0u  /* identity: the reference's conv2d op with the `ones` slope (net/build.rs:210-220) */
+#define FHC_ACT_PRELU 1u /* v > 0 ? v : slope[co] * v (shaders/conv.wgsl:33, conv_tiled.wgsl:64-66) */
+#define FHC_ACT_LEAKY 2u /* v > 0 ? v : alpha * v, alpha an f32 constant */
+
+/* The conv descriptor. Mirrors ImplicitGemmParams (crates/flyhigh-engine/src/ops/params.rs:188-210) and ConvArgs
+ * (ops/conv/kernels.rs:7-22) with NHWC views added. Zero in a cstride means "dense" (cin for x, cout for y/r). */
+typedef struct fhc_conv_desc {
+    uint32_t n, h, w;            /* batch (1 in the reference), input height and width                       */
+    uint32_t cin, cout;          /* true channel counts (no padding)                                           */
+    uint32_t kh, kw;             /* 3,3 (the reference) or 1,1 (the 1x1 extension)                            */
+    uint32_t stride, pad;        /* 3x3: stride 1 or 2, pad 1 (kernels.rs:40-42); 1x1: stride 1, pad 0         */
+    uint32_t x_cstride, x_c0;    /* input view                                                                  */
+    uint32_t y_cstride, y_c0;    /* output view (a concat slice)                                                */
+    uint32_t r_cstride, r_c0;    /* residual view                                                               */
+    uint32_t act;                /* FHC_ACT_*                                                                   */
+    float alpha;                 /* FHC_ACT_LEAKY slope                                                         */
+    uint32_t residual;           /* 1: y = f16(f32(f16(act(acc + bias))) + f32(r)) (conv_tiled.wgsl:57-61)      */
+    uint32_t variant;            /* 0: planner (tune table, else heuristic); else a forced MI355X variant code  */
+    uint32_t ksplit;             /* 0: planner; else a forced split-K count (1, 2, 4, 8)                        */
+    uint32_t ref_cand;           /* 0xFF: none; else the reference's candidate code (candidates.rs:3-16), taken
+                                    as a hint: its forced split-K nibble applies when ksplit is 0              */
+} fhc_conv_desc;
+
+typedef struct fhc_conv_plan fhc_conv_plan;
+
+/* Message of the last failed call on this thread ("" if none). Replaces fh_last_error
+ * (crates/flyhigh-capi/include/flyhigh.h:32) at conv granularity. */
+const char* fhc_last_error(void);
+
+/* Build a plan: validate the descriptor, choose the kernel variant and split-K (replaces BuildCtx::conv_pick,
+ * ops/conv/autotune.rs:159-235, fixed-routing and tune-table branches), pack the OIHW f16 weights
+ * [cout][cin][kh][kw] into MFMA fragment order (replaces Gpu::buildb / buildb_tap, ops/conv/kernels.rs:66-78,
+ * :194-207) and upload them, with bias and slope, to the current HIP device. w, bias and slope are host
+ * pointers; slope may be NULL unless act == FHC_ACT_PRELU. */
+int fhc_conv_plan_create(const fhc_conv_desc* desc, const uint16_t* w_oihw, const uint16_t* bias,
+                         const uint16_t* slope, fhc_conv_plan** out);
+
+/* Device scratch the plan needs per run, in bytes (split-K partials; 0 for most plans). The reference keeps this
+ * in arena scratch released after the op (gpu/alloc.rs:101-111, kernels.rs:178-179). */
+size_t fhc_conv_workspace_bytes(const fhc_conv_plan* plan);
+
+/* Output shape of the plan (hout, wout); any pointer may be NULL. Replaces out_size (kernels.rs:40-42). */
+int fhc_conv_out_shape(const fhc_conv_plan* plan, uint32_t* hout, uint32_t* wout);
+
+/* Enqueue the conv on `stream` (a hipStream_t; NULL = the null stream). x, y, res, workspace are device
+ * pointers; res is read only when desc.residual is 1; workspace must hold fhc_conv_workspace_bytes. Asynchronous:
+ * no allocation, no synchronisation, capturable in a hipGraph. Replaces the replay of the conv's Steps
+ * (gpu/exec.rs:15-87). 16-byte aligned pointers and cstride/c0 multiples of 8 select the vector load path. */
+int fhc_conv_run(const fhc_conv_plan* plan, const void* x, void* y, const void* res, void* workspace,
+                 void* stream);
+
+/* JSON description of the plan: variant, tile, split-K, grid, packed sizes, algorithmic FLOPs and bytes. Returns
+ * bytes written (without the NUL) or -1 when cap is too small. Replaces plan_dump for one conv
+ * (ops/step.rs:51-88). */
+int fhc_conv_describe(const fhc_conv_plan* plan, char* json, size_t cap);
+
+void fhc_conv_plan_destroy(fhc_conv_plan* plan);
+
+/* The planner's choice for a descriptor without creating a plan (no device call): the same JSON as
+ * fhc_conv_describe, sizes included. For host-side tests and for tools that print the plan of a graph
+ * (the reference's FH_TUNE_VERBOSE listing, ops/conv/autotune.rs:217-228). Bytes written or -1. */
+int fhc_conv_plan_dry(const fhc_conv_desc* desc, char* json, size_t cap);
+
+/* ---- The planner's choice table ------------------------------------------------------------------------
+ * Same key and text format as the reference's TuneTable (ops/conv/tune_cache.rs:6-9, :39-64): one
+ * "cin,cout,h,w,stride=code" per line, h and w the INPUT size; malformed lines are skipped. The codes are
+ * MI355X variant codes (fhc_variant_name). The table is process-wide and consulted by fhc_conv_plan_create when
+ * desc.variant is 0. */
+int fhc_tune_parse(const char* text);           /* merges; returns the number of entries read, or -1   */
+int fhc_tune_format(char* text, size_t cap);    /* sorted lines; bytes written, or -1 if cap too small */
+int fhc_tune_clear(void);
+int fhc_tune_get(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride); /* code or -1 */
+/* Name of an MI355X variant code ("igemm.t8x16.n64/k2" ...) into buf; bytes written or -1. */
+int fhc_variant_name(uint32_t code, char* buf, size_t cap);
+/* The MI355X variant codes worth timing for a descriptor (the counterpart of cand_list); count written, or -1. */
+int fhc_variant_list(const fhc_conv_desc* desc, uint32_t* codes, size_t cap);
+
+/* ---- The reference planner, restated (host logic, no GPU) ---------------------------------------------
+ * For parity of the planner itself: these reproduce the reference's kernel choice and dispatch words so that
+ * tests can compare them with the reference's golden plans (crates/flyhigh-engine/tests/golden/<config>.<class>.txt). */
+
+/* cand_list (ops/conv/candidates.rs:28-85); try_all stands for FH_TRY_ALL. Returns the count written, or -1. */
+int fhc_ref_cand_list(int coop, uint32_t cout, uint32_t hout, uint32_t wout, int direct_ok, int try_all,
+                      uint8_t* out, size_t cap);
+/* cand_name (ops/conv/candidates.rs:17-24) into buf; bytes written or -1. */
+int fhc_ref_cand_name(uint8_t code, char* buf, size_t cap);
+
+/* One conv of the reference graph at plan time (ConvOp, ops/conv/autotune.rs:100-109, plus the planner's
+ * residual peephole of net/build.rs:222-237). */
+typedef struct fhc_ref_conv {
+    uint32_t cin, cout, h, w, stride;
+    uint32_t residual;  /* a fused `add` follows                                                   */
+    uint32_t coop;      /* the device class has cooperative-matrix (tensor-core) kernels            */
+    uint32_t cand;      /* 0xFF: fixed routing (autotune off, autotune.rs:191-198); else a CAND code */
+    uint32_t ksplit_env;/* FH_KSPLIT (0 = unset)                                                    */
+    uint32_t f32_mode;  /* the portable-f32 class: weights stored as f32 (4-byte elements)             */
+} fhc_ref_conv;
+
+/* The dispatches the reference records for that conv (conv_cand, autotune.rs:115-154, and the Gpu::conv_* launch
+ * math, kernels.rs:99-279), one per line: "pipeline (gx,gy,gz) w<packed weight bytes> p<param words as 8-digit
+ * hex, space separated>". Returns bytes written or -1. */
+int fhc_ref_conv_steps(const fhc_ref_conv* c, char* text, size_t cap);
+
+/* ---- Diagnostics -----------------------------------------------------------------------------------------
+ * One v_mfma_f32_16x16x32_f16 with the operand layouts the conv kernels assume: d (16x16 f32, row-major) =
+ * a (16x32 f16, row-major) x b (32x16 f16, row-major). Device pointers; asynchronous on `stream`. It has no
+ * counterpart in the reference (the reference's own probes of its cooperative-matrix layout are
+ * crates/flyhigh-cli/src/cli/coop_tests.rs:7-113). */
+int fhc_probe_mfma_layout(const void* a, const void* b, void* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,119 @@
+"""ctypes front end of the CPU oracle (fh_oracle.c): TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's CPU-baseline leg import this module, as the checker.
+The product never imports it.
+
+Arrays are numpy uint16 holding f16 bit patterns. Tensors are NHWC with a pixel stride (``*_cstride``) and a
+channel offset (``*_c0``); weights are the reference's OIHW ``[cout][cin][kh][kw]``
+(crates/flyhigh-engine/src/model/blob.rs:32-41).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfhoracle.so")
+
+ORDER_TILED, ORDER_NAIVE, ORDER_SPLITK = 0, 1, 2
+
+
+class FhoConv(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "n", "h", "w", "cin", "cout", "kh", "kw", "stride", "pad",
+        "x_cstride", "x_c0", "y_cstride", "y_c0", "r_cstride", "r_c0", "act")] + [
+        ("alpha", ctypes.c_float), ("residual", ctypes.c_uint32)]
+
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-B", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        L.fho_conv_run.argtypes = [ctypes.POINTER(FhoConv), P, P, P, P, P, P, ctypes.c_int, ctypes.c_uint32]
+        L.fho_conv_run.restype = ctypes.c_int
+        L.fho_conv_run_mt.argtypes = [ctypes.POINTER(FhoConv), P, P, P, P, P, P, ctypes.c_int]
+        L.fho_conv_run_mt.restype = ctypes.c_int
+        L.fho_f32_to_f16.argtypes = [ctypes.c_float]
+        L.fho_f32_to_f16.restype = ctypes.c_uint16
+        L.fho_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.fho_f16_to_f32.restype = ctypes.c_float
+        L.fho_f32_to_f16_n.argtypes = [P, P, ctypes.c_size_t]
+        L.fho_f32_to_f16_n.restype = None
+        L.fho_f16_to_f32_n.argtypes = [P, P, ctypes.c_size_t]
+        L.fho_f16_to_f32_n.restype = None
+        L.fho_out_size.argtypes = [ctypes.c_uint32] * 4
+        L.fho_out_size.restype = ctypes.c_uint32
+        _lib = L
+    return _lib
+
+
+def out_size(n, k, s, p):
+    return (n + 2 * p - k) // s + 1
+
+
+def make_desc(n, h, w, cin, cout, k=3, stride=1, pad=None, act=1, alpha=0.0, residual=False,
+              x_cstride=None, x_c0=0, y_cstride=None, y_c0=0, r_cstride=None, r_c0=0):
+    if pad is None:
+        pad = 1 if k == 3 else 0
+    return dict(n=n, h=h, w=w, cin=cin, cout=cout, kh=k, kw=k, stride=stride, pad=pad,
+                x_cstride=x_cstride or cin, x_c0=x_c0, y_cstride=y_cstride or cout, y_c0=y_c0,
+                r_cstride=r_cstride or cout, r_c0=r_c0, act=act, alpha=alpha, residual=int(bool(residual)))
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _struct(d):
+    s = FhoConv()
+    for k, v in d.items():
+        setattr(s, k, v)
+    return s
+
+
+def conv(d, x, w, bias, slope=None, res=None, y=None, order=ORDER_TILED, ksplit=1, threads=0):
+    """Runs the oracle conv; returns y (uint16 f16 bits, NHWC with y_cstride)."""
+    if d["stride"] < 1 or d["kh"] < 1 or d["kw"] < 1:
+        raise ValueError("oracle rejected the conv descriptor")
+    hout = out_size(d["h"], d["kh"], d["stride"], d["pad"])
+    wout = out_size(d["w"], d["kw"], d["stride"], d["pad"])
+    arrs = [np.ascontiguousarray(a, dtype=np.uint16) if a is not None else None for a in (x, w, bias, slope, res)]
+    if y is None:
+        y = np.zeros(d["n"] * hout * wout * d["y_cstride"], dtype=np.uint16)
+    s = _struct(d)
+    if threads:
+        rc = lib().fho_conv_run_mt(ctypes.byref(s), *[_ptr(a) for a in arrs], _ptr(y), threads)
+    else:
+        rc = lib().fho_conv_run(ctypes.byref(s), *[_ptr(a) for a in arrs], _ptr(y), order, ksplit)
+    if rc != 0:
+        raise ValueError("oracle rejected the conv descriptor")
+    return y
+
+
+def f32_to_f16(a):
+    """float32 array -> uint16 f16 bits (round to nearest even)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().fho_f32_to_f16_n(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def f16_to_f32(a):
+    """uint16 f16 bits -> float32 array (exact)."""
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().fho_f16_to_f32_n(_ptr(a), _ptr(out), a.size)
+    return out

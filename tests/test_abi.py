@@ -1,0 +1,114 @@
+"""The C-ABI boundary without a GPU: the library loads, exports every function the header declares, and turns
+bad input into an error status with a message (never an abort), as the reference's C ABI does
+(crates/flyhigh-capi/src/lib.rs:27-48)."""
+import ctypes
+import os
+import re
+import threading
+
+import pytest
+
+from fhtest import ROOT, fhconv
+
+
+def declared_functions():
+    names = set()
+    inc = os.path.join(ROOT, "include")
+    for fn in os.listdir(inc):
+        if fn.endswith(".h"):
+            text = open(os.path.join(inc, fn)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names.update(re.findall(r"\b(fhc_\w+)\s*\(", text))
+    return names
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("fhc_conv_plan_create", "fhc_conv_run", "fhc_conv_workspace_bytes", "fhc_conv_describe",
+                     "fhc_conv_plan_destroy", "fhc_last_error", "fhc_ref_conv_steps", "fhc_tune_parse"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(fhconv.LIB_PATH)
+    missing = [n for n in sorted(declared_functions()) if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+BAD = [
+    dict(stride=3), dict(cin=0), dict(cout=0), dict(n=0), dict(k=5), dict(pad=0), dict(k=1, pad=1),
+    dict(k=1, stride=2), dict(x_cstride=16, x_c0=8), dict(y_cstride=30), dict(residual=True, r_cstride=10),
+    dict(act=7), dict(ksplit=3), dict(cin=5000), dict(variant=31), dict(variant=200),
+]
+
+
+@pytest.mark.parametrize("bad", BAD)
+def test_bad_descriptor_is_an_error_status(bad):
+    kw = dict(n=1, h=16, w=16, cin=16, cout=32)
+    for k in ("n", "cin", "cout"):
+        if k in bad:
+            kw[k] = bad.pop(k)
+    d = fhconv.make_desc(kw["n"], 16, 16, kw["cin"], kw["cout"], **bad)
+    with pytest.raises(fhconv.FhcError) as e:
+        fhconv.plan_dry(d)
+    assert "fhc_conv_plan_dry" in str(e.value)
+    # plan creation validates before touching the device: the same descriptor fails the same way
+    h = ctypes.c_void_p(123)
+    w = (ctypes.c_uint16 * (max(kw["cout"], 1) * max(kw["cin"], 1) * 25))()
+    b = (ctypes.c_uint16 * max(kw["cout"], 1))()
+    rc = fhconv.load().fhc_conv_plan_create(ctypes.byref(d), w, b, b, ctypes.byref(h))
+    assert rc == -1 and h.value is None
+    assert fhconv.last_error()
+
+
+def test_null_arguments_are_errors():
+    L = fhconv.load()
+    d = fhconv.make_desc(1, 8, 8, 8, 8)
+    h = ctypes.c_void_p()
+    assert L.fhc_conv_plan_create(None, None, None, None, ctypes.byref(h)) == -1
+    assert "NULL descriptor" in fhconv.last_error()
+    assert L.fhc_conv_plan_create(ctypes.byref(d), None, None, None, ctypes.byref(h)) == -1
+    assert "NULL weights" in fhconv.last_error()
+    assert L.fhc_conv_plan_create(ctypes.byref(d), None, None, None, None) == -1
+    assert L.fhc_conv_run(None, None, None, None, None, None) == -1
+    assert "NULL plan" in fhconv.last_error()
+    assert L.fhc_conv_describe(None, None, 0) == -1
+    assert L.fhc_conv_workspace_bytes(None) == 0
+    L.fhc_conv_plan_destroy(None)
+
+
+def test_prelu_without_slope_is_an_error():
+    L = fhconv.load()
+    d = fhconv.make_desc(1, 8, 8, 8, 8, act=fhconv.ACT_PRELU)
+    w = (ctypes.c_uint16 * (8 * 8 * 9))()
+    b = (ctypes.c_uint16 * 8)()
+    h = ctypes.c_void_p()
+    assert L.fhc_conv_plan_create(ctypes.byref(d), w, b, None, ctypes.byref(h)) == -1
+    assert "slope" in fhconv.last_error()
+
+
+def test_small_buffers_are_errors_not_overflows():
+    L = fhconv.load()
+    buf = ctypes.create_string_buffer(4)
+    assert L.fhc_ref_cand_name(2, buf, 4) == -1  # "tiled" needs 6 bytes
+    assert "too small" in fhconv.last_error()
+    out = (ctypes.c_uint8 * 2)()
+    assert L.fhc_ref_cand_list(1, 64, 60, 108, 0, 1, out, 2) == -1
+    d = fhconv.make_desc(1, 136, 240, 32, 32)
+    assert L.fhc_conv_plan_dry(ctypes.byref(d), ctypes.create_string_buffer(16), 16) == -1
+
+
+def test_last_error_is_thread_local():
+    L = fhconv.load()
+    d = fhconv.make_desc(1, 8, 8, 8, 8, stride=3)
+    assert L.fhc_conv_plan_dry(ctypes.byref(d), None, 0) == -1
+    mine = fhconv.last_error()
+    seen = []
+
+    def other():
+        seen.append(fhconv.last_error())
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert mine and seen == [""]

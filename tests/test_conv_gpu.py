@@ -1,0 +1,224 @@
+"""Parity of the HIP conv path (through the C ABI) with the CPU oracle, on the GPU.
+
+Bar (north star): per element |diff| <= 1e-2 * max|ref| for f16 results with f32 accumulation; indexing,
+padding and stride are checked bit-exactly by closed forms; the untouched parts of views must stay untouched.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from fhtest import Case, as_f64, f16_bits, fhconv, oracle, oracle_rows, parity, ulp_dist
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "conv_vectors.npz")
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def test_mfma_fragment_layout():
+    import torch
+    rng = np.random.default_rng(1)
+    a = f16_bits(rng.uniform(-1, 1, (16, 32)))
+    b = f16_bits(rng.uniform(-1, 1, (32, 16)))
+    da = torch.from_numpy(a.view(np.int16)).cuda()
+    db = torch.from_numpy(b.view(np.int16)).cuda()
+    dd = torch.zeros((16, 16), dtype=torch.float32, device="cuda")
+    fhconv.probe_mfma_layout(da, db, dd)
+    torch.cuda.synchronize()
+    want = as_f64(a) @ as_f64(b)
+    assert np.abs(dd.cpu().numpy() - want).max() < 1e-5
+
+
+def test_golden_vectors_on_the_gpu():
+    z = np.load(GOLDEN)
+    names = sorted({k.split(".")[0] for k in z.files})
+    for nm in names:
+        n, h, w, cin, cout, k, s, pad, act, res, xcs, xc0, ycs, yc0, rcs, rc0 = [int(v) for v in z[nm + ".meta"]]
+        say("golden", nm)
+        c = Case(n, h, w, cin, cout, k=k, stride=s, act=act, alpha=float(z[nm + ".alpha"][0]), residual=res,
+                 xv=(xcs, xc0), yv=(ycs, yc0), rv=(rcs, rc0))
+        c.x, c.wt, c.bias, c.slope = z[nm + ".x"], z[nm + ".w"], z[nm + ".bias"], z[nm + ".slope"]
+        c.res, c.y0 = z[nm + ".res"], z[nm + ".y0"]
+        got = c.run_gpu()
+        want = z[nm + ".y"]
+        ok, md, mref = parity(got, want)
+        assert ok, (nm, md, mref)
+        assert ulp_dist(got, want).max() <= 4, nm
+        # channels outside the output view keep their prior contents
+        mask = np.ones(ycs, bool)
+        mask[yc0:yc0 + cout] = False
+        assert np.array_equal(got[..., mask], c.y0[..., mask])
+
+
+SHAPES = [
+    # n, h, w, cin, cout, k, stride, act, residual
+    (1, 9, 11, 5, 7, 3, 1, 1, 0),
+    (1, 10, 13, 3, 6, 3, 2, 1, 0),
+    (1, 20, 37, 14, 24, 3, 1, 1, 1),
+    (2, 17, 23, 36, 36, 3, 1, 1, 1),
+    (1, 33, 35, 36, 72, 3, 2, 1, 0),
+    (1, 30, 54, 72, 72, 3, 1, 1, 1),
+    (1, 30, 54, 279, 96, 3, 1, 1, 0),
+    (1, 30, 54, 96, 12, 3, 1, 0, 0),
+    (1, 60, 108, 155, 48, 3, 1, 1, 0),
+    (1, 60, 108, 48, 7, 3, 1, 0, 0),
+    (1, 60, 108, 48, 36, 3, 1, 0, 0),
+    (1, 120, 216, 24, 3, 3, 1, 0, 0),
+    (1, 120, 216, 3, 36, 3, 2, 1, 0),
+    (1, 68, 120, 128, 64, 1, 1, 0, 0),
+    (1, 13, 29, 40, 130, 1, 1, 2, 1),
+    (1, 136, 240, 32, 32, 3, 1, 2, 0),
+    (1, 1, 1, 9, 4, 3, 1, 1, 0),
+    (1, 7, 1, 6, 5, 3, 2, 1, 0),
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_planner_choice_matches_the_oracle(shape):
+    n, h, w, cin, cout, k, s, act, res = shape
+    c = Case(n, h, w, cin, cout, k=k, stride=s, act=act, residual=res, seed=sum(shape))
+    got, plan = c.run_gpu(return_plan=True)
+    say("shape", shape, plan.describe()["name"])
+    ok, md, mref = parity(got, c.run_oracle(threads=8))
+    assert ok, (md, mref)
+
+
+VARIANT_SHAPES = [(1, 20, 37, 40, 72, 3, 1), (1, 19, 35, 24, 40, 3, 2), (1, 18, 33, 48, 40, 1, 1),
+                  (1, 12, 20, 130, 100, 3, 1)]
+
+
+@pytest.mark.parametrize("shape", VARIANT_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_every_variant_matches_the_oracle(shape):
+    n, h, w, cin, cout, k, s = shape
+    c = Case(n, h, w, cin, cout, k=k, stride=s, act=1, residual=True, seed=7)
+    want = c.run_oracle(threads=8)
+    codes = fhconv.variant_list(c.fhc_desc())
+    assert codes
+    for code in codes:
+        say("variant", shape, fhconv.variant_name(code))
+        ok, md, mref = parity(c.run_gpu(variant=code), want)
+        assert ok, (fhconv.variant_name(code), md, mref)
+
+
+def test_views_with_poisoned_neighbours():
+    # NaN in the input channels outside the view must never reach the result; NaN in the output channels outside
+    # the view must stay there; unaligned strides take the scalar load / store paths
+    for xv, yv, rv in [((48, 8), (80, 16), (40, 4)), ((37, 3), (35, 1), (33, 5)), ((24, 0), (24, 0), (24, 0))]:
+        c = Case(1, 21, 30, 20, 24, act=1, residual=True, xv=xv, yv=yv, rv=rv, poison=True, seed=11)
+        say("views", xv, yv, rv)
+        got = c.run_gpu()
+        want = c.run_oracle()
+        sl = slice(yv[1], yv[1] + 24)
+        ok, md, mref = parity(got, want, view=sl)
+        assert ok, (md, mref)
+        mask = np.ones(yv[0], bool)
+        mask[sl] = False
+        assert np.array_equal(got[..., mask], c.y0[..., mask])
+
+
+def test_batch_images_are_independent():
+    c = Case(3, 22, 35, 24, 40, act=1, residual=True, seed=12)
+    batched = c.run_gpu()
+    for i in range(3):
+        one = Case(1, 22, 35, 24, 40, act=1, residual=True, seed=12)
+        one.x, one.res, one.y0 = c.x[i:i + 1], c.res[i:i + 1], c.y0[i:i + 1]
+        one.wt, one.bias, one.slope = c.wt, c.bias, c.slope
+        assert np.array_equal(one.run_gpu(), batched[i:i + 1])
+
+
+@pytest.mark.parametrize("ks", [1, 2, 4, 8])
+def test_split_k_deep_small_spatial(ks):
+    # the deep 1080p/16 layer: 128 -> 128 at 68 x 120, K = 1152, split 1 / 2 / 4 / 8 ways (f32 partials)
+    c = Case(1, 68, 120, 128, 128, act=1, seed=13)
+    got, plan = c.run_gpu(ksplit=ks, return_plan=True)
+    d = plan.describe()
+    say("split", ks, d["name"], d["ksplit"])
+    assert d["ksplit"] == ks
+    ok, md, mref = parity(got, c.run_oracle(threads=8))
+    assert ok, (md, mref)
+    # the same conv split differently differs only by f32 reassociation
+    ref = as_f64(c.run_gpu(ksplit=1))
+    assert np.abs(as_f64(got) - ref).max() <= 4e-3 * np.abs(ref).max()
+
+
+def test_known_answer_closed_form_conv_on_the_gpu():
+    # crates/flyhigh-cli/src/cli/coop_tests.rs:337-346 and :612 (max|d| < 0.1 against unrounded f32 values)
+    import torch
+    cin, cout, h, w = 208, 64, 46, 80
+    x_chw = (((np.arange(cin * h * w) % 17) - 8) * 0.05).reshape(cin, h, w)
+    wv = (((np.arange(cout * cin * 9) % 13) - 6) * 0.04).reshape(cout, cin, 3, 3)
+    b = (np.arange(cout) % 5 - 2) * 0.1
+    want = torch.nn.functional.conv2d(torch.from_numpy(x_chw[None]), torch.from_numpy(wv), padding=1)[0].numpy()
+    want = want + b[:, None, None]
+    want = np.where(want > 0, want, 0.1 * want)
+    c = Case(1, h, w, cin, cout, act=1, seed=14)
+    c.x = f16_bits(x_chw.transpose(1, 2, 0)[None])
+    c.wt, c.bias, c.slope = f16_bits(wv), f16_bits(b), f16_bits(np.full(cout, 0.1))
+    got = c.run_gpu()
+    assert np.abs(as_f64(got)[0].transpose(2, 0, 1) - want).max() < 0.1
+    ok, md, mref = parity(got, c.run_oracle(threads=8))
+    assert ok, (md, mref)
+
+
+def test_full_size_ladder_rows():
+    # the 1080p/4 ladder at full size, chained on the GPU; every layer checked on three row bands against the
+    # oracle run on the very input the GPU layer read
+    import torch
+    layers = [(544, 960, 32, 64, 2, 0), (272, 480, 64, 64, 1, 0), (272, 480, 64, 64, 1, 0), (272, 480, 64, 64, 1, 1)]
+    x = None
+    first_out = None
+    for i, (h, w, cin, cout, s, res) in enumerate(layers):
+        c = Case(1, h, w, cin, cout, stride=s, act=1, residual=res, seed=20 + i)
+        if x is not None:
+            c.x = x
+        if res:
+            c.res = first_out
+        say("ladder layer", i, (h, w, cin, cout, s, res))
+        got = c.run_gpu()
+        for r0 in (0, c.hout // 2 - 3, c.hout - 6):
+            ok, md, mref = parity(got[0, r0:r0 + 6], oracle_rows(c, r0, r0 + 6, threads=8))
+            assert ok, (i, r0, md, mref)
+        x = got
+        if i == 0:
+            first_out = got
+
+
+def test_graph_capture_replays_match_eager():
+    import torch
+    c = Case(1, 40, 64, 32, 32, act=2, seed=15)
+    plan = fhconv.ConvPlan(c.fhc_desc(), c.wt, c.bias, None)
+    x = torch.from_numpy(c.x.view(np.int16)).cuda()
+    y = torch.zeros_like(torch.from_numpy(c.y0.view(np.int16))).cuda()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        plan.run(x, y)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    y.zero_()
+    with torch.cuda.graph(g):
+        plan.run(x, y)
+    for i in range(4):
+        y.fill_(i + 1)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager), i
+
+
+def test_plan_lifecycle_and_describe():
+    c = Case(1, 16, 16, 8, 8, act=1, seed=16)
+    for _ in range(50):
+        p = fhconv.ConvPlan(c.fhc_desc(), c.wt, c.bias, c.slope)
+        d = p.describe()
+        assert d["hout"] == 16 and d["wout"] == 16 and d["flops"] == 2 * 16 * 16 * 8 * 8 * 9
+        p.close()
+    p = fhconv.ConvPlan(c.fhc_desc(), c.wt, c.bias, c.slope)
+    with pytest.raises(fhconv.FhcError):
+        p.run(None, None)
