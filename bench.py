@@ -39,11 +39,12 @@ def roof(flops, nbytes):
 
 
 class Net:
-    """Plans and resident buffers of a list of conv layers, chained as the graph chains them."""
+    """Plans and resident buffers of a list of conv layers, chained as the graph chains them. With `tune`, each
+    conv shape is autotuned on its buffers before its plan is made (the reference's conv_pick with autotune on)."""
 
-    def __init__(self, layers, seed, torch, np, fhconv):
+    def __init__(self, layers, seed, torch, np, fhconv, tune=True):
         self.layers = layers
-        self.plans, self.bufs = {}, {}
+        self.plans, self.bufs, self.tuned = {}, {}, {}
         dev = torch.device("cuda", 0)
         rng = np.random.default_rng(seed)
         f16 = lambda a: torch.from_numpy(np.asarray(a, np.float32).astype(np.float16))  # noqa: E731
@@ -53,7 +54,6 @@ class Net:
             s = f16(rng.uniform(0.05, 0.3, L.cout)) if L.act == 1 else None
             d = fhconv.make_desc(1, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
                                  residual=L.residual)
-            p = fhconv.ConvPlan(d, wt, b, s)
             x = self.bufs[L.chain][1] if L.chain else \
                 f16(rng.uniform(-1, 1, (1, L.h, L.w, L.cin))).to(dev)
             y = torch.zeros((1, L.hout, L.wout, L.cout), dtype=torch.float16, device=dev)
@@ -62,6 +62,12 @@ class Net:
                     f16(rng.uniform(-1, 1, (1, L.hout, L.wout, L.cout))).to(dev)
             else:
                 r = None
+            if tune:
+                key = (L.cin, L.cout, L.h, L.w, L.stride, L.k)
+                if key not in self.tuned:
+                    code, us = fhconv.autotune(d, wt, b, s, x, y, r, reps=20)
+                    self.tuned[key] = (fhconv.variant_name(code), round(us, 3))
+            p = fhconv.ConvPlan(d, wt, b, s)
             ws = torch.empty(p.workspace_bytes // 4 + 4, dtype=torch.float32, device=dev) \
                 if p.workspace_bytes else None
             self.plans[L.name] = p
@@ -75,22 +81,24 @@ class Net:
 
 
 def time_graph(torch, fn, reps, graphs, stream):
-    """Median over `graphs` replays of a graph holding `reps` calls of fn, per call, in microseconds."""
+    """Median over `graphs` replays of a graph holding `reps` calls of fn, per call, in microseconds. Capture,
+    replays and events all run on `stream`."""
     g = torch.cuda.CUDAGraph()
+    ts = []
     with torch.cuda.stream(stream):
         fn()  # warm the path outside the capture
-        torch.cuda.synchronize()
+        stream.synchronize()
         with torch.cuda.graph(g, stream=stream):
             for i in range(reps):
                 fn(i)
-    ts = []
-    for _ in range(graphs):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
         g.replay()
-        e1.record(stream)
-        e1.synchronize()
-        ts.append(e0.elapsed_time(e1) * 1e3 / reps)
+        for _ in range(graphs):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3 / reps)
     return statistics.median(ts)
 
 
@@ -149,6 +157,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-configs", action="store_true", help="skip the single-layer configurations")
     ap.add_argument("--no-layers", action="store_true", help="skip the per-layer timing of the frame workload")
+    ap.add_argument("--no-autotune", action="store_true", help="plan with the heuristic only (no per-shape timing)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the conv path shards "
@@ -169,42 +178,46 @@ def main():
     pair = [L for L in layers if L.stage == "pair"]
     mid = [L for L in layers if L.stage == "mid"]
     log(f"bench: FlyHighFG conv layers at {net_w}x{net_h}: {len(pair)} pair + {len(mid)} mid")
-    net = Net(layers, 1, torch, np, fhconv)
+    net = Net(layers, 1, torch, np, fhconv, tune=not args.no_autotune)
+    log(f"bench: autotuned {len(net.tuned)} conv shapes")
     torch.cuda.synchronize()
 
-    gp, gm = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    # one graph per step (pair then mid: one launch per frame), and one per stage for the stage split
+    gs, gp, gm = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         net.run()
-        torch.cuda.synchronize()
+        stream.synchronize()
+        with torch.cuda.graph(gs, stream=stream):
+            net.run()
         with torch.cuda.graph(gp, stream=stream):
             net.run({L.name for L in pair})
         with torch.cuda.graph(gm, stream=stream):
             net.run({L.name for L in mid})
-    for _ in range(args.warmup):
-        gp.replay()
-        gm.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(args.steps):
-        gp.replay()
-        gm.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+        for _ in range(args.warmup):
+            gs.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(args.steps):
+            gs.replay()
+        e1.record(stream)
+        t_submit = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
     ev_ms = e0.elapsed_time(e1) / args.steps
-    log(f"bench: {ms_per_step * 1e3:.2f} us per pair+mid (wall), {ev_ms * 1e3:.2f} us (events)")
+    log(f"bench: {ms_per_step * 1e3:.2f} us per pair+mid (wall), {ev_ms * 1e3:.2f} us (events), "
+        f"{t_submit * 1e6 / args.steps:.2f} us to submit one replay")
 
-    # pair and mid separately (events on the replay stream)
     def stage_us(g, n=200):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(n):
-            g.replay()
-        b.record(stream)
-        b.synchronize()
+        with torch.cuda.stream(stream):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(n):
+                g.replay()
+            b.record(stream)
+            b.synchronize()
         return a.elapsed_time(b) * 1e3 / n
 
     pair_us, mid_us = stage_us(gp), stage_us(gm)
@@ -219,7 +232,7 @@ def main():
     if not args.no_configs:
         for c in (1, 2, 3):
             cl = flyhighfg.config_layers(c)
-            cnet = Net(cl, 100 + c, torch, np, fhconv)
+            cnet = Net(cl, 100 + c, torch, np, fhconv, tune=not args.no_autotune)
             for L in cl:
                 cfg_layers.append(dict(config=c, **layer_timing(torch, np, fhconv, cnet, L, args.reps,
                                                                 args.graphs, args.cold_mb << 20, stream)))
@@ -258,7 +271,9 @@ def main():
                     frame="1920x1080", network=f"{net_w}x{net_h}", conv_layers=len(layers), k=1,
                     parallelism="single GPU"),
         pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), event_ms_per_step=round(ev_ms, 6),
+        submit_us_per_step=round(t_submit * 1e6 / args.steps, 3),
         roofline=roofline, cpu_baseline=cpu, layers=per_layer, config_layers=cfg_layers,
+        tune_table=fhconv.format_tune().splitlines(),
     )
     print(json.dumps(out), flush=True)
     return 0

@@ -12,6 +12,7 @@
 
 #include "common.h"
 #include "conv_kernels.h"
+#include "direct_table.h"
 #include "fhc_conv.h"
 
 namespace fhc {
@@ -35,30 +36,50 @@ std::mutex g_tune_mu;
 std::map<TuneKey, uint32_t> g_tune;
 
 // ---- variant codes -------------------------------------------------------------------------------------------
-// code = tile configuration id (bits 0-4, 1..kNumCfg) | global split-K code (bits 5-6: 0 -> 1, 1 -> 2, 2 -> 4,
-// 3 -> 8 splits). Fits the reference table's u8 value (tune_cache.rs:82).
+// The code space of the choice table (a u8 like the reference table's value, tune_cache.rs:82):
+//   1..127   the chunked implicit-GEMM kernel: tile configuration id (bits 0-4, 1..kNumCfg) | global split-K code
+//            (bits 5-6: 0 -> 1, 1 -> 2, 2 -> 4, 3 -> 8 splits);
+//   128+i    the direct kernel's configuration i of direct_table.h (weights resident in VGPRs).
 constexpr uint32_t kSplitCodes[4] = {1, 2, 4, 8};
+constexpr uint32_t kDirectBase = 128;
+
+struct Variant {
+    int family;   // 0 chunked implicit GEMM, 1 direct
+    int cfg;      // chunked: tile configuration id; direct: index into kDirectCfgs
+    uint32_t ks;  // chunked: global split-K count
+};
+
 uint32_t make_code(int cfg, uint32_t ksplit) {
     uint32_t sc = 0;
     for (uint32_t i = 0; i < 4; i++)
         if (kSplitCodes[i] == ksplit) sc = i;
     return (uint32_t)cfg | (sc << 5);
 }
-bool decode_code(uint32_t code, int* cfg, uint32_t* ksplit) {
+bool decode_code(uint32_t code, Variant* v) {
+    if (code >= kDirectBase) {
+        if (code - kDirectBase >= (uint32_t)kNumDirect) return false;
+        *v = Variant{1, (int)(code - kDirectBase), 1};
+        return true;
+    }
     const int c = (int)(code & 31u);
-    if (c < 1 || c > kNumCfg || code > 127u) return false;
-    *cfg = c;
-    *ksplit = kSplitCodes[(code >> 5) & 3u];
+    if (c < 1 || c > kNumCfg) return false;
+    *v = Variant{0, c, kSplitCodes[(code >> 5) & 3u]};
     return true;
 }
 std::string code_name(uint32_t code) {
-    int cfg;
-    uint32_t ks;
-    if (!decode_code(code, &cfg, &ks)) return "";
-    const TileCfg& t = kTileCfgs[cfg];
+    Variant v;
+    if (!decode_code(code, &v)) return "";
     std::ostringstream o;
+    if (v.family == 1) {
+        const DirectCfg& c = kDirectCfgs[v.cfg];
+        o << "direct" << (c.ks == 1 ? ".k1" : c.stride == 2 ? ".s2" : "") << ".c" << c.cin32 << ".t" << c.fm * c.wm
+          << ".n" << 16 * c.wn;
+        if (c.wk > 1) o << "/rows";
+        return o.str();
+    }
+    const TileCfg& t = kTileCfgs[v.cfg];
     o << "igemm.t" << t.fm * t.wm << "x16.n" << t.fn * 16 * t.wn << ".w" << t.wm << "x" << t.wn << "x" << t.wk;
-    if (ks > 1) o << "/k" << ks;
+    if (v.ks > 1) o << "/k" << v.ks;
     return o.str();
 }
 
@@ -103,7 +124,9 @@ struct fhc_conv_plan {
     fhc_conv_desc d;
     Geometry g;
     uint32_t code;
-    int cfg;
+    int family;       // 0 chunked implicit GEMM, 1 direct
+    int cfg;          // chunked: tile configuration id; direct: index into kDirectCfgs
+    uint32_t tiles;   // spatial output tiles (all images)
     uint32_t ksplit;  // effective global split count (1 = none)
     ConvKArgs args;   // kernel arguments with the tensor pointers left null
     dim3 grid;
@@ -119,8 +142,86 @@ struct fhc_conv_plan {
 namespace fhc {
 namespace {
 
-// Fill the launch geometry of `p` for configuration `cfg` and global split `ks`; false if it does not fit.
-bool configure(fhc_conv_plan& p, int cfg, uint32_t ks, std::string* why) {
+void fill_args(fhc_conv_plan& p) {
+    const fhc_conv_desc& d = p.d;
+    ConvKArgs& a = p.args;
+    a = ConvKArgs{};
+    a.n = (int)d.n;
+    a.h = (int)d.h;
+    a.w = (int)d.w;
+    a.cin = (int)d.cin;
+    a.cout = (int)d.cout;
+    a.hout = (int)p.g.hout;
+    a.wout = (int)p.g.wout;
+    a.pad = (int)d.pad;
+    a.xcs = (int)d.x_cstride;
+    a.xc0 = (int)d.x_c0;
+    a.ycs = (int)d.y_cstride;
+    a.yc0 = (int)d.y_c0;
+    a.rcs = (int)d.r_cstride;
+    a.rc0 = (int)d.r_c0;
+    a.act = (int)d.act;
+    a.alpha = d.alpha;
+    a.residual = (int)d.residual;
+}
+
+// Whether the direct kernel's configuration `idx` serves this conv: same kernel size and stride, and the input
+// channels padded to 32 are exactly its channel count.
+bool direct_fits(const fhc_conv_desc& d, int idx) {
+    const DirectCfg& c = kDirectCfgs[idx];
+    return c.ks == (int)d.kh && c.stride == (int)d.stride && (uint32_t)c.cin32 == div_ceil(d.cin, 32) * 32;
+}
+
+// The direct kernel's launch geometry for configuration `idx`: input channels padded to 32 in one pass, weights
+// resident; one workgroup per spatial tile (grid x) and channel tile (grid y). False if it does not serve the conv.
+bool configure_direct(fhc_conv_plan& p, int idx, std::string* why) {
+    const fhc_conv_desc& d = p.d;
+    if (idx < 0 || idx >= kNumDirect || !direct_fits(d, idx)) {
+        *why = "the direct configuration does not serve " + std::to_string(d.kh) + "x" + std::to_string(d.kw) +
+               " stride " + std::to_string(d.stride) + " with " + std::to_string(d.cin) + " input channels";
+        return false;
+    }
+    const DirectCfg& c = kDirectCfgs[idx];
+    LaunchFn fn = direct_launcher(idx);
+    if (!fn) {
+        *why = "direct configuration not instantiated";
+        return false;
+    }
+    const int TH = c.fm * c.wm;
+    const uint32_t tiles_x = div_ceil(p.g.wout, 16), tiles_y = div_ceil(p.g.hout, TH);
+    const uint64_t tiles = (uint64_t)d.n * tiles_y * tiles_x;
+    const uint32_t ntn = div_ceil(d.cout, 16 * c.wn);
+    if (tiles > 0x7fffffffull || ntn > 65535) {
+        *why = "grid too large";
+        return false;
+    }
+    fill_args(p);
+    ConvKArgs& a = p.args;
+    a.cc = c.cin32;
+    a.nchunks = 1;
+    a.ksteps = (int)(p.g.taps * c.cin32 / 32);
+    a.tapgroups = (int)(p.g.taps * c.cin32 / 8);
+    a.tiles_x = (int)tiles_x;
+    a.tiles_y = (int)tiles_y;
+    a.ntn = (int)ntn;
+    a.chunks_per_split = 1;
+    a.np = (int)(ntn * 16 * c.wn);
+    p.family = 1;
+    p.cfg = idx;
+    p.tiles = (uint32_t)tiles;
+    p.ksplit = 1;
+    p.code = kDirectBase + (uint32_t)idx;
+    p.grid = dim3((unsigned)tiles, ntn, 1);
+    p.threads = 64u * c.wm * c.wn * c.wk;
+    p.lds = 0;
+    p.ws_bytes = 0;
+    p.launch = fn;
+    return true;
+}
+
+// Fill the launch geometry of `p` for the chunked kernel's configuration `cfg` and global split `ks`; false if it
+// does not fit.
+bool configure_igemm(fhc_conv_plan& p, int cfg, uint32_t ks, std::string* why) {
     const fhc_conv_desc& d = p.d;
     const TileCfg& t = kTileCfgs[cfg];
     const int KS = (int)d.kh, S = (int)d.stride;
@@ -168,25 +269,8 @@ bool configure(fhc_conv_plan& p, int cfg, uint32_t ks, std::string* why) {
         *why = "grid too large";
         return false;
     }
+    fill_args(p);
     ConvKArgs& a = p.args;
-    a = ConvKArgs{};
-    a.n = (int)d.n;
-    a.h = (int)d.h;
-    a.w = (int)d.w;
-    a.cin = (int)d.cin;
-    a.cout = (int)d.cout;
-    a.hout = (int)p.g.hout;
-    a.wout = (int)p.g.wout;
-    a.pad = (int)d.pad;
-    a.xcs = (int)d.x_cstride;
-    a.xc0 = (int)d.x_c0;
-    a.ycs = (int)d.y_cstride;
-    a.yc0 = (int)d.y_c0;
-    a.rcs = (int)d.r_cstride;
-    a.rc0 = (int)d.r_c0;
-    a.act = (int)d.act;
-    a.alpha = d.alpha;
-    a.residual = (int)d.residual;
     a.cc = (int)cc;
     a.nchunks = (int)nchunks;
     a.ksteps = (int)ksteps;
@@ -196,7 +280,9 @@ bool configure(fhc_conv_plan& p, int cfg, uint32_t ks, std::string* why) {
     a.ntn = (int)ntn;
     a.chunks_per_split = (int)cps;
     a.np = (int)(ntn * BN);
+    p.family = 0;
     p.cfg = cfg;
+    p.tiles = (uint32_t)(d.n * tiles_y * tiles_x);
     p.ksplit = zcount;
     p.code = make_code(cfg, zcount);
     p.grid = dim3((unsigned)blocks, zcount, 1);
@@ -207,9 +293,56 @@ bool configure(fhc_conv_plan& p, int cfg, uint32_t ks, std::string* why) {
     return true;
 }
 
-// The MI355X planner's default when neither the caller nor the table chose: the widest channel tile that
-// pads cout by at most a quarter, 8-row tiles (4 for stride 2 when the halo would not fit), and the 4-wave K split
-// for deep layers whose tile grid cannot fill the 256 CUs.
+int heuristic_cfg(const fhc_conv_desc& d, const Geometry& g);
+
+bool configure(fhc_conv_plan& p, const Variant& v, std::string* why) {
+    if (v.family == 1) {
+        if (v.ks > 1) {
+            *why = "the direct kernel has no split-K";
+            return false;
+        }
+        return configure_direct(p, v.cfg, why);
+    }
+    return configure_igemm(p, v.cfg, v.ks, why);
+}
+
+// The direct configuration the planner takes without a table entry, or -1: the narrowest channel tile that
+// covers cout in one tile (else the widest there is), and among the tile heights the tallest that still gives
+// about two workgroups per CU (the small layers of a frame take short tiles: more, shorter-running workgroups).
+int direct_default(const fhc_conv_desc& d, const Geometry& g) {
+    const int need = (int)div_ceil(d.cout, 16);
+    int best_wn = 0;
+    for (int i = 0; i < kNumDirect; i++) {
+        if (!direct_fits(d, i)) continue;
+        const int wn = kDirectCfgs[i].wn;
+        if (best_wn == 0 || (best_wn < need && wn > best_wn) || (wn >= need && wn < best_wn)) best_wn = wn;
+    }
+    if (best_wn == 0) return -1;
+    int pick = -1;
+    uint64_t pick_wgs = 0;
+    int pick_th = 0;
+    for (int i = 0; i < kNumDirect; i++) {
+        if (!direct_fits(d, i) || kDirectCfgs[i].wn != best_wn) continue;
+        const int th = kDirectCfgs[i].fm * kDirectCfgs[i].wm;
+        const uint64_t wgs = (uint64_t)d.n * div_ceil(g.hout, th) * div_ceil(g.wout, 16) * div_ceil(d.cout, 16 * best_wn);
+        const bool enough = wgs >= 512;
+        if (pick < 0 || (enough && (pick_wgs < 512 || th > pick_th)) || (!enough && pick_wgs < 512 && th < pick_th)) {
+            pick = i;
+            pick_wgs = wgs;
+            pick_th = th;
+        }
+    }
+    return pick;
+}
+
+// The MI355X planner's default when neither the caller nor the table chose: the direct kernel whenever a
+// configuration serves the input channels, else the chunked kernel.
+uint32_t heuristic_code(const fhc_conv_desc& d, const Geometry& g) {
+    const int idx = direct_default(d, g);
+    if (idx >= 0) return kDirectBase + (uint32_t)idx;
+    return (uint32_t)heuristic_cfg(d, g);
+}
+
 int heuristic_cfg(const fhc_conv_desc& d, const Geometry& g) {
     struct Opt {
         int bn, cfg8, cfg4;
@@ -229,12 +362,31 @@ int heuristic_cfg(const fhc_conv_desc& d, const Geometry& g) {
     return d.stride == 2 ? cfg4 : cfg8;
 }
 
+// Weights in MFMA A-fragment order, [nb16][chunk][kstep][lane][8]: lane l holds output channel nb*16 + l%16 and
+// the 8 K positions of its lane group l/16 in that K-step. K order per chunk: the chunked kernel walks 8-channel
+// groups j = 4*s + l/16 of k = tap * cc + ci; the direct kernel pads channels to 32 per tap, K-step s being tap
+// s / (cc/32), channels 32 * (s % (cc/32)) + 8 * (l/16) .. +7.
 void pack_weights(const fhc_conv_plan& p, const uint16_t* w, std::vector<uint16_t>& out) {
     const fhc_conv_desc& d = p.d;
     const ConvKArgs& a = p.args;
     const int nb16 = a.np / 16, gpt = a.cc / 8;
     out.assign((size_t)nb16 * a.nchunks * a.ksteps * 64 * 8, 0);
     size_t o = 0;
+    if (p.family == 1) {
+        const int m = a.cc / 32;
+        for (int nb = 0; nb < nb16; nb++)
+            for (int s = 0; s < a.ksteps; s++)
+                for (int l = 0; l < 64; l++)
+                    for (int i = 0; i < 8; i++, o++) {
+                        const int tap = s / m;
+                        const uint32_t ci = (uint32_t)((s % m) * 32 + (l >> 4) * 8 + i);
+                        const uint32_t co = (uint32_t)(nb * 16 + (l & 15));
+                        if (ci >= d.cin || co >= d.cout) continue;
+                        const uint32_t ky = (uint32_t)tap / d.kw, kx = (uint32_t)tap % d.kw;
+                        out[o] = w[(((size_t)co * d.cin + ci) * d.kh + ky) * d.kw + kx];
+                    }
+        return;
+    }
     for (int nb = 0; nb < nb16; nb++)
         for (int c = 0; c < a.nchunks; c++)
             for (int s = 0; s < a.ksteps; s++)
@@ -286,30 +438,40 @@ bool plan_choose(const fhc_conv_desc& d, fhc_conv_plan& p, std::string* why) {
     p.g.taps = d.kh * d.kw;
     p.g.cin8 = div_ceil(d.cin, 8) * 8;
     // the choice: forced variant, then the table, then the heuristic (conv_pick, autotune.rs:186-233)
-    int cfg = 0;
-    uint32_t ks = 1;
+    Variant v{};
     if (d.variant != 0) {
-        if (!decode_code(d.variant, &cfg, &ks)) {
+        if (!decode_code(d.variant, &v)) {
             *why = "unknown variant " + std::to_string(d.variant);
             return false;
         }
     } else {
         const int hit = fhc_tune_get(d.cin, d.cout, d.h, d.w, d.stride);
-        if (hit < 0 || !decode_code((uint32_t)hit, &cfg, &ks)) {
-            cfg = heuristic_cfg(d, p.g);
-            ks = 1;
-        }
+        if (hit < 0 || !decode_code((uint32_t)hit, &v)) decode_code(heuristic_code(d, p.g), &v);
     }
+    // a forced split (or the reference code's split nibble, candidates.rs:4) moves to the chunked kernel
+    uint32_t ks = 0;
     if (d.ksplit != 0)
         ks = d.ksplit;
-    else if (d.ref_cand != 0xFFu && d.ref_cand != 0 && (d.ref_cand >> 4) != 0 && d.variant == 0) {
-        const uint32_t rk = d.ref_cand >> 4;  // candidates.rs:4: forced split-K 1 / 2 / 4
+    else if (d.ref_cand != 0xFFu && (d.ref_cand >> 4) != 0 && d.variant == 0) {
+        const uint32_t rk = d.ref_cand >> 4;
         if (rk == 1 || rk == 2 || rk == 4) ks = rk;
     }
-    if (!configure(p, cfg, ks, why)) {
-        // a table entry or heuristic that does not fit this shape falls back to the 4-row tile
-        if (d.variant != 0 || !configure(p, d.cout <= 32 ? 5 : 4, ks, why)) {
-            *why += " (variant " + code_name(make_code(cfg, ks)) + ")";
+    if (ks != 0 && !(v.family == 1 && ks == 1)) {
+        if (v.family == 1) {
+            if (d.variant != 0) {
+                *why = "the direct kernel has no split-K";
+                return false;
+            }
+            v = Variant{0, heuristic_cfg(d, p.g), ks};
+        } else {
+            v.ks = ks;
+        }
+    }
+    if (!configure(p, v, why)) {
+        // a table entry or heuristic that does not fit this shape falls back to the chunked 4-row tile
+        const uint32_t code = v.family == 1 ? kDirectBase + (uint32_t)v.cfg : make_code(v.cfg, v.ks);
+        if (d.variant != 0 || !configure(p, Variant{0, d.cout <= 32 ? 5 : 4, v.family == 1 ? 1u : v.ks}, why)) {
+            *why += " (variant " + code_name(code) + ")";
             return false;
         }
     }
@@ -318,21 +480,36 @@ bool plan_choose(const fhc_conv_desc& d, fhc_conv_plan& p, std::string* why) {
 
 std::string describe_json(const fhc_conv_plan* p) {
     const fhc_conv_desc& d = p->d;
-    const TileCfg& t = kTileCfgs[p->cfg];
+    int rows, chans, wm, wnv, wk;
+    if (p->family == 1) {
+        const DirectCfg& c = kDirectCfgs[p->cfg];
+        rows = c.fm * c.wm;
+        chans = 16 * c.wn;
+        wm = c.wm;
+        wnv = c.wn;
+        wk = c.wk;
+    } else {
+        const TileCfg& t = kTileCfgs[p->cfg];
+        rows = t.fm * t.wm;
+        chans = t.fn * 16 * t.wn;
+        wm = t.wm;
+        wnv = t.wn;
+        wk = t.wk;
+    }
     const double flops = 2.0 * d.n * p->g.hout * p->g.wout * d.cout * d.cin * d.kh * d.kw;
     const double out_el = (double)d.n * p->g.hout * p->g.wout * d.cout;
     const double bytes = 2.0 * ((double)d.n * d.h * d.w * d.cin + out_el + (double)d.cout * d.cin * d.kh * d.kw +
                                 d.cout + (d.act == FHC_ACT_PRELU ? d.cout : 0) + (d.residual ? out_el : 0));
     const size_t packed = (size_t)(p->args.np / 16) * p->args.nchunks * p->args.ksteps * 64 * 16;
-    char b[1024];
+    char b[1200];
     snprintf(b, sizeof b,
-             "{\"variant\":%u,\"name\":\"%s\",\"cfg\":%d,\"tile_rows\":%d,\"tile_cols\":16,\"tile_channels\":%d,"
-             "\"waves\":[%d,%d,%d],\"ksplit\":%u,\"cc\":%d,\"nchunks\":%d,\"ksteps\":%d,\"grid\":[%u,%u],"
-             "\"threads\":%u,\"lds\":%zu,\"packed_weight_bytes\":%zu,\"workspace_bytes\":%zu,\"hout\":%u,"
-             "\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
-             p->code, code_name(p->code).c_str(), p->cfg, t.fm * t.wm, t.fn * 16 * t.wn, t.wm, t.wn, t.wk, p->ksplit,
-             p->args.cc, p->args.nchunks, p->args.ksteps, p->grid.x, p->grid.y, p->threads, p->lds, packed,
-             p->ws_bytes, p->g.hout, p->g.wout, flops, bytes);
+             "{\"variant\":%u,\"name\":\"%s\",\"family\":\"%s\",\"cfg\":%d,\"tile_rows\":%d,\"tile_cols\":16,"
+             "\"tile_channels\":%d,\"waves\":[%d,%d,%d],\"ksplit\":%u,\"cc\":%d,\"nchunks\":%d,\"ksteps\":%d,"
+             "\"tiles\":%u,\"ntn\":%d,\"grid\":[%u,%u],\"threads\":%u,\"lds\":%zu,\"packed_weight_bytes\":%zu,"
+             "\"workspace_bytes\":%zu,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
+             p->code, code_name(p->code).c_str(), p->family == 1 ? "direct" : "igemm", p->cfg, rows, chans, wm, wnv,
+             wk, p->ksplit, p->args.cc, p->args.nchunks, p->args.ksteps, p->tiles, p->args.ntn, p->grid.x, p->grid.y,
+             p->threads, p->lds, packed, p->ws_bytes, p->g.hout, p->g.wout, flops, bytes);
     return b;
 }
 
@@ -543,15 +720,22 @@ extern "C" int fhc_variant_list(const fhc_conv_desc* desc, uint32_t* codes, size
         p.g.wout = (d.w + 2 * d.pad - d.kw) / d.stride + 1;
         p.g.taps = d.kh * d.kw;
         p.g.cin8 = div_ceil(d.cin, 8) * 8;
-        // every configuration that fits, without split; with global splits where the tile grid is small
-        // (the counterpart of cand_list's split-K variants, candidates.rs:52-57)
+        // the direct kernel at every channel-tile width that is instantiated for this input and not mostly padding;
+        // every chunked configuration that fits, without split, and with global splits where the tile grid is
+        // small (the counterpart of cand_list's split-K variants, candidates.rs:52-57)
         std::vector<uint32_t> out;
+        for (int i = 0; i < kNumDirect; i++) {
+            if (!direct_fits(d, i)) continue;
+            const int wn = kDirectCfgs[i].wn;
+            if (16u * wn >= 2 * div_ceil(d.cout, 16) * 16 && wn > 1) continue;
+            if (configure_direct(p, i, &why)) out.push_back(p.code);
+        }
         for (int cfg = 1; cfg <= kNumCfg; cfg++) {
             const TileCfg& t = kTileCfgs[cfg];
             const uint32_t bn = (uint32_t)(t.fn * 16 * t.wn);
             if (bn >= 2 * div_ceil(d.cout, 16) * 16 && bn > 16) continue;  // mostly padding
             for (uint32_t ks : {1u, 2u, 4u, 8u}) {
-                if (!configure(p, cfg, ks, &why)) continue;
+                if (!configure_igemm(p, cfg, ks, &why)) continue;
                 if (p.ksplit != ks) continue;
                 if (ks > 1 && p.grid.x >= 512) continue;
                 out.push_back(p.code);
@@ -561,6 +745,80 @@ extern "C" int fhc_variant_list(const fhc_conv_desc* desc, uint32_t* codes, size
         if (out.size() > cap) return fail(-1, "fhc_variant_list: %zu variants do not fit in %zu", out.size(), cap);
         for (size_t i = 0; i < out.size(); i++) codes[i] = out[i];
         return (int)out.size();
+    });
+}
+
+extern "C" int fhc_conv_autotune(const fhc_conv_desc* desc, const uint16_t* w_oihw, const uint16_t* bias,
+                                 const uint16_t* slope, const void* x, void* y, const void* res, int reps,
+                                 float* best_us) {
+    return guard(-1, [&]() -> int {
+        if (!desc || !w_oihw || !bias || !x || !y) return fail(-1, "fhc_conv_autotune: NULL argument");
+        if (desc->residual && !res) return fail(-1, "fhc_conv_autotune: the conv has a residual but res is NULL");
+        if (reps < 1 || reps > 10000) return fail(-1, "fhc_conv_autotune: reps must be in 1..10000");
+        std::vector<uint32_t> codes(256);
+        const int n = fhc_variant_list(desc, codes.data(), codes.size());
+        if (n < 0) return -1;
+        hipStream_t s = nullptr;
+        if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess)
+            return fail(-1, "fhc_conv_autotune: stream creation failed");
+        hipEvent_t e0 = nullptr, e1 = nullptr;
+        (void)hipEventCreate(&e0);
+        (void)hipEventCreate(&e1);
+        float best = 0.0f;
+        int best_code = -1;
+        std::string err;
+        for (int i = 0; i < n && err.empty(); i++) {
+            fhc_conv_desc d = *desc;
+            d.variant = codes[i];
+            d.ksplit = 0;
+            d.ref_cand = 0xFF;
+            fhc_conv_plan* p = nullptr;
+            if (fhc_conv_plan_create(&d, w_oihw, bias, slope, &p) != 0) continue;  // not servable: skip
+            void* ws = nullptr;
+            if (p->ws_bytes && hipMalloc(&ws, p->ws_bytes) != hipSuccess) {
+                fhc_conv_plan_destroy(p);
+                continue;
+            }
+            hipGraph_t g = nullptr;
+            hipGraphExec_t ge = nullptr;
+            bool ok = fhc_conv_run(p, x, y, res, ws, s) == 0 && hipStreamSynchronize(s) == hipSuccess;
+            ok = ok && hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) == hipSuccess;
+            if (ok) {
+                for (int r = 0; r < reps && ok; r++) ok = fhc_conv_run(p, x, y, res, ws, s) == 0;
+                ok = hipStreamEndCapture(s, &g) == hipSuccess && ok;
+            }
+            ok = ok && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess;
+            ok = ok && hipGraphLaunch(ge, s) == hipSuccess;  // warm
+            float ms = 0.0f;
+            ok = ok && hipEventRecord(e0, s) == hipSuccess && hipGraphLaunch(ge, s) == hipSuccess &&
+                 hipEventRecord(e1, s) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+                 hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+            if (ge) (void)hipGraphExecDestroy(ge);
+            if (g) (void)hipGraphDestroy(g);
+            if (ws) (void)hipFree(ws);
+            fhc_conv_plan_destroy(p);
+            if (!ok) {
+                err = std::string("timing variant ") + code_name(codes[i]) + " failed: " + fhc_last_error();
+                break;
+            }
+            const float us = ms * 1000.0f / (float)reps;
+            if (best_code < 0 || us < best) {
+                best = us;
+                best_code = (int)codes[i];
+            }
+        }
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+        (void)hipStreamDestroy(s);
+        if (!err.empty()) return fail(-1, "fhc_conv_autotune: %s", err.c_str());
+        if (best_code < 0) return fail(-1, "fhc_conv_autotune: no variant could be planned");
+        {
+            std::lock_guard<std::mutex> lk(g_tune_mu);
+            g_tune[TuneKey(desc->cin, desc->cout, desc->h, desc->w, desc->stride)] = (uint32_t)best_code;
+        }
+        if (best_us) *best_us = best;
+        clear_error();
+        return best_code;
     });
 }
 

@@ -19,15 +19,9 @@
 // Split-K: WK > 1 waves of one workgroup take interleaved K-steps of the same tile and are summed through LDS
 // before the epilogue; a global split (grid.y = z) instead writes f32 partials that splitk_reduce sums in z order.
 #include "conv_kernels.h"
+#include "direct_impl.h"
 
 namespace fhc {
-
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-
-__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
 // bias, activation, f16 round, residual (rounded again), store: 4 consecutive channels co..co+3 of pixel `pix`.
 // The order is the reference's epilogue (shaders/conv_tiled.wgsl:57-67; splitk_reduce.wgsl:21-23).

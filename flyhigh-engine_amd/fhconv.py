@@ -79,6 +79,8 @@ def load():
         "fhc_ref_cand_name": ([ctypes.c_uint8, ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_ref_conv_steps": ([ctypes.POINTER(RefConv), ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_probe_mfma_layout": ([P, P, P, P], ctypes.c_int),
+        "fhc_conv_autotune": ([ctypes.POINTER(ConvDesc), P, P, P, P, P, P, ctypes.c_int,
+                               ctypes.POINTER(ctypes.c_float)], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -99,11 +101,14 @@ def _check(rc, what):
 
 
 def _ptr(t):
-    """Device pointer of a torch tensor (or an int), None for None."""
+    """Device pointer of a torch tensor (or an int), None for None. The ABI reads dense NHWC buffers whose layout
+    the descriptor states, so a torch tensor must be contiguous."""
     if t is None:
         return None
     if isinstance(t, int):
         return t
+    if not t.is_contiguous():
+        raise FhcError("tensors passed to the conv must be contiguous (NHWC with the descriptor's strides)")
     return t.data_ptr()
 
 
@@ -235,6 +240,18 @@ def plan_dry(desc: ConvDesc) -> dict:
     buf = ctypes.create_string_buffer(2048)
     _check(load().fhc_conv_plan_dry(ctypes.byref(desc), buf, len(buf)), "fhc_conv_plan_dry")
     return json.loads(buf.value.decode())
+
+
+def autotune(desc: ConvDesc, w_oihw, bias, slope, x, y, res=None, reps: int = 20):
+    """Time every variant for `desc` on these device buffers, record the fastest in the choice table; returns
+    (code, microseconds per launch). The per-shape autotune of conv_pick (ops/conv/autotune.rs:199-230)."""
+    _, wp = _host_u16(w_oihw)
+    _, bp = _host_u16(bias)
+    _, sp = _host_u16(slope)
+    us = ctypes.c_float()
+    code = _check(load().fhc_conv_autotune(ctypes.byref(desc), wp, bp, sp, _ptr(x), _ptr(y), _ptr(res), reps,
+                                           ctypes.byref(us)), "fhc_conv_autotune")
+    return code, us.value
 
 
 # ---- the reference planner restated, and the choice table ----------------------------------------------------

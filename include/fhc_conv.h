@@ -92,6 +92,15 @@ void fhc_conv_plan_destroy(fhc_conv_plan* plan);
  * (the reference's FH_TUNE_VERBOSE listing, ops/conv/autotune.rs:217-228). Bytes written or -1. */
 int fhc_conv_plan_dry(const fhc_conv_desc* desc, char* json, size_t cap);
 
+/* Time every variant fhc_variant_list gives for `desc` on the caller's device buffers (x, y, res: as for
+ * fhc_conv_run; y is overwritten) with `reps` back-to-back launches captured in a HIP graph on a private stream,
+ * record the fastest in the choice table under the descriptor's key, and return its code (or -1). *best_us
+ * receives its time per launch when not NULL. The per-shape autotune of the reference's conv_pick
+ * (ops/conv/autotune.rs:199-230): a blocking round trip per candidate, for plan time only. The host weights are
+ * those of fhc_conv_plan_create. */
+int fhc_conv_autotune(const fhc_conv_desc* desc, const uint16_t* w_oihw, const uint16_t* bias,
+                      const uint16_t* slope, const void* x, void* y, const void* res, int reps, float* best_us);
+
 /* ---- The planner's choice table ------------------------------------------------------------------------
  * Same key and text format as the reference's TuneTable (ops/conv/tune_cache.rs:6-9, :39-64): one
  * "cin,cout,h,w,stride=code" per line, h and w the INPUT size; malformed lines are skipped. The codes are

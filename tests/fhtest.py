@@ -36,7 +36,7 @@ def as_f64(u):
 
 
 def f16_bits(a):
-    return np.asarray(a, dtype=np.float64).astype(np.float16).view(np.uint16)
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float64).astype(np.float16).view(np.uint16))
 
 
 class Case:
@@ -92,9 +92,10 @@ class Case:
         if plan is None:
             plan = fhconv.ConvPlan(self.fhc_desc(variant, ksplit, ref_cand), self.wt, self.bias,
                                    self.slope if self.act == 1 else None)
-        x = torch.from_numpy(self.x.view(np.int16)).to(dev)
-        y = torch.from_numpy(self.y0.view(np.int16)).to(dev)
-        r = torch.from_numpy(self.res.view(np.int16)).to(dev) if self.residual else None
+        host = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16))  # noqa: E731
+        x = host(self.x).to(dev)
+        y = host(self.y0).to(dev)
+        r = host(self.res).to(dev) if self.residual else None
         ws = torch.empty(plan.workspace_bytes // 2 + 8, dtype=torch.int16, device=dev) \
             if plan.workspace_bytes else None
         plan.run(x, y, r, ws)

@@ -87,7 +87,7 @@ def test_planner_choice_matches_the_oracle(shape):
     assert ok, (md, mref)
 
 
-VARIANT_SHAPES = [(1, 20, 37, 40, 72, 3, 1), (1, 19, 35, 24, 40, 3, 2), (1, 18, 33, 48, 40, 1, 1),
+VARIANT_SHAPES = [(1, 20, 37, 40, 72, 3, 1), (1, 19, 35, 24, 40, 3, 2), (1, 18, 33, 48, 40, 1, 1), (1, 9, 21, 279, 40, 3, 1),
                   (1, 12, 20, 130, 100, 3, 1)]
 
 
@@ -222,3 +222,23 @@ def test_plan_lifecycle_and_describe():
     p = fhconv.ConvPlan(c.fhc_desc(), c.wt, c.bias, c.slope)
     with pytest.raises(fhconv.FhcError):
         p.run(None, None)
+
+
+def test_autotune_picks_a_listed_variant_and_records_it():
+    import torch
+    fhconv.tune_clear()
+    try:
+        c = Case(1, 40, 70, 48, 48, act=1, residual=True, seed=17)
+        d = c.fhc_desc()
+        host = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda()  # noqa: E731
+        x, y, r = host(c.x), host(c.y0), host(c.res)
+        code, us = fhconv.autotune(d, c.wt, c.bias, c.slope, x, y, r, reps=5)
+        say("autotune", fhconv.variant_name(code), us)
+        assert code in fhconv.variant_list(d) and us > 0
+        assert fhconv.tune_get(48, 48, 40, 70, 1) == code
+        got, plan = c.run_gpu(return_plan=True)
+        assert plan.describe()["variant"] == code
+        ok, md, mref = parity(got, c.run_oracle())
+        assert ok, (md, mref)
+    finally:
+        fhconv.tune_clear()

@@ -115,15 +115,34 @@ SHAPES = [
 ]
 
 
+def test_direct_kernel_where_the_channels_fit():
+    # small-channel layers go to the direct kernel (weights resident), deep ones to the chunked kernel
+    assert fhconv.plan_dry(fhconv.make_desc(1, 136, 240, 32, 32))["family"] == "direct"
+    assert fhconv.plan_dry(fhconv.make_desc(1, 544, 960, 32, 64, stride=2))["family"] == "direct"
+    assert fhconv.plan_dry(fhconv.make_desc(1, 68, 120, 128, 64, k=1))["family"] == "direct"
+    deep = fhconv.plan_dry(fhconv.make_desc(1, 30, 54, 279, 96))  # one kernel row of K per wave
+    assert deep["family"] == "direct" and deep["cc"] == 288 and deep["waves"][2] == 3
+    assert fhconv.plan_dry(fhconv.make_desc(1, 60, 108, 72, 36, stride=2))["family"] == "igemm"
+    assert fhconv.plan_dry(fhconv.make_desc(1, 30, 54, 300, 96))["family"] == "igemm"
+    d = fhconv.plan_dry(fhconv.make_desc(1, 60, 108, 36, 36))
+    assert d["family"] == "direct" and d["cc"] == 64 and d["tile_channels"] == 48 and d["ntn"] == 1
+
+
 @pytest.mark.parametrize("shape", SHAPES)
 def test_mi355x_plan_covers_the_output(shape):
     n, h, w, cin, cout, k, s = shape
     p = fhconv.plan_dry(fhconv.make_desc(n, h, w, cin, cout, k=k, stride=s))
     assert p["hout"] == (h + 2 * (k == 3) - k) // s + 1 and p["wout"] == (w + 2 * (k == 3) - k) // s + 1
-    tiles = -(-p["hout"] // p["tile_rows"]) * -(-p["wout"] // 16) * -(-cout // p["tile_channels"]) * n
-    assert p["grid"][0] == tiles
+    tiles = -(-p["hout"] // p["tile_rows"]) * -(-p["wout"] // 16) * n
+    assert p["tiles"] == tiles
+    assert p["ntn"] * p["tile_channels"] >= cout > (p["ntn"] - 1) * p["tile_channels"]
     assert p["cc"] % 8 == 0 and p["cc"] * p["nchunks"] >= cin and p["cc"] * (p["nchunks"] - 1) < cin
-    assert p["ksteps"] * 32 >= k * k * p["cc"]
+    if p["family"] == "igemm":
+        assert p["grid"][0] == tiles * p["ntn"]
+        assert p["ksteps"] * 32 >= k * k * p["cc"]
+    else:
+        assert p["grid"] == [tiles, p["ntn"]]
+        assert p["cc"] % 32 == 0 and p["ksteps"] * 32 == k * k * p["cc"] and p["nchunks"] == 1
     assert p["lds"] <= 64 * 1024
     assert p["flops"] == 2 * n * p["hout"] * p["wout"] * cout * cin * k * k
     name = fhconv.variant_name(p["variant"])
@@ -137,7 +156,7 @@ def test_variant_list_and_forced_variants():
     for code in codes:
         p = fhconv.plan_dry(fhconv.make_desc(1, 68, 120, 128, 128, variant=code))
         assert p["variant"] == code
-    split = [c for c in codes if c >> 5]
+    split = [c for c in codes if c < 128 and c >> 5]
     assert split, "a 68x120 layer has a small tile grid: split-K variants are listed"
     with pytest.raises(fhconv.FhcError):
         fhconv.plan_dry(fhconv.make_desc(1, 68, 120, 128, 128, variant=31))
