@@ -52,18 +52,18 @@ class Net:
             wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
             b = f16(rng.normal(0, 0.01, L.cout))
             s = f16(rng.uniform(0.05, 0.3, L.cout)) if L.act == 1 else None
-            d = fhconv.make_desc(1, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
+            d = fhconv.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
                                  residual=L.residual)
             x = self.bufs[L.chain][1] if L.chain else \
-                f16(rng.uniform(-1, 1, (1, L.h, L.w, L.cin))).to(dev)
-            y = torch.zeros((1, L.hout, L.wout, L.cout), dtype=torch.float16, device=dev)
+                f16(rng.uniform(-1, 1, (L.n, L.h, L.w, L.cin))).to(dev)
+            y = torch.zeros((L.n, L.hout, L.wout, L.cout), dtype=torch.float16, device=dev)
             if L.residual:
                 r = self.bufs[L.res_from][1] if L.res_from else \
-                    f16(rng.uniform(-1, 1, (1, L.hout, L.wout, L.cout))).to(dev)
+                    f16(rng.uniform(-1, 1, (L.n, L.hout, L.wout, L.cout))).to(dev)
             else:
                 r = None
             if tune:
-                key = (L.cin, L.cout, L.h, L.w, L.stride, L.k)
+                key = (L.n, L.cin, L.cout, L.h, L.w, L.stride, L.k)
                 if key not in self.tuned:
                     code, us = fhconv.autotune(d, wt, b, s, x, y, r, reps=20)
                     self.tuned[key] = (fhconv.variant_name(code), round(us, 3))
@@ -133,12 +133,12 @@ def cpu_baseline(np, layers, threads):
     f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).view(np.uint16)  # noqa: E731
     total = 0.0
     for L in layers:
-        x = f16(rng.uniform(-1, 1, (1, L.h, L.w, L.cin)))
+        x = f16(rng.uniform(-1, 1, (L.n, L.h, L.w, L.cin)))
         wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
         b = f16(rng.normal(0, 0.01, L.cout))
         s = f16(rng.uniform(0.05, 0.3, L.cout))
-        r = f16(rng.uniform(-1, 1, (1, L.hout, L.wout, L.cout)))
-        d = oracle.make_desc(1, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
+        r = f16(rng.uniform(-1, 1, (L.n, L.hout, L.wout, L.cout)))
+        d = oracle.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
                              residual=L.residual)
         t0 = time.perf_counter()
         oracle.conv(d, x, wt, b, s, r, threads=threads)
@@ -177,7 +177,8 @@ def main():
     layers = flyhighfg.flyhighfg_layers(net_w, net_h, k=1)
     pair = [L for L in layers if L.stage == "pair"]
     mid = [L for L in layers if L.stage == "mid"]
-    log(f"bench: FlyHighFG conv layers at {net_w}x{net_h}: {len(pair)} pair + {len(mid)} mid")
+    log(f"bench: FlyHighFG conv layers at {net_w}x{net_h}: {len(pair)} pair + {len(mid)} mid launches "
+        f"(the two encoders batched)")
     net = Net(layers, 1, torch, np, fhconv, tune=not args.no_autotune)
     log(f"bench: autotuned {len(net.tuned)} conv shapes")
     torch.cuda.synchronize()
@@ -257,7 +258,7 @@ def main():
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         secs = cpu_baseline(np, layers, threads)
         cpu = dict(value=round(1.0 / secs, 4), unit="frames/s", cores=threads, kind="port",
-                   sample=f"all {len(layers)} conv layers of one pair()+mid() at {net_w}x{net_h} once through the "
+                   sample=f"all 25 conv layers of one pair()+mid() at {net_w}x{net_h} once through the "
                           "C oracle (restatement of the reference WGSL conv arithmetic), not lavapipe",
                    seconds=round(secs, 3))
         log(f"bench: CPU baseline {secs:.3f} s per pair+mid on {threads} threads")
@@ -267,9 +268,9 @@ def main():
         warmup=args.warmup, ms_per_step=round(ms_per_step, 6), higher_is_better=True, scaling="weak",
         vs_baseline=None, dtype="f16", data="synthetic",
         config=dict(workload="FlyHighFG conv layers of one pair()+mid() at 1080p (network 856x480 padded to "
-                             "864x480), batch 1, NHWC f16, conv-only",
-                    frame="1920x1080", network=f"{net_w}x{net_h}", conv_layers=len(layers), k=1,
-                    parallelism="single GPU"),
+                             "864x480), NHWC f16, conv-only; the A/B encoders run as batch-2 convs",
+                    frame="1920x1080", network=f"{net_w}x{net_h}", conv_layers=25,
+                    conv_launches=len(layers), k=1, parallelism="single GPU"),
         pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), event_ms_per_step=round(ev_ms, 6),
         submit_us_per_step=round(t_submit * 1e6 / args.steps, 3),
         roofline=roofline, cpu_baseline=cpu, layers=per_layer, config_layers=cfg_layers,

@@ -29,6 +29,7 @@ class ConvLayer:
     act: int = 1          # 1 PReLU (graph op conv), 0 identity (conv2d), 2 LeakyReLU(alpha)
     alpha: float = 0.0
     residual: bool = False
+    n: int = 1            # batch: images this conv runs on (the A and B encoders share their weights)
     chain: Optional[str] = None  # the conv whose output is this conv's input (None: a non-conv op feeds it)
     res_from: Optional[str] = None  # the conv whose output is the fused residual (None: another op's output)
     weight: str = ""      # weight tensor name in the model manifest
@@ -45,13 +46,13 @@ class ConvLayer:
 
     @property
     def flops(self):
-        return 2 * self.hout * self.wout * self.cout * self.cin * self.k * self.k
+        return 2 * self.n * self.hout * self.wout * self.cout * self.cin * self.k * self.k
 
     @property
     def bytes(self):
         """Algorithmic bytes: f16 input + output + weights + bias + slope (+ residual), each touched once."""
-        out = self.hout * self.wout * self.cout
-        return 2 * (self.h * self.w * self.cin + out + self.cout * self.cin * self.k * self.k + self.cout
+        out = self.n * self.hout * self.wout * self.cout
+        return 2 * (self.n * self.h * self.w * self.cin + out + self.cout * self.cin * self.k * self.k + self.cout
                     + (self.cout if self.act == 1 else 0) + (out if self.residual else 0))
 
 
@@ -70,19 +71,23 @@ def pad32(v: int) -> int:
     return (v + 31) // 32 * 32
 
 
-def flyhighfg_layers(net_w: int = 864, net_h: int = 480, k: int = 1) -> List[ConvLayer]:
-    """Conv layers of one pair() and one mid() at a padded network size (default: 1080p's 856x480 -> 864x480)."""
+def flyhighfg_layers(net_w: int = 864, net_h: int = 480, k: int = 1, batch_encoders: bool = True) -> List[ConvLayer]:
+    """Conv layers of one pair() and one mid() at a padded network size (default: 1080p's 856x480 -> 864x480).
+    batch_encoders: the A and B encoders (the same weights on the two frames, models/graph.json enc.* ops) run as
+    one batch-2 conv per layer instead of two convs; the work is the same."""
     qw, qh = net_w // 4, net_h // 4
     e8w, e8h = (qw + 2 - 3) // 2 + 1, (qh + 2 - 3) // 2 + 1
     e16w, e16h = (e8w + 2 - 3) // 2 + 1, (e8h + 2 - 3) // 2 + 1
     L = []
-    for side in ("a", "b"):
+    for side in (("ab",) if batch_encoders else ("a", "b")):
+        n = 2 if side == "ab" else 1
         L += [
-            ConvLayer(f"enc.e1.{side}", "pair", 3, 36, qh, qw, 2, weight="enc.e1.0.weight"),
-            ConvLayer(f"enc.e2.{side}", "pair", 36, 36, e8h, e8w, residual=True, chain=f"enc.e1.{side}",
+            ConvLayer(f"enc.e1.{side}", "pair", 3, 36, qh, qw, 2, n=n, weight="enc.e1.0.weight"),
+            ConvLayer(f"enc.e2.{side}", "pair", 36, 36, e8h, e8w, residual=True, n=n, chain=f"enc.e1.{side}",
                       res_from=f"enc.e1.{side}", weight="enc.e2.0.weight"),
-            ConvLayer(f"enc.e3.{side}", "pair", 36, 72, e8h, e8w, 2, chain=f"enc.e2.{side}", weight="enc.e3.0.weight"),
-            ConvLayer(f"enc.e4.{side}", "pair", 72, 72, e16h, e16w, residual=True, chain=f"enc.e3.{side}",
+            ConvLayer(f"enc.e3.{side}", "pair", 36, 72, e8h, e8w, 2, n=n, chain=f"enc.e2.{side}",
+                      weight="enc.e3.0.weight"),
+            ConvLayer(f"enc.e4.{side}", "pair", 72, 72, e16h, e16w, residual=True, n=n, chain=f"enc.e3.{side}",
                       res_from=f"enc.e3.{side}", weight="enc.e4.0.weight"),
         ]
     L += [
