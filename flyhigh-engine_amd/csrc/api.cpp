@@ -72,9 +72,11 @@ std::string code_name(uint32_t code) {
     std::ostringstream o;
     if (v.family == 1) {
         const DirectCfg& c = kDirectCfgs[v.cfg];
-        o << "direct" << (c.ks == 1 ? ".k1" : c.stride == 2 ? ".s2" : "") << ".c" << c.cin32 << ".t" << c.fm * c.wm
-          << ".n" << 16 * c.wn;
+        o << "direct" << (c.ks == 1 ? ".k1" : c.stride == 2 ? ".s2" : "") << ".c" << c.cin32 << ".t" << c.fm << "x"
+          << c.wm << ".n" << 16 * c.na * c.wn;
+        if (c.na > 1) o << ".a" << c.na;
         if (c.wk > 1) o << "/rows";
+        if (c.persist) o << "/p";
         return o.str();
     }
     const TileCfg& t = kTileCfgs[v.cfg];
@@ -182,7 +184,7 @@ bool configure_direct(fhc_conv_plan& p, int idx, std::string* why) {
         return false;
     }
     const DirectCfg& c = kDirectCfgs[idx];
-    LaunchFn fn = direct_launcher(idx);
+    LaunchFn fn = direct_launcher(idx, nullptr);
     if (!fn) {
         *why = "direct configuration not instantiated";
         return false;
@@ -190,7 +192,7 @@ bool configure_direct(fhc_conv_plan& p, int idx, std::string* why) {
     const int TH = c.fm * c.wm;
     const uint32_t tiles_x = div_ceil(p.g.wout, 16), tiles_y = div_ceil(p.g.hout, TH);
     const uint64_t tiles = (uint64_t)d.n * tiles_y * tiles_x;
-    const uint32_t ntn = div_ceil(d.cout, 16 * c.wn);
+    const uint32_t ntn = div_ceil(d.cout, 16 * c.na * c.wn);
     if (tiles > 0x7fffffffull || ntn > 65535) {
         *why = "grid too large";
         return false;
@@ -205,13 +207,15 @@ bool configure_direct(fhc_conv_plan& p, int idx, std::string* why) {
     a.tiles_y = (int)tiles_y;
     a.ntn = (int)ntn;
     a.chunks_per_split = 1;
-    a.np = (int)(ntn * 16 * c.wn);
+    a.np = (int)(ntn * 16 * c.na * c.wn);
     p.family = 1;
     p.cfg = idx;
     p.tiles = (uint32_t)tiles;
     p.ksplit = 1;
     p.code = kDirectBase + (uint32_t)idx;
-    p.grid = dim3((unsigned)tiles, ntn, 1);
+    // a persistent configuration gets no more workgroups than fit at once (set from the device at plan creation;
+    // a dry plan assumes one per CU of an MI355X)
+    p.grid = dim3(c.persist ? (unsigned)std::min<uint64_t>(tiles, std::max(1u, 256u / ntn)) : (unsigned)tiles, ntn, 1);
     p.threads = 64u * c.wm * c.wn * c.wk;
     p.lds = 0;
     p.ws_bytes = 0;
@@ -306,14 +310,15 @@ bool configure(fhc_conv_plan& p, const Variant& v, std::string* why) {
     return configure_igemm(p, v.cfg, v.ks, why);
 }
 
-// The direct configuration the planner takes without a table entry, or -1: the narrowest channel tile that
-// covers cout in one tile (else the widest there is), and among the tile heights the tallest that still gives
-// about two workgroups per CU (the small layers of a frame take short tiles: more, shorter-running workgroups).
+// The direct configuration the planner takes without a table entry, or -1: among the one-block-per-wave
+// configurations that launch one workgroup per tile, the narrowest channel tile that covers cout in one tile (else
+// the widest there is), and among the tile heights the tallest that still gives about two workgroups per CU (the
+// small layers of a frame take short tiles: more, shorter-running workgroups).
 int direct_default(const fhc_conv_desc& d, const Geometry& g) {
     const int need = (int)div_ceil(d.cout, 16);
     int best_wn = 0;
     for (int i = 0; i < kNumDirect; i++) {
-        if (!direct_fits(d, i)) continue;
+        if (!direct_fits(d, i) || kDirectCfgs[i].na != 1) continue;
         const int wn = kDirectCfgs[i].wn;
         if (best_wn == 0 || (best_wn < need && wn > best_wn) || (wn >= need && wn < best_wn)) best_wn = wn;
     }
@@ -322,7 +327,8 @@ int direct_default(const fhc_conv_desc& d, const Geometry& g) {
     uint64_t pick_wgs = 0;
     int pick_th = 0;
     for (int i = 0; i < kNumDirect; i++) {
-        if (!direct_fits(d, i) || kDirectCfgs[i].wn != best_wn) continue;
+        if (!direct_fits(d, i) || kDirectCfgs[i].wn != best_wn || kDirectCfgs[i].persist || kDirectCfgs[i].na != 1)
+            continue;
         const int th = kDirectCfgs[i].fm * kDirectCfgs[i].wm;
         const uint64_t wgs = (uint64_t)d.n * div_ceil(g.hout, th) * div_ceil(g.wout, 16) * div_ceil(d.cout, 16 * best_wn);
         const bool enough = wgs >= 512;
@@ -484,7 +490,7 @@ std::string describe_json(const fhc_conv_plan* p) {
     if (p->family == 1) {
         const DirectCfg& c = kDirectCfgs[p->cfg];
         rows = c.fm * c.wm;
-        chans = 16 * c.wn;
+        chans = 16 * c.na * c.wn;
         wm = c.wm;
         wnv = c.wn;
         wk = c.wk;
@@ -536,6 +542,16 @@ extern "C" int fhc_conv_plan_create(const fhc_conv_desc* desc, const uint16_t* w
         if (!plan_choose(d, *p, &why)) return fail(-1, "fhc_conv_plan_create: %s", why.c_str());
         hipError_t e = hipGetDevice(&p->device);
         if (e != hipSuccess) return fail(-1, "fhc_conv_plan_create: hipGetDevice: %s", hipGetErrorString(e));
+        if (p->family == 1 && kDirectCfgs[p->cfg].persist) {
+            const void* k = nullptr;
+            direct_launcher(p->cfg, &k);
+            int per_cu = 0, cus = 0;
+            if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, (int)p->threads, 0) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess)
+                return fail(-1, "fhc_conv_plan_create: occupancy query failed");
+            const uint64_t resident = (uint64_t)std::max(1, per_cu) * (uint64_t)std::max(1, cus);
+            p->grid.x = (unsigned)std::min<uint64_t>(p->tiles, std::max<uint64_t>(1, resident / p->grid.y));
+        }
         std::vector<uint16_t> packed;
         pack_weights(*p, w_oihw, packed);
         e = upload(*p, packed, bias, slope);
@@ -579,7 +595,7 @@ extern "C" int fhc_conv_run(const fhc_conv_plan* p, const void* x, void* y, cons
         a.part = static_cast<float*>(workspace);
         a.xvec = ((uintptr_t)x % 16 == 0) && a.xcs % 8 == 0 && a.xc0 % 8 == 0;
         a.yvec = ((uintptr_t)y % 8 == 0) && a.ycs % 4 == 0 && a.yc0 % 4 == 0;
-        a.rvec = a.residual && ((uintptr_t)res % 8 == 0) && a.rcs % 4 == 0 && a.rc0 % 4 == 0;
+        a.rvec = a.residual && ((uintptr_t)res % 8 == 0) && a.rcs % 4 == 0 && a.rc0 % 4 == 0 && a.cout % 4 == 0;
         hipStream_t s = static_cast<hipStream_t>(stream);
         hipError_t e = p->launch(a, p->grid, p->lds, s);
         if (e != hipSuccess) return fail(-1, "fhc_conv_run: launch: %s", hipGetErrorString(e));
@@ -726,8 +742,8 @@ extern "C" int fhc_variant_list(const fhc_conv_desc* desc, uint32_t* codes, size
         std::vector<uint32_t> out;
         for (int i = 0; i < kNumDirect; i++) {
             if (!direct_fits(d, i)) continue;
-            const int wn = kDirectCfgs[i].wn;
-            if (16u * wn >= 2 * div_ceil(d.cout, 16) * 16 && wn > 1) continue;
+            const int width = kDirectCfgs[i].na * kDirectCfgs[i].wn;  // 16-channel blocks per channel tile
+            if (16u * width >= 2 * div_ceil(d.cout, 16) * 16 && width > 1) continue;
             if (configure_direct(p, i, &why)) out.push_back(p.code);
         }
         for (int cfg = 1; cfg <= kNumCfg; cfg++) {

@@ -1,17 +1,26 @@
-// The direct conv kernel for layers whose input channels fit one pass (cin padded to 32 <= 128): the weights of a
-// wave's 16 output channels stay in VGPRs for the whole launch, input tiles stream through a halo tile in LDS.
+// The direct conv kernel for layers whose input channels fit one pass (cin padded to 32 <= 128, or 160/288 with
+// the kernel-row K split WK = 3): the weights of a wave's 16 * NA output channels stay in registers for the whole
+// launch, input tiles stream through a halo tile in LDS.
 //
-// Workgroup: WN x WM waves; wave (wn, wm) owns output channels [16 wn, 16 wn + 16) of the workgroup's channel
-// tile and FM output rows of 16 pixels. Per spatial tile (TH = FM * WM rows x 16 columns) the workgroup writes the
+// Workgroup: WN x WM (x WK) waves; wave (wn, wm) owns output channels [16 NA wn, 16 NA (wn + 1)) of the
+// workgroup's channel tile and FM output rows of 16 pixels. Every B operand read from LDS feeds the wave's NA
+// channel blocks (NA MFMAs), which is what bounds the LDS read traffic (1 KB per NA MFMAs). Per spatial tile (TH = FM * WM rows x 16 columns) the workgroup writes the
 // input halo ((TH-1)*S + KS) x (15*S + KS) x CIN32 into LDS (zero outside the image and beyond cin), then each
 // wave runs KSTEPS = KS*KS*CIN32/32 MFMA K-steps reading its shifted windows from LDS. K order: k = tap * CIN32 + ci
 // (channels padded to 32 per tap), so K-step s is tap s / M, channels 32 (s % M) .. +31 with M = CIN32 / 32, and
 // lane group l/16 reads channels +8 (l/16): every LDS read is a per-row base register plus a compile-time offset.
 // The weights were packed in the same order (api.cpp, pack_weights).
-// One workgroup per spatial tile (blockIdx.x) and channel tile (blockIdx.y). Every global load the tile needs
-// (weights, halo, residual, bias) is issued before the first wait, so a tile costs one memory round trip; the
-// registers of the staging are dead before the MFMA chain, which reads LDS one K-step ahead of the MFMAs.
+// One workgroup per spatial tile (blockIdx.x) and channel tile (blockIdx.y), or, PERSIST, no more workgroups than
+// can be resident, each looping over spatial tiles with the next tile's halo loading while the current one
+// computes. Every global load a tile needs (halo, residual; weights and bias once) is issued before its first
+// wait, so a tile costs at most one memory round trip; the MFMA chain reads LDS one K-step ahead of the MFMAs.
 #pragma once
+#include <type_traits>
+
+#ifndef FULL_WAIT_BEFORE_CHAIN
+#define FULL_WAIT_BEFORE_CHAIN
+#endif
+
 #include "conv_kernels.h"
 
 namespace fhc {
@@ -22,19 +31,22 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+// The multiplier of negative values: PReLU slope, LeakyReLU alpha, 1 without activation (exact). Chosen where the
+// value is used, so that no wait for the slope load lands before the MFMA chain.
+__device__ __forceinline__ float negative_scale(const ConvKArgs& a, float slope) {
+    return a.act == 1 ? slope : a.act == 2 ? a.alpha : 1.0f;
+}
+
 // bias, activation, f16 round, residual add rounded again (shaders/conv_tiled.wgsl:57-67), store of 4
-// consecutive channels co..co+3 of output pixel `pix`. rv: the residual's 4 halves (ignored without residual).
+// consecutive channels co..co+3 of output pixel `pix`. sl: the PReLU slopes; rv: the residual's 4 halves (ignored
+// without residual).
 __device__ __forceinline__ void epilogue4r(const ConvKArgs& a, size_t pix, int co, f4 v, const float* b,
                                           const float* sl, uint2 rv) {
     uint16_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        float t = v[i] + b[i];
-        if (a.act == 1)
-            t = t > 0.0f ? t : sl[i] * t;
-        else if (a.act == 2)
-            t = t > 0.0f ? t : a.alpha * t;
-        o[i] = f2h(t);
+        const float t = v[i] + b[i];
+        o[i] = f2h(t > 0.0f ? t : negative_scale(a, sl[i]) * t);
     }
     if (a.residual) {
         const uint16_t r[4] = {(uint16_t)(rv.x & 0xffffu), (uint16_t)(rv.x >> 16), (uint16_t)(rv.y & 0xffffu),
@@ -55,13 +67,21 @@ __device__ __forceinline__ void epilogue4r(const ConvKArgs& a, size_t pix, int c
     }
 }
 
-// the residual's 4 halves at (pix, co..co+3), zeros past cout
-__device__ __forceinline__ uint2 load_res4(const ConvKArgs& a, size_t pix, int co) {
-    const uint16_t* rp = a.res + pix * (size_t)a.rcs + a.rc0 + co;
-    if (a.rvec && co + 4 <= a.cout) return *reinterpret_cast<const uint2*>(rp);
+// the residual's 4 halves at (pix, co..co+3), zeros past cout. Branch-free: a lane outside the output (!valid)
+// reads pixel 0, channel 0 of the view instead, so no load sits in divergent control flow (a load there forces a
+// wait for every outstanding memory operation, stores included, where the branches join). rvec (8-byte aligned
+// view, cout a multiple of 4): one 8-byte load; else 4 clamped 2-byte loads, whose zeroing waits for them.
+__device__ __forceinline__ uint2 load_res4(const ConvKArgs& a, size_t pix, int co, bool valid) {
+    // without a residual the loads read the bias array (at least 16 halves), and the values go unused
+    const uint16_t* rp = a.residual ? a.res + (valid ? pix * (size_t)a.rcs + co : 0) + a.rc0 : a.bias;
+    if (a.rvec || !a.residual) return *reinterpret_cast<const uint2*>(rp);  // the bias array is 256-byte aligned
+    const int rem = valid ? a.cout - co : a.cout;
     uint32_t r[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) r[i] = co + i < a.cout ? rp[i] : 0u;
+    for (int i = 0; i < 4; i++) {
+        const uint32_t v = rp[min(i, rem - 1)];
+        r[i] = i < rem ? v : 0u;
+    }
     return uint2{r[0] | (r[1] << 16), r[2] | (r[3] << 16)};
 }
 
@@ -81,8 +101,398 @@ __device__ __forceinline__ uint4 load_group(const uint16_t* p, int ch, int cin) 
     return uint4{q[0], q[1], q[2], q[3]};
 }
 
+// The MFMA schedule of one tile (WK == 1). The distinct B operands of a wave are the halo rows r = 0 .. R-1 it
+// touches (R = (FM-1)*S + KS) at each column step c = (kx, m); operand q = c*R + r feeds the MFMAs of every output
+// row f with ky = r - f*S in [0, KS), for each of the NA channel blocks. uses() counts those (f, ky) pairs.
+template <int FM, int S, int KS>
+__host__ __device__ constexpr int row_uses(int r) {
+    int u = 0;
+    for (int f = 0; f < FM; f++) u += (r - f * S >= 0 && r - f * S < KS) ? 1 : 0;
+    return u;
+}
+
+// Pins the order the scheduler keeps for the unrolled chain: the first D LDS reads, then per operand q the read of
+// operand q + D, q's MFMAs and, for q < NSQ, one global store (the previous tile's outputs, persistent grid).
+// Left alone, the scheduler issues each read about one MFMA before its use and bunches the stores.
+template <int Q, int NQ, int D, int R, int FM, int S, int KS, int NA, int NSQ>
+__device__ __forceinline__ void pin_mfma_pipeline() {
+    if constexpr (Q == 0) __builtin_amdgcn_sched_group_barrier(0x100, D, 0);
+    if constexpr (Q < NQ) {
+        if constexpr (Q + D < NQ) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, row_uses<FM, S, KS>(Q % R) * NA, 0);
+        if constexpr (Q < NSQ) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);
+        pin_mfma_pipeline<Q + 1, NQ, D, R, FM, S, KS, NA, NSQ>();
+    }
+}
+
+// Buffer accesses at this byte offset are out of range: loads return zeros, stores are dropped.
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Bytes a view spans from its tensor's first element: pixels * cstride + c0 + channels, in halves.
+__host__ __device__ inline uint64_t view_bytes(uint64_t pixels, int cstride, int c0, int channels) {
+    return pixels == 0 ? 0 : ((pixels - 1) * (uint64_t)cstride + (uint64_t)c0 + (uint64_t)channels) * 2;
+}
+
+// Waves per SIMD a persistent configuration is compiled for: one workgroup per CU, or two of 4 waves. Left to aim
+// for a higher occupancy that the resident grid cannot use, the scheduler trades away the LDS read pipeline for
+// registers (every MFMA then waits for its own LDS read).
+constexpr int persist_waves_per_simd(int waves) { return (waves + 3) / 4 < 2 ? 2 : (waves + 3) / 4; }
+
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int NA, int WK, bool PERSIST, int MODE>
+__global__ __launch_bounds__(64 * WM * WN * WK)
+__attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN * WK) : 8))) void conv_direct(
+    ConvKArgs a) {
+    static_assert(WK == 1 || (WK == 3 && KS == 3), "the K split runs one kernel row per wave");
+    static_assert(!PERSIST || MODE == 2, "the persistent configurations run the buffer loop");
+    constexpr bool VEC = MODE > 0;  // 16-byte aligned input
+    constexpr int TH = FM * WM, TW = 16, BN = 16 * NA * WN, NT = 64 * WM * WN * WK;
+    constexpr int IH = (TH - 1) * S + KS, IW = (TW - 1) * S + KS;
+    constexpr int GPT = CIN32 / 8, PSTR = CIN32 + 8, M = CIN32 / 32;
+    constexpr int KSTEPS = KS * KS * M, KW = KSTEPS / WK;  // K-steps of the whole conv / of one wave
+    constexpr int HALO = IH * IW * GPT, NLD = (HALO + NT - 1) / NT;
+    // LDS: the halo, padded so that the last staging round writes without a branch (its elements past the halo
+    // hold zeros), or the K-split partial sums
+    constexpr int HALO_BYTES = ((NLD * NT + GPT - 1) / GPT) * PSTR * 2, RED_BYTES = (WK - 1) * WM * WN * FM * NA * 64 * 16;
+    constexpr int NS = FM * NA;  // 8-byte output stores per lane and tile
+    __shared__ __align__(16) uint16_t halo[(HALO_BYTES > RED_BYTES ? HALO_BYTES : RED_BYTES) / 2];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wk = wave / (WM * WN), wmn = wave - wk * (WM * WN);
+    const int wn = wmn % WN, wm = wmn / WN;
+    const int co_w = blockIdx.y * BN + wn * 16 * NA;  // the wave's first output channel; block j at co_w + 16 j
+    const int co = co_w + 4 * (lane >> 4);            // the lane's 4 output channels of block 0 in the accumulator
+    const int tiles = a.n * a.tiles_y * a.tiles_x;
+
+    // this wave's weights (its K-steps, once per workgroup) in the order the MFMA chain first uses them, then
+    // bias and slope
+    h8 wr[NA][KW];
+    float bias[NA][4], slope[NA][4];
+    auto load_weights = [&]() {
+#pragma unroll
+        for (int j = 0; j < NA; j++) {
+            const h8* wp =
+                reinterpret_cast<const h8*>(a.wpk) + ((size_t)((co_w >> 4) + j) * KSTEPS + wk * KW) * 64 + lane;
+            if constexpr (WK == 1) {
+#pragma unroll
+                for (int c = 0; c < KS * M; c++)
+#pragma unroll
+                    for (int ky = 0; ky < KS; ky++) {
+                        const int st = (ky * KS + c / M) * M + c % M;
+                        wr[j][st] = wp[st * 64];
+                    }
+            } else {
+#pragma unroll
+                for (int st = 0; st < KW; st++) wr[j][st] = wp[st * 64];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NA; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // unconditional loads (the plan always holds a slope array): a load under a branch would make the
+                // compiler wait for every outstanding load where the branches join
+                bias[j][i] = h2f(a.bias[co + 16 * j + i]);
+                slope[j][i] = h2f(a.slope[co + 16 * j + i]);
+            }
+    };
+
+
+    auto tile_origin = [&](int t, int& img, int& oy0, int& ox0) {
+        const int tx = t % a.tiles_x, r = t / a.tiles_x;
+        const int ty = r % a.tiles_y;
+        img = r / a.tiles_y;
+        oy0 = ty * TH;
+        ox0 = tx * TW;
+    };
+
+    // the halo of tile t, staged in registers: element e = tid + i*NT is 8 channels (group g) of halo pixel pix.
+    // MODE 2 (the persistent loop; 16-byte aligned view within 2^31 bytes, checked by the launcher): buffer loads,
+    // out-of-range lanes (padding, past cin, past the halo) read zeros, so no load sits in a branch; the channels of
+    // a partial group past cin are zeroed when the halo goes to LDS. MODE 1: 16-byte loads; MODE 0: 2-byte loads at
+    // clamped addresses.
+    uint4 pre[NLD];
+    const auto rx = buffer_rsrc(a.x, MODE == 2 ? (uint32_t)view_bytes((uint64_t)a.n * a.h * a.w, a.xcs, a.xc0, a.cin) : 0u);
+    auto load_halo = [&](int t) {
+        int img, oy0, ox0;
+        tile_origin(t, img, oy0, ox0);
+        const int iy0 = oy0 * S - a.pad, ix0 = ox0 * S - a.pad;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * NT;
+            const int pix = e / GPT, g = e - pix * GPT;
+            const int iy = pix / IW, ix = pix - iy * IW;
+            const int gy = iy0 + iy, gx = ix0 + ix, ch = g * 8;
+            // bitwise &: selects, not branches
+            const bool ok = ((i + 1) * NT <= HALO || e < HALO) & (gy >= 0) & (gy < a.h) & (gx >= 0) & (gx < a.w) &
+                            (ch < a.cin);
+            if constexpr (MODE == 2) {
+                const uint32_t off =
+                    ok ? (((uint32_t)(img * a.h + gy) * (uint32_t)a.w + gx) * (uint32_t)a.xcs + a.xc0 + ch) * 2u : kOOB;
+                pre[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+            } else {
+                pre[i] = uint4{0u, 0u, 0u, 0u};
+                if (ok)
+                    pre[i] = load_group<VEC>(
+                        a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch, a.cin);
+            }
+        }
+    };
+    auto write_halo = [&]() {  // the staged halo into LDS (elements past the halo land in the padding)
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * NT;
+            {
+                const int pix = e / GPT, g = e - pix * GPT;
+                uint4 v = pre[i];
+                if constexpr (MODE == 2) {
+                    const int rem = a.cin - g * 8;
+                    auto keep = [&](int h) { return (2 * h < rem ? 0xffffu : 0u) | (2 * h + 1 < rem ? 0xffff0000u : 0u); };
+                    v.x &= keep(0);
+                    v.y &= keep(1);
+                    v.z &= keep(2);
+                    v.w &= keep(3);
+                }
+                *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = v;
+            }
+        }
+    };
+
+    // LDS base of the lane's pixel and channel group per output row; with the K split, wave wk runs kernel row wk
+    int pb[FM];
+#pragma unroll
+    for (int f = 0; f < FM; f++)
+        pb[f] = (((wm * FM + f) * S + wk * (WK > 1)) * IW + (lane & 15) * S) * PSTR + (lane >> 4) * 8;
+    auto koff = [](int s) {  // LDS offset of K-step s (of this wave) relative to pb
+        const int tap = s / M, m = s % M;
+        return WK > 1 ? tap * PSTR + m * 32 : ((tap / KS) * IW + tap % KS) * PSTR + m * 32;
+    };
+
+    // the MFMA chain over the LDS halo; every LDS read is a base register plus a compile-time offset, and each read
+    // feeds the NA channel blocks of the wave. side(k), k < NSQ, issues one global store between MFMA groups.
+    auto compute = [&](f4 (&acc)[FM][NA], auto side, auto nsq) {
+        constexpr int NSQ = decltype(nsq)::value;
+#pragma unroll
+        for (int f = 0; f < FM; f++)
+#pragma unroll
+            for (int j = 0; j < NA; j++) acc[f][j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (WK == 1) {
+            // each distinct B operand is read once and feeds all its (f, ky) uses; reads run D operands ahead
+            // through a ring of D + 1 registers, in the order pin_mfma_pipeline fixes
+            constexpr int R = (FM - 1) * S + KS, NQ = KS * M * R, D = NQ < 4 ? NQ : 4;
+            static_assert(NSQ <= NQ, "more stores than pipeline steps");
+            const int pr = (wm * FM * S * IW + (lane & 15) * S) * PSTR + (lane >> 4) * 8;
+            auto rd = [&](int q) {
+                const int c = q / R, r = q % R, kx = c / M, m = c % M;
+                return *reinterpret_cast<const h8*>(halo + pr + (r * IW + kx) * PSTR + m * 32);
+            };
+            h8 b[D + 1];
+#pragma unroll
+            for (int q = 0; q < D; q++) b[q] = rd(q);
+#pragma unroll
+            for (int q = 0; q < NQ; q++) {
+                if (q + D < NQ) b[(q + D) % (D + 1)] = rd(q + D);
+                const int c = q / R, r = q % R, kx = c / M, m = c % M;
+#pragma unroll
+                for (int f = FM - 1; f >= 0; f--) {
+                    const int ky = r - f * S;
+                    if (ky < 0 || ky >= KS) continue;
+                    const int st = (ky * KS + kx) * M + m;
+#pragma unroll
+                    for (int j = 0; j < NA; j++)
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wr[j][st], b[q % (D + 1)], acc[f][j], 0, 0, 0);
+                }
+                if (q < NSQ) side(q);
+            }
+            pin_mfma_pipeline<0, NQ, D, R, FM, S, KS, NA, NSQ>();
+        } else {
+            // one kernel row per wave: LDS reads one K-step ahead of the MFMAs that consume them
+            h8 bx[2][FM];
+#pragma unroll
+            for (int f = 0; f < FM; f++) bx[0][f] = *reinterpret_cast<const h8*>(halo + pb[f]);
+#pragma unroll
+            for (int s = 0; s < KW; s++) {
+                if (s + 1 < KW) {
+#pragma unroll
+                    for (int f = 0; f < FM; f++)
+                        bx[(s + 1) & 1][f] = *reinterpret_cast<const h8*>(halo + pb[f] + koff(s + 1));
+                }
+#pragma unroll
+                for (int f = 0; f < FM; f++)
+#pragma unroll
+                    for (int j = 0; j < NA; j++)
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wr[j][s], bx[s & 1][f], acc[f][j], 0, 0, 0);
+            }
+            // waves of kernel rows 1 and 2 hand their partial sums to the row-0 wave of the same (wm, wn), which
+            // adds them in row order
+            f4* red = reinterpret_cast<f4*>(halo);
+            __syncthreads();
+            if (wk > 0) {
+#pragma unroll
+                for (int f = 0; f < FM; f++)
+#pragma unroll
+                    for (int j = 0; j < NA; j++)
+                        red[((((wk - 1) * WM * WN + wmn) * FM + f) * NA + j) * 64 + lane] = acc[f][j];
+            }
+            __syncthreads();
+            if (wk == 0) {
+#pragma unroll
+                for (int k = 1; k < WK; k++)
+#pragma unroll
+                    for (int f = 0; f < FM; f++)
+#pragma unroll
+                        for (int j = 0; j < NA; j++)
+                            acc[f][j] += red[((((k - 1) * WM * WN + wmn) * FM + f) * NA + j) * 64 + lane];
+            }
+        }
+    };
+
+    f4 acc[FM][NA];
+    uint2 rres[FM][NA];
+    if constexpr (MODE < 2) {
+        // one tile per workgroup: every load issued up front, the weights first (at one tile per workgroup they are
+        // the larger transfer), and the chain starts once all have landed
+        const int t = blockIdx.x;
+        load_weights();
+        load_halo(t);
+        int img, oy0, ox0;
+        tile_origin(t, img, oy0, ox0);
+#pragma unroll
+        for (int f = 0; f < FM; f++)
+#pragma unroll
+            for (int j = 0; j < NA; j++) {
+                const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
+                const bool valid = (oy < a.hout) & (ox < a.wout) & (co + 16 * j < a.cout);
+                rres[f][j] = load_res4(a, ((size_t)img * a.hout + oy) * a.wout + ox, co + 16 * j, valid);
+            }
+        write_halo();
+        __syncthreads();
+        FULL_WAIT_BEFORE_CHAIN
+        compute(acc, [](int) {}, std::integral_constant<int, 0>{});
+        if (wk == 0) {
+#pragma unroll
+            for (int f = 0; f < FM; f++) {
+                const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
+                if (oy < a.hout && ox < a.wout) {
+#pragma unroll
+                    for (int j = 0; j < NA; j++)
+                        if (co + 16 * j < a.cout)
+                            epilogue4r(a, ((size_t)img * a.hout + oy) * a.wout + ox, co + 16 * j, acc[f][j], bias[j],
+                                       slope[j], rres[f][j]);
+                }
+            }
+        }
+    } else {
+        // The persistent configurations: G = gridDim.x resident workgroups loop over tiles t, t + G, ... Input, residual and output go through
+        // buffer instructions (out-of-range lanes: zero loads, dropped stores), so no memory access sits in a branch
+        // and the compiler's waits are exact. Per tile: the MFMA chain, which also issues the previous tile's stores
+        // one per pipeline step; tile t + G's halo (in registers since the previous tile) into LDS; tile t's
+        // epilogue into registers; then tile t + 2G's halo loads and tile t + G's residual loads. Every wait is for
+        // operations issued a whole chain earlier (the hardware counter that tracks loads also tracks stores, so a
+        // load issued before a store cannot be waited for alone), and the stores of all workgroups spread over the
+        // chain instead of leaving every CU at once. The first halo is loaded before the weights, so that its wait
+        // does not include them and the chain starts as the weights arrive. The launcher checks the alignment and the
+        // 2^31-byte extents this needs.
+        const int G = gridDim.x;
+        int t = blockIdx.x;
+        if (t >= tiles) return;  // uniform over the workgroup
+        const uint64_t pix_out = (uint64_t)a.n * a.hout * a.wout;
+        const auto ry = buffer_rsrc(a.y, (uint32_t)view_bytes(pix_out, a.ycs, a.yc0, a.cout));
+        const auto rr = buffer_rsrc(a.res, a.residual ? (uint32_t)view_bytes(pix_out, a.rcs, a.rc0, a.cout) : 0u);
+        auto load_res_buf = [&](int tt) {  // waves of kernel rows 1, 2 (K split) load nothing
+            int img, oy0, ox0;
+            tile_origin(tt, img, oy0, ox0);
+#pragma unroll
+            for (int f = 0; f < FM; f++)
+#pragma unroll
+                for (int j = 0; j < NA; j++) {
+                    const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
+                    const bool ok = (wk == 0) & (oy < a.hout) & (ox < a.wout) & (co + 16 * j < a.cout);
+                    const uint32_t off =
+                        ok ? (((uint32_t)(img * a.hout + oy) * (uint32_t)a.wout + ox) * (uint32_t)a.rcs + a.rc0 + co +
+                              16 * j) * 2u
+                           : kOOB;
+                    rres[f][j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rr, off, 0, 0));
+                }
+        };
+        // tile t's outputs, packed, and their byte offsets (kOOB: nothing to store)
+        uint2 ov[FM][NA];
+        uint32_t ooff[FM][NA];
+        auto epilogue_pack = [&](int tt) {
+            int img, oy0, ox0;
+            tile_origin(tt, img, oy0, ox0);
+#pragma unroll
+            for (int f = 0; f < FM; f++)
+#pragma unroll
+                for (int j = 0; j < NA; j++) {
+                    const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
+                    const bool ok = (wk == 0) & (oy < a.hout) & (ox < a.wout) & (co + 16 * j < a.cout);
+                    ooff[f][j] = ok ? (((uint32_t)(img * a.hout + oy) * (uint32_t)a.wout + ox) * (uint32_t)a.ycs +
+                                       a.yc0 + co + 16 * j) * 2u
+                                    : kOOB;
+                    uint16_t o[4];
+                    const uint32_t rw[2] = {rres[f][j].x, rres[f][j].y};
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const float v = acc[f][j][i] + bias[j][i];
+                        const uint16_t h = f2h(v > 0.0f ? v : negative_scale(a, slope[j][i]) * v);
+                        const uint16_t hr = f2h(h2f(h) + h2f((uint16_t)(rw[i >> 1] >> (16 * (i & 1)))));
+                        o[i] = a.residual ? hr : h;
+                    }
+                    ov[f][j] = uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+                }
+        };
+        auto store_one = [&](int k) {
+            const int f = k / NA, j = k % NA;
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) uint32_t, ov[f][j]),
+                                                  ry, ooff[f][j], 0, 0);
+        };
+        // stores interleaved with the next tile's chain (the K-split chain takes none: its tile's stores go out
+        // right after the epilogue)
+        constexpr int NSQ = WK == 1 ? NS : 0;
+
+        load_halo(t);
+        load_weights();
+        write_halo();
+        __syncthreads();
+        if (t + G < tiles) load_halo(t + G);
+        load_res_buf(t);
+#pragma unroll
+        for (int f = 0; f < FM; f++)
+#pragma unroll
+            for (int j = 0; j < NA; j++) {
+                ov[f][j] = uint2{0u, 0u};
+                ooff[f][j] = kOOB;
+            }
+        for (; t < tiles; t += G) {
+            compute(acc, store_one, std::integral_constant<int, NSQ>{});
+            __syncthreads();  // every wave is done reading tile t's halo
+            if (t + G < tiles) write_halo();
+            __syncthreads();
+            epilogue_pack(t);
+            if constexpr (NSQ == 0) {
+#pragma unroll
+                for (int k = 0; k < NS; k++) store_one(k);
+            }
+            if (t + 2 * G < tiles) load_halo(t + 2 * G);
+            if (t + G < tiles) load_res_buf(t + G);
+        }
+        if constexpr (NSQ > 0) {
+#pragma unroll
+            for (int k = 0; k < NS; k++) store_one(k);
+        }
+    }
+}
+
+// The one-tile-per-workgroup kernel of the configurations with one channel block per wave: every global load of
+// the tile issued before the first wait (weights, halo, residual, then bias and slope), the halo into LDS, the
+// MFMA chain reading LDS one K-step ahead, the epilogue per wave. Measured faster at one tile per workgroup than
+// the buffer loop above, whose deeper pipelining only pays over several tiles.
 template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK, bool VEC>
-__global__ __launch_bounds__(64 * WM * WN * WK) void conv_direct(ConvKArgs a) {
+__global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
     static_assert(WK == 1 || (WK == 3 && KS == 3), "the K split runs one kernel row per wave");
     constexpr int TH = FM * WM, TW = 16, BN = 16 * WN, NT = 64 * WM * WN * WK;
     constexpr int IH = (TH - 1) * S + KS, IW = (TW - 1) * S + KS;
@@ -102,8 +512,6 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_direct(ConvKArgs a) {
     const int ty = r % a.tiles_y, img = r / a.tiles_y;
     const int oy0 = ty * TH, ox0 = tx * TW;
 
-    // every global load of the tile is issued before the first wait: weights (this wave's K-steps), input halo,
-    // residual, bias
     h8 wr[KW];
     {
         const h8* wp = reinterpret_cast<const h8*>(a.wpk) + ((size_t)(co_w >> 4) * KSTEPS + wk * KW) * 64 + lane;
@@ -132,7 +540,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_direct(ConvKArgs a) {
         rres[f] = uint2{0u, 0u};
         const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
         if (wk == 0 && a.residual && oy < a.hout && ox < a.wout && co < a.cout)
-            rres[f] = load_res4(a, ((size_t)img * a.hout + oy) * a.wout + ox, co);
+            rres[f] = load_res4(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, true);
     }
     float bias[4], slope[4];
 #pragma unroll
@@ -207,16 +615,50 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_direct(ConvKArgs a) {
     }
 }
 
-// launches the 16-byte-load instantiation when the input view allows it (args.xvec), else the 2-byte one
-template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK>
+// Whether a launch can take the buffer-instruction loop of the persistent configurations: 16-byte aligned input, 8-byte aligned output and
+// residual with cout a multiple of 4, and views within the 2^31 bytes a buffer offset reaches.
+inline bool buffer_path_ok(const ConvKArgs& a) {
+    const uint64_t pin = (uint64_t)a.n * a.h * a.w, pout = (uint64_t)a.n * a.hout * a.wout;
+    const uint64_t lim = 1ull << 31;
+    return a.xvec && a.yvec && a.cout % 4 == 0 && (!a.residual || a.rvec) &&
+           view_bytes(pin, a.xcs, a.xc0, a.cin) < lim && view_bytes(pout, a.ycs, a.yc0, a.cout) < lim &&
+           (!a.residual || view_bytes(pout, a.rcs, a.rc0, a.cout) < lim);
+}
+
+// Launches a persistent configuration on its resident grid when the views allow the buffer loop, else one
+// workgroup per tile, with 16-byte input loads when the input view is 16-byte aligned.
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int NA, int WK, bool PERSIST>
 hipError_t launch_direct(const ConvKArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     (void)lds;
     const dim3 block(64 * WM * WN * WK);
-    if (a.xvec)
-        hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, WK, true>), grid, block, 0, s, a);
-    else
-        hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, WK, false>), grid, block, 0, s, a);
+    if constexpr (PERSIST) {
+        if (buffer_path_ok(a)) {
+            hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, true, 2>), grid, block, 0, s, a);
+            return hipGetLastError();
+        }
+        grid.x = (unsigned)(a.n * a.tiles_y * a.tiles_x);
+    }
+    if constexpr (NA == 1) {
+        if (a.xvec)
+            hipLaunchKernelGGL((conv_tile<KS, S, CIN32, FM, WM, WN, WK, true>), grid, block, 0, s, a);
+        else
+            hipLaunchKernelGGL((conv_tile<KS, S, CIN32, FM, WM, WN, WK, false>), grid, block, 0, s, a);
+    } else {
+        if (a.xvec)
+            hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, false, 1>), grid, block, 0, s, a);
+        else
+            hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, false, 0>), grid, block, 0, s, a);
+    }
     return hipGetLastError();
+}
+
+// the kernel of a configuration, for occupancy queries
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int NA, int WK, bool PERSIST>
+const void* direct_kernel() {
+    if constexpr (PERSIST || NA > 1)
+        return reinterpret_cast<const void*>(&conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, PERSIST, PERSIST ? 2 : 1>);
+    else
+        return reinterpret_cast<const void*>(&conv_tile<KS, S, CIN32, FM, WM, WN, WK, true>);
 }
 
 }  // namespace fhc

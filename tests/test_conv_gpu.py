@@ -107,17 +107,23 @@ def test_every_variant_matches_the_oracle(shape):
 def test_views_with_poisoned_neighbours():
     # NaN in the input channels outside the view must never reach the result; NaN in the output channels outside
     # the view must stay there; unaligned strides take the scalar load / store paths
+    # the planner's choice and every persistent variant: with aligned views these run the buffer-load loop (the
+    # input group at channel 16 holds 4 channels of the view next to 4 poisoned ones), with unaligned ones they fall
+    # back to one workgroup per tile
     for xv, yv, rv in [((48, 8), (80, 16), (40, 4)), ((37, 3), (35, 1), (33, 5)), ((24, 0), (24, 0), (24, 0))]:
         c = Case(1, 21, 30, 20, 24, act=1, residual=True, xv=xv, yv=yv, rv=rv, poison=True, seed=11)
-        say("views", xv, yv, rv)
-        got = c.run_gpu()
         want = c.run_oracle()
-        sl = slice(yv[1], yv[1] + 24)
-        ok, md, mref = parity(got, want, view=sl)
-        assert ok, (md, mref)
-        mask = np.ones(yv[0], bool)
-        mask[sl] = False
-        assert np.array_equal(got[..., mask], c.y0[..., mask])
+        persistent = [k for k in fhconv.variant_list(c.fhc_desc()) if fhconv.variant_name(k).endswith("/p")]
+        assert persistent
+        for code in [0] + persistent:
+            say("views", xv, yv, rv, fhconv.variant_name(code) if code else "planner")
+            got = c.run_gpu(variant=code)
+            sl = slice(yv[1], yv[1] + 24)
+            ok, md, mref = parity(got, want, view=sl)
+            assert ok, (code, md, mref)
+            mask = np.ones(yv[0], bool)
+            mask[sl] = False
+            assert np.array_equal(got[..., mask], c.y0[..., mask])
 
 
 def test_batch_images_are_independent():
@@ -242,3 +248,21 @@ def test_autotune_picks_a_listed_variant_and_records_it():
         assert ok, (md, mref)
     finally:
         fhconv.tune_clear()
+
+
+@pytest.mark.parametrize("shape", [(1, 272, 480, 64, 64, 1), (1, 544, 960, 32, 64, 2)], ids=["s1", "s2"])
+def test_persistent_variants_full_size(shape):
+    # the persistent variants loop over more tiles than workgroups at the 1080p/4 sizes: rows checked in bands
+    n, h, w, cin, cout, s = shape
+    c = Case(n, h, w, cin, cout, stride=s, act=1, residual=(s == 1), seed=18)
+    codes = [k for k in fhconv.variant_list(c.fhc_desc()) if fhconv.variant_name(k).endswith("/p")]
+    assert codes
+    bands = {r0: oracle_rows(c, r0, r0 + 4, threads=8) for r0 in (0, c.hout // 2 - 2, c.hout - 4)}
+    for code in codes:
+        got, plan = c.run_gpu(variant=code, return_plan=True)
+        d = plan.describe()
+        say("persistent", d["name"], d["grid"], d["tiles"])
+        assert d["grid"][0] < d["tiles"]
+        for r0, want in bands.items():
+            ok, md, mref = parity(got[0, r0:r0 + 4], want)
+            assert ok, (d["name"], r0, md, mref)
