@@ -33,6 +33,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def pad8(c):
+    return (c + 7) // 8 * 8
+
+
 def roof(flops, nbytes):
     t_hbm, t_mfma = nbytes / HBM_PEAK, flops / MFMA_F16_PEAK
     return ("hbm", t_hbm) if t_hbm >= t_mfma else ("mfma", t_mfma)
@@ -52,14 +56,17 @@ class Net:
             wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
             b = f16(rng.normal(0, 0.01, L.cout))
             s = f16(rng.uniform(0.05, 0.3, L.cout)) if L.act == 1 else None
+            # activations are NHWC with the channel stride padded to 8 halves (16 bytes): the concat buffers the
+            # graph's convs read (279, 155, 14 channels ...) are allocated that way, and the convs read views
+            cx, cy = pad8(L.cin), pad8(L.cout)
             d = fhconv.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
-                                 residual=L.residual)
+                                 residual=L.residual, x_cstride=cx, y_cstride=cy, r_cstride=cy if L.residual else 0)
             x = self.bufs[L.chain][1] if L.chain else \
-                f16(rng.uniform(-1, 1, (L.n, L.h, L.w, L.cin))).to(dev)
-            y = torch.zeros((L.n, L.hout, L.wout, L.cout), dtype=torch.float16, device=dev)
+                f16(rng.uniform(-1, 1, (L.n, L.h, L.w, cx))).to(dev)
+            y = torch.zeros((L.n, L.hout, L.wout, cy), dtype=torch.float16, device=dev)
             if L.residual:
                 r = self.bufs[L.res_from][1] if L.res_from else \
-                    f16(rng.uniform(-1, 1, (L.n, L.hout, L.wout, L.cout))).to(dev)
+                    f16(rng.uniform(-1, 1, (L.n, L.hout, L.wout, cy))).to(dev)
             else:
                 r = None
             if tune:

@@ -86,12 +86,14 @@ __device__ __forceinline__ uint2 load_res4(const ConvKArgs& a, size_t pix, int c
 }
 
 // 8 consecutive input channels ch..ch+7 of one pixel (p points at channel ch), zeros at and past cin. VEC: the
-// view is 16-byte aligned (cstride, c0 multiples of 8), so a full group is one 16-byte load; a partial group (and
-// every group without VEC) is 8 independent 2-byte loads at clamped in-bounds addresses, selected without branches.
+// view is 16-byte aligned (cstride, c0 multiples of 8), so a full group is one 16-byte load, and so is a partial
+// group when the view's channel stride holds the whole group (`whole`: c0 + cin rounded up to 8 <= cstride); its
+// channels past cin are then zeroed by the caller (mask_group) where the value is next used. Any other group is 8
+// independent 2-byte loads at clamped in-bounds addresses, selected without branches.
 template <bool VEC>
-__device__ __forceinline__ uint4 load_group(const uint16_t* p, int ch, int cin) {
+__device__ __forceinline__ uint4 load_group(const uint16_t* p, int ch, int cin, bool whole = false) {
     const int rem = cin - ch;
-    if (VEC && rem >= 8) return *reinterpret_cast<const uint4*>(p);
+    if (VEC && (rem >= 8 || whole)) return *reinterpret_cast<const uint4*>(p);
     uint32_t q[4];
 #pragma unroll
     for (int k = 0; k < 8; k += 2) {
@@ -99,6 +101,12 @@ __device__ __forceinline__ uint4 load_group(const uint16_t* p, int ch, int cin) 
         q[k >> 1] = (k < rem ? lo : 0u) | ((k + 1 < rem ? hi : 0u) << 16);
     }
     return uint4{q[0], q[1], q[2], q[3]};
+}
+
+// zeroes the halves of an 8-channel group at and past `rem` valid channels (rem >= 8: unchanged)
+__device__ __forceinline__ uint4 mask_group(uint4 v, int rem) {
+    auto keep = [&](int h) { return (2 * h < rem ? 0xffffu : 0u) | (2 * h + 1 < rem ? 0xffff0000u : 0u); };
+    return uint4{v.x & keep(0), v.y & keep(1), v.z & keep(2), v.w & keep(3)};
 }
 
 // The MFMA schedule of one tile (WK == 1). The distinct B operands of a wave are the halo rows r = 0 .. R-1 it
@@ -215,7 +223,9 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
     // a partial group past cin are zeroed when the halo goes to LDS. MODE 1: 16-byte loads; MODE 0: 2-byte loads at
     // clamped addresses.
     uint4 pre[NLD];
-    const auto rx = buffer_rsrc(a.x, MODE == 2 ? (uint32_t)view_bytes((uint64_t)a.n * a.h * a.w, a.xcs, a.xc0, a.cin) : 0u);
+    // the input resource spans the full strided extent (n*h*w*xcs halves, which the input buffer holds): a 16-byte
+    // group that crossed the resource's end would read zeros, valid channels included
+    const auto rx = buffer_rsrc(a.x, MODE == 2 ? (uint32_t)((uint64_t)a.n * a.h * a.w * a.xcs * 2) : 0u);
     auto load_halo = [&](int t) {
         int img, oy0, ox0;
         tile_origin(t, img, oy0, ox0);
@@ -248,14 +258,7 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
             {
                 const int pix = e / GPT, g = e - pix * GPT;
                 uint4 v = pre[i];
-                if constexpr (MODE == 2) {
-                    const int rem = a.cin - g * 8;
-                    auto keep = [&](int h) { return (2 * h < rem ? 0xffffu : 0u) | (2 * h + 1 < rem ? 0xffff0000u : 0u); };
-                    v.x &= keep(0);
-                    v.y &= keep(1);
-                    v.z &= keep(2);
-                    v.w &= keep(3);
-                }
+                if constexpr (MODE == 2) v = mask_group(v, a.cin - g * 8);
                 *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = v;
             }
         }
@@ -519,6 +522,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
         for (int s = 0; s < KW; s++) wr[s] = wp[s * 64];
     }
     uint4 pre[NLD];
+    const bool whole = VEC && a.xc0 + ((a.cin + 7) & ~7) <= a.xcs;  // partial groups load as one 16-byte group
     {
         const int iy0 = oy0 * S - a.pad, ix0 = ox0 * S - a.pad;
 #pragma unroll
@@ -531,7 +535,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
             if ((i + 1) * NT <= HALO || e < HALO)
                 if (gy >= 0 && gy < a.h && gx >= 0 && gx < a.w && ch < a.cin)
                     pre[i] = load_group<VEC>(
-                        a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch, a.cin);
+                        a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch, a.cin, whole);
         }
     }
     uint2 rres[FM];
@@ -554,7 +558,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
         const int e = tid + i * NT;
         if ((i + 1) * NT <= HALO || e < HALO) {
             const int pix = e / GPT, g = e - pix * GPT;
-            *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = pre[i];
+            *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = whole ? mask_group(pre[i], a.cin - g * 8) : pre[i];
         }
     }
     __syncthreads();
@@ -615,13 +619,14 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
     }
 }
 
-// Whether a launch can take the buffer-instruction loop of the persistent configurations: 16-byte aligned input, 8-byte aligned output and
-// residual with cout a multiple of 4, and views within the 2^31 bytes a buffer offset reaches.
+// Whether a launch can take the buffer-instruction loop of the persistent configurations: 16-byte aligned input
+// whose last 8-channel group lies inside the pixel's stride (the group loads whole), 8-byte aligned output and
+// residual with cout a multiple of 4, and extents within the 2^31 bytes a buffer offset reaches.
 inline bool buffer_path_ok(const ConvKArgs& a) {
     const uint64_t pin = (uint64_t)a.n * a.h * a.w, pout = (uint64_t)a.n * a.hout * a.wout;
     const uint64_t lim = 1ull << 31;
-    return a.xvec && a.yvec && a.cout % 4 == 0 && (!a.residual || a.rvec) &&
-           view_bytes(pin, a.xcs, a.xc0, a.cin) < lim && view_bytes(pout, a.ycs, a.yc0, a.cout) < lim &&
+    return a.xvec && a.yvec && a.cout % 4 == 0 && (!a.residual || a.rvec) && a.xc0 + ((a.cin + 7) & ~7) <= a.xcs &&
+           pin * (uint64_t)a.xcs * 2 < lim && view_bytes(pout, a.ycs, a.yc0, a.cout) < lim &&
            (!a.residual || view_bytes(pout, a.rcs, a.rc0, a.cout) < lim);
 }
 

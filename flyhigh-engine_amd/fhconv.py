@@ -57,6 +57,12 @@ def load():
         return _lib
     if not os.path.exists(LIB_PATH):
         raise FhcError(f"{LIB_PATH} is missing: build it first (__graft_entry__.build() or make -C {HERE})")
+    # torch (the driver's device memory and streams) loads its own HIP runtime; it must be in the process before the
+    # library pulls in a HIP runtime by soname, or torch finds no GPU afterwards. One runtime then serves both.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = ctypes.CDLL(LIB_PATH)
     P, U32, SZ = ctypes.c_void_p, ctypes.c_uint32, ctypes.c_size_t
     sig = {

@@ -19,7 +19,9 @@
  * Tensors are NHWC f16 (IEEE binary16 bit patterns in uint16_t), batch-major: element (img, y, x, c) of a view
  * lives at ((img * H + y) * W + x) * cstride + c0 + c. The reference stores planar [C][H][W] f16 with batch 1
  * (crates/flyhigh-engine/src/ops/tensor.rs:6-17); a channel view there (c0) is a channel offset here, and a
- * concat slice is written in place by giving the producer the slice's cstride/c0.
+ * concat slice is written in place by giving the producer the slice's cstride/c0. Each buffer spans its view's full
+ * strided extent: N * H * W * cstride halves (the input of a 16-byte aligned view may be read in whole 8-channel
+ * groups up to that extent; channels outside the view never reach the result).
  */
 #ifndef FHC_CONV_H
 #define FHC_CONV_H
@@ -76,7 +78,8 @@ int fhc_conv_out_shape(const fhc_conv_plan* plan, uint32_t* hout, uint32_t* wout
 /* Enqueue the conv on `stream` (a hipStream_t; NULL = the null stream). x, y, res, workspace are device
  * pointers; res is read only when desc.residual is 1; workspace must hold fhc_conv_workspace_bytes. Asynchronous:
  * no allocation, no synchronisation, capturable in a hipGraph. Replaces the replay of the conv's Steps
- * (gpu/exec.rs:15-87). 16-byte aligned pointers and cstride/c0 multiples of 8 select the vector load path. */
+ * (gpu/exec.rs:15-87). 16-byte aligned pointers and cstride/c0 multiples of 8 select the vector load path; with
+ * c0 + cin rounded up to 8 <= cstride a partial channel group loads as one 16-byte group too. */
 int fhc_conv_run(const fhc_conv_plan* plan, const void* x, void* y, const void* res, void* workspace,
                  void* stream);
 

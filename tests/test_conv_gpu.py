@@ -126,6 +126,27 @@ def test_views_with_poisoned_neighbours():
             assert np.array_equal(got[..., mask], c.y0[..., mask])
 
 
+PADDED_SHAPES = [(2, 24, 40, 3, 36, 2), (1, 12, 40, 279, 96, 1), (1, 20, 36, 14, 24, 1), (1, 14, 35, 155, 48, 1)]
+
+
+@pytest.mark.parametrize("shape", PADDED_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_padded_channel_stride_views(shape):
+    # the frame's odd channel counts in buffers whose channel stride is padded to 8: the partial last group loads
+    # as one 16-byte group and its channels past cin (NaN here) are masked; every variant against the oracle
+    n, h, w, cin, cout, s = shape
+    cx, cy = (cin + 7) // 8 * 8, (cout + 7) // 8 * 8
+    c = Case(n, h, w, cin, cout, stride=s, act=1, residual=(s == 1 and cin == cout), xv=(cx, 0), yv=(cy, 0),
+             rv=(cy, 0), poison=True, seed=23)
+    want = c.run_oracle(threads=8)
+    sl = slice(0, cout)
+    for code in [0] + list(fhconv.variant_list(c.fhc_desc())):
+        say("padded", shape, fhconv.variant_name(code) if code else "planner")
+        got = c.run_gpu(variant=code)
+        ok, md, mref = parity(got, want, view=sl)
+        assert ok, (fhconv.variant_name(code) if code else "planner", md, mref)
+        assert np.array_equal(got[..., cout:], c.y0[..., cout:])
+
+
 def test_batch_images_are_independent():
     c = Case(3, 22, 35, 24, 40, act=1, residual=True, seed=12)
     batched = c.run_gpu()
