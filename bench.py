@@ -133,12 +133,14 @@ def layer_timing(torch, np, fhconv, net, L, reps, graphs, cold_bytes, stream):
                 cold_sets=nsets)
 
 
-def cpu_baseline(np, layers, threads):
+def cpu_baseline(np, layers, threads, passes=10):
+    """Seconds per pair+mid of the C oracle on `threads` host threads: the median of `passes` passes over all the
+    frame's conv layers (inputs generated once, outside the timing)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
     rng = np.random.default_rng(5)
     f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).view(np.uint16)  # noqa: E731
-    total = 0.0
+    work = []
     for L in layers:
         x = f16(rng.uniform(-1, 1, (L.n, L.h, L.w, L.cin)))
         wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
@@ -147,10 +149,125 @@ def cpu_baseline(np, layers, threads):
         r = f16(rng.uniform(-1, 1, (L.n, L.hout, L.wout, L.cout)))
         d = oracle.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
                              residual=L.residual)
+        work.append((d, x, wt, b, s, r))
+    secs = []
+    for _ in range(passes):
         t0 = time.perf_counter()
-        oracle.conv(d, x, wt, b, s, r, threads=threads)
-        total += time.perf_counter() - t0
-    return total
+        for d, x, wt, b, s, r in work:
+            oracle.conv(d, x, wt, b, s, r, threads=threads)
+        secs.append(time.perf_counter() - t0)
+    return statistics.median(secs)
+
+
+def mfma_rate_probe(torch, fhconv, stream):
+    """The sustained dense f16 MFMA rate of this device (TFLOP/s): the library's register-only MFMA probe over
+    8 workgroups per CU, best of 3 timed launches on `stream`."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks, iters = cus * 8, 2048
+    out = torch.empty(blocks * 1024, dtype=torch.float32, device="cuda")
+    best = 0.0
+    with torch.cuda.stream(stream):
+        fhconv.probe_mfma_rate(blocks, 16, out, stream)
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            flops = fhconv.probe_mfma_rate(blocks, iters, out, stream)
+            e1.record(stream)
+            e1.synchronize()
+            best = max(best, flops / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+    return best
+
+
+COPY_BYTES = 256 << 20  # the calibration copy of the traffic passes
+
+
+def pmc_workload(args, torch, net, stream):
+    """One layer over rotating buffer sets (> 512 MB, so every launch reads from HBM), then a device copy of
+    COPY_BYTES the same number of times: rocprofv3 --pmc runs this to read FETCH_SIZE / WRITE_SIZE per dispatch."""
+    L = [L for L in net.layers if L.name == args.pmc_layer][0]
+    p = net.plans[L.name]
+    x, y, r, ws = net.bufs[L.name]
+    per = x.numel() * 2 + y.numel() * 2 + (r.numel() * 2 if r is not None else 0)
+    nsets = max(2, -(-(600 << 20) // per))
+    sets = [(torch.empty_like(x).uniform_(-1, 1), torch.empty_like(y),
+             torch.empty_like(r).uniform_(-1, 1) if r is not None else None) for _ in range(nsets)]
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device="cuda").uniform_(-1, 1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(args.pmc_reps):
+            sx, sy, sr = sets[i % nsets]
+            p.run(sx, sy, sr, ws, stream)
+        for _ in range(args.pmc_reps):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(pmc_layer=L.name, variant=p.describe()["name"], reps=args.pmc_reps, cold_sets=nsets,
+                          copy_bytes=COPY_BYTES)), flush=True)
+    return 0
+
+
+def _counter_per_dispatch(csv_path, counter):
+    """{kernel name: mean counter value per dispatch} from a rocprofv3 counter_collection.csv."""
+    import csv
+    import collections
+    tot, disp = collections.defaultdict(float), collections.defaultdict(set)
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            tot[row["Kernel_Name"]] += float(row["Counter_Value"])
+            disp[row["Kernel_Name"]].add(row["Dispatch_Id"])
+    return {k: tot[k] / len(disp[k]) for k in tot}
+
+
+def traffic_from(args):
+    """HBM bytes per launch of --pmc-layer's conv kernel from the FETCH_SIZE and WRITE_SIZE passes (KiB per
+    dispatch), each scaled by what the same counter reads for the copy of COPY_BYTES; written to
+    profiles/traffic_<layer>.txt."""
+    fetch = _counter_per_dispatch(args.traffic_from[0], "FETCH_SIZE")
+    write = _counter_per_dispatch(args.traffic_from[1], "WRITE_SIZE")
+    conv = [k for k in fetch if "conv" in k]
+    copy = [k for k in fetch if "copybuffer" in k.lower()]  # the runtime's device-to-device copy kernel
+    if len(conv) != 1 or len(copy) != 1:
+        raise SystemExit(f"expected one conv and one copy kernel, got {conv} / {copy}")
+    fk, wk = conv[0], copy[0]
+    f_scale = COPY_BYTES / (fetch[wk] * 1024.0)
+    w_scale = COPY_BYTES / (write[wk] * 1024.0)
+    traffic = fetch[fk] * 1024.0 * f_scale + write[fk] * 1024.0 * w_scale
+    # the variant the planner gives this layer under the same choice table (no GPU needed)
+    import fhconv
+    import flyhighfg
+    if args.tune:
+        with open(args.tune) as f:
+            fhconv.parse_tune(f.read())
+    L = [L for L in flyhighfg.flyhighfg_layers(864, 480, k=1) if L.name == args.pmc_layer][0]
+    desc = fhconv.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
+                            residual=L.residual, x_cstride=pad8(L.cin), y_cstride=pad8(L.cout),
+                            r_cstride=pad8(L.cout) if L.residual else 0)
+    variant = fhconv.plan_dry(desc)["name"]
+    text = (f"layer {args.pmc_layer}\nvariant {variant}\nkernel {fk}\n"
+            f"fetch_kib_per_launch {fetch[fk]:.1f}\nwrite_kib_per_launch {write[fk]:.1f}\n"
+            f"copy_kernel {wk}\ncopy_bytes {COPY_BYTES}\n"
+            f"copy_fetch_kib {fetch[wk]:.1f}\ncopy_write_kib {write[wk]:.1f}\n"
+            f"fetch_scale {f_scale:.4f}\nwrite_scale {w_scale:.4f}\n"
+            f"traffic_bytes_per_launch {traffic:.0f}\n")
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    with open(os.path.join(ROOT, "profiles", f"traffic_{args.pmc_layer}.txt"), "w") as f:
+        f.write(text)
+    print(text, end="")
+    return 0
+
+
+def measured_traffic(layer, variant):
+    """(bytes per launch, source) from profiles/traffic_<layer>.txt when it was measured on this variant's kernel,
+    else (None, reason)."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{layer}.txt")
+    if not os.path.exists(path):
+        return None, "no counter passes recorded for this layer"
+    kv = dict(line.split(" ", 1) for line in open(path).read().splitlines() if " " in line)
+    if kv.get("variant") != variant:
+        return None, f"profiles/traffic_{layer}.txt was measured on {kv.get('variant')}, this run uses {variant}"
+    return int(float(kv["traffic_bytes_per_launch"])), f"profiles/traffic_{layer}.txt ({kv['kernel'][:80]})"
 
 
 def main():
@@ -165,7 +282,17 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the single-layer configurations")
     ap.add_argument("--no-layers", action="store_true", help="skip the per-layer timing of the frame workload")
     ap.add_argument("--no-autotune", action="store_true", help="plan with the heuristic only (no per-shape timing)")
+    ap.add_argument("--tune", help="plan with this choice table (cin,cout,h,w,stride=code lines) instead of autotuning")
+    ap.add_argument("--pmc-layer", help="only run this frame layer --pmc-reps times over rotating (cold) buffers, "
+                                        "then a copy of known size as many times: the workload of the rocprofv3 "
+                                        "--pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-reps", type=int, default=64)
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="with --pmc-layer: turn the two passes' counter_collection.csv files into "
+                         "profiles/traffic_<layer>.txt (HBM bytes per launch, copy-calibrated)")
     args = ap.parse_args()
+    if args.traffic_from:
+        return traffic_from(args)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the conv path shards "
               "by frame pair, one independent pipeline per GPU, so N GPUs run N of these)", file=sys.stderr)
@@ -179,6 +306,10 @@ def main():
     torch.cuda.init()
     dev = torch.device("cuda", 0)
     stream = torch.cuda.Stream(device=dev)
+    if args.tune:
+        with open(args.tune) as f:
+            n_tune = fhconv.parse_tune(f.read())
+        log(f"bench: {n_tune} choices from {args.tune}")
     net_w, net_h = 864, 480  # default_internal(1920, 1080) = (856, 480), padded to a multiple of 32
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
     layers = flyhighfg.flyhighfg_layers(net_w, net_h, k=1)
@@ -186,9 +317,11 @@ def main():
     mid = [L for L in layers if L.stage == "mid"]
     log(f"bench: FlyHighFG conv layers at {net_w}x{net_h}: {len(pair)} pair + {len(mid)} mid launches "
         f"(the two encoders batched)")
-    net = Net(layers, 1, torch, np, fhconv, tune=not args.no_autotune)
+    net = Net(layers, 1, torch, np, fhconv, tune=not (args.no_autotune or args.tune))
     log(f"bench: autotuned {len(net.tuned)} conv shapes")
     torch.cuda.synchronize()
+    if args.pmc_layer:
+        return pmc_workload(args, torch, net, stream)
 
     # one graph per step (pair then mid: one launch per frame), and one per stage for the stage split
     gs, gp, gm = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
@@ -248,25 +381,33 @@ def main():
             del cnet
             torch.cuda.empty_cache()
 
-    # the dominant kernel of the step: the layer with the largest time (warm, as inside the frame graphs)
+    mfma_rate = mfma_rate_probe(torch, fhconv, stream)
+    log(f"bench: sustained dense f16 MFMA rate {mfma_rate:.0f} TFLOP/s")
+
+    # the dominant kernel of the step: the layer with the largest time (warm, as inside the frame graphs); its
+    # achieved rate is the algorithmic bytes (or FLOPs) per launch over its cold per-launch time
     roofline = None
     if per_layer:
         dom = max(per_layer, key=lambda r: r["us_warm"])
         unit = "GB/s" if dom["bound"] == "hbm" else "TFLOP/s"
         achieved = dom["gbs_cold"] if dom["bound"] == "hbm" else dom["tflops_cold"]
         peak = HBM_PEAK / 1e9 if dom["bound"] == "hbm" else MFMA_F16_PEAK / 1e12
+        traffic, traffic_note = measured_traffic(dom["name"], dom["variant"])
         roofline = dict(bound=dom["bound"], achieved=achieved, peak=peak, unit=unit,
-                        frac=round(achieved / peak, 4), traffic=None, kernel=dom["name"], variant=dom["variant"],
+                        frac=round(achieved / peak, 4), traffic=traffic, kernel=dom["name"], variant=dom["variant"],
                         us_cold=dom["us_cold"], us_warm=dom["us_warm"],
-                        per_launch_bytes=dom["bytes"], per_launch_flops=dom["flops"])
+                        per_launch_bytes=dom["bytes"], per_launch_flops=dom["flops"], traffic_source=traffic_note,
+                        sustained_mfma_tflops=round(mfma_rate, 1))
+        if dom["bound"] == "mfma":
+            roofline["frac_of_sustained"] = round(achieved / mfma_rate, 4)
 
     cpu = None
     if not args.no_cpu:
         threads = max(1, min(16, len(os.sched_getaffinity(0))))
         secs = cpu_baseline(np, layers, threads)
         cpu = dict(value=round(1.0 / secs, 4), unit="frames/s", cores=threads, kind="port",
-                   sample=f"all 25 conv layers of one pair()+mid() at {net_w}x{net_h} once through the "
-                          "C oracle (restatement of the reference WGSL conv arithmetic), not lavapipe",
+                   sample=f"all 25 conv layers of one pair()+mid() at {net_w}x{net_h} through the C oracle "
+                          "(restatement of the reference WGSL conv arithmetic), not lavapipe; median of 10 passes",
                    seconds=round(secs, 3))
         log(f"bench: CPU baseline {secs:.3f} s per pair+mid on {threads} threads")
 

@@ -641,7 +641,8 @@ extern "C" void fhc_conv_plan_destroy(fhc_conv_plan* p) {
 extern "C" int fhc_tune_parse(const char* text) {
     return guard(-1, [&]() -> int {
         if (!text) return fail(-1, "fhc_tune_parse: NULL text");
-        // parse_tune (tune_cache.rs:71-87): "cin,cout,h,w,stride=code" per line, malformed lines skipped
+        // parse_tune (tune_cache.rs:71-87): "cin,cout,h,w,stride=code" per line, malformed lines skipped; the value
+        // may also be a variant name
         std::istringstream in(text);
         std::string line;
         int n = 0;
@@ -671,10 +672,18 @@ extern "C" int fhc_tune_parse(const char* text) {
             const size_t a = v.find_first_not_of(" \t\r"), b = v.find_last_not_of(" \t\r");
             if (a == std::string::npos) continue;
             v = v.substr(a, b - a + 1);
-            if (v.empty() || v.size() > 3 || v.find_first_not_of("0123456789") != std::string::npos) continue;
-            const unsigned long code = std::stoul(v);
-            if (code > 255) continue;
-            g_tune[TuneKey(f[0], f[1], f[2], f[3], f[4])] = (uint32_t)code;
+            uint32_t code = 0;
+            if (!v.empty() && v.size() <= 3 && v.find_first_not_of("0123456789") == std::string::npos) {
+                const unsigned long c = std::stoul(v);
+                if (c > 255) continue;
+                code = (uint32_t)c;
+            } else {
+                // an MI355X variant name ("direct.c64.t1x2.n48"): stable across builds, unlike the code it maps to
+                for (uint32_t c = 1; c < 256 && !code; c++)
+                    if (code_name(c) == v) code = c;
+                if (!code) continue;
+            }
+            g_tune[TuneKey(f[0], f[1], f[2], f[3], f[4])] = code;
             n++;
         }
         return n;
@@ -835,6 +844,18 @@ extern "C" int fhc_conv_autotune(const fhc_conv_desc* desc, const uint16_t* w_oi
         if (best_us) *best_us = best;
         clear_error();
         return best_code;
+    });
+}
+
+extern "C" int fhc_probe_mfma_rate(uint32_t blocks, uint32_t iters, void* out, void* stream) {
+    return guard(-1, [&]() -> int {
+        if (!out) return fail(-1, "fhc_probe_mfma_rate: NULL output");
+        if (blocks == 0 || blocks > 65535 || iters == 0 || iters > (1u << 24))
+            return fail(-1, "fhc_probe_mfma_rate: blocks must be 1..65535 and iters 1..2^24");
+        hipError_t e = mfma_rate_probe_launch(blocks, (int)iters, static_cast<float*>(out),
+                                              static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return fail(-1, "fhc_probe_mfma_rate: %s", hipGetErrorString(e));
+        return 0;
     });
 }
 

@@ -67,5 +67,8 @@ hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s);
 // Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the
 // operand layouts the conv kernels assume. Device pointers.
 hipError_t mfma_probe_launch(const uint16_t* a, const uint16_t* b, float* d, hipStream_t s);
+// The sustained MFMA rate probe: `blocks` workgroups of 4 waves, each wave 8 * iters 16x16x32 f16 MFMAs (16384
+// FLOPs each); out holds blocks * 256 * 4 floats.
+hipError_t mfma_rate_probe_launch(unsigned blocks, int iters, float* out, hipStream_t s);
 
 }  // namespace fhc

@@ -230,6 +230,28 @@ __global__ __launch_bounds__(64) void mfma_probe(const uint16_t* A, const uint16
     for (int r = 0; r < 4; r++) D[(4 * (l >> 4) + r) * 16 + (l & 15)] = d[r];
 }
 
+// The dense f16 MFMA rate the chip sustains: each wave keeps 8 independent 16x16x32 accumulators busy for `iters`
+// rounds (operands in registers, no memory traffic besides one store per lane).
+__global__ __launch_bounds__(256) void mfma_rate_probe(f4* out, int iters) {
+    h8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = (_Float16)((threadIdx.x & 7) * 0.001f + i * 0.01f);
+        b[i] = (_Float16)(i * 0.02f);
+    }
+    f4 acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
+    }
+    f4 s = acc[0];
+#pragma unroll
+    for (int j = 1; j < 8; j++) s += acc[j];
+    out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
 template <int KS, int S, int CFG>
 hipError_t launch_cfg(const ConvKArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     constexpr TileCfg c = kTileCfgs[CFG];
@@ -270,6 +292,11 @@ hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s) {
 
 hipError_t mfma_probe_launch(const uint16_t* a, const uint16_t* b, float* d, hipStream_t s) {
     hipLaunchKernelGGL(mfma_probe, dim3(1), dim3(64), 0, s, a, b, d);
+    return hipGetLastError();
+}
+
+hipError_t mfma_rate_probe_launch(unsigned blocks, int iters, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(mfma_rate_probe, dim3(blocks), dim3(256), 0, s, reinterpret_cast<f4*>(out), iters);
     return hipGetLastError();
 }
 

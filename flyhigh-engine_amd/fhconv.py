@@ -84,6 +84,7 @@ def load():
                                ctypes.POINTER(ctypes.c_uint8), SZ], ctypes.c_int),
         "fhc_ref_cand_name": ([ctypes.c_uint8, ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_ref_conv_steps": ([ctypes.POINTER(RefConv), ctypes.c_char_p, SZ], ctypes.c_int),
+        "fhc_probe_mfma_rate": ([U32, U32, P, P], ctypes.c_int),
         "fhc_probe_mfma_layout": ([P, P, P, P], ctypes.c_int),
         "fhc_conv_autotune": ([ctypes.POINTER(ConvDesc), P, P, P, P, P, P, ctypes.c_int,
                                ctypes.POINTER(ctypes.c_float)], ctypes.c_int),
@@ -323,3 +324,9 @@ def variant_list(desc: ConvDesc) -> Sequence[int]:
 
 def probe_mfma_layout(a, b, d, stream=None):
     _check(load().fhc_probe_mfma_layout(_ptr(a), _ptr(b), _ptr(d), _stream_handle(stream)), "fhc_probe_mfma_layout")
+
+
+def probe_mfma_rate(blocks, iters, out, stream=None):
+    """Launch the sustained-MFMA-rate probe: blocks * 4 * 8 * iters * 16384 FLOPs (out: blocks * 1024 floats)."""
+    _check(load().fhc_probe_mfma_rate(blocks, iters, _ptr(out), _stream_handle(stream)), "fhc_probe_mfma_rate")
+    return blocks * 4 * 8 * iters * 16384

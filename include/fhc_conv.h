@@ -107,8 +107,9 @@ int fhc_conv_autotune(const fhc_conv_desc* desc, const uint16_t* w_oihw, const u
 /* ---- The planner's choice table ------------------------------------------------------------------------
  * Same key and text format as the reference's TuneTable (ops/conv/tune_cache.rs:6-9, :39-64): one
  * "cin,cout,h,w,stride=code" per line, h and w the INPUT size; malformed lines are skipped. The codes are
- * MI355X variant codes (fhc_variant_name). The table is process-wide and consulted by fhc_conv_plan_create when
- * desc.variant is 0. */
+ * MI355X variant codes (fhc_variant_name); fhc_tune_parse also takes a variant name in place of the code, which
+ * stays valid across builds. The table is process-wide and consulted by fhc_conv_plan_create when desc.variant
+ * is 0. */
 int fhc_tune_parse(const char* text);           /* merges; returns the number of entries read, or -1   */
 int fhc_tune_format(char* text, size_t cap);    /* sorted lines; bytes written, or -1 if cap too small */
 int fhc_tune_clear(void);
@@ -150,6 +151,12 @@ int fhc_ref_conv_steps(const fhc_ref_conv* c, char* text, size_t cap);
  * counterpart in the reference (the reference's own probes of its cooperative-matrix layout are
  * crates/flyhigh-cli/src/cli/coop_tests.rs:7-113). */
 int fhc_probe_mfma_layout(const void* a, const void* b, void* d, void* stream);
+
+/* The dense f16 MFMA rate the device sustains, for rooflines against an achievable peak next to the vendor one:
+ * `blocks` workgroups of 256 threads, each wave issuing 8 * iters v_mfma_f32_16x16x32_f16 (16384 FLOPs each) on
+ * register operands, so one launch does blocks * 4 * 8 * iters * 16384 FLOPs; the caller times it on `stream`.
+ * out: device memory of blocks * 1024 floats. No counterpart in the reference. */
+int fhc_probe_mfma_rate(uint32_t blocks, uint32_t iters, void* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -33,6 +33,24 @@ def test_mfma_fragment_layout():
     assert np.abs(dd.cpu().numpy() - want).max() < 1e-5
 
 
+def test_mfma_rate_probe():
+    # the sustained-rate probe runs and reports a plausible dense f16 rate (between 20% and 110% of 2.5 PFLOP/s)
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    out = torch.empty(cus * 8 * 1024, dtype=torch.float32, device="cuda")
+    fhconv.probe_mfma_rate(cus * 8, 16, out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    flops = fhconv.probe_mfma_rate(cus * 8, 1024, out)
+    e1.record()
+    e1.synchronize()
+    tflops = flops / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    say("mfma rate", round(tflops), "TFLOP/s")
+    assert 500 < tflops < 2750
+    assert torch.isfinite(out).all()
+
+
 def test_golden_vectors_on_the_gpu():
     z = np.load(GOLDEN)
     names = sorted({k.split(".")[0] for k in z.files})

@@ -184,3 +184,30 @@ def test_the_table_steers_the_planner():
         assert fhconv.plan_dry(d)["variant"] == other
     finally:
         fhconv.tune_clear()
+
+
+def test_tune_table_takes_variant_names():
+    # a committed table names variants (stable across builds); the parser maps each name to this build's code
+    fhconv.tune_clear()
+    try:
+        d = fhconv.make_desc(1, 60, 108, 48, 48)
+        names = {fhconv.variant_name(c): c for c in fhconv.variant_list(d)}
+        name = sorted(names)[0]
+        assert fhconv.parse_tune(f"48,48,60,108,1={name}\n48,48,60,108,2=no.such.variant\n") == 1
+        assert fhconv.tune_get(48, 48, 60, 108, 1) == names[name]
+        assert fhconv.tune_get(48, 48, 60, 108, 2) is None
+        assert f"48,48,60,108,1={names[name]}" in fhconv.format_tune()
+        assert fhconv.plan_dry(d)["name"] == name
+    finally:
+        fhconv.tune_clear()
+
+
+def test_committed_choice_table_parses():
+    # every line of the shipped MI355X table names a variant this build has
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "flyhigh-engine_amd", "tune_mi355x.txt")
+    text = open(path).read()
+    fhconv.tune_clear()
+    try:
+        assert fhconv.parse_tune(text) == len([ln for ln in text.splitlines() if ln.strip()])
+    finally:
+        fhconv.tune_clear()
