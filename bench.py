@@ -160,10 +160,10 @@ def cpu_baseline(np, layers, threads, passes=10):
 
 
 def mfma_rate_probe(torch, fhconv, stream):
-    """The sustained dense f16 MFMA rate of this device (TFLOP/s): the library's register-only MFMA probe over
-    8 workgroups per CU, best of 3 timed launches on `stream`."""
+    """The sustained dense f16 MFMA rate of this device (TFLOP/s): the library's register-only MFMA probe, 16
+    independent chains per wave at 4 workgroups (4 waves each) per CU, best of 3 timed launches on `stream`."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    blocks, iters = cus * 8, 2048
+    blocks, iters = cus * 4, 1024
     out = torch.empty(blocks * 1024, dtype=torch.float32, device="cuda")
     best = 0.0
     with torch.cuda.stream(stream):

@@ -137,7 +137,7 @@ struct fhc_conv_plan {
     size_t ws_bytes;
     size_t packed_bytes;
     int device;
-    void* dmem;  // packed weights | bias | slope
+    void* dmem;  // packed weights | bias | negative-value multipliers (upload)
     LaunchFn launch;
 };
 
@@ -408,18 +408,49 @@ void pack_weights(const fhc_conv_plan& p, const uint16_t* w, std::vector<uint16_
                     }
 }
 
+// f16 bits -> f32 (exact)
+static float half_bits_to_float(uint16_t h) {
+    const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+    uint32_t b;
+    if (e == 0x1f) {
+        b = s | 0x7f800000u | (m << 13);
+    } else if (e != 0) {
+        b = s | ((e + 112) << 23) | (m << 13);
+    } else if (m == 0) {
+        b = s;
+    } else {  // subnormal: normalize
+        int k = 0;
+        uint32_t mm = m;
+        while (!(mm & 0x400)) {
+            mm <<= 1;
+            k++;
+        }
+        b = s | ((uint32_t)(113 - k) << 23) | ((mm & 0x3ff) << 13);
+    }
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+// Device layout of a plan: packed weights | bias (f16, np) | negative-value multipliers (f32, np, 16-byte
+// aligned). The multiplier folds the activation into one array, so that every epilogue computes
+// t > 0 ? t : m * t without looking at the activation: the PReLU slope (f16 -> f32 is exact), the LeakyReLU alpha
+// (f32, as the reference's uniform holds it), or 1 for no activation (m * t == t, signed zero included).
 hipError_t upload(fhc_conv_plan& p, const std::vector<uint16_t>& packed, const uint16_t* bias, const uint16_t* slope) {
     const size_t np = (size_t)p.args.np;
     const size_t wbytes = (packed.size() * 2 + 255) & ~(size_t)255;
-    const size_t total = wbytes + 2 * np * 2 + 256;
+    const size_t bbytes = (np * 2 + 15) & ~(size_t)15;
+    const size_t total = wbytes + bbytes + np * 4 + 256;
     std::vector<uint16_t> host(total / 2, 0);
     memcpy(host.data(), packed.data(), packed.size() * 2);
     uint16_t* hb = host.data() + wbytes / 2;
-    uint16_t* hs = hb + np;
+    std::vector<float> neg(np, 1.0f);
     for (uint32_t i = 0; i < p.d.cout; i++) {
         hb[i] = bias[i];
-        hs[i] = slope ? slope[i] : (uint16_t)0x3c00;  // f16 1.0
+        if (p.d.act == FHC_ACT_PRELU) neg[i] = half_bits_to_float(slope[i]);
+        if (p.d.act == FHC_ACT_LEAKY) neg[i] = p.d.alpha;
     }
+    memcpy(reinterpret_cast<char*>(host.data()) + wbytes + bbytes, neg.data(), np * 4);
     hipError_t e = hipMalloc(&p.dmem, total);
     if (e != hipSuccess) {
         p.dmem = nullptr;
@@ -429,7 +460,7 @@ hipError_t upload(fhc_conv_plan& p, const std::vector<uint16_t>& packed, const u
     if (e != hipSuccess) return e;
     p.args.wpk = p.dmem;
     p.args.bias = reinterpret_cast<const uint16_t*>(static_cast<char*>(p.dmem) + wbytes);
-    p.args.slope = p.args.bias + np;
+    p.args.neg = reinterpret_cast<const float*>(static_cast<char*>(p.dmem) + wbytes + bbytes);
     p.packed_bytes = packed.size() * 2;
     return hipSuccess;
 }

@@ -15,7 +15,8 @@ struct ConvKArgs {
     const uint16_t* res;
     const void* wpk;        // packed weights, MFMA A-fragment order: [nb16][chunk][kstep][lane 64][8 halves]
     const uint16_t* bias;   // f16, padded to np
-    const uint16_t* slope;  // f16, padded to np (PReLU only)
+    const float* neg;       // f32 multiplier of negative values, padded to np: the PReLU slope (exact in f32), the
+                            // LeakyReLU alpha, or 1 without activation; 16-byte aligned
     float* part;            // split-K partials [z][n*hout*wout][np] f32 (global split only)
     int n, h, w, cin, cout, hout, wout, pad;
     int xcs, xc0, ycs, yc0, rcs, rc0;
@@ -67,8 +68,9 @@ hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s);
 // Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the
 // operand layouts the conv kernels assume. Device pointers.
 hipError_t mfma_probe_launch(const uint16_t* a, const uint16_t* b, float* d, hipStream_t s);
-// The sustained MFMA rate probe: `blocks` workgroups of 4 waves, each wave 8 * iters 16x16x32 f16 MFMAs (16384
-// FLOPs each); out holds blocks * 256 * 4 floats.
+// The sustained MFMA rate probe: `blocks` workgroups of 4 waves, each wave kRateAcc * iters 16x16x32 f16 MFMAs
+// (16384 FLOPs each); out holds blocks * 256 * 4 floats.
+constexpr int kRateAcc = 16;
 hipError_t mfma_rate_probe_launch(unsigned blocks, int iters, float* out, hipStream_t s);
 
 }  // namespace fhc

@@ -29,14 +29,7 @@ __device__ __forceinline__ void epilogue4(const ConvKArgs& a, size_t pix, int co
     uint16_t o[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        float t = v[i] + h2f(a.bias[co + i]);
-        if (a.act == 1) {
-            const float s = h2f(a.slope[co + i]);
-            t = t > 0.0f ? t : s * t;
-        } else if (a.act == 2) {
-            t = t > 0.0f ? t : a.alpha * t;
-        }
-        o[i] = f2h(t);
+        o[i] = f2h(activate(v[i] + h2f(a.bias[co + i]), a.neg[co + i]));
     }
     const bool full = co + 4 <= a.cout;
     if (a.residual) {
@@ -215,43 +208,6 @@ __global__ __launch_bounds__(256) void splitk_reduce(ConvKArgs a, int ksplit) {
     epilogue4(a, pix, co, s);
 }
 
-__global__ __launch_bounds__(64) void mfma_probe(const uint16_t* A, const uint16_t* B, float* D) {
-    // A row-major 16x32, B row-major 32x16, D row-major 16x16
-    const int l = threadIdx.x;
-    h8 av, bv;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int k = 8 * (l >> 4) + i;
-        av[i] = __builtin_bit_cast(_Float16, A[(l & 15) * 32 + k]);
-        bv[i] = __builtin_bit_cast(_Float16, B[k * 16 + (l & 15)]);
-    }
-    f4 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-#pragma unroll
-    for (int r = 0; r < 4; r++) D[(4 * (l >> 4) + r) * 16 + (l & 15)] = d[r];
-}
-
-// The dense f16 MFMA rate the chip sustains: each wave keeps 8 independent 16x16x32 accumulators busy for `iters`
-// rounds (operands in registers, no memory traffic besides one store per lane).
-__global__ __launch_bounds__(256) void mfma_rate_probe(f4* out, int iters) {
-    h8 a, b;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        a[i] = (_Float16)((threadIdx.x & 7) * 0.001f + i * 0.01f);
-        b[i] = (_Float16)(i * 0.02f);
-    }
-    f4 acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) acc[j] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int it = 0; it < iters; it++) {
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[j], 0, 0, 0);
-    }
-    f4 s = acc[0];
-#pragma unroll
-    for (int j = 1; j < 8; j++) s += acc[j];
-    out[blockIdx.x * 256 + threadIdx.x] = s;
-}
-
 template <int KS, int S, int CFG>
 hipError_t launch_cfg(const ConvKArgs& a, dim3 grid, size_t lds, hipStream_t s) {
     constexpr TileCfg c = kTileCfgs[CFG];
@@ -287,16 +243,6 @@ LaunchFn conv_launcher(int ks, int stride, int cfg) {
 hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s) {
     const size_t total = (size_t)a.n * a.hout * a.wout * ((a.cout + 3) / 4);
     hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a, ksplit);
-    return hipGetLastError();
-}
-
-hipError_t mfma_probe_launch(const uint16_t* a, const uint16_t* b, float* d, hipStream_t s) {
-    hipLaunchKernelGGL(mfma_probe, dim3(1), dim3(64), 0, s, a, b, d);
-    return hipGetLastError();
-}
-
-hipError_t mfma_rate_probe_launch(unsigned blocks, int iters, float* out, hipStream_t s) {
-    hipLaunchKernelGGL(mfma_rate_probe, dim3(blocks), dim3(256), 0, s, reinterpret_cast<f4*>(out), iters);
     return hipGetLastError();
 }
 

@@ -31,23 +31,21 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
-// The multiplier of negative values: PReLU slope, LeakyReLU alpha, 1 without activation (exact). Chosen where the
-// value is used, so that no wait for the slope load lands before the MFMA chain.
-__device__ __forceinline__ float negative_scale(const ConvKArgs& a, float slope) {
-    return a.act == 1 ? slope : a.act == 2 ? a.alpha : 1.0f;
+// The activation with the plan's multiplier of negative values m (PReLU slope, LeakyReLU alpha, or 1: m * t == t
+// for t <= 0, signed zero included): t > 0 ? t : m * t, both sides computed and selected, without a branch.
+__device__ __forceinline__ float activate(float t, float m) {
+    const float n = m * t;
+    return t > 0.0f ? t : n;
 }
 
 // bias, activation, f16 round, residual add rounded again (shaders/conv_tiled.wgsl:57-67), store of 4
-// consecutive channels co..co+3 of output pixel `pix`. sl: the PReLU slopes; rv: the residual's 4 halves (ignored
-// without residual).
+// consecutive channels co..co+3 of output pixel `pix`. ng: the negative-value multipliers; rv: the residual's 4
+// halves (ignored without residual).
 __device__ __forceinline__ void epilogue4r(const ConvKArgs& a, size_t pix, int co, f4 v, const float* b,
-                                          const float* sl, uint2 rv) {
+                                          const float* ng, uint2 rv) {
     uint16_t o[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float t = v[i] + b[i];
-        o[i] = f2h(t > 0.0f ? t : negative_scale(a, sl[i]) * t);
-    }
+    for (int i = 0; i < 4; i++) o[i] = f2h(activate(v[i] + b[i], ng[i]));
     if (a.residual) {
         const uint16_t r[4] = {(uint16_t)(rv.x & 0xffffu), (uint16_t)(rv.x >> 16), (uint16_t)(rv.y & 0xffffu),
                                (uint16_t)(rv.y >> 16)};
@@ -176,9 +174,9 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
     const int tiles = a.n * a.tiles_y * a.tiles_x;
 
     // this wave's weights (its K-steps, once per workgroup) in the order the MFMA chain first uses them, then
-    // bias and slope
+    // bias and negative-value multipliers
     h8 wr[NA][KW];
-    float bias[NA][4], slope[NA][4];
+    float bias[NA][4], neg[NA][4];
     auto load_weights = [&]() {
 #pragma unroll
         for (int j = 0; j < NA; j++) {
@@ -198,14 +196,17 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
             }
         }
 #pragma unroll
-        for (int j = 0; j < NA; j++)
+        for (int j = 0; j < NA; j++) {
+            // unconditional loads (both arrays span np channels): a load under a branch would make the compiler
+            // wait for every outstanding load where the branches join
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                // unconditional loads (the plan always holds a slope array): a load under a branch would make the
-                // compiler wait for every outstanding load where the branches join
-                bias[j][i] = h2f(a.bias[co + 16 * j + i]);
-                slope[j][i] = h2f(a.slope[co + 16 * j + i]);
-            }
+            for (int i = 0; i < 4; i++) bias[j][i] = h2f(a.bias[co + 16 * j + i]);
+            const float4 m = *reinterpret_cast<const float4*>(a.neg + co + 16 * j);
+            neg[j][0] = m.x;
+            neg[j][1] = m.y;
+            neg[j][2] = m.z;
+            neg[j][3] = m.w;
+        }
     };
 
 
@@ -236,9 +237,10 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
             const int pix = e / GPT, g = e - pix * GPT;
             const int iy = pix / IW, ix = pix - iy * IW;
             const int gy = iy0 + iy, gx = ix0 + ix, ch = g * 8;
-            // bitwise &: selects, not branches
+            // bitwise &: selects, not branches. A tile past the last (the persistent loop loads ahead without a
+            // branch) reads zeros.
             const bool ok = ((i + 1) * NT <= HALO || e < HALO) & (gy >= 0) & (gy < a.h) & (gx >= 0) & (gx < a.w) &
-                            (ch < a.cin);
+                            (ch < a.cin) & (t < tiles);
             if constexpr (MODE == 2) {
                 const uint32_t off =
                     ok ? (((uint32_t)(img * a.h + gy) * (uint32_t)a.w + gx) * (uint32_t)a.xcs + a.xc0 + ch) * 2u : kOOB;
@@ -384,7 +386,7 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
                     for (int j = 0; j < NA; j++)
                         if (co + 16 * j < a.cout)
                             epilogue4r(a, ((size_t)img * a.hout + oy) * a.wout + ox, co + 16 * j, acc[f][j], bias[j],
-                                       slope[j], rres[f][j]);
+                                       neg[j], rres[f][j]);
                 }
             }
         }
@@ -413,7 +415,7 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
 #pragma unroll
                 for (int j = 0; j < NA; j++) {
                     const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
-                    const bool ok = (wk == 0) & (oy < a.hout) & (ox < a.wout) & (co + 16 * j < a.cout);
+                    const bool ok = (wk == 0) & (oy < a.hout) & (ox < a.wout) & (co + 16 * j < a.cout) & (tt < tiles);
                     const uint32_t off =
                         ok ? (((uint32_t)(img * a.hout + oy) * (uint32_t)a.wout + ox) * (uint32_t)a.rcs + a.rc0 + co +
                               16 * j) * 2u
@@ -441,7 +443,7 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const float v = acc[f][j][i] + bias[j][i];
-                        const uint16_t h = f2h(v > 0.0f ? v : negative_scale(a, slope[j][i]) * v);
+                        const uint16_t h = f2h(activate(v, neg[j][i]));
                         const uint16_t hr = f2h(h2f(h) + h2f((uint16_t)(rw[i >> 1] >> (16 * (i & 1)))));
                         o[i] = a.residual ? hr : h;
                     }
@@ -461,7 +463,7 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
         load_weights();
         write_halo();
         __syncthreads();
-        if (t + G < tiles) load_halo(t + G);
+        load_halo(t + G);
         load_res_buf(t);
 #pragma unroll
         for (int f = 0; f < FM; f++)
@@ -470,18 +472,20 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
                 ov[f][j] = uint2{0u, 0u};
                 ooff[f][j] = kOOB;
             }
+        // The loads ahead are unconditional (a tile past the last reads zeros): a conditional load makes the
+        // compiler copy its registers where the paths join, and the copy waits for every outstanding load.
         for (; t < tiles; t += G) {
             compute(acc, store_one, std::integral_constant<int, NSQ>{});
             __syncthreads();  // every wave is done reading tile t's halo
-            if (t + G < tiles) write_halo();
+            write_halo();
             __syncthreads();
             epilogue_pack(t);
             if constexpr (NSQ == 0) {
 #pragma unroll
                 for (int k = 0; k < NS; k++) store_one(k);
             }
-            if (t + 2 * G < tiles) load_halo(t + 2 * G);
-            if (t + G < tiles) load_res_buf(t + G);
+            load_halo(t + 2 * G);
+            load_res_buf(t + G);
         }
         if constexpr (NSQ > 0) {
 #pragma unroll
@@ -491,7 +495,7 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
 }
 
 // The one-tile-per-workgroup kernel of the configurations with one channel block per wave: every global load of
-// the tile issued before the first wait (weights, halo, residual, then bias and slope), the halo into LDS, the
+// the tile issued before the first wait (weights, halo, residual, then bias and multipliers), the halo into LDS, the
 // MFMA chain reading LDS one K-step ahead, the epilogue per wave. Measured faster at one tile per workgroup than
 // the buffer loop above, whose deeper pipelining only pays over several tiles.
 template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK, bool VEC>
@@ -546,11 +550,15 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
         if (wk == 0 && a.residual && oy < a.hout && ox < a.wout && co < a.cout)
             rres[f] = load_res4(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, true);
     }
-    float bias[4], slope[4];
+    float bias[4], neg[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        bias[i] = h2f(a.bias[co + i]);
-        slope[i] = h2f(a.slope[co + i]);
+    for (int i = 0; i < 4; i++) bias[i] = h2f(a.bias[co + i]);
+    {
+        const float4 m = *reinterpret_cast<const float4*>(a.neg + co);
+        neg[0] = m.x;
+        neg[1] = m.y;
+        neg[2] = m.z;
+        neg[3] = m.w;
     }
 
 #pragma unroll
@@ -614,7 +622,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
         for (int f = 0; f < FM; f++) {
             const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
             if (oy < a.hout && ox < a.wout)
-                epilogue4r(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, acc[f], bias, slope, rres[f]);
+                epilogue4r(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, acc[f], bias, neg, rres[f]);
         }
     }
 }

@@ -327,6 +327,6 @@ def probe_mfma_layout(a, b, d, stream=None):
 
 
 def probe_mfma_rate(blocks, iters, out, stream=None):
-    """Launch the sustained-MFMA-rate probe: blocks * 4 * 8 * iters * 16384 FLOPs (out: blocks * 1024 floats)."""
+    """Launch the sustained-MFMA-rate probe: blocks * 4 * 16 * iters * 16384 FLOPs (out: blocks * 1024 floats)."""
     _check(load().fhc_probe_mfma_rate(blocks, iters, _ptr(out), _stream_handle(stream)), "fhc_probe_mfma_rate")
-    return blocks * 4 * 8 * iters * 16384
+    return blocks * 4 * 16 * iters * 16384

@@ -153,8 +153,9 @@ int fhc_ref_conv_steps(const fhc_ref_conv* c, char* text, size_t cap);
 int fhc_probe_mfma_layout(const void* a, const void* b, void* d, void* stream);
 
 /* The dense f16 MFMA rate the device sustains, for rooflines against an achievable peak next to the vendor one:
- * `blocks` workgroups of 256 threads, each wave issuing 8 * iters v_mfma_f32_16x16x32_f16 (16384 FLOPs each) on
- * register operands, so one launch does blocks * 4 * 8 * iters * 16384 FLOPs; the caller times it on `stream`.
+ * `blocks` workgroups of 256 threads, each wave issuing 16 * iters v_mfma_f32_16x16x32_f16 (16384 FLOPs each) on
+ * register operands in 16 independent chains, so one launch does blocks * 4 * 16 * iters * 16384 FLOPs; the caller
+ * times it on `stream` (4 workgroups per CU keep every SIMD busy).
  * out: device memory of blocks * 1024 floats. No counterpart in the reference. */
 int fhc_probe_mfma_rate(uint32_t blocks, uint32_t iters, void* out, void* stream);
 

@@ -34,20 +34,21 @@ def test_mfma_fragment_layout():
 
 
 def test_mfma_rate_probe():
-    # the sustained-rate probe runs and reports a plausible dense f16 rate (between 20% and 110% of 2.5 PFLOP/s)
+    # the sustained-rate probe runs and reports a plausible dense f16 rate: between 50% and 110% of 2.5 PFLOP/s
+    # (16 independent chains per wave at 4 waves per SIMD keep the MFMA pipe busy; compiled well it reaches ~90%)
     import torch
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    out = torch.empty(cus * 8 * 1024, dtype=torch.float32, device="cuda")
-    fhconv.probe_mfma_rate(cus * 8, 16, out)
+    out = torch.empty(cus * 4 * 1024, dtype=torch.float32, device="cuda")
+    fhconv.probe_mfma_rate(cus * 4, 16, out)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    flops = fhconv.probe_mfma_rate(cus * 8, 1024, out)
+    flops = fhconv.probe_mfma_rate(cus * 4, 1024, out)
     e1.record()
     e1.synchronize()
     tflops = flops / (e0.elapsed_time(e1) * 1e-3) / 1e12
     say("mfma rate", round(tflops), "TFLOP/s")
-    assert 500 < tflops < 2750
+    assert 1250 < tflops < 2750
     assert torch.isfinite(out).all()
 
 
