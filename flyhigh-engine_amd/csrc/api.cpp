@@ -575,7 +575,7 @@ extern "C" int fhc_conv_plan_create(const fhc_conv_desc* desc, const uint16_t* w
         if (e != hipSuccess) return fail(-1, "fhc_conv_plan_create: hipGetDevice: %s", hipGetErrorString(e));
         if (p->family == 1 && kDirectCfgs[p->cfg].persist) {
             const void* k = nullptr;
-            direct_launcher(p->cfg, &k);
+            direct_launcher(p->cfg, &k, d.residual != 0);
             int per_cu = 0, cus = 0;
             if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, (int)p->threads, 0) != hipSuccess ||
                 hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess)

@@ -61,8 +61,8 @@ using LaunchFn = hipError_t (*)(const ConvKArgs&, dim3 grid, size_t lds, hipStre
 // The launcher of configuration `cfg` for a (kernel size, stride) pair, or nullptr if not instantiated.
 LaunchFn conv_launcher(int ks, int stride, int cfg);
 // The launcher of the direct kernel's configuration `index` (direct_table.h), or nullptr; *kernel receives the
-// kernel's address (for occupancy queries) when not null.
-LaunchFn direct_launcher(int index, const void** kernel);
+// kernel's address (for occupancy queries; persistent configurations have a variant per `residual`) when not null.
+LaunchFn direct_launcher(int index, const void** kernel, bool residual = false);
 hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s);
 
 // Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the

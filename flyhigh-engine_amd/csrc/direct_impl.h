@@ -153,7 +153,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK)
 __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN * WK) : 8))) void conv_direct(
     ConvKArgs a) {
     static_assert(WK == 1 || (WK == 3 && KS == 3), "the K split runs one kernel row per wave");
-    static_assert(!PERSIST || MODE == 2, "the persistent configurations run the buffer loop");
+    static_assert(!PERSIST || MODE >= 2, "the persistent configurations run the buffer loop");
     constexpr bool VEC = MODE > 0;  // 16-byte aligned input
     constexpr int TH = FM * WM, TW = 16, BN = 16 * NA * WN, NT = 64 * WM * WN * WK;
     constexpr int IH = (TH - 1) * S + KS, IW = (TW - 1) * S + KS;
@@ -219,14 +219,12 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
     };
 
     // the halo of tile t, staged in registers: element e = tid + i*NT is 8 channels (group g) of halo pixel pix.
-    // MODE 2 (the persistent loop; 16-byte aligned view within 2^31 bytes, checked by the launcher): buffer loads,
-    // out-of-range lanes (padding, past cin, past the halo) read zeros, so no load sits in a branch; the channels of
-    // a partial group past cin are zeroed when the halo goes to LDS. MODE 1: 16-byte loads; MODE 0: 2-byte loads at
-    // clamped addresses.
+    // MODE 1: 16-byte loads; MODE 0: 2-byte loads at clamped addresses. (MODE 2 and 3, the persistent loop without
+    // and with a residual, have their own buffer-instruction versions below.)
     uint4 pre[NLD];
-    // the input resource spans the full strided extent (n*h*w*xcs halves, which the input buffer holds): a 16-byte
-    // group that crossed the resource's end would read zeros, valid channels included
-    const auto rx = buffer_rsrc(a.x, MODE == 2 ? (uint32_t)((uint64_t)a.n * a.h * a.w * a.xcs * 2) : 0u);
+    // the input resource of the persistent loop spans the full strided extent (n*h*w*xcs halves, which the input
+    // buffer holds): a 16-byte group that crossed the resource's end would read zeros, valid channels included
+    const auto rx = buffer_rsrc(a.x, MODE >= 2 ? (uint32_t)((uint64_t)a.n * a.h * a.w * a.xcs * 2) : 0u);
     auto load_halo = [&](int t) {
         int img, oy0, ox0;
         tile_origin(t, img, oy0, ox0);
@@ -237,32 +235,20 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
             const int pix = e / GPT, g = e - pix * GPT;
             const int iy = pix / IW, ix = pix - iy * IW;
             const int gy = iy0 + iy, gx = ix0 + ix, ch = g * 8;
-            // bitwise &: selects, not branches. A tile past the last (the persistent loop loads ahead without a
-            // branch) reads zeros.
             const bool ok = ((i + 1) * NT <= HALO || e < HALO) & (gy >= 0) & (gy < a.h) & (gx >= 0) & (gx < a.w) &
-                            (ch < a.cin) & (t < tiles);
-            if constexpr (MODE == 2) {
-                const uint32_t off =
-                    ok ? (((uint32_t)(img * a.h + gy) * (uint32_t)a.w + gx) * (uint32_t)a.xcs + a.xc0 + ch) * 2u : kOOB;
-                pre[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
-            } else {
-                pre[i] = uint4{0u, 0u, 0u, 0u};
-                if (ok)
-                    pre[i] = load_group<VEC>(
-                        a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch, a.cin);
-            }
+                            (ch < a.cin);
+            pre[i] = uint4{0u, 0u, 0u, 0u};
+            if (ok)
+                pre[i] = load_group<VEC>(a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch,
+                                         a.cin);
         }
     };
     auto write_halo = [&]() {  // the staged halo into LDS (elements past the halo land in the padding)
 #pragma unroll
         for (int i = 0; i < NLD; i++) {
             const int e = tid + i * NT;
-            {
-                const int pix = e / GPT, g = e - pix * GPT;
-                uint4 v = pre[i];
-                if constexpr (MODE == 2) v = mask_group(v, a.cin - g * 8);
-                *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = v;
-            }
+            const int pix = e / GPT, g = e - pix * GPT;
+            *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = pre[i];
         }
     };
 
@@ -391,63 +377,131 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
             }
         }
     } else {
-        // The persistent configurations: G = gridDim.x resident workgroups loop over tiles t, t + G, ... Input, residual and output go through
-        // buffer instructions (out-of-range lanes: zero loads, dropped stores), so no memory access sits in a branch
-        // and the compiler's waits are exact. Per tile: the MFMA chain, which also issues the previous tile's stores
-        // one per pipeline step; tile t + G's halo (in registers since the previous tile) into LDS; tile t's
-        // epilogue into registers; then tile t + 2G's halo loads and tile t + G's residual loads. Every wait is for
+        // The persistent configurations: G = gridDim.x resident workgroups loop over tiles. Input, residual and
+        // output go through buffer instructions (out-of-range lanes: zero loads, dropped stores), so no memory access
+        // sits in a branch and the compiler's waits are exact. Per tile: the MFMA chain, which also issues the
+        // previous tile's stores one per pipeline step; the next tile's halo (in registers since the previous tile)
+        // into LDS; this tile's epilogue into registers; then the halo loads of the tile after next and the next
+        // tile's residual loads. Every wait is for
         // operations issued a whole chain earlier (the hardware counter that tracks loads also tracks stores, so a
         // load issued before a store cannot be waited for alone), and the stores of all workgroups spread over the
         // chain instead of leaving every CU at once. The first halo is loaded before the weights, so that its wait
         // does not include them and the chain starts as the weights arrive. The launcher checks the alignment and the
         // 2^31-byte extents this needs.
+        // Tile order: workgroup b takes tiles b, b + G, ... (G = gridDim.x), so the tiles in flight at any time are
+        // consecutive in row-major order and their loads stream through contiguous rows of the input. (Ordering the
+        // tiles in column strips per XCD, for L2 locality of the shared halo rows, measured slower: the halo re-reads
+        // already hit in the caches, and the strips break up the row streams.)
         const int G = gridDim.x;
         int t = blockIdx.x;
         if (t >= tiles) return;  // uniform over the workgroup
         const uint64_t pix_out = (uint64_t)a.n * a.hout * a.wout;
         const auto ry = buffer_rsrc(a.y, (uint32_t)view_bytes(pix_out, a.ycs, a.yc0, a.cout));
-        const auto rr = buffer_rsrc(a.res, a.residual ? (uint32_t)view_bytes(pix_out, a.rcs, a.rc0, a.cout) : 0u);
-        auto load_res_buf = [&](int tt) {  // waves of kernel rows 1, 2 (K split) load nothing
+        // MODE 3 adds the residual; MODE 2 issues no residual load at all (each one costs the CU's address unit
+        // as much as a store of the tile)
+        constexpr bool RES = MODE == 3;
+        const auto rr = buffer_rsrc(a.res, RES ? (uint32_t)view_bytes(pix_out, a.rcs, a.rc0, a.cout) : 0u);
+
+        // Every address splits into a per-tile scalar base and a lane part fixed for the whole launch, computed
+        // here once: the loop then spends a few full-rate VALU instructions per memory access. Offsets are 32-bit
+        // unsigned (the launcher keeps every view below 2^31 bytes); a base that wraps below zero at the image's
+        // top-left corner comes back in range for every lane whose access is valid.
+        uint32_t hoff[NLD];  // halo element i: byte offset from the tile's first halo pixel
+        int hpos[NLD];       // its halo row << 16 | column
+        bool hst[NLD];       // inside the halo and below cin (tile-invariant part of its validity)
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * NT;
+            const int pix = e / GPT, g = e - pix * GPT;
+            const int iy = pix / IW, ix = pix - iy * IW;
+            hoff[i] = ((uint32_t)(iy * a.w + ix) * (uint32_t)a.xcs + (uint32_t)(a.xc0 + g * 8)) * 2u;
+            hpos[i] = (iy << 16) | ix;
+            hst[i] = ((i + 1) * NT <= HALO || e < HALO) & (g * 8 < a.cin);
+        }
+        const int lx = lane & 15;
+        const uint32_t rl = ((uint32_t)lx * (uint32_t)a.rcs + (uint32_t)(a.rc0 + co)) * 2u;
+        const uint32_t yl = ((uint32_t)lx * (uint32_t)a.ycs + (uint32_t)(a.yc0 + co)) * 2u;
+        const uint32_t rrow = (uint32_t)a.wout * (uint32_t)a.rcs * 2u, yrow = (uint32_t)a.wout * (uint32_t)a.ycs * 2u;
+
+        // tile tt's halo into registers (a tile past the last reads zeros)
+        auto load_halo_b = [&](int tt) {
             int img, oy0, ox0;
             tile_origin(tt, img, oy0, ox0);
+            const int iy0 = oy0 * S - a.pad, ix0 = ox0 * S - a.pad;
+            const uint32_t base =
+                (((uint32_t)(img * a.h + iy0) * (uint32_t)a.w + (uint32_t)ix0) * (uint32_t)a.xcs) * 2u;
+            const bool tv = tt < tiles;
+#pragma unroll
+            for (int i = 0; i < NLD; i++) {
+                const int gy = iy0 + (hpos[i] >> 16), gx = ix0 + (hpos[i] & 0xffff);
+                const bool ok = hst[i] & tv & ((uint32_t)gy < (uint32_t)a.h) & ((uint32_t)gx < (uint32_t)a.w);
+                pre[i] = __builtin_bit_cast(
+                    uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? base + hoff[i] : kOOB, 0, 0));
+            }
+        };
+        // the staged halo into LDS; the channels of a partial last group past cin are zeroed only when cin is not
+        // a multiple of 8 (a uniform branch around arithmetic)
+        auto write_halo_b = [&]() {
+            if ((a.cin & 7) == 0) {
+#pragma unroll
+                for (int i = 0; i < NLD; i++) {
+                    const int e = tid + i * NT;
+                    const int pix = e / GPT, g = e - pix * GPT;
+                    *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = pre[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < NLD; i++) {
+                    const int e = tid + i * NT;
+                    const int pix = e / GPT, g = e - pix * GPT;
+                    *reinterpret_cast<uint4*>(halo + pix * PSTR + g * 8) = mask_group(pre[i], a.cin - g * 8);
+                }
+            }
+        };
+        // validity of output row f, channel block j of tile (oy0, ox0) for this lane
+        auto out_ok = [&](int oy0, int ox0, int f, int j) {
+            return (wk == 0) & (oy0 + wm * FM + f < a.hout) & (ox0 + lx < a.wout) & (co + 16 * j < a.cout);
+        };
+        auto load_res_buf = [&](int tt) {  // waves of kernel rows 1, 2 (K split) load nothing
+            if constexpr (!RES) return;
+            int img, oy0, ox0;
+            tile_origin(tt, img, oy0, ox0);
+            const uint32_t base = ((uint32_t)(img * a.hout + oy0 + wm * FM) * (uint32_t)a.wout + (uint32_t)ox0) *
+                                  (uint32_t)a.rcs * 2u;
+            const bool tv = tt < tiles;
 #pragma unroll
             for (int f = 0; f < FM; f++)
 #pragma unroll
                 for (int j = 0; j < NA; j++) {
-                    const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
-                    const bool ok = (wk == 0) & (oy < a.hout) & (ox < a.wout) & (co + 16 * j < a.cout) & (tt < tiles);
-                    const uint32_t off =
-                        ok ? (((uint32_t)(img * a.hout + oy) * (uint32_t)a.wout + ox) * (uint32_t)a.rcs + a.rc0 + co +
-                              16 * j) * 2u
-                           : kOOB;
+                    const uint32_t off = out_ok(oy0, ox0, f, j) & tv ? base + f * rrow + rl + 32u * j : kOOB;
                     rres[f][j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rr, off, 0, 0));
                 }
         };
-        // tile t's outputs, packed, and their byte offsets (kOOB: nothing to store)
+        // tile t's outputs, packed, and their byte offsets (kOOB: nothing to store). The residual add is an f16
+        // add: f16(f32(h) + f32(r)) of two f16 values is their sum rounded once to f16 (the f32 sum is exact, or,
+        // when the exponents are more than 12 apart, off by less than a quarter of an f16 ulp of the larger).
         uint2 ov[FM][NA];
         uint32_t ooff[FM][NA];
+        typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
         auto epilogue_pack = [&](int tt) {
             int img, oy0, ox0;
             tile_origin(tt, img, oy0, ox0);
+            const uint32_t base = ((uint32_t)(img * a.hout + oy0 + wm * FM) * (uint32_t)a.wout + (uint32_t)ox0) *
+                                  (uint32_t)a.ycs * 2u;
 #pragma unroll
             for (int f = 0; f < FM; f++)
 #pragma unroll
                 for (int j = 0; j < NA; j++) {
-                    const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
-                    const bool ok = (wk == 0) & (oy < a.hout) & (ox < a.wout) & (co + 16 * j < a.cout);
-                    ooff[f][j] = ok ? (((uint32_t)(img * a.hout + oy) * (uint32_t)a.wout + ox) * (uint32_t)a.ycs +
-                                       a.yc0 + co + 16 * j) * 2u
-                                    : kOOB;
-                    uint16_t o[4];
-                    const uint32_t rw[2] = {rres[f][j].x, rres[f][j].y};
+                    ooff[f][j] = out_ok(oy0, ox0, f, j) ? base + f * yrow + yl + 32u * j : kOOB;
+                    float v[4];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float v = acc[f][j][i] + bias[j][i];
-                        const uint16_t h = f2h(activate(v, neg[j][i]));
-                        const uint16_t hr = f2h(h2f(h) + h2f((uint16_t)(rw[i >> 1] >> (16 * (i & 1)))));
-                        o[i] = a.residual ? hr : h;
+                    for (int i = 0; i < 4; i++) v[i] = activate(acc[f][j][i] + bias[j][i], neg[j][i]);
+                    hh2 p0 = hh2{(_Float16)v[0], (_Float16)v[1]}, p1 = hh2{(_Float16)v[2], (_Float16)v[3]};
+                    if constexpr (RES) {
+                        p0 += __builtin_bit_cast(hh2, rres[f][j].x);
+                        p1 += __builtin_bit_cast(hh2, rres[f][j].y);
                     }
-                    ov[f][j] = uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+                    ov[f][j] = uint2{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1)};
                 }
         };
         auto store_one = [&](int k) {
@@ -459,11 +513,11 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
         // right after the epilogue)
         constexpr int NSQ = WK == 1 ? NS : 0;
 
-        load_halo(t);
+        load_halo_b(t);
         load_weights();
-        write_halo();
+        write_halo_b();
         __syncthreads();
-        load_halo(t + G);
+        load_halo_b(t + G);
         load_res_buf(t);
 #pragma unroll
         for (int f = 0; f < FM; f++)
@@ -477,14 +531,14 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
         for (; t < tiles; t += G) {
             compute(acc, store_one, std::integral_constant<int, NSQ>{});
             __syncthreads();  // every wave is done reading tile t's halo
-            write_halo();
+            write_halo_b();
             __syncthreads();
             epilogue_pack(t);
             if constexpr (NSQ == 0) {
 #pragma unroll
                 for (int k = 0; k < NS; k++) store_one(k);
             }
-            load_halo(t + 2 * G);
+            load_halo_b(t + 2 * G);
             load_res_buf(t + G);
         }
         if constexpr (NSQ > 0) {
@@ -646,7 +700,10 @@ hipError_t launch_direct(const ConvKArgs& a, dim3 grid, size_t lds, hipStream_t 
     const dim3 block(64 * WM * WN * WK);
     if constexpr (PERSIST) {
         if (buffer_path_ok(a)) {
-            hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, true, 2>), grid, block, 0, s, a);
+            if (a.residual)
+                hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, true, 3>), grid, block, 0, s, a);
+            else
+                hipLaunchKernelGGL((conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, true, 2>), grid, block, 0, s, a);
             return hipGetLastError();
         }
         grid.x = (unsigned)(a.n * a.tiles_y * a.tiles_x);
@@ -665,11 +722,14 @@ hipError_t launch_direct(const ConvKArgs& a, dim3 grid, size_t lds, hipStream_t 
     return hipGetLastError();
 }
 
-// the kernel of a configuration, for occupancy queries
+// the kernel of a configuration, for occupancy queries (the persistent loop's variant with or without a residual)
 template <int KS, int S, int CIN32, int FM, int WM, int WN, int NA, int WK, bool PERSIST>
-const void* direct_kernel() {
-    if constexpr (PERSIST || NA > 1)
-        return reinterpret_cast<const void*>(&conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, PERSIST, PERSIST ? 2 : 1>);
+const void* direct_kernel(bool residual) {
+    if constexpr (PERSIST)
+        return residual ? reinterpret_cast<const void*>(&conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, true, 3>)
+                        : reinterpret_cast<const void*>(&conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, true, 2>);
+    else if constexpr (NA > 1)
+        return reinterpret_cast<const void*>(&conv_direct<KS, S, CIN32, FM, WM, WN, NA, WK, false, 1>);
     else
         return reinterpret_cast<const void*>(&conv_tile<KS, S, CIN32, FM, WM, WN, WK, true>);
 }
