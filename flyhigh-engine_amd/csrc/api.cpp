@@ -76,7 +76,8 @@ std::string code_name(uint32_t code) {
           << c.wm << ".n" << 16 * c.na * c.wn;
         if (c.na > 1) o << ".a" << c.na;
         if (c.wk > 1) o << "/rows";
-        if (c.persist) o << "/p";
+        if (c.persist == 1) o << "/p";
+        if (c.persist == 2) o << "/w";
         return o.str();
     }
     const TileCfg& t = kTileCfgs[v.cfg];
@@ -189,6 +190,13 @@ bool configure_direct(fhc_conv_plan& p, int idx, std::string* why) {
         *why = "direct configuration not instantiated";
         return false;
     }
+    // the wave-stream kernel moves whole 16-byte input groups by LDS DMA and has no residual path
+    if (c.persist == 2 && (d.cin % 8 || d.x_cstride % 8 || d.x_c0 % 8 || d.cout % 4 || d.y_cstride % 4 ||
+                           d.y_c0 % 4 || d.residual)) {
+        *why = "the wave-stream configuration needs cin, the input channel stride and offset multiples of 8, cout "
+               "and the output channel stride and offset multiples of 4, and no residual";
+        return false;
+    }
     const int TH = c.fm * c.wm;
     const uint32_t tiles_x = div_ceil(p.g.wout, 16), tiles_y = div_ceil(p.g.hout, TH);
     const uint64_t tiles = (uint64_t)d.n * tiles_y * tiles_x;
@@ -215,8 +223,9 @@ bool configure_direct(fhc_conv_plan& p, int idx, std::string* why) {
     p.code = kDirectBase + (uint32_t)idx;
     // a persistent configuration gets no more workgroups than fit at once (set from the device at plan creation;
     // a dry plan assumes one per CU of an MI355X)
-    p.grid = dim3(c.persist ? (unsigned)std::min<uint64_t>(tiles, std::max(1u, 256u / ntn)) : (unsigned)tiles, ntn, 1);
-    p.threads = 64u * c.wm * c.wn * c.wk;
+    const uint64_t units = c.persist == 2 ? (tiles + 3) / 4 : tiles;  // the wave-stream kernel: a tile per wave
+    p.grid = dim3(c.persist ? (unsigned)std::min<uint64_t>(units, std::max(1u, 256u / ntn)) : (unsigned)tiles, ntn, 1);
+    p.threads = c.persist == 2 ? 256u : 64u * c.wm * c.wn * c.wk;
     p.lds = 0;
     p.ws_bytes = 0;
     p.launch = fn;
@@ -581,7 +590,9 @@ extern "C" int fhc_conv_plan_create(const fhc_conv_desc* desc, const uint16_t* w
                 hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p->device) != hipSuccess)
                 return fail(-1, "fhc_conv_plan_create: occupancy query failed");
             const uint64_t resident = (uint64_t)std::max(1, per_cu) * (uint64_t)std::max(1, cus);
-            p->grid.x = (unsigned)std::min<uint64_t>(p->tiles, std::max<uint64_t>(1, resident / p->grid.y));
+            // the wave-stream kernel runs a tile per wave (4 per workgroup) at a time
+            const uint64_t units = kDirectCfgs[p->cfg].persist == 2 ? (p->tiles + 3) / 4 : p->tiles;
+            p->grid.x = (unsigned)std::min<uint64_t>(units, std::max<uint64_t>(1, resident / p->grid.y));
         }
         std::vector<uint16_t> packed;
         pack_weights(*p, w_oihw, packed);

@@ -473,7 +473,7 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
             for (int f = 0; f < FM; f++)
 #pragma unroll
                 for (int j = 0; j < NA; j++) {
-                    const uint32_t off = out_ok(oy0, ox0, f, j) & tv ? base + f * rrow + rl + 32u * j : kOOB;
+                    const uint32_t off = (out_ok(oy0, ox0, f, j) & tv) ? base + f * rrow + rl + 32u * j : kOOB;
                     rres[f][j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rr, off, 0, 0));
                 }
         };

@@ -306,3 +306,63 @@ def test_persistent_variants_full_size(shape):
         for r0, want in bands.items():
             ok, md, mref = parity(got[0, r0:r0 + 4], want)
             assert ok, (d["name"], r0, md, mref)
+
+
+WAVE_SHAPES = [(2, 37, 53, 32, 40, 1, 1, None, None), (1, 29, 71, 64, 64, 1, 2, None, None),
+               (1, 33, 47, 48, 24, 1, 0, (80, 8), (44, 4)), (1, 41, 67, 32, 64, 2, 1, None, None),
+               (1, 31, 45, 96, 96, 1, 1, None, None)]
+
+
+@pytest.mark.parametrize("shape", WAVE_SHAPES, ids=lambda s: "x".join(map(str, s[:7])))
+def test_wave_variants_match_the_oracle(shape):
+    # the wave-stream variants ("/w": halos by LDS DMA, one tile stream per wave): ragged tiles, several channel
+    # tiles with a partial last one, every activation, stride 2, and views inside poisoned wider tensors
+    n, h, w, cin, cout, s, act, xv, yv = shape
+    c = Case(n, h, w, cin, cout, stride=s, act=act, xv=xv, yv=yv, poison=xv is not None, seed=31)
+    want = c.run_oracle(threads=8)
+    codes = [k for k in fhconv.variant_list(c.fhc_desc()) if fhconv.variant_name(k).endswith("/w")]
+    assert codes
+    sl = slice(c.yc0, c.yc0 + cout)
+    for code in codes:
+        got, plan = c.run_gpu(variant=code, return_plan=True)
+        say("wave", shape[:7], plan.describe()["name"], plan.describe()["grid"])
+        ok, md, mref = parity(got, want, view=sl)
+        assert ok, (fhconv.variant_name(code), md, mref)
+        mask = np.ones(c.ycs, bool)
+        mask[sl] = False
+        assert np.array_equal(got[..., mask], c.y0[..., mask])
+
+
+def test_wave_variant_unaligned_input_falls_back():
+    # an input pointer off 16-byte alignment cannot take the LDS DMA: the launcher runs the one-tile kernel instead
+    import torch
+    c = Case(1, 21, 34, 32, 32, act=1, seed=32)
+    want = c.run_oracle()
+    code = [k for k in fhconv.variant_list(c.fhc_desc()) if fhconv.variant_name(k).endswith("/w")][0]
+    plan = fhconv.ConvPlan(c.fhc_desc(code), c.wt, c.bias, c.slope)
+    dev = torch.device("cuda", 0)
+    xb = torch.zeros(c.x.size + 4, dtype=torch.int16, device=dev)
+    xb[4:] = torch.from_numpy(c.x.ravel().view(np.int16)).to(dev)
+    y = torch.from_numpy(c.y0.view(np.int16)).to(dev)
+    plan.run(xb[4:], y)
+    torch.cuda.synchronize()
+    ok, md, mref = parity(y.cpu().numpy().view(np.uint16), want)
+    assert ok, (md, mref)
+
+
+@pytest.mark.parametrize("shape", [(1, 272, 480, 64, 64, 1, 1), (1, 544, 960, 32, 64, 2, 1), (1, 136, 240, 32, 32, 1, 2)],
+                         ids=["s1", "s2", "c1"])
+def test_wave_variants_full_size(shape):
+    # the 1080p/4 and /8 sizes: every wave runs several rounds of its two-buffer loop; rows checked in bands
+    n, h, w, cin, cout, s, act = shape
+    c = Case(n, h, w, cin, cout, stride=s, act=act, seed=19)
+    codes = [k for k in fhconv.variant_list(c.fhc_desc()) if fhconv.variant_name(k).endswith("/w")]
+    assert codes
+    bands = {r0: oracle_rows(c, r0, r0 + 4, threads=8) for r0 in (0, c.hout // 2 - 2, c.hout - 4)}
+    for code in codes:
+        got, plan = c.run_gpu(variant=code, return_plan=True)
+        d = plan.describe()
+        say("wave", d["name"], d["grid"], d["tiles"])
+        for r0, want in bands.items():
+            ok, md, mref = parity(got[0, r0:r0 + 4], want)
+            assert ok, (d["name"], r0, md, mref)
