@@ -48,7 +48,8 @@ class Net:
 
     def __init__(self, layers, seed, torch, np, fhconv, tune=True):
         self.layers = layers
-        self.plans, self.bufs, self.tuned = {}, {}, {}
+        self.plans, self.bufs, self.tuned, self.params = {}, {}, {}, {}
+        self.pairs = {}  # first layer's name -> (pair plan, second layer)
         dev = torch.device("cuda", 0)
         rng = np.random.default_rng(seed)
         f16 = lambda a: torch.from_numpy(np.asarray(a, np.float32).astype(np.float16))  # noqa: E731
@@ -79,10 +80,36 @@ class Net:
                 if p.workspace_bytes else None
             self.plans[L.name] = p
             self.bufs[L.name] = (x, y, r, ws)
+            self.params[L.name] = (d, wt, b, s)
 
-    def run(self, names=None):
+    def fuse(self, pairs, torch, fhconv, stream, time_fn):
+        """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; the
+        tile height (2 or 4 rows) timed on the real buffers, the faster kept."""
+        for A, B, res_mid in pairs:
+            da, wa, ba, sa = self.params[A.name]
+            db, wb, bb, sb = self.params[B.name]
+            x = self.bufs[A.name][0]
+            _, y, r, _ = self.bufs[B.name]
+            rx = None if res_mid else r
+            best = None
+            for th in (2, 4):
+                pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th)
+                us = time_fn(lambda i=0, pp=pp: pp.run(x, y, rx, stream=stream))
+                if best is None or us < best[1]:
+                    best = (pp, us)
+            self.pairs[A.name] = (best[0], B, round(best[1], 3), res_mid)
+
+    def run(self, names=None, fused=False):
+        skip = {B.name for _, B, _, _ in self.pairs.values()} if fused else set()
         for L in self.layers:
-            if names is None or L.name in names:
+            if names is not None and L.name not in names:
+                continue
+            if fused and L.name in self.pairs:
+                pp, B, _, res_mid = self.pairs[L.name]
+                x = self.bufs[L.name][0]
+                _, y, r, _ = self.bufs[B.name]
+                pp.run(x, y, None if res_mid else r)
+            elif L.name not in skip:
                 x, y, r, ws = self.bufs[L.name]
                 self.plans[L.name].run(x, y, r, ws)
 
@@ -131,6 +158,32 @@ def layer_timing(torch, np, fhconv, net, L, reps, graphs, cold_bytes, stream):
                 frac_warm=round(t_roof * 1e6 / warm, 4),
                 tflops_cold=round(L.flops / cold / 1e6, 2), gbs_cold=round(L.bytes / cold / 1e3, 1),
                 cold_sets=nsets)
+
+
+def pair_timing(torch, net, a_name, reps, graphs, cold_bytes, stream):
+    """Warm and cold per-launch time of a fused pair (graph of `reps` launches), with its algorithmic work: both
+    convs' FLOPs; bytes of the first's input, the second's output and residual, both weights (the intermediate
+    stays on chip)."""
+    pp, B, _, res_mid = net.pairs[a_name]
+    x = net.bufs[a_name][0]
+    _, y, r, _ = net.bufs[B.name]
+    r = None if res_mid else r
+    warm = time_graph(torch, lambda i=0: pp.run(x, y, r), reps, graphs, stream)
+    per = x.numel() * 2 + y.numel() * 2 + (r.numel() * 2 if r is not None else 0)
+    nsets = max(2, min(4096, -(-cold_bytes // per)))
+    creps = -(-max(reps, nsets) // nsets) * nsets
+    sets = [(torch.empty_like(x).uniform_(-1, 1), torch.empty_like(y),
+             torch.empty_like(r).uniform_(-1, 1) if r is not None else None) for _ in range(nsets)]
+    cold = time_graph(torch, lambda i=0: pp.run(sets[i % nsets][0], sets[i % nsets][1], sets[i % nsets][2]),
+                      creps, graphs, stream)
+    del sets
+    d = pp.describe()
+    flops, nbytes = d["flops"], d["bytes"]
+    bound, t_roof = roof(flops, nbytes)
+    return dict(name=a_name + "+" + B.name, variant=d["name"], us_warm=round(warm, 3), us_cold=round(cold, 3),
+                flops=flops, bytes=nbytes, bound=bound, roof_us=round(t_roof * 1e6, 3),
+                frac_cold=round(t_roof * 1e6 / cold, 4), frac_warm=round(t_roof * 1e6 / warm, 4),
+                tflops_cold=round(flops / cold / 1e6, 2), gbs_cold=round(nbytes / cold / 1e3, 1), cold_sets=nsets)
 
 
 def cpu_baseline(np, layers, threads, passes=10):
@@ -282,6 +335,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the single-layer configurations")
     ap.add_argument("--no-layers", action="store_true", help="skip the per-layer timing of the frame workload")
     ap.add_argument("--no-autotune", action="store_true", help="plan with the heuristic only (no per-shape timing)")
+    ap.add_argument("--no-fuse", action="store_true", help="one launch per conv (no fused conv pairs)")
     ap.add_argument("--tune", help="plan with this choice table (cin,cout,h,w,stride=code lines) instead of autotuning")
     ap.add_argument("--pmc-layer", help="only run this frame layer --pmc-reps times over rotating (cold) buffers, "
                                         "then a copy of known size as many times: the workload of the rocprofv3 "
@@ -322,18 +376,45 @@ def main():
     torch.cuda.synchronize()
     if args.pmc_layer:
         return pmc_workload(args, torch, net, stream)
+    fused = not args.no_fuse
+    if fused:
+        net.fuse(flyhighfg.fusible_pairs(layers), torch, fhconv, stream,
+                 lambda fn: time_graph(torch, fn, 50, 5, stream))
+        log(f"bench: {len(net.pairs)} conv pairs fused: " +
+            ", ".join(f"{a}+{B.name} ({pp.describe()['name']})" for a, (pp, B, _, _) in net.pairs.items()))
+    launches = len(layers) - len(net.pairs)
+
+    # the fused step against the one-launch-per-conv step: the pairs' outputs (and everything after them) agree
+    # within the parity bar (a pair computes each conv as its separate launch does, up to the f32 summation order)
+    fuse_check = None
+    if fused:
+        with torch.cuda.stream(stream):
+            net.run()
+            stream.synchronize()
+            ref = {L.name: net.bufs[L.name][1].float().clone() for L in layers if L.name not in net.pairs}
+            net.run(fused=True)
+            stream.synchronize()
+        worst = 0.0
+        for name, want in ref.items():
+            got = net.bufs[name][1].float()
+            worst = max(worst, float((got - want).abs().max()) / max(float(want.abs().max()), 1e-30))
+        fuse_check = dict(max_rel_diff=round(worst, 6), tol=1e-2, ok=worst <= 1e-2)
+        log(f"bench: fused step vs one launch per conv: max |diff| / max |ref| = {worst:.2e}")
+        del ref
 
     # one graph per step (pair then mid: one launch per frame), and one per stage for the stage split
-    gs, gp, gm = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    gs, gp, gm, gu = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        net.run()
+        net.run(fused=fused)
         stream.synchronize()
         with torch.cuda.graph(gs, stream=stream):
-            net.run()
+            net.run(fused=fused)
         with torch.cuda.graph(gp, stream=stream):
-            net.run({L.name for L in pair})
+            net.run({L.name for L in pair}, fused=fused)
         with torch.cuda.graph(gm, stream=stream):
-            net.run({L.name for L in mid})
+            net.run({L.name for L in mid}, fused=fused)
+        with torch.cuda.graph(gu, stream=stream):
+            net.run()
         for _ in range(args.warmup):
             gs.replay()
         torch.cuda.synchronize()
@@ -361,7 +442,8 @@ def main():
             b.synchronize()
         return a.elapsed_time(b) * 1e3 / n
 
-    pair_us, mid_us = stage_us(gp), stage_us(gm)
+    pair_us, mid_us, unfused_us = stage_us(gp), stage_us(gm), stage_us(gu)
+    log(f"bench: pair {pair_us:.2f} us + mid {mid_us:.2f} us; one launch per conv: {unfused_us:.2f} us")
 
     per_layer = []
     if not args.no_layers:
@@ -369,6 +451,11 @@ def main():
             per_layer.append(layer_timing(torch, np, fhconv, net, L, args.reps, args.graphs,
                                           args.cold_mb << 20, stream))
             log("layer", json.dumps(per_layer[-1]))
+    per_pair = []
+    if not args.no_layers:
+        for a_name in net.pairs:
+            per_pair.append(pair_timing(torch, net, a_name, args.reps, args.graphs, args.cold_mb << 20, stream))
+            log("pair", json.dumps(per_pair[-1]))
     cfg_layers = []
     if not args.no_configs:
         for c in (1, 2, 3):
@@ -388,7 +475,9 @@ def main():
     # achieved rate is the algorithmic bytes (or FLOPs) per launch over its cold per-launch time
     roofline = None
     if per_layer:
-        dom = max(per_layer, key=lambda r: r["us_warm"])
+        fused_b = {B.name for _, B, _, _ in net.pairs.values()}
+        step_launches = [r for r in per_layer if r["name"] not in net.pairs and r["name"] not in fused_b] + per_pair
+        dom = max(step_launches, key=lambda r: r["us_warm"])
         unit = "GB/s" if dom["bound"] == "hbm" else "TFLOP/s"
         achieved = dom["gbs_cold"] if dom["bound"] == "hbm" else dom["tflops_cold"]
         peak = HBM_PEAK / 1e9 if dom["bound"] == "hbm" else MFMA_F16_PEAK / 1e12
@@ -416,12 +505,16 @@ def main():
         warmup=args.warmup, ms_per_step=round(ms_per_step, 6), higher_is_better=True, scaling="weak",
         vs_baseline=None, dtype="f16", data="synthetic",
         config=dict(workload="FlyHighFG conv layers of one pair()+mid() at 1080p (network 856x480 padded to "
-                             "864x480), NHWC f16, conv-only; the A/B encoders run as batch-2 convs",
+                             "864x480), NHWC f16, conv-only; the A/B encoders run as batch-2 convs"
+                             + ("; consecutive convs whose intermediate has no other reader run as fused pairs"
+                                if net.pairs else ""),
                     frame="1920x1080", network=f"{net_w}x{net_h}", conv_layers=25,
-                    conv_launches=len(layers), k=1, parallelism="single GPU"),
-        pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), event_ms_per_step=round(ev_ms, 6),
+                    conv_launches=launches, fused_pairs=[f"{a}+{B.name}" for a, (_, B, _, _) in net.pairs.items()],
+                    k=1, parallelism="single GPU"),
+        pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), unfused_step_us=round(unfused_us, 3),
+        fuse_check=fuse_check, event_ms_per_step=round(ev_ms, 6),
         submit_us_per_step=round(t_submit * 1e6 / args.steps, 3),
-        roofline=roofline, cpu_baseline=cpu, layers=per_layer, config_layers=cfg_layers,
+        roofline=roofline, cpu_baseline=cpu, layers=per_layer, pairs=per_pair, config_layers=cfg_layers,
         tune_table=fhconv.format_tune().splitlines(),
     )
     print(json.dumps(out), flush=True)

@@ -127,8 +127,8 @@ struct fhc_conv_plan {
     fhc_conv_desc d;
     Geometry g;
     uint32_t code;
-    int family;       // 0 chunked implicit GEMM, 1 direct
-    int cfg;          // chunked: tile configuration id; direct: index into kDirectCfgs
+    int family;       // 0 chunked implicit GEMM, 1 direct, 2 fused pair (this plan is the pair's first conv)
+    int cfg;          // chunked: tile configuration id; direct: index into kDirectCfgs; pair: into kPairCfgs
     uint32_t tiles;   // spatial output tiles (all images)
     uint32_t ksplit;  // effective global split count (1 = none)
     ConvKArgs args;   // kernel arguments with the tensor pointers left null
@@ -140,6 +140,9 @@ struct fhc_conv_plan {
     int device;
     void* dmem;  // packed weights | bias | negative-value multipliers (upload)
     LaunchFn launch;
+    fhc_conv_plan* pair_b;  // fused pair: the second conv (its weights and output geometry), owned
+    int res_mid;            // fused pair: the second conv's residual is the first's output
+    PairLaunchFn pair_launch;
 };
 
 namespace fhc {
@@ -527,6 +530,24 @@ bool plan_choose(const fhc_conv_desc& d, fhc_conv_plan& p, std::string* why) {
 std::string describe_json(const fhc_conv_plan* p) {
     const fhc_conv_desc& d = p->d;
     int rows, chans, wm, wnv, wk;
+    if (p->family == 2) {
+        const PairCfg& c = kPairCfgs[p->cfg];
+        const fhc_conv_desc& b = p->pair_b->d;
+        const double fa = 2.0 * d.n * p->g.hout * p->g.wout * d.cout * d.cin * 9;
+        const double fb = 2.0 * b.n * p->g.hout * p->g.wout * b.cout * b.cin * 9;
+        const double out_el = (double)b.n * p->g.hout * p->g.wout * b.cout;
+        const double bytes = 2.0 * ((double)d.n * d.h * d.w * d.cin + out_el + 9.0 * (d.cout * d.cin + b.cout * b.cin) +
+                                    d.cout + b.cout + (d.act == FHC_ACT_PRELU ? d.cout : 0) +
+                                    (b.act == FHC_ACT_PRELU ? b.cout : 0) + (b.residual && !p->res_mid ? out_el : 0));
+        char buf[700];
+        snprintf(buf, sizeof buf,
+                 "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d\",\"family\":\"pair\",\"cfg\":%d,"
+                 "\"tile_rows\":%d,\"tile_cols\":%d,\"res_mid\":%d,\"tiles\":%u,\"grid\":[%u,%u],\"threads\":%u,"
+                 "\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
+                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, p->cfg, c.th, kPairTileW, p->res_mid,
+                 p->tiles, p->grid.x, p->grid.y, p->threads, p->g.hout, p->g.wout, fa + fb, bytes);
+        return buf;
+    }
     if (p->family == 1) {
         const DirectCfg& c = kDirectCfgs[p->cfg];
         rows = c.fm * c.wm;
@@ -630,6 +651,22 @@ extern "C" int fhc_conv_run(const fhc_conv_plan* p, const void* x, void* y, cons
         int dev = -1;
         if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
             return fail(-1, "fhc_conv_run: the plan belongs to device %d, the current device is %d", p->device, dev);
+        if (p->family == 2) {  // fused pair: x is the first conv's input, y and res the second's output and residual
+            const fhc_conv_plan* q = p->pair_b;
+            if (q->d.residual && !p->res_mid && !res)
+                return fail(-1, "fhc_conv_run: the pair's second conv has a residual but res is NULL");
+            PairKArgs pk{p->args, q->args, p->res_mid};
+            pk.a.x = static_cast<const uint16_t*>(x);
+            pk.a.xvec = ((uintptr_t)x % 16 == 0) && pk.a.xcs % 8 == 0 && pk.a.xc0 % 8 == 0;
+            pk.b.y = static_cast<uint16_t*>(y);
+            pk.b.res = static_cast<const uint16_t*>(res);
+            pk.b.yvec = ((uintptr_t)y % 8 == 0) && pk.b.ycs % 4 == 0 && pk.b.yc0 % 4 == 0;
+            pk.b.rvec = pk.b.residual && !p->res_mid && ((uintptr_t)res % 8 == 0) && pk.b.rcs % 4 == 0 &&
+                        pk.b.rc0 % 4 == 0 && pk.b.cout % 4 == 0;
+            hipError_t e = p->pair_launch(pk, p->grid, static_cast<hipStream_t>(stream));
+            if (e != hipSuccess) return fail(-1, "fhc_conv_run: launch: %s", hipGetErrorString(e));
+            return 0;
+        }
         ConvKArgs a = p->args;
         a.x = static_cast<const uint16_t*>(x);
         a.y = static_cast<uint16_t*>(y);
@@ -674,8 +711,121 @@ extern "C" int fhc_conv_plan_dry(const fhc_conv_desc* desc, char* json, size_t c
 
 extern "C" void fhc_conv_plan_destroy(fhc_conv_plan* p) {
     if (!p) return;
+    if (p->pair_b) fhc_conv_plan_destroy(p->pair_b);
     if (p->dmem) (void)hipFree(p->dmem);
     delete p;
+}
+
+namespace fhc {
+namespace {
+
+// One conv of a fused pair as a direct-kernel weight layout (CIN32 input channels per tap, nb 16-channel blocks):
+// the plan's geometry, arguments, packed weights and device arrays.
+hipError_t pair_part(fhc_conv_plan& p, const fhc_conv_desc& d, int cin32, int nb, const uint16_t* w,
+                     const uint16_t* bias, const uint16_t* slope) {
+    p.d = d;
+    p.dmem = nullptr;
+    p.pair_b = nullptr;
+    p.g.hout = (d.h + 2 * d.pad - d.kh) / d.stride + 1;
+    p.g.wout = (d.w + 2 * d.pad - d.kw) / d.stride + 1;
+    p.g.taps = d.kh * d.kw;
+    p.g.cin8 = div_ceil(d.cin, 8) * 8;
+    fill_args(p);
+    p.args.cc = cin32;
+    p.args.nchunks = 1;
+    p.args.ksteps = 9 * cin32 / 32;
+    p.args.tapgroups = 9 * cin32 / 8;
+    p.args.chunks_per_split = 1;
+    p.args.ntn = 1;
+    p.args.np = 16 * nb;
+    p.family = 1;
+    p.ksplit = 1;
+    std::vector<uint16_t> packed;
+    pack_weights(p, w, packed);
+    return upload(p, packed, bias, slope);
+}
+
+}  // namespace
+}  // namespace fhc
+
+extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
+                                         const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
+                                         const uint16_t* bias_b, const uint16_t* slope_b, uint32_t flags,
+                                         fhc_conv_plan** out) {
+    return guard(-1, [&]() -> int {
+        if (!desc_a || !desc_b || !w_a || !bias_a || !w_b || !bias_b || !out)
+            return fail(-1, "fhc_conv_pair_plan_create: NULL argument");
+        *out = nullptr;
+        fhc_conv_desc A = *desc_a, B = *desc_b;
+        for (fhc_conv_desc* d : {&A, &B}) {
+            if (d->x_cstride == 0) d->x_cstride = d->cin;
+            if (d->y_cstride == 0) d->y_cstride = d->cout;
+            if (d->r_cstride == 0) d->r_cstride = d->cout;
+        }
+        std::string why;
+        if (!valid_desc(A, &why)) return fail(-1, "fhc_conv_pair_plan_create: first conv: %s", why.c_str());
+        if (!valid_desc(B, &why)) return fail(-1, "fhc_conv_pair_plan_create: second conv: %s", why.c_str());
+        const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0;
+        const uint32_t th_req = (flags >> 8) & 0xffu;
+        if ((flags & ~(FHC_PAIR_RES_MID | 0xff00u)) != 0) return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
+        const uint32_t ha = (A.h + 2 * A.pad - A.kh) / A.stride + 1, wa = (A.w + 2 * A.pad - A.kw) / A.stride + 1;
+        if (A.kh != 3 || B.kh != 3 || B.stride != 1 || A.residual)
+            return fail(-1, "fhc_conv_pair_plan_create: the pair is a 3x3 conv (stride 1 or 2, no residual) then a 3x3 "
+                            "stride-1 conv");
+        if (B.n != A.n || B.h != ha || B.w != wa || B.cin != A.cout)
+            return fail(-1, "fhc_conv_pair_plan_create: the second conv must read the first's output (n %u/%u, h %u/%u, "
+                            "w %u/%u, channels %u/%u)", B.n, A.n, B.h, ha, B.w, wa, B.cin, A.cout);
+        if (res_mid && (!B.residual || B.cout != B.cin))
+            return fail(-1, "fhc_conv_pair_plan_create: a residual from the first conv's output needs the second conv's "
+                            "residual flag and cout == cin");
+        if ((A.act == FHC_ACT_PRELU && !slope_a) || (B.act == FHC_ACT_PRELU && !slope_b))
+            return fail(-1, "fhc_conv_pair_plan_create: PReLU needs a slope");
+        const int ca32 = (int)div_ceil(A.cin, 32) * 32, cb32 = (int)div_ceil(B.cin, 32) * 32;
+        const int nba = (int)div_ceil(A.cout, 16), nbb = (int)div_ceil(B.cout, 16);
+        const uint64_t tiles2 = (uint64_t)A.n * div_ceil(ha, 2) * div_ceil(wa, kPairTileW);
+        int idx = -1;
+        for (int i = 0; i < kNumPair; i++) {
+            const PairCfg& c = kPairCfgs[i];
+            if (c.sa != (int)A.stride || c.ca32 != ca32 || c.cb32 != cb32 || c.nba != nba || c.nbb != nbb) continue;
+            // default: 4-row tiles unless that leaves under 256 workgroups
+            const int th = th_req ? (int)th_req : (tiles2 / 2 >= 256 ? 4 : 2);
+            if (c.th == th) idx = i;
+        }
+        if (idx < 0)
+            return fail(-1, "fhc_conv_pair_plan_create: no fused pair instantiated for stride %u, %u -> %u -> %u "
+                            "channels%s", A.stride, A.cin, A.cout, B.cout, th_req ? " at that tile height" : "");
+        const PairCfg& c = kPairCfgs[idx];
+        auto pa = std::make_unique<fhc_conv_plan>();
+        auto pb = std::make_unique<fhc_conv_plan>();
+        hipError_t e = hipGetDevice(&pa->device);
+        if (e != hipSuccess) return fail(-1, "fhc_conv_pair_plan_create: hipGetDevice: %s", hipGetErrorString(e));
+        pb->device = pa->device;
+        e = pair_part(*pb, B, cb32, nbb, w_b, bias_b, slope_b);
+        if (e == hipSuccess) e = pair_part(*pa, A, ca32, nba, w_a, bias_a, slope_a);
+        if (e != hipSuccess) {
+            if (pa->dmem) (void)hipFree(pa->dmem);
+            if (pb->dmem) (void)hipFree(pb->dmem);
+            return fail(-1, "fhc_conv_pair_plan_create: device upload: %s", hipGetErrorString(e));
+        }
+        const uint32_t tiles_x = div_ceil(wa, kPairTileW), tiles_y = div_ceil(ha, (uint32_t)c.th);
+        pb->args.tiles_x = (int)tiles_x;
+        pb->args.tiles_y = (int)tiles_y;
+        pa->family = 2;
+        pa->cfg = idx;
+        pa->code = 0;
+        pa->tiles = (uint32_t)((uint64_t)A.n * tiles_y * tiles_x);
+        pa->grid = dim3(pa->tiles, 1, 1);
+        pa->threads = 64u * (uint32_t)std::max(c.nba, c.nbb);
+        pa->lds = 0;
+        pa->ws_bytes = 0;
+        pa->launch = nullptr;
+        pa->res_mid = res_mid ? 1 : 0;
+        pa->pair_launch = pair_launcher(idx);
+        pa->pair_b = pb.release();
+        *out = pa.release();
+        clear_error();
+        return 0;
+    });
 }
 
 // ---- choice table -------------------------------------------------------------------------------------------

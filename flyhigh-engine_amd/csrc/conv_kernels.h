@@ -65,6 +65,27 @@ LaunchFn conv_launcher(int ks, int stride, int cfg);
 LaunchFn direct_launcher(int index, const void** kernel, bool residual = false);
 hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s);
 
+// A fused pair of 3x3 convs (pair_impl.h): B (stride 1) reads A's output, which stays in LDS.
+struct PairKArgs {
+    ConvKArgs a, b;  // a: x, A's weights, bias, multipliers, input geometry; b: y, res, B's weights, output geometry
+    int res_mid;     // B's residual is A's output
+};
+constexpr int kPairTileW = 14;  // output columns per tile (B's 16-pixel MFMA block reads 16 + 2 columns of A)
+// The instantiated pairs: A's stride, A's and B's input channels padded to 32, A's and B's output channel blocks
+// of 16, and the output rows per tile.
+struct PairCfg {
+    int sa, ca32, cb32, nba, nbb, th;
+};
+constexpr int kNumPair = 8;
+inline constexpr PairCfg kPairCfgs[kNumPair] = {
+    {2, 32, 64, 3, 3, 2}, {2, 32, 64, 3, 3, 4},  // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
+    {1, 64, 64, 3, 3, 2}, {1, 64, 64, 3, 3, 4},  // 48 -> 48 -> 48 (FiLM head, fine block)
+    {1, 32, 32, 2, 2, 2}, {1, 32, 32, 2, 2, 4},  // <= 32 -> 32 -> 32 (refine head)
+    {1, 32, 32, 2, 1, 2}, {1, 32, 32, 2, 1, 4},  // <= 32 -> 32 -> 16 (refine head output)
+};
+using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);
+PairLaunchFn pair_launcher(int index);
+
 // Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the
 // operand layouts the conv kernels assume. Device pointers.
 hipError_t mfma_probe_launch(const uint16_t* a, const uint16_t* b, float* d, hipStream_t s);

@@ -1,0 +1,181 @@
+// Two 3x3 convs fused into one launch, B after A (B: stride 1, pad 1, reading A's output), with A's output tile
+// kept in LDS: the chains of small layers that a frame runs back to back (the encoder's conv pairs, the FiLM and
+// refine heads, the fine block) pay one launch and one round of weight and halo loads instead of two.
+//
+// One workgroup per output tile of B: TH rows x 14 columns. B's 16-pixel MFMA column block then reads 16 + 2
+// columns of A's output, so A is computed on (TH + 2) rows x 16 columns (one MFMA column block) around the tile,
+// from an input halo of ((TH + 1) * SA + 3) x (15 * SA + 3) pixels. A's output is rounded to f16 as the unfused
+// path stores it, and written to LDS as zero outside the image (B's zero padding), so both layers compute exactly
+// what the two separate launches compute.
+//
+// WN = max(NBA, NBB) waves: wave wn runs A's 16-channel block wn (if wn < NBA) over all A rows, then B's block wn
+// (if wn < NBB) over all B rows, weights of both resident in registers. K order, packing and LDS pixel stride are
+// those of direct_impl.h (k = tap * CIN32 + ci, channels padded to 32 per tap, pixel stride CIN32 + 8 halves).
+// B's residual is either the external tensor of the descriptor or A's output at the same pixel (read from LDS).
+#pragma once
+#include "direct_impl.h"
+
+namespace fhc {
+
+// The q-ring MFMA chain over an LDS tile (as direct_impl.h's WK == 1 chain, one channel block): output rows
+// f = 0 .. FM-1 of stride S read tile rows f * S + ky; operand q = (kx * M + m) * R + r is read once and feeds every
+// (f, ky) use; reads run D operands ahead. base: the lane's pixel (row 0, column (lane & 15) * S) and channel group.
+template <int FM, int S, int M, int IW, int PSTR>
+__device__ __forceinline__ void pair_chain(f4 (&acc)[FM], const h8* wr, const uint16_t* base) {
+    constexpr int KS = 3, R = (FM - 1) * S + KS, NQ = KS * M * R, D = NQ < 4 ? NQ : 4;
+    auto rd = [&](int q) {
+        const int c = q / R, r = q % R, kx = c / M, m = c % M;
+        return *reinterpret_cast<const h8*>(base + (r * IW + kx) * PSTR + m * 32);
+    };
+#pragma unroll
+    for (int f = 0; f < FM; f++) acc[f] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    h8 b[D + 1];
+#pragma unroll
+    for (int q = 0; q < D; q++) b[q] = rd(q);
+#pragma unroll
+    for (int q = 0; q < NQ; q++) {
+        if (q + D < NQ) b[(q + D) % (D + 1)] = rd(q + D);
+        const int c = q / R, r = q % R, kx = c / M, m = c % M;
+#pragma unroll
+        for (int f = FM - 1; f >= 0; f--) {
+            const int ky = r - f * S;
+            if (ky < 0 || ky >= KS) continue;
+            acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wr[(ky * KS + kx) * M + m], b[q % (D + 1)], acc[f], 0, 0, 0);
+        }
+    }
+    pin_mfma_pipeline<0, NQ, D, R, FM, S, KS, 1, 0>();
+}
+
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, bool VEC>
+__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB)) void conv_pair(PairKArgs pk) {
+    constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN, TWB = kPairTileW;
+    constexpr int FA = TH + 2;                                  // A's rows per tile
+    constexpr int IHA = (FA - 1) * SA + 3, IWA = 15 * SA + 3;   // A's input halo
+    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32;
+    constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;     // A's output tile in LDS: FA rows x 18 pixels
+    constexpr int HALO = IHA * IWA * GPA, NLD = (HALO + NT - 1) / NT;
+    static_assert(NBA * 16 <= CB32, "A's channel blocks exceed B's input channels");
+    __shared__ __align__(16) uint16_t hin[IHA * IWA * PSA];
+    __shared__ __align__(16) uint16_t mid[FA * MW * PSB];
+    const ConvKArgs& a = pk.a;
+    const ConvKArgs& b = pk.b;
+
+    const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6, lx = lane & 15;
+    const int t = blockIdx.x;
+    const int tx = t % b.tiles_x, rr = t / b.tiles_x;
+    const int ty = rr % b.tiles_y, img = rr / b.tiles_y;
+    const int oy0 = ty * TH, ox0 = tx * TWB;  // B's tile origin; A's tile starts one row and column earlier
+    const int wa = wn < NBA ? wn : NBA - 1, wb = wn < NBB ? wn : NBB - 1;  // loads stay unconditional
+    const int coa = wa * 16 + 4 * (lane >> 4), cob = wb * 16 + 4 * (lane >> 4);
+
+    // every global load first: both layers' weights, A's input halo, B's external residual, biases, multipliers
+    h8 wra[9 * MA], wrb[9 * MB];
+    {
+        const h8* wp = reinterpret_cast<const h8*>(a.wpk) + (size_t)wa * 9 * MA * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < 9 * MA; s++) wra[s] = wp[s * 64];
+        const h8* wq = reinterpret_cast<const h8*>(b.wpk) + (size_t)wb * 9 * MB * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < 9 * MB; s++) wrb[s] = wq[s * 64];
+    }
+    uint4 pre[NLD];
+    const bool whole = VEC && a.xc0 + ((a.cin + 7) & ~7) <= a.xcs;  // partial groups load as one 16-byte group
+    {
+        const int iy0 = (oy0 - 1) * SA - a.pad, ix0 = (ox0 - 1) * SA - a.pad;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * NT;
+            const int pix = e / GPA, g = e - pix * GPA;
+            const int iy = pix / IWA, ix = pix - iy * IWA;
+            const int gy = iy0 + iy, gx = ix0 + ix, ch = g * 8;
+            pre[i] = uint4{0u, 0u, 0u, 0u};
+            if ((i + 1) * NT <= HALO || e < HALO)
+                if (gy >= 0 && gy < a.h && gx >= 0 && gx < a.w && ch < a.cin)
+                    pre[i] = load_group<VEC>(
+                        a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch, a.cin, whole);
+        }
+    }
+    uint2 rres[TH];
+#pragma unroll
+    for (int f = 0; f < TH; f++) {
+        rres[f] = uint2{0u, 0u};
+        const int oy = oy0 + f, ox = ox0 + lx;
+        if (b.residual && !pk.res_mid && lx < TWB && oy < b.hout && ox < b.wout && cob < b.cout)
+            rres[f] = load_res4(b, ((size_t)img * b.hout + oy) * b.wout + ox, cob, true);
+    }
+    float biasa[4], nega[4], biasb[4], negb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        biasa[i] = h2f(a.bias[coa + i]);
+        biasb[i] = h2f(b.bias[cob + i]);
+    }
+    {
+        const float4 m = *reinterpret_cast<const float4*>(a.neg + coa);
+        const float4 n = *reinterpret_cast<const float4*>(b.neg + cob);
+        nega[0] = m.x, nega[1] = m.y, nega[2] = m.z, nega[3] = m.w;
+        negb[0] = n.x, negb[1] = n.y, negb[2] = n.z, negb[3] = n.w;
+    }
+
+    // A's output channels past its blocks (up to B's padded input channels) are zero for every pixel
+    if constexpr (NBA * 16 < CB32) {
+        constexpr int G0 = NBA * 2, GN = CB32 / 8 - G0, NZ = FA * MW * GN;
+        for (int e = tid; e < NZ; e += NT) {
+            const int pix = e / GN, g = G0 + e % GN;
+            *reinterpret_cast<uint4*>(mid + pix * PSB + g * 8) = uint4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NLD; i++) {
+        const int e = tid + i * NT;
+        if ((i + 1) * NT <= HALO || e < HALO) {
+            const int pix = e / GPA, g = e - pix * GPA;
+            *reinterpret_cast<uint4*>(hin + pix * PSA + g * 8) = whole ? mask_group(pre[i], a.cin - g * 8) : pre[i];
+        }
+    }
+    __syncthreads();
+
+    // A over FA rows x 16 columns; its f16 output (zero outside the image) into the LDS tile
+    if (wn < NBA) {
+        f4 acc[FA];
+        pair_chain<FA, SA, MA, IWA, PSA>(acc, wra, hin + (lx * SA) * PSA + (lane >> 4) * 8);
+#pragma unroll
+        for (int f = 0; f < FA; f++) {
+            const int oy = oy0 - 1 + f, ox = ox0 - 1 + lx;  // A's output pixel
+            const bool in = (oy >= 0) & (oy < a.hout) & (ox >= 0) & (ox < a.wout);
+            uint16_t o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = in ? f2h(activate(acc[f][i] + biasa[i], nega[i])) : (uint16_t)0;
+            *reinterpret_cast<uint2*>(mid + (f * MW + lx) * PSB + coa) =
+                uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+        }
+    }
+    __syncthreads();
+
+    // B over TH rows x 16 columns (the first 14 stored); columns 16 and 17 of the LDS tile feed only the two
+    // discarded lanes
+    if (wn < NBB) {
+        f4 acc[TH];
+        pair_chain<TH, 1, MB, MW, PSB>(acc, wrb, mid + lx * PSB + (lane >> 4) * 8);
+#pragma unroll
+        for (int f = 0; f < TH; f++) {
+            const int oy = oy0 + f, ox = ox0 + lx;
+            if (lx < TWB && oy < b.hout && ox < b.wout && cob < b.cout) {
+                const uint2 rv = pk.res_mid ? *reinterpret_cast<const uint2*>(mid + ((f + 1) * MW + lx + 1) * PSB + cob)
+                                            : rres[f];
+                epilogue4r(b, ((size_t)img * b.hout + oy) * b.wout + ox, cob, acc[f], biasb, negb, rv);
+            }
+        }
+    }
+}
+
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH>
+hipError_t launch_pair(const PairKArgs& pk, dim3 grid, hipStream_t s) {
+    const dim3 block(64 * (NBA > NBB ? NBA : NBB));
+    if (pk.a.xvec)
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, true>), grid, block, 0, s, pk);
+    else
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, false>), grid, block, 0, s, pk);
+    return hipGetLastError();
+}
+
+}  // namespace fhc

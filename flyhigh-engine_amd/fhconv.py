@@ -73,6 +73,8 @@ def load():
         "fhc_conv_run": ([P, P, P, P, P, P], ctypes.c_int),
         "fhc_conv_describe": ([P, ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_conv_plan_destroy": ([P], None),
+        "fhc_conv_pair_plan_create": ([ctypes.POINTER(ConvDesc), P, P, P, ctypes.POINTER(ConvDesc), P, P, P, U32,
+                                       ctypes.POINTER(P)], ctypes.c_int),
         "fhc_conv_plan_dry": ([ctypes.POINTER(ConvDesc), ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_tune_parse": ([ctypes.c_char_p], ctypes.c_int),
         "fhc_tune_format": ([ctypes.c_char_p, SZ], ctypes.c_int),
@@ -209,6 +211,44 @@ class ConvPlan:
             self.close()
         except Exception:
             pass
+
+
+PAIR_RES_MID = 1
+
+
+class ConvPairPlan(ConvPlan):
+    """Two convs fused into one launch (fhc_conv_pair_plan_create): A (3x3, stride 1 or 2) then B (3x3 stride 1) on
+    A's output, which stays on chip. run(x, y, res) takes A's input, B's output and B's external residual; with
+    res_mid B's residual is A's output. tile_rows 0 lets the library choose (2 or 4)."""
+
+    def __init__(self, desc_a: ConvDesc, w_a, bias_a, slope_a, desc_b: ConvDesc, w_b, bias_b, slope_b,
+                 res_mid=False, tile_rows=0):
+        L = load()
+        self.desc, self.desc_b = desc_a, desc_b
+        arrays = []
+        for d, w, b, sl in ((desc_a, w_a, bias_a, slope_a), (desc_b, w_b, bias_b, slope_b)):
+            wa, wp = _host_u16(w)
+            ba, bp = _host_u16(b)
+            sa, sp = _host_u16(sl)
+            if wa is None or wa.size != d.cout * d.cin * d.kh * d.kw:
+                raise FhcError("weights must hold cout*cin*kh*kw f16 values (OIHW)")
+            if ba is None or ba.size != d.cout or (sa is not None and sa.size != d.cout):
+                raise FhcError("bias and slope must hold cout f16 values")
+            arrays.append((wa, wp, ba, bp, sa, sp))
+        (_, wpa, _, bpa, _, spa), (_, wpb, _, bpb, _, spb) = arrays
+        flags = (PAIR_RES_MID if res_mid else 0) | (int(tile_rows) << 8)
+        h = ctypes.c_void_p()
+        _check(L.fhc_conv_pair_plan_create(ctypes.byref(desc_a), wpa, bpa, spa, ctypes.byref(desc_b), wpb, bpb,
+                                           spb, flags, ctypes.byref(h)), "fhc_conv_pair_plan_create")
+        self._h = h
+        ho, wo = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(L.fhc_conv_out_shape(h, ctypes.byref(ho), ctypes.byref(wo)), "fhc_conv_out_shape")
+        self.hout, self.wout = ho.value, wo.value
+        self.workspace_bytes = 0
+
+    def out_elems(self):
+        d = self.desc_b
+        return d.n * self.hout * self.wout * (d.y_cstride or d.cout)
 
 
 @dataclass

@@ -121,6 +121,27 @@ def flyhighfg_layers(net_w: int = 864, net_h: int = 480, k: int = 1, batch_encod
     return L
 
 
+# Consecutive convs of models/graph.json whose intermediate tensor has no other reader (enc.e1's output is also the
+# residual that enc.e2's "add" takes: the pair's second conv adds the first's output): each pair can run as one fused
+# launch (fhc_conv_pair_plan_create). (first conv, second conv, second's residual is the first's output)
+FUSIBLE_PAIRS = [("enc.e1", "enc.e2", True), ("fine.r2", "fine.r3", False), ("film.h1", "film.h2", False),
+                 ("refine.q1", "refine.q2", False), ("refine.q3", "refine.q4", False)]
+
+
+def fusible_pairs(layers: List[ConvLayer]):
+    """(first, second, res_mid) layer pairs of `layers` that FUSIBLE_PAIRS names (by prefix: enc.e1.ab, fine.r2.0)."""
+    by = {L.name: L for L in layers}
+    out = []
+    for a_pre, b_pre, res_mid in FUSIBLE_PAIRS:
+        for L in layers:
+            if L.name == a_pre or L.name.startswith(a_pre + "."):
+                b_name = b_pre + L.name[len(a_pre):]
+                B = by.get(b_name)
+                if B is not None and B.chain == L.name and (not res_mid or B.res_from == L.name):
+                    out.append((L, B, res_mid))
+    return out
+
+
 def config_layers(cfg: int) -> List[ConvLayer]:
     """The single-layer / ladder benchmark configurations C1-C3 (batch 1, NHWC f16)."""
     if cfg == 1:  # 3x3 32->32 at 1080p/8, LeakyReLU(0.1)

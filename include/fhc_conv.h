@@ -90,6 +90,25 @@ int fhc_conv_describe(const fhc_conv_plan* plan, char* json, size_t cap);
 
 void fhc_conv_plan_destroy(fhc_conv_plan* plan);
 
+/* A fused pair: conv A (3x3, stride 1 or 2, no residual) and conv B (3x3 stride 1) that reads A's output, run as
+ * one launch with A's output kept on chip. It serves two consecutive conv ops of the graph whose intermediate
+ * tensor has no other reader (graph.json's enc.e1 -> enc.e2, film.h1 -> film.h2, refine.q1 -> q2, q3 -> q4,
+ * fine.r2 -> r3). The result is the one the two plans give run in turn: A's output is rounded to f16 and B reads it
+ * with zero padding. No counterpart in the reference, which records one dispatch per conv op
+ * (net/build.rs:209-278).
+ * desc_b: B's n, h, w and cin equal A's n, output height and width and cout; B's input view is ignored.
+ * flags: FHC_PAIR_RES_MID makes B's residual A's output (B.residual set, B.cout == B.cin; graph.json's
+ * "add" of e2 and e1), else B's residual, if any, is the `res` tensor of fhc_conv_run; bits 8-15: output rows
+ * per tile (2 or 4; 0: the planner's choice). The plan runs with fhc_conv_run (x: A's input, y and res: B's output
+ * and residual), is described by fhc_conv_describe (family "pair") and freed by fhc_conv_plan_destroy. The
+ * instantiated pairs cover, in channels A.cin -> A.cout -> B.cout: stride 2 <= 32 -> 33..48 -> 33..48, and stride
+ * 1 33..64 -> 33..48 -> 33..48, <= 32 -> 17..32 -> 17..32 and <= 32 -> 17..32 -> <= 16; other shapes are an
+ * error status. */
+#define FHC_PAIR_RES_MID 1u
+int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
+                              const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
+                              const uint16_t* bias_b, const uint16_t* slope_b, uint32_t flags, fhc_conv_plan** out);
+
 /* The planner's choice for a descriptor without creating a plan (no device call): the same JSON as
  * fhc_conv_describe, sizes included. For host-side tests and for tools that print the plan of a graph
  * (the reference's FH_TUNE_VERBOSE listing, ops/conv/autotune.rs:217-228). Bytes written or -1. */

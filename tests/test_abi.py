@@ -6,6 +6,7 @@ import os
 import re
 import threading
 
+import numpy as np
 import pytest
 
 from fhtest import ROOT, fhconv
@@ -112,3 +113,23 @@ def test_last_error_is_thread_local():
     t.start()
     t.join()
     assert mine and seen == [""]
+
+
+def test_pair_plan_rejects_what_it_cannot_fuse():
+    # shape checks happen before any device call: a mismatched second conv, an unsupported channel combination and
+    # a residual from the first conv without the residual flag are error statuses
+    wa = np.zeros(36 * 3 * 9, np.uint16)
+    ba = np.zeros(36, np.uint16)
+    wb = np.zeros(36 * 36 * 9, np.uint16)
+    bb = np.zeros(36, np.uint16)
+    a = fhconv.make_desc(1, 40, 60, 3, 36, stride=2, act=0)
+    for b, flags in [(fhconv.make_desc(1, 21, 30, 36, 36, act=0), 0),        # B's height is not A's output height
+                     (fhconv.make_desc(1, 20, 30, 35, 36, act=0), 0),        # B's cin is not A's cout
+                     (fhconv.make_desc(1, 20, 30, 36, 36, act=0), 1),        # residual from A without B's flag
+                     (fhconv.make_desc(1, 20, 30, 36, 36, act=0, stride=2), 0)]:  # B must be stride 1
+        with pytest.raises(fhconv.FhcError):
+            fhconv.ConvPairPlan(a, wa, ba, None, b, wb if b.cin == 36 else np.zeros(36 * b.cin * 9, np.uint16), bb, None,
+                                res_mid=bool(flags))
+    big = fhconv.make_desc(1, 20, 30, 36, 96, act=0)  # 96 output channels: no pair instantiated
+    with pytest.raises(fhconv.FhcError):
+        fhconv.ConvPairPlan(a, wa, ba, None, big, np.zeros(96 * 36 * 9, np.uint16), np.zeros(96, np.uint16), None)

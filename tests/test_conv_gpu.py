@@ -366,3 +366,46 @@ def test_wave_variants_full_size(shape):
         for r0, want in bands.items():
             ok, md, mref = parity(got[0, r0:r0 + 4], want)
             assert ok, (d["name"], r0, md, mref)
+
+
+# fused pairs: n, h, w, cin, cmid, cout, A's stride, A's and B's activation, B's residual (None, "mid": A's
+# output, "ext": a tensor), A's input view, B's output view
+PAIR_CASES = [(2, 50, 90, 3, 36, 36, 2, 1, 1, "mid", (8, 0), None),
+              (1, 33, 61, 48, 48, 48, 1, 1, 1, None, None, None),
+              (1, 41, 75, 14, 24, 24, 1, 1, 1, None, (16, 0), None),
+              (1, 37, 53, 24, 24, 3, 1, 1, 0, None, None, (8, 0)),
+              (1, 30, 44, 48, 48, 48, 1, 2, 1, "ext", None, None)]
+
+
+@pytest.mark.parametrize("case", PAIR_CASES, ids=lambda c: "x".join(map(str, c[:7])) + (f"-{c[9]}" if c[9] else ""))
+@pytest.mark.parametrize("th", [2, 4])
+def test_pair_matches_the_two_convs(case, th):
+    # the fused pair against the oracle run twice (A, then B on A's f16 output): ragged tiles, stride 2, a residual
+    # from A's output or from a tensor, a padded input view with NaN past cin, an output view inside a wider tensor
+    import torch
+    n, h, w, cin, cmid, cout, sa, act_a, act_b, res, xv, yv = case
+    A = Case(n, h, w, cin, cmid, stride=sa, act=act_a, xv=xv, poison=xv is not None, seed=41)
+    ya = A.run_oracle(threads=8)
+    B = Case(n, A.hout, A.wout, cmid, cout, act=act_b, residual=res is not None, yv=yv, poison=yv is not None, seed=42)
+    B.x = ya
+    if res == "mid":
+        B.res = ya
+    want = B.run_oracle(threads=8)
+    plan = fhconv.ConvPairPlan(A.fhc_desc(), A.wt, A.bias, A.slope if act_a == 1 else None, B.fhc_desc(), B.wt, B.bias,
+                               B.slope if act_b == 1 else None, res_mid=res == "mid", tile_rows=th)
+    d = plan.describe()
+    say("pair", case, d["name"], d["grid"], d["tiles"])
+    assert d["family"] == "pair" and d["tile_rows"] == th
+    dev = torch.device("cuda", 0)
+    x = torch.from_numpy(np.ascontiguousarray(A.x).view(np.int16)).to(dev)
+    y = torch.from_numpy(np.ascontiguousarray(B.y0).view(np.int16)).to(dev)
+    r = torch.from_numpy(np.ascontiguousarray(B.res).view(np.int16)).to(dev) if res == "ext" else None
+    plan.run(x, y, r)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().view(np.uint16)
+    sl = slice(B.yc0, B.yc0 + cout)
+    ok, md, mref = parity(got, want, view=sl)
+    assert ok, (d["name"], md, mref)
+    mask = np.ones(B.ycs, bool)
+    mask[sl] = False
+    assert np.array_equal(got[..., mask], B.y0[..., mask])
