@@ -84,7 +84,7 @@ class Net:
 
     def fuse(self, pairs, torch, fhconv, stream, time_fn):
         """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; the
-        tile height (2 or 4 rows) timed on the real buffers, the faster kept."""
+        tile height (2 or 4 rows) and wave rows (1 or 2) timed on the real buffers, the fastest kept."""
         for A, B, res_mid in pairs:
             da, wa, ba, sa = self.params[A.name]
             db, wb, bb, sb = self.params[B.name]
@@ -92,8 +92,8 @@ class Net:
             _, y, r, _ = self.bufs[B.name]
             rx = None if res_mid else r
             best = None
-            for th in (2, 4):
-                pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th)
+            for th, wm in ((2, 1), (4, 1), (2, 2), (4, 2)):
+                pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th, wave_rows=wm)
                 us = time_fn(lambda i=0, pp=pp: pp.run(x, y, rx, stream=stream))
                 if best is None or us < best[1]:
                     best = (pp, us)

@@ -541,11 +541,11 @@ std::string describe_json(const fhc_conv_plan* p) {
                                     (b.act == FHC_ACT_PRELU ? b.cout : 0) + (b.residual && !p->res_mid ? out_el : 0));
         char buf[700];
         snprintf(buf, sizeof buf,
-                 "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d\",\"family\":\"pair\",\"cfg\":%d,"
-                 "\"tile_rows\":%d,\"tile_cols\":%d,\"res_mid\":%d,\"tiles\":%u,\"grid\":[%u,%u],\"threads\":%u,"
-                 "\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
-                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, p->cfg, c.th, kPairTileW, p->res_mid,
-                 p->tiles, p->grid.x, p->grid.y, p->threads, p->g.hout, p->g.wout, fa + fb, bytes);
+                 "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d.w%d\",\"family\":\"pair\",\"cfg\":%d,"
+                 "\"tile_rows\":%d,\"tile_cols\":%d,\"wave_rows\":%d,\"res_mid\":%d,\"tiles\":%u,\"grid\":[%u,%u],"
+                 "\"threads\":%u,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
+                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, c.wm, p->cfg, c.th, kPairTileW, c.wm,
+                 p->res_mid, p->tiles, p->grid.x, p->grid.y, p->threads, p->g.hout, p->g.wout, fa + fb, bytes);
         return buf;
     }
     if (p->family == 1) {
@@ -766,8 +766,8 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         if (!valid_desc(A, &why)) return fail(-1, "fhc_conv_pair_plan_create: first conv: %s", why.c_str());
         if (!valid_desc(B, &why)) return fail(-1, "fhc_conv_pair_plan_create: second conv: %s", why.c_str());
         const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0;
-        const uint32_t th_req = (flags >> 8) & 0xffu;
-        if ((flags & ~(FHC_PAIR_RES_MID | 0xff00u)) != 0) return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
+        const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu;
+        if ((flags & ~(FHC_PAIR_RES_MID | 0xfff00u)) != 0) return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
         const uint32_t ha = (A.h + 2 * A.pad - A.kh) / A.stride + 1, wa = (A.w + 2 * A.pad - A.kw) / A.stride + 1;
         if (A.kh != 3 || B.kh != 3 || B.stride != 1 || A.residual)
             return fail(-1, "fhc_conv_pair_plan_create: the pair is a 3x3 conv (stride 1 or 2, no residual) then a 3x3 "
@@ -789,11 +789,12 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
             if (c.sa != (int)A.stride || c.ca32 != ca32 || c.cb32 != cb32 || c.nba != nba || c.nbb != nbb) continue;
             // default: 4-row tiles unless that leaves under 256 workgroups
             const int th = th_req ? (int)th_req : (tiles2 / 2 >= 256 ? 4 : 2);
-            if (c.th == th) idx = i;
+            if (c.th == th && c.wm == (wm_req ? (int)wm_req : 1)) idx = i;
         }
         if (idx < 0)
             return fail(-1, "fhc_conv_pair_plan_create: no fused pair instantiated for stride %u, %u -> %u -> %u "
-                            "channels%s", A.stride, A.cin, A.cout, B.cout, th_req ? " at that tile height" : "");
+                            "channels%s", A.stride, A.cin, A.cout, B.cout,
+                        th_req || wm_req ? " at that tile height and wave split" : "");
         const PairCfg& c = kPairCfgs[idx];
         auto pa = std::make_unique<fhc_conv_plan>();
         auto pb = std::make_unique<fhc_conv_plan>();
@@ -815,7 +816,7 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         pa->code = 0;
         pa->tiles = (uint32_t)((uint64_t)A.n * tiles_y * tiles_x);
         pa->grid = dim3(pa->tiles, 1, 1);
-        pa->threads = 64u * (uint32_t)std::max(c.nba, c.nbb);
+        pa->threads = 64u * (uint32_t)std::max(c.nba, c.nbb) * (uint32_t)c.wm;
         pa->lds = 0;
         pa->ws_bytes = 0;
         pa->launch = nullptr;

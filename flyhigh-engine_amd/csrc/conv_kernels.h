@@ -72,16 +72,20 @@ struct PairKArgs {
 };
 constexpr int kPairTileW = 14;  // output columns per tile (B's 16-pixel MFMA block reads 16 + 2 columns of A)
 // The instantiated pairs: A's stride, A's and B's input channels padded to 32, A's and B's output channel blocks
-// of 16, and the output rows per tile.
+// of 16, the output rows per tile and the wave rows that split them.
 struct PairCfg {
-    int sa, ca32, cb32, nba, nbb, th;
+    int sa, ca32, cb32, nba, nbb, th, wm;
 };
-constexpr int kNumPair = 8;
+constexpr int kNumPair = 16;
 inline constexpr PairCfg kPairCfgs[kNumPair] = {
-    {2, 32, 64, 3, 3, 2}, {2, 32, 64, 3, 3, 4},  // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
-    {1, 64, 64, 3, 3, 2}, {1, 64, 64, 3, 3, 4},  // 48 -> 48 -> 48 (FiLM head, fine block)
-    {1, 32, 32, 2, 2, 2}, {1, 32, 32, 2, 2, 4},  // <= 32 -> 32 -> 32 (refine head)
-    {1, 32, 32, 2, 1, 2}, {1, 32, 32, 2, 1, 4},  // <= 32 -> 32 -> 16 (refine head output)
+    // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
+    {2, 32, 64, 3, 3, 2, 1}, {2, 32, 64, 3, 3, 4, 1}, {2, 32, 64, 3, 3, 2, 2}, {2, 32, 64, 3, 3, 4, 2},
+    // 48 -> 48 -> 48 (FiLM head, fine block)
+    {1, 64, 64, 3, 3, 2, 1}, {1, 64, 64, 3, 3, 4, 1}, {1, 64, 64, 3, 3, 2, 2}, {1, 64, 64, 3, 3, 4, 2},
+    // <= 32 -> 32 -> 32 (refine head)
+    {1, 32, 32, 2, 2, 2, 1}, {1, 32, 32, 2, 2, 4, 1}, {1, 32, 32, 2, 2, 2, 2}, {1, 32, 32, 2, 2, 4, 2},
+    // <= 32 -> 32 -> 16 (refine head output)
+    {1, 32, 32, 2, 1, 2, 1}, {1, 32, 32, 2, 1, 4, 1}, {1, 32, 32, 2, 1, 2, 2}, {1, 32, 32, 2, 1, 4, 2},
 };
 using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);
 PairLaunchFn pair_launcher(int index);

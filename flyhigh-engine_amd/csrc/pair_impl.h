@@ -8,8 +8,9 @@
 // path stores it, and written to LDS as zero outside the image (B's zero padding), so both layers compute exactly
 // what the two separate launches compute.
 //
-// WN = max(NBA, NBB) waves: wave wn runs A's 16-channel block wn (if wn < NBA) over all A rows, then B's block wn
-// (if wn < NBB) over all B rows, weights of both resident in registers. K order, packing and LDS pixel stride are
+// WN x WM waves, WN = max(NBA, NBB): wave (wn, wm) runs A's 16-channel block wn (if wn < NBA) over its share
+// (1 / WM) of A's rows, then B's block wn (if wn < NBB) over its share of B's rows, weights of both resident in
+// registers (WM = 2 halves the chains and doubles the workgroup's weight loads). K order, packing and LDS pixel stride are
 // those of direct_impl.h (k = tap * CIN32 + ci, channels padded to 32 per tap, pixel stride CIN32 + 8 halves).
 // B's residual is either the external tensor of the descriptor or A's output at the same pixel (read from LDS).
 #pragma once
@@ -46,10 +47,12 @@ __device__ __forceinline__ void pair_chain(f4 (&acc)[FM], const h8* wr, const ui
     pin_mfma_pipeline<0, NQ, D, R, FM, S, KS, 1, 0>();
 }
 
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, bool VEC>
-__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB)) void conv_pair(PairKArgs pk) {
-    constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN, TWB = kPairTileW;
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC>
+__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(PairKArgs pk) {
+    constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN * WM, TWB = kPairTileW;
     constexpr int FA = TH + 2;                                  // A's rows per tile
+    constexpr int FAW = FA / WM, THW = TH / WM;                 // rows per wave
+    static_assert(FA % WM == 0 && TH % WM == 0, "rows split evenly over the wave rows");
     constexpr int IHA = (FA - 1) * SA + 3, IWA = 15 * SA + 3;   // A's input halo
     constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32;
     constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;     // A's output tile in LDS: FA rows x 18 pixels
@@ -60,7 +63,7 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB)) void conv_pair(PairKA
     const ConvKArgs& a = pk.a;
     const ConvKArgs& b = pk.b;
 
-    const int tid = threadIdx.x, lane = tid & 63, wn = tid >> 6, lx = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, wn = (tid >> 6) % WN, wm = (tid >> 6) / WN, lx = lane & 15;
     const int t = blockIdx.x;
     const int tx = t % b.tiles_x, rr = t / b.tiles_x;
     const int ty = rr % b.tiles_y, img = rr / b.tiles_y;
@@ -95,11 +98,11 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB)) void conv_pair(PairKA
                         a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch, a.cin, whole);
         }
     }
-    uint2 rres[TH];
+    uint2 rres[THW];
 #pragma unroll
-    for (int f = 0; f < TH; f++) {
+    for (int f = 0; f < THW; f++) {
         rres[f] = uint2{0u, 0u};
-        const int oy = oy0 + f, ox = ox0 + lx;
+        const int oy = oy0 + wm * THW + f, ox = ox0 + lx;
         if (b.residual && !pk.res_mid && lx < TWB && oy < b.hout && ox < b.wout && cob < b.cout)
             rres[f] = load_res4(b, ((size_t)img * b.hout + oy) * b.wout + ox, cob, true);
     }
@@ -136,15 +139,16 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB)) void conv_pair(PairKA
 
     // A over FA rows x 16 columns; its f16 output (zero outside the image) into the LDS tile
     if (wn < NBA) {
-        f4 acc[FA];
-        pair_chain<FA, SA, MA, IWA, PSA>(acc, wra, hin + (lx * SA) * PSA + (lane >> 4) * 8);
+        f4 acc[FAW];
+        pair_chain<FAW, SA, MA, IWA, PSA>(acc, wra, hin + (wm * FAW * SA * IWA + lx * SA) * PSA + (lane >> 4) * 8);
 #pragma unroll
-        for (int f = 0; f < FA; f++) {
+        for (int fw = 0; fw < FAW; fw++) {
+            const int f = wm * FAW + fw;
             const int oy = oy0 - 1 + f, ox = ox0 - 1 + lx;  // A's output pixel
             const bool in = (oy >= 0) & (oy < a.hout) & (ox >= 0) & (ox < a.wout);
             uint16_t o[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = in ? f2h(activate(acc[f][i] + biasa[i], nega[i])) : (uint16_t)0;
+            for (int i = 0; i < 4; i++) o[i] = in ? f2h(activate(acc[fw][i] + biasa[i], nega[i])) : (uint16_t)0;
             *reinterpret_cast<uint2*>(mid + (f * MW + lx) * PSB + coa) =
                 uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
         }
@@ -154,27 +158,28 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB)) void conv_pair(PairKA
     // B over TH rows x 16 columns (the first 14 stored); columns 16 and 17 of the LDS tile feed only the two
     // discarded lanes
     if (wn < NBB) {
-        f4 acc[TH];
-        pair_chain<TH, 1, MB, MW, PSB>(acc, wrb, mid + lx * PSB + (lane >> 4) * 8);
+        f4 acc[THW];
+        pair_chain<THW, 1, MB, MW, PSB>(acc, wrb, mid + (wm * THW * MW + lx) * PSB + (lane >> 4) * 8);
 #pragma unroll
-        for (int f = 0; f < TH; f++) {
+        for (int fw = 0; fw < THW; fw++) {
+            const int f = wm * THW + fw;
             const int oy = oy0 + f, ox = ox0 + lx;
             if (lx < TWB && oy < b.hout && ox < b.wout && cob < b.cout) {
                 const uint2 rv = pk.res_mid ? *reinterpret_cast<const uint2*>(mid + ((f + 1) * MW + lx + 1) * PSB + cob)
-                                            : rres[f];
-                epilogue4r(b, ((size_t)img * b.hout + oy) * b.wout + ox, cob, acc[f], biasb, negb, rv);
+                                            : rres[fw];
+                epilogue4r(b, ((size_t)img * b.hout + oy) * b.wout + ox, cob, acc[fw], biasb, negb, rv);
             }
         }
     }
 }
 
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
 hipError_t launch_pair(const PairKArgs& pk, dim3 grid, hipStream_t s) {
-    const dim3 block(64 * (NBA > NBB ? NBA : NBB));
+    const dim3 block(64 * (NBA > NBB ? NBA : NBB) * WM);
     if (pk.a.xvec)
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, true>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true>), grid, block, 0, s, pk);
     else
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, false>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false>), grid, block, 0, s, pk);
     return hipGetLastError();
 }
 

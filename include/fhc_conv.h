@@ -99,7 +99,8 @@ void fhc_conv_plan_destroy(fhc_conv_plan* plan);
  * desc_b: B's n, h, w and cin equal A's n, output height and width and cout; B's input view is ignored.
  * flags: FHC_PAIR_RES_MID makes B's residual A's output (B.residual set, B.cout == B.cin; graph.json's
  * "add" of e2 and e1), else B's residual, if any, is the `res` tensor of fhc_conv_run; bits 8-15: output rows
- * per tile (2 or 4; 0: the planner's choice). The plan runs with fhc_conv_run (x: A's input, y and res: B's output
+ * per tile (2 or 4; 0: the planner's choice); bits 16-19: wave rows splitting them (1 or 2; 0: 1). The plan runs
+ * with fhc_conv_run (x: A's input, y and res: B's output
  * and residual), is described by fhc_conv_describe (family "pair") and freed by fhc_conv_plan_destroy. The
  * instantiated pairs cover, in channels A.cin -> A.cout -> B.cout: stride 2 <= 32 -> 33..48 -> 33..48, and stride
  * 1 33..64 -> 33..48 -> 33..48, <= 32 -> 17..32 -> 17..32 and <= 32 -> 17..32 -> <= 16; other shapes are an

@@ -378,8 +378,8 @@ PAIR_CASES = [(2, 50, 90, 3, 36, 36, 2, 1, 1, "mid", (8, 0), None),
 
 
 @pytest.mark.parametrize("case", PAIR_CASES, ids=lambda c: "x".join(map(str, c[:7])) + (f"-{c[9]}" if c[9] else ""))
-@pytest.mark.parametrize("th", [2, 4])
-def test_pair_matches_the_two_convs(case, th):
+@pytest.mark.parametrize("th,wm", [(2, 1), (4, 1), (2, 2), (4, 2)], ids=["t2w1", "t4w1", "t2w2", "t4w2"])
+def test_pair_matches_the_two_convs(case, th, wm):
     # the fused pair against the oracle run twice (A, then B on A's f16 output): ragged tiles, stride 2, a residual
     # from A's output or from a tensor, a padded input view with NaN past cin, an output view inside a wider tensor
     import torch
@@ -392,10 +392,10 @@ def test_pair_matches_the_two_convs(case, th):
         B.res = ya
     want = B.run_oracle(threads=8)
     plan = fhconv.ConvPairPlan(A.fhc_desc(), A.wt, A.bias, A.slope if act_a == 1 else None, B.fhc_desc(), B.wt, B.bias,
-                               B.slope if act_b == 1 else None, res_mid=res == "mid", tile_rows=th)
+                               B.slope if act_b == 1 else None, res_mid=res == "mid", tile_rows=th, wave_rows=wm)
     d = plan.describe()
     say("pair", case, d["name"], d["grid"], d["tiles"])
-    assert d["family"] == "pair" and d["tile_rows"] == th
+    assert d["family"] == "pair" and d["tile_rows"] == th and d["wave_rows"] == wm
     dev = torch.device("cuda", 0)
     x = torch.from_numpy(np.ascontiguousarray(A.x).view(np.int16)).to(dev)
     y = torch.from_numpy(np.ascontiguousarray(B.y0).view(np.int16)).to(dev)
