@@ -142,6 +142,16 @@ def fusible_pairs(layers: List[ConvLayer]):
     return out
 
 
+def batched_layers(pairs: int = 8, mids_per_pair: int = 3, net_w: int = 864, net_h: int = 480) -> List[ConvLayer]:
+    """The frame's conv layers batched over `pairs` independent frame pairs with `mids_per_pair` mid() phases each:
+    pair-stage convs on pairs images (the encoders on 2 * pairs: A and B), mid-stage convs on pairs * mids_per_pair.
+    8 pairs of 3840x2160 frames run at the same network size as 1080p (default_internal(3840, 2160) = (856, 480),
+    tests/defaults.rs:12)."""
+    import dataclasses
+    return [dataclasses.replace(L, n=L.n * (pairs if L.stage == "pair" else pairs * mids_per_pair))
+            for L in flyhighfg_layers(net_w, net_h)]
+
+
 def config_layers(cfg: int) -> List[ConvLayer]:
     """The single-layer / ladder benchmark configurations C1-C3 (batch 1, NHWC f16)."""
     if cfg == 1:  # 3x3 32->32 at 1080p/8, LeakyReLU(0.1)
