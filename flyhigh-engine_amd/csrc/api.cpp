@@ -37,23 +37,29 @@ std::map<TuneKey, uint32_t> g_tune;
 
 // ---- variant codes -------------------------------------------------------------------------------------------
 // The code space of the choice table (a u8 like the reference table's value, tune_cache.rs:82):
-//   1..127   the chunked implicit-GEMM kernel: tile configuration id (bits 0-4, 1..kNumCfg) | global split-K code
-//            (bits 5-6: 0 -> 1, 1 -> 2, 2 -> 4, 3 -> 8 splits);
+//   1..127   a K-chunked kernel: configuration (bits 0-4) | global split-K code (bits 5-6: 0 -> 1, 1 -> 2,
+//            2 -> 4, 3 -> 8 splits); configuration 1..kNumCfg is the chunked implicit-GEMM kernel's tile
+//            configuration, 16 + i the deep-layer kernel's configuration i of kGemmCfgs;
 //   128+i    the direct kernel's configuration i of direct_table.h (weights resident in VGPRs).
 constexpr uint32_t kSplitCodes[4] = {1, 2, 4, 8};
 constexpr uint32_t kDirectBase = 128;
+constexpr int kGemmBase = 16;
+static_assert(kNumCfg < kGemmBase && kGemmBase + kNumGemm <= 32, "configuration ids fit bits 0-4");
 
 struct Variant {
-    int family;   // 0 chunked implicit GEMM, 1 direct
-    int cfg;      // chunked: tile configuration id; direct: index into kDirectCfgs
-    uint32_t ks;  // chunked: global split-K count
+    int family;   // 0 chunked implicit GEMM, 1 direct, 3 deep-layer (gemm_impl.h)
+    int cfg;      // chunked: tile configuration id; direct: index into kDirectCfgs; deep-layer: into kGemmCfgs
+    uint32_t ks;  // chunked, deep-layer: global split-K count
 };
 
-uint32_t make_code(int cfg, uint32_t ksplit) {
+uint32_t make_code(int cfg, uint32_t ksplit, int family = 0) {
     uint32_t sc = 0;
     for (uint32_t i = 0; i < 4; i++)
         if (kSplitCodes[i] == ksplit) sc = i;
-    return (uint32_t)cfg | (sc << 5);
+    return (uint32_t)(family == 3 ? kGemmBase + cfg : cfg) | (sc << 5);
+}
+uint32_t variant_code(const Variant& v) {
+    return v.family == 1 ? kDirectBase + (uint32_t)v.cfg : make_code(v.cfg, v.ks, v.family);
 }
 bool decode_code(uint32_t code, Variant* v) {
     if (code >= kDirectBase) {
@@ -62,8 +68,13 @@ bool decode_code(uint32_t code, Variant* v) {
         return true;
     }
     const int c = (int)(code & 31u);
+    const uint32_t ks = kSplitCodes[(code >> 5) & 3u];
+    if (c >= kGemmBase && c < kGemmBase + kNumGemm) {
+        *v = Variant{3, c - kGemmBase, ks};
+        return true;
+    }
     if (c < 1 || c > kNumCfg) return false;
-    *v = Variant{0, c, kSplitCodes[(code >> 5) & 3u]};
+    *v = Variant{0, c, ks};
     return true;
 }
 std::string code_name(uint32_t code) {
@@ -78,6 +89,13 @@ std::string code_name(uint32_t code) {
         if (c.wk > 1) o << "/rows";
         if (c.persist == 1) o << "/p";
         if (c.persist == 2) o << "/w";
+        return o.str();
+    }
+    if (v.family == 3) {
+        const GemmCfg& c = kGemmCfgs[v.cfg];
+        o << "gemm" << (c.s == 2 ? ".s2" : "") << ".t" << c.fm * c.wm << "x16.n" << 16 * c.na * c.wn << ".f" << c.fm
+          << "x" << c.na << ".w" << c.wm << "x" << c.wn << ".c" << c.ck << ".p" << c.st;
+        if (v.ks > 1) o << "/k" << v.ks;
         return o.str();
     }
     const TileCfg& t = kTileCfgs[v.cfg];
@@ -127,8 +145,10 @@ struct fhc_conv_plan {
     fhc_conv_desc d;
     Geometry g;
     uint32_t code;
-    int family;       // 0 chunked implicit GEMM, 1 direct, 2 fused pair (this plan is the pair's first conv)
-    int cfg;          // chunked: tile configuration id; direct: index into kDirectCfgs; pair: into kPairCfgs
+    int family;       // 0 chunked implicit GEMM, 1 direct, 2 fused pair (this plan is the pair's first conv), 3
+                      // deep-layer
+    int cfg;          // chunked: tile configuration id; direct: index into kDirectCfgs; pair: into kPairCfgs;
+                      // deep-layer: into kGemmCfgs
     uint32_t tiles;   // spatial output tiles (all images)
     uint32_t ksplit;  // effective global split count (1 = none)
     ConvKArgs args;   // kernel arguments with the tensor pointers left null
@@ -309,6 +329,68 @@ bool configure_igemm(fhc_conv_plan& p, int cfg, uint32_t ks, std::string* why) {
     return true;
 }
 
+// The deep-layer kernel's launch geometry for configuration `idx` and global split `ks`: chunks of CK input
+// channels (the packed weights of the chunked layout with cc = CK), one workgroup per spatial tile (grid x), channel
+// tile (grid y) and split (grid z). False if it does not serve the conv: 3x3 of its stride, an input view of
+// 16-byte groups below 2^31 bytes, at least `ks` chunks.
+bool configure_gemm(fhc_conv_plan& p, int idx, uint32_t ks, std::string* why) {
+    const fhc_conv_desc& d = p.d;
+    if (idx < 0 || idx >= kNumGemm) {
+        *why = "unknown deep-layer configuration";
+        return false;
+    }
+    const GemmCfg& c = kGemmCfgs[idx];
+    if (d.kh != 3 || (int)d.stride != c.s) {
+        *why = "the deep-layer configuration serves 3x3 convs of stride " + std::to_string(c.s) + " only";
+        return false;
+    }
+    if (d.x_cstride % 8 || d.x_c0 % 8 || (uint64_t)d.n * d.h * d.w * d.x_cstride * 2 >= (1ull << 31)) {
+        *why = "the deep-layer kernel needs an input view of 16-byte channel groups below 2^31 bytes";
+        return false;
+    }
+    LaunchFn fn = gemm_launcher(idx, nullptr);
+    if (!fn) {
+        *why = "deep-layer configuration not instantiated";
+        return false;
+    }
+    const uint32_t nchunks = div_ceil(d.cin, (uint32_t)c.ck);
+    if (ks > nchunks) {
+        *why = "fewer input-channel chunks than splits";
+        return false;
+    }
+    const uint32_t cps = div_ceil(nchunks, ks), zcount = div_ceil(nchunks, cps);
+    const int TH = c.fm * c.wm, BN = 16 * c.na * c.wn;
+    const uint32_t tiles_x = div_ceil(p.g.wout, 16), tiles_y = div_ceil(p.g.hout, (uint32_t)TH);
+    const uint64_t tiles = (uint64_t)d.n * tiles_y * tiles_x;
+    const uint32_t ntn = div_ceil(d.cout, (uint32_t)BN);
+    if (tiles > 0x7fffffffull || ntn > 65535) {
+        *why = "grid too large";
+        return false;
+    }
+    fill_args(p);
+    ConvKArgs& a = p.args;
+    a.cc = c.ck;
+    a.nchunks = (int)nchunks;
+    a.ksteps = 9 * c.ck / 32;
+    a.tapgroups = 9 * c.ck / 8;
+    a.tiles_x = (int)tiles_x;
+    a.tiles_y = (int)tiles_y;
+    a.ntn = (int)ntn;
+    a.chunks_per_split = (int)cps;
+    a.np = (int)(ntn * BN);
+    p.family = 3;
+    p.cfg = idx;
+    p.tiles = (uint32_t)tiles;
+    p.ksplit = zcount;
+    p.code = make_code(idx, zcount, 3);
+    p.grid = dim3((unsigned)tiles, ntn, zcount);
+    p.threads = 64u * c.wm * c.wn;
+    p.lds = 0;
+    p.ws_bytes = zcount > 1 ? (size_t)zcount * d.n * p.g.hout * p.g.wout * a.np * sizeof(float) : 0;
+    p.launch = fn;
+    return true;
+}
+
 int heuristic_cfg(const fhc_conv_desc& d, const Geometry& g);
 
 bool configure(fhc_conv_plan& p, const Variant& v, std::string* why) {
@@ -319,6 +401,7 @@ bool configure(fhc_conv_plan& p, const Variant& v, std::string* why) {
         }
         return configure_direct(p, v.cfg, why);
     }
+    if (v.family == 3) return configure_gemm(p, v.cfg, v.ks, why);
     return configure_igemm(p, v.cfg, v.ks, why);
 }
 
@@ -353,11 +436,23 @@ int direct_default(const fhc_conv_desc& d, const Geometry& g) {
     return pick;
 }
 
-// The MI355X planner's default when neither the caller nor the table chose: the direct kernel whenever a
-// configuration serves the input channels, else the chunked kernel.
+// The deep-layer configuration the planner takes without a table entry: 8 rows x 48 channels, 4 waves of 2 rows x
+// 3 channel blocks, two chunk buffers (the fastest or within a few percent of it on every deep layer of the frame
+// and its batched form, and on the 128 -> 128 layer at 1080p/16).
+constexpr int kGemmDefault = 11;
+
+// The MI355X planner's default when neither the caller nor the table chose. The deep-layer kernel serves stride-1
+// 3x3 convs over at least 64 input channels whose input view has 16-byte channel groups; it takes those over 64
+// input channels with at least 4096 output pixels (on smaller ones its fixed cost per launch, the first chunk's
+// load and the epilogue, outweighs the direct kernel's longer chains). Then the direct kernel whenever a
+// configuration serves the input channels, then the deep-layer kernel where it serves, else the chunked kernel.
 uint32_t heuristic_code(const fhc_conv_desc& d, const Geometry& g) {
+    const bool gemm_ok = d.kh == 3 && d.stride == 1 && d.cin >= 64 && d.x_cstride % 8 == 0 && d.x_c0 % 8 == 0 &&
+                         (uint64_t)d.n * d.h * d.w * d.x_cstride * 2 < (1ull << 31);
+    if (gemm_ok && d.cin > 64 && (uint64_t)d.n * g.hout * g.wout >= 4096) return make_code(kGemmDefault, 1, 3);
     const int idx = direct_default(d, g);
     if (idx >= 0) return kDirectBase + (uint32_t)idx;
+    if (gemm_ok) return make_code(kGemmDefault, 1, 3);
     return (uint32_t)heuristic_cfg(d, g);
 }
 
@@ -518,7 +613,7 @@ bool plan_choose(const fhc_conv_desc& d, fhc_conv_plan& p, std::string* why) {
     }
     if (!configure(p, v, why)) {
         // a table entry or heuristic that does not fit this shape falls back to the chunked 4-row tile
-        const uint32_t code = v.family == 1 ? kDirectBase + (uint32_t)v.cfg : make_code(v.cfg, v.ks);
+        const uint32_t code = variant_code(v);
         if (d.variant != 0 || !configure(p, Variant{0, d.cout <= 32 ? 5 : 4, v.family == 1 ? 1u : v.ks}, why)) {
             *why += " (variant " + code_name(code) + ")";
             return false;
@@ -555,6 +650,13 @@ std::string describe_json(const fhc_conv_plan* p) {
         wm = c.wm;
         wnv = c.wn;
         wk = c.wk;
+    } else if (p->family == 3) {
+        const GemmCfg& c = kGemmCfgs[p->cfg];
+        rows = c.fm * c.wm;
+        chans = 16 * c.na * c.wn;
+        wm = c.wm;
+        wnv = c.wn;
+        wk = 1;
     } else {
         const TileCfg& t = kTileCfgs[p->cfg];
         rows = t.fm * t.wm;
@@ -572,10 +674,10 @@ std::string describe_json(const fhc_conv_plan* p) {
     snprintf(b, sizeof b,
              "{\"variant\":%u,\"name\":\"%s\",\"family\":\"%s\",\"cfg\":%d,\"tile_rows\":%d,\"tile_cols\":16,"
              "\"tile_channels\":%d,\"waves\":[%d,%d,%d],\"ksplit\":%u,\"cc\":%d,\"nchunks\":%d,\"ksteps\":%d,"
-             "\"tiles\":%u,\"ntn\":%d,\"grid\":[%u,%u],\"threads\":%u,\"lds\":%zu,\"packed_weight_bytes\":%zu,"
+             "\"tiles\":%u,\"ntn\":%d,\"grid\":[%u,%u,%u],\"threads\":%u,\"lds\":%zu,\"packed_weight_bytes\":%zu,"
              "\"workspace_bytes\":%zu,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
-             p->code, code_name(p->code).c_str(), p->family == 1 ? "direct" : "igemm", p->cfg, rows, chans, wm, wnv,
-             wk, p->ksplit, p->args.cc, p->args.nchunks, p->args.ksteps, p->tiles, p->args.ntn, p->grid.x, p->grid.y,
+             p->code, code_name(p->code).c_str(), p->family == 1 ? "direct" : p->family == 3 ? "gemm" : "igemm",
+             p->cfg, rows, chans, wm, wnv, wk, p->ksplit, p->args.cc, p->args.nchunks, p->args.ksteps, p->tiles, p->args.ntn, p->grid.x, p->grid.y, p->grid.z,
              p->threads, p->lds, packed, p->ws_bytes, p->g.hout, p->g.wout, flops, bytes);
     return b;
 }
@@ -947,6 +1049,19 @@ extern "C" int fhc_variant_list(const fhc_conv_desc* desc, uint32_t* codes, size
             const int width = kDirectCfgs[i].na * kDirectCfgs[i].wn;  // 16-channel blocks per channel tile
             if (16u * width >= 2 * div_ceil(d.cout, 16) * 16 && width > 1) continue;
             if (configure_direct(p, i, &why)) out.push_back(p.code);
+        }
+        // the deep-layer kernel where the channels fill its tile and the input is too deep for the direct kernel's
+        // registers or the work is large (at least 64 input channels)
+        for (int i = 0; i < kNumGemm && d.kh == 3 && d.cin >= 64; i++) {
+            const GemmCfg& c = kGemmCfgs[i];
+            const uint32_t bn = (uint32_t)(16 * c.na * c.wn);
+            if (bn >= 2 * div_ceil(d.cout, 16) * 16 && bn > 32) continue;  // mostly padding
+            for (uint32_t ks : {1u, 2u, 4u, 8u}) {
+                if (!configure_gemm(p, i, ks, &why)) continue;
+                if (p.ksplit != ks) continue;
+                if (ks > 1 && (uint64_t)p.grid.x * p.grid.y >= 512) continue;
+                out.push_back(p.code);
+            }
         }
         for (int cfg = 1; cfg <= kNumCfg; cfg++) {
             const TileCfg& t = kTileCfgs[cfg];

@@ -65,6 +65,31 @@ LaunchFn conv_launcher(int ks, int stride, int cfg);
 LaunchFn direct_launcher(int index, const void** kernel, bool residual = false);
 hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s);
 
+// The deep-layer conv (gemm_impl.h, 3x3 only): stride S, chunks of CK input channels through LDS in a ring of ST
+// buffers, waves WM x WN of FM rows x NA channel blocks each; TH = FM * WM rows x 16 columns x BN = 16 * NA * WN
+// channels per workgroup. The 2-wave configurations fit two workgroups per CU.
+struct GemmCfg {
+    int s, ck, fm, na, wm, wn, st;
+};
+constexpr int kNumGemm = 13;
+inline constexpr GemmCfg kGemmCfgs[kNumGemm] = {
+    {1, 32, 4, 2, 2, 2, 3},  // 0: TH 8, BN 64, 4 waves
+    {1, 32, 2, 2, 4, 2, 2},  // 1: TH 8, BN 64, 8 waves
+    {1, 32, 4, 2, 2, 1, 2},  // 2: TH 8, BN 32, 2 waves
+    {1, 32, 2, 2, 2, 2, 3},  // 3: TH 4, BN 64, 4 waves
+    {1, 32, 4, 3, 2, 2, 2},  // 4: TH 8, BN 96, 4 waves
+    {1, 32, 2, 3, 2, 2, 2},  // 5: TH 4, BN 96, 4 waves
+    {1, 32, 4, 2, 4, 1, 3},  // 6: TH 16, BN 32, 4 waves
+    {1, 32, 2, 3, 4, 1, 3},  // 7: TH 8, BN 48, 4 waves
+    {1, 32, 2, 2, 2, 1, 2},  // 8: TH 4, BN 32, 2 waves
+    {1, 32, 2, 3, 2, 1, 2},  // 9: TH 4, BN 48, 2 waves
+    {1, 64, 2, 2, 4, 1, 2},  // 10: TH 8, BN 32, 4 waves, 64-channel chunks
+    {1, 32, 2, 3, 4, 1, 2},  // 11: as 7 with two buffers
+    {1, 32, 4, 2, 2, 2, 2},  // 12: as 0 with two buffers
+};
+// The launcher of the deep-layer configuration `index`, or nullptr; *kernel receives the kernel's address.
+LaunchFn gemm_launcher(int index, const void** kernel);
+
 // A fused pair of 3x3 convs (pair_impl.h): B (stride 1) reads A's output, which stays in LDS.
 struct PairKArgs {
     ConvKArgs a, b;  // a: x, A's weights, bias, multipliers, input geometry; b: y, res, B's weights, output geometry

@@ -409,3 +409,74 @@ def test_pair_matches_the_two_convs(case, th, wm):
     mask = np.ones(B.ycs, bool)
     mask[sl] = False
     assert np.array_equal(got[..., mask], B.y0[..., mask])
+
+
+# the deep-layer kernel ("gemm.": weights and halos through LDS by DMA, chunks of 32 or 64 input channels):
+# n, h, w, cin, cout, act, residual, input view, output view
+GEMM_SHAPES = [(1, 30, 54, 279, 96, 1, 0, (280, 0), None),
+               (1, 27, 45, 155, 48, 1, 1, (160, 0), None),
+               (2, 19, 37, 128, 128, 2, 1, (136, 8), (136, 4)),
+               (1, 17, 33, 96, 12, 0, 0, None, None),
+               (1, 11, 18, 64, 100, 1, 0, None, (104, 0))]
+
+
+@pytest.mark.parametrize("shape", GEMM_SHAPES, ids=lambda s: "x".join(map(str, s[:7])))
+def test_gemm_variants_match_the_oracle(shape):
+    # every deep-layer configuration and split: partial last channel groups with NaN past cin in the tensor, ragged
+    # tiles, partial channel tiles, a residual, every activation, views inside poisoned wider tensors
+    n, h, w, cin, cout, act, res, xv, yv = shape
+    c = Case(n, h, w, cin, cout, act=act, residual=res, xv=xv, yv=yv, poison=xv is not None or yv is not None,
+             seed=51)
+    want = c.run_oracle(threads=8)
+    codes = [k for k in fhconv.variant_list(c.fhc_desc()) if fhconv.variant_name(k).startswith("gemm")]
+    assert codes
+    sl = slice(c.yc0, c.yc0 + cout)
+    for code in codes:
+        got, plan = c.run_gpu(variant=code, return_plan=True)
+        d = plan.describe()
+        say("gemm", shape[:7], d["name"], d["grid"], d["ksplit"])
+        assert d["family"] == "gemm"
+        ok, md, mref = parity(got, want, view=sl)
+        assert ok, (d["name"], md, mref)
+        mask = np.ones(c.ycs, bool)
+        mask[sl] = False
+        assert np.array_equal(got[..., mask], c.y0[..., mask])
+
+
+def test_gemm_variant_unaligned_input_falls_back():
+    # an input pointer off 16-byte alignment cannot take the LDS DMA: the launcher runs the chunked kernel on the
+    # same packed weights instead, with and without a split
+    import torch
+    c = Case(1, 21, 34, 155, 48, act=1, xv=(160, 0), seed=52)
+    want = c.run_oracle()
+    names = {fhconv.variant_name(k): k for k in fhconv.variant_list(c.fhc_desc())}
+    for name in ("gemm.t8x16.n64.f4x2.w2x2.c32.p3", "gemm.t8x16.n64.f4x2.w2x2.c32.p2/k2",
+                 "gemm.t8x16.n32.f2x2.w4x1.c64.p2"):
+        plan = fhconv.ConvPlan(c.fhc_desc(names[name]), c.wt, c.bias, c.slope)
+        dev = torch.device("cuda", 0)
+        xb = torch.zeros(c.x.size + 4, dtype=torch.int16, device=dev)
+        xb[4:] = torch.from_numpy(c.x.ravel().view(np.int16)).to(dev)
+        y = torch.from_numpy(c.y0.view(np.int16)).to(dev)
+        ws = torch.empty(plan.workspace_bytes // 4 + 4, dtype=torch.float32, device=dev) if plan.workspace_bytes else None
+        say("gemm fallback", name)
+        plan.run(xb[4:], y, None, ws)
+        torch.cuda.synchronize()
+        ok, md, mref = parity(y.cpu().numpy().view(np.uint16), want)
+        assert ok, (name, md, mref)
+
+
+@pytest.mark.parametrize("shape", [(1, 68, 120, 128, 128, 1, 0), (8, 30, 54, 279, 96, 1, 0)], ids=["deep", "c1x8"])
+def test_gemm_variants_full_size(shape):
+    # the 1080p/16 deep layer and the batched 279-channel layer: rows checked in bands of the first image
+    n, h, w, cin, cout, act, res = shape
+    c = Case(n, h, w, cin, cout, act=act, residual=res, xv=((cin + 7) // 8 * 8, 0), seed=53)
+    codes = [k for k in fhconv.variant_list(c.fhc_desc()) if fhconv.variant_name(k).startswith("gemm")]
+    assert codes
+    bands = {r0: oracle_rows(c, r0, r0 + 4, threads=8) for r0 in (0, c.hout // 2 - 2, c.hout - 4)}
+    for code in codes:
+        got, plan = c.run_gpu(variant=code, return_plan=True)
+        d = plan.describe()
+        say("gemm", d["name"], d["grid"], d["ksplit"])
+        for r0, want in bands.items():
+            ok, md, mref = parity(got[0, r0:r0 + 4], want)
+            assert ok, (d["name"], r0, md, mref)

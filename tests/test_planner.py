@@ -116,14 +116,17 @@ SHAPES = [
 
 
 def test_direct_kernel_where_the_channels_fit():
-    # small-channel layers go to the direct kernel (weights resident), deep ones to the chunked kernel
+    # small-channel layers go to the direct kernel (weights resident), deep ones to the deep-layer kernel where the
+    # input view has 16-byte channel groups, else to the chunked kernel
     assert fhconv.plan_dry(fhconv.make_desc(1, 136, 240, 32, 32))["family"] == "direct"
     assert fhconv.plan_dry(fhconv.make_desc(1, 544, 960, 32, 64, stride=2))["family"] == "direct"
     assert fhconv.plan_dry(fhconv.make_desc(1, 68, 120, 128, 64, k=1))["family"] == "direct"
     deep = fhconv.plan_dry(fhconv.make_desc(1, 30, 54, 279, 96))  # one kernel row of K per wave
     assert deep["family"] == "direct" and deep["cc"] == 288 and deep["waves"][2] == 3
     assert fhconv.plan_dry(fhconv.make_desc(1, 60, 108, 72, 36, stride=2))["family"] == "igemm"
-    assert fhconv.plan_dry(fhconv.make_desc(1, 30, 54, 300, 96))["family"] == "igemm"
+    assert fhconv.plan_dry(fhconv.make_desc(1, 30, 54, 300, 96))["family"] == "igemm"  # 300 % 8: no DMA path
+    assert fhconv.plan_dry(fhconv.make_desc(1, 30, 54, 300, 96, x_cstride=304))["family"] == "gemm"
+    assert fhconv.plan_dry(fhconv.make_desc(1, 68, 120, 128, 128))["name"] == "gemm.t8x16.n48.f2x3.w4x1.c32.p2"
     d = fhconv.plan_dry(fhconv.make_desc(1, 60, 108, 36, 36))
     assert d["family"] == "direct" and d["cc"] == 64 and d["tile_channels"] == 48 and d["ntn"] == 1
 
@@ -140,6 +143,9 @@ def test_mi355x_plan_covers_the_output(shape):
     if p["family"] == "igemm":
         assert p["grid"][0] == tiles * p["ntn"]
         assert p["ksteps"] * 32 >= k * k * p["cc"]
+    elif p["family"] == "gemm":  # deep-layer kernel: one workgroup per tile and channel tile, chunks of 32 or 64
+        assert p["grid"] == [tiles, p["ntn"], 1] and k == 3 and s == 1
+        assert p["cc"] in (32, 64) and p["ksteps"] * 32 == 9 * p["cc"]
     else:
         assert p["grid"][1] == p["ntn"] and 1 <= p["grid"][0] <= tiles
         assert p["cc"] % 32 == 0 and p["ksteps"] * 32 == k * k * p["cc"] and p["nchunks"] == 1
@@ -165,7 +171,7 @@ def test_variant_list_and_forced_variants():
 def test_forced_split_k_and_reference_hint():
     p = fhconv.plan_dry(fhconv.make_desc(1, 68, 120, 128, 128, ksplit=4))
     np_ = -(-128 // p["tile_channels"]) * p["tile_channels"]
-    assert p["ksplit"] == 4 and p["grid"][1] == 4
+    assert p["ksplit"] == 4 and p["grid"][1 if p["family"] == "igemm" else 2] == 4
     assert p["workspace_bytes"] == 4 * 68 * 120 * np_ * 4  # f32 partials [z][pixel][np]
     assert p["nchunks"] % 4 == 0
     h = fhconv.plan_dry(fhconv.make_desc(1, 68, 120, 128, 128, ref_cand=fhconv.CAND_TILED | 2 << 4))
