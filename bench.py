@@ -83,9 +83,9 @@ class Net:
             self.params[L.name] = (d, wt, b, s)
 
     def fuse(self, pairs, torch, fhconv, stream, time_fn):
-        """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; the
-        tile height (2 or 4 rows) and wave rows (1 or 2) timed on the real buffers, the fastest kept, and only where
-        it beats the two separate launches."""
+        """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; every
+        instantiated tile height (1, 2 or 4 rows) and wave rows (1 or 2) timed on the real buffers, the fastest kept,
+        and only where it beats the two separate launches."""
         for A, B, res_mid in pairs:
             sep = time_fn(lambda i=0: (self.run_one(A, stream=stream), self.run_one(B, stream=stream)))
             da, wa, ba, sa = self.params[A.name]
@@ -94,12 +94,16 @@ class Net:
             _, y, r, _ = self.bufs[B.name]
             rx = None if res_mid else r
             best = None
-            for th, wm in ((2, 1), (4, 1), (2, 2), (4, 2)):
-                pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th, wave_rows=wm)
+            for th, wm in ((1, 1), (2, 1), (4, 1), (2, 2), (4, 2)):
+                try:
+                    pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th,
+                                             wave_rows=wm)
+                except fhconv.FhcError:
+                    continue  # not instantiated for these channels
                 us = time_fn(lambda i=0, pp=pp: pp.run(x, y, rx, stream=stream))
                 if best is None or us < best[1]:
                     best = (pp, us)
-            if best[1] < sep:
+            if best is not None and best[1] < sep:
                 self.pairs[A.name] = (best[0], B, round(best[1], 3), res_mid)
 
     def run_one(self, L, stream=None):

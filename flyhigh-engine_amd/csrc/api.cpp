@@ -884,14 +884,23 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
             return fail(-1, "fhc_conv_pair_plan_create: PReLU needs a slope");
         const int ca32 = (int)div_ceil(A.cin, 32) * 32, cb32 = (int)div_ceil(B.cin, 32) * 32;
         const int nba = (int)div_ceil(A.cout, 16), nbb = (int)div_ceil(B.cout, 16);
-        const uint64_t tiles2 = (uint64_t)A.n * div_ceil(ha, 2) * div_ceil(wa, kPairTileW);
+        // the configuration at the requested tile height and wave rows; by default one wave row and the tallest
+        // instantiated tile that still gives 256 workgroups, else the shortest
+        const int wm = wm_req ? (int)wm_req : 1;
+        auto tiles_at = [&](int th) { return (uint64_t)A.n * div_ceil(ha, (uint32_t)th) * div_ceil(wa, kPairTileW); };
         int idx = -1;
         for (int i = 0; i < kNumPair; i++) {
             const PairCfg& c = kPairCfgs[i];
-            if (c.sa != (int)A.stride || c.ca32 != ca32 || c.cb32 != cb32 || c.nba != nba || c.nbb != nbb) continue;
-            // default: 4-row tiles unless that leaves under 256 workgroups
-            const int th = th_req ? (int)th_req : (tiles2 / 2 >= 256 ? 4 : 2);
-            if (c.th == th && c.wm == (wm_req ? (int)wm_req : 1)) idx = i;
+            if (c.sa != (int)A.stride || c.ca32 != ca32 || c.cb32 != cb32 || c.nba != nba || c.nbb != nbb ||
+                c.wm != wm)
+                continue;
+            if (th_req) {
+                if (c.th == (int)th_req) idx = i;
+                continue;
+            }
+            const int cur = idx < 0 ? 0 : kPairCfgs[idx].th;
+            const bool fills = tiles_at(c.th) >= 256, cur_fills = idx >= 0 && tiles_at(cur) >= 256;
+            if (idx < 0 || (fills && (!cur_fills || c.th > cur)) || (!fills && !cur_fills && c.th < cur)) idx = i;
         }
         if (idx < 0)
             return fail(-1, "fhc_conv_pair_plan_create: no fused pair instantiated for stride %u, %u -> %u -> %u "

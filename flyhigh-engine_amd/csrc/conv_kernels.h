@@ -101,7 +101,7 @@ constexpr int kPairTileW = 14;  // output columns per tile (B's 16-pixel MFMA bl
 struct PairCfg {
     int sa, ca32, cb32, nba, nbb, th, wm;
 };
-constexpr int kNumPair = 16;
+constexpr int kNumPair = 18;
 inline constexpr PairCfg kPairCfgs[kNumPair] = {
     // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
     {2, 32, 64, 3, 3, 2, 1}, {2, 32, 64, 3, 3, 4, 1}, {2, 32, 64, 3, 3, 2, 2}, {2, 32, 64, 3, 3, 4, 2},
@@ -111,6 +111,8 @@ inline constexpr PairCfg kPairCfgs[kNumPair] = {
     {1, 32, 32, 2, 2, 2, 1}, {1, 32, 32, 2, 2, 4, 1}, {1, 32, 32, 2, 2, 2, 2}, {1, 32, 32, 2, 2, 4, 2},
     // <= 32 -> 32 -> 16 (refine head output)
     {1, 32, 32, 2, 1, 2, 1}, {1, 32, 32, 2, 1, 4, 1}, {1, 32, 32, 2, 1, 2, 2}, {1, 32, 32, 2, 1, 4, 2},
+    // the encoder's second stride-2 conv and its successor (36 -> 72 -> 72)
+    {2, 64, 96, 5, 5, 1, 1}, {2, 64, 96, 5, 5, 2, 1},
 };
 using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);
 PairLaunchFn pair_launcher(int index);

@@ -121,10 +121,11 @@ def flyhighfg_layers(net_w: int = 864, net_h: int = 480, k: int = 1, batch_encod
     return L
 
 
-# Consecutive convs of models/graph.json whose intermediate tensor has no other reader (enc.e1's output is also the
-# residual that enc.e2's "add" takes: the pair's second conv adds the first's output): each pair can run as one fused
+# Consecutive convs of models/graph.json whose intermediate tensor has no other reader (enc.e1's and enc.e3's outputs
+# are also the residuals that enc.e2's and enc.e4's "add" take: the pair's second conv adds the first's output): each pair can run as one fused
 # launch (fhc_conv_pair_plan_create). (first conv, second conv, second's residual is the first's output)
-FUSIBLE_PAIRS = [("enc.e1", "enc.e2", True), ("fine.r2", "fine.r3", False), ("film.h1", "film.h2", False),
+FUSIBLE_PAIRS = [("enc.e1", "enc.e2", True), ("enc.e3", "enc.e4", True), ("fine.r2", "fine.r3", False),
+                 ("film.h1", "film.h2", False),
                  ("refine.q1", "refine.q2", False), ("refine.q3", "refine.q4", False)]
 
 

@@ -375,10 +375,16 @@ PAIR_CASES = [(2, 50, 90, 3, 36, 36, 2, 1, 1, "mid", (8, 0), None),
               (1, 41, 75, 14, 24, 24, 1, 1, 1, None, (16, 0), None),
               (1, 37, 53, 24, 24, 3, 1, 1, 0, None, None, (8, 0)),
               (1, 30, 44, 48, 48, 48, 1, 2, 1, "ext", None, None)]
+# the encoder's second pair (36 -> 72 -> 72, stride 2, A's output as B's residual): tiles of 1 or 2 rows
+PAIR_CASES_E3 = [(2, 61, 107, 36, 72, 72, 2, 1, 1, "mid", (40, 0), None),
+                 (1, 19, 29, 36, 72, 72, 2, 1, 1, "mid", None, (80, 8))]
+PAIR_RUNS = [(c, th, wm) for c in PAIR_CASES for th, wm in ((2, 1), (4, 1), (2, 2), (4, 2))] + \
+    [(c, th, 1) for c in PAIR_CASES_E3 for th in (1, 2)]
 
 
-@pytest.mark.parametrize("case", PAIR_CASES, ids=lambda c: "x".join(map(str, c[:7])) + (f"-{c[9]}" if c[9] else ""))
-@pytest.mark.parametrize("th,wm", [(2, 1), (4, 1), (2, 2), (4, 2)], ids=["t2w1", "t4w1", "t2w2", "t4w2"])
+@pytest.mark.parametrize("case,th,wm", PAIR_RUNS,
+                         ids=lambda v: "x".join(map(str, v[:7])) + (f"-{v[9]}" if v[9] else "")
+                         if isinstance(v, tuple) else str(v))
 def test_pair_matches_the_two_convs(case, th, wm):
     # the fused pair against the oracle run twice (A, then B on A's f16 output): ragged tiles, stride 2, a residual
     # from A's output or from a tensor, a padded input view with NaN past cin, an output view inside a wider tensor
