@@ -2,17 +2,18 @@
 """Benchmark of the FlyHigh conv hot path on one MI355X.
 
 Workload (one step): every conv layer of one FlyHighFG pair() and one mid() at 1080p (network 856x480, padded to
-864x480), batch 1, NHWC f16, random He-normal weights and seeded uniform inputs resident in HBM. The pair stage
-(17 convs) and the mid stage (8 convs) are each captured once as a HIP graph; a step replays both. The value is
-conv-only 1080p frames/s = 1000 / ms per step (the non-conv ops of pair()/mid() are not part of this path).
+864x480), batch 1, NHWC f16, random He-normal weights and seeded uniform inputs resident in HBM. Consecutive convs
+whose intermediate has no other reader run as one fused launch where that is faster (checked against the unfused
+step on every run). The whole step is captured once as a HIP graph and replayed. The value is conv-only 1080p
+frames/s = 1000 / ms per step (the non-conv ops of pair()/mid() are not part of this path).
 
-Alongside: per-layer time and roofline fraction (each layer's R launches captured in a graph, median of G replays
+Alongside: per-launch time and roofline fraction (each launch captured R times in a graph, median of G replays
 over R; "cold" rotates buffer sets larger than the 256 MB MALL, "warm" reuses one), the layers of the single-layer
-configurations (3x3 32->32 at 1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1), and the CPU
-baseline: the oracle (a C restatement of the reference's conv arithmetic) over the same conv layers on the host's
-cores.
+configurations (3x3 32->32 at 1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1), the batched
+workload (the frame's convs over 8 independent 4K frame pairs with 3 mid() phases each), and the CPU baseline: the
+oracle (a C restatement of the reference's conv arithmetic) over the same conv layers on the host's cores.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--no-batched] [--no-fuse]
 """
 import argparse
 import json
@@ -82,10 +83,11 @@ class Net:
             self.bufs[L.name] = (x, y, r, ws)
             self.params[L.name] = (d, wt, b, s)
 
-    def fuse(self, pairs, torch, fhconv, stream, time_fn):
+    def fuse(self, pairs, torch, fhconv, stream, time_fn, default_tile=False):
         """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; every
-        instantiated tile height (1, 2 or 4 rows) and wave rows (1 or 2) timed on the real buffers, the fastest kept,
-        and only where it beats the two separate launches."""
+        instantiated tile height (1, 2 or 4 rows) and wave rows (1 or 2) timed on the real buffers, the fastest kept
+        (default_tile: the pair planner's own choice, no timing), and only where it beats the two separate
+        launches."""
         for A, B, res_mid in pairs:
             sep = time_fn(lambda i=0: (self.run_one(A, stream=stream), self.run_one(B, stream=stream)))
             da, wa, ba, sa = self.params[A.name]
@@ -94,7 +96,7 @@ class Net:
             _, y, r, _ = self.bufs[B.name]
             rx = None if res_mid else r
             best = None
-            for th, wm in ((1, 1), (2, 1), (4, 1), (2, 2), (4, 2)):
+            for th, wm in ((0, 0),) if default_tile else ((1, 1), (2, 1), (4, 1), (2, 2), (4, 2)):
                 try:
                     pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th,
                                              wave_rows=wm)
@@ -206,7 +208,7 @@ def batched_workload(args, torch, np, fhconv, flyhighfg, stream, pairs=8, mids=3
     fused = not args.no_fuse
     if fused:
         net.fuse(flyhighfg.fusible_pairs(layers), torch, fhconv, stream,
-                 lambda fn: time_graph(torch, fn, 20, 3, stream))
+                 lambda fn: time_graph(torch, fn, 20, 3, stream), default_tile=bool(args.tune))
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
         net.run(fused=fused)
@@ -293,12 +295,26 @@ def mfma_rate_probe(torch, fhconv, stream):
 COPY_BYTES = 256 << 20  # the calibration copy of the traffic passes
 
 
-def pmc_workload(args, torch, net, stream):
-    """One layer over rotating buffer sets (> 512 MB, so every launch reads from HBM), then a device copy of
-    COPY_BYTES the same number of times: rocprofv3 --pmc runs this to read FETCH_SIZE / WRITE_SIZE per dispatch."""
-    L = [L for L in net.layers if L.name == args.pmc_layer][0]
-    p = net.plans[L.name]
-    x, y, r, ws = net.bufs[L.name]
+def pmc_workload(args, torch, fhconv, flyhighfg, net, stream):
+    """One layer, or one fused pair ("first+second", the pair planner's default tile, the same in both counter
+    passes), over rotating buffer sets (> 512 MB, so every launch reads from HBM), then a device copy of COPY_BYTES
+    the same number of times: rocprofv3 --pmc runs this to read FETCH_SIZE / WRITE_SIZE per dispatch."""
+    if "+" in args.pmc_layer:
+        a_name, b_name = args.pmc_layer.split("+")
+        pair = [(A, B, rm) for A, B, rm in flyhighfg.fusible_pairs(net.layers) if A.name == a_name and B.name == b_name]
+        if not pair:
+            raise SystemExit(f"{args.pmc_layer} is not a fusible pair of the frame")
+        A, B, res_mid = pair[0]
+        da, wa, ba, sa = net.params[A.name]
+        db, wb, bb, sb = net.params[B.name]
+        p = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid)
+        x, ws = net.bufs[A.name][0], None
+        _, y, r, _ = net.bufs[B.name]
+        r = None if res_mid else r
+    else:
+        L = [L for L in net.layers if L.name == args.pmc_layer][0]
+        p = net.plans[L.name]
+        x, y, r, ws = net.bufs[L.name]
     per = x.numel() * 2 + y.numel() * 2 + (r.numel() * 2 if r is not None else 0)
     nsets = max(2, -(-(600 << 20) // per))
     sets = [(torch.empty_like(x).uniform_(-1, 1), torch.empty_like(y),
@@ -313,8 +329,8 @@ def pmc_workload(args, torch, net, stream):
         for _ in range(args.pmc_reps):
             dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps(dict(pmc_layer=L.name, variant=p.describe()["name"], reps=args.pmc_reps, cold_sets=nsets,
-                          copy_bytes=COPY_BYTES)), flush=True)
+    print(json.dumps(dict(pmc_layer=args.pmc_layer, variant=p.describe()["name"], reps=args.pmc_reps,
+                          cold_sets=nsets, copy_bytes=COPY_BYTES)), flush=True)
     return 0
 
 
@@ -346,18 +362,33 @@ def traffic_from(args):
     f_scale = COPY_BYTES / (fetch[wk] * 1024.0)
     w_scale = COPY_BYTES / (write[wk] * 1024.0)
     traffic = fetch[fk] * 1024.0 * f_scale + write[fk] * 1024.0 * w_scale
-    # the variant the planner gives this layer under the same choice table (no GPU needed)
-    import fhconv
-    import flyhighfg
-    if args.tune:
-        with open(args.tune) as f:
-            fhconv.parse_tune(f.read())
-    L = [L for L in flyhighfg.flyhighfg_layers(864, 480, k=1) if L.name == args.pmc_layer][0]
-    desc = fhconv.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
-                            residual=L.residual, x_cstride=pad8(L.cin), y_cstride=pad8(L.cout),
-                            r_cstride=pad8(L.cout) if L.residual else 0)
-    variant = fhconv.plan_dry(desc)["name"]
-    text = (f"layer {args.pmc_layer}\nvariant {variant}\nkernel {fk}\n"
+    if len(args.traffic_from) > 2:
+        # the variant the counted workload ran: its JSON line in the third file (a pair's tile is chosen by timing)
+        runs = [json.loads(line) for line in open(args.traffic_from[2]) if line.startswith("{")]
+        variant = [r["variant"] for r in runs if r.get("pmc_layer") == args.pmc_layer][-1]
+    else:
+        # the variant the planner gives this layer under the same choice table (no GPU needed)
+        import fhconv
+        import flyhighfg
+        if args.tune:
+            with open(args.tune) as f:
+                fhconv.parse_tune(f.read())
+        L = [L for L in flyhighfg.flyhighfg_layers(864, 480, k=1) if L.name == args.pmc_layer][0]
+        desc = fhconv.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
+                                residual=L.residual, x_cstride=pad8(L.cin), y_cstride=pad8(L.cout),
+                                r_cstride=pad8(L.cout) if L.residual else 0)
+        variant = fhconv.plan_dry(desc)["name"]
+    tune = f" --tune {os.path.relpath(args.tune, ROOT)}" if args.tune else ""
+    cmd = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && timeout -s KILL 120 rocprofv3 --pmc "
+           "{counter} -d gpurun_out/{d} -o run --output-format csv -- python3 bench.py" + tune +
+           f" --pmc-layer {args.pmc_layer} > gpurun_out/{{d}}.out")
+    text = (f"# HBM traffic per launch from two counter passes (MI355X), then on any host:\n"
+            f"# {cmd.format(counter='FETCH_SIZE', d='pmc_fetch')}\n"
+            f"# {cmd.format(counter='WRITE_SIZE', d='pmc_write')}\n"
+            f"# python3 bench.py{tune} --pmc-layer {args.pmc_layer} --traffic-from "
+            f"gpurun_out/pmc_fetch/*/run_counter_collection.csv gpurun_out/pmc_write/*/run_counter_collection.csv"
+            f"{' gpurun_out/pmc_fetch.out' if len(args.traffic_from) > 2 else ''}\n"
+            f"layer {args.pmc_layer}\nvariant {variant}\nkernel {fk}\n"
             f"fetch_kib_per_launch {fetch[fk]:.1f}\nwrite_kib_per_launch {write[fk]:.1f}\n"
             f"copy_kernel {wk}\ncopy_bytes {COPY_BYTES}\n"
             f"copy_fetch_kib {fetch[wk]:.1f}\ncopy_write_kib {write[wk]:.1f}\n"
@@ -376,7 +407,7 @@ def measured_traffic(layer, variant):
     path = os.path.join(ROOT, "profiles", f"traffic_{layer}.txt")
     if not os.path.exists(path):
         return None, "no counter passes recorded for this layer"
-    kv = dict(line.split(" ", 1) for line in open(path).read().splitlines() if " " in line)
+    kv = dict(line.split(" ", 1) for line in open(path).read().splitlines() if " " in line and line[0] != "#")
     if kv.get("variant") != variant:
         return None, f"profiles/traffic_{layer}.txt was measured on {kv.get('variant')}, this run uses {variant}"
     return int(float(kv["traffic_bytes_per_launch"])), f"profiles/traffic_{layer}.txt ({kv['kernel'][:80]})"
@@ -401,9 +432,10 @@ def main():
                                         "then a copy of known size as many times: the workload of the rocprofv3 "
                                         "--pmc FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-reps", type=int, default=64)
-    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
-                    help="with --pmc-layer: turn the two passes' counter_collection.csv files into "
-                         "profiles/traffic_<layer>.txt (HBM bytes per launch, copy-calibrated)")
+    ap.add_argument("--traffic-from", nargs="+", metavar="CSV",
+                    help="with --pmc-layer: turn the two passes' counter_collection.csv files (FETCH, WRITE) into "
+                         "profiles/traffic_<layer>.txt (HBM bytes per launch, copy-calibrated); a third file, the "
+                         "counted run's stdout, names the variant it ran (needed for a fused pair)")
     args = ap.parse_args()
     if args.traffic_from:
         return traffic_from(args)
@@ -436,11 +468,13 @@ def main():
     tune_table = fhconv.format_tune().splitlines()  # the frame's choices (later workloads add their own)
     torch.cuda.synchronize()
     if args.pmc_layer:
-        return pmc_workload(args, torch, net, stream)
+        return pmc_workload(args, torch, fhconv, flyhighfg, net, stream)
     fused = not args.no_fuse
     if fused:
+        # with a committed choice table the pairs take the pair planner's default tile: the run is then repeatable
+        # (a profiler's own overhead cannot change the variants it traces)
         net.fuse(flyhighfg.fusible_pairs(layers), torch, fhconv, stream,
-                 lambda fn: time_graph(torch, fn, 50, 5, stream))
+                 lambda fn: time_graph(torch, fn, 50, 5, stream), default_tile=bool(args.tune))
         log(f"bench: {len(net.pairs)} conv pairs fused: " +
             ", ".join(f"{a}+{B.name} ({pp.describe()['name']})" for a, (pp, B, _, _) in net.pairs.items()))
     launches = len(layers) - len(net.pairs)

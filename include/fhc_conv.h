@@ -92,19 +92,20 @@ void fhc_conv_plan_destroy(fhc_conv_plan* plan);
 
 /* A fused pair: conv A (3x3, stride 1 or 2, no residual) and conv B (3x3 stride 1) that reads A's output, run as
  * one launch with A's output kept on chip. It serves two consecutive conv ops of the graph whose intermediate
- * tensor has no other reader (graph.json's enc.e1 -> enc.e2, film.h1 -> film.h2, refine.q1 -> q2, q3 -> q4,
- * fine.r2 -> r3). The result is the one the two plans give run in turn: A's output is rounded to f16 and B reads it
+ * tensor has no other reader (graph.json's enc.e1 -> enc.e2, enc.e3 -> enc.e4, film.h1 -> film.h2, refine.q1 -> q2,
+ * q3 -> q4, fine.r2 -> r3). The result is the one the two plans give run in turn: A's output is rounded to f16 and B reads it
  * with zero padding. No counterpart in the reference, which records one dispatch per conv op
  * (net/build.rs:209-278).
  * desc_b: B's n, h, w and cin equal A's n, output height and width and cout; B's input view is ignored.
  * flags: FHC_PAIR_RES_MID makes B's residual A's output (B.residual set, B.cout == B.cin; graph.json's
- * "add" of e2 and e1), else B's residual, if any, is the `res` tensor of fhc_conv_run; bits 8-15: output rows
- * per tile (2 or 4; 0: the planner's choice); bits 16-19: wave rows splitting them (1 or 2; 0: 1). The plan runs
- * with fhc_conv_run (x: A's input, y and res: B's output
- * and residual), is described by fhc_conv_describe (family "pair") and freed by fhc_conv_plan_destroy. The
- * instantiated pairs cover, in channels A.cin -> A.cout -> B.cout: stride 2 <= 32 -> 33..48 -> 33..48, and stride
- * 1 33..64 -> 33..48 -> 33..48, <= 32 -> 17..32 -> 17..32 and <= 32 -> 17..32 -> <= 16; other shapes are an
- * error status. */
+ * "add" of e2 and e1, e4 and e3), else B's residual, if any, is the `res` tensor of fhc_conv_run; bits 8-15:
+ * output rows per tile (1, 2 or 4 as instantiated; 0: the tallest that still gives 256 workgroups, else the
+ * shortest); bits 16-19: wave rows splitting them (1 or 2; 0: 1). The plan runs with fhc_conv_run (x: A's input,
+ * y and res: B's output and residual), is described by fhc_conv_describe (family "pair") and freed by
+ * fhc_conv_plan_destroy. The instantiated pairs cover, in channels A.cin -> A.cout -> B.cout: stride 2
+ * <= 32 -> 33..48 -> 33..48 (2 or 4 rows) and 33..64 -> 65..80 -> 65..80 (1 or 2 rows, one wave row), and stride 1
+ * 33..64 -> 33..48 -> 33..48, <= 32 -> 17..32 -> 17..32 and <= 32 -> 17..32 -> <= 16 (2 or 4 rows); other shapes
+ * are an error status. */
 #define FHC_PAIR_RES_MID 1u
 int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
                               const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
@@ -134,7 +135,10 @@ int fhc_tune_parse(const char* text);           /* merges; returns the number of
 int fhc_tune_format(char* text, size_t cap);    /* sorted lines; bytes written, or -1 if cap too small */
 int fhc_tune_clear(void);
 int fhc_tune_get(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride); /* code or -1 */
-/* Name of an MI355X variant code ("igemm.t8x16.n64/k2" ...) into buf; bytes written or -1. */
+/* Name of an MI355X variant code into buf; bytes written or -1. Codes 1..127 are the K-chunked kernels: bits 0-4
+ * the configuration (1..10 the chunked implicit GEMM, "igemm.t8x16.n64"; 16..28 the deep-layer kernel with LDS
+ * DMA, "gemm.t8x16.n48.f2x3.w4x1.c32.p2"), bits 5-6 the global split (1, 2, 4, 8: "/k2"); 128 + i the direct
+ * kernel's configuration i ("direct.c64.t4x1.n64/p"). */
 int fhc_variant_name(uint32_t code, char* buf, size_t cap);
 /* The MI355X variant codes worth timing for a descriptor (the counterpart of cand_list); count written, or -1. */
 int fhc_variant_list(const fhc_conv_desc* desc, uint32_t* codes, size_t cap);
