@@ -85,10 +85,14 @@ class Net:
 
     def fuse(self, pairs, torch, fhconv, stream, time_fn, default_tile=False):
         """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; every
-        instantiated tile height (1, 2 or 4 rows) and wave rows (1 or 2) timed on the real buffers, the fastest kept
-        (default_tile: the pair planner's own choice, no timing), and only where it beats the two separate
-        launches."""
+        instantiated tile height (1, 2, 4 or 8 rows), wave rows (1 or 2) and loop (one workgroup per tile, or a
+        resident grid) timed on the real buffers, the fastest kept (default_tile: the pair planner's own choice, no
+        timing), and only where it beats the two separate launches. A pair that shares a conv with one fused
+        before it is skipped."""
+        used = set()
         for A, B, res_mid in pairs:
+            if A.name in used or B.name in used:
+                continue
             sep = time_fn(lambda i=0: (self.run_one(A, stream=stream), self.run_one(B, stream=stream)))
             da, wa, ba, sa = self.params[A.name]
             db, wb, bb, sb = self.params[B.name]
@@ -96,10 +100,12 @@ class Net:
             _, y, r, _ = self.bufs[B.name]
             rx = None if res_mid else r
             best = None
-            for th, wm in ((0, 0),) if default_tile else ((1, 1), (2, 1), (4, 1), (2, 2), (4, 2)):
+            combos = [(0, 0, 0)] if default_tile else \
+                [(th, wm, lp) for lp in (1, 2) for th, wm in ((1, 1), (2, 1), (4, 1), (2, 2), (4, 2), (8, 2))]
+            for th, wm, lp in combos:
                 try:
                     pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th,
-                                             wave_rows=wm)
+                                             wave_rows=wm, loop=lp)
                 except fhconv.FhcError:
                     continue  # not instantiated for these channels
                 us = time_fn(lambda i=0, pp=pp: pp.run(x, y, rx, stream=stream))
@@ -107,6 +113,7 @@ class Net:
                     best = (pp, us)
             if best is not None and best[1] < sep:
                 self.pairs[A.name] = (best[0], B, round(best[1], 3), res_mid)
+                used |= {A.name, B.name}
 
     def run_one(self, L, stream=None):
         x, y, r, ws = self.bufs[L.name]
@@ -551,7 +558,7 @@ def main():
         for a_name in net.pairs:
             per_pair.append(pair_timing(torch, net, a_name, args.reps, args.graphs, args.cold_mb << 20, stream))
             log("pair", json.dumps(per_pair[-1]))
-    cfg_layers = []
+    cfg_layers, cfg_pairs = [], []
     if not args.no_configs:
         for c in (1, 2, 3):
             cl = flyhighfg.config_layers(c)
@@ -560,6 +567,14 @@ def main():
                 cfg_layers.append(dict(config=c, **layer_timing(torch, np, fhconv, cnet, L, args.reps,
                                                                 args.graphs, args.cold_mb << 20, stream)))
                 log("config layer", json.dumps(cfg_layers[-1]))
+            # the ladder's consecutive 64 -> 64 convs also as a fused pair (one launch, the intermediate on chip)
+            if not args.no_fuse:
+                cnet.fuse(flyhighfg.fusible_pairs(cl), torch, fhconv, stream,
+                          lambda fn: time_graph(torch, fn, 20, 3, stream), default_tile=bool(args.tune))
+                for a_name in cnet.pairs:
+                    cfg_pairs.append(dict(config=c, **pair_timing(torch, cnet, a_name, args.reps, args.graphs,
+                                                                  args.cold_mb << 20, stream)))
+                    log("config pair", json.dumps(cfg_pairs[-1]))
             del cnet
             torch.cuda.empty_cache()
 
@@ -615,6 +630,7 @@ def main():
         fuse_check=fuse_check, event_ms_per_step=round(ev_ms, 6),
         submit_us_per_step=round(t_submit * 1e6 / args.steps, 3),
         roofline=roofline, cpu_baseline=cpu, layers=per_layer, pairs=per_pair, config_layers=cfg_layers,
+        config_pairs=cfg_pairs,
         batched=batched,
         tune_table=tune_table,
     )

@@ -636,11 +636,12 @@ std::string describe_json(const fhc_conv_plan* p) {
                                     (b.act == FHC_ACT_PRELU ? b.cout : 0) + (b.residual && !p->res_mid ? out_el : 0));
         char buf[700];
         snprintf(buf, sizeof buf,
-                 "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d.w%d\",\"family\":\"pair\",\"cfg\":%d,"
-                 "\"tile_rows\":%d,\"tile_cols\":%d,\"wave_rows\":%d,\"res_mid\":%d,\"tiles\":%u,\"grid\":[%u,%u],"
-                 "\"threads\":%u,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
-                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, c.wm, p->cfg, c.th, kPairTileW, c.wm,
-                 p->res_mid, p->tiles, p->grid.x, p->grid.y, p->threads, p->g.hout, p->g.wout, fa + fb, bytes);
+                 "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d.w%d%s\",\"family\":\"pair\",\"cfg\":%d,"
+                 "\"tile_rows\":%d,\"tile_cols\":%d,\"wave_rows\":%d,\"persistent\":%d,\"res_mid\":%d,\"tiles\":%u,"
+                 "\"grid\":[%u,%u,%u],\"threads\":%u,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
+                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, c.wm, c.persist ? "/p" : "", p->cfg,
+                 c.th, kPairTileW, c.wm, c.persist, p->res_mid, p->tiles, p->grid.x, p->grid.y, p->grid.z, p->threads,
+                 p->g.hout, p->g.wout, fa + fb, bytes);
         return buf;
     }
     if (p->family == 1) {
@@ -868,8 +869,9 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         if (!valid_desc(A, &why)) return fail(-1, "fhc_conv_pair_plan_create: first conv: %s", why.c_str());
         if (!valid_desc(B, &why)) return fail(-1, "fhc_conv_pair_plan_create: second conv: %s", why.c_str());
         const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0;
-        const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu;
-        if ((flags & ~(FHC_PAIR_RES_MID | 0xfff00u)) != 0) return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
+        const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu, loop_req = (flags >> 20) & 3u;
+        if ((flags & ~(FHC_PAIR_RES_MID | 0x3fff00u)) != 0 || loop_req == 3)
+            return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
         const uint32_t ha = (A.h + 2 * A.pad - A.kh) / A.stride + 1, wa = (A.w + 2 * A.pad - A.kw) / A.stride + 1;
         if (A.kh != 3 || B.kh != 3 || B.stride != 1 || A.residual)
             return fail(-1, "fhc_conv_pair_plan_create: the pair is a 3x3 conv (stride 1 or 2, no residual) then a 3x3 "
@@ -884,15 +886,24 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
             return fail(-1, "fhc_conv_pair_plan_create: PReLU needs a slope");
         const int ca32 = (int)div_ceil(A.cin, 32) * 32, cb32 = (int)div_ceil(B.cin, 32) * 32;
         const int nba = (int)div_ceil(A.cout, 16), nbb = (int)div_ceil(B.cout, 16);
-        // the configuration at the requested tile height and wave rows; by default one wave row and the tallest
-        // instantiated tile that still gives 256 workgroups, else the shortest
+        // the configuration at the requested tile height, wave rows and loop; by default one wave row, the
+        // resident-grid loop when it is instantiated and there are at least 8 tiles per CU of an MI355X (256), and
+        // the tallest instantiated tile that still gives 256 workgroups, else the shortest
         const int wm = wm_req ? (int)wm_req : 1;
         auto tiles_at = [&](int th) { return (uint64_t)A.n * div_ceil(ha, (uint32_t)th) * div_ceil(wa, kPairTileW); };
+        int persist = loop_req == 2 ? 1 : 0;
+        if (loop_req == 0)
+            for (int i = 0; i < kNumPair; i++) {
+                const PairCfg& c = kPairCfgs[i];
+                if (c.persist && c.sa == (int)A.stride && c.ca32 == ca32 && c.cb32 == cb32 && c.nba == nba &&
+                    c.nbb == nbb && c.wm == wm && (!th_req || c.th == (int)th_req) && tiles_at(c.th) >= 8 * 256)
+                    persist = 1;
+            }
         int idx = -1;
         for (int i = 0; i < kNumPair; i++) {
             const PairCfg& c = kPairCfgs[i];
             if (c.sa != (int)A.stride || c.ca32 != ca32 || c.cb32 != cb32 || c.nba != nba || c.nbb != nbb ||
-                c.wm != wm)
+                c.wm != wm || c.persist != persist)
                 continue;
             if (th_req) {
                 if (c.th == (int)th_req) idx = i;
@@ -905,7 +916,7 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         if (idx < 0)
             return fail(-1, "fhc_conv_pair_plan_create: no fused pair instantiated for stride %u, %u -> %u -> %u "
                             "channels%s", A.stride, A.cin, A.cout, B.cout,
-                        th_req || wm_req ? " at that tile height and wave split" : "");
+                        th_req || wm_req || loop_req ? " at that tile height, wave split and loop" : "");
         const PairCfg& c = kPairCfgs[idx];
         auto pa = std::make_unique<fhc_conv_plan>();
         auto pb = std::make_unique<fhc_conv_plan>();
@@ -928,6 +939,18 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         pa->tiles = (uint32_t)((uint64_t)A.n * tiles_y * tiles_x);
         pa->grid = dim3(pa->tiles, 1, 1);
         pa->threads = 64u * (uint32_t)std::max(c.nba, c.nbb) * (uint32_t)c.wm;
+        if (c.persist) {  // the resident grid: as many workgroups as fit at once
+            const void* k = nullptr;
+            pair_launcher(idx, &k);
+            int per_cu = 0, cus = 0;
+            if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, (int)pa->threads, 0) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, pa->device) != hipSuccess) {
+                (void)hipFree(pa->dmem);
+                (void)hipFree(pb->dmem);
+                return fail(-1, "fhc_conv_pair_plan_create: occupancy query failed");
+            }
+            pa->grid.x = (unsigned)std::min<uint64_t>(pa->tiles, (uint64_t)std::max(1, per_cu) * std::max(1, cus));
+        }
         pa->lds = 0;
         pa->ws_bytes = 0;
         pa->launch = nullptr;

@@ -97,25 +97,34 @@ struct PairKArgs {
 };
 constexpr int kPairTileW = 14;  // output columns per tile (B's 16-pixel MFMA block reads 16 + 2 columns of A)
 // The instantiated pairs: A's stride, A's and B's input channels padded to 32, A's and B's output channel blocks
-// of 16, the output rows per tile and the wave rows that split them.
+// of 16, the output rows per tile, the wave rows that split them, and the loop: 0 one workgroup per tile (weights
+// loaded per tile: small frames), 1 a resident grid looping over tiles (weights loaded once: large tensors).
 struct PairCfg {
-    int sa, ca32, cb32, nba, nbb, th, wm;
+    int sa, ca32, cb32, nba, nbb, th, wm, persist;
 };
-constexpr int kNumPair = 18;
+constexpr int kNumPair = 30;
 inline constexpr PairCfg kPairCfgs[kNumPair] = {
     // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
-    {2, 32, 64, 3, 3, 2, 1}, {2, 32, 64, 3, 3, 4, 1}, {2, 32, 64, 3, 3, 2, 2}, {2, 32, 64, 3, 3, 4, 2},
+    {2, 32, 64, 3, 3, 2, 1, 0}, {2, 32, 64, 3, 3, 4, 1, 0}, {2, 32, 64, 3, 3, 2, 2, 0}, {2, 32, 64, 3, 3, 4, 2, 0},
     // 48 -> 48 -> 48 (FiLM head, fine block)
-    {1, 64, 64, 3, 3, 2, 1}, {1, 64, 64, 3, 3, 4, 1}, {1, 64, 64, 3, 3, 2, 2}, {1, 64, 64, 3, 3, 4, 2},
+    {1, 64, 64, 3, 3, 2, 1, 0}, {1, 64, 64, 3, 3, 4, 1, 0}, {1, 64, 64, 3, 3, 2, 2, 0}, {1, 64, 64, 3, 3, 4, 2, 0},
     // <= 32 -> 32 -> 32 (refine head)
-    {1, 32, 32, 2, 2, 2, 1}, {1, 32, 32, 2, 2, 4, 1}, {1, 32, 32, 2, 2, 2, 2}, {1, 32, 32, 2, 2, 4, 2},
+    {1, 32, 32, 2, 2, 2, 1, 0}, {1, 32, 32, 2, 2, 4, 1, 0}, {1, 32, 32, 2, 2, 2, 2, 0}, {1, 32, 32, 2, 2, 4, 2, 0},
     // <= 32 -> 32 -> 16 (refine head output)
-    {1, 32, 32, 2, 1, 2, 1}, {1, 32, 32, 2, 1, 4, 1}, {1, 32, 32, 2, 1, 2, 2}, {1, 32, 32, 2, 1, 4, 2},
+    {1, 32, 32, 2, 1, 2, 1, 0}, {1, 32, 32, 2, 1, 4, 1, 0}, {1, 32, 32, 2, 1, 2, 2, 0}, {1, 32, 32, 2, 1, 4, 2, 0},
     // the encoder's second stride-2 conv and its successor (36 -> 72 -> 72)
-    {2, 64, 96, 5, 5, 1, 1}, {2, 64, 96, 5, 5, 2, 1},
+    {2, 64, 96, 5, 5, 1, 1, 0}, {2, 64, 96, 5, 5, 2, 1, 0},
+    // resident-grid loops: 64 -> 64 -> 64 (the 1080p/4 ladder), then the frame's pairs at batch scale (the
+    // 36 -> 72 -> 72 pair and taller 64-channel tiles spill)
+    {1, 64, 64, 4, 4, 4, 1, 1}, {1, 64, 64, 4, 4, 4, 2, 1},
+    {1, 64, 64, 3, 3, 4, 1, 1}, {1, 64, 64, 3, 3, 4, 2, 1},
+    {2, 32, 64, 3, 3, 4, 1, 1}, {2, 32, 64, 3, 3, 4, 2, 1},
+    {1, 32, 32, 2, 2, 4, 1, 1}, {1, 32, 32, 2, 2, 4, 2, 1}, {1, 32, 32, 2, 2, 8, 2, 1},
+    {1, 32, 32, 2, 1, 4, 1, 1}, {1, 32, 32, 2, 1, 4, 2, 1}, {1, 32, 32, 2, 1, 8, 2, 1},
 };
 using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);
-PairLaunchFn pair_launcher(int index);
+// The launcher of pair configuration `index`, or nullptr; *kernel receives the (persistent) kernel's address.
+PairLaunchFn pair_launcher(int index, const void** kernel = nullptr);
 
 // Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the
 // operand layouts the conv kernels assume. Device pointers.

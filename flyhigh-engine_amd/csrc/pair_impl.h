@@ -18,6 +18,14 @@
 
 namespace fhc {
 
+// The value, made opaque to the optimizer (an empty asm that takes and returns it in VGPRs): a select between a
+// value loaded from LDS and a register array element is otherwise rewritten into one load from a select of the
+// two addresses, which puts the register array in scratch memory and reads it through a flat load.
+__device__ __forceinline__ uint2 opaque_u2(uint2 v) {
+    asm volatile("" : "+v"(v.x), "+v"(v.y));
+    return v;
+}
+
 // The q-ring MFMA chain over an LDS tile (as direct_impl.h's WK == 1 chain, one channel block): output rows
 // f = 0 .. FM-1 of stride S read tile rows f * S + ky; operand q = (kx * M + m) * R + r is read once and feeds every
 // (f, ky) use; reads run D operands ahead. base: the lane's pixel (row 0, column (lane & 15) * S) and channel group.
@@ -165,12 +173,231 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
             const int f = wm * THW + fw;
             const int oy = oy0 + f, ox = ox0 + lx;
             if (lx < TWB && oy < b.hout && ox < b.wout && cob < b.cout) {
-                const uint2 rv = pk.res_mid ? *reinterpret_cast<const uint2*>(mid + ((f + 1) * MW + lx + 1) * PSB + cob)
-                                            : rres[fw];
+                // both values read, then selected as values (opaque_u2); the LDS read is in bounds for every lane
+                const uint2 mv = opaque_u2(*reinterpret_cast<const uint2*>(mid + ((f + 1) * MW + lx + 1) * PSB + cob));
+                const uint2 rv = pk.res_mid ? mv : rres[fw];
                 epilogue4r(b, ((size_t)img * b.hout + oy) * b.wout + ox, cob, acc[fw], biasb, negb, rv);
             }
         }
     }
+}
+
+// The persistent pair: G = gridDim.x resident workgroups loop over B's output tiles t, t + G, ... with both layers'
+// weights, biases and multipliers loaded once. Input, external residual and output go through buffer instructions
+// (out-of-range lanes: zero loads, dropped stores), so no memory access sits in a branch and the compiler's waits
+// stay exact; waves without a channel block of A or B skip only the MFMAs and the LDS traffic. Per tile: A's chain
+// and epilogue into the LDS tile; a barrier; the next tile's halo (in registers since the previous tile) into LDS
+// and the loads of the tile after it, which then fly during B's chain and the next tile's A chain; B's chain and
+// epilogue with its stores; the next tile's residual loads; a barrier. The intermediate never leaves the CU.
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
+__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair_p(PairKArgs pk) {
+    constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN * WM, TWB = kPairTileW;
+    constexpr int FA = TH + 2, FAW = FA / WM, THW = TH / WM;
+    static_assert(FA % WM == 0 && TH % WM == 0, "rows split evenly over the wave rows");
+    constexpr int IHA = (FA - 1) * SA + 3, IWA = 15 * SA + 3;
+    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32;
+    constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;
+    constexpr int HALO = IHA * IWA * GPA, NLD = (HALO + NT - 1) / NT;
+    static_assert(NBA * 16 <= CB32, "A's channel blocks exceed B's input channels");
+    __shared__ __align__(16) uint16_t hin[IHA * IWA * PSA];
+    __shared__ __align__(16) uint16_t mid[FA * MW * PSB];
+    const ConvKArgs& a = pk.a;
+    const ConvKArgs& b = pk.b;
+
+    const int tid = threadIdx.x, lane = tid & 63, lx = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: the A / B branches are uniform
+    const int wn = wave % WN, wm = wave / WN;
+    const int wa = wn < NBA ? wn : NBA - 1, wb = wn < NBB ? wn : NBB - 1;
+    const int coa = wa * 16 + 4 * (lane >> 4), cob = wb * 16 + 4 * (lane >> 4);
+    const int tiles = b.n * b.tiles_y * b.tiles_x, G = gridDim.x;
+    int t = blockIdx.x;
+    if (t >= tiles) return;  // uniform over the workgroup
+    const bool ext_res = b.residual && !pk.res_mid;
+    const uint64_t pix_out = (uint64_t)b.n * b.hout * b.wout;
+    const auto rx = buffer_rsrc(a.x, (uint32_t)((uint64_t)a.n * a.h * a.w * a.xcs * 2));
+    const auto ry = buffer_rsrc(b.y, (uint32_t)view_bytes(pix_out, b.ycs, b.yc0, b.cout));
+    const auto rr = buffer_rsrc(b.res, ext_res ? (uint32_t)view_bytes(pix_out, b.rcs, b.rc0, b.cout) : 0u);
+
+    auto tile_origin = [&](int tt, int& img, int& oy0, int& ox0) {
+        const int tx = tt % b.tiles_x, r0 = tt / b.tiles_x;
+        oy0 = (r0 % b.tiles_y) * TH;
+        img = r0 / b.tiles_y;
+        ox0 = tx * TWB;
+    };
+    // lane parts of the halo addresses, fixed for the launch (as in the persistent direct loop)
+    uint32_t hoff[NLD];
+    int hpos[NLD];
+    bool hst[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; i++) {
+        const int e = tid + i * NT;
+        const int pix = e / GPA, g = e - pix * GPA;
+        const int iy = pix / IWA, ix = pix - iy * IWA;
+        hoff[i] = ((uint32_t)(iy * a.w + ix) * (uint32_t)a.xcs + (uint32_t)(a.xc0 + g * 8)) * 2u;
+        hpos[i] = (iy << 16) | ix;
+        hst[i] = ((i + 1) * NT <= HALO || e < HALO) & (g * 8 < a.cin);
+    }
+    uint4 pre[NLD];
+    auto load_halo = [&](int tt) {  // tile tt's A input halo into registers (a tile past the last reads zeros)
+        int img, oy0, ox0;
+        tile_origin(tt, img, oy0, ox0);
+        const int iy0 = (oy0 - 1) * SA - a.pad, ix0 = (ox0 - 1) * SA - a.pad;
+        const uint32_t base = (((uint32_t)(img * a.h + iy0) * (uint32_t)a.w + (uint32_t)ix0) * (uint32_t)a.xcs) * 2u;
+        const bool tv = tt < tiles;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int gy = iy0 + (hpos[i] >> 16), gx = ix0 + (hpos[i] & 0xffff);
+            const bool ok = hst[i] & tv & ((uint32_t)gy < (uint32_t)a.h) & ((uint32_t)gx < (uint32_t)a.w);
+            pre[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? base + hoff[i] : kOOB, 0, 0));
+        }
+    };
+    auto write_halo = [&]() {
+        const bool part = (a.cin & 7) != 0;  // uniform
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * NT;
+            if ((i + 1) * NT <= HALO || e < HALO) {
+                const int pix = e / GPA, g = e - pix * GPA;
+                *reinterpret_cast<uint4*>(hin + pix * PSA + g * 8) = part ? mask_group(pre[i], a.cin - g * 8) : pre[i];
+            }
+        }
+    };
+    // B's output and external residual: per-tile scalar base + lane part; validity of row f for this lane
+    const uint32_t yl = ((uint32_t)lx * (uint32_t)b.ycs + (uint32_t)(b.yc0 + cob)) * 2u;
+    const uint32_t rl = ((uint32_t)lx * (uint32_t)b.rcs + (uint32_t)(b.rc0 + cob)) * 2u;
+    const uint32_t yrow = (uint32_t)b.wout * (uint32_t)b.ycs * 2u, rrow = (uint32_t)b.wout * (uint32_t)b.rcs * 2u;
+    auto out_ok = [&](int oy0, int ox0, int f) {
+        return (wn < NBB) & (lx < TWB) & (oy0 + wm * THW + f < b.hout) & (ox0 + lx < b.wout) & (cob < b.cout);
+    };
+    uint2 rres[THW];
+    auto load_res = [&](int tt) {
+        int img, oy0, ox0;
+        tile_origin(tt, img, oy0, ox0);
+        const uint32_t base =
+            ((uint32_t)(img * b.hout + oy0 + wm * THW) * (uint32_t)b.wout + (uint32_t)ox0) * (uint32_t)b.rcs * 2u;
+        const bool tv = (tt < tiles) & ext_res;
+#pragma unroll
+        for (int f = 0; f < THW; f++)
+            rres[f] = __builtin_bit_cast(
+                uint2, __builtin_amdgcn_raw_buffer_load_b64(rr, (out_ok(oy0, ox0, f) & tv) ? base + f * rrow + rl : kOOB,
+                                                            0, 0));
+    };
+
+    // once: the first halo, both layers' weights, biases and multipliers, the zero channels of the LDS tile
+    load_halo(t);
+    h8 wra[9 * MA], wrb[9 * MB];
+    {
+        const h8* wp = reinterpret_cast<const h8*>(a.wpk) + (size_t)wa * 9 * MA * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < 9 * MA; s++) wra[s] = wp[s * 64];
+        const h8* wq = reinterpret_cast<const h8*>(b.wpk) + (size_t)wb * 9 * MB * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < 9 * MB; s++) wrb[s] = wq[s * 64];
+    }
+    float biasa[4], nega[4], biasb[4], negb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        biasa[i] = h2f(a.bias[coa + i]);
+        biasb[i] = h2f(b.bias[cob + i]);
+    }
+    {
+        const float4 m = *reinterpret_cast<const float4*>(a.neg + coa);
+        const float4 n = *reinterpret_cast<const float4*>(b.neg + cob);
+        nega[0] = m.x, nega[1] = m.y, nega[2] = m.z, nega[3] = m.w;
+        negb[0] = n.x, negb[1] = n.y, negb[2] = n.z, negb[3] = n.w;
+    }
+    if constexpr (NBA * 16 < CB32) {
+        constexpr int G0 = NBA * 2, GN = CB32 / 8 - G0, NZ = FA * MW * GN;
+        for (int e = tid; e < NZ; e += NT) {
+            const int pix = e / GN, g = G0 + e % GN;
+            *reinterpret_cast<uint4*>(mid + pix * PSB + g * 8) = uint4{0u, 0u, 0u, 0u};
+        }
+    }
+    write_halo();
+    __syncthreads();
+    load_halo(t + G);
+    load_res(t);
+
+    typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
+    for (; t < tiles; t += G) {
+        int img, oy0, ox0;
+        tile_origin(t, img, oy0, ox0);
+        // A over FA rows x 16 columns; its f16 output (zero outside the image) into the LDS tile
+        if (wn < NBA) {
+            f4 acc[FAW];
+            pair_chain<FAW, SA, MA, IWA, PSA>(acc, wra, hin + (wm * FAW * SA * IWA + lx * SA) * PSA + (lane >> 4) * 8);
+#pragma unroll
+            for (int fw = 0; fw < FAW; fw++) {
+                const int f = wm * FAW + fw;
+                const int oy = oy0 - 1 + f, ox = ox0 - 1 + lx;
+                const bool in = (oy >= 0) & (oy < a.hout) & (ox >= 0) & (ox < a.wout);
+                uint16_t o[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] = in ? f2h(activate(acc[fw][i] + biasa[i], nega[i])) : (uint16_t)0;
+                *reinterpret_cast<uint2*>(mid + (f * MW + lx) * PSB + coa) =
+                    uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+            }
+        }
+        __syncthreads();  // the LDS tile is complete and every wave is done reading the halo
+        write_halo();     // the next tile's halo
+        load_halo(t + 2 * G);
+        // B over TH rows x 16 columns (the first 14 stored)
+        f4 acc[THW];
+#pragma unroll
+        for (int fw = 0; fw < THW; fw++) acc[fw] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (wn < NBB)
+            pair_chain<THW, 1, MB, MW, PSB>(acc, wrb, mid + (wm * THW * MW + lx) * PSB + (lane >> 4) * 8);
+        const uint32_t ybase =
+            ((uint32_t)(img * b.hout + oy0 + wm * THW) * (uint32_t)b.wout + (uint32_t)ox0) * (uint32_t)b.ycs * 2u;
+#pragma unroll
+        for (int fw = 0; fw < THW; fw++) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = activate(acc[fw][i] + biasb[i], negb[i]);
+            hh2 p0 = hh2{(_Float16)v[0], (_Float16)v[1]}, p1 = hh2{(_Float16)v[2], (_Float16)v[3]};
+            if (b.residual) {  // uniform; A's output at the same pixel, or the external tensor
+                // both values read, then selected as values (opaque_u2)
+                const uint2 mv =
+                    opaque_u2(*reinterpret_cast<const uint2*>(mid + ((wm * THW + fw + 1) * MW + lx + 1) * PSB + cob));
+                const uint2 rv = pk.res_mid ? mv : rres[fw];
+                p0 += __builtin_bit_cast(hh2, rv.x);
+                p1 += __builtin_bit_cast(hh2, rv.y);
+            }
+            const uint32_t off = out_ok(oy0, ox0, fw) ? ybase + fw * yrow + yl : kOOB;
+            __builtin_amdgcn_raw_buffer_store_b64(
+                __builtin_bit_cast(__attribute__((ext_vector_type(2))) uint32_t,
+                                   uint2{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1)}),
+                ry, off, 0, 0);
+        }
+        load_res(t + G);
+        __syncthreads();  // the next halo is in LDS and every wave is done reading the LDS tile
+    }
+}
+
+// Whether the persistent pair's buffer loop serves these views (16-byte input groups, 8-byte output and
+// residual quads, every view below 2^31 bytes); else the one-tile kernel runs.
+inline bool pair_buffer_ok(const PairKArgs& pk) {
+    const ConvKArgs &a = pk.a, &b = pk.b;
+    const uint64_t lim = 1ull << 31, pout = (uint64_t)b.n * b.hout * b.wout;
+    const bool ext = b.residual && !pk.res_mid;
+    return a.xvec && b.yvec && b.cout % 4 == 0 && (!ext || b.rvec) &&
+           (uint64_t)a.n * a.h * a.w * (uint64_t)a.xcs * 2 < lim && view_bytes(pout, b.ycs, b.yc0, b.cout) < lim &&
+           (!ext || view_bytes(pout, b.rcs, b.rc0, b.cout) < lim);
+}
+
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
+hipError_t launch_pair_p(const PairKArgs& pk, dim3 grid, hipStream_t s) {
+    const dim3 block(64 * (NBA > NBB ? NBA : NBB) * WM);
+    if (pair_buffer_ok(pk)) {
+        hipLaunchKernelGGL((conv_pair_p<SA, CA32, CB32, NBA, NBB, TH, WM>), grid, block, 0, s, pk);
+        return hipGetLastError();
+    }
+    grid.x = (unsigned)(pk.b.n * pk.b.tiles_y * pk.b.tiles_x);  // one workgroup per tile
+    if (pk.a.xvec)
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true>), grid, block, 0, s, pk);
+    else
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false>), grid, block, 0, s, pk);
+    return hipGetLastError();
 }
 
 template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>

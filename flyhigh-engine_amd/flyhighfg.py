@@ -122,10 +122,11 @@ def flyhighfg_layers(net_w: int = 864, net_h: int = 480, k: int = 1, batch_encod
 
 
 # Consecutive convs of models/graph.json whose intermediate tensor has no other reader (enc.e1's and enc.e3's outputs
-# are also the residuals that enc.e2's and enc.e4's "add" take: the pair's second conv adds the first's output): each pair can run as one fused
+# are also the residuals that enc.e2's and enc.e4's "add" take: the pair's second conv adds the first's output),
+# and of the 1080p/4 ladder configuration (one of its two overlapping pairs runs fused): each pair can run as one fused
 # launch (fhc_conv_pair_plan_create). (first conv, second conv, second's residual is the first's output)
 FUSIBLE_PAIRS = [("enc.e1", "enc.e2", True), ("enc.e3", "enc.e4", True), ("fine.r2", "fine.r3", False),
-                 ("film.h1", "film.h2", False),
+                 ("film.h1", "film.h2", False), ("c2.b1", "c2.b2", False), ("c2.b2", "c2.b3", False),
                  ("refine.q1", "refine.q2", False), ("refine.q3", "refine.q4", False)]
 
 

@@ -486,3 +486,74 @@ def test_gemm_variants_full_size(shape):
         for r0, want in bands.items():
             ok, md, mref = parity(got[0, r0:r0 + 4], want)
             assert ok, (d["name"], r0, md, mref)
+
+
+# the resident-grid pair (weights loaded once, tiles looped over): cases with more tiles than the grid holds, so
+# every workgroup runs several iterations. n, h, w, cin, cmid, cout, A's stride, A's and B's activation, B's
+# residual, A's input view, B's output view
+PAIR_P_CASES = [(4, 64, 200, 48, 64, 64, 1, 1, 1, None, (56, 0), None),
+                (4, 61, 203, 48, 48, 48, 1, 1, 1, "ext", None, None),
+                (24, 50, 90, 3, 36, 36, 2, 1, 1, "mid", (8, 0), None),
+                (4, 120, 216, 14, 24, 24, 1, 1, 1, None, (16, 0), None),
+                (4, 119, 213, 24, 24, 3, 1, 2, 0, None, None, (8, 0))]
+
+
+def run_pair(A, B, res, **kw):
+    import torch
+    plan = fhconv.ConvPairPlan(A.fhc_desc(), A.wt, A.bias, A.slope if A.act == 1 else None, B.fhc_desc(), B.wt,
+                               B.bias, B.slope if B.act == 1 else None, res_mid=res == "mid", **kw)
+    dev = torch.device("cuda", 0)
+    x = torch.from_numpy(np.ascontiguousarray(A.x).view(np.int16)).to(dev)
+    y = torch.from_numpy(np.ascontiguousarray(B.y0).view(np.int16)).to(dev)
+    r = torch.from_numpy(np.ascontiguousarray(B.res).view(np.int16)).to(dev) if res == "ext" else None
+    plan.run(x, y, r)
+    torch.cuda.synchronize()
+    return y.cpu().numpy().view(np.uint16), plan
+
+
+@pytest.mark.parametrize("case", PAIR_P_CASES, ids=lambda c: "x".join(map(str, c[:7])) + (f"-{c[9]}" if c[9] else ""))
+@pytest.mark.parametrize("th,wm", [(4, 1), (4, 2), (8, 2)], ids=["t4w1", "t4w2", "t8w2"])
+def test_resident_pair_matches_the_two_convs(case, th, wm):
+    n, h, w, cin, cmid, cout, sa, act_a, act_b, res, xv, yv = case
+    A = Case(n, h, w, cin, cmid, stride=sa, act=act_a, xv=xv, poison=xv is not None, seed=61)
+    ya = A.run_oracle(threads=8)
+    B = Case(n, A.hout, A.wout, cmid, cout, act=act_b, residual=res is not None, yv=yv, poison=yv is not None, seed=62)
+    B.x = ya
+    if res == "mid":
+        B.res = ya
+    want = B.run_oracle(threads=8)
+    try:
+        got, plan = run_pair(A, B, res, tile_rows=th, wave_rows=wm, loop=2)
+    except fhconv.FhcError as e:
+        assert "no fused pair instantiated" in str(e)
+        pytest.skip(f"no resident pair at {th} rows x {wm} wave rows for these channels")
+    d = plan.describe()
+    say("pair/p", case[:7], d["name"], d["grid"], d["tiles"])
+    assert d["persistent"] == 1 and d["tile_rows"] == th and d["grid"][0] < d["tiles"]
+    sl = slice(B.yc0, B.yc0 + cout)
+    ok, md, mref = parity(got, want, view=sl)
+    assert ok, (d["name"], md, mref)
+    mask = np.ones(B.ycs, bool)
+    mask[sl] = False
+    assert np.array_equal(got[..., mask], B.y0[..., mask])
+
+
+def test_resident_pair_full_size_ladder():
+    # the 1080p/4 ladder's two 64 -> 64 convs as one resident-grid pair (the library's default for this size),
+    # rows checked in bands: B's rows [r0, r0 + 4) from the oracle of A's rows [r0 - 1, r0 + 5)
+    import copy
+    A = Case(1, 272, 480, 64, 64, act=1, seed=63)
+    B = Case(1, 272, 480, 64, 64, act=1, seed=64)
+    got, plan = run_pair(A, B, None)
+    d = plan.describe()
+    say("pair/p", d["name"], d["grid"], d["tiles"])
+    assert d["persistent"] == 1
+    for r0 in (0, 134, 268):
+        a0, a1 = max(0, r0 - 1), min(272, r0 + 5)
+        band = copy.copy(B)
+        band.h = band.hout = a1 - a0
+        band.x = oracle_rows(A, a0, a1, threads=8)
+        band.y0 = np.zeros((1, a1 - a0, 480, 64), np.uint16)
+        want = band.run_oracle(threads=8)[:, r0 - a0:r0 - a0 + 4]
+        ok, md, mref = parity(got[:, r0:r0 + 4], want)
+        assert ok, (r0, md, mref)
