@@ -886,27 +886,29 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
             return fail(-1, "fhc_conv_pair_plan_create: PReLU needs a slope");
         const int ca32 = (int)div_ceil(A.cin, 32) * 32, cb32 = (int)div_ceil(B.cin, 32) * 32;
         const int nba = (int)div_ceil(A.cout, 16), nbb = (int)div_ceil(B.cout, 16);
-        // the configuration at the requested tile height, wave rows and loop; by default one wave row, the
-        // resident-grid loop when it is instantiated and there are at least 8 tiles per CU of an MI355X (256), and
-        // the tallest instantiated tile that still gives 256 workgroups, else the shortest
-        const int wm = wm_req ? (int)wm_req : 1;
+        // the configuration at the requested tile height, wave rows and loop; by default the resident-grid loop
+        // when it is instantiated and there are at least 8 tiles per CU of an MI355X (256), one wave row where that
+        // is instantiated (else two), and the tallest instantiated tile that still gives 256 workgroups, else the
+        // shortest
         auto tiles_at = [&](int th) { return (uint64_t)A.n * div_ceil(ha, (uint32_t)th) * div_ceil(wa, kPairTileW); };
+        auto serves = [&](const PairCfg& c) {
+            return c.sa == (int)A.stride && c.ca32 == ca32 && c.cb32 == cb32 && c.nba == nba && c.nbb == nbb &&
+                   (!th_req || c.th == (int)th_req) && (!wm_req || c.wm == (int)wm_req);
+        };
         int persist = loop_req == 2 ? 1 : 0;
         if (loop_req == 0)
-            for (int i = 0; i < kNumPair; i++) {
-                const PairCfg& c = kPairCfgs[i];
-                if (c.persist && c.sa == (int)A.stride && c.ca32 == ca32 && c.cb32 == cb32 && c.nba == nba &&
-                    c.nbb == nbb && c.wm == wm && (!th_req || c.th == (int)th_req) && tiles_at(c.th) >= 8 * 256)
-                    persist = 1;
-            }
+            for (int i = 0; i < kNumPair; i++)
+                if (kPairCfgs[i].persist && serves(kPairCfgs[i]) && tiles_at(kPairCfgs[i].th) >= 8 * 256) persist = 1;
+        int wm = wm_req ? (int)wm_req : 2;
+        if (!wm_req)
+            for (int i = 0; i < kNumPair; i++)
+                if (kPairCfgs[i].persist == persist && serves(kPairCfgs[i]) && kPairCfgs[i].wm == 1) wm = 1;
         int idx = -1;
         for (int i = 0; i < kNumPair; i++) {
             const PairCfg& c = kPairCfgs[i];
-            if (c.sa != (int)A.stride || c.ca32 != ca32 || c.cb32 != cb32 || c.nba != nba || c.nbb != nbb ||
-                c.wm != wm || c.persist != persist)
-                continue;
+            if (!serves(c) || c.wm != wm || c.persist != persist) continue;
             if (th_req) {
-                if (c.th == (int)th_req) idx = i;
+                idx = i;
                 continue;
             }
             const int cur = idx < 0 ? 0 : kPairCfgs[idx].th;
@@ -939,17 +941,26 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         pa->tiles = (uint32_t)((uint64_t)A.n * tiles_y * tiles_x);
         pa->grid = dim3(pa->tiles, 1, 1);
         pa->threads = 64u * (uint32_t)std::max(c.nba, c.nbb) * (uint32_t)c.wm;
-        if (c.persist) {  // the resident grid: as many workgroups as fit at once
+        if (c.persist) {
+            // the resident grid: as many workgroups as fit at once. The kernel is compiled for 2 waves per SIMD
+            // (kPairResidentWaves per CU); the LDS per CU bounds it too. (The runtime's occupancy query counts
+            // only the LDS limit for these kernels and over-reports.)
             const void* k = nullptr;
             pair_launcher(idx, &k);
-            int per_cu = 0, cus = 0;
-            if (!k || hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, (int)pa->threads, 0) != hipSuccess ||
-                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, pa->device) != hipSuccess) {
+            hipFuncAttributes fa{};
+            int cus = 0, lds_cu = 0;
+            if (!k || hipFuncGetAttributes(&fa, k) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, pa->device) != hipSuccess ||
+                hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, pa->device) !=
+                    hipSuccess) {
                 (void)hipFree(pa->dmem);
                 (void)hipFree(pb->dmem);
-                return fail(-1, "fhc_conv_pair_plan_create: occupancy query failed");
+                return fail(-1, "fhc_conv_pair_plan_create: kernel attribute query failed");
             }
-            pa->grid.x = (unsigned)std::min<uint64_t>(pa->tiles, (uint64_t)std::max(1, per_cu) * std::max(1, cus));
+            const int waves = (int)pa->threads / 64;
+            int per_cu = std::max(1, kPairResidentWaves / waves);
+            if (fa.sharedSizeBytes > 0) per_cu = std::min(per_cu, std::max(1, lds_cu / (int)fa.sharedSizeBytes));
+            pa->grid.x = (unsigned)std::min<uint64_t>(pa->tiles, (uint64_t)per_cu * std::max(1, cus));
         }
         pa->lds = 0;
         pa->ws_bytes = 0;

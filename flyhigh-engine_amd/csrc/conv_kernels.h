@@ -102,7 +102,7 @@ constexpr int kPairTileW = 14;  // output columns per tile (B's 16-pixel MFMA bl
 struct PairCfg {
     int sa, ca32, cb32, nba, nbb, th, wm, persist;
 };
-constexpr int kNumPair = 30;
+constexpr int kNumPair = 27;
 inline constexpr PairCfg kPairCfgs[kNumPair] = {
     // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
     {2, 32, 64, 3, 3, 2, 1, 0}, {2, 32, 64, 3, 3, 4, 1, 0}, {2, 32, 64, 3, 3, 2, 2, 0}, {2, 32, 64, 3, 3, 4, 2, 0},
@@ -114,14 +114,15 @@ inline constexpr PairCfg kPairCfgs[kNumPair] = {
     {1, 32, 32, 2, 1, 2, 1, 0}, {1, 32, 32, 2, 1, 4, 1, 0}, {1, 32, 32, 2, 1, 2, 2, 0}, {1, 32, 32, 2, 1, 4, 2, 0},
     // the encoder's second stride-2 conv and its successor (36 -> 72 -> 72)
     {2, 64, 96, 5, 5, 1, 1, 0}, {2, 64, 96, 5, 5, 2, 1, 0},
-    // resident-grid loops: 64 -> 64 -> 64 (the 1080p/4 ladder), then the frame's pairs at batch scale (the
-    // 36 -> 72 -> 72 pair and taller 64-channel tiles spill)
-    {1, 64, 64, 4, 4, 4, 1, 1}, {1, 64, 64, 4, 4, 4, 2, 1},
-    {1, 64, 64, 3, 3, 4, 1, 1}, {1, 64, 64, 3, 3, 4, 2, 1},
-    {2, 32, 64, 3, 3, 4, 1, 1}, {2, 32, 64, 3, 3, 4, 2, 1},
+    // resident-grid loops (2 waves per SIMD): 64 -> 64 -> 64 (the 1080p/4 ladder), then the frame's pairs at batch
+    // scale (with 64-channel weights only two wave rows fit the 256 registers; the 36 -> 72 -> 72 pair spills)
+    {1, 64, 64, 4, 4, 4, 2, 1},
+    {1, 64, 64, 3, 3, 4, 2, 1},
+    {2, 32, 64, 3, 3, 4, 2, 1},
     {1, 32, 32, 2, 2, 4, 1, 1}, {1, 32, 32, 2, 2, 4, 2, 1}, {1, 32, 32, 2, 2, 8, 2, 1},
     {1, 32, 32, 2, 1, 4, 1, 1}, {1, 32, 32, 2, 1, 4, 2, 1}, {1, 32, 32, 2, 1, 8, 2, 1},
 };
+constexpr int kPairResidentWaves = 8;  // waves per CU of the resident-grid pair (2 per SIMD)
 using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);
 // The launcher of pair configuration `index`, or nullptr; *kernel receives the (persistent) kernel's address.
 PairLaunchFn pair_launcher(int index, const void** kernel = nullptr);

@@ -189,8 +189,11 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
 // and epilogue into the LDS tile; a barrier; the next tile's halo (in registers since the previous tile) into LDS
 // and the loads of the tile after it, which then fly during B's chain and the next tile's A chain; B's chain and
 // epilogue with its stores; the next tile's residual loads; a barrier. The intermediate never leaves the CU.
+// Compiled for exactly 2 waves per SIMD (at most 256 registers per lane, AGPRs included), so that the resident
+// grid the planner sizes (kPairResidentWaves waves per CU, or the LDS limit) is the one that fits.
 template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
-__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair_p(PairKArgs pk) {
+__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM)
+__attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_p(PairKArgs pk) {
     constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN * WM, TWB = kPairTileW;
     constexpr int FA = TH + 2, FAW = FA / WM, THW = TH / WM;
     static_assert(FA % WM == 0 && TH % WM == 0, "rows split evenly over the wave rows");
