@@ -36,13 +36,15 @@ std::mutex g_tune_mu;
 std::map<TuneKey, uint32_t> g_tune;
 
 // ---- variant codes -------------------------------------------------------------------------------------------
-// The code space of the choice table (a u8 like the reference table's value, tune_cache.rs:82):
+// The code space of the choice table (the reference table's value is a u8, tune_cache.rs:82; MI355X codes run to
+// kCodeEnd - 1, and a committed table names its variants instead):
 //   1..127   a K-chunked kernel: configuration (bits 0-4) | global split-K code (bits 5-6: 0 -> 1, 1 -> 2,
 //            2 -> 4, 3 -> 8 splits); configuration 1..kNumCfg is the chunked implicit-GEMM kernel's tile
 //            configuration, 16 + i the deep-layer kernel's configuration i of kGemmCfgs;
 //   128+i    the direct kernel's configuration i of direct_table.h (weights resident in VGPRs).
 constexpr uint32_t kSplitCodes[4] = {1, 2, 4, 8};
 constexpr uint32_t kDirectBase = 128;
+constexpr uint32_t kCodeEnd = kDirectBase + (uint32_t)kNumDirect;
 constexpr int kGemmBase = 16;
 static_assert(kNumCfg < kGemmBase && kGemmBase + kNumGemm <= 32, "configuration ids fit bits 0-4");
 
@@ -408,12 +410,16 @@ bool configure(fhc_conv_plan& p, const Variant& v, std::string* why) {
 // The direct configuration the planner takes without a table entry, or -1: among the one-block-per-wave
 // configurations that launch one workgroup per tile, the narrowest channel tile that covers cout in one tile (else
 // the widest there is), and among the tile heights the tallest that still gives about two workgroups per CU (the
-// small layers of a frame take short tiles: more, shorter-running workgroups).
+// small layers of a frame take short tiles: more, shorter-running workgroups). Up to 128 input channels the
+// kernel-row K split is left to the autotuner.
 int direct_default(const fhc_conv_desc& d, const Geometry& g) {
     const int need = (int)div_ceil(d.cout, 16);
+    auto eligible = [&](int i) {
+        return direct_fits(d, i) && kDirectCfgs[i].na == 1 && (kDirectCfgs[i].wk == 1 || kDirectCfgs[i].cin32 > 128);
+    };
     int best_wn = 0;
     for (int i = 0; i < kNumDirect; i++) {
-        if (!direct_fits(d, i) || kDirectCfgs[i].na != 1) continue;
+        if (!eligible(i)) continue;
         const int wn = kDirectCfgs[i].wn;
         if (best_wn == 0 || (best_wn < need && wn > best_wn) || (wn >= need && wn < best_wn)) best_wn = wn;
     }
@@ -422,8 +428,7 @@ int direct_default(const fhc_conv_desc& d, const Geometry& g) {
     uint64_t pick_wgs = 0;
     int pick_th = 0;
     for (int i = 0; i < kNumDirect; i++) {
-        if (!direct_fits(d, i) || kDirectCfgs[i].wn != best_wn || kDirectCfgs[i].persist || kDirectCfgs[i].na != 1)
-            continue;
+        if (!eligible(i) || kDirectCfgs[i].wn != best_wn || kDirectCfgs[i].persist) continue;
         const int th = kDirectCfgs[i].fm * kDirectCfgs[i].wm;
         const uint64_t wgs = (uint64_t)d.n * div_ceil(g.hout, th) * div_ceil(g.wout, 16) * div_ceil(d.cout, 16 * best_wn);
         const bool enough = wgs >= 512;
@@ -1013,11 +1018,11 @@ extern "C" int fhc_tune_parse(const char* text) {
             uint32_t code = 0;
             if (!v.empty() && v.size() <= 3 && v.find_first_not_of("0123456789") == std::string::npos) {
                 const unsigned long c = std::stoul(v);
-                if (c > 255) continue;
+                if (c >= kCodeEnd) continue;
                 code = (uint32_t)c;
             } else {
                 // an MI355X variant name ("direct.c64.t1x2.n48"): stable across builds, unlike the code it maps to
-                for (uint32_t c = 1; c < 256 && !code; c++)
+                for (uint32_t c = 1; c < kCodeEnd && !code; c++)
                     if (code_name(c) == v) code = c;
                 if (!code) continue;
             }

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 BAD = [
     dict(stride=3), dict(cin=0), dict(cout=0), dict(n=0), dict(k=5), dict(pad=0), dict(k=1, pad=1),
     dict(k=1, stride=2), dict(x_cstride=16, x_c0=8), dict(y_cstride=30), dict(residual=True, r_cstride=10),
-    dict(act=7), dict(ksplit=3), dict(cin=5000), dict(variant=31), dict(variant=255),
+    dict(act=7), dict(ksplit=3), dict(cin=5000), dict(variant=31), dict(variant=4000),
 ]
 
 

@@ -107,7 +107,7 @@ def test_planner_choice_matches_the_oracle(shape):
 
 
 VARIANT_SHAPES = [(1, 20, 37, 40, 72, 3, 1), (1, 19, 35, 24, 40, 3, 2), (1, 18, 33, 48, 40, 1, 1), (1, 9, 21, 279, 40, 3, 1),
-                  (1, 12, 20, 130, 100, 3, 1)]
+                  (1, 12, 20, 130, 100, 3, 1), (1, 17, 35, 90, 44, 3, 1)]
 
 
 @pytest.mark.parametrize("shape", VARIANT_SHAPES, ids=lambda s: "x".join(map(str, s)))
