@@ -85,8 +85,8 @@ class Net:
 
     def fuse(self, pairs, torch, fhconv, stream, time_fn, default_tile=False):
         """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; every
-        instantiated tile height (1, 2, 4 or 8 rows), wave rows (1 or 2) and loop (one workgroup per tile, or a
-        resident grid) timed on the real buffers, the fastest kept (default_tile: the pair planner's own choice, no
+        instantiated tile height (1, 2, 4 or 8 rows), wave rows (1 or 2) and loop (one workgroup per tile, a
+        resident grid, or a resident grid with the two stages on separate waves) timed on the real buffers, the fastest kept (default_tile: the pair planner's own choice, no
         timing), and only where it beats the two separate launches. A pair that shares a conv with one fused
         before it is skipped."""
         used = set()
@@ -101,7 +101,8 @@ class Net:
             rx = None if res_mid else r
             best = None
             combos = [(0, 0, 0)] if default_tile else \
-                [(th, wm, lp) for lp in (1, 2) for th, wm in ((1, 1), (2, 1), (4, 1), (2, 2), (4, 2), (8, 2))]
+                [(th, wm, lp) for lp in (1, 2) for th, wm in ((1, 1), (2, 1), (4, 1), (2, 2), (4, 2), (8, 2))] + \
+                [(th, 1, 3) for th in (4, 8)]
             for th, wm, lp in combos:
                 try:
                     pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid, tile_rows=th,

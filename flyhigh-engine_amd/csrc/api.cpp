@@ -644,7 +644,7 @@ std::string describe_json(const fhc_conv_plan* p) {
                  "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d.w%d%s\",\"family\":\"pair\",\"cfg\":%d,"
                  "\"tile_rows\":%d,\"tile_cols\":%d,\"wave_rows\":%d,\"persistent\":%d,\"res_mid\":%d,\"tiles\":%u,"
                  "\"grid\":[%u,%u,%u],\"threads\":%u,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
-                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, c.wm, c.persist ? "/p" : "", p->cfg,
+                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, c.wm, c.persist == 2 ? "/ws" : c.persist ? "/p" : "", p->cfg,
                  c.th, kPairTileW, c.wm, c.persist, p->res_mid, p->tiles, p->grid.x, p->grid.y, p->grid.z, p->threads,
                  p->g.hout, p->g.wout, fa + fb, bytes);
         return buf;
@@ -875,8 +875,7 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         if (!valid_desc(B, &why)) return fail(-1, "fhc_conv_pair_plan_create: second conv: %s", why.c_str());
         const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0;
         const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu, loop_req = (flags >> 20) & 3u;
-        if ((flags & ~(FHC_PAIR_RES_MID | 0x3fff00u)) != 0 || loop_req == 3)
-            return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
+        if ((flags & ~(FHC_PAIR_RES_MID | 0x3fff00u)) != 0) return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
         const uint32_t ha = (A.h + 2 * A.pad - A.kh) / A.stride + 1, wa = (A.w + 2 * A.pad - A.kw) / A.stride + 1;
         if (A.kh != 3 || B.kh != 3 || B.stride != 1 || A.residual)
             return fail(-1, "fhc_conv_pair_plan_create: the pair is a 3x3 conv (stride 1 or 2, no residual) then a 3x3 "
@@ -900,10 +899,11 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
             return c.sa == (int)A.stride && c.ca32 == ca32 && c.cb32 == cb32 && c.nba == nba && c.nbb == nbb &&
                    (!th_req || c.th == (int)th_req) && (!wm_req || c.wm == (int)wm_req);
         };
-        int persist = loop_req == 2 ? 1 : 0;
-        if (loop_req == 0)
+        int persist = loop_req >= 2 ? (int)loop_req - 1 : 0;
+        if (loop_req == 0)  // the resident grid where instantiated and big enough, stages on separate waves first
             for (int i = 0; i < kNumPair; i++)
-                if (kPairCfgs[i].persist && serves(kPairCfgs[i]) && tiles_at(kPairCfgs[i].th) >= 8 * 256) persist = 1;
+                if (kPairCfgs[i].persist && serves(kPairCfgs[i]) && tiles_at(kPairCfgs[i].th) >= 8 * 256)
+                    persist = std::max(persist, kPairCfgs[i].persist);
         int wm = wm_req ? (int)wm_req : 2;
         if (!wm_req)
             for (int i = 0; i < kNumPair; i++)
@@ -945,7 +945,8 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         pa->code = 0;
         pa->tiles = (uint32_t)((uint64_t)A.n * tiles_y * tiles_x);
         pa->grid = dim3(pa->tiles, 1, 1);
-        pa->threads = 64u * (uint32_t)std::max(c.nba, c.nbb) * (uint32_t)c.wm;
+        pa->threads = c.persist == 2 ? 64u * (uint32_t)(c.nba + c.nbb)
+                                     : 64u * (uint32_t)std::max(c.nba, c.nbb) * (uint32_t)c.wm;
         if (c.persist) {
             // the resident grid: as many workgroups as fit at once. The kernel is compiled for 2 waves per SIMD
             // (kPairResidentWaves per CU); the LDS per CU bounds it too. (The runtime's occupancy query counts

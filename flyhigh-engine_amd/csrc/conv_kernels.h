@@ -98,11 +98,12 @@ struct PairKArgs {
 constexpr int kPairTileW = 14;  // output columns per tile (B's 16-pixel MFMA block reads 16 + 2 columns of A)
 // The instantiated pairs: A's stride, A's and B's input channels padded to 32, A's and B's output channel blocks
 // of 16, the output rows per tile, the wave rows that split them, and the loop: 0 one workgroup per tile (weights
-// loaded per tile: small frames), 1 a resident grid looping over tiles (weights loaded once: large tensors).
+// loaded per tile: small frames), 1 a resident grid looping over tiles (weights loaded once: large tensors), 2 a
+// resident grid whose A and B stages run on separate waves, pipelined across tiles (one wave row).
 struct PairCfg {
     int sa, ca32, cb32, nba, nbb, th, wm, persist;
 };
-constexpr int kNumPair = 27;
+constexpr int kNumPair = 34;
 inline constexpr PairCfg kPairCfgs[kNumPair] = {
     // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
     {2, 32, 64, 3, 3, 2, 1, 0}, {2, 32, 64, 3, 3, 4, 1, 0}, {2, 32, 64, 3, 3, 2, 2, 0}, {2, 32, 64, 3, 3, 4, 2, 0},
@@ -121,6 +122,12 @@ inline constexpr PairCfg kPairCfgs[kNumPair] = {
     {2, 32, 64, 3, 3, 4, 2, 1},
     {1, 32, 32, 2, 2, 4, 1, 1}, {1, 32, 32, 2, 2, 4, 2, 1}, {1, 32, 32, 2, 2, 8, 2, 1},
     {1, 32, 32, 2, 1, 4, 1, 1}, {1, 32, 32, 2, 1, 4, 2, 1}, {1, 32, 32, 2, 1, 8, 2, 1},
+    // resident grids with the A and B stages on separate waves (at most 8 waves: 2 per SIMD)
+    {1, 64, 64, 4, 4, 4, 1, 2},
+    {1, 64, 64, 3, 3, 4, 1, 2},
+    {2, 32, 64, 3, 3, 4, 1, 2},
+    {1, 32, 32, 2, 2, 4, 1, 2}, {1, 32, 32, 2, 2, 8, 1, 2},
+    {1, 32, 32, 2, 1, 4, 1, 2}, {1, 32, 32, 2, 1, 8, 1, 2},
 };
 constexpr int kPairResidentWaves = 8;  // waves per CU of the resident-grid pair (2 per SIMD)
 using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);

@@ -377,6 +377,196 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_p(PairKArgs pk) {
     }
 }
 
+// The warp-specialized resident pair: NBA waves run only A (one channel block each, all FA rows) and NBB waves
+// run only B, so each wave holds one layer's weights, and the two stages pipeline across tiles: in step s the A
+// waves compute tile s from halo buffer s % 2 into LDS tile s % 2 while the B waves compute tile s - 1 from LDS
+// tile (s - 1) % 2, one barrier per step. Each SIMD then interleaves an A chain and a B chain instead of the whole
+// workgroup alternating between them. The A waves also stage the halos (tile s + 1 into LDS from registers, tile
+// s + 2 into registers); the B waves load the residual a step ahead and store. Every load and store is
+// unconditional through buffer instructions (tiles past the last read zeros and store nothing).
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH>
+__global__ __launch_bounds__(64 * (NBA + NBB))
+__attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_ws(PairKArgs pk) {
+    constexpr int NW = NBA + NBB, NTA = 64 * NBA, TWB = kPairTileW;
+    constexpr int FA = TH + 2;
+    constexpr int IHA = (FA - 1) * SA + 3, IWA = 15 * SA + 3;
+    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32;
+    constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;
+    constexpr int HALO = IHA * IWA * GPA, NLD = (HALO + NTA - 1) / NTA;  // the A waves stage the halo
+    constexpr int HB = IHA * IWA * PSA, MBUF = FA * MW * PSB;
+    static_assert(NBA * 16 <= CB32, "A's channel blocks exceed B's input channels");
+    __shared__ __align__(16) uint16_t hin[2 * HB];
+    __shared__ __align__(16) uint16_t mid[2 * MBUF];
+    const ConvKArgs& a = pk.a;
+    const ConvKArgs& b = pk.b;
+
+    const int tid = threadIdx.x, lane = tid & 63, lx = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool is_a = wave < NBA;  // uniform: this wave's stage
+    const int wa = is_a ? wave : 0, wb = is_a ? 0 : wave - NBA;
+    const int coa = wa * 16 + 4 * (lane >> 4), cob = wb * 16 + 4 * (lane >> 4);
+    const int tiles = b.n * b.tiles_y * b.tiles_x, G = gridDim.x, first = blockIdx.x;
+    if (first >= tiles) return;  // uniform over the workgroup
+    const int K = (tiles - first + G - 1) / G;  // this workgroup's tiles: first, first + G, ...
+    const bool ext_res = b.residual && !pk.res_mid;
+    const uint64_t pix_out = (uint64_t)b.n * b.hout * b.wout;
+    const auto rx = buffer_rsrc(a.x, (uint32_t)((uint64_t)a.n * a.h * a.w * a.xcs * 2));
+    const auto ry = buffer_rsrc(b.y, (uint32_t)view_bytes(pix_out, b.ycs, b.yc0, b.cout));
+    const auto rr = buffer_rsrc(b.res, ext_res ? (uint32_t)view_bytes(pix_out, b.rcs, b.rc0, b.cout) : 0u);
+
+    auto tile_origin = [&](int tt, int& img, int& oy0, int& ox0) {
+        const int tx = tt % b.tiles_x, r0 = tt / b.tiles_x;
+        oy0 = (r0 % b.tiles_y) * TH;
+        img = r0 / b.tiles_y;
+        ox0 = tx * TWB;
+    };
+    // the A waves' lane parts of the halo addresses (thread tid < NTA stages halo elements tid + i * NTA)
+    uint32_t hoff[NLD];
+    int hpos[NLD];
+    bool hst[NLD];
+#pragma unroll
+    for (int i = 0; i < NLD; i++) {
+        const int e = tid + i * NTA;
+        const int pix = e / GPA, g = e - pix * GPA;
+        const int iy = pix / IWA, ix = pix - iy * IWA;
+        hoff[i] = ((uint32_t)(iy * a.w + ix) * (uint32_t)a.xcs + (uint32_t)(a.xc0 + g * 8)) * 2u;
+        hpos[i] = (iy << 16) | ix;
+        hst[i] = ((i + 1) * NTA <= HALO || e < HALO) & (g * 8 < a.cin);
+    }
+    uint4 pre[NLD];
+    auto load_halo = [&](int k) {  // tile number k of this workgroup into registers (past the last: zeros)
+        const int tt = first + k * G;
+        int img, oy0, ox0;
+        tile_origin(tt, img, oy0, ox0);
+        const int iy0 = (oy0 - 1) * SA - a.pad, ix0 = (ox0 - 1) * SA - a.pad;
+        const uint32_t base = (((uint32_t)(img * a.h + iy0) * (uint32_t)a.w + (uint32_t)ix0) * (uint32_t)a.xcs) * 2u;
+        const bool tv = k < K;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int gy = iy0 + (hpos[i] >> 16), gx = ix0 + (hpos[i] & 0xffff);
+            const bool ok = hst[i] & tv & ((uint32_t)gy < (uint32_t)a.h) & ((uint32_t)gx < (uint32_t)a.w);
+            pre[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? base + hoff[i] : kOOB, 0, 0));
+        }
+    };
+    auto write_halo = [&](int buf) {
+        const bool part = (a.cin & 7) != 0;  // uniform
+        uint16_t* h = hin + buf * HB;
+#pragma unroll
+        for (int i = 0; i < NLD; i++) {
+            const int e = tid + i * NTA;
+            if ((i + 1) * NTA <= HALO || e < HALO) {
+                const int pix = e / GPA, g = e - pix * GPA;
+                *reinterpret_cast<uint4*>(h + pix * PSA + g * 8) = part ? mask_group(pre[i], a.cin - g * 8) : pre[i];
+            }
+        }
+    };
+    // the B waves' output and residual addresses; validity of row f of tile (oy0, ox0) for this lane
+    const uint32_t yl = ((uint32_t)lx * (uint32_t)b.ycs + (uint32_t)(b.yc0 + cob)) * 2u;
+    const uint32_t rl = ((uint32_t)lx * (uint32_t)b.rcs + (uint32_t)(b.rc0 + cob)) * 2u;
+    const uint32_t yrow = (uint32_t)b.wout * (uint32_t)b.ycs * 2u, rrow = (uint32_t)b.wout * (uint32_t)b.rcs * 2u;
+    auto out_ok = [&](int oy0, int ox0, int f) {
+        return (lx < TWB) & (oy0 + f < b.hout) & (ox0 + lx < b.wout) & (cob < b.cout);
+    };
+    uint2 rres[TH];
+    auto load_res = [&](int k) {
+        const int tt = first + k * G;
+        int img, oy0, ox0;
+        tile_origin(tt, img, oy0, ox0);
+        const uint32_t base = ((uint32_t)(img * b.hout + oy0) * (uint32_t)b.wout + (uint32_t)ox0) * (uint32_t)b.rcs * 2u;
+        const bool tv = (k < K) & ext_res;
+#pragma unroll
+        for (int f = 0; f < TH; f++)
+            rres[f] = __builtin_bit_cast(
+                uint2, __builtin_amdgcn_raw_buffer_load_b64(rr, (out_ok(oy0, ox0, f) & tv) ? base + f * rrow + rl : kOOB,
+                                                            0, 0));
+    };
+
+    // once: this wave's layer's weights, bias and multipliers; the first two halos (A) or the first residual (B);
+    // the zero channels of both LDS tiles
+    constexpr int NWR = 9 * (MA > MB ? MA : MB);
+    h8 wr[NWR];
+    float bias[4], neg[4];
+    {
+        const ConvKArgs& l = is_a ? a : b;
+        const int blk = is_a ? wa : wb, nk = is_a ? 9 * MA : 9 * MB, co = is_a ? coa : cob;
+        const h8* wp = reinterpret_cast<const h8*>(l.wpk) + (size_t)blk * nk * 64 + lane;
+#pragma unroll
+        for (int s = 0; s < NWR; s++) wr[s] = wp[(s < nk ? s : 0) * 64];
+#pragma unroll
+        for (int i = 0; i < 4; i++) bias[i] = h2f(l.bias[co + i]);
+        const float4 m = *reinterpret_cast<const float4*>(l.neg + co);
+        neg[0] = m.x, neg[1] = m.y, neg[2] = m.z, neg[3] = m.w;
+    }
+    if (is_a) {
+        load_halo(0);
+        write_halo(0);
+        load_halo(1);
+    }
+    if constexpr (NBA * 16 < CB32) {
+        constexpr int G0 = NBA * 2, GN = CB32 / 8 - G0, NZ = 2 * FA * MW * GN;
+        for (int e = tid; e < NZ; e += 64 * NW) {
+            const int pix = e / GN, g = G0 + e % GN;  // pixels of both buffers (MBUF = FA * MW * PSB apart)
+            *reinterpret_cast<uint4*>(mid + pix * PSB + g * 8) = uint4{0u, 0u, 0u, 0u};
+        }
+    }
+    __syncthreads();
+
+    typedef _Float16 hh2 __attribute__((ext_vector_type(2)));
+    for (int s = 0; s <= K; s++) {
+        if (is_a) {
+            if (s < K) {  // A over FA rows x 16 columns of tile s; its f16 output (zero outside the image)
+                int img, oy0, ox0;
+                tile_origin(first + s * G, img, oy0, ox0);
+                f4 acc[FA];
+                pair_chain<FA, SA, MA, IWA, PSA>(acc, wr, hin + (s & 1) * HB + (lx * SA) * PSA + (lane >> 4) * 8);
+                uint16_t* m = mid + (s & 1) * MBUF;
+#pragma unroll
+                for (int f = 0; f < FA; f++) {
+                    const int oy = oy0 - 1 + f, ox = ox0 - 1 + lx;
+                    const bool in = (oy >= 0) & (oy < a.hout) & (ox >= 0) & (ox < a.wout);
+                    uint16_t o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = in ? f2h(activate(acc[f][i] + bias[i], neg[i])) : (uint16_t)0;
+                    *reinterpret_cast<uint2*>(m + (f * MW + lx) * PSB + coa) =
+                        uint2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+                }
+                write_halo((s + 1) & 1);  // tile s + 1 (zeros past the last)
+            }
+            load_halo(s + 2);
+        } else {
+            if (s >= 1) {  // B over TH rows x 16 columns of tile s - 1 (the first 14 stored)
+                int img, oy0, ox0;
+                tile_origin(first + (s - 1) * G, img, oy0, ox0);
+                const uint16_t* m = mid + ((s - 1) & 1) * MBUF;
+                f4 acc[TH];
+                pair_chain<TH, 1, MB, MW, PSB>(acc, wr, m + lx * PSB + (lane >> 4) * 8);
+                const uint32_t ybase =
+                    ((uint32_t)(img * b.hout + oy0) * (uint32_t)b.wout + (uint32_t)ox0) * (uint32_t)b.ycs * 2u;
+#pragma unroll
+                for (int f = 0; f < TH; f++) {
+                    float v[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[i] = activate(acc[f][i] + bias[i], neg[i]);
+                    hh2 p0 = hh2{(_Float16)v[0], (_Float16)v[1]}, p1 = hh2{(_Float16)v[2], (_Float16)v[3]};
+                    if (b.residual) {  // uniform: A's output at the same pixel, or the external tensor
+                        const uint2 mv = opaque_u2(*reinterpret_cast<const uint2*>(m + ((f + 1) * MW + lx + 1) * PSB + cob));
+                        const uint2 rv = pk.res_mid ? mv : rres[f];
+                        p0 += __builtin_bit_cast(hh2, rv.x);
+                        p1 += __builtin_bit_cast(hh2, rv.y);
+                    }
+                    const uint32_t off = out_ok(oy0, ox0, f) ? ybase + f * yrow + yl : kOOB;
+                    __builtin_amdgcn_raw_buffer_store_b64(
+                        __builtin_bit_cast(__attribute__((ext_vector_type(2))) uint32_t,
+                                           uint2{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1)}),
+                        ry, off, 0, 0);
+                }
+            }
+            load_res(s);  // tile s's residual, for the next step
+        }
+        __syncthreads();  // LDS tile s and halo s + 1 are written; LDS tile s - 1 and halo s are read
+    }
+}
+
 // Whether the persistent pair's buffer loop serves these views (16-byte input groups, 8-byte output and
 // residual quads, every view below 2^31 bytes); else the one-tile kernel runs.
 inline bool pair_buffer_ok(const PairKArgs& pk) {
@@ -386,6 +576,22 @@ inline bool pair_buffer_ok(const PairKArgs& pk) {
     return a.xvec && b.yvec && b.cout % 4 == 0 && (!ext || b.rvec) &&
            (uint64_t)a.n * a.h * a.w * (uint64_t)a.xcs * 2 < lim && view_bytes(pout, b.ycs, b.yc0, b.cout) < lim &&
            (!ext || view_bytes(pout, b.rcs, b.rc0, b.cout) < lim);
+}
+
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH>
+hipError_t launch_pair_ws(const PairKArgs& pk, dim3 grid, hipStream_t s) {
+    if (pair_buffer_ok(pk)) {
+        hipLaunchKernelGGL((conv_pair_ws<SA, CA32, CB32, NBA, NBB, TH>), grid, dim3(64 * (NBA + NBB)), 0, s, pk);
+        return hipGetLastError();
+    }
+    // views the buffer loop cannot serve: one workgroup per tile
+    grid.x = (unsigned)(pk.b.n * pk.b.tiles_y * pk.b.tiles_x);
+    const dim3 block(64 * (NBA > NBB ? NBA : NBB));
+    if (pk.a.xvec)
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, 1, true>), grid, block, 0, s, pk);
+    else
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, 1, false>), grid, block, 0, s, pk);
+    return hipGetLastError();
 }
 
 template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>

@@ -10,7 +10,10 @@ namespace {
 template <int I>
 PairLaunchFn pair_entry(const void** kernel) {
     constexpr PairCfg c = kPairCfgs[I];
-    if constexpr (c.persist) {
+    if constexpr (c.persist == 2) {
+        if (kernel) *kernel = reinterpret_cast<const void*>(&conv_pair_ws<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th>);
+        return launch_pair_ws<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th>;
+    } else if constexpr (c.persist) {
         if (kernel) *kernel = reinterpret_cast<const void*>(&conv_pair_p<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm>);
         return launch_pair_p<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm>;
     } else {

@@ -220,7 +220,8 @@ class ConvPairPlan(ConvPlan):
     """Two convs fused into one launch (fhc_conv_pair_plan_create): A (3x3, stride 1 or 2) then B (3x3 stride 1) on
     A's output, which stays on chip. run(x, y, res) takes A's input, B's output and B's external residual; with
     res_mid B's residual is A's output. tile_rows / wave_rows / loop 0 let the library choose (1, 2 or 4 rows; 1
-    wave row; loop 1 one workgroup per tile, 2 a resident grid looping over tiles)."""
+    wave row; loop 1 one workgroup per tile, 2 a resident grid looping over tiles, 3 a resident grid with A and B
+    on separate waves)."""
 
     def __init__(self, desc_a: ConvDesc, w_a, bias_a, slope_a, desc_b: ConvDesc, w_b, bias_b, slope_b,
                  res_mid=False, tile_rows=0, wave_rows=0, loop=0):

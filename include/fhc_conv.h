@@ -90,26 +90,25 @@ int fhc_conv_describe(const fhc_conv_plan* plan, char* json, size_t cap);
 
 void fhc_conv_plan_destroy(fhc_conv_plan* plan);
 
-/* A fused pair: conv A (3x3, stride 1 or 2, no residual) and conv B (3x3 stride 1) that reads A's output, run as
- * one launch with A's output kept on chip. It serves two consecutive conv ops of the graph whose intermediate
- * tensor has no other reader (graph.json's enc.e1 -> enc.e2, enc.e3 -> enc.e4, film.h1 -> film.h2, refine.q1 -> q2,
- * q3 -> q4, fine.r2 -> r3). The result is the one the two plans give run in turn: A's output is rounded to f16 and B reads it
- * with zero padding. No counterpart in the reference, which records one dispatch per conv op
- * (net/build.rs:209-278).
- * desc_b: B's n, h, w and cin equal A's n, output height and width and cout; B's input view is ignored.
- * flags: FHC_PAIR_RES_MID makes B's residual A's output (B.residual set, B.cout == B.cin; graph.json's
- * "add" of e2 and e1, e4 and e3), else B's residual, if any, is the `res` tensor of fhc_conv_run; bits 8-15:
- * output rows per tile (1, 2, 4 or 8 as instantiated; 0: the tallest that still gives 256 workgroups, else the
- * shortest); bits 16-19: wave rows splitting them (1 or 2; 0: 1 where instantiated, else 2); bits 20-21: the
- * loop (1: one workgroup per tile, both layers' weights loaded per tile; 2: a resident grid that loads them once
- * and loops over the tiles, for 64 -> 64 -> 64 at 4 rows x 2 wave rows and for the frame's pairs at 4 or 8 rows,
- * 64-channel pairs with 2 wave rows; 0: the resident grid where it is instantiated and there are at least 2048
- * tiles). The plan runs with fhc_conv_run (x: A's input, y and res: B's output and residual), is described by
- * fhc_conv_describe (family "pair") and freed by fhc_conv_plan_destroy. The instantiated pairs cover, in channels A.cin -> A.cout -> B.cout: stride 1
- * 33..64 -> 49..64 -> 49..64 (resident grid only), stride 2
- * <= 32 -> 33..48 -> 33..48 (2 or 4 rows) and 33..64 -> 65..80 -> 65..80 (1 or 2 rows, one wave row), and stride 1
- * 33..64 -> 33..48 -> 33..48, <= 32 -> 17..32 -> 17..32 and <= 32 -> 17..32 -> <= 16 (2 or 4 rows); other shapes
- * are an error status. */
+/* A fused pair: conv A (3x3, stride 1 or 2, no residual) and conv B (3x3 stride 1) that reads A's output, run as one
+ * launch with A's output kept on chip. It serves two consecutive conv ops of the graph whose intermediate tensor has
+ * no other reader (graph.json's enc.e1 -> enc.e2, enc.e3 -> enc.e4, film.h1 -> film.h2, refine.q1 -> q2, q3 -> q4,
+ * fine.r2 -> r3). The result is the one the two plans give run in turn: A's output is rounded to f16 and B reads it
+ * with zero padding. No counterpart in the reference, which records one dispatch per conv op (net/build.rs:209-278).
+ * desc_b: B's n, h, w and cin equal A's n, output height and width and cout; B's input view is ignored. flags:
+ * FHC_PAIR_RES_MID makes B's residual A's output (B.residual set, B.cout == B.cin; graph.json's "add" of e2 and e1,
+ * e4 and e3), else B's residual, if any, is the `res` tensor of fhc_conv_run; bits 8-15: output rows per tile (1, 2,
+ * 4 or 8 as instantiated; 0: the tallest that still gives 256 workgroups, else the shortest); bits 16-19: wave rows
+ * splitting them (1 or 2; 0: 1 where instantiated, else 2); bits 20-21: the loop (1: one workgroup per tile, both
+ * layers' weights loaded per tile; 2: a resident grid that loads them once and loops over the tiles, for 64 -> 64 ->
+ * 64 at 4 rows x 2 wave rows and for the frame's pairs at 4 or 8 rows, 64-channel pairs with 2 wave rows; 3: a
+ * resident grid whose A and B stages run on separate waves, pipelined across tiles, at 4 rows, and 8 rows for
+ * 32-channel pairs; 0: the resident grid where it is instantiated and there are at least 2048 tiles, loop 3 first).
+ * The plan runs with fhc_conv_run (x: A's input, y and res: B's output and residual), is described by
+ * fhc_conv_describe (family "pair") and freed by fhc_conv_plan_destroy. The instantiated pairs cover, in channels
+ * A.cin -> A.cout -> B.cout: stride 1 33..64 -> 49..64 -> 49..64 (resident grid only), stride 2 <= 32 -> 33..48 ->
+ * 33..48 (2 or 4 rows) and 33..64 -> 65..80 -> 65..80 (1 or 2 rows, one wave row), and stride 1 33..64 -> 33..48 ->
+ * 33..48, <= 32 -> 17..32 -> 17..32 and <= 32 -> 17..32 -> <= 16 (2 or 4 rows); other shapes are an error status. */
 #define FHC_PAIR_RES_MID 1u
 int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
                               const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,

@@ -512,8 +512,10 @@ def run_pair(A, B, res, **kw):
 
 
 @pytest.mark.parametrize("case", PAIR_P_CASES, ids=lambda c: "x".join(map(str, c[:7])) + (f"-{c[9]}" if c[9] else ""))
-@pytest.mark.parametrize("th,wm", [(4, 1), (4, 2), (8, 2)], ids=["t4w1", "t4w2", "t8w2"])
-def test_resident_pair_matches_the_two_convs(case, th, wm):
+@pytest.mark.parametrize("th,wm,loop", [(4, 1, 2), (4, 2, 2), (8, 2, 2), (4, 1, 3), (8, 1, 3)],
+                         ids=["t4w1", "t4w2", "t8w2", "t4ws", "t8ws"])
+def test_resident_pair_matches_the_two_convs(case, th, wm, loop):
+    # loop 2: both stages on every wave; loop 3: A and B on separate waves, pipelined across tiles
     n, h, w, cin, cmid, cout, sa, act_a, act_b, res, xv, yv = case
     A = Case(n, h, w, cin, cmid, stride=sa, act=act_a, xv=xv, poison=xv is not None, seed=61)
     ya = A.run_oracle(threads=8)
@@ -523,13 +525,13 @@ def test_resident_pair_matches_the_two_convs(case, th, wm):
         B.res = ya
     want = B.run_oracle(threads=8)
     try:
-        got, plan = run_pair(A, B, res, tile_rows=th, wave_rows=wm, loop=2)
+        got, plan = run_pair(A, B, res, tile_rows=th, wave_rows=wm, loop=loop)
     except fhconv.FhcError as e:
         assert "no fused pair instantiated" in str(e)
-        pytest.skip(f"no resident pair at {th} rows x {wm} wave rows for these channels")
+        pytest.skip(f"no resident pair at {th} rows x {wm} wave rows, loop {loop}, for these channels")
     d = plan.describe()
     say("pair/p", case[:7], d["name"], d["grid"], d["tiles"])
-    assert d["persistent"] == 1 and d["tile_rows"] == th and d["grid"][0] < d["tiles"]
+    assert d["persistent"] == loop - 1 and d["tile_rows"] == th and d["grid"][0] < d["tiles"]
     sl = slice(B.yc0, B.yc0 + cout)
     ok, md, mref = parity(got, want, view=sl)
     assert ok, (d["name"], md, mref)
@@ -538,16 +540,17 @@ def test_resident_pair_matches_the_two_convs(case, th, wm):
     assert np.array_equal(got[..., mask], B.y0[..., mask])
 
 
-def test_resident_pair_full_size_ladder():
-    # the 1080p/4 ladder's two 64 -> 64 convs as one resident-grid pair (the library's default for this size),
-    # rows checked in bands: B's rows [r0, r0 + 4) from the oracle of A's rows [r0 - 1, r0 + 5)
+@pytest.mark.parametrize("loop", [2, 3], ids=["p", "ws"])
+def test_resident_pair_full_size_ladder(loop):
+    # the 1080p/4 ladder's two 64 -> 64 convs as one resident-grid pair, rows checked in bands: B's rows
+    # [r0, r0 + 4) from the oracle of A's rows [r0 - 1, r0 + 5)
     import copy
     A = Case(1, 272, 480, 64, 64, act=1, seed=63)
     B = Case(1, 272, 480, 64, 64, act=1, seed=64)
-    got, plan = run_pair(A, B, None)
+    got, plan = run_pair(A, B, None, loop=loop)
     d = plan.describe()
     say("pair/p", d["name"], d["grid"], d["tiles"])
-    assert d["persistent"] == 1
+    assert d["persistent"] == loop - 1
     for r0 in (0, 134, 268):
         a0, a1 = max(0, r0 - 1), min(272, r0 + 5)
         band = copy.copy(B)
