@@ -1,0 +1,172 @@
+"""Python host driver of the network ops between the convs (ctypes over include/fhc_ops.h in libfhconv.so).
+
+One function per Gpu method of the reference (crates/flyhigh-engine/src/ops/network.rs, interp.rs, render.rs):
+``warp``, ``luma``, ``sad`` (sad_volume), ``convex`` (convex_upsample after its conv), ``film``, ``blend``,
+``blendmix``, ``avgpool``, ``interp``. Inputs are torch NHWC f16 tensors on the GPU, or ``View`` objects that add the
+reference Tensor's channel offset and read scale (ops/tensor.rs); each function returns a new dense output unless an
+``out`` view is given (a concat slice is written in place). The module only passes device pointers: when the
+library is missing, loading it raises, and nothing is computed on the host.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import fhconv
+from fhconv import FhcError, _stream_handle
+
+
+class FhcTensor(ctypes.Structure):
+    _fields_ = [("p", ctypes.c_void_p), ("cstride", ctypes.c_uint32), ("c0", ctypes.c_uint32),
+                ("scale", ctypes.c_float)]
+
+
+class View:
+    """Channels c0.. of an NHWC device tensor t of shape (n, h, w, cstride), read times `scale`."""
+
+    def __init__(self, t, c0: int = 0, scale: float = 1.0):
+        if t.dim() != 4 or not t.is_contiguous() or t.element_size() != 2:
+            raise FhcError("a view needs a contiguous 4-d 16-bit NHWC tensor")
+        self.t, self.c0, self.scale = t, c0, scale
+
+    @property
+    def shape(self):
+        return tuple(self.t.shape)
+
+    @property
+    def channels(self):
+        return self.t.shape[3] - self.c0
+
+    def c_struct(self):
+        return FhcTensor(self.t.data_ptr(), self.t.shape[3], self.c0, self.scale)
+
+
+def _v(x) -> View:
+    return x if isinstance(x, View) else View(x)
+
+
+_typed = False
+
+
+def _lib():
+    global _typed
+    L = fhconv.load()
+    if not _typed:
+        T, U, I, P = ctypes.POINTER(FhcTensor), ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p
+        sig = {
+            "fhc_warp": [T, T, T, U, U, U, U, P],
+            "fhc_luma": [T, T, U, U, U, I, P],
+            "fhc_sad_volume": [T, T, T, U, U, U, U, P],
+            "fhc_convex_upsample": [T, T, T, U, U, U, U, P],
+            "fhc_film_modulate": [T, P, T, U, U, U, U, P],
+            "fhc_blend_weights": [T, T, U, U, U, P],
+            "fhc_blendmix": [T, T, T, T, U, U, U, P],
+            "fhc_avgpool": [T, T, U, U, U, U, U, P],
+            "fhc_interpolate": [T, T, U, U, U, U, U, U, I, P],
+        }
+        for name, args in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = ctypes.c_int
+        _typed = True
+    return L
+
+
+def _out(out, like: View, n, h, w, c) -> View:
+    if out is not None:
+        return _v(out)
+    import torch
+    return View(torch.empty((n, h, w, c), dtype=like.t.dtype, device=like.t.device))
+
+
+def _run(name, rc):
+    if rc < 0:
+        raise FhcError(f"{name}: {fhconv.last_error()}")
+
+
+def _ref(v: View):
+    return ctypes.byref(v.c_struct())
+
+
+def warp(img, flow, c: Optional[int] = None, out=None, stream=None):
+    """out[p] = img[p + flow[p]] (bilinear, border clamp); flow channels c0, c0 + 1 are x, y in pixels."""
+    img, flow = _v(img), _v(flow)
+    n, h, w, _ = img.shape
+    c = img.channels if c is None else c
+    o = _out(out, img, n, h, w, c)
+    _run("warp", _lib().fhc_warp(_ref(img), _ref(flow), _ref(o), n, h, w, c, _stream_handle(stream)))
+    return o.t
+
+
+def luma(x, grad: bool = False, out=None, stream=None):
+    x = _v(x)
+    n, h, w, _ = x.shape
+    o = _out(out, x, n, h, w, 1)
+    _run("luma", _lib().fhc_luma(_ref(x), _ref(o), n, h, w, int(grad), _stream_handle(stream)))
+    return o.t
+
+
+def sad(la, lb, radius: int, out=None, stream=None):
+    la, lb = _v(la), _v(lb)
+    n, h, w, _ = la.shape
+    o = _out(out, la, n, h, w, (2 * radius + 1) ** 2)
+    _run("sad_volume", _lib().fhc_sad_volume(_ref(la), _ref(lb), _ref(o), n, h, w, radius, _stream_handle(stream)))
+    return o.t
+
+
+def convex(wt, x, c: Optional[int] = None, out=None, stream=None):
+    wt, x = _v(wt), _v(x)
+    n, h, w, _ = x.shape
+    c = x.channels if c is None else c
+    o = _out(out, x, n, 2 * h, 2 * w, c)
+    _run("convex_upsample",
+         _lib().fhc_convex_upsample(_ref(wt), _ref(x), _ref(o), n, h, w, c, _stream_handle(stream)))
+    return o.t
+
+
+def film(hv, g, c: Optional[int] = None, out=None, stream=None):
+    """g: a contiguous device tensor of n * 2c f16 values (one FiLM vector per image)."""
+    hv = _v(hv)
+    n, h, w, _ = hv.shape
+    c = hv.channels if c is None else c
+    if not g.is_contiguous() or g.numel() != n * 2 * c or g.element_size() != 2:
+        raise FhcError(f"film: g needs {n * 2 * c} contiguous f16 values")
+    o = _out(out, hv, n, h, w, c)
+    _run("film_modulate",
+         _lib().fhc_film_modulate(_ref(hv), g.data_ptr(), _ref(o), n, h, w, c, _stream_handle(stream)))
+    return o.t
+
+
+def blend(vis, out=None, stream=None):
+    vis = _v(vis)
+    n, h, w, _ = vis.shape
+    o = _out(out, vis, n, h, w, 2)
+    _run("blend_weights", _lib().fhc_blend_weights(_ref(vis), _ref(o), n, h, w, _stream_handle(stream)))
+    return o.t
+
+
+def blendmix(wa, wb, vis, out=None, stream=None):
+    wa, wb, vis = _v(wa), _v(wb), _v(vis)
+    n, h, w, _ = vis.shape
+    o = _out(out, vis, n, h, w, 3)
+    _run("blendmix", _lib().fhc_blendmix(_ref(wa), _ref(wb), _ref(vis), _ref(o), n, h, w, _stream_handle(stream)))
+    return o.t
+
+
+def avgpool(x, k: int, c: Optional[int] = None, out=None, stream=None):
+    x = _v(x)
+    n, h, w, _ = x.shape
+    c = x.channels if c is None else c
+    o = _out(out, x, n, h // max(k, 1), w // max(k, 1), c)
+    _run("avgpool", _lib().fhc_avgpool(_ref(x), _ref(o), n, h, w, c, k, _stream_handle(stream)))
+    return o.t
+
+
+def interp(x, oh: int, ow: int, antialias: bool = False, c: Optional[int] = None, out=None, stream=None):
+    x = _v(x)
+    n, ih, iw, _ = x.shape
+    c = x.channels if c is None else c
+    o = _out(out, x, n, oh, ow, c)
+    _run("interpolate",
+         _lib().fhc_interpolate(_ref(x), _ref(o), n, c, ih, iw, oh, ow, int(antialias), _stream_handle(stream)))
+    return o.t

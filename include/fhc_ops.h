@@ -1,0 +1,92 @@
+/* fhc_ops: the FlyHighFG network ops between the convs, on MI355X (gfx950), as a C ABI.
+ *
+ * The reference runs each of these as one WGSL dispatch recorded by the planner (crates/flyhigh-engine/src/net/
+ * build.rs) through a Gpu method (ops/network.rs, ops/interp.rs, ops/render.rs); there is no FFI at op level, so
+ * each entry point below replaces that Gpu method plus the dispatch it records, and a maintainer would call it from
+ * the planner arm named in its comment (a Step::Foreign replayed in order with the conv steps of fhc_conv.h).
+ *
+ * Conventions are those of fhc_conv.h: 0 on success, a negative value on error with the message in
+ * fhc_last_error() (thread-local); nothing aborts or throws; the library allocates nothing and never synchronises,
+ * so calls can be captured in a HIP graph. An empty tensor (a zero size) is a no-op.
+ *
+ * Tensors are NHWC f16 views (fhc_tensor): element (img, y, x, ch) at p[((img * H + y) * W + x) * cstride + c0 +
+ * ch]. The reference's Tensor is planar [C][H][W] with batch 1 and carries a channel offset and a read scale
+ * (ops/tensor.rs); both are kept: `c0` is the channel offset, `scale` multiplies every value read where the
+ * reference's kernel applies its view's scale (noted per op; the other inputs must have scale 1). Outputs are
+ * written through a view, so an op can write straight into its slice of a concat (the graph's concat ops become
+ * free); an output's scale is not used. Arithmetic is f32 from f16 inputs, rounded once to f16 (RTNE) on store, in
+ * the reference kernel's order of operations.
+ */
+#ifndef FHC_OPS_H
+#define FHC_OPS_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct fhc_tensor {
+    void* p;          /* device memory, f16 bit patterns                                                */
+    uint32_t cstride; /* halves from one pixel to the next (>= c0 + the channels the op reads/writes)   */
+    uint32_t c0;      /* first channel of the view                                                       */
+    float scale;      /* read scale (Tensor::scale, ops/tensor.rs); 1 where the op takes none              */
+} fhc_tensor;
+
+/* Backward warp out[p] = img[p + flow[p]] in pixels, bilinear, coordinates clamped to the border; the flow view's
+ * channels c0 and c0 + 1 are x and y. Both scales apply. Replaces Gpu::warp (ops/network.rs:6-19,
+ * shaders/warp.wgsl:12-29), the planner's "warp" arm (net/build.rs:283). */
+int fhc_warp(const fhc_tensor* img, const fhc_tensor* flow, const fhc_tensor* out, uint32_t n, uint32_t h,
+             uint32_t w, uint32_t c, void* stream);
+
+/* Luma of a BGR view (channel 0 B, 1 G, 2 R) into one channel; grad != 0: |luma(x+1) - luma| + |luma(y+1) -
+ * luma| (0 past the last column / row). The scale applies. Replaces Gpu::luma (ops/network.rs:22-33,
+ * shaders/luma.wgsl:9-28), the "luma" and "luma_grad" arms (net/build.rs:321-325). */
+int fhc_luma(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, int grad,
+             void* stream);
+
+/* Luma SAD cost volume: for each displacement (dy, dx) in [-radius, radius]^2, channel (dy + r) * (2r + 1) + dx
+ * + r, the 3x3 zero-padded mean of |la(y, x) - lb(y + dy, x + dx)| with lb's coordinates clamped. One-channel
+ * inputs; radius <= 7. Replaces Gpu::sad (ops/network.rs:34-47, shaders/sad.wgsl:10-29), the "sad_volume" arm
+ * (net/build.rs:326-329). */
+int fhc_sad_volume(const fhc_tensor* la, const fhc_tensor* lb, const fhc_tensor* out, uint32_t n, uint32_t h,
+                   uint32_t w, uint32_t radius, void* stream);
+
+/* Convex x2 upsample: out (2h x 2w x c) = the softmax over 9 of wt's channels k * 4 + sy * 2 + sx (36 channels,
+ * at the input pixel) weighting x's zero-padded 3x3 neighbourhood. wt is the up.w conv's output. Replaces
+ * Gpu::convex (ops/network.rs:48-55, shaders/convex.wgsl:10-35), the "convex_upsample" arm after its conv
+ * (net/build.rs:379-416). */
+int fhc_convex_upsample(const fhc_tensor* wt, const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h,
+                        uint32_t w, uint32_t c, void* stream);
+
+/* FiLM modulate out = hv * (1 + g[c]) + g[C + c], g dense f16 [n][2C] in device memory (one vector per image: the
+ * reference's batch 1 has one). Replaces Gpu::film (ops/network.rs:56-62, shaders/film.wgsl:9-15), the
+ * "film_modulate" arm (net/build.rs:360-363). */
+int fhc_film_modulate(const fhc_tensor* hv, const void* g, const fhc_tensor* out, uint32_t n, uint32_t h,
+                      uint32_t w, uint32_t c, void* stream);
+
+/* Visibility blend weights: the softmax (p0, p1, p2) of 3 logits -> 2 channels (p0 + p2 / 2, p1 + p2 / 2). The
+ * scale applies. Replaces Gpu::blend (ops/network.rs:63-68, shaders/blend.wgsl:9-21), "blend_weights" unfused. */
+int fhc_blend_weights(const fhc_tensor* vis, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w,
+                      void* stream);
+
+/* The fused blend of two 3-channel images by those weights, each product and the weights rounded to f16 as the
+ * unfused path rounds them. vis's scale applies. Replaces Gpu::blendmix (ops/render.rs:102-115,
+ * shaders/blendmix.wgsl:12-28), the blend_weights + mul + mul + add peephole (net/build.rs:417-450). */
+int fhc_blendmix(const fhc_tensor* wa, const fhc_tensor* wb, const fhc_tensor* vis, const fhc_tensor* out,
+                 uint32_t n, uint32_t h, uint32_t w, void* stream);
+
+/* k x k average pool, stride k: out (h / k) x (w / k) x c (the remainder rows and columns are dropped). Replaces
+ * Gpu::avgpool (ops/interp.rs:12-18, shaders/avgpool.wgsl:8-19), the "avgpool" arm (net/build.rs:279-282). */
+int fhc_avgpool(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                uint32_t k, void* stream);
+
+/* Resize ih x iw -> oh x ow: bilinear with align_corners false (antialias 0) or the separable triangle filter of
+ * support max(scale, 1) (antialias 1, torch's antialiased bilinear). The scale applies to the result. Replaces
+ * Gpu::interp (ops/interp.rs:6-11, shaders/interp.wgsl:11-45), the "interpolate" arm (net/build.rs:199-208). */
+int fhc_interpolate(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t c, uint32_t ih, uint32_t iw,
+                    uint32_t oh, uint32_t ow, int antialias, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,58 @@
+/* CPU oracle of the FlyHighFG network ops around the convs: TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/ and bench.py's CPU-baseline leg call these functions, as the checker; the product (libfhconv.so)
+ * never links or loads them. Each function restates one WGSL kernel of the reference, element by element, in f32
+ * with the kernel's own order of operations, on NHWC f16 views: element (img, y, x, ch) of a view at
+ * p[((img * H + y) * W + x) * cs + c0 + ch]. The reference's tensors are planar [C][H][W] with batch 1; a view's
+ * channel offset there (Tensor::c0) is c0 here, and `scale` is its read scale (Tensor::scale,
+ * crates/flyhigh-engine/src/ops/tensor.rs). Outputs are written through a view (cs, c0) so that a result can land
+ * in a concat slice; their scale is not used.
+ */
+#ifndef FH_OPS_ORACLE_H
+#define FH_OPS_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct fho_view {
+    void* p;        /* f16 bit patterns */
+    uint32_t cs;    /* halves between consecutive pixels */
+    uint32_t c0;    /* first channel of the view */
+    float scale;    /* read scale (ops that take it) */
+} fho_view;
+
+/* backward warp, bilinear with border clamp: shaders/warp.wgsl:12-29 (flow channels c0, c0 + 1 = x, y pixels) */
+void fho_warp(const fho_view* img, const fho_view* flow, const fho_view* out, uint32_t n, uint32_t h, uint32_t w,
+              uint32_t c);
+/* BGR -> luma (grad 0) or |d/dx| + |d/dy| of luma (grad 1): shaders/luma.wgsl:9-28 */
+void fho_luma(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w, int grad);
+/* luma SAD cost volume over displacements |dy|, |dx| <= r, channel (dy + r) * (2r + 1) + dx + r:
+ * shaders/sad.wgsl:10-29 */
+void fho_sad(const fho_view* la, const fho_view* lb, const fho_view* out, uint32_t n, uint32_t h, uint32_t w,
+             uint32_t r);
+/* convex x2 upsample: softmax over 9 of wt (channel k * 4 + sy * 2 + sx) weighting x's 3x3 neighbourhood:
+ * shaders/convex.wgsl:10-35; out is 2h x 2w */
+void fho_convex(const fho_view* wt, const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w,
+                uint32_t c);
+/* FiLM modulate out = h * (1 + g[c]) + g[c + C], g f16 [n][2C]: shaders/film.wgsl:9-15 */
+void fho_film(const fho_view* hv, const uint16_t* g, const fho_view* out, uint32_t n, uint32_t h, uint32_t w,
+              uint32_t c);
+/* visibility blend weights (softmax of 3 logits; the third class split half/half) -> 2 channels:
+ * shaders/blend.wgsl:9-21 */
+void fho_blend(const fho_view* vis, const fho_view* out, uint32_t n, uint32_t h, uint32_t w);
+/* fused blend of two 3-channel images by those weights: shaders/blendmix.wgsl:12-28 */
+void fho_blendmix(const fho_view* wa, const fho_view* wb, const fho_view* vis, const fho_view* out, uint32_t n,
+                  uint32_t h, uint32_t w);
+/* k x k average pool, stride k, out (h / k) x (w / k): shaders/avgpool.wgsl:8-19, ops/interp.rs:12-18 */
+void fho_avgpool(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c, uint32_t k);
+/* bilinear resize (aa 0, align_corners false) or antialiased triangle-filter resize (aa 1):
+ * shaders/interp.wgsl:11-45 */
+void fho_interp(const fho_view* x, const fho_view* out, uint32_t n, uint32_t c, uint32_t ih, uint32_t iw,
+                uint32_t oh, uint32_t ow, int aa);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

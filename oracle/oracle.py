@@ -117,3 +117,109 @@ def f16_to_f32(a):
     out = np.empty(a.shape, dtype=np.float32)
     lib().fho_f16_to_f32_n(_ptr(a), _ptr(out), a.size)
     return out
+
+
+# ---- the network ops around the convs (fh_ops_oracle.c) --------------------------------------------------------
+# Inputs are uint16 arrays (n, h, w, cs) of f16 bits read through a view (channel offset c0, read scale); outputs
+# are new dense (n, oh, ow, c) arrays.
+
+class FhoView(ctypes.Structure):
+    _fields_ = [("p", ctypes.c_void_p), ("cs", ctypes.c_uint32), ("c0", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+def _view(a, c0=0, scale=1.0):
+    assert a.dtype == np.uint16 and a.ndim == 4 and a.flags.c_contiguous
+    return ctypes.byref(FhoView(a.ctypes.data, a.shape[3], c0, scale))
+
+
+def _ops_lib():
+    L = lib()
+    if not getattr(L, "_ops_typed", False):
+        V, U, I = ctypes.POINTER(FhoView), ctypes.c_uint32, ctypes.c_int
+        sig = {
+            "fho_warp": [V, V, V, U, U, U, U],
+            "fho_luma": [V, V, U, U, U, I],
+            "fho_sad": [V, V, V, U, U, U, U],
+            "fho_convex": [V, V, V, U, U, U, U],
+            "fho_film": [V, ctypes.c_void_p, V, U, U, U, U],
+            "fho_blend": [V, V, U, U, U],
+            "fho_blendmix": [V, V, V, V, U, U, U],
+            "fho_avgpool": [V, V, U, U, U, U, U],
+            "fho_interp": [V, V, U, U, U, U, U, U, I],
+        }
+        for name, args in sig.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = None
+        L._ops_typed = True
+    return L
+
+
+def _out(n, h, w, c):
+    return np.zeros((n, h, w, c), np.uint16)
+
+
+def warp(img, flow, c, img_c0=0, img_scale=1.0, flow_c0=0, flow_scale=1.0):
+    n, h, w, _ = img.shape
+    y = _out(n, h, w, c)
+    _ops_lib().fho_warp(_view(img, img_c0, img_scale), _view(flow, flow_c0, flow_scale), _view(y), n, h, w, c)
+    return y
+
+
+def luma(x, grad=False, c0=0, scale=1.0):
+    n, h, w, _ = x.shape
+    y = _out(n, h, w, 1)
+    _ops_lib().fho_luma(_view(x, c0, scale), _view(y), n, h, w, int(grad))
+    return y
+
+
+def sad(la, lb, r, la_c0=0, lb_c0=0):
+    n, h, w, _ = la.shape
+    y = _out(n, h, w, (2 * r + 1) ** 2)
+    _ops_lib().fho_sad(_view(la, la_c0), _view(lb, lb_c0), _view(y), n, h, w, r)
+    return y
+
+
+def convex(wt, x, c, wt_c0=0, x_c0=0):
+    n, h, w, _ = x.shape
+    y = _out(n, 2 * h, 2 * w, c)
+    _ops_lib().fho_convex(_view(wt, wt_c0), _view(x, x_c0), _view(y), n, h, w, c)
+    return y
+
+
+def film(hv, g, c, c0=0):
+    """g: uint16 (n, 2c) f16 bits."""
+    n, h, w, _ = hv.shape
+    g = np.ascontiguousarray(g, np.uint16)
+    assert g.shape == (n, 2 * c)
+    y = _out(n, h, w, c)
+    _ops_lib().fho_film(_view(hv, c0), g.ctypes.data_as(ctypes.c_void_p), _view(y), n, h, w, c)
+    return y
+
+
+def blend(vis, c0=0, scale=1.0):
+    n, h, w, _ = vis.shape
+    y = _out(n, h, w, 2)
+    _ops_lib().fho_blend(_view(vis, c0, scale), _view(y), n, h, w)
+    return y
+
+
+def blendmix(wa, wb, vis, vis_c0=0, vis_scale=1.0, wa_c0=0, wb_c0=0):
+    n, h, w, _ = vis.shape
+    y = _out(n, h, w, 3)
+    _ops_lib().fho_blendmix(_view(wa, wa_c0), _view(wb, wb_c0), _view(vis, vis_c0, vis_scale), _view(y), n, h, w)
+    return y
+
+
+def avgpool(x, c, k, c0=0):
+    n, h, w, _ = x.shape
+    y = _out(n, h // k, w // k, c)
+    _ops_lib().fho_avgpool(_view(x, c0), _view(y), n, h, w, c, k)
+    return y
+
+
+def interp(x, c, oh, ow, aa=False, c0=0, scale=1.0):
+    n, ih, iw, _ = x.shape
+    y = _out(n, oh, ow, c)
+    _ops_lib().fho_interp(_view(x, c0, scale), _view(y), n, c, ih, iw, oh, ow, int(aa))
+    return y

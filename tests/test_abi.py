@@ -133,3 +133,48 @@ def test_pair_plan_rejects_what_it_cannot_fuse():
     big = fhconv.make_desc(1, 20, 30, 36, 96, act=0)  # 96 output channels: no pair instantiated
     with pytest.raises(fhconv.FhcError):
         fhconv.ConvPairPlan(a, wa, ba, None, big, np.zeros(96 * 36 * 9, np.uint16), np.zeros(96, np.uint16), None)
+
+
+def _ops():
+    import fhops
+    return fhops, fhops._lib()
+
+
+def _tv(p=0x1000, cs=4, c0=0, scale=1.0):
+    import fhops
+    return ctypes.byref(fhops.FhcTensor(p, cs, c0, scale))
+
+
+def test_network_ops_reject_bad_views_before_any_launch():
+    """Validation happens on the host before any HIP call (no GPU needed): views too narrow for the channels an op
+    reads or writes, scales on inputs an op reads unscaled, null views, out-of-range parameters."""
+    fh, L = _ops()
+    cases = [
+        ("fhc_warp", (_tv(cs=3), _tv(cs=2), _tv(cs=4), 1, 4, 4, 4, None), "does not hold"),
+        ("fhc_warp", (_tv(), _tv(cs=1), _tv(), 1, 4, 4, 4, None), "warp flow"),
+        ("fhc_luma", (_tv(cs=2), _tv(), 1, 4, 4, 0, None), "luma x"),
+        ("fhc_sad_volume", (_tv(), _tv(), _tv(cs=24), 1, 4, 4, 2, None), "sad_volume out"),
+        ("fhc_sad_volume", (_tv(scale=0.5), _tv(), _tv(cs=64), 1, 4, 4, 2, None), "unscaled"),
+        ("fhc_sad_volume", (_tv(), _tv(), _tv(cs=300), 1, 4, 4, 8, None), "radius"),
+        ("fhc_convex_upsample", (_tv(cs=35), _tv(), _tv(), 1, 4, 4, 4, None), "convex_upsample wt"),
+        ("fhc_film_modulate", (_tv(), None, _tv(), 1, 4, 4, 4, None), "null g"),
+        ("fhc_blend_weights", (_tv(cs=3, c0=1), _tv(), 1, 4, 4, None), "blend_weights vis"),
+        ("fhc_blendmix", (_tv(), _tv(cs=2), _tv(), _tv(), 1, 4, 4, None), "blendmix wb"),
+        ("fhc_avgpool", (_tv(), _tv(), 1, 4, 4, 4, 0, None), "k is 0"),
+        ("fhc_interpolate", (_tv(), _tv(p=0), 1, 4, 4, 4, 2, 2, 0, None), "null pointer"),
+        ("fhc_interpolate", (_tv(scale=float("nan")), _tv(), 1, 4, 4, 4, 2, 2, 0, None), "not finite"),
+        ("fhc_interpolate", (_tv(), _tv(), 1, 4, 0, 4, 2, 2, 1, None), "empty input"),
+        ("fhc_warp", (None, _tv(), _tv(), 1, 4, 4, 4, None), "null view"),
+    ]
+    for name, args, msg in cases:
+        rc = getattr(L, name)(*args)
+        assert rc == -1, (name, msg, rc)
+        assert msg in fhconv.last_error(), (name, fhconv.last_error())
+
+
+def test_network_ops_on_empty_tensors_are_no_ops():
+    fh, L = _ops()
+    assert L.fhc_warp(None, None, None, 0, 4, 4, 4, None) == 0
+    assert L.fhc_sad_volume(None, None, None, 1, 0, 4, 3, None) == 0
+    assert L.fhc_avgpool(None, None, 1, 1, 1, 4, 2, None) == 0  # a 1x1 input pools to 0x0
+    assert L.fhc_interpolate(None, None, 1, 3, 4, 4, 0, 8, 1, None) == 0

@@ -1,0 +1,205 @@
+"""Parity of the HIP network ops (through the C ABI, include/fhc_ops.h) with the CPU oracle, on the GPU.
+
+Bar: bit-exact f16 results for the ops without a transcendental (warp, luma, luma_grad, sad_volume, film_modulate,
+avgpool, interpolate: the same f32 operations in the same order, one RTNE rounding); where a softmax's expf is
+involved (the GPU's expf and the host's may differ in the last f32 bit) at most 1 f16 ulp for blend_weights and
+blendmix, and for convex_upsample, whose 9 signed terms can cancel, 1 ulp or 2^-16 of the input's largest
+magnitude. Views (channel offsets, wider pixel strides, read scales), batches, ragged sizes, flows reaching
+far outside the image and outputs written into a concat slice are covered; channels outside an output view must
+stay untouched. Sizes include the FlyHighFG shapes at 1080p (network 864x480: 216x120, 108x60, 54x30).
+"""
+import numpy as np
+import pytest
+
+from fhtest import f16_bits, oracle, ulp_dist
+
+pytestmark = pytest.mark.gpu
+
+SENTINEL = 0x7BFF  # f16 65504: what untouched channels of an output buffer hold
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to("cuda")
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy().view(np.uint16)
+
+
+def fhops():
+    import fhops as m  # noqa: E402  (flyhigh-engine_amd is on sys.path through fhtest)
+    return m
+
+
+def rand(rng, shape, lo=-1.0, hi=1.0):
+    return f16_bits(rng.uniform(lo, hi, shape))
+
+
+def exact(got, want, what):
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{what}: {len(bad)} elements differ, first at {bad[0].tolist()}"
+
+
+def within_ulp(got, want, what, ulps=1):
+    d = ulp_dist(got, want)
+    assert d.max() <= ulps, f"{what}: max {d.max()} ulps at {np.unravel_index(d.argmax(), d.shape)}"
+
+
+def softmax_close(got, want, xmax, what):
+    """1 f16 ulp, or 2^-16 * max|x| where the weighted sum cancels: a weight from a different last f32 bit of expf
+    moves a sum of 9 terms by at most a few 2^-24 * max|x|."""
+    g, w = got.view(np.float16).astype(np.float64), want.view(np.float16).astype(np.float64)
+    unit = np.spacing(np.abs(w).astype(np.float16)).astype(np.float64)
+    bad = np.abs(g - w) > np.maximum(unit, 2.0 ** -16 * xmax)
+    assert not bad.any(), f"{what}: {bad.sum()} elements off, first at {np.argwhere(bad)[0].tolist()}"
+
+
+def sliced_out(n, h, w, cs, c0):
+    """An output buffer of cstride cs filled with the sentinel; the op writes channels c0.."""
+    return np.full((n, h, w, cs), SENTINEL, np.uint16)
+
+
+def check_slice(buf, got_dev, c0, c, want, what, ulps=0):
+    got = host(got_dev)
+    assert np.all(got[..., :c0] == SENTINEL) and np.all(got[..., c0 + c:] == SENTINEL), f"{what}: wrote outside view"
+    (exact if ulps == 0 else within_ulp)(got[..., c0:c0 + c], want, what)
+
+
+WARP_CASES = [  # n, h, w, c, img cstride, img c0, flow cstride, flow c0, flow range, flow scale, img scale
+    (2, 60, 108, 36, 36, 0, 4, 0, 6.0, 0.125, 1.0),     # features at 1/8 (vector path)
+    (1, 120, 216, 3, 3, 0, 4, 2, 40.0, 0.25, 1.0),      # the refine warp of a 3-channel image by a view of flow_tq
+    (2, 17, 23, 5, 9, 3, 5, 1, 30.0, 1.0, 0.5),         # ragged, strided views, far outside the image
+    (1, 30, 54, 8, 16, 8, 2, 0, 3.0, 2.0, 2.0),         # vector path through an offset view
+]
+
+
+@pytest.mark.parametrize("case", WARP_CASES)
+def test_warp_matches_oracle(case):
+    n, h, w, c, ics, ic0, fcs, fc0, fr, fs, isc = case
+    say("warp", case)
+    fh = fhops()
+    rng = np.random.default_rng(hash(case) % 2**32)
+    img, flow = rand(rng, (n, h, w, ics), -2, 2), rand(rng, (n, h, w, fcs), -fr, fr)
+    want = oracle.warp(img, flow, c, img_c0=ic0, img_scale=isc, flow_c0=fc0, flow_scale=fs)
+    buf = sliced_out(n, h, w, c + 6, 2)
+    out = dev(buf)
+    fh.warp(fh.View(dev(img), ic0, isc), fh.View(dev(flow), fc0, fs), c, out=fh.View(out, 2))
+    check_slice(buf, out, 2, c, want, f"warp {case}")
+
+
+@pytest.mark.parametrize("grad", [False, True])
+@pytest.mark.parametrize("n,h,w,cs,c0,scale", [(2, 30, 54, 3, 0, 1.0), (1, 120, 216, 7, 4, 1.0),
+                                                (1, 13, 9, 5, 1, 0.5)])
+def test_luma_matches_oracle(grad, n, h, w, cs, c0, scale):
+    say("luma", grad, n, h, w, cs, c0, scale)
+    fh = fhops()
+    rng = np.random.default_rng(n * h * w + cs + grad)
+    x = rand(rng, (n, h, w, cs), 0, 1)
+    want = oracle.luma(x, grad=grad, c0=c0, scale=scale)
+    got = host(fh.luma(fh.View(dev(x), c0, scale), grad=grad))
+    exact(got, want, f"luma grad={grad}")
+
+
+@pytest.mark.parametrize("n,h,w,r", [(2, 30, 54, 3), (3, 60, 108, 2), (1, 5, 4, 3), (1, 1, 1, 2), (2, 9, 31, 0)])
+def test_sad_volume_matches_oracle(n, h, w, r):
+    say("sad", n, h, w, r)
+    fh = fhops()
+    rng = np.random.default_rng(n * h * w + r)
+    la, lb = rand(rng, (n, h, w, 2), 0, 1), rand(rng, (n, h, w, 1), 0, 1)
+    want = oracle.sad(la, lb, r, la_c0=1)
+    s2 = (2 * r + 1) ** 2
+    buf = sliced_out(n, h, w, s2 + 3, 3)
+    out = dev(buf)
+    fh.sad(fh.View(dev(la), 1), dev(lb), r, out=fh.View(out, 3))
+    check_slice(buf, out, 3, s2, want, f"sad r={r}")
+
+
+@pytest.mark.parametrize("n,h,w,c,logit", [(1, 60, 108, 7, 3.0), (2, 11, 6, 3, 20.0), (1, 30, 54, 16, 1.0)])
+def test_convex_upsample_matches_oracle(n, h, w, c, logit):
+    say("convex", n, h, w, c, logit)
+    fh = fhops()
+    rng = np.random.default_rng(n * h * w + c)
+    wt = f16_bits(rng.normal(0, logit, (n, h, w, 40)))
+    x = rand(rng, (n, h, w, c + 1), -4, 4)
+    want = oracle.convex(wt, x, c, wt_c0=4, x_c0=1)
+    got = host(fh.convex(fh.View(dev(wt), 4), fh.View(dev(x), 1), c))
+    softmax_close(got, want, np.abs(x.view(np.float16)).max(), "convex")
+
+
+@pytest.mark.parametrize("n,h,w,c,cs,c0", [(2, 60, 108, 48, 48, 0), (3, 7, 5, 6, 9, 2), (1, 30, 54, 12, 16, 4)])
+def test_film_modulate_matches_oracle(n, h, w, c, cs, c0):
+    say("film", n, h, w, c, cs, c0)
+    fh = fhops()
+    rng = np.random.default_rng(n * h * w + c)
+    hv, g = rand(rng, (n, h, w, cs), -3, 3), rand(rng, (n, 2 * c), -1, 1)
+    want = oracle.film(hv, g, c, c0=c0)
+    got = host(fh.film(fh.View(dev(hv), c0), dev(g), c))
+    exact(got, want, "film")
+
+
+@pytest.mark.parametrize("n,h,w,cs,c0,scale", [(1, 120, 216, 3, 0, 1.0), (2, 13, 17, 7, 4, 2.0),
+                                                (1, 60, 108, 5, 2, 0.5)])
+def test_blend_weights_and_blendmix_match_oracle(n, h, w, cs, c0, scale):
+    say("blend", n, h, w, cs, c0, scale)
+    fh = fhops()
+    rng = np.random.default_rng(n * h * w + cs)
+    vis = f16_bits(rng.normal(0, 4, (n, h, w, cs)))
+    wa, wb = rand(rng, (n, h, w, 3), 0, 1), rand(rng, (n, h, w, 3), 0, 1)
+    vv = fh.View(dev(vis), c0, scale)
+    within_ulp(host(fh.blend(vv)), oracle.blend(vis, c0=c0, scale=scale), "blend_weights")
+    within_ulp(host(fh.blendmix(dev(wa), dev(wb), vv)), oracle.blendmix(wa, wb, vis, vis_c0=c0, vis_scale=scale),
+               "blendmix")
+
+
+@pytest.mark.parametrize("n,h,w,c,cs,c0,k", [(2, 120, 216, 3, 3, 0, 2), (2, 60, 108, 3, 3, 0, 2),
+                                              (1, 61, 109, 8, 12, 4, 2), (1, 25, 14, 5, 5, 0, 3), (1, 8, 8, 4, 4, 0, 1)])
+def test_avgpool_matches_oracle(n, h, w, c, cs, c0, k):
+    say("avgpool", n, h, w, c, cs, c0, k)
+    fh = fhops()
+    rng = np.random.default_rng(n * h * w + c + k)
+    x = rand(rng, (n, h, w, cs), 0, 1)
+    want = oracle.avgpool(x, c, k, c0=c0)
+    got = host(fh.avgpool(fh.View(dev(x), c0), k, c))
+    exact(got, want, "avgpool")
+
+
+INTERP_CASES = [  # n, ih, iw, oh, ow, c, cs, c0, aa, scale
+    (1, 480, 864, 120, 216, 3, 3, 0, True, 1.0),   # the graph's A -> aq (antialiased quarter)
+    (2, 30, 54, 60, 108, 4, 16, 0, False, 1.0),     # flow16 -> flow (vector path)
+    (2, 30, 54, 60, 108, 3, 16, 4, False, 16.0),    # vis16 of an offset view, scaled
+    (1, 23, 41, 7, 9, 5, 6, 1, True, 0.5),          # ragged antialias
+    (1, 7, 9, 20, 31, 2, 2, 0, True, 1.0),          # antialias flag on an upsample (support 1)
+]
+
+
+@pytest.mark.parametrize("case", INTERP_CASES)
+def test_interpolate_matches_oracle(case):
+    n, ih, iw, oh, ow, c, cs, c0, aa, scale = case
+    say("interp", case)
+    fh = fhops()
+    rng = np.random.default_rng(ih * iw + oh + c)
+    x = rand(rng, (n, ih, iw, cs), 0, 1)
+    want = oracle.interp(x, c, oh, ow, aa=aa, c0=c0, scale=scale)
+    got = host(fh.interp(fh.View(dev(x), c0, scale), oh, ow, antialias=aa, c=c))
+    exact(got, want, f"interp {case}")
+
+
+def test_empty_inputs_are_no_ops_and_bad_views_are_errors():
+    import torch
+    fh = fhops()
+    x = dev(np.zeros((1, 4, 4, 3), np.uint16))
+    assert fh.luma(x[:, :0]).shape == (1, 0, 4, 1)
+    with pytest.raises(fh.FhcError, match="does not hold"):
+        fh.warp(x, x, 5)  # 5 channels from a 3-channel view
+    with pytest.raises(fh.FhcError, match="unscaled"):
+        fh.sad(fh.View(x, 0, 2.0), x, 1)
+    with pytest.raises(fh.FhcError, match="radius"):
+        fh.sad(x, x, 8)
+    torch.cuda.synchronize()

@@ -1,0 +1,232 @@
+"""Pins the CPU oracle of the network ops around the convs (oracle/fh_ops_oracle.c) without the reference running.
+
+The reference's tests hold no vectors for these ops (its warp tests cover the camera warp, a different feature), so
+each op is checked against what its mathematics fixes: identities, exact shifted copies, closed forms on ramps and
+constants, softmax invariants, and torch's CPU interpolate, which shaders/interp.wgsl:1-3 says it matches. Each check
+is chosen so that a plausible slip (swapped flow channels, a wrong clamp, mirrored weights, a wrong softmax channel
+order, a batch index ignored) fails it.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+sys.path.insert(0, os.path.join(os.path.dirname(__file__), "..", "oracle"))
+import oracle  # noqa: E402
+
+
+def f16(a):
+    return np.ascontiguousarray(np.asarray(a, np.float32).astype(np.float16)).view(np.uint16)
+
+
+def val(a):
+    return a.view(np.float16).astype(np.float32)
+
+
+def ulp_close(got, want, ulps=1):
+    """|got - want| within `ulps` f16 units of the larger magnitude (denormal floor 2^-24)."""
+    g, w = val(got), np.asarray(want, np.float32)
+    unit = np.maximum(np.spacing(np.maximum(np.abs(g), np.abs(w)).astype(np.float16)).astype(np.float32), 2.0 ** -24)
+    return np.all(np.abs(g - w) <= ulps * unit + 1e-30)
+
+
+rng = np.random.default_rng(7)
+
+
+# ---- warp (shaders/warp.wgsl) ---------------------------------------------------------------------------------
+
+def test_warp_zero_flow_is_identity_and_views_are_honoured():
+    img = f16(rng.uniform(-2, 2, (2, 9, 13, 6)))
+    flow = np.zeros((2, 9, 13, 5), np.uint16)
+    out = oracle.warp(img, flow, 4, img_c0=2, flow_c0=3)
+    assert np.array_equal(out, img[..., 2:6])
+
+
+def test_warp_integer_flow_is_a_clamped_shift():
+    n, h, w, c = 2, 10, 12, 3
+    img = f16(rng.uniform(-1, 1, (n, h, w, c)))
+    flow = np.zeros((n, h, w, 2), np.float32)
+    flow[0, ..., 0], flow[0, ..., 1] = 2.0, -1.0  # image 0: x + 2, y - 1
+    flow[1, ..., 0], flow[1, ..., 1] = -3.0, 4.0  # image 1: x - 3, y + 4
+    out = oracle.warp(img, f16(flow), c)
+    for b, (dx, dy) in enumerate(((2, -1), (-3, 4))):
+        ys = np.clip(np.arange(h) + dy, 0, h - 1)
+        xs = np.clip(np.arange(w) + dx, 0, w - 1)
+        assert np.array_equal(out[b], img[b][ys][:, xs])
+
+
+def test_warp_fractional_flow_on_a_ramp_and_the_scales():
+    h, w = 5, 40
+    ramp = np.broadcast_to((np.arange(w, dtype=np.float32) / 64)[None, :, None], (h, w, 1))
+    img = f16(ramp[None])
+    flow = np.zeros((1, h, w, 2), np.float32)
+    flow[..., 0] = 0.125  # read scale 2: a quarter pixel to the right
+    out = oracle.warp(img, f16(flow), 1, flow_scale=2.0, img_scale=0.5)
+    want = np.minimum(np.arange(w) + 0.25, w - 1) / 64 * 0.5  # the last column clamps onto itself
+    assert np.array_equal(val(out)[0, :, :, 0], np.broadcast_to(want.astype(np.float32), (h, w)))
+    flow[..., 0], flow[..., 1] = 0.0, 0.5  # vertical: a vertical ramp
+    vimg = f16(np.broadcast_to((np.arange(h, dtype=np.float32) / 8)[:, None, None], (h, w, 1))[None])
+    outv = oracle.warp(vimg, f16(flow), 1)
+    wantv = np.minimum(np.arange(h) + 0.5, h - 1) / 8
+    assert np.array_equal(val(outv)[0, :, 0, 0], wantv.astype(np.float32))
+
+
+# ---- luma and luma_grad (shaders/luma.wgsl) ---------------------------------------------------------------------
+
+def test_luma_weights_follow_bgr_order_and_scale():
+    x = np.zeros((1, 1, 3, 5), np.float32)
+    for ch in range(3):
+        x[0, 0, ch, 1 + ch] = 1.0  # view channel ch of pixel ch (view c0 = 1)
+    out = val(oracle.luma(f16(x), c0=1, scale=2.0))[0, 0, :, 0]
+    want = np.array([0.114, 0.587, 0.299], np.float32) * 2  # channel 0 is B, 2 is R
+    assert ulp_close(f16(out), want)
+    assert not ulp_close(f16(out), want[::-1])
+
+
+def test_luma_grad_of_constant_is_zero_and_of_a_ramp_is_its_slope():
+    const = f16(np.full((1, 6, 7, 3), 0.75, np.float32))
+    assert np.all(val(oracle.luma(const, grad=True)) == 0)
+    ramp = np.broadcast_to((np.arange(8, dtype=np.float32) / 32)[None, :, None], (5, 8, 3))[None]
+    g = val(oracle.luma(f16(ramp), grad=True))[0, :, :, 0]
+    assert np.allclose(g[:, :-1], 1 / 32, atol=2e-4)  # the sum of the three weights is 1 up to f32 rounding
+    assert np.all(g[:, -1] == 0)  # no right neighbour, and no change downwards
+
+
+# ---- sad_volume (shaders/sad.wgsl) -------------------------------------------------------------------------------
+
+def test_sad_of_a_shifted_copy_is_zero_in_its_displacement_channel():
+    r, h, w = 3, 16, 20
+    big = f16(rng.uniform(0, 1, (h + 8, w + 8)))
+    dy0, dx0 = 2, -1
+    la = big[4:4 + h, 4:4 + w][None, :, :, None].copy()
+    lb = big[4 - dy0:4 - dy0 + h, 4 - dx0:4 - dx0 + w][None, :, :, None].copy()  # lb(y + dy0, x + dx0) = la(y, x)
+    out = val(oracle.sad(la, lb, r))[0]
+    ch = (dy0 + r) * (2 * r + 1) + dx0 + r
+    inner = out[1 + max(0, -dy0) + 1:h - 1 - max(0, dy0) - 1, 1 + max(0, -dx0) + 1:w - 1 - max(0, dx0) - 1, ch]
+    assert inner.size and np.all(inner == 0)
+    assert np.all(out[1:-1, 1:-1, ch ^ 1] > 0)  # a neighbouring displacement is not zero
+    same = val(oracle.sad(la, la, r))[0, :, :, r * (2 * r + 1) + r]
+    assert np.all(same == 0)
+
+
+def test_sad_of_constants_counts_the_window_inside_the_image():
+    h, w, r = 6, 7, 2
+    la = f16(np.full((2, h, w, 1), 0.75, np.float32))
+    lb = f16(np.full((2, h, w, 1), 0.25, np.float32))
+    out = val(oracle.sad(la, lb, r))
+    cy = np.array([2] + [3] * (h - 2) + [2])
+    cx = np.array([2] + [3] * (w - 2) + [2])
+    count = (cy[:, None] * cx[None, :]).astype(np.float32)
+    want = np.float16(np.float32(0.5) * count / np.float32(9))  # 0.5 summed `count` times is exact in f32
+    assert np.all(out == want.astype(np.float32)[None, :, :, None])
+
+
+# ---- convex upsample (shaders/convex.wgsl) -----------------------------------------------------------------------
+
+def test_convex_with_equal_weights_is_a_zero_padded_box_average():
+    n, h, w, c = 2, 5, 6, 3
+    x = f16(rng.uniform(-1, 1, (n, h, w, c)))
+    wt = np.zeros((n, h, w, 36), np.uint16)
+    out = val(oracle.convex(wt, x, c))
+    xp = np.pad(val(x), ((0, 0), (1, 1), (1, 1), (0, 0)))
+    box = sum(xp[:, ky:ky + h, kx:kx + w] for ky in range(3) for kx in range(3)) / 9
+    want = np.repeat(np.repeat(box, 2, axis=1), 2, axis=2)
+    assert ulp_close(f16(out), want, ulps=2)
+
+
+def test_convex_with_one_dominant_weight_picks_that_neighbour():
+    n, h, w, c = 1, 4, 5, 2
+    x = f16(rng.uniform(-1, 1, (n, h, w, c)))
+    wt = np.zeros((n, h, w, 40), np.float32)
+    pick = {(0, 0): 0, (0, 1): 5, (1, 0): 7, (1, 1): 4}  # sub-pixel (sy, sx) -> neighbour k
+    for (sy, sx), k in pick.items():
+        wt[..., 4 + k * 4 + sy * 2 + sx] = 40.0  # a view at channel offset 4
+    out = val(oracle.convex(f16(wt), x, c, wt_c0=4))
+    xp = np.pad(val(x), ((0, 0), (1, 1), (1, 1), (0, 0)))
+    for (sy, sx), k in pick.items():
+        ky, kx = divmod(k, 3)
+        assert np.array_equal(out[:, sy::2, sx::2], xp[:, ky:ky + h, kx:kx + w])
+
+
+# ---- film_modulate (shaders/film.wgsl) ---------------------------------------------------------------------------
+
+def test_film_identity_scale_and_shift_per_image():
+    n, h, w, c = 2, 3, 4, 5
+    hv = f16(rng.uniform(-1, 1, (n, h, w, c + 2)))
+    g = np.zeros((n, 2 * c), np.float32)
+    assert np.array_equal(oracle.film(hv, f16(g), c, c0=2), hv[..., 2:])
+    g[0, :c] = 1.0  # image 0: doubled
+    g[1, c:] = np.arange(c) / 4  # image 1: shifted per channel
+    out = val(oracle.film(hv, f16(g), c, c0=2))
+    assert np.array_equal(out[0], 2 * val(hv)[0, ..., 2:])
+    assert ulp_close(f16(out[1]), val(hv)[1, ..., 2:] + np.arange(c, dtype=np.float32) / 4)
+
+
+# ---- blend_weights and blendmix (shaders/blend.wgsl, blendmix.wgsl) ---------------------------------------------------
+
+def test_blend_weights_invariants():
+    vis = np.zeros((2, 3, 4, 3), np.float32)
+    out = val(oracle.blend(f16(vis)))
+    assert ulp_close(f16(out), np.full(out.shape, 0.5, np.float32))  # equal logits: 1/3 + 1/6 each
+    vis[0, ..., 0] = 12.0  # class A dominates, read at scale 2
+    vis[1, ..., 2] = 12.0  # the shared class dominates
+    out = val(oracle.blend(f16(vis), scale=2.0))
+    assert np.all(out[0, ..., 0] > 0.999) and np.all(out[0, ..., 1] < 1e-3)
+    assert ulp_close(f16(out[1]), np.full(out[1].shape, 0.5, np.float32))
+    rnd = val(oracle.blend(f16(rng.normal(0, 3, (1, 8, 8, 3)))))
+    assert np.allclose(rnd.sum(-1), 1.0, atol=2e-3) and np.all(rnd >= 0)
+
+
+def test_blendmix_is_the_blend_of_the_two_images():
+    n, h, w = 1, 6, 5
+    wa, wb = f16(rng.uniform(0, 1, (n, h, w, 3))), f16(rng.uniform(0, 1, (n, h, w, 3)))
+    vis = np.zeros((n, h, w, 4), np.float32)
+    vis[:, :3, :, 1] = 30.0  # rows 0-2: class A (view c0 = 1); rows 3-5: class B
+    vis[:, 3:, :, 2] = 30.0
+    out = val(oracle.blendmix(wa, wb, f16(vis), vis_c0=1))
+    assert np.array_equal(out[:, :3], val(wa)[:, :3])
+    assert np.array_equal(out[:, 3:], val(wb)[:, 3:])
+    logits = f16(rng.normal(0, 2, (n, h, w, 3)))
+    bw = val(oracle.blend(logits))
+    mix = val(oracle.blendmix(wa, wb, logits))
+    want = val(wa) * bw[..., :1] + val(wb) * bw[..., 1:2]
+    assert np.allclose(mix, want, atol=2e-3)
+
+
+# ---- avgpool (shaders/avgpool.wgsl) ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("k", [1, 2, 4])
+def test_avgpool_is_the_block_mean(k):
+    n, h, w, c = 2, 9, 14, 3  # h, w not multiples of k: the remainder rows and columns are dropped
+    x = f16(rng.uniform(-1, 1, (n, h, w, c + 1)))
+    out = oracle.avgpool(x, c, k, c0=1)
+    oh, ow = h // k, w // k
+    blocks = val(x)[:, :oh * k, :ow * k, 1:].reshape(n, oh, k, ow, k, c).mean(axis=(2, 4))
+    if k == 1:
+        assert np.array_equal(out, x[..., 1:])
+    assert ulp_close(out, blocks)
+
+
+# ---- interpolate (shaders/interp.wgsl) ---------------------------------------------------------------------------
+
+def _torch_resize(x, c, oh, ow, aa):
+    torch = pytest.importorskip("torch")
+    t = torch.from_numpy(val(x)[..., :c].copy()).permute(0, 3, 1, 2)
+    y = torch.nn.functional.interpolate(t, size=(oh, ow), mode="bilinear", align_corners=False, antialias=aa)
+    return y.permute(0, 2, 3, 1).numpy()
+
+
+@pytest.mark.parametrize("ih,iw,oh,ow,aa", [(8, 12, 16, 24, False), (30, 54, 60, 108, False), (13, 7, 5, 3, False),
+                                            (120, 216, 30, 54, True), (24, 40, 12, 20, True), (17, 23, 5, 11, True)])
+def test_interp_matches_torch_bilinear(ih, iw, oh, ow, aa):
+    x = f16(rng.uniform(-1, 1, (2, ih, iw, 3)))
+    out = oracle.interp(x, 3, oh, ow, aa=aa)
+    assert ulp_close(out, _torch_resize(x, 3, oh, ow, aa), ulps=2)
+
+
+def test_interp_same_size_is_a_copy_and_scale_applies():
+    x = f16(rng.uniform(-1, 1, (1, 7, 9, 4)))
+    assert np.array_equal(oracle.interp(x, 4, 7, 9), x)
+    assert np.array_equal(oracle.interp(x, 2, 7, 9, aa=True, c0=1), x[..., 1:3])  # triangle of width 1 at scale 1
+    assert np.array_equal(val(oracle.interp(x, 4, 7, 9, scale=0.5)), val(x) * 0.5)
