@@ -10,10 +10,13 @@ frames/s = 1000 / ms per step (the non-conv ops of pair()/mid() are not part of 
 Alongside: per-launch time and roofline fraction (each launch captured R times in a graph, median of G replays
 over R; "cold" rotates buffer sets larger than the 256 MB MALL, "warm" reuses one), the layers of the single-layer
 configurations (3x3 32->32 at 1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1), the batched
-workload (the frame's convs over 8 independent 4K frame pairs with 3 mid() phases each), and the CPU baseline: the
-oracle (a C restatement of the reference's conv arithmetic) over the same conv layers on the host's cores.
+workload (the frame's convs over 8 independent 4K frame pairs with 3 mid() phases each), the network ops between
+the convs (warp, luma, sad volume, convex upsample, FiLM, blendmix, avgpool, resize: each op instance of one frame and
+of the batched workload against its HBM roofline), and the CPU baseline: the oracle (a C restatement of the
+reference's conv arithmetic) over the same conv layers on the host's cores.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--no-batched] [--no-fuse]
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--no-batched] [--no-fuse] [--no-ops]
+    python bench.py --only-ops
 """
 import argparse
 import json
@@ -205,6 +208,65 @@ def pair_timing(torch, net, a_name, reps, graphs, cold_bytes, stream):
                 flops=flops, bytes=nbytes, bound=bound, roof_us=round(t_roof * 1e6, 3),
                 frac_cold=round(t_roof * 1e6 / cold, 4), frac_warm=round(t_roof * 1e6 / warm, 4),
                 tflops_cold=round(flops / cold / 1e6, 2), gbs_cold=round(nbytes / cold / 1e3, 1), cold_sets=nsets)
+
+
+def net_op_call(fh, op, ins, out, stream):
+    """One launch of the network op `op` (flyhighfg.NetOp) on device tensors ins -> out."""
+    k = op.kw
+    if op.op == "interp":
+        return fh.interp(ins[0], k["oh"], k["ow"], k["aa"], out=out, stream=stream)
+    if op.op == "avgpool":
+        return fh.avgpool(ins[0], k["k"], out=out, stream=stream)
+    if op.op == "luma":
+        return fh.luma(ins[0], k["grad"], out=out, stream=stream)
+    if op.op == "sad":
+        return fh.sad(ins[0], ins[1], k["r"], out=out, stream=stream)
+    if op.op == "warp":
+        return fh.warp(ins[0], ins[1], out=out, stream=stream)
+    if op.op == "film":
+        return fh.film(ins[0], ins[1], out=out, stream=stream)
+    if op.op == "convex":
+        return fh.convex(ins[0], ins[1], out=out, stream=stream)
+    if op.op == "blendmix":
+        return fh.blendmix(ins[0], ins[1], ins[2], out=out, stream=stream)
+    raise ValueError(op.op)
+
+
+def net_ops_timing(torch, fhops, ops, reps, graphs, cold_bytes, stream):
+    """Warm and cold per-launch time of each network op instance (graph of `reps` launches) against its HBM
+    roofline: the algorithmic bytes (inputs read once, output written once) at 8 TB/s."""
+    rows = []
+    for op in ops:
+        def make():
+            ins = [torch.empty((op.n,) + s, dtype=torch.float16, device="cuda").uniform_(0, 1) for s in op.ins]
+            return ins, torch.empty((op.n,) + op.out, dtype=torch.float16, device="cuda")
+        i0, o0 = make()
+        warm = time_graph(torch, lambda i=0: net_op_call(fhops, op, i0, o0, stream), reps, graphs, stream)
+        nsets = max(2, min(4096, -(-cold_bytes // op.bytes)))
+        creps = -(-max(reps, nsets) // nsets) * nsets
+        sets = [make() for _ in range(nsets)]
+        cold = time_graph(torch, lambda i=0: net_op_call(fhops, op, *sets[i % nsets], stream), creps, graphs, stream)
+        del sets
+        roof_us = op.bytes / HBM_PEAK * 1e6
+        rows.append(dict(name=op.name, op=op.op, n=op.n, bytes=op.bytes, us_warm=round(warm, 3),
+                         us_cold=round(cold, 3), roof_us=round(roof_us, 3), frac_cold=round(roof_us / cold, 4),
+                         frac_warm=round(roof_us / warm, 4), gbs_cold=round(op.bytes / cold / 1e3, 1),
+                         cold_sets=nsets))
+        log("net op", json.dumps(rows[-1]))
+    return rows
+
+
+def net_ops_report(args, torch, flyhighfg, stream, net_w, net_h):
+    """The network ops of one frame (1 pair, 1 mid) and of the batched workload (8 pairs, 3 mids each)."""
+    import fhops
+    frame = net_ops_timing(torch, fhops, flyhighfg.network_ops(net_w, net_h, 1, 1), args.reps, args.graphs,
+                           args.cold_mb << 20, stream)
+    batched = net_ops_timing(torch, fhops, flyhighfg.network_ops(net_w, net_h, 8, 24), args.reps, args.graphs,
+                             args.cold_mb << 20, stream)
+    torch.cuda.empty_cache()
+    return dict(frame=frame, frame_us_warm_sum=round(sum(r["us_warm"] for r in frame), 3),
+                batched=batched, batched_us_warm_sum=round(sum(r["us_warm"] for r in batched), 3),
+                batched_workload="8 frame pairs (A/B ops over 16 frames) and 24 mid() phases at network 864x480")
 
 
 def batched_workload(args, torch, np, fhconv, flyhighfg, stream, pairs=8, mids=3):
@@ -435,6 +497,9 @@ def main():
     ap.add_argument("--no-autotune", action="store_true", help="plan with the heuristic only (no per-shape timing)")
     ap.add_argument("--no-fuse", action="store_true", help="one launch per conv (no fused conv pairs)")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched workload (8 pairs, 3 mids each)")
+    ap.add_argument("--no-ops", action="store_true", help="skip the timing of the network ops between the convs")
+    ap.add_argument("--only-ops", action="store_true",
+                    help="only time the network ops (frame and batched shapes) and print them as one JSON line")
     ap.add_argument("--tune", help="plan with this choice table (cin,cout,h,w,stride=code lines) instead of autotuning")
     ap.add_argument("--pmc-layer", help="only run this frame layer --pmc-reps times over rotating (cold) buffers, "
                                         "then a copy of known size as many times: the workload of the rocprofv3 "
@@ -466,6 +531,9 @@ def main():
         log(f"bench: {n_tune} choices from {args.tune}")
     net_w, net_h = 864, 480  # default_internal(1920, 1080) = (856, 480), padded to a multiple of 32
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
+    if args.only_ops:
+        print(json.dumps(dict(net_ops=net_ops_report(args, torch, flyhighfg, stream, net_w, net_h))), flush=True)
+        return 0
     layers = flyhighfg.flyhighfg_layers(net_w, net_h, k=1)
     pair = [L for L in layers if L.stage == "pair"]
     mid = [L for L in layers if L.stage == "mid"]
@@ -584,6 +652,8 @@ def main():
         batched = batched_workload(args, torch, np, fhconv, flyhighfg, stream)
         torch.cuda.empty_cache()
 
+    net_ops = None if args.no_ops else net_ops_report(args, torch, flyhighfg, stream, net_w, net_h)
+
     mfma_rate = mfma_rate_probe(torch, fhconv, stream)
     log(f"bench: sustained dense f16 MFMA rate {mfma_rate:.0f} TFLOP/s")
 
@@ -633,6 +703,7 @@ def main():
         roofline=roofline, cpu_baseline=cpu, layers=per_layer, pairs=per_pair, config_layers=cfg_layers,
         config_pairs=cfg_pairs,
         batched=batched,
+        net_ops=net_ops,
         tune_table=tune_table,
     )
     print(json.dumps(out), flush=True)

@@ -45,8 +45,13 @@ __device__ __forceinline__ void ld4(const View& v, size_t pix, uint32_t ch, uint
         o[0] = h2f((uint16_t)q.x), o[1] = h2f((uint16_t)(q.x >> 16));
         o[2] = h2f((uint16_t)q.y), o[3] = h2f((uint16_t)(q.y >> 16));
     } else {
+        // the channel index clamped to the view, the load unconditional and the value selected afterwards: a load
+        // under a condition becomes a branch that waits for it, one memory latency per load
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) o[i] = ch + i < c ? ld(v, pix, ch + i) : 0.0f;
+        for (uint32_t i = 0; i < 4; i++) {
+            const float val = ld(v, pix, min(ch + i, c - 1));
+            o[i] = ch + i < c ? val : 0.0f;
+        }
     }
 }
 template <bool VEC>
@@ -122,29 +127,71 @@ __global__ __launch_bounds__(kThreads) void sad_kernel(View la, View lb, OView o
     for (int wy = -1; wy <= 1; wy++)
 #pragma unroll
         for (int wx = -1; wx <= 1; wx++) {
+            // every load unconditional (clamped coordinates), so the 18 loads issue together; a tap outside the
+            // image adds +0, which leaves the sum as the reference's skipped tap does
             const int yy = (int)y + wy, xx = (int)x + wx;
-            if (yy >= 0 && yy < (int)h && xx >= 0 && xx < (int)w) {
-                const float lav = ld(la, (size_t)(img0 + yy) * w + xx, 0);
-                const int syy = clampi(yy + dy, 0, (int)h - 1), sxx = clampi(xx + dx, 0, (int)w - 1);
-                acc = acc + fabsf(lav - ld(lb, (size_t)(img0 + syy) * w + sxx, 0));
-            }
+            const bool in = yy >= 0 && yy < (int)h && xx >= 0 && xx < (int)w;
+            const int cy = clampi(yy, 0, (int)h - 1), cx = clampi(xx, 0, (int)w - 1);
+            const float lav = ld(la, (size_t)(img0 + cy) * w + cx, 0);
+            const int syy = clampi(yy + dy, 0, (int)h - 1), sxx = clampi(xx + dx, 0, (int)w - 1);
+            const float d = fabsf(lav - ld(lb, (size_t)(img0 + syy) * w + sxx, 0));
+            acc = acc + (in ? d : 0.0f);
         }
     st(out, pix, d, acc / 9.0f);
 }
 
-// ---- convex upsample: shaders/convex.wgsl:12-34; one lane per output pixel, all channels ------------------------
-__global__ __launch_bounds__(kThreads) void convex_kernel(View wt, View x, OView out, uint32_t h, uint32_t w,
-                                                          uint32_t c, uint32_t items) {
-    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-    if (t >= items) return;
-    const uint32_t ow = 2 * w, oh = 2 * h;
-    const uint32_t ox = t % ow, row = t / ow, oy = row % oh, img = row / oh;
-    const uint32_t ih = oy / 2, iw = ox / 2, sub = (oy % 2) * 2 + ox % 2;
-    const size_t ipix = ((size_t)img * h + ih) * w + iw;
+// ---- convex upsample: shaders/convex.wgsl:12-34 ------------------------------------------------------------------
+// A workgroup computes 16 x 16 output pixels (8 x 8 input pixels, 4 sub-pixels each): it stages the 36 weight
+// channels of its input pixels and the 10 x 10 neighbourhood of x (zeros outside the image: adding 0 * weight is
+// what the reference's zero branch adds) in LDS with coalesced reads, then one lane per output pixel computes its
+// softmax once and every channel from LDS, in the reference's order.
+constexpr uint32_t kCvIn = 8, kCvHalo = kCvIn + 2;
+
+__global__ __launch_bounds__(kThreads) void convex_tile_kernel(View wt, View x, OView out, uint32_t h, uint32_t w,
+                                                               uint32_t c, uint32_t tiles_x, uint32_t tiles_y) {
+    extern __shared__ __align__(16) uint16_t lds[];
+    uint16_t* lw = lds;                       // [kCvIn * kCvIn][36]
+    uint16_t* lx = lds + kCvIn * kCvIn * 36;  // [kCvHalo * kCvHalo][c]
+    const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+    const uint32_t bt = blockIdx.x, txi = bt % tiles_x, r = bt / tiles_x, tyi = r % tiles_y, img = r / tiles_y;
+    const int ix0 = (int)(txi * kCvIn), iy0 = (int)(tyi * kCvIn);
+    // staging with every load unconditional (clamped to the image / the view) and unrolled, so they issue together
+#pragma unroll
+    for (uint32_t k = 0; k < (kCvIn * kCvIn * 9 + kThreads - 1) / kThreads; k++) {  // 9 quads of 4 channels a pixel
+        const uint32_t e = min(tid + k * kThreads, kCvIn * kCvIn * 9 - 1);
+        const uint32_t p = e / 9, q = e - p * 9, py = p / kCvIn, px = p % kCvIn;
+        const int gy = min(iy0 + (int)py, (int)h - 1), gx = min(ix0 + (int)px, (int)w - 1);
+        const uint16_t* src = wt.p + (((size_t)img * h + gy) * w + gx) * wt.cs + wt.c0 + q * 4;
+        // lanes past the last quad rewrite that quad with its own value (a conditional store would pull the load
+        // into the branch and serialise the loads again)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) lw[p * 36 + q * 4 + i] = src[i];
+    }
+    if (tid < kCvHalo * kCvHalo) {  // one lane per halo pixel, channels 8 at a time
+        const uint32_t py = tid / kCvHalo, px = tid % kCvHalo;
+        const int gy = iy0 - 1 + (int)py, gx = ix0 - 1 + (int)px;
+        const bool in = gy >= 0 && gy < (int)h && gx >= 0 && gx < (int)w;
+        const uint16_t* src =
+            x.p + (((size_t)img * h + clampi(gy, 0, (int)h - 1)) * w + clampi(gx, 0, (int)w - 1)) * x.cs + x.c0;
+        for (uint32_t c8 = 0; c8 < c; c8 += 8) {
+            // channels past c rewrite channel c - 1 with its own value: unconditional loads and stores
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                const uint32_t cc = min(c8 + i, c - 1);
+                const uint16_t v = src[cc];
+                lx[tid * c + cc] = in ? v : (uint16_t)0;
+            }
+        }
+    }
+    __syncthreads();
+    const uint32_t ox = txi * 2 * kCvIn + tx, oy = tyi * 2 * kCvIn + ty;
+    if (ox >= 2 * w || oy >= 2 * h) return;
+    const uint32_t lix = tx / 2, liy = ty / 2, sub = (ty % 2) * 2 + tx % 2;
+    const uint16_t* pw = lw + (liy * kCvIn + lix) * 36 + sub;
     float m = -3.0e38f, ws[9];
 #pragma unroll
     for (uint32_t k = 0; k < 9; k++) {
-        ws[k] = ld(wt, ipix, k * 4 + sub);
+        ws[k] = h2f(pw[k * 4]);
         m = fmaxf(m, ws[k]);
     }
     float denom = 0.0f;
@@ -155,16 +202,13 @@ __global__ __launch_bounds__(kThreads) void convex_kernel(View wt, View x, OView
     }
 #pragma unroll
     for (uint32_t k = 0; k < 9; k++) ws[k] = ws[k] / denom;
+    const size_t opix = ((size_t)img * 2 * h + oy) * 2 * w + ox;
     for (uint32_t co = 0; co < c; co++) {
         float acc = 0.0f;
 #pragma unroll
-        for (uint32_t k = 0; k < 9; k++) {
-            const int ny = (int)ih - 1 + (int)(k / 3), nx = (int)iw - 1 + (int)(k % 3);
-            const bool in = ny >= 0 && ny < (int)h && nx >= 0 && nx < (int)w;
-            const float xv = in ? ld(x, ((size_t)img * h + ny) * w + nx, co) : 0.0f;
-            acc = acc + ws[k] * xv;
-        }
-        st(out, t, co, acc);
+        for (uint32_t k = 0; k < 9; k++)
+            acc = acc + ws[k] * h2f(lx[((liy + k / 3) * kCvHalo + lix + k % 3) * c + co]);
+        st(out, opix, co, acc);
     }
 }
 
@@ -216,16 +260,20 @@ __global__ __launch_bounds__(kThreads) void blendmix_kernel(View wa, View wb, Vi
 }
 
 // ---- avgpool: shaders/avgpool.wgsl:10-18 -------------------------------------------------------------------------
-template <bool VEC>
+// K > 0: the pool size at compile time (the loads of the window then issue together); K == 0: k at run time
+template <bool VEC, int K>
 __global__ __launch_bounds__(kThreads) void avgpool_kernel(View x, OView out, uint32_t h, uint32_t w, uint32_t oh,
-                                                           uint32_t ow, uint32_t c, uint32_t k, uint32_t groups,
+                                                           uint32_t ow, uint32_t c, uint32_t kr, uint32_t groups,
                                                            uint32_t items) {
+    const uint32_t k = K > 0 ? (uint32_t)K : kr;
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     if (t >= items) return;
     const uint32_t opix = t / groups, ch = (t - opix * groups) * 4;
     const uint32_t ox = opix % ow, row = opix / ow, oy = row % oh, img = row / oh;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, v[4];
+#pragma unroll
     for (uint32_t ky = 0; ky < k; ky++)
+#pragma unroll
         for (uint32_t kx = 0; kx < k; kx++) {
             ld4<VEC>(x, ((size_t)img * h + oy * k + ky) * w + ox * k + kx, ch, c, v);
 #pragma unroll
@@ -285,6 +333,156 @@ __global__ __launch_bounds__(kThreads) void interp_kernel(View x, OView out, uin
 #pragma unroll
     for (int i = 0; i < 4; i++) val[i] = val[i] * x.scale;
     st4<VEC>(out, opix, ch, c, val);
+}
+
+// The antialiased resize with its taps unrolled to a compile-time bound KM per dimension (the host picks the
+// smallest KM that covers every output's window, from the same f32 formulas): every tap loads from a clamped,
+// in-bounds address unconditionally, so a lane's loads issue together instead of one tap per memory latency; a tap
+// outside the window gets weight 0 and value 0, and adding +0 leaves acc and norm as the reference's loop leaves
+// them (neither is ever -0). The per-column weights are computed once per lane (the reference recomputes the same
+// value per tap). The sum runs rows, then columns, as in the reference.
+template <int KM>
+__global__ __launch_bounds__(kThreads) void interp_aa_kernel(View x, OView out, uint32_t ih, uint32_t iw, uint32_t oh,
+                                                             uint32_t ow, uint32_t c, uint32_t groups,
+                                                             uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t opix = t / groups, ch = (t - opix * groups) * 4;
+    const uint32_t ox = opix % ow, row = opix / ow, oy = row % oh, img = row / oh;
+    const float sh = (float)ih / (float)oh, sw = (float)iw / (float)ow;
+    const float fsh = fmaxf(sh, 1.0f), fsw = fmaxf(sw, 1.0f);
+    const float cy = ((float)oy + 0.5f) * sh, cx = ((float)ox + 0.5f) * sw;
+    const int ymin = max(0, (int)floorf(cy - fsh + 0.5f)), ymax = min((int)ih, (int)floorf(cy + fsh + 0.5f));
+    const int xmin = max(0, (int)floorf(cx - fsw + 0.5f)), xmax = min((int)iw, (int)floorf(cx + fsw + 0.5f));
+    float wx[KM];
+    int xs[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+        const int xx = xmin + j;
+        wx[j] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
+        xs[j] = min(xx, (int)iw - 1);
+    }
+    const size_t base = (size_t)img * ih;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, norm = 0.0f;
+#pragma unroll
+    for (int jy = 0; jy < KM; jy++) {
+        const int y = ymin + jy;
+        const float wy = y < ymax ? fmaxf(0.0f, 1.0f - fabsf(((float)y + 0.5f - cy) / fsh)) : 0.0f;
+        const size_t rbase = (base + min(y, (int)ih - 1)) * iw;
+#pragma unroll
+        for (int jx = 0; jx < KM; jx++) {
+            const bool in = (y < ymax) & (xmin + jx < xmax);
+            const float wgt = wx[jx] * wy;
+            float v[4];
+            ld4<false>(x, rbase + xs[jx], ch, c, v);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = acc[i] + (in ? v[i] : 0.0f) * wgt;
+            norm = norm + wgt;
+        }
+    }
+    float val[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) val[i] = acc[i] / norm * x.scale;
+    st4<false>(out, opix, ch, c, val);
+}
+
+// The same resize for views of at most 4 channels through LDS: a workgroup computes 16 x 16 output pixels from the
+// union of their windows (at most kAaExt x kAaExt input pixels, the host checks the worst tile), staged once with
+// coalesced loads, 4 channels a pixel (one 8-byte LDS read per tap); the L1 then serves no overlapping windows.
+// Staging is a fixed kAaR x kAaR grid of clamped, unconditional loads per lane (lanes past the window rewrite its
+// last row / column with the same values), so it takes one memory round trip. The per-output sum is the one above.
+constexpr uint32_t kAaT = 16, kAaR = 5, kAaExt = kAaT * kAaR;
+
+template <int KM>
+__global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView out, uint32_t ih, uint32_t iw,
+                                                                 uint32_t oh, uint32_t ow, uint32_t c,
+                                                                 uint32_t tiles_x, uint32_t tiles_y) {
+    __shared__ uint2 tile[kAaExt * kAaExt];
+    const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
+    const uint32_t bt = blockIdx.x, txi = bt % tiles_x, r = bt / tiles_x, tyi = r % tiles_y, img = r / tiles_y;
+    const uint32_t ox0 = txi * kAaT, oy0 = tyi * kAaT;
+    const uint32_t ox_last = min(ox0 + kAaT, ow) - 1, oy_last = min(oy0 + kAaT, oh) - 1;
+    const float sh = (float)ih / (float)oh, sw = (float)iw / (float)ow;
+    const float fsh = fmaxf(sh, 1.0f), fsw = fmaxf(sw, 1.0f);
+    const int ylo = max(0, (int)floorf(((float)oy0 + 0.5f) * sh - fsh + 0.5f));
+    const int yhi = min((int)ih, (int)floorf(((float)oy_last + 0.5f) * sh + fsh + 0.5f));
+    const int xlo = max(0, (int)floorf(((float)ox0 + 0.5f) * sw - fsw + 0.5f));
+    const int xhi = min((int)iw, (int)floorf(((float)ox_last + 0.5f) * sw + fsw + 0.5f));
+    const int ny = max(1, min(yhi - ylo, (int)kAaExt)), nx = max(1, min(xhi - xlo, (int)kAaExt));
+    const size_t rowbase = (size_t)img * ih + ylo;
+#pragma unroll
+    for (uint32_t i = 0; i < kAaR; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < kAaR; j++) {
+            const int row = min((int)(ty + kAaT * i), ny - 1), col = min((int)(tx + kAaT * j), nx - 1);
+            const uint16_t* src = x.p + ((rowbase + row) * iw + xlo + col) * x.cs + x.c0;
+            uint16_t v[4];
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++) v[k] = src[min(k, c - 1)];
+            tile[row * kAaExt + col] = uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
+        }
+    __syncthreads();
+    const uint32_t ox = ox0 + tx, oy = oy0 + ty;
+    if (ox >= ow || oy >= oh) return;
+    const float cy = ((float)oy + 0.5f) * sh, cx = ((float)ox + 0.5f) * sw;
+    const int ymin = max(0, (int)floorf(cy - fsh + 0.5f)), ymax = min((int)ih, (int)floorf(cy + fsh + 0.5f));
+    const int xmin = max(0, (int)floorf(cx - fsw + 0.5f)), xmax = min((int)iw, (int)floorf(cx + fsw + 0.5f));
+    float wx[KM];
+    int lc[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+        const int xx = xmin + j;
+        wx[j] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
+        lc[j] = min(max(xx - xlo, 0), nx - 1);
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, norm = 0.0f;
+#pragma unroll
+    for (int jy = 0; jy < KM; jy++) {
+        const int y = ymin + jy;
+        const float wy = y < ymax ? fmaxf(0.0f, 1.0f - fabsf(((float)y + 0.5f - cy) / fsh)) : 0.0f;
+        const uint2* lrow = tile + min(max(y - ylo, 0), ny - 1) * kAaExt;
+#pragma unroll
+        for (int jx = 0; jx < KM; jx++) {
+            const bool in = (y < ymax) & (xmin + jx < xmax);
+            const float wgt = wx[jx] * wy;
+            const uint2 q = lrow[lc[jx]];
+            const float v[4] = {h2f((uint16_t)q.x), h2f((uint16_t)(q.x >> 16)), h2f((uint16_t)q.y),
+                                h2f((uint16_t)(q.y >> 16))};
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = acc[i] + (in ? v[i] : 0.0f) * wgt;
+            norm = norm + wgt;
+        }
+    }
+    float val[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) val[i] = acc[i] / norm * x.scale;
+    st4<false>(out, ((size_t)img * oh + oy) * ow + ox, 0, c, val);
+}
+
+// The largest input extent (rows or columns) of any kAaT-output tile's windows, from the kernel's f32 formulas.
+uint32_t aa_tile_extent(uint32_t in, uint32_t outn) {
+    const float s = (float)in / (float)outn, f = fmaxf(s, 1.0f);
+    int most = 0;
+    for (uint32_t o0 = 0; o0 < outn; o0 += kAaT) {
+        const uint32_t o1 = std::min(o0 + kAaT, outn) - 1;
+        const int lo = std::max(0, (int)floorf(((float)o0 + 0.5f) * s - f + 0.5f));
+        const int hi = std::min((int)in, (int)floorf(((float)o1 + 0.5f) * s + f + 0.5f));
+        most = std::max(most, hi - lo);
+    }
+    return (uint32_t)most;
+}
+
+// The largest number of taps of any output's antialiased window along one axis (in - 1 rows / columns of the
+// output), from the kernel's own f32 formulas.
+uint32_t aa_taps(uint32_t in, uint32_t outn) {
+    const float s = (float)in / (float)outn, f = fmaxf(s, 1.0f);
+    int most = 0;
+    for (uint32_t o = 0; o < outn; o++) {
+        const float cc = ((float)o + 0.5f) * s;
+        const int lo = std::max(0, (int)floorf(cc - f + 0.5f)), hi = std::min((int)in, (int)floorf(cc + f + 0.5f));
+        most = std::max(most, hi - lo);
+    }
+    return (uint32_t)most;
 }
 
 // ---- host side ----------------------------------------------------------------------------------------------------
@@ -394,10 +592,14 @@ extern "C" int fhc_convex_upsample(const fhc_tensor* wt, const fhc_tensor* x, co
         FHC_TRY(check(wt, "convex_upsample wt", 36, false));
         FHC_TRY(check(x, "convex_upsample x", c, false));
         FHC_TRY(check(out, "convex_upsample out", c, false, true));
-        return launch("convex_upsample", (uint64_t)n * 4 * h * w, [&](dim3 g, uint32_t items) {
-            hipLaunchKernelGGL(convex_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(wt), in(x), outv(out), h,
-                               w, c, items);
-        });
+        if (c > 256) return fail(-1, "convex_upsample: %u channels above 256", c);
+        const uint32_t tx = (w + kCvIn - 1) / kCvIn, ty = (h + kCvIn - 1) / kCvIn;
+        if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "convex_upsample: too many tiles");
+        const size_t lds = (kCvIn * kCvIn * 36 + kCvHalo * kCvHalo * c) * 2;
+        hipLaunchKernelGGL(convex_tile_kernel, dim3(n * tx * ty), dim3(kThreads), lds, (hipStream_t)stream, in(wt),
+                           in(x), outv(out), h, w, c, tx, ty);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "convex_upsample: launch failed: %s", hipGetErrorString(e));
     });
 }
 
@@ -460,7 +662,8 @@ extern "C" int fhc_avgpool(const fhc_tensor* x, const fhc_tensor* out, uint32_t 
         const uint32_t groups = (c + 3) / 4;
         const bool v = vec4(c, {x, out});
         return launch("avgpool", (uint64_t)n * oh * ow * groups, [&](dim3 g, uint32_t items) {
-            auto kern = v ? avgpool_kernel<true> : avgpool_kernel<false>;
+            auto kern = k == 2 ? (v ? avgpool_kernel<true, 2> : avgpool_kernel<false, 2>)
+                               : (v ? avgpool_kernel<true, 0> : avgpool_kernel<false, 0>);
             hipLaunchKernelGGL(kern, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), h, w, oh, ow, c, k,
                                groups, items);
         });
@@ -476,6 +679,30 @@ extern "C" int fhc_interpolate(const fhc_tensor* x, const fhc_tensor* out, uint3
         FHC_TRY(check(x, "interpolate x", c, true));
         FHC_TRY(check(out, "interpolate out", c, false, true));
         const uint32_t groups = (c + 3) / 4;
+        if (antialias) {
+            const uint32_t taps = std::max(aa_taps(ih, oh), aa_taps(iw, ow));
+            if (c <= 4 && taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt) {
+                const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
+                if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "interpolate: too many tiles");
+                auto kl = taps <= 4 ? interp_aa_lds_kernel<4> : interp_aa_lds_kernel<8>;
+                hipLaunchKernelGGL(kl, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out),
+                                   ih, iw, oh, ow, c, tx, ty);
+                const hipError_t e = hipGetLastError();
+                return e == hipSuccess ? 0 : fail(-2, "interpolate: launch failed: %s", hipGetErrorString(e));
+            }
+            decltype(&interp_aa_kernel<3>) k = nullptr;
+            if (taps <= 3) k = interp_aa_kernel<3>;
+            else if (taps <= 4) k = interp_aa_kernel<4>;
+            else if (taps <= 6) k = interp_aa_kernel<6>;
+            else if (taps <= 8) k = interp_aa_kernel<8>;
+            else if (taps <= 12) k = interp_aa_kernel<12>;
+            else if (taps <= 16) k = interp_aa_kernel<16>;
+            if (k)
+                return launch("interpolate", (uint64_t)n * oh * ow * groups, [&](dim3 g, uint32_t items) {
+                    hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), ih, iw, oh, ow,
+                                       c, groups, items);
+                });
+        }
         const bool v = vec4(c, {x, out});
         return launch("interpolate", (uint64_t)n * oh * ow * groups, [&](dim3 g, uint32_t items) {
             auto k = antialias ? (v ? interp_kernel<true, true> : interp_kernel<false, true>)

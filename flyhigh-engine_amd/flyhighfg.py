@@ -171,3 +171,50 @@ def config_layers(cfg: int) -> List[ConvLayer]:
             ConvLayer("c3.pw", "pair", 128, 64, 68, 120, k=1, act=0),
         ]
     raise ValueError(f"unknown configuration {cfg}")
+
+
+@dataclass
+class NetOp:
+    """One non-conv op instance of models/graph.json as the planner runs it (net/build.rs:199-450): its kind, batch
+    (the A and B branches run as a batch of 2 per frame pair), NHWC input shapes (h, w, c), output shape, and
+    parameters (radius, pool k, resize size and antialias)."""
+    name: str
+    op: str
+    n: int
+    ins: List[tuple]
+    out: tuple
+    kw: dict
+
+    @property
+    def bytes(self):
+        """Algorithmic HBM bytes: every input read once and the output written once (f16)."""
+        return 2 * self.n * (sum(h * w * c for h, w, c in self.ins) + self.out[0] * self.out[1] * self.out[2])
+
+
+def network_ops(net_w: int = 864, net_h: int = 480, pairs: int = 1, mids: int = 1) -> List[NetOp]:
+    """The non-conv ops of pair() (per frame pair) and mid() (per mid phase) at a padded network size, fine loop
+    k = 1; `pairs` frame pairs and `mids` mid() phases in total. The graph's slices, scales and concats are views (no
+    launch); its film_mlp is a 64-wide MLP of the scalar t on the host (net/build.rs:331-357); render_pix, rgba_in /
+    rgba_out and affine_out sit outside the network (frame I/O) and are not listed."""
+    qw, qh = net_w // 4, net_h // 4
+    e8w, e8h = (qw + 2 - 3) // 2 + 1, (qh + 2 - 3) // 2 + 1
+    e16w, e16h = (e8w + 2 - 3) // 2 + 1, (e8h + 2 - 3) // 2 + 1
+    ab, m = 2 * pairs, mids
+    return [
+        NetOp("interp A,B -> aq,bq", "interp", ab, [(net_h, net_w, 3)], (qh, qw, 3), dict(oh=qh, ow=qw, aa=True)),
+        NetOp("avgpool aq -> i8", "avgpool", ab, [(qh, qw, 3)], (qh // 2, qw // 2, 3), dict(k=2)),
+        NetOp("avgpool i8 -> i16", "avgpool", ab, [(e8h, e8w, 3)], (e8h // 2, e8w // 2, 3), dict(k=2)),
+        NetOp("luma i16", "luma", ab, [(e16h, e16w, 3)], (e16h, e16w, 1), dict(grad=False)),
+        NetOp("sad_volume r3", "sad", pairs, [(e16h, e16w, 1), (e16h, e16w, 1)], (e16h, e16w, 49), dict(r=3)),
+        NetOp("interp flow16", "interp", pairs, [(e16h, e16w, 4)], (e8h, e8w, 4), dict(oh=e8h, ow=e8w, aa=False)),
+        NetOp("interp vis16", "interp", pairs, [(e16h, e16w, 3)], (e8h, e8w, 3), dict(oh=e8h, ow=e8w, aa=False)),
+        NetOp("warp f8a,f8b", "warp", ab, [(e8h, e8w, 36), (e8h, e8w, 2)], (e8h, e8w, 36), {}),
+        NetOp("warp i8a,i8b", "warp", ab, [(e8h, e8w, 3), (e8h, e8w, 2)], (e8h, e8w, 3), {}),
+        NetOp("luma ia,ib", "luma", ab, [(e8h, e8w, 3)], (e8h, e8w, 1), dict(grad=False)),
+        NetOp("sad_volume r2", "sad", pairs, [(e8h, e8w, 1), (e8h, e8w, 1)], (e8h, e8w, 25), dict(r=2)),
+        NetOp("film_modulate", "film", m, [(e8h, e8w, 48), (1, 1, 96)], (e8h, e8w, 48), {}),
+        NetOp("convex_upsample", "convex", m, [(e8h, e8w, 36), (e8h, e8w, 7)], (qh, qw, 7), {}),
+        NetOp("warp aq,bq (refine)", "warp", 2 * m, [(qh, qw, 3), (qh, qw, 2)], (qh, qw, 3), {}),
+        NetOp("blendmix", "blendmix", m, [(qh, qw, 3), (qh, qw, 3), (qh, qw, 3)], (qh, qw, 3), {}),
+        NetOp("luma_grad", "luma", m, [(qh, qw, 3)], (qh, qw, 1), dict(grad=True)),
+    ]

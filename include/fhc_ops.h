@@ -52,7 +52,7 @@ int fhc_sad_volume(const fhc_tensor* la, const fhc_tensor* lb, const fhc_tensor*
                    uint32_t w, uint32_t radius, void* stream);
 
 /* Convex x2 upsample: out (2h x 2w x c) = the softmax over 9 of wt's channels k * 4 + sy * 2 + sx (36 channels,
- * at the input pixel) weighting x's zero-padded 3x3 neighbourhood. wt is the up.w conv's output. Replaces
+ * at the input pixel) weighting x's zero-padded 3x3 neighbourhood; c <= 256. wt is the up.w conv's output. Replaces
  * Gpu::convex (ops/network.rs:48-55, shaders/convex.wgsl:10-35), the "convex_upsample" arm after its conv
  * (net/build.rs:379-416). */
 int fhc_convex_upsample(const fhc_tensor* wt, const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h,

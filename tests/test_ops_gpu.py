@@ -176,6 +176,7 @@ INTERP_CASES = [  # n, ih, iw, oh, ow, c, cs, c0, aa, scale
     (2, 30, 54, 60, 108, 3, 16, 4, False, 16.0),    # vis16 of an offset view, scaled
     (1, 23, 41, 7, 9, 5, 6, 1, True, 0.5),          # ragged antialias
     (1, 7, 9, 20, 31, 2, 2, 0, True, 1.0),          # antialias flag on an upsample (support 1)
+    (1, 240, 432, 30, 54, 8, 8, 0, True, 1.0),      # a tile beyond the LDS budget: the per-output kernel
 ]
 
 
