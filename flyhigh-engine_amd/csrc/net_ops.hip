@@ -485,6 +485,56 @@ uint32_t aa_taps(uint32_t in, uint32_t outn) {
     return (uint32_t)most;
 }
 
+// ---- elementwise: binary.wgsl:11-16, unary.wgsl:11-19, chcopy.wgsl:19-22 ------------------------------------
+// One lane per (pixel, 4-channel group); VEC: 8-byte accesses (every view 4-channel aligned).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void binary_kernel(View a, View b, OView out, uint32_t c, uint32_t cb,
+                                                          int op, uint32_t groups, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t pix = t / groups, ch = (t - pix * groups) * 4;
+    float av[4], bv[4], o[4];
+    ld4<VEC>(a, pix, ch, c, av);
+    if (cb == 1) {  // b's one channel over all of a's
+        const float v = ld(b, pix, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) bv[i] = v;
+    } else {
+        ld4<VEC>(b, pix, ch, c, bv);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float x = av[i] * a.scale, y = bv[i] * b.scale;
+        o[i] = op == 1 ? x * y : x + y;
+    }
+    st4<VEC>(out, pix, ch, c, o);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void unary_kernel(View x, OView out, uint32_t c, int op, float pa, float pb,
+                                                         uint32_t groups, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t pix = t / groups, ch = (t - pix * groups) * 4;
+    float v[4], o[4];
+    ld4<VEC>(x, pix, ch, c, v);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float u = v[i] * x.scale;
+        o[i] = op == 0 ? u * pa : op == 1 ? fminf(fmaxf(u, pa), pb) : op == 2 ? 2.0f / (1.0f + expf(-u)) - 1.0f : -u;
+    }
+    st4<VEC>(out, pix, ch, c, o);
+}
+
+// a channel copy: the bits at scale 1 (the reference copies u32 pairs untouched), else f16(x * scale)
+__global__ __launch_bounds__(kThreads) void chcopy_kernel(View x, OView out, uint32_t c, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t pix = t / c, ch = t - pix * c;
+    const uint16_t v = x.p[(size_t)pix * x.cs + x.c0 + ch];
+    out.p[(size_t)pix * out.cs + out.c0 + ch] = x.scale == 1.0f ? v : f2h(h2f(v) * x.scale);
+}
+
 // ---- host side ----------------------------------------------------------------------------------------------------
 
 constexpr uint64_t kMaxItems = 1ull << 31;
@@ -709,6 +759,57 @@ extern "C" int fhc_interpolate(const fhc_tensor* x, const fhc_tensor* out, uint3
                                : (v ? interp_kernel<true, false> : interp_kernel<false, false>);
             hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), ih, iw, oh, ow, c,
                                groups, items);
+        });
+    });
+}
+
+extern "C" int fhc_binary(const fhc_tensor* a, const fhc_tensor* b, const fhc_tensor* out, uint32_t n, uint32_t h,
+                          uint32_t w, uint32_t c, uint32_t cb, int op, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if (op != 0 && op != 1) return fail(-1, "binary: op %d is neither 0 (add) nor 1 (mul)", op);
+        if (cb != 1 && cb != c) return fail(-1, "binary: b has %u channels, neither 1 nor %u", cb, c);
+        if ((uint64_t)n * h * w * c == 0) return 0;
+        FHC_TRY(check(a, "binary a", c, true));
+        FHC_TRY(check(b, "binary b", cb, true));
+        FHC_TRY(check(out, "binary out", c, false, true));
+        const uint32_t groups = (c + 3) / 4;
+        const bool v = vec4(c, {a, out}) && (cb == 1 || vec4(c, {b}));
+        return launch("binary", (uint64_t)n * h * w * groups, [&](dim3 g, uint32_t items) {
+            auto k = v ? binary_kernel<true> : binary_kernel<false>;
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(a), in(b), outv(out), c, cb, op,
+                               groups, items);
+        });
+    });
+}
+
+extern "C" int fhc_unary(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                         int op, float a, float b, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if (op < 0 || op > 3) return fail(-1, "unary: op %d outside 0..3", op);
+        if ((uint64_t)n * h * w * c == 0) return 0;
+        FHC_TRY(check(x, "unary x", c, true));
+        FHC_TRY(check(out, "unary out", c, false, true));
+        const uint32_t groups = (c + 3) / 4;
+        const bool v = vec4(c, {x, out});
+        return launch("unary", (uint64_t)n * h * w * groups, [&](dim3 g, uint32_t items) {
+            auto k = v ? unary_kernel<true> : unary_kernel<false>;
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), c, op, a, b, groups,
+                               items);
+        });
+    });
+}
+
+extern "C" int fhc_chcopy(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                          void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)n * h * w * c == 0) return 0;
+        FHC_TRY(check(x, "chcopy x", c, true));
+        FHC_TRY(check(out, "chcopy out", c, false, true));
+        return launch("chcopy", (uint64_t)n * h * w * c, [&](dim3 g, uint32_t items) {
+            hipLaunchKernelGGL(chcopy_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), c, items);
         });
     });
 }

@@ -2,7 +2,8 @@
 
 One function per Gpu method of the reference (crates/flyhigh-engine/src/ops/network.rs, interp.rs, render.rs):
 ``warp``, ``luma``, ``sad`` (sad_volume), ``convex`` (convex_upsample after its conv), ``film``, ``blend``,
-``blendmix``, ``avgpool``, ``interp``. Inputs are torch NHWC f16 tensors on the GPU, or ``View`` objects that add the
+``blendmix``, ``avgpool``, ``interp``, and the elementwise ``binary`` (add / mul), ``unary`` (mul_t, affine_out,
+clamp, neg) and ``chcopy`` (a scaled view into a concat slice). Inputs are torch NHWC f16 tensors on the GPU, or ``View`` objects that add the
 reference Tensor's channel offset and read scale (ops/tensor.rs); each function returns a new dense output unless an
 ``out`` view is given (a concat slice is written in place). The module only passes device pointers: when the
 library is missing, loading it raises, and nothing is computed on the host.
@@ -63,6 +64,9 @@ def _lib():
             "fhc_blendmix": [T, T, T, T, U, U, U, P],
             "fhc_avgpool": [T, T, U, U, U, U, U, P],
             "fhc_interpolate": [T, T, U, U, U, U, U, U, I, P],
+            "fhc_binary": [T, T, T, U, U, U, U, U, I, P],
+            "fhc_unary": [T, T, U, U, U, U, I, ctypes.c_float, ctypes.c_float, P],
+            "fhc_chcopy": [T, T, U, U, U, U, P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -169,4 +173,33 @@ def interp(x, oh: int, ow: int, antialias: bool = False, c: Optional[int] = None
     o = _out(out, x, n, oh, ow, c)
     _run("interpolate",
          _lib().fhc_interpolate(_ref(x), _ref(o), n, c, ih, iw, oh, ow, int(antialias), _stream_handle(stream)))
+    return o.t
+
+
+def binary(a, b, op: int = 0, c: Optional[int] = None, out=None, stream=None):
+    """op 0: a * sa + b * sb; op 1: (a * sa) * (b * sb); b with one channel broadcasts."""
+    a, b = _v(a), _v(b)
+    n, h, w, _ = a.shape
+    c = a.channels if c is None else c
+    cb = 1 if b.channels == 1 else c
+    o = _out(out, a, n, h, w, c)
+    _run("binary", _lib().fhc_binary(_ref(a), _ref(b), _ref(o), n, h, w, c, cb, op, _stream_handle(stream)))
+    return o.t
+
+
+def unary(x, op: int, a: float = 0.0, b: float = 0.0, c: Optional[int] = None, out=None, stream=None):
+    x = _v(x)
+    n, h, w, _ = x.shape
+    c = x.channels if c is None else c
+    o = _out(out, x, n, h, w, c)
+    _run("unary", _lib().fhc_unary(_ref(x), _ref(o), n, h, w, c, op, a, b, _stream_handle(stream)))
+    return o.t
+
+
+def chcopy(x, c: Optional[int] = None, out=None, stream=None):
+    x = _v(x)
+    n, h, w, _ = x.shape
+    c = x.channels if c is None else c
+    o = _out(out, x, n, h, w, c)
+    _run("chcopy", _lib().fhc_chcopy(_ref(x), _ref(o), n, h, w, c, _stream_handle(stream)))
     return o.t

@@ -1,0 +1,312 @@
+"""One FlyHighFG pair() and mid() end to end: every op of models/graph.json from the network-size inputs A, B to the
+network's outputs (R_t, flow_tq, vis_tq, the streaming state), as the reference's planner walks it
+(crates/flyhigh-engine/src/net/build.rs:186-450), over a backend.
+
+The program is written once (``FlyHighFG.pair`` / ``mid``) against a small backend interface: ``GpuBackend`` runs it
+through libfhconv.so (conv plans and fused pairs of fhc_conv.h, the ops of fhc_ops.h) on a HIP stream, so it can be
+captured in a HIP graph; a checker can run the same program over the CPU oracle with the same weights. Tensors are
+NHWC f16 buffers (n, h, w, cstride) with the channel stride padded to 8 where a conv or an 8-byte path reads them;
+the graph's slices and scales are views (``V``) and its concats are buffers the producers write into by slice, so
+only a scaled input of a concat costs a copy (as the reference's chcopy does). The A and B branches share weights
+and run as a batch of 2 where their consumers read one tensor (resize, the first encoder pair, the first pool);
+render_pix (the full-resolution output) is not part of the network and not run here.
+
+Differences of launch structure from the reference (same arithmetic): the encoders' second pair and the second pool
+run per image so that their outputs land in their slices of the 279-channel concat; consecutive convs whose
+intermediate has no other reader run as fused pairs on the GPU when asked.
+"""
+from __future__ import annotations
+
+import os
+from typing import Dict, Optional
+
+import numpy as np
+
+# The graph's convs (models/flyhighfg.json shapes): name -> (cin, cout, stride, act). act 1: the graph's "conv"
+# (PReLU with its own slope); 0: "conv2d" and the convex-upsample conv up.w (no activation, net/build.rs:210-220, :381)
+CONVS = {
+    "enc.e1": (3, 36, 2, 1), "enc.e2": (36, 36, 1, 1), "enc.e3": (36, 72, 2, 1), "enc.e4": (72, 72, 1, 1),
+    "coarse.c1": (279, 96, 1, 1), "coarse.c2": (96, 96, 1, 1), "coarse.c3": (96, 96, 1, 1),
+    "coarse.c4": (96, 96, 1, 1), "coarse.head": (96, 12, 1, 0),
+    "fine.r1": (155, 48, 1, 1), "fine.r2": (48, 48, 1, 1), "fine.r3": (48, 48, 1, 1), "fine.out": (48, 7, 1, 0),
+    "film.h1": (48, 48, 1, 1), "film.h2": (48, 48, 1, 1), "film.out": (48, 5, 1, 0), "up.w": (48, 36, 1, 0),
+    "refine.q1": (14, 24, 1, 1), "refine.q2": (24, 24, 1, 1), "refine.q3": (24, 24, 1, 1), "refine.q4": (24, 3, 1, 0),
+}
+FILM_HIDDEN, FILM_OUT = 64, 96  # film.film.0: [64, 1]; film.film.2: [96, 64] (models/flyhighfg.json:385-414)
+
+
+def f16_bits(a):
+    return np.ascontiguousarray(np.asarray(a, np.float64).astype(np.float16).view(np.uint16))
+
+
+def make_weights(seed: int = 0) -> dict:
+    """Random weights of the graph's architecture (there is no network access for the trained ones): He-normal
+    convs, small biases, PReLU slopes in [0.05, 0.3], an f16-representable FiLM MLP. Returns name -> (w OIHW, bias,
+    slope or None) as f16 bits, and "film" -> (w1, b1, w2, b2) as f32 (the reference decodes its f16 weights to
+    f32 for the MLP, model/blob.rs:32-41)."""
+    rng = np.random.default_rng(seed)
+    W = {}
+    for name, (cin, cout, _, act) in CONVS.items():
+        w = f16_bits(rng.normal(0, np.sqrt(2.0 / (9 * cin)), (cout, cin, 3, 3)))
+        b = f16_bits(rng.normal(0, 0.01, cout))
+        s = f16_bits(rng.uniform(0.05, 0.3, cout)) if act == 1 else None
+        W[name] = (w, b, s)
+    q = lambda a: np.asarray(a, np.float64).astype(np.float16).astype(np.float32)  # noqa: E731
+    W["film"] = (q(rng.normal(0, 1, FILM_HIDDEN)), q(rng.normal(0, 0.1, FILM_HIDDEN)),
+                 q(rng.normal(0, 0.1, (FILM_OUT, FILM_HIDDEN))), q(rng.normal(0, 0.01, FILM_OUT)))
+    return W
+
+
+def film_mlp(W: dict, t: float) -> np.ndarray:
+    """The FiLM vector g(t) on the host, f16 bits [96]: g[o] = b2[o] + sum_i w2[o][i] relu(w1[i] t + b1[i]), f32,
+    the sum in index order (net/build.rs:331-340); stored as f16 (:345-355)."""
+    w1, b1, w2, b2 = W["film"]
+    t = np.float32(t)
+    hv = np.maximum(w1 * t + b1, np.float32(0))
+    g = np.empty(FILM_OUT, np.float32)
+    for o in range(FILM_OUT):
+        acc = np.float32(0)
+        for i in range(FILM_HIDDEN):
+            acc = np.float32(acc + w2[o, i] * hv[i])
+        g[o] = np.float32(b2[o] + acc)
+    return f16_bits(g)
+
+
+class V:
+    """A view: channels c0.. of a backend buffer (n, h, w, cstride), read times `scale`."""
+    __slots__ = ("buf", "c0", "scale")
+
+    def __init__(self, buf, c0: int = 0, scale: float = 1.0):
+        self.buf, self.c0, self.scale = buf, c0, scale
+
+
+def pad8(c):
+    return (c + 7) // 8 * 8
+
+
+# Consecutive convs whose intermediate has no other reader: (first, second, second's residual is the first's output)
+PAIRS = {("enc.e1", "enc.e2"): True, ("enc.e3", "enc.e4"): True, ("fine.r2", "fine.r3"): False,
+         ("film.h1", "film.h2"): False, ("refine.q1", "refine.q2"): False, ("refine.q3", "refine.q4"): False}
+
+
+class GpuBackend:
+    """The program's ops on the GPU through libfhconv.so, on one stream. Plans are made on first use (the first
+    run of the program; a captured replay then finds them all)."""
+
+    def __init__(self, W, stream=None, fuse: bool = True, device: str = "cuda"):
+        import torch
+        import fhconv
+        import fhops
+        self.torch, self.fhconv, self.fh = torch, fhconv, fhops
+        self.W, self.stream, self.fuse, self.dev = W, stream, fuse, device
+        self.plans: Dict[tuple, object] = {}
+        self.g = None
+
+    def zeros(self, n, h, w, cs):
+        return self.torch.zeros((n, h, w, cs), dtype=self.torch.int16, device=self.dev)
+
+    def image(self, buf, i):
+        return buf[i:i + 1]
+
+    def upload(self, a):
+        return self.torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(self.dev)
+
+    def host(self, buf):
+        self.torch.cuda.synchronize()
+        return buf.cpu().numpy().view(np.uint16)
+
+    def set_g(self, g_bits):
+        if self.g is None:
+            self.g = self.upload(g_bits)
+        else:
+            self.g.copy_(self.torch.from_numpy(np.ascontiguousarray(g_bits).view(np.int16)))
+
+    def _v(self, v: V):
+        return self.fh.View(v.buf, v.c0, v.scale)
+
+    def _desc(self, name, x: V, y: V, res: Optional[V], mid_res=False):
+        cin, cout, stride, act = CONVS[name]
+        n, h, w, xcs = x.buf.shape
+        ycs = y.buf.shape[3]
+        return self.fhconv.make_desc(n, h, w, cin, cout, stride=stride, act=act, residual=res is not None or mid_res,
+                                     x_cstride=xcs, x_c0=x.c0, y_cstride=ycs, y_c0=y.c0,
+                                     r_cstride=res.buf.shape[3] if res is not None else (ycs if mid_res else 0),
+                                     r_c0=res.c0 if res is not None else 0)
+
+    def conv(self, name, x: V, y: V, res: Optional[V] = None):
+        key = ("conv", name, x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0, None if res is None else res.buf.data_ptr())
+        p = self.plans.get(key)
+        if p is None:
+            w, b, s = self.W[name]
+            p = self.plans[key] = self.fhconv.ConvPlan(self._desc(name, x, y, res), w, b, s)
+            if p.workspace_bytes:
+                raise RuntimeError(f"{name}: a split-K plan needs a workspace; give the frame convs a table entry")
+        p.run(x.buf, y.buf, None if res is None else res.buf, stream=self.stream)
+
+    def pair(self, a, b, x: V, mid: V, y: V, res_mid: bool):
+        if not self.fuse:
+            self.conv(a, x, mid)
+            self.conv(b, mid, y, mid if res_mid else None)
+            return
+        key = ("pair", a, b, x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0)
+        p = self.plans.get(key)
+        if p is None:
+            da = self._desc(a, x, mid, None)
+            db = self._desc(b, mid, y, None, mid_res=res_mid)
+            (wa, ba, sa), (wb, bb, sb) = self.W[a], self.W[b]
+            try:
+                p = self.fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid)
+            except self.fhconv.FhcError:
+                p = False  # no fused kernel for these channels: two launches
+            self.plans[key] = p
+        if p is False:
+            self.conv(a, x, mid)
+            self.conv(b, mid, y, mid if res_mid else None)
+        else:
+            p.run(x.buf, y.buf, None, stream=self.stream)
+
+    def interp(self, x: V, c, out: V, oh, ow, aa):
+        self.fh.interp(self._v(x), oh, ow, aa, c, out=self._v(out), stream=self.stream)
+
+    def avgpool(self, x: V, c, out: V, k):
+        self.fh.avgpool(self._v(x), k, c, out=self._v(out), stream=self.stream)
+
+    def luma(self, x: V, out: V, grad=False):
+        self.fh.luma(self._v(x), grad, out=self._v(out), stream=self.stream)
+
+    def sad(self, la: V, lb: V, out: V, r):
+        self.fh.sad(self._v(la), self._v(lb), r, out=self._v(out), stream=self.stream)
+
+    def warp(self, img: V, c, flow: V, out: V):
+        self.fh.warp(self._v(img), self._v(flow), c, out=self._v(out), stream=self.stream)
+
+    def chcopy(self, x: V, c, out: V):
+        self.fh.chcopy(self._v(x), c, out=self._v(out), stream=self.stream)
+
+    def binary(self, a: V, b: V, c, out: V, op=0):
+        self.fh.binary(self._v(a), self._v(b), op, c, out=self._v(out), stream=self.stream)
+
+    def unary(self, x: V, c, out: V, op, a=0.0):
+        self.fh.unary(self._v(x), op, a, 0.0, c, out=self._v(out), stream=self.stream)
+
+    def film(self, hv: V, c, out: V):
+        self.fh.film(self._v(hv), self.g, c, out=self._v(out), stream=self.stream)
+
+    def convex(self, wt: V, x: V, c, out: V):
+        self.fh.convex(self._v(wt), self._v(x), c, out=self._v(out), stream=self.stream)
+
+    def blendmix(self, wa: V, wb: V, vis: V, out: V):
+        self.fh.blendmix(self._v(wa), self._v(wb), self._v(vis), out=self._v(out), stream=self.stream)
+
+
+class FlyHighFG:
+    """The buffers of one frame pair at network size net_w x net_h and the program of pair() and mid(t) over them.
+    Outputs after mid(): ``up7`` (flow_tq channels 0-3, vis_tq 4-6, quarter size), ``Rt`` (R_t, 3 channels),
+    ``state_out`` (f16b then flow16, 1/16 size); ``o`` holds the coarse head (conf, gate, sal in channels 7-11)."""
+
+    def __init__(self, be, net_w: int = 864, net_h: int = 480):
+        self.be = be
+        qh, qw = net_h // 4, net_w // 4
+        e8h, e8w = (qh - 1) // 2 + 1, (qw - 1) // 2 + 1
+        e16h, e16w = (e8h - 1) // 2 + 1, (e8w - 1) // 2 + 1
+        self.shape = dict(net=(net_h, net_w), q=(qh, qw), e8=(e8h, e8w), e16=(e16h, e16w))
+        Z = be.zeros
+        self.AB = Z(2, net_h, net_w, 8)        # the inputs A, B at network size (BGR in [0, 1])
+        self.aq = Z(2, qh, qw, 8)              # aq, bq
+        self.e1 = Z(2, e8h, e8w, 40)           # a_e1, b_e1
+        self.f8 = Z(2, e8h, e8w, 40)           # f8a, f8b
+        self.e3 = [Z(1, e16h, e16w, 72) for _ in range(2)]
+        self.i8 = Z(2, e8h, e8w, 8)            # i8a, i8b
+        self.cin = Z(1, e16h, e16w, 280)       # f16a 0 | f16b 72 | img16 144 | side 150 | state 154 | cv 230
+        self.la, self.lb = Z(1, e16h, e16w, 1), Z(1, e16h, e16w, 1)
+        self.ch1, self.ch2, self.ch3r, self.hc = (Z(1, e16h, e16w, 96) for _ in range(4))
+        self.o = Z(1, e16h, e16w, 16)          # coarse head: flow 0-3, vis 4-6, conf, gate, sal
+        self.flow, self.vis = Z(1, e8h, e8w, 8), Z(1, e8h, e8w, 8)
+        self.state_out = Z(1, e16h, e16w, 80)  # f16b 0 | flow16 72
+        self.fx = Z(1, e8h, e8w, 160)          # wa 0 | wb 36 | ia 72 | ib 75 | flow8 78 | h 82 | fcv 130
+        self.la8, self.lb8 = Z(1, e8h, e8w, 1), Z(1, e8h, e8w, 1)
+        self.fr1, self.fr2, self.h = (Z(1, e8h, e8w, 48) for _ in range(3))
+        self.d = Z(1, e8h, e8w, 8)             # fine.out: flow delta 0-3, vis delta 4-6
+        self.lin = Z(1, e8h, e8w, 8)           # linf | linb
+        self.hm, self.fh1, self.fh2 = (Z(1, e8h, e8w, 48) for _ in range(3))
+        self.dfilm = Z(1, e8h, e8w, 8)         # d_flow 0-3, d_mask 4
+        self.dvis = Z(1, e8h, e8w, 8)          # d_mask | -d_mask | 0
+        self.ftvt = Z(1, e8h, e8w, 8)          # flow_t 0-3 | vis_t 4-6
+        self.wt36 = Z(1, e8h, e8w, 40)
+        self.up7 = Z(1, qh, qw, 8)             # flow_tq 0-3 | vis_tq 4-6
+        self.blend = Z(1, qh, qw, 8)
+        self.rx = Z(1, qh, qw, 16)             # rwa 0 | rwb 3 | vis_tq 6 | flow_tq20 9 | lg 13
+        self.rq1, self.rq2, self.rq3 = (Z(1, qh, qw, 24) for _ in range(3))
+        self.rr, self.Rt = Z(1, qh, qw, 8), Z(1, qh, qw, 8)
+
+    def pair(self):
+        """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1)."""
+        be, S = self.be, self.shape
+        (qh, qw), (e8h, e8w) = S["q"], S["e8"]
+        img = be.image
+        be.interp(V(self.AB), 3, V(self.aq), qh, qw, True)                                   # 0, 1
+        be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)               # 2-4, 8-10
+        for i in range(2):                                                                    # 5-7, 11-13
+            be.pair("enc.e3", "enc.e4", V(img(self.f8, i)), V(self.e3[i]), V(self.cin, 72 * i), True)
+        be.avgpool(V(self.aq), 3, V(self.i8), 2)                                              # 14, 15
+        for i in range(2):                                                                    # 16-18
+            be.avgpool(V(img(self.i8, i)), 3, V(self.cin, 144 + 3 * i), 2)
+        be.luma(V(self.cin, 144), V(self.la))                                                 # 21-24 (side, state:
+        be.luma(V(self.cin, 147), V(self.lb))                                                 # zeros, 19-20)
+        be.sad(V(self.la), V(self.lb), V(self.cin, 230), 3)                                   # 25, 26
+        be.conv("coarse.c1", V(self.cin), V(self.ch1))                                        # 27
+        be.conv("coarse.c2", V(self.ch1), V(self.ch2))                                        # 28
+        be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30
+        be.conv("coarse.c4", V(self.ch3r), V(self.hc))                                        # 31
+        be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
+        be.interp(V(self.o, 0, 16.0), 4, V(self.flow), e8h, e8w, False)                       # 33-34, 39
+        be.interp(V(self.o, 4), 3, V(self.vis), e8h, e8w, False)                              # 35, 40
+        # the fine loop, K = 1 (op 42): h enters as zeros (op 41: the fx slice is never written)
+        be.warp(V(img(self.f8, 0)), 36, V(self.flow, 0, 0.125), V(self.fx, 0))                # wa
+        be.warp(V(img(self.f8, 1)), 36, V(self.flow, 2, 0.125), V(self.fx, 36))               # wb
+        be.warp(V(img(self.i8, 0)), 3, V(self.flow, 0, 0.125), V(self.fx, 72))                # ia
+        be.warp(V(img(self.i8, 1)), 3, V(self.flow, 2, 0.125), V(self.fx, 75))                # ib
+        be.luma(V(self.fx, 72), V(self.la8))                                                  # fla
+        be.luma(V(self.fx, 75), V(self.lb8))                                                  # flb
+        be.sad(V(self.la8), V(self.lb8), V(self.fx, 130), 2)                                  # fcv
+        be.chcopy(V(self.flow, 0, 0.125), 4, V(self.fx, 78))                                  # flow8 into fx
+        be.conv("fine.r1", V(self.fx), V(self.fr1))
+        be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
+        be.conv("fine.out", V(self.h), V(self.d))
+        be.binary(V(self.flow), V(self.d, 0), 4, V(self.flow))                                # flow += d[0:4]
+        be.binary(V(self.vis), V(self.d, 4), 3, V(self.vis))                                  # vis += d[4:7]
+        be.chcopy(V(self.cin, 72), 72, V(self.state_out, 0))                                  # 43: state_out
+        be.chcopy(V(self.o, 0, 16.0), 4, V(self.state_out, 72))
+
+    def mid(self, t: float, W: Optional[dict]):
+        """mid(t): models/graph.json ops 44-81 (render_pix, op 82, excluded). With W None the FiLM vector of t must
+        already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes it that way, as the
+        reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22)."""
+        be, (qh, qw) = self.be, self.shape["q"]
+        img = be.image
+        be.unary(V(self.flow, 0), 2, V(self.lin, 0), 0, 2.0 * t)                              # 44, 46: linf
+        be.unary(V(self.flow, 2), 2, V(self.lin, 2), 0, 2.0 * (1.0 - t))                      # 45, 47: linb
+        if W is not None:
+            be.set_g(film_mlp(W, t))                                                          # 49
+        be.film(V(self.h), 48, V(self.hm))                                                    # 50
+        be.pair("film.h1", "film.h2", V(self.hm), V(self.fh1), V(self.fh2), False)            # 51, 52
+        be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
+        be.binary(V(self.lin), V(self.dfilm, 0), 4, V(self.ftvt, 0))                          # 56: flow_t
+        be.chcopy(V(self.dfilm, 4), 1, V(self.dvis, 0))                                       # 57-59: dvis
+        be.chcopy(V(self.dfilm, 4, -1.0), 1, V(self.dvis, 1))
+        be.binary(V(self.vis), V(self.dvis), 3, V(self.ftvt, 4))                              # 60: vis_t
+        be.conv("up.w", V(self.h), V(self.wt36))                                              # 62
+        be.convex(V(self.wt36), V(self.ftvt), 7, V(self.up7))
+        be.warp(V(img(self.aq, 0)), 3, V(self.up7, 0, 0.25), V(self.rx, 0))                   # 65-68: rwa
+        be.warp(V(img(self.aq, 1)), 3, V(self.up7, 2, 0.25), V(self.rx, 3))                   # 69: rwb
+        be.blendmix(V(self.rx, 0), V(self.rx, 3), V(self.up7, 4), V(self.blend))              # 70-73
+        be.luma(V(self.blend), V(self.rx, 13), grad=True)                                     # 75: lg
+        be.chcopy(V(self.up7, 4), 3, V(self.rx, 6))                                           # 76: vis_tq
+        be.chcopy(V(self.up7, 0, 0.05), 4, V(self.rx, 9))                                     # 74, 76: flow_tq20
+        be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
+        be.pair("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), False)        # 79, 80
+        be.unary(V(self.rr), 3, V(self.Rt), 2)                                                # 81: affine_out
+
+
+def cpu_threads():
+    return max(1, min(16, len(os.sched_getaffinity(0))))

@@ -86,6 +86,24 @@ int fhc_avgpool(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t
 int fhc_interpolate(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t c, uint32_t ih, uint32_t iw,
                     uint32_t oh, uint32_t ow, int antialias, void* stream);
 
+/* Elementwise binary: op 0 out = a * sa + b * sb, op 1 out = (a * sa) * (b * sb), sa and sb the views' scales;
+ * cb (b's channels) is c, or 1 to broadcast b's one channel. Replaces Gpu::binary (ops/elementwise.rs:8-27,
+ * shaders/binary.wgsl:9-17), the "add" and "mul" arms (net/build.rs:310-311). */
+int fhc_binary(const fhc_tensor* a, const fhc_tensor* b, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w,
+               uint32_t c, uint32_t cb, int op, void* stream);
+
+/* Elementwise unary of v = x * scale: op 0 v * a, 1 clamp(v, a, b), 2 2 / (1 + exp(-v)) - 1, 3 -v. Replaces
+ * Gpu::unary (shaders/unary.wgsl:9-20): the "mul_t" arm (op 0 with a = 2t or 2(1 - t), net/build.rs:290-308),
+ * "affine_out" (op 2) and "clamp" (op 1). */
+int fhc_unary(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c, int op,
+              float a, float b, void* stream);
+
+/* Channel copy of a view into an output view (a concat slice): the bits at scale 1, else f16(x * scale). One input
+ * of the reference's concat (Gpu::concat, ops/elementwise.rs:65-77, shaders/chcopy.wgsl:19-36); the graph's other
+ * concat inputs need no copy here, since their producers write into the slice. */
+int fhc_chcopy(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -233,3 +233,45 @@ void fho_interp(const fho_view* x, const fho_view* out, uint32_t n, uint32_t c, 
                     wr(out, oh, ow, b, oy, ox, ch, val * x->scale);
                 }
 }
+
+/* shaders/binary.wgsl:11-16 */
+void fho_binary(const fho_view* a, const fho_view* b, const fho_view* out, uint32_t n, uint32_t h, uint32_t w,
+                uint32_t c, uint32_t cb, int op) {
+    for (uint32_t i = 0; i < n; i++)
+        for (uint32_t y = 0; y < h; y++)
+            for (uint32_t x = 0; x < w; x++)
+                for (uint32_t ch = 0; ch < c; ch++) {
+                    const float av = rd(a, h, w, i, (int)y, (int)x, ch) * a->scale;
+                    const float bv = rd(b, h, w, i, (int)y, (int)x, cb == 1 ? 0 : ch) * b->scale;
+                    wr(out, h, w, i, y, x, ch, op == 1 ? av * bv : av + bv);
+                }
+}
+
+/* shaders/unary.wgsl:11-19 */
+void fho_unary(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c, int op,
+               float a, float b) {
+    for (uint32_t i = 0; i < n; i++)
+        for (uint32_t y = 0; y < h; y++)
+            for (uint32_t xx = 0; xx < w; xx++)
+                for (uint32_t ch = 0; ch < c; ch++) {
+                    const float v = rd(x, h, w, i, (int)y, (int)xx, ch) * x->scale;
+                    float r;
+                    if (op == 0) r = v * a;
+                    else if (op == 1) r = fminf(fmaxf(v, a), b);
+                    else if (op == 2) r = 2.0f / (1.0f + expf(-v)) - 1.0f;
+                    else r = -v;
+                    wr(out, h, w, i, y, xx, ch, r);
+                }
+}
+
+/* shaders/chcopy.wgsl:19-22 (scl) for one input */
+void fho_chcopy(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c) {
+    const uint16_t* src = (const uint16_t*)x->p;
+    uint16_t* dst = (uint16_t*)out->p;
+    for (size_t pix = 0; pix < (size_t)n * h * w; pix++)
+        for (uint32_t ch = 0; ch < c; ch++) {
+            const uint16_t v = src[pix * x->cs + x->c0 + ch];
+            dst[pix * out->cs + out->c0 + ch] =
+                x->scale == 1.0f ? v : fho_f32_to_f16(fho_f16_to_f32(v) * x->scale);
+        }
+}

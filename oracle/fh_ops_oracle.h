@@ -52,6 +52,18 @@ void fho_avgpool(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h,
 void fho_interp(const fho_view* x, const fho_view* out, uint32_t n, uint32_t c, uint32_t ih, uint32_t iw,
                 uint32_t oh, uint32_t ow, int aa);
 
+/* elementwise binary: op 0 f16(a * sa + b * sb), op 1 f16((a * sa) * (b * sb)); cb == 1 broadcasts b's single
+ * channel: shaders/binary.wgsl:9-17 */
+void fho_binary(const fho_view* a, const fho_view* b, const fho_view* out, uint32_t n, uint32_t h, uint32_t w,
+                uint32_t c, uint32_t cb, int op);
+/* elementwise unary of v = x * scale: op 0 v * a, 1 clamp(v, a, b), 2 2 / (1 + exp(-v)) - 1 (affine_out), 3 -v:
+ * shaders/unary.wgsl:9-20 */
+void fho_unary(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c, int op,
+               float a, float b);
+/* channel copy of a view into an output view, f16(x * scale) unless the scale is 1 (then the bits are copied):
+ * one input of shaders/chcopy.wgsl:19-36 */
+void fho_chcopy(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c);
+
 #ifdef __cplusplus
 }
 #endif

@@ -146,6 +146,9 @@ def _ops_lib():
             "fho_blendmix": [V, V, V, V, U, U, U],
             "fho_avgpool": [V, V, U, U, U, U, U],
             "fho_interp": [V, V, U, U, U, U, U, U, I],
+            "fho_binary": [V, V, V, U, U, U, U, U, I],
+            "fho_unary": [V, V, U, U, U, U, I, ctypes.c_float, ctypes.c_float],
+            "fho_chcopy": [V, V, U, U, U, U],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -222,4 +225,27 @@ def interp(x, c, oh, ow, aa=False, c0=0, scale=1.0):
     n, ih, iw, _ = x.shape
     y = _out(n, oh, ow, c)
     _ops_lib().fho_interp(_view(x, c0, scale), _view(y), n, c, ih, iw, oh, ow, int(aa))
+    return y
+
+
+def binary(a, b, c, op=0, a_c0=0, a_scale=1.0, b_c0=0, b_scale=1.0, cb=None):
+    """cb: b's channel count (1 broadcasts)."""
+    n, h, w, _ = a.shape
+    y = _out(n, h, w, c)
+    _ops_lib().fho_binary(_view(a, a_c0, a_scale), _view(b, b_c0, b_scale), _view(y), n, h, w, c,
+                          c if cb is None else cb, op)
+    return y
+
+
+def unary(x, c, op, a=0.0, b=0.0, c0=0, scale=1.0):
+    n, h, w, _ = x.shape
+    y = _out(n, h, w, c)
+    _ops_lib().fho_unary(_view(x, c0, scale), _view(y), n, h, w, c, op, a, b)
+    return y
+
+
+def chcopy(x, c, c0=0, scale=1.0):
+    n, h, w, _ = x.shape
+    y = _out(n, h, w, c)
+    _ops_lib().fho_chcopy(_view(x, c0, scale), _view(y), n, h, w, c)
     return y

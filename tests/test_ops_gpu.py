@@ -192,6 +192,45 @@ def test_interpolate_matches_oracle(case):
     exact(got, want, f"interp {case}")
 
 
+@pytest.mark.parametrize("c,cs_a,a0,cb,op,sa,sb", [(4, 4, 0, 4, 0, 1.0, 1.0), (3, 7, 4, 3, 0, 0.125, -1.0),
+                                                   (3, 3, 0, 1, 1, 1.0, 2.0), (8, 12, 4, 1, 0, 2.0, 0.5)])
+def test_binary_matches_oracle(c, cs_a, a0, cb, op, sa, sb):
+    say("binary", c, cs_a, a0, cb, op, sa, sb)
+    fh = fhops()
+    rng = np.random.default_rng(c * 10 + cb + op)
+    n, h, w = 2, 60, 108
+    a, b = rand(rng, (n, h, w, cs_a), -3, 3), rand(rng, (n, h, w, cb + 1), -3, 3)
+    want = oracle.binary(a, b, c, op=op, a_c0=a0, a_scale=sa, b_c0=1, b_scale=sb, cb=cb)
+    got = host(fh.binary(fh.View(dev(a), a0, sa), fh.View(dev(b), 1, sb) if cb == 1 else
+                         fh.View(dev(b)[..., :cb + 1].contiguous(), 1, sb), op, c))
+    exact(got, want, "binary")
+
+
+@pytest.mark.parametrize("op,a,b", [(0, 1.0, 0.0), (1, -0.5, 0.75), (2, 0.0, 0.0), (3, 0.0, 0.0)])
+def test_unary_matches_oracle(op, a, b):
+    say("unary", op, a, b)
+    fh = fhops()
+    rng = np.random.default_rng(op)
+    x = rand(rng, (1, 120, 216, 5), -5, 5)
+    want = oracle.unary(x, 3, op, a=a, b=b, c0=2, scale=0.5)
+    got = host(fh.unary(fh.View(dev(x), 2, 0.5), op, a, b, 3))
+    (exact if op != 2 else within_ulp)(got, want, f"unary {op}")
+
+
+@pytest.mark.parametrize("c,c0,scale", [(4, 0, 0.125), (3, 4, 1.0), (72, 0, 1.0)])
+def test_chcopy_into_a_concat_slice_matches_oracle(c, c0, scale):
+    say("chcopy", c, c0, scale)
+    fh = fhops()
+    rng = np.random.default_rng(c)
+    n, h, w = 1, 30, 54
+    x = rand(rng, (n, h, w, c0 + c + 1), -8, 8)
+    want = oracle.chcopy(x, c, c0=c0, scale=scale)
+    buf = sliced_out(n, h, w, c + 10, 5)
+    out = dev(buf)
+    fh.chcopy(fh.View(dev(x), c0, scale), c, out=fh.View(out, 5))
+    check_slice(buf, out, 5, c, want, "chcopy")
+
+
 def test_empty_inputs_are_no_ops_and_bad_views_are_errors():
     import torch
     fh = fhops()

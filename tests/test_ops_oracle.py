@@ -230,3 +230,36 @@ def test_interp_same_size_is_a_copy_and_scale_applies():
     assert np.array_equal(oracle.interp(x, 4, 7, 9), x)
     assert np.array_equal(oracle.interp(x, 2, 7, 9, aa=True, c0=1), x[..., 1:3])  # triangle of width 1 at scale 1
     assert np.array_equal(val(oracle.interp(x, 4, 7, 9, scale=0.5)), val(x) * 0.5)
+
+
+# ---- elementwise: binary, unary, chcopy (shaders/binary.wgsl, unary.wgsl, chcopy.wgsl) ----------------------------
+# The f32 operation of each element is one IEEE operation (or two) followed by one RTNE rounding, which numpy's
+# float32 arithmetic and float16 conversion perform identically: these are exact checks.
+
+def test_binary_add_mul_and_broadcast_match_numpy_float32():
+    a, b = f16(rng.uniform(-4, 4, (2, 5, 7, 6))), f16(rng.uniform(-4, 4, (2, 5, 7, 3)))
+    A, B = val(a)[..., 1:5], val(b)[..., 2:3]
+    got = oracle.binary(a, b, 4, op=0, a_c0=1, a_scale=0.5, b_c0=2, b_scale=-2.0, cb=1)
+    want = (A * np.float32(0.5) + B * np.float32(-2.0)).astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    got = oracle.binary(a, b, 3, op=1, b_c0=0)
+    want = (val(a)[..., :3] * val(b)[..., :3]).astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_unary_ops_match_their_closed_forms():
+    x = f16(rng.uniform(-6, 6, (1, 4, 9, 3)))
+    v = val(x) * np.float32(2.0)
+    assert np.array_equal(oracle.unary(x, 3, 0, a=0.25, scale=2.0), (v * np.float32(0.25)).astype(np.float16).view(np.uint16))
+    assert np.array_equal(oracle.unary(x, 3, 1, a=-1.0, b=1.5, scale=2.0), np.clip(v, -1, 1.5).astype(np.float16).view(np.uint16))
+    assert np.array_equal(oracle.unary(x, 3, 3, scale=2.0), (-v).astype(np.float16).view(np.uint16))
+    aff = val(oracle.unary(x, 3, 2))
+    assert np.allclose(aff, np.tanh(val(x) / 2), atol=1e-3)  # 2 sigmoid(v) - 1 = tanh(v / 2)
+    assert np.all(np.abs(aff) <= 1)
+
+
+def test_chcopy_copies_bits_at_scale_one_and_rounds_scaled_values():
+    x = np.ascontiguousarray(rng.integers(0, 0x7C00, (1, 3, 4, 6)).astype(np.uint16))  # finite f16 patterns
+    assert np.array_equal(oracle.chcopy(x, 4, c0=2), x[..., 2:])
+    got = oracle.chcopy(x, 3, c0=1, scale=0.125)
+    assert np.array_equal(got, (val(x)[..., 1:4] * np.float32(0.125)).astype(np.float16).view(np.uint16))
