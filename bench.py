@@ -269,6 +269,53 @@ def net_ops_report(args, torch, flyhighfg, stream, net_w, net_h):
                 batched_workload="8 frame pairs (A/B ops over 16 frames) and 24 mid() phases at network 864x480")
 
 
+def network_frame(args, torch, np, stream, net_w, net_h, t=0.5):
+    """The whole network of one frame: every op of pair() and mid(t) (flyhighfg_net: the 25 convs and up.w, fused
+    pairs, the network ops, render_pix excluded) captured as one HIP graph on `stream`; per-frame time over
+    args.steps replays (after args.warmup) between events on that stream. Random weights of the architecture
+    (seed 7), a synthetic picture and the same picture moved 12 pixels as A and B."""
+    import flyhighfg_net as fnet
+    W = fnet.make_weights(7)
+    be = fnet.GpuBackend(W, stream=stream, fuse=not args.no_fuse)
+    f = fnet.FlyHighFG(be, net_w, net_h)
+    yy, xx = np.mgrid[0:net_h, 0:net_w] / 16.0
+    base = 0.5 + 0.25 * np.sin(xx)[..., None] * np.cos(yy)[..., None] + 0.1 * np.sin(3.7 * xx + 1.3 * yy)[..., None]
+    ab = np.zeros((2, net_h, net_w, 8), np.float32)
+    ab[0, ..., :3], ab[1, ..., :3] = base, np.roll(base, 12, axis=1)
+    f.AB.copy_(be.upload(np.ascontiguousarray(ab.astype(np.float16)).view(np.uint16)))
+    be.set_g(fnet.film_mlp(W, t))
+    with torch.cuda.stream(stream):
+        for _ in range(2):  # plans are made on the first run
+            f.pair()
+            f.mid(t, None)
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            f.pair()
+            f.mid(t, None)
+        for _ in range(args.warmup):
+            g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            g.replay()
+        e1.record(stream)
+        e1.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / args.steps
+    outs = {k: be.host(getattr(f, k))[..., :c].view(np.float16) for k, c in (("Rt", 3), ("up7", 7))}
+    finite = all(bool(np.all(np.isfinite(v))) for v in outs.values())
+    fused = sum(1 for k, p in be.plans.items() if k[0] == "pair" and p is not False)
+    res = dict(us_per_frame=round(us, 3), frames_per_s=round(1e6 / us, 2), finite_outputs=finite,
+               conv_plans=sum(1 for k in be.plans if k[0] == "conv"), fused_pairs=fused,
+               workload=f"every op of one FlyHighFG pair() and mid(t={t}) at network {net_w}x{net_h} (1080p): the "
+                        "convs (fused pairs where the library has a kernel), resize, pools, luma, SAD volumes, warps, "
+                        "FiLM, convex upsample, blendmix, elementwise and concat copies, as one HIP graph; "
+                        "render_pix (the full-resolution output) excluded; random weights, synthetic frames")
+    del g, f, be
+    torch.cuda.empty_cache()
+    return res
+
+
 def batched_workload(args, torch, np, fhconv, flyhighfg, stream, pairs=8, mids=3):
     """The batched throughput configuration: the frame's convs over 8 independent frame pairs (3840x2160, network
     856x480) with 3 mid() phases each, one batched conv (or fused pair) per layer; step time, generated frames per
@@ -653,6 +700,10 @@ def main():
         torch.cuda.empty_cache()
 
     net_ops = None if args.no_ops else net_ops_report(args, torch, flyhighfg, stream, net_w, net_h)
+    netframe = None
+    if not args.no_ops:
+        netframe = network_frame(args, torch, np, stream, net_w, net_h)
+        log("bench: network frame", json.dumps(netframe))
 
     mfma_rate = mfma_rate_probe(torch, fhconv, stream)
     log(f"bench: sustained dense f16 MFMA rate {mfma_rate:.0f} TFLOP/s")
@@ -704,6 +755,7 @@ def main():
         config_pairs=cfg_pairs,
         batched=batched,
         net_ops=net_ops,
+        network_frame=netframe,
         tune_table=tune_table,
     )
     print(json.dumps(out), flush=True)

@@ -29,7 +29,15 @@ struct OView {
 };
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// f32 -> f16, RTNE (the default rounding mode), of the f32 value as rounded: the conversion is written as its
+// instruction, because the compiler otherwise contracts a product or sum feeding it into one mixed-precision FMA
+// (v_fma_mixlo_f16) that rounds the exact result once, where the reference rounds it to f32 and then to f16 (the two
+// differ next to f16 midpoints). A pure asm: the compiler may move or merge it, but cannot look inside it.
+__device__ __forceinline__ uint16_t f2h(float f) {
+    uint32_t r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(f));
+    return (uint16_t)r;
+}
 __device__ __forceinline__ float ld(const View& v, size_t pix, uint32_t ch) { return h2f(v.p[pix * v.cs + v.c0 + ch]); }
 __device__ __forceinline__ void st(const OView& v, size_t pix, uint32_t ch, float x) {
     v.p[pix * v.cs + v.c0 + ch] = f2h(x);
@@ -67,21 +75,18 @@ __device__ __forceinline__ void st4(const OView& v, size_t pix, uint32_t ch, uin
 }
 
 // ---- warp: shaders/warp.wgsl:14-28 ----------------------------------------------------------------------------
+// channels ch .. ch + 3 of image img0 / h of `img` (img0 = image * h) sampled at (x + fx, y + fy), bilinear with the
+// coordinates clamped, times the view's scale
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void warp_kernel(View img, View flow, OView out, uint32_t h, uint32_t w,
-                                                        uint32_t c, uint32_t groups, uint32_t items) {
-    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-    if (t >= items) return;
-    const uint32_t pix = t / groups, ch = (t - pix * groups) * 4;
-    const uint32_t x = pix % w, row = pix / w, y = row % h, img0 = row - y;  // img0 = image * h
-    const float fx = ld(flow, pix, 0) * flow.scale, fy = ld(flow, pix, 1) * flow.scale;
+__device__ __forceinline__ void warp4(const View& img, uint32_t img0, uint32_t x, uint32_t y, uint32_t h, uint32_t w,
+                                      float fx, float fy, uint32_t ch, uint32_t c, float (&o)[4]) {
     const float gx = (float)x + fx, gy = (float)y + fy;
     const int x0 = (int)floorf(gx), y0 = (int)floorf(gy);
     const float ax = gx - (float)x0, ay = gy - (float)y0;
     const int x0c = clampi(x0, 0, (int)w - 1), x1c = clampi(x0 + 1, 0, (int)w - 1);
     const int y0c = clampi(y0, 0, (int)h - 1), y1c = clampi(y0 + 1, 0, (int)h - 1);
     const size_t r0 = (size_t)(img0 + y0c) * w, r1 = (size_t)(img0 + y1c) * w;
-    float v00[4], v01[4], v10[4], v11[4], o[4];
+    float v00[4], v01[4], v10[4], v11[4];
     ld4<VEC>(img, r0 + x0c, ch, c, v00);
     ld4<VEC>(img, r0 + x1c, ch, c, v01);
     ld4<VEC>(img, r1 + x0c, ch, c, v10);
@@ -91,6 +96,17 @@ __global__ __launch_bounds__(kThreads) void warp_kernel(View img, View flow, OVi
         const float top = v00[i] * (1.0f - ax) + v01[i] * ax, bot = v10[i] * (1.0f - ax) + v11[i] * ax;
         o[i] = (top * (1.0f - ay) + bot * ay) * img.scale;
     }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void warp_kernel(View img, View flow, OView out, uint32_t h, uint32_t w,
+                                                        uint32_t c, uint32_t groups, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t pix = t / groups, ch = (t - pix * groups) * 4;
+    const uint32_t x = pix % w, row = pix / w, y = row % h, img0 = row - y;  // img0 = image * h
+    float o[4];
+    warp4<VEC>(img, img0, x, y, h, w, ld(flow, pix, 0) * flow.scale, ld(flow, pix, 1) * flow.scale, ch, c, o);
     st4<VEC>(out, pix, ch, c, o);
 }
 
@@ -510,8 +526,10 @@ __global__ __launch_bounds__(kThreads) void binary_kernel(View a, View b, OView 
     st4<VEC>(out, pix, ch, c, o);
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void unary_kernel(View x, OView out, uint32_t c, int op, float pa, float pb,
+// OP at compile time, one straight-line kernel per op (a run-time choice among the four, written as nested
+// conditionals, compiled to code that skipped the negation of op 3)
+template <bool VEC, int OP>
+__global__ __launch_bounds__(kThreads) void unary_kernel(View x, OView out, uint32_t c, float pa, float pb,
                                                          uint32_t groups, uint32_t items) {
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     if (t >= items) return;
@@ -521,7 +539,10 @@ __global__ __launch_bounds__(kThreads) void unary_kernel(View x, OView out, uint
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const float u = v[i] * x.scale;
-        o[i] = op == 0 ? u * pa : op == 1 ? fminf(fmaxf(u, pa), pb) : op == 2 ? 2.0f / (1.0f + expf(-u)) - 1.0f : -u;
+        if constexpr (OP == 0) o[i] = u * pa;
+        else if constexpr (OP == 1) o[i] = fminf(fmaxf(u, pa), pb);
+        else if constexpr (OP == 2) o[i] = 2.0f / (1.0f + expf(-u)) - 1.0f;
+        else o[i] = -u;
     }
     st4<VEC>(out, pix, ch, c, o);
 }
@@ -533,6 +554,164 @@ __global__ __launch_bounds__(kThreads) void chcopy_kernel(View x, OView out, uin
     const uint32_t pix = t / c, ch = t - pix * c;
     const uint16_t v = x.p[(size_t)pix * x.cs + x.c0 + ch];
     out.p[(size_t)pix * out.cs + out.c0 + ch] = x.scale == 1.0f ? v : f2h(h2f(v) * x.scale);
+}
+
+// ---- the graph's op chains, fused: each kernel computes what its ops compute one after another, with the same
+// f32 operations and the same f16 roundings at the tensors the ops store (bit for bit) ----------------------------------
+
+__device__ __forceinline__ float lum3(float b, float g, float r) { return 0.299f * r + 0.587f * g + 0.114f * b; }
+
+// The pictures' pyramid of pair() (graph.json ops 14-18, 21-24): avgpool k 2 of the A and B pictures q (batch 2,
+// 3 channels) to i8, again to the 1/4 pictures (written into channels 3 * image of i16, the img16 slice of the
+// coarse input) and their luma (channel image of l16). One lane per 2 x 2 block of i8 pixels of one picture; the
+// second pool reads the first's f16 values and the luma the second's, as the separate ops read stored tensors.
+__global__ __launch_bounds__(kThreads) void pair_pyramid_kernel(View q, OView i8, OView i16, OView l16, uint32_t h,
+                                                                uint32_t w, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t h8 = h / 2, w8 = w / 2, h16 = h8 / 2, w16 = w8 / 2, hb = (h8 + 1) / 2, wb = (w8 + 1) / 2;
+    const uint32_t x2 = t % wb, r = t / wb, y2 = r % hb, img = r / hb;
+    float v8[2][2][3];
+#pragma unroll
+    for (uint32_t dy = 0; dy < 2; dy++)
+#pragma unroll
+        for (uint32_t dx = 0; dx < 2; dx++) {
+            const uint32_t y8 = min(2 * y2 + dy, h8 - 1), x8 = min(2 * x2 + dx, w8 - 1);
+            float acc[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t ky = 0; ky < 2; ky++)
+#pragma unroll
+                for (uint32_t kx = 0; kx < 2; kx++) {
+                    const size_t p = ((size_t)img * h + 2 * y8 + ky) * w + 2 * x8 + kx;
+#pragma unroll
+                    for (uint32_t ch = 0; ch < 3; ch++) acc[ch] = acc[ch] + ld(q, p, ch);
+                }
+            const size_t p8 = ((size_t)img * h8 + y8) * w8 + x8;
+            const bool own = 2 * y2 + dy < h8 && 2 * x2 + dx < w8;
+#pragma unroll
+            for (uint32_t ch = 0; ch < 3; ch++) {
+                const uint16_t hv = f2h(acc[ch] / 4.0f);
+                v8[dy][dx][ch] = h2f(hv);
+                if (own) i8.p[p8 * i8.cs + i8.c0 + ch] = hv;
+            }
+        }
+    if (y2 >= h16 || x2 >= w16) return;
+    const size_t p16 = (size_t)y2 * w16 + x2;
+    float v16[3];
+#pragma unroll
+    for (uint32_t ch = 0; ch < 3; ch++) {
+        const float acc = ((0.0f + v8[0][0][ch]) + v8[0][1][ch]) + v8[1][0][ch] + v8[1][1][ch];
+        const uint16_t hv = f2h(acc / 4.0f);
+        v16[ch] = h2f(hv);
+        i16.p[p16 * i16.cs + i16.c0 + 3 * img + ch] = hv;
+    }
+    st(l16, p16, img, lum3(v16[0], v16[1], v16[2]));
+}
+
+// The fine block's input (graph.json op 42, its body up to the concat): both feature maps f8 (batch 2, c channels)
+// and both 1/2 pictures i8 (3 channels) warped by the flow (channels 0-1 for A, 2-3 for B, at the view's read scale:
+// the flow at 1/8), the warped pictures' luma (channel image of l8) and the scaled flow itself, written into their
+// slices of the block's input fx (c0: wa, +c: wb, +2c: ia, +2c+3: ib, +2c+6: flow8). One lane per (pixel, task):
+// tasks 0 .. 2G-1 warp 4 feature channels (G groups per map), 2G and 2G+1 a picture with its luma, 2G+2 the flow.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, View fl, OView fx, OView l8,
+                                                              uint32_t h, uint32_t w, uint32_t c, uint32_t groups,
+                                                              uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t tasks = 2 * groups + 3, pix = t / tasks, task = t - pix * tasks;
+    const uint32_t x = pix % w, y = pix / w;
+    if (task < 2 * groups + 2) {
+        const uint32_t img = task < 2 * groups ? task / groups : task - 2 * groups;
+        const float fxv = ld(fl, pix, 2 * img) * fl.scale, fyv = ld(fl, pix, 2 * img + 1) * fl.scale;
+        float o[4];
+        if (task < 2 * groups) {
+            const uint32_t ch = (task - img * groups) * 4;
+            warp4<VEC>(f8, img * h, x, y, h, w, fxv, fyv, ch, c, o);
+            OView dst{fx.p, fx.cs, fx.c0 + img * c};
+            st4<VEC>(dst, pix, ch, c, o);
+        } else {
+            warp4<false>(i8, img * h, x, y, h, w, fxv, fyv, 0, 3, o);
+            float r[3];
+#pragma unroll
+            for (uint32_t ch = 0; ch < 3; ch++) {
+                const uint16_t hv = f2h(o[ch]);
+                r[ch] = h2f(hv);
+                fx.p[(size_t)pix * fx.cs + fx.c0 + 2 * c + 3 * img + ch] = hv;
+            }
+            st(l8, pix, img, lum3(r[0], r[1], r[2]));
+        }
+    } else {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+            const uint16_t v = fl.p[(size_t)pix * fl.cs + fl.c0 + i];
+            fx.p[(size_t)pix * fx.cs + fx.c0 + 2 * c + 6 + i] = fl.scale == 1.0f ? v : f2h(h2f(v) * fl.scale);
+        }
+    }
+}
+
+// mid()'s flow_t and vis_t (graph.json ops 44-48, 54-60): lin = mul_t(flow) (2t on the forward flow, 2(1 - t) on
+// the backward one, stored f16), flow_t = lin + d_flow; dvis = (d_mask, -d_mask, 0) and vis_t = vis + dvis. fv
+// holds flow (channels 0-3) and vis (4-6), df the FiLM head's output (d_flow 0-3, d_mask 4), out flow_t | vis_t.
+__global__ __launch_bounds__(kThreads) void flow_vis_t_kernel(View fv, View df, OView out, float af, float ab,
+                                                              uint32_t items) {
+    const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
+    if (pix >= items) return;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+        const float lin = h2f(f2h(ld(fv, pix, i) * fv.scale * (i < 2 ? af : ab)));
+        st(out, pix, i, lin + ld(df, pix, i) * df.scale);
+    }
+    const uint16_t dm = df.p[(size_t)pix * df.cs + df.c0 + 4];
+    const float dv[3] = {h2f(dm), h2f(f2h(h2f(dm) * -1.0f)), 0.0f};
+#pragma unroll
+    for (uint32_t j = 0; j < 3; j++) st(out, pix, 4 + j, ld(fv, pix, 4 + j) * fv.scale + dv[j]);
+}
+
+// The refine head's input (graph.json ops 65-76): both 1/4 pictures q (batch 2, 3 channels) warped by the upsampled
+// flow (channels 0-1 A, 2-3 B, at the flow view's read scale), their blend by the upsampled visibility logits
+// (blendmix), and the blend's luma gradient, written as the concat rx: c0 rwa, +3 rwb, +6 vis_tq, +9 flow_tq * fs,
+// +13 the gradient. The gradient reads the blend at the right and lower neighbours: a lane recomputes those blends
+// (from the same warps and weights, so the same values) instead of a second launch.
+__device__ __forceinline__ void blend_at(const View& q, const View& fl, const View& vis, uint32_t x, uint32_t y,
+                                         uint32_t h, uint32_t w, float (&ra)[3], float (&rb)[3], float (&bl)[3]) {
+    const size_t pix = (size_t)y * w + x;
+    float oa[4], ob[4];
+    warp4<false>(q, 0, x, y, h, w, ld(fl, pix, 0) * fl.scale, ld(fl, pix, 1) * fl.scale, 0, 3, oa);
+    warp4<false>(q, h, x, y, h, w, ld(fl, pix, 2) * fl.scale, ld(fl, pix, 3) * fl.scale, 0, 3, ob);
+    float ea, eb, ec, s;
+    soft3(vis, pix, ea, eb, ec, s);
+    const float pa = h2f(f2h((ea + 0.5f * ec) / s)), pb = h2f(f2h((eb + 0.5f * ec) / s));
+#pragma unroll
+    for (uint32_t ch = 0; ch < 3; ch++) {
+        ra[ch] = h2f(f2h(oa[ch]));
+        rb[ch] = h2f(f2h(ob[ch]));
+        bl[ch] = h2f(f2h(h2f(f2h(ra[ch] * pa)) + h2f(f2h(rb[ch] * pb))));
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void refine_input_kernel(View q, View fl, View vis, OView rx, uint32_t h,
+                                                                uint32_t w, float fs, uint32_t items) {
+    const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
+    if (pix >= items) return;
+    const uint32_t x = pix % w, y = pix / w;
+    float ra[3], rb[3], bl[3], na[3], nb[3], br[3], bd[3];
+    blend_at(q, fl, vis, x, y, h, w, ra, rb, bl);
+    blend_at(q, fl, vis, min(x + 1, w - 1), y, h, w, na, nb, br);  // clamped: unused past the last column
+    blend_at(q, fl, vis, x, min(y + 1, h - 1), h, w, na, nb, bd);
+    uint16_t* o = rx.p + (size_t)pix * rx.cs + rx.c0;
+#pragma unroll
+    for (uint32_t ch = 0; ch < 3; ch++) {
+        o[ch] = f2h(ra[ch]);
+        o[3 + ch] = f2h(rb[ch]);
+        o[6 + ch] = vis.p[(size_t)pix * vis.cs + vis.c0 + ch];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) o[9 + i] = f2h(ld(fl, pix, i) * fs);
+    const float cl = lum3(bl[0], bl[1], bl[2]);
+    const float gx = x + 1 < w ? lum3(br[0], br[1], br[2]) - cl : 0.0f;
+    const float gy = y + 1 < h ? lum3(bd[0], bd[1], bd[2]) - cl : 0.0f;
+    o[13] = f2h(fabsf(gx) + fabsf(gy));
 }
 
 // ---- host side ----------------------------------------------------------------------------------------------------
@@ -794,9 +973,12 @@ extern "C" int fhc_unary(const fhc_tensor* x, const fhc_tensor* out, uint32_t n,
         const uint32_t groups = (c + 3) / 4;
         const bool v = vec4(c, {x, out});
         return launch("unary", (uint64_t)n * h * w * groups, [&](dim3 g, uint32_t items) {
-            auto k = v ? unary_kernel<true> : unary_kernel<false>;
-            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), c, op, a, b, groups,
-                               items);
+            using K = decltype(&unary_kernel<true, 0>);
+            static const K table[2][4] = {
+                {unary_kernel<false, 0>, unary_kernel<false, 1>, unary_kernel<false, 2>, unary_kernel<false, 3>},
+                {unary_kernel<true, 0>, unary_kernel<true, 1>, unary_kernel<true, 2>, unary_kernel<true, 3>}};
+            hipLaunchKernelGGL(table[v][op], g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), c, a, b,
+                               groups, items);
         });
     });
 }
@@ -810,6 +992,78 @@ extern "C" int fhc_chcopy(const fhc_tensor* x, const fhc_tensor* out, uint32_t n
         FHC_TRY(check(out, "chcopy out", c, false, true));
         return launch("chcopy", (uint64_t)n * h * w * c, [&](dim3 g, uint32_t items) {
             hipLaunchKernelGGL(chcopy_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), c, items);
+        });
+    });
+}
+
+extern "C" int fhc_pair_pyramid(const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16,
+                                const fhc_tensor* l16, uint32_t h, uint32_t w, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if (h < 4 || w < 4) return h == 0 || w == 0 ? 0 : fail(-1, "pair_pyramid: %u x %u is below 4 x 4", h, w);
+        FHC_TRY(check(q, "pair_pyramid q", 3, false));
+        FHC_TRY(check(i8, "pair_pyramid i8", 3, false, true));
+        FHC_TRY(check(i16, "pair_pyramid i16", 6, false, true));
+        FHC_TRY(check(l16, "pair_pyramid l16", 2, false, true));
+        const uint64_t items = 2ull * ((h / 2 + 1) / 2) * ((w / 2 + 1) / 2);
+        return launch("pair_pyramid", items, [&](dim3 g, uint32_t n) {
+            hipLaunchKernelGGL(pair_pyramid_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(q), outv(i8),
+                               outv(i16), outv(l16), h, w, n);
+        });
+    });
+}
+
+extern "C" int fhc_fine_input(const fhc_tensor* f8, const fhc_tensor* i8, const fhc_tensor* flow,
+                              const fhc_tensor* fx, const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c,
+                              void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)h * w * c == 0) return 0;
+        FHC_TRY(check(f8, "fine_input f8", c, true));
+        FHC_TRY(check(i8, "fine_input i8", 3, true));
+        FHC_TRY(check(flow, "fine_input flow", 4, true));
+        FHC_TRY(check(fx, "fine_input fx", 2 * c + 10, false, true));
+        FHC_TRY(check(l8, "fine_input l8", 2, false, true));
+        const uint32_t groups = (c + 3) / 4;
+        fhc_tensor fxb = *fx;  // the second map's slice must be 8-byte aligned too for the vector path
+        fxb.c0 += c;
+        const bool v = vec4(c, {f8, fx, &fxb});
+        return launch("fine_input", (uint64_t)h * w * (2 * groups + 3), [&](dim3 g, uint32_t n) {
+            auto k = v ? fine_input_kernel<true> : fine_input_kernel<false>;
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8), in(flow), outv(fx),
+                               outv(l8), h, w, c, groups, n);
+        });
+    });
+}
+
+extern "C" int fhc_flow_vis_t(const fhc_tensor* fv, const fhc_tensor* dfilm, const fhc_tensor* out, uint32_t n,
+                              uint32_t h, uint32_t w, float t, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)n * h * w == 0) return 0;
+        FHC_TRY(check(fv, "flow_vis_t fv", 7, true));
+        FHC_TRY(check(dfilm, "flow_vis_t dfilm", 5, true));
+        FHC_TRY(check(out, "flow_vis_t out", 7, false, true));
+        const float af = 2.0f * t, ab = 2.0f * (1.0f - t);  // the mul_t factors (net/build.rs:293)
+        return launch("flow_vis_t", (uint64_t)n * h * w, [&](dim3 g, uint32_t items) {
+            hipLaunchKernelGGL(flow_vis_t_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(fv), in(dfilm),
+                               outv(out), af, ab, items);
+        });
+    });
+}
+
+extern "C" int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tensor* vis,
+                                const fhc_tensor* rx, uint32_t h, uint32_t w, float flow_out_scale, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)h * w == 0) return 0;
+        FHC_TRY(check(q, "refine_input q", 3, true));
+        FHC_TRY(check(flow, "refine_input flow", 4, true));
+        FHC_TRY(check(vis, "refine_input vis", 3, true));
+        FHC_TRY(check(rx, "refine_input rx", 14, false, true));
+        return launch("refine_input", (uint64_t)h * w, [&](dim3 g, uint32_t items) {
+            hipLaunchKernelGGL(refine_input_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(q), in(flow),
+                               in(vis), outv(rx), h, w, flow_out_scale, items);
         });
     });
 }

@@ -3,10 +3,10 @@
 One function per Gpu method of the reference (crates/flyhigh-engine/src/ops/network.rs, interp.rs, render.rs):
 ``warp``, ``luma``, ``sad`` (sad_volume), ``convex`` (convex_upsample after its conv), ``film``, ``blend``,
 ``blendmix``, ``avgpool``, ``interp``, and the elementwise ``binary`` (add / mul), ``unary`` (mul_t, affine_out,
-clamp, neg) and ``chcopy`` (a scaled view into a concat slice). Inputs are torch NHWC f16 tensors on the GPU, or ``View`` objects that add the
-reference Tensor's channel offset and read scale (ops/tensor.rs); each function returns a new dense output unless an
-``out`` view is given (a concat slice is written in place). The module only passes device pointers: when the
-library is missing, loading it raises, and nothing is computed on the host.
+clamp, neg) and ``chcopy`` (a scaled view into a concat slice). Inputs are torch NHWC f16 tensors on the GPU, or
+``View`` objects that add the reference Tensor's channel offset and read scale (ops/tensor.rs); each function returns
+a new dense output unless an ``out`` view is given (a concat slice is written in place). The module only passes
+device pointers: when the library is missing, loading it raises, and nothing is computed on the host.
 """
 from __future__ import annotations
 
@@ -67,6 +67,10 @@ def _lib():
             "fhc_binary": [T, T, T, U, U, U, U, U, I, P],
             "fhc_unary": [T, T, U, U, U, U, I, ctypes.c_float, ctypes.c_float, P],
             "fhc_chcopy": [T, T, U, U, U, U, P],
+            "fhc_pair_pyramid": [T, T, T, T, U, U, P],
+            "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
+            "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
+            "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -203,3 +207,33 @@ def chcopy(x, c: Optional[int] = None, out=None, stream=None):
     o = _out(out, x, n, h, w, c)
     _run("chcopy", _lib().fhc_chcopy(_ref(x), _ref(o), n, h, w, c, _stream_handle(stream)))
     return o.t
+
+
+# ---- the graph's op chains, fused (include/fhc_ops.h); outputs are views into the caller's buffers ----------------
+
+def pair_pyramid(q, i8, i16, l16, stream=None):
+    q = _v(q)
+    _, h, w, _ = q.shape
+    _run("pair_pyramid", _lib().fhc_pair_pyramid(_ref(q), _ref(_v(i8)), _ref(_v(i16)), _ref(_v(l16)), h, w,
+                                                 _stream_handle(stream)))
+
+
+def fine_input(f8, i8, flow, fx, l8, c, stream=None):
+    f8 = _v(f8)
+    _, h, w, _ = f8.shape
+    _run("fine_input", _lib().fhc_fine_input(_ref(f8), _ref(_v(i8)), _ref(_v(flow)), _ref(_v(fx)), _ref(_v(l8)),
+                                             h, w, c, _stream_handle(stream)))
+
+
+def flow_vis_t(fv, dfilm, out, t, stream=None):
+    fv = _v(fv)
+    n, h, w, _ = fv.shape
+    _run("flow_vis_t", _lib().fhc_flow_vis_t(_ref(fv), _ref(_v(dfilm)), _ref(_v(out)), n, h, w, t,
+                                             _stream_handle(stream)))
+
+
+def refine_input(q, flow, vis, rx, flow_out_scale, stream=None):
+    flow = _v(flow)
+    _, h, w, _ = flow.shape
+    _run("refine_input", _lib().fhc_refine_input(_ref(_v(q)), _ref(flow), _ref(_v(vis)), _ref(_v(rx)), h, w,
+                                                 flow_out_scale, _stream_handle(stream)))

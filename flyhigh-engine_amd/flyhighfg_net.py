@@ -13,7 +13,9 @@ render_pix (the full-resolution output) is not part of the network and not run h
 
 Differences of launch structure from the reference (same arithmetic): the encoders' second pair and the second pool
 run per image so that their outputs land in their slices of the 279-channel concat; consecutive convs whose
-intermediate has no other reader run as fused pairs on the GPU when asked.
+intermediate has no other reader run as fused pairs on the GPU when asked; and flow and vis share one buffer, so
+the fine loop's two adds are one. (Independent branches on a second stream, joined by events, made the captured frame
+slower, 241 against 225 us: the graph runtime did not overlap them.)
 """
 from __future__ import annotations
 
@@ -84,21 +86,54 @@ def pad8(c):
     return (c + 7) // 8 * 8
 
 
-# Consecutive convs whose intermediate has no other reader: (first, second, second's residual is the first's output)
-PAIRS = {("enc.e1", "enc.e2"): True, ("enc.e3", "enc.e4"): True, ("fine.r2", "fine.r3"): False,
-         ("film.h1", "film.h2"): False, ("refine.q1", "refine.q2"): False, ("refine.q3", "refine.q4"): False}
+class ComposedChains:
+    """The graph's fused op chains as their ops run one after another (the reference's launches): the CPU oracle
+    backend always runs them this way, the GPU backend when asked to (a check of the fused kernels)."""
+
+    def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
+        self.avgpool(q, 3, i8, 2)
+        for i in range(2):
+            self.avgpool(V(self.image(i8.buf, i), i8.c0), 3, V(i16.buf, i16.c0 + 3 * i), 2)
+        for i in range(2):
+            self.luma(V(i16.buf, i16.c0 + 3 * i), V(l16.buf, l16.c0 + i))
+
+    def fine_input(self, f8: V, i8: V, flow: V, fx: V, l8: V, c: int):
+        for i in range(2):
+            fl = V(flow.buf, flow.c0 + 2 * i, flow.scale)
+            self.warp(V(self.image(f8.buf, i), f8.c0), c, fl, V(fx.buf, fx.c0 + c * i))
+            self.warp(V(self.image(i8.buf, i), i8.c0), 3, fl, V(fx.buf, fx.c0 + 2 * c + 3 * i))
+            self.luma(V(fx.buf, fx.c0 + 2 * c + 3 * i), V(l8.buf, l8.c0 + i))
+        self.chcopy(flow, 4, V(fx.buf, fx.c0 + 2 * c + 6))
+
+    def flow_vis_t(self, fv: V, dfilm: V, out: V, t: float, lin: V, dvis: V):
+        self.unary(V(fv.buf, fv.c0), 2, V(lin.buf, lin.c0), 0, 2.0 * t)
+        self.unary(V(fv.buf, fv.c0 + 2), 2, V(lin.buf, lin.c0 + 2), 0, 2.0 * (1.0 - t))
+        self.binary(lin, V(dfilm.buf, dfilm.c0), 4, V(out.buf, out.c0))
+        self.chcopy(V(dfilm.buf, dfilm.c0 + 4), 1, V(dvis.buf, dvis.c0))
+        self.chcopy(V(dfilm.buf, dfilm.c0 + 4, -1.0), 1, V(dvis.buf, dvis.c0 + 1))
+        self.binary(V(fv.buf, fv.c0 + 4), dvis, 3, V(out.buf, out.c0 + 4))
+
+    def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
+        for i in range(2):
+            self.warp(V(self.image(q.buf, i), q.c0), 3, V(flow.buf, flow.c0 + 2 * i, flow.scale),
+                      V(rx.buf, rx.c0 + 3 * i))
+        self.chcopy(vis, 3, V(rx.buf, rx.c0 + 6))
+        self.chcopy(V(flow.buf, flow.c0, flow_out_scale), 4, V(rx.buf, rx.c0 + 9))
+        self.blendmix(V(rx.buf, rx.c0), V(rx.buf, rx.c0 + 3), vis, blend)
+        self.luma(blend, V(rx.buf, rx.c0 + 13), grad=True)
 
 
-class GpuBackend:
+class GpuBackend(ComposedChains):
     """The program's ops on the GPU through libfhconv.so, on one stream. Plans are made on first use (the first
     run of the program; a captured replay then finds them all)."""
 
-    def __init__(self, W, stream=None, fuse: bool = True, device: str = "cuda"):
+    def __init__(self, W, stream=None, fuse: bool = True, device: str = "cuda", chains: bool = True):
         import torch
         import fhconv
         import fhops
         self.torch, self.fhconv, self.fh = torch, fhconv, fhops
-        self.W, self.stream, self.fuse, self.dev = W, stream, fuse, device
+        self.W, self.fuse, self.dev, self.chains = W, fuse, device, chains
+        self.stream = stream if stream is not None else torch.cuda.current_stream()
         self.plans: Dict[tuple, object] = {}
         self.g = None
 
@@ -134,7 +169,8 @@ class GpuBackend:
                                      r_c0=res.c0 if res is not None else 0)
 
     def conv(self, name, x: V, y: V, res: Optional[V] = None):
-        key = ("conv", name, x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0, None if res is None else res.buf.data_ptr())
+        key = ("conv", name, x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0,
+               None if res is None else res.buf.data_ptr())
         p = self.plans.get(key)
         if p is None:
             w, b, s = self.W[name]
@@ -198,6 +234,27 @@ class GpuBackend:
     def blendmix(self, wa: V, wb: V, vis: V, out: V):
         self.fh.blendmix(self._v(wa), self._v(wb), self._v(vis), out=self._v(out), stream=self.stream)
 
+    # the fused chains (one launch each) unless asked for the ops one by one
+    def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
+        if not self.chains:
+            return super().pair_pyramid(q, i8, i16, l16)
+        self.fh.pair_pyramid(self._v(q), self._v(i8), self._v(i16), self._v(l16), stream=self.stream)
+
+    def fine_input(self, f8: V, i8: V, flow: V, fx: V, l8: V, c: int):
+        if not self.chains:
+            return super().fine_input(f8, i8, flow, fx, l8, c)
+        self.fh.fine_input(self._v(f8), self._v(i8), self._v(flow), self._v(fx), self._v(l8), c, stream=self.stream)
+
+    def flow_vis_t(self, fv: V, dfilm: V, out: V, t: float, lin: V, dvis: V):
+        if not self.chains:
+            return super().flow_vis_t(fv, dfilm, out, t, lin, dvis)
+        self.fh.flow_vis_t(self._v(fv), self._v(dfilm), self._v(out), t, stream=self.stream)
+
+    def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
+        if not self.chains:
+            return super().refine_input(q, flow, vis, rx, flow_out_scale, blend)
+        self.fh.refine_input(self._v(q), self._v(flow), self._v(vis), self._v(rx), flow_out_scale, stream=self.stream)
+
 
 class FlyHighFG:
     """The buffers of one frame pair at network size net_w x net_h and the program of pair() and mid(t) over them.
@@ -218,13 +275,13 @@ class FlyHighFG:
         self.e3 = [Z(1, e16h, e16w, 72) for _ in range(2)]
         self.i8 = Z(2, e8h, e8w, 8)            # i8a, i8b
         self.cin = Z(1, e16h, e16w, 280)       # f16a 0 | f16b 72 | img16 144 | side 150 | state 154 | cv 230
-        self.la, self.lb = Z(1, e16h, e16w, 1), Z(1, e16h, e16w, 1)
+        self.l16 = Z(1, e16h, e16w, 2)         # la | lb
         self.ch1, self.ch2, self.ch3r, self.hc = (Z(1, e16h, e16w, 96) for _ in range(4))
         self.o = Z(1, e16h, e16w, 16)          # coarse head: flow 0-3, vis 4-6, conf, gate, sal
-        self.flow, self.vis = Z(1, e8h, e8w, 8), Z(1, e8h, e8w, 8)
+        self.fv = Z(1, e8h, e8w, 8)            # flow 0-3 | vis 4-6 (the fine loop updates both in one add)
         self.state_out = Z(1, e16h, e16w, 80)  # f16b 0 | flow16 72
         self.fx = Z(1, e8h, e8w, 160)          # wa 0 | wb 36 | ia 72 | ib 75 | flow8 78 | h 82 | fcv 130
-        self.la8, self.lb8 = Z(1, e8h, e8w, 1), Z(1, e8h, e8w, 1)
+        self.l8 = Z(1, e8h, e8w, 2)            # fla | flb
         self.fr1, self.fr2, self.h = (Z(1, e8h, e8w, 48) for _ in range(3))
         self.d = Z(1, e8h, e8w, 8)             # fine.out: flow delta 0-3, vis delta 4-6
         self.lin = Z(1, e8h, e8w, 8)           # linf | linb
@@ -244,65 +301,43 @@ class FlyHighFG:
         be, S = self.be, self.shape
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
         img = be.image
-        be.interp(V(self.AB), 3, V(self.aq), qh, qw, True)                                   # 0, 1
-        be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)               # 2-4, 8-10
+        be.interp(V(self.AB), 3, V(self.aq), qh, qw, True)                                    # 0, 1
+        be.pair_pyramid(V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16))                # 14-18, 21-24
+        be.sad(V(self.l16, 0), V(self.l16, 1), V(self.cin, 230), 3)                           # 25, 26; 19-20 zeros
+        be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)                 # 2-4, 8-10
         for i in range(2):                                                                    # 5-7, 11-13
             be.pair("enc.e3", "enc.e4", V(img(self.f8, i)), V(self.e3[i]), V(self.cin, 72 * i), True)
-        be.avgpool(V(self.aq), 3, V(self.i8), 2)                                              # 14, 15
-        for i in range(2):                                                                    # 16-18
-            be.avgpool(V(img(self.i8, i)), 3, V(self.cin, 144 + 3 * i), 2)
-        be.luma(V(self.cin, 144), V(self.la))                                                 # 21-24 (side, state:
-        be.luma(V(self.cin, 147), V(self.lb))                                                 # zeros, 19-20)
-        be.sad(V(self.la), V(self.lb), V(self.cin, 230), 3)                                   # 25, 26
         be.conv("coarse.c1", V(self.cin), V(self.ch1))                                        # 27
         be.conv("coarse.c2", V(self.ch1), V(self.ch2))                                        # 28
         be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30
         be.conv("coarse.c4", V(self.ch3r), V(self.hc))                                        # 31
         be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
-        be.interp(V(self.o, 0, 16.0), 4, V(self.flow), e8h, e8w, False)                       # 33-34, 39
-        be.interp(V(self.o, 4), 3, V(self.vis), e8h, e8w, False)                              # 35, 40
+        be.chcopy(V(self.cin, 72), 72, V(self.state_out, 0))                                  # 43: state_out
+        be.chcopy(V(self.o, 0, 16.0), 4, V(self.state_out, 72))
+        be.interp(V(self.o, 0, 16.0), 4, V(self.fv, 0), e8h, e8w, False)                      # 33-34, 39: flow
+        be.interp(V(self.o, 4), 3, V(self.fv, 4), e8h, e8w, False)                            # 35, 40: vis
         # the fine loop, K = 1 (op 42): h enters as zeros (op 41: the fx slice is never written)
-        be.warp(V(img(self.f8, 0)), 36, V(self.flow, 0, 0.125), V(self.fx, 0))                # wa
-        be.warp(V(img(self.f8, 1)), 36, V(self.flow, 2, 0.125), V(self.fx, 36))               # wb
-        be.warp(V(img(self.i8, 0)), 3, V(self.flow, 0, 0.125), V(self.fx, 72))                # ia
-        be.warp(V(img(self.i8, 1)), 3, V(self.flow, 2, 0.125), V(self.fx, 75))                # ib
-        be.luma(V(self.fx, 72), V(self.la8))                                                  # fla
-        be.luma(V(self.fx, 75), V(self.lb8))                                                  # flb
-        be.sad(V(self.la8), V(self.lb8), V(self.fx, 130), 2)                                  # fcv
-        be.chcopy(V(self.flow, 0, 0.125), 4, V(self.fx, 78))                                  # flow8 into fx
+        be.fine_input(V(self.f8), V(self.i8), V(self.fv, 0, 0.125), V(self.fx), V(self.l8), 36)  # wa .. flow8
+        be.sad(V(self.l8, 0), V(self.l8, 1), V(self.fx, 130), 2)                              # fcv
         be.conv("fine.r1", V(self.fx), V(self.fr1))
         be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
         be.conv("fine.out", V(self.h), V(self.d))
-        be.binary(V(self.flow), V(self.d, 0), 4, V(self.flow))                                # flow += d[0:4]
-        be.binary(V(self.vis), V(self.d, 4), 3, V(self.vis))                                  # vis += d[4:7]
-        be.chcopy(V(self.cin, 72), 72, V(self.state_out, 0))                                  # 43: state_out
-        be.chcopy(V(self.o, 0, 16.0), 4, V(self.state_out, 72))
+        be.binary(V(self.fv), V(self.d), 7, V(self.fv))                                       # flow, vis += d
 
     def mid(self, t: float, W: Optional[dict]):
         """mid(t): models/graph.json ops 44-81 (render_pix, op 82, excluded). With W None the FiLM vector of t must
         already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes it that way, as the
         reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22)."""
-        be, (qh, qw) = self.be, self.shape["q"]
-        img = be.image
-        be.unary(V(self.flow, 0), 2, V(self.lin, 0), 0, 2.0 * t)                              # 44, 46: linf
-        be.unary(V(self.flow, 2), 2, V(self.lin, 2), 0, 2.0 * (1.0 - t))                      # 45, 47: linb
+        be = self.be
         if W is not None:
             be.set_g(film_mlp(W, t))                                                          # 49
+        be.conv("up.w", V(self.h), V(self.wt36))                                              # 62
         be.film(V(self.h), 48, V(self.hm))                                                    # 50
         be.pair("film.h1", "film.h2", V(self.hm), V(self.fh1), V(self.fh2), False)            # 51, 52
         be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
-        be.binary(V(self.lin), V(self.dfilm, 0), 4, V(self.ftvt, 0))                          # 56: flow_t
-        be.chcopy(V(self.dfilm, 4), 1, V(self.dvis, 0))                                       # 57-59: dvis
-        be.chcopy(V(self.dfilm, 4, -1.0), 1, V(self.dvis, 1))
-        be.binary(V(self.vis), V(self.dvis), 3, V(self.ftvt, 4))                              # 60: vis_t
-        be.conv("up.w", V(self.h), V(self.wt36))                                              # 62
-        be.convex(V(self.wt36), V(self.ftvt), 7, V(self.up7))
-        be.warp(V(img(self.aq, 0)), 3, V(self.up7, 0, 0.25), V(self.rx, 0))                   # 65-68: rwa
-        be.warp(V(img(self.aq, 1)), 3, V(self.up7, 2, 0.25), V(self.rx, 3))                   # 69: rwb
-        be.blendmix(V(self.rx, 0), V(self.rx, 3), V(self.up7, 4), V(self.blend))              # 70-73
-        be.luma(V(self.blend), V(self.rx, 13), grad=True)                                     # 75: lg
-        be.chcopy(V(self.up7, 4), 3, V(self.rx, 6))                                           # 76: vis_tq
-        be.chcopy(V(self.up7, 0, 0.05), 4, V(self.rx, 9))                                     # 74, 76: flow_tq20
+        be.flow_vis_t(V(self.fv), V(self.dfilm), V(self.ftvt), t, V(self.lin), V(self.dvis))   # 44-48, 54-61
+        be.convex(V(self.wt36), V(self.ftvt), 7, V(self.up7))                                 # 62
+        be.refine_input(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend))  # 63-76
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
         be.pair("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), False)        # 79, 80
         be.unary(V(self.rr), 3, V(self.Rt), 2)                                                # 81: affine_out

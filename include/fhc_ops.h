@@ -104,6 +104,35 @@ int fhc_unary(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h
 int fhc_chcopy(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                void* stream);
 
+/* ---- The graph's op chains, fused. Each computes what its ops compute one after another (the same f32 operations
+ * and f16 roundings at the tensors the ops store); no reference counterpart as one call: each replaces the listed
+ * planner arms run in sequence. A and B arrive as a batch of 2. */
+
+/* models/graph.json ops 14-18, 21-24: avgpool k 2 of q (2, h, w, 3) into i8 (2, h/2, w/2, 3), again into i16's
+ * channels 3 * image (1, h/4, w/4: the img16 slice of the coarse input), and their luma into l16's channel image
+ * (avgpool.wgsl:8-19, luma.wgsl:14-19; arms net/build.rs:279-282, :321). h, w >= 4. */
+int fhc_pair_pyramid(const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16, const fhc_tensor* l16,
+                     uint32_t h, uint32_t w, void* stream);
+
+/* graph.json op 42's body up to the concat: f8 (2, h, w, c) and i8 (2, h, w, 3) warped by flow (1, h, w: channels
+ * 0-1 for A, 2-3 for B, at its read scale), written into fx's slices c0: wa, +c: wb, +2c: ia, +2c+3: ib, +2c+6: the
+ * scaled flow (4 channels); the warped pictures' luma into l8's channel image (warp.wgsl, luma.wgsl, chcopy.wgsl). */
+int fhc_fine_input(const fhc_tensor* f8, const fhc_tensor* i8, const fhc_tensor* flow, const fhc_tensor* fx,
+                   const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c, void* stream);
+
+/* graph.json ops 44-48, 54-60: fv holds flow (channels 0-3) and vis (4-6), dfilm the FiLM head's output (d_flow
+ * 0-3, d_mask 4); out = flow_t (0-3) = f16(flow * 2t) (forward, channels 0-1; 2(1 - t) backward, 2-3) + d_flow,
+ * and vis_t (4-6) = vis + (d_mask, -d_mask, 0) (unary.wgsl op 0, binary.wgsl op 0, chcopy.wgsl; arms
+ * net/build.rs:290-311). */
+int fhc_flow_vis_t(const fhc_tensor* fv, const fhc_tensor* dfilm, const fhc_tensor* out, uint32_t n, uint32_t h,
+                   uint32_t w, float t, void* stream);
+
+/* graph.json ops 65-76: q (2, h, w, 3) warped by flow (1, h, w: channels 0-1 A, 2-3 B, at its read scale), the
+ * blend of the two by the visibility logits vis (blendmix.wgsl), and the blend's luma gradient, written as rx:
+ * c0 rwa, +3 rwb, +6 vis (copied), +9 the raw flow times flow_out_scale, +13 the gradient. */
+int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rx,
+                     uint32_t h, uint32_t w, float flow_out_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -4,10 +4,10 @@ buffers with the same views and slices as the GPU backend."""
 import numpy as np
 
 from fhtest import oracle
-from flyhighfg_net import CONVS, cpu_threads
+from flyhighfg_net import CONVS, ComposedChains, cpu_threads
 
 
-class CpuBackend:
+class CpuBackend(ComposedChains):
     def __init__(self, W):
         self.W, self.threads, self.g = W, cpu_threads(), None
 

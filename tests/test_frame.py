@@ -66,3 +66,25 @@ def test_gpu_frame_matches_the_oracle_composition(net_w, net_h, fuse):
         err, tol = np.abs(g - r).max(), 1e-2 * np.abs(r).max()
         print(f"  {name}: max|diff| {err:.3g} (bar {tol:.3g}, max|ref| {np.abs(r).max():.3g})", flush=True)
         assert err <= tol, name
+
+
+@pytest.mark.gpu
+def test_fused_chains_equal_their_ops_on_the_gpu():
+    """The four fused op chains (pyramid, fine input, flow_t / vis_t, refine input) against the same chains run op
+    by op on the GPU, in the whole frame: the same f32 operations and roundings, so every output is bit-identical."""
+    import torch
+    W = net.make_weights(3)
+    ab = inputs(3, 256, 128)
+    outs = []
+    for chains in (True, False):
+        gb = net.GpuBackend(W, stream=torch.cuda.current_stream(), chains=chains)
+        f = run(gb, W, 256, 128, ab, t=0.3)
+        extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("ftvt", 7), ("d", 7),
+                 ("dfilm", 5), ("wt36", 36)]
+        outs.append({name: gb.host(getattr(f, name))[..., :c].copy() for name, c in OUTPUTS + extra})
+    diffs = []
+    for name in outs[0]:
+        bad = np.argwhere(outs[0][name] != outs[1][name])
+        if bad.size:
+            diffs.append(f"{name}: {len(bad)} differ, first at {bad[0].tolist()}")
+    assert not diffs, "; ".join(diffs)
