@@ -16,7 +16,7 @@ of the batched workload against its HBM roofline), and the CPU baseline: the ora
 reference's conv arithmetic) over the same conv layers on the host's cores.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--no-batched] [--no-fuse] [--no-ops]
-    python bench.py --only-ops
+    python bench.py --only-ops | --only-network
 """
 import argparse
 import json
@@ -280,7 +280,7 @@ def network_frame(args, torch, np, stream, net_w, net_h, t=0.5):
     f = fnet.FlyHighFG(be, net_w, net_h)
     yy, xx = np.mgrid[0:net_h, 0:net_w] / 16.0
     base = 0.5 + 0.25 * np.sin(xx)[..., None] * np.cos(yy)[..., None] + 0.1 * np.sin(3.7 * xx + 1.3 * yy)[..., None]
-    ab = np.zeros((2, net_h, net_w, 8), np.float32)
+    ab = np.zeros((2, net_h, net_w, 4), np.float32)
     ab[0, ..., :3], ab[1, ..., :3] = base, np.roll(base, 12, axis=1)
     f.AB.copy_(be.upload(np.ascontiguousarray(ab.astype(np.float16)).view(np.uint16)))
     be.set_g(fnet.film_mlp(W, t))
@@ -547,6 +547,9 @@ def main():
     ap.add_argument("--no-ops", action="store_true", help="skip the timing of the network ops between the convs")
     ap.add_argument("--only-ops", action="store_true",
                     help="only time the network ops (frame and batched shapes) and print them as one JSON line")
+    ap.add_argument("--only-network", action="store_true",
+                    help="only time the whole-network frame (every op of pair() + mid() as one HIP graph) and print "
+                         "it as one JSON line")
     ap.add_argument("--tune", help="plan with this choice table (cin,cout,h,w,stride=code lines) instead of autotuning")
     ap.add_argument("--pmc-layer", help="only run this frame layer --pmc-reps times over rotating (cold) buffers, "
                                         "then a copy of known size as many times: the workload of the rocprofv3 "
@@ -578,6 +581,9 @@ def main():
         log(f"bench: {n_tune} choices from {args.tune}")
     net_w, net_h = 864, 480  # default_internal(1920, 1080) = (856, 480), padded to a multiple of 32
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
+    if args.only_network:
+        print(json.dumps(dict(network_frame=network_frame(args, torch, np, stream, net_w, net_h))), flush=True)
+        return 0
     if args.only_ops:
         print(json.dumps(dict(net_ops=net_ops_report(args, torch, flyhighfg, stream, net_w, net_h))), flush=True)
         return 0

@@ -43,6 +43,8 @@ __device__ __forceinline__ void st(const OView& v, size_t pix, uint32_t ch, floa
     v.p[pix * v.cs + v.c0 + ch] = f2h(x);
 }
 __device__ __forceinline__ int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+// luma of f32 B, G, R at read scale 1: luma.wgsl:9-12
+__device__ __forceinline__ float lum3(float b, float g, float r) { return 0.299f * r + 0.587f * g + 0.114f * b; }
 
 // channels ch .. ch + 3 (those below c; 0 for the rest) of pixel pix. VEC: one 8-byte load, valid when the view's
 // cs and c0, ch and the base address are 4-channel (8-byte) aligned and c is a multiple of 4.
@@ -409,11 +411,21 @@ __global__ __launch_bounds__(kThreads) void interp_aa_kernel(View x, OView out, 
 // last row / column with the same values), so it takes one memory round trip. The per-output sum is the one above.
 constexpr uint32_t kAaT = 16, kAaR = 5, kAaExt = kAaT * kAaR;
 
-template <int KM>
+// PYR (3 channels, a batch of the two pictures): the tile's outputs also go through the pair() pyramid (avgpool k 2
+// twice and the luma, graph.json ops 14-18, 21-24) from LDS: a 16 x 16 tile holds whole 2 x 2 and 4 x 4 blocks, so
+// i8 (8 x 8 of them), i16 (4 x 4, into channels 3 * image of its view) and l16 (channel image) need no other
+// launch; each pool reads the f16 values the previous stage stores, in avgpool's order.
+struct PyrOut {
+    OView i8, i16, l16;
+};
+
+// V4: the input view's pixels are 8-byte aligned 4-channel groups (cs and c0 multiples of 4): one load a pixel
+template <int KM, bool PYR, bool V4>
 __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView out, uint32_t ih, uint32_t iw,
                                                                  uint32_t oh, uint32_t ow, uint32_t c,
-                                                                 uint32_t tiles_x, uint32_t tiles_y) {
+                                                                 uint32_t tiles_x, uint32_t tiles_y, PyrOut pyr) {
     __shared__ uint2 tile[kAaExt * kAaExt];
+    __shared__ float qt[PYR ? kAaT * kAaT * 3 : 1], q8[PYR ? 64 * 3 : 1];
     const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
     const uint32_t bt = blockIdx.x, txi = bt % tiles_x, r = bt / tiles_x, tyi = r % tiles_y, img = r / tiles_y;
     const uint32_t ox0 = txi * kAaT, oy0 = tyi * kAaT;
@@ -432,15 +444,22 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
         for (uint32_t j = 0; j < kAaR; j++) {
             const int row = min((int)(ty + kAaT * i), ny - 1), col = min((int)(tx + kAaT * j), nx - 1);
             const uint16_t* src = x.p + ((rowbase + row) * iw + xlo + col) * x.cs + x.c0;
-            uint16_t v[4];
+            if constexpr (V4) {  // channels past c are never read from the tile
+                tile[row * kAaExt + col] = *reinterpret_cast<const uint2*>(src);
+            } else {
+                uint16_t v[4];
 #pragma unroll
-            for (uint32_t k = 0; k < 4; k++) v[k] = src[min(k, c - 1)];
-            tile[row * kAaExt + col] = uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
+                for (uint32_t k = 0; k < 4; k++) v[k] = src[min(k, c - 1)];
+                tile[row * kAaExt + col] =
+                    uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
+            }
         }
     __syncthreads();
     const uint32_t ox = ox0 + tx, oy = oy0 + ty;
-    if (ox >= ow || oy >= oh) return;
-    const float cy = ((float)oy + 0.5f) * sh, cx = ((float)ox + 0.5f) * sw;
+    const bool valid = ox < ow && oy < oh;
+    if (!PYR && !valid) return;
+    // an invalid lane (PYR only: it must reach the barriers) computes a clamped pixel and stores nothing
+    const float cy = ((float)min(oy, oh - 1) + 0.5f) * sh, cx = ((float)min(ox, ow - 1) + 0.5f) * sw;
     const int ymin = max(0, (int)floorf(cy - fsh + 0.5f)), ymax = min((int)ih, (int)floorf(cy + fsh + 0.5f));
     const int xmin = max(0, (int)floorf(cx - fsw + 0.5f)), xmax = min((int)iw, (int)floorf(cx + fsw + 0.5f));
     float wx[KM];
@@ -472,7 +491,43 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
     float val[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) val[i] = acc[i] / norm * x.scale;
-    st4<false>(out, ((size_t)img * oh + oy) * ow + ox, 0, c, val);
+    if (valid) st4<false>(out, ((size_t)img * oh + oy) * ow + ox, 0, c, val);
+    if constexpr (PYR) {
+        if (valid)
+#pragma unroll
+            for (uint32_t ch = 0; ch < 3; ch++) qt[(ty * kAaT + tx) * 3 + ch] = h2f(f2h(val[ch]));
+        __syncthreads();
+        const uint32_t h8 = oh / 2, w8 = ow / 2, h16 = h8 / 2, w16 = w8 / 2;
+        if (tid < 64) {
+            const uint32_t ly = tid / 8, lx = tid % 8, y8 = oy0 / 2 + ly, x8 = ox0 / 2 + lx;
+            if (y8 < h8 && x8 < w8) {  // its 2 x 2 block lies in the tile and the picture
+                const float* b = qt + ((2 * ly) * kAaT + 2 * lx) * 3;
+#pragma unroll
+                for (uint32_t ch = 0; ch < 3; ch++) {
+                    const float a = ((0.0f + b[ch]) + b[3 + ch]) + b[kAaT * 3 + ch] + b[kAaT * 3 + 3 + ch];
+                    const uint16_t hv = f2h(a / 4.0f);
+                    q8[tid * 3 + ch] = h2f(hv);
+                    pyr.i8.p[(((size_t)img * h8 + y8) * w8 + x8) * pyr.i8.cs + pyr.i8.c0 + ch] = hv;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < 16) {
+            const uint32_t ly = tid / 4, lx = tid % 4, y16 = oy0 / 4 + ly, x16 = ox0 / 4 + lx;
+            if (y16 < h16 && x16 < w16) {
+                const float* b = q8 + ((2 * ly) * 8 + 2 * lx) * 3;
+                float v[3];
+#pragma unroll
+                for (uint32_t ch = 0; ch < 3; ch++) {
+                    const float a = ((0.0f + b[ch]) + b[3 + ch]) + b[8 * 3 + ch] + b[8 * 3 + 3 + ch];
+                    const uint16_t hv = f2h(a / 4.0f);
+                    v[ch] = h2f(hv);
+                    pyr.i16.p[((size_t)y16 * w16 + x16) * pyr.i16.cs + pyr.i16.c0 + 3 * img + ch] = hv;
+                }
+                st(pyr.l16, (size_t)y16 * w16 + x16, img, lum3(v[0], v[1], v[2]));
+            }
+        }
+    }
 }
 
 // The largest input extent (rows or columns) of any kAaT-output tile's windows, from the kernel's f32 formulas.
@@ -558,8 +613,6 @@ __global__ __launch_bounds__(kThreads) void chcopy_kernel(View x, OView out, uin
 
 // ---- the graph's op chains, fused: each kernel computes what its ops compute one after another, with the same
 // f32 operations and the same f16 roundings at the tensors the ops store (bit for bit) ----------------------------------
-
-__device__ __forceinline__ float lum3(float b, float g, float r) { return 0.299f * r + 0.587f * g + 0.114f * b; }
 
 // The pictures' pyramid of pair() (graph.json ops 14-18, 21-24): avgpool k 2 of the A and B pictures q (batch 2,
 // 3 channels) to i8, again to the 1/4 pictures (written into channels 3 * image of i16, the img16 slice of the
@@ -690,16 +743,31 @@ __device__ __forceinline__ void blend_at(const View& q, const View& fl, const Vi
     }
 }
 
+// One workgroup per 16 x 16 pixels: each lane's blend goes to LDS, 33 lanes add the blends of the column to the
+// right and the row below (clamped to the picture; unused past its edge), and the gradient reads them from there.
 __global__ __launch_bounds__(kThreads) void refine_input_kernel(View q, View fl, View vis, OView rx, uint32_t h,
-                                                                uint32_t w, float fs, uint32_t items) {
-    const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
-    if (pix >= items) return;
-    const uint32_t x = pix % w, y = pix / w;
-    float ra[3], rb[3], bl[3], na[3], nb[3], br[3], bd[3];
-    blend_at(q, fl, vis, x, y, h, w, ra, rb, bl);
-    blend_at(q, fl, vis, min(x + 1, w - 1), y, h, w, na, nb, br);  // clamped: unused past the last column
-    blend_at(q, fl, vis, x, min(y + 1, h - 1), h, w, na, nb, bd);
-    uint16_t* o = rx.p + (size_t)pix * rx.cs + rx.c0;
+                                                                uint32_t w, float fs, uint32_t tiles_x) {
+    __shared__ float bt[17 * 17 * 3];
+    const uint32_t tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const uint32_t x0 = (blockIdx.x % tiles_x) * 16, y0 = (blockIdx.x / tiles_x) * 16;
+    const uint32_t x = x0 + tx, y = y0 + ty;
+    float ra[3], rb[3], bl[3];
+    blend_at(q, fl, vis, min(x, w - 1), min(y, h - 1), h, w, ra, rb, bl);
+#pragma unroll
+    for (uint32_t ch = 0; ch < 3; ch++) bt[(ty * 17 + tx) * 3 + ch] = bl[ch];
+    if (threadIdx.x < 33) {  // the halo: (16, 0..16) and (0..15, 16)
+        const uint32_t hx = threadIdx.x < 17 ? 16 : threadIdx.x - 17, hy = threadIdx.x < 17 ? threadIdx.x : 16;
+        float na[3], nb[3], nl[3];
+        blend_at(q, fl, vis, min(x0 + hx, w - 1), min(y0 + hy, h - 1), h, w, na, nb, nl);
+#pragma unroll
+        for (uint32_t ch = 0; ch < 3; ch++) bt[(hy * 17 + hx) * 3 + ch] = nl[ch];
+    }
+    __syncthreads();
+    if (x >= w || y >= h) return;
+    const float* br = bt + (ty * 17 + tx + 1) * 3;
+    const float* bd = bt + ((ty + 1) * 17 + tx) * 3;
+    const size_t pix = (size_t)y * w + x;
+    uint16_t* o = rx.p + pix * rx.cs + rx.c0;
 #pragma unroll
     for (uint32_t ch = 0; ch < 3; ch++) {
         o[ch] = f2h(ra[ch]);
@@ -913,9 +981,11 @@ extern "C" int fhc_interpolate(const fhc_tensor* x, const fhc_tensor* out, uint3
             if (c <= 4 && taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt) {
                 const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
                 if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "interpolate: too many tiles");
-                auto kl = taps <= 4 ? interp_aa_lds_kernel<4> : interp_aa_lds_kernel<8>;
+                const bool v4 = vec4(4, {x});
+                auto kl = taps <= 4 ? (v4 ? interp_aa_lds_kernel<4, false, true> : interp_aa_lds_kernel<4, false, false>)
+                                    : (v4 ? interp_aa_lds_kernel<8, false, true> : interp_aa_lds_kernel<8, false, false>);
                 hipLaunchKernelGGL(kl, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out),
-                                   ih, iw, oh, ow, c, tx, ty);
+                                   ih, iw, oh, ow, c, tx, ty, PyrOut{});
                 const hipError_t e = hipGetLastError();
                 return e == hipSuccess ? 0 : fail(-2, "interpolate: launch failed: %s", hipGetErrorString(e));
             }
@@ -1061,9 +1131,39 @@ extern "C" int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, con
         FHC_TRY(check(flow, "refine_input flow", 4, true));
         FHC_TRY(check(vis, "refine_input vis", 3, true));
         FHC_TRY(check(rx, "refine_input rx", 14, false, true));
-        return launch("refine_input", (uint64_t)h * w, [&](dim3 g, uint32_t items) {
+        const uint32_t tx = (w + 15) / 16, ty = (h + 15) / 16;
+        return launch("refine_input", (uint64_t)tx * ty * kThreads, [&](dim3 g, uint32_t) {
             hipLaunchKernelGGL(refine_input_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(q), in(flow),
-                               in(vis), outv(rx), h, w, flow_out_scale, items);
+                               in(vis), outv(rx), h, w, flow_out_scale, tx);
         });
+    });
+}
+
+extern "C" int fhc_pair_input(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16,
+                              const fhc_tensor* l16, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow,
+                              void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)ih * iw * oh * ow == 0) return 0;
+        FHC_TRY(check(ab, "pair_input ab", 3, true));
+        FHC_TRY(check(q, "pair_input q", 3, false, true));
+        const uint32_t taps = std::max(aa_taps(ih, oh), aa_taps(iw, ow));
+        if (!(taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt)) {
+            // no one-launch form for this scale: the resize, then the pyramid
+            FHC_TRY(fhc_interpolate(ab, q, 2, 3, ih, iw, oh, ow, 1, stream));
+            return fhc_pair_pyramid(q, i8, i16, l16, oh, ow, stream);
+        }
+        if (oh < 4 || ow < 4) return fail(-1, "pair_input: %u x %u is below 4 x 4", oh, ow);
+        FHC_TRY(check(i8, "pair_input i8", 3, false, true));
+        FHC_TRY(check(i16, "pair_input i16", 6, false, true));
+        FHC_TRY(check(l16, "pair_input l16", 2, false, true));
+        const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
+        const bool v4 = vec4(4, {ab});
+        auto kl = taps <= 4 ? (v4 ? interp_aa_lds_kernel<4, true, true> : interp_aa_lds_kernel<4, true, false>)
+                            : (v4 ? interp_aa_lds_kernel<8, true, true> : interp_aa_lds_kernel<8, true, false>);
+        hipLaunchKernelGGL(kl, dim3(2 * tx * ty), dim3(kThreads), 0, (hipStream_t)stream, in(ab), outv(q), ih, iw, oh,
+                           ow, 3u, tx, ty, PyrOut{outv(i8), outv(i16), outv(l16)});
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "pair_input: launch failed: %s", hipGetErrorString(e));
     });
 }

@@ -68,6 +68,7 @@ def _lib():
             "fhc_unary": [T, T, U, U, U, U, I, ctypes.c_float, ctypes.c_float, P],
             "fhc_chcopy": [T, T, U, U, U, U, P],
             "fhc_pair_pyramid": [T, T, T, T, U, U, P],
+            "fhc_pair_input": [T, T, T, T, T, U, U, U, U, P],
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
@@ -237,3 +238,10 @@ def refine_input(q, flow, vis, rx, flow_out_scale, stream=None):
     _, h, w, _ = flow.shape
     _run("refine_input", _lib().fhc_refine_input(_ref(_v(q)), _ref(flow), _ref(_v(vis)), _ref(_v(rx)), h, w,
                                                  flow_out_scale, _stream_handle(stream)))
+
+
+def pair_input(ab, q, i8, i16, l16, oh, ow, stream=None):
+    ab = _v(ab)
+    _, ih, iw, _ = ab.shape
+    _run("pair_input", _lib().fhc_pair_input(_ref(ab), _ref(_v(q)), _ref(_v(i8)), _ref(_v(i16)), _ref(_v(l16)), ih,
+                                             iw, oh, ow, _stream_handle(stream)))

@@ -90,6 +90,10 @@ class ComposedChains:
     """The graph's fused op chains as their ops run one after another (the reference's launches): the CPU oracle
     backend always runs them this way, the GPU backend when asked to (a check of the fused kernels)."""
 
+    def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
+        self.interp(ab, 3, q, oh, ow, True)
+        self.pair_pyramid(q, i8, i16, l16)
+
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
         for i in range(2):
@@ -235,6 +239,12 @@ class GpuBackend(ComposedChains):
         self.fh.blendmix(self._v(wa), self._v(wb), self._v(vis), out=self._v(out), stream=self.stream)
 
     # the fused chains (one launch each) unless asked for the ops one by one
+    def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
+        if not self.chains:
+            return super().pair_input(ab, q, i8, i16, l16, oh, ow)
+        self.fh.pair_input(self._v(ab), self._v(q), self._v(i8), self._v(i16), self._v(l16), oh, ow,
+                           stream=self.stream)
+
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         if not self.chains:
             return super().pair_pyramid(q, i8, i16, l16)
@@ -268,7 +278,7 @@ class FlyHighFG:
         e16h, e16w = (e8h - 1) // 2 + 1, (e8w - 1) // 2 + 1
         self.shape = dict(net=(net_h, net_w), q=(qh, qw), e8=(e8h, e8w), e16=(e16h, e16w))
         Z = be.zeros
-        self.AB = Z(2, net_h, net_w, 8)        # the inputs A, B at network size (BGR in [0, 1])
+        self.AB = Z(2, net_h, net_w, 4)        # the inputs A, B at network size (BGR in [0, 1]), 8-byte pixels
         self.aq = Z(2, qh, qw, 8)              # aq, bq
         self.e1 = Z(2, e8h, e8w, 40)           # a_e1, b_e1
         self.f8 = Z(2, e8h, e8w, 40)           # f8a, f8b
@@ -301,8 +311,7 @@ class FlyHighFG:
         be, S = self.be, self.shape
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
         img = be.image
-        be.interp(V(self.AB), 3, V(self.aq), qh, qw, True)                                    # 0, 1
-        be.pair_pyramid(V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16))                # 14-18, 21-24
+        be.pair_input(V(self.AB), V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16), qh, qw)  # 0-1, 14-24
         be.sad(V(self.l16, 0), V(self.l16, 1), V(self.cin, 230), 3)                           # 25, 26; 19-20 zeros
         be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)                 # 2-4, 8-10
         for i in range(2):                                                                    # 5-7, 11-13

@@ -114,6 +114,12 @@ int fhc_chcopy(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t 
 int fhc_pair_pyramid(const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16, const fhc_tensor* l16,
                      uint32_t h, uint32_t w, void* stream);
 
+/* graph.json ops 0-1, 14-18, 21-24: the antialiased resize of the pictures ab (2, ih, iw, 3) to q (2, oh, ow, 3), and
+ * from it the pyramid of fhc_pair_pyramid (i8, i16, l16), in one launch where the resize's tiles hold whole pool
+ * blocks (else the two calls). */
+int fhc_pair_input(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16,
+                   const fhc_tensor* l16, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow, void* stream);
+
 /* graph.json op 42's body up to the concat: f8 (2, h, w, c) and i8 (2, h, w, 3) warped by flow (1, h, w: channels
  * 0-1 for A, 2-3 for B, at its read scale), written into fx's slices c0: wa, +c: wb, +2c: ia, +2c+3: ib, +2c+6: the
  * scaled flow (4 channels); the warped pictures' luma into l8's channel image (warp.wgsl, luma.wgsl, chcopy.wgsl). */

@@ -18,7 +18,7 @@ OUTPUTS = [("up7", 7), ("Rt", 3), ("state_out", 76), ("o", 12), ("h", 48), ("cin
 
 def inputs(seed, net_w, net_h):
     rng = np.random.default_rng(seed)
-    ab = np.zeros((2, net_h, net_w, 8), np.float32)
+    ab = np.zeros((2, net_h, net_w, 4), np.float32)
     yy, xx = np.mgrid[0:net_h, 0:net_w] / 16.0
     base = 0.5 + 0.25 * np.sin(xx)[..., None] * np.cos(yy)[..., None] + 0.1 * rng.uniform(-1, 1, (net_h, net_w, 3))
     ab[0, ..., :3] = base

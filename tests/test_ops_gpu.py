@@ -172,6 +172,7 @@ def test_avgpool_matches_oracle(n, h, w, c, cs, c0, k):
 
 INTERP_CASES = [  # n, ih, iw, oh, ow, c, cs, c0, aa, scale
     (1, 480, 864, 120, 216, 3, 3, 0, True, 1.0),   # the graph's A -> aq (antialiased quarter)
+    (2, 480, 864, 120, 216, 3, 4, 0, True, 1.0),   # the same from 8-byte pixels (one load a pixel into LDS)
     (2, 30, 54, 60, 108, 4, 16, 0, False, 1.0),     # flow16 -> flow (vector path)
     (2, 30, 54, 60, 108, 3, 16, 4, False, 16.0),    # vis16 of an offset view, scaled
     (1, 23, 41, 7, 9, 5, 6, 1, True, 0.5),          # ragged antialias
