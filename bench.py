@@ -700,16 +700,21 @@ def main():
             del cnet
             torch.cuda.empty_cache()
 
-    batched = None
-    if not args.no_batched:
-        batched = batched_workload(args, torch, np, fhconv, flyhighfg, stream)
-        torch.cuda.empty_cache()
-
+    # the network frame plans its convs from the choice table the frame's autotuning filled; the batched workload
+    # autotunes at batch 8-24 under the same keys (the key has no batch), so it runs after, and the table is restored
     net_ops = None if args.no_ops else net_ops_report(args, torch, flyhighfg, stream, net_w, net_h)
     netframe = None
     if not args.no_ops:
         netframe = network_frame(args, torch, np, stream, net_w, net_h)
         log("bench: network frame", json.dumps(netframe))
+
+    batched = None
+    if not args.no_batched:
+        frame_table = fhconv.format_tune()
+        batched = batched_workload(args, torch, np, fhconv, flyhighfg, stream)
+        fhconv.tune_clear()
+        fhconv.parse_tune(frame_table)
+        torch.cuda.empty_cache()
 
     mfma_rate = mfma_rate_probe(torch, fhconv, stream)
     log(f"bench: sustained dense f16 MFMA rate {mfma_rate:.0f} TFLOP/s")
