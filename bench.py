@@ -271,7 +271,7 @@ def net_ops_report(args, torch, flyhighfg, stream, net_w, net_h):
 
 def network_frame(args, torch, np, stream, net_w, net_h, t=0.5):
     """The whole network of one frame: every op of pair() and mid(t) (flyhighfg_net: the 25 convs and up.w, fused
-    pairs, the network ops, render_pix excluded) captured as one HIP graph on `stream`; per-frame time over
+    pairs, the network ops, render_pix with the model's bicubic sampler) captured as one HIP graph on `stream`; per-frame time over
     args.steps replays (after args.warmup) between events on that stream. Random weights of the architecture
     (seed 7), a synthetic picture and the same picture moved 12 pixels as A and B."""
     import flyhighfg_net as fnet
@@ -302,15 +302,15 @@ def network_frame(args, torch, np, stream, net_w, net_h, t=0.5):
         e1.record(stream)
         e1.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / args.steps
-    outs = {k: be.host(getattr(f, k))[..., :c].view(np.float16) for k, c in (("Rt", 3), ("up7", 7))}
+    outs = {k: be.host(getattr(f, k))[..., :c].view(np.float16) for k, c in (("out", 3), ("Rt", 3), ("up7", 7))}
     finite = all(bool(np.all(np.isfinite(v))) for v in outs.values())
     fused = sum(1 for k, p in be.plans.items() if k[0] == "pair" and p is not False)
     res = dict(us_per_frame=round(us, 3), frames_per_s=round(1e6 / us, 2), finite_outputs=finite,
                conv_plans=sum(1 for k in be.plans if k[0] == "conv"), fused_pairs=fused,
                workload=f"every op of one FlyHighFG pair() and mid(t={t}) at network {net_w}x{net_h} (1080p): the "
                         "convs (fused pairs where the library has a kernel), resize, pools, luma, SAD volumes, warps, "
-                        "FiLM, convex upsample, blendmix, elementwise and concat copies, as one HIP graph; "
-                        "render_pix (the full-resolution output) excluded; random weights, synthetic frames")
+                        "FiLM, convex upsample, blendmix, elementwise and concat copies, render_pix (bicubic), as one "
+                        "HIP graph; the host's 8-bit frame conversion excluded; random weights, synthetic frames")
     del g, f, be
     torch.cuda.empty_cache()
     return res

@@ -782,6 +782,122 @@ __global__ __launch_bounds__(kThreads) void refine_input_kernel(View q, View fl,
     o[13] = f2h(fabsf(gx) + fabsf(gy));
 }
 
+// ---- render_pix: shaders/render.wgsl:83-160 ------------------------------------------------------------------
+// One lane per output pixel: flow, visibility logits and residual upsampled bilinearly from the quarter maps, A and
+// B sampled at the displaced positions (bilinear, or bicubic: Keys a = -0.75 with every tap clamped to the border),
+// blended, + residual, clamped. All taps load from clamped addresses unconditionally (one round of loads).
+__device__ __forceinline__ float bil4(float v00, float v01, float v10, float v11, float fx, float fy) {
+    return (v00 * (1.0f - fx) + v01 * fx) * (1.0f - fy) + (v10 * (1.0f - fx) + v11 * fx) * fy;
+}
+// the Keys weights for a = -0.75 in the shader's order ((a + 2) = 1.25, (a + 3) = 2.25, 5a, 8a, 4a)
+__device__ __forceinline__ float cub1(float x) { return ((1.25f * x - 2.25f) * x) * x + 1.0f; }
+__device__ __forceinline__ float cub2(float x) { return ((-0.75f * x - -3.75f) * x + -6.0f) * x - -3.0f; }
+
+template <bool VEC>
+__device__ __forceinline__ void tap3(const View& v, uint32_t h, uint32_t w, int y, int x, float (&o)[4]) {
+    ld4<VEC>(v, (size_t)clampi(y, 0, (int)h - 1) * w + clampi(x, 0, (int)w - 1), 0, 3, o);
+}
+
+template <bool VEC, bool CUBIC>
+__device__ __forceinline__ void sample3(const View& v, uint32_t h, uint32_t w, float gx, float gy, float (&o)[3]) {
+    const int px = (int)floorf(gx), py = (int)floorf(gy);
+    const float tx = gx - (float)px, ty = gy - (float)py;
+    if constexpr (CUBIC) {
+        const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
+        const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+        float t[4][4][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) tap3<VEC>(v, h, w, py - 1 + j, px - 1 + i, t[j][i]);
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float row = t[j][0][c] * cx[0] + t[j][1][c] * cx[1] + t[j][2][c] * cx[2] + t[j][3][c] * cx[3];
+                acc = j == 0 ? row * cy[0] : acc + row * cy[j];
+            }
+            o[c] = acc;
+        }
+    } else {
+        float t00[4], t01[4], t10[4], t11[4];
+        tap3<VEC>(v, h, w, py, px, t00);
+        tap3<VEC>(v, h, w, py, px + 1, t01);
+        tap3<VEC>(v, h, w, py + 1, px, t10);
+        tap3<VEC>(v, h, w, py + 1, px + 1, t11);
+#pragma unroll
+        for (int c = 0; c < 3; c++) o[c] = bil4(t00[c], t01[c], t10[c], t11[c], tx, ty);
+    }
+}
+
+template <bool VEC, bool CUBIC>
+__global__ __launch_bounds__(kThreads) void render_kernel(View a, View b, View fl, View vis, View rt, OView out,
+                                                          uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx,
+                                                          float fsy, uint32_t flags, uint32_t items) {
+    const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
+    if (pix >= items) return;
+    const uint32_t x = pix % w, y = pix / w;
+    const float sh = (float)hq / (float)h, sw = (float)wq / (float)w;
+    const float iy = ((float)y + 0.5f) * sh - 0.5f, ix = ((float)x + 0.5f) * sw - 0.5f;
+    const int qy0 = (int)floorf(iy), qx0 = (int)floorf(ix);
+    const float qfy = iy - (float)qy0, qfx = ix - (float)qx0;
+    const uint32_t y0 = clampi(qy0, 0, (int)hq - 1), y1 = clampi(qy0 + 1, 0, (int)hq - 1);
+    const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
+    const size_t q00 = (size_t)y0 * wq + x0, q01 = (size_t)y0 * wq + x1, q10 = (size_t)y1 * wq + x0,
+                 q11 = (size_t)y1 * wq + x1;
+    float f[4], v[3], r[3];
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++)
+        f[c] = bil4(ld(fl, q00, c), ld(fl, q01, c), ld(fl, q10, c), ld(fl, q11, c), qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
+#pragma unroll
+    for (uint32_t c = 0; c < 3; c++) {
+        v[c] = bil4(ld(vis, q00, c), ld(vis, q01, c), ld(vis, q10, c), ld(vis, q11, c), qfx, qfy) * vis.scale;
+        r[c] = bil4(ld(rt, q00, c), ld(rt, q01, c), ld(rt, q10, c), ld(rt, q11, c), qfx, qfy);
+    }
+    const float m = fmaxf(v[0], fmaxf(v[1], v[2]));
+    const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
+    const float wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
+    float ca[3], cb[3];
+    sample3<VEC, CUBIC>(a, h, w, (float)x + f[0], (float)y + f[1], ca);
+    sample3<VEC, CUBIC>(b, h, w, (float)x + f[2], (float)y + f[3], cb);
+    float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
+    const float third = 1.0f / 3.0f;
+    const float ef = fabsf(ca[0] - cb[0]) * third + fabsf(ca[1] - cb[1]) * third + fabsf(ca[2] - cb[2]) * third;
+    if (flags & 2u) {  // the still test (render.wgsl:134-148)
+        float es = 0.0f;
+#pragma unroll
+        for (int dy = -1; dy <= 1; dy++)
+#pragma unroll
+            for (int dx = -1; dx <= 1; dx++) {
+                float pa[4], pb[4];
+                tap3<VEC>(a, h, w, (int)y + dy, (int)x + dx, pa);
+                tap3<VEC>(b, h, w, (int)y + dy, (int)x + dx, pb);
+#pragma unroll
+                for (int c = 0; c < 3; c++) es += fabsf(pa[c] - pb[c]);
+            }
+        es = es / 27.0f;
+        float pa[4], pb[4];
+        tap3<VEC>(a, h, w, (int)y, (int)x, pa);
+        tap3<VEC>(b, h, w, (int)y, (int)x, pb);
+#pragma unroll
+        for (int c = 0; c < 3; c++) own[c] = 0.5f * (pa[c] + pb[c]);
+        stillw = fminf(fmaxf((ef - es) / 0.04f, 0.0f), 1.0f) * (es < 0.03f ? 1.0f : 0.0f);
+    }
+    if (flags & 1u) {  // the decisive blend (render.wgsl:149-153)
+        const float k = fminf(fmaxf((ef - 0.04f) / 0.08f, 0.0f), 1.0f);
+        const float pa = wa_w >= wb_w ? 1.0f : 0.0f;
+        bwa = wa_w * (1.0f - k) + pa * k;
+        bwb = wb_w * (1.0f - k) + (1.0f - pa) * k;
+        rk = 1.0f - k;
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < 3; c++) {
+        const float mixed = ca[c] * bwa + cb[c] * bwb + r[c] * rk;
+        st(out, pix, c, fminf(fmaxf(mixed * (1.0f - stillw) + own[c] * stillw, 0.0f), 1.0f));
+    }
+}
+
 // ---- host side ----------------------------------------------------------------------------------------------------
 
 constexpr uint64_t kMaxItems = 1ull << 31;
@@ -1165,5 +1281,29 @@ extern "C" int fhc_pair_input(const fhc_tensor* ab, const fhc_tensor* q, const f
                            ow, 3u, tx, ty, PyrOut{outv(i8), outv(i16), outv(l16)});
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "pair_input: launch failed: %s", hipGetErrorString(e));
+    });
+}
+
+extern "C" int fhc_render(const fhc_tensor* a, const fhc_tensor* b, const fhc_tensor* flow, const fhc_tensor* vis,
+                          const fhc_tensor* rt, const fhc_tensor* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq,
+                          float fsx, float fsy, int cubic, uint32_t flags, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)h * w == 0) return 0;
+        if (hq == 0 || wq == 0) return fail(-1, "render: empty quarter maps (%u x %u)", hq, wq);
+        if (flags > 3) return fail(-1, "render: flags %u (bit 0 decisive, bit 1 still)", flags);
+        FHC_TRY(check(a, "render a", 3, false));
+        FHC_TRY(check(b, "render b", 3, false));
+        FHC_TRY(check(flow, "render flow", 4, false));
+        FHC_TRY(check(vis, "render vis", 3, true));
+        FHC_TRY(check(rt, "render rt", 3, false));
+        FHC_TRY(check(out, "render out", 3, false, true));
+        const bool v = vec4(4, {a, b});
+        return launch("render", (uint64_t)h * w, [&](dim3 g, uint32_t items) {
+            auto k = cubic ? (v ? render_kernel<true, true> : render_kernel<false, true>)
+                           : (v ? render_kernel<true, false> : render_kernel<false, false>);
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(a), in(b), in(flow), in(vis), in(rt),
+                               outv(out), h, w, hq, wq, fsx, fsy, flags, items);
+        });
     });
 }

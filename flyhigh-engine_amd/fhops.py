@@ -69,6 +69,7 @@ def _lib():
             "fhc_chcopy": [T, T, U, U, U, U, P],
             "fhc_pair_pyramid": [T, T, T, T, U, U, P],
             "fhc_pair_input": [T, T, T, T, T, U, U, U, U, P],
+            "fhc_render": [T, T, T, T, T, T, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U, P],
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
@@ -245,3 +246,14 @@ def pair_input(ab, q, i8, i16, l16, oh, ow, stream=None):
     _, ih, iw, _ = ab.shape
     _run("pair_input", _lib().fhc_pair_input(_ref(ab), _ref(_v(q)), _ref(_v(i8)), _ref(_v(i16)), _ref(_v(l16)), ih,
                                              iw, oh, ow, _stream_handle(stream)))
+
+
+def render(a, b, flow, vis, rt, cubic=True, flags=0, fsx=1.0, fsy=1.0, out=None, stream=None):
+    """render_pix: a, b at full size; flow (4), vis (3), rt (3) at quarter size; returns / writes 3 channels."""
+    a, b, flow, vis, rt = _v(a), _v(b), _v(flow), _v(vis), _v(rt)
+    _, h, w, _ = a.shape
+    _, hq, wq, _ = flow.shape
+    o = _out(out, a, 1, h, w, 3)
+    _run("render", _lib().fhc_render(_ref(a), _ref(b), _ref(flow), _ref(vis), _ref(rt), _ref(o), h, w, hq, wq, fsx,
+                                     fsy, int(cubic), flags, _stream_handle(stream)))
+    return o.t

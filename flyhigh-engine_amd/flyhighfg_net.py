@@ -1,5 +1,6 @@
 """One FlyHighFG pair() and mid() end to end: every op of models/graph.json from the network-size inputs A, B to the
-network's outputs (R_t, flow_tq, vis_tq, the streaming state), as the reference's planner walks it
+network's outputs (the rendered in-between picture, R_t, flow_tq, vis_tq, the streaming state), as the reference's
+planner walks it
 (crates/flyhigh-engine/src/net/build.rs:186-450), over a backend.
 
 The program is written once (``FlyHighFG.pair`` / ``mid``) against a small backend interface: ``GpuBackend`` runs it
@@ -8,8 +9,8 @@ captured in a HIP graph; a checker can run the same program over the CPU oracle 
 NHWC f16 buffers (n, h, w, cstride) with the channel stride padded to 8 where a conv or an 8-byte path reads them;
 the graph's slices and scales are views (``V``) and its concats are buffers the producers write into by slice, so
 only a scaled input of a concat costs a copy (as the reference's chcopy does). The A and B branches share weights
-and run as a batch of 2 where their consumers read one tensor (resize, the first encoder pair, the first pool);
-render_pix (the full-resolution output) is not part of the network and not run here.
+and run as a batch of 2 where their consumers read one tensor (resize, the first encoder pair, the first pool). The
+frame I/O around the network (rgba_in / rgba_out: the host's 8-bit frames) is not run here.
 
 Differences of launch structure from the reference (same arithmetic): the encoders' second pair and the second pool
 run per image so that their outputs land in their slices of the 279-channel concat; consecutive convs whose
@@ -238,6 +239,10 @@ class GpuBackend(ComposedChains):
     def blendmix(self, wa: V, wb: V, vis: V, out: V):
         self.fh.blendmix(self._v(wa), self._v(wb), self._v(vis), out=self._v(out), stream=self.stream)
 
+    def render(self, a: V, b: V, flow: V, vis: V, rt: V, out: V, cubic: bool, flags: int):
+        self.fh.render(self._v(a), self._v(b), self._v(flow), self._v(vis), self._v(rt), cubic, flags, flow.scale,
+                       flow.scale, out=self._v(out), stream=self.stream)
+
     # the fused chains (one launch each) unless asked for the ops one by one
     def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
         if not self.chains:
@@ -268,10 +273,13 @@ class GpuBackend(ComposedChains):
 
 class FlyHighFG:
     """The buffers of one frame pair at network size net_w x net_h and the program of pair() and mid(t) over them.
-    Outputs after mid(): ``up7`` (flow_tq channels 0-3, vis_tq 4-6, quarter size), ``Rt`` (R_t, 3 channels),
-    ``state_out`` (f16b then flow16, 1/16 size); ``o`` holds the coarse head (conf, gate, sal in channels 7-11)."""
+    Outputs after mid(): ``out`` (render_pix, the in-between picture), ``up7`` (flow_tq channels 0-3, vis_tq 4-6,
+    quarter size), ``Rt`` (R_t, 3 channels), ``state_out`` (f16b then flow16, 1/16 size); ``o`` holds the coarse head
+    (conf, gate, sal in channels 7-11). cubic / render_flags: render_pix's sampler (the model's manifest asks for
+    bicubic, models/flyhighfg.json:67) and mode word (0: neither the decisive blend nor the still test, the
+    engine's defaults, options.rs:306-327)."""
 
-    def __init__(self, be, net_w: int = 864, net_h: int = 480):
+    def __init__(self, be, net_w: int = 864, net_h: int = 480, cubic: bool = True, render_flags: int = 0):
         self.be = be
         qh, qw = net_h // 4, net_w // 4
         e8h, e8w = (qh - 1) // 2 + 1, (qw - 1) // 2 + 1
@@ -305,6 +313,8 @@ class FlyHighFG:
         self.rx = Z(1, qh, qw, 16)             # rwa 0 | rwb 3 | vis_tq 6 | flow_tq20 9 | lg 13
         self.rq1, self.rq2, self.rq3 = (Z(1, qh, qw, 24) for _ in range(3))
         self.rr, self.Rt = Z(1, qh, qw, 8), Z(1, qh, qw, 8)
+        self.out = Z(1, net_h, net_w, 4)        # render_pix: the in-between picture at network size
+        self.cubic, self.render_flags = cubic, render_flags
 
     def pair(self):
         """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1)."""
@@ -334,7 +344,7 @@ class FlyHighFG:
         be.binary(V(self.fv), V(self.d), 7, V(self.fv))                                       # flow, vis += d
 
     def mid(self, t: float, W: Optional[dict]):
-        """mid(t): models/graph.json ops 44-81 (render_pix, op 82, excluded). With W None the FiLM vector of t must
+        """mid(t): models/graph.json ops 44-82, render_pix included. With W None the FiLM vector of t must
         already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes it that way, as the
         reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22)."""
         be = self.be
@@ -350,6 +360,8 @@ class FlyHighFG:
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
         be.pair("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), False)        # 79, 80
         be.unary(V(self.rr), 3, V(self.Rt), 2)                                                # 81: affine_out
+        be.render(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.up7, 0), V(self.up7, 4), V(self.Rt),
+                  V(self.out), self.cubic, self.render_flags)                                 # 82: render_pix
 
 
 def cpu_threads():

@@ -104,6 +104,17 @@ int fhc_unary(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h
 int fhc_chcopy(const fhc_tensor* x, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                void* stream);
 
+/* render_pix: flow (4 channels: A's x, y then B's, times fsx for x and fsy for y), vis (3 logits, read scale) and rt
+ * (3 channels) upsampled bilinearly from hq x wq to h x w; a warped by the forward flow and b by the backward one
+ * (bilinear, or bicubic with cubic != 0: Keys a = -0.75, every tap clamped to the border), blended by the visibility
+ * weights, + rt, clamped to [0, 1], 3 channels into out. flags: bit 0 the decisive blend, bit 1 the still test.
+ * Replaces Gpu::render_ex_to (ops/render.rs:43-101, shaders/render.wgsl:83-160), the "render_pix" arm
+ * (net/build.rs:364-378); the static-age variant is not built. Views of a and b with 8-byte pixels (4-channel
+ * strides and offsets) read each tap with one load. */
+int fhc_render(const fhc_tensor* a, const fhc_tensor* b, const fhc_tensor* flow, const fhc_tensor* vis,
+               const fhc_tensor* rt, const fhc_tensor* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx,
+               float fsy, int cubic, uint32_t flags, void* stream);
+
 /* ---- The graph's op chains, fused. Each computes what its ops compute one after another (the same f32 operations
  * and f16 roundings at the tensors the ops store); no reference counterpart as one call: each replaces the listed
  * planner arms run in sequence. A and B arrive as a batch of 2. */

@@ -275,3 +275,100 @@ void fho_chcopy(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, 
                 x->scale == 1.0f ? v : fho_f32_to_f16(fho_f16_to_f32(v) * x->scale);
         }
 }
+
+/* ---- render_pix: shaders/render.wgsl ---------------------------------------------------------------------- */
+
+/* bil4 (render.wgsl:29-31) */
+static float bil4(float v00, float v01, float v10, float v11, float fx, float fy) {
+    return (v00 * (1.0f - fx) + v01 * fx) * (1.0f - fy) + (v10 * (1.0f - fx) + v11 * fx) * fy;
+}
+/* Keys cubic convolution, a = -0.75 (render.wgsl:50-53): (a + 2) = 1.25, (a + 3) = 2.25, 5a = -3.75, 8a = -6,
+ * 4a = -3, in the shader's order */
+static float cub1(float x) { return ((1.25f * x - 2.25f) * x) * x + 1.0f; }
+static float cub2(float x) { return ((-0.75f * x - -3.75f) * x + -6.0f) * x - -3.0f; }
+static float rpx(const fho_view* v, uint32_t h, uint32_t w, int y, int x, uint32_t ch) {
+    return rd(v, h, w, 0, clampi(y, 0, (int)h - 1), clampi(x, 0, (int)w - 1), ch);
+}
+/* one bicubic sample (render.wgsl:54-81) */
+static float cubic_at(const fho_view* v, uint32_t h, uint32_t w, uint32_t ch, float gx, float gy) {
+    const int px = (int)floorf(gx), py = (int)floorf(gy);
+    const float tx = gx - (float)px, ty = gy - (float)py;
+    const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
+    const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+    float acc = 0.0f;
+    for (int j = 0; j < 4; j++) {
+        const int yy = py - 1 + j;
+        const float row = rpx(v, h, w, yy, px - 1, ch) * cx[0] + rpx(v, h, w, yy, px, ch) * cx[1] +
+                          rpx(v, h, w, yy, px + 1, ch) * cx[2] + rpx(v, h, w, yy, px + 2, ch) * cx[3];
+        acc = j == 0 ? row * cy[0] : acc + row * cy[j];
+    }
+    return acc;
+}
+/* one bilinear sample with clamped corners (render.wgsl:43-48, 105-114) */
+static float bil_at(const fho_view* v, uint32_t h, uint32_t w, uint32_t ch, float gx, float gy) {
+    const int x0 = (int)floorf(gx), y0 = (int)floorf(gy);
+    const float ax = gx - (float)x0, ay = gy - (float)y0;
+    return bil4(rpx(v, h, w, y0, x0, ch), rpx(v, h, w, y0, x0 + 1, ch), rpx(v, h, w, y0 + 1, x0, ch),
+                rpx(v, h, w, y0 + 1, x0 + 1, ch), ax, ay);
+}
+static float clampf01(float v) { return fminf(fmaxf(v, 0.0f), 1.0f); }
+
+void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, const fho_view* vis, const fho_view* rt,
+                const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx, float fsy,
+                int cubic, uint32_t flags) {
+    const float sh = (float)hq / (float)h, sw = (float)wq / (float)w;
+    for (uint32_t y = 0; y < h; y++)
+        for (uint32_t x = 0; x < w; x++) {
+            const float iy = ((float)y + 0.5f) * sh - 0.5f, ix = ((float)x + 0.5f) * sw - 0.5f;
+            const int qy0 = (int)floorf(iy), qx0 = (int)floorf(ix);
+            const float qfy = iy - (float)qy0, qfx = ix - (float)qx0;
+            const int y0 = clampi(qy0, 0, (int)hq - 1), y1 = clampi(qy0 + 1, 0, (int)hq - 1);
+            const int x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
+            float f[4], v[3], r[3];
+            for (uint32_t c = 0; c < 4; c++)
+                f[c] = bil4(rd(flow, hq, wq, 0, y0, x0, c), rd(flow, hq, wq, 0, y0, x1, c), rd(flow, hq, wq, 0, y1, x0, c),
+                            rd(flow, hq, wq, 0, y1, x1, c), qfx, qfy) *
+                       ((c & 1u) == 0 ? fsx : fsy);
+            for (uint32_t c = 0; c < 3; c++) {
+                v[c] = bil4(rd(vis, hq, wq, 0, y0, x0, c), rd(vis, hq, wq, 0, y0, x1, c), rd(vis, hq, wq, 0, y1, x0, c),
+                            rd(vis, hq, wq, 0, y1, x1, c), qfx, qfy) *
+                       vis->scale;
+                r[c] = bil4(rd(rt, hq, wq, 0, y0, x0, c), rd(rt, hq, wq, 0, y0, x1, c), rd(rt, hq, wq, 0, y1, x0, c),
+                            rd(rt, hq, wq, 0, y1, x1, c), qfx, qfy);
+            }
+            const float m = fmaxf(v[0], fmaxf(v[1], v[2]));
+            const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
+            const float wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
+            const float gxa = (float)x + f[0], gya = (float)y + f[1], gxb = (float)x + f[2], gyb = (float)y + f[3];
+            float ca[3], cb[3];
+            for (uint32_t c = 0; c < 3; c++) {
+                ca[c] = cubic ? cubic_at(a, h, w, c, gxa, gya) : bil_at(a, h, w, c, gxa, gya);
+                cb[c] = cubic ? cubic_at(b, h, w, c, gxb, gyb) : bil_at(b, h, w, c, gxb, gyb);
+            }
+            float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
+            const float third = 1.0f / 3.0f;
+            const float ef = fabsf(ca[0] - cb[0]) * third + fabsf(ca[1] - cb[1]) * third + fabsf(ca[2] - cb[2]) * third;
+            if (flags & 2u) { /* render.wgsl:134-148 */
+                float es = 0.0f;
+                for (int dy = -1; dy <= 1; dy++)
+                    for (int dx = -1; dx <= 1; dx++)
+                        for (uint32_t c = 0; c < 3; c++)
+                            es += fabsf(rpx(a, h, w, (int)y + dy, (int)x + dx, c) - rpx(b, h, w, (int)y + dy, (int)x + dx, c));
+                es = es / 27.0f;
+                for (uint32_t c = 0; c < 3; c++)
+                    own[c] = 0.5f * (rd(a, h, w, 0, (int)y, (int)x, c) + rd(b, h, w, 0, (int)y, (int)x, c));
+                stillw = fminf(fmaxf((ef - es) / 0.04f, 0.0f), 1.0f) * (es < 0.03f ? 1.0f : 0.0f);
+            }
+            if (flags & 1u) { /* render.wgsl:149-153 */
+                const float k = fminf(fmaxf((ef - 0.04f) / 0.08f, 0.0f), 1.0f);
+                const float pa = wa_w >= wb_w ? 1.0f : 0.0f;
+                bwa = wa_w * (1.0f - k) + pa * k;
+                bwb = wb_w * (1.0f - k) + (1.0f - pa) * k;
+                rk = 1.0f - k;
+            }
+            for (uint32_t c = 0; c < 3; c++) {
+                const float mixed = ca[c] * bwa + cb[c] * bwb + r[c] * rk;
+                wr(out, h, w, 0, y, x, c, clampf01(mixed * (1.0f - stillw) + own[c] * stillw));
+            }
+        }
+}

@@ -63,6 +63,13 @@ void fho_unary(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, u
 /* channel copy of a view into an output view, f16(x * scale) unless the scale is 1 (then the bits are copied):
  * one input of shaders/chcopy.wgsl:19-36 */
 void fho_chcopy(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, uint32_t w, uint32_t c);
+/* render_pix: flow_tq (4 channels at the view's c0, x scaled by fsx, y by fsy), vis_tq (3 logits, read scale) and
+ * R_t (3 channels) upsampled bilinearly from hq x wq to h x w; A warped by the forward flow, B by the backward one
+ * (bilinear, or bicubic with cubic != 0); blended by the visibility weights; + R_t; clamped to [0, 1]. flags bit 0
+ * the decisive blend, bit 1 the still test: shaders/render.wgsl:83-160. */
+void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, const fho_view* vis, const fho_view* rt,
+                const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx, float fsy,
+                int cubic, uint32_t flags);
 
 #ifdef __cplusplus
 }

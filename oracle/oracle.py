@@ -149,6 +149,7 @@ def _ops_lib():
             "fho_binary": [V, V, V, U, U, U, U, U, I],
             "fho_unary": [V, V, U, U, U, U, I, ctypes.c_float, ctypes.c_float],
             "fho_chcopy": [V, V, U, U, U, U],
+            "fho_render": [V, V, V, V, V, V, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -248,4 +249,14 @@ def chcopy(x, c, c0=0, scale=1.0):
     n, h, w, _ = x.shape
     y = _out(n, h, w, c)
     _ops_lib().fho_chcopy(_view(x, c0, scale), _view(y), n, h, w, c)
+    return y
+
+
+def render(a, b, flow, vis, rt, hq, wq, cubic=True, flags=0, a_c0=0, b_c0=0, flow_c0=0, fsx=1.0, fsy=1.0, vis_c0=0,
+           vis_scale=1.0, rt_c0=0):
+    """a, b: (1, h, w, cs) pictures; flow, vis, rt: (1, hq, wq, cs) quarter-size maps; returns (1, h, w, 3)."""
+    _, h, w, _ = a.shape
+    y = _out(1, h, w, 3)
+    _ops_lib().fho_render(_view(a, a_c0), _view(b, b_c0), _view(flow, flow_c0), _view(vis, vis_c0, vis_scale),
+                          _view(rt, rt_c0), _view(y), h, w, hq, wq, fsx, fsy, int(cubic), flags)
     return y

@@ -80,3 +80,9 @@ class CpuBackend(ComposedChains):
     def blendmix(self, wa, wb, vis, out):
         self._put(out, 3, oracle.blendmix(wa.buf, wb.buf, vis.buf, vis_c0=vis.c0, vis_scale=vis.scale,
                                           wa_c0=wa.c0, wb_c0=wb.c0))
+
+    def render(self, a, b, flow, vis, rt, out, cubic, flags):
+        _, hq, wq, _ = flow.buf.shape
+        self._put(out, 3, oracle.render(a.buf, b.buf, flow.buf, vis.buf, rt.buf, hq, wq, cubic=cubic, flags=flags,
+                                        a_c0=a.c0, b_c0=b.c0, flow_c0=flow.c0, fsx=flow.scale, fsy=flow.scale,
+                                        vis_c0=vis.c0, vis_scale=vis.scale, rt_c0=rt.c0))

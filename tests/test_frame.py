@@ -13,7 +13,7 @@ from fhtest import f16_bits
 from frame_oracle import CpuBackend
 import flyhighfg_net as net
 
-OUTPUTS = [("up7", 7), ("Rt", 3), ("state_out", 76), ("o", 12), ("h", 48), ("cin", 279)]
+OUTPUTS = [("out", 3), ("up7", 7), ("Rt", 3), ("state_out", 76), ("o", 12), ("h", 48), ("cin", 279)]
 
 
 def inputs(seed, net_w, net_h):

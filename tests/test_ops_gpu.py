@@ -235,6 +235,29 @@ def test_chcopy_into_a_concat_slice_matches_oracle(c, c0, scale):
     check_slice(buf, out, 5, c, want, "chcopy")
 
 
+@pytest.mark.parametrize("cubic,flags,cs", [(True, 0, 4), (False, 0, 4), (True, 0, 3), (True, 1, 4), (False, 2, 4),
+                                             (True, 3, 3)])
+def test_render_matches_oracle(cubic, flags, cs):
+    """Bit-exact except where expf's last bit moves the visibility weights (an f16 ulp or two of the output) or,
+    with the decisive blend, flips which picture is trusted where the two weights are equal to the last bit."""
+    say("render", cubic, flags, cs)
+    fh = fhops()
+    rng = np.random.default_rng(7 + flags + 10 * cubic + cs)
+    h, w, hq, wq = 120, 216, 30, 54
+    ab = rand(rng, (2, h, w, cs), 0, 1)
+    up = np.zeros((1, hq, wq, 8), np.float32)
+    up[..., :4] = rng.uniform(-6, 6, (hq, wq, 4))
+    up[..., 4:7] = rng.normal(0, 2, (hq, wq, 3))
+    up = f16_bits(up)
+    rt = rand(rng, (1, hq, wq, 4), -0.1, 0.1)
+    want = oracle.render(ab[:1].copy(), ab[1:].copy(), up, up, rt, hq, wq, cubic=cubic, flags=flags, vis_c0=4)
+    dab, dup = dev(ab), dev(up)
+    got = host(fh.render(dab[0:1], dab[1:2], dup, fh.View(dup, 4), dev(rt), cubic=cubic, flags=flags))
+    d = np.abs(got.view(np.float16).astype(np.float32) - want.view(np.float16).astype(np.float32))
+    assert np.mean(d == 0) > 0.99, f"only {np.mean(d == 0):.4f} bit-equal"
+    assert d.max() <= (0.5 if flags & 1 else 2e-3), d.max()
+
+
 def test_empty_inputs_are_no_ops_and_bad_views_are_errors():
     import torch
     fh = fhops()

@@ -263,3 +263,60 @@ def test_chcopy_copies_bits_at_scale_one_and_rounds_scaled_values():
     assert np.array_equal(oracle.chcopy(x, 4, c0=2), x[..., 2:])
     got = oracle.chcopy(x, 3, c0=1, scale=0.125)
     assert np.array_equal(got, (val(x)[..., 1:4] * np.float32(0.125)).astype(np.float16).view(np.uint16))
+
+
+# ---- render_pix (shaders/render.wgsl) ------------------------------------------------------------------------------
+
+def _render_maps(hq, wq, flow=(0.0, 0.0, 0.0, 0.0), logits=(0.0, 0.0, 0.0), r=0.0):
+    fl = np.zeros((1, hq, wq, 4), np.float32) + np.asarray(flow, np.float32)
+    vis = np.zeros((1, hq, wq, 3), np.float32) + np.asarray(logits, np.float32)
+    return f16(fl), f16(vis), f16(np.full((1, hq, wq, 3), r, np.float32))
+
+
+@pytest.mark.parametrize("cubic", [False, True])
+def test_render_of_still_equal_pictures_is_the_picture_plus_the_residual(cubic):
+    h, w = 16, 24
+    pic = f16(rng.uniform(0.1, 0.8, (1, h, w, 3)))
+    fl, vis, rt = _render_maps(h // 4, w // 4)
+    assert np.array_equal(oracle.render(pic, pic, fl, vis, rt, h // 4, w // 4, cubic=cubic), pic)  # cubw(0) = e1
+    fl, vis, rt = _render_maps(h // 4, w // 4, r=0.125)
+    got = val(oracle.render(pic, pic, fl, vis, rt, h // 4, w // 4, cubic=cubic))
+    assert ulp_close(f16(got), np.minimum(val(pic) + np.float32(0.125), 1))
+
+
+@pytest.mark.parametrize("cubic", [False, True])
+def test_render_warp_matches_torch_grid_sample(cubic):
+    """render.wgsl:6-7 names its sampler: torch.grid_sample with align_corners=True and border padding (bicubic: Keys
+    a = -0.75, which does not reproduce linear ramps, so a library check rather than a closed form)."""
+    torch = pytest.importorskip("torch")
+    h, w = 20, 28
+    pic = f16(rng.uniform(0.05, 0.95, (1, h, w, 3)))
+    fx, fy = 1.3, -0.6
+    fl, vis, rt = _render_maps(h // 4, w // 4, flow=(fx, fy, 0.0, 0.0), logits=(40.0, 0.0, 0.0))
+    got = val(oracle.render(pic, pic, fl, vis, rt, h // 4, w // 4, cubic=cubic))
+    yy, xx = np.mgrid[0:h, 0:w].astype(np.float64)
+    grid = np.stack([-1 + 2 * (xx + fx) / (w - 1), -1 + 2 * (yy + fy) / (h - 1)], -1)[None]
+    t = torch.from_numpy(val(pic).astype(np.float64)).permute(0, 3, 1, 2)
+    ref = torch.nn.functional.grid_sample(t, torch.from_numpy(grid), mode="bicubic" if cubic else "bilinear",
+                                          padding_mode="border", align_corners=True)
+    want = np.clip(ref.permute(0, 2, 3, 1).numpy(), 0, 1)
+    assert np.allclose(got, want, atol=2e-3)
+
+
+def test_render_visibility_picks_the_dominant_picture_and_clamps():
+    h, w = 8, 8
+    a, b = f16(np.full((1, h, w, 3), 0.25, np.float32)), f16(np.full((1, h, w, 3), 0.75, np.float32))
+    for logits, want in (((30.0, 0.0, 0.0), 0.25), ((0.0, 30.0, 0.0), 0.75), ((0.0, 0.0, 30.0), 0.5)):
+        fl, vis, rt = _render_maps(2, 2, logits=logits)
+        assert ulp_close(oracle.render(a, b, fl, vis, rt, 2, 2), np.full((1, h, w, 3), want, np.float32))
+    fl, vis, rt = _render_maps(2, 2, r=0.5)
+    assert np.all(val(oracle.render(b, b, fl, vis, rt, 2, 2)) == 1.0)  # 0.75 + 0.5 clamps to 1
+
+
+def test_render_decisive_blend_takes_the_trusted_picture_where_they_disagree():
+    h, w = 8, 8
+    a, b = f16(np.full((1, h, w, 3), 0.2, np.float32)), f16(np.full((1, h, w, 3), 0.8, np.float32))
+    fl, vis, rt = _render_maps(2, 2, logits=(1.0, 0.0, 0.0), r=0.05)
+    soft = val(oracle.render(a, b, fl, vis, rt, 2, 2))
+    hard = val(oracle.render(a, b, fl, vis, rt, 2, 2, flags=1))
+    assert np.all(soft > 0.3) and np.allclose(hard, 0.2, atol=1e-3)  # |A - B| = 0.6 >> 0.12: k = 1, no residual
