@@ -782,6 +782,31 @@ __global__ __launch_bounds__(kThreads) void refine_input_kernel(View q, View fl,
     o[13] = f2h(fabsf(gx) + fabsf(gy));
 }
 
+// ---- the encoders' outputs into their concat slices (graph.json ops 7, 13 and 26's f16a, f16b; 43's f16b) -----
+// x holds the two pictures' features as a batch (2, h, w, c); image i goes to channels c0 + i * c of out (batch 1),
+// and image 1 also to `also` (the streaming state's f16b), when given. Bits are copied. One lane per (pixel,
+// image, 4 channels); VEC: 8-byte copies.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void fold_pair_kernel(View x, OView out, OView also, uint32_t hw, uint32_t c,
+                                                             uint32_t groups, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t g = t % groups, r = t / groups, img = r % 2, pix = r / 2, ch = g * 4;
+    const uint16_t* src = x.p + ((size_t)img * hw + pix) * x.cs + x.c0 + ch;
+    uint16_t* dst = out.p + (size_t)pix * out.cs + out.c0 + img * c + ch;
+    uint16_t* dst2 = also.p ? also.p + (size_t)pix * also.cs + also.c0 + ch : nullptr;
+    if constexpr (VEC) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        *reinterpret_cast<uint2*>(dst) = v;
+        if (img == 1 && dst2) *reinterpret_cast<uint2*>(dst2) = v;
+    } else {
+        for (uint32_t i = 0; i < 4 && ch + i < c; i++) {
+            dst[i] = src[i];
+            if (img == 1 && dst2) dst2[i] = src[i];
+        }
+    }
+}
+
 // ---- render_pix: shaders/render.wgsl:83-160 ------------------------------------------------------------------
 // One lane per output pixel: flow, visibility logits and residual upsampled bilinearly from the quarter maps, A and
 // B sampled at the displaced positions (bilinear, or bicubic: Keys a = -0.75 with every tap clamped to the border),
@@ -1304,6 +1329,27 @@ extern "C" int fhc_render(const fhc_tensor* a, const fhc_tensor* b, const fhc_te
                            : (v ? render_kernel<true, false> : render_kernel<false, false>);
             hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(a), in(b), in(flow), in(vis), in(rt),
                                outv(out), h, w, hq, wq, fsx, fsy, flags, items);
+        });
+    });
+}
+
+extern "C" int fhc_fold_pair(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h,
+                             uint32_t w, uint32_t c, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)h * w * c == 0) return 0;
+        FHC_TRY(check(x, "fold_pair x", c, false));
+        FHC_TRY(check(out, "fold_pair out", 2 * c, false, true));
+        if (also) FHC_TRY(check(also, "fold_pair also", c, false, true));
+        fhc_tensor out1 = *out;  // image 1's slice must be aligned too for the vector path
+        out1.c0 += c;
+        const bool v = also ? vec4(c, {x, out, &out1, also}) : vec4(c, {x, out, &out1});
+        const uint32_t groups = (c + 3) / 4;
+        const OView a2 = also ? outv(also) : OView{nullptr, 0, 0};
+        return launch("fold_pair", (uint64_t)h * w * 2 * groups, [&](dim3 g, uint32_t items) {
+            auto k = v ? fold_pair_kernel<true> : fold_pair_kernel<false>;
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), a2, h * w, c, groups,
+                               items);
         });
     });
 }

@@ -70,6 +70,7 @@ def _lib():
             "fhc_pair_pyramid": [T, T, T, T, U, U, P],
             "fhc_pair_input": [T, T, T, T, T, U, U, U, U, P],
             "fhc_render": [T, T, T, T, T, T, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U, P],
+            "fhc_fold_pair": [T, T, T, U, U, U, P],
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
@@ -257,3 +258,13 @@ def render(a, b, flow, vis, rt, cubic=True, flags=0, fsx=1.0, fsy=1.0, out=None,
     _run("render", _lib().fhc_render(_ref(a), _ref(b), _ref(flow), _ref(vis), _ref(rt), _ref(o), h, w, hq, wq, fsx,
                                      fsy, int(cubic), flags, _stream_handle(stream)))
     return o.t
+
+
+def fold_pair(x, out, also=None, stream=None):
+    """Images 0 and 1 of x (2, h, w, c) side by side into out's channels (out.c0, out.c0 + c); image 1 also into
+    `also` when given."""
+    x = _v(x)
+    _, h, w, _ = x.shape
+    c = x.channels
+    _run("fold_pair", _lib().fhc_fold_pair(_ref(x), _ref(_v(out)), None if also is None else _ref(_v(also)), h, w, c,
+                                           _stream_handle(stream)))

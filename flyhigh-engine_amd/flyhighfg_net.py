@@ -12,8 +12,8 @@ only a scaled input of a concat costs a copy (as the reference's chcopy does). T
 and run as a batch of 2 where their consumers read one tensor (resize, the first encoder pair, the first pool). The
 frame I/O around the network (rgba_in / rgba_out: the host's 8-bit frames) is not run here.
 
-Differences of launch structure from the reference (same arithmetic): the encoders' second pair and the second pool
-run per image so that their outputs land in their slices of the 279-channel concat; consecutive convs whose
+Differences of launch structure from the reference (same arithmetic): the encoders' outputs are copied into their
+slices of the 279-channel concat (and f16b into the streaming state) by one copy launch; consecutive convs whose
 intermediate has no other reader run as fused pairs on the GPU when asked; and flow and vis share one buffer, so
 the fine loop's two adds are one. (Independent branches on a second stream, joined by events, made the captured frame
 slower, 241 against 225 us: the graph runtime did not overlap them.)
@@ -94,6 +94,12 @@ class ComposedChains:
     def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
         self.interp(ab, 3, q, oh, ow, True)
         self.pair_pyramid(q, i8, i16, l16)
+
+    def fold_pair(self, x: V, c: int, out: V, also: Optional[V]):
+        for i in range(2):
+            self.chcopy(V(self.image(x.buf, i), x.c0), c, V(out.buf, out.c0 + c * i))
+        if also is not None:
+            self.chcopy(V(self.image(x.buf, 1), x.c0), c, also)
 
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
@@ -244,6 +250,11 @@ class GpuBackend(ComposedChains):
                        flow.scale, out=self._v(out), stream=self.stream)
 
     # the fused chains (one launch each) unless asked for the ops one by one
+    def fold_pair(self, x: V, c: int, out: V, also: Optional[V]):
+        if not self.chains:
+            return super().fold_pair(x, c, out, also)
+        self.fh.fold_pair(self._v(x), self._v(out), None if also is None else self._v(also), stream=self.stream)
+
     def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
         if not self.chains:
             return super().pair_input(ab, q, i8, i16, l16, oh, ow)
@@ -290,7 +301,8 @@ class FlyHighFG:
         self.aq = Z(2, qh, qw, 8)              # aq, bq
         self.e1 = Z(2, e8h, e8w, 40)           # a_e1, b_e1
         self.f8 = Z(2, e8h, e8w, 40)           # f8a, f8b
-        self.e3 = [Z(1, e16h, e16w, 72) for _ in range(2)]
+        self.e3 = Z(2, e16h, e16w, 72)         # a_e3, b_e3
+        self.f16 = Z(2, e16h, e16w, 72)        # f16a, f16b (then folded into the concat)
         self.i8 = Z(2, e8h, e8w, 8)            # i8a, i8b
         self.cin = Z(1, e16h, e16w, 280)       # f16a 0 | f16b 72 | img16 144 | side 150 | state 154 | cv 230
         self.l16 = Z(1, e16h, e16w, 2)         # la | lb
@@ -320,19 +332,17 @@ class FlyHighFG:
         """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1)."""
         be, S = self.be, self.shape
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
-        img = be.image
         be.pair_input(V(self.AB), V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16), qh, qw)  # 0-1, 14-24
         be.sad(V(self.l16, 0), V(self.l16, 1), V(self.cin, 230), 3)                           # 25, 26; 19-20 zeros
         be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)                 # 2-4, 8-10
-        for i in range(2):                                                                    # 5-7, 11-13
-            be.pair("enc.e3", "enc.e4", V(img(self.f8, i)), V(self.e3[i]), V(self.cin, 72 * i), True)
+        be.pair("enc.e3", "enc.e4", V(self.f8), V(self.e3), V(self.f16), True)                # 5-7, 11-13
+        be.fold_pair(V(self.f16), 72, V(self.cin, 0), V(self.state_out, 0))                   # 26, 43: f16a f16b
         be.conv("coarse.c1", V(self.cin), V(self.ch1))                                        # 27
         be.conv("coarse.c2", V(self.ch1), V(self.ch2))                                        # 28
         be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30
         be.conv("coarse.c4", V(self.ch3r), V(self.hc))                                        # 31
         be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
-        be.chcopy(V(self.cin, 72), 72, V(self.state_out, 0))                                  # 43: state_out
-        be.chcopy(V(self.o, 0, 16.0), 4, V(self.state_out, 72))
+        be.chcopy(V(self.o, 0, 16.0), 4, V(self.state_out, 72))                               # 43: flow16
         be.interp(V(self.o, 0, 16.0), 4, V(self.fv, 0), e8h, e8w, False)                      # 33-34, 39: flow
         be.interp(V(self.o, 4), 3, V(self.fv, 4), e8h, e8w, False)                            # 35, 40: vis
         # the fine loop, K = 1 (op 42): h enters as zeros (op 41: the fx slice is never written)

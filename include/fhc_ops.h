@@ -131,6 +131,12 @@ int fhc_pair_pyramid(const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor
 int fhc_pair_input(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16,
                    const fhc_tensor* l16, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow, void* stream);
 
+/* graph.json ops 7, 13 (the encoders' outputs f16a, f16b), their places in the concat of op 26 and f16b's in the
+ * streaming state of op 43: x (2, h, w, c) holds both pictures' features as a batch; image i is copied to channels
+ * c0 + i * c of out (batch 1) and image 1 also to `also` when not NULL. Lets the encoders run as one batch. */
+int fhc_fold_pair(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h, uint32_t w,
+                  uint32_t c, void* stream);
+
 /* graph.json op 42's body up to the concat: f8 (2, h, w, c) and i8 (2, h, w, 3) warped by flow (1, h, w: channels
  * 0-1 for A, 2-3 for B, at its read scale), written into fx's slices c0: wa, +c: wb, +2c: ia, +2c+3: ib, +2c+6: the
  * scaled flow (4 channels); the warped pictures' luma into l8's channel image (warp.wgsl, luma.wgsl, chcopy.wgsl). */
