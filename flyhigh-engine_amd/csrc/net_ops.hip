@@ -807,6 +807,35 @@ __global__ __launch_bounds__(kThreads) void fold_pair_kernel(View x, OView out, 
     }
 }
 
+// ---- the coarse head's outputs (graph.json ops 33-40 and 43's flow16) ------------------------------------------
+// o (1, hi, wi) holds the coarse flow (channels 0-3, read times fs: flow16) and visibility logits (4-6). Out (1, oh, ow)
+// gets both resized bilinearly (interp.wgsl, align_corners false; the scale applies to the result): flow 0-3, vis
+// 4-6; `state` (when given) gets the scaled flow itself at the input size (chcopy). One lane per output pixel; the
+// lanes of the first hi x wi pixels also write the state.
+__global__ __launch_bounds__(kThreads) void coarse_up_kernel(View o, OView out, OView state, uint32_t hi, uint32_t wi,
+                                                             uint32_t oh, uint32_t ow, float fs, uint32_t items) {
+    const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
+    if (pix >= items) return;
+    const uint32_t ox = pix % ow, oy = pix / ow;
+    const float sh = (float)hi / (float)oh, sw = (float)wi / (float)ow;
+    const float fiy = ((float)oy + 0.5f) * sh - 0.5f, fix = ((float)ox + 0.5f) * sw - 0.5f;
+    const int y0 = (int)floorf(fiy), x0 = (int)floorf(fix);
+    const float fy = fiy - (float)y0, fx = fix - (float)x0;
+    const size_t r0 = (size_t)clampi(y0, 0, (int)hi - 1) * wi, r1 = (size_t)clampi(y0 + 1, 0, (int)hi - 1) * wi;
+    const uint32_t c0 = clampi(x0, 0, (int)wi - 1), c1 = clampi(x0 + 1, 0, (int)wi - 1);
+#pragma unroll
+    for (uint32_t ch = 0; ch < 7; ch++) {
+        const float v00 = ld(o, r0 + c0, ch), v01 = ld(o, r0 + c1, ch), v10 = ld(o, r1 + c0, ch), v11 = ld(o, r1 + c1, ch);
+        const float val = (v00 * (1.0f - fx) + v01 * fx) * (1.0f - fy) + (v10 * (1.0f - fx) + v11 * fx) * fy;
+        st(out, pix, ch, val * (ch < 4 ? fs : 1.0f));
+    }
+    if (state.p && ox < wi && oy < hi) {
+        const size_t sp = (size_t)oy * wi + ox;
+#pragma unroll
+        for (uint32_t ch = 0; ch < 4; ch++) st(state, sp, ch, ld(o, sp, ch) * fs);
+    }
+}
+
 // ---- render_pix: shaders/render.wgsl:83-160 ------------------------------------------------------------------
 // One lane per output pixel: flow, visibility logits and residual upsampled bilinearly from the quarter maps, A and
 // B sampled at the displaced positions (bilinear, or bicubic: Keys a = -0.75 with every tap clamped to the border),
@@ -1350,6 +1379,24 @@ extern "C" int fhc_fold_pair(const fhc_tensor* x, const fhc_tensor* out, const f
             auto k = v ? fold_pair_kernel<true> : fold_pair_kernel<false>;
             hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(x), outv(out), a2, h * w, c, groups,
                                items);
+        });
+    });
+}
+
+extern "C" int fhc_coarse_up(const fhc_tensor* o, const fhc_tensor* out, const fhc_tensor* state, uint32_t hi,
+                             uint32_t wi, uint32_t oh, uint32_t ow, float flow_scale, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)oh * ow == 0) return 0;
+        if (hi == 0 || wi == 0) return fail(-1, "coarse_up: empty input (%u x %u)", hi, wi);
+        if (state && (hi > oh || wi > ow)) return fail(-1, "coarse_up: the state is larger than the output");
+        FHC_TRY(check(o, "coarse_up o", 7, false));
+        FHC_TRY(check(out, "coarse_up out", 7, false, true));
+        if (state) FHC_TRY(check(state, "coarse_up state", 4, false, true));
+        const OView sv = state ? outv(state) : OView{nullptr, 0, 0};
+        return launch("coarse_up", (uint64_t)oh * ow, [&](dim3 g, uint32_t items) {
+            hipLaunchKernelGGL(coarse_up_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(o), outv(out), sv, hi,
+                               wi, oh, ow, flow_scale, items);
         });
     });
 }

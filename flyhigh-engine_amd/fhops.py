@@ -71,6 +71,7 @@ def _lib():
             "fhc_pair_input": [T, T, T, T, T, U, U, U, U, P],
             "fhc_render": [T, T, T, T, T, T, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U, P],
             "fhc_fold_pair": [T, T, T, U, U, U, P],
+            "fhc_coarse_up": [T, T, T, U, U, U, U, ctypes.c_float, P],
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
@@ -268,3 +269,10 @@ def fold_pair(x, out, also=None, stream=None):
     c = x.channels
     _run("fold_pair", _lib().fhc_fold_pair(_ref(x), _ref(_v(out)), None if also is None else _ref(_v(also)), h, w, c,
                                            _stream_handle(stream)))
+
+
+def coarse_up(o, out, state, oh, ow, flow_scale, stream=None):
+    o = _v(o)
+    _, hi, wi, _ = o.shape
+    _run("coarse_up", _lib().fhc_coarse_up(_ref(o), _ref(_v(out)), None if state is None else _ref(_v(state)), hi,
+                                           wi, oh, ow, flow_scale, _stream_handle(stream)))

@@ -95,6 +95,12 @@ class ComposedChains:
         self.interp(ab, 3, q, oh, ow, True)
         self.pair_pyramid(q, i8, i16, l16)
 
+    def coarse_up(self, o: V, out: V, state: Optional[V], oh: int, ow: int, flow_scale: float):
+        if state is not None:
+            self.chcopy(V(o.buf, o.c0, flow_scale), 4, state)
+        self.interp(V(o.buf, o.c0, flow_scale), 4, V(out.buf, out.c0), oh, ow, False)
+        self.interp(V(o.buf, o.c0 + 4), 3, V(out.buf, out.c0 + 4), oh, ow, False)
+
     def fold_pair(self, x: V, c: int, out: V, also: Optional[V]):
         for i in range(2):
             self.chcopy(V(self.image(x.buf, i), x.c0), c, V(out.buf, out.c0 + c * i))
@@ -250,6 +256,12 @@ class GpuBackend(ComposedChains):
                        flow.scale, out=self._v(out), stream=self.stream)
 
     # the fused chains (one launch each) unless asked for the ops one by one
+    def coarse_up(self, o: V, out: V, state: Optional[V], oh: int, ow: int, flow_scale: float):
+        if not self.chains:
+            return super().coarse_up(o, out, state, oh, ow, flow_scale)
+        self.fh.coarse_up(self._v(o), self._v(out), None if state is None else self._v(state), oh, ow, flow_scale,
+                          stream=self.stream)
+
     def fold_pair(self, x: V, c: int, out: V, also: Optional[V]):
         if not self.chains:
             return super().fold_pair(x, c, out, also)
@@ -342,9 +354,7 @@ class FlyHighFG:
         be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30
         be.conv("coarse.c4", V(self.ch3r), V(self.hc))                                        # 31
         be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
-        be.chcopy(V(self.o, 0, 16.0), 4, V(self.state_out, 72))                               # 43: flow16
-        be.interp(V(self.o, 0, 16.0), 4, V(self.fv, 0), e8h, e8w, False)                      # 33-34, 39: flow
-        be.interp(V(self.o, 4), 3, V(self.fv, 4), e8h, e8w, False)                            # 35, 40: vis
+        be.coarse_up(V(self.o), V(self.fv), V(self.state_out, 72), e8h, e8w, 16.0)            # 33-40; 43: flow16
         # the fine loop, K = 1 (op 42): h enters as zeros (op 41: the fx slice is never written)
         be.fine_input(V(self.f8), V(self.i8), V(self.fv, 0, 0.125), V(self.fx), V(self.l8), 36)  # wa .. flow8
         be.sad(V(self.l8, 0), V(self.l8, 1), V(self.fx, 130), 2)                              # fcv

@@ -137,6 +137,13 @@ int fhc_pair_input(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* 
 int fhc_fold_pair(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h, uint32_t w,
                   uint32_t c, void* stream);
 
+/* graph.json ops 33-40 and 43's flow16: o (1, hi, wi) holds the coarse head's flow (channels 0-3) and visibility
+ * logits (4-6); out (1, oh, ow) gets both resized bilinearly (align_corners false), the flow times flow_scale (flow16
+ * = o * 16), in channels 0-3 and 4-6; state (when not NULL, hi <= oh, wi <= ow) gets the scaled flow at the input
+ * size, as the copy into the streaming state does. */
+int fhc_coarse_up(const fhc_tensor* o, const fhc_tensor* out, const fhc_tensor* state, uint32_t hi, uint32_t wi,
+                  uint32_t oh, uint32_t ow, float flow_scale, void* stream);
+
 /* graph.json op 42's body up to the concat: f8 (2, h, w, c) and i8 (2, h, w, 3) warped by flow (1, h, w: channels
  * 0-1 for A, 2-3 for B, at its read scale), written into fx's slices c0: wa, +c: wb, +2c: ia, +2c+3: ib, +2c+6: the
  * scaled flow (4 channels); the warped pictures' luma into l8's channel image (warp.wgsl, luma.wgsl, chcopy.wgsl). */
