@@ -235,18 +235,23 @@ def test_chcopy_into_a_concat_slice_matches_oracle(c, c0, scale):
     check_slice(buf, out, 5, c, want, "chcopy")
 
 
-@pytest.mark.parametrize("cubic,flags,cs", [(True, 0, 4), (False, 0, 4), (True, 0, 3), (True, 1, 4), (False, 2, 4),
-                                             (True, 3, 3)])
-def test_render_matches_oracle(cubic, flags, cs):
+# amp is the range of the quarter-resolution flow (4x that at full resolution): amp 0.4 keeps every tap near its
+# pixel, amp 6 scatters them and clamps many at the picture's edges; 118x203 is a size no block shape divides.
+@pytest.mark.parametrize("cubic,flags,cs,amp,hw", [(True, 0, 4, 6, (120, 216)), (False, 0, 4, 6, (120, 216)),
+                                                   (True, 0, 3, 6, (120, 216)), (True, 1, 4, 6, (120, 216)),
+                                                   (False, 2, 4, 6, (120, 216)), (True, 3, 3, 6, (120, 216)),
+                                                   (True, 0, 4, 0.4, (120, 216)), (True, 2, 4, 0.4, (118, 203)),
+                                                   (True, 1, 4, 2, (120, 216)), (True, 3, 4, 6, (118, 203))])
+def test_render_matches_oracle(cubic, flags, cs, amp, hw):
     """Bit-exact except where expf's last bit moves the visibility weights (an f16 ulp or two of the output) or,
     with the decisive blend, flips which picture is trusted where the two weights are equal to the last bit."""
-    say("render", cubic, flags, cs)
+    say("render", cubic, flags, cs, amp, hw)
     fh = fhops()
-    rng = np.random.default_rng(7 + flags + 10 * cubic + cs)
-    h, w, hq, wq = 120, 216, 30, 54
+    rng = np.random.default_rng(7 + flags + 10 * cubic + cs + int(10 * amp) + hw[1])
+    (h, w), hq, wq = hw, 30, 54
     ab = rand(rng, (2, h, w, cs), 0, 1)
     up = np.zeros((1, hq, wq, 8), np.float32)
-    up[..., :4] = rng.uniform(-6, 6, (hq, wq, 4))
+    up[..., :4] = rng.uniform(-amp, amp, (hq, wq, 4))
     up[..., 4:7] = rng.normal(0, 2, (hq, wq, 3))
     up = f16_bits(up)
     rt = rand(rng, (1, hq, wq, 4), -0.1, 0.1)
