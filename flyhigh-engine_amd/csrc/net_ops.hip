@@ -885,6 +885,28 @@ __device__ __forceinline__ void sample3(const View& v, uint32_t h, uint32_t w, f
     }
 }
 
+// the bicubic sum of one picture's 16 raw 8-byte taps (rows j, columns i), in sample3's order
+__device__ __forceinline__ void cubic_sum(const uint2* t, float tx, float ty, float (&o)[3]) {
+    const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
+    const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint2 q = t[j * 4 + i];
+                v[i] = h2f((uint16_t)((c < 2 ? q.x : q.y) >> (c == 1 ? 16 : 0)));
+            }
+            const float row = v[0] * cx[0] + v[1] * cx[1] + v[2] * cx[2] + v[3] * cx[3];
+            acc = j == 0 ? row * cy[0] : acc + row * cy[j];
+        }
+        o[c] = acc;
+    }
+}
+
 template <bool VEC, bool CUBIC>
 __global__ __launch_bounds__(kThreads) void render_kernel(View a, View b, View fl, View vis, View rt, OView out,
                                                           uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx,
@@ -900,21 +922,59 @@ __global__ __launch_bounds__(kThreads) void render_kernel(View a, View b, View f
     const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
     const size_t q00 = (size_t)y0 * wq + x0, q01 = (size_t)y0 * wq + x1, q10 = (size_t)y1 * wq + x0,
                  q11 = (size_t)y1 * wq + x1;
+    // every quarter-map value is loaded before any is used: one round of memory latency, not two
+    const size_t qs[4] = {q00, q01, q10, q11};
+    float fq[4][4], vq[4][3], rq[4][3];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+#pragma unroll
+        for (uint32_t c = 0; c < 4; c++) fq[k][c] = ld(fl, qs[k], c);
+#pragma unroll
+        for (uint32_t c = 0; c < 3; c++) vq[k][c] = ld(vis, qs[k], c), rq[k][c] = ld(rt, qs[k], c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     float f[4], v[3], r[3];
 #pragma unroll
     for (uint32_t c = 0; c < 4; c++)
-        f[c] = bil4(ld(fl, q00, c), ld(fl, q01, c), ld(fl, q10, c), ld(fl, q11, c), qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
+        f[c] = bil4(fq[0][c], fq[1][c], fq[2][c], fq[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
 #pragma unroll
     for (uint32_t c = 0; c < 3; c++) {
-        v[c] = bil4(ld(vis, q00, c), ld(vis, q01, c), ld(vis, q10, c), ld(vis, q11, c), qfx, qfy) * vis.scale;
-        r[c] = bil4(ld(rt, q00, c), ld(rt, q01, c), ld(rt, q10, c), ld(rt, q11, c), qfx, qfy);
+        v[c] = bil4(vq[0][c], vq[1][c], vq[2][c], vq[3][c], qfx, qfy) * vis.scale;
+        r[c] = bil4(rq[0][c], rq[1][c], rq[2][c], rq[3][c], qfx, qfy);
     }
     const float m = fmaxf(v[0], fmaxf(v[1], v[2]));
     const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
     const float wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
     float ca[3], cb[3];
-    sample3<VEC, CUBIC>(a, h, w, (float)x + f[0], (float)y + f[1], ca);
-    sample3<VEC, CUBIC>(b, h, w, (float)x + f[2], (float)y + f[3], cb);
+    if constexpr (VEC && CUBIC) {  // both pictures' 32 taps as raw 8-byte values, loaded before any is used
+        uint2 t[2][16];
+        float tx[2], ty[2];
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const View& src = p == 0 ? a : b;
+            const float gx = (float)x + f[2 * p], gy = (float)y + f[2 * p + 1];
+            const int px = (int)floorf(gx), py = (int)floorf(gy);
+            tx[p] = gx - (float)px, ty[p] = gy - (float)py;
+            // 32-bit element offsets from one 24-bit product per row and per column: the launch takes this path
+            // only when a row holds fewer than 2^24 elements and a picture fewer than 2^31
+            uint32_t col[4], row[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) col[i] = __umul24((uint32_t)clampi(px - 1 + i, 0, (int)w - 1), src.cs) + src.c0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) row[j] = __umul24((uint32_t)clampi(py - 1 + j, 0, (int)h - 1), w * src.cs);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    t[p][j * 4 + i] = *reinterpret_cast<const uint2*>(src.p + (row[j] + col[i]));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        cubic_sum(t[0], tx[0], ty[0], ca);
+        cubic_sum(t[1], tx[1], ty[1], cb);
+    } else {
+        sample3<VEC, CUBIC>(a, h, w, (float)x + f[0], (float)y + f[1], ca);
+        sample3<VEC, CUBIC>(b, h, w, (float)x + f[2], (float)y + f[3], cb);
+    }
     float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
     const float third = 1.0f / 3.0f;
     const float ef = fabsf(ca[0] - cb[0]) * third + fabsf(ca[1] - cb[1]) * third + fabsf(ca[2] - cb[2]) * third;
@@ -1352,7 +1412,11 @@ extern "C" int fhc_render(const fhc_tensor* a, const fhc_tensor* b, const fhc_te
         FHC_TRY(check(vis, "render vis", 3, true));
         FHC_TRY(check(rt, "render rt", 3, false));
         FHC_TRY(check(out, "render out", 3, false, true));
-        const bool v = vec4(4, {a, b});
+        // the bicubic 8-byte path addresses its taps with 32-bit element offsets
+        const auto fits32 = [&](const fhc_tensor* t) {
+            return (uint64_t)w * t->cstride < (1u << 24) && (uint64_t)h * w * t->cstride + t->c0 < (1u << 31);
+        };
+        const bool v = vec4(4, {a, b}) && (!cubic || (fits32(a) && fits32(b)));
         return launch("render", (uint64_t)h * w, [&](dim3 g, uint32_t items) {
             auto k = cubic ? (v ? render_kernel<true, true> : render_kernel<false, true>)
                            : (v ? render_kernel<true, false> : render_kernel<false, false>);
