@@ -295,17 +295,22 @@ def network_frame(args, torch, np, stream, net_w, net_h, t=0.5):
             f.mid(t, None)
         for _ in range(args.warmup):
             g.replay()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
         e0.record(stream)
         for _ in range(args.steps):
             g.replay()
         e1.record(stream)
-        e1.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / args.steps
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    us = wall * 1e6 / args.steps
+    ev_us = e0.elapsed_time(e1) * 1e3 / args.steps
     outs = {k: be.host(getattr(f, k))[..., :c].view(np.float16) for k, c in (("out", 3), ("Rt", 3), ("up7", 7))}
     finite = all(bool(np.all(np.isfinite(v))) for v in outs.values())
     fused = sum(1 for k, p in be.plans.items() if k[0] == "pair" and p is not False)
-    res = dict(us_per_frame=round(us, 3), frames_per_s=round(1e6 / us, 2), finite_outputs=finite,
+    res = dict(us_per_frame=round(us, 3), frames_per_s=round(1e6 / us, 2), event_us_per_frame=round(ev_us, 3),
+               steps=args.steps, warmup=args.warmup, network=f"{net_w}x{net_h}", finite_outputs=finite,
                conv_plans=sum(1 for k in be.plans if k[0] == "conv"), fused_pairs=fused,
                workload=f"every op of one FlyHighFG pair() and mid(t={t}) at network {net_w}x{net_h} (1080p): the "
                         "convs (fused pairs where the library has a kernel), resize, pools, luma, SAD volumes, warps, "
@@ -555,6 +560,9 @@ def main():
                                         "then a copy of known size as many times: the workload of the rocprofv3 "
                                         "--pmc FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-reps", type=int, default=64)
+    ap.add_argument("--detail", default=os.path.join("gpurun_out", "bench_detail.json"),
+                    help="file for the full record (per-launch tables, configurations, batched launches, choice "
+                         "table); '' for none")
     ap.add_argument("--traffic-from", nargs="+", metavar="CSV",
                     help="with --pmc-layer: turn the two passes' counter_collection.csv files (FETCH, WRITE) into "
                          "profiles/traffic_<layer>.txt (HBM bytes per launch, copy-calibrated); a third file, the "
@@ -700,20 +708,15 @@ def main():
             del cnet
             torch.cuda.empty_cache()
 
-    # the network frame plans its convs from the choice table the frame's autotuning filled; the batched workload
-    # autotunes at batch 8-24 under the same keys (the key has no batch), so it runs after, and the table is restored
+    # the network frame plans its convs from the choice table the frame's autotuning filled; the batched workload's
+    # choices sit under keys of their own (the table's key holds the batch)
     net_ops = None if args.no_ops else net_ops_report(args, torch, flyhighfg, stream, net_w, net_h)
-    netframe = None
-    if not args.no_ops:
-        netframe = network_frame(args, torch, np, stream, net_w, net_h)
-        log("bench: network frame", json.dumps(netframe))
+    netframe = network_frame(args, torch, np, stream, net_w, net_h)
+    log("bench: network frame", json.dumps(netframe))
 
     batched = None
     if not args.no_batched:
-        frame_table = fhconv.format_tune()
         batched = batched_workload(args, torch, np, fhconv, flyhighfg, stream)
-        fhconv.tune_clear()
-        fhconv.parse_tune(frame_table)
         torch.cuda.empty_cache()
 
     mfma_rate = mfma_rate_probe(torch, fhconv, stream)
@@ -748,28 +751,51 @@ def main():
                    seconds=round(secs, 3))
         log(f"bench: CPU baseline {secs:.3f} s per pair+mid on {threads} threads")
 
-    out = dict(
-        metric=METRIC, value=round(1000.0 / ms_per_step, 2), unit="frames/s", n_gpus=1, steps=args.steps,
-        warmup=args.warmup, ms_per_step=round(ms_per_step, 6), higher_is_better=True, scaling="weak",
-        vs_baseline=None, dtype="f16", data="synthetic",
-        config=dict(workload="FlyHighFG conv layers of one pair()+mid() at 1080p (network 856x480 padded to "
-                             "864x480), NHWC f16, conv-only; the A/B encoders run as batch-2 convs"
-                             + ("; consecutive convs whose intermediate has no other reader run as fused pairs"
-                                if net.pairs else ""),
-                    frame="1920x1080", network=f"{net_w}x{net_h}", conv_layers=25,
-                    conv_launches=launches, fused_pairs=[f"{a}+{B.name}" for a, (_, B, _, _) in net.pairs.items()],
-                    k=1, parallelism="single GPU"),
+    conv_step = dict(
+        workload="FlyHighFG conv layers of one pair()+mid() at 1080p (network 856x480 padded to 864x480), NHWC "
+                 "f16, conv-only; the A/B encoders run as batch-2 convs"
+                 + ("; consecutive convs whose intermediate has no other reader run as fused pairs"
+                    if net.pairs else ""),
+        us_per_step=round(ms_per_step * 1e3, 3), frames_per_s=round(1000.0 / ms_per_step, 2), conv_layers=25,
+        conv_launches=launches, fused_pairs=[f"{a}+{B.name}" for a, (_, B, _, _) in net.pairs.items()],
         pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), unfused_step_us=round(unfused_us, 3),
         fuse_check=fuse_check, event_ms_per_step=round(ev_ms, 6),
-        submit_us_per_step=round(t_submit * 1e6 / args.steps, 3),
-        roofline=roofline, cpu_baseline=cpu, layers=per_layer, pairs=per_pair, config_layers=cfg_layers,
-        config_pairs=cfg_pairs,
-        batched=batched,
-        net_ops=net_ops,
-        network_frame=netframe,
-        tune_table=tune_table,
-    )
-    print(json.dumps(out), flush=True)
+        submit_us_per_step=round(t_submit * 1e6 / args.steps, 3))
+    detail = dict(conv_step=conv_step, roofline=roofline, cpu_baseline=cpu, layers=per_layer, pairs=per_pair,
+                  config_layers=cfg_layers, config_pairs=cfg_pairs, batched=batched, net_ops=net_ops,
+                  network_frame=netframe, tune_table=tune_table)
+    return emit(args, netframe, conv_step, roofline, cpu, batched, detail)
+
+
+def emit(args, frame, conv_step, roofline, cpu, batched, detail):
+    """Write the whole record to args.detail and print the one compact JSON line (under 4 KB) that is the bench's
+    result: the headline is the whole frame (frame), with the conv-only step, the roofline of the dominant kernel,
+    the CPU baseline and the batched workload's summary beside it."""
+    if args.detail:
+        os.makedirs(os.path.dirname(os.path.abspath(args.detail)), exist_ok=True)
+        with open(args.detail, "w") as f:
+            json.dump(detail, f, indent=1)
+        log(f"bench: full record in {args.detail}")
+    keep_roof = ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel", "variant", "us_cold", "us_warm",
+                 "per_launch_bytes", "per_launch_flops", "sustained_mfma_tflops", "frac_of_sustained")
+    line = dict(
+        metric=METRIC, value=frame["frames_per_s"], unit="frames/s", n_gpus=1, steps=frame["steps"],
+        warmup=frame["warmup"], ms_per_step=round(frame["us_per_frame"] / 1e3, 6), higher_is_better=True,
+        scaling="weak", vs_baseline=None, dtype="f16", data="synthetic",
+        config=dict(workload=frame["workload"], frame="1920x1080", network=frame["network"],
+                    launches=frame.get("launches"), parallelism="single GPU"),
+        roofline=None if roofline is None else {k: roofline[k] for k in keep_roof if k in roofline},
+        cpu_baseline=cpu,
+        conv_step=None if conv_step is None else {k: conv_step[k] for k in ("us_per_step", "frames_per_s",
+                                                                            "conv_launches", "pair_us", "mid_us")},
+        batched=None if batched is None else {k: batched[k] for k in ("step_us", "generated_frames_per_s",
+                                                                      "step_tflops")},
+        detail=args.detail or None)
+    text = json.dumps(line)
+    if len(text) > 4000:
+        line["config"]["workload"] = line["config"]["workload"][:200]
+        text = json.dumps(line)
+    print(text, flush=True)
     return 0
 
 

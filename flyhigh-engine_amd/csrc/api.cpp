@@ -31,7 +31,12 @@ constexpr size_t kLdsBudget = 64 * 1024;  // dynamic LDS per workgroup the plann
 uint32_t div_ceil(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
 // ---- the choice table (TuneTable, ops/conv/tune_cache.rs:6-9) ----------------------------------------------
-using TuneKey = std::tuple<uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>;
+// Key: the reference's (cin, cout, h, w, stride) plus the batch n and the kernel size k (the reference runs batch 1
+// and 3x3 only). Batch 1 of a 3x3 conv is written in the reference's 5-field text; other keys carry n and k as
+// fields 6 and 7, so the batch-1 and batched choices for one layer shape, or a 1x1 and a 3x3 conv over the same
+// channels, do not overwrite each other.
+using TuneKey = std::tuple<uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>;
+TuneKey tune_key(const fhc_conv_desc& d) { return TuneKey(d.cin, d.cout, d.h, d.w, d.stride, d.n, d.kh); }
 std::mutex g_tune_mu;
 std::map<TuneKey, uint32_t> g_tune;
 
@@ -594,7 +599,7 @@ bool plan_choose(const fhc_conv_desc& d, fhc_conv_plan& p, std::string* why) {
             return false;
         }
     } else {
-        const int hit = fhc_tune_get(d.cin, d.cout, d.h, d.w, d.stride);
+        const int hit = fhc_tune_get_ex(d.cin, d.cout, d.h, d.w, d.stride, d.n, d.kh);
         if (hit < 0 || !decode_code((uint32_t)hit, &v)) decode_code(heuristic_code(d, p.g), &v);
     }
     // a forced split (or the reference code's split nibble, candidates.rs:4) moves to the chunked kernel
@@ -985,8 +990,8 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
 extern "C" int fhc_tune_parse(const char* text) {
     return guard(-1, [&]() -> int {
         if (!text) return fail(-1, "fhc_tune_parse: NULL text");
-        // parse_tune (tune_cache.rs:71-87): "cin,cout,h,w,stride=code" per line, malformed lines skipped; the value
-        // may also be a variant name
+        // parse_tune (tune_cache.rs:71-87): "cin,cout,h,w,stride=code" per line (batch 1, 3x3), or
+        // "cin,cout,h,w,stride,n,k=code"; malformed lines skipped; the value may also be a variant name
         std::istringstream in(text);
         std::string line;
         int n = 0;
@@ -1011,7 +1016,12 @@ extern "C" int fhc_tune_parse(const char* text) {
                 }
                 f.push_back((uint32_t)std::stoul(v));
             }
-            if (!ok || f.size() != 5) continue;
+            if (!ok || (f.size() != 5 && f.size() != 7)) continue;
+            if (f.size() == 5) {
+                f.push_back(1);
+                f.push_back(3);
+            }
+            if (f[5] == 0 || (f[6] != 1 && f[6] != 3)) continue;
             std::string v = line.substr(eq + 1);
             const size_t a = v.find_first_not_of(" \t\r"), b = v.find_last_not_of(" \t\r");
             if (a == std::string::npos) continue;
@@ -1027,7 +1037,7 @@ extern "C" int fhc_tune_parse(const char* text) {
                     if (code_name(c) == v) code = c;
                 if (!code) continue;
             }
-            g_tune[TuneKey(f[0], f[1], f[2], f[3], f[4])] = code;
+            g_tune[TuneKey(f[0], f[1], f[2], f[3], f[4], f[5], f[6])] = code;
             n++;
         }
         return n;
@@ -1036,15 +1046,19 @@ extern "C" int fhc_tune_parse(const char* text) {
 
 extern "C" int fhc_tune_format(char* text, size_t cap) {
     return guard(-1, [&]() -> int {
-        // format_tune (tune_cache.rs:88-94): lines sorted as strings, joined by newlines
+        // format_tune (tune_cache.rs:88-94): lines sorted as strings, joined by newlines; batch 1 of a 3x3 conv in
+        // the reference's 5 fields, other keys with n and k appended
         std::vector<std::string> lines;
         {
             std::lock_guard<std::mutex> lk(g_tune_mu);
             for (const auto& kv : g_tune) {
                 const TuneKey& k = kv.first;
-                lines.push_back(std::to_string(std::get<0>(k)) + "," + std::to_string(std::get<1>(k)) + "," +
-                                std::to_string(std::get<2>(k)) + "," + std::to_string(std::get<3>(k)) + "," +
-                                std::to_string(std::get<4>(k)) + "=" + std::to_string(kv.second));
+                std::string line = std::to_string(std::get<0>(k)) + "," + std::to_string(std::get<1>(k)) + "," +
+                                   std::to_string(std::get<2>(k)) + "," + std::to_string(std::get<3>(k)) + "," +
+                                   std::to_string(std::get<4>(k));
+                if (std::get<5>(k) != 1 || std::get<6>(k) != 3)
+                    line += "," + std::to_string(std::get<5>(k)) + "," + std::to_string(std::get<6>(k));
+                lines.push_back(line + "=" + std::to_string(kv.second));
             }
         }
         std::sort(lines.begin(), lines.end());
@@ -1061,8 +1075,13 @@ extern "C" int fhc_tune_clear(void) {
 }
 
 extern "C" int fhc_tune_get(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride) {
+    return fhc_tune_get_ex(cin, cout, h, w, stride, 1, 3);
+}
+
+extern "C" int fhc_tune_get_ex(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride, uint32_t n,
+                               uint32_t k) {
     std::lock_guard<std::mutex> lk(g_tune_mu);
-    auto it = g_tune.find(TuneKey(cin, cout, h, w, stride));
+    auto it = g_tune.find(TuneKey(cin, cout, h, w, stride, n, k));
     return it == g_tune.end() ? -1 : (int)it->second;
 }
 
@@ -1196,7 +1215,7 @@ extern "C" int fhc_conv_autotune(const fhc_conv_desc* desc, const uint16_t* w_oi
         if (best_code < 0) return fail(-1, "fhc_conv_autotune: no variant could be planned");
         {
             std::lock_guard<std::mutex> lk(g_tune_mu);
-            g_tune[TuneKey(desc->cin, desc->cout, desc->h, desc->w, desc->stride)] = (uint32_t)best_code;
+            g_tune[tune_key(*desc)] = (uint32_t)best_code;
         }
         if (best_us) *best_us = best;
         clear_error();

@@ -80,6 +80,7 @@ def load():
         "fhc_tune_format": ([ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_tune_clear": ([], ctypes.c_int),
         "fhc_tune_get": ([U32] * 5, ctypes.c_int),
+        "fhc_tune_get_ex": ([U32] * 7, ctypes.c_int),
         "fhc_variant_name": ([U32, ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_variant_list": ([ctypes.POINTER(ConvDesc), ctypes.POINTER(U32), SZ], ctypes.c_int),
         "fhc_ref_cand_list": ([ctypes.c_int, U32, U32, U32, ctypes.c_int, ctypes.c_int,
@@ -347,8 +348,10 @@ def tune_clear():
     load().fhc_tune_clear()
 
 
-def tune_get(cin, cout, h, w, stride) -> Optional[int]:
-    v = load().fhc_tune_get(cin, cout, h, w, stride)
+def tune_get(cin, cout, h, w, stride, n=1, k=3) -> Optional[int]:
+    """The table's code for a conv of batch n and kernel size k (None without an entry)."""
+    v = load().fhc_tune_get(cin, cout, h, w, stride) if (n, k) == (1, 3) else \
+        load().fhc_tune_get_ex(cin, cout, h, w, stride, n, k)
     return None if v < 0 else v
 
 

@@ -129,15 +129,20 @@ int fhc_conv_autotune(const fhc_conv_desc* desc, const uint16_t* w_oihw, const u
                       const uint16_t* slope, const void* x, void* y, const void* res, int reps, float* best_us);
 
 /* ---- The planner's choice table ------------------------------------------------------------------------
- * Same key and text format as the reference's TuneTable (ops/conv/tune_cache.rs:6-9, :39-64): one
- * "cin,cout,h,w,stride=code" per line, h and w the INPUT size; malformed lines are skipped. The codes are
- * MI355X variant codes (fhc_variant_name); fhc_tune_parse also takes a variant name in place of the code, which
- * stays valid across builds. The table is process-wide and consulted by fhc_conv_plan_create when desc.variant
- * is 0. */
+ * The reference's TuneTable (ops/conv/tune_cache.rs:6-9, :39-64) keys a choice by (cin, cout, h, w, stride), h and
+ * w the INPUT size, one "cin,cout,h,w,stride=code" per line. This table adds the batch n and the kernel size k (1 or
+ * 3) to the key, since a batched conv and a 1x1 conv need choices of their own: the key of a batch-1 3x3 conv is
+ * written in the reference's 5 fields, any other as "cin,cout,h,w,stride,n,k=code"; both forms parse, malformed
+ * lines are skipped. The codes are MI355X variant codes (fhc_variant_name); fhc_tune_parse also takes a variant
+ * name in place of the code, which stays valid across builds. The table is process-wide and consulted by
+ * fhc_conv_plan_create (under the descriptor's n and kh) when desc.variant is 0. */
 int fhc_tune_parse(const char* text);           /* merges; returns the number of entries read, or -1   */
 int fhc_tune_format(char* text, size_t cap);    /* sorted lines; bytes written, or -1 if cap too small */
 int fhc_tune_clear(void);
-int fhc_tune_get(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride); /* code or -1 */
+/* code or -1: the entry of a batch-1 3x3 conv (the reference's key) */
+int fhc_tune_get(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride);
+/* code or -1: the entry of batch n, kernel size k */
+int fhc_tune_get_ex(uint32_t cin, uint32_t cout, uint32_t h, uint32_t w, uint32_t stride, uint32_t n, uint32_t k);
 /* Name of an MI355X variant code into buf; bytes written or -1. Codes 1..127 are the K-chunked kernels: bits 0-4
  * the configuration (1..10 the chunked implicit GEMM, "igemm.t8x16.n64"; 16..28 the deep-layer kernel with LDS
  * DMA, "gemm.t8x16.n48.f2x3.w4x1.c32.p2"), bits 5-6 the global split (1, 2, 4, 8: "/k2"); 128 + i the direct

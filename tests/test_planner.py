@@ -180,6 +180,33 @@ def test_forced_split_k_and_reference_hint():
     assert none["ksplit"] == 1 and none["workspace_bytes"] == 0
 
 
+def test_tune_table_keys_batch_and_kernel_size():
+    # the batch and the kernel size extend the reference's key: the batch-1 3x3 entry keeps the reference's 5
+    # fields, a batched or 1x1 entry carries n and k, and none of them overwrites another
+    fhconv.tune_clear()
+    try:
+        text = "48,48,60,108,1=18\n48,48,60,108,1,24,3=17\n48,48,60,108,1,1,1=130\n48,48,60,108,1,0,3=5\n" \
+               "48,48,60,108,1,2,5=5\n48,48,60,108,1,2=5\n"
+        assert fhconv.parse_tune(text) == 3
+        assert fhconv.tune_get(48, 48, 60, 108, 1) == 18
+        assert fhconv.tune_get(48, 48, 60, 108, 1, n=24) == 17
+        assert fhconv.tune_get(48, 48, 60, 108, 1, k=1) == 130
+        assert fhconv.tune_get(48, 48, 60, 108, 1, n=8) is None
+        out = fhconv.format_tune()
+        assert out == "48,48,60,108,1,1,1=130\n48,48,60,108,1,24,3=17\n48,48,60,108,1=18"
+        fhconv.tune_clear()
+        assert fhconv.parse_tune(out) == 3 and fhconv.format_tune() == out
+        # the planner looks the descriptor's own batch up
+        d1, d24 = fhconv.make_desc(1, 60, 108, 48, 48), fhconv.make_desc(24, 60, 108, 48, 48)
+        codes = fhconv.variant_list(d24)
+        fhconv.tune_clear()
+        fhconv.parse_tune(f"48,48,60,108,1,24,3={codes[0]}\n48,48,60,108,1={codes[1]}")
+        assert fhconv.plan_dry(d24)["variant"] == codes[0]
+        assert fhconv.plan_dry(d1)["variant"] == codes[1]
+    finally:
+        fhconv.tune_clear()
+
+
 def test_the_table_steers_the_planner():
     fhconv.tune_clear()
     try:
