@@ -399,6 +399,7 @@ bool configure_gemm(fhc_conv_plan& p, int idx, uint32_t ks, std::string* why) {
 }
 
 int heuristic_cfg(const fhc_conv_desc& d, const Geometry& g);
+void* static_scratch(int dev);
 
 bool configure(fhc_conv_plan& p, const Variant& v, std::string* why) {
     if (v.family == 1) {
@@ -735,6 +736,9 @@ extern "C" int fhc_conv_plan_create(const fhc_conv_desc* desc, const uint16_t* w
             if (p->dmem) (void)hipFree(p->dmem);
             return fail(-1, "fhc_conv_plan_create: device upload: %s", hipGetErrorString(e));
         }
+        // set-up of fhc_conv_run_noalloc: the static scratch's address on this device, looked up here, outside any
+        // stream capture (a failure is reported again by fhc_conv_run_noalloc)
+        if (p->ws_bytes > 0 && p->ws_bytes <= FHC_STATIC_SCRATCH_BYTES) (void)static_scratch(p->device);
         *out = p.release();
         clear_error();
         return 0;
@@ -1242,5 +1246,59 @@ extern "C" int fhc_probe_mfma_layout(const void* a, const void* b, void* d, void
                                          static_cast<float*>(d), static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return fail(-1, "fhc_probe_mfma_layout: %s", hipGetErrorString(e));
         return 0;
+    });
+}
+
+// ---- the run entry point that allocates nothing ------------------------------------------------------------
+// fhc_conv_run_noalloc takes the plan's scratch (the split-K partials) from a file-scope device array instead of a
+// caller workspace. Each device holds its own copy of the array, at its own address; host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol), but the address
+// hipGetSymbolAddress gives with that device current, looked up once per device and kept here.
+namespace fhc {
+namespace {
+constexpr size_t kStaticScratchBytes = FHC_STATIC_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) float scratch[kStaticScratchBytes / sizeof(float)];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// the scratch array's device address on `dev` (the current device), or nullptr with the last error set
+void* static_scratch(int dev) {
+    if (dev < 0 || dev >= kMaxDevices) {
+        fail(-1, "fhc_conv_run_noalloc: device %d is beyond the %d the library keeps scratch for", dev, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            fail(-1, "fhc_conv_run_noalloc: hipGetSymbolAddress of the scratch array: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = ptr;
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+}  // namespace fhc
+
+extern "C" int fhc_conv_run_noalloc(const fhc_conv_plan* p, const void* x, void* y, const void* res, void* stream) {
+    return guard(-1, [&]() -> int {
+        if (!p) return fail(-1, "fhc_conv_run_noalloc: NULL plan");
+        if (p->ws_bytes > kStaticScratchBytes)
+            return fail(-1, "fhc_conv_run_noalloc: the plan needs %zu bytes of scratch, the static scratch holds %zu "
+                            "(use fhc_conv_run with a workspace, or a smaller split-K)",
+                        p->ws_bytes, kStaticScratchBytes);
+        void* ws = nullptr;
+        if (p->ws_bytes) {
+            int dev = -1;
+            if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
+                return fail(-1, "fhc_conv_run_noalloc: the plan belongs to device %d, the current device is %d",
+                            p->device, dev);
+            ws = static_scratch(dev);
+            if (!ws) return -1;
+        }
+        return fhc_conv_run(p, x, y, res, ws, stream);
     });
 }

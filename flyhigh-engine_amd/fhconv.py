@@ -71,6 +71,7 @@ def load():
         "fhc_conv_workspace_bytes": ([P], SZ),
         "fhc_conv_out_shape": ([P, ctypes.POINTER(U32), ctypes.POINTER(U32)], ctypes.c_int),
         "fhc_conv_run": ([P, P, P, P, P, P], ctypes.c_int),
+        "fhc_conv_run_noalloc": ([P, P, P, P, P], ctypes.c_int),
         "fhc_conv_describe": ([P, ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_conv_plan_destroy": ([P], None),
         "fhc_conv_pair_plan_create": ([ctypes.POINTER(ConvDesc), P, P, P, ctypes.POINTER(ConvDesc), P, P, P, U32,
@@ -197,6 +198,12 @@ class ConvPlan:
     def run(self, x, y, res=None, workspace=None, stream=None):
         _check(load().fhc_conv_run(self._h, _ptr(x), _ptr(y), _ptr(res), _ptr(workspace),
                                    _stream_handle(stream)), "fhc_conv_run")
+
+    def run_noalloc(self, x, y, res=None, stream=None):
+        """fhc_conv_run_noalloc: the plan's scratch from the library's static device array (no workspace, nothing
+        allocated)."""
+        _check(load().fhc_conv_run_noalloc(self._h, _ptr(x), _ptr(y), _ptr(res), _stream_handle(stream)),
+               "fhc_conv_run_noalloc")
 
     def out_elems(self):
         d = self.desc
