@@ -1012,6 +1012,268 @@ __global__ __launch_bounds__(kThreads) void render_kernel(View a, View b, View f
     }
 }
 
+// ---- the host's 8-bit frames: rgba_in.wgsl:11-19, rgba_out.wgsl:9-18 -------------------------------------------
+// A frame is RGBA8, one 32-bit word per pixel (R | G << 8 | B << 16 | A << 24), rows `pitch` words apart. The network
+// reads BGR f16 in [0, 1] replicate-padded to hp x wp: padded pixel (x, y) is frame pixel (min(x, w - 1),
+// min(y, h - 1)). A sampler that clamps its coordinates to the padded picture therefore reads exactly what clamping
+// them to the frame reads, which the fused kernels below use to sample the 8-bit frame directly.
+
+// BGR channel ch (0 B, 1 G, 2 R) of an RGBA8 word, as f16(f32(byte) / 255): the product with the f32 reciprocal of
+// 255 rounds to the same f16 as the quotient for each of the 256 bytes (and both to the f16 of the exact fraction)
+__device__ __forceinline__ uint16_t unit_f16(uint32_t v, int ch) {
+    return f2h((float)((v >> (16 - 8 * ch)) & 0xffu) * (1.0f / 255.0f));
+}
+__device__ __forceinline__ float unit_f32(uint32_t v, int ch) { return h2f(unit_f16(v, ch)); }
+// rgba_out.wgsl:10: an f16 value in [0, 1] to its byte (v * 255 + 0.5 is exact in f32 for every f16 v)
+__device__ __forceinline__ uint32_t byte_of(uint16_t hv) {
+    return (uint32_t)(fminf(fmaxf(h2f(hv), 0.0f), 1.0f) * 255.0f + 0.5f);
+}
+
+// one lane per padded pixel; VEC4: the output view has 8-byte 4-channel pixels (channel 3 written 0)
+template <bool VEC4>
+__global__ __launch_bounds__(kThreads) void rgba_in_kernel(const uint32_t* src, uint32_t w, uint32_t h, uint32_t pitch,
+                                                           uint64_t fstride, OView out, uint32_t hp, uint32_t wp,
+                                                           uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t x = t % wp, r = t / wp, y = r % hp, img = r / hp;
+    const uint32_t v = src[img * fstride + (size_t)min(y, h - 1) * pitch + min(x, w - 1)];
+    const uint16_t b = unit_f16(v, 0), g = unit_f16(v, 1), rr = unit_f16(v, 2);
+    if constexpr (VEC4) {
+        *reinterpret_cast<uint2*>(out.p + (size_t)t * out.cs) = uint2{(uint32_t)b | ((uint32_t)g << 16), rr};
+    } else {
+        uint16_t* o = out.p + (size_t)t * out.cs + out.c0;
+        o[0] = b, o[1] = g, o[2] = rr;
+    }
+}
+
+// one lane per frame pixel: channels 0-2 (B, G, R) of the padded view, cropped to w x h
+__global__ __launch_bounds__(kThreads) void rgba_out_kernel(View in, uint32_t hp, uint32_t wp, uint32_t* dst,
+                                                            uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                                                            uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t x = t % w, r = t / w, y = r % h, img = r / h;
+    const uint16_t* p = in.p + (((size_t)img * hp + y) * wp + x) * in.cs + in.c0;
+    dst[img * fstride + (size_t)y * pitch + x] =
+        byte_of(p[2]) | (byte_of(p[1]) << 8) | (byte_of(p[0]) << 16) | 0xff000000u;
+}
+
+// 16 and 8 bytes of a frame row at a 4-byte aligned address (global loads need only dword alignment)
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2_a4 __attribute__((ext_vector_type(2), aligned(4)));
+
+// The 4 words of frame row y at the clamped columns px - 1 .. px + 2 (w >= 4): one 16-byte load at column
+// clamp(px - 1, 0, w - 4), whose 4 words hold every clamped column (each lies 0..3 past it), then a pick per tap.
+__device__ __forceinline__ void row_taps4(const uint32_t* f, uint32_t pitch, uint32_t y, int px, uint32_t w,
+                                          uint32_t (&t)[4]) {
+    const int base = clampi(px - 1, 0, (int)w - 4);
+    const u32x4_a4 q = *reinterpret_cast<const u32x4_a4*>(f + (size_t)y * pitch + base);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int off = clampi(px - 1 + i, 0, (int)w - 1) - base;
+        t[i] = off == 0 ? q.x : off == 1 ? q.y : off == 2 ? q.z : q.w;
+    }
+}
+// the 2 words of row y at the clamped columns px, px + 1 (w >= 2), the same way
+__device__ __forceinline__ void row_taps2(const uint32_t* f, uint32_t pitch, uint32_t y, int px, uint32_t w,
+                                          uint32_t (&t)[2]) {
+    const int base = clampi(px, 0, (int)w - 2);
+    const u32x2_a4 q = *reinterpret_cast<const u32x2_a4*>(f + (size_t)y * pitch + base);
+#pragma unroll
+    for (int i = 0; i < 2; i++) t[i] = clampi(px + i, 0, (int)w - 1) - base == 0 ? q.x : q.y;
+}
+
+// render_pix of the padded frame (hp x wp) from the two RGBA8 frames, written as RGBA8 (rgba_out of the f16 result),
+// cropped to w x h: render.wgsl:83-160 with its sources replaced by rgba_in.wgsl's conversion of the frames, then
+// rgba_out.wgsl. One lane per frame pixel. QV: flow and vis are channels 0-3 and 4-6 of one 8-channel view (16-byte
+// pixels) and rt has 8-byte pixels, so each quarter-map tap is two loads.
+template <bool CUBIC, bool QV>
+__global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
+                                                               uint32_t h, uint32_t pitch, uint32_t hp, uint32_t wp,
+                                                               View fl, View vis, View rt, uint32_t hq, uint32_t wq,
+                                                               float fsx, float fsy, uint32_t flags, uint32_t* dst,
+                                                               uint32_t opitch, uint32_t items) {
+    const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
+    if (pix >= items) return;
+    const uint32_t x = pix % w, y = pix / w;
+    const float sh = (float)hq / (float)hp, sw = (float)wq / (float)wp;
+    const float iy = ((float)y + 0.5f) * sh - 0.5f, ix = ((float)x + 0.5f) * sw - 0.5f;
+    const int qy0 = (int)floorf(iy), qx0 = (int)floorf(ix);
+    const float qfy = iy - (float)qy0, qfx = ix - (float)qx0;
+    const uint32_t y0 = clampi(qy0, 0, (int)hq - 1), y1 = clampi(qy0 + 1, 0, (int)hq - 1);
+    const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
+    const size_t qs[4] = {(size_t)y0 * wq + x0, (size_t)y0 * wq + x1, (size_t)y1 * wq + x0, (size_t)y1 * wq + x1};
+    float fq[4][4], vq[4][3], rq[4][3];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        if constexpr (QV) {
+            const uint4 a = *reinterpret_cast<const uint4*>(fl.p + qs[k] * fl.cs);
+            const uint2 r = *reinterpret_cast<const uint2*>(rt.p + qs[k] * rt.cs + rt.c0);
+            const uint32_t wv[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) fq[k][c] = h2f((uint16_t)(wv[c >> 1] >> (16 * (c & 1))));
+#pragma unroll
+            for (int c = 0; c < 3; c++) vq[k][c] = h2f((uint16_t)(wv[2 + (c >> 1)] >> (16 * (c & 1))));
+            rq[k][0] = h2f((uint16_t)r.x), rq[k][1] = h2f((uint16_t)(r.x >> 16)), rq[k][2] = h2f((uint16_t)r.y);
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) fq[k][c] = ld(fl, qs[k], c);
+#pragma unroll
+            for (uint32_t c = 0; c < 3; c++) vq[k][c] = ld(vis, qs[k], c), rq[k][c] = ld(rt, qs[k], c);
+        }
+    }
+    float f[4], v[3], r[3];
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++)
+        f[c] = bil4(fq[0][c], fq[1][c], fq[2][c], fq[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
+#pragma unroll
+    for (uint32_t c = 0; c < 3; c++) {
+        v[c] = bil4(vq[0][c], vq[1][c], vq[2][c], vq[3][c], qfx, qfy) * vis.scale;
+        r[c] = bil4(rq[0][c], rq[1][c], rq[2][c], rq[3][c], qfx, qfy);
+    }
+    const float m = fmaxf(v[0], fmaxf(v[1], v[2]));
+    const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
+    const float wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
+    float ca[3], cb[3];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const uint32_t* src = p == 0 ? fa : fb;
+        float* o = p == 0 ? ca : cb;
+        const float gx = (float)x + f[2 * p], gy = (float)y + f[2 * p + 1];
+        const int px = (int)floorf(gx), py = (int)floorf(gy);
+        const float tx = gx - (float)px, ty = gy - (float)py;
+        if constexpr (CUBIC) {
+            const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
+            const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+            uint32_t t[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) row_taps4(src, pitch, (uint32_t)clampi(py - 1 + j, 0, (int)h - 1), px, w, t[j]);
+#pragma unroll
+            for (int c = 0; c < 3; c++) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float row = unit_f32(t[j][0], c) * cx[0] + unit_f32(t[j][1], c) * cx[1] +
+                                      unit_f32(t[j][2], c) * cx[2] + unit_f32(t[j][3], c) * cx[3];
+                    acc = j == 0 ? row * cy[0] : acc + row * cy[j];
+                }
+                o[c] = acc;
+            }
+        } else {
+            uint32_t t0[2], t1[2];
+            row_taps2(src, pitch, (uint32_t)clampi(py, 0, (int)h - 1), px, w, t0);
+            row_taps2(src, pitch, (uint32_t)clampi(py + 1, 0, (int)h - 1), px, w, t1);
+#pragma unroll
+            for (int c = 0; c < 3; c++)
+                o[c] = bil4(unit_f32(t0[0], c), unit_f32(t0[1], c), unit_f32(t1[0], c), unit_f32(t1[1], c), tx, ty);
+        }
+    }
+    float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
+    const float third = 1.0f / 3.0f;
+    const float ef = fabsf(ca[0] - cb[0]) * third + fabsf(ca[1] - cb[1]) * third + fabsf(ca[2] - cb[2]) * third;
+    if (flags & 2u) {  // the still test (render.wgsl:134-148) on the 3 x 3 neighbourhood, clamped to the frame
+        uint32_t ta[3][4], tb[3][4];
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const uint32_t yy = (uint32_t)clampi((int)y - 1 + j, 0, (int)h - 1);
+            row_taps4(fa, pitch, yy, (int)x, w, ta[j]);
+            row_taps4(fb, pitch, yy, (int)x, w, tb[j]);
+        }
+        float es = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 3; j++)
+#pragma unroll
+            for (int i = 0; i < 3; i++)
+#pragma unroll
+                for (int c = 0; c < 3; c++) es += fabsf(unit_f32(ta[j][i], c) - unit_f32(tb[j][i], c));
+        es = es / 27.0f;
+#pragma unroll
+        for (int c = 0; c < 3; c++) own[c] = 0.5f * (unit_f32(ta[1][1], c) + unit_f32(tb[1][1], c));
+        stillw = fminf(fmaxf((ef - es) / 0.04f, 0.0f), 1.0f) * (es < 0.03f ? 1.0f : 0.0f);
+    }
+    if (flags & 1u) {  // the decisive blend (render.wgsl:149-153)
+        const float k = fminf(fmaxf((ef - 0.04f) / 0.08f, 0.0f), 1.0f);
+        const float pa = wa_w >= wb_w ? 1.0f : 0.0f;
+        bwa = wa_w * (1.0f - k) + pa * k;
+        bwb = wb_w * (1.0f - k) + (1.0f - pa) * k;
+        rk = 1.0f - k;
+    }
+    uint32_t bytes[3];
+#pragma unroll
+    for (int c = 0; c < 3; c++) {
+        const float mixed = ca[c] * bwa + cb[c] * bwb + r[c] * rk;
+        bytes[c] = byte_of(f2h(fminf(fmaxf(mixed * (1.0f - stillw) + own[c] * stillw, 0.0f), 1.0f)));
+    }
+    dst[(size_t)y * opitch + x] = bytes[2] | (bytes[1] << 8) | (bytes[0] << 16) | 0xff000000u;
+}
+
+// The antialiased resize of n padded RGBA8 frames (hp x wp, rgba_in's BGR f16) to oh x ow, into a view of 8-byte
+// 4-channel pixels (channel 3 written 0): rgba_in.wgsl then interp.wgsl:11-45 with antialias, as
+// interp_aa_lds_kernel computes it. A workgroup stages the union of its 16 x 16 outputs' windows, at most
+// 16 * R x 16 * R padded pixels, converted to f16 once (R = 3 covers downscales up to about 2.9x).
+template <int KM, int R>
+__global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* src, uint32_t w, uint32_t h,
+                                                               uint32_t pitch, uint64_t fstride, uint32_t ih,
+                                                               uint32_t iw, OView out, uint32_t oh, uint32_t ow,
+                                                               uint32_t tiles_x, uint32_t tiles_y) {
+    constexpr uint32_t EXT = kAaT * R;
+    __shared__ uint2 tile[EXT * EXT];
+    const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
+    const uint32_t bt = blockIdx.x, txi = bt % tiles_x, rr = bt / tiles_x, tyi = rr % tiles_y, img = rr / tiles_y;
+    const uint32_t ox0 = txi * kAaT, oy0 = tyi * kAaT;
+    const uint32_t ox_last = min(ox0 + kAaT, ow) - 1, oy_last = min(oy0 + kAaT, oh) - 1;
+    const float sh = (float)ih / (float)oh, sw = (float)iw / (float)ow;
+    const float fsh = fmaxf(sh, 1.0f), fsw = fmaxf(sw, 1.0f);
+    const int ylo = max(0, (int)floorf(((float)oy0 + 0.5f) * sh - fsh + 0.5f));
+    const int yhi = min((int)ih, (int)floorf(((float)oy_last + 0.5f) * sh + fsh + 0.5f));
+    const int xlo = max(0, (int)floorf(((float)ox0 + 0.5f) * sw - fsw + 0.5f));
+    const int xhi = min((int)iw, (int)floorf(((float)ox_last + 0.5f) * sw + fsw + 0.5f));
+    const int ny = max(1, min(yhi - ylo, (int)EXT)), nx = max(1, min(xhi - xlo, (int)EXT));
+    const uint32_t* frame = src + img * fstride;
+#pragma unroll
+    for (uint32_t i = 0; i < R; i++)
+#pragma unroll
+        for (uint32_t j = 0; j < R; j++) {
+            const int row = min((int)(ty + kAaT * i), ny - 1), col = min((int)(tx + kAaT * j), nx - 1);
+            const uint32_t v = frame[(size_t)min(ylo + row, (int)h - 1) * pitch + min(xlo + col, (int)w - 1)];
+            tile[row * EXT + col] = uint2{(uint32_t)unit_f16(v, 0) | ((uint32_t)unit_f16(v, 1) << 16), unit_f16(v, 2)};
+        }
+    __syncthreads();
+    const uint32_t ox = ox0 + tx, oy = oy0 + ty;
+    if (ox >= ow || oy >= oh) return;
+    const float cy = ((float)oy + 0.5f) * sh, cx = ((float)ox + 0.5f) * sw;
+    const int ymin = max(0, (int)floorf(cy - fsh + 0.5f)), ymax = min((int)ih, (int)floorf(cy + fsh + 0.5f));
+    const int xmin = max(0, (int)floorf(cx - fsw + 0.5f)), xmax = min((int)iw, (int)floorf(cx + fsw + 0.5f));
+    float wx[KM];
+    int lc[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+        const int xx = xmin + j;
+        wx[j] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
+        lc[j] = min(max(xx - xlo, 0), nx - 1);
+    }
+    float acc[3] = {0.0f, 0.0f, 0.0f}, norm = 0.0f;
+#pragma unroll
+    for (int jy = 0; jy < KM; jy++) {
+        const int y = ymin + jy;
+        const float wy = y < ymax ? fmaxf(0.0f, 1.0f - fabsf(((float)y + 0.5f - cy) / fsh)) : 0.0f;
+        const uint2* lrow = tile + min(max(y - ylo, 0), ny - 1) * EXT;
+#pragma unroll
+        for (int jx = 0; jx < KM; jx++) {
+            const bool inw = (y < ymax) & (xmin + jx < xmax);
+            const float wgt = wx[jx] * wy;
+            const uint2 q = lrow[lc[jx]];
+            const float vv[3] = {h2f((uint16_t)q.x), h2f((uint16_t)(q.x >> 16)), h2f((uint16_t)q.y)};
+#pragma unroll
+            for (int i = 0; i < 3; i++) acc[i] = acc[i] + (inw ? vv[i] : 0.0f) * wgt;
+            norm = norm + wgt;
+        }
+    }
+    *reinterpret_cast<uint2*>(out.p + (((size_t)img * oh + oy) * ow + ox) * out.cs) =
+        uint2{(uint32_t)f2h(acc[0] / norm) | ((uint32_t)f2h(acc[1] / norm) << 16), (uint32_t)f2h(acc[2] / norm)};
+}
+
 // ---- host side ----------------------------------------------------------------------------------------------------
 
 constexpr uint64_t kMaxItems = 1ull << 31;
@@ -1461,6 +1723,105 @@ extern "C" int fhc_coarse_up(const fhc_tensor* o, const fhc_tensor* out, const f
         return launch("coarse_up", (uint64_t)oh * ow, [&](dim3 g, uint32_t items) {
             hipLaunchKernelGGL(coarse_up_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(o), outv(out), sv, hi,
                                wi, oh, ow, flow_scale, items);
+        });
+    });
+}
+
+// ---- the host's 8-bit frames -----------------------------------------------------------------------------------
+
+namespace {
+int check_frames(const char* op, const void* p, uint32_t n, uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                 uint32_t hp, uint32_t wp) {
+    if (!p) return fail(-1, "%s: null frame pointer", op);
+    if (reinterpret_cast<uintptr_t>(p) % 4) return fail(-1, "%s: frames must be 4-byte aligned", op);
+    if (pitch < w) return fail(-1, "%s: row pitch %u is below the width %u", op, pitch, w);
+    if (n > 1 && fstride < (uint64_t)pitch * h) return fail(-1, "%s: frame stride below pitch * h", op);
+    if (hp < h || wp < w) return fail(-1, "%s: padded size %u x %u below the frame's %u x %u", op, wp, hp, w, h);
+    if ((uint64_t)n * hp * wp >= kMaxItems) return fail(-1, "%s: too many pixels", op);
+    return 0;
+}
+}  // namespace
+
+extern "C" int fhc_rgba_in(const void* rgba, uint32_t n, uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                           const fhc_tensor* out, uint32_t hp, uint32_t wp, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)n * w * h == 0) return 0;
+        FHC_TRY(check_frames("rgba_in", rgba, n, w, h, pitch, fstride, hp, wp));
+        FHC_TRY(check(out, "rgba_in out", 3, false, true));
+        const bool v4 = out->cstride == 4 && out->c0 == 0 && reinterpret_cast<uintptr_t>(out->p) % 8 == 0;
+        return launch("rgba_in", (uint64_t)n * hp * wp, [&](dim3 g, uint32_t items) {
+            auto k = v4 ? rgba_in_kernel<true> : rgba_in_kernel<false>;
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, static_cast<const uint32_t*>(rgba), w, h,
+                               pitch, fstride, outv(out), hp, wp, items);
+        });
+    });
+}
+
+extern "C" int fhc_rgba_out(const fhc_tensor* in_, uint32_t n, uint32_t hp, uint32_t wp, void* rgba, uint32_t w,
+                            uint32_t h, uint32_t pitch, uint64_t fstride, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)n * w * h == 0) return 0;
+        FHC_TRY(check_frames("rgba_out", rgba, n, w, h, pitch, fstride, hp, wp));
+        FHC_TRY(check(in_, "rgba_out in", 3, false));
+        return launch("rgba_out", (uint64_t)n * h * w, [&](dim3 g, uint32_t items) {
+            hipLaunchKernelGGL(rgba_out_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(in_), hp, wp,
+                               static_cast<uint32_t*>(rgba), w, h, pitch, fstride, items);
+        });
+    });
+}
+
+extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                               uint32_t hp, uint32_t wp, const fhc_tensor* out, uint32_t oh, uint32_t ow,
+                               void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)n * oh * ow == 0) return 0;
+        FHC_TRY(check_frames("rgba_resize", rgba, n, w, h, pitch, fstride, hp, wp));
+        FHC_TRY(check(out, "rgba_resize out", 3, false, true));
+        if (out->cstride != 4 || out->c0 != 0 || reinterpret_cast<uintptr_t>(out->p) % 8)
+            return fail(-1, "rgba_resize: the output must have 8-byte 4-channel pixels (cstride 4, c0 0)");
+        if (oh > hp || ow > wp) return fail(-1, "rgba_resize: %u x %u is not a downscale of %u x %u", ow, oh, wp, hp);
+        const uint32_t taps = std::max(aa_taps(hp, oh), aa_taps(wp, ow));
+        const uint32_t ext = std::max(aa_tile_extent(hp, oh), aa_tile_extent(wp, ow));
+        if (taps > 8 || ext > 5 * kAaT)
+            return fail(-1, "rgba_resize: %u x %u -> %u x %u needs %u taps, a %u-pixel tile window (at most 8 and %u)",
+                        wp, hp, ow, oh, taps, ext, 5 * kAaT);
+        const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
+        auto k = ext <= 3 * kAaT ? (taps <= 6 ? rgba_resize_kernel<6, 3> : rgba_resize_kernel<8, 3>)
+                                 : (taps <= 6 ? rgba_resize_kernel<6, 5> : rgba_resize_kernel<8, 5>);
+        hipLaunchKernelGGL(k, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream,
+                           static_cast<const uint32_t*>(rgba), w, h, pitch, fstride, hp, wp, outv(out), oh, ow, tx, ty);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "rgba_resize: launch failed: %s", hipGetErrorString(e));
+    });
+}
+
+extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_t h, uint32_t pitch, uint32_t hp,
+                               uint32_t wp, const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rt,
+                               uint32_t hq, uint32_t wq, float fsx, float fsy, int cubic, uint32_t flags, void* out,
+                               uint32_t opitch, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)h * w == 0) return 0;
+        if (hq == 0 || wq == 0) return fail(-1, "render_rgba: empty quarter maps (%u x %u)", hq, wq);
+        if (flags > 3) return fail(-1, "render_rgba: flags %u (bit 0 decisive, bit 1 still)", flags);
+        if (w < 4) return fail(-1, "render_rgba: frames narrower than 4 pixels");
+        FHC_TRY(check_frames("render_rgba a", a, 1, w, h, pitch, 0, hp, wp));
+        FHC_TRY(check_frames("render_rgba b", b, 1, w, h, pitch, 0, hp, wp));
+        FHC_TRY(check_frames("render_rgba out", out, 1, w, h, opitch, 0, hp, wp));
+        FHC_TRY(check(flow, "render_rgba flow", 4, false));
+        FHC_TRY(check(vis, "render_rgba vis", 3, true));
+        FHC_TRY(check(rt, "render_rgba rt", 3, false));
+        const bool qv = flow->p == vis->p && flow->cstride == 8 && vis->cstride == 8 && flow->c0 == 0 &&
+                        vis->c0 == 4 && reinterpret_cast<uintptr_t>(flow->p) % 16 == 0 && vec4(4, {rt});
+        return launch("render_rgba", (uint64_t)h * w, [&](dim3 g, uint32_t items) {
+            auto k = cubic ? (qv ? render_rgba_kernel<true, true> : render_rgba_kernel<true, false>)
+                           : (qv ? render_rgba_kernel<false, true> : render_rgba_kernel<false, false>);
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, static_cast<const uint32_t*>(a),
+                               static_cast<const uint32_t*>(b), w, h, pitch, hp, wp, in(flow), in(vis), in(rt), hq,
+                               wq, fsx, fsy, flags, static_cast<uint32_t*>(out), opitch, items);
         });
     });
 }

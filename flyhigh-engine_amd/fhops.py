@@ -75,6 +75,11 @@ def _lib():
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
+            "fhc_rgba_in": [P, U, U, U, U, ctypes.c_uint64, T, U, U, P],
+            "fhc_rgba_out": [T, U, U, U, P, U, U, U, ctypes.c_uint64, P],
+            "fhc_rgba_resize": [P, U, U, U, U, ctypes.c_uint64, U, U, T, U, U, P],
+            "fhc_render_rgba": [P, P, U, U, U, U, U, T, T, T, U, U, ctypes.c_float, ctypes.c_float, I, U, P, U,
+                                P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -276,3 +281,64 @@ def coarse_up(o, out, state, oh, ow, flow_scale, stream=None):
     _, hi, wi, _ = o.shape
     _run("coarse_up", _lib().fhc_coarse_up(_ref(o), _ref(_v(out)), None if state is None else _ref(_v(state)), hi,
                                            wi, oh, ow, flow_scale, _stream_handle(stream)))
+
+
+# ---- the host's 8-bit frames (rgba_in.wgsl, rgba_out.wgsl; the Session's first and last steps, net/session.rs:56-63)
+# A batch of frames is a contiguous (n, h, w) int32 / uint32 device tensor of RGBA8 words (R | G << 8 | B << 16 |
+# A << 24); the padded size (hp, wp) is the frame's rounded up to 32 (the reference's working size).
+
+def _frames(f):
+    if f.dim() != 3 or not f.is_contiguous() or f.element_size() != 4:
+        raise FhcError("frames must be a contiguous (n, h, w) tensor of 32-bit RGBA8 words")
+    return f.shape
+
+
+def rgba_in(frames, hp: int, wp: int, out=None, stream=None):
+    """frames (n, h, w) -> BGR f16 (n, hp, wp, 4) (or into `out`: channels c0..c0+2; channel 3 of a 4-channel
+    pixel view written 0)."""
+    n, h, w = _frames(frames)
+    o = View(_pixels_like(frames, n, hp, wp)) if out is None else _v(out)
+    _run("rgba_in", _lib().fhc_rgba_in(frames.data_ptr(), n, w, h, w, h * w, _ref(o), hp, wp, _stream_handle(stream)))
+    return o.t
+
+
+def _pixels_like(t, n, h, w):
+    import torch
+    return torch.empty((n, h, w, 4), dtype=torch.int16, device=t.device)
+
+
+def rgba_out(x, h: int, w: int, out=None, stream=None):
+    """x: (n, hp, wp, cs) BGR f16 (view channels c0..c0+2) -> (n, h, w) int32 RGBA8 words, cropped, alpha 255."""
+    import torch
+    x = _v(x)
+    n, hp, wp, _ = x.shape
+    o = torch.empty((n, h, w), dtype=torch.int32, device=x.t.device) if out is None else out
+    _frames(o)
+    _run("rgba_out", _lib().fhc_rgba_out(_ref(x), n, hp, wp, o.data_ptr(), w, h, w, h * w, _stream_handle(stream)))
+    return o
+
+
+def rgba_resize(frames, hp: int, wp: int, oh: int, ow: int, out=None, stream=None):
+    """rgba_in of the frames at the padded size hp x wp, then the antialiased resize to oh x ow, in one launch:
+    (n, oh, ow, 4) BGR f16 with channel 3 zero."""
+    n, h, w = _frames(frames)
+    o = View(_pixels_like(frames, n, oh, ow)) if out is None else _v(out)
+    _run("rgba_resize", _lib().fhc_rgba_resize(frames.data_ptr(), n, w, h, w, h * w, hp, wp, _ref(o), oh, ow,
+                                               _stream_handle(stream)))
+    return o.t
+
+
+def render_rgba(fa, fb, flow, vis, rt, hp: int, wp: int, cubic=True, flags=0, fsx=1.0, fsy=1.0, out=None,
+                stream=None):
+    """render_pix of the padded frames (hp x wp) sampled from the RGBA8 frames fa, fb ((1, h, w) each) with the
+    quarter maps flow (4), vis (3), rt (3), written as RGBA8 (1, h, w): rgba_in, render, rgba_out in one launch."""
+    import torch
+    _, h, w = _frames(fa)
+    _frames(fb)
+    flow, vis, rt = _v(flow), _v(vis), _v(rt)
+    _, hq, wq, _ = flow.shape
+    o = torch.empty((1, h, w), dtype=torch.int32, device=fa.device) if out is None else out
+    _run("render_rgba", _lib().fhc_render_rgba(fa.data_ptr(), fb.data_ptr(), w, h, w, hp, wp, _ref(flow), _ref(vis),
+                                               _ref(rt), hq, wq, fsx, fsy, int(cubic), flags, o.data_ptr(), w,
+                                               _stream_handle(stream)))
+    return o

@@ -9,8 +9,11 @@ captured in a HIP graph; a checker can run the same program over the CPU oracle 
 NHWC f16 buffers (n, h, w, cstride) with the channel stride padded to 8 where a conv or an 8-byte path reads them;
 the graph's slices and scales are views (``V``) and its concats are buffers the producers write into by slice, so
 only a scaled input of a concat costs a copy (as the reference's chcopy does). The A and B branches share weights
-and run as a batch of 2 where their consumers read one tensor (resize, the first encoder pair, the first pool). The
-frame I/O around the network (rgba_in / rgba_out: the host's 8-bit frames) is not run here.
+and run as a batch of 2 where their consumers read one tensor (resize, the first encoder pair, the first pool). Given a
+frame size, the program starts from the host's two RGBA8 frames and ends with the generated RGBA8 frame, as the
+reference's Session does (net/session.rs:26-66): rgba_in, the antialiased downscale to the network size, the network,
+the render at the frame size and rgba_out (the downscale and the render each one launch on the GPU, reading the 8-bit
+frames directly).
 
 Differences of launch structure from the reference (same arithmetic): the encoders' outputs are copied into their
 slices of the 279-channel concat (and f16b into the streaming state) by one copy launch; consecutive convs whose
@@ -43,7 +46,8 @@ def f16_bits(a):
 
 
 def make_weights(seed: int = 0) -> dict:
-    """Random weights of the graph's architecture (there is no network access for the trained ones): He-normal
+    """Random weights of the graph's architecture (the trained ones, models/flyhighfg.bin, are licensed CC BY-NC
+    and stay out of this repository; model/blob.rs reads them where a host provides them): He-normal
     convs, small biases, PReLU slopes in [0.05, 0.3], an f16-representable FiLM MLP. Returns name -> (w OIHW, bias,
     slope or None) as f16 bits, and "film" -> (w1, b1, w2, b2) as f32 (the reference decodes its f16 weights to
     f32 for the MLP, model/blob.rs:32-41)."""
@@ -130,6 +134,21 @@ class ComposedChains:
         self.chcopy(V(dfilm.buf, dfilm.c0 + 4, -1.0), 1, V(dvis.buf, dvis.c0 + 1))
         self.binary(V(fv.buf, fv.c0 + 4), dvis, 3, V(out.buf, out.c0 + 4))
 
+    def frame_input(self, frames, full, ab: V, hp: int, wp: int, oh: int, ow: int):
+        """The two RGBA8 frames -> the network's inputs A, B at oh x ow: rgba_in to the padded frame size, then the
+        antialiased resize (net/session.rs:56-60, net/build.rs:615-620)."""
+        self.rgba_in(frames, V(full), hp, wp)
+        self.interp(V(full), 3, ab, oh, ow, True)
+
+    def frame_render(self, frames, full, pic, flow: V, vis: V, rt: V, out_frames, hp: int, wp: int, fsx: float,
+                     fsy: float, cubic: bool, flags: int):
+        """The frame-size render of the internal-size mode (net/build.rs:717-736) and rgba_out (net/session.rs:63):
+        render_pix of the padded frames A, B (rgba_in) at hp x wp with the flow scaled per axis, then the crop to
+        the frame's RGBA8."""
+        self.rgba_in(frames, V(full), hp, wp)
+        self.render(V(self.image(full, 0)), V(self.image(full, 1)), flow, vis, rt, V(pic), cubic, flags, fsx, fsy)
+        self.rgba_out(V(pic), out_frames)
+
     def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
         for i in range(2):
             self.warp(V(self.image(q.buf, i), q.c0), 3, V(flow.buf, flow.c0 + 2 * i, flow.scale),
@@ -156,6 +175,16 @@ class GpuBackend(ComposedChains):
 
     def zeros(self, n, h, w, cs):
         return self.torch.zeros((n, h, w, cs), dtype=self.torch.int16, device=self.dev)
+
+    def frames(self, n, h, w):
+        return self.torch.zeros((n, h, w), dtype=self.torch.int32, device=self.dev)
+
+    def upload_frames(self, buf, rgba):
+        buf.copy_(self.torch.from_numpy(np.ascontiguousarray(rgba, np.uint32).view(np.int32)))
+
+    def host_frames(self, buf):
+        self.torch.cuda.synchronize()
+        return buf.cpu().numpy().view(np.uint32)
 
     def image(self, buf, i):
         return buf[i:i + 1]
@@ -251,9 +280,29 @@ class GpuBackend(ComposedChains):
     def blendmix(self, wa: V, wb: V, vis: V, out: V):
         self.fh.blendmix(self._v(wa), self._v(wb), self._v(vis), out=self._v(out), stream=self.stream)
 
-    def render(self, a: V, b: V, flow: V, vis: V, rt: V, out: V, cubic: bool, flags: int):
-        self.fh.render(self._v(a), self._v(b), self._v(flow), self._v(vis), self._v(rt), cubic, flags, flow.scale,
-                       flow.scale, out=self._v(out), stream=self.stream)
+    def render(self, a: V, b: V, flow: V, vis: V, rt: V, out: V, cubic: bool, flags: int, fsx=None, fsy=None):
+        self.fh.render(self._v(a), self._v(b), self._v(flow), self._v(vis), self._v(rt), cubic, flags,
+                       flow.scale if fsx is None else fsx, flow.scale if fsy is None else fsy, out=self._v(out),
+                       stream=self.stream)
+
+    def rgba_in(self, frames, out: V, hp: int, wp: int):
+        self.fh.rgba_in(frames, hp, wp, out=self._v(out), stream=self.stream)
+
+    def rgba_out(self, x: V, out_frames):
+        _, h, w = out_frames.shape
+        self.fh.rgba_out(self._v(x), h, w, out=out_frames, stream=self.stream)
+
+    def frame_input(self, frames, full, ab: V, hp: int, wp: int, oh: int, ow: int):
+        if not self.chains:
+            return super().frame_input(frames, full, ab, hp, wp, oh, ow)
+        self.fh.rgba_resize(frames, hp, wp, oh, ow, out=self._v(ab), stream=self.stream)
+
+    def frame_render(self, frames, full, pic, flow: V, vis: V, rt: V, out_frames, hp: int, wp: int, fsx: float,
+                     fsy: float, cubic: bool, flags: int):
+        if not self.chains:
+            return super().frame_render(frames, full, pic, flow, vis, rt, out_frames, hp, wp, fsx, fsy, cubic, flags)
+        self.fh.render_rgba(frames[0:1], frames[1:2], self._v(flow), self._v(vis), self._v(rt), hp, wp, cubic, flags,
+                            fsx, fsy, out=out_frames, stream=self.stream)
 
     # the fused chains (one launch each) unless asked for the ops one by one
     def coarse_up(self, o: V, out: V, state: Optional[V], oh: int, ow: int, flow_scale: float):
@@ -302,8 +351,29 @@ class FlyHighFG:
     bicubic, models/flyhighfg.json:67) and mode word (0: neither the decisive blend nor the still test, the
     engine's defaults, options.rs:306-327)."""
 
-    def __init__(self, be, net_w: int = 864, net_h: int = 480, cubic: bool = True, render_flags: int = 0):
+    def __init__(self, be, net_w: int = 864, net_h: int = 480, cubic: bool = True, render_flags: int = 0,
+                 frame: Optional[tuple] = None):
         self.be = be
+        # frame (w, h): the program starts from the host's two RGBA8 frames (``frames``, uploaded by the caller) and
+        # ends with the generated RGBA8 frame (``rgba``), as the reference's Session does (net/session.rs:26-66).
+        # The frames are padded to a multiple of 32; when that differs from the network size the network runs on
+        # the antialiased downscale and the render runs at the padded frame size (the internal-size mode,
+        # net/build.rs:549-551, :615-620, :717-736). Without a frame the caller fills AB at network size.
+        self.frame = frame
+        if frame is not None:
+            fw, fh = frame
+            self.hp, self.wp = (fh + 31) // 32 * 32, (fw + 31) // 32 * 32
+            self.internal = (self.wp, self.hp) != (net_w, net_h)
+            self.frames = be.frames(2, fh, fw)     # A, B: RGBA8 words
+            self.rgba = be.frames(1, fh, fw)       # the generated frame
+            # the composed chains' full-size intermediates (rgba_in's pictures, the render's f16 picture); the fused
+            # GPU chains never touch them
+            composed = not getattr(be, "chains", False)
+            self.full = be.zeros(2, self.hp, self.wp, 4) if composed else None
+            self.pic = be.zeros(1, self.hp, self.wp, 4) if composed and self.internal else None
+            # the flow's scale per axis at the frame size: ftq.scale * wp / iwp (net/build.rs:720), in f32
+            self.fsx = float(np.float32(self.wp) / np.float32(net_w))
+            self.fsy = float(np.float32(self.hp) / np.float32(net_h))
         qh, qw = net_h // 4, net_w // 4
         e8h, e8w = (qh - 1) // 2 + 1, (qw - 1) // 2 + 1
         e16h, e16w = (e8h - 1) // 2 + 1, (e8w - 1) // 2 + 1
@@ -344,6 +414,12 @@ class FlyHighFG:
         """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1)."""
         be, S = self.be, self.shape
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
+        if self.frame is not None:  # the frames -> A, B (rgba_in; in the internal-size mode, the downscale)
+            nh, nw = S["net"]
+            if self.internal:
+                be.frame_input(self.frames, self.full, V(self.AB), self.hp, self.wp, nh, nw)
+            else:
+                be.rgba_in(self.frames, V(self.AB), nh, nw)
         be.pair_input(V(self.AB), V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16), qh, qw)  # 0-1, 14-24
         be.sad(V(self.l16, 0), V(self.l16, 1), V(self.cin, 230), 3)                           # 25, 26; 19-20 zeros
         be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)                 # 2-4, 8-10
@@ -380,9 +456,31 @@ class FlyHighFG:
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
         be.pair("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), False)        # 79, 80
         be.unary(V(self.rr), 3, V(self.Rt), 2)                                                # 81: affine_out
+        if self.frame is not None and self.internal:  # the render at the frame size, to the RGBA8 frame
+            be.frame_render(self.frames, self.full, self.pic, V(self.up7, 0), V(self.up7, 4), V(self.Rt), self.rgba,
+                            self.hp, self.wp, self.fsx, self.fsy, self.cubic, self.render_flags)
+            return
         be.render(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.up7, 0), V(self.up7, 4), V(self.Rt),
                   V(self.out), self.cubic, self.render_flags)                                 # 82: render_pix
+        if self.frame is not None:
+            be.rgba_out(V(self.out), self.rgba)
 
 
 def cpu_threads():
     return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def procedural_frame(w: int, h: int, dx: int = 0, dy: int = 0) -> np.ndarray:
+    """A synthetic RGBA8 frame (h, w) of uint32 words, the kind the reference's bench generates
+    (crates/flyhigh-cli/src/cli/bench.rs:33-51): smooth sine patterns per channel plus 0.1 of hashed noise, the
+    whole picture shifted by (dx, dy) pixels, alpha 255. Test and benchmark data only."""
+    yy, xx = np.mgrid[0:h, 0:w].astype(np.int64)
+    sx, sy = xx + dx, yy + dy
+    hsh = ((sx * 73856093) & 0xFFFFFFFF) ^ ((sy * 19349663) & 0xFFFFFFFF)
+    n = (((hsh * 2654435761) & 0xFFFFFFFF) >> 24).astype(np.float32) / np.float32(255.0)
+    fx, fy = sx.astype(np.float32), sy.astype(np.float32)
+    r = 0.5 + 0.35 * np.sin(fx * 0.013) * np.cos(fy * 0.017) + 0.1 * n
+    g = 0.5 + 0.35 * np.cos(fx * 0.009 + 1.0) * np.sin(fy * 0.021) + 0.1 * n
+    b = 0.5 + 0.35 * np.sin((fx + fy) * 0.011) + 0.1 * n
+    byte = lambda v: (np.clip(v, 0.0, 1.0) * 255.0).astype(np.uint32)  # noqa: E731
+    return (byte(r) | (byte(g) << 8) | (byte(b) << 16) | np.uint32(0xFF000000)).astype(np.uint32)

@@ -115,6 +115,40 @@ int fhc_render(const fhc_tensor* a, const fhc_tensor* b, const fhc_tensor* flow,
                const fhc_tensor* rt, const fhc_tensor* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx,
                float fsy, int cubic, uint32_t flags, void* stream);
 
+/* ---- The host's 8-bit frames. A frame is RGBA8, one 32-bit word per pixel (R | G << 8 | B << 16 | A << 24), rows
+ * `pitch` words apart, n frames `fstride` words apart; hp x wp is the padded working size (the frame rounded up to
+ * 32). The network reads BGR f16 in [0, 1], replicate-padded: padded pixel (x, y) is frame pixel (min(x, w - 1),
+ * min(y, h - 1)). Frames must be 4-byte aligned. */
+
+/* rgba_in: n frames -> BGR f16(byte / 255), padded to hp x wp, channels c0..c0 + 2 of out (n, hp, wp); a view of
+ * 4-channel pixels (cstride 4, c0 0, 8-byte aligned) gets channel 3 written 0. Replaces the Session's rgba_in steps
+ * (crates/flyhigh-engine/src/net/session.rs:56-60, shaders/rgba_in.wgsl:11-19). */
+int fhc_rgba_in(const void* rgba, uint32_t n, uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                const fhc_tensor* out, uint32_t hp, uint32_t wp, void* stream);
+
+/* rgba_out: channels c0..c0 + 2 (B, G, R) of in (n, hp, wp) -> n frames of w x h, each byte
+ * u32(clamp(v, 0, 1) * 255 + 0.5), alpha 255 (the crop of the padding). Replaces the Session's rgba_out step
+ * (net/session.rs:63, shaders/rgba_out.wgsl:9-18). */
+int fhc_rgba_out(const fhc_tensor* in, uint32_t n, uint32_t hp, uint32_t wp, void* rgba, uint32_t w, uint32_t h,
+                 uint32_t pitch, uint64_t fstride, void* stream);
+
+/* rgba_in of n frames at hp x wp, then the antialiased resize to oh x ow (fhc_interpolate with antialias 1), in one
+ * launch that reads the 8-bit frames directly: the internal-size mode's inputs A, B (net/session.rs:56-60, then
+ * net/build.rs:615-620). out has 4-channel pixels (cstride 4, c0 0, 8-byte aligned), channel 3 written 0.
+ * Bit-identical to the two steps. Downscales up to about 5x (at most 8 taps per axis). */
+int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                    uint32_t hp, uint32_t wp, const fhc_tensor* out, uint32_t oh, uint32_t ow, void* stream);
+
+/* The frame-size render of the internal-size mode and rgba_out in one launch: render_pix (fhc_render) of the padded
+ * frames a and b (each w x h RGBA8, rows `pitch` words apart, read as rgba_in converts them) at hp x wp from the maps
+ * flow / vis / rt at hq x wq, the flow's x times fsx and y times fsy (ftq.scale * wp / iwp and * hp / ihp,
+ * net/build.rs:717-736), each result rounded to f16 and written as the RGBA8 frame out (w x h, rows opitch words
+ * apart, alpha 255). Bit-identical to rgba_in, fhc_render and rgba_out in turn. Flow and vis as channels 0-3 and
+ * 4-6 of one 16-byte aligned 8-channel view, with rt of 4-channel pixels, take two loads a map tap. w >= 4. */
+int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_t h, uint32_t pitch, uint32_t hp, uint32_t wp,
+                    const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rt, uint32_t hq, uint32_t wq,
+                    float fsx, float fsy, int cubic, uint32_t flags, void* out, uint32_t opitch, void* stream);
+
 /* ---- The graph's op chains, fused. Each computes what its ops compute one after another (the same f32 operations
  * and f16 roundings at the tensors the ops store); no reference counterpart as one call: each replaces the listed
  * planner arms run in sequence. A and B arrive as a batch of 2. */

@@ -372,3 +372,31 @@ void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, cons
             }
         }
 }
+
+/* shaders/rgba_in.wgsl:11-19 (the planar output [3][hp][wp] written as channels 0-2 of an NHWC view) */
+void fho_rgba_in(const uint32_t* rgba, uint32_t n, uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                 const fho_view* out, uint32_t hp, uint32_t wp) {
+    for (uint32_t b = 0; b < n; b++)
+        for (uint32_t y = 0; y < hp; y++)
+            for (uint32_t x = 0; x < wp; x++) {
+                const uint32_t v = rgba[b * fstride + (size_t)(y < h ? y : h - 1) * pitch + (x < w ? x : w - 1)];
+                wr(out, hp, wp, b, y, x, 0, (float)((v >> 16) & 0xffu) / 255.0f);
+                wr(out, hp, wp, b, y, x, 1, (float)((v >> 8) & 0xffu) / 255.0f);
+                wr(out, hp, wp, b, y, x, 2, (float)(v & 0xffu) / 255.0f);
+            }
+}
+
+/* rgba_out.wgsl:10: q(v) = u32(clamp(f32(v), 0, 1) * 255 + 0.5) */
+static uint32_t q8(float v) { return (uint32_t)(fminf(fmaxf(v, 0.0f), 1.0f) * 255.0f + 0.5f); }
+
+/* shaders/rgba_out.wgsl:12-18 (channels 0-2 of an NHWC view of hp x wp, cropped to w x h) */
+void fho_rgba_out(const fho_view* in, uint32_t n, uint32_t hp, uint32_t wp, uint32_t* rgba, uint32_t w, uint32_t h,
+                  uint32_t pitch, uint64_t fstride) {
+    for (uint32_t b = 0; b < n; b++)
+        for (uint32_t y = 0; y < h; y++)
+            for (uint32_t x = 0; x < w; x++)
+                rgba[b * fstride + (size_t)y * pitch + x] = q8(rd(in, hp, wp, b, (int)y, (int)x, 2)) |
+                                                            (q8(rd(in, hp, wp, b, (int)y, (int)x, 1)) << 8) |
+                                                            (q8(rd(in, hp, wp, b, (int)y, (int)x, 0)) << 16) |
+                                                            0xff000000u;
+}

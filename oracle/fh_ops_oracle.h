@@ -71,6 +71,16 @@ void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, cons
                 const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx, float fsy,
                 int cubic, uint32_t flags);
 
+/* rgba_in: n RGBA8 frames (R | G << 8 | B << 16 | A << 24 per 32-bit word, rows `pitch` words apart, frame i at
+ * rgba + i * fstride words) -> BGR f16(byte / 255), replicate-padded to hp x wp, channels 0-2 of out:
+ * shaders/rgba_in.wgsl:11-19 */
+void fho_rgba_in(const uint32_t* rgba, uint32_t n, uint32_t w, uint32_t h, uint32_t pitch, uint64_t fstride,
+                 const fho_view* out, uint32_t hp, uint32_t wp);
+/* rgba_out: channels 0-2 (BGR) of an hp x wp view -> RGBA8 words, cropped to w x h, alpha 255:
+ * shaders/rgba_out.wgsl:9-18 */
+void fho_rgba_out(const fho_view* in, uint32_t n, uint32_t hp, uint32_t wp, uint32_t* rgba, uint32_t w, uint32_t h,
+                  uint32_t pitch, uint64_t fstride);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,10 +1,19 @@
-"""The CPU oracle as a backend of flyhighfg_net's program (the checker of the end-to-end frame): every conv through
-the oracle's tiled-order conv (multithreaded over rows), every other op through fh_ops_oracle.c, on numpy NHWC
-buffers with the same views and slices as the GPU backend."""
+"""The CPU oracle as a backend of flyhighfg_net's program: TEST INFRASTRUCTURE ONLY (the checker of the end-to-end
+frame in tests/, and the CPU baseline of bench.py). Every conv runs through the oracle's tiled-order conv
+(multithreaded over rows), every other op through fh_ops_oracle.c, on numpy NHWC buffers with the same views and
+slices as the GPU backend; the fused op chains run as their ops one after another (ComposedChains)."""
+import os
+import sys
+
 import numpy as np
 
-from fhtest import oracle
-from flyhighfg_net import CONVS, ComposedChains, cpu_threads
+HERE = os.path.dirname(os.path.abspath(__file__))
+for _p in (HERE, os.path.join(HERE, "..", "flyhigh-engine_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import oracle  # noqa: E402
+from flyhighfg_net import CONVS, ComposedChains, cpu_threads  # noqa: E402
 
 
 class CpuBackend(ComposedChains):
@@ -13,6 +22,15 @@ class CpuBackend(ComposedChains):
 
     def zeros(self, n, h, w, cs):
         return np.zeros((n, h, w, cs), np.uint16)
+
+    def frames(self, n, h, w):
+        return np.zeros((n, h, w), np.uint32)
+
+    def upload_frames(self, buf, rgba):
+        buf[...] = rgba
+
+    def host_frames(self, buf):
+        return buf
 
     def image(self, buf, i):
         return buf[i:i + 1]
@@ -81,8 +99,17 @@ class CpuBackend(ComposedChains):
         self._put(out, 3, oracle.blendmix(wa.buf, wb.buf, vis.buf, vis_c0=vis.c0, vis_scale=vis.scale,
                                           wa_c0=wa.c0, wb_c0=wb.c0))
 
-    def render(self, a, b, flow, vis, rt, out, cubic, flags):
+    def render(self, a, b, flow, vis, rt, out, cubic, flags, fsx=None, fsy=None):
         _, hq, wq, _ = flow.buf.shape
         self._put(out, 3, oracle.render(a.buf, b.buf, flow.buf, vis.buf, rt.buf, hq, wq, cubic=cubic, flags=flags,
-                                        a_c0=a.c0, b_c0=b.c0, flow_c0=flow.c0, fsx=flow.scale, fsy=flow.scale,
+                                        a_c0=a.c0, b_c0=b.c0, flow_c0=flow.c0,
+                                        fsx=flow.scale if fsx is None else fsx,
+                                        fsy=flow.scale if fsy is None else fsy,
                                         vis_c0=vis.c0, vis_scale=vis.scale, rt_c0=rt.c0))
+
+    def rgba_in(self, frames, out, hp, wp):
+        self._put(out, 3, oracle.rgba_in(frames, hp, wp))
+
+    def rgba_out(self, x, out_frames):
+        _, h, w = out_frames.shape
+        out_frames[...] = oracle.rgba_out(x.buf, h, w, c0=x.c0)

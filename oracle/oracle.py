@@ -150,6 +150,8 @@ def _ops_lib():
             "fho_unary": [V, V, U, U, U, U, I, ctypes.c_float, ctypes.c_float],
             "fho_chcopy": [V, V, U, U, U, U],
             "fho_render": [V, V, V, V, V, V, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U],
+            "fho_rgba_in": [ctypes.c_void_p, U, U, U, U, ctypes.c_uint64, V, U, U],
+            "fho_rgba_out": [V, U, U, U, ctypes.c_void_p, U, U, U, ctypes.c_uint64],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -260,3 +262,20 @@ def render(a, b, flow, vis, rt, hq, wq, cubic=True, flags=0, a_c0=0, b_c0=0, flo
     _ops_lib().fho_render(_view(a, a_c0), _view(b, b_c0), _view(flow, flow_c0), _view(vis, vis_c0, vis_scale),
                           _view(rt, rt_c0), _view(y), h, w, hq, wq, fsx, fsy, int(cubic), flags)
     return y
+
+
+def rgba_in(frames, hp, wp, cs=3):
+    """frames: (n, h, w) uint32 RGBA8 words; returns (n, hp, wp, cs) f16 bits, channels 0-2 BGR (the rest 0)."""
+    frames = np.ascontiguousarray(frames, np.uint32)
+    n, h, w = frames.shape
+    y = _out(n, hp, wp, cs)
+    _ops_lib().fho_rgba_in(frames.ctypes.data, n, w, h, w, h * w, _view(y), hp, wp)
+    return y
+
+
+def rgba_out(x, h, w, c0=0):
+    """x: (n, hp, wp, cs) f16 bits (channels c0.. BGR); returns (n, h, w) uint32 RGBA8 words, alpha 255."""
+    n, hp, wp, _ = x.shape
+    out = np.zeros((n, h, w), np.uint32)
+    _ops_lib().fho_rgba_out(_view(x, c0), n, hp, wp, out.ctypes.data, w, h, w, h * w)
+    return out

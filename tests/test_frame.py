@@ -1,10 +1,12 @@
 """The end-to-end FlyHighFG pair() + mid() program (flyhigh-engine_amd/flyhighfg_net.py).
 
 On the CPU: the program's wiring runs over the oracle backend at a small network size (shapes, slices, every op
-called with views it accepts, finite outputs, a FiLM vector that depends on t). On the GPU: the same program through
-libfhconv.so (fused conv pairs, the network ops) against the oracle composition with the same weights and inputs,
-per output tensor |diff| <= 1e-2 * max|ref| (the conv path's bar; the ops themselves are bit-exact or within an ulp,
-and the convs' f32 summation order differs from the oracle's, so differences propagate through ~20 layers).
+called with views it accepts, finite outputs, a FiLM vector that depends on t), and from 8-bit frames through the
+internal-size mode. On the GPU: the same program through libfhconv.so (fused conv pairs, the network ops, the fused
+frame input and render) against the oracle composition with the same weights and inputs: per network tensor
+|diff| <= 1e-2 * max|ref| (the conv path's bar; the ops themselves are bit-exact or within an ulp, and the convs'
+f32 summation order differs from the oracle's, so differences propagate through ~20 layers), and for the generated
+8-bit frame the same bar in bytes (1e-2 * 255) plus one quantization step.
 """
 import numpy as np
 import pytest
@@ -14,6 +16,7 @@ from frame_oracle import CpuBackend
 import flyhighfg_net as net
 
 OUTPUTS = [("out", 3), ("up7", 7), ("Rt", 3), ("state_out", 76), ("o", 12), ("h", 48), ("cin", 279)]
+FRAME_OUTPUTS = [("up7", 7), ("Rt", 3), ("state_out", 76), ("o", 12), ("h", 48), ("cin", 279), ("AB", 3)]
 
 
 def inputs(seed, net_w, net_h):
@@ -26,12 +29,26 @@ def inputs(seed, net_w, net_h):
     return f16_bits(ab)
 
 
+def frames(w, h, dx=12, dy=0):
+    """Two RGBA8 frames: the procedural picture and the same moved by (dx, dy)."""
+    return np.stack([net.procedural_frame(w, h), net.procedural_frame(w, h, dx, dy)])
+
+
 def run(be, W, net_w, net_h, ab, t=0.5):
     f = net.FlyHighFG(be, net_w, net_h)
     if isinstance(f.AB, np.ndarray):
         f.AB[...] = ab
     else:
         f.AB.copy_(be.upload(ab))
+    f.pair()
+    f.mid(t, W)
+    return f
+
+
+def run_frames(be, W, net_w, net_h, fr, t=0.5):
+    h, w = fr.shape[1:]
+    f = net.FlyHighFG(be, net_w, net_h, frame=(w, h))
+    be.upload_frames(f.frames, fr)
     f.pair()
     f.mid(t, W)
     return f
@@ -47,6 +64,25 @@ def test_program_runs_on_the_oracle_backend():
     assert np.all(f.cin[..., 150:230] == 0)  # side and state enter as zeros
     assert np.all(f.fx[..., 82:130] == 0)    # h enters the fine loop as zeros
     assert not np.array_equal(net.film_mlp(W, 0.25), net.film_mlp(W, 0.75))
+
+
+def test_program_runs_from_frames_in_both_modes():
+    """From two RGBA8 frames: 300 x 150 pads to 320 x 160, which is the network size (no internal mode: rgba_in
+    feeds the network and rgba_out crops the graph's own render); with a 128 x 64 network the same frames take the
+    internal-size mode (downscale, frame-size render). Both give a full RGBA8 frame with alpha 255; a still pair
+    (A == B) renders A back where the picture is smooth."""
+    W = net.make_weights(4)
+    fr = frames(300, 150, dx=3)
+    direct = run_frames(CpuBackend(W), W, 320, 160, fr)
+    assert not direct.internal and direct.rgba.shape == (1, 150, 300)
+    internal = run_frames(CpuBackend(W), W, 128, 64, fr)
+    assert internal.internal and (internal.wp, internal.hp) == (320, 160)
+    assert internal.fsx == np.float32(320) / np.float32(128) and internal.fsy == np.float32(160) / np.float32(64)
+    for f in (direct, internal):
+        assert np.all(f.rgba >> 24 == 255)
+        assert np.any(f.rgba != f.rgba[0, 0, 0])
+    # the network-size input is the downscale of the padded frame (channels B, G, R)
+    assert np.array_equal(internal.AB[..., 3], np.zeros_like(internal.AB[..., 3]))
 
 
 @pytest.mark.gpu
@@ -68,20 +104,69 @@ def test_gpu_frame_matches_the_oracle_composition(net_w, net_h, fuse):
         assert err <= tol, name
 
 
+def _check_frame(gb, got, ref):
+    for name, c in FRAME_OUTPUTS:
+        g = gb.host(getattr(got, name))[..., :c].view(np.float16).astype(np.float64)
+        r = getattr(ref, name)[..., :c].view(np.float16).astype(np.float64)
+        err, tol = np.abs(g - r).max(), 1e-2 * np.abs(r).max()
+        print(f"  {name}: max|diff| {err:.3g} (bar {tol:.3g})", flush=True)
+        assert err <= tol, name
+    g, r = gb.host_frames(got.rgba), ref.rgba
+    diff = np.zeros(g.shape, np.int32)
+    for sh in (0, 8, 16, 24):
+        diff = np.maximum(diff, np.abs(((g >> sh) & 0xFF).astype(np.int32) - ((r >> sh) & 0xFF).astype(np.int32)))
+    print(f"  rgba: max byte diff {diff.max()}, {np.mean(diff == 0):.5f} of the pixels identical", flush=True)
+    assert diff.max() <= int(1e-2 * 255) + 1
+
+
+@pytest.mark.gpu
+def test_gpu_1080p_frame_from_rgba_matches_the_oracle_composition():
+    """The 1080p configuration as the reference runs it (net/session.rs:26-66 with Internal::Auto): two seeded
+    1920 x 1080 RGBA8 frames (the procedural picture and the same moved 12 pixels), padded to 1920 x 1088, downscaled
+    to the 864 x 480 network, pair() and mid(0.5), rendered at 1920 x 1088 and cropped to the RGBA8 frame."""
+    import torch
+    print("frame 1920x1080 from rgba", flush=True)
+    W = net.make_weights(5)
+    fr = frames(1920, 1080)
+    ref = run_frames(CpuBackend(W), W, 864, 480, fr)
+    gb = net.GpuBackend(W, stream=torch.cuda.current_stream())
+    got = run_frames(gb, W, 864, 480, fr)
+    torch.cuda.synchronize()
+    assert got.internal and (got.wp, got.hp) == (1920, 1088)
+    _check_frame(gb, got, ref)
+
+
+@pytest.mark.gpu
+def test_gpu_small_frame_without_internal_mode_matches_the_oracle():
+    import torch
+    print("frame 300x150 from rgba, network = padded frame", flush=True)
+    W = net.make_weights(6)
+    fr = frames(300, 150, dx=5, dy=-2)
+    ref = run_frames(CpuBackend(W), W, 320, 160, fr)
+    gb = net.GpuBackend(W, stream=torch.cuda.current_stream())
+    got = run_frames(gb, W, 320, 160, fr)
+    torch.cuda.synchronize()
+    assert not got.internal
+    _check_frame(gb, got, ref)
+
+
 @pytest.mark.gpu
 def test_fused_chains_equal_their_ops_on_the_gpu():
-    """The four fused op chains (pyramid, fine input, flow_t / vis_t, refine input) against the same chains run op
-    by op on the GPU, in the whole frame: the same f32 operations and roundings, so every output is bit-identical."""
+    """The fused op chains (pyramid, fine input, flow_t / vis_t, refine input, and the frame's input and render
+    from RGBA8) against the same chains run op by op on the GPU, in a whole frame from RGBA8 frames in the
+    internal-size mode: the same f32 operations and roundings, so every output is bit-identical."""
     import torch
     W = net.make_weights(3)
-    ab = inputs(3, 256, 128)
+    fr = frames(600, 300, dx=7, dy=2)
     outs = []
     for chains in (True, False):
         gb = net.GpuBackend(W, stream=torch.cuda.current_stream(), chains=chains)
-        f = run(gb, W, 256, 128, ab, t=0.3)
+        f = run_frames(gb, W, 256, 128, fr, t=0.3)
         extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("ftvt", 7), ("d", 7),
-                 ("dfilm", 5), ("wt36", 36), ("f16", 72)]
-        outs.append({name: gb.host(getattr(f, name))[..., :c].copy() for name, c in OUTPUTS + extra})
+                 ("dfilm", 5), ("wt36", 36), ("f16", 72), ("AB", 4)]
+        got = {name: gb.host(getattr(f, name))[..., :c].copy() for name, c in FRAME_OUTPUTS + extra}
+        got["rgba"] = gb.host_frames(f.rgba).copy()
+        outs.append(got)
     diffs = []
     for name in outs[0]:
         bad = np.argwhere(outs[0][name] != outs[1][name])

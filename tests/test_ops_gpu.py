@@ -275,3 +275,106 @@ def test_empty_inputs_are_no_ops_and_bad_views_are_errors():
     with pytest.raises(fh.FhcError, match="radius"):
         fh.sad(x, x, 8)
     torch.cuda.synchronize()
+
+
+# ---- the host's 8-bit frames (rgba_in.wgsl, rgba_out.wgsl) and the fused frame-size kernels -------------------------
+
+def _frames(rng, n, h, w):
+    return rng.integers(0, 2 ** 32, (n, h, w), dtype=np.uint64).astype(np.uint32)
+
+
+def dev32(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.uint32).view(np.int32)).to("cuda")
+
+
+def host32(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy().view(np.uint32)
+
+
+@pytest.mark.parametrize("n,h,w,hp,wp,cs,c0", [(2, 1080, 1920, 1088, 1920, 4, 0), (1, 37, 53, 64, 64, 4, 0),
+                                               (2, 37, 53, 64, 64, 7, 2)])
+def test_rgba_in_and_out_match_oracle(n, h, w, hp, wp, cs, c0):
+    """Bit-exact: rgba_in's f16 values (BGR, /255, replicate padding) through a 4-channel pixel view (channel 3
+    written 0) or a wider view (its other channels untouched), and rgba_out's bytes of the crop."""
+    import torch
+    say("rgba in/out", n, h, w, hp, wp, cs, c0)
+    fh = fhops()
+    rng = np.random.default_rng(h + cs)
+    fr = _frames(rng, n, h, w)
+    want = oracle.rgba_in(fr, hp, wp)
+    buf = dev(np.full((n, hp, wp, cs), SENTINEL, np.uint16))
+    fh.rgba_in(dev32(fr), hp, wp, out=fh.View(buf, c0))
+    got = host(buf)
+    exact(got[..., c0:c0 + 3], want, "rgba_in")
+    if cs == 4:
+        exact(got[..., 3], np.zeros_like(got[..., 3]), "rgba_in channel 3")
+    else:
+        assert np.all(got[..., :c0] == SENTINEL) and np.all(got[..., c0 + 3:] == SENTINEL)
+    # rgba_out of random f16 pictures in [-0.2, 1.2] (clamped) and of rgba_in's own output (the round trip)
+    pic = rand(rng, (n, hp, wp, cs), -0.2, 1.2)
+    exact(host32(fh.rgba_out(fh.View(dev(pic), c0), h, w)), oracle.rgba_out(pic, h, w, c0=c0), "rgba_out")
+    exact(host32(fh.rgba_out(fh.View(buf, c0), h, w)), fr | np.uint32(0xFF000000), "rgba_out(rgba_in)")
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("h,w,oh,ow", [(1080, 1920, 480, 864), (150, 300, 64, 128), (61, 97, 30, 40)])
+def test_rgba_resize_equals_rgba_in_then_the_antialiased_resize(h, w, oh, ow):
+    """The fused frame input against the oracle's rgba_in at the padded size then its antialiased interpolate:
+    bit-exact (the same f16 inputs, f32 operations in the same order, one rounding)."""
+    say("rgba_resize", h, w, oh, ow)
+    fh = fhops()
+    rng = np.random.default_rng(w)
+    hp, wp = (h + 31) // 32 * 32, (w + 31) // 32 * 32
+    fr = _frames(rng, 2, h, w)
+    full = oracle.rgba_in(fr, hp, wp)
+    want = oracle.interp(full, 3, oh, ow, aa=True)
+    got = host(fh.rgba_resize(dev32(fr), hp, wp, oh, ow))
+    exact(got[..., :3], want, "rgba_resize")
+    exact(got[..., 3], np.zeros_like(got[..., 3]), "rgba_resize channel 3")
+
+
+@pytest.mark.parametrize("cubic,flags,amp,size", [(True, 0, 6, (1080, 1920)), (False, 0, 6, (1080, 1920)),
+                                                  (True, 2, 3, (150, 300)), (True, 3, 6, (150, 300)),
+                                                  (False, 3, 2, (97, 130)), (True, 0, 40, (97, 130))])
+def test_render_rgba_matches_rgba_in_render_rgba_out(cubic, flags, amp, size):
+    """The fused frame-size render from the RGBA8 frames to the RGBA8 frame, against the oracle's rgba_in (padded),
+    render at the padded size with the flow scaled per axis (the internal-size mode, maps at a non-integer ratio),
+    and rgba_out: bytes within 1 everywhere (expf's last bit can move an f16 result next to a byte boundary), almost
+    all identical; and bit-identical to the GPU's own unfused composition (the same device expf). amp: the range of
+    the map-size flow; 40 sends taps far outside the frame (clamped)."""
+    import torch
+    say("render_rgba", cubic, flags, amp, size)
+    fh = fhops()
+    rng = np.random.default_rng(int(amp) + flags + 10 * cubic + size[1])
+    h, w = size
+    hp, wp = (h + 31) // 32 * 32, (w + 31) // 32 * 32
+    hq, wq = max(2, hp // 9), max(2, wp // 9)
+    fsx, fsy = float(np.float32(wp) / np.float32(4 * wq)), float(np.float32(hp) / np.float32(4 * hq))
+    fr = _frames(rng, 2, h, w)
+    if flags & 2:  # make B mostly equal to A so the still test fires somewhere
+        fr[1] = np.where(rng.uniform(size=(h, w)) < 0.7, fr[0], fr[1])
+    up = np.zeros((1, hq, wq, 8), np.float32)
+    up[..., :4] = rng.uniform(-amp, amp, (hq, wq, 4))
+    up[..., 4:7] = rng.normal(0, 2, (hq, wq, 3))
+    up = f16_bits(up)
+    rt = rand(rng, (1, hq, wq, 4), -0.1, 0.1)
+    full = oracle.rgba_in(fr, hp, wp, cs=4)
+    pic = oracle.render(full[:1].copy(), full[1:].copy(), up, up, rt, hq, wq, cubic=cubic, flags=flags, vis_c0=4,
+                        fsx=fsx, fsy=fsy)
+    want = oracle.rgba_out(pic, h, w)
+    dfr, dup, drt = dev32(fr), dev(up), dev(rt)
+    got = host32(fh.render_rgba(dfr[0:1], dfr[1:2], dup, fh.View(dup, 4), drt, hp, wp, cubic=cubic, flags=flags,
+                                fsx=fsx, fsy=fsy))
+    diff = np.zeros(got.shape, np.int32)
+    for sh in (0, 8, 16, 24):
+        diff = np.maximum(diff, np.abs(((got >> sh) & 0xFF).astype(np.int32) - ((want >> sh) & 0xFF).astype(np.int32)))
+    say(f"  max byte diff {diff.max()}, {np.mean(diff == 0):.6f} identical")
+    assert diff.max() <= (255 if flags & 1 else 1) and np.mean(diff == 0) > 0.999
+    # the GPU's unfused path: rgba_in, render, rgba_out
+    dfull = fh.rgba_in(dfr, hp, wp)
+    dpic = fh.render(dfull[0:1], dfull[1:2], dup, fh.View(dup, 4), drt, cubic=cubic, flags=flags, fsx=fsx, fsy=fsy)
+    exact(got, host32(fh.rgba_out(dpic, h, w)), "render_rgba against the unfused GPU composition")
+    torch.cuda.synchronize()

@@ -320,3 +320,153 @@ def test_render_decisive_blend_takes_the_trusted_picture_where_they_disagree():
     soft = val(oracle.render(a, b, fl, vis, rt, 2, 2))
     hard = val(oracle.render(a, b, fl, vis, rt, 2, 2, flags=1))
     assert np.all(soft > 0.3) and np.allclose(hard, 0.2, atol=1e-3)  # |A - B| = 0.6 >> 0.12: k = 1, no residual
+
+
+def _stripes(h, w, lo, hi):
+    """A still picture whose columns alternate lo / hi (all 3 channels)."""
+    col = np.where(np.arange(w) % 2 == 0, lo, hi).astype(np.float32)
+    return f16(np.broadcast_to(col[None, None, :, None], (1, h, w, 3)))
+
+
+def test_render_still_test_keeps_a_still_picture_where_the_flow_disagrees():
+    """render.wgsl:134-148 (flags bit 1). A == B, so es = 0 < 0.03 and own = A. A's flow moves one column, B's none:
+    on stripes of 0.2 / 0.8 the two warped pictures differ by 0.6 >= 0.04, so stillw = 1 and the output is the still
+    picture itself (the plain blend would give 0.5 grey); at the last column both warps read the same pixel, ef = 0,
+    and the blend is the picture too."""
+    h, w = 8, 12
+    pic = _stripes(h, w, 0.2, 0.8)
+    fl, vis, rt = _render_maps(2, 3, flow=(1.0, 0.0, 0.0, 0.0))
+    got = oracle.render(pic, pic, fl, vis, rt, 2, 3, cubic=False, flags=2)
+    assert np.array_equal(got, pic)
+    plain = val(oracle.render(pic, pic, fl, vis, rt, 2, 3, cubic=False, flags=0))
+    assert np.allclose(plain[:, :, :-1], 0.5, atol=1e-3)
+
+
+def test_render_still_test_weight_ramps_with_the_flow_disagreement():
+    """stillw = clamp((ef - es) / 0.04, 0, 1): stripes 0.49 / 0.51 give ef = |0.49 - 0.51| (their f16 values), about
+    half of 0.04, so the output is the blend (0.5 with equal logits) mixed halfway toward the picture."""
+    h, w = 6, 10
+    pic = _stripes(h, w, 0.49, 0.51)
+    fl, vis, rt = _render_maps(2, 2, flow=(1.0, 0.0, 0.0, 0.0))
+    got = val(oracle.render(pic, pic, fl, vis, rt, 2, 2, cubic=False, flags=2))[0, :, :-1, 0]
+    p = val(pic)[0, :, :-1, 0].astype(np.float64)
+    q = val(pic)[0, :, 1:, 0].astype(np.float64)     # A warped one column
+    ef = np.abs(q - p)
+    stillw = np.clip(ef / 0.04, 0, 1)
+    blend = 0.5 * q + 0.5 * p
+    want = blend * (1 - stillw) + p * stillw
+    assert 0.3 < stillw.min() and stillw.max() < 0.7
+    assert ulp_close(f16(got), want.astype(np.float32), ulps=1)
+
+
+def test_render_still_test_is_off_where_the_pictures_differ():
+    """es >= 0.03 (A and B differ by 0.1 everywhere) makes stillw 0: the still test changes nothing."""
+    h, w = 8, 12
+    a = f16(rng.uniform(0.1, 0.8, (1, h, w, 3)))
+    b = f16(val(a) + np.float32(0.1))
+    fl, vis, rt = _render_maps(2, 3, flow=(0.7, -0.4, -0.3, 0.5), logits=(0.5, -0.2, 0.1), r=0.02)
+    for cubic in (False, True):
+        assert np.array_equal(oracle.render(a, b, fl, vis, rt, 2, 3, cubic=cubic, flags=2),
+                              oracle.render(a, b, fl, vis, rt, 2, 3, cubic=cubic, flags=0))
+
+
+def test_render_at_a_non_integer_ratio_upsamples_and_scales_the_flow():
+    """The internal-size render (net/build.rs:717-736): maps at hq x wq, the output at a padded frame size about 9x
+    larger per axis (the 1080p case is 120 x 216 -> 1088 x 1920), the flow's x scaled by fsx and y by fsy. A flow
+    that is linear in x at map resolution upsamples to F(x) = a * ix + b with ix = (x + 0.5) * wq / w - 0.5 (away
+    from the clamped border), and a bilinear warp of a linear ramp picture is exact, so the output is the ramp at
+    x + fsx * F(x) (y: a constant flow times fsy over a picture constant in y)."""
+    hq, wq, h, w = 6, 11, 56, 96
+    fsx, fsy = 2.25, 2.0
+    a_, b_ = 0.25, 0.5
+    qx = np.arange(wq, dtype=np.float32)
+    fl = np.zeros((1, hq, wq, 4), np.float32)
+    fl[..., 0] = a_ * qx[None, None, :] + b_
+    fl[..., 1] = 0.75
+    c, d = 1.0 / 256, 0.125
+    xs = np.arange(w, dtype=np.float32)
+    pic = f16(np.broadcast_to((c * xs + d)[None, None, :, None], (1, h, w, 3)))
+    vis = f16(np.zeros((1, hq, wq, 3), np.float32) + np.asarray((40.0, 0.0, 0.0), np.float32))
+    rt = f16(np.zeros((1, hq, wq, 3), np.float32))
+    got = val(oracle.render(pic, pic, f16(fl), vis, rt, hq, wq, cubic=False, fsx=fsx, fsy=fsy))[0]
+    ix = (xs.astype(np.float64) + 0.5) * wq / w - 0.5
+    F = a_ * ix + b_
+    want = c * (xs + fsx * F) + d
+    inner = (ix >= 0) & (ix <= wq - 1) & (xs + fsx * F <= w - 1)
+    assert inner.sum() > w // 2
+    assert np.allclose(got[:, inner, 0], want[None, inner], atol=2e-3)
+    # a y-flow scaled by fsx instead of fsy, or the map ratio taken from the wrong size, fails the check above or
+    # this one: the y flow over a picture constant in y changes nothing
+    assert np.allclose(got[:, inner, 1], want[None, inner], atol=2e-3)
+
+
+def test_render_at_the_1080p_internal_ratio_matches_torch_grid_sample():
+    """The internal-size render at the 1080p ratios (maps 120 x 216, output 1088 x 1920 rows scaled down by 8 to keep
+    the check fast: 15 x 27 -> 136 x 240) with a constant flow: torch's grid_sample (bicubic, align_corners, border)
+    of the picture at (x + fx * fsx, y + fy * fsy)."""
+    torch = pytest.importorskip("torch")
+    hq, wq, h, w = 15, 27, 136, 240
+    fsx, fsy = 1920 / 864, 1088 / 480
+    fx, fy = 1.5, -0.75
+    pic = f16(rng.uniform(0.05, 0.95, (1, h, w, 3)))
+    fl, vis, rt = _render_maps(hq, wq, flow=(fx, fy, 0.0, 0.0), logits=(40.0, 0.0, 0.0))
+    got = val(oracle.render(pic, pic, fl, vis, rt, hq, wq, cubic=True, fsx=fsx, fsy=fsy))
+    yy, xx = np.mgrid[0:h, 0:w].astype(np.float64)
+    gx, gy = xx + fx * np.float32(fsx), yy + fy * np.float32(fsy)
+    grid = np.stack([-1 + 2 * gx / (w - 1), -1 + 2 * gy / (h - 1)], -1)[None]
+    t = torch.from_numpy(val(pic).astype(np.float64)).permute(0, 3, 1, 2)
+    ref = torch.nn.functional.grid_sample(t, torch.from_numpy(grid), mode="bicubic", padding_mode="border",
+                                          align_corners=True)
+    want = np.clip(ref.permute(0, 2, 3, 1).numpy(), 0, 1)
+    assert np.allclose(got, want, atol=2e-3)
+
+
+# ---- the host's 8-bit frames (shaders/rgba_in.wgsl, rgba_out.wgsl) ---------------------------------------------------
+
+def _rgba(r, g, b, a=255):
+    return (np.uint32(r) | (np.uint32(g) << 8) | (np.uint32(b) << 16) | (np.uint32(a) << 24)).astype(np.uint32)
+
+
+def test_rgba_in_is_bgr_over_255_for_every_byte():
+    """Channel 0 is blue (bits 16-23), 1 green, 2 red; each is the f16 of byte / 255 (numpy's float16 rounding of
+    the exact quotient, every byte); alpha is ignored."""
+    v = np.arange(256, dtype=np.uint32)
+    frames = np.stack([_rgba(v, 0, 0, 7), _rgba(0, v, 0, 0), _rgba(0, 0, v, 255)])[:, None, :]  # (3, 1, 256)
+    x = oracle.rgba_in(frames, 1, 256)
+    unit = (v.astype(np.float64) / 255.0).astype(np.float16).view(np.uint16)
+    zero = np.zeros(256, np.uint16)
+    assert np.array_equal(x[0, 0, :, 2], unit) and np.array_equal(x[0, 0, :, :2], np.stack([zero, zero], -1))
+    assert np.array_equal(x[1, 0, :, 1], unit) and np.array_equal(x[1, 0, :, 0], zero)
+    assert np.array_equal(x[2, 0, :, 0], unit) and np.array_equal(x[2, 0, :, 1], zero)
+
+
+def test_rgba_in_replicates_the_last_row_and_column_into_the_padding():
+    f = rng.integers(0, 2 ** 32, (1, 5, 7), dtype=np.uint64).astype(np.uint32)
+    x = oracle.rgba_in(f, 8, 12)
+    assert np.array_equal(x[:, :5, :7], oracle.rgba_in(f, 5, 7))
+    assert np.array_equal(x[:, 5:, :7], np.broadcast_to(x[:, 4:5, :7], (1, 3, 7, 3)))
+    assert np.array_equal(x[:, :, 7:], np.broadcast_to(x[:, :, 6:7], (1, 8, 5, 3)))
+
+
+def test_rgba_out_quantizes_every_f16_and_round_trips_every_byte():
+    """q(v) = floor(clamp(v, 0, 1) * 255 + 0.5) for every non-NaN f16 pattern (WGSL leaves clamp of a NaN to the
+    implementation; a rendered picture holds none), the BGR -> R | G << 8 | B << 16 packing with alpha 255, and
+    rgba_out(rgba_in(f)) == f with alpha 255 for every byte in every channel."""
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = np.zeros((1, 256, 256, 3), np.uint16)
+    x[..., 0] = pats.reshape(256, 256)
+    got = oracle.rgba_out(x, 256, 256)[0].ravel()
+    v = pats.view(np.float16).astype(np.float64)
+    q = np.floor(np.clip(np.nan_to_num(v, nan=0.0), 0, 1) * 255 + 0.5).astype(np.uint32)
+    ok = ~np.isnan(v)
+    assert ok.sum() == 65536 - 2046
+    assert np.array_equal(got[ok], ((q << 16) | 0xff000000)[ok])
+    b = np.arange(256, dtype=np.uint32)
+    f = _rgba(b, b[::-1], (b * 7) % 256, 3)[None, None, :]
+    assert np.array_equal(oracle.rgba_out(oracle.rgba_in(f, 1, 256), 1, 256), f | np.uint32(0xff000000))
+
+
+def test_rgba_out_crops_the_padding():
+    f = rng.integers(0, 2 ** 32, (2, 5, 7), dtype=np.uint64).astype(np.uint32)
+    x = oracle.rgba_in(f, 32, 32, cs=4)
+    assert np.array_equal(oracle.rgba_out(x, 5, 7), f | np.uint32(0xff000000))
