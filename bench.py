@@ -1,22 +1,23 @@
 #!/usr/bin/env python3
-"""Benchmark of the FlyHigh conv hot path on one MI355X.
+"""Benchmark of the FlyHigh frame path on one MI355X.
 
-Workload (one step): every conv layer of one FlyHighFG pair() and one mid() at 1080p (network 856x480, padded to
-864x480), batch 1, NHWC f16, random He-normal weights and seeded uniform inputs resident in HBM. Consecutive convs
-whose intermediate has no other reader run as one fused launch where that is faster (checked against the unfused
-step on every run). The whole step is captured once as a HIP graph and replayed. The value is conv-only 1080p
-frames/s = 1000 / ms per step (the non-conv ops of pair()/mid() are not part of this path).
+Workload (one step): one 1080p pair() + mid(0.5) as the reference's Session runs it: two 1920x1080 RGBA8 frames
+resident in HBM -> rgba_in and the antialiased downscale to the 864x480 network -> every op of the FlyHighFG graph
+(the convs, fused conv pairs, the network ops) -> render_pix at 1920x1088 and rgba_out -> the RGBA8 in-between frame.
+Random weights of the architecture, synthetic frames (a procedural picture and the same moved 12 px). The frame is
+captured once as a HIP graph and replayed; value = frames/s = 1e6 / us per frame (wall clock over the timed replays,
+synchronised on both sides).
 
-Alongside: per-launch time and roofline fraction (each launch captured R times in a graph, median of G replays
-over R; "cold" rotates buffer sets larger than the 256 MB MALL, "warm" reuses one), the layers of the single-layer
-configurations (3x3 32->32 at 1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1), the batched
-workload (the frame's convs over 8 independent 4K frame pairs with 3 mid() phases each), the network ops between
-the convs (warp, luma, sad volume, convex upsample, FiLM, blendmix, avgpool, resize: each op instance of one frame and
-of the batched workload against its HBM roofline), and the CPU baseline: the oracle (a C restatement of the
-reference's conv arithmetic) over the same conv layers on the host's cores.
+Alongside (the last stdout line is one compact JSON record; the full record goes to --detail): every launch of the
+frame timed alone against its roofline, the dominant one cold; the conv-only step (every conv of pair()+mid(), one
+graph) with per-layer warm/cold time and roofline fraction (each launch captured R times in a graph, median of G
+replays; "cold" rotates buffer sets larger than the 256 MB MALL); the single-layer configurations (3x3 32->32 at
+1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1); the batched workload (the frame's convs over
+8 independent 4K frame pairs with 3 mid() phases each); the sustained MFMA rate; and the CPU baseline: the same frame
+through the oracle (a C restatement of the reference's arithmetic) on the host's cores.
 
-    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--no-batched] [--no-fuse] [--no-ops]
-    python bench.py --only-ops | --only-network
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--no-batched] [--no-fuse] [--ops]
+    python bench.py --only-frame | --only-ops
 """
 import argparse
 import json
@@ -50,7 +51,7 @@ class Net:
     """Plans and resident buffers of a list of conv layers, chained as the graph chains them. With `tune`, each
     conv shape is autotuned on its buffers before its plan is made (the reference's conv_pick with autotune on)."""
 
-    def __init__(self, layers, seed, torch, np, fhconv, tune=True):
+    def __init__(self, layers, seed, torch, np, fhconv, tune=True, slope=None):
         self.layers = layers
         self.plans, self.bufs, self.tuned, self.params = {}, {}, {}, {}
         self.pairs = {}  # first layer's name -> (pair plan, second layer)
@@ -60,7 +61,8 @@ class Net:
         for L in layers:
             wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
             b = f16(rng.normal(0, 0.01, L.cout))
-            s = f16(rng.uniform(0.05, 0.3, L.cout)) if L.act == 1 else None
+            s = (f16(np.full(L.cout, slope)) if slope is not None else f16(rng.uniform(0.05, 0.3, L.cout))) \
+                if L.act == 1 else None
             # activations are NHWC with the channel stride padded to 8 halves (16 bytes): the concat buffers the
             # graph's convs read (279, 155, 14 channels ...) are allocated that way, and the convs read views
             cx, cy = pad8(L.cin), pad8(L.cout)
@@ -269,20 +271,20 @@ def net_ops_report(args, torch, flyhighfg, stream, net_w, net_h):
                 batched_workload="8 frame pairs (A/B ops over 16 frames) and 24 mid() phases at network 864x480")
 
 
-def network_frame(args, torch, np, stream, net_w, net_h, t=0.5):
-    """The whole network of one frame: every op of pair() and mid(t) (flyhighfg_net: the 25 convs and up.w, fused
-    pairs, the network ops, render_pix with the model's bicubic sampler) captured as one HIP graph on `stream`; per-frame time over
-    args.steps replays (after args.warmup) between events on that stream. Random weights of the architecture
-    (seed 7), a synthetic picture and the same picture moved 12 pixels as A and B."""
+def frame_1080p(args, torch, np, stream, t=0.5):
+    """The headline workload: one 1080p pair() + mid(t) as the reference's Session runs it (net/session.rs:26-66,
+    Internal::Auto): two 1920x1080 RGBA8 frames (the procedural picture and the same moved 12 px) resident in HBM ->
+    rgba_in + antialiased downscale to the 864x480 network (one launch) -> every op of the graph (convs, fused pairs,
+    the network ops and chains) -> render_pix at 1920x1088 + rgba_out to the RGBA8 frame (one launch). Random weights
+    of the architecture (seed 7). Captured as one HIP graph on `stream`; args.steps replays after args.warmup,
+    bracketed by a device synchronisation on both sides (wall clock; events on the stream beside it). Then every
+    launch of the frame alone, a graph of args.reps launches, median of args.graphs replays (warm)."""
     import flyhighfg_net as fnet
     W = fnet.make_weights(7)
     be = fnet.GpuBackend(W, stream=stream, fuse=not args.no_fuse)
-    f = fnet.FlyHighFG(be, net_w, net_h)
-    yy, xx = np.mgrid[0:net_h, 0:net_w] / 16.0
-    base = 0.5 + 0.25 * np.sin(xx)[..., None] * np.cos(yy)[..., None] + 0.1 * np.sin(3.7 * xx + 1.3 * yy)[..., None]
-    ab = np.zeros((2, net_h, net_w, 4), np.float32)
-    ab[0, ..., :3], ab[1, ..., :3] = base, np.roll(base, 12, axis=1)
-    f.AB.copy_(be.upload(np.ascontiguousarray(ab.astype(np.float16)).view(np.uint16)))
+    net_w, net_h = 864, 480
+    f = fnet.FlyHighFG(be, net_w, net_h, frame=(1920, 1080))
+    be.upload_frames(f.frames, np.stack([fnet.procedural_frame(1920, 1080), fnet.procedural_frame(1920, 1080, 12, 0)]))
     be.set_g(fnet.film_mlp(W, t))
     with torch.cuda.stream(stream):
         for _ in range(2):  # plans are made on the first run
@@ -304,21 +306,83 @@ def network_frame(args, torch, np, stream, net_w, net_h, t=0.5):
         e1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-    us = wall * 1e6 / args.steps
-    ev_us = e0.elapsed_time(e1) * 1e3 / args.steps
-    outs = {k: be.host(getattr(f, k))[..., :c].view(np.float16) for k, c in (("out", 3), ("Rt", 3), ("up7", 7))}
-    finite = all(bool(np.all(np.isfinite(v))) for v in outs.values())
-    fused = sum(1 for k, p in be.plans.items() if k[0] == "pair" and p is not False)
+    us, ev_us = wall * 1e6 / args.steps, e0.elapsed_time(e1) * 1e3 / args.steps
+    rgba = be.host_frames(f.rgba)
+    ok = bool(np.all(rgba >> 24 == 255)) and len(np.unique(rgba)) > 1000
+    # every launch of the frame, timed alone (the recorder re-issues each with the frame's own buffers)
+    be.record = []
+    with torch.cuda.stream(stream):
+        f.pair()
+        f.mid(t, None)
+        stream.synchronize()
+    rec, be.record = be.record, None
+    launches = []
+    for i, r in enumerate(rec):
+        us_l = time_graph(torch, lambda j=0, fn=r["fn"]: fn(), args.reps, args.graphs, stream)
+        bound, t_roof = roof(r["flops"], r["bytes"])
+        launches.append(dict(i=i, label=r["label"], kind=r["kind"], us_warm=round(us_l, 3), bytes=r["bytes"],
+                             flops=r["flops"], bound=bound, roof_us=round(t_roof * 1e6, 4),
+                             frac_warm=round(t_roof * 1e6 / us_l, 4)))
+        log("frame launch", json.dumps(launches[-1]))
     res = dict(us_per_frame=round(us, 3), frames_per_s=round(1e6 / us, 2), event_us_per_frame=round(ev_us, 3),
-               steps=args.steps, warmup=args.warmup, network=f"{net_w}x{net_h}", finite_outputs=finite,
-               conv_plans=sum(1 for k in be.plans if k[0] == "conv"), fused_pairs=fused,
-               workload=f"every op of one FlyHighFG pair() and mid(t={t}) at network {net_w}x{net_h} (1080p): the "
-                        "convs (fused pairs where the library has a kernel), resize, pools, luma, SAD volumes, warps, "
-                        "FiLM, convex upsample, blendmix, elementwise and concat copies, render_pix (bicubic), as one "
-                        "HIP graph; the host's 8-bit frame conversion excluded; random weights, synthetic frames")
-    del g, f, be
-    torch.cuda.empty_cache()
-    return res
+               steps=args.steps, warmup=args.warmup, network=f"{net_w}x{net_h}", frame="1920x1080",
+               launches=len(rec), launch_us_sum=round(sum(x["us_warm"] for x in launches), 3),
+               output_ok=ok, launch_table=launches,
+               workload="one 1080p pair()+mid(0.5) from two 1920x1080 RGBA8 frames to the RGBA8 in-between frame: "
+                        "rgba_in + downscale to the 864x480 network, every graph op (convs, fused pairs, ops), "
+                        "render_pix (bicubic) at 1920x1088 + rgba_out; one HIP graph; random weights, synthetic "
+                        "frames (12 px translation)")
+    return res, (be, f, rec)
+
+
+def render_cold(args, torch, be, f, reps, graphs, cold_bytes, stream):
+    """The frame-size render (fhc_render_rgba) over rotating sets of input frames and output frames larger than the
+    MALL, so every launch reads its frames from HBM: per-launch microseconds."""
+    per = 3 * f.frames.numel() // 2 * 4
+    nsets = max(2, min(512, -(-cold_bytes // per)))
+    sets = [(torch.randint_like(f.frames, -2 ** 31, 2 ** 31 - 1), torch.empty_like(f.rgba)) for _ in range(nsets)]
+    fh = be.fh
+    vf, vv, vr = fh.View(f.up7, 0), fh.View(f.up7, 4), fh.View(f.Rt, 0)
+
+    def call(i=0):
+        fr, out = sets[i % nsets]
+        fh.render_rgba(fr[0:1], fr[1:2], vf, vv, vr, f.hp, f.wp, f.cubic, f.render_flags, f.fsx, f.fsy, out=out,
+                       stream=stream)
+    creps = -(-max(reps, nsets) // nsets) * nsets
+    us = time_graph(torch, call, creps, graphs, stream)
+    del sets
+    return us, nsets
+
+
+def cpu_frame_baseline(np, frames_n=3):
+    """Seconds per 1080p pair()+mid() of the CPU oracle composition (the same program over oracle/: its C
+    restatement of the reference's WGSL arithmetic, the convs multithreaded over rows), median of `frames_n` frames,
+    inputs generated outside the timing."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import flyhighfg_net as fnet
+    from frame_oracle import CpuBackend
+    W = fnet.make_weights(7)
+    be = CpuBackend(W)
+    fr = np.stack([fnet.procedural_frame(1920, 1080), fnet.procedural_frame(1920, 1080, 12, 0)])
+    secs = []
+    for _ in range(frames_n):
+        f = fnet.FlyHighFG(be, 864, 480, frame=(1920, 1080))
+        be.upload_frames(f.frames, fr)
+        t0 = time.perf_counter()
+        f.pair()
+        f.mid(0.5, W)
+        secs.append(time.perf_counter() - t0)
+    return statistics.median(secs), be.threads
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def batched_workload(args, torch, np, fhconv, flyhighfg, stream, pairs=8, mids=3):
@@ -367,32 +431,6 @@ def batched_workload(args, torch, np, fhconv, flyhighfg, stream, pairs=8, mids=3
                 pairs_per_s=round(pairs / step_us * 1e6, 1), step_tflops=round(flops / step_us / 1e6, 2),
                 launches=launches, fused_pairs=[f"{a}+{B.name}" for a, (_, B, _, _) in net.pairs.items()],
                 tune_table=fhconv.format_tune().splitlines())
-
-
-def cpu_baseline(np, layers, threads, passes=10):
-    """Seconds per pair+mid of the C oracle on `threads` host threads: the median of `passes` passes over all the
-    frame's conv layers (inputs generated once, outside the timing)."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle
-    rng = np.random.default_rng(5)
-    f16 = lambda a: np.asarray(a, np.float64).astype(np.float16).view(np.uint16)  # noqa: E731
-    work = []
-    for L in layers:
-        x = f16(rng.uniform(-1, 1, (L.n, L.h, L.w, L.cin)))
-        wt = f16(rng.normal(0, np.sqrt(2.0 / (L.k * L.k * L.cin)), (L.cout, L.cin, L.k, L.k)))
-        b = f16(rng.normal(0, 0.01, L.cout))
-        s = f16(rng.uniform(0.05, 0.3, L.cout))
-        r = f16(rng.uniform(-1, 1, (L.n, L.hout, L.wout, L.cout)))
-        d = oracle.make_desc(L.n, L.h, L.w, L.cin, L.cout, k=L.k, stride=L.stride, act=L.act, alpha=L.alpha,
-                             residual=L.residual)
-        work.append((d, x, wt, b, s, r))
-    secs = []
-    for _ in range(passes):
-        t0 = time.perf_counter()
-        for d, x, wt, b, s, r in work:
-            oracle.conv(d, x, wt, b, s, r, threads=threads)
-        secs.append(time.perf_counter() - t0)
-    return statistics.median(secs)
 
 
 def mfma_rate_probe(torch, fhconv, stream):
@@ -523,16 +561,21 @@ def traffic_from(args):
     return 0
 
 
-def measured_traffic(layer, variant):
-    """(bytes per launch, source) from profiles/traffic_<layer>.txt when it was measured on this variant's kernel,
-    else (None, reason)."""
-    path = os.path.join(ROOT, "profiles", f"traffic_{layer}.txt")
+def traffic_name(label):
+    """The file stem of a launch's traffic record: its label up to the first space ("frame_render", "enc.e3+enc.e4")."""
+    return label.split(" ")[0]
+
+
+def measured_traffic(label, variant=None):
+    """(bytes per launch, source) from profiles/traffic_<name>.txt when it was measured (on this variant's kernel, when
+    a variant is named), else (None, reason)."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{traffic_name(label)}.txt")
     if not os.path.exists(path):
-        return None, "no counter passes recorded for this layer"
+        return None, "no counter passes recorded for this launch"
     kv = dict(line.split(" ", 1) for line in open(path).read().splitlines() if " " in line and line[0] != "#")
-    if kv.get("variant") != variant:
-        return None, f"profiles/traffic_{layer}.txt was measured on {kv.get('variant')}, this run uses {variant}"
-    return int(float(kv["traffic_bytes_per_launch"])), f"profiles/traffic_{layer}.txt ({kv['kernel'][:80]})"
+    if variant is not None and kv.get("variant") != variant:
+        return None, f"{os.path.relpath(path, ROOT)} was measured on {kv.get('variant')}, this run uses {variant}"
+    return int(float(kv["traffic_bytes_per_launch"])), f"{os.path.relpath(path, ROOT)} ({kv['kernel'][:80]})"
 
 
 def main():
@@ -549,12 +592,13 @@ def main():
     ap.add_argument("--no-autotune", action="store_true", help="plan with the heuristic only (no per-shape timing)")
     ap.add_argument("--no-fuse", action="store_true", help="one launch per conv (no fused conv pairs)")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched workload (8 pairs, 3 mids each)")
-    ap.add_argument("--no-ops", action="store_true", help="skip the timing of the network ops between the convs")
+    ap.add_argument("--ops", action="store_true", help="also time each network op instance over rotating buffers "
+                                                        "(frame and batched shapes)")
     ap.add_argument("--only-ops", action="store_true",
                     help="only time the network ops (frame and batched shapes) and print them as one JSON line")
-    ap.add_argument("--only-network", action="store_true",
-                    help="only time the whole-network frame (every op of pair() + mid() as one HIP graph) and print "
-                         "it as one JSON line")
+    ap.add_argument("--only-frame", action="store_true",
+                    help="only time the 1080p frame (RGBA8 in, every op of pair() + mid(), RGBA8 out, one HIP graph) "
+                         "and print it as one JSON line")
     ap.add_argument("--tune", help="plan with this choice table (cin,cout,h,w,stride=code lines) instead of autotuning")
     ap.add_argument("--pmc-layer", help="only run this frame layer --pmc-reps times over rotating (cold) buffers, "
                                         "then a copy of known size as many times: the workload of the rocprofv3 "
@@ -589,8 +633,9 @@ def main():
         log(f"bench: {n_tune} choices from {args.tune}")
     net_w, net_h = 864, 480  # default_internal(1920, 1080) = (856, 480), padded to a multiple of 32
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
-    if args.only_network:
-        print(json.dumps(dict(network_frame=network_frame(args, torch, np, stream, net_w, net_h))), flush=True)
+    if args.only_frame:
+        frame, _ = frame_1080p(args, torch, np, stream)
+        print(json.dumps({k: v for k, v in frame.items() if k != "launch_table"}), flush=True)
         return 0
     if args.only_ops:
         print(json.dumps(dict(net_ops=net_ops_report(args, torch, flyhighfg, stream, net_w, net_h))), flush=True)
@@ -692,7 +737,8 @@ def main():
     if not args.no_configs:
         for c in (1, 2, 3):
             cl = flyhighfg.config_layers(c)
-            cnet = Net(cl, 100 + c, torch, np, fhconv, tune=not args.no_autotune)
+            # the configurations' PReLU slopes are 0.25 (the He-normal ladder of the 1080p/4 configuration)
+            cnet = Net(cl, 100 + c, torch, np, fhconv, tune=not args.no_autotune, slope=0.25)
             for L in cl:
                 cfg_layers.append(dict(config=c, **layer_timing(torch, np, fhconv, cnet, L, args.reps,
                                                                 args.graphs, args.cold_mb << 20, stream)))
@@ -708,11 +754,13 @@ def main():
             del cnet
             torch.cuda.empty_cache()
 
-    # the network frame plans its convs from the choice table the frame's autotuning filled; the batched workload's
-    # choices sit under keys of their own (the table's key holds the batch)
-    net_ops = None if args.no_ops else net_ops_report(args, torch, flyhighfg, stream, net_w, net_h)
-    netframe = network_frame(args, torch, np, stream, net_w, net_h)
-    log("bench: network frame", json.dumps(netframe))
+    # the headline: the whole 1080p frame from RGBA8 to RGBA8; its conv plans come from the choice table the
+    # conv step's autotuning filled (or --tune); the batched workload's choices sit under keys of their own (the
+    # table's key holds the batch)
+    frame, (fbe, fobj, frec) = frame_1080p(args, torch, np, stream)
+    log(f"bench: 1080p frame {frame['us_per_frame']:.2f} us ({frame['frames_per_s']:.0f} frames/s), "
+        f"{frame['launches']} launches, per-launch sum {frame['launch_us_sum']:.1f} us")
+    net_ops = net_ops_report(args, torch, flyhighfg, stream, net_w, net_h) if args.ops else None
 
     batched = None
     if not args.no_batched:
@@ -722,34 +770,40 @@ def main():
     mfma_rate = mfma_rate_probe(torch, fhconv, stream)
     log(f"bench: sustained dense f16 MFMA rate {mfma_rate:.0f} TFLOP/s")
 
-    # the dominant kernel of the step: the layer with the largest time (warm, as inside the frame graphs); its
-    # achieved rate is the algorithmic bytes (or FLOPs) per launch over its cold per-launch time
-    roofline = None
-    if per_layer:
-        fused_b = {B.name for _, B, _, _ in net.pairs.values()}
-        step_launches = [r for r in per_layer if r["name"] not in net.pairs and r["name"] not in fused_b] + per_pair
-        dom = max(step_launches, key=lambda r: r["us_warm"])
-        unit = "GB/s" if dom["bound"] == "hbm" else "TFLOP/s"
-        achieved = dom["gbs_cold"] if dom["bound"] == "hbm" else dom["tflops_cold"]
-        peak = HBM_PEAK / 1e9 if dom["bound"] == "hbm" else MFMA_F16_PEAK / 1e12
-        traffic, traffic_note = measured_traffic(dom["name"], dom["variant"])
-        roofline = dict(bound=dom["bound"], achieved=achieved, peak=peak, unit=unit,
-                        frac=round(achieved / peak, 4), traffic=traffic, kernel=dom["name"], variant=dom["variant"],
-                        us_cold=dom["us_cold"], us_warm=dom["us_warm"],
-                        per_launch_bytes=dom["bytes"], per_launch_flops=dom["flops"], traffic_source=traffic_note,
-                        sustained_mfma_tflops=round(mfma_rate, 1))
-        if dom["bound"] == "mfma":
-            roofline["frac_of_sustained"] = round(achieved / mfma_rate, 4)
+    # the dominant kernel of the frame: the launch with the largest time alone (warm); its achieved rate is its
+    # algorithmic bytes (or FLOPs) per launch over its per-launch time, cold (inputs from HBM) where the launch can
+    # be rotated over fresh buffers: the frame-size render, a conv layer or fused pair of the conv step
+    dom = max(frame["launch_table"], key=lambda r: r["us_warm"])
+    us_cold, cold_note = None, "warm only"
+    if dom["label"].startswith("frame_render"):
+        us_cold, nsets = render_cold(args, torch, fbe, fobj, args.reps, args.graphs, args.cold_mb << 20, stream)
+        cold_note = f"cold: {nsets} rotating sets of input and output frames"
+    elif dom["kind"] == "conv":
+        rows = [r for r in per_layer + per_pair if r["name"].replace(".ab", "") == dom["label"]]
+        if rows:
+            us_cold, cold_note = rows[0]["us_cold"], "cold: the conv step's rotating buffer sets"
+    us = us_cold if us_cold is not None else dom["us_warm"]
+    if dom["bound"] == "hbm":
+        unit, achieved, peak = "GB/s", dom["bytes"] / us / 1e3, HBM_PEAK / 1e9
+    else:
+        unit, achieved, peak = "TFLOP/s", dom["flops"] / us / 1e6, MFMA_F16_PEAK / 1e12
+    traffic, traffic_note = measured_traffic(dom["label"], None)
+    roofline = dict(bound=dom["bound"], achieved=round(achieved, 2), peak=peak, unit=unit, frac=round(achieved / peak, 4),
+                    traffic=traffic, kernel=dom["label"], us_warm=dom["us_warm"],
+                    us_cold=None if us_cold is None else round(us_cold, 3), timing=cold_note,
+                    per_launch_bytes=dom["bytes"], per_launch_flops=dom["flops"], traffic_source=traffic_note,
+                    sustained_mfma_tflops=round(mfma_rate, 1))
+    log("bench: dominant launch", json.dumps(roofline))
 
     cpu = None
     if not args.no_cpu:
-        threads = max(1, min(16, len(os.sched_getaffinity(0))))
-        secs = cpu_baseline(np, layers, threads)
+        secs, threads = cpu_frame_baseline(np)
         cpu = dict(value=round(1.0 / secs, 4), unit="frames/s", cores=threads, kind="port",
-                   sample=f"all 25 conv layers of one pair()+mid() at {net_w}x{net_h} through the C oracle "
-                          "(restatement of the reference WGSL conv arithmetic), not lavapipe; median of 10 passes",
-                   seconds=round(secs, 3))
-        log(f"bench: CPU baseline {secs:.3f} s per pair+mid on {threads} threads")
+                   sample="one 1080p pair()+mid(0.5) from two RGBA8 frames through the oracle composition (the C "
+                          "restatement of the reference's WGSL ops and conv arithmetic, convs multithreaded over "
+                          "rows), not lavapipe; median of 3 frames",
+                   seconds=round(secs, 3), cpu_model=cpu_model(), host_cpus=os.cpu_count())
+        log(f"bench: CPU baseline {secs:.3f} s per frame on {threads} threads")
 
     conv_step = dict(
         workload="FlyHighFG conv layers of one pair()+mid() at 1080p (network 856x480 padded to 864x480), NHWC "
@@ -761,10 +815,10 @@ def main():
         pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), unfused_step_us=round(unfused_us, 3),
         fuse_check=fuse_check, event_ms_per_step=round(ev_ms, 6),
         submit_us_per_step=round(t_submit * 1e6 / args.steps, 3))
-    detail = dict(conv_step=conv_step, roofline=roofline, cpu_baseline=cpu, layers=per_layer, pairs=per_pair,
-                  config_layers=cfg_layers, config_pairs=cfg_pairs, batched=batched, net_ops=net_ops,
-                  network_frame=netframe, tune_table=tune_table)
-    return emit(args, netframe, conv_step, roofline, cpu, batched, detail)
+    detail = dict(frame=frame, conv_step=conv_step, roofline=roofline, cpu_baseline=cpu, layers=per_layer,
+                  pairs=per_pair, config_layers=cfg_layers, config_pairs=cfg_pairs, batched=batched, net_ops=net_ops,
+                  tune_table=tune_table)
+    return emit(args, frame, conv_step, roofline, cpu, batched, detail)
 
 
 def emit(args, frame, conv_step, roofline, cpu, batched, detail):
@@ -776,8 +830,8 @@ def emit(args, frame, conv_step, roofline, cpu, batched, detail):
         with open(args.detail, "w") as f:
             json.dump(detail, f, indent=1)
         log(f"bench: full record in {args.detail}")
-    keep_roof = ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel", "variant", "us_cold", "us_warm",
-                 "per_launch_bytes", "per_launch_flops", "sustained_mfma_tflops", "frac_of_sustained")
+    keep_roof = ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel", "us_cold", "us_warm", "timing",
+                 "per_launch_bytes", "per_launch_flops", "sustained_mfma_tflops")
     line = dict(
         metric=METRIC, value=frame["frames_per_s"], unit="frames/s", n_gpus=1, steps=frame["steps"],
         warmup=frame["warmup"], ms_per_step=round(frame["us_per_frame"] / 1e3, 6), higher_is_better=True,

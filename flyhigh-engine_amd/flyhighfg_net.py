@@ -161,7 +161,9 @@ class ComposedChains:
 
 class GpuBackend(ComposedChains):
     """The program's ops on the GPU through libfhconv.so, on one stream. Plans are made on first use (the first
-    run of the program; a captured replay then finds them all)."""
+    run of the program; a captured replay then finds them all). With ``record`` a list, every launch is also
+    appended to it as a dict (label, kind, fn: a callable that issues the same launch again, bytes and flops: its
+    algorithmic work, f16 tensors read and written once), for per-launch measurement."""
 
     def __init__(self, W, stream=None, fuse: bool = True, device: str = "cuda", chains: bool = True):
         import torch
@@ -172,6 +174,12 @@ class GpuBackend(ComposedChains):
         self.stream = stream if stream is not None else torch.cuda.current_stream()
         self.plans: Dict[tuple, object] = {}
         self.g = None
+        self.record = None
+
+    def _go(self, label, fn, nbytes, flops=0, kind="op"):
+        fn()
+        if self.record is not None:
+            self.record.append(dict(label=label, kind=kind, fn=fn, bytes=int(nbytes), flops=int(flops)))
 
     def zeros(self, n, h, w, cs):
         return self.torch.zeros((n, h, w, cs), dtype=self.torch.int16, device=self.dev)
@@ -205,6 +213,12 @@ class GpuBackend(ComposedChains):
     def _v(self, v: V):
         return self.fh.View(v.buf, v.c0, v.scale)
 
+    @staticmethod
+    def _px(v: V) -> int:
+        """pixels (all images) of a view's buffer"""
+        n, h, w, _ = v.buf.shape
+        return n * h * w
+
     def _desc(self, name, x: V, y: V, res: Optional[V], mid_res=False):
         cin, cout, stride, act = CONVS[name]
         n, h, w, xcs = x.buf.shape
@@ -223,7 +237,9 @@ class GpuBackend(ComposedChains):
             p = self.plans[key] = self.fhconv.ConvPlan(self._desc(name, x, y, res), w, b, s)
             if p.workspace_bytes:
                 raise RuntimeError(f"{name}: a split-K plan needs a workspace; give the frame convs a table entry")
-        p.run(x.buf, y.buf, None if res is None else res.buf, stream=self.stream)
+            p._work = p.describe()
+        xb, yb, rb, st = x.buf, y.buf, None if res is None else res.buf, self.stream
+        self._go(name, lambda: p.run(xb, yb, rb, stream=st), p._work["bytes"], p._work["flops"], "conv")
 
     def pair(self, a, b, x: V, mid: V, y: V, res_mid: bool):
         if not self.fuse:
@@ -238,6 +254,7 @@ class GpuBackend(ComposedChains):
             (wa, ba, sa), (wb, bb, sb) = self.W[a], self.W[b]
             try:
                 p = self.fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid)
+                p._work = p.describe()
             except self.fhconv.FhcError:
                 p = False  # no fused kernel for these channels: two launches
             self.plans[key] = p
@@ -245,102 +262,150 @@ class GpuBackend(ComposedChains):
             self.conv(a, x, mid)
             self.conv(b, mid, y, mid if res_mid else None)
         else:
-            p.run(x.buf, y.buf, None, stream=self.stream)
+            xb, yb, st = x.buf, y.buf, self.stream
+            self._go(f"{a}+{b}", lambda: p.run(xb, yb, None, stream=st), p._work["bytes"], p._work["flops"], "conv")
 
     def interp(self, x: V, c, out: V, oh, ow, aa):
-        self.fh.interp(self._v(x), oh, ow, aa, c, out=self._v(out), stream=self.stream)
+        n = x.buf.shape[0]
+        fx, fo = self._v(x), self._v(out)
+        self._go("interp", lambda: self.fh.interp(fx, oh, ow, aa, c, out=fo, stream=self.stream),
+                 2 * c * (self._px(x) + n * oh * ow))
 
     def avgpool(self, x: V, c, out: V, k):
-        self.fh.avgpool(self._v(x), k, c, out=self._v(out), stream=self.stream)
+        fx, fo = self._v(x), self._v(out)
+        self._go("avgpool", lambda: self.fh.avgpool(fx, k, c, out=fo, stream=self.stream),
+                 2 * c * (self._px(x) + self._px(out)))
 
     def luma(self, x: V, out: V, grad=False):
-        self.fh.luma(self._v(x), grad, out=self._v(out), stream=self.stream)
+        fx, fo = self._v(x), self._v(out)
+        self._go("luma_grad" if grad else "luma", lambda: self.fh.luma(fx, grad, out=fo, stream=self.stream),
+                 2 * 4 * self._px(x))
 
     def sad(self, la: V, lb: V, out: V, r):
-        self.fh.sad(self._v(la), self._v(lb), r, out=self._v(out), stream=self.stream)
+        fa, fb, fo = self._v(la), self._v(lb), self._v(out)
+        self._go("sad_volume", lambda: self.fh.sad(fa, fb, r, out=fo, stream=self.stream),
+                 2 * (2 + (2 * r + 1) ** 2) * self._px(la))
 
     def warp(self, img: V, c, flow: V, out: V):
-        self.fh.warp(self._v(img), self._v(flow), c, out=self._v(out), stream=self.stream)
+        fi, ff, fo = self._v(img), self._v(flow), self._v(out)
+        self._go("warp", lambda: self.fh.warp(fi, ff, c, out=fo, stream=self.stream), 2 * (2 * c + 2) * self._px(img))
 
     def chcopy(self, x: V, c, out: V):
-        self.fh.chcopy(self._v(x), c, out=self._v(out), stream=self.stream)
+        fx, fo = self._v(x), self._v(out)
+        self._go("chcopy", lambda: self.fh.chcopy(fx, c, out=fo, stream=self.stream), 2 * 2 * c * self._px(x))
 
     def binary(self, a: V, b: V, c, out: V, op=0):
-        self.fh.binary(self._v(a), self._v(b), op, c, out=self._v(out), stream=self.stream)
+        fa, fb, fo = self._v(a), self._v(b), self._v(out)
+        self._go("binary", lambda: self.fh.binary(fa, fb, op, c, out=fo, stream=self.stream), 2 * 3 * c * self._px(a))
 
     def unary(self, x: V, c, out: V, op, a=0.0):
-        self.fh.unary(self._v(x), op, a, 0.0, c, out=self._v(out), stream=self.stream)
+        fx, fo = self._v(x), self._v(out)
+        self._go("unary", lambda: self.fh.unary(fx, op, a, 0.0, c, out=fo, stream=self.stream),
+                 2 * 2 * c * self._px(x))
 
     def film(self, hv: V, c, out: V):
-        self.fh.film(self._v(hv), self.g, c, out=self._v(out), stream=self.stream)
+        fh_, fo, g = self._v(hv), self._v(out), self.g
+        self._go("film_modulate", lambda: self.fh.film(fh_, g, c, out=fo, stream=self.stream),
+                 2 * (2 * c * self._px(hv) + 2 * c))
 
     def convex(self, wt: V, x: V, c, out: V):
-        self.fh.convex(self._v(wt), self._v(x), c, out=self._v(out), stream=self.stream)
+        fw, fx, fo = self._v(wt), self._v(x), self._v(out)
+        self._go("convex_upsample", lambda: self.fh.convex(fw, fx, c, out=fo, stream=self.stream),
+                 2 * (36 + c + 4 * c) * self._px(x))
 
     def blendmix(self, wa: V, wb: V, vis: V, out: V):
-        self.fh.blendmix(self._v(wa), self._v(wb), self._v(vis), out=self._v(out), stream=self.stream)
+        fa, fb, fv, fo = self._v(wa), self._v(wb), self._v(vis), self._v(out)
+        self._go("blendmix", lambda: self.fh.blendmix(fa, fb, fv, out=fo, stream=self.stream),
+                 2 * 12 * self._px(wa))
 
     def render(self, a: V, b: V, flow: V, vis: V, rt: V, out: V, cubic: bool, flags: int, fsx=None, fsy=None):
-        self.fh.render(self._v(a), self._v(b), self._v(flow), self._v(vis), self._v(rt), cubic, flags,
-                       flow.scale if fsx is None else fsx, flow.scale if fsy is None else fsy, out=self._v(out),
-                       stream=self.stream)
+        fsx = flow.scale if fsx is None else fsx
+        fsy = flow.scale if fsy is None else fsy
+        va, vb, vf, vv, vr, vo = (self._v(t) for t in (a, b, flow, vis, rt, out))
+        self._go("render_pix", lambda: self.fh.render(va, vb, vf, vv, vr, cubic, flags, fsx, fsy, out=vo,
+                                                      stream=self.stream),
+                 2 * (3 * 3 * self._px(out) + 10 * self._px(flow)))
 
     def rgba_in(self, frames, out: V, hp: int, wp: int):
-        self.fh.rgba_in(frames, hp, wp, out=self._v(out), stream=self.stream)
+        fo = self._v(out)
+        self._go("rgba_in", lambda: self.fh.rgba_in(frames, hp, wp, out=fo, stream=self.stream),
+                 4 * frames.numel() + 2 * 3 * self._px(out))
 
     def rgba_out(self, x: V, out_frames):
         _, h, w = out_frames.shape
-        self.fh.rgba_out(self._v(x), h, w, out=out_frames, stream=self.stream)
+        fx = self._v(x)
+        self._go("rgba_out", lambda: self.fh.rgba_out(fx, h, w, out=out_frames, stream=self.stream),
+                 (2 * 3 + 4) * out_frames.numel())
 
     def frame_input(self, frames, full, ab: V, hp: int, wp: int, oh: int, ow: int):
         if not self.chains:
             return super().frame_input(frames, full, ab, hp, wp, oh, ow)
-        self.fh.rgba_resize(frames, hp, wp, oh, ow, out=self._v(ab), stream=self.stream)
+        fo = self._v(ab)
+        self._go("frame_input (rgba_in + resize)",
+                 lambda: self.fh.rgba_resize(frames, hp, wp, oh, ow, out=fo, stream=self.stream),
+                 4 * frames.numel() + 2 * 3 * self._px(ab))
 
     def frame_render(self, frames, full, pic, flow: V, vis: V, rt: V, out_frames, hp: int, wp: int, fsx: float,
                      fsy: float, cubic: bool, flags: int):
         if not self.chains:
             return super().frame_render(frames, full, pic, flow, vis, rt, out_frames, hp, wp, fsx, fsy, cubic, flags)
-        self.fh.render_rgba(frames[0:1], frames[1:2], self._v(flow), self._v(vis), self._v(rt), hp, wp, cubic, flags,
-                            fsx, fsy, out=out_frames, stream=self.stream)
+        vf, vv, vr = self._v(flow), self._v(vis), self._v(rt)
+        fa, fb = frames[0:1], frames[1:2]
+        self._go("frame_render (render_pix + rgba_out)",
+                 lambda: self.fh.render_rgba(fa, fb, vf, vv, vr, hp, wp, cubic, flags, fsx, fsy, out=out_frames,
+                                             stream=self.stream),
+                 4 * (frames.numel() + out_frames.numel()) + 2 * 10 * self._px(flow))
 
     # the fused chains (one launch each) unless asked for the ops one by one
     def coarse_up(self, o: V, out: V, state: Optional[V], oh: int, ow: int, flow_scale: float):
         if not self.chains:
             return super().coarse_up(o, out, state, oh, ow, flow_scale)
-        self.fh.coarse_up(self._v(o), self._v(out), None if state is None else self._v(state), oh, ow, flow_scale,
-                          stream=self.stream)
+        vo, vout, vs = self._v(o), self._v(out), None if state is None else self._v(state)
+        self._go("coarse_up", lambda: self.fh.coarse_up(vo, vout, vs, oh, ow, flow_scale, stream=self.stream),
+                 2 * (7 + (0 if state is None else 4)) * self._px(o) + 2 * 7 * oh * ow)
 
     def fold_pair(self, x: V, c: int, out: V, also: Optional[V]):
         if not self.chains:
             return super().fold_pair(x, c, out, also)
-        self.fh.fold_pair(self._v(x), self._v(out), None if also is None else self._v(also), stream=self.stream)
+        vx, vo, va = self._v(x), self._v(out), None if also is None else self._v(also)
+        self._go("fold_pair", lambda: self.fh.fold_pair(vx, vo, va, stream=self.stream),
+                 2 * c * (2 * self._px(x) + (self._px(x) // 2 if also is not None else 0)))
 
     def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
         if not self.chains:
             return super().pair_input(ab, q, i8, i16, l16, oh, ow)
-        self.fh.pair_input(self._v(ab), self._v(q), self._v(i8), self._v(i16), self._v(l16), oh, ow,
-                           stream=self.stream)
+        vs = [self._v(t) for t in (ab, q, i8, i16, l16)]
+        self._go("pair_input (resize + pyramid)",
+                 lambda: self.fh.pair_input(*vs, oh, ow, stream=self.stream),
+                 2 * (3 * self._px(ab) + 3 * self._px(q) + 3 * self._px(i8) + 6 * self._px(i16) + 2 * self._px(l16)))
 
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         if not self.chains:
             return super().pair_pyramid(q, i8, i16, l16)
-        self.fh.pair_pyramid(self._v(q), self._v(i8), self._v(i16), self._v(l16), stream=self.stream)
+        vs = [self._v(t) for t in (q, i8, i16, l16)]
+        self._go("pair_pyramid", lambda: self.fh.pair_pyramid(*vs, stream=self.stream),
+                 2 * (3 * self._px(q) + 3 * self._px(i8) + 6 * self._px(i16) + 2 * self._px(l16)))
 
     def fine_input(self, f8: V, i8: V, flow: V, fx: V, l8: V, c: int):
         if not self.chains:
             return super().fine_input(f8, i8, flow, fx, l8, c)
-        self.fh.fine_input(self._v(f8), self._v(i8), self._v(flow), self._v(fx), self._v(l8), c, stream=self.stream)
+        vs = [self._v(t) for t in (f8, i8, flow, fx, l8)]
+        p1 = self._px(flow)
+        self._go("fine_input", lambda: self.fh.fine_input(*vs, c, stream=self.stream),
+                 2 * p1 * (2 * c + 6 + 4 + (2 * c + 6 + 4) + 2))
 
     def flow_vis_t(self, fv: V, dfilm: V, out: V, t: float, lin: V, dvis: V):
         if not self.chains:
             return super().flow_vis_t(fv, dfilm, out, t, lin, dvis)
-        self.fh.flow_vis_t(self._v(fv), self._v(dfilm), self._v(out), t, stream=self.stream)
+        vs = [self._v(x) for x in (fv, dfilm, out)]
+        self._go("flow_vis_t", lambda: self.fh.flow_vis_t(*vs, t, stream=self.stream), 2 * (7 + 5 + 7) * self._px(fv))
 
     def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
         if not self.chains:
             return super().refine_input(q, flow, vis, rx, flow_out_scale, blend)
-        self.fh.refine_input(self._v(q), self._v(flow), self._v(vis), self._v(rx), flow_out_scale, stream=self.stream)
+        vs = [self._v(x) for x in (q, flow, vis, rx)]
+        self._go("refine_input", lambda: self.fh.refine_input(*vs, flow_out_scale, stream=self.stream),
+                 2 * self._px(flow) * (6 + 4 + 3 + 14))
 
 
 class FlyHighFG:

@@ -511,9 +511,16 @@ def run_pair(A, B, res, **kw):
     return y.cpu().numpy().view(np.uint16), plan
 
 
-@pytest.mark.parametrize("case", PAIR_P_CASES, ids=lambda c: "x".join(map(str, c[:7])) + (f"-{c[9]}" if c[9] else ""))
-@pytest.mark.parametrize("th,wm,loop", [(4, 1, 2), (4, 2, 2), (8, 2, 2), (4, 1, 3), (8, 1, 3)],
-                         ids=["t4w1", "t4w2", "t8w2", "t4ws", "t8ws"])
+# the resident-grid loops (tile rows, wave rows, loop) instantiated per case: 4 rows x 2 wave rows and the
+# warp-specialised loop at 4 rows for every pair; 4 rows x 1 wave row, 8 rows x 2 and the warp-specialised loop at 8
+# rows only for the 14/24-channel refine-head pairs
+PAIR_P_LOOPS = {(4, 1, 2): "t4w1", (4, 2, 2): "t4w2", (8, 2, 2): "t8w2", (4, 1, 3): "t4ws", (8, 1, 3): "t8ws"}
+PAIR_P_PARAMS = [pytest.param(c, *t, id=PAIR_P_LOOPS[t] + "-" + "x".join(map(str, c[:7])) + (f"-{c[9]}" if c[9] else ""))
+                 for c in PAIR_P_CASES for t in PAIR_P_LOOPS
+                 if c[4] <= 24 or t in ((4, 2, 2), (4, 1, 3))]
+
+
+@pytest.mark.parametrize("case,th,wm,loop", PAIR_P_PARAMS)
 def test_resident_pair_matches_the_two_convs(case, th, wm, loop):
     # loop 2: both stages on every wave; loop 3: A and B on separate waves, pipelined across tiles
     n, h, w, cin, cmid, cout, sa, act_a, act_b, res, xv, yv = case
@@ -524,11 +531,7 @@ def test_resident_pair_matches_the_two_convs(case, th, wm, loop):
     if res == "mid":
         B.res = ya
     want = B.run_oracle(threads=8)
-    try:
-        got, plan = run_pair(A, B, res, tile_rows=th, wave_rows=wm, loop=loop)
-    except fhconv.FhcError as e:
-        assert "no fused pair instantiated" in str(e)
-        pytest.skip(f"no resident pair at {th} rows x {wm} wave rows, loop {loop}, for these channels")
+    got, plan = run_pair(A, B, res, tile_rows=th, wave_rows=wm, loop=loop)
     d = plan.describe()
     say("pair/p", case[:7], d["name"], d["grid"], d["tiles"])
     assert d["persistent"] == loop - 1 and d["tile_rows"] == th and d["grid"][0] < d["tiles"]
