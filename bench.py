@@ -634,6 +634,8 @@ def main():
     net_w, net_h = 864, 480  # default_internal(1920, 1080) = (856, 480), padded to a multiple of 32
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
     if args.only_frame:
+        if not args.tune:  # no autotuning here: the frame's convs take the committed MI355X choices
+            fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
         frame, _ = frame_1080p(args, torch, np, stream)
         print(json.dumps({k: v for k, v in frame.items() if k != "launch_table"}), flush=True)
         return 0

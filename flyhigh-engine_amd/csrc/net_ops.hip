@@ -1261,12 +1261,14 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
         const uint2* lrow = tile + min(max(y - ylo, 0), ny - 1) * EXT;
 #pragma unroll
         for (int jx = 0; jx < KM; jx++) {
-            const bool inw = (y < ymax) & (xmin + jx < xmax);
+            // a tap outside the window has weight +0 and a value in [0, 1]: it adds +0, leaving acc and norm as the
+            // reference's skipped tap leaves them (interp_aa_lds_kernel selects the value instead, for views that
+            // may hold any value)
             const float wgt = wx[jx] * wy;
             const uint2 q = lrow[lc[jx]];
             const float vv[3] = {h2f((uint16_t)q.x), h2f((uint16_t)(q.x >> 16)), h2f((uint16_t)q.y)};
 #pragma unroll
-            for (int i = 0; i < 3; i++) acc[i] = acc[i] + (inw ? vv[i] : 0.0f) * wgt;
+            for (int i = 0; i < 3; i++) acc[i] = acc[i] + vv[i] * wgt;
             norm = norm + wgt;
         }
     }
@@ -1789,8 +1791,9 @@ extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_
             return fail(-1, "rgba_resize: %u x %u -> %u x %u needs %u taps, a %u-pixel tile window (at most 8 and %u)",
                         wp, hp, ow, oh, taps, ext, 5 * kAaT);
         const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
-        auto k = ext <= 3 * kAaT ? (taps <= 6 ? rgba_resize_kernel<6, 3> : rgba_resize_kernel<8, 3>)
-                                 : (taps <= 6 ? rgba_resize_kernel<6, 5> : rgba_resize_kernel<8, 5>);
+        auto k = ext <= 3 * kAaT
+                     ? (taps <= 5 ? rgba_resize_kernel<5, 3> : taps <= 6 ? rgba_resize_kernel<6, 3> : rgba_resize_kernel<8, 3>)
+                     : (taps <= 6 ? rgba_resize_kernel<6, 5> : rgba_resize_kernel<8, 5>);
         hipLaunchKernelGGL(k, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream,
                            static_cast<const uint32_t*>(rgba), w, h, pitch, fstride, hp, wp, outv(out), oh, ow, tx, ty);
         const hipError_t e = hipGetLastError();

@@ -105,8 +105,8 @@ def flyhighfg_layers(net_w: int = 864, net_h: int = 480, k: int = 1, batch_encod
             ConvLayer(f"fine.r1{sfx}", "pair", 155, 48, e8h, e8w, weight="fine.r1.0.weight"),
             ConvLayer(f"fine.r2{sfx}", "pair", 48, 48, e8h, e8w, chain=f"fine.r1{sfx}", weight="fine.r2.0.weight"),
             ConvLayer(f"fine.r3{sfx}", "pair", 48, 48, e8h, e8w, chain=f"fine.r2{sfx}", weight="fine.r3.0.weight"),
-            ConvLayer(f"fine.out{sfx}", "pair", 48, 7, e8h, e8w, act=0, chain=f"fine.r3{sfx}",
-                      weight="fine.out.weight"),
+            ConvLayer(f"fine.out{sfx}", "pair", 48, 7, e8h, e8w, act=0, residual=True, chain=f"fine.r3{sfx}",
+                      weight="fine.out.weight"),  # flow, vis += its output: the add fused as the residual
         ]
     L += [
         ConvLayer("film.h1", "mid", 48, 48, e8h, e8w, weight="film.h1.0.weight"),

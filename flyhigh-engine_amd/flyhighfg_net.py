@@ -460,7 +460,6 @@ class FlyHighFG:
         self.fx = Z(1, e8h, e8w, 160)          # wa 0 | wb 36 | ia 72 | ib 75 | flow8 78 | h 82 | fcv 130
         self.l8 = Z(1, e8h, e8w, 2)            # fla | flb
         self.fr1, self.fr2, self.h = (Z(1, e8h, e8w, 48) for _ in range(3))
-        self.d = Z(1, e8h, e8w, 8)             # fine.out: flow delta 0-3, vis delta 4-6
         self.lin = Z(1, e8h, e8w, 8)           # linf | linb
         self.hm, self.fh1, self.fh2 = (Z(1, e8h, e8w, 48) for _ in range(3))
         self.dfilm = Z(1, e8h, e8w, 8)         # d_flow 0-3, d_mask 4
@@ -501,8 +500,9 @@ class FlyHighFG:
         be.sad(V(self.l8, 0), V(self.l8, 1), V(self.fx, 130), 2)                              # fcv
         be.conv("fine.r1", V(self.fx), V(self.fr1))
         be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
-        be.conv("fine.out", V(self.h), V(self.d))
-        be.binary(V(self.fv), V(self.d), 7, V(self.fv))                                       # flow, vis += d
+        # flow, vis += d: the add of fine.out's output as the conv's residual, written in place (the planner's
+        # residual peephole, net/build.rs:222-237; f16(f32(d) + f32(fv)) either way)
+        be.conv("fine.out", V(self.h), V(self.fv), V(self.fv))
 
     def mid(self, t: float, W: Optional[dict]):
         """mid(t): models/graph.json ops 44-82, render_pix included. With W None the FiLM vector of t must

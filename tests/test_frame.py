@@ -162,7 +162,7 @@ def test_fused_chains_equal_their_ops_on_the_gpu():
     for chains in (True, False):
         gb = net.GpuBackend(W, stream=torch.cuda.current_stream(), chains=chains)
         f = run_frames(gb, W, 256, 128, fr, t=0.3)
-        extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("ftvt", 7), ("d", 7),
+        extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("ftvt", 7),
                  ("dfilm", 5), ("wt36", 36), ("f16", 72), ("AB", 4)]
         got = {name: gb.host(getattr(f, name))[..., :c].copy() for name, c in FRAME_OUTPUTS + extra}
         got["rgba"] = gb.host_frames(f.rgba).copy()
