@@ -549,3 +549,108 @@ def procedural_frame(w: int, h: int, dx: int = 0, dy: int = 0) -> np.ndarray:
     b = 0.5 + 0.35 * np.sin((fx + fy) * 0.011) + 0.1 * n
     byte = lambda v: (np.clip(v, 0.0, 1.0) * 255.0).astype(np.uint32)  # noqa: E731
     return (byte(r) | (byte(g) << 8) | (byte(b) << 16) | np.uint32(0xFF000000)).astype(np.uint32)
+
+
+def conv_layer(weight_name: str) -> str:
+    """The conv layer a weight tensor belongs to: "enc.e1.0.weight" -> "enc.e1", "coarse.head.weight" -> "coarse.head"."""
+    for sfx in (".0.weight", ".weight"):
+        if weight_name.endswith(sfx):
+            return weight_name[:-len(sfx)]
+    raise ValueError(f"not a conv weight: {weight_name}")
+
+
+def weights_from_model(model) -> dict:
+    """The model's weights (fhmodel.Model, the manifest's f16 tensors) in make_weights' form: conv layer -> (w OIHW,
+    bias, slope or None) as f16 bits, "film" -> (w1, b1, w2, b2) as f32 (model/blob.rs:32-41 decodes to f32)."""
+    W = {}
+    for name, (_, _, _, act) in CONVS.items():
+        w = model.weight(f"{name}.0.weight" if act else f"{name}.weight")
+        b = model.weight(f"{name}.0.bias" if act else f"{name}.bias")
+        s = model.weight(f"{name}.1.weight") if act else None
+        W[name] = (w, b, s)
+    f32 = lambda n: model.weight(n).view(np.float16).astype(np.float32)  # noqa: E731
+    W["film"] = (f32("film.film.0.weight").reshape(-1), f32("film.film.0.bias"), f32("film.film.2.weight"),
+                 f32("film.film.2.bias"))
+    return W
+
+
+class GraphProgram:
+    """One pair() + mid(t) replayed from the static plan of fhc_model_plan (fhmodel.Model.plan): the graph walk of
+    the reference's planner (net/build.rs:149-484) with its views, materialisations and peepholes, one backend call
+    per plan step, on the backend interface FlyHighFG uses. Buffers are NHWC (1, h, w, c rounded up to 8). The
+    frames are ``frames`` (2, h, w) RGBA8 words; the result is ``rgba`` (1, h, w). It runs the graph as the
+    reference records it, without this library's fused chains and pairs, and so serves as the check of the
+    hand-written frame program's wiring."""
+
+    def __init__(self, be, plan: dict, cubic: bool = True, render_flags: int = 0):
+        self.be, self.plan, self.cubic, self.render_flags = be, plan, cubic, render_flags
+        fw, fh = plan["frame"]
+        self.frames, self.rgba = be.frames(2, fh, fw), be.frames(1, fh, fw)
+        self.bufs = [be.zeros(1, b["h"], b["w"], pad8(b["c"])) for b in plan["buffers"]]
+        self.named = {}
+        for b, info in zip(self.bufs, plan["buffers"]):
+            if info["name"]:
+                self.named[info["name"]] = b  # the last buffer of a name (the graph rebinds carried names)
+
+    def _v(self, v: dict) -> V:
+        return V(self.bufs[v["buf"]], v["c0"], v["scale"])
+
+    def run(self, t: float, W: dict):
+        be, P = self.be, self.plan
+        be.set_g(film_mlp(W, t))
+        for s in P["steps"]:
+            op, ins, out = s["op"], [self._v(v) for v in s["in"]], self._v(s["out"])
+            c = s["out"]["c"]
+            ob = P["buffers"][s["out"]["buf"]]
+            if op == "rgba_in":
+                be.rgba_in(be.image(self.frames, s["frame"]), out, ob["h"], ob["w"])
+            elif op == "rgba_out":
+                be.rgba_out(ins[0], self.rgba)
+            elif op == "interp":
+                be.interp(ins[0], c, out, ob["h"], ob["w"], s["antialias"])
+            elif op == "conv":
+                name = conv_layer(s["weight"])
+                if CONVS[name] != (s["cin"], s["cout"], s["stride"], s["act"]):
+                    raise ValueError(f"{name}: the graph's conv {s['cin'], s['cout'], s['stride'], s['act']} differs "
+                                     f"from the program's {CONVS[name]}")
+                res = None if s["residual"] is None else self._v(s["residual"])
+                be.conv(name, ins[0], out, res)
+            elif op == "mat":
+                be.chcopy(ins[0], c, out)
+            elif op == "concat":
+                off = 0
+                for v, iv in zip(ins, s["in"]):
+                    be.chcopy(v, iv["c"], V(out.buf, out.c0 + off))
+                    off += iv["c"]
+            elif op == "avgpool":
+                be.avgpool(ins[0], c, out, s["k"])
+            elif op == "warp":
+                be.warp(ins[0], c, ins[1], out)
+            elif op == "binary":
+                be.binary(ins[0], ins[1], c, out, s["fn"])
+            elif op == "unary":
+                if s["fn"] == 0:
+                    be.unary(ins[0], c, out, 0, 2.0 * t if s["mode"] == "fwd" else 2.0 * (1.0 - t))
+                elif s["fn"] == 2:
+                    be.unary(ins[0], c, out, 2)
+                else:
+                    raise ValueError("the graph's clamp is not in this program")
+            elif op == "luma":
+                be.luma(ins[0], out)
+            elif op == "luma_grad":
+                be.luma(ins[0], out, grad=True)
+            elif op == "sad":
+                be.sad(ins[0], ins[1], out, s["radius"])
+            elif op == "film_mlp":
+                pass  # the FiLM vector: set on the backend above (the host computes it, net/build.rs:331-357)
+            elif op == "film":
+                be.film(ins[0], c, out)
+            elif op == "convex":
+                be.convex(ins[0], ins[1], c, out)
+            elif op == "blendmix":
+                be.blendmix(ins[0], ins[1], ins[2], out)
+            elif op == "render":
+                be.render(ins[0], ins[1], ins[2], ins[3], ins[4], out, self.cubic, self.render_flags, s["fsx"],
+                          s["fsy"])
+            else:
+                raise ValueError(f"plan step {op} has no backend call")

@@ -5,6 +5,8 @@ test, tests/golden_plans.rs:125-154, compares plans against) and writes ref_conv
 one record per conv the planner recorded, holding the conv's inputs (cin, cout, input h/w, stride, whether a
 residual add was fused) and the dispatches the reference recorded for it (pipeline, grid, packed-weight bytes,
 parameter words). The planner restatement (fhc_ref_conv_steps) must reproduce the dispatches from the inputs.
+Also writes ref_plan_steps.json: every plan's whole step sequence (pipeline names and grids, the mid stage's first
+step), against which the static plan of fhc_model_plan is checked step by step.
 
 Line format of the reference files (ops/step.rs:51-88): "idx pipeline (gx,gy,gz) [bindings] <u32 words as hex>".
 Run in the build container only (the reference is not present on the GPU box):
@@ -17,6 +19,7 @@ import re
 
 REF = "/root/reference/crates/flyhigh-engine/tests/golden"
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_conv_plans.json")
+OUT_STEPS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "ref_plan_steps.json")
 
 CONV = {"fused", "fused2", "fdirect", "fdirect32", "fdirect64", "tconv", "tconv8", "tconv88", "tconv8p",
         "tconvm32", "tconv16", "tconv32", "tconvn8"}
@@ -92,6 +95,25 @@ def main():
         json.dump(records, f, separators=(",", ":"))
         f.write("\n")
     print(f"{len(records)} conv records from {len(glob.glob(os.path.join(REF, '*.txt')))} golden plans -> {OUT}")
+    # the whole step sequence of every golden plan: pipeline names and grids, and where the mid stage starts
+    plans = {}
+    for path in sorted(glob.glob(os.path.join(REF, "*.txt"))):
+        base = os.path.basename(path)[:-4]
+        header, mid = "", None
+        steps = []
+        for ln in open(path):
+            if ln.startswith("# ") and not header:
+                header = ln[2:].strip()
+            elif ln.strip() == "# mid":
+                mid = len(steps)
+            m = LINE.match(ln)
+            if m:
+                steps.append([m.group(2), [int(m.group(3)), int(m.group(4)), int(m.group(5))]])
+        plans[base] = dict(header=header, mid=mid, steps=steps)
+    with open(OUT_STEPS, "w") as f:
+        json.dump(plans, f, separators=(",", ":"))
+        f.write("\n")
+    print(f"{len(plans)} step sequences -> {OUT_STEPS}")
 
 
 if __name__ == "__main__":
