@@ -1084,16 +1084,80 @@ __device__ __forceinline__ void row_taps2(const uint32_t* f, uint32_t pitch, uin
     for (int i = 0; i < 2; i++) t[i] = clampi(px + i, 0, (int)w - 1) - base == 0 ? q.x : q.y;
 }
 
+// The conversion unit_f32 as a table: entry b is f32(f16(b / 255)), the value rgba_in stores for byte b. A block
+// fills its copy (1 KiB of LDS) before any lane reads it; a read costs one VALU op (the byte times 4, a shift with a
+// byte select) where the arithmetic takes four.
+__device__ __forceinline__ void fill_unit_table(float* tab) {
+    for (uint32_t i = threadIdx.x; i < 256; i += kThreads) tab[i] = unit_f32(i << 16, 0);
+    __syncthreads();
+}
+__device__ __forceinline__ float unit_tab(const float* tab, uint32_t v, int ch) {
+    return tab[(v >> (16 - 8 * ch)) & 0xffu];
+}
+
+// The three channels of one render.wgsl sample (bicubic: :20-47, bilinear: :9-18) of an RGBA8 frame at the sample
+// point (px + tx, py + ty), px, py = floor of its coordinates, each tap converted as rgba_in converts it. INNER: the
+// columns px - 1 .. px + 2 (bicubic) or px, px + 1 (bilinear) all lie inside the frame for every lane of the wave,
+// so one 16- (8-) byte load per row holds the taps in order; otherwise each tap column is clamped to the frame.
+template <bool CUBIC, bool INNER>
+__device__ __forceinline__ void sample_rgba(const uint32_t* src, uint32_t pitch, uint32_t w, uint32_t h, int px,
+                                            int py, float tx, float ty, const float* tab, float (&o)[3]) {
+    if constexpr (CUBIC) {
+        const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
+        const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+        uint32_t t[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t yy = (uint32_t)clampi(py - 1 + j, 0, (int)h - 1);
+            if constexpr (INNER) {
+                const u32x4_a4 q = *reinterpret_cast<const u32x4_a4*>(src + (size_t)yy * pitch + (px - 1));
+                t[j][0] = q.x, t[j][1] = q.y, t[j][2] = q.z, t[j][3] = q.w;
+            } else {
+                row_taps4(src, pitch, yy, px, w, t[j]);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float row = unit_tab(tab, t[j][0], c) * cx[0] + unit_tab(tab, t[j][1], c) * cx[1] +
+                                  unit_tab(tab, t[j][2], c) * cx[2] + unit_tab(tab, t[j][3], c) * cx[3];
+                acc = j == 0 ? row * cy[0] : acc + row * cy[j];
+            }
+            o[c] = acc;
+        }
+    } else {
+        uint32_t t0[2], t1[2];
+        const uint32_t ya = (uint32_t)clampi(py, 0, (int)h - 1), yb = (uint32_t)clampi(py + 1, 0, (int)h - 1);
+        if constexpr (INNER) {
+            const u32x2_a4 q0 = *reinterpret_cast<const u32x2_a4*>(src + (size_t)ya * pitch + px);
+            const u32x2_a4 q1 = *reinterpret_cast<const u32x2_a4*>(src + (size_t)yb * pitch + px);
+            t0[0] = q0.x, t0[1] = q0.y, t1[0] = q1.x, t1[1] = q1.y;
+        } else {
+            row_taps2(src, pitch, ya, px, w, t0);
+            row_taps2(src, pitch, yb, px, w, t1);
+        }
+#pragma unroll
+        for (int c = 0; c < 3; c++)
+            o[c] = bil4(unit_tab(tab, t0[0], c), unit_tab(tab, t0[1], c), unit_tab(tab, t1[0], c),
+                        unit_tab(tab, t1[1], c), tx, ty);
+    }
+}
+
 // render_pix of the padded frame (hp x wp) from the two RGBA8 frames, written as RGBA8 (rgba_out of the f16 result),
 // cropped to w x h: render.wgsl:83-160 with its sources replaced by rgba_in.wgsl's conversion of the frames, then
 // rgba_out.wgsl. One lane per frame pixel. QV: flow and vis are channels 0-3 and 4-6 of one 8-channel view (16-byte
-// pixels) and rt has 8-byte pixels, so each quarter-map tap is two loads.
+// pixels) and rt has 8-byte pixels, so each quarter-map tap is two loads. A wave whose sample windows all lie inside
+// the frame takes the unclamped tap loads (the same values: clamping changes no column there).
 template <bool CUBIC, bool QV>
 __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
                                                                uint32_t h, uint32_t pitch, uint32_t hp, uint32_t wp,
                                                                View fl, View vis, View rt, uint32_t hq, uint32_t wq,
                                                                float fsx, float fsy, uint32_t flags, uint32_t* dst,
                                                                uint32_t opitch, uint32_t items) {
+    __shared__ float tab[256];
+    fill_unit_table(tab);
     const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
     if (pix >= items) return;
     const uint32_t x = pix % w, y = pix / w;
@@ -1136,38 +1200,17 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
     const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
     const float wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
     float ca[3], cb[3];
-#pragma unroll
-    for (int p = 0; p < 2; p++) {
-        const uint32_t* src = p == 0 ? fa : fb;
-        float* o = p == 0 ? ca : cb;
-        const float gx = (float)x + f[2 * p], gy = (float)y + f[2 * p + 1];
-        const int px = (int)floorf(gx), py = (int)floorf(gy);
-        const float tx = gx - (float)px, ty = gy - (float)py;
-        if constexpr (CUBIC) {
-            const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
-            const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
-            uint32_t t[4][4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) row_taps4(src, pitch, (uint32_t)clampi(py - 1 + j, 0, (int)h - 1), px, w, t[j]);
-#pragma unroll
-            for (int c = 0; c < 3; c++) {
-                float acc = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float row = unit_f32(t[j][0], c) * cx[0] + unit_f32(t[j][1], c) * cx[1] +
-                                      unit_f32(t[j][2], c) * cx[2] + unit_f32(t[j][3], c) * cx[3];
-                    acc = j == 0 ? row * cy[0] : acc + row * cy[j];
-                }
-                o[c] = acc;
-            }
-        } else {
-            uint32_t t0[2], t1[2];
-            row_taps2(src, pitch, (uint32_t)clampi(py, 0, (int)h - 1), px, w, t0);
-            row_taps2(src, pitch, (uint32_t)clampi(py + 1, 0, (int)h - 1), px, w, t1);
-#pragma unroll
-            for (int c = 0; c < 3; c++)
-                o[c] = bil4(unit_f32(t0[0], c), unit_f32(t0[1], c), unit_f32(t1[0], c), unit_f32(t1[1], c), tx, ty);
-        }
+    const float gxa = (float)x + f[0], gya = (float)y + f[1], gxb = (float)x + f[2], gyb = (float)y + f[3];
+    const int pxa = (int)floorf(gxa), pya = (int)floorf(gya), pxb = (int)floorf(gxb), pyb = (int)floorf(gyb);
+    const float txa = gxa - (float)pxa, tya = gya - (float)pya, txb = gxb - (float)pxb, tyb = gyb - (float)pyb;
+    const int lo = CUBIC ? 1 : 0, hi = (int)w - (CUBIC ? 3 : 2);
+    const bool inner = pxa >= lo && pxa <= hi && pxb >= lo && pxb <= hi;
+    if (__all(inner)) {
+        sample_rgba<CUBIC, true>(fa, pitch, w, h, pxa, pya, txa, tya, tab, ca);
+        sample_rgba<CUBIC, true>(fb, pitch, w, h, pxb, pyb, txb, tyb, tab, cb);
+    } else {
+        sample_rgba<CUBIC, false>(fa, pitch, w, h, pxa, pya, txa, tya, tab, ca);
+        sample_rgba<CUBIC, false>(fb, pitch, w, h, pxb, pyb, txb, tyb, tab, cb);
     }
     float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
     const float third = 1.0f / 3.0f;
@@ -1186,10 +1229,10 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
 #pragma unroll
             for (int i = 0; i < 3; i++)
 #pragma unroll
-                for (int c = 0; c < 3; c++) es += fabsf(unit_f32(ta[j][i], c) - unit_f32(tb[j][i], c));
+                for (int c = 0; c < 3; c++) es += fabsf(unit_tab(tab, ta[j][i], c) - unit_tab(tab, tb[j][i], c));
         es = es / 27.0f;
 #pragma unroll
-        for (int c = 0; c < 3; c++) own[c] = 0.5f * (unit_f32(ta[1][1], c) + unit_f32(tb[1][1], c));
+        for (int c = 0; c < 3; c++) own[c] = 0.5f * (unit_tab(tab, ta[1][1], c) + unit_tab(tab, tb[1][1], c));
         stillw = fminf(fmaxf((ef - es) / 0.04f, 0.0f), 1.0f) * (es < 0.03f ? 1.0f : 0.0f);
     }
     if (flags & 1u) {  // the decisive blend (render.wgsl:149-153)
@@ -1211,14 +1254,21 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
 // The antialiased resize of n padded RGBA8 frames (hp x wp, rgba_in's BGR f16) to oh x ow, into a view of 8-byte
 // 4-channel pixels (channel 3 written 0): rgba_in.wgsl then interp.wgsl:11-45 with antialias, as
 // interp_aa_lds_kernel computes it. A workgroup stages the union of its 16 x 16 outputs' windows, at most
-// 16 * R x 16 * R padded pixels, converted to f16 once (R = 3 covers downscales up to about 2.9x).
+// 16 * R x 16 * R padded pixels, each converted once (R = 3 covers downscales up to about 2.9x); the values are those
+// of the f16 picture rgba_in writes, held widened to f32 where the window fits (R = 3).
 template <int KM, int R>
 __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* src, uint32_t w, uint32_t h,
                                                                uint32_t pitch, uint64_t fstride, uint32_t ih,
                                                                uint32_t iw, OView out, uint32_t oh, uint32_t ow,
                                                                uint32_t tiles_x, uint32_t tiles_y) {
     constexpr uint32_t EXT = kAaT * R;
-    __shared__ uint2 tile[EXT * EXT];
+    // the staged window in f32 (37 KiB at R 3: no widening per tap) or, for the 80-pixel window, in f16
+    constexpr bool F32 = R <= 3;
+    using Cell = typename std::conditional<F32, float4, uint2>::type;
+    static_assert(kAaT * KM <= kThreads / 2, "a weight table per axis takes half the block");
+    __shared__ Cell tile[EXT * EXT];
+    __shared__ float tab[256], wxs[kAaT * KM], wys[kAaT * KM];
+    __shared__ int lcs[kAaT * KM], lrs[kAaT * KM];
     const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
     const uint32_t bt = blockIdx.x, txi = bt % tiles_x, rr = bt / tiles_x, tyi = rr % tiles_y, img = rr / tiles_y;
     const uint32_t ox0 = txi * kAaT, oy0 = tyi * kAaT;
@@ -1230,6 +1280,26 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
     const int xlo = max(0, (int)floorf(((float)ox0 + 0.5f) * sw - fsw + 0.5f));
     const int xhi = min((int)iw, (int)floorf(((float)ox_last + 0.5f) * sw + fsw + 0.5f));
     const int ny = max(1, min(yhi - ylo, (int)EXT)), nx = max(1, min(xhi - xlo, (int)EXT));
+    // the tap weights and window indices of the block's 16 columns (first half of the block) and 16 rows (second
+    // half): interp_aa.wgsl's per-tap weight, which depends on the output column (row) alone, once per block
+    tab[tid] = unit_f32(tid << 16, 0);
+    {
+        const bool rows = tid >= kThreads / 2;
+        const uint32_t k = rows ? tid - kThreads / 2 : tid;
+        if (k < kAaT * KM) {
+            const uint32_t o = (rows ? oy0 : ox0) + k / KM;
+            const float sc = rows ? sh : sw, fs = rows ? fsh : fsw;
+            const int n = rows ? (int)ih : (int)iw, lo = rows ? ylo : xlo, nn = rows ? ny : nx;
+            const float c = ((float)o + 0.5f) * sc;
+            const int tmin = max(0, (int)floorf(c - fs + 0.5f)), tmax = min(n, (int)floorf(c + fs + 0.5f));
+            const int tt = tmin + (int)(k % KM);
+            const float wgt = tt < tmax ? fmaxf(0.0f, 1.0f - fabsf(((float)tt + 0.5f - c) / fs)) : 0.0f;
+            const int li = min(max(tt - lo, 0), nn - 1);
+            if (rows) wys[k] = wgt, lrs[k] = li;
+            else wxs[k] = wgt, lcs[k] = li;
+        }
+    }
+    __syncthreads();
     const uint32_t* frame = src + img * fstride;
 #pragma unroll
     for (uint32_t i = 0; i < R; i++)
@@ -1237,36 +1307,35 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
         for (uint32_t j = 0; j < R; j++) {
             const int row = min((int)(ty + kAaT * i), ny - 1), col = min((int)(tx + kAaT * j), nx - 1);
             const uint32_t v = frame[(size_t)min(ylo + row, (int)h - 1) * pitch + min(xlo + col, (int)w - 1)];
-            tile[row * EXT + col] = uint2{(uint32_t)unit_f16(v, 0) | ((uint32_t)unit_f16(v, 1) << 16), unit_f16(v, 2)};
+            if constexpr (F32)
+                tile[row * EXT + col] = float4{unit_tab(tab, v, 0), unit_tab(tab, v, 1), unit_tab(tab, v, 2), 0.0f};
+            else
+                tile[row * EXT + col] = uint2{(uint32_t)f2h(unit_tab(tab, v, 0)) |
+                                                  ((uint32_t)f2h(unit_tab(tab, v, 1)) << 16),
+                                              (uint32_t)f2h(unit_tab(tab, v, 2))};
         }
     __syncthreads();
     const uint32_t ox = ox0 + tx, oy = oy0 + ty;
     if (ox >= ow || oy >= oh) return;
-    const float cy = ((float)oy + 0.5f) * sh, cx = ((float)ox + 0.5f) * sw;
-    const int ymin = max(0, (int)floorf(cy - fsh + 0.5f)), ymax = min((int)ih, (int)floorf(cy + fsh + 0.5f));
-    const int xmin = max(0, (int)floorf(cx - fsw + 0.5f)), xmax = min((int)iw, (int)floorf(cx + fsw + 0.5f));
     float wx[KM];
     int lc[KM];
 #pragma unroll
-    for (int j = 0; j < KM; j++) {
-        const int xx = xmin + j;
-        wx[j] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
-        lc[j] = min(max(xx - xlo, 0), nx - 1);
-    }
+    for (int j = 0; j < KM; j++) wx[j] = wxs[tx * KM + j], lc[j] = lcs[tx * KM + j];
     float acc[3] = {0.0f, 0.0f, 0.0f}, norm = 0.0f;
 #pragma unroll
     for (int jy = 0; jy < KM; jy++) {
-        const int y = ymin + jy;
-        const float wy = y < ymax ? fmaxf(0.0f, 1.0f - fabsf(((float)y + 0.5f - cy) / fsh)) : 0.0f;
-        const uint2* lrow = tile + min(max(y - ylo, 0), ny - 1) * EXT;
+        const float wy = wys[ty * KM + jy];
+        const Cell* lrow = tile + lrs[ty * KM + jy] * EXT;
 #pragma unroll
         for (int jx = 0; jx < KM; jx++) {
             // a tap outside the window has weight +0 and a value in [0, 1]: it adds +0, leaving acc and norm as the
             // reference's skipped tap leaves them (interp_aa_lds_kernel selects the value instead, for views that
             // may hold any value)
             const float wgt = wx[jx] * wy;
-            const uint2 q = lrow[lc[jx]];
-            const float vv[3] = {h2f((uint16_t)q.x), h2f((uint16_t)(q.x >> 16)), h2f((uint16_t)q.y)};
+            const Cell q = lrow[lc[jx]];
+            float vv[3];
+            if constexpr (F32) vv[0] = q.x, vv[1] = q.y, vv[2] = q.z;
+            else vv[0] = h2f((uint16_t)q.x), vv[1] = h2f((uint16_t)(q.x >> 16)), vv[2] = h2f((uint16_t)q.y);
 #pragma unroll
             for (int i = 0; i < 3; i++) acc[i] = acc[i] + vv[i] * wgt;
             norm = norm + wgt;
