@@ -310,7 +310,7 @@ def frame_1080p(args, torch, np, stream, t=0.5):
     rgba = be.host_frames(f.rgba)
     ok = bool(np.all(rgba >> 24 == 255)) and len(np.unique(rgba)) > 1000
     # every launch of the frame, timed alone (the recorder re-issues each with the frame's own buffers)
-    be.record = []
+    be.record = []  # each launch re-issued alone
     with torch.cuda.stream(stream):
         f.pair()
         f.mid(t, None)
@@ -326,12 +326,12 @@ def frame_1080p(args, torch, np, stream, t=0.5):
         log("frame launch", json.dumps(launches[-1]))
     res = dict(us_per_frame=round(us, 3), frames_per_s=round(1e6 / us, 2), event_us_per_frame=round(ev_us, 3),
                steps=args.steps, warmup=args.warmup, network=f"{net_w}x{net_h}", frame="1920x1080",
-               launches=len(rec), launch_us_sum=round(sum(x["us_warm"] for x in launches), 3),
+               launches=sum(x.get("kernels", 1) for x in rec),
+               launch_us_sum=round(sum(x["us_warm"] for x in launches), 3),
                output_ok=ok, launch_table=launches,
-               workload="one 1080p pair()+mid(0.5) from two 1920x1080 RGBA8 frames to the RGBA8 in-between frame: "
-                        "rgba_in + downscale to the 864x480 network, every graph op (convs, fused pairs, ops), "
-                        "render_pix (bicubic) at 1920x1088 + rgba_out; one HIP graph; random weights, synthetic "
-                        "frames (12 px translation)")
+               workload="1080p pair()+mid(0.5), two 1920x1080 RGBA8 frames to the RGBA8 in-between frame: "
+                        "rgba_in+downscale to 864x480, every graph op, GMHS repair (level 1), bicubic render_pix at "
+                        "1920x1088 + rgba_out; one HIP graph; random weights, synthetic frames (12 px shift)")
     return res, (be, f, rec)
 
 

@@ -633,7 +633,8 @@ size_t mid_start(const Json& ops, size_t n) {
     return n;
 }
 
-std::string plan_json(const fhc_model& m, uint32_t k, uint32_t fw, uint32_t fh, uint32_t nw, uint32_t nh) {
+std::string plan_json(const fhc_model& m, uint32_t k, uint32_t fw, uint32_t fh, uint32_t nw, uint32_t nh,
+                      uint32_t repair) {
     const uint32_t hp = (fh + 31) / 32 * 32, wp = (fw + 31) / 32 * 32;
     const uint32_t ihp = (nh + 31) / 32 * 32, iwp = (nw + 31) / 32 * 32;
     if (ihp > hp || iwp > wp) throw std::runtime_error("the network size exceeds the frame");
@@ -666,6 +667,21 @@ std::string plan_json(const fhc_model& m, uint32_t k, uint32_t fw, uint32_t fh, 
     const size_t body = internal && rend < n ? rend : n;
     const size_t ms = mid_start(m.ops, body);
     p.walk(m.ops, 0, ms);
+    if (repair > 0) {  // build.rs:640-660: the periodic-structure repair of the pair's flow, in place
+        auto it = p.env.find("flow");
+        View f;
+        if (it != p.env.end()) {
+            f = it->second;
+        } else {  // the flow's readers are built; its buffer lives on in the flowf view
+            auto jt = p.env.find("flowf");
+            if (jt == p.env.end()) throw std::runtime_error("graph.json: the pair flow is not found for the repair");
+            f = jt->second;
+            f.c = 4, f.c0 = 0, f.scale = 1.0f;
+        }
+        if (!f.plain() || f.c != 4) throw std::runtime_error("graph.json: the pair flow is not a plain 4-channel tensor");
+        p.step("gmhs", {p.get("A"), p.get("B"), f}, f,
+               "\"level\":" + std::to_string(repair) + ",\"full_w\":" + std::to_string(wp));
+    }
     p.stage = "mid";
     p.walk(m.ops, ms, body);
     View render;
@@ -787,16 +803,17 @@ extern "C" int64_t fhc_model_weight(const fhc_model* m, const char* name, uint16
 }
 
 extern "C" int fhc_model_plan(const fhc_model* m, uint32_t k, uint32_t frame_w, uint32_t frame_h, uint32_t net_w,
-                              uint32_t net_h, char* json, size_t cap) {
+                              uint32_t net_h, uint32_t repair, char* json, size_t cap) {
     return guard(-1, [&]() -> int {
         if (!m) return fail(-1, "fhc_model_plan: NULL model");
         if (!frame_w || !frame_h || !net_w || !net_h || frame_w > 16384 || frame_h > 16384)
             return fail(-1, "fhc_model_plan: bad sizes (frame %u x %u, network %u x %u)", frame_w, frame_h, net_w,
                         net_h);
         if (k == 0 || k > 16) return fail(-1, "fhc_model_plan: k must be 1..16");
+        if (repair > 2) return fail(-1, "fhc_model_plan: repair level %u (0 off, 1 safe, 2 aggressive)", repair);
         std::string s;
         try {
-            s = plan_json(*m, k, frame_w, frame_h, net_w, net_h);
+            s = plan_json(*m, k, frame_w, frame_h, net_w, net_h, repair);
         } catch (const std::exception& e) {
             return fail(-1, "fhc_model_plan: %s", e.what());
         }

@@ -1345,6 +1345,250 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
         uint2{(uint32_t)f2h(acc[0] / norm) | ((uint32_t)f2h(acc[1] / norm) << 16), (uint32_t)f2h(acc[2] / norm)};
 }
 
+// ---- GMHS: the periodic-structure repair of the pair's E8 flow (gmhs.rs:149-206) ----------------------------------
+// Eight launches where the reference records fourteen dispatches: four fit rounds (gm_fit_reduce.wgsl, each round
+// solving the previous one's normal equations first, gm_fit_solve.wgsl), the cost maps (gm_cost.wgsl, solving the
+// last round), the two box windows, box_h + box_v fused (gm_box.wgsl), and the select (gm_select.wgsl). Every value
+// is the reference kernels' arithmetic in their order: the fit keeps gm_fit_reduce's 32 workgroups of 256 lanes with
+// their strided per-lane sums and pairwise lane tree (its last levels as in-wave shuffles, the same pairs), so the
+// sums round as there; a box sums its clamped taps in order, from a window staged in LDS. The stage is
+// latency-bound (a few MB of L2-resident maps, 6480 flow cells at 1080p): the kernels are shaped for waves in flight,
+// one block per tile and map channel, tap loads unrolled ahead of their in-order sums; a host runs the stage beside
+// independent work (the frame program forks it beside the FiLM branch of mid()).
+constexpr uint32_t kGmNwg = 32, kGmWg = 256;  // gm_fit_reduce's workgroups and workgroup size (gmhs.rs:160)
+constexpr uint32_t kGmPart = kGmNwg * 4 * 9;  // one round's partial sums [workgroup][channel][9]
+constexpr uint32_t kGmT = 16;                 // the cost kernel's block edge and the box tile's, in cells
+constexpr uint32_t kGmRmax = 32;              // largest box radius: r_dwin = round(16 s), s <= 2
+constexpr uint32_t kGmWin = kGmT + 2 * kGmRmax;
+
+// gm_fit_solve.wgsl:13-24: the normal equations of one flow channel, s = its summed partials; o = a0, a1, a2
+__device__ void gm_solve(const float* s, float* o) {
+    const float m00 = s[0] + 1e-6f, m01 = s[1], m02 = s[2], m11 = s[3] + 1e-6f, m12 = s[4], m22 = s[5] + 1e-6f;
+    const float det = m00 * (m11 * m22 - m12 * m12) - m01 * (m01 * m22 - m12 * m02) + m02 * (m01 * m12 - m11 * m02);
+    if (fabsf(det) < 1e-12f) {
+        o[0] = s[6] / fmaxf(s[0], 1e-6f), o[1] = 0.0f, o[2] = 0.0f;
+        return;
+    }
+    const float i00 = (m11 * m22 - m12 * m12) / det, i01 = (m02 * m12 - m01 * m22) / det;
+    const float i02 = (m01 * m12 - m02 * m11) / det, i11 = (m00 * m22 - m02 * m02) / det;
+    const float i12 = (m01 * m02 - m00 * m12) / det, i22 = (m00 * m11 - m01 * m01) / det;
+    o[0] = i00 * s[6] + i01 * s[7] + i02 * s[8];
+    o[1] = i01 * s[6] + i11 * s[7] + i12 * s[8];
+    o[2] = i02 * s[6] + i12 * s[7] + i22 * s[8];
+}
+
+// the coefficients of the channels `chans` (bit c: channel c) from a round's partials, into cf[c][0..2]: lane
+// c * 9 + k sums partial k over the workgroups in order (gm_fit_solve.wgsl:11-12; the 32 loads issued together),
+// lane c solves. Every lane of the block takes part in the barriers.
+__device__ void gm_solve_block(const float* part, uint32_t chans, float (*ss)[9], float (*cf)[3]) {
+    const uint32_t t = threadIdx.x;
+    if (t < 36 && (chans >> (t / 9) & 1u)) {
+        const uint32_t c = t / 9, k = t % 9;
+        float v[kGmNwg];
+#pragma unroll
+        for (uint32_t g = 0; g < kGmNwg; g++) v[g] = part[(g * 4 + c) * 9 + k];
+        float a = 0.0f;
+#pragma unroll
+        for (uint32_t g = 0; g < kGmNwg; g++) a = a + v[g];
+        ss[c][k] = a;
+    }
+    __syncthreads();
+    if (t < 4 && (chans >> t & 1u)) gm_solve(ss[t], cf[t]);
+    __syncthreads();
+}
+
+// one fit round (gm_fit_reduce.wgsl:15-44) for workgroup blockIdx.x of channel blockIdx.y; rounds after the first
+// weight each element by delta / max(delta, |residual|) against the coefficients of the previous round's partials
+__global__ __launch_bounds__(kGmWg) void gm_fit_kernel(View flow, uint32_t h8, uint32_t w8, float delta, uint32_t round,
+                                                       const float* part_in, float* part_out) {
+    __shared__ float sh[9][kGmWg / 2];
+    __shared__ float ss[4][9], cf[4][3];
+    const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+    const uint32_t n = h8 * w8, stride = kGmWg * kGmNwg, i0 = g * kGmWg + t;
+    const float f0 = i0 < n ? ld(flow, i0, c) : 0.0f;  // in flight while the previous round is solved
+    if (round > 0) gm_solve_block(part_in, 1u << c, ss, cf);
+    const float sx = 2.0f / (float)max(w8 - 1, 1u), sy = 2.0f / (float)max(h8 - 1, 1u);
+    float s[9] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t i = i0; i < n; i += stride) {
+        const uint32_t yy = i / w8, xx = i - yy * w8;
+        const float x = -1.0f + sx * (float)xx, y = -1.0f + sy * (float)yy;
+        const float f = i == i0 ? f0 : ld(flow, i, c);
+        float w2 = 1.0f;
+        if (round > 0) w2 = delta / fmaxf(delta, fabsf(f - (cf[c][0] + cf[c][1] * x + cf[c][2] * y)));
+        s[0] = s[0] + w2, s[1] = s[1] + w2 * x, s[2] = s[2] + w2 * y;
+        s[3] = s[3] + w2 * x * x, s[4] = s[4] + w2 * x * y, s[5] = s[5] + w2 * y * y;
+        s[6] = s[6] + w2 * f, s[7] = s[7] + w2 * x * f, s[8] = s[8] + w2 * y * f;
+    }
+    // the lane tree, pairs (t, t + off) for off = 128 .. 1: the first level through LDS, the rest in the first wave
+    if (t >= kGmWg / 2)
+#pragma unroll
+        for (uint32_t k = 0; k < 9; k++) sh[k][t - kGmWg / 2] = s[k];
+    __syncthreads();
+    if (t < kGmWg / 2)
+#pragma unroll
+        for (uint32_t k = 0; k < 9; k++) sh[k][t] = s[k] + sh[k][t];
+    __syncthreads();
+    if (t < 64) {
+#pragma unroll
+        for (uint32_t k = 0; k < 9; k++) {
+            float v = sh[k][t] + sh[k][t + 64];
+#pragma unroll
+            for (uint32_t off = 32; off > 0; off >>= 1) v = v + __shfl_down(v, off);
+            if (t == 0) part_out[(g * 4 + c) * 9 + k] = v;
+        }
+    }
+}
+
+// the B, G, R of pixel pix of a picture view (VEC: one 8-byte load, 4-channel aligned views)
+template <bool VEC>
+__device__ __forceinline__ void bgr(const View& v, size_t pix, float (&o)[3]) {
+    if constexpr (VEC) {
+        const uint2 q = *reinterpret_cast<const uint2*>(v.p + pix * v.cs + v.c0);
+        o[0] = h2f((uint16_t)q.x), o[1] = h2f((uint16_t)(q.x >> 16)), o[2] = h2f((uint16_t)q.y);
+    } else {
+        o[0] = ld(v, pix, 0), o[1] = ld(v, pix, 1), o[2] = ld(v, pix, 2);
+    }
+}
+template <bool VEC>
+__device__ __forceinline__ float gm_lum(const View& v, uint32_t w, int y, int x) {
+    float p[3];
+    bgr<VEC>(v, (size_t)y * w + x, p);
+    return lum3(p[0], p[1], p[2]);
+}
+// gm_cost.wgsl:23-29: bilinear luma, coordinates clamped
+template <bool VEC>
+__device__ float gm_samp(const View& v, uint32_t h, uint32_t w, float gx, float gy) {
+    const int x0 = (int)floorf(gx), y0 = (int)floorf(gy);
+    const float ax = gx - (float)x0, ay = gy - (float)y0;
+    const int x0c = clampi(x0, 0, (int)w - 1), x1c = clampi(x0 + 1, 0, (int)w - 1);
+    const int y0c = clampi(y0, 0, (int)h - 1), y1c = clampi(y0 + 1, 0, (int)h - 1);
+    const float top = gm_lum<VEC>(v, w, y0c, x0c) * (1.0f - ax) + gm_lum<VEC>(v, w, y0c, x1c) * ax;
+    const float bot = gm_lum<VEC>(v, w, y1c, x0c) * (1.0f - ax) + gm_lum<VEC>(v, w, y1c, x1c) * ax;
+    return top * (1.0f - ay) + bot * ay;
+}
+
+// gm_cost.wgsl:55-75, maps 0-4 (planar [5][hc][wc]); one lane per cell of a 16 x 16 block, the block solving the
+// last fit round first (block 0 also stores the coefficients, [4][4], for the select and the caller). VEC: the
+// pictures and the flow are 4-channel aligned views (one 8-byte load per pixel).
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint32_t h, uint32_t w, View flow,
+                                                           uint32_t h8, uint32_t w8, const float* part, float* coef,
+                                                           float* maps, uint32_t hc, uint32_t wc) {
+    __shared__ float ss[4][9], cf[4][3];
+    const uint32_t t = threadIdx.x;
+    const uint32_t x = blockIdx.x * 16 + t % 16, y = blockIdx.y * 16 + t / 16;
+    const bool valid = x < wc && y < hc;
+    const float rx = ((float)x + 0.5f) * 2.0f - 0.5f, ry = ((float)y + 0.5f) * 2.0f - 0.5f;
+    // the E8 flow at (rx, ry), bilinear (gm_cost.wgsl:38-48), loaded before the block's solve
+    const float ix = (rx + 0.5f) * (float)w8 / (float)w - 0.5f, iy = (ry + 0.5f) * (float)h8 / (float)h - 0.5f;
+    const int qx0 = (int)floorf(ix), qy0 = (int)floorf(iy);
+    const float fx = ix - (float)qx0, fy = iy - (float)qy0;
+    const uint32_t x0 = clampi(qx0, 0, (int)w8 - 1), x1 = clampi(qx0 + 1, 0, (int)w8 - 1);
+    const uint32_t y0 = clampi(qy0, 0, (int)h8 - 1), y1 = clampi(qy0 + 1, 0, (int)h8 - 1);
+    float q[4][4] = {};
+    if (valid) {
+        const size_t taps[4] = {(size_t)y0 * w8 + x0, (size_t)y0 * w8 + x1, (size_t)y1 * w8 + x0, (size_t)y1 * w8 + x1};
+#pragma unroll
+        for (uint32_t k = 0; k < 4; k++) {
+            if constexpr (VEC) {
+                const uint2 v = *reinterpret_cast<const uint2*>(flow.p + taps[k] * flow.cs + flow.c0);
+                q[k][0] = h2f((uint16_t)v.x), q[k][1] = h2f((uint16_t)(v.x >> 16));
+                q[k][2] = h2f((uint16_t)v.y), q[k][3] = h2f((uint16_t)(v.y >> 16));
+            } else {
+#pragma unroll
+                for (uint32_t c = 0; c < 4; c++) q[k][c] = ld(flow, taps[k], c);
+            }
+        }
+    }
+    gm_solve_block(part, 0xfu, ss, cf);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && t < 16) coef[t] = (t & 3u) == 3u ? 0.0f : cf[t >> 2][t & 3u];
+    if (!valid) return;
+    const size_t n = (size_t)hc * wc, i = (size_t)y * wc + x;
+    const float xn = -1.0f + 2.0f * ix / (float)max(w8 - 1, 1u), yn = -1.0f + 2.0f * iy / (float)max(h8 - 1, 1u);
+    float f[4], gh[4];
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++) {
+        const float top = q[0][c] * (1.0f - fx) + q[1][c] * fx, bot = q[2][c] * (1.0f - fx) + q[3][c] * fx;
+        f[c] = top * (1.0f - fy) + bot * fy;
+        gh[c] = cf[c][0] + cf[c][1] * xn + cf[c][2] * yn;
+    }
+    const float cm =
+        fabsf(gm_samp<VEC>(a, h, w, rx + f[0], ry + f[1]) - gm_samp<VEC>(b, h, w, rx + f[2], ry + f[3]));
+    const float wm = (float)w - 1.0f, hm = (float)h - 1.0f;
+    const float ax = rx + gh[0], ay = ry + gh[1], bx = rx + gh[2], by = ry + gh[3];
+    const bool inside = ax >= 0.0f && ax <= wm && ay >= 0.0f && ay <= hm && bx >= 0.0f && bx <= wm && by >= 0.0f &&
+                        by <= hm;
+    const float ca = inside ? fabsf(gm_samp<VEC>(a, h, w, ax, ay) - gm_samp<VEC>(b, h, w, bx, by)) : cm;
+    const float l = gm_samp<VEC>(a, h, w, rx, ry);
+    const float dvx = (gh[2] - gh[0]) - (f[2] - f[0]), dvy = (gh[3] - gh[1]) - (f[3] - f[1]);
+    maps[i] = cm, maps[n + i] = ca, maps[2 * n + i] = sqrtf(dvx * dvx + dvy * dvy);
+    maps[3 * n + i] = l, maps[4 * n + i] = l * l;
+}
+
+// box_h then box_v of radius r (gm_box.wgsl:8-25) on map channel blockIdx.z of src ([c][hc][wc]) into the same
+// channel of dst, for the block's 16 x 16 tile of cells; channels from `nfilt` on are copied unfiltered. The window
+// of clamped rows and columns the tile's taps reach is staged in LDS; box_h runs on every window row (a window row
+// is a clamped map row, so its sums are the map's own), box_v on the tile; the taps of each sum are loaded 8 at a
+// time ahead of their in-order additions.
+__global__ __launch_bounds__(kThreads) void gm_box_kernel(const float* src, float* dst, uint32_t nfilt, uint32_t hc,
+                                                          uint32_t wc, uint32_t r) {
+    __shared__ float win[kGmWin * kGmWin], hs[kGmWin * kGmT];
+    const uint32_t t = threadIdx.x, x0 = blockIdx.x * kGmT, y0 = blockIdx.y * kGmT, ch = blockIdx.z;
+    const uint32_t ty = t / kGmT, tx = t % kGmT;
+    const size_t n = (size_t)hc * wc;
+    const float* plane = src + ch * n;
+    const bool inside = x0 + tx < wc && y0 + ty < hc;
+    const size_t at = (size_t)(y0 + ty) * wc + x0 + tx;
+    if (ch >= nfilt) {
+        if (inside) dst[ch * n + at] = plane[at];
+        return;
+    }
+    const uint32_t span = 2 * r + 1, rows = kGmT + 2 * r;
+    const float den = (float)span;
+    for (uint32_t k = t; k < rows * rows; k += kThreads) {
+        const uint32_t j = k / rows, i = k % rows;
+        const int yy = clampi((int)y0 - (int)r + (int)j, 0, (int)hc - 1);
+        const int xx = clampi((int)x0 - (int)r + (int)i, 0, (int)wc - 1);
+        win[j * kGmWin + i] = plane[(size_t)yy * wc + xx];
+    }
+    __syncthreads();
+    for (uint32_t k = t; k < rows * kGmT; k += kThreads) {
+        const uint32_t j = k / kGmT, xo = k % kGmT;
+        const float* row = win + j * kGmWin + xo;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (uint32_t d = 0; d < span; d++) acc = acc + row[d];
+        hs[j * kGmT + xo] = acc / den;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+#pragma unroll 8
+    for (uint32_t d = 0; d < span; d++) acc = acc + hs[(ty + d) * kGmT + tx];
+    if (inside) dst[ch * n + at] = acc / den;
+}
+
+// gm_select.wgsl:14-27, one lane per E8 cell: the cell adopts the affine motion where the nearest cost cell's
+// decision maps say so
+__global__ __launch_bounds__(kThreads) void gm_select_kernel(const float* maps, const float* coef, OView flow,
+                                                             uint32_t h8, uint32_t w8, uint32_t hc, uint32_t wc,
+                                                             float eps, float dmin, float tex, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t i = t / w8, j = t % w8;
+    const int x = clampi((int)floorf(((float)j + 0.5f) * (float)wc / (float)w8), 0, (int)wc - 1);
+    const int y = clampi((int)floorf(((float)i + 0.5f) * (float)hc / (float)h8), 0, (int)hc - 1);
+    const size_t n = (size_t)hc * wc, idx = (size_t)y * wc + x;
+    const float cm = maps[idx], ca = maps[n + idx], dv = maps[2 * n + idx], lm = maps[3 * n + idx];
+    const float l2 = maps[4 * n + idx];
+    const float sd = sqrtf(fmaxf(l2 - lm * lm, 0.0f));
+    if (ca + eps < cm && dv > dmin && sd > tex) {
+        const float xn = -1.0f + 2.0f * (float)j / (float)max(w8 - 1, 1u);
+        const float yn = -1.0f + 2.0f * (float)i / (float)max(h8 - 1, 1u);
+#pragma unroll
+        for (uint32_t c = 0; c < 4; c++) st(flow, t, c, coef[c * 4] + coef[c * 4 + 1] * xn + coef[c * 4 + 2] * yn);
+    }
+}
+
 // ---- host side ----------------------------------------------------------------------------------------------------
 
 constexpr uint64_t kMaxItems = 1ull << 31;
@@ -1388,6 +1632,29 @@ int launch(const char* op, uint64_t items, F&& f) {
         const int rc_ = (x);    \
         if (rc_ < 0) return rc_; \
     } while (0)
+
+// gmhs.rs:149-160: the cost grid (DS = 2), the two box radii, the jump and Huber thresholds; eps 0, tex 0.015
+// (gmhs.rs:195). The workspace: the coefficients [4][4] at byte 0, two rounds of fit partials, then the decision
+// maps [5][hc][wc] and their box-filtered copy, 256-byte aligned.
+int gm_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc_gmhs_par* p) {
+    if (!p) return fail(-1, "gmhs: null parameter block");
+    if (h == 0 || w == 0) return fail(-1, "gmhs: empty network (%u x %u)", w, h);
+    if (level < 1 || level > 2) return fail(-1, "gmhs: repair level %u (1 safe, 2 aggressive)", level);
+    if (full_w < w) return fail(-1, "gmhs: the network (%u wide) is wider than the padded frame (%u)", w, full_w);
+    p->hc = (h + 1) / 2, p->wc = (w + 1) / 2;
+    const float s = (float)w / ((float)full_w / 2.0f);
+    const float rb = std::round(20.0f * s / 2.0f), rw = std::round(32.0f * s / 2.0f);
+    p->s = s;
+    p->r_blk = rb < 1.0f ? 1u : (uint32_t)rb;
+    p->r_dwin = rw < 1.0f ? 1u : (uint32_t)rw;
+    p->dmin = level >= 2 ? 0.0f : 8.0f * s;
+    p->delta = 1.5f * s;
+    p->eps = 0.0f, p->tex = 0.015f;
+    const uint64_t head = (16 + 2 * (uint64_t)kGmPart) * sizeof(float), cells = (uint64_t)p->hc * p->wc;
+    p->maps_offset = (head + 255) / 256 * 256;
+    p->ws_bytes = p->maps_offset + 2 * 5 * cells * sizeof(float);
+    return 0;
+}
 
 }  // namespace
 
@@ -1895,5 +2162,58 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
                                static_cast<const uint32_t*>(b), w, h, pitch, hp, wp, in(flow), in(vis), in(rt), hq,
                                wq, fsx, fsy, flags, static_cast<uint32_t*>(out), opitch, items);
         });
+    });
+}
+
+extern "C" int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc_gmhs_par* out) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        return gm_params(h, w, full_w, level, out);
+    });
+}
+
+extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
+                        uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
+                        void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if (level == 0) return 0;
+        fhc_gmhs_par p;
+        FHC_TRY(gm_params(h, w, full_w, level, &p));
+        if (h8 == 0 || w8 == 0) return fail(-1, "gmhs: empty E8 flow (%u x %u)", w8, h8);
+        FHC_TRY(check(a, "gmhs a", 3, false));
+        FHC_TRY(check(b, "gmhs b", 3, false));
+        FHC_TRY(check(flow, "gmhs flow", 4, false));
+        if (!ws) return fail(-1, "gmhs: null workspace");
+        if (ws_bytes < p.ws_bytes)
+            return fail(-1, "gmhs: workspace of %zu bytes, %llu needed", ws_bytes, (unsigned long long)p.ws_bytes);
+        if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(-1, "gmhs: the workspace must be 256-byte aligned");
+        if (p.r_blk > kGmRmax || p.r_dwin > kGmRmax)
+            return fail(-1, "gmhs: box radii %u, %u exceed %u", p.r_blk, p.r_dwin, kGmRmax);
+        if ((uint64_t)h8 * w8 >= kMaxItems || (uint64_t)h * w >= kMaxItems)
+            return fail(-1, "gmhs: %u x %u network, %u x %u flow: too large", w, h, w8, h8);
+        float* coef = static_cast<float*>(ws);
+        float* part[2] = {coef + 16, coef + 16 + kGmPart};
+        float* maps = reinterpret_cast<float*>(static_cast<char*>(ws) + p.maps_offset);
+        float* tmp = maps + 5 * (size_t)p.hc * p.wc;
+        const hipStream_t st = (hipStream_t)stream;
+        for (uint32_t round = 0; round < 4; round++)
+            hipLaunchKernelGGL(gm_fit_kernel, dim3(kGmNwg, 4), dim3(kGmWg), 0, st, in(flow), h8, w8, p.delta, round,
+                               part[(round + 1) & 1u], part[round & 1u]);
+        const bool v = vec4(4, {a, b, flow});
+        const dim3 tiles((p.wc + kGmT - 1) / kGmT, (p.hc + kGmT - 1) / kGmT);
+        hipLaunchKernelGGL(v ? gm_cost_kernel<true> : gm_cost_kernel<false>, tiles, dim3(kThreads), 0, st, in(a), in(b),
+                           h, w, in(flow), h8, w8, part[1], coef, maps, p.hc, p.wc);
+        // the texture window over the 5 maps (maps -> tmp), the decision window over maps 0-2 with maps 3 and 4
+        // copied (tmp -> maps), the select
+        hipLaunchKernelGGL(gm_box_kernel, dim3(tiles.x, tiles.y, 5), dim3(kThreads), 0, st, maps, tmp, 5u, p.hc, p.wc,
+                           p.r_blk);
+        hipLaunchKernelGGL(gm_box_kernel, dim3(tiles.x, tiles.y, 5), dim3(kThreads), 0, st, tmp, maps, 3u, p.hc, p.wc,
+                           p.r_dwin);
+        const uint32_t cells = h8 * w8;
+        hipLaunchKernelGGL(gm_select_kernel, dim3((cells + kThreads - 1) / kThreads), dim3(kThreads), 0, st, maps, coef,
+                           outv(flow), h8, w8, p.hc, p.wc, p.eps, p.dmin, p.tex, cells);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "gmhs: launch failed: %s", hipGetErrorString(e));
     });
 }

@@ -3,7 +3,7 @@ static plan of a frame.
 
 ``Model.load(dir)`` reads graph.json, flyhighfg.json and flyhighfg.bin from a directory the caller names (the
 reference's Model::from_dir, crates/flyhigh-engine/src/model/mod.rs:38-96); ``info()``, ``shape(name)`` and
-``weight(name)`` (f16 bits, model/blob.rs:29-41) read it; ``plan(k, frame, network)`` walks the graph into the plan
+``weight(name)`` (f16 bits, model/blob.rs:29-41) read it; ``plan(k, frame, network, repair)`` walks the graph into the plan
 of one pair() + mid() (net/build.rs:149-736, net/session.rs:26-66). Errors raise ``FhcError`` with the library's
 message. No model file travels with this repository.
 """
@@ -33,7 +33,7 @@ def _lib():
             "fhc_model_tensor": ([P, ctypes.c_char_p, ctypes.POINTER(U32), SZ, ctypes.POINTER(ctypes.c_uint64)],
                                  ctypes.c_int),
             "fhc_model_weight": ([P, ctypes.c_char_p, P, SZ], ctypes.c_int64),
-            "fhc_model_plan": ([P, U32, U32, U32, U32, U32, ctypes.c_char_p, SZ], ctypes.c_int),
+            "fhc_model_plan": ([P, U32, U32, U32, U32, U32, U32, ctypes.c_char_p, SZ], ctypes.c_int),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -88,12 +88,13 @@ class Model:
         _check(_lib().fhc_model_weight(self._h, name.encode(), out.ctypes.data, out.size), "fhc_model_weight")
         return out.reshape(shape)
 
-    def plan(self, k: int, frame: Tuple[int, int], network: Tuple[int, int]) -> dict:
-        """The static plan of one pair() + mid() for frames of frame = (w, h) at the network size (w, h)."""
+    def plan(self, k: int, frame: Tuple[int, int], network: Tuple[int, int], repair: int = 1) -> dict:
+        """The static plan of one pair() + mid() for frames of frame = (w, h) at the network size (w, h), with the
+        periodic-structure repair at level `repair` (0 off; 1, the reference's default)."""
         cap = 1 << 20
         while True:
             buf = ctypes.create_string_buffer(cap)
-            rc = _lib().fhc_model_plan(self._h, k, frame[0], frame[1], network[0], network[1], buf, cap)
+            rc = _lib().fhc_model_plan(self._h, k, frame[0], frame[1], network[0], network[1], repair, buf, cap)
             if rc >= 0:
                 return json.loads(buf.value.decode())
             if "buffer too small" not in fhconv.last_error():

@@ -42,6 +42,12 @@ class View:
         return FhcTensor(self.t.data_ptr(), self.t.shape[3], self.c0, self.scale)
 
 
+class GmhsPar(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("hc", "wc", "r_blk", "r_dwin")] + [
+        (n, ctypes.c_float) for n in ("s", "dmin", "delta", "eps", "tex")] + [
+        ("ws_bytes", ctypes.c_uint64), ("maps_offset", ctypes.c_uint64)]
+
+
 def _v(x) -> View:
     return x if isinstance(x, View) else View(x)
 
@@ -80,6 +86,8 @@ def _lib():
             "fhc_rgba_resize": [P, U, U, U, U, ctypes.c_uint64, U, U, T, U, U, P],
             "fhc_render_rgba": [P, P, U, U, U, U, U, T, T, T, U, U, ctypes.c_float, ctypes.c_float, I, U, P, U,
                                 P],
+            "fhc_gmhs_params": [U, U, U, U, ctypes.POINTER(GmhsPar)],
+            "fhc_gmhs": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -342,3 +350,39 @@ def render_rgba(fa, fb, flow, vis, rt, hp: int, wp: int, cubic=True, flags=0, fs
                                                _ref(rt), hq, wq, fsx, fsy, int(cubic), flags, o.data_ptr(), w,
                                                _stream_handle(stream)))
     return o
+
+
+def gmhs_params(h: int, w: int, full_w: int, level: int = 1) -> dict:
+    """The periodic-structure repair's grid, radii, thresholds and workspace for an h x w network of frames padded
+    to full_w columns (fhc_gmhs_params)."""
+    p = GmhsPar()
+    _run("gmhs_params", _lib().fhc_gmhs_params(h, w, full_w, level, ctypes.byref(p)))
+    return {n: getattr(p, n) for n, _ in GmhsPar._fields_}
+
+
+def gmhs_workspace(h: int, w: int, full_w: int, level: int = 1, device="cuda"):
+    """A workspace for fhc_gmhs (uint8, 256-byte aligned as torch's allocator aligns)."""
+    import torch
+    return torch.empty(gmhs_params(h, w, full_w, level)["ws_bytes"], dtype=torch.uint8, device=device)
+
+
+def gmhs(a, b, flow, full_w: int, level: int = 1, ws=None, stream=None):
+    """The repair of flow channels c0 .. c0 + 3 (the E8 flow) in place, from the network pictures a, b (BGR). Returns
+    the workspace: the coefficients and decision maps are gmhs_results(ws, ...)."""
+    a, b, flow = _v(a), _v(b), _v(flow)
+    _, h, w, _ = a.shape
+    _, h8, w8, _ = flow.shape
+    if ws is None:
+        ws = gmhs_workspace(h, w, full_w, max(level, 1), a.t.device)
+    _run("gmhs", _lib().fhc_gmhs(_ref(a), _ref(b), h, w, _ref(flow), h8, w8, full_w, level, ws.data_ptr(),
+                                 ws.numel() * ws.element_size(), _stream_handle(stream)))
+    return ws
+
+
+def gmhs_results(ws, h: int, w: int, full_w: int, level: int = 1):
+    """(coefficients (4, 4), decision maps (5, hc, wc)) as float32 device views of a workspace after gmhs."""
+    p = gmhs_params(h, w, full_w, level)
+    import torch
+    f = ws.view(torch.float32)
+    off = p["maps_offset"] // 4
+    return f[:16].view(4, 4), f[off:off + 5 * p["hc"] * p["wc"]].view(5, p["hc"], p["wc"])

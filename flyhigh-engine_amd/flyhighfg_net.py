@@ -17,9 +17,13 @@ frames directly).
 
 Differences of launch structure from the reference (same arithmetic): the encoders' outputs are copied into their
 slices of the 279-channel concat (and f16b into the streaming state) by one copy launch; consecutive convs whose
-intermediate has no other reader run as fused pairs on the GPU when asked; and flow and vis share one buffer, so
-the fine loop's two adds are one. (Independent branches on a second stream, joined by events, made the captured frame
-slower, 241 against 225 us: the graph runtime did not overlap them.)
+intermediate has no other reader run as fused pairs on the GPU when asked; flow and vis share one buffer, so the fine
+loop's two adds are one, and that add is fine.out's residual (the planner's residual peephole, net/build.rs:222-237);
+the periodic-structure repair (gmhs.rs, level 1 by default as in the engine) ends pair() in 8 launches where the
+reference records 14. The program is one chain of launches: independent stretches (the pair's cost volume beside the
+encoders, the repair beside up.w and the FiLM branch) on side streams, joined by events, made the captured 1080p frame
+slower, by 16 to 43 us per fork (the graph's cross-stream dependencies cost more than the overlap returns at these
+kernel sizes).
 """
 from __future__ import annotations
 
@@ -176,10 +180,11 @@ class GpuBackend(ComposedChains):
         self.g = None
         self.record = None
 
-    def _go(self, label, fn, nbytes, flops=0, kind="op"):
+    def _go(self, label, fn, nbytes, flops=0, kind="op", kernels=1):
         fn()
         if self.record is not None:
-            self.record.append(dict(label=label, kind=kind, fn=fn, bytes=int(nbytes), flops=int(flops)))
+            self.record.append(dict(label=label, kind=kind, fn=fn, bytes=int(nbytes), flops=int(flops),
+                                    kernels=kernels))
 
     def zeros(self, n, h, w, cs):
         return self.torch.zeros((n, h, w, cs), dtype=self.torch.int16, device=self.dev)
@@ -356,6 +361,22 @@ class GpuBackend(ComposedChains):
                                              stream=self.stream),
                  4 * (frames.numel() + out_frames.numel()) + 2 * 10 * self._px(flow))
 
+    def gmhs(self, a: V, b: V, flow: V, full_w: int, level: int):
+        va, vb, vf = self._v(a), self._v(b), self._v(flow)
+        _, h, w, _ = va.shape
+        _, h8, w8, _ = vf.shape
+        key = ("gmhs", h, w, full_w, level)
+        if key not in self.plans:
+            self.plans[key] = self.fh.gmhs_workspace(h, w, full_w, level, self.dev)
+        ws = self.plans[key]
+        p = self.fh.gmhs_params(h, w, full_w, level)
+        cells = p["hc"] * p["wc"]
+        # algorithmic bytes: the flow read by 4 fit rounds and the cost maps, the two pictures' BGR, the maps written,
+        # box-filtered twice (read + written) and read by the select, the flow written
+        nbytes = 5 * 4 * 2 * h8 * w8 + 2 * 3 * 2 * h * w + 4 * cells * (5 + 2 * 5 + 2 * 5 + 3) + 4 * 2 * h8 * w8
+        self._go("gmhs (fit x4, cost, box, box + select)",
+                 lambda: self.fh.gmhs(va, vb, vf, full_w, level, ws=ws, stream=self.stream), nbytes, kernels=8)
+
     # the fused chains (one launch each) unless asked for the ops one by one
     def coarse_up(self, o: V, out: V, state: Optional[V], oh: int, ow: int, flow_scale: float):
         if not self.chains:
@@ -417,8 +438,11 @@ class FlyHighFG:
     engine's defaults, options.rs:306-327)."""
 
     def __init__(self, be, net_w: int = 864, net_h: int = 480, cubic: bool = True, render_flags: int = 0,
-                 frame: Optional[tuple] = None):
+                 frame: Optional[tuple] = None, repair: int = 1):
         self.be = be
+        # repair: the periodic-structure repair's level (gmhs.rs; 0 off, 1 the engine's default, options.rs:305,
+        # 2 aggressive), run on the E8 flow at the end of pair() (net/build.rs:640-660)
+        self.repair = repair
         # frame (w, h): the program starts from the host's two RGBA8 frames (``frames``, uploaded by the caller) and
         # ends with the generated RGBA8 frame (``rgba``), as the reference's Session does (net/session.rs:26-66).
         # The frames are padded to a multiple of 32; when that differs from the network size the network runs on
@@ -473,6 +497,8 @@ class FlyHighFG:
         self.rr, self.Rt = Z(1, qh, qw, 8), Z(1, qh, qw, 8)
         self.out = Z(1, net_h, net_w, 4)        # render_pix: the in-between picture at network size
         self.cubic, self.render_flags = cubic, render_flags
+        # the padded frame width the repair's windows scale with (the network's own without a frame)
+        self.full_w = self.wp if frame is not None else net_w
 
     def pair(self):
         """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1)."""
@@ -503,6 +529,8 @@ class FlyHighFG:
         # flow, vis += d: the add of fine.out's output as the conv's residual, written in place (the planner's
         # residual peephole, net/build.rs:222-237; f16(f32(d) + f32(fv)) either way)
         be.conv("fine.out", V(self.h), V(self.fv), V(self.fv))
+        if self.repair:  # the periodic-structure repair of the pair's flow, in place (gmhs.rs:149-206)
+            be.gmhs(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair)
 
     def mid(self, t: float, W: Optional[dict]):
         """mid(t): models/graph.json ops 44-82, render_pix included. With W None the FiLM vector of t must
@@ -652,5 +680,7 @@ class GraphProgram:
             elif op == "render":
                 be.render(ins[0], ins[1], ins[2], ins[3], ins[4], out, self.cubic, self.render_flags, s["fsx"],
                           s["fsy"])
+            elif op == "gmhs":
+                be.gmhs(ins[0], ins[1], out, s["full_w"], s["level"])
             else:
                 raise ValueError(f"plan step {op} has no backend call")

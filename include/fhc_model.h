@@ -50,13 +50,15 @@ int64_t fhc_model_weight(const fhc_model* model, const char* name, uint16_t* out
  *   k: the fine loop's repeat count (the session's K); frame_w x frame_h: the host's frames (padded to 32);
  *   net_w x net_h: the internal network size (padded to 32 here); equal to the padded frame, the graph's own
  *   render_pix renders; smaller, the frames are downscaled (antialiased) into the network and the render runs at
- *   the padded frame size with the flow scaled per axis (build.rs:615-620, :717-736).
+ *   the padded frame size with the flow scaled per axis (build.rs:615-620, :717-736);
+ *   repair: the periodic-structure repair's level (0 off, 1 safe, the reference's default, 2 aggressive): above 0
+ *   a "gmhs" step {level, full_w} rewrites the pair's plain 4-channel flow in place after the pair stage
+ *   (build.rs:640-660; fhc_gmhs of fhc_ops.h).
  * The walk keeps the reference's rules: slices, scales, neg and copy are views; an op whose outputs nobody reads is
  * skipped; a view a kernel needs plain is materialised first ("mat"); a conv followed by an add of its output
  * (read once) and a plain same-shape tensor takes the add as its residual (:222-237); blend_weights + mul + mul +
  * add is one blendmix (:417-450); the repeat body runs k times; the pair / mid boundary is mid_start
- * (model/graph.rs:182). The periodic-structure repair (gmhs.rs), static protection and the fast render path are not
- * part of this plan. Output:
+ * (model/graph.rs:182). Static protection and the fast render path are not part of this plan. Output:
  *   {"frame":[w,h], "padded":[wp,hp], "network":[iwp,ihp], "internal":b, "k":k, "mid_start":i,
  *    "buffers":[{"c","h","w","zeros","name"}...],
  *    "steps":[{"stage":"pair"|"mid", "op":..., "in":[view...], "out":view, ...}...]}
@@ -65,9 +67,10 @@ int64_t fhc_model_weight(const fhc_model* model, const char* name, uint16_t* out
  * stride, act, residual: view|null, name}; mat; concat; avgpool {k}; warp; binary {fn: 0 add, 1 mul}; unary {fn: 0
  * scale (mul_t, t-dependent: mode fwd|bwd), 1 clamp {lo, hi}, 2 affine_out}; luma; luma_grad; sad {radius};
  * film_mlp (host, t-dependent); film {g: view}; convex {weights: view}; blend; blendmix; render {fsx, fsy} (the
- * graph's render_pix, or the frame-size render of the internal mode). Bytes written or -1. */
+ * graph's render_pix, or the frame-size render of the internal mode); gmhs {level, full_w} (ins: A, B, the flow).
+ * Bytes written or -1. */
 int fhc_model_plan(const fhc_model* model, uint32_t k, uint32_t frame_w, uint32_t frame_h, uint32_t net_w,
-                   uint32_t net_h, char* json, size_t cap);
+                   uint32_t net_h, uint32_t repair, char* json, size_t cap);
 
 #ifdef __cplusplus
 }

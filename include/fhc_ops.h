@@ -197,6 +197,39 @@ int fhc_flow_vis_t(const fhc_tensor* fv, const fhc_tensor* dfilm, const fhc_tens
 int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rx,
                      uint32_t h, uint32_t w, float flow_out_scale, void* stream);
 
+
+/* GMHS, the periodic-structure repair of the pair's E8 flow (crates/flyhigh-engine/src/gmhs.rs:149-206, run at the
+ * end of the pair stage when the repair level is above 0, net/build.rs:640-660; the reference's default level is 1,
+ * options.rs:305). A robust affine motion is fitted to the flow (4 rounds of reweighted least squares,
+ * gm_fit_reduce.wgsl and gm_fit_solve.wgsl); on a grid of 2 x 2 network pixels the luma mismatch under the flow and
+ * under the affine motion, their displacement difference and the texture are mapped (gm_cost.wgsl) and box-filtered
+ * (gm_box.wgsl); the flow is rewritten in place with the affine motion where that explains the frames better, differs
+ * by a real jump and the texture is not flat (gm_select.wgsl). */
+typedef struct fhc_gmhs_par {
+    uint32_t hc, wc;        /* the cost grid, ceil(h / 2) x ceil(w / 2) */
+    uint32_t r_blk, r_dwin; /* box radii: the texture window (all 5 maps), then the decision window (maps 0-2) */
+    float s;                /* network pixels per half-frame pixel, w / (full_w / 2) */
+    float dmin;             /* the jump a cell must show (0 at level 2) */
+    float delta;            /* the fit's Huber scale */
+    float eps, tex;         /* cost margin 0, texture floor 0.015 */
+    uint64_t ws_bytes;      /* the workspace fhc_gmhs needs */
+    uint64_t maps_offset;   /* byte offset of the decision maps in it: f32 [5][hc][wc] (mismatch under the flow,
+                               under the affine motion, displacement difference, luma, luma^2) after a call; the
+                               affine coefficients, f32 [4][4] (a0, a1, a2, 0 per flow channel, a1 and a2 per unit
+                               of the coordinates normalised to [-1, 1]), are at byte 0 */
+} fhc_gmhs_par;
+
+/* The stage's parameters for an h x w network of frames padded to full_w columns (gm_steps, gmhs.rs:149-160).
+ * level 1 (safe) or 2 (aggressive, no jump gate). */
+int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc_gmhs_par* out);
+
+/* The repair, in place on channels 0-3 of `flow` (h8 x w8, the pair's plain E8 flow: x, y towards frame a, x, y
+ * towards frame b, in network pixels). a, b: the network pictures (h x w, BGR in channels 0-2, scale 1). ws: a
+ * 256-byte aligned workspace of fhc_gmhs_params' ws_bytes; nothing in it need be initialised. level 0 is a no-op.
+ * Eight launches on `stream`. Replaces gmhs::gm_steps and its 14 dispatches. */
+int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
+             uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

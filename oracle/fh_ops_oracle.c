@@ -400,3 +400,204 @@ void fho_rgba_out(const fho_view* in, uint32_t n, uint32_t hp, uint32_t wp, uint
                                                             (q8(rd(in, hp, wp, b, (int)y, (int)x, 0)) << 16) |
                                                             0xff000000u;
 }
+
+/* ---- GMHS: the periodic-structure repair of the pair's E8 flow (crates/flyhigh-engine/src/gmhs.rs) ------------ */
+
+#define GM_NWG 32u  /* gm_fit_reduce's workgroups (gmhs.rs:160) */
+#define GM_WG 256u  /* its workgroup size (gm_fit_reduce.wgsl:13) */
+
+/* gmhs.rs:149-160, :195 (DS = 2, gmhs.rs:129; eps 0, tex 0.015) */
+void fho_gm_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fho_gm_par* p) {
+    p->hc = (h + 1) / 2;
+    p->wc = (w + 1) / 2;
+    const float s = (float)w / ((float)full_w / 2.0f);
+    const float rb = roundf(20.0f * s / 2.0f), rw = roundf(32.0f * s / 2.0f);
+    p->s = s;
+    p->r_blk = rb < 1.0f ? 1u : (uint32_t)rb;
+    p->r_dwin = rw < 1.0f ? 1u : (uint32_t)rw;
+    p->dmin = level >= 2 ? 0.0f : 8.0f * s;
+    p->delta = 1.5f * s;
+    p->eps = 0.0f;
+    p->tex = 0.015f;
+}
+
+/* gm_fit_reduce.wgsl:15-44: GM_NWG workgroups of GM_WG lanes; lane t of workgroup g sums the elements g * 256 + t +
+ * k * 8192 in order, then the workgroup adds its lanes pairwise (t, t + off) for off = 128 .. 1 */
+static void gm_fit_reduce(const fho_view* flow, uint32_t h8, uint32_t w8, const float* coef, int use_w, float delta,
+                          float* part) {
+    const uint32_t n = h8 * w8, stride = GM_WG * GM_NWG;
+    const float sx = 2.0f / (float)(w8 - 1 > 1 ? w8 - 1 : 1), sy = 2.0f / (float)(h8 - 1 > 1 ? h8 - 1 : 1);
+    float sh[9][GM_WG];
+    for (uint32_t g = 0; g < GM_NWG; g++)
+        for (uint32_t c = 0; c < 4; c++) {
+            for (uint32_t t = 0; t < GM_WG; t++) {
+                float s[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+                for (uint32_t i = g * GM_WG + t; i < n; i += stride) {
+                    const uint32_t yy = i / w8, xx = i - yy * w8;
+                    const float x = -1.0f + sx * (float)xx, y = -1.0f + sy * (float)yy;
+                    const float f = rd(flow, h8, w8, 0, (int)yy, (int)xx, c);
+                    float w2 = 1.0f;
+                    if (use_w) {
+                        const float r = fabsf(f - (coef[c * 4] + coef[c * 4 + 1] * x + coef[c * 4 + 2] * y));
+                        w2 = delta / fmaxf(delta, r);
+                    }
+                    s[0] = s[0] + w2, s[1] = s[1] + w2 * x, s[2] = s[2] + w2 * y;
+                    s[3] = s[3] + w2 * x * x, s[4] = s[4] + w2 * x * y, s[5] = s[5] + w2 * y * y;
+                    s[6] = s[6] + w2 * f, s[7] = s[7] + w2 * x * f, s[8] = s[8] + w2 * y * f;
+                }
+                for (uint32_t k = 0; k < 9; k++) sh[k][t] = s[k];
+            }
+            for (uint32_t off = GM_WG / 2; off > 0; off >>= 1)
+                for (uint32_t t = 0; t < off; t++)
+                    for (uint32_t k = 0; k < 9; k++) sh[k][t] = sh[k][t] + sh[k][t + off];
+            for (uint32_t k = 0; k < 9; k++) part[(g * 4 + c) * 9 + k] = sh[k][0];
+        }
+}
+
+/* gm_fit_solve.wgsl:8-25: the partials summed in workgroup order, the 3 x 3 normal equations inverted by cofactors */
+static void gm_fit_solve(const float* part, float* coef) {
+    for (uint32_t c = 0; c < 4; c++) {
+        float s[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+        for (uint32_t g = 0; g < GM_NWG; g++)
+            for (uint32_t k = 0; k < 9; k++) s[k] = s[k] + part[(g * 4 + c) * 9 + k];
+        const float m00 = s[0] + 1e-6f, m01 = s[1], m02 = s[2], m11 = s[3] + 1e-6f, m12 = s[4], m22 = s[5] + 1e-6f;
+        const float det = m00 * (m11 * m22 - m12 * m12) - m01 * (m01 * m22 - m12 * m02) + m02 * (m01 * m12 - m11 * m02);
+        float* o = coef + c * 4;
+        if (fabsf(det) < 1e-12f) {
+            o[0] = s[6] / fmaxf(s[0], 1e-6f), o[1] = 0.0f, o[2] = 0.0f, o[3] = 0.0f;
+            continue;
+        }
+        const float i00 = (m11 * m22 - m12 * m12) / det, i01 = (m02 * m12 - m01 * m22) / det;
+        const float i02 = (m01 * m12 - m02 * m11) / det, i11 = (m00 * m22 - m02 * m02) / det;
+        const float i12 = (m01 * m02 - m00 * m12) / det, i22 = (m00 * m11 - m01 * m01) / det;
+        o[0] = i00 * s[6] + i01 * s[7] + i02 * s[8];
+        o[1] = i01 * s[6] + i11 * s[7] + i12 * s[8];
+        o[2] = i02 * s[6] + i12 * s[7] + i22 * s[8];
+        o[3] = 0.0f;
+    }
+}
+
+/* the fit of gmhs.rs:161-171: `iters` rounds of reduce + solve, the first unweighted */
+void fho_gm_fit(const fho_view* flow, uint32_t h8, uint32_t w8, float delta, uint32_t iters, float* coef) {
+    float part[GM_NWG * 4 * 9];
+    for (uint32_t k = 0; k < 16; k++) coef[k] = 0.0f;
+    for (uint32_t it = 0; it < iters; it++) {
+        gm_fit_reduce(flow, h8, w8, coef, it > 0, delta, part);
+        gm_fit_solve(part, coef);
+    }
+}
+
+/* gm_cost.wgsl:14-17: luma of a BGR view, no read scale */
+static float gm_lum(const fho_view* v, uint32_t h, uint32_t w, int y, int x) {
+    return 0.299f * rd(v, h, w, 0, y, x, 2) + 0.587f * rd(v, h, w, 0, y, x, 1) + 0.114f * rd(v, h, w, 0, y, x, 0);
+}
+
+/* gm_cost.wgsl:23-29: bilinear luma, coordinates clamped */
+static float gm_samp(const fho_view* v, uint32_t h, uint32_t w, float gx, float gy) {
+    const int x0 = (int)floorf(gx), y0 = (int)floorf(gy);
+    const float ax = gx - (float)x0, ay = gy - (float)y0;
+    const int x0c = clampi(x0, 0, (int)w - 1), x1c = clampi(x0 + 1, 0, (int)w - 1);
+    const int y0c = clampi(y0, 0, (int)h - 1), y1c = clampi(y0 + 1, 0, (int)h - 1);
+    const float top = gm_lum(v, h, w, y0c, x0c) * (1.0f - ax) + gm_lum(v, h, w, y0c, x1c) * ax;
+    const float bot = gm_lum(v, h, w, y1c, x0c) * (1.0f - ax) + gm_lum(v, h, w, y1c, x1c) * ax;
+    return top * (1.0f - ay) + bot * ay;
+}
+
+/* gm_cost.wgsl:38-48: the E8 flow at a network position, bilinear, align_corners false */
+static float gm_flow8(const fho_view* fl, uint32_t h8, uint32_t w8, uint32_t h, uint32_t w, uint32_t c, float rx,
+                      float ry) {
+    const float ix = (rx + 0.5f) * (float)w8 / (float)w - 0.5f, iy = (ry + 0.5f) * (float)h8 / (float)h - 0.5f;
+    const int x0 = (int)floorf(ix), y0 = (int)floorf(iy);
+    const float fx = ix - (float)x0, fy = iy - (float)y0;
+    const int x0c = clampi(x0, 0, (int)w8 - 1), x1c = clampi(x0 + 1, 0, (int)w8 - 1);
+    const int y0c = clampi(y0, 0, (int)h8 - 1), y1c = clampi(y0 + 1, 0, (int)h8 - 1);
+    const float top = rd(fl, h8, w8, 0, y0c, x0c, c) * (1.0f - fx) + rd(fl, h8, w8, 0, y0c, x1c, c) * fx;
+    const float bot = rd(fl, h8, w8, 0, y1c, x0c, c) * (1.0f - fx) + rd(fl, h8, w8, 0, y1c, x1c, c) * fx;
+    return top * (1.0f - fy) + bot * fy;
+}
+
+/* gm_cost.wgsl:49-53: the affine hypothesis at a network position */
+static float gm_aff(const float* coef, uint32_t c, uint32_t h8, uint32_t w8, uint32_t h, uint32_t w, float rx,
+                    float ry) {
+    const float ix = (rx + 0.5f) * (float)w8 / (float)w - 0.5f, iy = (ry + 0.5f) * (float)h8 / (float)h - 0.5f;
+    const float xn = -1.0f + 2.0f * ix / (float)(w8 - 1 > 1 ? w8 - 1 : 1);
+    const float yn = -1.0f + 2.0f * iy / (float)(h8 - 1 > 1 ? h8 - 1 : 1);
+    return coef[c * 4] + coef[c * 4 + 1] * xn + coef[c * 4 + 2] * yn;
+}
+
+/* gm_cost.wgsl:55-75, channels 0-4 (channel 5, the plain frame change, feeds cadence smoothing only) */
+void fho_gm_cost(const fho_view* a, const fho_view* b, uint32_t h, uint32_t w, const fho_view* flow, uint32_t h8,
+                 uint32_t w8, const float* coef, uint32_t hc, uint32_t wc, float* maps) {
+    const size_t n = (size_t)hc * wc;
+    const float ds = 2.0f;
+    for (uint32_t y = 0; y < hc; y++)
+        for (uint32_t x = 0; x < wc; x++) {
+            const size_t i = (size_t)y * wc + x;
+            const float rx = ((float)x + 0.5f) * ds - 0.5f, ry = ((float)y + 0.5f) * ds - 0.5f;
+            const float f0x = gm_flow8(flow, h8, w8, h, w, 0, rx, ry), f0y = gm_flow8(flow, h8, w8, h, w, 1, rx, ry);
+            const float f1x = gm_flow8(flow, h8, w8, h, w, 2, rx, ry), f1y = gm_flow8(flow, h8, w8, h, w, 3, rx, ry);
+            const float cm = fabsf(gm_samp(a, h, w, rx + f0x, ry + f0y) - gm_samp(b, h, w, rx + f1x, ry + f1y));
+            const float g0x = gm_aff(coef, 0, h8, w8, h, w, rx, ry), g0y = gm_aff(coef, 1, h8, w8, h, w, rx, ry);
+            const float g1x = gm_aff(coef, 2, h8, w8, h, w, rx, ry), g1y = gm_aff(coef, 3, h8, w8, h, w, rx, ry);
+            const float wm = (float)w - 1.0f, hm = (float)h - 1.0f;
+            const float ax = rx + g0x, ay = ry + g0y, bx = rx + g1x, by = ry + g1y;
+            const int inside = ax >= 0.0f && ax <= wm && ay >= 0.0f && ay <= hm && bx >= 0.0f && bx <= wm &&
+                               by >= 0.0f && by <= hm;
+            const float ca = inside ? fabsf(gm_samp(a, h, w, ax, ay) - gm_samp(b, h, w, bx, by)) : cm;
+            const float l = gm_samp(a, h, w, rx, ry);
+            const float dvx = (g1x - g0x) - (f1x - f0x), dvy = (g1y - g0y) - (f1y - f0y);
+            maps[i] = cm, maps[n + i] = ca, maps[2 * n + i] = sqrtf(dvx * dvx + dvy * dvy);
+            maps[3 * n + i] = l, maps[4 * n + i] = l * l;
+        }
+}
+
+/* gm_box.wgsl:8-25: box mean of radius r along x (vert 0) or y, edges replicated, over c planes [c][h][w] */
+void fho_gm_box(const float* src, float* dst, uint32_t c, uint32_t h, uint32_t w, uint32_t r, int vert) {
+    for (uint32_t ch = 0; ch < c; ch++)
+        for (uint32_t y = 0; y < h; y++)
+            for (uint32_t x = 0; x < w; x++) {
+                const size_t plane = (size_t)ch * h * w;
+                float acc = 0.0f;
+                for (int d = -(int)r; d <= (int)r; d++) {
+                    const size_t at = vert ? (size_t)clampi((int)y + d, 0, (int)h - 1) * w + x
+                                           : (size_t)y * w + (size_t)clampi((int)x + d, 0, (int)w - 1);
+                    acc = acc + src[plane + at];
+                }
+                dst[plane + (size_t)y * w + x] = acc / (float)(2 * r + 1);
+            }
+}
+
+/* gm_select.wgsl:14-27: the cells that adopt the affine hypothesis, rewritten in the E8 flow */
+void fho_gm_select(const float* maps, const float* coef, const fho_view* flow, uint32_t h8, uint32_t w8, uint32_t hc,
+                   uint32_t wc, float eps, float dmin, float tex) {
+    const size_t n = (size_t)hc * wc;
+    for (uint32_t i = 0; i < h8; i++)
+        for (uint32_t j = 0; j < w8; j++) {
+            const int x = clampi((int)floorf(((float)j + 0.5f) * (float)wc / (float)w8), 0, (int)wc - 1);
+            const int y = clampi((int)floorf(((float)i + 0.5f) * (float)hc / (float)h8), 0, (int)hc - 1);
+            const size_t idx = (size_t)y * wc + (size_t)x;
+            const float cm = maps[idx], ca = maps[n + idx], dv = maps[2 * n + idx];
+            const float lm = maps[3 * n + idx], l2 = maps[4 * n + idx];
+            const float sd = sqrtf(fmaxf(l2 - lm * lm, 0.0f));
+            if (ca + eps < cm && dv > dmin && sd > tex) {
+                const float xn = -1.0f + 2.0f * (float)j / (float)(w8 - 1 > 1 ? w8 - 1 : 1);
+                const float yn = -1.0f + 2.0f * (float)i / (float)(h8 - 1 > 1 ? h8 - 1 : 1);
+                for (uint32_t c = 0; c < 4; c++) wr(flow, h8, w8, 0, i, j, c, coef[c * 4] + coef[c * 4 + 1] * xn + coef[c * 4 + 2] * yn);
+            }
+        }
+}
+
+/* gm_steps (gmhs.rs:149-206): fit, cost maps, the two box windows (5 maps, then the costs and the displacement
+ * difference), select */
+void fho_gmhs(const fho_view* a, const fho_view* b, uint32_t h, uint32_t w, const fho_view* flow, uint32_t h8,
+              uint32_t w8, uint32_t full_w, uint32_t level, float* coef, float* maps, float* tmp) {
+    fho_gm_par p;
+    fho_gm_params(h, w, full_w, level, &p);
+    fho_gm_fit(flow, h8, w8, p.delta, 4, coef);
+    fho_gm_cost(a, b, h, w, flow, h8, w8, coef, p.hc, p.wc, maps);
+    fho_gm_box(maps, tmp, 5, p.hc, p.wc, p.r_blk, 0);
+    fho_gm_box(tmp, maps, 5, p.hc, p.wc, p.r_blk, 1);
+    fho_gm_box(maps, tmp, 3, p.hc, p.wc, p.r_dwin, 0);
+    fho_gm_box(tmp, maps, 3, p.hc, p.wc, p.r_dwin, 1);
+    fho_gm_select(maps, coef, flow, h8, w8, p.hc, p.wc, p.eps, p.dmin, p.tex);
+}

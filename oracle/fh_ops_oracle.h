@@ -81,6 +81,31 @@ void fho_rgba_in(const uint32_t* rgba, uint32_t n, uint32_t w, uint32_t h, uint3
 void fho_rgba_out(const fho_view* in, uint32_t n, uint32_t hp, uint32_t wp, uint32_t* rgba, uint32_t w, uint32_t h,
                   uint32_t pitch, uint64_t fstride);
 
+
+/* GMHS, the periodic-structure repair of the pair's E8 flow (crates/flyhigh-engine/src/gmhs.rs:149-206): a robust
+ * affine fit of the 4 flow channels, photometric cost maps of the model flow and the affine hypothesis on a grid of
+ * 2 x 2 network pixels, two box windows, and a select that rewrites the flow where the hypothesis wins. Maps are
+ * planar f32 [5][hc][wc]; coef is [4][4] (a0, a1, a2, 0 per flow channel). */
+typedef struct fho_gm_par {
+    uint32_t hc, wc, r_blk, r_dwin;
+    float s, dmin, delta, eps, tex;
+} fho_gm_par;
+/* gmhs.rs:149-160: the grid and windows for an h x w network of a frame padded to full_w columns, repair level */
+void fho_gm_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fho_gm_par* p);
+/* `iters` rounds of gm_fit_reduce.wgsl (32 workgroups) + gm_fit_solve.wgsl on the E8 flow (channels c0 .. c0 + 3) */
+void fho_gm_fit(const fho_view* flow, uint32_t h8, uint32_t w8, float delta, uint32_t iters, float* coef);
+/* gm_cost.wgsl:55-75, maps 0-4 (a, b: the network pictures, BGR) */
+void fho_gm_cost(const fho_view* a, const fho_view* b, uint32_t h, uint32_t w, const fho_view* flow, uint32_t h8,
+                 uint32_t w8, const float* coef, uint32_t hc, uint32_t wc, float* maps);
+/* gm_box.wgsl: box_h (vert 0) or box_v of radius r over c planes */
+void fho_gm_box(const float* src, float* dst, uint32_t c, uint32_t h, uint32_t w, uint32_t r, int vert);
+/* gm_select.wgsl:14-27, the flow rewritten in place */
+void fho_gm_select(const float* maps, const float* coef, const fho_view* flow, uint32_t h8, uint32_t w8, uint32_t hc,
+                   uint32_t wc, float eps, float dmin, float tex);
+/* the whole stage (gmhs.rs:149-206); maps and tmp hold 5 * hc * wc floats, maps ends as the decision maps */
+void fho_gmhs(const fho_view* a, const fho_view* b, uint32_t h, uint32_t w, const fho_view* flow, uint32_t h8,
+              uint32_t w8, uint32_t full_w, uint32_t level, float* coef, float* maps, float* tmp);
+
 #ifdef __cplusplus
 }
 #endif

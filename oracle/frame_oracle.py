@@ -107,6 +107,10 @@ class CpuBackend(ComposedChains):
                                         fsy=flow.scale if fsy is None else fsy,
                                         vis_c0=vis.c0, vis_scale=vis.scale, rt_c0=rt.c0))
 
+    def gmhs(self, a, b, flow, full_w, level):
+        out, _, _ = oracle.gmhs(a.buf, b.buf, flow.buf, full_w, level, a_c0=a.c0, b_c0=b.c0, flow_c0=flow.c0)
+        flow.buf[...] = out
+
     def rgba_in(self, frames, out, hp, wp):
         self._put(out, 3, oracle.rgba_in(frames, hp, wp))
 

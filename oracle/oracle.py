@@ -127,6 +127,11 @@ class FhoView(ctypes.Structure):
     _fields_ = [("p", ctypes.c_void_p), ("cs", ctypes.c_uint32), ("c0", ctypes.c_uint32), ("scale", ctypes.c_float)]
 
 
+class FhoGmPar(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("hc", "wc", "r_blk", "r_dwin")] + [
+        (n, ctypes.c_float) for n in ("s", "dmin", "delta", "eps", "tex")]
+
+
 def _view(a, c0=0, scale=1.0):
     assert a.dtype == np.uint16 and a.ndim == 4 and a.flags.c_contiguous
     return ctypes.byref(FhoView(a.ctypes.data, a.shape[3], c0, scale))
@@ -152,6 +157,13 @@ def _ops_lib():
             "fho_render": [V, V, V, V, V, V, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U],
             "fho_rgba_in": [ctypes.c_void_p, U, U, U, U, ctypes.c_uint64, V, U, U],
             "fho_rgba_out": [V, U, U, U, ctypes.c_void_p, U, U, U, ctypes.c_uint64],
+            "fho_gm_params": [U, U, U, U, ctypes.POINTER(FhoGmPar)],
+            "fho_gm_fit": [V, U, U, ctypes.c_float, U, ctypes.c_void_p],
+            "fho_gm_cost": [V, V, U, U, V, U, U, ctypes.c_void_p, U, U, ctypes.c_void_p],
+            "fho_gm_box": [ctypes.c_void_p, ctypes.c_void_p, U, U, U, U, I],
+            "fho_gm_select": [ctypes.c_void_p, ctypes.c_void_p, V, U, U, U, U, ctypes.c_float, ctypes.c_float,
+                              ctypes.c_float],
+            "fho_gmhs": [V, V, U, U, V, U, U, U, U, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -279,3 +291,65 @@ def rgba_out(x, h, w, c0=0):
     out = np.zeros((n, h, w), np.uint32)
     _ops_lib().fho_rgba_out(_view(x, c0), n, hp, wp, out.ctypes.data, w, h, w, h * w)
     return out
+
+
+# ---- GMHS (fh_ops_oracle.c, gmhs.rs): maps are float32 (5, hc, wc), coef float32 (4, 4) ----------------------------
+
+def gm_params(h, w, full_w, level=1):
+    """The GMHS grid and windows (gmhs.rs:149-160) as a dict."""
+    p = FhoGmPar()
+    _ops_lib().fho_gm_params(h, w, full_w, level, ctypes.byref(p))
+    return {n: getattr(p, n) for n, _ in FhoGmPar._fields_}
+
+
+def gm_fit(flow, delta, iters=4, c0=0):
+    """The robust affine fit of flow channels c0 .. c0 + 3 of a (1, h8, w8, cs) E8 flow; (4, 4) coefficients."""
+    _, h8, w8, _ = flow.shape
+    coef = np.zeros((4, 4), np.float32)
+    _ops_lib().fho_gm_fit(_view(flow, c0), h8, w8, float(delta), iters, coef.ctypes.data)
+    return coef
+
+
+def gm_cost(a, b, flow, coef, hc, wc, a_c0=0, b_c0=0, flow_c0=0):
+    """The 5 cost maps (5, hc, wc) of network pictures a, b (1, h, w, cs) under the E8 flow and the affine fit."""
+    _, h, w, _ = a.shape
+    _, h8, w8, _ = flow.shape
+    maps = np.zeros((5, hc, wc), np.float32)
+    coef = np.ascontiguousarray(coef, np.float32)
+    _ops_lib().fho_gm_cost(_view(a, a_c0), _view(b, b_c0), h, w, _view(flow, flow_c0), h8, w8, coef.ctypes.data,
+                           hc, wc, maps.ctypes.data)
+    return maps
+
+
+def gm_box(src, r, vert):
+    """gm_box.wgsl over the planes of src (c, h, w) float32."""
+    src = np.ascontiguousarray(src, np.float32)
+    c, h, w = src.shape
+    dst = np.zeros_like(src)
+    _ops_lib().fho_gm_box(src.ctypes.data, dst.ctypes.data, c, h, w, r, int(vert))
+    return dst
+
+
+def gm_select(maps, coef, flow, eps, dmin, tex, c0=0):
+    """gm_select.wgsl: a copy of flow (1, h8, w8, cs) with the selected cells rewritten."""
+    out = np.ascontiguousarray(flow, np.uint16).copy()
+    _, h8, w8, _ = out.shape
+    maps = np.ascontiguousarray(maps, np.float32)
+    coef = np.ascontiguousarray(coef, np.float32)
+    _ops_lib().fho_gm_select(maps.ctypes.data, coef.ctypes.data, _view(out, c0), h8, w8, maps.shape[1],
+                             maps.shape[2], eps, dmin, tex)
+    return out
+
+
+def gmhs(a, b, flow, full_w, level=1, a_c0=0, b_c0=0, flow_c0=0):
+    """The whole repair (gmhs.rs:149-206): (repaired flow copy, coef (4, 4), decision maps (5, hc, wc))."""
+    _, h, w, _ = a.shape
+    out = np.ascontiguousarray(flow, np.uint16).copy()
+    _, h8, w8, _ = out.shape
+    p = gm_params(h, w, full_w, level)
+    coef = np.zeros((4, 4), np.float32)
+    maps = np.zeros((5, p["hc"], p["wc"]), np.float32)
+    tmp = np.zeros_like(maps)
+    _ops_lib().fho_gmhs(_view(a, a_c0), _view(b, b_c0), h, w, _view(out, flow_c0), h8, w8, full_w, level,
+                        coef.ctypes.data, maps.ctypes.data, tmp.ctypes.data)
+    return out, coef, maps

@@ -6,7 +6,8 @@ one record per conv the planner recorded, holding the conv's inputs (cin, cout, 
 residual add was fused) and the dispatches the reference recorded for it (pipeline, grid, packed-weight bytes,
 parameter words). The planner restatement (fhc_ref_conv_steps) must reproduce the dispatches from the inputs.
 Also writes ref_plan_steps.json: every plan's whole step sequence (pipeline names and grids, the mid stage's first
-step), against which the static plan of fhc_model_plan is checked step by step.
+step, and the parameter words of the periodic-structure repair's gm_* steps), against which the static plan of
+fhc_model_plan is checked step by step.
 
 Line format of the reference files (ops/step.rs:51-88): "idx pipeline (gx,gy,gz) [bindings] <u32 words as hex>".
 Run in the build container only (the reference is not present on the GPU box):
@@ -108,7 +109,10 @@ def main():
                 mid = len(steps)
             m = LINE.match(ln)
             if m:
-                steps.append([m.group(2), [int(m.group(3)), int(m.group(4)), int(m.group(5))]])
+                step = [m.group(2), [int(m.group(3)), int(m.group(4)), int(m.group(5))]]
+                if m.group(2).startswith("gm_"):  # the repair's parameter words (FitP, CostP, BoxP, SelP)
+                    step.append([int(v, 16) for v in m.group(7).split()])
+                steps.append(step)
         plans[base] = dict(header=header, mid=mid, steps=steps)
     with open(OUT_STEPS, "w") as f:
         json.dump(plans, f, separators=(",", ":"))

@@ -6,7 +6,11 @@ internal-size mode. On the GPU: the same program through libfhconv.so (fused con
 frame input and render) against the oracle composition with the same weights and inputs: per network tensor
 |diff| <= 1e-2 * max|ref| (the conv path's bar; the ops themselves are bit-exact or within an ulp, and the convs'
 f32 summation order differs from the oracle's, so differences propagate through ~20 layers), and for the generated
-8-bit frame the same bar in bytes (1e-2 * 255) plus one quantization step.
+8-bit frame the same bar in bytes (1e-2 * 255) plus one quantization step. These whole-program comparisons run with
+the periodic-structure repair off: its select is a threshold decision (a cell takes the affine motion or keeps its
+flow), so a flow within the bar on both sides can be rewritten on one side only, moving that cell by the whole
+correction. The repair is pinned instead bit for bit on the GPU's own pair-stage flow and pictures, in the 1080p
+frame (test_gpu_1080p_frame_repair_on_the_gpus_own_flow), besides its own parity tests (test_gmhs_gpu.py).
 """
 import numpy as np
 import pytest
@@ -34,8 +38,8 @@ def frames(w, h, dx=12, dy=0):
     return np.stack([net.procedural_frame(w, h), net.procedural_frame(w, h, dx, dy)])
 
 
-def run(be, W, net_w, net_h, ab, t=0.5):
-    f = net.FlyHighFG(be, net_w, net_h)
+def run(be, W, net_w, net_h, ab, t=0.5, repair=0):
+    f = net.FlyHighFG(be, net_w, net_h, repair=repair)
     if isinstance(f.AB, np.ndarray):
         f.AB[...] = ab
     else:
@@ -45,9 +49,9 @@ def run(be, W, net_w, net_h, ab, t=0.5):
     return f
 
 
-def run_frames(be, W, net_w, net_h, fr, t=0.5):
+def run_frames(be, W, net_w, net_h, fr, t=0.5, repair=0):
     h, w = fr.shape[1:]
-    f = net.FlyHighFG(be, net_w, net_h, frame=(w, h))
+    f = net.FlyHighFG(be, net_w, net_h, frame=(w, h), repair=repair)
     be.upload_frames(f.frames, fr)
     f.pair()
     f.mid(t, W)
@@ -134,6 +138,31 @@ def test_gpu_1080p_frame_from_rgba_matches_the_oracle_composition():
     torch.cuda.synchronize()
     assert got.internal and (got.wp, got.hp) == (1920, 1088)
     _check_frame(gb, got, ref)
+
+
+@pytest.mark.gpu
+def test_gpu_1080p_frame_repair_on_the_gpus_own_flow():
+    """The repair as the 1080p frame runs it (the network pictures and the E8 flow views, the padded frame width
+    1920, level 1, on the program's stream): after the GPU's pair(), the stage rewrites the flow exactly as the
+    oracle's stage does from the same pictures and flow."""
+    import torch
+    import oracle
+    print("frame 1920x1080 repair", flush=True)
+    W = net.make_weights(5)
+    fr = frames(1920, 1080)
+    gb = net.GpuBackend(W, stream=torch.cuda.current_stream())
+    f = net.FlyHighFG(gb, 864, 480, frame=(1920, 1080), repair=0)
+    gb.upload_frames(f.frames, fr)
+    f.pair()
+    torch.cuda.synchronize()
+    ab, before = gb.host(f.AB), gb.host(f.fv)
+    gb.gmhs(net.V(gb.image(f.AB, 0)), net.V(gb.image(f.AB, 1)), net.V(f.fv), f.full_w, 1)
+    after = gb.host(f.fv)
+    want, _, _ = oracle.gmhs(ab[0:1], ab[1:2], before, f.full_w, 1)
+    print(f"  cells repaired: {int((want != before).any(-1).sum())} of {before.shape[1] * before.shape[2]}",
+          flush=True)
+    assert f.full_w == 1920
+    assert np.array_equal(after, want)
 
 
 @pytest.mark.gpu

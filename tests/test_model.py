@@ -14,6 +14,7 @@ import pytest
 
 from fhtest import fhconv
 import fhmodel
+import fhops
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 MODEL_DIR = "/root/reference/models"
@@ -126,6 +127,16 @@ def dispatches(plan, coop, f32):
             out.append(({"luma_grad": "grad"}.get(op, op), wg(w, h, 1), s["stage"]))
         elif op == "sad":
             out.append(("sad", wg(w, h, (2 * s["radius"] + 1) ** 2), s["stage"]))
+        elif op == "gmhs":  # gm_steps' 14 dispatches (gmhs.rs:161-198)
+            ah, aw = dims(s["in"][0])
+            par = fhops.gmhs_params(ah, aw, s["full_w"], s["level"])
+            cg = [-(-par["wc"] // 8), -(-par["hc"] // 8)]
+            for _ in range(4):
+                out += [("gm_fit_reduce", [32, 1, 1], s["stage"]), ("gm_fit_solve", [1, 1, 1], s["stage"])]
+            out.append(("gm_cost", cg + [1], s["stage"]))
+            for pipe, c in (("gm_box_h", 5), ("gm_box_v", 5), ("gm_box_h", 3), ("gm_box_v", 3)):
+                out.append((pipe, cg + [c], s["stage"]))
+            out.append(("gm_select", wg(w, h, 1), s["stage"]))
         else:  # interp, avgpool, warp, binary, unary, film, convex: one lane per output element of 8 x 8 tiles
             out.append((op, wg(w, h, o["c"]), s["stage"]))
     return out
@@ -150,8 +161,9 @@ def golden_configs():
 def test_static_plan_reproduces_the_golden_plan(model, name):
     """Every dispatch of the reference's golden plan (crates/flyhigh-engine/tests/golden/<name>.txt), in order and
     with its grid, from the static plan: the walk's order, shapes, views and their materialisation, the dead-op
-    rule, both peepholes, the repeat and the internal-size mode. The periodic-structure repair's dispatches (gm_*,
-    sessions with repair >= 1) and the session's frame steps are left out on the golden side."""
+    rule, both peepholes, the repeat, the internal-size mode and the periodic-structure repair's place and grids
+    (its parameter words are checked in test_gmhs_oracle.py). The session's frame steps are left out on the golden
+    side."""
     p = json.load(open(STEPS))[name]
     hdr = p["header"]
     m = re.match(r"\S+ (\d+)x(\d+) k=(\d+)(?: internal=(\d+)x(\d+))?", hdr)
@@ -163,13 +175,14 @@ def test_static_plan_reproduces_the_golden_plan(model, name):
         fw, fh, k = int(mm.group(1)), int(mm.group(2)), int(mm.group(3))
         nw, nh = fw, fh
     cls = name.rsplit(".", 1)[1]
-    plan = model.plan(k, (fw, fh), (nw, nh))
+    rm = re.search(r"repair=(\d)", hdr)
+    plan = model.plan(k, (fw, fh), (nw, nh), repair=int(rm.group(1)) if rm else 1)
     got = dispatches(plan, coop=cls.startswith("tc"), f32=cls.endswith("f32"))
-    want = [(s[0], s[1]) for s in p["steps"] if s[0] not in SESSION and not s[0].startswith("gm_")]
+    want = [(s[0], s[1]) for s in p["steps"] if s[0] not in SESSION]
     assert [(n, g) for n, g, _ in got] == want
     # the pair / mid boundary (mid_start, model/graph.rs:182) falls where the golden plan's "# mid" does
     if p["mid"] is not None:
-        pre = [s for s in p["steps"][:p["mid"]] if s[0] not in SESSION and not s[0].startswith("gm_")]
+        pre = [s for s in p["steps"][:p["mid"]] if s[0] not in SESSION]
         assert [st for _, _, st in got].index("mid") == len(pre)
 
 
