@@ -1,7 +1,10 @@
 // The model files and the static plan (include/fhc_model.h): a small JSON reader, the loader with the reference's
 // validation, and the graph walk into plan steps. Host code only.
+#include <hip/hip_runtime_api.h>
+
 #include <cmath>
 #include <cstring>
+#include <set>
 #include <fstream>
 #include <map>
 #include <memory>
@@ -11,6 +14,7 @@
 #include <vector>
 
 #include "common.h"
+#include "fhc_conv.h"
 #include "fhc_model.h"
 
 namespace fhc {
@@ -369,10 +373,18 @@ struct View {
     }
 };
 
+// one conv of the plan, as the reference's discovery build records it (ConvShape, ops/conv/autotune.rs:153-164)
+struct ConvUse {
+    std::string w, b, s;                  // weight, bias and slope tensors (s empty without an activation)
+    uint32_t cin, cout, h, wd, stride;    // h, wd: the input size
+    bool act, res;
+};
+
 struct Planner {
     const fhc_model& m;
     uint32_t k, hs, ws;  // the repeat count and the network size (interpolate's "HW")
     std::vector<Buf> bufs;
+    std::vector<ConvUse> convs;
     std::map<std::string, View> env;
     std::map<std::string, size_t> uses;
     std::vector<std::string> steps;
@@ -440,6 +452,7 @@ struct Planner {
                             ",\"act\":" + std::to_string(act) + ",\"residual\":" + (res ? vjson(*res) : "null") +
                             ",\"name\":" + jstr(out_name);
         step("conv", ins, y, extra);
+        convs.push_back(ConvUse{w, b, s, cin, cout, x.h, x.w, stride, act != 0, res != nullptr});
         return y;
     }
 
@@ -634,12 +647,12 @@ size_t mid_start(const Json& ops, size_t n) {
 }
 
 std::string plan_json(const fhc_model& m, uint32_t k, uint32_t fw, uint32_t fh, uint32_t nw, uint32_t nh,
-                      uint32_t repair) {
+                      uint32_t repair, std::vector<ConvUse>* convs = nullptr) {
     const uint32_t hp = (fh + 31) / 32 * 32, wp = (fw + 31) / 32 * 32;
     const uint32_t ihp = (nh + 31) / 32 * 32, iwp = (nw + 31) / 32 * 32;
     if (ihp > hp || iwp > wp) throw std::runtime_error("the network size exceeds the frame");
     const bool internal = ihp != hp || iwp != wp;
-    Planner p{m, k, ihp, iwp, {}, {}, {}, {}, "pair"};
+    Planner p{m, k, ihp, iwp, {}, {}, {}, {}, {}, "pair"};
     p.count_uses(m.ops);
     p.uses["t"] = 0;
     // the Session's inputs (net/session.rs:56-60): both frames through rgba_in at the padded size
@@ -699,6 +712,7 @@ std::string plan_json(const fhc_model& m, uint32_t k, uint32_t fw, uint32_t fh, 
         render = it->second;
     }
     p.step("rgba_out", {render}, render);  // net/session.rs:63: the crop to the frame
+    if (convs) *convs = p.convs;
     std::ostringstream o;
     o << "{\"frame\":[" << fw << "," << fh << "],\"padded\":[" << wp << "," << hp << "],\"network\":[" << iwp << ","
       << ihp << "],\"internal\":" << (internal ? "true" : "false") << ",\"k\":" << k << ",\"mid_start\":" << ms
@@ -818,5 +832,126 @@ extern "C" int fhc_model_plan(const fhc_model* m, uint32_t k, uint32_t frame_w, 
             return fail(-1, "fhc_model_plan: %s", e.what());
         }
         return write_string(s, json, cap);
+    });
+}
+
+namespace fhc {
+namespace {
+
+struct ShapeKey {
+    uint32_t v[7];
+    bool operator<(const ShapeKey& o) const { return std::memcmp(v, o.v, sizeof v) < 0; }
+};
+
+// the plan's distinct conv shapes at batch n, in plan order, with the first use of each
+std::vector<std::pair<ShapeKey, ConvUse>> conv_shapes(const fhc_model& m, uint32_t k, uint32_t fw, uint32_t fh,
+                                                      uint32_t nw, uint32_t nh, uint32_t n) {
+    std::vector<ConvUse> convs;
+    plan_json(m, k, fw, fh, nw, nh, 0, &convs);
+    std::vector<std::pair<ShapeKey, ConvUse>> out;
+    std::set<ShapeKey> seen;
+    for (const ConvUse& c : convs) {
+        const ShapeKey key{{c.cin, c.cout, c.h, c.wd, c.stride, n, 3}};
+        if (seen.insert(key).second) out.emplace_back(key, c);
+    }
+    return out;
+}
+
+int plan_args(const fhc_model* m, uint32_t k, uint32_t fw, uint32_t fh, uint32_t nw, uint32_t nh, const char* what) {
+    if (!m) return fail(-1, "%s: NULL model", what);
+    if (!fw || !fh || !nw || !nh || fw > 16384 || fh > 16384)
+        return fail(-1, "%s: bad sizes (frame %u x %u, network %u x %u)", what, fw, fh, nw, nh);
+    if (k == 0 || k > 16) return fail(-1, "%s: k must be 1..16", what);
+    return 0;
+}
+
+// seeded f16 values of magnitude 2^-5 .. 2^-1 with random signs and mantissas (finite, no conversion needed)
+void seeded_f16(std::vector<uint16_t>& v, uint32_t seed) {
+    uint32_t x = seed * 2654435761u + 12345u;
+    for (uint16_t& h : v) {
+        x = x * 1664525u + 1013904223u;
+        h = (uint16_t)(((x >> 31) << 15) | ((10u + (x >> 24) % 5u) << 10) | ((x >> 8) & 0x3ffu));
+    }
+}
+
+std::vector<uint16_t> weight_bits(const fhc_model& m, const std::string& name) {
+    const auto& t = m.tensors.at(name);
+    std::vector<uint16_t> out(t.count);
+    const uint8_t* p = m.blob.data() + t.offset * 2;
+    for (uint64_t i = 0; i < t.count; i++) out[i] = (uint16_t)(p[2 * i] | (p[2 * i + 1] << 8));
+    return out;
+}
+
+}  // namespace
+}  // namespace fhc
+
+extern "C" int fhc_model_conv_shapes(const fhc_model* m, uint32_t k, uint32_t frame_w, uint32_t frame_h,
+                                     uint32_t net_w, uint32_t net_h, uint32_t n, uint32_t* out, size_t cap) {
+    return guard(-1, [&]() -> int {
+        clear_error();
+        const int rc = plan_args(m, k, frame_w, frame_h, net_w, net_h, "fhc_model_conv_shapes");
+        if (rc < 0) return rc;
+        if (n == 0) return fail(-1, "fhc_model_conv_shapes: batch 0");
+        std::vector<std::pair<ShapeKey, ConvUse>> shapes;
+        try {
+            shapes = conv_shapes(*m, k, frame_w, frame_h, net_w, net_h, n);
+        } catch (const std::exception& e) {
+            return fail(-1, "fhc_model_conv_shapes: %s", e.what());
+        }
+        for (size_t i = 0; i < shapes.size() && (i + 1) * 7 <= cap; i++)
+            std::memcpy(out + 7 * i, shapes[i].first.v, sizeof shapes[i].first.v);
+        return (int)shapes.size();
+    });
+}
+
+extern "C" int fhc_model_autotune(const fhc_model* m, uint32_t k, uint32_t frame_w, uint32_t frame_h, uint32_t net_w,
+                                  uint32_t net_h, uint32_t n, int reps) {
+    return guard(-1, [&]() -> int {
+        clear_error();
+        const int rc = plan_args(m, k, frame_w, frame_h, net_w, net_h, "fhc_model_autotune");
+        if (rc < 0) return rc;
+        if (n == 0 || n > 64) return fail(-1, "fhc_model_autotune: batch %u (1..64)", n);
+        std::vector<std::pair<ShapeKey, ConvUse>> shapes;
+        try {
+            shapes = conv_shapes(*m, k, frame_w, frame_h, net_w, net_h, n);
+        } catch (const std::exception& e) {
+            return fail(-1, "fhc_model_autotune: %s", e.what());
+        }
+        auto pad8 = [](uint32_t c) { return (c + 7) / 8 * 8; };
+        int tuned = 0;
+        for (const auto& [key, c] : shapes) {
+            fhc_conv_desc d{};
+            d.n = n, d.h = c.h, d.w = c.wd, d.cin = c.cin, d.cout = c.cout, d.kh = d.kw = 3, d.stride = c.stride;
+            d.pad = 1, d.act = c.act ? FHC_ACT_PRELU : FHC_ACT_NONE, d.residual = c.res ? 1 : 0, d.ref_cand = 0xFF;
+            d.x_cstride = pad8(c.cin), d.y_cstride = pad8(c.cout), d.r_cstride = c.res ? pad8(c.cout) : 0;
+            const uint32_t ho = (c.h + 2 - 3) / c.stride + 1, wo = (c.wd + 2 - 3) / c.stride + 1;
+            const size_t xe = (size_t)n * c.h * c.wd * d.x_cstride, ye = (size_t)n * ho * wo * d.y_cstride;
+            std::vector<uint16_t> xh(xe), rh(c.res ? ye : 0);
+            seeded_f16(xh, key.v[0] * 31u + key.v[2]);
+            seeded_f16(rh, key.v[1] * 37u + key.v[3]);
+            const std::vector<uint16_t> w = weight_bits(*m, c.w), b = weight_bits(*m, c.b);
+            const std::vector<uint16_t> sl = c.act ? weight_bits(*m, c.s) : std::vector<uint16_t>();
+            void *x = nullptr, *y = nullptr, *r = nullptr;
+            auto release = [&]() {
+                if (x) (void)hipFree(x);
+                if (y) (void)hipFree(y);
+                if (r) (void)hipFree(r);
+            };
+            if (hipMalloc(&x, xe * 2) != hipSuccess || hipMalloc(&y, ye * 2) != hipSuccess ||
+                (c.res && hipMalloc(&r, ye * 2) != hipSuccess) ||
+                hipMemcpy(x, xh.data(), xe * 2, hipMemcpyHostToDevice) != hipSuccess ||
+                (c.res && hipMemcpy(r, rh.data(), ye * 2, hipMemcpyHostToDevice) != hipSuccess)) {
+                release();
+                return fail(-2, "fhc_model_autotune: device buffers for %s (%u -> %u at %u x %u, batch %u)",
+                            c.w.c_str(), c.cin, c.cout, c.wd, c.h, n);
+            }
+            float us = 0.0f;
+            const int code = fhc_conv_autotune(&d, w.data(), b.data(), c.act ? sl.data() : nullptr, x, y, r,
+                                               reps, &us);
+            release();
+            if (code < 0) return code;
+            tuned++;
+        }
+        return tuned;
     });
 }

@@ -3,8 +3,9 @@ static plan of a frame.
 
 ``Model.load(dir)`` reads graph.json, flyhighfg.json and flyhighfg.bin from a directory the caller names (the
 reference's Model::from_dir, crates/flyhigh-engine/src/model/mod.rs:38-96); ``info()``, ``shape(name)`` and
-``weight(name)`` (f16 bits, model/blob.rs:29-41) read it; ``plan(k, frame, network, repair)`` walks the graph into the plan
-of one pair() + mid() (net/build.rs:149-736, net/session.rs:26-66). Errors raise ``FhcError`` with the library's
+``weight(name)`` (f16 bits, model/blob.rs:29-41) read it; ``plan(k, frame, network, repair)`` walks the graph into
+the plan of one pair() + mid() (net/build.rs:149-736, net/session.rs:26-66); ``conv_shapes`` and ``autotune``
+discover and tune its conv shapes (ops/conv/autotune.rs:153-245). Errors raise ``FhcError`` with the library's
 message. No model file travels with this repository.
 """
 from __future__ import annotations
@@ -34,6 +35,8 @@ def _lib():
                                  ctypes.c_int),
             "fhc_model_weight": ([P, ctypes.c_char_p, P, SZ], ctypes.c_int64),
             "fhc_model_plan": ([P, U32, U32, U32, U32, U32, U32, ctypes.c_char_p, SZ], ctypes.c_int),
+            "fhc_model_conv_shapes": ([P, U32, U32, U32, U32, U32, U32, ctypes.POINTER(U32), SZ], ctypes.c_int),
+            "fhc_model_autotune": ([P, U32, U32, U32, U32, U32, U32, ctypes.c_int], ctypes.c_int),
         }
         for name, (args, res) in sig.items():
             f = getattr(L, name)
@@ -100,6 +103,19 @@ class Model:
             if "buffer too small" not in fhconv.last_error():
                 _check(rc, "fhc_model_plan")
             cap *= 4
+
+    def conv_shapes(self, k: int, frame: Tuple[int, int], network: Tuple[int, int], n: int = 1) -> list:
+        """The plan's distinct conv shapes at batch n: (cin, cout, h, w, stride, n, kernel size), h, w the input."""
+        cap = 7 * 256
+        buf = (ctypes.c_uint32 * cap)()
+        cnt = _check(_lib().fhc_model_conv_shapes(self._h, k, frame[0], frame[1], network[0], network[1], n, buf,
+                                                   cap), "fhc_model_conv_shapes")
+        return [tuple(buf[7 * i:7 * i + 7]) for i in range(min(cnt, cap // 7))]
+
+    def autotune(self, k: int, frame: Tuple[int, int], network: Tuple[int, int], n: int = 1, reps: int = 10) -> int:
+        """Tune every conv shape of the plan into the choice table (fhc_model_autotune); the number tuned."""
+        return _check(_lib().fhc_model_autotune(self._h, k, frame[0], frame[1], network[0], network[1], n, reps),
+                      "fhc_model_autotune")
 
     def close(self):
         if getattr(self, "_h", None) is not None and self._h.value:

@@ -72,6 +72,22 @@ int64_t fhc_model_weight(const fhc_model* model, const char* name, uint16_t* out
 int fhc_model_plan(const fhc_model* model, uint32_t k, uint32_t frame_w, uint32_t frame_h, uint32_t net_w,
                    uint32_t net_h, uint32_t repair, char* json, size_t cap);
 
+
+/* The distinct conv shapes of the static plan (the walk of fhc_model_plan, repair aside) at batch n, in plan order:
+ * 7 words each (cin, cout, h, w, stride, n, kernel size 3), h and w the input size: the key of the choice table
+ * (fhc_tune_get_ex). The reference's discovery build (autotune(), ops/conv/autotune.rs:186-213: every ConvShape
+ * of the plan, deduplicated by its key). Returns the count (the first cap / 7 written) or -1. */
+int fhc_model_conv_shapes(const fhc_model* model, uint32_t k, uint32_t frame_w, uint32_t frame_h, uint32_t net_w,
+                          uint32_t net_h, uint32_t n, uint32_t* out, size_t cap);
+
+/* Time every variant for each of those shapes (fhc_conv_autotune, `reps` launches per candidate) on device buffers
+ * this call allocates and frees (the layout of fhc_conv.h with channel strides rounded up to 8; seeded inputs; the
+ * model's weights; the residual of the shape's first use), recording the fastest in the process-wide choice table:
+ * the reference's autotune of a plan (ops/conv/autotune.rs:180-245, a TuneRequest's table) as one blocking call at
+ * plan time. Fused pairs are not tuned here. Returns the number of shapes tuned or a negative status. */
+int fhc_model_autotune(const fhc_model* model, uint32_t k, uint32_t frame_w, uint32_t frame_h, uint32_t net_w,
+                       uint32_t net_h, uint32_t n, int reps);
+
 #ifdef __cplusplus
 }
 #endif

@@ -279,3 +279,76 @@ def test_trained_model_generates_the_inbetween(model):
     to_mid, to_f0, to_f1 = mae(got, mid), mae(got, f0), mae(got, f1)
     print(f"MAE to the true middle {to_mid:.2f}, to f0 {to_f0:.2f}, to f1 {to_f1:.2f}")
     assert to_mid < to_f0 and to_mid < to_f1 and to_mid < 6.0
+
+
+# ---- discovery of the plan's conv shapes, and their autotune -------------------------------------------------------
+
+@have_model
+def test_conv_shapes_are_the_golden_plans_convs(model):
+    """The distinct conv shapes of the plan at the 856 x 480 network, in plan order, are those of the reference's
+    golden plan at that network with the full graph (rt-720p-default: every conv it records,
+    tests/golden/ref_conv_plans.json), keyed as the reference's discovery build keys them (cin, cout, h, w, stride,
+    autotune.rs:214-217); the frame size does not change them (1280 x 720 and 1920 x 1080 alike)."""
+    recs = json.load(open(os.path.join(HERE, "golden", "ref_conv_plans.json")))
+    want = []
+    for r in recs:
+        if r["source"].startswith("rt-720p-default.tc-f16:"):
+            c = r["conv"]
+            key = (c["cin"], c["cout"], c["h"], c["w"], c["stride"])
+            if key not in want:
+                want.append(key)
+    got = model.conv_shapes(1, (1280, 720), (856, 480))
+    assert [s[:5] for s in got] == want
+    assert model.conv_shapes(1, (1920, 1080), (856, 480)) == got
+    assert all(s[5:] == (1, 3) for s in got)
+    assert [s[5] for s in model.conv_shapes(1, (1920, 1080), (856, 480), n=8)] == [8] * len(got)
+
+
+def synthetic_model(rng):
+    """A small model of this library's own making (three convs and the render, random weights): graph.json,
+    manifest and blob bytes in the reference's formats (model/graph.rs, model/mod.rs:57-119)."""
+    layers = [("s.c1", 3, 16, True), ("s.c2", 16, 16, True), ("s.c3", 16, 10, False)]
+    tensors, blob, off = {}, [], 0
+    for name, cin, cout, act in layers:
+        parts = [(f"{name}.0.weight" if act else f"{name}.weight", [cout, cin, 3, 3]),
+                 (f"{name}.0.bias" if act else f"{name}.bias", [cout])]
+        if act:
+            parts.append((f"{name}.1.weight", [cout]))
+        for tname, shape in parts:
+            n = int(np.prod(shape))
+            tensors[tname] = {"shape": shape, "offset": off}
+            blob.append(rng.normal(0, 0.2, n).astype(np.float16).view(np.uint16))
+            off += n
+    ops = [{"in": ["A"], "out": ["x1"], "w": ["s.c1.0.weight", "s.c1.0.bias", "s.c1.1.weight"], "stride": 2,
+            "op": "conv"},
+           {"in": ["x1"], "out": ["x2"], "w": ["s.c2.0.weight", "s.c2.0.bias", "s.c2.1.weight"], "op": "conv"},
+           {"in": ["x2"], "out": ["x3"], "w": ["s.c3.weight", "s.c3.bias"], "op": "conv2d"},
+           {"in": ["x3"], "out": ["f"], "a": 0, "b": 4, "op": "slice"},
+           {"in": ["x3"], "out": ["v"], "a": 4, "b": 7, "op": "slice"},
+           {"in": ["x3"], "out": ["r"], "a": 7, "b": 10, "op": "slice"},
+           {"in": ["A", "B", "f", "v", "r"], "out": ["render"], "output": True, "op": "render_pix"}]
+    graph = json.dumps({"meta": {}, "ops": ops}).encode()
+    manifest = json.dumps({"meta": {"model": "synthetic", "format_version": 1, "train_step": 0,
+                                    "render_sampling": "bilinear", "n_params": off},
+                           "tensors": tensors}).encode()
+    return graph, manifest, np.concatenate(blob).astype("<u2").tobytes()
+
+
+def test_synthetic_model_plans_its_convs():
+    g, m, b = synthetic_model(np.random.default_rng(0))
+    mdl = fhmodel.Model.from_bytes(g, m, b)
+    assert mdl.conv_shapes(1, (64, 64), (64, 64)) == [(3, 16, 64, 64, 2, 1, 3), (16, 16, 32, 32, 1, 1, 3),
+                                                     (16, 10, 32, 32, 1, 1, 3)]
+
+
+@pytest.mark.gpu
+def test_autotune_of_a_model_fills_the_choice_table():
+    """fhc_model_autotune times every discovered shape and records its choice under the shape's key, at batch 1
+    and 2 (a synthetic model: the reference's model files stay where they lie)."""
+    g, m, b = synthetic_model(np.random.default_rng(1))
+    mdl = fhmodel.Model.from_bytes(g, m, b)
+    for n in (1, 2):
+        shapes = mdl.conv_shapes(1, (64, 64), (64, 64), n=n)
+        assert mdl.autotune(1, (64, 64), (64, 64), n=n, reps=3) == len(shapes) == 3
+        for s in shapes:
+            assert fhconv.load().fhc_tune_get_ex(*s) >= 0, s
