@@ -30,6 +30,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "flyhigh-engine_amd"))
 
 METRIC = "1080p frames/s (pair+mid); per-conv-layer % of MFMA or HBM roofline"
+# the reference's published time for the same workload (1080p frames, network 856x480, k = 1, repair 1): pair 1.61 ms +
+# mid 0.81 ms per generated frame on an RTX 4060 Ti (README.md:160 of the reference)
+PUBLISHED_MS_PER_FRAME = 2.41
 HBM_PEAK = 8.0e12       # B/s
 MFMA_F16_PEAK = 2.5e15  # FLOP/s, dense
 
@@ -271,19 +274,20 @@ def net_ops_report(args, torch, flyhighfg, stream, net_w, net_h):
                 batched_workload="8 frame pairs (A/B ops over 16 frames) and 24 mid() phases at network 864x480")
 
 
-def frame_1080p(args, torch, np, stream, t=0.5):
+def frame_1080p(args, torch, np, stream, t=0.5, repair=1, per_launch=True):
     """The headline workload: one 1080p pair() + mid(t) as the reference's Session runs it (net/session.rs:26-66,
     Internal::Auto): two 1920x1080 RGBA8 frames (the procedural picture and the same moved 12 px) resident in HBM ->
     rgba_in + antialiased downscale to the 864x480 network (one launch) -> every op of the graph (convs, fused pairs,
     the network ops and chains) -> render_pix at 1920x1088 + rgba_out to the RGBA8 frame (one launch). Random weights
     of the architecture (seed 7). Captured as one HIP graph on `stream`; args.steps replays after args.warmup,
-    bracketed by a device synchronisation on both sides (wall clock; events on the stream beside it). Then every
-    launch of the frame alone, a graph of args.reps launches, median of args.graphs replays (warm)."""
+    bracketed by a device synchronisation on both sides (wall clock; events on the stream beside it). Then (with
+    per_launch) every launch of the frame alone, a graph of args.reps launches, median of args.graphs replays
+    (warm). repair: the periodic-structure repair's level (1, the engine's default; 0 for the frame without it)."""
     import flyhighfg_net as fnet
     W = fnet.make_weights(7)
     be = fnet.GpuBackend(W, stream=stream, fuse=not args.no_fuse)
     net_w, net_h = 864, 480
-    f = fnet.FlyHighFG(be, net_w, net_h, frame=(1920, 1080))
+    f = fnet.FlyHighFG(be, net_w, net_h, frame=(1920, 1080), repair=repair)
     be.upload_frames(f.frames, np.stack([fnet.procedural_frame(1920, 1080), fnet.procedural_frame(1920, 1080, 12, 0)]))
     be.set_g(fnet.film_mlp(W, t))
     with torch.cuda.stream(stream):
@@ -309,6 +313,8 @@ def frame_1080p(args, torch, np, stream, t=0.5):
     us, ev_us = wall * 1e6 / args.steps, e0.elapsed_time(e1) * 1e3 / args.steps
     rgba = be.host_frames(f.rgba)
     ok = bool(np.all(rgba >> 24 == 255)) and len(np.unique(rgba)) > 1000
+    if not per_launch:
+        return dict(us_per_frame=round(us, 3), event_us_per_frame=round(ev_us, 3), output_ok=ok), (be, f, None)
     # every launch of the frame, timed alone (the recorder re-issues each with the frame's own buffers)
     be.record = []  # each launch re-issued alone
     with torch.cuda.stream(stream):
@@ -322,7 +328,7 @@ def frame_1080p(args, torch, np, stream, t=0.5):
         bound, t_roof = roof(r["flops"], r["bytes"])
         launches.append(dict(i=i, label=r["label"], kind=r["kind"], us_warm=round(us_l, 3), bytes=r["bytes"],
                              flops=r["flops"], bound=bound, roof_us=round(t_roof * 1e6, 4),
-                             frac_warm=round(t_roof * 1e6 / us_l, 4)))
+                             frac_warm=round(t_roof * 1e6 / us_l, 4), kernels=r.get("kernels", 1)))
         log("frame launch", json.dumps(launches[-1]))
     res = dict(us_per_frame=round(us, 3), frames_per_s=round(1e6 / us, 2), event_us_per_frame=round(ev_us, 3),
                steps=args.steps, warmup=args.warmup, network=f"{net_w}x{net_h}", frame="1920x1080",
@@ -637,6 +643,7 @@ def main():
         if not args.tune:  # no autotuning here: the frame's convs take the committed MI355X choices
             fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
         frame, _ = frame_1080p(args, torch, np, stream)
+        frame["no_repair"], _ = frame_1080p(args, torch, np, stream, repair=0, per_launch=False)
         print(json.dumps({k: v for k, v in frame.items() if k != "launch_table"}), flush=True)
         return 0
     if args.only_ops:
@@ -760,8 +767,10 @@ def main():
     # conv step's autotuning filled (or --tune); the batched workload's choices sit under keys of their own (the
     # table's key holds the batch)
     frame, (fbe, fobj, frec) = frame_1080p(args, torch, np, stream)
+    frame["no_repair"], _ = frame_1080p(args, torch, np, stream, repair=0, per_launch=False)
     log(f"bench: 1080p frame {frame['us_per_frame']:.2f} us ({frame['frames_per_s']:.0f} frames/s), "
-        f"{frame['launches']} launches, per-launch sum {frame['launch_us_sum']:.1f} us")
+        f"{frame['launches']} launches, per-launch sum {frame['launch_us_sum']:.1f} us; without the repair "
+        f"{frame['no_repair']['us_per_frame']:.2f} us")
     net_ops = net_ops_report(args, torch, flyhighfg, stream, net_w, net_h) if args.ops else None
 
     batched = None
@@ -775,7 +784,7 @@ def main():
     # the dominant kernel of the frame: the launch with the largest time alone (warm); its achieved rate is its
     # algorithmic bytes (or FLOPs) per launch over its per-launch time, cold (inputs from HBM) where the launch can
     # be rotated over fresh buffers: the frame-size render, a conv layer or fused pair of the conv step
-    dom = max(frame["launch_table"], key=lambda r: r["us_warm"])
+    dom = max((r for r in frame["launch_table"] if r["kernels"] == 1), key=lambda r: r["us_warm"])
     us_cold, cold_note = None, "warm only"
     if dom["label"].startswith("frame_render"):
         us_cold, nsets = render_cold(args, torch, fbe, fobj, args.reps, args.graphs, args.cold_mb << 20, stream)
@@ -837,9 +846,11 @@ def emit(args, frame, conv_step, roofline, cpu, batched, detail):
     line = dict(
         metric=METRIC, value=frame["frames_per_s"], unit="frames/s", n_gpus=1, steps=frame["steps"],
         warmup=frame["warmup"], ms_per_step=round(frame["us_per_frame"] / 1e3, 6), higher_is_better=True,
-        scaling="weak", vs_baseline=None, dtype="f16", data="synthetic",
+        scaling="weak", vs_baseline=round(frame["frames_per_s"] * PUBLISHED_MS_PER_FRAME / 1e3, 3), dtype="f16",
+        data="synthetic",
         config=dict(workload=frame["workload"], frame="1920x1080", network=frame["network"],
                     launches=frame.get("launches"), parallelism="single GPU"),
+        frame_without_repair_us=frame.get("no_repair", {}).get("us_per_frame"),
         roofline=None if roofline is None else {k: roofline[k] for k in keep_roof if k in roofline},
         cpu_baseline=cpu,
         conv_step=None if conv_step is None else {k: conv_step[k] for k in ("us_per_step", "frames_per_s",
