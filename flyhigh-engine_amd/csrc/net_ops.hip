@@ -165,8 +165,26 @@ __global__ __launch_bounds__(kThreads) void sad_kernel(View la, View lb, OView o
 // softmax once and every channel from LDS, in the reference's order.
 constexpr uint32_t kCvIn = 8, kCvHalo = kCvIn + 2;
 
+// FVT: x is mid()'s flow_t | vis_t (7 channels), computed while staging from fv (flow 0-3, vis 4-6) and the FiLM
+// head's output df (d_flow 0-3, d_mask 4) with flow_vis_t_kernel's arithmetic, so that x is never stored: the same
+// f16 values the two launches produce
+__device__ __forceinline__ void flow_vis_t_at(const View& fv, const View& df, size_t pix, float af, float ab,
+                                              uint16_t (&o)[7]) {
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+        const float lin = h2f(f2h(ld(fv, pix, i) * fv.scale * (i < 2 ? af : ab)));
+        o[i] = f2h(lin + ld(df, pix, i) * df.scale);
+    }
+    const uint16_t dm = df.p[pix * df.cs + df.c0 + 4];
+    const float dv[3] = {h2f(dm), h2f(f2h(h2f(dm) * -1.0f)), 0.0f};
+#pragma unroll
+    for (uint32_t j = 0; j < 3; j++) o[4 + j] = f2h(ld(fv, pix, 4 + j) * fv.scale + dv[j]);
+}
+
+template <bool FVT>
 __global__ __launch_bounds__(kThreads) void convex_tile_kernel(View wt, View x, OView out, uint32_t h, uint32_t w,
-                                                               uint32_t c, uint32_t tiles_x, uint32_t tiles_y) {
+                                                               uint32_t c, uint32_t tiles_x, uint32_t tiles_y,
+                                                               View fv, View df, float af, float ab) {
     extern __shared__ __align__(16) uint16_t lds[];
     uint16_t* lw = lds;                       // [kCvIn * kCvIn][36]
     uint16_t* lx = lds + kCvIn * kCvIn * 36;  // [kCvHalo * kCvHalo][c]
@@ -185,7 +203,16 @@ __global__ __launch_bounds__(kThreads) void convex_tile_kernel(View wt, View x, 
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) lw[p * 36 + q * 4 + i] = src[i];
     }
-    if (tid < kCvHalo * kCvHalo) {  // one lane per halo pixel, channels 8 at a time
+    if (FVT && tid < kCvHalo * kCvHalo) {  // one lane per halo pixel: flow_t | vis_t from fv and df
+        const uint32_t py = tid / kCvHalo, px = tid % kCvHalo;
+        const int gy = iy0 - 1 + (int)py, gx = ix0 - 1 + (int)px;
+        const bool in = gy >= 0 && gy < (int)h && gx >= 0 && gx < (int)w;
+        uint16_t v[7];
+        flow_vis_t_at(fv, df, ((size_t)img * h + clampi(gy, 0, (int)h - 1)) * w + clampi(gx, 0, (int)w - 1), af, ab,
+                      v);
+#pragma unroll
+        for (uint32_t cc = 0; cc < 7; cc++) lx[tid * 7 + cc] = in ? v[cc] : (uint16_t)0;
+    } else if (!FVT && tid < kCvHalo * kCvHalo) {  // one lane per halo pixel, channels 8 at a time
         const uint32_t py = tid / kCvHalo, px = tid % kCvHalo;
         const int gy = iy0 - 1 + (int)py, gx = ix0 - 1 + (int)px;
         const bool in = gy >= 0 && gy < (int)h && gx >= 0 && gx < (int)w;
@@ -666,17 +693,43 @@ __global__ __launch_bounds__(kThreads) void pair_pyramid_kernel(View q, OView i8
 // the flow at 1/8), the warped pictures' luma (channel image of l8) and the scaled flow itself, written into their
 // slices of the block's input fx (c0: wa, +c: wb, +2c: ia, +2c+3: ib, +2c+6: flow8). One lane per (pixel, task):
 // tasks 0 .. 2G-1 warp 4 feature channels (G groups per map), 2G and 2G+1 a picture with its luma, 2G+2 the flow.
-template <bool VEC>
+// The coarse head's output resized to the fine grid (coarse_up_kernel's arithmetic): channel ch of out pixel (x, y)
+// (h x w) bilinear from o (hi x wi), times fs for the flow channels 0-3, as the f16 coarse_up stores.
+__device__ __forceinline__ uint16_t coarse_up_at(const View& o, uint32_t hi, uint32_t wi, uint32_t h, uint32_t w,
+                                                 float fs, uint32_t x, uint32_t y, uint32_t ch) {
+    const float sh = (float)hi / (float)h, sw = (float)wi / (float)w;
+    const float fiy = ((float)y + 0.5f) * sh - 0.5f, fix = ((float)x + 0.5f) * sw - 0.5f;
+    const int y0 = (int)floorf(fiy), x0 = (int)floorf(fix);
+    const float fy = fiy - (float)y0, fx = fix - (float)x0;
+    const size_t r0 = (size_t)clampi(y0, 0, (int)hi - 1) * wi, r1 = (size_t)clampi(y0 + 1, 0, (int)hi - 1) * wi;
+    const uint32_t c0 = clampi(x0, 0, (int)wi - 1), c1 = clampi(x0 + 1, 0, (int)wi - 1);
+    const float v00 = ld(o, r0 + c0, ch), v01 = ld(o, r0 + c1, ch), v10 = ld(o, r1 + c0, ch), v11 = ld(o, r1 + c1, ch);
+    const float val = (v00 * (1.0f - fx) + v01 * fx) * (1.0f - fy) + (v10 * (1.0f - fx) + v11 * fx) * fy;
+    return f2h(val * (ch < 4 ? fs : 1.0f));
+}
+
+// UP: the flow comes from the coarse head's output o (hi x wi) resized here (coarse_up fused): each lane resizes
+// the two flow channels it warps by (read at fl.scale, as the flow view of the fine block reads the stored fv), and
+// the flow task also stores all 7 channels into fv (flow times fs, vis) and the flow16 copy into the state (the
+// lanes whose pixel index falls in the coarse grid), as coarse_up_kernel does.
+template <bool VEC, bool UP>
 __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, View fl, OView fx, OView l8,
                                                               uint32_t h, uint32_t w, uint32_t c, uint32_t groups,
-                                                              uint32_t items) {
+                                                              uint32_t items, View o, OView fv, OView state,
+                                                              uint32_t hi, uint32_t wi, float fs) {
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     if (t >= items) return;
     const uint32_t tasks = 2 * groups + 3, pix = t / tasks, task = t - pix * tasks;
     const uint32_t x = pix % w, y = pix / w;
     if (task < 2 * groups + 2) {
         const uint32_t img = task < 2 * groups ? task / groups : task - 2 * groups;
-        const float fxv = ld(fl, pix, 2 * img) * fl.scale, fyv = ld(fl, pix, 2 * img + 1) * fl.scale;
+        float fxv, fyv;
+        if constexpr (UP) {
+            fxv = h2f(coarse_up_at(o, hi, wi, h, w, fs, x, y, 2 * img)) * fl.scale;
+            fyv = h2f(coarse_up_at(o, hi, wi, h, w, fs, x, y, 2 * img + 1)) * fl.scale;
+        } else {
+            fxv = ld(fl, pix, 2 * img) * fl.scale, fyv = ld(fl, pix, 2 * img + 1) * fl.scale;
+        }
         float o[4];
         if (task < 2 * groups) {
             const uint32_t ch = (task - img * groups) * 4;
@@ -695,11 +748,25 @@ __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, 
             st(l8, pix, img, lum3(r[0], r[1], r[2]));
         }
     } else {
+        uint16_t v[7];
+        if constexpr (UP) {
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) {
-            const uint16_t v = fl.p[(size_t)pix * fl.cs + fl.c0 + i];
-            fx.p[(size_t)pix * fx.cs + fx.c0 + 2 * c + 6 + i] = fl.scale == 1.0f ? v : f2h(h2f(v) * fl.scale);
+            for (uint32_t ch = 0; ch < 7; ch++) {
+                v[ch] = coarse_up_at(o, hi, wi, h, w, fs, x, y, ch);
+                fv.p[(size_t)pix * fv.cs + fv.c0 + ch] = v[ch];
+            }
+            if (state.p && x < wi && y < hi) {
+                const size_t sp = (size_t)y * wi + x;
+#pragma unroll
+                for (uint32_t ch = 0; ch < 4; ch++) st(state, sp, ch, ld(o, sp, ch) * fs);
+            }
+        } else {
+#pragma unroll
+            for (uint32_t i = 0; i < 4; i++) v[i] = fl.p[(size_t)pix * fl.cs + fl.c0 + i];
         }
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++)
+            fx.p[(size_t)pix * fx.cs + fx.c0 + 2 * c + 6 + i] = fl.scale == 1.0f ? v[i] : f2h(h2f(v[i]) * fl.scale);
     }
 }
 
@@ -1723,8 +1790,9 @@ extern "C" int fhc_convex_upsample(const fhc_tensor* wt, const fhc_tensor* x, co
         const uint32_t tx = (w + kCvIn - 1) / kCvIn, ty = (h + kCvIn - 1) / kCvIn;
         if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "convex_upsample: too many tiles");
         const size_t lds = (kCvIn * kCvIn * 36 + kCvHalo * kCvHalo * c) * 2;
-        hipLaunchKernelGGL(convex_tile_kernel, dim3(n * tx * ty), dim3(kThreads), lds, (hipStream_t)stream, in(wt),
-                           in(x), outv(out), h, w, c, tx, ty);
+        const View none{nullptr, 0, 0, 1.0f};
+        hipLaunchKernelGGL(convex_tile_kernel<false>, dim3(n * tx * ty), dim3(kThreads), lds, (hipStream_t)stream,
+                           in(wt), in(x), outv(out), h, w, c, tx, ty, none, none, 0.0f, 0.0f);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "convex_upsample: launch failed: %s", hipGetErrorString(e));
     });
@@ -1928,10 +1996,12 @@ extern "C" int fhc_fine_input(const fhc_tensor* f8, const fhc_tensor* i8, const 
         fhc_tensor fxb = *fx;  // the second map's slice must be 8-byte aligned too for the vector path
         fxb.c0 += c;
         const bool v = vec4(c, {f8, fx, &fxb});
+        const View none{nullptr, 0, 0, 1.0f};
+        const OView onone{nullptr, 0, 0};
         return launch("fine_input", (uint64_t)h * w * (2 * groups + 3), [&](dim3 g, uint32_t n) {
-            auto k = v ? fine_input_kernel<true> : fine_input_kernel<false>;
+            auto k = v ? fine_input_kernel<true, false> : fine_input_kernel<false, false>;
             hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8), in(flow), outv(fx),
-                               outv(l8), h, w, c, groups, n);
+                               outv(l8), h, w, c, groups, n, none, onone, onone, 0u, 0u, 0.0f);
         });
     });
 }
@@ -2215,5 +2285,57 @@ extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, ui
                            outv(flow), h8, w8, p.hc, p.wc, p.eps, p.dmin, p.tex, cells);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "gmhs: launch failed: %s", hipGetErrorString(e));
+    });
+}
+
+extern "C" int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state,
+                                     uint32_t hi, uint32_t wi, float flow_scale, const fhc_tensor* f8,
+                                     const fhc_tensor* i8, float fine_scale, const fhc_tensor* fx,
+                                     const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)h * w * c == 0) return 0;
+        if (hi == 0 || wi == 0) return fail(-1, "coarse_fine_input: empty coarse output (%u x %u)", hi, wi);
+        if (state && (hi > h || wi > w)) return fail(-1, "coarse_fine_input: the state is larger than the fine grid");
+        FHC_TRY(check(o, "coarse_fine_input o", 7, false));
+        FHC_TRY(check(fv, "coarse_fine_input fv", 7, false, true));
+        if (state) FHC_TRY(check(state, "coarse_fine_input state", 4, false, true));
+        FHC_TRY(check(f8, "coarse_fine_input f8", c, true));
+        FHC_TRY(check(i8, "coarse_fine_input i8", 3, true));
+        FHC_TRY(check(fx, "coarse_fine_input fx", 2 * c + 10, false, true));
+        FHC_TRY(check(l8, "coarse_fine_input l8", 2, false, true));
+        if (!std::isfinite(fine_scale)) return fail(-1, "coarse_fine_input: the flow's read scale is not finite");
+        const uint32_t groups = (c + 3) / 4;
+        fhc_tensor fxb = *fx;
+        fxb.c0 += c;
+        const bool v = vec4(c, {f8, fx, &fxb});
+        const View fl{static_cast<const uint16_t*>(fv->p), fv->cstride, fv->c0, fine_scale};
+        const OView sv = state ? outv(state) : OView{nullptr, 0, 0};
+        return launch("coarse_fine_input", (uint64_t)h * w * (2 * groups + 3), [&](dim3 g, uint32_t n) {
+            auto k = v ? fine_input_kernel<true, true> : fine_input_kernel<false, true>;
+            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8), fl, outv(fx), outv(l8),
+                               h, w, c, groups, n, in(o), outv(fv), sv, hi, wi, flow_scale);
+        });
+    });
+}
+
+extern "C" int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, float t,
+                                     const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)n * h * w == 0) return 0;
+        FHC_TRY(check(wt, "flow_vis_t_convex wt", 36, false));
+        FHC_TRY(check(fv, "flow_vis_t_convex fv", 7, true));
+        FHC_TRY(check(dfilm, "flow_vis_t_convex dfilm", 5, true));
+        FHC_TRY(check(out, "flow_vis_t_convex out", 7, false, true));
+        const uint32_t tx = (w + kCvIn - 1) / kCvIn, ty = (h + kCvIn - 1) / kCvIn;
+        if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "flow_vis_t_convex: too many tiles");
+        const size_t lds = (kCvIn * kCvIn * 36 + kCvHalo * kCvHalo * 7) * 2;
+        const float af = 2.0f * t, ab = 2.0f * (1.0f - t);  // the mul_t factors (net/build.rs:293)
+        const View none{nullptr, 0, 0, 1.0f};
+        hipLaunchKernelGGL(convex_tile_kernel<true>, dim3(n * tx * ty), dim3(kThreads), lds, (hipStream_t)stream,
+                           in(wt), none, outv(out), h, w, 7u, tx, ty, in(fv), in(dfilm), af, ab);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "flow_vis_t_convex: launch failed: %s", hipGetErrorString(e));
     });
 }

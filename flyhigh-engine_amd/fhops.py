@@ -80,6 +80,8 @@ def _lib():
             "fhc_coarse_up": [T, T, T, U, U, U, U, ctypes.c_float, P],
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
+            "fhc_coarse_fine_input": [T, T, T, U, U, ctypes.c_float, T, T, ctypes.c_float, T, T, U, U, U, P],
+            "fhc_flow_vis_t_convex": [T, T, T, ctypes.c_float, T, U, U, U, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
             "fhc_rgba_in": [P, U, U, U, U, ctypes.c_uint64, T, U, U, P],
             "fhc_rgba_out": [T, U, U, U, P, U, U, U, ctypes.c_uint64, P],
@@ -247,6 +249,25 @@ def flow_vis_t(fv, dfilm, out, t, stream=None):
     n, h, w, _ = fv.shape
     _run("flow_vis_t", _lib().fhc_flow_vis_t(_ref(fv), _ref(_v(dfilm)), _ref(_v(out)), n, h, w, t,
                                              _stream_handle(stream)))
+
+
+def coarse_fine_input(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c, stream=None):
+    """coarse_up(o, fv, state, ...) to f8's grid, then fine_input(f8, i8, (fv, fine_scale), fx, l8, c): one launch."""
+    o, f8 = _v(o), _v(f8)
+    _, hi, wi, _ = o.shape
+    _, h, w, _ = f8.shape
+    _run("coarse_fine_input",
+         _lib().fhc_coarse_fine_input(_ref(o), _ref(_v(fv)), None if state is None else _ref(_v(state)), hi, wi,
+                                      flow_scale, _ref(f8), _ref(_v(i8)), fine_scale, _ref(_v(fx)), _ref(_v(l8)), h,
+                                      w, c, _stream_handle(stream)))
+
+
+def flow_vis_t_convex(wt, fv, dfilm, t, out, stream=None):
+    """flow_vis_t(fv, dfilm, ., t) then convex(wt, ., 7, out), the intermediate never stored: one launch."""
+    fv = _v(fv)
+    n, h, w, _ = fv.shape
+    _run("flow_vis_t_convex", _lib().fhc_flow_vis_t_convex(_ref(_v(wt)), _ref(fv), _ref(_v(dfilm)), t, _ref(_v(out)),
+                                                           n, h, w, _stream_handle(stream)))
 
 
 def refine_input(q, flow, vis, rx, flow_out_scale, stream=None):

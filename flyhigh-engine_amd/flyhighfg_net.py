@@ -130,6 +130,17 @@ class ComposedChains:
             self.luma(V(fx.buf, fx.c0 + 2 * c + 3 * i), V(l8.buf, l8.c0 + i))
         self.chcopy(flow, 4, V(fx.buf, fx.c0 + 2 * c + 6))
 
+    def coarse_fine_input(self, o: V, fv: V, state: Optional[V], flow_scale: float, f8: V, i8: V,
+                          fine_scale: float, fx: V, l8: V, c: int):
+        _, h, w, _ = f8.buf.shape
+        self.coarse_up(o, fv, state, h, w, flow_scale)
+        self.fine_input(f8, i8, V(fv.buf, fv.c0, fine_scale), fx, l8, c)
+
+    def flow_vis_t_convex(self, wt: V, fv: V, dfilm: V, t: float, out: V, ftvt: V, lin: V, dvis: V):
+        """ftvt, lin, dvis: where the op-by-op chain keeps its intermediates (the fused launch stores none)."""
+        self.flow_vis_t(fv, dfilm, ftvt, t, lin, dvis)
+        self.convex(wt, ftvt, 7, out)
+
     def flow_vis_t(self, fv: V, dfilm: V, out: V, t: float, lin: V, dvis: V):
         self.unary(V(fv.buf, fv.c0), 2, V(lin.buf, lin.c0), 0, 2.0 * t)
         self.unary(V(fv.buf, fv.c0 + 2), 2, V(lin.buf, lin.c0 + 2), 0, 2.0 * (1.0 - t))
@@ -421,6 +432,28 @@ class GpuBackend(ComposedChains):
         vs = [self._v(x) for x in (fv, dfilm, out)]
         self._go("flow_vis_t", lambda: self.fh.flow_vis_t(*vs, t, stream=self.stream), 2 * (7 + 5 + 7) * self._px(fv))
 
+    def coarse_fine_input(self, o: V, fv: V, state: Optional[V], flow_scale: float, f8: V, i8: V,
+                          fine_scale: float, fx: V, l8: V, c: int):
+        if not self.chains:
+            return super().coarse_fine_input(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c)
+        vo, vfv, vs = self._v(o), self._v(fv), None if state is None else self._v(state)
+        vf8, vi8, vfx, vl8 = (self._v(x) for x in (f8, i8, fx, l8))
+        p1, po = self._px(f8) // 2, self._px(o)
+        # o read (7 channels, +4 for the state), fv (7) and the state (4) written, then fine_input's traffic
+        self._go("coarse_fine_input (coarse_up + fine_input)",
+                 lambda: self.fh.coarse_fine_input(vo, vfv, vs, flow_scale, vf8, vi8, fine_scale, vfx, vl8, c,
+                                                   stream=self.stream),
+                 2 * (7 + (0 if state is None else 8)) * po + 2 * 7 * p1 + 2 * p1 * (2 * c + 6 + (2 * c + 6 + 4) + 2))
+
+    def flow_vis_t_convex(self, wt: V, fv: V, dfilm: V, t: float, out: V, ftvt: V, lin: V, dvis: V):
+        if not self.chains:
+            return super().flow_vis_t_convex(wt, fv, dfilm, t, out, ftvt, lin, dvis)
+        vw, vfv, vd, vo = (self._v(x) for x in (wt, fv, dfilm, out))
+        px = self._px(fv)
+        self._go("flow_vis_t_convex (flow_vis_t + convex_upsample)",
+                 lambda: self.fh.flow_vis_t_convex(vw, vfv, vd, t, vo, stream=self.stream),
+                 2 * (36 + 7 + 5 + 4 * 7) * px)
+
     def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
         if not self.chains:
             return super().refine_input(q, flow, vis, rx, flow_out_scale, blend)
@@ -520,9 +553,10 @@ class FlyHighFG:
         be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30
         be.conv("coarse.c4", V(self.ch3r), V(self.hc))                                        # 31
         be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
-        be.coarse_up(V(self.o), V(self.fv), V(self.state_out, 72), e8h, e8w, 16.0)            # 33-40; 43: flow16
-        # the fine loop, K = 1 (op 42): h enters as zeros (op 41: the fx slice is never written)
-        be.fine_input(V(self.f8), V(self.i8), V(self.fv, 0, 0.125), V(self.fx), V(self.l8), 36)  # wa .. flow8
+        # 33-40 (43: flow16), then the fine loop's input, K = 1 (op 42: wa .. flow8); h enters as zeros (op 41: the
+        # fx slice is never written)
+        be.coarse_fine_input(V(self.o), V(self.fv), V(self.state_out, 72), 16.0, V(self.f8), V(self.i8), 0.125,
+                             V(self.fx), V(self.l8), 36)
         be.sad(V(self.l8, 0), V(self.l8, 1), V(self.fx, 130), 2)                              # fcv
         be.conv("fine.r1", V(self.fx), V(self.fr1))
         be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
@@ -543,8 +577,8 @@ class FlyHighFG:
         be.film(V(self.h), 48, V(self.hm))                                                    # 50
         be.pair("film.h1", "film.h2", V(self.hm), V(self.fh1), V(self.fh2), False)            # 51, 52
         be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
-        be.flow_vis_t(V(self.fv), V(self.dfilm), V(self.ftvt), t, V(self.lin), V(self.dvis))   # 44-48, 54-61
-        be.convex(V(self.wt36), V(self.ftvt), 7, V(self.up7))                                 # 62
+        be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(self.dfilm), t, V(self.up7), V(self.ftvt), V(self.lin),
+                             V(self.dvis))                                                    # 44-48, 54-62
         be.refine_input(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend))  # 63-76
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
         be.pair("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), False)        # 79, 80

@@ -198,6 +198,22 @@ int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tens
                      uint32_t h, uint32_t w, float flow_out_scale, void* stream);
 
 
+/* coarse_up then the fine block's input in one launch (graph ops 33-40 with 43's flow16, then op 42's input): the
+ * coarse head's output o (hi x wi, 7 channels) resized bilinearly to the fine grid h x w, the flow channels times
+ * flow_scale, stored into fv (7 channels) and the flow16 copy into state (NULL: none), as fhc_coarse_up; then, read
+ * at fine_scale, the flow that warps f8 and i8 into fx with the lumas into l8, as fhc_fine_input on the view (fv,
+ * fine_scale). Bit-identical to the two calls. */
+int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state, uint32_t hi, uint32_t wi,
+                          float flow_scale, const fhc_tensor* f8, const fhc_tensor* i8, float fine_scale,
+                          const fhc_tensor* fx, const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c,
+                          void* stream);
+
+/* fhc_flow_vis_t then fhc_convex_upsample of its output in one launch (graph ops 44-48, 54-62): the convex
+ * upsample's 7-channel input (flow_t | vis_t) computed from fv and dfilm at phase t while it is staged, never
+ * stored. Bit-identical to the two calls. */
+int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, float t,
+                          const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, void* stream);
+
 /* GMHS, the periodic-structure repair of the pair's E8 flow (crates/flyhigh-engine/src/gmhs.rs:149-206, run at the
  * end of the pair stage when the repair level is above 0, net/build.rs:640-660; the reference's default level is 1,
  * options.rs:305). A robust affine motion is fitted to the flow (4 rounds of reweighted least squares,

@@ -165,6 +165,12 @@ def test_network_ops_reject_bad_views_before_any_launch():
         ("fhc_interpolate", (_tv(scale=float("nan")), _tv(), 1, 4, 4, 4, 2, 2, 0, None), "not finite"),
         ("fhc_interpolate", (_tv(), _tv(), 1, 4, 0, 4, 2, 2, 1, None), "empty input"),
         ("fhc_warp", (None, _tv(), _tv(), 1, 4, 4, 4, None), "null view"),
+        ("fhc_coarse_fine_input", (_tv(cs=8), _tv(cs=8), None, 2, 2, 16.0, _tv(cs=8), _tv(), 0.125, _tv(cs=16),
+                                   _tv(), 4, 4, 4, None), "coarse_fine_input fx"),
+        ("fhc_coarse_fine_input", (_tv(cs=8), _tv(cs=8), _tv(), 8, 8, 16.0, _tv(cs=8), _tv(), 0.125, _tv(cs=24),
+                                   _tv(), 4, 4, 4, None), "state is larger"),
+        ("fhc_flow_vis_t_convex", (_tv(cs=40), _tv(cs=8), _tv(cs=4), ctypes.c_float(0.5), _tv(cs=8), 1, 4, 4, None),
+         "flow_vis_t_convex dfilm"),
     ]
     for name, args, msg in cases:
         rc = getattr(L, name)(*args)

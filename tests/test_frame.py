@@ -181,9 +181,10 @@ def test_gpu_small_frame_without_internal_mode_matches_the_oracle():
 
 @pytest.mark.gpu
 def test_fused_chains_equal_their_ops_on_the_gpu():
-    """The fused op chains (pyramid, fine input, flow_t / vis_t, refine input, and the frame's input and render
-    from RGBA8) against the same chains run op by op on the GPU, in a whole frame from RGBA8 frames in the
-    internal-size mode: the same f32 operations and roundings, so every output is bit-identical."""
+    """The fused op chains (pyramid, coarse upsample + fine input, flow_t / vis_t + convex upsample, refine input,
+    and the frame's input and render from RGBA8) against the same chains run op by op on the GPU, in a whole frame
+    from RGBA8 frames in the internal-size mode: the same f32 operations and roundings, so every output is
+    bit-identical."""
     import torch
     W = net.make_weights(3)
     fr = frames(600, 300, dx=7, dy=2)
@@ -191,8 +192,9 @@ def test_fused_chains_equal_their_ops_on_the_gpu():
     for chains in (True, False):
         gb = net.GpuBackend(W, stream=torch.cuda.current_stream(), chains=chains)
         f = run_frames(gb, W, 256, 128, fr, t=0.3)
-        extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("ftvt", 7),
-                 ("dfilm", 5), ("wt36", 36), ("f16", 72), ("AB", 4)]
+        # (flow_t | vis_t, ftvt, is compared through up7: the fused launch that makes up7 never stores it)
+        extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("dfilm", 5),
+                 ("wt36", 36), ("f16", 72), ("AB", 4)]
         got = {name: gb.host(getattr(f, name))[..., :c].copy() for name, c in FRAME_OUTPUTS + extra}
         got["rgba"] = gb.host_frames(f.rgba).copy()
         outs.append(got)
