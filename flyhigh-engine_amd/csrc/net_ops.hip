@@ -1593,62 +1593,120 @@ __global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint3
 }
 
 // box_h then box_v of radius r (gm_box.wgsl:8-25) on map channel blockIdx.z of src ([c][hc][wc]) into the same
-// channel of dst, for the block's 16 x 16 tile of cells; channels from `nfilt` on are copied unfiltered. The window
-// of clamped rows and columns the tile's taps reach is staged in LDS; box_h runs on every window row (a window row
-// is a clamped map row, so its sums are the map's own), box_v on the tile; the taps of each sum are loaded 8 at a
-// time ahead of their in-order additions.
-__global__ __launch_bounds__(kThreads) void gm_box_kernel(const float* src, float* dst, uint32_t nfilt, uint32_t hc,
-                                                          uint32_t wc, uint32_t r) {
-    __shared__ float win[kGmWin * kGmWin], hs[kGmWin * kGmT];
+// channel of dst, for the block's 16 x 16 tile of cells. The window of clamped rows and columns the tile's taps
+// reach ((16 + 2r)^2 cells, NB x NB blocks of 16 x 16, dynamic LDS) is staged with every load issued before the
+// first store; box_h runs on every window row (a window row is a clamped map row, so its sums are the map's own),
+// box_v on the tile, each sum over its taps in order.
+template <uint32_t NB>
+__global__ __launch_bounds__(kThreads) void gm_box_kernel(const float* src, float* dst, uint32_t hc, uint32_t wc,
+                                                          uint32_t r) {
+    extern __shared__ float glds[];
     const uint32_t t = threadIdx.x, x0 = blockIdx.x * kGmT, y0 = blockIdx.y * kGmT, ch = blockIdx.z;
     const uint32_t ty = t / kGmT, tx = t % kGmT;
+    const uint32_t span = 2 * r + 1, rows = kGmT + 2 * r;
+    float* win = glds;                // [rows][rows]
+    float* hs = glds + rows * rows;   // [rows][16]
     const size_t n = (size_t)hc * wc;
     const float* plane = src + ch * n;
-    const bool inside = x0 + tx < wc && y0 + ty < hc;
-    const size_t at = (size_t)(y0 + ty) * wc + x0 + tx;
-    if (ch >= nfilt) {
-        if (inside) dst[ch * n + at] = plane[at];
-        return;
-    }
-    const uint32_t span = 2 * r + 1, rows = kGmT + 2 * r;
     const float den = (float)span;
-    for (uint32_t k = t; k < rows * rows; k += kThreads) {
-        const uint32_t j = k / rows, i = k % rows;
-        const int yy = clampi((int)y0 - (int)r + (int)j, 0, (int)hc - 1);
-        const int xx = clampi((int)x0 - (int)r + (int)i, 0, (int)wc - 1);
-        win[j * kGmWin + i] = plane[(size_t)yy * wc + xx];
-    }
+    float v[NB][NB];
+#pragma unroll
+    for (uint32_t bj = 0; bj < NB; bj++)
+#pragma unroll
+        for (uint32_t bi = 0; bi < NB; bi++) {
+            const uint32_t j = min(ty + kGmT * bj, rows - 1), i = min(tx + kGmT * bi, rows - 1);
+            const int yy = clampi((int)y0 - (int)r + (int)j, 0, (int)hc - 1);
+            const int xx = clampi((int)x0 - (int)r + (int)i, 0, (int)wc - 1);
+            v[bj][bi] = plane[(size_t)yy * wc + xx];
+        }
+#pragma unroll
+    for (uint32_t bj = 0; bj < NB; bj++)
+#pragma unroll
+        for (uint32_t bi = 0; bi < NB; bi++) {
+            const uint32_t j = ty + kGmT * bj, i = tx + kGmT * bi;
+            if (j < rows && i < rows) win[j * rows + i] = v[bj][bi];
+        }
     __syncthreads();
-    for (uint32_t k = t; k < rows * kGmT; k += kThreads) {
-        const uint32_t j = k / kGmT, xo = k % kGmT;
-        const float* row = win + j * kGmWin + xo;
-        float acc = 0.0f;
+#pragma unroll
+    for (uint32_t bj = 0; bj < NB; bj++) {
+        const uint32_t j = ty + kGmT * bj;
+        if (j < rows) {
+            const float* row = win + j * rows + tx;
+            float acc = 0.0f;
 #pragma unroll 8
-        for (uint32_t d = 0; d < span; d++) acc = acc + row[d];
-        hs[j * kGmT + xo] = acc / den;
+            for (uint32_t d = 0; d < span; d++) acc = acc + row[d];
+            hs[j * kGmT + tx] = acc / den;
+        }
     }
     __syncthreads();
     float acc = 0.0f;
 #pragma unroll 8
     for (uint32_t d = 0; d < span; d++) acc = acc + hs[(ty + d) * kGmT + tx];
-    if (inside) dst[ch * n + at] = acc / den;
+    if (x0 + tx < wc && y0 + ty < hc) dst[ch * n + (size_t)(y0 + ty) * wc + x0 + tx] = acc / den;
 }
 
-// gm_select.wgsl:14-27, one lane per E8 cell: the cell adopts the affine motion where the nearest cost cell's
-// decision maps say so
-__global__ __launch_bounds__(kThreads) void gm_select_kernel(const float* maps, const float* coef, OView flow,
-                                                             uint32_t h8, uint32_t w8, uint32_t hc, uint32_t wc,
-                                                             float eps, float dmin, float tex, uint32_t items) {
+// the cost cell the select reads for E8 row i (column j): gm_select.wgsl:17-18
+__host__ __device__ __forceinline__ int gm_sel_row(uint32_t i, uint32_t hc, uint32_t h8) {
+    const int v = (int)floorf(((float)i + 0.5f) * (float)hc / (float)h8);
+    return v < 0 ? 0 : v > (int)hc - 1 ? (int)hc - 1 : v;
+}
+
+// The decision window (box_h then box_v of radius r on maps 0-2, gm_box.wgsl:8-25) is needed only at the cost
+// cells the select reads: box_h at their columns (every row), then box_v at their rows, the same sums in the same
+// order as the full windows there. NT >= 2r + 1: a sum's taps are loaded together (clamped addresses; the loads
+// past the window repeat its last tap and are not added), then added in order.
+// box_h of maps 0-2 of tex ([5][hc][wc], after the texture window) at the select's columns: hs [3][hc][w8]
+template <uint32_t NT>
+__global__ __launch_bounds__(kThreads) void gm_dwin_h_kernel(const float* tex, float* hs, uint32_t hc, uint32_t wc,
+                                                             uint32_t w8, uint32_t r, uint32_t items) {
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     if (t >= items) return;
-    const uint32_t i = t / w8, j = t % w8;
-    const int x = clampi((int)floorf(((float)j + 0.5f) * (float)wc / (float)w8), 0, (int)wc - 1);
-    const int y = clampi((int)floorf(((float)i + 0.5f) * (float)hc / (float)h8), 0, (int)hc - 1);
+    const uint32_t j = t % w8, rr = t / w8, row = rr % hc, m = rr / hc, span = 2 * r + 1;
+    const int x = gm_sel_row(j, wc, w8);
+    const float* src = tex + m * (size_t)hc * wc + (size_t)row * wc;
+    float v[NT];
+#pragma unroll
+    for (uint32_t d = 0; d < NT; d++) v[d] = src[clampi(x - (int)r + (int)min(d, span - 1), 0, (int)wc - 1)];
+    float acc = 0.0f;
+#pragma unroll
+    for (uint32_t d = 0; d < NT; d++)
+        if (d < span) acc = acc + v[d];
+    hs[t] = acc / (float)span;
+}
+
+// box_v of hs at the select's rows, then the select (gm_select.wgsl:14-27), one lane per E8 cell; dec [5][h8][w8]
+// receives the five values the cell decides on (maps 0-2 after both windows, maps 3-4 after the texture window)
+template <uint32_t NT>
+__global__ __launch_bounds__(kThreads) void gm_dwin_v_select_kernel(const float* hs, const float* tex,
+                                                                    const float* coef, OView flow, float* dec,
+                                                                    uint32_t h8, uint32_t w8, uint32_t hc, uint32_t wc,
+                                                                    uint32_t r, float eps, float dmin, float texf,
+                                                                    uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t >= items) return;
+    const uint32_t i = t / w8, j = t % w8, span = 2 * r + 1;
+    const int y = gm_sel_row(i, hc, h8), x = gm_sel_row(j, wc, w8);
     const size_t n = (size_t)hc * wc, idx = (size_t)y * wc + x;
-    const float cm = maps[idx], ca = maps[n + idx], dv = maps[2 * n + idx], lm = maps[3 * n + idx];
-    const float l2 = maps[4 * n + idx];
+    const float lm = tex[3 * n + idx], l2 = tex[4 * n + idx];
+    float dw[3];
+#pragma unroll
+    for (uint32_t m = 0; m < 3; m++) {
+        const float* col = hs + (size_t)m * hc * w8 + j;
+        float v[NT];
+#pragma unroll
+        for (uint32_t d = 0; d < NT; d++)
+            v[d] = col[(size_t)clampi(y - (int)r + (int)min(d, span - 1), 0, (int)hc - 1) * w8];
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t d = 0; d < NT; d++)
+            if (d < span) acc = acc + v[d];
+        dw[m] = acc / (float)span;
+    }
+    const float cm = dw[0], ca = dw[1], dv = dw[2];
+    const size_t n8 = (size_t)h8 * w8;
+    dec[t] = cm, dec[n8 + t] = ca, dec[2 * n8 + t] = dv, dec[3 * n8 + t] = lm, dec[4 * n8 + t] = l2;
     const float sd = sqrtf(fmaxf(l2 - lm * lm, 0.0f));
-    if (ca + eps < cm && dv > dmin && sd > tex) {
+    if (ca + eps < cm && dv > dmin && sd > texf) {
         const float xn = -1.0f + 2.0f * (float)j / (float)max(w8 - 1, 1u);
         const float yn = -1.0f + 2.0f * (float)i / (float)max(h8 - 1, 1u);
 #pragma unroll
@@ -1719,7 +1777,8 @@ int gm_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc_gmhs_
     p->eps = 0.0f, p->tex = 0.015f;
     const uint64_t head = (16 + 2 * (uint64_t)kGmPart) * sizeof(float), cells = (uint64_t)p->hc * p->wc;
     p->maps_offset = (head + 255) / 256 * 256;
-    p->ws_bytes = p->maps_offset + 2 * 5 * cells * sizeof(float);
+    p->dec_offset = p->maps_offset + 5 * cells * sizeof(float);
+    p->ws_bytes = p->dec_offset + 5 * cells * sizeof(float);
     return 0;
 }
 
@@ -2262,10 +2321,15 @@ extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, ui
             return fail(-1, "gmhs: box radii %u, %u exceed %u", p.r_blk, p.r_dwin, kGmRmax);
         if ((uint64_t)h8 * w8 >= kMaxItems || (uint64_t)h * w >= kMaxItems)
             return fail(-1, "gmhs: %u x %u network, %u x %u flow: too large", w, h, w8, h8);
+        // the raw cost maps' region, once the texture window has read them, holds dec [5][h8][w8] then hs [3][hc][w8]
+        const uint64_t cells = (uint64_t)p.hc * p.wc, hs_off = ((uint64_t)5 * h8 * w8 + 63) / 64 * 64;
+        if (h8 > p.hc || w8 > p.wc || hs_off + (uint64_t)3 * p.hc * w8 > 5 * cells)
+            return fail(-1, "gmhs: the E8 flow (%u x %u) is too large for the cost grid (%u x %u)", w8, h8, p.wc, p.hc);
         float* coef = static_cast<float*>(ws);
         float* part[2] = {coef + 16, coef + 16 + kGmPart};
-        float* maps = reinterpret_cast<float*>(static_cast<char*>(ws) + p.maps_offset);
-        float* tmp = maps + 5 * (size_t)p.hc * p.wc;
+        float* maps = reinterpret_cast<float*>(static_cast<char*>(ws) + p.maps_offset);  // after the texture window
+        float* raw = reinterpret_cast<float*>(static_cast<char*>(ws) + p.dec_offset);    // the cost maps, then dec
+        float* hs = raw + hs_off;
         const hipStream_t st = (hipStream_t)stream;
         for (uint32_t round = 0; round < 4; round++)
             hipLaunchKernelGGL(gm_fit_kernel, dim3(kGmNwg, 4), dim3(kGmWg), 0, st, in(flow), h8, w8, p.delta, round,
@@ -2273,16 +2337,20 @@ extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, ui
         const bool v = vec4(4, {a, b, flow});
         const dim3 tiles((p.wc + kGmT - 1) / kGmT, (p.hc + kGmT - 1) / kGmT);
         hipLaunchKernelGGL(v ? gm_cost_kernel<true> : gm_cost_kernel<false>, tiles, dim3(kThreads), 0, st, in(a), in(b),
-                           h, w, in(flow), h8, w8, part[1], coef, maps, p.hc, p.wc);
-        // the texture window over the 5 maps (maps -> tmp), the decision window over maps 0-2 with maps 3 and 4
-        // copied (tmp -> maps), the select
-        hipLaunchKernelGGL(gm_box_kernel, dim3(tiles.x, tiles.y, 5), dim3(kThreads), 0, st, maps, tmp, 5u, p.hc, p.wc,
-                           p.r_blk);
-        hipLaunchKernelGGL(gm_box_kernel, dim3(tiles.x, tiles.y, 5), dim3(kThreads), 0, st, tmp, maps, 3u, p.hc, p.wc,
-                           p.r_dwin);
-        const uint32_t cells = h8 * w8;
-        hipLaunchKernelGGL(gm_select_kernel, dim3((cells + kThreads - 1) / kThreads), dim3(kThreads), 0, st, maps, coef,
-                           outv(flow), h8, w8, p.hc, p.wc, p.eps, p.dmin, p.tex, cells);
+                           h, w, in(flow), h8, w8, part[1], coef, raw, p.hc, p.wc);
+        // the texture window over the 5 maps (raw -> maps), then the decision window at the cells the select reads
+        // (its rows at their columns, its columns at their rows) and the select (maps -> dec, flow)
+        const uint32_t rows = kGmT + 2 * p.r_blk, nb = (rows + kGmT - 1) / kGmT;  // r <= 32: 2 .. 5 blocks a side
+        auto box = nb <= 2 ? gm_box_kernel<2> : nb == 3 ? gm_box_kernel<3> : nb == 4 ? gm_box_kernel<4> : gm_box_kernel<5>;
+        hipLaunchKernelGGL(box, dim3(tiles.x, tiles.y, 5), dim3(kThreads), (rows * rows + rows * kGmT) * 4, st, raw,
+                           maps, p.hc, p.wc, p.r_blk);
+        const bool wide = 2 * p.r_dwin + 1 > 33;
+        const uint32_t nh = 3 * p.hc * w8, ne = h8 * w8;
+        hipLaunchKernelGGL(wide ? gm_dwin_h_kernel<65> : gm_dwin_h_kernel<33>, dim3((nh + kThreads - 1) / kThreads),
+                           dim3(kThreads), 0, st, maps, hs, p.hc, p.wc, w8, p.r_dwin, nh);
+        hipLaunchKernelGGL(wide ? gm_dwin_v_select_kernel<65> : gm_dwin_v_select_kernel<33>,
+                           dim3((ne + kThreads - 1) / kThreads), dim3(kThreads), 0, st, hs, maps, coef, outv(flow), raw,
+                           h8, w8, p.hc, p.wc, p.r_dwin, p.eps, p.dmin, p.tex, ne);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "gmhs: launch failed: %s", hipGetErrorString(e));
     });

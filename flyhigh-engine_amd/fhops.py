@@ -45,7 +45,7 @@ class View:
 class GmhsPar(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in ("hc", "wc", "r_blk", "r_dwin")] + [
         (n, ctypes.c_float) for n in ("s", "dmin", "delta", "eps", "tex")] + [
-        ("ws_bytes", ctypes.c_uint64), ("maps_offset", ctypes.c_uint64)]
+        ("ws_bytes", ctypes.c_uint64), ("maps_offset", ctypes.c_uint64), ("dec_offset", ctypes.c_uint64)]
 
 
 def _v(x) -> View:
@@ -400,10 +400,14 @@ def gmhs(a, b, flow, full_w: int, level: int = 1, ws=None, stream=None):
     return ws
 
 
-def gmhs_results(ws, h: int, w: int, full_w: int, level: int = 1):
-    """(coefficients (4, 4), decision maps (5, hc, wc)) as float32 device views of a workspace after gmhs."""
+def gmhs_results(ws, h: int, w: int, full_w: int, level: int = 1, h8: int = None, w8: int = None):
+    """(coefficients (4, 4), the cost maps after the texture window (5, hc, wc), the values each E8 cell decided on
+    (5, h8, w8)) as float32 device views of a workspace after gmhs of an h8 x w8 flow (default: h // 8, w // 8)."""
     p = gmhs_params(h, w, full_w, level)
+    h8 = h // 8 if h8 is None else h8
+    w8 = w // 8 if w8 is None else w8
     import torch
     f = ws.view(torch.float32)
-    off = p["maps_offset"] // 4
-    return f[:16].view(4, 4), f[off:off + 5 * p["hc"] * p["wc"]].view(5, p["hc"], p["wc"])
+    off, doff = p["maps_offset"] // 4, p["dec_offset"] // 4
+    return (f[:16].view(4, 4), f[off:off + 5 * p["hc"] * p["wc"]].view(5, p["hc"], p["wc"]),
+            f[doff:doff + 5 * h8 * w8].view(5, h8, w8))

@@ -382,10 +382,10 @@ class GpuBackend(ComposedChains):
         ws = self.plans[key]
         p = self.fh.gmhs_params(h, w, full_w, level)
         cells = p["hc"] * p["wc"]
-        # algorithmic bytes: the flow read by 4 fit rounds and the cost maps, the two pictures' BGR, the maps written,
-        # box-filtered twice (read + written) and read by the select, the flow written
-        nbytes = 5 * 4 * 2 * h8 * w8 + 2 * 3 * 2 * h * w + 4 * cells * (5 + 2 * 5 + 2 * 5 + 3) + 4 * 2 * h8 * w8
-        self._go("gmhs (fit x4, cost, box, box + select)",
+        # algorithmic bytes: the flow read by 4 fit rounds and the cost maps, the two pictures' BGR, the 5 maps
+        # written, read and written by the texture window, maps 0-2 read by the decision window, the flow written
+        nbytes = 5 * 4 * 2 * h8 * w8 + 2 * 3 * 2 * h * w + 4 * cells * (5 + 5 + 5 + 3) + 4 * 2 * h8 * w8
+        self._go("gmhs (fit x4, cost, texture window, decision window x2)",
                  lambda: self.fh.gmhs(va, vb, vf, full_w, level, ws=ws, stream=self.stream), nbytes, kernels=8)
 
     # the fused chains (one launch each) unless asked for the ops one by one

@@ -229,10 +229,12 @@ typedef struct fhc_gmhs_par {
     float delta;            /* the fit's Huber scale */
     float eps, tex;         /* cost margin 0, texture floor 0.015 */
     uint64_t ws_bytes;      /* the workspace fhc_gmhs needs */
-    uint64_t maps_offset;   /* byte offset of the decision maps in it: f32 [5][hc][wc] (mismatch under the flow,
-                               under the affine motion, displacement difference, luma, luma^2) after a call; the
-                               affine coefficients, f32 [4][4] (a0, a1, a2, 0 per flow channel, a1 and a2 per unit
-                               of the coordinates normalised to [-1, 1]), are at byte 0 */
+    uint64_t maps_offset;   /* byte offset of the cost maps after the texture window: f32 [5][hc][wc] (mismatch
+                               under the flow, under the affine motion, displacement difference, luma, luma^2)
+                               after a call; the affine coefficients, f32 [4][4] (a0, a1, a2, 0 per flow channel, a1
+                               and a2 per unit of the coordinates normalised to [-1, 1]), are at byte 0 */
+    uint64_t dec_offset;    /* byte offset of the values each E8 cell decides on: f32 [5][h8][w8], maps 0-2 after
+                               the decision window and maps 3-4, at the cost cell the select reads for it */
 } fhc_gmhs_par;
 
 /* The stage's parameters for an h x w network of frames padded to full_w columns (gm_steps, gmhs.rs:149-160).
@@ -242,6 +244,7 @@ int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc
 /* The repair, in place on channels 0-3 of `flow` (h8 x w8, the pair's plain E8 flow: x, y towards frame a, x, y
  * towards frame b, in network pixels). a, b: the network pictures (h x w, BGR in channels 0-2, scale 1). ws: a
  * 256-byte aligned workspace of fhc_gmhs_params' ws_bytes; nothing in it need be initialised. level 0 is a no-op.
+ * The flow is the E8 grid of the network (h8 = h / 8, w8 = w / 8; a flow near the cost grid's size is an error).
  * Eight launches on `stream`. Replaces gmhs::gm_steps and its 14 dispatches. */
 int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
              uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, void* stream);

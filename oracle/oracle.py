@@ -341,6 +341,31 @@ def gm_select(maps, coef, flow, eps, dmin, tex, c0=0):
     return out
 
 
+def gm_select_cells(n8, nc):
+    """The cost-grid index the select reads for each of n8 E8 rows (or columns) of an nc-cell grid
+    (gm_select.wgsl:17-18), in float32 as there."""
+    i = np.arange(n8, dtype=np.float32)
+    v = np.floor((i + np.float32(0.5)) * np.float32(nc) / np.float32(n8)).astype(np.int64)
+    return np.clip(v, 0, nc - 1)
+
+
+def gmhs_stages(a, b, flow, full_w, level=1, a_c0=0, b_c0=0, flow_c0=0):
+    """The repair step by step (gmhs.rs:149-206): (repaired flow copy, coef (4, 4), the cost maps after the texture
+    window (5, hc, wc), the five values each E8 cell decides on (5, h8, w8): maps 0-2 after the decision window and
+    maps 3-4, at the cost cell the select reads)."""
+    _, h, w, _ = a.shape
+    _, h8, w8, _ = flow.shape
+    p = gm_params(h, w, full_w, level)
+    coef = gm_fit(flow, p["delta"], 4, flow_c0)
+    raw = gm_cost(a, b, flow, coef, p["hc"], p["wc"], a_c0, b_c0, flow_c0)
+    tex = gm_box(gm_box(raw, p["r_blk"], 0), p["r_blk"], 1)
+    final = np.concatenate([gm_box(gm_box(tex[:3], p["r_dwin"], 0), p["r_dwin"], 1), tex[3:]])
+    ys, xs = gm_select_cells(h8, p["hc"]), gm_select_cells(w8, p["wc"])
+    dec = final[:, ys[:, None], xs[None, :]]
+    out = gm_select(final, coef, flow, p["eps"], p["dmin"], p["tex"], flow_c0)
+    return out, coef, tex, dec
+
+
 def gmhs(a, b, flow, full_w, level=1, a_c0=0, b_c0=0, flow_c0=0):
     """The whole repair (gmhs.rs:149-206): (repaired flow copy, coef (4, 4), decision maps (5, hc, wc))."""
     _, h, w, _ = a.shape

@@ -1,9 +1,10 @@
 """Parity of the periodic-structure repair (fhc_gmhs, include/fhc_ops.h) with the oracle's GMHS, on the GPU.
 
-Bar: bit-exact. The affine coefficients, the five decision maps and the repaired flow equal the oracle's
-(oracle/fh_ops_oracle.c, gmhs.rs and its shaders restated) bit for bit: the fit keeps the reference's 32 workgroups
-of 256 strided lanes and their pairwise lane tree, every other value is the same f32 operations in the same order,
-and the square roots and quotients are correctly rounded on both sides. Cases: the 1080p network (864 x 480 of
+Bar: bit-exact. The affine coefficients, the five cost maps after the texture window (every cell), the five values
+each E8 cell decides on (the decision window at the cells the select reads) and the repaired flow equal the
+oracle's (oracle/fh_ops_oracle.c, gmhs.rs and its shaders restated) bit for bit: the fit keeps the reference's 32
+workgroups of 256 strided lanes and their pairwise lane tree, every other value is the same f32 operations in the
+same order, and the square roots and quotients are correctly rounded on both sides. Cases: the 1080p network (864 x 480 of
 1920-wide frames), a network as wide as its frame (the largest windows), ragged sizes whose cost grid is no multiple
 of the 16-cell tiles, the E8 flow as a view of a wider buffer, level 2, a striped scene where the select fires, and
 a workspace full of NaN (nothing in it is read before it is written).
@@ -61,17 +62,20 @@ def run(a, b, flow, full_w, level, poison=True):
         ws.view(torch.float32)[:p["ws_bytes"] // 4].fill_(float("nan"))
     fd = dev(flow)
     fh.gmhs(dev(a), dev(b), fd, full_w, level, ws=ws)
-    coef, maps = fh.gmhs_results(ws, h, w, full_w, level)
-    return host(fd).view(np.uint16), host(coef), host(maps)
+    _, h8, w8, _ = flow.shape
+    coef, maps, dec = fh.gmhs_results(ws, h, w, full_w, level, h8, w8)
+    return host(fd).view(np.uint16), host(coef), host(maps), host(dec)
 
 
 def check(a, b, flow, full_w, level, what):
-    got_flow, got_coef, got_maps = run(a, b, flow, full_w, level)
-    want_flow, want_coef, want_maps = oracle.gmhs(a, b, flow, full_w, level)
+    got_flow, got_coef, got_maps, got_dec = run(a, b, flow, full_w, level)
+    want_flow, want_coef, want_maps, want_dec = oracle.gmhs_stages(a, b, flow, full_w, level)
     assert np.array_equal(got_coef.view(np.uint32), want_coef.view(np.uint32)), f"{what}: coef {got_coef} {want_coef}"
     for k in range(5):
         bad = np.argwhere(got_maps[k].view(np.uint32) != want_maps[k].view(np.uint32))
         assert bad.size == 0, f"{what}: map {k}: {len(bad)} cells differ, first at {bad[0].tolist()}"
+        bad = np.argwhere(got_dec[k].view(np.uint32) != want_dec[k].view(np.uint32))
+        assert bad.size == 0, f"{what}: decision value {k}: {len(bad)} cells differ, first at {bad[0].tolist()}"
     bad = np.argwhere(got_flow != want_flow)
     assert bad.size == 0, f"{what}: flow: {len(bad)} elements differ, first at {bad[0].tolist()}"
     return (want_flow != flow).any(-1).sum()

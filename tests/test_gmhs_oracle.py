@@ -323,3 +323,37 @@ def test_stage_repairs_a_blob_one_period_off():
     assert np.array_equal(out[..., 4:], flow[..., 4:])
     p2 = oracle.gm_params(h, w, 2 * w, 2)
     assert p2["dmin"] == 0.0 and math.isclose(p2["delta"], 1.5)
+
+
+def test_select_cells_closed_form():
+    """The cost cell the select reads: 4i + 2 on the 1080p network's grids (hc = 4 h8), the nearest cell centre
+    otherwise (floor((i + 1/2) hc / h8), exact in f32 at these sizes)."""
+    assert np.array_equal(oracle.gm_select_cells(60, 240), 4 * np.arange(60) + 2)
+    for n8, nc in [(12, 50), (9, 45), (1, 7), (18, 75)]:
+        want = np.floor((np.arange(n8) + 0.5) * nc / n8).astype(np.int64)
+        assert np.array_equal(oracle.gm_select_cells(n8, nc), np.clip(want, 0, nc - 1))
+
+
+def test_stages_compose_to_the_stage():
+    """gmhs_stages (the steps called one by one, the decision values gathered at the select's cells) against the
+    whole stage: the same flow and coefficients, maps 3-4 untouched by the decision window, and the decision values
+    the final maps hold at the select's cells."""
+    rng = np.random.default_rng(5)
+    h, w = 100, 150
+    a = f16(rng.uniform(0, 1, (1, h, w, 4)))
+    b = np.roll(a, (2, -3), axis=(1, 2)).copy()
+    h8, w8 = h // 8, w // 8
+    flow = f16(rng.normal(0, 3, (1, h8, w8, 8)))
+    for level in (1, 2):
+        out, coef, maps = oracle.gmhs(a, b, flow, 160, level)
+        out2, coef2, tex, dec = oracle.gmhs_stages(a, b, flow, 160, level)
+        assert np.array_equal(out, out2) and np.array_equal(coef.view(np.uint32), coef2.view(np.uint32))
+        assert np.array_equal(tex[3:].view(np.uint32), maps[3:].view(np.uint32))
+        p = oracle.gm_params(h, w, 160, level)
+        ys, xs = oracle.gm_select_cells(h8, p["hc"]), oracle.gm_select_cells(w8, p["wc"])
+        assert dec.shape == (5, h8, w8)
+        assert np.array_equal(dec.view(np.uint32), maps[:, ys[:, None], xs[None, :]].view(np.uint32))
+        # the texture window alone: the oracle's box of the cost maps
+        raw = oracle.gm_cost(a, b, flow, coef, p["hc"], p["wc"])
+        want = oracle.gm_box(oracle.gm_box(raw, p["r_blk"], 0), p["r_blk"], 1)
+        assert np.array_equal(tex.view(np.uint32), want.view(np.uint32))
