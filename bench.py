@@ -274,6 +274,27 @@ def net_ops_report(args, torch, flyhighfg, stream, net_w, net_h):
                 batched_workload="8 frame pairs (A/B ops over 16 frames) and 24 mid() phases at network 864x480")
 
 
+def eager_frames(args, torch, np, stream, t=0.5):
+    """The 1080p frame of frame_1080p (committed MI355X choices, repair on) run args.eager_frames times eagerly with
+    no timing and no graph: one dispatch per launch, for profilers' counter passes."""
+    import fhconv
+    import flyhighfg_net as fnet
+    if not args.tune:
+        fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
+    W = fnet.make_weights(7)
+    be = fnet.GpuBackend(W, stream=stream, fuse=not args.no_fuse)
+    f = fnet.FlyHighFG(be, 864, 480, frame=(1920, 1080), repair=1)
+    be.upload_frames(f.frames, np.stack([fnet.procedural_frame(1920, 1080), fnet.procedural_frame(1920, 1080, 12, 0)]))
+    be.set_g(fnet.film_mlp(W, t))
+    with torch.cuda.stream(stream):
+        for _ in range(args.eager_frames):
+            f.pair()
+            f.mid(t, None)
+    stream.synchronize()
+    log(f"bench: {args.eager_frames} eager 1080p frames done")
+    return 0
+
+
 def frame_1080p(args, torch, np, stream, t=0.5, repair=1, per_launch=True):
     """The headline workload: one 1080p pair() + mid(t) as the reference's Session runs it (net/session.rs:26-66,
     Internal::Auto): two 1920x1080 RGBA8 frames (the procedural picture and the same moved 12 px) resident in HBM ->
@@ -610,6 +631,9 @@ def main():
                                         "then a copy of known size as many times: the workload of the rocprofv3 "
                                         "--pmc FETCH_SIZE / WRITE_SIZE passes")
     ap.add_argument("--pmc-reps", type=int, default=64)
+    ap.add_argument("--eager-frames", type=int, default=0,
+                    help="only run the 1080p frame (as --only-frame builds it) this many times eagerly, untimed: the "
+                         "workload of rocprofv3 counter passes over the frame's kernels")
     ap.add_argument("--detail", default=os.path.join("gpurun_out", "bench_detail.json"),
                     help="file for the full record (per-launch tables, configurations, batched launches, choice "
                          "table); '' for none")
@@ -639,6 +663,8 @@ def main():
         log(f"bench: {n_tune} choices from {args.tune}")
     net_w, net_h = 864, 480  # default_internal(1920, 1080) = (856, 480), padded to a multiple of 32
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
+    if args.eager_frames:
+        return eager_frames(args, torch, np, stream)
     if args.only_frame:
         if not args.tune:  # no autotuning here: the frame's convs take the committed MI355X choices
             fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
@@ -804,6 +830,10 @@ def main():
                     us_cold=None if us_cold is None else round(us_cold, 3), timing=cold_note,
                     per_launch_bytes=dom["bytes"], per_launch_flops=dom["flops"], traffic_source=traffic_note,
                     sustained_mfma_tflops=round(mfma_rate, 1))
+    if dom["label"].startswith("frame_render"):
+        # 1920 x 1088 lanes of bicubic sampling in the reference's f32 order: the SQ counters put it at ~900 VALU
+        # instructions per wave over 32,400 waves, the VALU issue rate of the chip, far below the HBM roofline
+        roofline["note"] = "VALU issue-bound: ~900 VALU instructions per wave, 32,400 waves (SQ counter pass)"
     log("bench: dominant launch", json.dumps(roofline))
 
     cpu = None
@@ -842,7 +872,7 @@ def emit(args, frame, conv_step, roofline, cpu, batched, detail):
             json.dump(detail, f, indent=1)
         log(f"bench: full record in {args.detail}")
     keep_roof = ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel", "us_cold", "us_warm", "timing",
-                 "per_launch_bytes", "per_launch_flops", "sustained_mfma_tflops")
+                 "per_launch_bytes", "per_launch_flops", "sustained_mfma_tflops", "note")
     line = dict(
         metric=METRIC, value=frame["frames_per_s"], unit="frames/s", n_gpus=1, steps=frame["steps"],
         warmup=frame["warmup"], ms_per_step=round(frame["us_per_frame"] / 1e3, 6), higher_is_better=True,

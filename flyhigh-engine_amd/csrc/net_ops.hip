@@ -1415,13 +1415,13 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
 // ---- GMHS: the periodic-structure repair of the pair's E8 flow (gmhs.rs:149-206) ----------------------------------
 // Eight launches where the reference records fourteen dispatches: four fit rounds (gm_fit_reduce.wgsl, each round
 // solving the previous one's normal equations first, gm_fit_solve.wgsl), the cost maps (gm_cost.wgsl, solving the
-// last round), the two box windows, box_h + box_v fused (gm_box.wgsl), and the select (gm_select.wgsl). Every value
-// is the reference kernels' arithmetic in their order: the fit keeps gm_fit_reduce's 32 workgroups of 256 lanes with
+// last round), the texture window (box_h + box_v fused, gm_box.wgsl), and the decision window at the cells the select
+// reads (its box_h at their columns, then its box_v at their rows with the select, gm_select.wgsl). Every value is
+// the reference kernels' arithmetic in their order: the fit keeps gm_fit_reduce's 32 workgroups of 256 lanes with
 // their strided per-lane sums and pairwise lane tree (its last levels as in-wave shuffles, the same pairs), so the
-// sums round as there; a box sums its clamped taps in order, from a window staged in LDS. The stage is
-// latency-bound (a few MB of L2-resident maps, 6480 flow cells at 1080p): the kernels are shaped for waves in flight,
-// one block per tile and map channel, tap loads unrolled ahead of their in-order sums; a host runs the stage beside
-// independent work (the frame program forks it beside the FiLM branch of mid()).
+// sums round as there; a box sums its clamped taps in order. The stage is latency-bound (a few MB of L2-resident
+// maps, 6480 flow cells at 1080p): the kernels are shaped for waves in flight, with every tap load of a sum issued
+// before its in-order additions.
 constexpr uint32_t kGmNwg = 32, kGmWg = 256;  // gm_fit_reduce's workgroups and workgroup size (gmhs.rs:160)
 constexpr uint32_t kGmPart = kGmNwg * 4 * 9;  // one round's partial sums [workgroup][channel][9]
 constexpr uint32_t kGmT = 16;                 // the cost kernel's block edge and the box tile's, in cells
