@@ -1212,35 +1212,85 @@ __device__ __forceinline__ void sample_rgba(const uint32_t* src, uint32_t pitch,
     }
 }
 
+// A buffer resource over `bytes` bytes at base: loads through it take a 32-bit byte offset (one 24-bit multiply-add
+// per row address instead of 64-bit address arithmetic); offsets past `bytes` read 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// sample_rgba's INNER case (every tap column inside the frame for the whole wave) through a buffer resource over
+// the frame: row y's taps at byte offset y * pitch4 + 4 (px - 1) (bicubic) or y * pitch4 + 4 px (bilinear); the same
+// taps, the same arithmetic.
+template <bool CUBIC>
+__device__ __forceinline__ void sample_rgba_inner(__amdgpu_buffer_rsrc_t rs, uint32_t pitch4, int hm1, int px, int py,
+                                                  float tx, float ty, const float* tab, float (&o)[3]) {
+    if constexpr (CUBIC) {
+        const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
+        const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+        const uint32_t col4 = (uint32_t)(px - 1) * 4u;
+        uint32_t t[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t yy = (uint32_t)min(max(py - 1 + j, 0), hm1);
+            const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, __umul24(yy, pitch4) + col4, 0, 0));
+            t[j][0] = q.x, t[j][1] = q.y, t[j][2] = q.z, t[j][3] = q.w;
+        }
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float row = unit_tab(tab, t[j][0], c) * cx[0] + unit_tab(tab, t[j][1], c) * cx[1] +
+                                  unit_tab(tab, t[j][2], c) * cx[2] + unit_tab(tab, t[j][3], c) * cx[3];
+                acc = j == 0 ? row * cy[0] : acc + row * cy[j];
+            }
+            o[c] = acc;
+        }
+    } else {
+        const uint32_t col4 = (uint32_t)px * 4u;
+        const uint32_t ya = (uint32_t)min(max(py, 0), hm1), yb = (uint32_t)min(max(py + 1, 0), hm1);
+        const uint2 q0 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, __umul24(ya, pitch4) + col4, 0, 0));
+        const uint2 q1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, __umul24(yb, pitch4) + col4, 0, 0));
+#pragma unroll
+        for (int c = 0; c < 3; c++)
+            o[c] = bil4(unit_tab(tab, q0.x, c), unit_tab(tab, q0.y, c), unit_tab(tab, q1.x, c), unit_tab(tab, q1.y, c), tx,
+                        ty);
+    }
+}
+
 // render_pix of the padded frame (hp x wp) from the two RGBA8 frames, written as RGBA8 (rgba_out of the f16 result),
 // cropped to w x h: render.wgsl:83-160 with its sources replaced by rgba_in.wgsl's conversion of the frames, then
 // rgba_out.wgsl. One lane per frame pixel. QV: flow and vis are channels 0-3 and 4-6 of one 8-channel view (16-byte
 // pixels) and rt has 8-byte pixels, so each quarter-map tap is two loads. A wave whose sample windows all lie inside
 // the frame takes the unclamped tap loads (the same values: clamping changes no column there).
+// A block is 64 x 4 pixels (a wave per row segment); sh = hq / hp and sw = wq / wp come from the host (the same f32
+// quotients the reference forms per pixel).
 template <bool CUBIC, bool QV>
 __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
-                                                               uint32_t h, uint32_t pitch, uint32_t hp, uint32_t wp,
+                                                               uint32_t h, uint32_t pitch, float sh, float sw,
                                                                View fl, View vis, View rt, uint32_t hq, uint32_t wq,
                                                                float fsx, float fsy, uint32_t flags, uint32_t* dst,
-                                                               uint32_t opitch, uint32_t items) {
+                                                               uint32_t opitch) {
     __shared__ float tab[256];
     fill_unit_table(tab);
-    const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
-    if (pix >= items) return;
-    const uint32_t x = pix % w, y = pix / w;
-    const float sh = (float)hq / (float)hp, sw = (float)wq / (float)wp;
+    const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63u), y = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (x >= w || y >= h) return;
     const float iy = ((float)y + 0.5f) * sh - 0.5f, ix = ((float)x + 0.5f) * sw - 0.5f;
     const int qy0 = (int)floorf(iy), qx0 = (int)floorf(ix);
     const float qfy = iy - (float)qy0, qfx = ix - (float)qx0;
     const uint32_t y0 = clampi(qy0, 0, (int)hq - 1), y1 = clampi(qy0 + 1, 0, (int)hq - 1);
     const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
-    const size_t qs[4] = {(size_t)y0 * wq + x0, (size_t)y0 * wq + x1, (size_t)y1 * wq + x0, (size_t)y1 * wq + x1};
+    const uint32_t r0 = __umul24(y0, wq), r1 = __umul24(y1, wq);
+    const uint32_t qs[4] = {r0 + x0, r0 + x1, r1 + x0, r1 + x1};
     float fq[4][4], vq[4][3], rq[4][3];
+    const uint32_t nq = hq * wq;
+    const auto rfl = buf_rsrc(fl.p, QV ? nq * 16u : 0u), rrt = buf_rsrc(rt.p, QV ? nq * rt.cs * 2u : 0u);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         if constexpr (QV) {
-            const uint4 a = *reinterpret_cast<const uint4*>(fl.p + qs[k] * fl.cs);
-            const uint2 r = *reinterpret_cast<const uint2*>(rt.p + qs[k] * rt.cs + rt.c0);
+            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rfl, qs[k] * 16u, 0, 0));
+            const uint2 r =
+                __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rrt, (qs[k] * rt.cs + rt.c0) * 2u, 0, 0));
             const uint32_t wv[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
             for (int c = 0; c < 4; c++) fq[k][c] = h2f((uint16_t)(wv[c >> 1] >> (16 * (c & 1))));
@@ -1273,15 +1323,18 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
     const int lo = CUBIC ? 1 : 0, hi = (int)w - (CUBIC ? 3 : 2);
     const bool inner = pxa >= lo && pxa <= hi && pxb >= lo && pxb <= hi;
     if (__all(inner)) {
-        sample_rgba<CUBIC, true>(fa, pitch, w, h, pxa, pya, txa, tya, tab, ca);
-        sample_rgba<CUBIC, true>(fb, pitch, w, h, pxb, pyb, txb, tyb, tab, cb);
+        const uint32_t fbytes = ((h - 1) * pitch + w) * 4u, pitch4 = pitch * 4u;
+        sample_rgba_inner<CUBIC>(buf_rsrc(fa, fbytes), pitch4, (int)h - 1, pxa, pya, txa, tya, tab, ca);
+        sample_rgba_inner<CUBIC>(buf_rsrc(fb, fbytes), pitch4, (int)h - 1, pxb, pyb, txb, tyb, tab, cb);
     } else {
         sample_rgba<CUBIC, false>(fa, pitch, w, h, pxa, pya, txa, tya, tab, ca);
         sample_rgba<CUBIC, false>(fb, pitch, w, h, pxb, pyb, txb, tyb, tab, cb);
     }
     float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
     const float third = 1.0f / 3.0f;
-    const float ef = fabsf(ca[0] - cb[0]) * third + fabsf(ca[1] - cb[1]) * third + fabsf(ca[2] - cb[2]) * third;
+    float ef = 0.0f;
+    if (flags)
+        ef = fabsf(ca[0] - cb[0]) * third + fabsf(ca[1] - cb[1]) * third + fabsf(ca[2] - cb[2]) * third;
     if (flags & 2u) {  // the still test (render.wgsl:134-148) on the 3 x 3 neighbourhood, clamped to the frame
         uint32_t ta[3][4], tb[3][4];
 #pragma unroll
@@ -2279,18 +2332,25 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
         FHC_TRY(check_frames("render_rgba a", a, 1, w, h, pitch, 0, hp, wp));
         FHC_TRY(check_frames("render_rgba b", b, 1, w, h, pitch, 0, hp, wp));
         FHC_TRY(check_frames("render_rgba out", out, 1, w, h, opitch, 0, hp, wp));
+        // the tap rows' 32-bit byte offsets (24-bit row multiply) and the quarter maps' buffer sizes
+        if ((uint64_t)pitch * 4 >= (1u << 24) || (uint64_t)h * pitch * 4 >= (1u << 31) ||
+            (uint64_t)hq * wq * std::max(16u, 2 * rt->cstride) >= (1u << 31) || hq >= (1u << 24) || wq >= (1u << 24))
+            return fail(-1, "render_rgba: frame (pitch %u, %u rows) or quarter maps (%u x %u) too large", pitch, h, wq, hq);
         FHC_TRY(check(flow, "render_rgba flow", 4, false));
         FHC_TRY(check(vis, "render_rgba vis", 3, true));
         FHC_TRY(check(rt, "render_rgba rt", 3, false));
         const bool qv = flow->p == vis->p && flow->cstride == 8 && vis->cstride == 8 && flow->c0 == 0 &&
                         vis->c0 == 4 && reinterpret_cast<uintptr_t>(flow->p) % 16 == 0 && vec4(4, {rt});
-        return launch("render_rgba", (uint64_t)h * w, [&](dim3 g, uint32_t items) {
-            auto k = cubic ? (qv ? render_rgba_kernel<true, true> : render_rgba_kernel<true, false>)
-                           : (qv ? render_rgba_kernel<false, true> : render_rgba_kernel<false, false>);
-            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, static_cast<const uint32_t*>(a),
-                               static_cast<const uint32_t*>(b), w, h, pitch, hp, wp, in(flow), in(vis), in(rt), hq,
-                               wq, fsx, fsy, flags, static_cast<uint32_t*>(out), opitch, items);
-        });
+        if ((uint64_t)h * w >= kMaxItems || h > 4u * 65535u)
+            return fail(-1, "render_rgba: %u x %u pixels exceed the launch limits", w, h);
+        auto k = cubic ? (qv ? render_rgba_kernel<true, true> : render_rgba_kernel<true, false>)
+                       : (qv ? render_rgba_kernel<false, true> : render_rgba_kernel<false, false>);
+        hipLaunchKernelGGL(k, dim3((w + 63) / 64, (h + 3) / 4), dim3(kThreads), 0, (hipStream_t)stream,
+                           static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h, pitch,
+                           (float)hq / (float)hp, (float)wq / (float)wp, in(flow), in(vis), in(rt), hq, wq, fsx, fsy,
+                           flags, static_cast<uint32_t*>(out), opitch);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "render_rgba: launch failed: %s", hipGetErrorString(e));
     });
 }
 
