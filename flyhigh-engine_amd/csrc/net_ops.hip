@@ -1380,7 +1380,7 @@ template <int KM, int R>
 __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* src, uint32_t w, uint32_t h,
                                                                uint32_t pitch, uint64_t fstride, uint32_t ih,
                                                                uint32_t iw, OView out, uint32_t oh, uint32_t ow,
-                                                               uint32_t tiles_x, uint32_t tiles_y) {
+                                                               uint32_t tiles_x, uint32_t tiles_y, float sh, float sw) {
     constexpr uint32_t EXT = kAaT * R;
     // the staged window in f32 (37 KiB at R 3: no widening per tap) or, for the 80-pixel window, in f16
     constexpr bool F32 = R <= 3;
@@ -1393,8 +1393,7 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
     const uint32_t bt = blockIdx.x, txi = bt % tiles_x, rr = bt / tiles_x, tyi = rr % tiles_y, img = rr / tiles_y;
     const uint32_t ox0 = txi * kAaT, oy0 = tyi * kAaT;
     const uint32_t ox_last = min(ox0 + kAaT, ow) - 1, oy_last = min(oy0 + kAaT, oh) - 1;
-    const float sh = (float)ih / (float)oh, sw = (float)iw / (float)ow;
-    const float fsh = fmaxf(sh, 1.0f), fsw = fmaxf(sw, 1.0f);
+    const float fsh = fmaxf(sh, 1.0f), fsw = fmaxf(sw, 1.0f);  // sh = ih / oh, sw = iw / ow from the host
     const int ylo = max(0, (int)floorf(((float)oy0 + 0.5f) * sh - fsh + 0.5f));
     const int yhi = min((int)ih, (int)floorf(((float)oy_last + 0.5f) * sh + fsh + 0.5f));
     const int xlo = max(0, (int)floorf(((float)ox0 + 0.5f) * sw - fsw + 0.5f));
@@ -1420,13 +1419,17 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
         }
     }
     __syncthreads();
-    const uint32_t* frame = src + img * fstride;
+    // the frame through a buffer resource: a tap's byte offset is one 24-bit multiply-add
+    const auto rf = buf_rsrc(src + img * fstride, ((h - 1) * pitch + w) * 4u);
+    const uint32_t pitch4 = pitch * 4u;
 #pragma unroll
     for (uint32_t i = 0; i < R; i++)
 #pragma unroll
         for (uint32_t j = 0; j < R; j++) {
             const int row = min((int)(ty + kAaT * i), ny - 1), col = min((int)(tx + kAaT * j), nx - 1);
-            const uint32_t v = frame[(size_t)min(ylo + row, (int)h - 1) * pitch + min(xlo + col, (int)w - 1)];
+            const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(
+                rf, __umul24((uint32_t)min(ylo + row, (int)h - 1), pitch4) + (uint32_t)min(xlo + col, (int)w - 1) * 4u,
+                0, 0);
             if constexpr (F32)
                 tile[row * EXT + col] = float4{unit_tab(tab, v, 0), unit_tab(tab, v, 1), unit_tab(tab, v, 2), 0.0f};
             else
@@ -2312,8 +2315,11 @@ extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_
         auto k = ext <= 3 * kAaT
                      ? (taps <= 5 ? rgba_resize_kernel<5, 3> : taps <= 6 ? rgba_resize_kernel<6, 3> : rgba_resize_kernel<8, 3>)
                      : (taps <= 6 ? rgba_resize_kernel<6, 5> : rgba_resize_kernel<8, 5>);
+        if ((uint64_t)pitch * 4 >= (1u << 24) || (uint64_t)h * pitch * 4 >= (1u << 31))
+            return fail(-1, "rgba_resize: frames of pitch %u and %u rows are too large", pitch, h);
         hipLaunchKernelGGL(k, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream,
-                           static_cast<const uint32_t*>(rgba), w, h, pitch, fstride, hp, wp, outv(out), oh, ow, tx, ty);
+                           static_cast<const uint32_t*>(rgba), w, h, pitch, fstride, hp, wp, outv(out), oh, ow, tx, ty,
+                           (float)hp / (float)oh, (float)wp / (float)ow);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "rgba_resize: launch failed: %s", hipGetErrorString(e));
     });
