@@ -451,7 +451,11 @@ template <int KM, bool PYR, bool V4>
 __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView out, uint32_t ih, uint32_t iw,
                                                                  uint32_t oh, uint32_t ow, uint32_t c,
                                                                  uint32_t tiles_x, uint32_t tiles_y, PyrOut pyr) {
-    __shared__ uint2 tile[kAaExt * kAaExt];
+    // rows of kAaExt + 1 cells: the last cell of each row, and a whole extra row, hold zeros, the value every tap
+    // outside its pixel's window reads (times its weight +0 it adds +0 to the sums, which never hold -0: what the
+    // reference's skipped tap leaves, for any input values)
+    constexpr uint32_t S = kAaExt + 1;
+    __shared__ uint2 tile[S * kAaExt + S];
     __shared__ float qt[PYR ? kAaT * kAaT * 3 : 1], q8[PYR ? 64 * 3 : 1];
     const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
     const uint32_t bt = blockIdx.x, txi = bt % tiles_x, r = bt / tiles_x, tyi = r % tiles_y, img = r / tiles_y;
@@ -472,15 +476,17 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
             const int row = min((int)(ty + kAaT * i), ny - 1), col = min((int)(tx + kAaT * j), nx - 1);
             const uint16_t* src = x.p + ((rowbase + row) * iw + xlo + col) * x.cs + x.c0;
             if constexpr (V4) {  // channels past c are never read from the tile
-                tile[row * kAaExt + col] = *reinterpret_cast<const uint2*>(src);
+                tile[row * S + col] = *reinterpret_cast<const uint2*>(src);
             } else {
                 uint16_t v[4];
 #pragma unroll
                 for (uint32_t k = 0; k < 4; k++) v[k] = src[min(k, c - 1)];
-                tile[row * kAaExt + col] =
+                tile[row * S + col] =
                     uint2{(uint32_t)v[0] | ((uint32_t)v[1] << 16), (uint32_t)v[2] | ((uint32_t)v[3] << 16)};
             }
         }
+    if (tid < kAaExt) tile[tid * S + kAaExt] = uint2{0u, 0u};  // the zero column
+    if (tid < S) tile[kAaExt * S + tid] = uint2{0u, 0u};       // the zero row
     __syncthreads();
     const uint32_t ox = ox0 + tx, oy = oy0 + ty;
     const bool valid = ox < ow && oy < oh;
@@ -495,23 +501,22 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
     for (int j = 0; j < KM; j++) {
         const int xx = xmin + j;
         wx[j] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
-        lc[j] = min(max(xx - xlo, 0), nx - 1);
+        lc[j] = xx < xmax ? xx - xlo : (int)kAaExt;
     }
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, norm = 0.0f;
 #pragma unroll
     for (int jy = 0; jy < KM; jy++) {
         const int y = ymin + jy;
         const float wy = y < ymax ? fmaxf(0.0f, 1.0f - fabsf(((float)y + 0.5f - cy) / fsh)) : 0.0f;
-        const uint2* lrow = tile + min(max(y - ylo, 0), ny - 1) * kAaExt;
+        const uint2* lrow = tile + (y < ymax ? (y - ylo) * (int)S : (int)(kAaExt * S));
 #pragma unroll
         for (int jx = 0; jx < KM; jx++) {
-            const bool in = (y < ymax) & (xmin + jx < xmax);
             const float wgt = wx[jx] * wy;
             const uint2 q = lrow[lc[jx]];
             const float v[4] = {h2f((uint16_t)q.x), h2f((uint16_t)(q.x >> 16)), h2f((uint16_t)q.y),
                                 h2f((uint16_t)(q.y >> 16))};
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] = acc[i] + (in ? v[i] : 0.0f) * wgt;
+            for (int i = 0; i < 4; i++) acc[i] = acc[i] + v[i] * wgt;
             norm = norm + wgt;
         }
     }
