@@ -815,29 +815,24 @@ __device__ __forceinline__ void blend_at(const View& q, const View& fl, const Vi
     }
 }
 
-// One workgroup per 16 x 16 pixels: each lane's blend goes to LDS, 33 lanes add the blends of the column to the
-// right and the row below (clamped to the picture; unused past its edge), and the gradient reads them from there.
-__global__ __launch_bounds__(kThreads) void refine_input_kernel(View q, View fl, View vis, OView rx, uint32_t h,
-                                                                uint32_t w, float fs, uint32_t tiles_x) {
-    __shared__ float bt[17 * 17 * 3];
-    const uint32_t tx = threadIdx.x % 16, ty = threadIdx.x / 16;
-    const uint32_t x0 = (blockIdx.x % tiles_x) * 16, y0 = (blockIdx.x / tiles_x) * 16;
+// One wave per 7 x 7 output pixels: each lane computes the blend of one pixel of the 8 x 8 block around them (the
+// block's last column and row are the right and lower neighbours of its outputs; clamped to the picture, unused past
+// its edge), so no lane computes two; the gradient reads the neighbours' blends from LDS.
+constexpr uint32_t kRiT = 7;
+__global__ __launch_bounds__(64) void refine_input_kernel(View q, View fl, View vis, OView rx, uint32_t h, uint32_t w,
+                                                          float fs, uint32_t tiles_x) {
+    __shared__ float bt[8 * 8 * 3];
+    const uint32_t tx = threadIdx.x % 8, ty = threadIdx.x / 8;
+    const uint32_t x0 = (blockIdx.x % tiles_x) * kRiT, y0 = (blockIdx.x / tiles_x) * kRiT;
     const uint32_t x = x0 + tx, y = y0 + ty;
     float ra[3], rb[3], bl[3];
     blend_at(q, fl, vis, min(x, w - 1), min(y, h - 1), h, w, ra, rb, bl);
 #pragma unroll
-    for (uint32_t ch = 0; ch < 3; ch++) bt[(ty * 17 + tx) * 3 + ch] = bl[ch];
-    if (threadIdx.x < 33) {  // the halo: (16, 0..16) and (0..15, 16)
-        const uint32_t hx = threadIdx.x < 17 ? 16 : threadIdx.x - 17, hy = threadIdx.x < 17 ? threadIdx.x : 16;
-        float na[3], nb[3], nl[3];
-        blend_at(q, fl, vis, min(x0 + hx, w - 1), min(y0 + hy, h - 1), h, w, na, nb, nl);
-#pragma unroll
-        for (uint32_t ch = 0; ch < 3; ch++) bt[(hy * 17 + hx) * 3 + ch] = nl[ch];
-    }
+    for (uint32_t ch = 0; ch < 3; ch++) bt[(ty * 8 + tx) * 3 + ch] = bl[ch];
     __syncthreads();
-    if (x >= w || y >= h) return;
-    const float* br = bt + (ty * 17 + tx + 1) * 3;
-    const float* bd = bt + ((ty + 1) * 17 + tx) * 3;
+    if (tx >= kRiT || ty >= kRiT || x >= w || y >= h) return;
+    const float* br = bt + (ty * 8 + tx + 1) * 3;
+    const float* bd = bt + ((ty + 1) * 8 + tx) * 3;
     const size_t pix = (size_t)y * w + x;
     uint16_t* o = rx.p + pix * rx.cs + rx.c0;
 #pragma unroll
@@ -2151,11 +2146,12 @@ extern "C" int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, con
         FHC_TRY(check(flow, "refine_input flow", 4, true));
         FHC_TRY(check(vis, "refine_input vis", 3, true));
         FHC_TRY(check(rx, "refine_input rx", 14, false, true));
-        const uint32_t tx = (w + 15) / 16, ty = (h + 15) / 16;
-        return launch("refine_input", (uint64_t)tx * ty * kThreads, [&](dim3 g, uint32_t) {
-            hipLaunchKernelGGL(refine_input_kernel, g, dim3(kThreads), 0, (hipStream_t)stream, in(q), in(flow),
-                               in(vis), outv(rx), h, w, flow_out_scale, tx);
-        });
+        const uint32_t tx = (w + kRiT - 1) / kRiT, ty = (h + kRiT - 1) / kRiT;
+        if ((uint64_t)tx * ty >= kMaxItems / 64) return fail(-1, "refine_input: %u x %u is too large", w, h);
+        hipLaunchKernelGGL(refine_input_kernel, dim3(tx * ty), dim3(64), 0, (hipStream_t)stream, in(q), in(flow),
+                           in(vis), outv(rx), h, w, flow_out_scale, tx);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "refine_input: launch failed: %s", hipGetErrorString(e));
     });
 }
 
