@@ -159,11 +159,12 @@ __global__ __launch_bounds__(kThreads) void sad_kernel(View la, View lb, OView o
 }
 
 // ---- convex upsample: shaders/convex.wgsl:12-34 ------------------------------------------------------------------
-// A workgroup computes 16 x 16 output pixels (8 x 8 input pixels, 4 sub-pixels each): it stages the 36 weight
-// channels of its input pixels and the 10 x 10 neighbourhood of x (zeros outside the image: adding 0 * weight is
-// what the reference's zero branch adds) in LDS with coalesced reads, then one lane per output pixel computes its
-// softmax once and every channel from LDS, in the reference's order.
-constexpr uint32_t kCvIn = 8, kCvHalo = kCvIn + 2;
+// A workgroup (one wave) computes 8 x 8 output pixels (4 x 4 input pixels, 4 sub-pixels each): it stages the 36
+// weight channels of its input pixels and the 6 x 6 neighbourhood of x (zeros outside the image: adding 0 * weight
+// is what the reference's zero branch adds) in LDS with coalesced reads, then one lane per output pixel computes its
+// softmax once and every channel from LDS, in the reference's order. Small tiles: the frame's quarter maps are
+// 60 x 108 input pixels, and one wave per 16 outputs' worth of inputs spreads them over every CU.
+constexpr uint32_t kCvIn = 4, kCvHalo = kCvIn + 2, kCvThreads = 4 * kCvIn * kCvIn;
 
 // FVT: x is mid()'s flow_t | vis_t (7 channels), computed while staging from fv (flow 0-3, vis 4-6) and the FiLM
 // head's output df (d_flow 0-3, d_mask 4) with flow_vis_t_kernel's arithmetic, so that x is never stored: the same
@@ -182,19 +183,19 @@ __device__ __forceinline__ void flow_vis_t_at(const View& fv, const View& df, si
 }
 
 template <bool FVT>
-__global__ __launch_bounds__(kThreads) void convex_tile_kernel(View wt, View x, OView out, uint32_t h, uint32_t w,
+__global__ __launch_bounds__(kCvThreads) void convex_tile_kernel(View wt, View x, OView out, uint32_t h, uint32_t w,
                                                                uint32_t c, uint32_t tiles_x, uint32_t tiles_y,
                                                                View fv, View df, float af, float ab) {
     extern __shared__ __align__(16) uint16_t lds[];
     uint16_t* lw = lds;                       // [kCvIn * kCvIn][36]
     uint16_t* lx = lds + kCvIn * kCvIn * 36;  // [kCvHalo * kCvHalo][c]
-    const uint32_t tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
+    const uint32_t tid = threadIdx.x, tx = tid % (2 * kCvIn), ty = tid / (2 * kCvIn);
     const uint32_t bt = blockIdx.x, txi = bt % tiles_x, r = bt / tiles_x, tyi = r % tiles_y, img = r / tiles_y;
     const int ix0 = (int)(txi * kCvIn), iy0 = (int)(tyi * kCvIn);
     // staging with every load unconditional (clamped to the image / the view) and unrolled, so they issue together
 #pragma unroll
-    for (uint32_t k = 0; k < (kCvIn * kCvIn * 9 + kThreads - 1) / kThreads; k++) {  // 9 quads of 4 channels a pixel
-        const uint32_t e = min(tid + k * kThreads, kCvIn * kCvIn * 9 - 1);
+    for (uint32_t k = 0; k < (kCvIn * kCvIn * 9 + kCvThreads - 1) / kCvThreads; k++) {  // 9 quads of 4 channels a pixel
+        const uint32_t e = min(tid + k * kCvThreads, kCvIn * kCvIn * 9 - 1);
         const uint32_t p = e / 9, q = e - p * 9, py = p / kCvIn, px = p % kCvIn;
         const int gy = min(iy0 + (int)py, (int)h - 1), gx = min(ix0 + (int)px, (int)w - 1);
         const uint16_t* src = wt.p + (((size_t)img * h + gy) * w + gx) * wt.cs + wt.c0 + q * 4;
@@ -1906,7 +1907,7 @@ extern "C" int fhc_convex_upsample(const fhc_tensor* wt, const fhc_tensor* x, co
         if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "convex_upsample: too many tiles");
         const size_t lds = (kCvIn * kCvIn * 36 + kCvHalo * kCvHalo * c) * 2;
         const View none{nullptr, 0, 0, 1.0f};
-        hipLaunchKernelGGL(convex_tile_kernel<false>, dim3(n * tx * ty), dim3(kThreads), lds, (hipStream_t)stream,
+        hipLaunchKernelGGL(convex_tile_kernel<false>, dim3(n * tx * ty), dim3(kCvThreads), lds, (hipStream_t)stream,
                            in(wt), in(x), outv(out), h, w, c, tx, ty, none, none, 0.0f, 0.0f);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "convex_upsample: launch failed: %s", hipGetErrorString(e));
@@ -2468,7 +2469,7 @@ extern "C" int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv,
         const size_t lds = (kCvIn * kCvIn * 36 + kCvHalo * kCvHalo * 7) * 2;
         const float af = 2.0f * t, ab = 2.0f * (1.0f - t);  // the mul_t factors (net/build.rs:293)
         const View none{nullptr, 0, 0, 1.0f};
-        hipLaunchKernelGGL(convex_tile_kernel<true>, dim3(n * tx * ty), dim3(kThreads), lds, (hipStream_t)stream,
+        hipLaunchKernelGGL(convex_tile_kernel<true>, dim3(n * tx * ty), dim3(kCvThreads), lds, (hipStream_t)stream,
                            in(wt), none, outv(out), h, w, 7u, tx, ty, in(fv), in(dfilm), af, ab);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "flow_vis_t_convex: launch failed: %s", hipGetErrorString(e));
