@@ -700,10 +700,10 @@ __global__ __launch_bounds__(kThreads) void pair_pyramid_kernel(View q, OView i8
 // slices of the block's input fx (c0: wa, +c: wb, +2c: ia, +2c+3: ib, +2c+6: flow8). One lane per (pixel, task):
 // tasks 0 .. 2G-1 warp 4 feature channels (G groups per map), 2G and 2G+1 a picture with its luma, 2G+2 the flow.
 // The coarse head's output resized to the fine grid (coarse_up_kernel's arithmetic): channel ch of out pixel (x, y)
-// (h x w) bilinear from o (hi x wi), times fs for the flow channels 0-3, as the f16 coarse_up stores.
-__device__ __forceinline__ uint16_t coarse_up_at(const View& o, uint32_t hi, uint32_t wi, uint32_t h, uint32_t w,
+// (h x w) bilinear from o (hi x wi; sh = hi / h, sw = wi / w), times fs for the flow channels 0-3, as the f16
+// coarse_up stores.
+__device__ __forceinline__ uint16_t coarse_up_at(const View& o, uint32_t hi, uint32_t wi, float sh, float sw,
                                                  float fs, uint32_t x, uint32_t y, uint32_t ch) {
-    const float sh = (float)hi / (float)h, sw = (float)wi / (float)w;
     const float fiy = ((float)y + 0.5f) * sh - 0.5f, fix = ((float)x + 0.5f) * sw - 0.5f;
     const int y0 = (int)floorf(fiy), x0 = (int)floorf(fix);
     const float fy = fiy - (float)y0, fx = fix - (float)x0;
@@ -718,11 +718,15 @@ __device__ __forceinline__ uint16_t coarse_up_at(const View& o, uint32_t hi, uin
 // the two flow channels it warps by (read at fl.scale, as the flow view of the fine block reads the stored fv), and
 // the flow task also stores all 7 channels into fv (flow times fs, vis) and the flow16 copy into the state (the
 // lanes whose pixel index falls in the coarse grid), as coarse_up_kernel does.
+// Lanes: a pixel's 2 groups + 3 tasks are consecutive, so the group lanes of a tap pixel read one cache line
+// (measured faster than waves of one task over 64 pixels, whose lanes each touch their own line). csh = hi / h and
+// csw = wi / w come from the host.
 template <bool VEC, bool UP>
 __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, View fl, OView fx, OView l8,
                                                               uint32_t h, uint32_t w, uint32_t c, uint32_t groups,
                                                               uint32_t items, View o, OView fv, OView state,
-                                                              uint32_t hi, uint32_t wi, float fs) {
+                                                              uint32_t hi, uint32_t wi, float fs, float csh,
+                                                              float csw) {
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     if (t >= items) return;
     const uint32_t tasks = 2 * groups + 3, pix = t / tasks, task = t - pix * tasks;
@@ -731,8 +735,8 @@ __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, 
         const uint32_t img = task < 2 * groups ? task / groups : task - 2 * groups;
         float fxv, fyv;
         if constexpr (UP) {
-            fxv = h2f(coarse_up_at(o, hi, wi, h, w, fs, x, y, 2 * img)) * fl.scale;
-            fyv = h2f(coarse_up_at(o, hi, wi, h, w, fs, x, y, 2 * img + 1)) * fl.scale;
+            fxv = h2f(coarse_up_at(o, hi, wi, csh, csw, fs, x, y, 2 * img)) * fl.scale;
+            fyv = h2f(coarse_up_at(o, hi, wi, csh, csw, fs, x, y, 2 * img + 1)) * fl.scale;
         } else {
             fxv = ld(fl, pix, 2 * img) * fl.scale, fyv = ld(fl, pix, 2 * img + 1) * fl.scale;
         }
@@ -758,7 +762,7 @@ __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, 
         if constexpr (UP) {
 #pragma unroll
             for (uint32_t ch = 0; ch < 7; ch++) {
-                v[ch] = coarse_up_at(o, hi, wi, h, w, fs, x, y, ch);
+                v[ch] = coarse_up_at(o, hi, wi, csh, csw, fs, x, y, ch);
                 fv.p[(size_t)pix * fv.cs + fv.c0 + ch] = v[ch];
             }
             if (state.p && x < wi && y < hi) {
@@ -2117,7 +2121,7 @@ extern "C" int fhc_fine_input(const fhc_tensor* f8, const fhc_tensor* i8, const 
         return launch("fine_input", (uint64_t)h * w * (2 * groups + 3), [&](dim3 g, uint32_t n) {
             auto k = v ? fine_input_kernel<true, false> : fine_input_kernel<false, false>;
             hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8), in(flow), outv(fx),
-                               outv(l8), h, w, c, groups, n, none, onone, onone, 0u, 0u, 0.0f);
+                               outv(l8), h, w, c, groups, n, none, onone, onone, 0u, 0u, 0.0f, 0.0f, 0.0f);
         });
     });
 }
@@ -2450,7 +2454,8 @@ extern "C" int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, 
         return launch("coarse_fine_input", (uint64_t)h * w * (2 * groups + 3), [&](dim3 g, uint32_t n) {
             auto k = v ? fine_input_kernel<true, true> : fine_input_kernel<false, true>;
             hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8), fl, outv(fx), outv(l8),
-                               h, w, c, groups, n, in(o), outv(fv), sv, hi, wi, flow_scale);
+                               h, w, c, groups, n, in(o), outv(fv), sv, hi, wi, flow_scale, (float)hi / (float)h,
+                               (float)wi / (float)w);
         });
     });
 }
