@@ -1,0 +1,118 @@
+"""The fused op chains of the frame, each one launch, against the same chains run op by op on the GPU, at shapes the
+1080p frame does not have.
+
+Bar: bit-exact. Each op of a chain is pinned to the oracle by its own parity test (test_ops_gpu.py), and a chain's
+launch computes the same f32 operations with the same roundings, so its outputs must equal the op-by-op outputs bit
+for bit. The whole-frame check (test_frame.py::test_fused_chains_equal_their_ops_on_the_gpu) covers the chains at
+the 1080p frame's shapes; here, for the coarse output with the fine block's input, flow_t / vis_t with the convex
+upsample, the pictures' resize with the pyramid and the refine head's input: ragged grids whose coarse-to-fine ratio
+is no integer, downscales other than 4x, channel counts that are no multiple of 4 (the 2-byte path), views into wider
+buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample.
+"""
+import numpy as np
+import pytest
+
+import fhtest  # noqa: F401 (puts the package and the oracle on the path)
+import flyhighfg_net as net
+from flyhighfg_net import V
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def backends():
+    import torch
+    W = net.make_weights(3)
+    s = torch.cuda.current_stream()
+    return net.GpuBackend(W, stream=s, chains=True), net.GpuBackend(W, stream=s, chains=False)
+
+
+def fill(be, rng, n, h, w, cs, lo=-1.0, hi=1.0):
+    return be.upload(rng.uniform(lo, hi, (n, h, w, cs)).astype(np.float16).view(np.uint16))
+
+
+def same(a, b, what):
+    bad = np.argwhere(a != b)
+    assert bad.size == 0, f"{what}: {len(bad)} elements differ, first at {bad[0].tolist()}"
+
+
+# coarse grid (hi, wi), fine grid (h, w), the fine block's feature channels c and their view's channel stride, the
+# flow16 state (or none), the fine block's flow read scale
+CFI_CASES = [
+    (5, 9, 13, 21, 36, 40, True, 0.125),    # ragged ratio, the frame's 36 channels (8-byte path)
+    (7, 6, 20, 11, 6, 9, False, 0.125),     # 6 channels (2-byte path), no state, views into wider buffers
+    (30, 54, 60, 108, 12, 16, True, 1.0),   # the frame's grids, 12 channels, read scale 1
+]
+
+
+@pytest.mark.parametrize("hi,wi,h,w,c,cs,state,fine_scale", CFI_CASES)
+def test_coarse_fine_input_equals_coarse_up_then_fine_input(hi, wi, h, w, c, cs, state, fine_scale):
+    say("coarse_fine_input", hi, wi, h, w, c, cs, state, fine_scale)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(hi * 1000 + w)
+        o = fill(be, rng, 1, hi, wi, 16, -3.0, 3.0)
+        f8 = fill(be, rng, 2, h, w, cs)
+        i8 = fill(be, rng, 2, h, w, 4, 0.0, 1.0)
+        fv = fill(be, rng, 1, h, w, 8)
+        fx = fill(be, rng, 1, h, w, 2 * c + 12)
+        l8 = fill(be, rng, 1, h, w, 4)
+        st = fill(be, rng, 1, hi, wi, 80) if state else None
+        be.coarse_fine_input(V(o), V(fv), None if st is None else V(st, 72), 16.0, V(f8, cs - c), V(i8), fine_scale,
+                             V(fx, 1), V(l8, 1), c)
+        outs.append({k: be.host(t).copy() for k, t in (("fv", fv), ("fx", fx), ("l8", l8), ("state", st))
+                     if t is not None})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k)
+
+
+@pytest.mark.parametrize("n,h,w,t", [(2, 9, 13, 0.3), (1, 60, 108, 0.5), (1, 5, 4, 1.0)])
+def test_flow_vis_t_convex_equals_flow_vis_t_then_convex(n, h, w, t):
+    say("flow_vis_t_convex", n, h, w, t)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(n * 100 + h)
+        wt = fill(be, rng, n, h, w, 40, -4.0, 4.0)
+        fv = fill(be, rng, n, h, w, 8, -2.0, 2.0)
+        df = fill(be, rng, n, h, w, 8)
+        # the op-by-op chain's intermediates: dvis's third channel is the graph's constant zero, never written
+        scratch = [be.zeros(n, h, w, 8) for _ in range(3)]
+        out = fill(be, rng, n, 2 * h, 2 * w, 8)
+        be.flow_vis_t_convex(V(wt, 2), V(fv), V(df, 1), t, V(out), *(V(x) for x in scratch))
+        outs.append(be.host(out).copy())
+    same(outs[0], outs[1], "out")
+
+
+@pytest.mark.parametrize("H,W,oh,ow", [(100, 150, 24, 36), (200, 328, 48, 80), (64, 64, 16, 16)])
+def test_pair_input_equals_resize_then_pyramid(H, W, oh, ow):
+    say("pair_input", H, W, oh, ow)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(H + ow)
+        ab = fill(be, rng, 2, H, W, 4, 0.0, 1.0)
+        q = fill(be, rng, 2, oh, ow, 8)
+        i8 = fill(be, rng, 2, oh // 2, ow // 2, 8)
+        i16 = fill(be, rng, 1, oh // 4, ow // 4, 16)
+        l16 = fill(be, rng, 1, oh // 4, ow // 4, 4)
+        be.pair_input(V(ab), V(q), V(i8), V(i16, 6), V(l16, 1), oh, ow)
+        outs.append({k: be.host(t).copy() for k, t in (("q", q), ("i8", i8), ("i16", i16), ("l16", l16))})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k)
+
+
+@pytest.mark.parametrize("h,w", [(13, 21), (120, 216), (7, 9)])
+def test_refine_input_equals_its_ops(h, w):
+    say("refine_input", h, w)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(h * w)
+        q = fill(be, rng, 2, h, w, 8, 0.0, 1.0)
+        up7 = fill(be, rng, 1, h, w, 8, -6.0, 6.0)
+        rx = fill(be, rng, 1, h, w, 16)
+        blend = be.zeros(1, h, w, 8)  # the op-by-op chain's intermediate (the fused launch keeps it in LDS)
+        be.refine_input(V(q), V(up7, 0, 0.25), V(up7, 4), V(rx), 0.05, V(blend))
+        outs.append(be.host(rx)[..., :14].copy())
+    same(outs[0], outs[1], "rx")
