@@ -1457,8 +1457,8 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
 #pragma unroll
         for (int jx = 0; jx < KM; jx++) {
             // a tap outside the window has weight +0 and a value in [0, 1]: it adds +0, leaving acc and norm as the
-            // reference's skipped tap leaves them (interp_aa_lds_kernel selects the value instead, for views that
-            // may hold any value)
+            // reference's skipped tap leaves them (interp_aa_lds_kernel, whose views may hold any value, points such
+            // taps at a zero cell instead)
             const float wgt = wx[jx] * wy;
             const Cell q = lrow[lc[jx]];
             float vv[3];
