@@ -133,10 +133,8 @@ __global__ __launch_bounds__(kThreads) void luma_kernel(View x, OView out, uint3
 
 // ---- sad_volume: shaders/sad.wgsl:12-28; one lane per (pixel, displacement), so a wave stores consecutive
 // channels of the cost volume -----------------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void sad_kernel(View la, View lb, OView out, uint32_t h, uint32_t w,
-                                                       uint32_t r, uint32_t span2, uint32_t items) {
-    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-    if (t >= items) return;
+__device__ __forceinline__ void sad_at(const View& la, const View& lb, const OView& out, uint32_t h, uint32_t w,
+                                       uint32_t r, uint32_t span2, uint32_t t) {
     const uint32_t pix = t / span2, d = t - pix * span2, span = 2 * r + 1;
     const uint32_t x = pix % w, row = pix / w, y = row % h, img0 = row - y;
     const int dy = (int)(d / span) - (int)r, dx = (int)(d % span) - (int)r;
@@ -156,6 +154,11 @@ __global__ __launch_bounds__(kThreads) void sad_kernel(View la, View lb, OView o
             acc = acc + (in ? d : 0.0f);
         }
     st(out, pix, d, acc / 9.0f);
+}
+__global__ __launch_bounds__(kThreads) void sad_kernel(View la, View lb, OView out, uint32_t h, uint32_t w,
+                                                       uint32_t r, uint32_t span2, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t < items) sad_at(la, lb, out, h, w, r, span2, t);
 }
 
 // ---- convex upsample: shaders/convex.wgsl:12-34 ------------------------------------------------------------------
@@ -859,10 +862,8 @@ __global__ __launch_bounds__(64) void refine_input_kernel(View q, View fl, View 
 // and image 1 also to `also` (the streaming state's f16b), when given. Bits are copied. One lane per (pixel,
 // image, 4 channels); VEC: 8-byte copies.
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void fold_pair_kernel(View x, OView out, OView also, uint32_t hw, uint32_t c,
-                                                             uint32_t groups, uint32_t items) {
-    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-    if (t >= items) return;
+__device__ __forceinline__ void fold_pair_at(const View& x, const OView& out, const OView& also, uint32_t hw,
+                                             uint32_t c, uint32_t groups, uint32_t t) {
     const uint32_t g = t % groups, r = t / groups, img = r % 2, pix = r / 2, ch = g * 4;
     const uint16_t* src = x.p + ((size_t)img * hw + pix) * x.cs + x.c0 + ch;
     uint16_t* dst = out.p + (size_t)pix * out.cs + out.c0 + img * c + ch;
@@ -876,6 +877,33 @@ __global__ __launch_bounds__(kThreads) void fold_pair_kernel(View x, OView out, 
             dst[i] = src[i];
             if (img == 1 && dst2) dst2[i] = src[i];
         }
+    }
+}
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void fold_pair_kernel(View x, OView out, OView also, uint32_t hw, uint32_t c,
+                                                             uint32_t groups, uint32_t items) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t < items) fold_pair_at<VEC>(x, out, also, hw, c, groups, t);
+}
+
+// fold_pair and a sad_volume that neither reads what the other writes, side by side in one launch: blocks below
+// fold_blocks run the fold, the rest the cost volume (pair() folds the second encoder pair's output while the 1/16
+// lumas' cost volume, ready since the pyramid, is computed)
+struct SadArgs {
+    View la, lb;
+    OView out;
+    uint32_t h, w, r, span2, items;
+};
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void fold_pair_sad_kernel(View x, OView out, OView also, uint32_t hw,
+                                                                 uint32_t c, uint32_t groups, uint32_t items,
+                                                                 uint32_t fold_blocks, SadArgs sa) {
+    if (blockIdx.x < fold_blocks) {
+        const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+        if (t < items) fold_pair_at<VEC>(x, out, also, hw, c, groups, t);
+    } else {
+        const uint32_t t = (blockIdx.x - fold_blocks) * kThreads + threadIdx.x;
+        if (t < sa.items) sad_at(sa.la, sa.lb, sa.out, sa.h, sa.w, sa.r, sa.span2, t);
     }
 }
 
@@ -2478,5 +2506,51 @@ extern "C" int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv,
                            in(wt), none, outv(out), h, w, 7u, tx, ty, in(fv), in(dfilm), af, ab);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "flow_vis_t_convex: launch failed: %s", hipGetErrorString(e));
+    });
+}
+
+extern "C" int fhc_fold_pair_sad(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h,
+                                 uint32_t w, uint32_t c, const fhc_tensor* la, const fhc_tensor* lb,
+                                 const fhc_tensor* sad_out, uint32_t sn, uint32_t sh, uint32_t sw, uint32_t radius,
+                                 void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        const uint64_t fold_items = (uint64_t)h * w * 2 * ((c + 3) / 4);
+        if (radius > 7) return fail(-1, "fold_pair_sad: radius %u above 7", radius);
+        const uint32_t span2 = (2 * radius + 1) * (2 * radius + 1);
+        const uint64_t sad_items = (uint64_t)sn * sh * sw * span2;
+        if (fold_items == 0 && sad_items == 0) return 0;
+        if (fold_items) {
+            FHC_TRY(check(x, "fold_pair_sad x", c, false));
+            FHC_TRY(check(out, "fold_pair_sad out", 2 * c, false, true));
+            if (also) FHC_TRY(check(also, "fold_pair_sad also", c, false, true));
+        }
+        if (sad_items) {
+            FHC_TRY(check(la, "fold_pair_sad la", 1, false));
+            FHC_TRY(check(lb, "fold_pair_sad lb", 1, false));
+            FHC_TRY(check(sad_out, "fold_pair_sad sad out", span2, false, true));
+        }
+        const uint64_t fb = (fold_items + kThreads - 1) / kThreads, sb = (sad_items + kThreads - 1) / kThreads;
+        if (fold_items >= kMaxItems || sad_items >= kMaxItems || fb + sb >= (1u << 31))
+            return fail(-1, "fold_pair_sad: too many work items");
+        bool v = false;
+        OView a2{nullptr, 0, 0};
+        View xv{nullptr, 0, 0, 1.0f};
+        OView ov{nullptr, 0, 0};
+        if (fold_items) {
+            fhc_tensor out1 = *out;  // image 1's slice must be aligned too for the vector path
+            out1.c0 += c;
+            v = also ? vec4(c, {x, out, &out1, also}) : vec4(c, {x, out, &out1});
+            a2 = also ? outv(also) : a2;
+            xv = in(x), ov = outv(out);
+        }
+        const View none{nullptr, 0, 0, 1.0f};
+        const SadArgs sa{sad_items ? in(la) : none, sad_items ? in(lb) : none,
+                         sad_items ? outv(sad_out) : OView{nullptr, 0, 0}, sh, sw, radius, span2, (uint32_t)sad_items};
+        auto k = v ? fold_pair_sad_kernel<true> : fold_pair_sad_kernel<false>;
+        hipLaunchKernelGGL(k, dim3((uint32_t)(fb + sb)), dim3(kThreads), 0, (hipStream_t)stream, xv, ov, a2, h * w, c,
+                           (c + 3) / 4, (uint32_t)fold_items, (uint32_t)fb, sa);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "fold_pair_sad: launch failed: %s", hipGetErrorString(e));
     });
 }

@@ -77,6 +77,7 @@ def _lib():
             "fhc_pair_input": [T, T, T, T, T, U, U, U, U, P],
             "fhc_render": [T, T, T, T, T, T, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U, P],
             "fhc_fold_pair": [T, T, T, U, U, U, P],
+            "fhc_fold_pair_sad": [T, T, T, U, U, U, T, T, T, U, U, U, U, P],
             "fhc_coarse_up": [T, T, T, U, U, U, U, ctypes.c_float, P],
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
@@ -295,14 +296,27 @@ def render(a, b, flow, vis, rt, cubic=True, flags=0, fsx=1.0, fsy=1.0, out=None,
     return o.t
 
 
-def fold_pair(x, out, also=None, stream=None):
+def fold_pair(x, out, also=None, stream=None, c=None):
     """Images 0 and 1 of x (2, h, w, c) side by side into out's channels (out.c0, out.c0 + c); image 1 also into
-    `also` when given."""
+    `also` when given. c defaults to the channels of x's view."""
     x = _v(x)
     _, h, w, _ = x.shape
-    c = x.channels
+    c = x.channels if c is None else c
     _run("fold_pair", _lib().fhc_fold_pair(_ref(x), _ref(_v(out)), None if also is None else _ref(_v(also)), h, w, c,
                                            _stream_handle(stream)))
+
+
+def fold_pair_sad(x, out, also, la, lb, sad_out, radius, stream=None, c=None):
+    """fold_pair(x, out, also, c=c) and sad(la, lb, radius, out=sad_out), which touch none of each other's tensors,
+    in one launch."""
+    x, la = _v(x), _v(la)
+    _, h, w, _ = x.shape
+    n, sh, sw, _ = la.shape
+    c = x.channels if c is None else c
+    _run("fold_pair_sad",
+         _lib().fhc_fold_pair_sad(_ref(x), _ref(_v(out)), None if also is None else _ref(_v(also)), h, w, c,
+                                  _ref(la), _ref(_v(lb)), _ref(_v(sad_out)), n, sh, sw, radius,
+                                  _stream_handle(stream)))
 
 
 def coarse_up(o, out, state, oh, ow, flow_scale, stream=None):

@@ -115,6 +115,11 @@ class ComposedChains:
         if also is not None:
             self.chcopy(V(self.image(x.buf, 1), x.c0), c, also)
 
+    def fold_pair_sad(self, x: V, c: int, out: V, also: Optional[V], la: V, lb: V, sad_out: V, r: int):
+        """fold_pair and a sad that neither reads what the other writes (one launch on the GPU)."""
+        self.fold_pair(x, c, out, also)
+        self.sad(la, lb, sad_out, r)
+
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
         for i in range(2):
@@ -400,8 +405,18 @@ class GpuBackend(ComposedChains):
         if not self.chains:
             return super().fold_pair(x, c, out, also)
         vx, vo, va = self._v(x), self._v(out), None if also is None else self._v(also)
-        self._go("fold_pair", lambda: self.fh.fold_pair(vx, vo, va, stream=self.stream),
+        self._go("fold_pair", lambda: self.fh.fold_pair(vx, vo, va, stream=self.stream, c=c),
                  2 * c * (2 * self._px(x) + (self._px(x) // 2 if also is not None else 0)))
+
+    def fold_pair_sad(self, x: V, c: int, out: V, also: Optional[V], la: V, lb: V, sad_out: V, r: int):
+        if not self.chains:
+            return super().fold_pair_sad(x, c, out, also, la, lb, sad_out, r)
+        vx, vo, va = self._v(x), self._v(out), None if also is None else self._v(also)
+        fa, fb, fs = self._v(la), self._v(lb), self._v(sad_out)
+        self._go("fold_pair_sad (fold_pair + sad_volume)",
+                 lambda: self.fh.fold_pair_sad(vx, vo, va, fa, fb, fs, r, stream=self.stream, c=c),
+                 2 * c * (2 * self._px(x) + (self._px(x) // 2 if also is not None else 0))
+                 + 2 * (2 + (2 * r + 1) ** 2) * self._px(la))
 
     def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
         if not self.chains:
@@ -544,10 +559,12 @@ class FlyHighFG:
             else:
                 be.rgba_in(self.frames, V(self.AB), nh, nw)
         be.pair_input(V(self.AB), V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16), qh, qw)  # 0-1, 14-24
-        be.sad(V(self.l16, 0), V(self.l16, 1), V(self.cin, 230), 3)                           # 25, 26; 19-20 zeros
         be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)                 # 2-4, 8-10
         be.pair("enc.e3", "enc.e4", V(self.f8), V(self.e3), V(self.f16), True)                # 5-7, 11-13
-        be.fold_pair(V(self.f16), 72, V(self.cin, 0), V(self.state_out, 0))                   # 26, 43: f16a f16b
+        # 26, 43: f16a f16b into the concat and the state, beside the 1/16 lumas' cost volume (25, 26; 19-20 zeros),
+        # which reads and writes nothing the encoders touch
+        be.fold_pair_sad(V(self.f16), 72, V(self.cin, 0), V(self.state_out, 0), V(self.l16, 0), V(self.l16, 1),
+                         V(self.cin, 230), 3)
         be.conv("coarse.c1", V(self.cin), V(self.ch1))                                        # 27
         be.conv("coarse.c2", V(self.ch1), V(self.ch2))                                        # 28
         be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30

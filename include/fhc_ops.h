@@ -214,6 +214,14 @@ int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, const fhc_t
 int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, float t,
                           const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, void* stream);
 
+/* fhc_fold_pair and fhc_sad_volume in one launch, for a sad_volume that reads nothing the fold writes and writes
+ * nothing it reads (pair(): the second encoder pair's fold, op 26 and 43's f16b, beside the 1/16 lumas' cost volume,
+ * ops 25-26, ready since the pyramid). The fold's arguments as fhc_fold_pair's (h x w, c channels); the cost
+ * volume's as fhc_sad_volume's (sn x sh x sw, radius). Bit-identical to the two calls. */
+int fhc_fold_pair_sad(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h, uint32_t w,
+                      uint32_t c, const fhc_tensor* la, const fhc_tensor* lb, const fhc_tensor* sad_out, uint32_t sn,
+                      uint32_t sh, uint32_t sw, uint32_t radius, void* stream);
+
 /* GMHS, the periodic-structure repair of the pair's E8 flow (crates/flyhigh-engine/src/gmhs.rs:149-206, run at the
  * end of the pair stage when the repair level is above 0, net/build.rs:640-660; the reference's default level is 1,
  * options.rs:305). A robust affine motion is fitted to the flow (4 rounds of reweighted least squares,

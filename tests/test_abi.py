@@ -171,6 +171,10 @@ def test_network_ops_reject_bad_views_before_any_launch():
                                    _tv(), 4, 4, 4, None), "state is larger"),
         ("fhc_flow_vis_t_convex", (_tv(cs=40), _tv(cs=8), _tv(cs=4), ctypes.c_float(0.5), _tv(cs=8), 1, 4, 4, None),
          "flow_vis_t_convex dfilm"),
+        ("fhc_fold_pair_sad", (_tv(cs=8), _tv(cs=16), None, 4, 4, 8, _tv(), _tv(), _tv(cs=24), 1, 4, 4, 2, None),
+         "fold_pair_sad sad out"),
+        ("fhc_fold_pair_sad", (_tv(cs=8), _tv(cs=12), None, 4, 4, 8, _tv(), _tv(), _tv(cs=32), 1, 4, 4, 2, None),
+         "fold_pair_sad out"),
     ]
     for name, args, msg in cases:
         rc = getattr(L, name)(*args)

@@ -5,7 +5,8 @@ Bar: bit-exact. Each op of a chain is pinned to the oracle by its own parity tes
 launch computes the same f32 operations with the same roundings, so its outputs must equal the op-by-op outputs bit
 for bit. The whole-frame check (test_frame.py::test_fused_chains_equal_their_ops_on_the_gpu) covers the chains at
 the 1080p frame's shapes; here, for the coarse output with the fine block's input, flow_t / vis_t with the convex
-upsample, the pictures' resize with the pyramid and the refine head's input: ragged grids whose coarse-to-fine ratio
+upsample, the pictures' resize with the pyramid, the refine head's input, and the encoders' fold beside a cost
+volume: ragged grids whose coarse-to-fine ratio
 is no integer, downscales other than 4x, channel counts that are no multiple of 4 (the 2-byte path), views into wider
 buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample.
 """
@@ -116,3 +117,25 @@ def test_refine_input_equals_its_ops(h, w):
         be.refine_input(V(q), V(up7, 0, 0.25), V(up7, 4), V(rx), 0.05, V(blend))
         outs.append(be.host(rx)[..., :14].copy())
     same(outs[0], outs[1], "rx")
+
+
+@pytest.mark.parametrize("h,w,c,also,sh,sw,r", [(30, 54, 72, True, 30, 54, 3), (9, 13, 6, False, 5, 7, 2),
+                                                 (4, 4, 8, True, 17, 3, 1)])
+def test_fold_pair_sad_equals_fold_pair_and_sad(h, w, c, also, sh, sw, r):
+    say("fold_pair_sad", h, w, c, also, sh, sw, r)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(h * 7 + sw)
+        x = fill(be, rng, 2, h, w, c + 4)
+        out = fill(be, rng, 1, h, w, 2 * c + 8)
+        st = fill(be, rng, 1, h, w, c + 4) if also else None
+        l = fill(be, rng, 3, sh, sw, 4, 0.0, 1.0)
+        so = fill(be, rng, 3, sh, sw, (2 * r + 1) ** 2 + 4)
+        be.fold_pair_sad(V(x, 2), c, V(out, 4), None if st is None else V(st, 1), V(l, 0), V(l, 2), V(so, 3), r)
+        # the fold alone too: x's view is wider than the c channels folded
+        out2 = fill(be, rng, 1, h, w, 2 * c + 8)
+        be.fold_pair(V(x, 1), c, V(out2, 2), None)
+        outs.append({k: be.host(t).copy() for k, t in (("out", out), ("also", st), ("sad", so), ("out2", out2))
+                     if t is not None})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k)
