@@ -1515,7 +1515,6 @@ constexpr uint32_t kGmNwg = 32, kGmWg = 256;  // gm_fit_reduce's workgroups and 
 constexpr uint32_t kGmPart = kGmNwg * 4 * 9;  // one round's partial sums [workgroup][channel][9]
 constexpr uint32_t kGmT = 16;                 // the cost kernel's block edge and the box tile's, in cells
 constexpr uint32_t kGmRmax = 32;              // largest box radius: r_dwin = round(16 s), s <= 2
-constexpr uint32_t kGmWin = kGmT + 2 * kGmRmax;
 
 // gm_fit_solve.wgsl:13-24: the normal equations of one flow channel, s = its summed partials; o = a0, a1, a2
 __device__ void gm_solve(const float* s, float* o) {
