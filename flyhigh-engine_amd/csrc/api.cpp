@@ -882,9 +882,17 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         std::string why;
         if (!valid_desc(A, &why)) return fail(-1, "fhc_conv_pair_plan_create: first conv: %s", why.c_str());
         if (!valid_desc(B, &why)) return fail(-1, "fhc_conv_pair_plan_create: second conv: %s", why.c_str());
-        const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0;
-        const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu, loop_req = (flags >> 20) & 3u;
-        if ((flags & ~(FHC_PAIR_RES_MID | 0x3fff00u)) != 0) return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
+        const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0, post = (flags & FHC_PAIR_AFFINE_OUT) != 0;
+        const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu;
+        // affine_out after the second conv: the one-workgroup-per-tile loop, whose epilogue applies it
+        const uint32_t loop_req = post ? 1u : (flags >> 20) & 3u;
+        if ((flags & ~(FHC_PAIR_RES_MID | FHC_PAIR_AFFINE_OUT | 0x3fff00u)) != 0)
+            return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
+        if (post && ((flags >> 20) & 3u) > 1)
+            return fail(-1, "fhc_conv_pair_plan_create: affine_out runs in the one-workgroup-per-tile loop only");
+        if (post && (B.cout > 4 || B.residual))
+            return fail(-1, "fhc_conv_pair_plan_create: affine_out needs a second conv of at most 4 output channels "
+                            "without residual");
         const uint32_t ha = (A.h + 2 * A.pad - A.kh) / A.stride + 1, wa = (A.w + 2 * A.pad - A.kw) / A.stride + 1;
         if (A.kh != 3 || B.kh != 3 || B.stride != 1 || A.residual)
             return fail(-1, "fhc_conv_pair_plan_create: the pair is a 3x3 conv (stride 1 or 2, no residual) then a 3x3 "
@@ -949,6 +957,7 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         const uint32_t tiles_x = div_ceil(wa, kPairTileW), tiles_y = div_ceil(ha, (uint32_t)c.th);
         pb->args.tiles_x = (int)tiles_x;
         pb->args.tiles_y = (int)tiles_y;
+        pb->args.post = post ? 1 : 0;
         pa->family = 2;
         pa->cfg = idx;
         pa->code = 0;

@@ -32,6 +32,8 @@ struct ConvKArgs {
     int np;                     // output channels padded to ntn * BN
     int xvec, yvec, rvec;       // vector paths: 16-byte input loads, 8-byte output stores / residual loads
                                 // (rvec also needs cout % 4 == 0)
+    int post;                   // 1: the f16 output goes through affine_out, 2 / (1 + exp(-v)) - 1, rounded again
+                                // (the one-tile pair kernel's second conv, cout <= 4, no residual)
 };
 
 // A tile configuration: wave grid WM x WN x WK (WK > 1 splits K inside the workgroup), each wave FM output rows

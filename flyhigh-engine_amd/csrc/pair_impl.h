@@ -165,7 +165,35 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
 
     // B over TH rows x 16 columns (the first 14 stored); columns 16 and 17 of the LDS tile feed only the two
     // discarded lanes
-    if (wn < NBB) {
+    if (wn < NBB && b.post) {  // uniform
+        // B then affine_out (B.cout <= 4, no residual: the host checks). B's outputs sit in lanes 0-15, the 4
+        // channels of pixel lx each; lane group g = lane / 16 takes rows g, g + 4, ... of the wave from them, so
+        // all 64 lanes share the exponentials and divisions (unary.wgsl's op 2 on the f16 output, rounded again)
+        f4 acc[THW];
+        pair_chain<THW, 1, MB, MW, PSB>(acc, wrb, mid + (wm * THW * MW + lx) * PSB + (lane >> 4) * 8);
+        const int g = lane >> 4;
+#pragma unroll
+        for (int fw0 = 0; fw0 < THW; fw0 += 4) {
+            float mine[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // row fw0 + g, pixel lx
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                if (fw0 + k >= THW) break;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float v = h2f(f2h(activate(acc[fw0 + k][i] + biasb[i], negb[i])));
+                    const float s = __shfl(v, lx);
+                    mine[i] = g == k ? s : mine[i];
+                }
+            }
+            const int fw = fw0 + g, oy = oy0 + wm * THW + fw, ox = ox0 + lx;
+            if (fw < THW && lx < TWB && oy < b.hout && ox < b.wout) {
+                uint16_t* yp = b.y + (((size_t)img * b.hout + oy) * b.wout + ox) * (size_t)b.ycs + b.yc0;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (i < b.cout) yp[i] = f2h(2.0f / (1.0f + expf(-mine[i])) - 1.0f);
+            }
+        }
+    } else if (wn < NBB) {
         f4 acc[THW];
         pair_chain<THW, 1, MB, MW, PSB>(acc, wrb, mid + (wm * THW * MW + lx) * PSB + (lane >> 4) * 8);
 #pragma unroll

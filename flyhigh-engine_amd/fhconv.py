@@ -222,6 +222,7 @@ class ConvPlan:
 
 
 PAIR_RES_MID = 1
+PAIR_AFFINE_OUT = 2
 
 
 class ConvPairPlan(ConvPlan):
@@ -229,10 +230,11 @@ class ConvPairPlan(ConvPlan):
     A's output, which stays on chip. run(x, y, res) takes A's input, B's output and B's external residual; with
     res_mid B's residual is A's output. tile_rows / wave_rows / loop 0 let the library choose (1, 2 or 4 rows; 1
     wave row; loop 1 one workgroup per tile, 2 a resident grid looping over tiles, 3 a resident grid with A and B
-    on separate waves)."""
+    on separate waves). affine_out: B's f16 output goes through the graph's affine_out op (2 / (1 + exp(-v)) - 1,
+    rounded again) before it is stored; one workgroup per tile."""
 
     def __init__(self, desc_a: ConvDesc, w_a, bias_a, slope_a, desc_b: ConvDesc, w_b, bias_b, slope_b,
-                 res_mid=False, tile_rows=0, wave_rows=0, loop=0):
+                 res_mid=False, tile_rows=0, wave_rows=0, loop=0, affine_out=False):
         L = load()
         self.desc, self.desc_b = desc_a, desc_b
         arrays = []
@@ -246,7 +248,8 @@ class ConvPairPlan(ConvPlan):
                 raise FhcError("bias and slope must hold cout f16 values")
             arrays.append((wa, wp, ba, bp, sa, sp))
         (_, wpa, _, bpa, _, spa), (_, wpb, _, bpb, _, spb) = arrays
-        flags = (PAIR_RES_MID if res_mid else 0) | (int(tile_rows) << 8) | (int(wave_rows) << 16) | (int(loop) << 20)
+        flags = ((PAIR_RES_MID if res_mid else 0) | (PAIR_AFFINE_OUT if affine_out else 0) | (int(tile_rows) << 8) |
+                 (int(wave_rows) << 16) | (int(loop) << 20))
         h = ctypes.c_void_p()
         _check(L.fhc_conv_pair_plan_create(ctypes.byref(desc_a), wpa, bpa, spa, ctypes.byref(desc_b), wpb, bpb,
                                            spb, flags, ctypes.byref(h)), "fhc_conv_pair_plan_create")

@@ -120,6 +120,12 @@ class ComposedChains:
         self.fold_pair(x, c, out, also)
         self.sad(la, lb, sad_out, r)
 
+    def pair_affine_out(self, a, b, x: V, mid: V, y: V, out: V, c: int):
+        """The pair a, b (no residual) into y, then affine_out of y's c channels into out (on the GPU one launch,
+        which writes out and neither mid nor y)."""
+        self.pair(a, b, x, mid, y, False)
+        self.unary(y, c, out, 2)
+
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
         for i in range(2):
@@ -285,6 +291,27 @@ class GpuBackend(ComposedChains):
         else:
             xb, yb, st = x.buf, y.buf, self.stream
             self._go(f"{a}+{b}", lambda: p.run(xb, yb, None, stream=st), p._work["bytes"], p._work["flops"], "conv")
+
+    def pair_affine_out(self, a, b, x: V, mid: V, y: V, out: V, c: int):
+        if not (self.chains and self.fuse) or CONVS[b][1] != c:
+            return super().pair_affine_out(a, b, x, mid, y, out, c)
+        key = ("pair_affine_out", a, b, x.buf.data_ptr(), x.c0, out.buf.data_ptr(), out.c0)
+        p = self.plans.get(key)
+        if p is None:
+            da = self._desc(a, x, mid, None)
+            db = self._desc(b, mid, out, None)
+            (wa, ba, sa), (wb, bb, sb) = self.W[a], self.W[b]
+            try:
+                p = self.fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, affine_out=True)
+                p._work = p.describe()
+            except self.fhconv.FhcError:
+                p = False  # no fused kernel for these channels
+            self.plans[key] = p
+        if p is False:
+            return super().pair_affine_out(a, b, x, mid, y, out, c)
+        xb, ob, st = x.buf, out.buf, self.stream
+        self._go(f"{a}+{b}+affine_out", lambda: p.run(xb, ob, None, stream=st), p._work["bytes"], p._work["flops"],
+                 "conv")
 
     def interp(self, x: V, c, out: V, oh, ow, aa):
         n = x.buf.shape[0]
@@ -598,8 +625,7 @@ class FlyHighFG:
                              V(self.dvis))                                                    # 44-48, 54-62
         be.refine_input(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend))  # 63-76
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
-        be.pair("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), False)        # 79, 80
-        be.unary(V(self.rr), 3, V(self.Rt), 2)                                                # 81: affine_out
+        be.pair_affine_out("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), V(self.Rt), 3)  # 79-81
         if self.frame is not None and self.internal:  # the render at the frame size, to the RGBA8 frame
             be.frame_render(self.frames, self.full, self.pic, V(self.up7, 0), V(self.up7, 4), V(self.Rt), self.rgba,
                             self.hp, self.wp, self.fsx, self.fsy, self.cubic, self.render_flags)

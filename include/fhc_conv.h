@@ -121,6 +121,11 @@ void fhc_conv_plan_destroy(fhc_conv_plan* plan);
  * 33..48 (2 or 4 rows) and 33..64 -> 65..80 -> 65..80 (1 or 2 rows, one wave row), and stride 1 33..64 -> 33..48 ->
  * 33..48, <= 32 -> 17..32 -> 17..32 and <= 32 -> 17..32 -> <= 16 (2 or 4 rows); other shapes are an error status. */
 #define FHC_PAIR_RES_MID 1u
+/* FHC_PAIR_AFFINE_OUT: B's f16 output then goes through the graph's affine_out op (unary.wgsl's op 2:
+ * 2 / (1 + exp(-v)) - 1 in f32, rounded to f16 again; graph.json op 81 after refine.q4), so the pair writes that op's
+ * output; it runs the one-workgroup-per-tile loop (bits 20-21 0 or 1) and needs B.cout <= 4 and no residual. No
+ * counterpart in the reference, which dispatches the op on its own. */
+#define FHC_PAIR_AFFINE_OUT 2u
 int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
                               const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
                               const uint16_t* bias_b, const uint16_t* slope_b, uint32_t flags, fhc_conv_plan** out);

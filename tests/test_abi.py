@@ -133,6 +133,14 @@ def test_pair_plan_rejects_what_it_cannot_fuse():
     big = fhconv.make_desc(1, 20, 30, 36, 96, act=0)  # 96 output channels: no pair instantiated
     with pytest.raises(fhconv.FhcError):
         fhconv.ConvPairPlan(a, wa, ba, None, big, np.zeros(96 * 36 * 9, np.uint16), np.zeros(96, np.uint16), None)
+    # affine_out after the second conv runs in the one-workgroup-per-tile loop only
+    b = fhconv.make_desc(1, 20, 30, 36, 36, act=0)
+    for loop in (2, 3):
+        with pytest.raises(fhconv.FhcError, match="one-workgroup-per-tile"):
+            fhconv.ConvPairPlan(a, wa, ba, None, b, wb, bb, None, loop=loop, affine_out=True)
+    # ... on a second conv of at most 4 output channels
+    with pytest.raises(fhconv.FhcError, match="at most 4 output channels"):
+        fhconv.ConvPairPlan(a, wa, ba, None, b, wb, bb, None, affine_out=True)
 
 
 def _ops():

@@ -5,8 +5,8 @@ Bar: bit-exact. Each op of a chain is pinned to the oracle by its own parity tes
 launch computes the same f32 operations with the same roundings, so its outputs must equal the op-by-op outputs bit
 for bit. The whole-frame check (test_frame.py::test_fused_chains_equal_their_ops_on_the_gpu) covers the chains at
 the 1080p frame's shapes; here, for the coarse output with the fine block's input, flow_t / vis_t with the convex
-upsample, the pictures' resize with the pyramid, the refine head's input, and the encoders' fold beside a cost
-volume: ragged grids whose coarse-to-fine ratio
+upsample, the pictures' resize with the pyramid, the refine head's input, the encoders' fold beside a cost volume,
+and the refine head's last pair with affine_out: ragged grids whose coarse-to-fine ratio
 is no integer, downscales other than 4x, channel counts that are no multiple of 4 (the 2-byte path), views into wider
 buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample.
 """
@@ -139,3 +139,17 @@ def test_fold_pair_sad_equals_fold_pair_and_sad(h, w, c, also, sh, sw, r):
                      if t is not None})
     for k in outs[0]:
         same(outs[0][k], outs[1][k], k)
+
+
+@pytest.mark.parametrize("h,w", [(120, 216), (13, 30), (5, 7)])
+def test_pair_affine_out_equals_pair_then_affine_out(h, w):
+    say("pair_affine_out", h, w)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(h + w)
+        x = fill(be, rng, 1, h, w, 32)
+        mid, y = fill(be, rng, 1, h, w, 24), fill(be, rng, 1, h, w, 4)
+        out = fill(be, rng, 1, h, w, 4)
+        be.pair_affine_out("refine.q3", "refine.q4", V(x, 4), V(mid), V(y), V(out), 3)
+        outs.append(be.host(out).copy())
+    same(outs[0], outs[1], "out")
