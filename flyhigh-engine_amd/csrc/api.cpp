@@ -169,6 +169,7 @@ struct fhc_conv_plan {
     LaunchFn launch;
     fhc_conv_plan* pair_b;  // fused pair: the second conv (its weights and output geometry), owned
     int res_mid;            // fused pair: the second conv's residual is the first's output
+    int film_in;            // fused pair: FiLM on the first conv's input (runs with fhc_conv_pair_run_film)
     PairLaunchFn pair_launch;
 };
 
@@ -754,6 +755,45 @@ extern "C" int fhc_conv_out_shape(const fhc_conv_plan* p, uint32_t* hout, uint32
     return 0;
 }
 
+namespace {
+// the launch of a fused pair plan (validated by the caller): x is the first conv's input, y and res the second's
+// output and residual, film the FiLM vectors of a FHC_PAIR_FILM_IN plan
+int run_pair(const fhc_conv_plan* p, const void* x, void* y, const void* res, const void* film, void* stream,
+             const char* who) {
+    const fhc_conv_plan* q = p->pair_b;
+    if (q->d.residual && !p->res_mid && !res)
+        return fail(-1, "%s: the pair's second conv has a residual but res is NULL", who);
+    PairKArgs pk{p->args, q->args, p->res_mid};
+    pk.a.x = static_cast<const uint16_t*>(x);
+    pk.a.xvec = ((uintptr_t)x % 16 == 0) && pk.a.xcs % 8 == 0 && pk.a.xc0 % 8 == 0;
+    pk.a.film = static_cast<const uint16_t*>(film);
+    pk.b.y = static_cast<uint16_t*>(y);
+    pk.b.res = static_cast<const uint16_t*>(res);
+    pk.b.yvec = ((uintptr_t)y % 8 == 0) && pk.b.ycs % 4 == 0 && pk.b.yc0 % 4 == 0;
+    pk.b.rvec = pk.b.residual && !p->res_mid && ((uintptr_t)res % 8 == 0) && pk.b.rcs % 4 == 0 &&
+                pk.b.rc0 % 4 == 0 && pk.b.cout % 4 == 0;
+    hipError_t e = p->pair_launch(pk, p->grid, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(-1, "%s: launch: %s", who, hipGetErrorString(e));
+    return 0;
+}
+}  // namespace
+
+extern "C" int fhc_conv_pair_run_film(const fhc_conv_plan* p, const void* x, const void* film, void* y, void* stream) {
+    return guard(-1, [&]() -> int {
+        if (!p) return fail(-1, "fhc_conv_pair_run_film: NULL plan");
+        if (p->family != 2 || !p->film_in)
+            return fail(-1, "fhc_conv_pair_run_film: not a pair plan created with FHC_PAIR_FILM_IN");
+        if (!x || !y || !film) return fail(-1, "fhc_conv_pair_run_film: NULL input, output or FiLM vectors");
+        if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)film) & 1u)
+            return fail(-1, "fhc_conv_pair_run_film: f16 tensors must be 2-byte aligned");
+        int dev = -1;
+        if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
+            return fail(-1, "fhc_conv_pair_run_film: the plan belongs to device %d, the current device is %d",
+                        p->device, dev);
+        return run_pair(p, x, y, nullptr, film, stream, "fhc_conv_pair_run_film");
+    });
+}
+
 extern "C" int fhc_conv_run(const fhc_conv_plan* p, const void* x, void* y, const void* res, void* workspace,
                             void* stream) {
     return guard(-1, [&]() -> int {
@@ -769,20 +809,8 @@ extern "C" int fhc_conv_run(const fhc_conv_plan* p, const void* x, void* y, cons
         if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
             return fail(-1, "fhc_conv_run: the plan belongs to device %d, the current device is %d", p->device, dev);
         if (p->family == 2) {  // fused pair: x is the first conv's input, y and res the second's output and residual
-            const fhc_conv_plan* q = p->pair_b;
-            if (q->d.residual && !p->res_mid && !res)
-                return fail(-1, "fhc_conv_run: the pair's second conv has a residual but res is NULL");
-            PairKArgs pk{p->args, q->args, p->res_mid};
-            pk.a.x = static_cast<const uint16_t*>(x);
-            pk.a.xvec = ((uintptr_t)x % 16 == 0) && pk.a.xcs % 8 == 0 && pk.a.xc0 % 8 == 0;
-            pk.b.y = static_cast<uint16_t*>(y);
-            pk.b.res = static_cast<const uint16_t*>(res);
-            pk.b.yvec = ((uintptr_t)y % 8 == 0) && pk.b.ycs % 4 == 0 && pk.b.yc0 % 4 == 0;
-            pk.b.rvec = pk.b.residual && !p->res_mid && ((uintptr_t)res % 8 == 0) && pk.b.rcs % 4 == 0 &&
-                        pk.b.rc0 % 4 == 0 && pk.b.cout % 4 == 0;
-            hipError_t e = p->pair_launch(pk, p->grid, static_cast<hipStream_t>(stream));
-            if (e != hipSuccess) return fail(-1, "fhc_conv_run: launch: %s", hipGetErrorString(e));
-            return 0;
+            if (p->film_in) return fail(-1, "fhc_conv_run: the pair takes FiLM vectors: run it with fhc_conv_pair_run_film");
+            return run_pair(p, x, y, res, nullptr, stream, "fhc_conv_run");
         }
         ConvKArgs a = p->args;
         a.x = static_cast<const uint16_t*>(x);
@@ -883,13 +911,19 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         if (!valid_desc(A, &why)) return fail(-1, "fhc_conv_pair_plan_create: first conv: %s", why.c_str());
         if (!valid_desc(B, &why)) return fail(-1, "fhc_conv_pair_plan_create: second conv: %s", why.c_str());
         const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0, post = (flags & FHC_PAIR_AFFINE_OUT) != 0;
+        const bool film = (flags & FHC_PAIR_FILM_IN) != 0;
         const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu;
-        // affine_out after the second conv: the one-workgroup-per-tile loop, whose epilogue applies it
-        const uint32_t loop_req = post ? 1u : (flags >> 20) & 3u;
-        if ((flags & ~(FHC_PAIR_RES_MID | FHC_PAIR_AFFINE_OUT | 0x3fff00u)) != 0)
+        // affine_out after the second conv, FiLM before the first: the one-workgroup-per-tile loop applies them
+        const uint32_t loop_req = post || film ? 1u : (flags >> 20) & 3u;
+        if ((flags & ~(FHC_PAIR_RES_MID | FHC_PAIR_AFFINE_OUT | FHC_PAIR_FILM_IN | 0x3fff00u)) != 0)
             return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
         if (post && ((flags >> 20) & 3u) > 1)
             return fail(-1, "fhc_conv_pair_plan_create: affine_out runs in the one-workgroup-per-tile loop only");
+        if (film && ((flags >> 20) & 3u) > 1)
+            return fail(-1, "fhc_conv_pair_plan_create: FiLM on the input runs in the one-workgroup-per-tile loop "
+                            "only");
+        if (film && B.residual && !res_mid)
+            return fail(-1, "fhc_conv_pair_plan_create: FiLM on the input leaves no argument for an external residual");
         if (post && (B.cout > 4 || B.residual))
             return fail(-1, "fhc_conv_pair_plan_create: affine_out needs a second conv of at most 4 output channels "
                             "without residual");
@@ -990,6 +1024,7 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         pa->ws_bytes = 0;
         pa->launch = nullptr;
         pa->res_mid = res_mid ? 1 : 0;
+        pa->film_in = film ? 1 : 0;
         pa->pair_launch = pair_launcher(idx);
         pa->pair_b = pb.release();
         *out = pa.release();

@@ -34,6 +34,8 @@ struct ConvKArgs {
                                 // (rvec also needs cout % 4 == 0)
     int post;                   // 1: the f16 output goes through affine_out, 2 / (1 + exp(-v)) - 1, rounded again
                                 // (the one-tile pair kernel's second conv, cout <= 4, no residual)
+    const uint16_t* film;       // the one-tile pair kernel's first conv: FiLM vectors [n][gamma cin | beta cin]
+                                // (f16) applied to the input as it is staged, or null
 };
 
 // A tile configuration: wave grid WM x WN x WK (WK > 1 splits K inside the workgroup), each wave FM output rows

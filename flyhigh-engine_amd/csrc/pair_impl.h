@@ -55,7 +55,22 @@ __device__ __forceinline__ void pair_chain(f4 (&acc)[FM], const h8* wr, const ui
     pin_mfma_pipeline<0, NQ, D, R, FM, S, KS, 1, 0>();
 }
 
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC>
+// film_modulate (film.wgsl) on one staged 8-channel group: channel j < n becomes f16(v * gm[j] + bt[j]) with
+// gm = 1 + gamma, bt = beta in f32, as the op computes it; channels past n stay as they are (zero)
+__device__ __forceinline__ uint4 film_group(uint4 q, const float* gm, const float* bt, int n) {
+    uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t lo = w[k] & 0xffffu, hi = w[k] >> 16;
+        if (2 * k < n) lo = f2h(h2f((uint16_t)lo) * gm[2 * k] + bt[2 * k]);
+        if (2 * k + 1 < n) hi = f2h(h2f((uint16_t)hi) * gm[2 * k + 1] + bt[2 * k + 1]);
+        w[k] = lo | (hi << 16);
+    }
+    return uint4{w[0], w[1], w[2], w[3]};
+}
+
+// FILM: A's input goes through film_modulate as it is staged (a.film, the one-tile loop only)
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC, bool FILM = false>
 __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(PairKArgs pk) {
     constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN * WM, TWB = kPairTileW;
     constexpr int FA = TH + 2;                                  // A's rows per tile
@@ -90,6 +105,8 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
         for (int s = 0; s < 9 * MB; s++) wrb[s] = wq[s * 64];
     }
     uint4 pre[NLD];
+    uint32_t inside = 0;  // bit i: pre[i] holds input values (not the zero padding)
+    static_assert(NLD <= 32 && NT % GPA == 0, "a lane stages the same channel group in every round");
     const bool whole = VEC && a.xc0 + ((a.cin + 7) & ~7) <= a.xcs;  // partial groups load as one 16-byte group
     {
         const int iy0 = (oy0 - 1) * SA - a.pad, ix0 = (ox0 - 1) * SA - a.pad;
@@ -101,9 +118,23 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
             const int gy = iy0 + iy, gx = ix0 + ix, ch = g * 8;
             pre[i] = uint4{0u, 0u, 0u, 0u};
             if ((i + 1) * NT <= HALO || e < HALO)
-                if (gy >= 0 && gy < a.h && gx >= 0 && gx < a.w && ch < a.cin)
+                if (gy >= 0 && gy < a.h && gx >= 0 && gx < a.w && ch < a.cin) {
                     pre[i] = load_group<VEC>(
                         a.x + (((size_t)img * a.h + gy) * a.w + gx) * (size_t)a.xcs + a.xc0 + ch, ch, a.cin, whole);
+                    if constexpr (FILM) inside |= 1u << i;
+                }
+        }
+    }
+    // FiLM on A's input (film_modulate, graph op 50, before film.h1): this lane's channel group tid % GPA, the
+    // tile's image's vector; the zero padding stays zero, as the modulated tensor's padding is
+    float fgm[8], fbt[8];
+    if constexpr (FILM) {
+        const uint16_t* gv = a.film + (size_t)img * 2 * a.cin;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int c = (tid % GPA) * 8 + j, cc = c < a.cin ? c : 0;
+            fgm[j] = 1.0f + h2f(gv[cc]);
+            fbt[j] = h2f(gv[a.cin + cc]);
         }
     }
     uint2 rres[THW];
@@ -140,7 +171,10 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
         const int e = tid + i * NT;
         if ((i + 1) * NT <= HALO || e < HALO) {
             const int pix = e / GPA, g = e - pix * GPA;
-            *reinterpret_cast<uint4*>(hin + pix * PSA + g * 8) = whole ? mask_group(pre[i], a.cin - g * 8) : pre[i];
+            uint4 q = whole ? mask_group(pre[i], a.cin - g * 8) : pre[i];
+            if constexpr (FILM)
+                if ((inside >> i) & 1u) q = film_group(q, fgm, fbt, a.cin - g * 8);
+            *reinterpret_cast<uint4*>(hin + pix * PSA + g * 8) = q;
         }
     }
     __syncthreads();
@@ -640,10 +674,16 @@ hipError_t launch_pair_p(const PairKArgs& pk, dim3 grid, hipStream_t s) {
 template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
 hipError_t launch_pair(const PairKArgs& pk, dim3 grid, hipStream_t s) {
     const dim3 block(64 * (NBA > NBB ? NBA : NBB) * WM);
-    if (pk.a.xvec)
+    if (pk.a.film) {  // FiLM on the input: its own instantiations, so the others stage as before
+        if (pk.a.xvec)
+            hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true, true>), grid, block, 0, s, pk);
+        else
+            hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false, true>), grid, block, 0, s, pk);
+    } else if (pk.a.xvec) {
         hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true>), grid, block, 0, s, pk);
-    else
+    } else {
         hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false>), grid, block, 0, s, pk);
+    }
     return hipGetLastError();
 }
 

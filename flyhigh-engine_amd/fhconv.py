@@ -71,6 +71,7 @@ def load():
         "fhc_conv_workspace_bytes": ([P], SZ),
         "fhc_conv_out_shape": ([P, ctypes.POINTER(U32), ctypes.POINTER(U32)], ctypes.c_int),
         "fhc_conv_run": ([P, P, P, P, P, P], ctypes.c_int),
+        "fhc_conv_pair_run_film": ([P, P, P, P, P], ctypes.c_int),
         "fhc_conv_run_noalloc": ([P, P, P, P, P], ctypes.c_int),
         "fhc_conv_describe": ([P, ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_conv_plan_destroy": ([P], None),
@@ -223,6 +224,7 @@ class ConvPlan:
 
 PAIR_RES_MID = 1
 PAIR_AFFINE_OUT = 2
+PAIR_FILM_IN = 4
 
 
 class ConvPairPlan(ConvPlan):
@@ -231,10 +233,11 @@ class ConvPairPlan(ConvPlan):
     res_mid B's residual is A's output. tile_rows / wave_rows / loop 0 let the library choose (1, 2 or 4 rows; 1
     wave row; loop 1 one workgroup per tile, 2 a resident grid looping over tiles, 3 a resident grid with A and B
     on separate waves). affine_out: B's f16 output goes through the graph's affine_out op (2 / (1 + exp(-v)) - 1,
-    rounded again) before it is stored; one workgroup per tile."""
+    rounded again) before it is stored; film_in: A's input goes through film_modulate as it is staged, with the FiLM
+    vectors given to run_film (which runs such a plan; run refuses it); both one workgroup per tile."""
 
     def __init__(self, desc_a: ConvDesc, w_a, bias_a, slope_a, desc_b: ConvDesc, w_b, bias_b, slope_b,
-                 res_mid=False, tile_rows=0, wave_rows=0, loop=0, affine_out=False):
+                 res_mid=False, tile_rows=0, wave_rows=0, loop=0, affine_out=False, film_in=False):
         L = load()
         self.desc, self.desc_b = desc_a, desc_b
         arrays = []
@@ -248,8 +251,8 @@ class ConvPairPlan(ConvPlan):
                 raise FhcError("bias and slope must hold cout f16 values")
             arrays.append((wa, wp, ba, bp, sa, sp))
         (_, wpa, _, bpa, _, spa), (_, wpb, _, bpb, _, spb) = arrays
-        flags = ((PAIR_RES_MID if res_mid else 0) | (PAIR_AFFINE_OUT if affine_out else 0) | (int(tile_rows) << 8) |
-                 (int(wave_rows) << 16) | (int(loop) << 20))
+        flags = ((PAIR_RES_MID if res_mid else 0) | (PAIR_AFFINE_OUT if affine_out else 0) |
+                 (PAIR_FILM_IN if film_in else 0) | (int(tile_rows) << 8) | (int(wave_rows) << 16) | (int(loop) << 20))
         h = ctypes.c_void_p()
         _check(L.fhc_conv_pair_plan_create(ctypes.byref(desc_a), wpa, bpa, spa, ctypes.byref(desc_b), wpb, bpb,
                                            spb, flags, ctypes.byref(h)), "fhc_conv_pair_plan_create")
@@ -262,6 +265,14 @@ class ConvPairPlan(ConvPlan):
     def out_elems(self):
         d = self.desc_b
         return d.n * self.hout * self.wout * (d.y_cstride or d.cout)
+
+    def run_film(self, x, film, y, stream=None):
+        """A film_in plan on device tensors: x A's input before the modulation, film the FiLM vectors (n x 2 x
+        A.cin f16, contiguous), y B's output."""
+        if not film.is_contiguous() or film.numel() != self.desc.n * 2 * self.desc.cin or film.element_size() != 2:
+            raise FhcError(f"run_film: film needs {self.desc.n * 2 * self.desc.cin} contiguous f16 values")
+        _check(load().fhc_conv_pair_run_film(self._h, _ptr(x), _ptr(film), _ptr(y), _stream_handle(stream)),
+               "fhc_conv_pair_run_film")
 
 
 @dataclass

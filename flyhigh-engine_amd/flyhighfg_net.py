@@ -126,6 +126,12 @@ class ComposedChains:
         self.pair(a, b, x, mid, y, False)
         self.unary(y, c, out, 2)
 
+    def film_pair(self, a, b, h: V, c: int, hm: V, mid: V, y: V):
+        """film_modulate of h's c channels into hm, then the pair a, b (no residual) on hm into y (on the GPU one
+        launch, which writes y and neither hm nor mid)."""
+        self.film(h, c, hm)
+        self.pair(a, b, hm, mid, y, False)
+
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
         for i in range(2):
@@ -312,6 +318,27 @@ class GpuBackend(ComposedChains):
         xb, ob, st = x.buf, out.buf, self.stream
         self._go(f"{a}+{b}+affine_out", lambda: p.run(xb, ob, None, stream=st), p._work["bytes"], p._work["flops"],
                  "conv")
+
+    def film_pair(self, a, b, h: V, c: int, hm: V, mid: V, y: V):
+        if not (self.chains and self.fuse) or CONVS[a][0] != c or h.scale != 1.0:
+            return super().film_pair(a, b, h, c, hm, mid, y)
+        key = ("film_pair", a, b, h.buf.data_ptr(), h.c0, y.buf.data_ptr(), y.c0)
+        p = self.plans.get(key)
+        if p is None:
+            da = self._desc(a, h, mid, None)
+            db = self._desc(b, mid, y, None)
+            (wa, ba, sa), (wb, bb, sb) = self.W[a], self.W[b]
+            try:
+                p = self.fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, film_in=True)
+                p._work = p.describe()
+            except self.fhconv.FhcError:
+                p = False  # no fused kernel for these channels
+            self.plans[key] = p
+        if p is False:
+            return super().film_pair(a, b, h, c, hm, mid, y)
+        hb, yb, g, st = h.buf, y.buf, self.g, self.stream
+        self._go(f"film_modulate+{a}+{b}", lambda: p.run_film(hb, g, yb, stream=st),
+                 p._work["bytes"] + 2 * 2 * c, p._work["flops"], "conv")
 
     def interp(self, x: V, c, out: V, oh, ow, aa):
         n = x.buf.shape[0]
@@ -618,8 +645,7 @@ class FlyHighFG:
         if W is not None:
             be.set_g(film_mlp(W, t))                                                          # 49
         be.conv("up.w", V(self.h), V(self.wt36))                                              # 62
-        be.film(V(self.h), 48, V(self.hm))                                                    # 50
-        be.pair("film.h1", "film.h2", V(self.hm), V(self.fh1), V(self.fh2), False)            # 51, 52
+        be.film_pair("film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))  # 50-52
         be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
         be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(self.dfilm), t, V(self.up7), V(self.ftvt), V(self.lin),
                              V(self.dvis))                                                    # 44-48, 54-62

@@ -126,9 +126,22 @@ void fhc_conv_plan_destroy(fhc_conv_plan* plan);
  * output; it runs the one-workgroup-per-tile loop (bits 20-21 0 or 1) and needs B.cout <= 4 and no residual. No
  * counterpart in the reference, which dispatches the op on its own. */
 #define FHC_PAIR_AFFINE_OUT 2u
+/* FHC_PAIR_FILM_IN: A's input is modulated per channel as it is staged, the graph's film_modulate op
+ * (film.wgsl: f16(x * (1 + gamma[c]) + beta[c]) in f32; graph.json op 50 before film.h1), so the pair reads the op's
+ * input and the op's dispatch goes; the zero padding stays zero. The FiLM vectors (per image: cin gammas, then cin
+ * betas, f16) are an argument of each run: the plan runs with fhc_conv_pair_run_film only (fhc_conv_run refuses it),
+ * in the one-workgroup-per-tile loop (bits 20-21 0 or 1), without an external residual for B. No counterpart in the
+ * reference, which dispatches the op on its own. */
+#define FHC_PAIR_FILM_IN 4u
 int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
                               const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
                               const uint16_t* bias_b, const uint16_t* slope_b, uint32_t flags, fhc_conv_plan** out);
+
+/* Runs a pair plan created with FHC_PAIR_FILM_IN: x is A's input before the modulation, film the FiLM vectors
+ * (n x 2 x A.cin f16, device memory), y B's output. Async on `stream`, no allocation, capturable in a HIP graph, as
+ * fhc_conv_run. Stands in for fhc_conv_run(film_modulate's output, ...) after the reference's film dispatch
+ * (`Gpu::film`, ops/network.rs:56-61, shaders/film.wgsl:11-14). */
+int fhc_conv_pair_run_film(const fhc_conv_plan* pair, const void* x, const void* film, void* y, void* stream);
 
 /* The planner's choice for a descriptor without creating a plan (no device call): the same JSON as
  * fhc_conv_describe, sizes included. For host-side tests and for tools that print the plan of a graph

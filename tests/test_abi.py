@@ -73,6 +73,8 @@ def test_null_arguments_are_errors():
     assert L.fhc_conv_plan_create(ctypes.byref(d), None, None, None, None) == -1
     assert L.fhc_conv_run(None, None, None, None, None, None) == -1
     assert "NULL plan" in fhconv.last_error()
+    assert L.fhc_conv_pair_run_film(None, None, None, None, None) == -1
+    assert "NULL plan" in fhconv.last_error()
     assert L.fhc_conv_describe(None, None, 0) == -1
     assert L.fhc_conv_workspace_bytes(None) == 0
     L.fhc_conv_plan_destroy(None)
@@ -141,6 +143,13 @@ def test_pair_plan_rejects_what_it_cannot_fuse():
     # ... on a second conv of at most 4 output channels
     with pytest.raises(fhconv.FhcError, match="at most 4 output channels"):
         fhconv.ConvPairPlan(a, wa, ba, None, b, wb, bb, None, affine_out=True)
+    # FiLM on the first conv's input: the one-workgroup-per-tile loop, no external residual for the second
+    for loop in (2, 3):
+        with pytest.raises(fhconv.FhcError, match="one-workgroup-per-tile"):
+            fhconv.ConvPairPlan(a, wa, ba, None, b, wb, bb, None, loop=loop, film_in=True)
+    br = fhconv.make_desc(1, 20, 30, 36, 36, act=0, residual=True)
+    with pytest.raises(fhconv.FhcError, match="external residual"):
+        fhconv.ConvPairPlan(a, wa, ba, None, br, wb, bb, None, film_in=True)
 
 
 def _ops():

@@ -6,9 +6,10 @@ launch computes the same f32 operations with the same roundings, so its outputs 
 for bit. The whole-frame check (test_frame.py::test_fused_chains_equal_their_ops_on_the_gpu) covers the chains at
 the 1080p frame's shapes; here, for the coarse output with the fine block's input, flow_t / vis_t with the convex
 upsample, the pictures' resize with the pyramid, the refine head's input, the encoders' fold beside a cost volume,
-and the refine head's last pair with affine_out: ragged grids whose coarse-to-fine ratio
+the refine head's last pair with affine_out, and the FiLM head's pair with film_modulate on its input: ragged grids whose coarse-to-fine ratio
 is no integer, downscales other than 4x, channel counts that are no multiple of 4 (the 2-byte path), views into wider
-buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample.
+buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample and the FiLM pair
+(one FiLM vector per image).
 """
 import numpy as np
 import pytest
@@ -153,3 +154,17 @@ def test_pair_affine_out_equals_pair_then_affine_out(h, w):
         be.pair_affine_out("refine.q3", "refine.q4", V(x, 4), V(mid), V(y), V(out), 3)
         outs.append(be.host(out).copy())
     same(outs[0], outs[1], "out")
+
+
+@pytest.mark.parametrize("n,h,w,c0,cs", [(1, 60, 108, 0, 48), (2, 13, 30, 4, 52), (1, 5, 7, 4, 52)])
+def test_film_pair_equals_film_then_pair(n, h, w, c0, cs):
+    say("film_pair", n, h, w, c0, cs)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(n * 1000 + h)
+        hb = fill(be, rng, n, h, w, cs)
+        be.set_g(rng.uniform(-0.5, 0.5, n * 96).astype(np.float16).view(np.uint16))  # one FiLM vector per image
+        hm, mid, y = fill(be, rng, n, h, w, 48), fill(be, rng, n, h, w, 48), fill(be, rng, n, h, w, 56)
+        be.film_pair("film.h1", "film.h2", V(hb, c0), 48, V(hm), V(mid), V(y, 8))
+        outs.append(be.host(y).copy())
+    same(outs[0], outs[1], "y")
