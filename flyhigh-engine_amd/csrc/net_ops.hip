@@ -1297,8 +1297,10 @@ __device__ __forceinline__ void sample_rgba_inner(__amdgpu_buffer_rsrc_t rs, uin
 // pixels) and rt has 8-byte pixels, so each quarter-map tap is two loads. A wave whose sample windows all lie inside
 // the frame takes the unclamped tap loads (the same values: clamping changes no column there).
 // A block is 64 x 4 pixels (a wave per row segment); sh = hq / hp and sw = wq / wp come from the host (the same f32
-// quotients the reference forms per pixel).
-template <bool CUBIC, bool QV>
+// quotients the reference forms per pixel). FL: flags may be nonzero. Without flags (the engine's default) stillw = 0
+// and rk = 1, so r * rk is r and mixed * (1 - stillw) + own * stillw is mixed (or +0 for a mixed of -0, which the
+// clamp and the byte conversion turn into the same byte 0): that variant leaves those terms out.
+template <bool CUBIC, bool QV, bool FL>
 __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
                                                                uint32_t h, uint32_t pitch, float sh, float sw,
                                                                View fl, View vis, View rt, uint32_t hq, uint32_t wq,
@@ -1366,9 +1368,9 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
     float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
     const float third = 1.0f / 3.0f;
     float ef = 0.0f;
-    if (flags)
+    if (FL)
         ef = fabsf(ca[0] - cb[0]) * third + fabsf(ca[1] - cb[1]) * third + fabsf(ca[2] - cb[2]) * third;
-    if (flags & 2u) {  // the still test (render.wgsl:134-148) on the 3 x 3 neighbourhood, clamped to the frame
+    if (FL && (flags & 2u)) {  // the still test (render.wgsl:134-148) on the 3 x 3 neighbourhood, clamped to the frame
         uint32_t ta[3][4], tb[3][4];
 #pragma unroll
         for (int j = 0; j < 3; j++) {
@@ -1388,7 +1390,7 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
         for (int c = 0; c < 3; c++) own[c] = 0.5f * (unit_tab(tab, ta[1][1], c) + unit_tab(tab, tb[1][1], c));
         stillw = fminf(fmaxf((ef - es) / 0.04f, 0.0f), 1.0f) * (es < 0.03f ? 1.0f : 0.0f);
     }
-    if (flags & 1u) {  // the decisive blend (render.wgsl:149-153)
+    if (FL && (flags & 1u)) {  // the decisive blend (render.wgsl:149-153)
         const float k = fminf(fmaxf((ef - 0.04f) / 0.08f, 0.0f), 1.0f);
         const float pa = wa_w >= wb_w ? 1.0f : 0.0f;
         bwa = wa_w * (1.0f - k) + pa * k;
@@ -1398,8 +1400,12 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
     uint32_t bytes[3];
 #pragma unroll
     for (int c = 0; c < 3; c++) {
-        const float mixed = ca[c] * bwa + cb[c] * bwb + r[c] * rk;
-        bytes[c] = byte_of(f2h(fminf(fmaxf(mixed * (1.0f - stillw) + own[c] * stillw, 0.0f), 1.0f)));
+        if constexpr (FL) {
+            const float mixed = ca[c] * bwa + cb[c] * bwb + r[c] * rk;
+            bytes[c] = byte_of(f2h(fminf(fmaxf(mixed * (1.0f - stillw) + own[c] * stillw, 0.0f), 1.0f)));
+        } else {
+            bytes[c] = byte_of(f2h(fminf(fmaxf(ca[c] * bwa + cb[c] * bwb + r[c], 0.0f), 1.0f)));
+        }
     }
     dst[(size_t)y * opitch + x] = bytes[2] | (bytes[1] << 8) | (bytes[0] << 16) | 0xff000000u;
 }
@@ -2382,8 +2388,13 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
                         vis->c0 == 4 && reinterpret_cast<uintptr_t>(flow->p) % 16 == 0 && vec4(4, {rt});
         if ((uint64_t)h * w >= kMaxItems || h > 4u * 65535u)
             return fail(-1, "render_rgba: %u x %u pixels exceed the launch limits", w, h);
-        auto k = cubic ? (qv ? render_rgba_kernel<true, true> : render_rgba_kernel<true, false>)
-                       : (qv ? render_rgba_kernel<false, true> : render_rgba_kernel<false, false>);
+        using K = decltype(&render_rgba_kernel<true, true, true>);
+        static const K ks[2][2][2] = {
+            {{render_rgba_kernel<false, false, false>, render_rgba_kernel<false, false, true>},
+             {render_rgba_kernel<false, true, false>, render_rgba_kernel<false, true, true>}},
+            {{render_rgba_kernel<true, false, false>, render_rgba_kernel<true, false, true>},
+             {render_rgba_kernel<true, true, false>, render_rgba_kernel<true, true, true>}}};
+        const K k = ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0];
         hipLaunchKernelGGL(k, dim3((w + 63) / 64, (h + 3) / 4), dim3(kThreads), 0, (hipStream_t)stream,
                            static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h, pitch,
                            (float)hq / (float)hp, (float)wq / (float)wp, in(flow), in(vis), in(rt), hq, wq, fsx, fsy,
