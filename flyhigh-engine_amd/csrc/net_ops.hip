@@ -1291,63 +1291,13 @@ __device__ __forceinline__ void sample_rgba_inner(__amdgpu_buffer_rsrc_t rs, uin
     }
 }
 
-// render_pix of the padded frame (hp x wp) from the two RGBA8 frames, written as RGBA8 (rgba_out of the f16 result),
-// cropped to w x h: render.wgsl:83-160 with its sources replaced by rgba_in.wgsl's conversion of the frames, then
-// rgba_out.wgsl. One lane per frame pixel. QV: flow and vis are channels 0-3 and 4-6 of one 8-channel view (16-byte
-// pixels) and rt has 8-byte pixels, so each quarter-map tap is two loads. A wave whose sample windows all lie inside
-// the frame takes the unclamped tap loads (the same values: clamping changes no column there).
-// A block is 64 x 4 pixels (a wave per row segment); sh = hq / hp and sw = wq / wp come from the host (the same f32
-// quotients the reference forms per pixel). FL: flags may be nonzero. Without flags (the engine's default) stillw = 0
-// and rk = 1, so r * rk is r and mixed * (1 - stillw) + own * stillw is mixed (or +0 for a mixed of -0, which the
-// clamp and the byte conversion turn into the same byte 0): that variant leaves those terms out.
-template <bool CUBIC, bool QV, bool FL>
-__global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
-                                                               uint32_t h, uint32_t pitch, float sh, float sw,
-                                                               View fl, View vis, View rt, uint32_t hq, uint32_t wq,
-                                                               float fsx, float fsy, uint32_t flags, uint32_t* dst,
-                                                               uint32_t opitch) {
-    __shared__ float tab[256];
-    fill_unit_table(tab);
-    const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63u), y = blockIdx.y * 4 + (threadIdx.x >> 6);
-    if (x >= w || y >= h) return;
-    const float iy = ((float)y + 0.5f) * sh - 0.5f, ix = ((float)x + 0.5f) * sw - 0.5f;
-    const int qy0 = (int)floorf(iy), qx0 = (int)floorf(ix);
-    const float qfy = iy - (float)qy0, qfx = ix - (float)qx0;
-    const uint32_t y0 = clampi(qy0, 0, (int)hq - 1), y1 = clampi(qy0 + 1, 0, (int)hq - 1);
-    const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
-    const uint32_t r0 = __umul24(y0, wq), r1 = __umul24(y1, wq);
-    const uint32_t qs[4] = {r0 + x0, r0 + x1, r1 + x0, r1 + x1};
-    float fq[4][4], vq[4][3], rq[4][3];
-    const uint32_t nq = hq * wq;
-    const auto rfl = buf_rsrc(fl.p, QV ? nq * 16u : 0u), rrt = buf_rsrc(rt.p, QV ? nq * rt.cs * 2u : 0u);
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        if constexpr (QV) {
-            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rfl, qs[k] * 16u, 0, 0));
-            const uint2 r =
-                __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rrt, (qs[k] * rt.cs + rt.c0) * 2u, 0, 0));
-            const uint32_t wv[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-            for (int c = 0; c < 4; c++) fq[k][c] = h2f((uint16_t)(wv[c >> 1] >> (16 * (c & 1))));
-#pragma unroll
-            for (int c = 0; c < 3; c++) vq[k][c] = h2f((uint16_t)(wv[2 + (c >> 1)] >> (16 * (c & 1))));
-            rq[k][0] = h2f((uint16_t)r.x), rq[k][1] = h2f((uint16_t)(r.x >> 16)), rq[k][2] = h2f((uint16_t)r.y);
-        } else {
-#pragma unroll
-            for (uint32_t c = 0; c < 4; c++) fq[k][c] = ld(fl, qs[k], c);
-#pragma unroll
-            for (uint32_t c = 0; c < 3; c++) vq[k][c] = ld(vis, qs[k], c), rq[k][c] = ld(rt, qs[k], c);
-        }
-    }
-    float f[4], v[3], r[3];
-#pragma unroll
-    for (uint32_t c = 0; c < 4; c++)
-        f[c] = bil4(fq[0][c], fq[1][c], fq[2][c], fq[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
-#pragma unroll
-    for (uint32_t c = 0; c < 3; c++) {
-        v[c] = bil4(vq[0][c], vq[1][c], vq[2][c], vq[3][c], qfx, qfy) * vis.scale;
-        r[c] = bil4(rq[0][c], rq[1][c], rq[2][c], rq[3][c], qfx, qfy);
-    }
+// One frame pixel of render_rgba from its upsampled flow f (x, y for A, then for B, in frame pixels), visibility
+// logits v and residual r: the blend weights, A and B sampled at the displaced positions, the blend, rgba_out.
+template <bool CUBIC, bool FL>
+__device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const float (&f)[4], const float (&v)[3],
+                                               const float (&r)[3], const uint32_t* fa, const uint32_t* fb, uint32_t w,
+                                               uint32_t h, uint32_t pitch, const float* tab, uint32_t flags,
+                                               uint32_t* dst, uint32_t opitch) {
     const float m = fmaxf(v[0], fmaxf(v[1], v[2]));
     const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
     const float wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
@@ -1408,6 +1358,156 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
         }
     }
     dst[(size_t)y * opitch + x] = bytes[2] | (bytes[1] << 8) | (bytes[0] << 16) | 0xff000000u;
+}
+
+// render_pix of the padded frame (hp x wp) from the two RGBA8 frames, written as RGBA8 (rgba_out of the f16 result),
+// cropped to w x h: render.wgsl:83-160 with its sources replaced by rgba_in.wgsl's conversion of the frames, then
+// rgba_out.wgsl. One lane per frame pixel. QV: flow and vis are channels 0-3 and 4-6 of one 8-channel view (16-byte
+// pixels) and rt has 8-byte pixels, so each quarter-map tap is two loads. A wave whose sample windows all lie inside
+// the frame takes the unclamped tap loads (the same values: clamping changes no column there).
+// A block is 64 x 4 pixels (a wave per row segment); sh = hq / hp and sw = wq / wp come from the host (the same f32
+// quotients the reference forms per pixel). FL: flags may be nonzero. Without flags (the engine's default) stillw = 0
+// and rk = 1, so r * rk is r and mixed * (1 - stillw) + own * stillw is mixed (or +0 for a mixed of -0, which the
+// clamp and the byte conversion turn into the same byte 0): that variant leaves those terms out.
+template <bool CUBIC, bool QV, bool FL>
+__global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
+                                                               uint32_t h, uint32_t pitch, float sh, float sw,
+                                                               View fl, View vis, View rt, uint32_t hq, uint32_t wq,
+                                                               float fsx, float fsy, uint32_t flags, uint32_t* dst,
+                                                               uint32_t opitch) {
+    __shared__ float tab[256];
+    fill_unit_table(tab);
+    const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63u), y = blockIdx.y * 4 + (threadIdx.x >> 6);
+    if (x >= w || y >= h) return;
+    const float iy = ((float)y + 0.5f) * sh - 0.5f, ix = ((float)x + 0.5f) * sw - 0.5f;
+    const int qy0 = (int)floorf(iy), qx0 = (int)floorf(ix);
+    const float qfy = iy - (float)qy0, qfx = ix - (float)qx0;
+    const uint32_t y0 = clampi(qy0, 0, (int)hq - 1), y1 = clampi(qy0 + 1, 0, (int)hq - 1);
+    const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
+    const uint32_t r0 = __umul24(y0, wq), r1 = __umul24(y1, wq);
+    const uint32_t qs[4] = {r0 + x0, r0 + x1, r1 + x0, r1 + x1};
+    float fq[4][4], vq[4][3], rq[4][3];
+    const uint32_t nq = hq * wq;
+    const auto rfl = buf_rsrc(fl.p, QV ? nq * 16u : 0u), rrt = buf_rsrc(rt.p, QV ? nq * rt.cs * 2u : 0u);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        if constexpr (QV) {
+            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rfl, qs[k] * 16u, 0, 0));
+            const uint2 r =
+                __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rrt, (qs[k] * rt.cs + rt.c0) * 2u, 0, 0));
+            const uint32_t wv[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int c = 0; c < 4; c++) fq[k][c] = h2f((uint16_t)(wv[c >> 1] >> (16 * (c & 1))));
+#pragma unroll
+            for (int c = 0; c < 3; c++) vq[k][c] = h2f((uint16_t)(wv[2 + (c >> 1)] >> (16 * (c & 1))));
+            rq[k][0] = h2f((uint16_t)r.x), rq[k][1] = h2f((uint16_t)(r.x >> 16)), rq[k][2] = h2f((uint16_t)r.y);
+        } else {
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) fq[k][c] = ld(fl, qs[k], c);
+#pragma unroll
+            for (uint32_t c = 0; c < 3; c++) vq[k][c] = ld(vis, qs[k], c), rq[k][c] = ld(rt, qs[k], c);
+        }
+    }
+    float f[4], v[3], r[3];
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++)
+        f[c] = bil4(fq[0][c], fq[1][c], fq[2][c], fq[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
+#pragma unroll
+    for (uint32_t c = 0; c < 3; c++) {
+        v[c] = bil4(vq[0][c], vq[1][c], vq[2][c], vq[3][c], qfx, qfy) * vis.scale;
+        r[c] = bil4(rq[0][c], rq[1][c], rq[2][c], rq[3][c], qfx, qfy);
+    }
+    render_rgba_px<CUBIC, FL>(x, y, f, v, r, fa, fb, w, h, pitch, tab, flags, dst, opitch);
+}
+
+// render_rgba with two frame rows per lane (ya and ya + 1, same column; QV layout): the quarter maps' x
+// interpolation at a quarter row (the first half of bil4, v0 * (1 - fx) + v1 * fx) depends on the column and the
+// quarter row alone, so the lane computes it once for both pixels. With sh <= 1/2 (the host's condition) row ya + 1
+// reads quarter rows qb, qb + 1 with qb = qa or qa + 1, so three quarter rows cover both pixels (the third only
+// when qb = qa + 1, which is uniform over the wave). A block is 64 x 8 pixels.
+template <bool CUBIC, bool FL>
+__global__ __launch_bounds__(kThreads) void render_rgba2_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
+                                                                uint32_t h, uint32_t pitch, float sh, float sw,
+                                                                View fl, View vis, View rt, uint32_t hq, uint32_t wq,
+                                                                float fsx, float fsy, uint32_t flags, uint32_t* dst,
+                                                                uint32_t opitch) {
+    __shared__ float tab[256];
+    fill_unit_table(tab);
+    const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63u), ya = blockIdx.y * 8 + (threadIdx.x >> 6) * 2;
+    if (x >= w || ya >= h) return;
+    const float ix = ((float)x + 0.5f) * sw - 0.5f;
+    const float iya = ((float)ya + 0.5f) * sh - 0.5f, iyb = ((float)(ya + 1) + 0.5f) * sh - 0.5f;
+    const int qx0 = (int)floorf(ix), qa = (int)floorf(iya), qb = (int)floorf(iyb);
+    const float qfx = ix - (float)qx0, fya = iya - (float)qa, fyb = iyb - (float)qb;
+    const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
+    const uint32_t nq = hq * wq;
+    const auto rfl = buf_rsrc(fl.p, nq * 16u), rrt = buf_rsrc(rt.p, nq * rt.cs * 2u);
+    // the taps of quarter rows qa, qa + 1, qa + 2 (clamped) at columns x0, x1: 16 bytes of flow | vis, 8 of rt each
+    uint4 qv[3][2];
+    uint2 qr[3][2];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const uint32_t row = __umul24((uint32_t)clampi(qa + j, 0, (int)hq - 1), wq);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t q = row + (i ? x1 : x0);
+            qv[j][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rfl, q * 16u, 0, 0));
+            qr[j][i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rrt, (q * rt.cs + rt.c0) * 2u, 0, 0));
+        }
+    }
+    // the x interpolation of quarter row j's 10 channels (flow 4, vis 3, rt 3)
+    auto xlerp = [&](int j, float (&o)[10]) {
+        float t[2][10];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t wv[4] = {qv[j][i].x, qv[j][i].y, qv[j][i].z, qv[j][i].w};
+#pragma unroll
+            for (int c = 0; c < 7; c++) t[i][c] = h2f((uint16_t)(wv[c >> 1] >> (16 * (c & 1))));
+            t[i][7] = h2f((uint16_t)qr[j][i].x), t[i][8] = h2f((uint16_t)(qr[j][i].x >> 16));
+            t[i][9] = h2f((uint16_t)qr[j][i].y);
+        }
+#pragma unroll
+        for (int c = 0; c < 10; c++) o[c] = t[0][c] * (1.0f - qfx) + t[1][c] * qfx;
+    };
+    // bil4's second half for one pixel from its two quarter rows' x interpolations
+    auto finish = [&](const float (&l0)[10], const float (&l1)[10], float fy, float (&f)[4], float (&v)[3],
+                      float (&r)[3]) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) f[c] = (l0[c] * (1.0f - fy) + l1[c] * fy) * ((c & 1) == 0 ? fsx : fsy);
+#pragma unroll
+        for (int c = 0; c < 3; c++) {
+            v[c] = (l0[4 + c] * (1.0f - fy) + l1[4 + c] * fy) * vis.scale;
+            r[c] = l0[7 + c] * (1.0f - fy) + l1[7 + c] * fy;
+        }
+    };
+    float l0[10], l1[10];
+    xlerp(0, l0);
+    xlerp(1, l1);
+    float fA[4], vA[3], rA[3], fB[4], vB[3], rB[3];
+    finish(l0, l1, fya, fA, vA, rA);
+    if (qb == qa) {  // uniform
+        finish(l0, l1, fyb, fB, vB, rB);
+    } else {
+        float l2[10];
+        xlerp(2, l2);
+        finish(l1, l2, fyb, fB, vB, rB);
+    }
+    // pixel B's 10 values wait in LDS (this lane's own slots: no barrier) while pixel A renders, so they hold no
+    // registers through A's sampling
+    __shared__ float park[10][kThreads];
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int c = 0; c < 4; c++) park[c][t] = fB[c];
+#pragma unroll
+    for (int c = 0; c < 3; c++) park[4 + c][t] = vB[c], park[7 + c][t] = rB[c];
+    render_rgba_px<CUBIC, FL>(x, ya, fA, vA, rA, fa, fb, w, h, pitch, tab, flags, dst, opitch);
+    if (ya + 1 < h) {  // uniform
+#pragma unroll
+        for (int c = 0; c < 4; c++) fB[c] = park[c][t];
+#pragma unroll
+        for (int c = 0; c < 3; c++) vB[c] = park[4 + c][t], rB[c] = park[7 + c][t];
+        render_rgba_px<CUBIC, FL>(x, ya + 1, fB, vB, rB, fa, fb, w, h, pitch, tab, flags, dst, opitch);
+    }
 }
 
 // The antialiased resize of n padded RGBA8 frames (hp x wp, rgba_in's BGR f16) to oh x ow, into a view of 8-byte
@@ -2394,11 +2494,15 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
              {render_rgba_kernel<false, true, false>, render_rgba_kernel<false, true, true>}},
             {{render_rgba_kernel<true, false, false>, render_rgba_kernel<true, false, true>},
              {render_rgba_kernel<true, true, false>, render_rgba_kernel<true, true, true>}}};
-        const K k = ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0];
-        hipLaunchKernelGGL(k, dim3((w + 63) / 64, (h + 3) / 4), dim3(kThreads), 0, (hipStream_t)stream,
-                           static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h, pitch,
-                           (float)hq / (float)hp, (float)wq / (float)wp, in(flow), in(vis), in(rt), hq, wq, fsx, fsy,
-                           flags, static_cast<uint32_t*>(out), opitch);
+        // two rows per lane where the quarter maps are upsampled 2x or more vertically (a frame render's are 4x+)
+        const bool two = qv && 2ull * hq <= hp;
+        static const K k2[2][2] = {{render_rgba2_kernel<false, false>, render_rgba2_kernel<false, true>},
+                                   {render_rgba2_kernel<true, false>, render_rgba2_kernel<true, true>}};
+        const K k = two ? k2[cubic ? 1 : 0][flags ? 1 : 0] : ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0];
+        hipLaunchKernelGGL(k, dim3((w + 63) / 64, two ? (h + 7) / 8 : (h + 3) / 4), dim3(kThreads), 0,
+                           (hipStream_t)stream, static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h,
+                           pitch, (float)hq / (float)hp, (float)wq / (float)wp, in(flow), in(vis), in(rt), hq, wq, fsx,
+                           fsy, flags, static_cast<uint32_t*>(out), opitch);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "render_rgba: launch failed: %s", hipGetErrorString(e));
     });

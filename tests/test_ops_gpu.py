@@ -338,22 +338,24 @@ def test_rgba_resize_equals_rgba_in_then_the_antialiased_resize(h, w, oh, ow):
     exact(got[..., 3], np.zeros_like(got[..., 3]), "rgba_resize channel 3")
 
 
-@pytest.mark.parametrize("cubic,flags,amp,size", [(True, 0, 6, (1080, 1920)), (False, 0, 6, (1080, 1920)),
-                                                  (True, 2, 3, (150, 300)), (True, 3, 6, (150, 300)),
-                                                  (False, 3, 2, (97, 130)), (True, 0, 40, (97, 130))])
-def test_render_rgba_matches_rgba_in_render_rgba_out(cubic, flags, amp, size):
+@pytest.mark.parametrize("cubic,flags,amp,size,qdiv", [(True, 0, 6, (1080, 1920), 9), (False, 0, 6, (1080, 1920), 9),
+                                                       (True, 2, 3, (150, 300), 9), (True, 3, 6, (150, 300), 9),
+                                                       (False, 3, 2, (97, 130), 9), (True, 0, 40, (97, 130), 9),
+                                                       (True, 0, 6, (97, 130), 1.5), (True, 3, 3, (150, 300), 1.5)])
+def test_render_rgba_matches_rgba_in_render_rgba_out(cubic, flags, amp, size, qdiv):
     """The fused frame-size render from the RGBA8 frames to the RGBA8 frame, against the oracle's rgba_in (padded),
     render at the padded size with the flow scaled per axis (the internal-size mode, maps at a non-integer ratio),
     and rgba_out: bytes within 1 everywhere (expf's last bit can move an f16 result next to a byte boundary), almost
     all identical; and bit-identical to the GPU's own unfused composition (the same device expf). amp: the range of
-    the map-size flow; 40 sends taps far outside the frame (clamped)."""
+    the map-size flow; 40 sends taps far outside the frame (clamped). qdiv: frame rows per quarter-map row (9: the
+    kernel with two frame rows per lane, an odd frame height leaving its last row alone; 1.5: one row per lane)."""
     import torch
-    say("render_rgba", cubic, flags, amp, size)
+    say("render_rgba", cubic, flags, amp, size, qdiv)
     fh = fhops()
     rng = np.random.default_rng(int(amp) + flags + 10 * cubic + size[1])
     h, w = size
     hp, wp = (h + 31) // 32 * 32, (w + 31) // 32 * 32
-    hq, wq = max(2, hp // 9), max(2, wp // 9)
+    hq, wq = max(2, int(hp // qdiv)), max(2, int(wp // qdiv))
     fsx, fsy = float(np.float32(wp) / np.float32(4 * wq)), float(np.float32(hp) / np.float32(4 * hq))
     fr = _frames(rng, 2, h, w)
     if flags & 2:  # make B mostly equal to A so the still test fires somewhere
