@@ -521,30 +521,74 @@ def pmc_workload(args, torch, fhconv, flyhighfg, net, stream):
     return 0
 
 
-def _counter_per_dispatch(csv_path, counter):
-    """{kernel name: mean counter value per dispatch} from a rocprofv3 counter_collection.csv."""
+def pmc_render(args, torch, np, stream):
+    """The 1080p frame's render (fhc_render_rgba, as the frame runs it) --pmc-reps times over rotating sets of input
+    and output frames (> 512 MB, so every launch reads its frames from HBM), after one eager frame that fills the
+    quarter maps, then a device copy of COPY_BYTES as many times: the workload of the render's FETCH_SIZE /
+    WRITE_SIZE passes (the eager frame's own render is the kernel's first dispatch, left out of the mean)."""
+    import flyhighfg_net as fnet
+    W = fnet.make_weights(7)
+    be = fnet.GpuBackend(W, stream=stream)
+    f = fnet.FlyHighFG(be, 864, 480, frame=(1920, 1080), repair=1)
+    be.upload_frames(f.frames, np.stack([fnet.procedural_frame(1920, 1080), fnet.procedural_frame(1920, 1080, 12, 0)]))
+    be.set_g(fnet.film_mlp(W, 0.5))
+    with torch.cuda.stream(stream):
+        f.pair()
+        f.mid(0.5, None)
+    torch.cuda.synchronize()
+    per = 3 * f.frames.numel() // 2 * 4
+    nsets = max(2, -(-(600 << 20) // per))
+    sets = [(torch.randint_like(f.frames, -2 ** 31, 2 ** 31 - 1), torch.empty_like(f.rgba)) for _ in range(nsets)]
+    fh = be.fh
+    vf, vv, vr = fh.View(f.up7, 0), fh.View(f.up7, 4), fh.View(f.Rt, 0)
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device="cuda").uniform_(-1, 1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(args.pmc_reps):
+            fr, out = sets[i % nsets]
+            fh.render_rgba(fr[0:1], fr[1:2], vf, vv, vr, f.hp, f.wp, f.cubic, f.render_flags, f.fsx, f.fsy, out=out,
+                           stream=stream)
+        for _ in range(args.pmc_reps):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps(dict(pmc_layer=args.pmc_layer, variant="render_rgba (two frame rows per lane)",
+                          reps=args.pmc_reps, cold_sets=nsets, copy_bytes=COPY_BYTES)), flush=True)
+    return 0
+
+
+def _counter_per_dispatch(csv_path, counter, skip_first=()):
+    """{kernel name: mean counter value per dispatch} from a rocprofv3 counter_collection.csv; for the kernels whose
+    name contains one of skip_first, the first dispatch is left out."""
     import csv
     import collections
-    tot, disp = collections.defaultdict(float), collections.defaultdict(set)
+    vals = collections.defaultdict(lambda: collections.defaultdict(float))
     with open(csv_path) as f:
         for row in csv.DictReader(f):
             if row["Counter_Name"] != counter:
                 continue
-            tot[row["Kernel_Name"]] += float(row["Counter_Value"])
-            disp[row["Kernel_Name"]].add(row["Dispatch_Id"])
-    return {k: tot[k] / len(disp[k]) for k in tot}
+            vals[row["Kernel_Name"]][int(row["Dispatch_Id"])] += float(row["Counter_Value"])
+    out = {}
+    for k, d in vals.items():
+        ids = sorted(d)
+        if any(s in k for s in skip_first) and len(ids) > 1:
+            ids = ids[1:]
+        out[k] = sum(d[i] for i in ids) / len(ids)
+    return out
 
 
 def traffic_from(args):
     """HBM bytes per launch of --pmc-layer's conv kernel from the FETCH_SIZE and WRITE_SIZE passes (KiB per
     dispatch), each scaled by what the same counter reads for the copy of COPY_BYTES; written to
     profiles/traffic_<layer>.txt."""
-    fetch = _counter_per_dispatch(args.traffic_from[0], "FETCH_SIZE")
-    write = _counter_per_dispatch(args.traffic_from[1], "WRITE_SIZE")
-    conv = [k for k in fetch if "conv" in k]
+    render = args.pmc_layer == "frame_render"
+    skip = ("render_rgba",) if render else ()
+    fetch = _counter_per_dispatch(args.traffic_from[0], "FETCH_SIZE", skip)
+    write = _counter_per_dispatch(args.traffic_from[1], "WRITE_SIZE", skip)
+    conv = [k for k in fetch if ("render_rgba" in k if render else "conv" in k)]
     copy = [k for k in fetch if "copybuffer" in k.lower()]  # the runtime's device-to-device copy kernel
     if len(conv) != 1 or len(copy) != 1:
-        raise SystemExit(f"expected one conv and one copy kernel, got {conv} / {copy}")
+        raise SystemExit(f"expected one {'render' if render else 'conv'} and one copy kernel, got {conv} / {copy}")
     fk, wk = conv[0], copy[0]
     f_scale = COPY_BYTES / (fetch[wk] * 1024.0)
     w_scale = COPY_BYTES / (write[wk] * 1024.0)
@@ -627,9 +671,10 @@ def main():
                     help="only time the 1080p frame (RGBA8 in, every op of pair() + mid(), RGBA8 out, one HIP graph) "
                          "and print it as one JSON line")
     ap.add_argument("--tune", help="plan with this choice table (cin,cout,h,w,stride=code lines) instead of autotuning")
-    ap.add_argument("--pmc-layer", help="only run this frame layer --pmc-reps times over rotating (cold) buffers, "
-                                        "then a copy of known size as many times: the workload of the rocprofv3 "
-                                        "--pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-layer", help="only run this frame layer (or fused pair, or frame_render: the frame-size "
+                                        "render) --pmc-reps times over rotating (cold) buffers, then a copy of "
+                                        "known size as many times: the workload of the rocprofv3 --pmc FETCH_SIZE / "
+                                        "WRITE_SIZE passes")
     ap.add_argument("--pmc-reps", type=int, default=64)
     ap.add_argument("--eager-frames", type=int, default=0,
                     help="only run the 1080p frame (as --only-frame builds it) this many times eagerly, untimed: the "
@@ -665,6 +710,9 @@ def main():
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
     if args.eager_frames:
         return eager_frames(args, torch, np, stream)
+    if args.pmc_layer == "frame_render" and not args.traffic_from:
+        fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
+        return pmc_render(args, torch, np, stream)
     if args.only_frame:
         if not args.tune:  # no autotuning here: the frame's convs take the committed MI355X choices
             fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())

@@ -1424,16 +1424,21 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
 // interpolation at a quarter row (the first half of bil4, v0 * (1 - fx) + v1 * fx) depends on the column and the
 // quarter row alone, so the lane computes it once for both pixels. With sh <= 1/2 (the host's condition) row ya + 1
 // reads quarter rows qb, qb + 1 with qb = qa or qa + 1, so three quarter rows cover both pixels (the third only
-// when qb = qa + 1, which is uniform over the wave). A block is 64 x 8 pixels.
+// when qb = qa + 1, which is uniform over the wave). A block is 64 x 8 pixels. The grid is 1-D: workgroups b with
+// the same b % 8 run on one XCD, and class k = b % 8 takes block rows [k * rows8, (k + 1) * rows8) in row-major
+// order, so the tap rows and cache lines that neighbouring blocks share are fetched into one L2.
 template <bool CUBIC, bool FL>
 __global__ __launch_bounds__(kThreads) void render_rgba2_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
                                                                 uint32_t h, uint32_t pitch, float sh, float sw,
                                                                 View fl, View vis, View rt, uint32_t hq, uint32_t wq,
                                                                 float fsx, float fsy, uint32_t flags, uint32_t* dst,
-                                                                uint32_t opitch) {
+                                                                uint32_t opitch, uint32_t nbx, uint32_t rows8) {
+    const uint32_t k = blockIdx.x & 7u, j = blockIdx.x >> 3;
+    const uint32_t by = k * rows8 + j / nbx, bx = j % nbx;
+    if (j >= rows8 * nbx) return;  // uniform over the workgroup
     __shared__ float tab[256];
     fill_unit_table(tab);
-    const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63u), ya = blockIdx.y * 8 + (threadIdx.x >> 6) * 2;
+    const uint32_t x = bx * 64 + (threadIdx.x & 63u), ya = by * 8 + (threadIdx.x >> 6) * 2;
     if (x >= w || ya >= h) return;
     const float ix = ((float)x + 0.5f) * sw - 0.5f;
     const float iya = ((float)ya + 0.5f) * sh - 0.5f, iyb = ((float)(ya + 1) + 0.5f) * sh - 0.5f;
@@ -2496,13 +2501,23 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
              {render_rgba_kernel<true, true, false>, render_rgba_kernel<true, true, true>}}};
         // two rows per lane where the quarter maps are upsampled 2x or more vertically (a frame render's are 4x+)
         const bool two = qv && 2ull * hq <= hp;
-        static const K k2[2][2] = {{render_rgba2_kernel<false, false>, render_rgba2_kernel<false, true>},
-                                   {render_rgba2_kernel<true, false>, render_rgba2_kernel<true, true>}};
-        const K k = two ? k2[cubic ? 1 : 0][flags ? 1 : 0] : ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0];
-        hipLaunchKernelGGL(k, dim3((w + 63) / 64, two ? (h + 7) / 8 : (h + 3) / 4), dim3(kThreads), 0,
-                           (hipStream_t)stream, static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h,
-                           pitch, (float)hq / (float)hp, (float)wq / (float)wp, in(flow), in(vis), in(rt), hq, wq, fsx,
-                           fsy, flags, static_cast<uint32_t*>(out), opitch);
+        const float sh = (float)hq / (float)hp, sw = (float)wq / (float)wp;
+        if (two) {
+            // 8 XCD classes of rows8 block rows each (the last ones may run past the frame: their workgroups return)
+            const uint32_t nbx = (w + 63) / 64, rows8 = ((h + 7) / 8 + 7) / 8;
+            using K2 = decltype(&render_rgba2_kernel<true, true>);
+            const K2 k2 = cubic ? (flags ? render_rgba2_kernel<true, true> : render_rgba2_kernel<true, false>)
+                                : (flags ? render_rgba2_kernel<false, true> : render_rgba2_kernel<false, false>);
+            hipLaunchKernelGGL(k2, dim3(8 * rows8 * nbx), dim3(kThreads), 0, (hipStream_t)stream,
+                               static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h, pitch, sh, sw,
+                               in(flow), in(vis), in(rt), hq, wq, fsx, fsy, flags, static_cast<uint32_t*>(out), opitch,
+                               nbx, rows8);
+        } else {
+            hipLaunchKernelGGL(ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0], dim3((w + 63) / 64, (h + 3) / 4),
+                               dim3(kThreads), 0, (hipStream_t)stream, static_cast<const uint32_t*>(a),
+                               static_cast<const uint32_t*>(b), w, h, pitch, sh, sw, in(flow), in(vis), in(rt), hq, wq,
+                               fsx, fsy, flags, static_cast<uint32_t*>(out), opitch);
+        }
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "render_rgba: launch failed: %s", hipGetErrorString(e));
     });
