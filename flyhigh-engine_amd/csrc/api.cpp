@@ -808,6 +808,7 @@ extern "C" int fhc_conv_run(const fhc_conv_plan* p, const void* x, void* y, cons
         int dev = -1;
         if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
             return fail(-1, "fhc_conv_run: the plan belongs to device %d, the current device is %d", p->device, dev);
+        if (p->args.split) return fail(-1, "fhc_conv_run: a sibling plan runs with fhc_conv_sibling_run");
         if (p->family == 2) {  // fused pair: x is the first conv's input, y and res the second's output and residual
             if (p->film_in) return fail(-1, "fhc_conv_run: the pair takes FiLM vectors: run it with fhc_conv_pair_run_film");
             return run_pair(p, x, y, res, nullptr, stream, "fhc_conv_run");
@@ -1344,5 +1345,125 @@ extern "C" int fhc_conv_run_noalloc(const fhc_conv_plan* p, const void* x, void*
             if (!ws) return -1;
         }
         return fhc_conv_run(p, x, y, res, ws, stream);
+    });
+}
+
+extern "C" int fhc_conv_sibling_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
+                                            const uint16_t* slope_a, const fhc_conv_desc* desc_b,
+                                            const uint16_t* w_b, const uint16_t* bias_b, const uint16_t* slope_b,
+                                            fhc_conv_plan** out) {
+    return guard(-1, [&]() -> int {
+        const char* who = "fhc_conv_sibling_plan_create";
+        if (!out) return fail(-1, "%s: NULL output handle", who);
+        *out = nullptr;
+        if (!desc_a || !desc_b) return fail(-1, "%s: NULL descriptor", who);
+        if (!w_a || !bias_a || !w_b || !bias_b) return fail(-1, "%s: NULL weights or bias", who);
+        fhc_conv_desc A = *desc_a, B = *desc_b;
+        for (fhc_conv_desc* d : {&A, &B}) {
+            if (d->x_cstride == 0) d->x_cstride = d->cin;
+            if (d->y_cstride == 0) d->y_cstride = d->cout;
+            if (d->r_cstride == 0) d->r_cstride = d->cout;
+        }
+        std::string why;
+        if (!valid_desc(A, &why)) return fail(-1, "%s: first conv: %s", who, why.c_str());
+        if (!valid_desc(B, &why)) return fail(-1, "%s: second conv: %s", who, why.c_str());
+        if (A.n != B.n || A.h != B.h || A.w != B.w || A.cin != B.cin || A.kh != B.kh || A.kw != B.kw ||
+            A.stride != B.stride || A.pad != B.pad || A.x_cstride != B.x_cstride || A.x_c0 != B.x_c0)
+            return fail(-1, "%s: the two convs must read the same input view with the same geometry", who);
+        if (B.residual) return fail(-1, "%s: the second conv cannot take a residual", who);
+        if (A.act == FHC_ACT_LEAKY || B.act == FHC_ACT_LEAKY)
+            return fail(-1, "%s: identity or PReLU activations only", who);
+        if ((A.act == FHC_ACT_PRELU && !slope_a) || (B.act == FHC_ACT_PRELU && !slope_b))
+            return fail(-1, "%s: PReLU needs a slope", who);
+        // the combined conv: A's channels, zero channels up to a multiple of 4, B's. Its K order per output channel
+        // is the kernel-row split's or the plain chain's: the one the planner gives both convs alone when it gives
+        // both a direct configuration with the same split (the outputs are then bit-identical), else the split's
+        const uint32_t split = (A.cout + 3) & ~3u, total = split + B.cout, cin32 = div_ceil(A.cin, 32) * 32;
+        int wk = 3;
+        {
+            fhc_conv_plan pa{}, pb{};
+            std::string w1, w2;
+            if (plan_choose(A, pa, &w1) && plan_choose(B, pb, &w2) && pa.family == 1 && pb.family == 1 &&
+                kDirectCfgs[pa.cfg].na == 1 && kDirectCfgs[pb.cfg].na == 1 &&
+                kDirectCfgs[pa.cfg].wk == kDirectCfgs[pb.cfg].wk && kDirectCfgs[pa.cfg].cin32 == (int)cin32 &&
+                kDirectCfgs[pb.cfg].cin32 == (int)cin32)
+                wk = kDirectCfgs[pa.cfg].wk;
+        }
+        int idx = -1;
+        for (int i = 0; i < kNumDirect; i++) {
+            const DirectCfg& c = kDirectCfgs[i];
+            if (c.ks == (int)A.kh && c.stride == (int)A.stride && c.cin32 == (int)cin32 && c.na == 1 && c.wk == wk &&
+                !c.persist && 16u * c.wn >= total && sibling_launcher(i) && (idx < 0 || c.wn < kDirectCfgs[idx].wn))
+                idx = i;
+        }
+        if (idx < 0)
+            return fail(-1, "%s: no sibling kernel for %u -> %u + %u channels (3x3 stride 1, 33-64 input channels, at "
+                            "most 48 output channels with the first conv's padded to 4)", who, A.cin, A.cout, B.cout);
+        fhc_conv_desc C = A;
+        C.cout = total;
+        C.act = A.act == FHC_ACT_PRELU || B.act == FHC_ACT_PRELU ? FHC_ACT_PRELU : FHC_ACT_NONE;
+        C.variant = 0;
+        C.ksplit = 0;
+        auto p = std::make_unique<fhc_conv_plan>();
+        p->d = C;  // A's output and residual views: the kernel stores A's channels through them, B's through y2
+        p->dmem = nullptr;
+        p->g.hout = (C.h + 2 * C.pad - C.kh) / C.stride + 1;
+        p->g.wout = (C.w + 2 * C.pad - C.kw) / C.stride + 1;
+        p->g.taps = C.kh * C.kw;
+        p->g.cin8 = div_ceil(C.cin, 8) * 8;
+        if (!configure_direct(*p, idx, &why)) return fail(-1, "%s: %s", who, why.c_str());
+        p->launch = sibling_launcher(idx);
+        p->args.split = (int)split;
+        p->args.cout1 = (int)A.cout;
+        p->args.y2cs = (int)B.y_cstride;
+        p->args.y2c0 = (int)B.y_c0;
+        hipError_t e = hipGetDevice(&p->device);
+        if (e != hipSuccess) return fail(-1, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+        const size_t kk = (size_t)A.cin * A.kh * A.kw;
+        std::vector<uint16_t> w(total * kk, 0), b(total, 0), sl(total, 0x3c00);  // slope 1: no activation
+        memcpy(w.data(), w_a, A.cout * kk * 2);
+        memcpy(w.data() + split * kk, w_b, B.cout * kk * 2);
+        memcpy(b.data(), bias_a, A.cout * 2);
+        memcpy(b.data() + split, bias_b, B.cout * 2);
+        if (A.act == FHC_ACT_PRELU) memcpy(sl.data(), slope_a, A.cout * 2);
+        if (B.act == FHC_ACT_PRELU) memcpy(sl.data() + split, slope_b, B.cout * 2);
+        std::vector<uint16_t> packed;
+        pack_weights(*p, w.data(), packed);
+        e = upload(*p, packed, b.data(), sl.data());
+        if (e != hipSuccess) {
+            if (p->dmem) (void)hipFree(p->dmem);
+            return fail(-1, "%s: device upload: %s", who, hipGetErrorString(e));
+        }
+        *out = p.release();
+        clear_error();
+        return 0;
+    });
+}
+
+extern "C" int fhc_conv_sibling_run(const fhc_conv_plan* p, const void* x, void* y_a, const void* res_a, void* y_b,
+                                    void* stream) {
+    return guard(-1, [&]() -> int {
+        const char* who = "fhc_conv_sibling_run";
+        if (!p) return fail(-1, "%s: NULL plan", who);
+        if (!p->args.split) return fail(-1, "%s: not a sibling plan", who);
+        if (!x || !y_a || !y_b) return fail(-1, "%s: NULL input or output", who);
+        if (p->d.residual && !res_a) return fail(-1, "%s: the first conv has a residual but res_a is NULL", who);
+        if (((uintptr_t)x | (uintptr_t)y_a | (uintptr_t)res_a | (uintptr_t)y_b) & 1u)
+            return fail(-1, "%s: f16 tensors must be 2-byte aligned", who);
+        int dev = -1;
+        if (hipGetDevice(&dev) != hipSuccess || dev != p->device)
+            return fail(-1, "%s: the plan belongs to device %d, the current device is %d", who, p->device, dev);
+        ConvKArgs a = p->args;
+        a.x = static_cast<const uint16_t*>(x);
+        a.y = static_cast<uint16_t*>(y_a);
+        a.res = static_cast<const uint16_t*>(res_a);
+        a.y2 = static_cast<uint16_t*>(y_b);
+        a.xvec = ((uintptr_t)x % 16 == 0) && a.xcs % 8 == 0 && a.xc0 % 8 == 0;
+        a.yvec = ((uintptr_t)y_a % 8 == 0) && a.ycs % 4 == 0 && a.yc0 % 4 == 0;
+        a.y2vec = ((uintptr_t)y_b % 8 == 0) && a.y2cs % 4 == 0 && a.y2c0 % 4 == 0;
+        a.rvec = a.residual && ((uintptr_t)res_a % 8 == 0) && a.rcs % 4 == 0 && a.rc0 % 4 == 0 && a.cout1 % 4 == 0;
+        const hipError_t e = p->launch(a, p->grid, p->lds, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return fail(-1, "%s: launch: %s", who, hipGetErrorString(e));
+        return 0;
     });
 }

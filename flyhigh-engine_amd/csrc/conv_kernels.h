@@ -36,6 +36,12 @@ struct ConvKArgs {
                                 // (the one-tile pair kernel's second conv, cout <= 4, no residual)
     const uint16_t* film;       // the one-tile pair kernel's first conv: FiLM vectors [n][gamma cin | beta cin]
                                 // (f16) applied to the input as it is staged, or null
+    // sibling convs (two convs of one input in one launch, the one-tile direct kernel's SPLIT form): output channels
+    // below `split` belong to the first conv (its cout1 of them stored through y with the residual), the rest to the
+    // second, stored through y2 at channel co - split without residual
+    int split, cout1;
+    uint16_t* y2;
+    int y2cs, y2c0, y2vec;
 };
 
 // A tile configuration: wave grid WM x WN x WK (WK > 1 splits K inside the workgroup), each wave FM output rows
@@ -61,6 +67,8 @@ inline constexpr TileCfg kTileCfgs[kNumCfg + 1] = {
 };
 
 using LaunchFn = hipError_t (*)(const ConvKArgs&, dim3 grid, size_t lds, hipStream_t);
+// the SPLIT (sibling convs) launcher of direct configuration `index`, or null where it is not instantiated
+LaunchFn sibling_launcher(int index);
 
 // The launcher of configuration `cfg` for a (kernel size, stride) pair, or nullptr if not instantiated.
 LaunchFn conv_launcher(int ks, int stride, int cfg);

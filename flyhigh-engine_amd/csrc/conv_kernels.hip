@@ -20,6 +20,7 @@
 // before the epilogue; a global split (grid.y = z) instead writes f32 partials that splitk_reduce sums in z order.
 #include "conv_kernels.h"
 #include "direct_impl.h"
+#include "direct_table.h"
 
 namespace fhc {
 
@@ -244,6 +245,31 @@ hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s) {
     const size_t total = (size_t)a.n * a.hout * a.wout * ((a.cout + 3) / 4);
     hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a, ksplit);
     return hipGetLastError();
+}
+
+// The sibling convs' configurations, 33-64 input channels, 2 or 3 channel blocks (the frame's fine.out + up.w:
+// 48 -> 7 + 36): one row of 16 pixels with the kernel-row K split (3 waves per channel block, the configuration the
+// committed choice table gives both), or two rows without it (the K order of the planner's default for both)
+constexpr int find_direct(int ks, int s, int cin32, int fm, int wm, int wn, int na, int wk) {
+    for (int i = 0; i < kNumDirect; i++) {
+        const DirectCfg& c = kDirectCfgs[i];
+        if (c.ks == ks && c.stride == s && c.cin32 == cin32 && c.fm == fm && c.wm == wm && c.wn == wn && c.na == na &&
+            c.wk == wk && !c.persist)
+            return i;
+    }
+    return -1;
+}
+
+LaunchFn sibling_launcher(int index) {
+    constexpr int k64_2 = find_direct(3, 1, 64, 1, 1, 2, 1, 3), k64_3 = find_direct(3, 1, 64, 1, 1, 3, 1, 3);
+    constexpr int r64_2 = find_direct(3, 1, 64, 1, 2, 2, 1, 1), r64_3 = find_direct(3, 1, 64, 1, 2, 3, 1, 1);
+    static_assert(k64_2 >= 0 && k64_3 >= 0 && r64_2 >= 0 && r64_3 >= 0, "sibling configurations in the table");
+    if (index < 0) return nullptr;
+    if (index == k64_2) return launch_tile_split<3, 1, 64, 1, 1, 2, 3>;
+    if (index == k64_3) return launch_tile_split<3, 1, 64, 1, 1, 3, 3>;
+    if (index == r64_2) return launch_tile_split<3, 1, 64, 1, 2, 2, 1>;
+    if (index == r64_3) return launch_tile_split<3, 1, 64, 1, 2, 3, 1>;
+    return nullptr;
 }
 
 }  // namespace fhc

@@ -551,8 +551,9 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
 // The one-tile-per-workgroup kernel of the configurations with one channel block per wave: every global load of
 // the tile issued before the first wait (weights, halo, residual, then bias and multipliers), the halo into LDS, the
 // MFMA chain reading LDS one K-step ahead, the epilogue per wave. Measured faster at one tile per workgroup than
-// the buffer loop above, whose deeper pipelining only pays over several tiles.
-template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK, bool VEC>
+// the buffer loop above, whose deeper pipelining only pays over several tiles. SPLIT: sibling convs (the fields
+// split, cout1, y2 of ConvKArgs): the same K loop for every output channel, two epilogues.
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK, bool VEC, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
     static_assert(WK == 1 || (WK == 3 && KS == 3), "the K split runs one kernel row per wave");
     constexpr int TH = FM * WM, TW = 16, BN = 16 * WN, NT = 64 * WM * WN * WK;
@@ -601,8 +602,15 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
     for (int f = 0; f < FM; f++) {
         rres[f] = uint2{0u, 0u};
         const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
-        if (wk == 0 && a.residual && oy < a.hout && ox < a.wout && co < a.cout)
-            rres[f] = load_res4(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, true);
+        if constexpr (SPLIT) {  // the first conv's channels only, cout1 of them
+            ConvKArgs a1 = a;
+            a1.cout = a.cout1;
+            if (wk == 0 && a.residual && oy < a.hout && ox < a.wout && co < a.split)
+                rres[f] = load_res4(a1, ((size_t)img * a.hout + oy) * a.wout + ox, co, true);
+        } else {
+            if (wk == 0 && a.residual && oy < a.hout && ox < a.wout && co < a.cout)
+                rres[f] = load_res4(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, true);
+        }
     }
     float bias[4], neg[4];
 #pragma unroll
@@ -671,7 +679,26 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
             for (int f = 0; f < FM; f++) acc[f] += red[(((k - 1) * WM * WN + wmn) * FM + f) * 64 + lane];
     }
 
-    if (co < a.cout) {
+    if constexpr (SPLIT) {
+        // channel groups below split: the first conv (cout1 stored, with its residual); the rest: the second conv
+        ConvKArgs o = a;
+        int c = co;
+        if (co < a.split) {
+            o.cout = a.cout1;
+        } else {
+            o.y = a.y2, o.ycs = a.y2cs, o.yc0 = a.y2c0, o.yvec = a.y2vec;
+            o.residual = 0, o.cout = a.cout - a.split;
+            c = co - a.split;
+        }
+        if (co < a.cout) {
+#pragma unroll
+            for (int f = 0; f < FM; f++) {
+                const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
+                if (oy < a.hout && ox < a.wout)
+                    epilogue4r(o, ((size_t)img * a.hout + oy) * a.wout + ox, c, acc[f], bias, neg, rres[f]);
+            }
+        }
+    } else if (co < a.cout) {
 #pragma unroll
         for (int f = 0; f < FM; f++) {
             const int oy = oy0 + wm * FM + f, ox = ox0 + (lane & 15);
@@ -679,6 +706,18 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
                 epilogue4r(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, acc[f], bias, neg, rres[f]);
         }
     }
+}
+
+// The sibling convs' launch of a one-tile configuration (one workgroup per tile, one channel tile)
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK>
+hipError_t launch_tile_split(const ConvKArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+    (void)lds;
+    const dim3 block(64 * WM * WN * WK);
+    if (a.xvec)
+        hipLaunchKernelGGL((conv_tile<KS, S, CIN32, FM, WM, WN, WK, true, true>), grid, block, 0, s, a);
+    else
+        hipLaunchKernelGGL((conv_tile<KS, S, CIN32, FM, WM, WN, WK, false, true>), grid, block, 0, s, a);
+    return hipGetLastError();
 }
 
 // Whether a launch can take the buffer-instruction loop of the persistent configurations: 16-byte aligned input

@@ -72,6 +72,8 @@ def load():
         "fhc_conv_out_shape": ([P, ctypes.POINTER(U32), ctypes.POINTER(U32)], ctypes.c_int),
         "fhc_conv_run": ([P, P, P, P, P, P], ctypes.c_int),
         "fhc_conv_pair_run_film": ([P, P, P, P, P], ctypes.c_int),
+        "fhc_conv_sibling_plan_create": ([P, P, P, P, P, P, P, P, P], ctypes.c_int),
+        "fhc_conv_sibling_run": ([P, P, P, P, P, P], ctypes.c_int),
         "fhc_conv_run_noalloc": ([P, P, P, P, P], ctypes.c_int),
         "fhc_conv_describe": ([P, ctypes.c_char_p, SZ], ctypes.c_int),
         "fhc_conv_plan_destroy": ([P], None),
@@ -273,6 +275,39 @@ class ConvPairPlan(ConvPlan):
             raise FhcError(f"run_film: film needs {self.desc.n * 2 * self.desc.cin} contiguous f16 values")
         _check(load().fhc_conv_pair_run_film(self._h, _ptr(x), _ptr(film), _ptr(y), _stream_handle(stream)),
                "fhc_conv_pair_run_film")
+
+
+class ConvSiblingPlan(ConvPlan):
+    """Two convs A and B of one input view in one launch (fhc_conv_sibling_plan_create): A's output channels, then
+    B's, each computed as its own plan computes it. run(x, y_a, res_a, y_b) takes the shared input, A's output and
+    residual and B's output."""
+
+    def __init__(self, desc_a: ConvDesc, w_a, bias_a, slope_a, desc_b: ConvDesc, w_b, bias_b, slope_b):
+        L = load()
+        self.desc, self.desc_b = desc_a, desc_b
+        ptrs = []
+        for d, w, b, sl in ((desc_a, w_a, bias_a, slope_a), (desc_b, w_b, bias_b, slope_b)):
+            wa, wp = _host_u16(w)
+            ba, bp = _host_u16(b)
+            sa, sp = _host_u16(sl)
+            if wa is None or wa.size != d.cout * d.cin * d.kh * d.kw:
+                raise FhcError("weights must hold cout*cin*kh*kw f16 values (OIHW)")
+            if ba is None or ba.size != d.cout or (sa is not None and sa.size != d.cout):
+                raise FhcError("bias and slope must hold cout f16 values")
+            ptrs.append((wa, wp, ba, bp, sa, sp))
+        (_, wpa, _, bpa, _, spa), (_, wpb, _, bpb, _, spb) = ptrs
+        h = ctypes.c_void_p()
+        _check(L.fhc_conv_sibling_plan_create(ctypes.byref(desc_a), wpa, bpa, spa, ctypes.byref(desc_b), wpb, bpb,
+                                              spb, ctypes.byref(h)), "fhc_conv_sibling_plan_create")
+        self._h = h
+        ho, wo = ctypes.c_uint32(), ctypes.c_uint32()
+        _check(L.fhc_conv_out_shape(h, ctypes.byref(ho), ctypes.byref(wo)), "fhc_conv_out_shape")
+        self.hout, self.wout = ho.value, wo.value
+        self.workspace_bytes = 0
+
+    def run(self, x, y_a, res_a=None, y_b=None, stream=None):
+        _check(load().fhc_conv_sibling_run(self._h, _ptr(x), _ptr(y_a), _ptr(res_a), _ptr(y_b),
+                                           _stream_handle(stream)), "fhc_conv_sibling_run")
 
 
 @dataclass

@@ -132,6 +132,11 @@ class ComposedChains:
         self.film(h, c, hm)
         self.pair(a, b, hm, mid, y, False)
 
+    def conv_siblings(self, a, b, x: V, ya: V, res_a: Optional[V], yb: V):
+        """The convs a (with its residual, if any) and b of the same input x (on the GPU one launch)."""
+        self.conv(a, x, ya, res_a)
+        self.conv(b, x, yb)
+
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
         for i in range(2):
@@ -339,6 +344,27 @@ class GpuBackend(ComposedChains):
         hb, yb, g, st = h.buf, y.buf, self.g, self.stream
         self._go(f"film_modulate+{a}+{b}", lambda: p.run_film(hb, g, yb, stream=st),
                  p._work["bytes"] + 2 * 2 * c, p._work["flops"], "conv")
+
+    def conv_siblings(self, a, b, x: V, ya: V, res_a: Optional[V], yb: V):
+        if not (self.chains and self.fuse):
+            return super().conv_siblings(a, b, x, ya, res_a, yb)
+        key = ("siblings", a, b, x.buf.data_ptr(), x.c0, ya.buf.data_ptr(), ya.c0, yb.buf.data_ptr(), yb.c0)
+        p = self.plans.get(key)
+        if p is None:
+            da, db = self._desc(a, x, ya, res_a), self._desc(b, x, yb, None)
+            (wa, ba, sa), (wb, bb, sb) = self.W[a], self.W[b]
+            try:
+                p = self.fhconv.ConvSiblingPlan(da, wa, ba, sa, db, wb, bb, sb)
+                w = p.describe()
+                p._work = dict(flops=w["flops"], bytes=w["bytes"])
+            except self.fhconv.FhcError:
+                p = False  # no sibling kernel for these channels
+            self.plans[key] = p
+        if p is False:
+            return super().conv_siblings(a, b, x, ya, res_a, yb)
+        xb, yab, rb, ybb, st = x.buf, ya.buf, None if res_a is None else res_a.buf, yb.buf, self.stream
+        self._go(f"{a}+{b} (siblings)", lambda: p.run(xb, yab, rb, ybb, stream=st), p._work["bytes"],
+                 p._work["flops"], "conv")
 
     def interp(self, x: V, c, out: V, oh, ow, aa):
         n = x.buf.shape[0]
@@ -603,7 +629,7 @@ class FlyHighFG:
         self.full_w = self.wp if frame is not None else net_w
 
     def pair(self):
-        """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1)."""
+        """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1), and op 62 (up.w, which reads only h)."""
         be, S = self.be, self.shape
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
         if self.frame is not None:  # the frames -> A, B (rgba_in; in the internal-size mode, the downscale)
@@ -633,18 +659,19 @@ class FlyHighFG:
         be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
         # flow, vis += d: the add of fine.out's output as the conv's residual, written in place (the planner's
         # residual peephole, net/build.rs:222-237; f16(f32(d) + f32(fv)) either way)
-        be.conv("fine.out", V(self.h), V(self.fv), V(self.fv))
+        # up.w (graph op 62, mid's first conv) reads only h, so it runs here beside fine.out, which reads h too: one
+        # launch, and a pair() followed by several mid(t) computes it once
+        be.conv_siblings("fine.out", "up.w", V(self.h), V(self.fv), V(self.fv), V(self.wt36))
         if self.repair:  # the periodic-structure repair of the pair's flow, in place (gmhs.rs:149-206)
             be.gmhs(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair)
 
     def mid(self, t: float, W: Optional[dict]):
-        """mid(t): models/graph.json ops 44-82, render_pix included. With W None the FiLM vector of t must
-        already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes it that way, as the
-        reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22)."""
+        """mid(t): models/graph.json ops 44-82 but 62 (up.w, run by pair()), render_pix included. With W None the
+        FiLM vector of t must already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes
+        it that way, as the reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22)."""
         be = self.be
         if W is not None:
             be.set_g(film_mlp(W, t))                                                          # 49
-        be.conv("up.w", V(self.h), V(self.wt36))                                              # 62
         be.film_pair("film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))  # 50-52
         be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
         be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(self.dfilm), t, V(self.up7), V(self.ftvt), V(self.lin),

@@ -137,6 +137,21 @@ int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, 
                               const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
                               const uint16_t* bias_b, const uint16_t* slope_b, uint32_t flags, fhc_conv_plan** out);
 
+/* Sibling convs: two convs A and B that read the same input view with the same geometry, as one launch (the
+ * one-tile direct kernel computing A's output channels, zero channels up to a multiple of 4, then B's, each with
+ * the K loop the same configuration runs for it alone). A may take a residual; B takes none; identity or PReLU
+ * activations. Instantiated: 3x3 stride 1, 33-64 input channels, A.cout rounded up to 4 plus B.cout at most 48
+ * (graph.json's fine.out and up.w, which both read the fine block's h: 48 -> 7 + 36). The plan runs with
+ * fhc_conv_sibling_run only (fhc_conv_run refuses it) and is freed by fhc_conv_plan_destroy. No counterpart in the
+ * reference, which records a dispatch per conv (net/build.rs:209-278). */
+int fhc_conv_sibling_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
+                                 const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
+                                 const uint16_t* bias_b, const uint16_t* slope_b, fhc_conv_plan** out);
+/* x: the shared input; y_a, res_a: A's output and residual (res_a NULL without one); y_b: B's output. Async on
+ * `stream`, no allocation, capturable in a HIP graph, as fhc_conv_run. Stands in for fhc_conv_run of A then of B. */
+int fhc_conv_sibling_run(const fhc_conv_plan* plan, const void* x, void* y_a, const void* res_a, void* y_b,
+                         void* stream);
+
 /* Runs a pair plan created with FHC_PAIR_FILM_IN: x is A's input before the modulation, film the FiLM vectors
  * (n x 2 x A.cin f16, device memory), y B's output. Async on `stream`, no allocation, capturable in a HIP graph, as
  * fhc_conv_run. Stands in for fhc_conv_run(film_modulate's output, ...) after the reference's film dispatch

@@ -75,6 +75,8 @@ def test_null_arguments_are_errors():
     assert "NULL plan" in fhconv.last_error()
     assert L.fhc_conv_pair_run_film(None, None, None, None, None) == -1
     assert "NULL plan" in fhconv.last_error()
+    assert L.fhc_conv_sibling_run(None, None, None, None, None, None) == -1
+    assert "NULL plan" in fhconv.last_error()
     assert L.fhc_conv_describe(None, None, 0) == -1
     assert L.fhc_conv_workspace_bytes(None) == 0
     L.fhc_conv_plan_destroy(None)
@@ -150,6 +152,23 @@ def test_pair_plan_rejects_what_it_cannot_fuse():
     br = fhconv.make_desc(1, 20, 30, 36, 36, act=0, residual=True)
     with pytest.raises(fhconv.FhcError, match="external residual"):
         fhconv.ConvPairPlan(a, wa, ba, None, br, wb, bb, None, film_in=True)
+
+
+def test_sibling_plan_rejects_what_it_cannot_fuse():
+    # checked before any device call: another input geometry, a residual on the second conv, LeakyReLU, input
+    # channels or output channels no sibling kernel serves
+    z = lambda co, ci: (np.zeros(co * ci * 9, np.uint16), np.zeros(co, np.uint16))  # noqa: E731
+    a = fhconv.make_desc(1, 20, 30, 48, 7, act=0, residual=True)
+    cases = [(fhconv.make_desc(1, 20, 31, 48, 36, act=0), "same input view"),
+             (fhconv.make_desc(1, 20, 30, 48, 36, act=0, residual=True), "cannot take a residual"),
+             (fhconv.make_desc(1, 20, 30, 48, 36, act=fhconv.ACT_LEAKY, alpha=0.1), "identity or PReLU"),
+             (fhconv.make_desc(1, 20, 30, 48, 44, act=0), "no sibling kernel")]
+    for b, msg in cases:
+        with pytest.raises(fhconv.FhcError, match=msg):
+            fhconv.ConvSiblingPlan(a, *z(7, 48), None, b, *z(b.cout, 48), None)
+    small = fhconv.make_desc(1, 20, 30, 24, 7, act=0)
+    with pytest.raises(fhconv.FhcError, match="no sibling kernel"):
+        fhconv.ConvSiblingPlan(small, *z(7, 24), None, fhconv.make_desc(1, 20, 30, 24, 36, act=0), *z(36, 24), None)
 
 
 def _ops():

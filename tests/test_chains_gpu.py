@@ -6,7 +6,8 @@ launch computes the same f32 operations with the same roundings, so its outputs 
 for bit. The whole-frame check (test_frame.py::test_fused_chains_equal_their_ops_on_the_gpu) covers the chains at
 the 1080p frame's shapes; here, for the coarse output with the fine block's input, flow_t / vis_t with the convex
 upsample, the pictures' resize with the pyramid, the refine head's input, the encoders' fold beside a cost volume,
-the refine head's last pair with affine_out, and the FiLM head's pair with film_modulate on its input: ragged grids whose coarse-to-fine ratio
+the refine head's last pair with affine_out, the FiLM head's pair with film_modulate on its input, and fine.out
+with up.w as sibling convs of h: ragged grids whose coarse-to-fine ratio
 is no integer, downscales other than 4x, channel counts that are no multiple of 4 (the 2-byte path), views into wider
 buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample and the FiLM pair
 (one FiLM vector per image).
@@ -168,3 +169,18 @@ def test_film_pair_equals_film_then_pair(n, h, w, c0, cs):
         be.film_pair("film.h1", "film.h2", V(hb, c0), 48, V(hm), V(mid), V(y, 8))
         outs.append(be.host(y).copy())
     same(outs[0], outs[1], "y")
+
+
+@pytest.mark.parametrize("n,h,w,c0,cs", [(1, 60, 108, 0, 48), (2, 13, 30, 4, 52), (1, 5, 7, 4, 52)])
+def test_conv_siblings_equal_the_two_convs(n, h, w, c0, cs):
+    say("conv_siblings", n, h, w, c0, cs)
+    outs = []
+    for be in backends():
+        rng = np.random.default_rng(n * 100 + w)
+        x = fill(be, rng, n, h, w, cs)
+        fv = fill(be, rng, n, h, w, 8)      # fine.out's output and residual, in place
+        wt = fill(be, rng, n, h, w, 40)     # up.w's output, in a view at channel 2
+        be.conv_siblings("fine.out", "up.w", V(x, c0), V(fv), V(fv), V(wt, 2))
+        outs.append({"fv": be.host(fv).copy(), "wt": be.host(wt).copy()})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k)
