@@ -552,7 +552,7 @@ def pmc_render(args, torch, np, stream):
         for _ in range(args.pmc_reps):
             dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps(dict(pmc_layer=args.pmc_layer, variant="render_rgba (two frame rows per lane)",
+    print(json.dumps(dict(pmc_layer=args.pmc_layer, variant="render_rgba (one frame pixel per lane)",
                           reps=args.pmc_reps, cold_sets=nsets, copy_bytes=COPY_BYTES)), flush=True)
     return 0
 
@@ -881,7 +881,7 @@ def main():
     if dom["label"].startswith("frame_render"):
         # 1920 x 1088 lanes of bicubic sampling in the reference's f32 order: the SQ counters put it at ~900 VALU
         # instructions per wave over 32,400 waves, the VALU issue rate of the chip, far below the HBM roofline
-        roofline["note"] = "VALU issue-bound: ~707 VALU instructions per pixel (two pixels per lane), 16,200 waves (SQ counter pass)"
+        roofline["note"] = "VALU issue-bound: ~770 VALU instructions per wave, 32,400 waves (SQ counter pass)"
     log("bench: dominant launch", json.dumps(roofline))
 
     cpu = None

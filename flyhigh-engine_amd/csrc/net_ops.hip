@@ -1420,101 +1420,6 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
     render_rgba_px<CUBIC, FL>(x, y, f, v, r, fa, fb, w, h, pitch, tab, flags, dst, opitch);
 }
 
-// render_rgba with two frame rows per lane (ya and ya + 1, same column; QV layout): the quarter maps' x
-// interpolation at a quarter row (the first half of bil4, v0 * (1 - fx) + v1 * fx) depends on the column and the
-// quarter row alone, so the lane computes it once for both pixels. With sh <= 1/2 (the host's condition) row ya + 1
-// reads quarter rows qb, qb + 1 with qb = qa or qa + 1, so three quarter rows cover both pixels (the third only
-// when qb = qa + 1, which is uniform over the wave). A block is 64 x 8 pixels. The grid is 1-D: workgroups b with
-// the same b % 8 run on one XCD, and class k = b % 8 takes block rows [k * rows8, (k + 1) * rows8) in row-major
-// order, so the tap rows and cache lines that neighbouring blocks share are fetched into one L2.
-template <bool CUBIC, bool FL>
-__global__ __launch_bounds__(kThreads) void render_rgba2_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
-                                                                uint32_t h, uint32_t pitch, float sh, float sw,
-                                                                View fl, View vis, View rt, uint32_t hq, uint32_t wq,
-                                                                float fsx, float fsy, uint32_t flags, uint32_t* dst,
-                                                                uint32_t opitch, uint32_t nbx, uint32_t rows8) {
-    const uint32_t k = blockIdx.x & 7u, j = blockIdx.x >> 3;
-    const uint32_t by = k * rows8 + j / nbx, bx = j % nbx;
-    if (j >= rows8 * nbx) return;  // uniform over the workgroup
-    __shared__ float tab[256];
-    fill_unit_table(tab);
-    const uint32_t x = bx * 64 + (threadIdx.x & 63u), ya = by * 8 + (threadIdx.x >> 6) * 2;
-    if (x >= w || ya >= h) return;
-    const float ix = ((float)x + 0.5f) * sw - 0.5f;
-    const float iya = ((float)ya + 0.5f) * sh - 0.5f, iyb = ((float)(ya + 1) + 0.5f) * sh - 0.5f;
-    const int qx0 = (int)floorf(ix), qa = (int)floorf(iya), qb = (int)floorf(iyb);
-    const float qfx = ix - (float)qx0, fya = iya - (float)qa, fyb = iyb - (float)qb;
-    const uint32_t x0 = clampi(qx0, 0, (int)wq - 1), x1 = clampi(qx0 + 1, 0, (int)wq - 1);
-    const uint32_t nq = hq * wq;
-    const auto rfl = buf_rsrc(fl.p, nq * 16u), rrt = buf_rsrc(rt.p, nq * rt.cs * 2u);
-    // the taps of quarter rows qa, qa + 1, qa + 2 (clamped) at columns x0, x1: 16 bytes of flow | vis, 8 of rt each
-    uint4 qv[3][2];
-    uint2 qr[3][2];
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-        const uint32_t row = __umul24((uint32_t)clampi(qa + j, 0, (int)hq - 1), wq);
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t q = row + (i ? x1 : x0);
-            qv[j][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rfl, q * 16u, 0, 0));
-            qr[j][i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rrt, (q * rt.cs + rt.c0) * 2u, 0, 0));
-        }
-    }
-    // the x interpolation of quarter row j's 10 channels (flow 4, vis 3, rt 3)
-    auto xlerp = [&](int j, float (&o)[10]) {
-        float t[2][10];
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t wv[4] = {qv[j][i].x, qv[j][i].y, qv[j][i].z, qv[j][i].w};
-#pragma unroll
-            for (int c = 0; c < 7; c++) t[i][c] = h2f((uint16_t)(wv[c >> 1] >> (16 * (c & 1))));
-            t[i][7] = h2f((uint16_t)qr[j][i].x), t[i][8] = h2f((uint16_t)(qr[j][i].x >> 16));
-            t[i][9] = h2f((uint16_t)qr[j][i].y);
-        }
-#pragma unroll
-        for (int c = 0; c < 10; c++) o[c] = t[0][c] * (1.0f - qfx) + t[1][c] * qfx;
-    };
-    // bil4's second half for one pixel from its two quarter rows' x interpolations
-    auto finish = [&](const float (&l0)[10], const float (&l1)[10], float fy, float (&f)[4], float (&v)[3],
-                      float (&r)[3]) {
-#pragma unroll
-        for (int c = 0; c < 4; c++) f[c] = (l0[c] * (1.0f - fy) + l1[c] * fy) * ((c & 1) == 0 ? fsx : fsy);
-#pragma unroll
-        for (int c = 0; c < 3; c++) {
-            v[c] = (l0[4 + c] * (1.0f - fy) + l1[4 + c] * fy) * vis.scale;
-            r[c] = l0[7 + c] * (1.0f - fy) + l1[7 + c] * fy;
-        }
-    };
-    float l0[10], l1[10];
-    xlerp(0, l0);
-    xlerp(1, l1);
-    float fA[4], vA[3], rA[3], fB[4], vB[3], rB[3];
-    finish(l0, l1, fya, fA, vA, rA);
-    if (qb == qa) {  // uniform
-        finish(l0, l1, fyb, fB, vB, rB);
-    } else {
-        float l2[10];
-        xlerp(2, l2);
-        finish(l1, l2, fyb, fB, vB, rB);
-    }
-    // pixel B's 10 values wait in LDS (this lane's own slots: no barrier) while pixel A renders, so they hold no
-    // registers through A's sampling
-    __shared__ float park[10][kThreads];
-    const uint32_t t = threadIdx.x;
-#pragma unroll
-    for (int c = 0; c < 4; c++) park[c][t] = fB[c];
-#pragma unroll
-    for (int c = 0; c < 3; c++) park[4 + c][t] = vB[c], park[7 + c][t] = rB[c];
-    render_rgba_px<CUBIC, FL>(x, ya, fA, vA, rA, fa, fb, w, h, pitch, tab, flags, dst, opitch);
-    if (ya + 1 < h) {  // uniform
-#pragma unroll
-        for (int c = 0; c < 4; c++) fB[c] = park[c][t];
-#pragma unroll
-        for (int c = 0; c < 3; c++) vB[c] = park[4 + c][t], rB[c] = park[7 + c][t];
-        render_rgba_px<CUBIC, FL>(x, ya + 1, fB, vB, rB, fa, fb, w, h, pitch, tab, flags, dst, opitch);
-    }
-}
-
 // The antialiased resize of n padded RGBA8 frames (hp x wp, rgba_in's BGR f16) to oh x ow, into a view of 8-byte
 // 4-channel pixels (channel 3 written 0): rgba_in.wgsl then interp.wgsl:11-45 with antialias, as
 // interp_aa_lds_kernel computes it. A workgroup stages the union of its 16 x 16 outputs' windows, at most
@@ -2499,25 +2404,10 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
              {render_rgba_kernel<false, true, false>, render_rgba_kernel<false, true, true>}},
             {{render_rgba_kernel<true, false, false>, render_rgba_kernel<true, false, true>},
              {render_rgba_kernel<true, true, false>, render_rgba_kernel<true, true, true>}}};
-        // two rows per lane where the quarter maps are upsampled 2x or more vertically (a frame render's are 4x+)
-        const bool two = qv && 2ull * hq <= hp;
-        const float sh = (float)hq / (float)hp, sw = (float)wq / (float)wp;
-        if (two) {
-            // 8 XCD classes of rows8 block rows each (the last ones may run past the frame: their workgroups return)
-            const uint32_t nbx = (w + 63) / 64, rows8 = ((h + 7) / 8 + 7) / 8;
-            using K2 = decltype(&render_rgba2_kernel<true, true>);
-            const K2 k2 = cubic ? (flags ? render_rgba2_kernel<true, true> : render_rgba2_kernel<true, false>)
-                                : (flags ? render_rgba2_kernel<false, true> : render_rgba2_kernel<false, false>);
-            hipLaunchKernelGGL(k2, dim3(8 * rows8 * nbx), dim3(kThreads), 0, (hipStream_t)stream,
-                               static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h, pitch, sh, sw,
-                               in(flow), in(vis), in(rt), hq, wq, fsx, fsy, flags, static_cast<uint32_t*>(out), opitch,
-                               nbx, rows8);
-        } else {
-            hipLaunchKernelGGL(ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0], dim3((w + 63) / 64, (h + 3) / 4),
-                               dim3(kThreads), 0, (hipStream_t)stream, static_cast<const uint32_t*>(a),
-                               static_cast<const uint32_t*>(b), w, h, pitch, sh, sw, in(flow), in(vis), in(rt), hq, wq,
-                               fsx, fsy, flags, static_cast<uint32_t*>(out), opitch);
-        }
+        hipLaunchKernelGGL(ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0], dim3((w + 63) / 64, (h + 3) / 4),
+                           dim3(kThreads), 0, (hipStream_t)stream, static_cast<const uint32_t*>(a),
+                           static_cast<const uint32_t*>(b), w, h, pitch, (float)hq / (float)hp, (float)wq / (float)wp,
+                           in(flow), in(vis), in(rt), hq, wq, fsx, fsy, flags, static_cast<uint32_t*>(out), opitch);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "render_rgba: launch failed: %s", hipGetErrorString(e));
     });

@@ -347,8 +347,8 @@ def test_render_rgba_matches_rgba_in_render_rgba_out(cubic, flags, amp, size, qd
     render at the padded size with the flow scaled per axis (the internal-size mode, maps at a non-integer ratio),
     and rgba_out: bytes within 1 everywhere (expf's last bit can move an f16 result next to a byte boundary), almost
     all identical; and bit-identical to the GPU's own unfused composition (the same device expf). amp: the range of
-    the map-size flow; 40 sends taps far outside the frame (clamped). qdiv: frame rows per quarter-map row (9: the
-    kernel with two frame rows per lane, an odd frame height leaving its last row alone; 1.5: one row per lane)."""
+    the map-size flow; 40 sends taps far outside the frame (clamped). qdiv: frame rows per quarter-map row (9 as in
+    the frame, 1.5 a mild upscale; with odd frame heights)."""
     import torch
     say("render_rgba", cubic, flags, amp, size, qdiv)
     fh = fhops()
