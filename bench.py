@@ -288,8 +288,7 @@ def eager_frames(args, torch, np, stream, t=0.5):
     be.set_g(fnet.film_mlp(W, t))
     with torch.cuda.stream(stream):
         for _ in range(args.eager_frames):
-            f.pair()
-            f.mid(t, None)
+            f.pair_mid(t)
     stream.synchronize()
     log(f"bench: {args.eager_frames} eager 1080p frames done")
     return 0
@@ -313,13 +312,11 @@ def frame_1080p(args, torch, np, stream, t=0.5, repair=1, per_launch=True):
     be.set_g(fnet.film_mlp(W, t))
     with torch.cuda.stream(stream):
         for _ in range(2):  # plans are made on the first run
-            f.pair()
-            f.mid(t, None)
+            f.pair_mid(t)
         stream.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            f.pair()
-            f.mid(t, None)
+            f.pair_mid(t)
         for _ in range(args.warmup):
             g.replay()
         torch.cuda.synchronize()
@@ -339,8 +336,7 @@ def frame_1080p(args, torch, np, stream, t=0.5, repair=1, per_launch=True):
     # every launch of the frame, timed alone (the recorder re-issues each with the frame's own buffers)
     be.record = []  # each launch re-issued alone
     with torch.cuda.stream(stream):
-        f.pair()
-        f.mid(t, None)
+        f.pair_mid(t)
         stream.synchronize()
     rec, be.record = be.record, None
     launches = []
@@ -396,8 +392,7 @@ def cpu_frame_baseline(np, frames_n=3):
         f = fnet.FlyHighFG(be, 864, 480, frame=(1920, 1080))
         be.upload_frames(f.frames, fr)
         t0 = time.perf_counter()
-        f.pair()
-        f.mid(0.5, W)
+        f.pair_mid(0.5, W)
         secs.append(time.perf_counter() - t0)
     return statistics.median(secs), be.threads
 
@@ -533,8 +528,7 @@ def pmc_render(args, torch, np, stream):
     be.upload_frames(f.frames, np.stack([fnet.procedural_frame(1920, 1080), fnet.procedural_frame(1920, 1080, 12, 0)]))
     be.set_g(fnet.film_mlp(W, 0.5))
     with torch.cuda.stream(stream):
-        f.pair()
-        f.mid(0.5, None)
+        f.pair_mid(0.5)
     torch.cuda.synchronize()
     per = 3 * f.frames.numel() // 2 * 4
     nsets = max(2, -(-(600 << 20) // per))

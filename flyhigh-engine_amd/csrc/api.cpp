@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "common.h"
+#include "gm_corun.h"
 #include "conv_kernels.h"
 #include "direct_table.h"
 #include "fhc_conv.h"
@@ -756,13 +757,10 @@ extern "C" int fhc_conv_out_shape(const fhc_conv_plan* p, uint32_t* hout, uint32
 }
 
 namespace {
-// the launch of a fused pair plan (validated by the caller): x is the first conv's input, y and res the second's
-// output and residual, film the FiLM vectors of a FHC_PAIR_FILM_IN plan
-int run_pair(const fhc_conv_plan* p, const void* x, void* y, const void* res, const void* film, void* stream,
-             const char* who) {
+// the arguments of a fused pair plan's launch: x is the first conv's input, y and res the second's output and
+// residual, film the FiLM vectors of a FHC_PAIR_FILM_IN plan
+PairKArgs pair_args(const fhc_conv_plan* p, const void* x, void* y, const void* res, const void* film) {
     const fhc_conv_plan* q = p->pair_b;
-    if (q->d.residual && !p->res_mid && !res)
-        return fail(-1, "%s: the pair's second conv has a residual but res is NULL", who);
     PairKArgs pk{p->args, q->args, p->res_mid};
     pk.a.x = static_cast<const uint16_t*>(x);
     pk.a.xvec = ((uintptr_t)x % 16 == 0) && pk.a.xcs % 8 == 0 && pk.a.xc0 % 8 == 0;
@@ -772,6 +770,15 @@ int run_pair(const fhc_conv_plan* p, const void* x, void* y, const void* res, co
     pk.b.yvec = ((uintptr_t)y % 8 == 0) && pk.b.ycs % 4 == 0 && pk.b.yc0 % 4 == 0;
     pk.b.rvec = pk.b.residual && !p->res_mid && ((uintptr_t)res % 8 == 0) && pk.b.rcs % 4 == 0 &&
                 pk.b.rc0 % 4 == 0 && pk.b.cout % 4 == 0;
+    return pk;
+}
+
+// the launch of a fused pair plan (validated by the caller)
+int run_pair(const fhc_conv_plan* p, const void* x, void* y, const void* res, const void* film, void* stream,
+             const char* who) {
+    if (p->pair_b->d.residual && !p->res_mid && !res)
+        return fail(-1, "%s: the pair's second conv has a residual but res is NULL", who);
+    const PairKArgs pk = pair_args(p, x, y, res, film);
     hipError_t e = p->pair_launch(pk, p->grid, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(-1, "%s: launch: %s", who, hipGetErrorString(e));
     return 0;
@@ -1465,5 +1472,30 @@ extern "C" int fhc_conv_sibling_run(const fhc_conv_plan* p, const void* x, void*
         const hipError_t e = p->launch(a, p->grid, p->lds, static_cast<hipStream_t>(stream));
         if (e != hipSuccess) return fail(-1, "%s: launch: %s", who, hipGetErrorString(e));
         return 0;
+    });
+}
+
+extern "C" int fhc_gmhs_film_pair(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w,
+                                  const fhc_tensor* flow, uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level,
+                                  void* ws, size_t ws_bytes, const fhc_conv_plan* pair, const void* pair_x,
+                                  const void* pair_film, void* pair_y, void* stream) {
+    return guard(-1, [&]() -> int {
+        const char* who = "fhc_gmhs_film_pair";
+        if (!pair) return fail(-1, "%s: NULL pair plan", who);
+        if (pair->family != 2 || !pair->film_in)
+            return fail(-1, "%s: not a pair plan created with FHC_PAIR_FILM_IN", who);
+        const FitPairLaunchFn fn = fit_pair_launcher(pair->cfg);
+        if (!fn)
+            return fail(-1, "%s: no launch of the fit beside this pair's configuration (one tile per workgroup, 3 + 3 "
+                            "channel blocks, one wave row)", who);
+        if (!pair_x || !pair_y || !pair_film) return fail(-1, "%s: NULL pair input, output or FiLM vectors", who);
+        if (((uintptr_t)pair_x | (uintptr_t)pair_y | (uintptr_t)pair_film) & 1u)
+            return fail(-1, "%s: f16 tensors must be 2-byte aligned", who);
+        int dev = -1;
+        if (hipGetDevice(&dev) != hipSuccess || dev != pair->device)
+            return fail(-1, "%s: the plan belongs to device %d, the current device is %d", who, pair->device, dev);
+        if (level == 0) return run_pair(pair, pair_x, pair_y, nullptr, pair_film, stream, who);  // no repair
+        const GmCoRun co{fn, pair_args(pair, pair_x, pair_y, nullptr, pair_film), pair->tiles};
+        return gmhs_run(a, b, h, w, flow, h8, w8, full_w, level, ws, ws_bytes, &co, stream);
     });
 }

@@ -146,6 +146,23 @@ using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);
 // The launcher of pair configuration `index`, or nullptr; *kernel receives the (persistent) kernel's address.
 PairLaunchFn pair_launcher(int index, const void** kernel = nullptr);
 
+// One round of the repair's affine fit (gm_fit.h) and the tiles of a FiLM pair (FHC_PAIR_FILM_IN) in one launch of
+// 192-thread workgroups: workgroups 0-127 run the fit (workgroup g of channel c at c * 32 + g), the rest the pair's
+// tiles. The two touch none of each other's data; the fit's workgroups are few and latency-bound, so the pair's
+// work fills the machine beside them.
+struct FitRoundArgs {
+    const uint16_t* flow;  // the E8 flow, channel c at flow[i * cs + c0 + c]
+    uint32_t cs, c0, h8, w8;
+    float delta;
+    uint32_t round;
+    const float* part_in;
+    float* part_out;
+};
+using FitPairLaunchFn = hipError_t (*)(const FitRoundArgs&, const PairKArgs&, uint32_t pair_tiles, hipStream_t);
+// the launcher for pair configuration `index` (one tile per workgroup, 3 + 3 channel blocks on one wave row: 192
+// threads), or nullptr
+FitPairLaunchFn fit_pair_launcher(int index);
+
 // Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the
 // operand layouts the conv kernels assume. Device pointers.
 hipError_t mfma_probe_launch(const uint16_t* a, const uint16_t* b, float* d, hipStream_t s);

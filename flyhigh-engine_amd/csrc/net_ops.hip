@@ -12,6 +12,9 @@
 #include "common.h"
 #include "fhc_ops.h"
 
+#include "gm_corun.h"
+#include "gm_fit.h"
+
 namespace fhc {
 
 namespace {
@@ -1527,87 +1530,18 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
 // sums round as there; a box sums its clamped taps in order. The stage is latency-bound (a few MB of L2-resident
 // maps, 6480 flow cells at 1080p): the kernels are shaped for waves in flight, with every tap load of a sum issued
 // before its in-order additions.
-constexpr uint32_t kGmNwg = 32, kGmWg = 256;  // gm_fit_reduce's workgroups and workgroup size (gmhs.rs:160)
-constexpr uint32_t kGmPart = kGmNwg * 4 * 9;  // one round's partial sums [workgroup][channel][9]
+constexpr uint32_t kGmNwg = gmfit::kNwg, kGmWg = gmfit::kWg;  // gm_fit_reduce's workgroups and their size
+constexpr uint32_t kGmPart = gmfit::kPart;                     // one round's partial sums [workgroup][channel][9]
 constexpr uint32_t kGmT = 16;                 // the cost kernel's block edge and the box tile's, in cells
 constexpr uint32_t kGmRmax = 32;              // largest box radius: r_dwin = round(16 s), s <= 2
 
-// gm_fit_solve.wgsl:13-24: the normal equations of one flow channel, s = its summed partials; o = a0, a1, a2
-__device__ void gm_solve(const float* s, float* o) {
-    const float m00 = s[0] + 1e-6f, m01 = s[1], m02 = s[2], m11 = s[3] + 1e-6f, m12 = s[4], m22 = s[5] + 1e-6f;
-    const float det = m00 * (m11 * m22 - m12 * m12) - m01 * (m01 * m22 - m12 * m02) + m02 * (m01 * m12 - m11 * m02);
-    if (fabsf(det) < 1e-12f) {
-        o[0] = s[6] / fmaxf(s[0], 1e-6f), o[1] = 0.0f, o[2] = 0.0f;
-        return;
-    }
-    const float i00 = (m11 * m22 - m12 * m12) / det, i01 = (m02 * m12 - m01 * m22) / det;
-    const float i02 = (m01 * m12 - m02 * m11) / det, i11 = (m00 * m22 - m02 * m02) / det;
-    const float i12 = (m01 * m02 - m00 * m12) / det, i22 = (m00 * m11 - m01 * m01) / det;
-    o[0] = i00 * s[6] + i01 * s[7] + i02 * s[8];
-    o[1] = i01 * s[6] + i11 * s[7] + i12 * s[8];
-    o[2] = i02 * s[6] + i12 * s[7] + i22 * s[8];
-}
-
-// the coefficients of the channels `chans` (bit c: channel c) from a round's partials, into cf[c][0..2]: lane
-// c * 9 + k sums partial k over the workgroups in order (gm_fit_solve.wgsl:11-12; the 32 loads issued together),
-// lane c solves. Every lane of the block takes part in the barriers.
-__device__ void gm_solve_block(const float* part, uint32_t chans, float (*ss)[9], float (*cf)[3]) {
-    const uint32_t t = threadIdx.x;
-    if (t < 36 && (chans >> (t / 9) & 1u)) {
-        const uint32_t c = t / 9, k = t % 9;
-        float v[kGmNwg];
-#pragma unroll
-        for (uint32_t g = 0; g < kGmNwg; g++) v[g] = part[(g * 4 + c) * 9 + k];
-        float a = 0.0f;
-#pragma unroll
-        for (uint32_t g = 0; g < kGmNwg; g++) a = a + v[g];
-        ss[c][k] = a;
-    }
-    __syncthreads();
-    if (t < 4 && (chans >> t & 1u)) gm_solve(ss[t], cf[t]);
-    __syncthreads();
-}
-
-// one fit round (gm_fit_reduce.wgsl:15-44) for workgroup blockIdx.x of channel blockIdx.y; rounds after the first
-// weight each element by delta / max(delta, |residual|) against the coefficients of the previous round's partials
+// one fit round (gm_fit_reduce.wgsl:15-44, the round before solved first) for workgroup blockIdx.x of channel
+// blockIdx.y: the shared round body (gm_fit.h) at 256 threads
 __global__ __launch_bounds__(kGmWg) void gm_fit_kernel(View flow, uint32_t h8, uint32_t w8, float delta, uint32_t round,
                                                        const float* part_in, float* part_out) {
-    __shared__ float sh[9][kGmWg / 2];
-    __shared__ float ss[4][9], cf[4][3];
-    const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
-    const uint32_t n = h8 * w8, stride = kGmWg * kGmNwg, i0 = g * kGmWg + t;
-    const float f0 = i0 < n ? ld(flow, i0, c) : 0.0f;  // in flight while the previous round is solved
-    if (round > 0) gm_solve_block(part_in, 1u << c, ss, cf);
-    const float sx = 2.0f / (float)max(w8 - 1, 1u), sy = 2.0f / (float)max(h8 - 1, 1u);
-    float s[9] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t i = i0; i < n; i += stride) {
-        const uint32_t yy = i / w8, xx = i - yy * w8;
-        const float x = -1.0f + sx * (float)xx, y = -1.0f + sy * (float)yy;
-        const float f = i == i0 ? f0 : ld(flow, i, c);
-        float w2 = 1.0f;
-        if (round > 0) w2 = delta / fmaxf(delta, fabsf(f - (cf[c][0] + cf[c][1] * x + cf[c][2] * y)));
-        s[0] = s[0] + w2, s[1] = s[1] + w2 * x, s[2] = s[2] + w2 * y;
-        s[3] = s[3] + w2 * x * x, s[4] = s[4] + w2 * x * y, s[5] = s[5] + w2 * y * y;
-        s[6] = s[6] + w2 * f, s[7] = s[7] + w2 * x * f, s[8] = s[8] + w2 * y * f;
-    }
-    // the lane tree, pairs (t, t + off) for off = 128 .. 1: the first level through LDS, the rest in the first wave
-    if (t >= kGmWg / 2)
-#pragma unroll
-        for (uint32_t k = 0; k < 9; k++) sh[k][t - kGmWg / 2] = s[k];
-    __syncthreads();
-    if (t < kGmWg / 2)
-#pragma unroll
-        for (uint32_t k = 0; k < 9; k++) sh[k][t] = s[k] + sh[k][t];
-    __syncthreads();
-    if (t < 64) {
-#pragma unroll
-        for (uint32_t k = 0; k < 9; k++) {
-            float v = sh[k][t] + sh[k][t + 64];
-#pragma unroll
-            for (uint32_t off = 32; off > 0; off >>= 1) v = v + __shfl_down(v, off);
-            if (t == 0) part_out[(g * 4 + c) * 9 + k] = v;
-        }
-    }
+    __shared__ gmfit::RoundLds lds;
+    gmfit::round_body<kGmWg>(flow.p, flow.cs, flow.c0, h8, w8, delta, round, part_in, part_out, blockIdx.x, blockIdx.y,
+                             lds);
 }
 
 // the B, G, R of pixel pix of a picture view (VEC: one 8-byte load, 4-channel aligned views)
@@ -1671,7 +1605,7 @@ __global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint3
             }
         }
     }
-    gm_solve_block(part, 0xfu, ss, cf);
+    gmfit::solve_block(part, 0xfu, ss, cf);
     if (blockIdx.x == 0 && blockIdx.y == 0 && t < 16) coef[t] = (t & 3u) == 3u ? 0.0f : cf[t >> 2][t & 3u];
     if (!valid) return;
     const size_t n = (size_t)hc * wc, i = (size_t)y * wc + x;
@@ -2420,9 +2354,9 @@ extern "C" int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t
     });
 }
 
-extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
-                        uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
-                        void* stream) {
+int fhc::gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
+                  uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
+                  const GmCoRun* co, void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
         if (level == 0) return 0;
@@ -2450,9 +2384,16 @@ extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, ui
         float* raw = reinterpret_cast<float*>(static_cast<char*>(ws) + p.dec_offset);    // the cost maps, then dec
         float* hs = raw + hs_off;
         const hipStream_t st = (hipStream_t)stream;
-        for (uint32_t round = 0; round < 4; round++)
+        for (uint32_t round = 0; round < 4; round++) {
+            if (round == 0 && co) {  // the co-runner's workgroups beside the first round's
+                const FitRoundArgs fa{static_cast<const uint16_t*>(flow->p), flow->cstride, flow->c0, h8, w8, p.delta, 0, part[1], part[0]};
+                const hipError_t ce = co->fn(fa, co->pk, co->tiles, st);
+                if (ce != hipSuccess) return fail(-2, "gmhs: launch failed: %s", hipGetErrorString(ce));
+                continue;
+            }
             hipLaunchKernelGGL(gm_fit_kernel, dim3(kGmNwg, 4), dim3(kGmWg), 0, st, in(flow), h8, w8, p.delta, round,
                                part[(round + 1) & 1u], part[round & 1u]);
+        }
         const bool v = vec4(4, {a, b, flow});
         const dim3 tiles((p.wc + kGmT - 1) / kGmT, (p.hc + kGmT - 1) / kGmT);
         hipLaunchKernelGGL(v ? gm_cost_kernel<true> : gm_cost_kernel<false>, tiles, dim3(kThreads), 0, st, in(a), in(b),
@@ -2473,6 +2414,12 @@ extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, ui
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "gmhs: launch failed: %s", hipGetErrorString(e));
     });
+}
+
+extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
+                        uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
+                        void* stream) {
+    return gmhs_run(a, b, h, w, flow, h8, w8, full_w, level, ws, ws_bytes, nullptr, stream);
 }
 
 extern "C" int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state,

@@ -69,9 +69,19 @@ __device__ __forceinline__ uint4 film_group(uint4 q, const float* gm, const floa
     return uint4{w[0], w[1], w[2], w[3]};
 }
 
-// FILM: A's input goes through film_modulate as it is staged (a.film, the one-tile loop only)
+// The LDS of one conv_pair tile: A's input halo, A's output tile
+template <int SA, int CA32, int CB32, int TH>
+struct PairLds {
+    static constexpr int IHA = (TH + 1) * SA + 3, IWA = 15 * SA + 3, PSA = CA32 + 8, MW = 18, PSB = CB32 + 8;
+    uint16_t hin[IHA * IWA * PSA];
+    uint16_t mid[(TH + 2) * MW * PSB];
+};
+
+// FILM: A's input goes through film_modulate as it is staged (a.film, the one-tile loop only). The body of one
+// tile t (conv_pair's workgroup t; a launch that runs other work beside the pair passes its own numbering) in the
+// workgroup's LDS L; the block is 64 * WN * WM threads.
 template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC, bool FILM = false>
-__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(PairKArgs pk) {
+__device__ __forceinline__ void conv_pair_tile(const PairKArgs& pk, const int t, PairLds<SA, CA32, CB32, TH>& L) {
     constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN * WM, TWB = kPairTileW;
     constexpr int FA = TH + 2;                                  // A's rows per tile
     constexpr int FAW = FA / WM, THW = TH / WM;                 // rows per wave
@@ -81,13 +91,13 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
     constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;     // A's output tile in LDS: FA rows x 18 pixels
     constexpr int HALO = IHA * IWA * GPA, NLD = (HALO + NT - 1) / NT;
     static_assert(NBA * 16 <= CB32, "A's channel blocks exceed B's input channels");
-    __shared__ __align__(16) uint16_t hin[IHA * IWA * PSA];
-    __shared__ __align__(16) uint16_t mid[FA * MW * PSB];
+    static_assert(sizeof(L.hin) == IHA * IWA * PSA * 2 && sizeof(L.mid) == FA * MW * PSB * 2, "the tile's LDS");
+    uint16_t* const hin = L.hin;
+    uint16_t* const mid = L.mid;
     const ConvKArgs& a = pk.a;
     const ConvKArgs& b = pk.b;
 
     const int tid = threadIdx.x, lane = tid & 63, wn = (tid >> 6) % WN, wm = (tid >> 6) / WN, lx = lane & 15;
-    const int t = blockIdx.x;
     const int tx = t % b.tiles_x, rr = t / b.tiles_x;
     const int ty = rr % b.tiles_y, img = rr / b.tiles_y;
     const int oy0 = ty * TH, ox0 = tx * TWB;  // B's tile origin; A's tile starts one row and column earlier
@@ -242,6 +252,12 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
             }
         }
     }
+}
+
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC, bool FILM = false>
+__global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(PairKArgs pk) {
+    __shared__ __align__(16) PairLds<SA, CA32, CB32, TH> lds;
+    conv_pair_tile<SA, CA32, CB32, NBA, NBB, TH, WM, VEC, FILM>(pk, blockIdx.x, lds);
 }
 
 // The persistent pair: G = gridDim.x resident workgroups loop over B's output tiles t, t + G, ... with both layers'

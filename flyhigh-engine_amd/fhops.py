@@ -91,6 +91,7 @@ def _lib():
                                 P],
             "fhc_gmhs_params": [U, U, U, U, ctypes.POINTER(GmhsPar)],
             "fhc_gmhs": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P],
+            "fhc_gmhs_film_pair": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P, P, P, P, P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -411,6 +412,22 @@ def gmhs(a, b, flow, full_w: int, level: int = 1, ws=None, stream=None):
         ws = gmhs_workspace(h, w, full_w, max(level, 1), a.t.device)
     _run("gmhs", _lib().fhc_gmhs(_ref(a), _ref(b), h, w, _ref(flow), h8, w8, full_w, level, ws.data_ptr(),
                                  ws.numel() * ws.element_size(), _stream_handle(stream)))
+    return ws
+
+
+def gmhs_film_pair(a, b, flow, full_w: int, level, ws, pair, pair_x, pair_film, pair_y, stream=None):
+    """gmhs(a, b, flow, ...) and pair.run_film(pair_x, pair_film, pair_y) (a fhconv.ConvPairPlan made with film_in),
+    the pair's workgroups inside the repair's first launch."""
+    a, b, flow = _v(a), _v(b), _v(flow)
+    _, h, w, _ = a.shape
+    _, h8, w8, _ = flow.shape
+    d = pair.desc
+    if not pair_film.is_contiguous() or pair_film.numel() != d.n * 2 * d.cin or pair_film.element_size() != 2:
+        raise FhcError(f"gmhs_film_pair: the FiLM vectors need {d.n * 2 * d.cin} contiguous f16 values")
+    _run("gmhs_film_pair",
+         _lib().fhc_gmhs_film_pair(_ref(a), _ref(b), h, w, _ref(flow), h8, w8, full_w, level, ws.data_ptr(),
+                                   ws.numel() * ws.element_size(), pair._h, pair_x.data_ptr(), pair_film.data_ptr(),
+                                   pair_y.data_ptr(), _stream_handle(stream)))
     return ws
 
 

@@ -137,6 +137,12 @@ class ComposedChains:
         self.conv(a, x, ya, res_a)
         self.conv(b, x, yb)
 
+    def gmhs_film(self, a: V, b: V, flow: V, full_w: int, level: int, fa, fb, h: V, c: int, hm: V, mid: V, y: V):
+        """The repair, and the FiLM pair of film_pair(fa, fb, h, c, hm, mid, y), which touch none of each other's
+        data (on the GPU the pair's workgroups run inside the repair's first launch)."""
+        self.gmhs(a, b, flow, full_w, level)
+        self.film_pair(fa, fb, h, c, hm, mid, y)
+
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
         for i in range(2):
@@ -324,9 +330,10 @@ class GpuBackend(ComposedChains):
         self._go(f"{a}+{b}+affine_out", lambda: p.run(xb, ob, None, stream=st), p._work["bytes"], p._work["flops"],
                  "conv")
 
-    def film_pair(self, a, b, h: V, c: int, hm: V, mid: V, y: V):
+    def _film_plan(self, a, b, h: V, c: int, mid: V, y: V):
+        """The FiLM pair's plan (film_modulate in a, b's staging), or False where there is none."""
         if not (self.chains and self.fuse) or CONVS[a][0] != c or h.scale != 1.0:
-            return super().film_pair(a, b, h, c, hm, mid, y)
+            return False
         key = ("film_pair", a, b, h.buf.data_ptr(), h.c0, y.buf.data_ptr(), y.c0)
         p = self.plans.get(key)
         if p is None:
@@ -339,6 +346,29 @@ class GpuBackend(ComposedChains):
             except self.fhconv.FhcError:
                 p = False  # no fused kernel for these channels
             self.plans[key] = p
+        return p
+
+    def gmhs_film(self, a: V, b: V, flow: V, full_w: int, level: int, fa, fb, h: V, c: int, hm: V, mid: V, y: V):
+        p = self._film_plan(fa, fb, h, c, mid, y)
+        if p is False or level == 0:
+            return super().gmhs_film(a, b, flow, full_w, level, fa, fb, h, c, hm, mid, y)
+        va, vb, vf = self._v(a), self._v(b), self._v(flow)
+        _, hh, ww, _ = va.shape
+        _, h8, w8, _ = vf.shape
+        key = ("gmhs", hh, ww, full_w, level)
+        if key not in self.plans:
+            self.plans[key] = self.fh.gmhs_workspace(hh, ww, full_w, level, self.dev)
+        ws = self.plans[key]
+        gp = self.fh.gmhs_params(hh, ww, full_w, level)
+        cells = gp["hc"] * gp["wc"]
+        nbytes = 5 * 4 * 2 * h8 * w8 + 2 * 3 * 2 * hh * ww + 4 * cells * (5 + 5 + 5 + 3) + 4 * 2 * h8 * w8
+        hb, yb, g, st = h.buf, y.buf, self.g, self.stream
+        self._go(f"gmhs + film_modulate+{fa}+{fb} (the pair in the first fit launch)",
+                 lambda: self.fh.gmhs_film_pair(va, vb, vf, full_w, level, ws, p, hb, g, yb, stream=st),
+                 nbytes + p._work["bytes"] + 2 * 2 * c, p._work["flops"], "op", kernels=8)
+
+    def film_pair(self, a, b, h: V, c: int, hm: V, mid: V, y: V):
+        p = self._film_plan(a, b, h, c, mid, y)
         if p is False:
             return super().film_pair(a, b, h, c, hm, mid, y)
         hb, yb, g, st = h.buf, y.buf, self.g, self.stream
@@ -628,8 +658,10 @@ class FlyHighFG:
         # the padded frame width the repair's windows scale with (the network's own without a frame)
         self.full_w = self.wp if frame is not None else net_w
 
-    def pair(self):
-        """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1), and op 62 (up.w, which reads only h)."""
+    def pair(self, cofilm: bool = False) -> bool:
+        """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1), and op 62 (up.w, which reads only h).
+        cofilm: also the next mid(t)'s FiLM pair (ops 50-52: it reads only h and the FiLM vector of t, which must be
+        in place), inside the repair's first launch; returns whether it ran (mid(t, film_done=True) then skips it)."""
         be, S = self.be, self.shape
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
         if self.frame is not None:  # the frames -> A, B (rgba_in; in the internal-size mode, the downscale)
@@ -662,17 +694,31 @@ class FlyHighFG:
         # up.w (graph op 62, mid's first conv) reads only h, so it runs here beside fine.out, which reads h too: one
         # launch, and a pair() followed by several mid(t) computes it once
         be.conv_siblings("fine.out", "up.w", V(self.h), V(self.fv), V(self.fv), V(self.wt36))
+        if self.repair and cofilm:  # the repair, with mid's FiLM pair in its first launch (pair_mid())
+            be.gmhs_film(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair,
+                         "film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))
+            return True
         if self.repair:  # the periodic-structure repair of the pair's flow, in place (gmhs.rs:149-206)
             be.gmhs(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair)
+        return False
 
-    def mid(self, t: float, W: Optional[dict]):
+    def pair_mid(self, t: float, W: Optional[dict] = None):
+        """pair() then mid(t), the FiLM pair of t run inside the repair's first launch (one launch fewer). With W
+        None the FiLM vector of t must already be in place, as for mid()."""
+        if W is not None:
+            self.be.set_g(film_mlp(W, t))
+        self.mid(t, None, film_done=self.pair(cofilm=True))
+
+    def mid(self, t: float, W: Optional[dict], film_done: bool = False):
         """mid(t): models/graph.json ops 44-82 but 62 (up.w, run by pair()), render_pix included. With W None the
         FiLM vector of t must already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes
-        it that way, as the reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22)."""
+        it that way, as the reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22).
+        film_done: the FiLM pair (ops 50-52) already ran with this t's vector (pair(cofilm=True))."""
         be = self.be
         if W is not None:
             be.set_g(film_mlp(W, t))                                                          # 49
-        be.film_pair("film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))  # 50-52
+        if not film_done:
+            be.film_pair("film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))  # 50-52
         be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
         be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(self.dfilm), t, V(self.up7), V(self.ftvt), V(self.lin),
                              V(self.dvis))                                                    # 44-48, 54-62

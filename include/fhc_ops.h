@@ -257,6 +257,19 @@ int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc
 int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
              uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, void* stream);
 
+/* fhc_gmhs, and a FiLM pair plan (fhc_conv_pair_plan_create with FHC_PAIR_FILM_IN, include/fhc_conv.h) run as
+ * fhc_conv_pair_run_film(pair, pair_x, pair_film, pair_y) would run it, with the pair's workgroups inside the
+ * repair's first launch: the fit's 128 workgroups are latency-bound and leave the GPU to the pair. The two touch
+ * none of each other's data (the frame: the repair of pair()'s flow, and mid()'s FiLM head, which reads h and the
+ * FiLM vectors of t). The pair plan's configuration must be a one-tile configuration of 3 + 3 channel blocks on one
+ * wave row (the 48 -> 48 -> 48 FiLM head at 2 or 4 rows per tile); level 0 runs the pair alone. Seven launches
+ * where the two take nine. No counterpart in the reference. */
+struct fhc_conv_plan;
+int fhc_gmhs_film_pair(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
+                       uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
+                       const struct fhc_conv_plan* pair, const void* pair_x, const void* pair_film, void* pair_y,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

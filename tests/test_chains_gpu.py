@@ -6,8 +6,8 @@ launch computes the same f32 operations with the same roundings, so its outputs 
 for bit. The whole-frame check (test_frame.py::test_fused_chains_equal_their_ops_on_the_gpu) covers the chains at
 the 1080p frame's shapes; here, for the coarse output with the fine block's input, flow_t / vis_t with the convex
 upsample, the pictures' resize with the pyramid, the refine head's input, the encoders' fold beside a cost volume,
-the refine head's last pair with affine_out, the FiLM head's pair with film_modulate on its input, and fine.out
-with up.w as sibling convs of h: ragged grids whose coarse-to-fine ratio
+the refine head's last pair with affine_out, the FiLM head's pair with film_modulate on its input, fine.out with
+up.w as sibling convs of h, and the repair with the FiLM pair inside its first launch: ragged grids whose coarse-to-fine ratio
 is no integer, downscales other than 4x, channel counts that are no multiple of 4 (the 2-byte path), views into wider
 buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample and the FiLM pair
 (one FiLM vector per image).
@@ -182,5 +182,26 @@ def test_conv_siblings_equal_the_two_convs(n, h, w, c0, cs):
         wt = fill(be, rng, n, h, w, 40)     # up.w's output, in a view at channel 2
         be.conv_siblings("fine.out", "up.w", V(x, c0), V(fv), V(fv), V(wt, 2))
         outs.append({"fv": be.host(fv).copy(), "wt": be.host(wt).copy()})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k)
+
+
+@pytest.mark.parametrize("net_h,net_w,full_w", [(480, 864, 1920), (128, 256, 608)])
+def test_gmhs_film_pair_equals_gmhs_and_film_pair(net_h, net_w, full_w):
+    """The repair with the FiLM pair's workgroups inside its first launch (the fit at 192 threads per workgroup, the
+    pair's tiles beside) against the repair's own launches and the pair's own launch."""
+    say("gmhs_film_pair", net_h, net_w, full_w)
+    outs = []
+    h8, w8 = net_h // 8, net_w // 8
+    for be in backends():
+        rng = np.random.default_rng(net_w)
+        ab = fill(be, rng, 2, net_h, net_w, 4, 0.0, 1.0)
+        fv = fill(be, rng, 1, h8, w8, 8, -4.0, 4.0)
+        hb = fill(be, rng, 1, h8, w8, 48)
+        be.set_g(rng.uniform(-0.5, 0.5, 96).astype(np.float16).view(np.uint16))
+        hm, mid, y = fill(be, rng, 1, h8, w8, 48), fill(be, rng, 1, h8, w8, 48), fill(be, rng, 1, h8, w8, 48)
+        be.gmhs_film(V(be.image(ab, 0)), V(be.image(ab, 1)), V(fv), full_w, 1, "film.h1", "film.h2", V(hb), 48, V(hm),
+                     V(mid), V(y))
+        outs.append({"fv": be.host(fv).copy(), "y": be.host(y).copy()})
     for k in outs[0]:
         same(outs[0][k], outs[1][k], k)

@@ -44,8 +44,7 @@ def run(be, W, net_w, net_h, ab, t=0.5, repair=0):
         f.AB[...] = ab
     else:
         f.AB.copy_(be.upload(ab))
-    f.pair()
-    f.mid(t, W)
+    f.pair_mid(t, W)
     return f
 
 
@@ -53,8 +52,7 @@ def run_frames(be, W, net_w, net_h, fr, t=0.5, repair=0):
     h, w = fr.shape[1:]
     f = net.FlyHighFG(be, net_w, net_h, frame=(w, h), repair=repair)
     be.upload_frames(f.frames, fr)
-    f.pair()
-    f.mid(t, W)
+    f.pair_mid(t, W)
     return f
 
 
@@ -180,18 +178,21 @@ def test_gpu_small_frame_without_internal_mode_matches_the_oracle():
 
 
 @pytest.mark.gpu
-def test_fused_chains_equal_their_ops_on_the_gpu():
+@pytest.mark.parametrize("repair", [0, 1])
+def test_fused_chains_equal_their_ops_on_the_gpu(repair):
     """The fused op chains (pyramid, coarse upsample + fine input, flow_t / vis_t + convex upsample, refine input,
-    and the frame's input and render from RGBA8) against the same chains run op by op on the GPU, in a whole frame
-    from RGBA8 frames in the internal-size mode: the same f32 operations and roundings, so every output is
-    bit-identical."""
+    the fused pairs' film_modulate and affine_out, the sibling convs, with the repair the FiLM pair inside the
+    repair's first launch, and the frame's input and render from RGBA8) against the same chains run op by op on the
+    GPU, in a whole frame from RGBA8 frames in the internal-size mode: the same f32 operations and roundings, so
+    every output is bit-identical."""
     import torch
+    print("frame 600x300 -> 256x128, repair", repair, flush=True)
     W = net.make_weights(3)
     fr = frames(600, 300, dx=7, dy=2)
     outs = []
     for chains in (True, False):
         gb = net.GpuBackend(W, stream=torch.cuda.current_stream(), chains=chains)
-        f = run_frames(gb, W, 256, 128, fr, t=0.3)
+        f = run_frames(gb, W, 256, 128, fr, t=0.3, repair=repair)
         # (flow_t | vis_t, ftvt, is compared through up7: the fused launch that makes up7 never stores it)
         extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("dfilm", 5),
                  ("wt36", 36), ("f16", 72), ("AB", 4)]
