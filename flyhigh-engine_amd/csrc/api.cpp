@@ -1475,12 +1475,13 @@ extern "C" int fhc_conv_sibling_run(const fhc_conv_plan* p, const void* x, void*
     });
 }
 
-extern "C" int fhc_gmhs_film_pair(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w,
-                                  const fhc_tensor* flow, uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level,
-                                  void* ws, size_t ws_bytes, const fhc_conv_plan* pair, const void* pair_x,
-                                  const void* pair_film, void* pair_y, void* stream) {
+extern "C" int fhc_gmhs_film(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w,
+                             const fhc_tensor* flow, uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level,
+                             void* ws, size_t ws_bytes, const fhc_conv_plan* pair, const void* pair_x,
+                             const void* pair_film, void* pair_y, const fhc_conv_plan* conv, const void* conv_x,
+                             void* conv_y, void* stream) {
     return guard(-1, [&]() -> int {
-        const char* who = "fhc_gmhs_film_pair";
+        const char* who = "fhc_gmhs_film";
         if (!pair) return fail(-1, "%s: NULL pair plan", who);
         if (pair->family != 2 || !pair->film_in)
             return fail(-1, "%s: not a pair plan created with FHC_PAIR_FILM_IN", who);
@@ -1494,8 +1495,30 @@ extern "C" int fhc_gmhs_film_pair(const fhc_tensor* a, const fhc_tensor* b, uint
         int dev = -1;
         if (hipGetDevice(&dev) != hipSuccess || dev != pair->device)
             return fail(-1, "%s: the plan belongs to device %d, the current device is %d", who, pair->device, dev);
-        if (level == 0) return run_pair(pair, pair_x, pair_y, nullptr, pair_film, stream, who);  // no repair
-        const GmCoRun co{fn, pair_args(pair, pair_x, pair_y, nullptr, pair_film), pair->tiles};
-        return gmhs_run(a, b, h, w, flow, h8, w8, full_w, level, ws, ws_bytes, &co, stream);
+        GmCoRun co{fn, pair_args(pair, pair_x, pair_y, nullptr, pair_film), pair->tiles, nullptr, {}, dim3()};
+        if (conv) {
+            if (!conv_x || !conv_y) return fail(-1, "%s: NULL conv input or output", who);
+            if (conv->family != 1 || conv->args.split || conv->d.residual || conv->ws_bytes || conv->device != dev)
+                return fail(-1, "%s: the conv must be a one-launch direct plan without residual on this device", who);
+            if (((uintptr_t)conv_x | (uintptr_t)conv_y) & 1u)
+                return fail(-1, "%s: f16 tensors must be 2-byte aligned", who);
+            co.cfn = fit_conv_launcher(conv->cfg);  // null: the conv runs in its own launch after the repair
+            ConvKArgs& ca = co.ca;
+            ca = conv->args;
+            ca.x = static_cast<const uint16_t*>(conv_x);
+            ca.y = static_cast<uint16_t*>(conv_y);
+            ca.res = nullptr;
+            ca.xvec = ((uintptr_t)conv_x % 16 == 0) && ca.xcs % 8 == 0 && ca.xc0 % 8 == 0;
+            ca.yvec = ((uintptr_t)conv_y % 8 == 0) && ca.ycs % 4 == 0 && ca.yc0 % 4 == 0;
+            ca.rvec = 0;
+            co.cgrid = conv->grid;
+        }
+        if (level == 0) {  // no repair: the pair, then the conv
+            const int rc = run_pair(pair, pair_x, pair_y, nullptr, pair_film, stream, who);
+            return rc || !conv ? rc : fhc_conv_run(conv, conv_x, conv_y, nullptr, nullptr, stream);
+        }
+        const int rc = gmhs_run(a, b, h, w, flow, h8, w8, full_w, level, ws, ws_bytes, &co, stream);
+        if (rc || !conv || co.cfn) return rc;
+        return fhc_conv_run(conv, conv_x, conv_y, nullptr, nullptr, stream);  // no fused launch for its configuration
     });
 }

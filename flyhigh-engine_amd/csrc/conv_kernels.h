@@ -162,6 +162,10 @@ using FitPairLaunchFn = hipError_t (*)(const FitRoundArgs&, const PairKArgs&, ui
 // the launcher for pair configuration `index` (one tile per workgroup, 3 + 3 channel blocks on one wave row: 192
 // threads), or nullptr
 FitPairLaunchFn fit_pair_launcher(int index);
+// The same with a conv plan's workgroups (conv_tile, 192 threads: tile t, channel tile ct at t + tiles * ct)
+using FitConvLaunchFn = hipError_t (*)(const FitRoundArgs&, const ConvKArgs&, dim3 conv_grid, hipStream_t);
+// the launcher for direct configuration `index` (one tile per workgroup, 192 threads), or nullptr
+FitConvLaunchFn fit_conv_launcher(int index);
 
 // Fragment-layout probe: D(16x16 f32) = A(16x32 f16) x B(32x16 f16) through one v_mfma_f32_16x16x32_f16 with the
 // operand layouts the conv kernels assume. Device pointers.

@@ -21,6 +21,7 @@
 #include "conv_kernels.h"
 #include "direct_impl.h"
 #include "direct_table.h"
+#include "gm_fit.h"
 
 namespace fhc {
 
@@ -269,6 +270,50 @@ LaunchFn sibling_launcher(int index) {
     if (index == k64_3) return launch_tile_split<3, 1, 64, 1, 1, 3, 3>;
     if (index == r64_2) return launch_tile_split<3, 1, 64, 1, 2, 2, 1>;
     if (index == r64_3) return launch_tile_split<3, 1, 64, 1, 2, 3, 1>;
+    return nullptr;
+}
+
+namespace {
+
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK>
+union FitTileLds {
+    gmfit::RoundLds fit;
+    TileLds<KS, S, CIN32, FM, WM, WN, WK> tile;
+};
+
+// one fit round of the repair (workgroups 0-127, gm_fit.h at 192 threads) and a conv plan's workgroups (the rest:
+// tile t, channel tile ct at 128 + t + tiles * ct) in one launch
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK, bool VEC>
+__global__ __launch_bounds__(192) void fit_conv_kernel(FitRoundArgs f, ConvKArgs a, uint32_t tiles) {
+    static_assert(64 * WM * WN * WK == 192, "the conv's workgroup is 192 threads");
+    constexpr uint32_t NFIT = gmfit::kNwg * 4;
+    __shared__ __align__(16) FitTileLds<KS, S, CIN32, FM, WM, WN, WK> lds;
+    if (blockIdx.x < NFIT) {  // uniform over the workgroup
+        gmfit::round_body<192>(f.flow, f.cs, f.c0, f.h8, f.w8, f.delta, f.round, f.part_in, f.part_out,
+                               blockIdx.x % gmfit::kNwg, blockIdx.x / gmfit::kNwg, lds.fit);
+    } else {
+        const uint32_t b = blockIdx.x - NFIT;
+        conv_tile_body<KS, S, CIN32, FM, WM, WN, WK, VEC>(a, (int)(b % tiles), (int)(b / tiles), lds.tile);
+    }
+}
+
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK>
+hipError_t fit_conv_launch(const FitRoundArgs& f, const ConvKArgs& a, dim3 cg, hipStream_t s) {
+    const dim3 grid(gmfit::kNwg * 4 + cg.x * cg.y);
+    if (a.xvec)
+        hipLaunchKernelGGL((fit_conv_kernel<KS, S, CIN32, FM, WM, WN, WK, true>), grid, dim3(192), 0, s, f, a, cg.x);
+    else
+        hipLaunchKernelGGL((fit_conv_kernel<KS, S, CIN32, FM, WM, WN, WK, false>), grid, dim3(192), 0, s, f, a, cg.x);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+FitConvLaunchFn fit_conv_launcher(int index) {
+    // the FiLM head's output conv (48 -> 5 at one row of 16 pixels per workgroup, the kernel-row split)
+    constexpr int k64_1 = find_direct(3, 1, 64, 1, 1, 1, 1, 3);
+    static_assert(k64_1 >= 0, "the FiLM output conv's configuration");
+    if (index == k64_1) return fit_conv_launch<3, 1, 64, 1, 1, 1, 3>;
     return nullptr;
 }
 

@@ -553,23 +553,32 @@ __attribute__((amdgpu_waves_per_eu(1, PERSIST ? persist_waves_per_simd(WM * WN *
 // MFMA chain reading LDS one K-step ahead, the epilogue per wave. Measured faster at one tile per workgroup than
 // the buffer loop above, whose deeper pipelining only pays over several tiles. SPLIT: sibling convs (the fields
 // split, cout1, y2 of ConvKArgs): the same K loop for every output channel, two epilogues.
+// The LDS of one conv_tile workgroup: the input halo, or the K split's partial sums
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK>
+struct TileLds {
+    static constexpr int TH = FM * WM, IH = (TH - 1) * S + KS, IW = 15 * S + KS, PSTR = CIN32 + 8;
+    static constexpr int HALO_BYTES = IH * IW * PSTR * 2, RED_BYTES = (WK - 1) * WM * WN * FM * 64 * 16;
+    uint16_t halo[(HALO_BYTES > RED_BYTES ? HALO_BYTES : RED_BYTES) / 2];
+};
+
+// the body of one conv_tile workgroup: spatial tile t, channel tile ct (conv_tile's blockIdx.x, .y; a launch that
+// runs other work beside the conv passes its own numbering), in the workgroup's LDS L
 template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK, bool VEC, bool SPLIT = false>
-__global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
+__device__ __forceinline__ void conv_tile_body(const ConvKArgs& a, const int t, const int ct,
+                                               TileLds<KS, S, CIN32, FM, WM, WN, WK>& L) {
     static_assert(WK == 1 || (WK == 3 && KS == 3), "the K split runs one kernel row per wave");
     constexpr int TH = FM * WM, TW = 16, BN = 16 * WN, NT = 64 * WM * WN * WK;
     constexpr int IH = (TH - 1) * S + KS, IW = (TW - 1) * S + KS;
     constexpr int GPT = CIN32 / 8, PSTR = CIN32 + 8, M = CIN32 / 32;
     constexpr int KSTEPS = KS * KS * M, KW = KSTEPS / WK;  // K-steps of the whole conv / of one wave
     constexpr int HALO = IH * IW * GPT, NLD = (HALO + NT - 1) / NT;
-    constexpr int HALO_BYTES = IH * IW * PSTR * 2, RED_BYTES = (WK - 1) * WM * WN * FM * 64 * 16;
-    __shared__ __align__(16) uint16_t halo[(HALO_BYTES > RED_BYTES ? HALO_BYTES : RED_BYTES) / 2];
+    uint16_t* const halo = L.halo;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wk = wave / (WM * WN), wmn = wave - wk * (WM * WN);
     const int wn = wmn % WN, wm = wmn / WN;
-    const int co_w = blockIdx.y * BN + wn * 16;
+    const int co_w = ct * BN + wn * 16;
     const int co = co_w + 4 * (lane >> 4);  // the lane's 4 output channels in the accumulator
-    const int t = blockIdx.x;
     const int tx = t % a.tiles_x, r = t / a.tiles_x;
     const int ty = r % a.tiles_y, img = r / a.tiles_y;
     const int oy0 = ty * TH, ox0 = tx * TW;
@@ -706,6 +715,12 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
                 epilogue4r(a, ((size_t)img * a.hout + oy) * a.wout + ox, co, acc[f], bias, neg, rres[f]);
         }
     }
+}
+
+template <int KS, int S, int CIN32, int FM, int WM, int WN, int WK, bool VEC, bool SPLIT = false>
+__global__ __launch_bounds__(64 * WM * WN * WK) void conv_tile(ConvKArgs a) {
+    __shared__ __align__(16) TileLds<KS, S, CIN32, FM, WM, WN, WK> lds;
+    conv_tile_body<KS, S, CIN32, FM, WM, WN, WK, VEC, SPLIT>(a, blockIdx.x, blockIdx.y, lds);
 }
 
 // The sibling convs' launch of a one-tile configuration (one workgroup per tile, one channel tile)

@@ -7,12 +7,16 @@
 namespace fhc {
 
 struct GmCoRun {
-    FitPairLaunchFn fn;  // fit round 0 with the pair's tiles (fit_pair_launcher)
-    PairKArgs pk;        // the pair's arguments, pointers bound
-    uint32_t tiles;      // the pair's tiles
+    FitPairLaunchFn fn;   // fit round 0 with the pair's tiles (fit_pair_launcher)
+    PairKArgs pk;         // the pair's arguments, pointers bound
+    uint32_t tiles;       // the pair's tiles
+    FitConvLaunchFn cfn;  // fit round 1 with a conv's workgroups (fit_conv_launcher), or null
+    ConvKArgs ca;         // the conv's arguments, pointers bound
+    dim3 cgrid;           // the conv's grid (tiles, channel tiles)
 };
 
-// fhc_gmhs with round 0 of the fit launched by co->fn beside co's work when co is not null
+// fhc_gmhs with round 0 of the fit launched by co->fn beside co's pair, and round 1 by co->cfn beside co's conv
+// (when given), when co is not null
 int gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
              uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, const GmCoRun* co, void* stream);
 

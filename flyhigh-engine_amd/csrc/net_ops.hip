@@ -2385,9 +2385,15 @@ int fhc::gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t
         float* hs = raw + hs_off;
         const hipStream_t st = (hipStream_t)stream;
         for (uint32_t round = 0; round < 4; round++) {
-            if (round == 0 && co) {  // the co-runner's workgroups beside the first round's
-                const FitRoundArgs fa{static_cast<const uint16_t*>(flow->p), flow->cstride, flow->c0, h8, w8, p.delta, 0, part[1], part[0]};
+            const FitRoundArgs fa{static_cast<const uint16_t*>(flow->p), flow->cstride, flow->c0, h8, w8, p.delta,
+                                  round, part[(round + 1) & 1u], part[round & 1u]};
+            if (co && round == 0) {  // the co-runner's pair beside the first round's workgroups
                 const hipError_t ce = co->fn(fa, co->pk, co->tiles, st);
+                if (ce != hipSuccess) return fail(-2, "gmhs: launch failed: %s", hipGetErrorString(ce));
+                continue;
+            }
+            if (co && co->cfn && round == 1) {  // its conv beside the second round's
+                const hipError_t ce = co->cfn(fa, co->ca, co->cgrid, st);
                 if (ce != hipSuccess) return fail(-2, "gmhs: launch failed: %s", hipGetErrorString(ce));
                 continue;
             }

@@ -91,7 +91,7 @@ def _lib():
                                 P],
             "fhc_gmhs_params": [U, U, U, U, ctypes.POINTER(GmhsPar)],
             "fhc_gmhs": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P],
-            "fhc_gmhs_film_pair": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P, P, P, P, P],
+            "fhc_gmhs_film": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P, P, P, P, P, P, P, P],
         }
         for name, args in sig.items():
             f = getattr(L, name)
@@ -415,19 +415,23 @@ def gmhs(a, b, flow, full_w: int, level: int = 1, ws=None, stream=None):
     return ws
 
 
-def gmhs_film_pair(a, b, flow, full_w: int, level, ws, pair, pair_x, pair_film, pair_y, stream=None):
-    """gmhs(a, b, flow, ...) and pair.run_film(pair_x, pair_film, pair_y) (a fhconv.ConvPairPlan made with film_in),
-    the pair's workgroups inside the repair's first launch."""
+def gmhs_film(a, b, flow, full_w: int, level, ws, pair, pair_x, pair_film, pair_y, conv=None, conv_x=None,
+              conv_y=None, stream=None):
+    """gmhs(a, b, flow, ...), pair.run_film(pair_x, pair_film, pair_y) (a fhconv.ConvPairPlan made with film_in) and
+    conv.run(conv_x, conv_y) (a fhconv.ConvPlan, optional): the pair's workgroups inside the repair's first launch,
+    the conv's inside the second (fhc_gmhs_film)."""
     a, b, flow = _v(a), _v(b), _v(flow)
     _, h, w, _ = a.shape
     _, h8, w8, _ = flow.shape
     d = pair.desc
     if not pair_film.is_contiguous() or pair_film.numel() != d.n * 2 * d.cin or pair_film.element_size() != 2:
-        raise FhcError(f"gmhs_film_pair: the FiLM vectors need {d.n * 2 * d.cin} contiguous f16 values")
-    _run("gmhs_film_pair",
-         _lib().fhc_gmhs_film_pair(_ref(a), _ref(b), h, w, _ref(flow), h8, w8, full_w, level, ws.data_ptr(),
-                                   ws.numel() * ws.element_size(), pair._h, pair_x.data_ptr(), pair_film.data_ptr(),
-                                   pair_y.data_ptr(), _stream_handle(stream)))
+        raise FhcError(f"gmhs_film: the FiLM vectors need {d.n * 2 * d.cin} contiguous f16 values")
+    _run("gmhs_film",
+         _lib().fhc_gmhs_film(_ref(a), _ref(b), h, w, _ref(flow), h8, w8, full_w, level, ws.data_ptr(),
+                              ws.numel() * ws.element_size(), pair._h, pair_x.data_ptr(), pair_film.data_ptr(),
+                              pair_y.data_ptr(), None if conv is None else conv._h,
+                              None if conv_x is None else conv_x.data_ptr(),
+                              None if conv_y is None else conv_y.data_ptr(), _stream_handle(stream)))
     return ws
 
 

@@ -137,11 +137,14 @@ class ComposedChains:
         self.conv(a, x, ya, res_a)
         self.conv(b, x, yb)
 
-    def gmhs_film(self, a: V, b: V, flow: V, full_w: int, level: int, fa, fb, h: V, c: int, hm: V, mid: V, y: V):
-        """The repair, and the FiLM pair of film_pair(fa, fb, h, c, hm, mid, y), which touch none of each other's
-        data (on the GPU the pair's workgroups run inside the repair's first launch)."""
+    def gmhs_film(self, a: V, b: V, flow: V, full_w: int, level: int, fa, fb, h: V, c: int, hm: V, mid: V, y: V,
+                  fo, yo: V):
+        """The repair, the FiLM pair of film_pair(fa, fb, h, c, hm, mid, y) and the conv fo of y into yo, which touch
+        none of the repair's data (on the GPU the pair's workgroups run inside the repair's first launch, the
+        conv's inside the second)."""
         self.gmhs(a, b, flow, full_w, level)
         self.film_pair(fa, fb, h, c, hm, mid, y)
+        self.conv(fo, y, yo)
 
     def pair_pyramid(self, q: V, i8: V, i16: V, l16: V):
         self.avgpool(q, 3, i8, 2)
@@ -272,7 +275,7 @@ class GpuBackend(ComposedChains):
                                      r_cstride=res.buf.shape[3] if res is not None else (ycs if mid_res else 0),
                                      r_c0=res.c0 if res is not None else 0)
 
-    def conv(self, name, x: V, y: V, res: Optional[V] = None):
+    def _conv_plan(self, name, x: V, y: V, res: Optional[V] = None):
         key = ("conv", name, x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0,
                None if res is None else res.buf.data_ptr())
         p = self.plans.get(key)
@@ -282,6 +285,10 @@ class GpuBackend(ComposedChains):
             if p.workspace_bytes:
                 raise RuntimeError(f"{name}: a split-K plan needs a workspace; give the frame convs a table entry")
             p._work = p.describe()
+        return p
+
+    def conv(self, name, x: V, y: V, res: Optional[V] = None):
+        p = self._conv_plan(name, x, y, res)
         xb, yb, rb, st = x.buf, y.buf, None if res is None else res.buf, self.stream
         self._go(name, lambda: p.run(xb, yb, rb, stream=st), p._work["bytes"], p._work["flops"], "conv")
 
@@ -348,10 +355,12 @@ class GpuBackend(ComposedChains):
             self.plans[key] = p
         return p
 
-    def gmhs_film(self, a: V, b: V, flow: V, full_w: int, level: int, fa, fb, h: V, c: int, hm: V, mid: V, y: V):
+    def gmhs_film(self, a: V, b: V, flow: V, full_w: int, level: int, fa, fb, h: V, c: int, hm: V, mid: V, y: V,
+                  fo, yo: V):
         p = self._film_plan(fa, fb, h, c, mid, y)
         if p is False or level == 0:
-            return super().gmhs_film(a, b, flow, full_w, level, fa, fb, h, c, hm, mid, y)
+            return super().gmhs_film(a, b, flow, full_w, level, fa, fb, h, c, hm, mid, y, fo, yo)
+        q = self._conv_plan(fo, y, yo)
         va, vb, vf = self._v(a), self._v(b), self._v(flow)
         _, hh, ww, _ = va.shape
         _, h8, w8, _ = vf.shape
@@ -362,10 +371,11 @@ class GpuBackend(ComposedChains):
         gp = self.fh.gmhs_params(hh, ww, full_w, level)
         cells = gp["hc"] * gp["wc"]
         nbytes = 5 * 4 * 2 * h8 * w8 + 2 * 3 * 2 * hh * ww + 4 * cells * (5 + 5 + 5 + 3) + 4 * 2 * h8 * w8
-        hb, yb, g, st = h.buf, y.buf, self.g, self.stream
-        self._go(f"gmhs + film_modulate+{fa}+{fb} (the pair in the first fit launch)",
-                 lambda: self.fh.gmhs_film_pair(va, vb, vf, full_w, level, ws, p, hb, g, yb, stream=st),
-                 nbytes + p._work["bytes"] + 2 * 2 * c, p._work["flops"], "op", kernels=8)
+        hb, yb, ob, g, st = h.buf, y.buf, yo.buf, self.g, self.stream
+        self._go(f"gmhs + film_modulate+{fa}+{fb} + {fo} (in the first two fit launches)",
+                 lambda: self.fh.gmhs_film(va, vb, vf, full_w, level, ws, p, hb, g, yb, q, yb, ob, stream=st),
+                 nbytes + p._work["bytes"] + 2 * 2 * c + q._work["bytes"], p._work["flops"] + q._work["flops"], "op",
+                 kernels=8)
 
     def film_pair(self, a, b, h: V, c: int, hm: V, mid: V, y: V):
         p = self._film_plan(a, b, h, c, mid, y)
@@ -660,8 +670,9 @@ class FlyHighFG:
 
     def pair(self, cofilm: bool = False) -> bool:
         """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1), and op 62 (up.w, which reads only h).
-        cofilm: also the next mid(t)'s FiLM pair (ops 50-52: it reads only h and the FiLM vector of t, which must be
-        in place), inside the repair's first launch; returns whether it ran (mid(t, film_done=True) then skips it)."""
+        cofilm: also the next mid(t)'s FiLM head (ops 50-53: it reads only h and the FiLM vector of t, which must be
+        in place), inside the repair's first two launches; returns whether it ran (mid(t, film_done=True) then skips
+        it)."""
         be, S = self.be, self.shape
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
         if self.frame is not None:  # the frames -> A, B (rgba_in; in the internal-size mode, the downscale)
@@ -696,15 +707,16 @@ class FlyHighFG:
         be.conv_siblings("fine.out", "up.w", V(self.h), V(self.fv), V(self.fv), V(self.wt36))
         if self.repair and cofilm:  # the repair, with mid's FiLM pair in its first launch (pair_mid())
             be.gmhs_film(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair,
-                         "film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))
+                         "film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2), "film.out",
+                         V(self.dfilm))
             return True
         if self.repair:  # the periodic-structure repair of the pair's flow, in place (gmhs.rs:149-206)
             be.gmhs(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair)
         return False
 
     def pair_mid(self, t: float, W: Optional[dict] = None):
-        """pair() then mid(t), the FiLM pair of t run inside the repair's first launch (one launch fewer). With W
-        None the FiLM vector of t must already be in place, as for mid()."""
+        """pair() then mid(t), the FiLM head of t run inside the repair's first two launches (two launches fewer).
+        With W None the FiLM vector of t must already be in place, as for mid()."""
         if W is not None:
             self.be.set_g(film_mlp(W, t))
         self.mid(t, None, film_done=self.pair(cofilm=True))
@@ -713,13 +725,13 @@ class FlyHighFG:
         """mid(t): models/graph.json ops 44-82 but 62 (up.w, run by pair()), render_pix included. With W None the
         FiLM vector of t must already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes
         it that way, as the reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22).
-        film_done: the FiLM pair (ops 50-52) already ran with this t's vector (pair(cofilm=True))."""
+        film_done: the FiLM head (ops 50-53) already ran with this t's vector (pair(cofilm=True))."""
         be = self.be
         if W is not None:
             be.set_g(film_mlp(W, t))                                                          # 49
         if not film_done:
             be.film_pair("film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))  # 50-52
-        be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
+            be.conv("film.out", V(self.fh2), V(self.dfilm))                                   # 53
         be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(self.dfilm), t, V(self.up7), V(self.ftvt), V(self.lin),
                              V(self.dvis))                                                    # 44-48, 54-62
         be.refine_input(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend))  # 63-76

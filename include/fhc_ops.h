@@ -257,18 +257,22 @@ int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc
 int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
              uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, void* stream);
 
-/* fhc_gmhs, and a FiLM pair plan (fhc_conv_pair_plan_create with FHC_PAIR_FILM_IN, include/fhc_conv.h) run as
- * fhc_conv_pair_run_film(pair, pair_x, pair_film, pair_y) would run it, with the pair's workgroups inside the
- * repair's first launch: the fit's 128 workgroups are latency-bound and leave the GPU to the pair. The two touch
- * none of each other's data (the frame: the repair of pair()'s flow, and mid()'s FiLM head, which reads h and the
- * FiLM vectors of t). The pair plan's configuration must be a one-tile configuration of 3 + 3 channel blocks on one
- * wave row (the 48 -> 48 -> 48 FiLM head at 2 or 4 rows per tile); level 0 runs the pair alone. Seven launches
- * where the two take nine. No counterpart in the reference. */
+/* fhc_gmhs and the FiLM head: a FiLM pair plan (fhc_conv_pair_plan_create with FHC_PAIR_FILM_IN, fhc_conv.h) run
+ * as fhc_conv_pair_run_film(pair, pair_x, pair_film, pair_y) runs it, with its workgroups inside the repair's first
+ * launch, and, when conv is not NULL, a conv plan (the FiLM head's output conv on pair_y) run as
+ * fhc_conv_run(conv, conv_x, conv_y, NULL, NULL) runs it, with its workgroups inside the second: the fit's 128
+ * workgroups are latency-bound and leave the GPU to them. They touch none of the repair's data (the frame: the
+ * repair of pair()'s flow, and mid()'s FiLM head, which reads h and the FiLM vectors of t). The pair's
+ * configuration must be a one-tile configuration of 3 + 3 channel blocks on one wave row (the 48 -> 48 -> 48 FiLM
+ * head at 2 or 4 rows per tile); the conv a one-launch direct plan without residual (its workgroups join the fit's
+ * where its configuration is the one-row 64-channel kernel-row split, else it runs in its own launch after the
+ * repair). level 0 runs the pair, then the conv. Eight launches (seven with the conv joined) where the three take
+ * ten. No counterpart in the reference. */
 struct fhc_conv_plan;
-int fhc_gmhs_film_pair(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
-                       uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
-                       const struct fhc_conv_plan* pair, const void* pair_x, const void* pair_film, void* pair_y,
-                       void* stream);
+int fhc_gmhs_film(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
+                  uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
+                  const struct fhc_conv_plan* pair, const void* pair_x, const void* pair_film, void* pair_y,
+                  const struct fhc_conv_plan* conv, const void* conv_x, void* conv_y, void* stream);
 
 #ifdef __cplusplus
 }

@@ -7,11 +7,13 @@ for bit. The whole-frame check (test_frame.py::test_fused_chains_equal_their_ops
 the 1080p frame's shapes; here, for the coarse output with the fine block's input, flow_t / vis_t with the convex
 upsample, the pictures' resize with the pyramid, the refine head's input, the encoders' fold beside a cost volume,
 the refine head's last pair with affine_out, the FiLM head's pair with film_modulate on its input, fine.out with
-up.w as sibling convs of h, and the repair with the FiLM pair inside its first launch: ragged grids whose coarse-to-fine ratio
+up.w as sibling convs of h, and the repair with the FiLM head inside its first two launches: ragged grids whose coarse-to-fine ratio
 is no integer, downscales other than 4x, channel counts that are no multiple of 4 (the 2-byte path), views into wider
 buffers, no streaming state, a flow read scale of 1, and a batch of 2 for the convex upsample and the FiLM pair
 (one FiLM vector per image).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -20,6 +22,7 @@ import flyhighfg_net as net
 from flyhighfg_net import V
 
 pytestmark = pytest.mark.gpu
+TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "flyhigh-engine_amd", "tune_mi355x.txt")
 
 
 def say(*a):
@@ -187,10 +190,22 @@ def test_conv_siblings_equal_the_two_convs(n, h, w, c0, cs):
 
 
 @pytest.mark.parametrize("net_h,net_w,full_w", [(480, 864, 1920), (128, 256, 608)])
-def test_gmhs_film_pair_equals_gmhs_and_film_pair(net_h, net_w, full_w):
-    """The repair with the FiLM pair's workgroups inside its first launch (the fit at 192 threads per workgroup, the
-    pair's tiles beside) against the repair's own launches and the pair's own launch."""
-    say("gmhs_film_pair", net_h, net_w, full_w)
+def test_gmhs_film_equals_gmhs_film_pair_and_film_out(net_h, net_w, full_w):
+    """The repair with the FiLM pair's workgroups inside its first launch and film.out's inside its second (the fit
+    at 192 threads per workgroup, the other work's tiles beside) against the repair's own launches and theirs.
+    film.out joins the fit only in its committed configuration, so the choice table is loaded for both runs."""
+    say("gmhs_film", net_h, net_w, full_w)
+    import fhconv
+    saved = fhconv.format_tune()
+    fhconv.parse_tune(open(TABLE).read())
+    try:
+        _gmhs_film_case(net_h, net_w, full_w)
+    finally:  # the choice table is process-wide: leave it as found
+        fhconv.load().fhc_tune_clear()
+        fhconv.parse_tune(saved)
+
+
+def _gmhs_film_case(net_h, net_w, full_w):
     outs = []
     h8, w8 = net_h // 8, net_w // 8
     for be in backends():
@@ -200,8 +215,9 @@ def test_gmhs_film_pair_equals_gmhs_and_film_pair(net_h, net_w, full_w):
         hb = fill(be, rng, 1, h8, w8, 48)
         be.set_g(rng.uniform(-0.5, 0.5, 96).astype(np.float16).view(np.uint16))
         hm, mid, y = fill(be, rng, 1, h8, w8, 48), fill(be, rng, 1, h8, w8, 48), fill(be, rng, 1, h8, w8, 48)
+        df = fill(be, rng, 1, h8, w8, 8)
         be.gmhs_film(V(be.image(ab, 0)), V(be.image(ab, 1)), V(fv), full_w, 1, "film.h1", "film.h2", V(hb), 48, V(hm),
-                     V(mid), V(y))
-        outs.append({"fv": be.host(fv).copy(), "y": be.host(y).copy()})
+                     V(mid), V(y), "film.out", V(df))
+        outs.append({"fv": be.host(fv).copy(), "y": be.host(y).copy(), "dfilm": be.host(df).copy()})
     for k in outs[0]:
         same(outs[0][k], outs[1][k], k)
