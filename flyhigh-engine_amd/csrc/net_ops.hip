@@ -1426,19 +1426,23 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
 // The antialiased resize of n padded RGBA8 frames (hp x wp, rgba_in's BGR f16) to oh x ow, into a view of 8-byte
 // 4-channel pixels (channel 3 written 0): rgba_in.wgsl then interp.wgsl:11-45 with antialias, as
 // interp_aa_lds_kernel computes it. A workgroup stages the union of its 16 x 16 outputs' windows, at most
-// 16 * R x 16 * R padded pixels, each converted once (R = 3 covers downscales up to about 2.9x); the values are those
-// of the f16 picture rgba_in writes, held widened to f32 where the window fits (R = 3).
-template <int KM, int R>
+// EXT x EXT padded pixels (EXT <= 16 * R, the lanes' R x R load stripes covering it), each converted once; the
+// values are those of the f16 picture rgba_in writes. LAY: how a staged pixel is held in LDS, as a float4 (16 bytes,
+// no widening per tap), as f16 (8 bytes: three widenings per tap) or as an f32 pair plus an f32 (12 bytes, two reads
+// per tap, no widening). The LDS a workgroup holds sets how many share a CU, and the kernel runs at the rate its
+// waves in flight allow: at 1080p (a 39 x 38 window) 40 x 40 pixels held as f32 pair + f32 (21 KiB with the tables)
+// let seven workgroups share a CU and take 12.8 us, as f16 (15 KiB, eight) 13.1 us, as float4 (27 KiB, five)
+// 15.7 us, 48 x 48 as float4 (38 KiB, four) 16.0 us.
+template <int KM, int R, int EXT, int LAY>
 __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* src, uint32_t w, uint32_t h,
                                                                uint32_t pitch, uint64_t fstride, uint32_t ih,
                                                                uint32_t iw, OView out, uint32_t oh, uint32_t ow,
                                                                uint32_t tiles_x, uint32_t tiles_y, float sh, float sw) {
-    constexpr uint32_t EXT = kAaT * R;
-    // the staged window in f32 (37 KiB at R 3: no widening per tap) or, for the 80-pixel window, in f16
-    constexpr bool F32 = R <= 3;
-    using Cell = typename std::conditional<F32, float4, uint2>::type;
+    static_assert(EXT <= kAaT * R && LAY >= 0 && LAY <= 2, "the load stripes cover the window");
     static_assert(kAaT * KM <= kThreads / 2, "a weight table per axis takes half the block");
+    using Cell = typename std::conditional<LAY == 0, float4, typename std::conditional<LAY == 1, uint2, float2>::type>::type;
     __shared__ Cell tile[EXT * EXT];
+    __shared__ float tileb[LAY == 2 ? EXT * EXT : 1];
     __shared__ float tab[256], wxs[kAaT * KM], wys[kAaT * KM];
     __shared__ int lcs[kAaT * KM], lrs[kAaT * KM];
     const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
@@ -1482,12 +1486,15 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
             const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(
                 rf, __umul24((uint32_t)min(ylo + row, (int)h - 1), pitch4) + (uint32_t)min(xlo + col, (int)w - 1) * 4u,
                 0, 0);
-            if constexpr (F32)
+            if constexpr (LAY == 0)
                 tile[row * EXT + col] = float4{unit_tab(tab, v, 0), unit_tab(tab, v, 1), unit_tab(tab, v, 2), 0.0f};
-            else
+            else if constexpr (LAY == 1)
                 tile[row * EXT + col] = uint2{(uint32_t)f2h(unit_tab(tab, v, 0)) |
                                                   ((uint32_t)f2h(unit_tab(tab, v, 1)) << 16),
                                               (uint32_t)f2h(unit_tab(tab, v, 2))};
+            else
+                tile[row * EXT + col] = float2{unit_tab(tab, v, 0), unit_tab(tab, v, 1)},
+                tileb[row * EXT + col] = unit_tab(tab, v, 2);
         }
     __syncthreads();
     const uint32_t ox = ox0 + tx, oy = oy0 + ty;
@@ -1500,17 +1507,18 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
 #pragma unroll
     for (int jy = 0; jy < KM; jy++) {
         const float wy = wys[ty * KM + jy];
-        const Cell* lrow = tile + lrs[ty * KM + jy] * EXT;
+        const uint32_t lrow = lrs[ty * KM + jy] * EXT;
 #pragma unroll
         for (int jx = 0; jx < KM; jx++) {
             // a tap outside the window has weight +0 and a value in [0, 1]: it adds +0, leaving acc and norm as the
             // reference's skipped tap leaves them (interp_aa_lds_kernel, whose views may hold any value, points such
             // taps at a zero cell instead)
             const float wgt = wx[jx] * wy;
-            const Cell q = lrow[lc[jx]];
+            const Cell q = tile[lrow + lc[jx]];
             float vv[3];
-            if constexpr (F32) vv[0] = q.x, vv[1] = q.y, vv[2] = q.z;
-            else vv[0] = h2f((uint16_t)q.x), vv[1] = h2f((uint16_t)(q.x >> 16)), vv[2] = h2f((uint16_t)q.y);
+            if constexpr (LAY == 0) vv[0] = q.x, vv[1] = q.y, vv[2] = q.z;
+            else if constexpr (LAY == 1) vv[0] = h2f((uint16_t)q.x), vv[1] = h2f((uint16_t)(q.x >> 16)), vv[2] = h2f((uint16_t)q.y);
+            else vv[0] = q.x, vv[1] = q.y, vv[2] = tileb[lrow + lc[jx]];
 #pragma unroll
             for (int i = 0; i < 3; i++) acc[i] = acc[i] + vv[i] * wgt;
             norm = norm + wgt;
@@ -2295,9 +2303,12 @@ extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_
             return fail(-1, "rgba_resize: %u x %u -> %u x %u needs %u taps, a %u-pixel tile window (at most 8 and %u)",
                         wp, hp, ow, oh, taps, ext, 5 * kAaT);
         const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
-        auto k = ext <= 3 * kAaT
-                     ? (taps <= 5 ? rgba_resize_kernel<5, 3> : taps <= 6 ? rgba_resize_kernel<6, 3> : rgba_resize_kernel<8, 3>)
-                     : (taps <= 6 ? rgba_resize_kernel<6, 5> : rgba_resize_kernel<8, 5>);
+        // the 40-pixel window covers the common downscales (1080p to 864 x 480: 39 x 38)
+        auto k = ext <= 40 && taps <= 5 ? rgba_resize_kernel<5, 3, 40, 2>
+                 : ext <= 3 * kAaT
+                     ? (taps <= 5 ? rgba_resize_kernel<5, 3, 48, 2> : taps <= 6 ? rgba_resize_kernel<6, 3, 48, 2>
+                                                                    : rgba_resize_kernel<8, 3, 48, 2>)
+                     : (taps <= 6 ? rgba_resize_kernel<6, 5, 80, 1> : rgba_resize_kernel<8, 5, 80, 1>);
         if ((uint64_t)pitch * 4 >= (1u << 24) || (uint64_t)h * pitch * 4 >= (1u << 31))
             return fail(-1, "rgba_resize: frames of pitch %u and %u rows are too large", pitch, h);
         hipLaunchKernelGGL(k, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream,

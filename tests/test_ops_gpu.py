@@ -320,7 +320,8 @@ def test_rgba_in_and_out_match_oracle(n, h, w, hp, wp, cs, c0):
     torch.cuda.synchronize()
 
 
-# the shapes reach each kernel instantiation (taps, window): (5, 48) at 1080p, (8, 80), (8, 48), (6, 48), (6, 80)
+# the shapes reach each kernel instantiation (taps, window): (5, 40) at 1080p, (5, 48), (8, 80), (8, 48), (6, 48),
+# (6, 80)
 @pytest.mark.parametrize("h,w,oh,ow", [(1080, 1920, 480, 864), (150, 300, 64, 128), (61, 97, 30, 40),
                                        (60, 30, 40, 8), (60, 30, 40, 11), (60, 90, 40, 32)])
 def test_rgba_resize_equals_rgba_in_then_the_antialiased_resize(h, w, oh, ow):
