@@ -1720,23 +1720,26 @@ __global__ __launch_bounds__(kThreads) void gm_dwin_h_kernel(const float* tex, f
     hs[t] = acc / (float)span;
 }
 
-// box_v of hs at the select's rows, then the select (gm_select.wgsl:14-27), one lane per E8 cell; dec [5][h8][w8]
-// receives the five values the cell decides on (maps 0-2 after both windows, maps 3-4 after the texture window)
+// box_v of hs at the select's rows, then the select (gm_select.wgsl:14-27); dec [5][h8][w8] receives the five values
+// an E8 cell decides on (maps 0-2 after both windows, maps 3-4 after the texture window). Four consecutive lanes per
+// cell: lane m < 3 sums map m's window (its NT loads in one batch), lane 3 loads maps 3-4, and every lane of the
+// four gathers the five values (in-wave shuffles), decides as the select does and stores flow channel m. The lanes
+// past the last cell shadow it (in-bounds loads, so that every lane of a wave takes part in the shuffles) and store
+// nothing. items: cells.
 template <uint32_t NT>
 __global__ __launch_bounds__(kThreads) void gm_dwin_v_select_kernel(const float* hs, const float* tex,
                                                                     const float* coef, OView flow, float* dec,
                                                                     uint32_t h8, uint32_t w8, uint32_t hc, uint32_t wc,
                                                                     uint32_t r, float eps, float dmin, float texf,
                                                                     uint32_t items) {
-    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-    if (t >= items) return;
-    const uint32_t i = t / w8, j = t % w8, span = 2 * r + 1;
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x, cell = t / 4, m = t % 4;
+    const bool live = cell < items;
+    const uint32_t cl = live ? cell : items - 1;
+    const uint32_t i = cl / w8, j = cl % w8, span = 2 * r + 1;
     const int y = gm_sel_row(i, hc, h8), x = gm_sel_row(j, wc, w8);
     const size_t n = (size_t)hc * wc, idx = (size_t)y * wc + x;
-    const float lm = tex[3 * n + idx], l2 = tex[4 * n + idx];
-    float dw[3];
-#pragma unroll
-    for (uint32_t m = 0; m < 3; m++) {
+    float own, own2 = 0.0f;
+    if (m < 3) {
         const float* col = hs + (size_t)m * hc * w8 + j;
         float v[NT];
 #pragma unroll
@@ -1746,17 +1749,22 @@ __global__ __launch_bounds__(kThreads) void gm_dwin_v_select_kernel(const float*
 #pragma unroll
         for (uint32_t d = 0; d < NT; d++)
             if (d < span) acc = acc + v[d];
-        dw[m] = acc / (float)span;
+        own = acc / (float)span;
+    } else {
+        own = tex[3 * n + idx], own2 = tex[4 * n + idx];
     }
-    const float cm = dw[0], ca = dw[1], dv = dw[2];
+    const int q = (int)(threadIdx.x % 64 - m);  // the cell's first lane in the wave
+    const float cm = __shfl(own, q), ca = __shfl(own, q + 1), dv = __shfl(own, q + 2);
+    const float lm = __shfl(own, q + 3), l2 = __shfl(own2, q + 3);
+    if (!live) return;
     const size_t n8 = (size_t)h8 * w8;
-    dec[t] = cm, dec[n8 + t] = ca, dec[2 * n8 + t] = dv, dec[3 * n8 + t] = lm, dec[4 * n8 + t] = l2;
+    dec[m * n8 + cell] = own;
+    if (m == 3) dec[4 * n8 + cell] = own2;
     const float sd = sqrtf(fmaxf(l2 - lm * lm, 0.0f));
     if (ca + eps < cm && dv > dmin && sd > texf) {
         const float xn = -1.0f + 2.0f * (float)j / (float)max(w8 - 1, 1u);
         const float yn = -1.0f + 2.0f * (float)i / (float)max(h8 - 1, 1u);
-#pragma unroll
-        for (uint32_t c = 0; c < 4; c++) st(flow, t, c, coef[c * 4] + coef[c * 4 + 1] * xn + coef[c * 4 + 2] * yn);
+        st(flow, cell, m, coef[m * 4] + coef[m * 4 + 1] * xn + coef[m * 4 + 2] * yn);
     }
 }
 
@@ -2426,7 +2434,7 @@ int fhc::gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t
         hipLaunchKernelGGL(wide ? gm_dwin_h_kernel<65> : gm_dwin_h_kernel<33>, dim3((nh + kThreads - 1) / kThreads),
                            dim3(kThreads), 0, st, maps, hs, p.hc, p.wc, w8, p.r_dwin, nh);
         hipLaunchKernelGGL(wide ? gm_dwin_v_select_kernel<65> : gm_dwin_v_select_kernel<33>,
-                           dim3((ne + kThreads - 1) / kThreads), dim3(kThreads), 0, st, hs, maps, coef, outv(flow), raw,
+                           dim3((4 * ne + kThreads - 1) / kThreads), dim3(kThreads), 0, st, hs, maps, coef, outv(flow), raw,
                            h8, w8, p.hc, p.wc, p.r_dwin, p.eps, p.dmin, p.tex, ne);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "gmhs: launch failed: %s", hipGetErrorString(e));
