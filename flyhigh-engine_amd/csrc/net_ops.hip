@@ -510,6 +510,7 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
         wx[j] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
         lc[j] = xx < xmax ? xx - xlo : (int)kAaExt;
     }
+    constexpr int NC = PYR ? 3 : 4;  // the channels summed: the pyramid's pictures have 3
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, norm = 0.0f;
 #pragma unroll
     for (int jy = 0; jy < KM; jy++) {
@@ -523,13 +524,13 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
             const float v[4] = {h2f((uint16_t)q.x), h2f((uint16_t)(q.x >> 16)), h2f((uint16_t)q.y),
                                 h2f((uint16_t)(q.y >> 16))};
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] = acc[i] + v[i] * wgt;
+            for (int i = 0; i < NC; i++) acc[i] = acc[i] + v[i] * wgt;
             norm = norm + wgt;
         }
     }
-    float val[4];
+    float val[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int i = 0; i < 4; i++) val[i] = acc[i] / norm * x.scale;
+    for (int i = 0; i < NC; i++) val[i] = acc[i] / norm * x.scale;
     if (valid) st4<false>(out, ((size_t)img * oh + oy) * ow + ox, 0, c, val);
     if constexpr (PYR) {
         if (valid)
