@@ -1581,16 +1581,19 @@ __device__ float gm_samp(const View& v, uint32_t h, uint32_t w, float gx, float 
     return top * (1.0f - ay) + bot * ay;
 }
 
-// gm_cost.wgsl:55-75, maps 0-4 (planar [5][hc][wc]); one lane per cell of a 16 x 16 block, the block solving the
-// last fit round first (block 0 also stores the coefficients, [4][4], for the select and the caller). VEC: the
-// pictures and the flow are 4-channel aligned views (one 8-byte load per pixel).
+// gm_cost.wgsl:55-75, maps 0-4 (planar [5][hc][wc]) for a 16 x 8 block of cells, the block solving the last fit
+// round first (block 0 also stores the coefficients, [4][4], for the select and the caller). Two lanes per cell,
+// in different waves: threads 0-127 sample for cm and l (maps 0, 3, 4), threads 128-255 for ca and dv (maps 1, 2);
+// ca outside the pictures is cm, handed over through LDS. VEC: the pictures and the flow are 4-channel aligned
+// views (one 8-byte load per pixel).
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint32_t h, uint32_t w, View flow,
                                                            uint32_t h8, uint32_t w8, const float* part, float* coef,
                                                            float* maps, uint32_t hc, uint32_t wc) {
-    __shared__ float ss[4][9], cf[4][3];
-    const uint32_t t = threadIdx.x;
-    const uint32_t x = blockIdx.x * 16 + t % 16, y = blockIdx.y * 16 + t / 16;
+    __shared__ float ss[4][9], cf[4][3], cms[128];
+    const uint32_t t = threadIdx.x, cl = t % 128;
+    const bool second = t >= 128;  // uniform over each wave
+    const uint32_t x = blockIdx.x * 16 + cl % 16, y = blockIdx.y * 8 + cl / 16;
     const bool valid = x < wc && y < hc;
     const float rx = ((float)x + 0.5f) * 2.0f - 0.5f, ry = ((float)y + 0.5f) * 2.0f - 0.5f;
     // the E8 flow at (rx, ry), bilinear (gm_cost.wgsl:38-48), loaded before the block's solve
@@ -1616,7 +1619,6 @@ __global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint3
     }
     gmfit::solve_block(part, 0xfu, ss, cf);
     if (blockIdx.x == 0 && blockIdx.y == 0 && t < 16) coef[t] = (t & 3u) == 3u ? 0.0f : cf[t >> 2][t & 3u];
-    if (!valid) return;
     const size_t n = (size_t)hc * wc, i = (size_t)y * wc + x;
     const float xn = -1.0f + 2.0f * ix / (float)max(w8 - 1, 1u), yn = -1.0f + 2.0f * iy / (float)max(h8 - 1, 1u);
     float f[4], gh[4];
@@ -1626,17 +1628,26 @@ __global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint3
         f[c] = top * (1.0f - fy) + bot * fy;
         gh[c] = cf[c][0] + cf[c][1] * xn + cf[c][2] * yn;
     }
-    const float cm =
-        fabsf(gm_samp<VEC>(a, h, w, rx + f[0], ry + f[1]) - gm_samp<VEC>(b, h, w, rx + f[2], ry + f[3]));
-    const float wm = (float)w - 1.0f, hm = (float)h - 1.0f;
-    const float ax = rx + gh[0], ay = ry + gh[1], bx = rx + gh[2], by = ry + gh[3];
-    const bool inside = ax >= 0.0f && ax <= wm && ay >= 0.0f && ay <= hm && bx >= 0.0f && bx <= wm && by >= 0.0f &&
-                        by <= hm;
-    const float ca = inside ? fabsf(gm_samp<VEC>(a, h, w, ax, ay) - gm_samp<VEC>(b, h, w, bx, by)) : cm;
-    const float l = gm_samp<VEC>(a, h, w, rx, ry);
-    const float dvx = (gh[2] - gh[0]) - (f[2] - f[0]), dvy = (gh[3] - gh[1]) - (f[3] - f[1]);
-    maps[i] = cm, maps[n + i] = ca, maps[2 * n + i] = sqrtf(dvx * dvx + dvy * dvy);
-    maps[3 * n + i] = l, maps[4 * n + i] = l * l;
+    float ca = 0.0f;
+    bool inside = false;
+    if (!second) {
+        float cm = 0.0f;
+        if (valid) {
+            cm = fabsf(gm_samp<VEC>(a, h, w, rx + f[0], ry + f[1]) - gm_samp<VEC>(b, h, w, rx + f[2], ry + f[3]));
+            const float l = gm_samp<VEC>(a, h, w, rx, ry);
+            maps[i] = cm, maps[3 * n + i] = l, maps[4 * n + i] = l * l;
+        }
+        cms[cl] = cm;
+    } else if (valid) {
+        const float wm = (float)w - 1.0f, hm = (float)h - 1.0f;
+        const float ax = rx + gh[0], ay = ry + gh[1], bx = rx + gh[2], by = ry + gh[3];
+        inside = ax >= 0.0f && ax <= wm && ay >= 0.0f && ay <= hm && bx >= 0.0f && bx <= wm && by >= 0.0f && by <= hm;
+        if (inside) ca = fabsf(gm_samp<VEC>(a, h, w, ax, ay) - gm_samp<VEC>(b, h, w, bx, by));
+        const float dvx = (gh[2] - gh[0]) - (f[2] - f[0]), dvy = (gh[3] - gh[1]) - (f[3] - f[1]);
+        maps[2 * n + i] = sqrtf(dvx * dvx + dvy * dvy);
+    }
+    __syncthreads();
+    if (second && valid) maps[n + i] = inside ? ca : cms[cl];
 }
 
 // box_h then box_v of radius r (gm_box.wgsl:8-25) on map channel blockIdx.z of src ([c][hc][wc]) into the same
@@ -2422,7 +2433,8 @@ int fhc::gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t
         }
         const bool v = vec4(4, {a, b, flow});
         const dim3 tiles((p.wc + kGmT - 1) / kGmT, (p.hc + kGmT - 1) / kGmT);
-        hipLaunchKernelGGL(v ? gm_cost_kernel<true> : gm_cost_kernel<false>, tiles, dim3(kThreads), 0, st, in(a), in(b),
+        const dim3 ctiles(tiles.x, (p.hc + 7) / 8);  // the cost kernel's 16 x 8 blocks
+        hipLaunchKernelGGL(v ? gm_cost_kernel<true> : gm_cost_kernel<false>, ctiles, dim3(kThreads), 0, st, in(a), in(b),
                            h, w, in(flow), h8, w8, part[1], coef, raw, p.hc, p.wc);
         // the texture window over the 5 maps (raw -> maps), then the decision window at the cells the select reads
         // (its rows at their columns, its columns at their rows) and the select (maps -> dec, flow)
