@@ -1541,7 +1541,7 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
 // before its in-order additions.
 constexpr uint32_t kGmNwg = gmfit::kNwg, kGmWg = gmfit::kWg;  // gm_fit_reduce's workgroups and their size
 constexpr uint32_t kGmPart = gmfit::kPart;                     // one round's partial sums [workgroup][channel][9]
-constexpr uint32_t kGmT = 16;                 // the cost kernel's block edge and the box tile's, in cells
+constexpr uint32_t kGmT = 16;                 // the box tile's edge and the cost block's width, in cells
 constexpr uint32_t kGmRmax = 32;              // largest box radius: r_dwin = round(16 s), s <= 2
 
 // one fit round (gm_fit_reduce.wgsl:15-44, the round before solved first) for workgroup blockIdx.x of channel
