@@ -53,6 +53,14 @@ __device__ inline void solve_block(const float* part, uint32_t chans, float (*ss
     __syncthreads();
 }
 
+// v of lane l + N for lanes l with l % 16 + N < 16 (a DPP row shift; the other lanes read 0): the tree's last
+// levels, whose lanes that matter (l < N) read lanes below 16
+template <int N>
+__device__ __forceinline__ float row_down(float v) {
+    static_assert(N >= 1 && N <= 8, "a row shift within 16 lanes");
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 | N, 0xf, 0xf, true));
+}
+
 // the LDS a round needs
 struct RoundLds {
     float sh[9][kWg / 2];
@@ -100,7 +108,7 @@ __device__ inline void round_body(const uint16_t* fp, uint32_t cs, uint32_t c0, 
         }
     }
     // the lane tree, pairs (l, l + off) for off = 128 .. 1: the first level through LDS (lanes 128-255 write), the
-    // rest in the first wave
+    // rest in the first wave (offsets 32 and 16 across rows, 8 .. 1 as row shifts)
 #pragma unroll
     for (uint32_t v = 0; v < NV; v++)
         if (lanes[v] >= kWg / 2 && lanes[v] < kWg)
@@ -115,8 +123,12 @@ __device__ inline void round_body(const uint16_t* fp, uint32_t cs, uint32_t c0, 
 #pragma unroll
         for (uint32_t k = 0; k < 9; k++) {
             float v = L.sh[k][t] + L.sh[k][t + 64];
-#pragma unroll
-            for (uint32_t off = 32; off > 0; off >>= 1) v = v + __shfl_down(v, off);
+            v = v + __shfl_down(v, 32);
+            v = v + __shfl_down(v, 16);
+            v = v + row_down<8>(v);
+            v = v + row_down<4>(v);
+            v = v + row_down<2>(v);
+            v = v + row_down<1>(v);
             if (t == 0) part_out[(g * 4 + c) * 9 + k] = v;
         }
     }
