@@ -1732,10 +1732,16 @@ __global__ __launch_bounds__(kThreads) void gm_dwin_h_kernel(const float* tex, f
     hs[t] = acc / (float)span;
 }
 
+// v of lane K of each aligned group of four lanes, in all four (a DPP quad permutation)
+template <int K>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), K * 0x55, 0xf, 0xf, false));
+}
+
 // box_v of hs at the select's rows, then the select (gm_select.wgsl:14-27); dec [5][h8][w8] receives the five values
 // an E8 cell decides on (maps 0-2 after both windows, maps 3-4 after the texture window). Four consecutive lanes per
 // cell: lane m < 3 sums map m's window (its NT loads in one batch), lane 3 loads maps 3-4, and every lane of the
-// four gathers the five values (in-wave shuffles), decides as the select does and stores flow channel m. The lanes
+// four gathers the five values (quad broadcasts), decides as the select does and stores flow channel m. The lanes
 // past the last cell shadow it (in-bounds loads, so that every lane of a wave takes part in the shuffles) and store
 // nothing. items: cells.
 template <uint32_t NT>
@@ -1765,9 +1771,9 @@ __global__ __launch_bounds__(kThreads) void gm_dwin_v_select_kernel(const float*
     } else {
         own = tex[3 * n + idx], own2 = tex[4 * n + idx];
     }
-    const int q = (int)(threadIdx.x % 64 - m);  // the cell's first lane in the wave
-    const float cm = __shfl(own, q), ca = __shfl(own, q + 1), dv = __shfl(own, q + 2);
-    const float lm = __shfl(own, q + 3), l2 = __shfl(own2, q + 3);
+    // lane m of the cell's quad of lanes broadcast to the quad (DPP quad_perm(m, m, m, m))
+    const float cm = quad_lane<0>(own), ca = quad_lane<1>(own), dv = quad_lane<2>(own);
+    const float lm = quad_lane<3>(own), l2 = quad_lane<3>(own2);
     if (!live) return;
     const size_t n8 = (size_t)h8 * w8;
     dec[m * n8 + cell] = own;
