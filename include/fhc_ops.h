@@ -266,8 +266,8 @@ int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, c
  * configuration must be a one-tile configuration of 3 + 3 channel blocks on one wave row (the 48 -> 48 -> 48 FiLM
  * head at 2 or 4 rows per tile); the conv a one-launch direct plan without residual (its workgroups join the fit's
  * where its configuration is the one-row 64-channel kernel-row split, else it runs in its own launch after the
- * repair). level 0 runs the pair, then the conv. Eight launches (seven with the conv joined) where the three take
- * ten. No counterpart in the reference. */
+ * repair). level 0 runs the pair, then the conv. Eight launches (nine when the conv runs on its own) where the
+ * three calls take ten. No counterpart in the reference. */
 struct fhc_conv_plan;
 int fhc_gmhs_film(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
                   uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
