@@ -12,12 +12,14 @@ Alongside (the last stdout line is one compact JSON record; the full record goes
 frame timed alone against its roofline, the dominant one cold; the conv-only step (every conv of pair()+mid(), one
 graph) with per-layer warm/cold time and roofline fraction (each launch captured R times in a graph, median of G
 replays; "cold" rotates buffer sets larger than the 256 MB MALL); the single-layer configurations (3x3 32->32 at
-1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1); the batched workload (the frame's convs over
-8 independent 4K frame pairs with 3 mid() phases each); the sustained MFMA rate; and the CPU baseline: the same frame
-through the oracle (a C restatement of the reference's arithmetic) on the host's cores.
+1080p/8; the 1080p/4 stride-2 ladder; the 1080p/16 deep layer and 1x1); the frame over 8 rotating sets of frames
+and buffers (each replay reading what another wrote, beyond the MALL); the batched workload (8 independent 3840x2160
+RGBA8 frame pairs through the whole graph with 3 mid() phases each, 24 generated frames a step, one HIP graph), and
+its convs alone; the sustained MFMA rate; and the CPU baseline: the same frame through the oracle (a C restatement of
+the reference's arithmetic) on the host's cores.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--no-configs] [--no-batched] [--no-fuse] [--ops]
-    python bench.py --only-frame | --only-ops
+    python bench.py --only-frame | --only-ops | --only-batched
 """
 import argparse
 import json
@@ -358,6 +360,97 @@ def frame_1080p(args, torch, np, stream, t=0.5, repair=1, per_launch=True):
     return res, (be, f, rec)
 
 
+def frame_rotating(args, torch, np, stream, sets=8, t=0.5):
+    """The 1080p frame (frame_1080p's program, repair on) over `sets` independent frame pairs, each with its own
+    buffers and HIP graph, replayed in turn: every replay reads frames and intermediates another replay wrote last
+    (about 70 MB a set, more than the 256 MB MALL over the sets), as a stream of new frame pairs would. Microseconds
+    per frame (wall clock over args.steps replays)."""
+    import flyhighfg_net as fnet
+    W = fnet.make_weights(7)
+    be = fnet.GpuBackend(W, stream=stream, fuse=not args.no_fuse)
+    progs, graphs = [], []
+    with torch.cuda.stream(stream):
+        for k in range(sets):
+            f = fnet.FlyHighFG(be, 864, 480, frame=(1920, 1080), repair=1)
+            be.upload_frames(f.frames, fnet.pair_frames(1920, 1080, 100 + k, shift=16))
+            be.set_g(fnet.film_mlp(W, t))
+            f.pair_mid(t)
+            stream.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                f.pair_mid(t)
+            progs.append(f)
+            graphs.append(g)
+        for i in range(max(args.warmup, sets)):
+            graphs[i % sets].replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            graphs[i % sets].replay()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    del graphs, progs
+    return wall * 1e6 / args.steps
+
+
+def batched_frames(args, torch, np, stream, pairs=8, phases=(0.25, 0.5, 0.75), steps=20, warmup=3):
+    """The batched configuration as written: `pairs` independent 3840x2160 RGBA8 frame pairs (seeded textures, a
+    per-pair translation in [-32, 32] px) resident in HBM -> the downscale to the 864x480 network (the internal size
+    of 2160p) -> every op of pair() (the repair on) -> mid(t) at each of `phases` -> the bicubic render of every
+    in-between frame at 3840x2176 and rgba_out: pairs x phases RGBA8 frames per step. Every conv runs once per layer
+    over the whole batch (16, 8 or 24 images); one HIP graph per step. Random weights (seed 7)."""
+    import flyhighfg_net as fnet
+    W = fnet.make_weights(7)
+    be = fnet.GpuBackend(W, stream=stream, fuse=not args.no_fuse)
+    f = fnet.FlyHighFG(be, 864, 480, frame=(3840, 2160), repair=1, pairs=pairs, mids=len(phases))
+    t0 = time.perf_counter()
+    be.upload_frames(f.frames, np.concatenate([fnet.pair_frames(3840, 2160, p) for p in range(pairs)]))
+    log(f"bench: {pairs} 3840x2160 frame pairs generated in {time.perf_counter() - t0:.1f} s")
+    for j, t in enumerate(phases):
+        be.set_g(f.film_vectors(W, t), j)
+    with torch.cuda.stream(stream):
+        for _ in range(2):  # plans are made on the first run
+            f.run(phases)
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        be.record = []
+        with torch.cuda.graph(g, stream=stream):
+            f.run(phases)
+        rec, be.record = be.record, None
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    step_us, ev_us = wall * 1e6 / steps, e0.elapsed_time(e1) * 1e3 / steps
+    rgba = be.host_frames(f.rgba)
+    ok = bool(np.all(rgba >> 24 == 255)) and all(len(np.unique(rgba[i, ::64, ::64])) > 100 for i in range(len(rgba)))
+    n_out = pairs * len(phases)
+    flops = sum(r["flops"] for r in rec)
+    kinds = {}
+    for r in rec:
+        k = r["label"].split(" ")[0]
+        kinds[k] = kinds.get(k, 0) + r.get("kernels", 1)
+    log(f"bench: batched {pairs} pairs x {len(phases)} phases at 3840x2160: {step_us:.1f} us per step, "
+        f"{n_out / step_us * 1e6:.0f} generated frames/s, {sum(kinds.values())} launches")
+    del g, f
+    return dict(workload=f"{pairs} independent 3840x2160 RGBA8 frame pairs (seeded textures, per-pair translation in "
+                         f"[-32, 32] px) -> downscale to the 864x480 network -> pair() with the repair -> mid(t) at "
+                         f"t = {', '.join(str(t) for t in phases)} -> bicubic render at 3840x2176 + rgba_out: "
+                         f"{n_out} RGBA8 frames per step; every conv batched over the pairs (encoders over both "
+                         "frames) or pairs x phases; one HIP graph; random weights",
+                step_us=round(step_us, 2), event_step_us=round(ev_us, 2),
+                generated_frames_per_s=round(n_out / step_us * 1e6, 1), pairs_per_s=round(pairs / step_us * 1e6, 1),
+                step_tflops=round(flops / step_us / 1e6, 2), launches=sum(kinds.values()), launch_kinds=kinds,
+                steps=steps, output_ok=ok)
+
+
 def render_cold(args, torch, be, f, reps, graphs, cold_bytes, stream):
     """The frame-size render (fhc_render_rgba) over rotating sets of input frames and output frames larger than the
     MALL, so every launch reads its frames from HBM: per-launch microseconds."""
@@ -408,9 +501,9 @@ def cpu_model():
 
 
 def batched_workload(args, torch, np, fhconv, flyhighfg, stream, pairs=8, mids=3):
-    """The batched throughput configuration: the frame's convs over 8 independent frame pairs (3840x2160, network
-    856x480) with 3 mid() phases each, one batched conv (or fused pair) per layer; step time, generated frames per
-    second (3 per pair), and each launch's warm and cold time against its roofline."""
+    """The convs alone of the batched configuration: the frame's convs over 8 independent frame pairs (network
+    856x480) with 3 mid() phases each, one batched conv (or fused pair) per layer; the convs' step time and TFLOP/s,
+    and each launch's warm and cold time against its roofline (the whole configuration is batched_frames)."""
     layers = flyhighfg.batched_layers(pairs, mids)
     net = Net(layers, 3, torch, np, fhconv, tune=not (args.no_autotune or args.tune))
     fused = not args.no_fuse
@@ -444,13 +537,12 @@ def batched_workload(args, torch, np, fhconv, flyhighfg, stream, pairs=8, mids=3
             continue
         log("batched", json.dumps(launches[-1]))
     flops = sum(L.flops for L in layers)
-    log(f"bench: batched ({pairs} pairs x {mids} mids): {step_us:.1f} us per step, "
-        f"{pairs * mids / step_us * 1e6:.0f} generated frames/s, {flops / step_us / 1e6:.1f} TFLOP/s over the step")
-    return dict(workload=f"{pairs} independent 3840x2160 frame pairs (network 856x480), {mids} mid() phases each: "
-                         "pair-stage convs batched over the pairs (encoders over both frames), mid-stage convs over "
-                         "pairs x mids; synthetic inputs, random weights",
-                step_us=round(step_us, 2), generated_frames_per_s=round(pairs * mids / step_us * 1e6, 1),
-                pairs_per_s=round(pairs / step_us * 1e6, 1), step_tflops=round(flops / step_us / 1e6, 2),
+    log(f"bench: batched convs ({pairs} pairs x {mids} mids): {step_us:.1f} us per step of the convs alone, "
+        f"{flops / step_us / 1e6:.1f} TFLOP/s over the step")
+    return dict(workload=f"the convs alone of {pairs} independent frame pairs (network 856x480), {mids} mid() phases "
+                         "each: pair-stage convs batched over the pairs (encoders over both frames), mid-stage convs "
+                         "over pairs x mids; synthetic inputs, random weights",
+                convs_step_us=round(step_us, 2), step_tflops=round(flops / step_us / 1e6, 2),
                 launches=launches, fused_pairs=[f"{a}+{B.name}" for a, (_, B, _, _) in net.pairs.items()],
                 tune_table=fhconv.format_tune().splitlines())
 
@@ -657,6 +749,9 @@ def main():
     ap.add_argument("--no-autotune", action="store_true", help="plan with the heuristic only (no per-shape timing)")
     ap.add_argument("--no-fuse", action="store_true", help="one launch per conv (no fused conv pairs)")
     ap.add_argument("--no-batched", action="store_true", help="skip the batched workload (8 pairs, 3 mids each)")
+    ap.add_argument("--only-batched", action="store_true",
+                    help="only time the batched workload (8 3840x2160 pairs, 3 phases each, every op, one HIP graph) "
+                         "and print it as one JSON line")
     ap.add_argument("--ops", action="store_true", help="also time each network op instance over rotating buffers "
                                                         "(frame and batched shapes)")
     ap.add_argument("--only-ops", action="store_true",
@@ -712,7 +807,13 @@ def main():
             fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
         frame, _ = frame_1080p(args, torch, np, stream)
         frame["no_repair"], _ = frame_1080p(args, torch, np, stream, repair=0, per_launch=False)
+        frame["rotating_us_per_frame"] = round(frame_rotating(args, torch, np, stream), 3)
         print(json.dumps({k: v for k, v in frame.items() if k != "launch_table"}), flush=True)
+        return 0
+    if args.only_batched:
+        if not args.tune:
+            fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
+        print(json.dumps(dict(batched=batched_frames(args, torch, np, stream))), flush=True)
         return 0
     if args.only_ops:
         print(json.dumps(dict(net_ops=net_ops_report(args, torch, flyhighfg, stream, net_w, net_h))), flush=True)
@@ -836,14 +937,17 @@ def main():
     # table's key holds the batch)
     frame, (fbe, fobj, frec) = frame_1080p(args, torch, np, stream)
     frame["no_repair"], _ = frame_1080p(args, torch, np, stream, repair=0, per_launch=False)
+    frame["rotating_us_per_frame"] = round(frame_rotating(args, torch, np, stream), 3)
     log(f"bench: 1080p frame {frame['us_per_frame']:.2f} us ({frame['frames_per_s']:.0f} frames/s), "
         f"{frame['launches']} launches, per-launch sum {frame['launch_us_sum']:.1f} us; without the repair "
-        f"{frame['no_repair']['us_per_frame']:.2f} us")
+        f"{frame['no_repair']['us_per_frame']:.2f} us; over 8 rotating frame sets {frame['rotating_us_per_frame']:.2f} us")
     net_ops = net_ops_report(args, torch, flyhighfg, stream, net_w, net_h) if args.ops else None
 
-    batched = None
+    batched = batched_convs = None
     if not args.no_batched:
-        batched = batched_workload(args, torch, np, fhconv, flyhighfg, stream)
+        batched = batched_frames(args, torch, np, stream)
+        torch.cuda.empty_cache()
+        batched_convs = batched_workload(args, torch, np, fhconv, flyhighfg, stream)
         torch.cuda.empty_cache()
 
     mfma_rate = mfma_rate_probe(torch, fhconv, stream)
@@ -899,7 +1003,8 @@ def main():
         fuse_check=fuse_check, event_ms_per_step=round(ev_ms, 6),
         submit_us_per_step=round(t_submit * 1e6 / args.steps, 3))
     detail = dict(frame=frame, conv_step=conv_step, roofline=roofline, cpu_baseline=cpu, layers=per_layer,
-                  pairs=per_pair, config_layers=cfg_layers, config_pairs=cfg_pairs, batched=batched, net_ops=net_ops,
+                  pairs=per_pair, config_layers=cfg_layers, config_pairs=cfg_pairs, batched=batched,
+                  batched_convs=batched_convs, net_ops=net_ops,
                   tune_table=tune_table)
     return emit(args, frame, conv_step, roofline, cpu, batched, detail)
 
@@ -923,12 +1028,14 @@ def emit(args, frame, conv_step, roofline, cpu, batched, detail):
         config=dict(workload=frame["workload"], frame="1920x1080", network=frame["network"],
                     launches=frame.get("launches"), parallelism="single GPU"),
         frame_without_repair_us=frame.get("no_repair", {}).get("us_per_frame"),
+        frame_rotating_us=frame.get("rotating_us_per_frame"),
         roofline=None if roofline is None else {k: roofline[k] for k in keep_roof if k in roofline},
         cpu_baseline=cpu,
         conv_step=None if conv_step is None else {k: conv_step[k] for k in ("us_per_step", "frames_per_s",
                                                                             "conv_launches", "pair_us", "mid_us")},
         batched=None if batched is None else {k: batched[k] for k in ("step_us", "generated_frames_per_s",
-                                                                      "step_tflops")},
+                                                                      "pairs_per_s", "launches", "output_ok")},
+        batched_convs_step_us=(detail.get("batched_convs") or {}).get("convs_step_us"),
         detail=args.detail or None)
     text = json.dumps(line)
     if len(text) > 4000:

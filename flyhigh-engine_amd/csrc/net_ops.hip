@@ -1440,7 +1440,6 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
                                                                uint32_t iw, OView out, uint32_t oh, uint32_t ow,
                                                                uint32_t tiles_x, uint32_t tiles_y, float sh, float sw) {
     static_assert(EXT <= kAaT * R && LAY >= 0 && LAY <= 2, "the load stripes cover the window");
-    static_assert(kAaT * KM <= kThreads / 2, "a weight table per axis takes half the block");
     using Cell = typename std::conditional<LAY == 0, float4, typename std::conditional<LAY == 1, uint2, float2>::type>::type;
     __shared__ Cell tile[EXT * EXT];
     __shared__ float tileb[LAY == 2 ? EXT * EXT : 1];
@@ -1456,24 +1455,22 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
     const int xlo = max(0, (int)floorf(((float)ox0 + 0.5f) * sw - fsw + 0.5f));
     const int xhi = min((int)iw, (int)floorf(((float)ox_last + 0.5f) * sw + fsw + 0.5f));
     const int ny = max(1, min(yhi - ylo, (int)EXT)), nx = max(1, min(xhi - xlo, (int)EXT));
-    // the tap weights and window indices of the block's 16 columns (first half of the block) and 16 rows (second
-    // half): interp_aa.wgsl's per-tap weight, which depends on the output column (row) alone, once per block
+    // the tap weights and window indices of the block's 16 columns (entries 0 .. kAaT KM - 1) and 16 rows (the next
+    // kAaT KM): interp_aa.wgsl's per-tap weight, which depends on the output column (row) alone, once per block
     tab[tid] = unit_f32(tid << 16, 0);
-    {
-        const bool rows = tid >= kThreads / 2;
-        const uint32_t k = rows ? tid - kThreads / 2 : tid;
-        if (k < kAaT * KM) {
-            const uint32_t o = (rows ? oy0 : ox0) + k / KM;
-            const float sc = rows ? sh : sw, fs = rows ? fsh : fsw;
-            const int n = rows ? (int)ih : (int)iw, lo = rows ? ylo : xlo, nn = rows ? ny : nx;
-            const float c = ((float)o + 0.5f) * sc;
-            const int tmin = max(0, (int)floorf(c - fs + 0.5f)), tmax = min(n, (int)floorf(c + fs + 0.5f));
-            const int tt = tmin + (int)(k % KM);
-            const float wgt = tt < tmax ? fmaxf(0.0f, 1.0f - fabsf(((float)tt + 0.5f - c) / fs)) : 0.0f;
-            const int li = min(max(tt - lo, 0), nn - 1);
-            if (rows) wys[k] = wgt, lrs[k] = li;
-            else wxs[k] = wgt, lcs[k] = li;
-        }
+    for (uint32_t e = tid; e < 2 * kAaT * KM; e += kThreads) {
+        const bool rows = e >= kAaT * KM;
+        const uint32_t k = rows ? e - kAaT * KM : e;
+        const uint32_t o = (rows ? oy0 : ox0) + k / KM;
+        const float sc = rows ? sh : sw, fs = rows ? fsh : fsw;
+        const int n = rows ? (int)ih : (int)iw, lo = rows ? ylo : xlo, nn = rows ? ny : nx;
+        const float c = ((float)o + 0.5f) * sc;
+        const int tmin = max(0, (int)floorf(c - fs + 0.5f)), tmax = min(n, (int)floorf(c + fs + 0.5f));
+        const int tt = tmin + (int)(k % KM);
+        const float wgt = tt < tmax ? fmaxf(0.0f, 1.0f - fabsf(((float)tt + 0.5f - c) / fs)) : 0.0f;
+        const int li = min(max(tt - lo, 0), nn - 1);
+        if (rows) wys[k] = wgt, lrs[k] = li;
+        else wxs[k] = wgt, lcs[k] = li;
     }
     __syncthreads();
     // the frame through a buffer resource: a tap's byte offset is one 24-bit multiply-add
@@ -2325,16 +2322,21 @@ extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_
         if (oh > hp || ow > wp) return fail(-1, "rgba_resize: %u x %u is not a downscale of %u x %u", ow, oh, wp, hp);
         const uint32_t taps = std::max(aa_taps(hp, oh), aa_taps(wp, ow));
         const uint32_t ext = std::max(aa_tile_extent(hp, oh), aa_tile_extent(wp, ow));
-        if (taps > 8 || ext > 5 * kAaT)
-            return fail(-1, "rgba_resize: %u x %u -> %u x %u needs %u taps, a %u-pixel tile window (at most 8 and %u)",
-                        wp, hp, ow, oh, taps, ext, 5 * kAaT);
+        if (taps > 10 || ext > 84)
+            return fail(-1, "rgba_resize: %u x %u -> %u x %u needs %u taps, a %u-pixel tile window (at most 10 and 84)",
+                        wp, hp, ow, oh, taps, ext);
         const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
-        // the 40-pixel window covers the common downscales (1080p to 864 x 480: 39 x 38)
+        // the 40-pixel window covers the common downscales (1080p to 864 x 480: 39 x 38); 2160p to 864 x 480 takes
+        // 10 taps and a 78 x 76 window (4096 x 2176: 81 columns); the 84 x 84 window of 8-byte cells keeps the
+        // workgroup's LDS under 64 KiB
         auto k = ext <= 40 && taps <= 5 ? rgba_resize_kernel<5, 3, 40, 2>
                  : ext <= 3 * kAaT
                      ? (taps <= 5 ? rgba_resize_kernel<5, 3, 48, 2> : taps <= 6 ? rgba_resize_kernel<6, 3, 48, 2>
                                                                     : rgba_resize_kernel<8, 3, 48, 2>)
-                     : (taps <= 6 ? rgba_resize_kernel<6, 5, 80, 1> : rgba_resize_kernel<8, 5, 80, 1>);
+                 : ext <= 5 * kAaT
+                     ? (taps <= 6 ? rgba_resize_kernel<6, 5, 80, 1> : taps <= 8 ? rgba_resize_kernel<8, 5, 80, 1>
+                                                                    : rgba_resize_kernel<10, 5, 80, 1>)
+                     : rgba_resize_kernel<10, 6, 84, 1>;
         if ((uint64_t)pitch * 4 >= (1u << 24) || (uint64_t)h * pitch * 4 >= (1u << 31))
             return fail(-1, "rgba_resize: frames of pitch %u and %u rows are too large", pitch, h);
         hipLaunchKernelGGL(k, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream,
@@ -2358,13 +2360,13 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
         FHC_TRY(check_frames("render_rgba a", a, 1, w, h, pitch, 0, hp, wp));
         FHC_TRY(check_frames("render_rgba b", b, 1, w, h, pitch, 0, hp, wp));
         FHC_TRY(check_frames("render_rgba out", out, 1, w, h, opitch, 0, hp, wp));
+        FHC_TRY(check(flow, "render_rgba flow", 4, false));
+        FHC_TRY(check(vis, "render_rgba vis", 3, true));
+        FHC_TRY(check(rt, "render_rgba rt", 3, false));
         // the tap rows' 32-bit byte offsets (24-bit row multiply) and the quarter maps' buffer sizes
         if ((uint64_t)pitch * 4 >= (1u << 24) || (uint64_t)h * pitch * 4 >= (1u << 31) ||
             (uint64_t)hq * wq * std::max(16u, 2 * rt->cstride) >= (1u << 31) || hq >= (1u << 24) || wq >= (1u << 24))
             return fail(-1, "render_rgba: frame (pitch %u, %u rows) or quarter maps (%u x %u) too large", pitch, h, wq, hq);
-        FHC_TRY(check(flow, "render_rgba flow", 4, false));
-        FHC_TRY(check(vis, "render_rgba vis", 3, true));
-        FHC_TRY(check(rt, "render_rgba rt", 3, false));
         const bool qv = flow->p == vis->p && flow->cstride == 8 && vis->cstride == 8 && flow->c0 == 0 &&
                         vis->c0 == 4 && reinterpret_cast<uintptr_t>(flow->p) % 16 == 0 && vec4(4, {rt});
         if ((uint64_t)h * w >= kMaxItems || h > 4u * 65535u)

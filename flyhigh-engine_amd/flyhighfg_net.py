@@ -219,7 +219,8 @@ class GpuBackend(ComposedChains):
         self.W, self.fuse, self.dev, self.chains = W, fuse, device, chains
         self.stream = stream if stream is not None else torch.cuda.current_stream()
         self.plans: Dict[tuple, object] = {}
-        self.g = None
+        self.gs: Dict[int, object] = {}  # FiLM vector slots (one per phase of a batched program)
+        self.g_slot = 0
         self.record = None
 
     def _go(self, label, fn, nbytes, flops=0, kind="op", kernels=1):
@@ -251,11 +252,20 @@ class GpuBackend(ComposedChains):
         self.torch.cuda.synchronize()
         return buf.cpu().numpy().view(np.uint16)
 
-    def set_g(self, g_bits):
-        if self.g is None:
-            self.g = self.upload(g_bits)
+    def set_g(self, g_bits, slot: int = 0):
+        """The FiLM vector of slot `slot` (f16 bits [96]); a slot keeps its device buffer, so a captured program
+        reads whatever was last written to it."""
+        if slot not in self.gs:
+            self.gs[slot] = self.upload(g_bits)
         else:
-            self.g.copy_(self.torch.from_numpy(np.ascontiguousarray(g_bits).view(np.int16)))
+            self.gs[slot].copy_(self.torch.from_numpy(np.ascontiguousarray(g_bits).view(np.int16)))
+
+    def use_g(self, slot: int):
+        self.g_slot = slot
+
+    @property
+    def g(self):
+        return self.gs[self.g_slot]
 
     def _v(self, v: V):
         return self.fh.View(v.buf, v.c0, v.scale)
@@ -276,7 +286,7 @@ class GpuBackend(ComposedChains):
                                      r_c0=res.c0 if res is not None else 0)
 
     def _conv_plan(self, name, x: V, y: V, res: Optional[V] = None):
-        key = ("conv", name, x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0,
+        key = ("conv", name, x.buf.shape[0], x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0,
                None if res is None else res.buf.data_ptr())
         p = self.plans.get(key)
         if p is None:
@@ -297,7 +307,7 @@ class GpuBackend(ComposedChains):
             self.conv(a, x, mid)
             self.conv(b, mid, y, mid if res_mid else None)
             return
-        key = ("pair", a, b, x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0)
+        key = ("pair", a, b, x.buf.shape[0], x.buf.data_ptr(), x.c0, y.buf.data_ptr(), y.c0)
         p = self.plans.get(key)
         if p is None:
             da = self._desc(a, x, mid, None)
@@ -319,7 +329,7 @@ class GpuBackend(ComposedChains):
     def pair_affine_out(self, a, b, x: V, mid: V, y: V, out: V, c: int):
         if not (self.chains and self.fuse) or CONVS[b][1] != c:
             return super().pair_affine_out(a, b, x, mid, y, out, c)
-        key = ("pair_affine_out", a, b, x.buf.data_ptr(), x.c0, out.buf.data_ptr(), out.c0)
+        key = ("pair_affine_out", a, b, x.buf.shape[0], x.buf.data_ptr(), x.c0, out.buf.data_ptr(), out.c0)
         p = self.plans.get(key)
         if p is None:
             da = self._desc(a, x, mid, None)
@@ -341,7 +351,7 @@ class GpuBackend(ComposedChains):
         """The FiLM pair's plan (film_modulate in a, b's staging), or False where there is none."""
         if not (self.chains and self.fuse) or CONVS[a][0] != c or h.scale != 1.0:
             return False
-        key = ("film_pair", a, b, h.buf.data_ptr(), h.c0, y.buf.data_ptr(), y.c0)
+        key = ("film_pair", a, b, h.buf.shape[0], h.buf.data_ptr(), h.c0, y.buf.data_ptr(), y.c0)
         p = self.plans.get(key)
         if p is None:
             da = self._desc(a, h, mid, None)
@@ -388,7 +398,8 @@ class GpuBackend(ComposedChains):
     def conv_siblings(self, a, b, x: V, ya: V, res_a: Optional[V], yb: V):
         if not (self.chains and self.fuse):
             return super().conv_siblings(a, b, x, ya, res_a, yb)
-        key = ("siblings", a, b, x.buf.data_ptr(), x.c0, ya.buf.data_ptr(), ya.c0, yb.buf.data_ptr(), yb.c0)
+        key = ("siblings", a, b, x.buf.shape[0], x.buf.data_ptr(), x.c0, ya.buf.data_ptr(), ya.c0, yb.buf.data_ptr(),
+               yb.c0)
         p = self.plans.get(key)
         if p is None:
             da, db = self._desc(a, x, ya, res_a), self._desc(b, x, yb, None)
@@ -597,17 +608,32 @@ class GpuBackend(ComposedChains):
                  2 * self._px(flow) * (6 + 4 + 3 + 14))
 
 
+def sl(buf, i: int, n: int = 1):
+    """Images i .. i + n - 1 of a buffer (a view of the same memory on either backend)."""
+    return buf[i:i + n]
+
+
 class FlyHighFG:
-    """The buffers of one frame pair at network size net_w x net_h and the program of pair() and mid(t) over them.
+    """The buffers of frame pairs at network size net_w x net_h and the program of pair() and mid(t) over them.
     Outputs after mid(): ``out`` (render_pix, the in-between picture), ``up7`` (flow_tq channels 0-3, vis_tq 4-6,
     quarter size), ``Rt`` (R_t, 3 channels), ``state_out`` (f16b then flow16, 1/16 size); ``o`` holds the coarse head
     (conf, gate, sal in channels 7-11). cubic / render_flags: render_pix's sampler (the model's manifest asks for
     bicubic, models/flyhighfg.json:67) and mode word (0: neither the decisive blend nor the still test, the
-    engine's defaults, options.rs:306-327)."""
+    engine's defaults, options.rs:306-327).
+
+    pairs P independent frame pairs and mids M phases per pair run as one batch: the reference's sessions of one
+    pair each, side by side. The pictures of pair p are images 2p (A) and 2p + 1 (B) of the A/B buffers, so each
+    pair's A and B are one contiguous batch of 2, as every op chain of one pair takes them; the pair stage's one-image
+    tensors hold pair p at image p, and the mid stage's hold phase j of pair p at image j * P + p (each phase's P
+    images contiguous). Every conv runs once per layer over the whole batch (2P, P or M * P images); the op chains
+    of one pair run per pair, those of one phase per phase. P = M = 1 is the reference's single session."""
 
     def __init__(self, be, net_w: int = 864, net_h: int = 480, cubic: bool = True, render_flags: int = 0,
-                 frame: Optional[tuple] = None, repair: int = 1):
+                 frame: Optional[tuple] = None, repair: int = 1, pairs: int = 1, mids: int = 1):
         self.be = be
+        self.P, self.M = P, M = int(pairs), int(mids)
+        if P < 1 or M < 1:
+            raise ValueError("pairs and mids must be at least 1")
         # repair: the periodic-structure repair's level (gmhs.rs; 0 off, 1 the engine's default, options.rs:305,
         # 2 aggressive), run on the E8 flow at the end of pair() (net/build.rs:640-660)
         self.repair = repair
@@ -621,12 +647,12 @@ class FlyHighFG:
             fw, fh = frame
             self.hp, self.wp = (fh + 31) // 32 * 32, (fw + 31) // 32 * 32
             self.internal = (self.wp, self.hp) != (net_w, net_h)
-            self.frames = be.frames(2, fh, fw)     # A, B: RGBA8 words
-            self.rgba = be.frames(1, fh, fw)       # the generated frame
+            self.frames = be.frames(2 * P, fh, fw)  # A, B of each pair: RGBA8 words
+            self.rgba = be.frames(M * P, fh, fw)     # the generated frames, phase-major
             # the composed chains' full-size intermediates (rgba_in's pictures, the render's f16 picture); the fused
             # GPU chains never touch them
             composed = not getattr(be, "chains", False)
-            self.full = be.zeros(2, self.hp, self.wp, 4) if composed else None
+            self.full = be.zeros(2 * P, self.hp, self.wp, 4) if composed else None
             self.pic = be.zeros(1, self.hp, self.wp, 4) if composed and self.internal else None
             # the flow's scale per axis at the frame size: ftq.scale * wp / iwp (net/build.rs:720), in f32
             self.fsx = float(np.float32(self.wp) / np.float32(net_w))
@@ -635,45 +661,48 @@ class FlyHighFG:
         e8h, e8w = (qh - 1) // 2 + 1, (qw - 1) // 2 + 1
         e16h, e16w = (e8h - 1) // 2 + 1, (e8w - 1) // 2 + 1
         self.shape = dict(net=(net_h, net_w), q=(qh, qw), e8=(e8h, e8w), e16=(e16h, e16w))
-        Z = be.zeros
-        self.AB = Z(2, net_h, net_w, 4)        # the inputs A, B at network size (BGR in [0, 1]), 8-byte pixels
-        self.aq = Z(2, qh, qw, 8)              # aq, bq
-        self.e1 = Z(2, e8h, e8w, 40)           # a_e1, b_e1
-        self.f8 = Z(2, e8h, e8w, 40)           # f8a, f8b
-        self.e3 = Z(2, e16h, e16w, 72)         # a_e3, b_e3
-        self.f16 = Z(2, e16h, e16w, 72)        # f16a, f16b (then folded into the concat)
-        self.i8 = Z(2, e8h, e8w, 8)            # i8a, i8b
-        self.cin = Z(1, e16h, e16w, 280)       # f16a 0 | f16b 72 | img16 144 | side 150 | state 154 | cv 230
-        self.l16 = Z(1, e16h, e16w, 2)         # la | lb
-        self.ch1, self.ch2, self.ch3r, self.hc = (Z(1, e16h, e16w, 96) for _ in range(4))
-        self.o = Z(1, e16h, e16w, 16)          # coarse head: flow 0-3, vis 4-6, conf, gate, sal
-        self.fv = Z(1, e8h, e8w, 8)            # flow 0-3 | vis 4-6 (the fine loop updates both in one add)
-        self.state_out = Z(1, e16h, e16w, 80)  # f16b 0 | flow16 72
-        self.fx = Z(1, e8h, e8w, 160)          # wa 0 | wb 36 | ia 72 | ib 75 | flow8 78 | h 82 | fcv 130
-        self.l8 = Z(1, e8h, e8w, 2)            # fla | flb
-        self.fr1, self.fr2, self.h = (Z(1, e8h, e8w, 48) for _ in range(3))
-        self.lin = Z(1, e8h, e8w, 8)           # linf | linb
-        self.hm, self.fh1, self.fh2 = (Z(1, e8h, e8w, 48) for _ in range(3))
-        self.dfilm = Z(1, e8h, e8w, 8)         # d_flow 0-3, d_mask 4
-        self.dvis = Z(1, e8h, e8w, 8)          # d_mask | -d_mask | 0
-        self.ftvt = Z(1, e8h, e8w, 8)          # flow_t 0-3 | vis_t 4-6
-        self.wt36 = Z(1, e8h, e8w, 40)
-        self.up7 = Z(1, qh, qw, 8)             # flow_tq 0-3 | vis_tq 4-6
-        self.blend = Z(1, qh, qw, 8)
-        self.rx = Z(1, qh, qw, 16)             # rwa 0 | rwb 3 | vis_tq 6 | flow_tq20 9 | lg 13
-        self.rq1, self.rq2, self.rq3 = (Z(1, qh, qw, 24) for _ in range(3))
-        self.rr, self.Rt = Z(1, qh, qw, 8), Z(1, qh, qw, 8)
-        self.out = Z(1, net_h, net_w, 4)        # render_pix: the in-between picture at network size
+        Z, AB, PP, MP = be.zeros, 2 * P, P, M * P
+        # the A/B stage: image 2p is pair p's A, 2p + 1 its B
+        self.AB = Z(AB, net_h, net_w, 4)        # the inputs A, B at network size (BGR in [0, 1]), 8-byte pixels
+        self.aq = Z(AB, qh, qw, 8)              # aq, bq
+        self.e1 = Z(AB, e8h, e8w, 40)           # a_e1, b_e1
+        self.f8 = Z(AB, e8h, e8w, 40)           # f8a, f8b
+        self.e3 = Z(AB, e16h, e16w, 72)         # a_e3, b_e3
+        self.f16 = Z(AB, e16h, e16w, 72)        # f16a, f16b (then folded into the concat)
+        self.i8 = Z(AB, e8h, e8w, 8)            # i8a, i8b
+        # the pair stage: image p is pair p
+        self.cin = Z(PP, e16h, e16w, 280)       # f16a 0 | f16b 72 | img16 144 | side 150 | state 154 | cv 230
+        self.l16 = Z(PP, e16h, e16w, 2)         # la | lb
+        self.ch1, self.ch2, self.ch3r, self.hc = (Z(PP, e16h, e16w, 96) for _ in range(4))
+        self.o = Z(PP, e16h, e16w, 16)          # coarse head: flow 0-3, vis 4-6, conf, gate, sal
+        self.fv = Z(PP, e8h, e8w, 8)            # flow 0-3 | vis 4-6 (the fine loop updates both in one add)
+        self.state_out = Z(PP, e16h, e16w, 80)  # f16b 0 | flow16 72
+        self.fx = Z(PP, e8h, e8w, 160)          # wa 0 | wb 36 | ia 72 | ib 75 | flow8 78 | h 82 | fcv 130
+        self.l8 = Z(PP, e8h, e8w, 2)            # fla | flb
+        self.fr1, self.fr2, self.h = (Z(PP, e8h, e8w, 48) for _ in range(3))
+        self.wt36 = Z(PP, e8h, e8w, 40)
+        # the mid stage: image j * P + p is phase j of pair p
+        self.lin = Z(MP, e8h, e8w, 8)           # linf | linb
+        self.hm, self.fh1, self.fh2 = (Z(MP, e8h, e8w, 48) for _ in range(3))
+        self.dfilm = Z(MP, e8h, e8w, 8)         # d_flow 0-3, d_mask 4
+        self.dvis = Z(MP, e8h, e8w, 8)          # d_mask | -d_mask | 0
+        self.ftvt = Z(MP, e8h, e8w, 8)          # flow_t 0-3 | vis_t 4-6
+        self.up7 = Z(MP, qh, qw, 8)             # flow_tq 0-3 | vis_tq 4-6
+        self.blend = Z(MP, qh, qw, 8)
+        self.rx = Z(MP, qh, qw, 16)             # rwa 0 | rwb 3 | vis_tq 6 | flow_tq20 9 | lg 13
+        self.rq1, self.rq2, self.rq3 = (Z(MP, qh, qw, 24) for _ in range(3))
+        self.rr, self.Rt = Z(MP, qh, qw, 8), Z(MP, qh, qw, 8)
+        self.out = Z(MP, net_h, net_w, 4)        # render_pix: the in-between picture at network size
         self.cubic, self.render_flags = cubic, render_flags
         # the padded frame width the repair's windows scale with (the network's own without a frame)
         self.full_w = self.wp if frame is not None else net_w
 
     def pair(self, cofilm: bool = False) -> bool:
-        """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1), and op 62 (up.w, which reads only h).
-        cofilm: also the next mid(t)'s FiLM head (ops 50-53: it reads only h and the FiLM vector of t, which must be
-        in place), inside the repair's first two launches; returns whether it ran (mid(t, film_done=True) then skips
-        it)."""
-        be, S = self.be, self.shape
+        """pair(): models/graph.json ops 0-43 (the fine loop once, K = 1), and op 62 (up.w, which reads only h), for
+        every pair. cofilm: also the next mid(t)'s FiLM head (ops 50-53: it reads only h and the FiLM vector of t,
+        which must be in place), inside the repair's first two launches (one pair, one phase); returns whether it ran
+        (mid(t, film_done=True) then skips it)."""
+        be, S, P = self.be, self.shape, self.P
         (qh, qw), (e8h, e8w) = S["q"], S["e8"]
         if self.frame is not None:  # the frames -> A, B (rgba_in; in the internal-size mode, the downscale)
             nh, nw = S["net"]
@@ -681,13 +710,17 @@ class FlyHighFG:
                 be.frame_input(self.frames, self.full, V(self.AB), self.hp, self.wp, nh, nw)
             else:
                 be.rgba_in(self.frames, V(self.AB), nh, nw)
-        be.pair_input(V(self.AB), V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16), qh, qw)  # 0-1, 14-24
+        for p in range(P):                                                                    # 0-1, 14-24
+            be.pair_input(V(sl(self.AB, 2 * p, 2)), V(sl(self.aq, 2 * p, 2)), V(sl(self.i8, 2 * p, 2)),
+                          V(sl(self.cin, p), 144), V(sl(self.l16, p)), qh, qw)
         be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)                 # 2-4, 8-10
         be.pair("enc.e3", "enc.e4", V(self.f8), V(self.e3), V(self.f16), True)                # 5-7, 11-13
         # 26, 43: f16a f16b into the concat and the state, beside the 1/16 lumas' cost volume (25, 26; 19-20 zeros),
         # which reads and writes nothing the encoders touch
-        be.fold_pair_sad(V(self.f16), 72, V(self.cin, 0), V(self.state_out, 0), V(self.l16, 0), V(self.l16, 1),
-                         V(self.cin, 230), 3)
+        for p in range(P):
+            cin, l16 = sl(self.cin, p), sl(self.l16, p)
+            be.fold_pair_sad(V(sl(self.f16, 2 * p, 2)), 72, V(cin, 0), V(sl(self.state_out, p), 0), V(l16, 0),
+                             V(l16, 1), V(cin, 230), 3)
         be.conv("coarse.c1", V(self.cin), V(self.ch1))                                        # 27
         be.conv("coarse.c2", V(self.ch1), V(self.ch2))                                        # 28
         be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30
@@ -695,8 +728,10 @@ class FlyHighFG:
         be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
         # 33-40 (43: flow16), then the fine loop's input, K = 1 (op 42: wa .. flow8); h enters as zeros (op 41: the
         # fx slice is never written)
-        be.coarse_fine_input(V(self.o), V(self.fv), V(self.state_out, 72), 16.0, V(self.f8), V(self.i8), 0.125,
-                             V(self.fx), V(self.l8), 36)
+        for p in range(P):
+            be.coarse_fine_input(V(sl(self.o, p)), V(sl(self.fv, p)), V(sl(self.state_out, p), 72), 16.0,
+                                 V(sl(self.f8, 2 * p, 2)), V(sl(self.i8, 2 * p, 2)), 0.125, V(sl(self.fx, p)),
+                                 V(sl(self.l8, p)), 36)
         be.sad(V(self.l8, 0), V(self.l8, 1), V(self.fx, 130), 2)                              # fcv
         be.conv("fine.r1", V(self.fx), V(self.fr1))
         be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
@@ -705,66 +740,137 @@ class FlyHighFG:
         # up.w (graph op 62, mid's first conv) reads only h, so it runs here beside fine.out, which reads h too: one
         # launch, and a pair() followed by several mid(t) computes it once
         be.conv_siblings("fine.out", "up.w", V(self.h), V(self.fv), V(self.fv), V(self.wt36))
-        if self.repair and cofilm:  # the repair, with mid's FiLM pair in its first launch (pair_mid())
+        if self.repair and cofilm and P == 1 and self.M == 1:  # the repair, with mid's FiLM pair in its first launch
             be.gmhs_film(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair,
                          "film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2), "film.out",
                          V(self.dfilm))
             return True
-        if self.repair:  # the periodic-structure repair of the pair's flow, in place (gmhs.rs:149-206)
-            be.gmhs(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.fv), self.full_w, self.repair)
+        if self.repair:  # the periodic-structure repair of each pair's flow, in place (gmhs.rs:149-206)
+            for p in range(P):
+                be.gmhs(V(sl(self.AB, 2 * p)), V(sl(self.AB, 2 * p + 1)), V(sl(self.fv, p)), self.full_w,
+                        self.repair)
         return False
 
     def pair_mid(self, t: float, W: Optional[dict] = None):
         """pair() then mid(t), the FiLM head of t run inside the repair's first two launches (two launches fewer).
         With W None the FiLM vector of t must already be in place, as for mid()."""
         if W is not None:
-            self.be.set_g(film_mlp(W, t))
+            self.be.set_g(self.film_vectors(W, t))
         self.mid(t, None, film_done=self.pair(cofilm=True))
 
+    def film_vectors(self, W: dict, t: float) -> np.ndarray:
+        """The FiLM vector of t once per pair (f16 bits [P * 96]): the FiLM ops take one vector per image."""
+        return np.tile(film_mlp(W, t), self.P)
+
     def mid(self, t: float, W: Optional[dict], film_done: bool = False):
-        """mid(t): models/graph.json ops 44-82 but 62 (up.w, run by pair()), render_pix included. With W None the
-        FiLM vector of t must already be in place (be.set_g(film_mlp(W, t))): a program captured in a HIP graph takes
-        it that way, as the reference rewrites its t-dependent buffers before a replay (net/build.rs:16-22).
-        film_done: the FiLM head (ops 50-53) already ran with this t's vector (pair(cofilm=True))."""
-        be = self.be
+        """mid(t): models/graph.json ops 44-82 but 62 (up.w, run by pair()), render_pix included, for every pair (one
+        phase). With W None the FiLM vectors of t must already be in place (be.set_g(self.film_vectors(W, t))): a
+        program captured in a HIP graph takes them that way, as the reference rewrites its t-dependent buffers before
+        a replay (net/build.rs:16-22). film_done: the FiLM head (ops 50-53) already ran with this t's vector
+        (pair(cofilm=True))."""
+        if self.M != 1:
+            raise ValueError("mid(t) runs one phase: a program of several phases runs them with mids()")
         if W is not None:
-            be.set_g(film_mlp(W, t))                                                          # 49
+            self.be.set_g(self.film_vectors(W, t))                                            # 49
+        self._mid_phase(0, t, film_done)
+        self._mid_tail()
+
+    def mids(self, ts, W: Optional[dict] = None):
+        """mid(t) for each of the M phases ts of every pair: each phase's FiLM head, flow_t / vis_t and refine input
+        with that phase's FiLM vectors (slot j of the backend's vectors: be.set_g(self.film_vectors(W, t), j), set
+        here when W is given), then the refine head over all M * P images at once and the renders."""
+        ts = tuple(ts)
+        if len(ts) != self.M:
+            raise ValueError(f"{len(ts)} phases for a program of {self.M}")
+        if W is not None:
+            for j, t in enumerate(ts):
+                self.be.set_g(self.film_vectors(W, t), j)
+        for j, t in enumerate(ts):
+            self._mid_phase(j, t, False)
+        self._mid_tail()
+
+    def run(self, ts, W: Optional[dict] = None):
+        """pair() and mids(ts): the whole batched step (P pairs, M phases each)."""
+        if self.P == 1 and self.M == 1:
+            return self.pair_mid(ts[0], W)
+        if W is not None:
+            for j, t in enumerate(ts):
+                self.be.set_g(self.film_vectors(W, t), j)
+        self.pair()
+        self.mids(ts)
+
+    def _mid_phase(self, j: int, t: float, film_done: bool):
+        """ops 44-61, 63-76 of phase j (FiLM vector slot j) for every pair."""
+        be, P = self.be, self.P
+        m = lambda b: sl(b, j * P, P)  # noqa: E731  phase j's images
+        be.use_g(j)
         if not film_done:
-            be.film_pair("film.h1", "film.h2", V(self.h), 48, V(self.hm), V(self.fh1), V(self.fh2))  # 50-52
-            be.conv("film.out", V(self.fh2), V(self.dfilm))                                   # 53
-        be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(self.dfilm), t, V(self.up7), V(self.ftvt), V(self.lin),
-                             V(self.dvis))                                                    # 44-48, 54-62
-        be.refine_input(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend))  # 63-76
+            be.film_pair("film.h1", "film.h2", V(self.h), 48, V(m(self.hm)), V(m(self.fh1)), V(m(self.fh2)))  # 50-52
+            be.conv("film.out", V(m(self.fh2)), V(m(self.dfilm)))                             # 53
+        be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(m(self.dfilm)), t, V(m(self.up7)), V(m(self.ftvt)),
+                             V(m(self.lin)), V(m(self.dvis)))                                 # 44-48, 54-62
+        for p in range(P):                                                                    # 63-76
+            i = j * P + p
+            be.refine_input(V(sl(self.aq, 2 * p, 2)), V(sl(self.up7, i), 0, 0.25), V(sl(self.up7, i), 4),
+                            V(sl(self.rx, i)), 0.05, V(sl(self.blend, i)))
+
+    def _mid_tail(self):
+        """ops 77-82 for all M * P images: the refine head at once, then each image's render."""
+        be, P = self.be, self.P
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
         be.pair_affine_out("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), V(self.Rt), 3)  # 79-81
-        if self.frame is not None and self.internal:  # the render at the frame size, to the RGBA8 frame
-            be.frame_render(self.frames, self.full, self.pic, V(self.up7, 0), V(self.up7, 4), V(self.Rt), self.rgba,
-                            self.hp, self.wp, self.fsx, self.fsy, self.cubic, self.render_flags)
-            return
-        be.render(V(be.image(self.AB, 0)), V(be.image(self.AB, 1)), V(self.up7, 0), V(self.up7, 4), V(self.Rt),
-                  V(self.out), self.cubic, self.render_flags)                                 # 82: render_pix
-        if self.frame is not None:
-            be.rgba_out(V(self.out), self.rgba)
+        for i in range(self.M * P):
+            p = i % P
+            up7, rt = sl(self.up7, i), sl(self.Rt, i)
+            if self.frame is not None and self.internal:  # the render at the frame size, to the RGBA8 frame
+                be.frame_render(sl(self.frames, 2 * p, 2), None if self.full is None else sl(self.full, 2 * p, 2),
+                                self.pic, V(up7, 0), V(up7, 4), V(rt), sl(self.rgba, i), self.hp, self.wp, self.fsx,
+                                self.fsy, self.cubic, self.render_flags)
+                continue
+            out = sl(self.out, i)
+            be.render(V(sl(self.AB, 2 * p)), V(sl(self.AB, 2 * p + 1)), V(up7, 0), V(up7, 4), V(rt), V(out),
+                      self.cubic, self.render_flags)                                          # 82: render_pix
+            if self.frame is not None:
+                be.rgba_out(V(out), sl(self.rgba, i))
 
 
 def cpu_threads():
     return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
-def procedural_frame(w: int, h: int, dx: int = 0, dy: int = 0) -> np.ndarray:
+def procedural_frame(w: int, h: int, dx: int = 0, dy: int = 0, seed: int = 0) -> np.ndarray:
     """A synthetic RGBA8 frame (h, w) of uint32 words, the kind the reference's bench generates
     (crates/flyhigh-cli/src/cli/bench.rs:33-51): smooth sine patterns per channel plus 0.1 of hashed noise, the
-    whole picture shifted by (dx, dy) pixels, alpha 255. Test and benchmark data only."""
-    yy, xx = np.mgrid[0:h, 0:w].astype(np.int64)
-    sx, sy = xx + dx, yy + dy
-    hsh = ((sx * 73856093) & 0xFFFFFFFF) ^ ((sy * 19349663) & 0xFFFFFFFF)
-    n = (((hsh * 2654435761) & 0xFFFFFFFF) >> 24).astype(np.float32) / np.float32(255.0)
+    whole picture shifted by (dx, dy) pixels, alpha 255. seed 0 is that picture; another seed shifts the patterns'
+    phases and salts the noise hash, a texture of its own. Test and benchmark data only."""
+    if seed:
+        rng = np.random.default_rng(seed)
+        ph = rng.uniform(0.0, 2.0 * np.pi, 3).astype(np.float32)
+        salt = np.uint32(rng.integers(1, 1 << 32))
+    else:
+        ph, salt = np.zeros(3, np.float32), np.uint32(0)
+    # a row of columns and a column of rows, broadcast: every pixel's value comes from the same f32 operations as
+    # over full grids
+    sx = np.arange(w, dtype=np.int64)[None, :] + dx
+    sy = np.arange(h, dtype=np.int64)[:, None] + dy
+    # the hash in wrapping 32-bit arithmetic (equal to the 64-bit products masked to 32 bits)
+    ux, uy = (sx & 0xFFFFFFFF).astype(np.uint32), (sy & 0xFFFFFFFF).astype(np.uint32)
+    with np.errstate(over="ignore"):
+        hsh = (ux * np.uint32(73856093)) ^ (uy * np.uint32(19349663)) ^ salt
+        n = ((hsh * np.uint32(2654435761)) >> np.uint32(24)).astype(np.float32) / np.float32(255.0)
     fx, fy = sx.astype(np.float32), sy.astype(np.float32)
-    r = 0.5 + 0.35 * np.sin(fx * 0.013) * np.cos(fy * 0.017) + 0.1 * n
-    g = 0.5 + 0.35 * np.cos(fx * 0.009 + 1.0) * np.sin(fy * 0.021) + 0.1 * n
-    b = 0.5 + 0.35 * np.sin((fx + fy) * 0.011) + 0.1 * n
+    r = 0.5 + 0.35 * np.sin(fx * 0.013 + ph[0]) * np.cos(fy * 0.017) + 0.1 * n
+    g = 0.5 + 0.35 * np.cos(fx * 0.009 + 1.0 + ph[1]) * np.sin(fy * 0.021) + 0.1 * n
+    b = 0.5 + 0.35 * np.sin((fx + fy) * 0.011 + ph[2]) + 0.1 * n
     byte = lambda v: (np.clip(v, 0.0, 1.0) * 255.0).astype(np.uint32)  # noqa: E731
     return (byte(r) | (byte(g) << 8) | (byte(b) << 16) | np.uint32(0xFF000000)).astype(np.uint32)
+
+
+def pair_frames(w: int, h: int, seed: int, shift: int = 32) -> np.ndarray:
+    """Frame pair `seed` of the batched workload, (2, h, w) RGBA8 words: a seeded texture (procedural_frame with
+    seed + 1) and the same moved by a translation drawn uniformly from [-shift, shift] pixels per axis."""
+    dx, dy = (int(v) for v in np.random.default_rng(1000 + seed).integers(-shift, shift + 1, 2))
+    return np.stack([procedural_frame(w, h, 0, 0, seed + 1), procedural_frame(w, h, dx, dy, seed + 1)])
 
 
 def conv_layer(weight_name: str) -> str:

@@ -313,11 +313,12 @@ static float bil_at(const fho_view* v, uint32_t h, uint32_t w, uint32_t ch, floa
 }
 static float clampf01(float v) { return fminf(fmaxf(v, 0.0f), 1.0f); }
 
-void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, const fho_view* vis, const fho_view* rt,
-                const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx, float fsy,
-                int cubic, uint32_t flags) {
+/* rows y0 .. y1 - 1 of the render; every output pixel is independent of the others */
+void fho_render_rows(const fho_view* a, const fho_view* b, const fho_view* flow, const fho_view* vis,
+                     const fho_view* rt, const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq,
+                     float fsx, float fsy, int cubic, uint32_t flags, uint32_t y0_, uint32_t y1_) {
     const float sh = (float)hq / (float)h, sw = (float)wq / (float)w;
-    for (uint32_t y = 0; y < h; y++)
+    for (uint32_t y = y0_; y < y1_ && y < h; y++)
         for (uint32_t x = 0; x < w; x++) {
             const float iy = ((float)y + 0.5f) * sh - 0.5f, ix = ((float)x + 0.5f) * sw - 0.5f;
             const int qy0 = (int)floorf(iy), qx0 = (int)floorf(ix);
@@ -371,6 +372,12 @@ void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, cons
                 wr(out, h, w, 0, y, x, c, clampf01(mixed * (1.0f - stillw) + own[c] * stillw));
             }
         }
+}
+
+void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, const fho_view* vis, const fho_view* rt,
+                const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx, float fsy,
+                int cubic, uint32_t flags) {
+    fho_render_rows(a, b, flow, vis, rt, out, h, w, hq, wq, fsx, fsy, cubic, flags, 0, h);
 }
 
 /* shaders/rgba_in.wgsl:11-19 (the planar output [3][hp][wp] written as channels 0-2 of an NHWC view) */

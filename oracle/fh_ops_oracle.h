@@ -70,6 +70,10 @@ void fho_chcopy(const fho_view* x, const fho_view* out, uint32_t n, uint32_t h, 
 void fho_render(const fho_view* a, const fho_view* b, const fho_view* flow, const fho_view* vis, const fho_view* rt,
                 const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq, float fsx, float fsy,
                 int cubic, uint32_t flags);
+/* rows y0 .. y1 - 1 of fho_render's output (the rows are independent: bands on threads give fho_render's result) */
+void fho_render_rows(const fho_view* a, const fho_view* b, const fho_view* flow, const fho_view* vis,
+                     const fho_view* rt, const fho_view* out, uint32_t h, uint32_t w, uint32_t hq, uint32_t wq,
+                     float fsx, float fsy, int cubic, uint32_t flags, uint32_t y0, uint32_t y1);
 
 /* rgba_in: n RGBA8 frames (R | G << 8 | B << 16 | A << 24 per 32-bit word, rows `pitch` words apart, frame i at
  * rgba + i * fstride words) -> BGR f16(byte / 255), replicate-padded to hp x wp, channels 0-2 of out:

@@ -18,7 +18,7 @@ from flyhighfg_net import CONVS, ComposedChains, cpu_threads  # noqa: E402
 
 class CpuBackend(ComposedChains):
     def __init__(self, W):
-        self.W, self.threads, self.g = W, cpu_threads(), None
+        self.W, self.threads, self.gs, self.g_slot = W, cpu_threads(), {}, 0
 
     def zeros(self, n, h, w, cs):
         return np.zeros((n, h, w, cs), np.uint16)
@@ -41,8 +41,15 @@ class CpuBackend(ComposedChains):
     def host(self, buf):
         return buf
 
-    def set_g(self, g_bits):
-        self.g = np.asarray(g_bits, np.uint16).reshape(1, -1)
+    def set_g(self, g_bits, slot=0):
+        self.gs[slot] = np.asarray(g_bits, np.uint16).reshape(-1, 96)  # one FiLM vector per image
+
+    def use_g(self, slot):
+        self.g_slot = slot
+
+    @property
+    def g(self):
+        return self.gs[self.g_slot]
 
     @staticmethod
     def _put(out, c, y):
@@ -105,7 +112,7 @@ class CpuBackend(ComposedChains):
                                         a_c0=a.c0, b_c0=b.c0, flow_c0=flow.c0,
                                         fsx=flow.scale if fsx is None else fsx,
                                         fsy=flow.scale if fsy is None else fsy,
-                                        vis_c0=vis.c0, vis_scale=vis.scale, rt_c0=rt.c0))
+                                        vis_c0=vis.c0, vis_scale=vis.scale, rt_c0=rt.c0, threads=self.threads))
 
     def gmhs(self, a, b, flow, full_w, level):
         out, _, _ = oracle.gmhs(a.buf, b.buf, flow.buf, full_w, level, a_c0=a.c0, b_c0=b.c0, flow_c0=flow.c0)

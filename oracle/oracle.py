@@ -155,6 +155,7 @@ def _ops_lib():
             "fho_unary": [V, V, U, U, U, U, I, ctypes.c_float, ctypes.c_float],
             "fho_chcopy": [V, V, U, U, U, U],
             "fho_render": [V, V, V, V, V, V, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U],
+            "fho_render_rows": [V, V, V, V, V, V, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U, U, U],
             "fho_rgba_in": [ctypes.c_void_p, U, U, U, U, ctypes.c_uint64, V, U, U],
             "fho_rgba_out": [V, U, U, U, ctypes.c_void_p, U, U, U, ctypes.c_uint64],
             "fho_gm_params": [U, U, U, U, ctypes.POINTER(FhoGmPar)],
@@ -267,12 +268,22 @@ def chcopy(x, c, c0=0, scale=1.0):
 
 
 def render(a, b, flow, vis, rt, hq, wq, cubic=True, flags=0, a_c0=0, b_c0=0, flow_c0=0, fsx=1.0, fsy=1.0, vis_c0=0,
-           vis_scale=1.0, rt_c0=0):
-    """a, b: (1, h, w, cs) pictures; flow, vis, rt: (1, hq, wq, cs) quarter-size maps; returns (1, h, w, 3)."""
+           vis_scale=1.0, rt_c0=0, threads=0):
+    """a, b: (1, h, w, cs) pictures; flow, vis, rt: (1, hq, wq, cs) quarter-size maps; returns (1, h, w, 3).
+    threads > 1: bands of rows on that many threads (the same result)."""
     _, h, w, _ = a.shape
     y = _out(1, h, w, 3)
-    _ops_lib().fho_render(_view(a, a_c0), _view(b, b_c0), _view(flow, flow_c0), _view(vis, vis_c0, vis_scale),
-                          _view(rt, rt_c0), _view(y), h, w, hq, wq, fsx, fsy, int(cubic), flags)
+    args = (_view(a, a_c0), _view(b, b_c0), _view(flow, flow_c0), _view(vis, vis_c0, vis_scale), _view(rt, rt_c0),
+            _view(y), h, w, hq, wq, fsx, fsy, int(cubic), flags)
+    nt = min(threads or 1, max(1, h // 16))
+    if nt <= 1:
+        _ops_lib().fho_render(*args)
+        return y
+    # bands of rows on threads (the foreign call releases the GIL); each output pixel is computed alone
+    from concurrent.futures import ThreadPoolExecutor
+    step = (h + nt - 1) // nt
+    with ThreadPoolExecutor(nt) as ex:
+        list(ex.map(lambda y0: _ops_lib().fho_render_rows(*args, y0, min(h, y0 + step)), range(0, h, step)))
     return y
 
 

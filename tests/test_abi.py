@@ -211,6 +211,17 @@ def test_network_ops_reject_bad_views_before_any_launch():
          "fold_pair_sad sad out"),
         ("fhc_fold_pair_sad", (_tv(cs=8), _tv(cs=12), None, 4, 4, 8, _tv(), _tv(), _tv(cs=32), 1, 4, 4, 2, None),
          "fold_pair_sad out"),
+        # the frame input: at most 10 taps (2160p to 432 x 240 takes 19) and an 84-pixel window; frames present
+        ("fhc_rgba_resize", (0x1000, 1, 3840, 2160, 3840, 0, 2176, 3840, _tv(), 240, 432, None), "needs 19 taps"),
+        ("fhc_rgba_resize", (None, 1, 3840, 2160, 3840, 0, 2176, 3840, _tv(), 480, 864, None), "null frame"),
+        ("fhc_rgba_resize", (0x1000, 1, 3840, 2160, 3840, 0, 2176, 3840, _tv(cs=8), 480, 864, None), "8-byte"),
+        # the frame render: every map view is checked before any of it is read
+        ("fhc_render_rgba", (0x1000, 0x2000, 64, 32, 64, 32, 64, _tv(cs=8), _tv(cs=8, c0=4), None, 8, 16,
+                             ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, None), "render_rgba rt"),
+        ("fhc_render_rgba", (0x1000, 0x2000, 64, 32, 64, 32, 64, None, _tv(cs=8, c0=4), _tv(), 8, 16,
+                             ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, None), "render_rgba flow"),
+        ("fhc_render_rgba", (0x1000, None, 64, 32, 64, 32, 64, _tv(cs=8), _tv(cs=8, c0=4), _tv(), 8, 16,
+                             ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, None), "null frame"),
     ]
     for name, args, msg in cases:
         rc = getattr(L, name)(*args)

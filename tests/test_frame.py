@@ -87,6 +87,51 @@ def test_program_runs_from_frames_in_both_modes():
     assert np.array_equal(internal.AB[..., 3], np.zeros_like(internal.AB[..., 3]))
 
 
+PAIR_TENSORS = [("cin", 279), ("o", 12), ("fv", 7), ("h", 48), ("state_out", 76), ("wt36", 36)]
+MID_TENSORS = [("up7", 7), ("Rt", 3), ("dfilm", 5), ("rx", 14)]
+
+
+def run_batch(be, W, net_w, net_h, frs, ts, repair=1):
+    """P frame pairs (a list of (2, h, w) RGBA8 arrays) and the phases ts as one batched program."""
+    h, w = frs[0].shape[1:]
+    f = net.FlyHighFG(be, net_w, net_h, frame=(w, h), repair=repair, pairs=len(frs), mids=len(ts))
+    be.upload_frames(f.frames, np.concatenate(frs))
+    f.run(ts, W)
+    return f
+
+
+def compare_batch_to_single(be_of, W, net_w, net_h, frs, ts, repair, pairs_checked, exact):
+    """Each pair p (in pairs_checked) of the batched program against pair() then mid(t) of that pair alone (per
+    phase), on the backends be_of() makes; exact: bit for bit, else the conv path's bar."""
+    bb = be_of()
+    big = run_batch(bb, W, net_w, net_h, frs, ts, repair)
+    P = len(frs)
+    for p in pairs_checked:
+        for j, t in enumerate(ts):
+            sb = be_of()
+            one = run_batch(sb, W, net_w, net_h, [frs[p]], (t,), repair)
+            names = [(n, c, p) for n, c in PAIR_TENSORS] + [(n, c, j * P + p) for n, c in MID_TENSORS]
+            for name, c, i in names:
+                g = bb.host(getattr(big, name))[i:i + 1, ..., :c]
+                r = sb.host(getattr(one, name))[..., :c]
+                if exact:
+                    assert np.array_equal(g, r), (name, p, t)
+                else:
+                    g64, r64 = g.view(np.float16).astype(np.float64), r.view(np.float16).astype(np.float64)
+                    assert np.abs(g64 - r64).max() <= 1e-2 * np.abs(r64).max(), (name, p, t)
+            gr, rr = bb.host_frames(big.rgba)[j * P + p], sb.host_frames(one.rgba)[0]
+            assert np.array_equal(gr, rr), ("rgba", p, t)
+
+
+def test_batched_program_equals_single_pairs_on_the_oracle_backend():
+    """Batch independence: P = 2 pairs with M = 2 phases as one program (A/B interleaved per pair, phase-major mid
+    images, every conv over the whole batch), from RGBA8 frames in the internal-size mode with the repair on,
+    equals each pair's own pair() + mid(t) bit for bit."""
+    W = net.make_weights(8)
+    frs = [net.pair_frames(300, 150, s, shift=6) for s in (0, 1)]
+    compare_batch_to_single(lambda: CpuBackend(W), W, 128, 64, frs, (0.25, 0.75), 1, (0, 1), True)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("net_w,net_h,fuse", [(256, 128, True), (256, 128, False), (864, 480, True)])
 def test_gpu_frame_matches_the_oracle_composition(net_w, net_h, fuse):
@@ -104,6 +149,14 @@ def test_gpu_frame_matches_the_oracle_composition(net_w, net_h, fuse):
         err, tol = np.abs(g - r).max(), 1e-2 * np.abs(r).max()
         print(f"  {name}: max|diff| {err:.3g} (bar {tol:.3g}, max|ref| {np.abs(r).max():.3g})", flush=True)
         assert err <= tol, name
+
+
+def _byte_diff(g, r):
+    """The largest difference of the 4 bytes of each RGBA8 word, per pixel."""
+    diff = np.zeros(g.shape, np.int32)
+    for sh in (0, 8, 16, 24):
+        diff = np.maximum(diff, np.abs(((g >> sh) & 0xFF).astype(np.int32) - ((r >> sh) & 0xFF).astype(np.int32)))
+    return diff
 
 
 def _check_frame(gb, got, ref):
@@ -161,6 +214,97 @@ def test_gpu_1080p_frame_repair_on_the_gpus_own_flow():
           flush=True)
     assert f.full_w == 1920
     assert np.array_equal(after, want)
+
+
+C5_PHASES = (0.25, 0.5, 0.75)
+
+
+def _c5_frames(pairs=8):
+    return [net.pair_frames(3840, 2160, p) for p in range(pairs)]
+
+
+@pytest.mark.gpu
+def test_gpu_batched_4k_pairs_match_the_oracle_composition():
+    """The batched workload as written: 8 independent 3840 x 2160 RGBA8 pairs (seeded textures, per-pair translation
+    in [-32, 32] px), the 864 x 480 network (the internal size of 2160p, tests/defaults.rs:12 with the padding to 32),
+    3 mid() phases per pair, as one program: every conv once per layer over the batch (16, 8 or 24 images), the
+    frame-size render of all 24 in-between frames at 3840 x 2176. Pairs 0 and 7 against the oracle composition of
+    that pair alone (the repair off, as in the 1080p comparison): the pair stage's tensors and each phase's maps to
+    the conv path's bar; each generated 8-bit frame against the oracle's render (rgba_in, render_pix, rgba_out) of
+    the GPU's own maps, bytes within 1 (expf's last bit) and almost all identical. End to end, the frames differ
+    more than at 1080p: a flow within the bar moves by up to ~0.2 network pixels, 4.44 times that at 2160p, over a
+    texture whose hashed noise steps by up to 25 levels between neighbouring pixels (pair 0: 0.05-0.13% of the pixels
+    beyond the 8-bit bar of 1e-2 * 255 plus one step, mean 0.55); there the test keeps a sanity bound, at most 1%
+    beyond that bar and a mean within one step: the pins are the network's tensors and the render of its maps."""
+    import torch
+    print("batched 8 x 3840x2160 pairs, 3 phases", flush=True)
+    W = net.make_weights(11)
+    frs = _c5_frames()
+    gb = net.GpuBackend(W, stream=torch.cuda.current_stream())
+    got = run_batch(gb, W, 864, 480, frs, C5_PHASES, repair=0)
+    torch.cuda.synchronize()
+    assert got.internal and (got.wp, got.hp) == (3840, 2176) and got.rgba.shape == (24, 2160, 3840)
+    P = got.P
+    for p in (0, 7):
+        print(f" pair {p} against the oracle", flush=True)
+        ref = run_batch(CpuBackend(W), W, 864, 480, [frs[p]], C5_PHASES, repair=0)
+        checks = [("AB", 3, 2 * p, 2, 0), ("cin", 279, p, 1, 0), ("o", 12, p, 1, 0), ("h", 48, p, 1, 0),
+                  ("state_out", 76, p, 1, 0)]
+        checks += [(n, c, j * P + p, 1, j) for j in range(len(C5_PHASES)) for n, c in (("up7", 7), ("Rt", 3))]
+        for name, c, i, k, j in checks:
+            g = gb.host(getattr(got, name))[i:i + k, ..., :c].view(np.float16).astype(np.float64)
+            r = getattr(ref, name)[j:j + k, ..., :c].view(np.float16).astype(np.float64)
+            err, tol = np.abs(g - r).max(), 1e-2 * np.abs(r).max()
+            print(f"  {name}[{i}]: max|diff| {err:.3g} (bar {tol:.3g})", flush=True)
+            assert err <= tol, (name, p)
+        for j in range(len(C5_PHASES)):
+            i = j * P + p
+            g = gb.host_frames(got.rgba)[i]
+            # the render stage alone: the oracle's render of the GPU's maps
+            up7, rt = gb.host(net.sl(got.up7, i)).copy(), gb.host(net.sl(got.Rt, i)).copy()
+            cb = CpuBackend(W)
+            own = np.zeros((1,) + g.shape, np.uint32)
+            cb.frame_render(frs[p], cb.zeros(2, got.hp, got.wp, 4), cb.zeros(1, got.hp, got.wp, 4), net.V(up7, 0),
+                            net.V(up7, 4), net.V(rt), own, got.hp, got.wp, got.fsx, got.fsy, got.cubic,
+                            got.render_flags)
+            d_own, d_end = _byte_diff(g, own[0]), _byte_diff(g, ref.rgba[j])
+            beyond = np.mean(d_end > int(1e-2 * 255) + 1)
+            print(f"  rgba[{i}]: render of its own maps: max byte diff {d_own.max()}, {np.mean(d_own == 0):.5f} "
+                  f"identical; end to end: max {d_end.max()}, mean {d_end.mean():.4f}, {beyond:.2e} beyond the bar",
+                  flush=True)
+            assert d_own.max() <= 1 and np.mean(d_own == 0) >= 0.999, (p, j)
+            assert beyond <= 1e-2 and d_end.mean() <= 1.0, (p, j)
+
+
+@pytest.mark.gpu
+def test_gpu_batched_4k_repair_on_the_gpus_own_flow():
+    """The repair of the batched workload (level 1, the padded frame width 3840): after the GPU's batched pair() with
+    the repair off, the stage run on pair p's pictures and flow rewrites the flow exactly as the oracle's stage does
+    from the same inputs (pairs 0 and 7), and the batched pair() with the repair on leaves every pair's flow as that
+    (all 8 pairs)."""
+    import torch
+    import oracle
+    print("batched 8 x 3840x2160 pairs, repair", flush=True)
+    W = net.make_weights(11)
+    frs = _c5_frames()
+    gb = net.GpuBackend(W, stream=torch.cuda.current_stream())
+    f = net.FlyHighFG(gb, 864, 480, frame=(3840, 2160), repair=0, pairs=8, mids=3)
+    gb.upload_frames(f.frames, np.concatenate(frs))
+    f.pair()
+    torch.cuda.synchronize()
+    ab, before = gb.host(f.AB).copy(), gb.host(f.fv).copy()
+    for p in range(8):
+        gb.gmhs(net.V(net.sl(f.AB, 2 * p)), net.V(net.sl(f.AB, 2 * p + 1)), net.V(net.sl(f.fv, p)), f.full_w, 1)
+    after = gb.host(f.fv).copy()
+    assert f.full_w == 3840
+    for p in (0, 7):
+        want, _, _ = oracle.gmhs(ab[2 * p:2 * p + 1], ab[2 * p + 1:2 * p + 2], before[p:p + 1], f.full_w, 1)
+        print(f"  pair {p}: cells repaired {int((want != before[p:p + 1]).any(-1).sum())}", flush=True)
+        assert np.array_equal(after[p:p + 1], want), p
+    g = net.FlyHighFG(gb, 864, 480, frame=(3840, 2160), repair=1, pairs=8, mids=3)
+    gb.upload_frames(g.frames, np.concatenate(frs))
+    g.pair()
+    assert np.array_equal(gb.host(g.fv), after)
 
 
 @pytest.mark.gpu

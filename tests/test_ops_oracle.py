@@ -303,6 +303,20 @@ def test_render_warp_matches_torch_grid_sample(cubic):
     assert np.allclose(got, want, atol=2e-3)
 
 
+@pytest.mark.parametrize("cubic", [False, True])
+def test_render_in_row_bands_on_threads_equals_one_pass(cubic):
+    """The render's row bands (each output pixel computed alone) on several threads give the one-pass result bit for
+    bit, bands of unequal length and random maps included."""
+    h, w, hq, wq = 150, 44, 37, 11
+    a, b = f16(rng.uniform(0, 1, (1, h, w, 3))), f16(rng.uniform(0, 1, (1, h, w, 3)))
+    fl, vis, rt = f16(rng.uniform(-3, 3, (1, hq, wq, 4))), f16(rng.uniform(-2, 2, (1, hq, wq, 3))), \
+        f16(rng.uniform(-0.1, 0.1, (1, hq, wq, 3)))
+    one = oracle.render(a, b, fl, vis, rt, hq, wq, cubic=cubic, fsx=1.5, fsy=0.75)
+    for threads in (2, 3, 7):
+        assert np.array_equal(oracle.render(a, b, fl, vis, rt, hq, wq, cubic=cubic, fsx=1.5, fsy=0.75,
+                                            threads=threads), one)
+
+
 def test_render_visibility_picks_the_dominant_picture_and_clamps():
     h, w = 8, 8
     a, b = f16(np.full((1, h, w, 3), 0.25, np.float32)), f16(np.full((1, h, w, 3), 0.75, np.float32))

@@ -49,11 +49,19 @@ def test_noalloc_without_scratch_and_beyond_its_limit():
     say("noalloc without scratch")
     plan, y_ws, y_na = _run_both(c, 0)
     assert plan.workspace_bytes == 0 and np.array_equal(y_ws, y_na)
-    # a split-K plan whose partials exceed the static array: refused before any launch
+    # a split-K plan whose partials exceed the static array: refused before any launch, on real input and output
+    # buffers of the plan's shape (the output keeps its sentinel: nothing ran)
+    import torch
     big = Case(1, 272, 480, 128, 128, act=1, seed=34)
     plan = fhconv.ConvPlan(big.fhc_desc(ksplit=4), big.wt, big.bias, big.slope)
     limit = 64 << 20
     say("noalloc beyond the limit:", plan.workspace_bytes, "bytes")
     assert plan.workspace_bytes > limit
-    rc = fhconv.load().fhc_conv_run_noalloc(plan.handle, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None)
+    dev = torch.device("cuda", 0)
+    x = torch.zeros((1, 272, 480, 128), dtype=torch.int16, device=dev)
+    y = torch.full((1, 272, 480, 128), 0x7E00, dtype=torch.int16, device=dev)
+    rc = fhconv.load().fhc_conv_run_noalloc(plan.handle, ctypes.c_void_p(x.data_ptr()),
+                                            ctypes.c_void_p(y.data_ptr()), None, None)
     assert rc < 0 and "static scratch" in fhconv.last_error()
+    torch.cuda.synchronize()
+    assert bool((y == 0x7E00).all())
