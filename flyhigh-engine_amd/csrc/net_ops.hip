@@ -1199,16 +1199,56 @@ __device__ __forceinline__ float unit_tab(const float* tab, uint32_t v, int ch) 
     return tab[(v >> (16 - 8 * ch)) & 0xffu];
 }
 
+// a * b + c: one fused multiply-add (one rounding) with FMA, else the product rounded, then the sum
+template <bool FMA>
+__device__ __forceinline__ float mac(float a, float b, float c) {
+    if constexpr (FMA) return __builtin_fmaf(a, b, c);
+    else return a * b + c;
+}
+// bil4 and the Keys weights in the same expression order, each product feeding a sum fused with it when FMA
+template <bool FMA>
+__device__ __forceinline__ float bil4m(float v00, float v01, float v10, float v11, float fx, float fy) {
+    if constexpr (!FMA) return bil4(v00, v01, v10, v11, fx, fy);
+    const float gx = 1.0f - fx;
+    return mac<true>(mac<true>(v11, fx, v10 * gx), fy, mac<true>(v01, fx, v00 * gx) * (1.0f - fy));
+}
+template <bool FMA>
+__device__ __forceinline__ float cub1m(float x) {
+    if constexpr (!FMA) return cub1(x);
+    return mac<true>(mac<true>(1.25f, x, -2.25f) * x, x, 1.0f);
+}
+template <bool FMA>
+__device__ __forceinline__ float cub2m(float x) {
+    if constexpr (!FMA) return cub2(x);
+    return mac<true>(mac<true>(mac<true>(-0.75f, x, 3.75f), x, -6.0f), x, 3.0f);
+}
+
+// Channel c of the bicubic sum over the 4 x 4 taps t (rows j, columns i) with the weights cx, cy (render.wgsl:
+// 37-46): each row's four products summed in order, the rows times cy summed in order
+template <bool FMA>
+__device__ __forceinline__ float cubic_sum(const uint32_t (&t)[4][4], const float (&cx)[4], const float (&cy)[4],
+                                           const float* tab, int c) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float row = unit_tab(tab, t[j][0], c) * cx[0];
+#pragma unroll
+        for (int i = 1; i < 4; i++) row = mac<FMA>(unit_tab(tab, t[j][i], c), cx[i], row);
+        acc = j == 0 ? row * cy[0] : mac<FMA>(row, cy[j], acc);
+    }
+    return acc;
+}
+
 // The three channels of one render.wgsl sample (bicubic: :20-47, bilinear: :9-18) of an RGBA8 frame at the sample
 // point (px + tx, py + ty), px, py = floor of its coordinates, each tap converted as rgba_in converts it. INNER: the
 // columns px - 1 .. px + 2 (bicubic) or px, px + 1 (bilinear) all lie inside the frame for every lane of the wave,
 // so one 16- (8-) byte load per row holds the taps in order; otherwise each tap column is clamped to the frame.
-template <bool CUBIC, bool INNER>
+template <bool CUBIC, bool INNER, bool FMA = false>
 __device__ __forceinline__ void sample_rgba(const uint32_t* src, uint32_t pitch, uint32_t w, uint32_t h, int px,
                                             int py, float tx, float ty, const float* tab, float (&o)[3]) {
     if constexpr (CUBIC) {
-        const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
-        const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+        const float cx[4] = {cub2m<FMA>(tx + 1.0f), cub1m<FMA>(tx), cub1m<FMA>(1.0f - tx), cub2m<FMA>(2.0f - tx)};
+        const float cy[4] = {cub2m<FMA>(ty + 1.0f), cub1m<FMA>(ty), cub1m<FMA>(1.0f - ty), cub2m<FMA>(2.0f - ty)};
         uint32_t t[4][4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -1221,16 +1261,7 @@ __device__ __forceinline__ void sample_rgba(const uint32_t* src, uint32_t pitch,
             }
         }
 #pragma unroll
-        for (int c = 0; c < 3; c++) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float row = unit_tab(tab, t[j][0], c) * cx[0] + unit_tab(tab, t[j][1], c) * cx[1] +
-                                  unit_tab(tab, t[j][2], c) * cx[2] + unit_tab(tab, t[j][3], c) * cx[3];
-                acc = j == 0 ? row * cy[0] : acc + row * cy[j];
-            }
-            o[c] = acc;
-        }
+        for (int c = 0; c < 3; c++) o[c] = cubic_sum<FMA>(t, cx, cy, tab, c);
     } else {
         uint32_t t0[2], t1[2];
         const uint32_t ya = (uint32_t)clampi(py, 0, (int)h - 1), yb = (uint32_t)clampi(py + 1, 0, (int)h - 1);
@@ -1244,8 +1275,8 @@ __device__ __forceinline__ void sample_rgba(const uint32_t* src, uint32_t pitch,
         }
 #pragma unroll
         for (int c = 0; c < 3; c++)
-            o[c] = bil4(unit_tab(tab, t0[0], c), unit_tab(tab, t0[1], c), unit_tab(tab, t1[0], c),
-                        unit_tab(tab, t1[1], c), tx, ty);
+            o[c] = bil4m<FMA>(unit_tab(tab, t0[0], c), unit_tab(tab, t0[1], c), unit_tab(tab, t1[0], c),
+                              unit_tab(tab, t1[1], c), tx, ty);
     }
 }
 
@@ -1258,12 +1289,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uin
 // sample_rgba's INNER case (every tap column inside the frame for the whole wave) through a buffer resource over
 // the frame: row y's taps at byte offset y * pitch4 + 4 (px - 1) (bicubic) or y * pitch4 + 4 px (bilinear); the same
 // taps, the same arithmetic.
-template <bool CUBIC>
+template <bool CUBIC, bool FMA>
 __device__ __forceinline__ void sample_rgba_inner(__amdgpu_buffer_rsrc_t rs, uint32_t pitch4, int hm1, int px, int py,
                                                   float tx, float ty, const float* tab, float (&o)[3]) {
     if constexpr (CUBIC) {
-        const float cx[4] = {cub2(tx + 1.0f), cub1(tx), cub1(1.0f - tx), cub2(2.0f - tx)};
-        const float cy[4] = {cub2(ty + 1.0f), cub1(ty), cub1(1.0f - ty), cub2(2.0f - ty)};
+        const float cx[4] = {cub2m<FMA>(tx + 1.0f), cub1m<FMA>(tx), cub1m<FMA>(1.0f - tx), cub2m<FMA>(2.0f - tx)};
+        const float cy[4] = {cub2m<FMA>(ty + 1.0f), cub1m<FMA>(ty), cub1m<FMA>(1.0f - ty), cub2m<FMA>(2.0f - ty)};
         const uint32_t col4 = (uint32_t)(px - 1) * 4u;
         uint32_t t[4][4];
 #pragma unroll
@@ -1273,16 +1304,7 @@ __device__ __forceinline__ void sample_rgba_inner(__amdgpu_buffer_rsrc_t rs, uin
             t[j][0] = q.x, t[j][1] = q.y, t[j][2] = q.z, t[j][3] = q.w;
         }
 #pragma unroll
-        for (int c = 0; c < 3; c++) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float row = unit_tab(tab, t[j][0], c) * cx[0] + unit_tab(tab, t[j][1], c) * cx[1] +
-                                  unit_tab(tab, t[j][2], c) * cx[2] + unit_tab(tab, t[j][3], c) * cx[3];
-                acc = j == 0 ? row * cy[0] : acc + row * cy[j];
-            }
-            o[c] = acc;
-        }
+        for (int c = 0; c < 3; c++) o[c] = cubic_sum<FMA>(t, cx, cy, tab, c);
     } else {
         const uint32_t col4 = (uint32_t)px * 4u;
         const uint32_t ya = (uint32_t)min(max(py, 0), hm1), yb = (uint32_t)min(max(py + 1, 0), hm1);
@@ -1290,14 +1312,14 @@ __device__ __forceinline__ void sample_rgba_inner(__amdgpu_buffer_rsrc_t rs, uin
         const uint2 q1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, __umul24(yb, pitch4) + col4, 0, 0));
 #pragma unroll
         for (int c = 0; c < 3; c++)
-            o[c] = bil4(unit_tab(tab, q0.x, c), unit_tab(tab, q0.y, c), unit_tab(tab, q1.x, c), unit_tab(tab, q1.y, c), tx,
-                        ty);
+            o[c] = bil4m<FMA>(unit_tab(tab, q0.x, c), unit_tab(tab, q0.y, c), unit_tab(tab, q1.x, c),
+                              unit_tab(tab, q1.y, c), tx, ty);
     }
 }
 
 // One frame pixel of render_rgba from its upsampled flow f (x, y for A, then for B, in frame pixels), visibility
 // logits v and residual r: the blend weights, A and B sampled at the displaced positions, the blend, rgba_out.
-template <bool CUBIC, bool FL>
+template <bool CUBIC, bool FL, bool FMA>
 __device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const float (&f)[4], const float (&v)[3],
                                                const float (&r)[3], const uint32_t* fa, const uint32_t* fb, uint32_t w,
                                                uint32_t h, uint32_t pitch, const float* tab, uint32_t flags,
@@ -1313,11 +1335,11 @@ __device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const flo
     const bool inner = pxa >= lo && pxa <= hi && pxb >= lo && pxb <= hi;
     if (__all(inner)) {
         const uint32_t fbytes = ((h - 1) * pitch + w) * 4u, pitch4 = pitch * 4u;
-        sample_rgba_inner<CUBIC>(buf_rsrc(fa, fbytes), pitch4, (int)h - 1, pxa, pya, txa, tya, tab, ca);
-        sample_rgba_inner<CUBIC>(buf_rsrc(fb, fbytes), pitch4, (int)h - 1, pxb, pyb, txb, tyb, tab, cb);
+        sample_rgba_inner<CUBIC, FMA>(buf_rsrc(fa, fbytes), pitch4, (int)h - 1, pxa, pya, txa, tya, tab, ca);
+        sample_rgba_inner<CUBIC, FMA>(buf_rsrc(fb, fbytes), pitch4, (int)h - 1, pxb, pyb, txb, tyb, tab, cb);
     } else {
-        sample_rgba<CUBIC, false>(fa, pitch, w, h, pxa, pya, txa, tya, tab, ca);
-        sample_rgba<CUBIC, false>(fb, pitch, w, h, pxb, pyb, txb, tyb, tab, cb);
+        sample_rgba<CUBIC, false, FMA>(fa, pitch, w, h, pxa, pya, txa, tya, tab, ca);
+        sample_rgba<CUBIC, false, FMA>(fb, pitch, w, h, pxb, pyb, txb, tyb, tab, cb);
     }
     float bwa = wa_w, bwb = wb_w, rk = 1.0f, stillw = 0.0f, own[3] = {0.0f, 0.0f, 0.0f};
     const float third = 1.0f / 3.0f;
@@ -1355,10 +1377,10 @@ __device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const flo
 #pragma unroll
     for (int c = 0; c < 3; c++) {
         if constexpr (FL) {
-            const float mixed = ca[c] * bwa + cb[c] * bwb + r[c] * rk;
-            bytes[c] = byte_of(f2h(fminf(fmaxf(mixed * (1.0f - stillw) + own[c] * stillw, 0.0f), 1.0f)));
+            const float mixed = mac<FMA>(r[c], rk, mac<FMA>(cb[c], bwb, ca[c] * bwa));
+            bytes[c] = byte_of(f2h(fminf(fmaxf(mac<FMA>(own[c], stillw, mixed * (1.0f - stillw)), 0.0f), 1.0f)));
         } else {
-            bytes[c] = byte_of(f2h(fminf(fmaxf(ca[c] * bwa + cb[c] * bwb + r[c], 0.0f), 1.0f)));
+            bytes[c] = byte_of(f2h(fminf(fmaxf(mac<FMA>(cb[c], bwb, ca[c] * bwa) + r[c], 0.0f), 1.0f)));
         }
     }
     dst[(size_t)y * opitch + x] = bytes[2] | (bytes[1] << 8) | (bytes[0] << 16) | 0xff000000u;
@@ -1373,7 +1395,7 @@ __device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const flo
 // quotients the reference forms per pixel). FL: flags may be nonzero. Without flags (the engine's default) stillw = 0
 // and rk = 1, so r * rk is r and mixed * (1 - stillw) + own * stillw is mixed (or +0 for a mixed of -0, which the
 // clamp and the byte conversion turn into the same byte 0): that variant leaves those terms out.
-template <bool CUBIC, bool QV, bool FL>
+template <bool CUBIC, bool QV, bool FL, bool FMA>
 __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
                                                                uint32_t h, uint32_t pitch, float sh, float sw,
                                                                View fl, View vis, View rt, uint32_t hq, uint32_t wq,
@@ -1415,13 +1437,13 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
     float f[4], v[3], r[3];
 #pragma unroll
     for (uint32_t c = 0; c < 4; c++)
-        f[c] = bil4(fq[0][c], fq[1][c], fq[2][c], fq[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
+        f[c] = bil4m<FMA>(fq[0][c], fq[1][c], fq[2][c], fq[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
 #pragma unroll
     for (uint32_t c = 0; c < 3; c++) {
-        v[c] = bil4(vq[0][c], vq[1][c], vq[2][c], vq[3][c], qfx, qfy) * vis.scale;
-        r[c] = bil4(rq[0][c], rq[1][c], rq[2][c], rq[3][c], qfx, qfy);
+        v[c] = bil4m<FMA>(vq[0][c], vq[1][c], vq[2][c], vq[3][c], qfx, qfy) * vis.scale;
+        r[c] = bil4m<FMA>(rq[0][c], rq[1][c], rq[2][c], rq[3][c], qfx, qfy);
     }
-    render_rgba_px<CUBIC, FL>(x, y, f, v, r, fa, fb, w, h, pitch, tab, flags, dst, opitch);
+    render_rgba_px<CUBIC, FL, FMA>(x, y, f, v, r, fa, fb, w, h, pitch, tab, flags, dst, opitch);
 }
 
 // The antialiased resize of n padded RGBA8 frames (hp x wp, rgba_in's BGR f16) to oh x ow, into a view of 8-byte
@@ -2355,7 +2377,8 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
         clear_error();
         if ((uint64_t)h * w == 0) return 0;
         if (hq == 0 || wq == 0) return fail(-1, "render_rgba: empty quarter maps (%u x %u)", hq, wq);
-        if (flags > 3) return fail(-1, "render_rgba: flags %u (bit 0 decisive, bit 1 still)", flags);
+        if (flags > 7)
+            return fail(-1, "render_rgba: flags %u (bit 0 decisive, bit 1 still, bit 2 exact f32 order)", flags);
         if (w < 4) return fail(-1, "render_rgba: frames narrower than 4 pixels");
         FHC_TRY(check_frames("render_rgba a", a, 1, w, h, pitch, 0, hp, wp));
         FHC_TRY(check_frames("render_rgba b", b, 1, w, h, pitch, 0, hp, wp));
@@ -2371,16 +2394,23 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
                         vis->c0 == 4 && reinterpret_cast<uintptr_t>(flow->p) % 16 == 0 && vec4(4, {rt});
         if ((uint64_t)h * w >= kMaxItems || h > 4u * 65535u)
             return fail(-1, "render_rgba: %u x %u pixels exceed the launch limits", w, h);
-        using K = decltype(&render_rgba_kernel<true, true, true>);
-        static const K ks[2][2][2] = {
-            {{render_rgba_kernel<false, false, false>, render_rgba_kernel<false, false, true>},
-             {render_rgba_kernel<false, true, false>, render_rgba_kernel<false, true, true>}},
-            {{render_rgba_kernel<true, false, false>, render_rgba_kernel<true, false, true>},
-             {render_rgba_kernel<true, true, false>, render_rgba_kernel<true, true, true>}}};
-        hipLaunchKernelGGL(ks[cubic ? 1 : 0][qv ? 1 : 0][flags ? 1 : 0], dim3((w + 63) / 64, (h + 3) / 4),
-                           dim3(kThreads), 0, (hipStream_t)stream, static_cast<const uint32_t*>(a),
-                           static_cast<const uint32_t*>(b), w, h, pitch, (float)hq / (float)hp, (float)wq / (float)wp,
-                           in(flow), in(vis), in(rt), hq, wq, fsx, fsy, flags, static_cast<uint32_t*>(out), opitch);
+        using K = decltype(&render_rgba_kernel<true, true, true, true>);
+        // [exact order][cubic][quarter-map vectors][mode flags]
+        static const K ks[2][2][2][2] = {
+            {{{render_rgba_kernel<false, false, false, true>, render_rgba_kernel<false, false, true, true>},
+              {render_rgba_kernel<false, true, false, true>, render_rgba_kernel<false, true, true, true>}},
+             {{render_rgba_kernel<true, false, false, true>, render_rgba_kernel<true, false, true, true>},
+              {render_rgba_kernel<true, true, false, true>, render_rgba_kernel<true, true, true, true>}}},
+            {{{render_rgba_kernel<false, false, false, false>, render_rgba_kernel<false, false, true, false>},
+              {render_rgba_kernel<false, true, false, false>, render_rgba_kernel<false, true, true, false>}},
+             {{render_rgba_kernel<true, false, false, false>, render_rgba_kernel<true, false, true, false>},
+              {render_rgba_kernel<true, true, false, false>, render_rgba_kernel<true, true, true, false>}}}};
+        const uint32_t modes = flags & 3u;
+        hipLaunchKernelGGL(ks[(flags >> 2) & 1u][cubic ? 1 : 0][qv ? 1 : 0][modes ? 1 : 0],
+                           dim3((w + 63) / 64, (h + 3) / 4), dim3(kThreads), 0, (hipStream_t)stream,
+                           static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h, pitch,
+                           (float)hq / (float)hp, (float)wq / (float)wp, in(flow), in(vis), in(rt), hq, wq, fsx, fsy,
+                           modes, static_cast<uint32_t*>(out), opitch);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "render_rgba: launch failed: %s", hipGetErrorString(e));
     });

@@ -209,14 +209,17 @@ class GpuBackend(ComposedChains):
     """The program's ops on the GPU through libfhconv.so, on one stream. Plans are made on first use (the first
     run of the program; a captured replay then finds them all). With ``record`` a list, every launch is also
     appended to it as a dict (label, kind, fn: a callable that issues the same launch again, bytes and flops: its
-    algorithmic work, f16 tensors read and written once), for per-launch measurement."""
+    algorithmic work, f16 tensors read and written once), for per-launch measurement. The frame-size render fuses
+    each product into the sum it feeds (bytes within 1 of the reference's order); exact_render takes the
+    reference's f32 order instead (bit-identical to its ops one by one)."""
 
-    def __init__(self, W, stream=None, fuse: bool = True, device: str = "cuda", chains: bool = True):
+    def __init__(self, W, stream=None, fuse: bool = True, device: str = "cuda", chains: bool = True,
+                 exact_render: bool = False):
         import torch
         import fhconv
         import fhops
         self.torch, self.fhconv, self.fh = torch, fhconv, fhops
-        self.W, self.fuse, self.dev, self.chains = W, fuse, device, chains
+        self.W, self.fuse, self.dev, self.chains, self.exact_render = W, fuse, device, chains, exact_render
         self.stream = stream if stream is not None else torch.cuda.current_stream()
         self.plans: Dict[tuple, object] = {}
         self.gs: Dict[int, object] = {}  # FiLM vector slots (one per phase of a batched program)
@@ -503,8 +506,9 @@ class GpuBackend(ComposedChains):
             return super().frame_render(frames, full, pic, flow, vis, rt, out_frames, hp, wp, fsx, fsy, cubic, flags)
         vf, vv, vr = self._v(flow), self._v(vis), self._v(rt)
         fa, fb = frames[0:1], frames[1:2]
+        fl = flags | (4 if self.exact_render else 0)  # bit 2: the reference's f32 order
         self._go("frame_render (render_pix + rgba_out)",
-                 lambda: self.fh.render_rgba(fa, fb, vf, vv, vr, hp, wp, cubic, flags, fsx, fsy, out=out_frames,
+                 lambda: self.fh.render_rgba(fa, fb, vf, vv, vr, hp, wp, cubic, fl, fsx, fsy, out=out_frames,
                                              stream=self.stream),
                  4 * (frames.numel() + out_frames.numel()) + 2 * 10 * self._px(flow))
 

@@ -144,8 +144,11 @@ int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_t h, uint32
  * frames a and b (each w x h RGBA8, rows `pitch` words apart, read as rgba_in converts them) at hp x wp from the maps
  * flow / vis / rt at hq x wq, the flow's x times fsx and y times fsy (ftq.scale * wp / iwp and * hp / ihp,
  * net/build.rs:717-736), each result rounded to f16 and written as the RGBA8 frame out (w x h, rows opitch words
- * apart, alpha 255). Bit-identical to rgba_in, fhc_render and rgba_out in turn. Flow and vis as channels 0-3 and
- * 4-6 of one 16-byte aligned 8-channel view, with rt of 4-channel pixels, take two loads a map tap. w >= 4. */
+ * apart, alpha 255). flags: bits 0-1 fhc_render's modes; bit 2 set: the reference's f32 operations in its order,
+ * bit-identical to rgba_in, fhc_render and rgba_out in turn; bit 2 clear (the frame path): the same expressions with
+ * each product fused into the sum it feeds (one rounding where the reference rounds twice: about a fifth fewer
+ * instructions), bytes within 1 of the exact order. Flow and vis as channels 0-3 and 4-6 of one 16-byte aligned
+ * 8-channel view, with rt of 4-channel pixels, take two loads a map tap. w >= 4. */
 int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_t h, uint32_t pitch, uint32_t hp, uint32_t wp,
                     const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rt, uint32_t hq, uint32_t wq,
                     float fsx, float fsy, int cubic, uint32_t flags, void* out, uint32_t opitch, void* stream);

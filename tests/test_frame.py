@@ -326,16 +326,17 @@ def test_gpu_small_frame_without_internal_mode_matches_the_oracle():
 def test_fused_chains_equal_their_ops_on_the_gpu(repair):
     """The fused op chains (pyramid, coarse upsample + fine input, flow_t / vis_t + convex upsample, refine input,
     the fused pairs' film_modulate and affine_out, the sibling convs, with the repair the FiLM pair inside the
-    repair's first launch, and the frame's input and render from RGBA8) against the same chains run op by op on the
-    GPU, in a whole frame from RGBA8 frames in the internal-size mode: the same f32 operations and roundings, so
-    every output is bit-identical."""
+    repair's first launch, and the frame's input and render from RGBA8, the render in the reference's f32 order)
+    against the same chains run op by op on the GPU, in a whole frame from RGBA8 frames in the internal-size mode:
+    the same f32 operations and roundings, so every output is bit-identical. The frame path's render (products fused
+    into sums) then gives bytes within 1 of that frame, almost all identical."""
     import torch
     print("frame 600x300 -> 256x128, repair", repair, flush=True)
     W = net.make_weights(3)
     fr = frames(600, 300, dx=7, dy=2)
     outs = []
     for chains in (True, False):
-        gb = net.GpuBackend(W, stream=torch.cuda.current_stream(), chains=chains)
+        gb = net.GpuBackend(W, stream=torch.cuda.current_stream(), chains=chains, exact_render=True)
         f = run_frames(gb, W, 256, 128, fr, t=0.3, repair=repair)
         # (flow_t | vis_t, ftvt, is compared through up7: the fused launch that makes up7 never stores it)
         extra = [("fx", 155), ("rx", 14), ("i8", 3), ("l16", 2), ("l8", 2), ("fv", 7), ("dfilm", 5),
@@ -349,3 +350,8 @@ def test_fused_chains_equal_their_ops_on_the_gpu(repair):
         if bad.size:
             diffs.append(f"{name}: {len(bad)} differ, first at {bad[0].tolist()}")
     assert not diffs, "; ".join(diffs)
+    gb = net.GpuBackend(W, stream=torch.cuda.current_stream())
+    f = run_frames(gb, W, 256, 128, fr, t=0.3, repair=repair)
+    d = _byte_diff(gb.host_frames(f.rgba), outs[0]["rgba"])
+    print(f"  the frame path's render: max byte diff {d.max()}, {np.mean(d == 0):.5f} identical", flush=True)
+    assert d.max() <= 1 and np.mean(d == 0) >= 0.995
