@@ -93,15 +93,26 @@ class Net:
             self.bufs[L.name] = (x, y, r, ws)
             self.params[L.name] = (d, wt, b, s)
 
-    def fuse(self, pairs, torch, fhconv, stream, time_fn, default_tile=False):
+    def fuse(self, pairs, torch, fhconv, stream, time_fn, default_tile=False, always=False):
         """Pair plans for (first, second, res_mid) layer pairs: the second's output buffer, the first's input; every
         instantiated tile height (1, 2, 4 or 8 rows), wave rows (1 or 2) and loop (one workgroup per tile, a
         resident grid, or a resident grid with the two stages on separate waves) timed on the real buffers, the fastest kept (default_tile: the pair planner's own choice, no
-        timing), and only where it beats the two separate launches. A pair that shares a conv with one fused
+        timing), and only where it beats the two separate launches (always: every pair the library instantiates, with
+        the default tile and no timing, as the frame program fuses them). A pair that shares a conv with one fused
         before it is skipped."""
         used = set()
         for A, B, res_mid in pairs:
             if A.name in used or B.name in used:
+                continue
+            if always:
+                da, wa, ba, sa = self.params[A.name]
+                db, wb, bb, sb = self.params[B.name]
+                try:
+                    pp = fhconv.ConvPairPlan(da, wa, ba, sa, db, wb, bb, sb, res_mid=res_mid)
+                except fhconv.FhcError:
+                    continue
+                self.pairs[A.name] = (pp, B, None, res_mid)
+                used |= {A.name, B.name}
                 continue
             sep = time_fn(lambda i=0: (self.run_one(A, stream=stream), self.run_one(B, stream=stream)))
             da, wa, ba, sa = self.params[A.name]
@@ -608,6 +619,222 @@ def pmc_workload(args, torch, fhconv, flyhighfg, net, stream):
     return 0
 
 
+POOL_BYTES = 2 << 30  # the counter workload's rotating buffer pool
+
+
+def conv_launches(args, torch, np, fhconv, flyhighfg, stream):
+    """Every conv launch the counter workload measures, as (group, label, plan, x, y, r, ws, flops, bytes): the 1080p
+    frame's convs (the committed choices; every instantiated pair fused with the pair planner's default tile, as the
+    frame program runs them), the single-layer configurations (3x3 32 -> 32 at 1080p/8, the 1080p/4 ladder, the
+    1080p/16 deep layer and 1x1), and the batched workload's convs (8 pairs, 3 phases) fused the same way. Nothing
+    is chosen by timing, so every counter pass runs the same launches."""
+    out = []
+    tf = lambda fn: time_graph(torch, fn, 20, 3, stream)  # noqa: E731
+    groups = [("frame", flyhighfg.flyhighfg_layers(864, 480, k=1), 1, None, True)]
+    groups += [(f"C{c}", flyhighfg.config_layers(c), 100 + c, 0.25, False) for c in (1, 2, 3)]
+    groups += [("batched", flyhighfg.batched_layers(8, 3), 3, None, True)]
+    nets = []
+    for group, layers, seed, slope, fuse in groups:
+        net = Net(layers, seed, torch, np, fhconv, tune=False, slope=slope)
+        if fuse:
+            net.fuse(flyhighfg.fusible_pairs(layers), torch, fhconv, stream, tf, default_tile=True, always=True)
+        nets.append(net)
+        skip = {B.name for _, B, _, _ in net.pairs.values()}
+        for L in layers:
+            if L.name in net.pairs:
+                pp, B, _, res_mid = net.pairs[L.name]
+                _, y, r, _ = net.bufs[B.name]
+                d = pp.describe()
+                out.append((group, L.name + "+" + B.name, pp, net.bufs[L.name][0], y, None if res_mid else r, None,
+                            d["flops"], d["bytes"]))
+            elif L.name not in skip:
+                x, y, r, ws = net.bufs[L.name]
+                out.append((group, L.name, net.plans[L.name], x, y, r, ws, L.flops, L.bytes))
+    return out, nets
+
+
+def pmc_convs(args, torch, np, fhconv, flyhighfg, stream):
+    """The counter workload of every conv launch (conv_launches): each launch --pmc-reps times, every call on a set
+    of input, output and residual buffers of its own carved from one pre-filled 2 GiB pool (so each call reads
+    tensors no earlier call of it touched: HBM or the MALL, never the L2, which the acquire at every kernel boundary
+    invalidates), then a device copy of COPY_BYTES as many times. Prints one JSON line per launch (its order, variant
+    and kernels per call), the manifest --counters-from attributes the dispatches by."""
+    items, nets = conv_launches(args, torch, np, fhconv, flyhighfg, stream)
+    pool = torch.empty(POOL_BYTES // 2, dtype=torch.float16, device="cuda").uniform_(-1, 1)
+    src = torch.empty(COPY_BYTES // 2, dtype=torch.float16, device="cuda").uniform_(-1, 1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    manifest = []
+    al = 128  # elements between carved tensors (256-byte alignment)
+    with torch.cuda.stream(stream):
+        off = 0
+        for order, (group, label, plan, x, y, r, ws, flops, nbytes) in enumerate(items):
+            d = plan.describe()
+            kernels = 2 if d.get("ksplit", 1) > 1 else 1
+            for i in range(args.pmc_reps):
+                views = []
+                for t in (x, y, r):
+                    if t is None:
+                        views.append(None)
+                        continue
+                    n = -(-t.numel() // al) * al
+                    if off + n > pool.numel():
+                        off = 0
+                    views.append(pool[off:off + t.numel()].view(t.shape))
+                    off += n
+                if ws is None:
+                    plan.run(views[0], views[1], views[2], stream=stream)
+                else:
+                    plan.run(views[0], views[1], views[2], ws, stream=stream)
+            manifest.append(dict(order=order, group=group, label=label, variant=d["name"], kernels=kernels,
+                                 reps=args.pmc_reps, flops=int(flops), bytes=int(nbytes)))
+        # the calibration of the MFMA counters: the register-only MFMA probe (16 independent chains per wave, 4
+        # workgroups of 4 waves per CU), whose rate the bench times on its own
+        blocks = torch.cuda.get_device_properties(0).multi_processor_count * 4
+        pout = torch.empty(blocks * 1024, dtype=torch.float32, device="cuda")
+        for _ in range(args.pmc_reps):
+            pflops = fhconv.probe_mfma_rate(blocks, 256, pout, stream)
+        manifest.append(dict(order=len(manifest), group="calibration", label="mfma_probe", variant="probe",
+                             kernels=1, reps=args.pmc_reps, flops=int(pflops), bytes=0))
+        for _ in range(args.pmc_reps):
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    for m in manifest:
+        print(json.dumps(dict(pmc_conv=m)), flush=True)
+    print(json.dumps(dict(pmc_copy=dict(reps=args.pmc_reps, copy_bytes=COPY_BYTES))), flush=True)
+    return 0
+
+
+def _dispatches(csv_path):
+    """[(dispatch id, kernel name, {counter: value})] of a rocprofv3 counter_collection.csv, in dispatch order: the
+    SQ and TCC counters summed over their instances, GRBM_GUI_ACTIVE (one per XCD) the largest of them, as rocprof's
+    own derived metrics reduce them; of a kernel_trace.csv, the duration in ns as "duration"."""
+    import csv
+    import collections
+    rows = collections.OrderedDict()
+    with open(csv_path) as f:
+        for row in csv.DictReader(f):
+            k = int(row["Dispatch_Id"])
+            if k not in rows:
+                rows[k] = (row["Kernel_Name"], collections.defaultdict(float))
+            c = rows[k][1]
+            if "Counter_Name" not in row:
+                c["duration"] = float(row["End_Timestamp"]) - float(row["Start_Timestamp"])
+            elif row["Counter_Name"].startswith("GRBM_"):
+                c[row["Counter_Name"]] = max(c[row["Counter_Name"]], float(row["Counter_Value"]))
+            else:
+                c[row["Counter_Name"]] += float(row["Counter_Value"])
+    return [(k, rows[k][0], rows[k][1]) for k in sorted(rows)]
+
+
+def counters_from(args):
+    """profiles/conv_counters.txt from the three counter passes over the --pmc-convs workload (FETCH_SIZE;
+    WRITE_SIZE; the SQ/GRBM group) and that run's stdout (the manifest): per conv launch, HBM bytes per call (the
+    two size counters scaled by what they read for the copy of COPY_BYTES) against its algorithmic bytes, MFMA busy
+    cycles over GRBM active cycles x 1024 SIMDs (rocprof's MfmaUtil), the MFMA FLOPs executed (512 per
+    SQ_INSTS_VALU_MFMA_MOPS_F16) against the algorithmic FLOPs (K padding and halo recompute show as a ratio above
+    1), and VALU instructions per wave."""
+    f_csv, w_csv, q_csv, t_csv, man = args.counters_from
+    manifest = [json.loads(line)["pmc_conv"] for line in open(man) if line.startswith('{"pmc_conv"')]
+    for path in (f_csv, w_csv, q_csv, t_csv):  # every pass ran the same launches (its stdout beside its folder)
+        other = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(path))),
+                             os.path.basename(os.path.dirname(os.path.abspath(path))) + ".out")
+        if os.path.exists(other):
+            om = [json.loads(line)["pmc_conv"] for line in open(other) if line.startswith('{"pmc_conv"')]
+            if [(m["label"], m["variant"], m["kernels"]) for m in om] != \
+                    [(m["label"], m["variant"], m["kernels"]) for m in manifest]:
+                raise SystemExit(f"{other} ran other launches than {man}")
+    reps = manifest[0]["reps"]
+
+    def ours(csv_path):
+        ds = _dispatches(csv_path)
+        need = sum(m["kernels"] * m["reps"] for m in manifest)
+        # the workload's calls are the last library dispatches (set-up launches, such as the pair planner's timing,
+        # come before them), and the copies follow them
+        conv = [d for d in ds if "fhc::" in d[1]][-need:]
+        copy = [d for d in ds if "copybuffer" in d[1].lower()][-reps:]
+        if len(conv) != need or len(copy) != reps or conv[-1][0] > copy[0][0]:
+            raise SystemExit(f"{csv_path}: {len(conv)} library dispatches for {need} expected, {len(copy)} copies")
+        return conv, copy
+
+    passes = {name: ours(path) for name, path in (("fetch", f_csv), ("write", w_csv), ("sq", q_csv),
+                                                    ("trace", t_csv))}
+    cf = sum(d[2]["FETCH_SIZE"] for d in passes["fetch"][1]) / reps
+    cw = sum(d[2]["WRITE_SIZE"] for d in passes["write"][1]) / reps
+    f_scale, w_scale = COPY_BYTES / (cf * 1024.0), COPY_BYTES / (cw * 1024.0)
+    # MI355X's engine clock: the MFMA busy cycles are SIMD cycles at it (the MFMA probe, 82% of the dense peak by its
+    # FLOPs, reads 0.82 so); the dispatch's GRBM_GUI_ACTIVE as reported is the sum of its 8 XCDs' counters
+    f_clk, xcds = 2.4e9, 8
+    lines = []
+    pos = 0
+    for m in manifest:
+        n = m["kernels"] * m["reps"]
+        seg = {k: v[0][pos:pos + n] for k, v in passes.items()}
+        pos += n
+        first = seg["fetch"][0][1]
+        kern = first.split("(")[0].replace("void ", "").strip()[:90]
+        fetch = sum(d[2]["FETCH_SIZE"] for d in seg["fetch"]) / m["reps"] * 1024.0 * f_scale
+        write = sum(d[2]["WRITE_SIZE"] for d in seg["write"]) / m["reps"] * 1024.0 * w_scale
+        sq = seg["sq"]
+        busy = sum(d[2]["SQ_VALU_MFMA_BUSY_CYCLES"] for d in sq)
+        active = sum(d[2]["GRBM_GUI_ACTIVE"] for d in sq)
+        mops = sum(d[2]["SQ_INSTS_VALU_MFMA_MOPS_F16"] for d in sq) / m["reps"]
+        waves = sum(d[2]["SQ_WAVES"] for d in sq) / m["reps"]
+        valu = sum(d[2]["SQ_INSTS_VALU"] for d in sq) / m["reps"]
+        t_call = sum(d[2]["duration"] for d in seg["trace"]) / m["reps"] * 1e-9
+        busy_call = busy / m["reps"]
+        lines.append(f"{m['group']} {m['label']} variant={m['variant']} kernel={kern.replace(' ', '')} "
+                     f"calls={m['reps']} kernels_per_call={m['kernels']} flops={m['flops']} bytes={m['bytes']} "
+                     f"us={t_call * 1e6:.3f} traffic={fetch + write:.0f} fetch={fetch:.0f} write={write:.0f} "
+                     f"traffic_ratio={(fetch + write) / max(m['bytes'], 1):.3f} "
+                     f"mfma_util={busy * xcds / (active * 1024):.4f} "
+                     f"mfma_busy={busy_call / (1024 * f_clk * t_call):.4f} "
+                     f"mfma_flops={mops * 512:.0f} mfma_pad={mops * 512 / max(m['flops'], 1):.3f} "
+                     f"mfma_tflops={mops * 512 / t_call / 1e12:.1f} "
+                     f"waves={waves:.0f} valu_per_wave={valu / max(waves, 1):.1f}")
+    tune = f" --tune {os.path.relpath(args.tune, ROOT)}" if args.tune else ""
+    cmd = ("cd /tmp && export TMPDIR=/tmp && cd $GRAFT_REPO_ROOT && timeout -s KILL 300 rocprofv3 {c} "
+           "-d gpurun_out/{d} -o run --output-format csv -- python3 bench.py" + tune +
+           f" --pmc-convs --pmc-reps {reps} > gpurun_out/{{d}}.out")
+    head = ["# Counters of every conv launch (MI355X): four passes over the same workload, then on any host",
+            "# " + cmd.format(c="--pmc FETCH_SIZE", d="pmc_cf"), "# " + cmd.format(c="--pmc WRITE_SIZE", d="pmc_cw"),
+            "# " + cmd.format(c="--pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_WAVES SQ_INSTS_VALU "
+                                "GRBM_GUI_ACTIVE", d="pmc_cq"),
+            "# " + cmd.format(c="--kernel-trace", d="pmc_ct"),
+            f"# python3 bench.py{tune} --counters-from gpurun_out/pmc_cf/run_counter_collection.csv "
+            "gpurun_out/pmc_cw/run_counter_collection.csv gpurun_out/pmc_cq/run_counter_collection.csv "
+            "gpurun_out/pmc_ct/run_kernel_trace.csv gpurun_out/pmc_cf.out",
+            "# per call (of its 'calls' calls, each on tensors of its own): us = kernel duration in the trace pass; "
+            "traffic = FETCH_SIZE x fetch_scale + WRITE_SIZE x write_scale (KiB), the scales making the copy of "
+            f"{COPY_BYTES} bytes read and write that; mfma_util = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 "
+            "SIMDs / 8 XCDs: the reported GRBM value sums the XCDs), rocprof's MfmaUtil over the counted dispatch's "
+            "active window (which the counting stretches for short kernels); mfma_busy = the same busy cycles over the "
+            "kernel's own duration (1024 SIMDs at 2.4 GHz); mfma_flops = 512 x SQ_INSTS_VALU_MFMA_MOPS_F16 (what the "
+            "MFMAs compute, padding included), mfma_pad = that over the algorithmic FLOPs; the MFMA probe (the "
+            "calibration line) checks the busy scale against its FLOP rate",
+            f"# fetch_scale {f_scale:.4f} write_scale {w_scale:.4f}"]
+    text = "\n".join(head + lines) + "\n"
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    with open(os.path.join(ROOT, "profiles", "conv_counters.txt"), "w") as f:
+        f.write(text)
+    print(text, end="")
+    return 0
+
+
+def conv_counters():
+    """{(group, label): {key: value}} from profiles/conv_counters.txt, or {} where it was not recorded."""
+    path = os.path.join(ROOT, "profiles", "conv_counters.txt")
+    if not os.path.exists(path):
+        return {}
+    out = {}
+    for line in open(path).read().splitlines():
+        if not line or line[0] == "#":
+            continue
+        group, label, *kv = line.split(" ")
+        out[(group, label)] = dict(x.split("=", 1) for x in kv)
+    return out
+
+
 def pmc_render(args, torch, np, stream):
     """The 1080p frame's render (fhc_render_rgba, as the frame runs it) --pmc-reps times over rotating sets of input
     and output frames (> 512 MB, so every launch reads its frames from HBM), after one eager frame that fills the
@@ -765,6 +992,13 @@ def main():
                                         "known size as many times: the workload of the rocprofv3 --pmc FETCH_SIZE / "
                                         "WRITE_SIZE passes")
     ap.add_argument("--pmc-reps", type=int, default=64)
+    ap.add_argument("--pmc-convs", action="store_true",
+                    help="only run every conv launch (the frame's conv step, the single-layer configurations, the "
+                         "batched convs) --pmc-reps times over carved cold buffers, then a copy of known size: the "
+                         "workload of the conv counter passes")
+    ap.add_argument("--counters-from", nargs=5, metavar="FILE",
+                    help="turn the --pmc-convs passes' counter_collection.csv files (FETCH_SIZE, WRITE_SIZE, the SQ "
+                         "group), its kernel_trace.csv and that run's stdout into profiles/conv_counters.txt")
     ap.add_argument("--eager-frames", type=int, default=0,
                     help="only run the 1080p frame (as --only-frame builds it) this many times eagerly, untimed: the "
                          "workload of rocprofv3 counter passes over the frame's kernels")
@@ -778,6 +1012,8 @@ def main():
     args = ap.parse_args()
     if args.traffic_from:
         return traffic_from(args)
+    if args.counters_from:
+        return counters_from(args)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported (the conv path shards "
               "by frame pair, one independent pipeline per GPU, so N GPUs run N of these)", file=sys.stderr)
@@ -799,6 +1035,9 @@ def main():
     assert flyhighfg.default_internal(1920, 1080) == (856, 480)
     if args.eager_frames:
         return eager_frames(args, torch, np, stream)
+    if args.pmc_convs:
+        fhconv.parse_tune(open(args.tune or os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
+        return pmc_convs(args, torch, np, fhconv, flyhighfg, stream)
     if args.pmc_layer == "frame_render" and not args.traffic_from:
         fhconv.parse_tune(open(os.path.join(ROOT, "flyhigh-engine_amd", "tune_mi355x.txt")).read())
         return pmc_render(args, torch, np, stream)
@@ -992,6 +1231,9 @@ def main():
                    seconds=round(secs, 3), cpu_model=cpu_model(), host_cpus=os.cpu_count())
         log(f"bench: CPU baseline {secs:.3f} s per frame on {threads} threads")
 
+    conv_roof = conv_roofline(per_layer, per_pair, net, cfg_layers, batched_convs)
+    log("bench: conv roofline", json.dumps(conv_roof))
+
     conv_step = dict(
         workload="FlyHighFG conv layers of one pair()+mid() at 1080p (network 856x480 padded to 864x480), NHWC "
                  "f16, conv-only; the A/B encoders run as batch-2 convs"
@@ -1002,11 +1244,51 @@ def main():
         pair_us=round(pair_us, 3), mid_us=round(mid_us, 3), unfused_step_us=round(unfused_us, 3),
         fuse_check=fuse_check, event_ms_per_step=round(ev_ms, 6),
         submit_us_per_step=round(t_submit * 1e6 / args.steps, 3))
-    detail = dict(frame=frame, conv_step=conv_step, roofline=roofline, cpu_baseline=cpu, layers=per_layer,
+    detail = dict(frame=frame, conv_step=conv_step, roofline=roofline, conv_roofline=conv_roof, cpu_baseline=cpu,
+                  layers=per_layer,
                   pairs=per_pair, config_layers=cfg_layers, config_pairs=cfg_pairs, batched=batched,
                   batched_convs=batched_convs, net_ops=net_ops,
                   tune_table=tune_table)
     return emit(args, frame, conv_step, roofline, cpu, batched, detail)
+
+
+def conv_roofline(per_layer, per_pair, net, cfg_layers, batched_convs):
+    """The conv layers' roofline in brief: the dominant conv launch of the frame's conv step (the largest warm time
+    among its launches: the fused pairs and the convs not fused), its cold roofline fraction and bound, with the MFMA
+    busy fraction, MFMA padding and HBM traffic ratio its counter passes recorded (profiles/conv_counters.txt, when
+    they ran on the same variant); the least and median cold fraction over the step's launches; each single-layer
+    configuration's fraction; the batched convs' dominant launch likewise."""
+    if not per_layer:
+        return None
+    ctr = conv_counters()
+
+    def counted(group, r):
+        c = ctr.get((group, r["name"]))
+        if c is None or c.get("variant") != r["variant"]:
+            return {}
+        return dict(mfma_busy=float(c["mfma_busy"]), mfma_pad=float(c["mfma_pad"]),
+                    traffic_ratio=float(c["traffic_ratio"]))
+
+    fused_b = {B.name for _, B, _, _ in net.pairs.values()}
+    step = [r for r in per_pair] + [r for r in per_layer if r["name"] not in net.pairs and r["name"] not in fused_b]
+    if not step:
+        return None
+    fr = sorted(r["frac_cold"] for r in step)
+    dom = max(step, key=lambda r: r["us_warm"])
+    out = dict(dominant=dict(name=dom["name"], variant=dom["variant"], bound=dom["bound"], frac=dom["frac_cold"],
+                             us_cold=dom["us_cold"], roof_us=dom["roof_us"], **counted("frame", dom)),
+               frame_frac_min=fr[0], frame_frac_median=fr[len(fr) // 2], frame_launches=len(step),
+               configs={f"C{r['config']} {r['name']}": dict(frac=r["frac_cold"], bound=r["bound"],
+                                                           **{k: v for k, v in counted(f"C{r['config']}", r).items()
+                                                              if k == "mfma_busy"})
+                        for r in cfg_layers},
+               counters="profiles/conv_counters.txt")
+    if batched_convs:
+        bl = batched_convs["launches"]
+        bd = max(bl, key=lambda r: r["us_warm"])
+        out["batched_dominant"] = dict(name=bd["name"], variant=bd["variant"], bound=bd["bound"],
+                                       frac=bd["frac_cold"], us_cold=bd["us_cold"], **counted("batched", bd))
+    return out
 
 
 def emit(args, frame, conv_step, roofline, cpu, batched, detail):
@@ -1036,6 +1318,7 @@ def emit(args, frame, conv_step, roofline, cpu, batched, detail):
         batched=None if batched is None else {k: batched[k] for k in ("step_us", "generated_frames_per_s",
                                                                       "pairs_per_s", "launches", "output_ok")},
         batched_convs_step_us=(detail.get("batched_convs") or {}).get("convs_step_us"),
+        conv_roofline=detail.get("conv_roofline"),
         detail=args.detail or None)
     text = json.dumps(line)
     if len(text) > 4000:
