@@ -528,6 +528,27 @@ void pack_weights(const fhc_conv_plan& p, const uint16_t* w, std::vector<uint16_
                     }
 }
 
+// A pair's first conv with taps packed into its K-steps (cp = 8 or 16 input channels per tap, cin <= cp): the
+// A-fragment order of pack_weights, [nb16][kstep][lane][8], K-step s holding taps s * (32 / cp) .. in cp-channel
+// slots, lane l's 8 positions channels (g % (cp / 8)) * 8 .. +7 of tap s * (32 / cp) + g / (cp / 8), g = l / 16;
+// positions past the 9th tap or the input channels are zero.
+void pack_weights_taps(const fhc_conv_desc& d, int nb16, int ksteps, int cp, const uint16_t* w,
+                       std::vector<uint16_t>& out) {
+    const int tps = 32 / cp, gpt = cp / 8;
+    out.assign((size_t)nb16 * ksteps * 64 * 8, 0);
+    size_t o = 0;
+    for (int nb = 0; nb < nb16; nb++)
+        for (int s = 0; s < ksteps; s++)
+            for (int l = 0; l < 64; l++)
+                for (int i = 0; i < 8; i++, o++) {
+                    const int g = l >> 4, tap = s * tps + g / gpt;
+                    const uint32_t ci = (uint32_t)((g % gpt) * 8 + i), co = (uint32_t)(nb * 16 + (l & 15));
+                    if (tap >= 9 || ci >= d.cin || co >= d.cout) continue;
+                    const uint32_t ky = (uint32_t)tap / 3, kx = (uint32_t)tap % 3;
+                    out[o] = w[(((size_t)co * d.cin + ci) * d.kh + ky) * d.kw + kx];
+                }
+}
+
 // f16 bits -> f32 (exact)
 static float half_bits_to_float(uint16_t h) {
     const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1f, m = h & 0x3ff;
@@ -649,12 +670,14 @@ std::string describe_json(const fhc_conv_plan* p) {
                                     (b.act == FHC_ACT_PRELU ? b.cout : 0) + (b.residual && !p->res_mid ? out_el : 0));
         char buf[700];
         snprintf(buf, sizeof buf,
-                 "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d.w%d%s\",\"family\":\"pair\",\"cfg\":%d,"
+                 "{\"variant\":0,\"name\":\"pair.s%d.c%dx%d.n%dx%d.t%dx%d.w%d%s%s\",\"family\":\"pair\",\"cfg\":%d,"
                  "\"tile_rows\":%d,\"tile_cols\":%d,\"wave_rows\":%d,\"persistent\":%d,\"res_mid\":%d,\"tiles\":%u,"
-                 "\"grid\":[%u,%u,%u],\"threads\":%u,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f}",
-                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, c.wm, c.persist == 2 ? "/ws" : c.persist ? "/p" : "", p->cfg,
+                 "\"grid\":[%u,%u,%u],\"threads\":%u,\"hout\":%u,\"wout\":%u,\"flops\":%.0f,\"bytes\":%.0f,"
+                 "\"a_channels_per_tap\":%d,\"a_ksteps\":%d}",
+                 c.sa, c.ca32, c.cb32, 16 * c.nba, 16 * c.nbb, c.th, kPairTileW, c.wm,
+                 c.cpa == 8 ? ".k8" : c.cpa == 16 ? ".k16" : "", c.persist == 2 ? "/ws" : c.persist ? "/p" : "", p->cfg,
                  c.th, kPairTileW, c.wm, c.persist, p->res_mid, p->tiles, p->grid.x, p->grid.y, p->grid.z, p->threads,
-                 p->g.hout, p->g.wout, fa + fb, bytes);
+                 p->g.hout, p->g.wout, fa + fb, bytes, c.cpa ? c.cpa : 32, p->args.ksteps);
         return buf;
     }
     if (p->family == 1) {
@@ -875,7 +898,7 @@ namespace {
 // One conv of a fused pair as a direct-kernel weight layout (CIN32 input channels per tap, nb 16-channel blocks):
 // the plan's geometry, arguments, packed weights and device arrays.
 hipError_t pair_part(fhc_conv_plan& p, const fhc_conv_desc& d, int cin32, int nb, const uint16_t* w,
-                     const uint16_t* bias, const uint16_t* slope) {
+                     const uint16_t* bias, const uint16_t* slope, int cp = 32) {
     p.d = d;
     p.dmem = nullptr;
     p.pair_b = nullptr;
@@ -894,7 +917,13 @@ hipError_t pair_part(fhc_conv_plan& p, const fhc_conv_desc& d, int cin32, int nb
     p.family = 1;
     p.ksplit = 1;
     std::vector<uint16_t> packed;
-    pack_weights(p, w, packed);
+    if (cp < 32) {  // taps packed into the K-steps (pair_impl.h, tap_chain)
+        p.args.ksteps = (9 + 32 / cp - 1) / (32 / cp);
+        p.args.tapgroups = p.args.ksteps * 4;
+        pack_weights_taps(d, nb, p.args.ksteps, cp, w, packed);
+    } else {
+        pack_weights(p, w, packed);
+    }
     return upload(p, packed, bias, slope);
 }
 
@@ -919,11 +948,11 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         if (!valid_desc(A, &why)) return fail(-1, "fhc_conv_pair_plan_create: first conv: %s", why.c_str());
         if (!valid_desc(B, &why)) return fail(-1, "fhc_conv_pair_plan_create: second conv: %s", why.c_str());
         const bool res_mid = (flags & FHC_PAIR_RES_MID) != 0, post = (flags & FHC_PAIR_AFFINE_OUT) != 0;
-        const bool film = (flags & FHC_PAIR_FILM_IN) != 0;
+        const bool film = (flags & FHC_PAIR_FILM_IN) != 0, tap32 = (flags & FHC_PAIR_TAP32) != 0;
         const uint32_t th_req = (flags >> 8) & 0xffu, wm_req = (flags >> 16) & 0xfu;
         // affine_out after the second conv, FiLM before the first: the one-workgroup-per-tile loop applies them
         const uint32_t loop_req = post || film ? 1u : (flags >> 20) & 3u;
-        if ((flags & ~(FHC_PAIR_RES_MID | FHC_PAIR_AFFINE_OUT | FHC_PAIR_FILM_IN | 0x3fff00u)) != 0)
+        if ((flags & ~(FHC_PAIR_RES_MID | FHC_PAIR_AFFINE_OUT | FHC_PAIR_FILM_IN | FHC_PAIR_TAP32 | 0x3fff00u)) != 0)
             return fail(-1, "fhc_conv_pair_plan_create: unknown flags");
         if (post && ((flags >> 20) & 3u) > 1)
             return fail(-1, "fhc_conv_pair_plan_create: affine_out runs in the one-workgroup-per-tile loop only");
@@ -954,31 +983,46 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         // is instantiated (else two), and the tallest instantiated tile that still gives 256 workgroups, else the
         // shortest
         auto tiles_at = [&](int th) { return (uint64_t)A.n * div_ceil(ha, (uint32_t)th) * div_ceil(wa, kPairTileW); };
-        auto serves = [&](const PairCfg& c) {
+        // A's channels per tap: 8 or 16 where its input has at most that many and a configuration at the requested
+        // tile, wave split and loop packs them (the taps then share K-steps), else 32 (or 32 on request,
+        // FHC_PAIR_TAP32)
+        auto serves_cp = [&](const PairCfg& c, int cp) {
             return c.sa == (int)A.stride && c.ca32 == ca32 && c.cb32 == cb32 && c.nba == nba && c.nbb == nbb &&
-                   (!th_req || c.th == (int)th_req) && (!wm_req || c.wm == (int)wm_req);
+                   (c.cpa ? c.cpa : 32) == cp && (!th_req || c.th == (int)th_req) && (!wm_req || c.wm == (int)wm_req);
         };
-        int persist = loop_req >= 2 ? (int)loop_req - 1 : 0;
-        if (loop_req == 0)  // the resident grid where instantiated and big enough, stages on separate waves first
-            for (int i = 0; i < kNumPair; i++)
-                if (kPairCfgs[i].persist && serves(kPairCfgs[i]) && tiles_at(kPairCfgs[i].th) >= 8 * 256)
-                    persist = std::max(persist, kPairCfgs[i].persist);
-        int wm = wm_req ? (int)wm_req : 2;
-        if (!wm_req)
-            for (int i = 0; i < kNumPair; i++)
-                if (kPairCfgs[i].persist == persist && serves(kPairCfgs[i]) && kPairCfgs[i].wm == 1) wm = 1;
-        int idx = -1;
-        for (int i = 0; i < kNumPair; i++) {
-            const PairCfg& c = kPairCfgs[i];
-            if (!serves(c) || c.wm != wm || c.persist != persist) continue;
-            if (th_req) {
-                idx = i;
-                continue;
+        // the configuration for channels per tap cp: by default the resident-grid loop when it is instantiated and
+        // there are at least 8 tiles per CU of an MI355X (256), one wave row where that is instantiated (else two),
+        // and the tallest instantiated tile that still gives 256 workgroups, else the shortest; -1 if none
+        auto select = [&](int cp) {
+            auto serves = [&](const PairCfg& c) { return serves_cp(c, cp); };
+            int persist = loop_req >= 2 ? (int)loop_req - 1 : 0;
+            if (loop_req == 0)  // the resident grid where instantiated and big enough, stages on separate waves first
+                for (int i = 0; i < kNumPair; i++)
+                    if (kPairCfgs[i].persist && serves(kPairCfgs[i]) && tiles_at(kPairCfgs[i].th) >= 8 * 256)
+                        persist = std::max(persist, kPairCfgs[i].persist);
+            int wm = wm_req ? (int)wm_req : 2;
+            if (!wm_req)
+                for (int i = 0; i < kNumPair; i++)
+                    if (kPairCfgs[i].persist == persist && serves(kPairCfgs[i]) && kPairCfgs[i].wm == 1) wm = 1;
+            int best = -1;
+            for (int i = 0; i < kNumPair; i++) {
+                const PairCfg& c = kPairCfgs[i];
+                if (!serves(c) || c.wm != wm || c.persist != persist) continue;
+                if (th_req) {
+                    best = i;
+                    continue;
+                }
+                const int cur = best < 0 ? 0 : kPairCfgs[best].th;
+                const bool fills = tiles_at(c.th) >= 256, cur_fills = best >= 0 && tiles_at(cur) >= 256;
+                if (best < 0 || (fills && (!cur_fills || c.th > cur)) || (!fills && !cur_fills && c.th < cur)) best = i;
             }
-            const int cur = idx < 0 ? 0 : kPairCfgs[idx].th;
-            const bool fills = tiles_at(c.th) >= 256, cur_fills = idx >= 0 && tiles_at(cur) >= 256;
-            if (idx < 0 || (fills && (!cur_fills || c.th > cur)) || (!fills && !cur_fills && c.th < cur)) idx = i;
-        }
+            return best;
+        };
+        int idx = -1, cpa = 32;
+        if (!tap32 && !film)
+            for (int cp : {8, 16})
+                if (idx < 0 && (int)A.cin <= cp && (idx = select(cp)) >= 0) cpa = cp;
+        if (idx < 0) idx = select(32);
         if (idx < 0)
             return fail(-1, "fhc_conv_pair_plan_create: no fused pair instantiated for stride %u, %u -> %u -> %u "
                             "channels%s", A.stride, A.cin, A.cout, B.cout,
@@ -990,7 +1034,7 @@ extern "C" int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint
         if (e != hipSuccess) return fail(-1, "fhc_conv_pair_plan_create: hipGetDevice: %s", hipGetErrorString(e));
         pb->device = pa->device;
         e = pair_part(*pb, B, cb32, nbb, w_b, bias_b, slope_b);
-        if (e == hipSuccess) e = pair_part(*pa, A, ca32, nba, w_a, bias_a, slope_a);
+        if (e == hipSuccess) e = pair_part(*pa, A, ca32, nba, w_a, bias_a, slope_a, cpa);
         if (e != hipSuccess) {
             if (pa->dmem) (void)hipFree(pa->dmem);
             if (pb->dmem) (void)hipFree(pb->dmem);

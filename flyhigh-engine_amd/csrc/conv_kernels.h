@@ -111,11 +111,13 @@ constexpr int kPairTileW = 14;  // output columns per tile (B's 16-pixel MFMA bl
 // The instantiated pairs: A's stride, A's and B's input channels padded to 32, A's and B's output channel blocks
 // of 16, the output rows per tile, the wave rows that split them, and the loop: 0 one workgroup per tile (weights
 // loaded per tile: small frames), 1 a resident grid looping over tiles (weights loaded once: large tensors), 2 a
-// resident grid whose A and B stages run on separate waves, pipelined across tiles (one wave row).
+// resident grid whose A and B stages run on separate waves, pipelined across tiles (one wave row). cpa: A's input
+// channels per tap in its K-steps, 0 (32: one tap per 32-wide step) or 8 / 16 (at most that many input channels:
+// 4 or 2 taps packed into each step, 3 or 5 steps where one tap a step takes 9).
 struct PairCfg {
-    int sa, ca32, cb32, nba, nbb, th, wm, persist;
+    int sa, ca32, cb32, nba, nbb, th, wm, persist, cpa;
 };
-constexpr int kNumPair = 34;
+constexpr int kNumPair = 44;
 inline constexpr PairCfg kPairCfgs[kNumPair] = {
     // the encoder's stride-2 conv and its successor (3 -> 36 -> 36)
     {2, 32, 64, 3, 3, 2, 1, 0}, {2, 32, 64, 3, 3, 4, 1, 0}, {2, 32, 64, 3, 3, 2, 2, 0}, {2, 32, 64, 3, 3, 4, 2, 0},
@@ -140,6 +142,12 @@ inline constexpr PairCfg kPairCfgs[kNumPair] = {
     {2, 32, 64, 3, 3, 4, 1, 2},
     {1, 32, 32, 2, 2, 4, 1, 2}, {1, 32, 32, 2, 2, 8, 1, 2},
     {1, 32, 32, 2, 1, 4, 1, 2}, {1, 32, 32, 2, 1, 8, 1, 2},
+    // taps packed into A's K-steps: the encoder's first pair (3 input channels, 8 per tap: 3 steps) and the refine
+    // head's first pair (14 input channels, 16 per tap: 5 steps), in each loop
+    {2, 32, 64, 3, 3, 2, 1, 0, 8}, {2, 32, 64, 3, 3, 4, 1, 0, 8}, {2, 32, 64, 3, 3, 4, 2, 1, 8},
+    {2, 32, 64, 3, 3, 4, 1, 2, 8},
+    {1, 32, 32, 2, 2, 2, 1, 0, 16}, {1, 32, 32, 2, 2, 4, 1, 0, 16}, {1, 32, 32, 2, 2, 4, 2, 1, 16},
+    {1, 32, 32, 2, 2, 8, 2, 1, 16}, {1, 32, 32, 2, 2, 4, 1, 2, 16}, {1, 32, 32, 2, 2, 8, 1, 2, 16},
 };
 constexpr int kPairResidentWaves = 8;  // waves per CU of the resident-grid pair (2 per SIMD)
 using PairLaunchFn = hipError_t (*)(const PairKArgs&, dim3 grid, hipStream_t);

@@ -55,6 +55,48 @@ __device__ __forceinline__ void pair_chain(f4 (&acc)[FM], const h8* wr, const ui
     pin_mfma_pipeline<0, NQ, D, R, FM, S, KS, 1, 0>();
 }
 
+// A's K-steps for CP input channels per tap: CP = 32 one tap per 32-wide K-step (M = CA32 / 32 steps per tap); CP
+// = 8 or 16 (at most that many input channels): 32 / CP taps packed into each K-step, 3 or 5 steps for the 9 taps
+template <int CP, int MA>
+constexpr int pair_ksteps() { return CP == 32 ? 9 * MA : (9 + 32 / CP - 1) / (32 / CP); }
+
+// The chain of A over an LDS tile with CP < 32: K-step s holds taps s * T .. s * T + T - 1 (T = 32 / CP), tap t's
+// input channels c in K positions (t - s * T) * CP + c. Lane group g (lane >> 4) feeds 8 of them: channels
+// (g % (CP / 8)) * 8 .. +7 of tap s * T + g / (CP / 8), one 16-byte LDS read at the lane's pixel shifted by the
+// tap; past the 9th tap (zero weights) it reads channels CP .. CP + 7 of the lane's own pixel, zero in the staged
+// halo (at most CP input channels), so no value of the tensor meets a padding weight. base: the lane's pixel (row
+// 0, column (lane & 15) * S), channel 0. Output rows f = 0 .. FM - 1 read tile rows f * S + ky.
+template <int FM, int S, int CP, int IW, int PSTR>
+__device__ __forceinline__ void tap_chain(f4 (&acc)[FM], const h8* wr, const uint16_t* base, int g) {
+    constexpr int T = 32 / CP, KS = pair_ksteps<CP, 1>(), GPT = CP / 8;
+    static_assert(CP == 8 || CP == 16, "8 or 16 channels per tap");
+    const int tg = g / GPT, c8 = (g % GPT) * 8;
+    int off[KS];
+#pragma unroll
+    for (int s = 0; s < KS; s++) {
+        const int tap = s * T + tg;
+        off[s] = tap < 9 ? ((tap / 3) * IW + tap % 3) * PSTR + c8 : CP;
+    }
+    h8 v[KS][FM];
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int f = 0; f < FM; f++) v[s][f] = *reinterpret_cast<const h8*>(base + f * S * IW * PSTR + off[s]);
+#pragma unroll
+    for (int f = 0; f < FM; f++) acc[f] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int f = 0; f < FM; f++) acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wr[s], v[s][f], acc[f], 0, 0, 0);
+}
+
+// A's chain: per tap (pair_chain) at CP = 32, taps packed (tap_chain) below
+template <int FM, int S, int MA, int CP, int IW, int PSTR>
+__device__ __forceinline__ void a_chain(f4 (&acc)[FM], const h8* wr, const uint16_t* px, int lane) {
+    if constexpr (CP == 32) pair_chain<FM, S, MA, IW, PSTR>(acc, wr, px + (lane >> 4) * 8);
+    else tap_chain<FM, S, CP, IW, PSTR>(acc, wr, px, lane >> 4);
+}
+
 // film_modulate (film.wgsl) on one staged 8-channel group: channel j < n becomes f16(v * gm[j] + bt[j]) with
 // gm = 1 + gamma, bt = beta in f32, as the op computes it; channels past n stay as they are (zero)
 __device__ __forceinline__ uint4 film_group(uint4 q, const float* gm, const float* bt, int n) {
@@ -80,17 +122,18 @@ struct PairLds {
 // FILM: A's input goes through film_modulate as it is staged (a.film, the one-tile loop only). The body of one
 // tile t (conv_pair's workgroup t; a launch that runs other work beside the pair passes its own numbering) in the
 // workgroup's LDS L; the block is 64 * WN * WM threads.
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC, bool FILM = false>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC, bool FILM = false, int CPA = 32>
 __device__ __forceinline__ void conv_pair_tile(const PairKArgs& pk, const int t, PairLds<SA, CA32, CB32, TH>& L) {
     constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN * WM, TWB = kPairTileW;
     constexpr int FA = TH + 2;                                  // A's rows per tile
     constexpr int FAW = FA / WM, THW = TH / WM;                 // rows per wave
     static_assert(FA % WM == 0 && TH % WM == 0, "rows split evenly over the wave rows");
     constexpr int IHA = (FA - 1) * SA + 3, IWA = 15 * SA + 3;   // A's input halo
-    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32;
+    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32, KA = pair_ksteps<CPA, MA>();
     constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;     // A's output tile in LDS: FA rows x 18 pixels
     constexpr int HALO = IHA * IWA * GPA, NLD = (HALO + NT - 1) / NT;
     static_assert(NBA * 16 <= CB32, "A's channel blocks exceed B's input channels");
+    static_assert(CPA == 32 || CA32 == 32, "packed taps read the zero channels CPA .. CPA + 7 of the staged halo");
     static_assert(sizeof(L.hin) == IHA * IWA * PSA * 2 && sizeof(L.mid) == FA * MW * PSB * 2, "the tile's LDS");
     uint16_t* const hin = L.hin;
     uint16_t* const mid = L.mid;
@@ -105,11 +148,11 @@ __device__ __forceinline__ void conv_pair_tile(const PairKArgs& pk, const int t,
     const int coa = wa * 16 + 4 * (lane >> 4), cob = wb * 16 + 4 * (lane >> 4);
 
     // every global load first: both layers' weights, A's input halo, B's external residual, biases, multipliers
-    h8 wra[9 * MA], wrb[9 * MB];
+    h8 wra[KA], wrb[9 * MB];
     {
-        const h8* wp = reinterpret_cast<const h8*>(a.wpk) + (size_t)wa * 9 * MA * 64 + lane;
+        const h8* wp = reinterpret_cast<const h8*>(a.wpk) + (size_t)wa * KA * 64 + lane;
 #pragma unroll
-        for (int s = 0; s < 9 * MA; s++) wra[s] = wp[s * 64];
+        for (int s = 0; s < KA; s++) wra[s] = wp[s * 64];
         const h8* wq = reinterpret_cast<const h8*>(b.wpk) + (size_t)wb * 9 * MB * 64 + lane;
 #pragma unroll
         for (int s = 0; s < 9 * MB; s++) wrb[s] = wq[s * 64];
@@ -192,7 +235,7 @@ __device__ __forceinline__ void conv_pair_tile(const PairKArgs& pk, const int t,
     // A over FA rows x 16 columns; its f16 output (zero outside the image) into the LDS tile
     if (wn < NBA) {
         f4 acc[FAW];
-        pair_chain<FAW, SA, MA, IWA, PSA>(acc, wra, hin + (wm * FAW * SA * IWA + lx * SA) * PSA + (lane >> 4) * 8);
+        a_chain<FAW, SA, MA, CPA, IWA, PSA>(acc, wra, hin + (wm * FAW * SA * IWA + lx * SA) * PSA, lane);
 #pragma unroll
         for (int fw = 0; fw < FAW; fw++) {
             const int f = wm * FAW + fw;
@@ -254,10 +297,10 @@ __device__ __forceinline__ void conv_pair_tile(const PairKArgs& pk, const int t,
     }
 }
 
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC, bool FILM = false>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, bool VEC, bool FILM = false, int CPA = 32>
 __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(PairKArgs pk) {
     __shared__ __align__(16) PairLds<SA, CA32, CB32, TH> lds;
-    conv_pair_tile<SA, CA32, CB32, NBA, NBB, TH, WM, VEC, FILM>(pk, blockIdx.x, lds);
+    conv_pair_tile<SA, CA32, CB32, NBA, NBB, TH, WM, VEC, FILM, CPA>(pk, blockIdx.x, lds);
 }
 
 // The persistent pair: G = gridDim.x resident workgroups loop over B's output tiles t, t + G, ... with both layers'
@@ -269,14 +312,15 @@ __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM) void conv_pair(P
 // epilogue with its stores; the next tile's residual loads; a barrier. The intermediate never leaves the CU.
 // Compiled for exactly 2 waves per SIMD (at most 256 registers per lane, AGPRs included), so that the resident
 // grid the planner sizes (kPairResidentWaves waves per CU, or the LDS limit) is the one that fits.
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, int CPA = 32>
 __global__ __launch_bounds__(64 * (NBA > NBB ? NBA : NBB) * WM)
 __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_p(PairKArgs pk) {
     constexpr int WN = NBA > NBB ? NBA : NBB, NT = 64 * WN * WM, TWB = kPairTileW;
     constexpr int FA = TH + 2, FAW = FA / WM, THW = TH / WM;
     static_assert(FA % WM == 0 && TH % WM == 0, "rows split evenly over the wave rows");
     constexpr int IHA = (FA - 1) * SA + 3, IWA = 15 * SA + 3;
-    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32;
+    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32, KA = pair_ksteps<CPA, MA>();
+    static_assert(CPA == 32 || CA32 == 32, "packed taps read the zero channels CPA .. CPA + 7 of the staged halo");
     constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;
     constexpr int HALO = IHA * IWA * GPA, NLD = (HALO + NT - 1) / NT;
     static_assert(NBA * 16 <= CB32, "A's channel blocks exceed B's input channels");
@@ -366,11 +410,11 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_p(PairKArgs pk) {
 
     // once: the first halo, both layers' weights, biases and multipliers, the zero channels of the LDS tile
     load_halo(t);
-    h8 wra[9 * MA], wrb[9 * MB];
+    h8 wra[KA], wrb[9 * MB];
     {
-        const h8* wp = reinterpret_cast<const h8*>(a.wpk) + (size_t)wa * 9 * MA * 64 + lane;
+        const h8* wp = reinterpret_cast<const h8*>(a.wpk) + (size_t)wa * KA * 64 + lane;
 #pragma unroll
-        for (int s = 0; s < 9 * MA; s++) wra[s] = wp[s * 64];
+        for (int s = 0; s < KA; s++) wra[s] = wp[s * 64];
         const h8* wq = reinterpret_cast<const h8*>(b.wpk) + (size_t)wb * 9 * MB * 64 + lane;
 #pragma unroll
         for (int s = 0; s < 9 * MB; s++) wrb[s] = wq[s * 64];
@@ -406,7 +450,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_p(PairKArgs pk) {
         // A over FA rows x 16 columns; its f16 output (zero outside the image) into the LDS tile
         if (wn < NBA) {
             f4 acc[FAW];
-            pair_chain<FAW, SA, MA, IWA, PSA>(acc, wra, hin + (wm * FAW * SA * IWA + lx * SA) * PSA + (lane >> 4) * 8);
+            a_chain<FAW, SA, MA, CPA, IWA, PSA>(acc, wra, hin + (wm * FAW * SA * IWA + lx * SA) * PSA, lane);
 #pragma unroll
             for (int fw = 0; fw < FAW; fw++) {
                 const int f = wm * FAW + fw;
@@ -462,13 +506,14 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_p(PairKArgs pk) {
 // workgroup alternating between them. The A waves also stage the halos (tile s + 1 into LDS from registers, tile
 // s + 2 into registers); the B waves load the residual a step ahead and store. Every load and store is
 // unconditional through buffer instructions (tiles past the last read zeros and store nothing).
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int CPA = 32>
 __global__ __launch_bounds__(64 * (NBA + NBB))
 __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_ws(PairKArgs pk) {
     constexpr int NW = NBA + NBB, NTA = 64 * NBA, TWB = kPairTileW;
     constexpr int FA = TH + 2;
     constexpr int IHA = (FA - 1) * SA + 3, IWA = 15 * SA + 3;
-    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32;
+    constexpr int GPA = CA32 / 8, PSA = CA32 + 8, MA = CA32 / 32, KA = pair_ksteps<CPA, MA>();
+    static_assert(CPA == 32 || CA32 == 32, "packed taps read the zero channels CPA .. CPA + 7 of the staged halo");
     constexpr int MW = 18, PSB = CB32 + 8, MB = CB32 / 32;
     constexpr int HALO = IHA * IWA * GPA, NLD = (HALO + NTA - 1) / NTA;  // the A waves stage the halo
     constexpr int HB = IHA * IWA * PSA, MBUF = FA * MW * PSB;
@@ -561,12 +606,12 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_ws(PairKArgs pk) {
 
     // once: this wave's layer's weights, bias and multipliers; the first two halos (A) or the first residual (B);
     // the zero channels of both LDS tiles
-    constexpr int NWR = 9 * (MA > MB ? MA : MB);
+    constexpr int NWR = KA > 9 * MB ? KA : 9 * MB;
     h8 wr[NWR];
     float bias[4], neg[4];
     {
         const ConvKArgs& l = is_a ? a : b;
-        const int blk = is_a ? wa : wb, nk = is_a ? 9 * MA : 9 * MB, co = is_a ? coa : cob;
+        const int blk = is_a ? wa : wb, nk = is_a ? KA : 9 * MB, co = is_a ? coa : cob;
         const h8* wp = reinterpret_cast<const h8*>(l.wpk) + (size_t)blk * nk * 64 + lane;
 #pragma unroll
         for (int s = 0; s < NWR; s++) wr[s] = wp[(s < nk ? s : 0) * 64];
@@ -596,7 +641,7 @@ __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_pair_ws(PairKArgs pk) {
                 int img, oy0, ox0;
                 tile_origin(first + s * G, img, oy0, ox0);
                 f4 acc[FA];
-                pair_chain<FA, SA, MA, IWA, PSA>(acc, wr, hin + (s & 1) * HB + (lx * SA) * PSA + (lane >> 4) * 8);
+                a_chain<FA, SA, MA, CPA, IWA, PSA>(acc, wr, hin + (s & 1) * HB + (lx * SA) * PSA, lane);
                 uint16_t* m = mid + (s & 1) * MBUF;
 #pragma unroll
                 for (int f = 0; f < FA; f++) {
@@ -656,49 +701,49 @@ inline bool pair_buffer_ok(const PairKArgs& pk) {
            (!ext || view_bytes(pout, b.rcs, b.rc0, b.cout) < lim);
 }
 
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int CPA = 32>
 hipError_t launch_pair_ws(const PairKArgs& pk, dim3 grid, hipStream_t s) {
     if (pair_buffer_ok(pk)) {
-        hipLaunchKernelGGL((conv_pair_ws<SA, CA32, CB32, NBA, NBB, TH>), grid, dim3(64 * (NBA + NBB)), 0, s, pk);
+        hipLaunchKernelGGL((conv_pair_ws<SA, CA32, CB32, NBA, NBB, TH, CPA>), grid, dim3(64 * (NBA + NBB)), 0, s, pk);
         return hipGetLastError();
     }
     // views the buffer loop cannot serve: one workgroup per tile
     grid.x = (unsigned)(pk.b.n * pk.b.tiles_y * pk.b.tiles_x);
     const dim3 block(64 * (NBA > NBB ? NBA : NBB));
     if (pk.a.xvec)
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, 1, true>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, 1, true, false, CPA>), grid, block, 0, s, pk);
     else
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, 1, false>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, 1, false, false, CPA>), grid, block, 0, s, pk);
     return hipGetLastError();
 }
 
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, int CPA = 32>
 hipError_t launch_pair_p(const PairKArgs& pk, dim3 grid, hipStream_t s) {
     const dim3 block(64 * (NBA > NBB ? NBA : NBB) * WM);
     if (pair_buffer_ok(pk)) {
-        hipLaunchKernelGGL((conv_pair_p<SA, CA32, CB32, NBA, NBB, TH, WM>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair_p<SA, CA32, CB32, NBA, NBB, TH, WM, CPA>), grid, block, 0, s, pk);
         return hipGetLastError();
     }
     grid.x = (unsigned)(pk.b.n * pk.b.tiles_y * pk.b.tiles_x);  // one workgroup per tile
     if (pk.a.xvec)
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true, false, CPA>), grid, block, 0, s, pk);
     else
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false, false, CPA>), grid, block, 0, s, pk);
     return hipGetLastError();
 }
 
-template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM>
+template <int SA, int CA32, int CB32, int NBA, int NBB, int TH, int WM, int CPA = 32>
 hipError_t launch_pair(const PairKArgs& pk, dim3 grid, hipStream_t s) {
     const dim3 block(64 * (NBA > NBB ? NBA : NBB) * WM);
     if (pk.a.film) {  // FiLM on the input: its own instantiations, so the others stage as before
         if (pk.a.xvec)
-            hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true, true>), grid, block, 0, s, pk);
+            hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true, true, CPA>), grid, block, 0, s, pk);
         else
-            hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false, true>), grid, block, 0, s, pk);
+            hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false, true, CPA>), grid, block, 0, s, pk);
     } else if (pk.a.xvec) {
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, true, false, CPA>), grid, block, 0, s, pk);
     } else {
-        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false>), grid, block, 0, s, pk);
+        hipLaunchKernelGGL((conv_pair<SA, CA32, CB32, NBA, NBB, TH, WM, false, false, CPA>), grid, block, 0, s, pk);
     }
     return hipGetLastError();
 }

@@ -11,15 +11,20 @@ namespace {
 template <int I>
 PairLaunchFn pair_entry(const void** kernel) {
     constexpr PairCfg c = kPairCfgs[I];
+    constexpr int cp = c.cpa ? c.cpa : 32;
     if constexpr (c.persist == 2) {
-        if (kernel) *kernel = reinterpret_cast<const void*>(&conv_pair_ws<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th>);
-        return launch_pair_ws<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th>;
+        if (kernel)
+            *kernel = reinterpret_cast<const void*>(&conv_pair_ws<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, cp>);
+        return launch_pair_ws<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, cp>;
     } else if constexpr (c.persist) {
-        if (kernel) *kernel = reinterpret_cast<const void*>(&conv_pair_p<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm>);
-        return launch_pair_p<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm>;
+        if (kernel)
+            *kernel = reinterpret_cast<const void*>(&conv_pair_p<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm, cp>);
+        return launch_pair_p<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm, cp>;
     } else {
-        if (kernel) *kernel = reinterpret_cast<const void*>(&conv_pair<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm, true>);
-        return launch_pair<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm>;
+        if (kernel)
+            *kernel = reinterpret_cast<const void*>(
+                &conv_pair<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm, true, false, cp>);
+        return launch_pair<c.sa, c.ca32, c.cb32, c.nba, c.nbb, c.th, c.wm, cp>;
     }
 }
 
@@ -74,7 +79,7 @@ constexpr int find_pair(int sa, int ca32, int cb32, int nba, int nbb, int th, in
     for (int i = 0; i < kNumPair; i++) {
         const PairCfg& c = kPairCfgs[i];
         if (c.sa == sa && c.ca32 == ca32 && c.cb32 == cb32 && c.nba == nba && c.nbb == nbb && c.th == th &&
-            c.wm == wm && c.persist == persist)
+            c.wm == wm && c.persist == persist && c.cpa == 0)
             return i;
     }
     return -1;

@@ -227,6 +227,7 @@ class ConvPlan:
 PAIR_RES_MID = 1
 PAIR_AFFINE_OUT = 2
 PAIR_FILM_IN = 4
+PAIR_TAP32 = 0x400000
 
 
 class ConvPairPlan(ConvPlan):
@@ -236,10 +237,11 @@ class ConvPairPlan(ConvPlan):
     wave row; loop 1 one workgroup per tile, 2 a resident grid looping over tiles, 3 a resident grid with A and B
     on separate waves). affine_out: B's f16 output goes through the graph's affine_out op (2 / (1 + exp(-v)) - 1,
     rounded again) before it is stored; film_in: A's input goes through film_modulate as it is staged, with the FiLM
-    vectors given to run_film (which runs such a plan; run refuses it); both one workgroup per tile."""
+    vectors given to run_film (which runs such a plan; run refuses it); both one workgroup per tile. tap32: one tap
+    per K-step of A even where its few input channels could share K-steps (8 or 16 channels per tap)."""
 
     def __init__(self, desc_a: ConvDesc, w_a, bias_a, slope_a, desc_b: ConvDesc, w_b, bias_b, slope_b,
-                 res_mid=False, tile_rows=0, wave_rows=0, loop=0, affine_out=False, film_in=False):
+                 res_mid=False, tile_rows=0, wave_rows=0, loop=0, affine_out=False, film_in=False, tap32=False):
         L = load()
         self.desc, self.desc_b = desc_a, desc_b
         arrays = []
@@ -254,7 +256,8 @@ class ConvPairPlan(ConvPlan):
             arrays.append((wa, wp, ba, bp, sa, sp))
         (_, wpa, _, bpa, _, spa), (_, wpb, _, bpb, _, spb) = arrays
         flags = ((PAIR_RES_MID if res_mid else 0) | (PAIR_AFFINE_OUT if affine_out else 0) |
-                 (PAIR_FILM_IN if film_in else 0) | (int(tile_rows) << 8) | (int(wave_rows) << 16) | (int(loop) << 20))
+                 (PAIR_FILM_IN if film_in else 0) | (PAIR_TAP32 if tap32 else 0) | (int(tile_rows) << 8) |
+                 (int(wave_rows) << 16) | (int(loop) << 20))
         h = ctypes.c_void_p()
         _check(L.fhc_conv_pair_plan_create(ctypes.byref(desc_a), wpa, bpa, spa, ctypes.byref(desc_b), wpb, bpb,
                                            spb, flags, ctypes.byref(h)), "fhc_conv_pair_plan_create")

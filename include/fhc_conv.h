@@ -133,6 +133,11 @@ void fhc_conv_plan_destroy(fhc_conv_plan* plan);
  * in the one-workgroup-per-tile loop (bits 20-21 0 or 1), without an external residual for B. No counterpart in the
  * reference, which dispatches the op on its own. */
 #define FHC_PAIR_FILM_IN 4u
+/* A's K order. By default, where A has at most 8 (or 16) input channels (graph.json's enc.e1: 3, refine.q1: 14) and
+ * a configuration packs them, 4 (2) taps share each 32-wide K-step, each tap's channels padded to 8 (16): 3 (5) MFMA
+ * K-steps per output where one tap a step takes 9, the reference's dense K (buildb, ops/conv/kernels.rs:64-78,
+ * ⌈9 cin / 16⌉ 16) taken to whole taps. FHC_PAIR_TAP32 keeps one tap a step, channels padded to 32. */
+#define FHC_PAIR_TAP32 0x400000u
 int fhc_conv_pair_plan_create(const fhc_conv_desc* desc_a, const uint16_t* w_a, const uint16_t* bias_a,
                               const uint16_t* slope_a, const fhc_conv_desc* desc_b, const uint16_t* w_b,
                               const uint16_t* bias_b, const uint16_t* slope_b, uint32_t flags, fhc_conv_plan** out);

@@ -165,9 +165,16 @@ PAIR_LOOPS = {(2, 20, 30, 3, 36, 36, 2, "mid"): (1, 2, 3), (1, 16, 30, 36, 72, 7
 B_WEIGHT = 2.0 ** -6
 
 
-@pytest.mark.parametrize("p,loop", [(p, loop) for p in PAIR_SHAPES for loop in PAIR_LOOPS[p]],
-                         ids=lambda v: "x".join(map(str, v[:7])) if isinstance(v, tuple) else f"loop{v}")
-def test_fused_pair_all_ones_bit_exact(p, loop):
+# A's K order: with at most 8 (16) input channels the taps share K-steps by default (8 or 16 channels a tap), and
+# FHC_PAIR_TAP32 keeps one tap a step; both are run for those shapes
+PAIR_RUNS = [(p, loop, tap32) for p in PAIR_SHAPES for loop in PAIR_LOOPS[p] for tap32 in
+             ((False, True) if p[3] <= 16 else (False,))]
+
+
+@pytest.mark.parametrize("p,loop,tap32", PAIR_RUNS,
+                         ids=lambda v: "x".join(map(str, v[:7])) if isinstance(v, tuple) else
+                         ("tap32" if v is True else "packed" if v is False else f"loop{v}"))
+def test_fused_pair_all_ones_bit_exact(p, loop, tap32):
     import torch
     n, h, w, cin, cmid, cout, sa, res = p
     A = Case(n, h, w, cin, cmid, stride=sa, act=0, seed=77)
@@ -184,12 +191,72 @@ def test_fused_pair_all_ones_bit_exact(p, loop):
     assert np.isfinite(yb).all() and np.isfinite(ya).all()
     want = np.broadcast_to(yb[None, :, :, None], (n, A.hout, A.wout, cout)).view(np.uint16)
     plan = fhconv.ConvPairPlan(A.fhc_desc(), A.wt, A.bias, None, B.fhc_desc(), B.wt, B.bias, None,
-                               res_mid=res == "mid", loop=loop)
+                               res_mid=res == "mid", loop=loop, tap32=tap32)
+    d = plan.describe()
+    assert d["a_channels_per_tap"] == (32 if tap32 or cin > 16 else 8 if cin <= 8 else 16), d["name"]
     dev = torch.device("cuda", 0)
     x = torch.from_numpy(np.ascontiguousarray(A.x).view(np.int16)).to(dev)
     y = torch.zeros((n, A.hout, A.wout, cout), dtype=torch.int16, device=dev)
     plan.run(x, y, None)
     got = y.cpu().numpy().view(np.uint16)
-    say("pair all ones", p[:7], "loop", loop, plan.describe()["name"])
+    say("pair all ones", p[:7], "loop", loop, d["name"], "A K-steps", d["a_ksteps"])
     bad = np.argwhere(got != want)
     assert bad.size == 0, (plan.describe()["name"], len(bad), bad[0].tolist())
+
+
+# fused pairs with a delta input: unit inputs at scattered pixels and channels (at least 4 input pixels apart, so an
+# output of A meets at most one of them), random f16 weights for A, B the identity (its centre tap of input channel
+# co into output channel co is 1): every output of A is the one weight its delta meets, exactly, and B (with A's
+# output as its residual where the pair has one) passes it on exactly, doubled with the residual. A wrong (tap,
+# channel) position in A's K order, packed or one tap a step, moves a weight to another pixel or channel.
+DELTA_PAIRS = [((2, 22, 34, 3, 36, 36, 2, "mid"), (1, 2, 3)), ((1, 17, 29, 14, 24, 24, 1, None), (1, 2, 3)),
+               ((1, 19, 27, 8, 24, 24, 1, None), (1,)), ((1, 21, 33, 16, 24, 24, 1, None), (1,))]
+DELTA_RUNS = [(p, loop, tap32) for p, loops in DELTA_PAIRS for loop in loops for tap32 in (False, True)]
+
+
+@pytest.mark.parametrize("p,loop,tap32", DELTA_RUNS,
+                         ids=lambda v: "x".join(map(str, v[:7])) if isinstance(v, tuple) else
+                         ("tap32" if v is True else "packed" if v is False else f"loop{v}"))
+def test_fused_pair_delta_input_bit_exact(p, loop, tap32):
+    import torch
+    n, h, w, cin, cmid, cout, sa, res = p
+    rng = np.random.default_rng(90 + cin + loop)
+    A = Case(n, h, w, cin, cmid, stride=sa, act=0, seed=91)
+    B = Case(n, A.hout, A.wout, cmid, cout, act=0, residual=res is not None, seed=92)
+    x = np.zeros((n, h, w, cin), np.float32)
+    deltas = [(i, yy, xx, int(rng.integers(cin))) for i in range(n) for yy in range(1, h, 4) for xx in range(2, w, 4)]
+    for i, yy, xx, ch in deltas:
+        x[i, yy, xx, ch] = 1.0
+    A.x, A.bias = f16(x), f16(np.zeros(cmid))
+    A.wt = f16(rng.uniform(-1, 1, (cmid, cin, 3, 3)))
+    wid = np.zeros((cout, cmid, 3, 3), np.float32)
+    for co in range(cout):
+        wid[co, co, 1, 1] = 1.0
+    B.wt, B.bias = f16(wid), f16(np.zeros(cout))
+    wa = A.wt.view(np.float16).astype(np.float32)
+    ya = np.zeros((n, A.hout, A.wout, cmid), np.float32)
+    for i, yy, xx, ch in deltas:
+        for ky in range(3):
+            for kx in range(3):
+                oy, ox = yy + 1 - ky, xx + 1 - kx  # the output whose tap (ky, kx) meets the delta
+                if oy % sa or ox % sa:
+                    continue
+                oy, ox = oy // sa, ox // sa
+                if 0 <= oy < A.hout and 0 <= ox < A.wout:
+                    assert ya[i, oy, ox].max() == 0 and ya[i, oy, ox].min() == 0, "deltas too close"
+                    ya[i, oy, ox] = wa[:, ch, ky, kx]
+    yb = ya * 2 if res == "mid" else ya  # f16 values doubled: exact
+    want = f16(yb)
+    plan = fhconv.ConvPairPlan(A.fhc_desc(), A.wt, A.bias, None, B.fhc_desc(), B.wt, B.bias, None,
+                               res_mid=res == "mid", loop=loop, tap32=tap32)
+    d = plan.describe()
+    # the packed configurations: 8 channels a tap for the stride-2 encoder pair, 16 for the stride-1 refine pair
+    assert d["a_channels_per_tap"] == (32 if tap32 else 8 if sa == 2 else 16), d["name"]
+    dev = torch.device("cuda", 0)
+    xd = torch.from_numpy(np.ascontiguousarray(A.x).view(np.int16)).to(dev)
+    y = torch.zeros((n, A.hout, A.wout, cout), dtype=torch.int16, device=dev)
+    plan.run(xd, y, None)
+    got = y.cpu().numpy().view(np.uint16)
+    say("pair delta", p[:7], "loop", loop, d["name"], len(deltas), "deltas")
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, (d["name"], len(bad), bad[0].tolist())

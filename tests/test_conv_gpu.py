@@ -378,14 +378,17 @@ PAIR_CASES = [(2, 50, 90, 3, 36, 36, 2, 1, 1, "mid", (8, 0), None),
 # the encoder's second pair (36 -> 72 -> 72, stride 2, A's output as B's residual): tiles of 1 or 2 rows
 PAIR_CASES_E3 = [(2, 61, 107, 36, 72, 72, 2, 1, 1, "mid", (40, 0), None),
                  (1, 19, 29, 36, 72, 72, 2, 1, 1, "mid", None, (80, 8))]
-PAIR_RUNS = [(c, th, wm) for c in PAIR_CASES for th, wm in ((2, 1), (4, 1), (2, 2), (4, 2))] + \
-    [(c, th, 1) for c in PAIR_CASES_E3 for th in (1, 2)]
+# A's K order: cases with at most 16 input channels pack taps into K-steps at one wave row (8 or 16 channels a
+# tap), and run once more with one tap a step (FHC_PAIR_TAP32); at two wave rows only one tap a step is instantiated
+PAIR_RUNS = [(c, th, wm, False) for c in PAIR_CASES for th, wm in ((2, 1), (4, 1), (2, 2), (4, 2))] + \
+    [(c, th, 1, True) for c in PAIR_CASES if c[3] <= 16 for th in (2, 4)] + \
+    [(c, th, 1, False) for c in PAIR_CASES_E3 for th in (1, 2)]
 
 
-@pytest.mark.parametrize("case,th,wm", PAIR_RUNS,
+@pytest.mark.parametrize("case,th,wm,tap32", PAIR_RUNS,
                          ids=lambda v: "x".join(map(str, v[:7])) + (f"-{v[9]}" if v[9] else "")
-                         if isinstance(v, tuple) else str(v))
-def test_pair_matches_the_two_convs(case, th, wm):
+                         if isinstance(v, tuple) else ("tap32" if v is True else "" if v is False else str(v)))
+def test_pair_matches_the_two_convs(case, th, wm, tap32):
     # the fused pair against the oracle run twice (A, then B on A's f16 output): ragged tiles, stride 2, a residual
     # from A's output or from a tensor, a padded input view with NaN past cin, an output view inside a wider tensor
     import torch
@@ -398,10 +401,13 @@ def test_pair_matches_the_two_convs(case, th, wm):
         B.res = ya
     want = B.run_oracle(threads=8)
     plan = fhconv.ConvPairPlan(A.fhc_desc(), A.wt, A.bias, A.slope if act_a == 1 else None, B.fhc_desc(), B.wt, B.bias,
-                               B.slope if act_b == 1 else None, res_mid=res == "mid", tile_rows=th, wave_rows=wm)
+                               B.slope if act_b == 1 else None, res_mid=res == "mid", tile_rows=th, wave_rows=wm,
+                               tap32=tap32)
     d = plan.describe()
     say("pair", case, d["name"], d["grid"], d["tiles"])
     assert d["family"] == "pair" and d["tile_rows"] == th and d["wave_rows"] == wm
+    packed = not tap32 and wm == 1 and cin <= 16
+    assert d["a_channels_per_tap"] == ((8 if cin <= 8 else 16) if packed else 32), d["name"]
     dev = torch.device("cuda", 0)
     x = torch.from_numpy(np.ascontiguousarray(A.x).view(np.int16)).to(dev)
     y = torch.from_numpy(np.ascontiguousarray(B.y0).view(np.int16)).to(dev)
