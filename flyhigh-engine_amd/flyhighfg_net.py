@@ -220,6 +220,7 @@ class GpuBackend(ComposedChains):
         import fhops
         self.torch, self.fhconv, self.fh = torch, fhconv, fhops
         self.W, self.fuse, self.dev, self.chains, self.exact_render = W, fuse, device, chains, exact_render
+        self.convs = dict(CONVS)  # conv layer -> (cin, cout, stride, act); a replayed plan adds its own
         self.stream = stream if stream is not None else torch.cuda.current_stream()
         self.plans: Dict[tuple, object] = {}
         self.gs: Dict[int, object] = {}  # FiLM vector slots (one per phase of a batched program)
@@ -280,7 +281,7 @@ class GpuBackend(ComposedChains):
         return n * h * w
 
     def _desc(self, name, x: V, y: V, res: Optional[V], mid_res=False):
-        cin, cout, stride, act = CONVS[name]
+        cin, cout, stride, act = self.convs[name]
         n, h, w, xcs = x.buf.shape
         ycs = y.buf.shape[3]
         return self.fhconv.make_desc(n, h, w, cin, cout, stride=stride, act=act, residual=res is not None or mid_res,
@@ -476,7 +477,8 @@ class GpuBackend(ComposedChains):
     def render(self, a: V, b: V, flow: V, vis: V, rt: V, out: V, cubic: bool, flags: int, fsx=None, fsy=None):
         fsx = flow.scale if fsx is None else fsx
         fsy = flow.scale if fsy is None else fsy
-        va, vb, vf, vv, vr, vo = (self._v(t) for t in (a, b, flow, vis, rt, out))
+        # the flow's scale is carried by fsx, fsy (render_pix multiplies the raw flow by them)
+        va, vb, vf, vv, vr, vo = (self._v(t) for t in (a, b, V(flow.buf, flow.c0), vis, rt, out))
         self._go("render_pix", lambda: self.fh.render(va, vb, vf, vv, vr, cubic, flags, fsx, fsy, out=vo,
                                                       stream=self.stream),
                  2 * (3 * 3 * self._px(out) + 10 * self._px(flow)))
@@ -885,18 +887,24 @@ def conv_layer(weight_name: str) -> str:
     raise ValueError(f"not a conv weight: {weight_name}")
 
 
-def weights_from_model(model) -> dict:
+def weights_from_model(model, plan: Optional[dict] = None) -> dict:
     """The model's weights (fhmodel.Model, the manifest's f16 tensors) in make_weights' form: conv layer -> (w OIHW,
-    bias, slope or None) as f16 bits, "film" -> (w1, b1, w2, b2) as f32 (model/blob.rs:32-41 decodes to f32)."""
+    bias, slope or None) as f16 bits, "film" -> (w1, b1, w2, b2) as f32 (model/blob.rs:32-41 decodes to f32). The
+    layers are FlyHighFG's, or with a plan those of its conv steps (and the FiLM MLP where the model has one)."""
     W = {}
-    for name, (_, _, _, act) in CONVS.items():
-        w = model.weight(f"{name}.0.weight" if act else f"{name}.weight")
-        b = model.weight(f"{name}.0.bias" if act else f"{name}.bias")
-        s = model.weight(f"{name}.1.weight") if act else None
-        W[name] = (w, b, s)
+    if plan is None:
+        layers = [(name, act, f"{name}.0.weight" if act else f"{name}.weight",
+                   f"{name}.0.bias" if act else f"{name}.bias", f"{name}.1.weight" if act else None)
+                  for name, (_, _, _, act) in CONVS.items()]
+    else:
+        layers = [(conv_layer(s["weight"]), s["act"], s["weight"], s["bias"], s["slope"])
+                  for s in plan["steps"] if s["op"] == "conv"]
+    for name, act, wn, bn, sn in layers:
+        W[name] = (model.weight(wn), model.weight(bn), model.weight(sn) if act else None)
     f32 = lambda n: model.weight(n).view(np.float16).astype(np.float32)  # noqa: E731
-    W["film"] = (f32("film.film.0.weight").reshape(-1), f32("film.film.0.bias"), f32("film.film.2.weight"),
-                 f32("film.film.2.bias"))
+    if plan is None or any(s["op"] == "film_mlp" for s in plan["steps"]):
+        W["film"] = (f32("film.film.0.weight").reshape(-1), f32("film.film.0.bias"), f32("film.film.2.weight"),
+                     f32("film.film.2.bias"))
     return W
 
 
@@ -910,6 +918,13 @@ class GraphProgram:
 
     def __init__(self, be, plan: dict, cubic: bool = True, render_flags: int = 0):
         self.be, self.plan, self.cubic, self.render_flags = be, plan, cubic, render_flags
+        # the plan's convs join the backend's table (a model other than FlyHighFG brings its own layers)
+        for s in plan["steps"]:
+            if s["op"] == "conv":
+                name, shape = conv_layer(s["weight"]), (s["cin"], s["cout"], s["stride"], s["act"])
+                if be.convs.setdefault(name, shape) != shape:
+                    raise ValueError(f"{name}: the graph's conv {shape} differs from the program's "
+                                     f"{be.convs[name]}")
         fw, fh = plan["frame"]
         self.frames, self.rgba = be.frames(2, fh, fw), be.frames(1, fh, fw)
         self.bufs = [be.zeros(1, b["h"], b["w"], pad8(b["c"])) for b in plan["buffers"]]
@@ -921,10 +936,12 @@ class GraphProgram:
     def _v(self, v: dict) -> V:
         return V(self.bufs[v["buf"]], v["c0"], v["scale"])
 
-    def run(self, t: float, W: dict):
+    def run(self, t: float, W: dict, steps=None):
+        """The plan's steps (or those of the index range `steps`) over the backend at phase t."""
         be, P = self.be, self.plan
-        be.set_g(film_mlp(W, t))
-        for s in P["steps"]:
+        if "film" in W:
+            be.set_g(film_mlp(W, t))
+        for s in (P["steps"] if steps is None else [P["steps"][i] for i in steps]):
             op, ins, out = s["op"], [self._v(v) for v in s["in"]], self._v(s["out"])
             c = s["out"]["c"]
             ob = P["buffers"][s["out"]["buf"]]
@@ -936,9 +953,6 @@ class GraphProgram:
                 be.interp(ins[0], c, out, ob["h"], ob["w"], s["antialias"])
             elif op == "conv":
                 name = conv_layer(s["weight"])
-                if CONVS[name] != (s["cin"], s["cout"], s["stride"], s["act"]):
-                    raise ValueError(f"{name}: the graph's conv {s['cin'], s['cout'], s['stride'], s['act']} differs "
-                                     f"from the program's {CONVS[name]}")
                 res = None if s["residual"] is None else self._v(s["residual"])
                 be.conv(name, ins[0], out, res)
             elif op == "mat":

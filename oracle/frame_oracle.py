@@ -19,6 +19,7 @@ from flyhighfg_net import CONVS, ComposedChains, cpu_threads  # noqa: E402
 class CpuBackend(ComposedChains):
     def __init__(self, W):
         self.W, self.threads, self.gs, self.g_slot = W, cpu_threads(), {}, 0
+        self.convs = dict(CONVS)  # conv layer -> (cin, cout, stride, act); a replayed plan adds its own
 
     def zeros(self, n, h, w, cs):
         return np.zeros((n, h, w, cs), np.uint16)
@@ -56,7 +57,7 @@ class CpuBackend(ComposedChains):
         out.buf[..., out.c0:out.c0 + c] = y.reshape(out.buf.shape[:3] + (c,))
 
     def conv(self, name, x, y, res=None):
-        cin, cout, stride, act = CONVS[name]
+        cin, cout, stride, act = self.convs[name]
         n, h, w, xcs = x.buf.shape
         d = oracle.make_desc(n, h, w, cin, cout, stride=stride, act=act, residual=res is not None, x_cstride=xcs,
                              x_c0=x.c0, y_cstride=y.buf.shape[3], y_c0=y.c0,

@@ -352,3 +352,48 @@ def test_autotune_of_a_model_fills_the_choice_table():
         assert mdl.autotune(1, (64, 64), (64, 64), n=n, reps=3) == len(shapes) == 3
         for s in shapes:
             assert fhconv.load().fhc_tune_get_ex(*s) >= 0, s
+
+
+# ---- a model of this library's own making whose plan holds every step kind (tests/synthetic_graph.py) ------------
+
+@pytest.mark.parametrize("frame", [(128, 64), (300, 140)], ids=["network-size", "internal-size"])
+def test_synthetic_plan_holds_every_step_kind(frame):
+    """The plan walk over the synthetic model emits every step kind (frame input and, in the internal-size mode,
+    its downscale; convs with and without activation and residual; views materialised; concat with a zeros buffer;
+    the ops; the repair; the frame output), the repeat body K = 2 times, the pair / mid boundary at film_mlp."""
+    import synthetic_graph as sg
+    g, m, b = sg.model_bytes(0)
+    mdl = fhmodel.Model.from_bytes(g, m, b)
+    plan = mdl.plan(2, frame, (128, 64), repair=1)
+    kinds = {s["op"] for s in plan["steps"]}
+    assert kinds == sg.STEP_KINDS, kinds ^ sg.STEP_KINDS
+    assert plan["internal"] == (frame != (128, 64))
+    convs = [s for s in plan["steps"] if s["op"] == "conv"]
+    assert sum(s["weight"] == "s.rd.weight" for s in convs) == 2                  # the repeat body twice
+    assert [s["weight"] for s in convs if s["residual"]] == ["s.e2.0.weight", "s.rd.weight", "s.rd.weight"]
+    stages = [s["stage"] for s in plan["steps"]]
+    first_mid = stages.index("mid")
+    assert "mid" not in stages[:first_mid] and "pair" not in stages[first_mid:]
+    assert plan["steps"][first_mid]["op"] in ("gmhs", "film_mlp")
+    assert [s["op"] for s in plan["steps"] if s["op"] in ("film_mlp", "gmhs")] == ["gmhs", "film_mlp"]
+    assert sum(s["op"] == "interp" for s in plan["steps"]) == (4 if plan["internal"] else 2)
+
+
+def test_synthetic_plan_replays_over_the_oracle():
+    """GraphProgram takes the synthetic model's own convs (names and shapes from the plan, weights from the model)
+    and runs every step over the oracle backend: finite maps, a whole RGBA8 frame."""
+    import synthetic_graph as sg
+    import flyhighfg_net as net
+    from frame_oracle import CpuBackend
+    g, m, b = sg.model_bytes(0)
+    mdl = fhmodel.Model.from_bytes(g, m, b)
+    plan = mdl.plan(2, (300, 140), (128, 64), repair=1)
+    W = net.weights_from_model(mdl, plan)
+    assert set(W) == {"s.e1", "s.e2", "s.h0", "s.fl", "s.vi", "s.hh", "s.rd", "s.fd", "s.vc", "up.w", "s.r1", "s.r2",
+                      "film"}
+    gp = net.GraphProgram(CpuBackend(W), plan)
+    gp.frames[...] = net.pair_frames(300, 140, 3, shift=5)
+    gp.run(0.4, W)
+    for name in ("up7", "rt", "flow", "hh", "cin"):
+        assert np.isfinite(gp.named[name].view(np.float16)).all(), name
+    assert np.all(gp.rgba >> 24 == 255) and len(np.unique(gp.rgba)) > 1000
