@@ -1212,6 +1212,14 @@ __device__ __forceinline__ float bil4m(float v00, float v01, float v10, float v1
     const float gx = 1.0f - fx;
     return mac<true>(mac<true>(v11, fx, v10 * gx), fy, mac<true>(v01, fx, v00 * gx) * (1.0f - fy));
 }
+// bil4m<true> with the four taps as f16: each product v * g is written as an FMA with a zero addend (the same value
+// up to the sign of a zero product, which no later step can see), so every conversion folds into a mixed-precision
+// FMA and no tap needs a conversion instruction of its own
+__device__ __forceinline__ float bil4h(_Float16 v00, _Float16 v01, _Float16 v10, _Float16 v11, float fx, float fy) {
+    const float gx = 1.0f - fx;
+    return __builtin_fmaf(__builtin_fmaf((float)v11, fx, __builtin_fmaf((float)v10, gx, 0.0f)), fy,
+                          __builtin_fmaf((float)v01, fx, __builtin_fmaf((float)v00, gx, 0.0f)) * (1.0f - fy));
+}
 template <bool FMA>
 __device__ __forceinline__ float cub1m(float x) {
     if constexpr (!FMA) return cub1(x);
@@ -1325,8 +1333,15 @@ __device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const flo
                                                uint32_t h, uint32_t pitch, const float* tab, uint32_t flags,
                                                uint32_t* dst, uint32_t opitch) {
     const float m = fmaxf(v[0], fmaxf(v[1], v[2]));
-    const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
-    const float wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
+    float wa_w, wb_w;
+    if constexpr (FMA) {  // the hardware exponential and reciprocal (s >= 1: the largest term is exp(0))
+        const float e0 = __expf(v[0] - m), e1 = __expf(v[1] - m), e2 = __expf(v[2] - m);
+        const float inv = __builtin_amdgcn_rcpf(e0 + e1 + e2);
+        wa_w = (e0 + 0.5f * e2) * inv, wb_w = (e1 + 0.5f * e2) * inv;
+    } else {
+        const float e0 = expf(v[0] - m), e1 = expf(v[1] - m), e2 = expf(v[2] - m), s = e0 + e1 + e2;
+        wa_w = (e0 + 0.5f * e2) / s, wb_w = (e1 + 0.5f * e2) / s;
+    }
     float ca[3], cb[3];
     const float gxa = (float)x + f[0], gya = (float)y + f[1], gxb = (float)x + f[2], gyb = (float)y + f[3];
     const int pxa = (int)floorf(gxa), pya = (int)floorf(gya), pxb = (int)floorf(gxb), pyb = (int)floorf(gyb);
@@ -1415,6 +1430,32 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
     float fq[4][4], vq[4][3], rq[4][3];
     const uint32_t nq = hq * wq;
     const auto rfl = buf_rsrc(fl.p, QV ? nq * 16u : 0u), rrt = buf_rsrc(rt.p, QV ? nq * rt.cs * 2u : 0u);
+    float f[4], v[3], r[3];
+    if constexpr (QV && FMA) {  // the taps stay f16 and feed bil4h
+        _Float16 hq4[4][8], hr4[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rfl, qs[k] * 16u, 0, 0));
+            const uint2 b =
+                __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rrt, (qs[k] * rt.cs + rt.c0) * 2u, 0, 0));
+            const uint32_t wv[6] = {a.x, a.y, a.z, a.w, b.x, b.y};
+#pragma unroll
+            for (int c = 0; c < 8; c++) hq4[k][c] = __builtin_bit_cast(_Float16, (uint16_t)(wv[c >> 1] >> (16 * (c & 1))));
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                hr4[k][c] = __builtin_bit_cast(_Float16, (uint16_t)(wv[4 + (c >> 1)] >> (16 * (c & 1))));
+        }
+#pragma unroll
+        for (uint32_t c = 0; c < 4; c++)
+            f[c] = bil4h(hq4[0][c], hq4[1][c], hq4[2][c], hq4[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
+#pragma unroll
+        for (uint32_t c = 0; c < 3; c++) {
+            v[c] = bil4h(hq4[0][4 + c], hq4[1][4 + c], hq4[2][4 + c], hq4[3][4 + c], qfx, qfy) * vis.scale;
+            r[c] = bil4h(hr4[0][c], hr4[1][c], hr4[2][c], hr4[3][c], qfx, qfy);
+        }
+        render_rgba_px<CUBIC, FL, FMA>(x, y, f, v, r, fa, fb, w, h, pitch, tab, flags, dst, opitch);
+        return;
+    }
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         if constexpr (QV) {
@@ -1434,7 +1475,6 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
             for (uint32_t c = 0; c < 3; c++) vq[k][c] = ld(vis, qs[k], c), rq[k][c] = ld(rt, qs[k], c);
         }
     }
-    float f[4], v[3], r[3];
 #pragma unroll
     for (uint32_t c = 0; c < 4; c++)
         f[c] = bil4m<FMA>(fq[0][c], fq[1][c], fq[2][c], fq[3][c], qfx, qfy) * ((c & 1u) == 0 ? fsx : fsy);
