@@ -83,7 +83,7 @@ hipError_t splitk_reduce_launch(const ConvKArgs& a, int ksplit, hipStream_t s);
 struct GemmCfg {
     int s, ck, fm, na, wm, wn, st;
 };
-constexpr int kNumGemm = 13;
+constexpr int kNumGemm = 14;
 inline constexpr GemmCfg kGemmCfgs[kNumGemm] = {
     {1, 32, 4, 2, 2, 2, 3},  // 0: TH 8, BN 64, 4 waves
     {1, 32, 2, 2, 4, 2, 2},  // 1: TH 8, BN 64, 8 waves
@@ -98,6 +98,10 @@ inline constexpr GemmCfg kGemmCfgs[kNumGemm] = {
     {1, 64, 2, 2, 4, 1, 2},  // 10: TH 8, BN 32, 4 waves, 64-channel chunks
     {1, 32, 2, 3, 4, 1, 2},  // 11: as 7 with two buffers
     {1, 32, 4, 2, 2, 2, 2},  // 12: as 0 with two buffers
+    // 4 rows x 3 channel blocks a wave: 12 accumulators, each LDS operand read feeding 4 MFMAs (weights) or up to
+    // 9 (halo rows); measured fastest where the image batch is large and cin is a few K-chunks (155 -> 48 at
+    // 8 x 60 x 108)
+    {1, 32, 4, 3, 4, 1, 2},  // 13: TH 16, BN 48, 4 waves
 };
 // The launcher of the deep-layer configuration `index`, or nullptr; *kernel receives the kernel's address.
 LaunchFn gemm_launcher(int index, const void** kernel);
