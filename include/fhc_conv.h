@@ -86,12 +86,15 @@ int fhc_conv_run(const fhc_conv_plan* plan, const void* x, void* y, const void* 
 /* fhc_conv_run without a workspace argument, for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, hosts that forbid hipMalloc). No counterpart in the reference. The plan's scratch
  * (the split-K partials, fhc_conv_workspace_bytes) comes from a device array the library holds, one per GPU for the
- * life of the process, of FHC_STATIC_SCRATCH_BYTES; a plan that needs more is refused with an error status. The call
+ * life of the process, of FHC_STATIC_SCRATCH_BYTES; a plan that needs more is refused with an error status. The array
+ * is a file-scope device variable of the library: its memory is reserved on every GPU the library's code is loaded
+ * onto, whether or not the process ever calls this function. 32 MiB holds the largest split-K plan of the 1080p
+ * frame's layers (the 1080p/16 128 -> 128 conv split 8 ways: 33,423,360 bytes of f32 partials). The call
  * allocates nothing. Every call on one GPU shares that GPU's array: calls whose plans need scratch and that may
  * overlap on one GPU (other streams, other threads) race on it, so run them in one stream order. The array keeps
  * the last call's partials; every partial a call reads it has written itself first. Plans without scratch run
  * exactly as fhc_conv_run runs them. */
-#define FHC_STATIC_SCRATCH_BYTES (64u << 20)
+#define FHC_STATIC_SCRATCH_BYTES (32u << 20)
 int fhc_conv_run_noalloc(const fhc_conv_plan* plan, const void* x, void* y, const void* res, void* stream);
 
 /* JSON description of the plan: variant, tile, split-K, grid, packed sizes, algorithmic FLOPs and bytes. Returns

@@ -54,7 +54,7 @@ def test_noalloc_without_scratch_and_beyond_its_limit():
     import torch
     big = Case(1, 272, 480, 128, 128, act=1, seed=34)
     plan = fhconv.ConvPlan(big.fhc_desc(ksplit=4), big.wt, big.bias, big.slope)
-    limit = 64 << 20
+    limit = 32 << 20
     say("noalloc beyond the limit:", plan.workspace_bytes, "bytes")
     assert plan.workspace_bytes > limit
     dev = torch.device("cuda", 0)
