@@ -56,6 +56,39 @@ def run_frames(be, W, net_w, net_h, fr, t=0.5, repair=0):
     return f
 
 
+def test_film_mlp_closed_forms():
+    """film_mlp (the reference's host MLP, net/build.rs:332-340: hv[i] = max(w1[i] t + b1[i], 0) in f32, then
+    g[o] = b2[o] + the f32 sum of w2[o][i] hv[i] in index order, stored as f16) on weights whose result is known in
+    closed form, chosen so that a transposed w2, a dropped bias, a wrong relu or a sum in another order each gives
+    other values."""
+    H, O = net.FILM_HIDDEN, net.FILM_OUT
+    i, o = np.arange(H), np.arange(O)
+    # a shifted one-hot w2 (row o reads hidden unit (o + 1) % 64; rows 64.. read none), a ramp of b1, a ramp of b2:
+    # at t = 0.5, hv[i] = max(0.5 - i / 64, 0) and g[o] = o / 256 + hv[(o + 1) % 64] for o < 64, o / 256 after
+    w1 = np.ones(H, np.float32)
+    b1 = (-i / 64).astype(np.float32)
+    w2 = np.zeros((O, H), np.float32)
+    w2[o[:H], (o[:H] + 1) % H] = 1
+    b2 = (o / 256).astype(np.float32)
+    W = {"film": (w1, b1, w2, b2)}
+    hv = np.maximum(0.5 - i / 64, 0)
+    want = o / 256 + np.where(o < H, hv[(o + 1) % H], 0)
+    assert np.array_equal(net.film_mlp(W, 0.5), f16_bits(want))
+    # t = 0: every hidden unit is cut off (b1 <= 0), so g = b2; t = 1.25: hv[i] = 1.25 - i / 64 for all i
+    assert np.array_equal(net.film_mlp(W, 0.0), f16_bits(o / 256))
+    want1 = o / 256 + np.where(o < H, 1.25 - ((o + 1) % H) / 64, 0)
+    assert np.array_equal(net.film_mlp(W, 1.25), f16_bits(want1))
+    # the sum's order: products 2^24, 1, 1, -2^24 add to 0 in index order (2^24 + 1 rounds back to 2^24 twice),
+    # to 1 pairwise ((2^24 + 1) + (1 - 2^24)) and to 2 from the end
+    w1 = np.zeros(H, np.float32)
+    b1 = np.zeros(H, np.float32)
+    b1[:4] = 1
+    w2 = np.zeros((O, H), np.float32)
+    w2[:, :4] = [2.0 ** 24, 1, 1, -2.0 ** 24]
+    b2 = np.full(O, 0.5, np.float32)
+    assert np.array_equal(net.film_mlp({"film": (w1, b1, w2, b2)}, 0.7), f16_bits(np.full(O, 0.5)))
+
+
 def test_program_runs_on_the_oracle_backend():
     W = net.make_weights(1)
     f = run(CpuBackend(W), W, 128, 64, inputs(1, 128, 64))
