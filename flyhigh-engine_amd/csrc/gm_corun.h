@@ -16,8 +16,9 @@ struct GmCoRun {
 };
 
 // fhc_gmhs with round 0 of the fit launched by co->fn beside co's pair, and round 1 by co->cfn beside co's conv
-// (when given), when co is not null
+// (when given), when co is not null; fhc_gmhs_n's `pairs` pairs (co null) otherwise
 int gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
-             uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, const GmCoRun* co, void* stream);
+             uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, const GmCoRun* co, void* stream,
+             uint32_t pairs = 1);
 
 }  // namespace fhc

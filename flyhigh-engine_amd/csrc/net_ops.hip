@@ -445,10 +445,11 @@ __global__ __launch_bounds__(kThreads) void interp_aa_kernel(View x, OView out, 
 // last row / column with the same values), so it takes one memory round trip. The per-output sum is the one above.
 constexpr uint32_t kAaT = 16, kAaR = 5, kAaExt = kAaT * kAaR;
 
-// PYR (3 channels, a batch of the two pictures): the tile's outputs also go through the pair() pyramid (avgpool k 2
-// twice and the luma, graph.json ops 14-18, 21-24) from LDS: a 16 x 16 tile holds whole 2 x 2 and 4 x 4 blocks, so
-// i8 (8 x 8 of them), i16 (4 x 4, into channels 3 * image of its view) and l16 (channel image) need no other
-// launch; each pool reads the f16 values the previous stage stores, in avgpool's order.
+// PYR (3 channels, pairs of pictures: images 2k, 2k + 1 are pair k's): the tile's outputs also go through the pair()
+// pyramid (avgpool k 2 twice and the luma, graph.json ops 14-18, 21-24) from LDS: a 16 x 16 tile holds whole 2 x 2
+// and 4 x 4 blocks, so i8 (8 x 8 of them), i16 (4 x 4, into channels 3 * (image % 2) of its image k) and l16
+// (channel image % 2 of image k) need no other launch; each pool reads the f16 values the previous stage stores, in
+// avgpool's order.
 struct PyrOut {
     OView i8, i16, l16;
 };
@@ -562,9 +563,10 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
                     const float a = ((0.0f + b[ch]) + b[3 + ch]) + b[8 * 3 + ch] + b[8 * 3 + 3 + ch];
                     const uint16_t hv = f2h(a / 4.0f);
                     v[ch] = h2f(hv);
-                    pyr.i16.p[((size_t)y16 * w16 + x16) * pyr.i16.cs + pyr.i16.c0 + 3 * img + ch] = hv;
+                    pyr.i16.p[(((size_t)(img / 2) * h16 + y16) * w16 + x16) * pyr.i16.cs + pyr.i16.c0 + 3 * (img % 2) +
+                              ch] = hv;
                 }
-                st(pyr.l16, (size_t)y16 * w16 + x16, img, lum3(v[0], v[1], v[2]));
+                st(pyr.l16, ((size_t)(img / 2) * h16 + y16) * w16 + x16, img % 2, lum3(v[0], v[1], v[2]));
             }
         }
     }
@@ -727,7 +729,8 @@ __device__ __forceinline__ uint16_t coarse_up_at(const View& o, uint32_t hi, uin
 // lanes whose pixel index falls in the coarse grid), as coarse_up_kernel does.
 // Lanes: a pixel's 2 groups + 3 tasks are consecutive, so the group lanes of a tap pixel read one cache line
 // (measured faster than waves of one task over 64 pixels, whose lanes each touch their own line). csh = hi / h and
-// csw = wi / w come from the host.
+// csw = wi / w come from the host. blockIdx.y: the pair (its maps and pictures images 2k, 2k + 1 of f8 and i8, its
+// image k of every other view).
 template <bool VEC, bool UP>
 __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, View fl, OView fx, OView l8,
                                                               uint32_t h, uint32_t w, uint32_t c, uint32_t groups,
@@ -736,6 +739,15 @@ __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, 
                                                               float csw) {
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     if (t >= items) return;
+    if (blockIdx.y) {
+        const size_t z = blockIdx.y, hw = (size_t)h * w;
+        f8.p += z * 2 * hw * f8.cs, i8.p += z * 2 * hw * i8.cs, fl.p += z * hw * fl.cs;
+        fx.p += z * hw * fx.cs, l8.p += z * hw * l8.cs;
+        if constexpr (UP) {
+            o.p += z * hi * wi * o.cs, fv.p += z * hw * fv.cs;
+            if (state.p) state.p += z * hi * wi * state.cs;
+        }
+    }
     const uint32_t tasks = 2 * groups + 3, pix = t / tasks, task = t - pix * tasks;
     const uint32_t x = pix % w, y = pix / w;
     if (task < 2 * groups + 2) {
@@ -831,9 +843,17 @@ __device__ __forceinline__ void blend_at(const View& q, const View& fl, const Vi
 // block's last column and row are the right and lower neighbours of its outputs; clamped to the picture, unused past
 // its edge), so no lane computes two; the gradient reads the neighbours' blends from LDS.
 constexpr uint32_t kRiT = 7;
+// blockIdx.y: image i of flow, vis and rx, whose pictures are pair (i % qmod) of q (images 2p, 2p + 1)
 __global__ __launch_bounds__(64) void refine_input_kernel(View q, View fl, View vis, OView rx, uint32_t h, uint32_t w,
-                                                          float fs, uint32_t tiles_x) {
+                                                          float fs, uint32_t tiles_x, uint32_t qmod) {
     __shared__ float bt[8 * 8 * 3];
+    {
+        const size_t hw = (size_t)h * w, img = blockIdx.y;
+        q.p += (img % qmod) * 2 * hw * q.cs;
+        fl.p += img * hw * fl.cs;
+        vis.p += img * hw * vis.cs;
+        rx.p += img * hw * rx.cs;
+    }
     const uint32_t tx = threadIdx.x % 8, ty = threadIdx.x / 8;
     const uint32_t x0 = (blockIdx.x % tiles_x) * kRiT, y0 = (blockIdx.x / tiles_x) * kRiT;
     const uint32_t x = x0 + tx, y = y0 + ty;
@@ -868,8 +888,9 @@ __global__ __launch_bounds__(64) void refine_input_kernel(View q, View fl, View 
 template <bool VEC>
 __device__ __forceinline__ void fold_pair_at(const View& x, const OView& out, const OView& also, uint32_t hw,
                                              uint32_t c, uint32_t groups, uint32_t t) {
-    const uint32_t g = t % groups, r = t / groups, img = r % 2, pix = r / 2, ch = g * 4;
-    const uint16_t* src = x.p + ((size_t)img * hw + pix) * x.cs + x.c0 + ch;
+    // pix runs over the pairs' pixels: pair k's pictures are images 2k, 2k + 1 of x, its output image k
+    const uint32_t g = t % groups, r = t / groups, img = r % 2, pix = r / 2, ch = g * 4, pair = pix / hw;
+    const uint16_t* src = x.p + ((size_t)(pair + img) * hw + pix) * x.cs + x.c0 + ch;
     uint16_t* dst = out.p + (size_t)pix * out.cs + out.c0 + img * c + ch;
     uint16_t* dst2 = also.p ? also.p + (size_t)pix * also.cs + also.c0 + ch : nullptr;
     if constexpr (VEC) {
@@ -1603,13 +1624,17 @@ constexpr uint32_t kGmPart = gmfit::kPart;                     // one round's pa
 constexpr uint32_t kGmT = 16;                 // the box tile's edge and the cost block's width, in cells
 constexpr uint32_t kGmRmax = 32;              // largest box radius: r_dwin = round(16 s), s <= 2
 
+// The repair of several pairs at once: every kernel below takes the pair from one grid dimension (pair k: pictures
+// 2k images past a and b, flow image k, workspace k at wsf floats past workspace 0); one pair is pair 0.
+
 // one fit round (gm_fit_reduce.wgsl:15-44, the round before solved first) for workgroup blockIdx.x of channel
-// blockIdx.y: the shared round body (gm_fit.h) at 256 threads
+// blockIdx.y of pair blockIdx.z: the shared round body (gm_fit.h) at 256 threads
 __global__ __launch_bounds__(kGmWg) void gm_fit_kernel(View flow, uint32_t h8, uint32_t w8, float delta, uint32_t round,
-                                                       const float* part_in, float* part_out) {
+                                                       const float* part_in, float* part_out, size_t wsf) {
     __shared__ gmfit::RoundLds lds;
-    gmfit::round_body<kGmWg>(flow.p, flow.cs, flow.c0, h8, w8, delta, round, part_in, part_out, blockIdx.x, blockIdx.y,
-                             lds);
+    const size_t z = blockIdx.z;
+    gmfit::round_body<kGmWg>(flow.p + z * h8 * w8 * flow.cs, flow.cs, flow.c0, h8, w8, delta, round, part_in + z * wsf,
+                             part_out + z * wsf, blockIdx.x, blockIdx.y, lds);
 }
 
 // the B, G, R of pixel pix of a picture view (VEC: one 8-byte load, 4-channel aligned views)
@@ -1644,12 +1669,17 @@ __device__ float gm_samp(const View& v, uint32_t h, uint32_t w, float gx, float 
 // round first (block 0 also stores the coefficients, [4][4], for the select and the caller). Two lanes per cell,
 // in different waves: threads 0-127 sample for cm and l (maps 0, 3, 4), threads 128-255 for ca and dv (maps 1, 2);
 // ca outside the pictures is cm, handed over through LDS. VEC: the pictures and the flow are 4-channel aligned
-// views (one 8-byte load per pixel).
+// views (one 8-byte load per pixel). blockIdx.z: the pair.
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint32_t h, uint32_t w, View flow,
                                                            uint32_t h8, uint32_t w8, const float* part, float* coef,
-                                                           float* maps, uint32_t hc, uint32_t wc) {
+                                                           float* maps, uint32_t hc, uint32_t wc, size_t wsf) {
     __shared__ float ss[4][9], cf[4][3], cms[128];
+    {
+        const size_t z = blockIdx.z;
+        a.p += z * 2 * h * w * a.cs, b.p += z * 2 * h * w * b.cs, flow.p += z * h8 * w8 * flow.cs;
+        part += z * wsf, coef += z * wsf, maps += z * wsf;
+    }
     const uint32_t t = threadIdx.x, cl = t % 128;
     const bool second = t >= 128;  // uniform over each wave
     const uint32_t x = blockIdx.x * 16 + cl % 16, y = blockIdx.y * 8 + cl / 16;
@@ -1709,16 +1739,17 @@ __global__ __launch_bounds__(kThreads) void gm_cost_kernel(View a, View b, uint3
     if (second && valid) maps[n + i] = inside ? ca : cms[cl];
 }
 
-// box_h then box_v of radius r (gm_box.wgsl:8-25) on map channel blockIdx.z of src ([c][hc][wc]) into the same
-// channel of dst, for the block's 16 x 16 tile of cells. The window of clamped rows and columns the tile's taps
-// reach ((16 + 2r)^2 cells, NB x NB blocks of 16 x 16, dynamic LDS) is staged with every load issued before the
-// first store; box_h runs on every window row (a window row is a clamped map row, so its sums are the map's own),
-// box_v on the tile, each sum over its taps in order.
+// box_h then box_v of radius r (gm_box.wgsl:8-25) on map channel blockIdx.z % 5 of src ([5][hc][wc]) into the same
+// channel of dst, for the block's 16 x 16 tile of cells, pair blockIdx.z / 5. The window of clamped rows and columns
+// the tile's taps reach ((16 + 2r)^2 cells, NB x NB blocks of 16 x 16, dynamic LDS) is staged with every load issued
+// before the first store; box_h runs on every window row (a window row is a clamped map row, so its sums are the
+// map's own), box_v on the tile, each sum over its taps in order.
 template <uint32_t NB>
 __global__ __launch_bounds__(kThreads) void gm_box_kernel(const float* src, float* dst, uint32_t hc, uint32_t wc,
-                                                          uint32_t r) {
+                                                          uint32_t r, size_t wsf) {
     extern __shared__ float glds[];
-    const uint32_t t = threadIdx.x, x0 = blockIdx.x * kGmT, y0 = blockIdx.y * kGmT, ch = blockIdx.z;
+    const uint32_t t = threadIdx.x, x0 = blockIdx.x * kGmT, y0 = blockIdx.y * kGmT, ch = blockIdx.z % 5;
+    src += (size_t)(blockIdx.z / 5) * wsf, dst += (size_t)(blockIdx.z / 5) * wsf;
     const uint32_t ty = t / kGmT, tx = t % kGmT;
     const uint32_t span = 2 * r + 1, rows = kGmT + 2 * r;
     float* win = glds;                // [rows][rows]
@@ -1772,12 +1803,14 @@ __host__ __device__ __forceinline__ int gm_sel_row(uint32_t i, uint32_t hc, uint
 // cells the select reads: box_h at their columns (every row), then box_v at their rows, the same sums in the same
 // order as the full windows there. NT >= 2r + 1: a sum's taps are loaded together (clamped addresses; the loads
 // past the window repeat its last tap and are not added), then added in order.
-// box_h of maps 0-2 of tex ([5][hc][wc], after the texture window) at the select's columns: hs [3][hc][w8]
+// box_h of maps 0-2 of tex ([5][hc][wc], after the texture window) at the select's columns: hs [3][hc][w8];
+// blockIdx.y: the pair
 template <uint32_t NT>
 __global__ __launch_bounds__(kThreads) void gm_dwin_h_kernel(const float* tex, float* hs, uint32_t hc, uint32_t wc,
-                                                             uint32_t w8, uint32_t r, uint32_t items) {
+                                                             uint32_t w8, uint32_t r, uint32_t items, size_t wsf) {
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
     if (t >= items) return;
+    tex += blockIdx.y * wsf, hs += blockIdx.y * wsf;
     const uint32_t j = t % w8, rr = t / w8, row = rr % hc, m = rr / hc, span = 2 * r + 1;
     const int x = gm_sel_row(j, wc, w8);
     const float* src = tex + m * (size_t)hc * wc + (size_t)row * wc;
@@ -1802,13 +1835,17 @@ __device__ __forceinline__ float quad_lane(float v) {
 // cell: lane m < 3 sums map m's window (its NT loads in one batch), lane 3 loads maps 3-4, and every lane of the
 // four gathers the five values (quad broadcasts), decides as the select does and stores flow channel m. The lanes
 // past the last cell shadow it (in-bounds loads, so that every lane of a wave takes part in the shuffles) and store
-// nothing. items: cells.
+// nothing. items: cells. blockIdx.y: the pair.
 template <uint32_t NT>
 __global__ __launch_bounds__(kThreads) void gm_dwin_v_select_kernel(const float* hs, const float* tex,
                                                                     const float* coef, OView flow, float* dec,
                                                                     uint32_t h8, uint32_t w8, uint32_t hc, uint32_t wc,
                                                                     uint32_t r, float eps, float dmin, float texf,
-                                                                    uint32_t items) {
+                                                                    uint32_t items, size_t wsf) {
+    {
+        const size_t z = blockIdx.y;
+        hs += z * wsf, tex += z * wsf, coef += z * wsf, dec += z * wsf, flow.p += z * h8 * w8 * flow.cs;
+    }
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x, cell = t / 4, m = t % 4;
     const bool live = cell < items;
     const uint32_t cl = live ? cell : items - 1;
@@ -2214,17 +2251,25 @@ extern "C" int fhc_flow_vis_t(const fhc_tensor* fv, const fhc_tensor* dfilm, con
 
 extern "C" int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tensor* vis,
                                 const fhc_tensor* rx, uint32_t h, uint32_t w, float flow_out_scale, void* stream) {
+    return fhc_refine_input_n(q, flow, vis, rx, h, w, flow_out_scale, 1, 1, stream);
+}
+
+extern "C" int fhc_refine_input_n(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tensor* vis,
+                                  const fhc_tensor* rx, uint32_t h, uint32_t w, float flow_out_scale, uint32_t n,
+                                  uint32_t qmod, void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
-        if ((uint64_t)h * w == 0) return 0;
+        if ((uint64_t)h * w * n == 0) return 0;
+        if (qmod == 0 || qmod > n) return fail(-1, "refine_input: %u picture pairs for %u images", qmod, n);
+        if (n > 65535) return fail(-1, "refine_input: %u images exceed the launch limit", n);
         FHC_TRY(check(q, "refine_input q", 3, true));
         FHC_TRY(check(flow, "refine_input flow", 4, true));
         FHC_TRY(check(vis, "refine_input vis", 3, true));
         FHC_TRY(check(rx, "refine_input rx", 14, false, true));
         const uint32_t tx = (w + kRiT - 1) / kRiT, ty = (h + kRiT - 1) / kRiT;
         if ((uint64_t)tx * ty >= kMaxItems / 64) return fail(-1, "refine_input: %u x %u is too large", w, h);
-        hipLaunchKernelGGL(refine_input_kernel, dim3(tx * ty), dim3(64), 0, (hipStream_t)stream, in(q), in(flow),
-                           in(vis), outv(rx), h, w, flow_out_scale, tx);
+        hipLaunchKernelGGL(refine_input_kernel, dim3(tx * ty, n), dim3(64), 0, (hipStream_t)stream, in(q), in(flow),
+                           in(vis), outv(rx), h, w, flow_out_scale, tx, qmod);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "refine_input: launch failed: %s", hipGetErrorString(e));
     });
@@ -2233,27 +2278,44 @@ extern "C" int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, con
 extern "C" int fhc_pair_input(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16,
                               const fhc_tensor* l16, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow,
                               void* stream) {
+    return fhc_pair_input_n(ab, q, i8, i16, l16, ih, iw, oh, ow, 1, stream);
+}
+
+extern "C" int fhc_pair_input_n(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* i8,
+                                const fhc_tensor* i16, const fhc_tensor* l16, uint32_t ih, uint32_t iw, uint32_t oh,
+                                uint32_t ow, uint32_t pairs, void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
-        if ((uint64_t)ih * iw * oh * ow == 0) return 0;
+        if ((uint64_t)ih * iw * oh * ow * pairs == 0) return 0;
         FHC_TRY(check(ab, "pair_input ab", 3, true));
         FHC_TRY(check(q, "pair_input q", 3, false, true));
-        const uint32_t taps = std::max(aa_taps(ih, oh), aa_taps(iw, ow));
-        if (!(taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt)) {
-            // no one-launch form for this scale: the resize, then the pyramid
-            FHC_TRY(fhc_interpolate(ab, q, 2, 3, ih, iw, oh, ow, 1, stream));
-            return fhc_pair_pyramid(q, i8, i16, l16, oh, ow, stream);
-        }
-        if (oh < 4 || ow < 4) return fail(-1, "pair_input: %u x %u is below 4 x 4", oh, ow);
         FHC_TRY(check(i8, "pair_input i8", 3, false, true));
         FHC_TRY(check(i16, "pair_input i16", 6, false, true));
         FHC_TRY(check(l16, "pair_input l16", 2, false, true));
+        const uint32_t taps = std::max(aa_taps(ih, oh), aa_taps(iw, ow));
+        if (!(taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt)) {
+            // no one-launch form for this scale: the resize of every picture, then each pair's pyramid
+            FHC_TRY(fhc_interpolate(ab, q, 2 * pairs, 3, ih, iw, oh, ow, 1, stream));
+            for (uint32_t k = 0; k < pairs; k++) {
+                const auto at = [k](const fhc_tensor* t, uint64_t image) {
+                    fhc_tensor v = *t;
+                    v.p = static_cast<uint16_t*>(v.p) + k * image * v.cstride;
+                    return v;
+                };
+                const fhc_tensor qk = at(q, 2ull * oh * ow), i8k = at(i8, 2ull * (oh / 2) * (ow / 2)),
+                                 i16k = at(i16, (uint64_t)(oh / 4) * (ow / 4)), l16k = at(l16, (uint64_t)(oh / 4) * (ow / 4));
+                FHC_TRY(fhc_pair_pyramid(&qk, &i8k, &i16k, &l16k, oh, ow, stream));
+            }
+            return 0;
+        }
+        if (oh < 4 || ow < 4) return fail(-1, "pair_input: %u x %u is below 4 x 4", oh, ow);
         const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
         const bool v4 = vec4(4, {ab});
         auto kl = taps <= 4 ? (v4 ? interp_aa_lds_kernel<4, true, true> : interp_aa_lds_kernel<4, true, false>)
                             : (v4 ? interp_aa_lds_kernel<8, true, true> : interp_aa_lds_kernel<8, true, false>);
-        hipLaunchKernelGGL(kl, dim3(2 * tx * ty), dim3(kThreads), 0, (hipStream_t)stream, in(ab), outv(q), ih, iw, oh,
-                           ow, 3u, tx, ty, PyrOut{outv(i8), outv(i16), outv(l16)});
+        if ((uint64_t)2 * pairs * tx * ty >= kMaxItems / kThreads) return fail(-1, "pair_input: too many tiles");
+        hipLaunchKernelGGL(kl, dim3(2 * pairs * tx * ty), dim3(kThreads), 0, (hipStream_t)stream, in(ab), outv(q), ih,
+                           iw, oh, ow, 3u, tx, ty, PyrOut{outv(i8), outv(i16), outv(l16)});
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "pair_input: launch failed: %s", hipGetErrorString(e));
     });
@@ -2465,10 +2527,12 @@ extern "C" int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t
 
 int fhc::gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
                   uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes,
-                  const GmCoRun* co, void* stream) {
+                  const GmCoRun* co, void* stream, uint32_t pairs) {
     return guard(-3, [&]() -> int {
         clear_error();
-        if (level == 0) return 0;
+        if (level == 0 || pairs == 0) return 0;
+        if (co && pairs != 1) return fail(-1, "gmhs: a co-runner goes with one pair, %u given", pairs);
+        if (pairs > 65535 / 5) return fail(-1, "gmhs: %u pairs exceed the launch limit", pairs);
         fhc_gmhs_par p;
         FHC_TRY(gm_params(h, w, full_w, level, &p));
         if (h8 == 0 || w8 == 0) return fail(-1, "gmhs: empty E8 flow (%u x %u)", w8, h8);
@@ -2476,8 +2540,11 @@ int fhc::gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t
         FHC_TRY(check(b, "gmhs b", 3, false));
         FHC_TRY(check(flow, "gmhs flow", 4, false));
         if (!ws) return fail(-1, "gmhs: null workspace");
-        if (ws_bytes < p.ws_bytes)
-            return fail(-1, "gmhs: workspace of %zu bytes, %llu needed", ws_bytes, (unsigned long long)p.ws_bytes);
+        // pair k's workspace starts at k * stride bytes (the last pair's needs only ws_bytes)
+        const uint64_t stride = (p.ws_bytes + 255) / 256 * 256, need = (pairs - 1) * stride + p.ws_bytes;
+        const size_t wsf = stride / sizeof(float);
+        if (ws_bytes < need)
+            return fail(-1, "gmhs: workspace of %zu bytes, %llu needed", ws_bytes, (unsigned long long)need);
         if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(-1, "gmhs: the workspace must be 256-byte aligned");
         if (p.r_blk > kGmRmax || p.r_dwin > kGmRmax)
             return fail(-1, "gmhs: box radii %u, %u exceed %u", p.r_blk, p.r_dwin, kGmRmax);
@@ -2506,27 +2573,28 @@ int fhc::gmhs_run(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t
                 if (ce != hipSuccess) return fail(-2, "gmhs: launch failed: %s", hipGetErrorString(ce));
                 continue;
             }
-            hipLaunchKernelGGL(gm_fit_kernel, dim3(kGmNwg, 4), dim3(kGmWg), 0, st, in(flow), h8, w8, p.delta, round,
-                               part[(round + 1) & 1u], part[round & 1u]);
+            hipLaunchKernelGGL(gm_fit_kernel, dim3(kGmNwg, 4, pairs), dim3(kGmWg), 0, st, in(flow), h8, w8, p.delta,
+                               round, part[(round + 1) & 1u], part[round & 1u], wsf);
         }
         const bool v = vec4(4, {a, b, flow});
         const dim3 tiles((p.wc + kGmT - 1) / kGmT, (p.hc + kGmT - 1) / kGmT);
-        const dim3 ctiles(tiles.x, (p.hc + 7) / 8);  // the cost kernel's 16 x 8 blocks
+        const dim3 ctiles(tiles.x, (p.hc + 7) / 8, pairs);  // the cost kernel's 16 x 8 blocks
         hipLaunchKernelGGL(v ? gm_cost_kernel<true> : gm_cost_kernel<false>, ctiles, dim3(kThreads), 0, st, in(a), in(b),
-                           h, w, in(flow), h8, w8, part[1], coef, raw, p.hc, p.wc);
+                           h, w, in(flow), h8, w8, part[1], coef, raw, p.hc, p.wc, wsf);
         // the texture window over the 5 maps (raw -> maps), then the decision window at the cells the select reads
         // (its rows at their columns, its columns at their rows) and the select (maps -> dec, flow)
         const uint32_t rows = kGmT + 2 * p.r_blk, nb = (rows + kGmT - 1) / kGmT;  // r <= 32: 2 .. 5 blocks a side
         auto box = nb <= 2 ? gm_box_kernel<2> : nb == 3 ? gm_box_kernel<3> : nb == 4 ? gm_box_kernel<4> : gm_box_kernel<5>;
-        hipLaunchKernelGGL(box, dim3(tiles.x, tiles.y, 5), dim3(kThreads), (rows * rows + rows * kGmT) * 4, st, raw,
-                           maps, p.hc, p.wc, p.r_blk);
+        hipLaunchKernelGGL(box, dim3(tiles.x, tiles.y, 5 * pairs), dim3(kThreads), (rows * rows + rows * kGmT) * 4, st,
+                           raw, maps, p.hc, p.wc, p.r_blk, wsf);
         const bool wide = 2 * p.r_dwin + 1 > 33;
         const uint32_t nh = 3 * p.hc * w8, ne = h8 * w8;
-        hipLaunchKernelGGL(wide ? gm_dwin_h_kernel<65> : gm_dwin_h_kernel<33>, dim3((nh + kThreads - 1) / kThreads),
-                           dim3(kThreads), 0, st, maps, hs, p.hc, p.wc, w8, p.r_dwin, nh);
+        hipLaunchKernelGGL(wide ? gm_dwin_h_kernel<65> : gm_dwin_h_kernel<33>,
+                           dim3((nh + kThreads - 1) / kThreads, pairs), dim3(kThreads), 0, st, maps, hs, p.hc, p.wc, w8,
+                           p.r_dwin, nh, wsf);
         hipLaunchKernelGGL(wide ? gm_dwin_v_select_kernel<65> : gm_dwin_v_select_kernel<33>,
-                           dim3((4 * ne + kThreads - 1) / kThreads), dim3(kThreads), 0, st, hs, maps, coef, outv(flow), raw,
-                           h8, w8, p.hc, p.wc, p.r_dwin, p.eps, p.dmin, p.tex, ne);
+                           dim3((4 * ne + kThreads - 1) / kThreads, pairs), dim3(kThreads), 0, st, hs, maps, coef,
+                           outv(flow), raw, h8, w8, p.hc, p.wc, p.r_dwin, p.eps, p.dmin, p.tex, ne, wsf);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "gmhs: launch failed: %s", hipGetErrorString(e));
     });
@@ -2538,13 +2606,28 @@ extern "C" int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, ui
     return gmhs_run(a, b, h, w, flow, h8, w8, full_w, level, ws, ws_bytes, nullptr, stream);
 }
 
+extern "C" int fhc_gmhs_n(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow,
+                          uint32_t h8, uint32_t w8, uint32_t full_w, uint32_t level, uint32_t pairs, void* ws,
+                          size_t ws_bytes, void* stream) {
+    return gmhs_run(a, b, h, w, flow, h8, w8, full_w, level, ws, ws_bytes, nullptr, stream, pairs);
+}
+
 extern "C" int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state,
                                      uint32_t hi, uint32_t wi, float flow_scale, const fhc_tensor* f8,
                                      const fhc_tensor* i8, float fine_scale, const fhc_tensor* fx,
                                      const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c, void* stream) {
+    return fhc_coarse_fine_input_n(o, fv, state, hi, wi, flow_scale, f8, i8, fine_scale, fx, l8, h, w, c, 1, stream);
+}
+
+extern "C" int fhc_coarse_fine_input_n(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state,
+                                       uint32_t hi, uint32_t wi, float flow_scale, const fhc_tensor* f8,
+                                       const fhc_tensor* i8, float fine_scale, const fhc_tensor* fx,
+                                       const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c, uint32_t pairs,
+                                       void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
-        if ((uint64_t)h * w * c == 0) return 0;
+        if ((uint64_t)h * w * c * pairs == 0) return 0;
+        if (pairs > 65535) return fail(-1, "coarse_fine_input: %u pairs exceed the launch limit", pairs);
         if (hi == 0 || wi == 0) return fail(-1, "coarse_fine_input: empty coarse output (%u x %u)", hi, wi);
         if (state && (hi > h || wi > w)) return fail(-1, "coarse_fine_input: the state is larger than the fine grid");
         FHC_TRY(check(o, "coarse_fine_input o", 7, false));
@@ -2563,9 +2646,9 @@ extern "C" int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, 
         const OView sv = state ? outv(state) : OView{nullptr, 0, 0};
         return launch("coarse_fine_input", (uint64_t)h * w * (2 * groups + 3), [&](dim3 g, uint32_t n) {
             auto k = v ? fine_input_kernel<true, true> : fine_input_kernel<false, true>;
-            hipLaunchKernelGGL(k, g, dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8), fl, outv(fx), outv(l8),
-                               h, w, c, groups, n, in(o), outv(fv), sv, hi, wi, flow_scale, (float)hi / (float)h,
-                               (float)wi / (float)w);
+            hipLaunchKernelGGL(k, dim3(g.x, pairs), dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8), fl,
+                               outv(fx), outv(l8), h, w, c, groups, n, in(o), outv(fv), sv, hi, wi, flow_scale,
+                               (float)hi / (float)h, (float)wi / (float)w);
         });
     });
 }
@@ -2595,9 +2678,16 @@ extern "C" int fhc_fold_pair_sad(const fhc_tensor* x, const fhc_tensor* out, con
                                  uint32_t w, uint32_t c, const fhc_tensor* la, const fhc_tensor* lb,
                                  const fhc_tensor* sad_out, uint32_t sn, uint32_t sh, uint32_t sw, uint32_t radius,
                                  void* stream) {
+    return fhc_fold_pair_sad_n(x, out, also, h, w, c, 1, la, lb, sad_out, sn, sh, sw, radius, stream);
+}
+
+extern "C" int fhc_fold_pair_sad_n(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h,
+                                   uint32_t w, uint32_t c, uint32_t pairs, const fhc_tensor* la, const fhc_tensor* lb,
+                                   const fhc_tensor* sad_out, uint32_t sn, uint32_t sh, uint32_t sw, uint32_t radius,
+                                   void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
-        const uint64_t fold_items = (uint64_t)h * w * 2 * ((c + 3) / 4);
+        const uint64_t fold_items = (uint64_t)pairs * h * w * 2 * ((c + 3) / 4);
         if (radius > 7) return fail(-1, "fold_pair_sad: radius %u above 7", radius);
         const uint32_t span2 = (2 * radius + 1) * (2 * radius + 1);
         const uint64_t sad_items = (uint64_t)sn * sh * sw * span2;

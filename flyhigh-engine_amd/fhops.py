@@ -75,15 +75,19 @@ def _lib():
             "fhc_chcopy": [T, T, U, U, U, U, P],
             "fhc_pair_pyramid": [T, T, T, T, U, U, P],
             "fhc_pair_input": [T, T, T, T, T, U, U, U, U, P],
+            "fhc_pair_input_n": [T, T, T, T, T, U, U, U, U, U, P],
             "fhc_render": [T, T, T, T, T, T, U, U, U, U, ctypes.c_float, ctypes.c_float, I, U, P],
             "fhc_fold_pair": [T, T, T, U, U, U, P],
             "fhc_fold_pair_sad": [T, T, T, U, U, U, T, T, T, U, U, U, U, P],
+            "fhc_fold_pair_sad_n": [T, T, T, U, U, U, U, T, T, T, U, U, U, U, P],
             "fhc_coarse_up": [T, T, T, U, U, U, U, ctypes.c_float, P],
             "fhc_fine_input": [T, T, T, T, T, U, U, U, P],
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
             "fhc_coarse_fine_input": [T, T, T, U, U, ctypes.c_float, T, T, ctypes.c_float, T, T, U, U, U, P],
+            "fhc_coarse_fine_input_n": [T, T, T, U, U, ctypes.c_float, T, T, ctypes.c_float, T, T, U, U, U, U, P],
             "fhc_flow_vis_t_convex": [T, T, T, ctypes.c_float, T, U, U, U, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
+            "fhc_refine_input_n": [T, T, T, T, U, U, ctypes.c_float, U, U, P],
             "fhc_rgba_in": [P, U, U, U, U, ctypes.c_uint64, T, U, U, P],
             "fhc_rgba_out": [T, U, U, U, P, U, U, U, ctypes.c_uint64, P],
             "fhc_rgba_resize": [P, U, U, U, U, ctypes.c_uint64, U, U, T, U, U, P],
@@ -91,6 +95,7 @@ def _lib():
                                 P],
             "fhc_gmhs_params": [U, U, U, U, ctypes.POINTER(GmhsPar)],
             "fhc_gmhs": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P],
+            "fhc_gmhs_n": [T, T, U, U, T, U, U, U, U, U, P, ctypes.c_size_t, P],
             "fhc_gmhs_film": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P, P, P, P, P, P, P, P],
         }
         for name, args in sig.items():
@@ -254,14 +259,17 @@ def flow_vis_t(fv, dfilm, out, t, stream=None):
 
 
 def coarse_fine_input(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c, stream=None):
-    """coarse_up(o, fv, state, ...) to f8's grid, then fine_input(f8, i8, (fv, fine_scale), fx, l8, c): one launch."""
+    """coarse_up(o, fv, state, ...) to f8's grid, then fine_input(f8, i8, (fv, fine_scale), fx, l8, c): one launch
+    for every pair (pair k: image k of o, fv, state, fx, l8; images 2k, 2k + 1 of f8 and i8)."""
     o, f8 = _v(o), _v(f8)
-    _, hi, wi, _ = o.shape
-    _, h, w, _ = f8.shape
+    pairs, hi, wi, _ = o.shape
+    n2, h, w, _ = f8.shape
+    if n2 != 2 * pairs:
+        raise FhcError(f"coarse_fine_input: {n2} feature maps for {pairs} pairs")
     _run("coarse_fine_input",
-         _lib().fhc_coarse_fine_input(_ref(o), _ref(_v(fv)), None if state is None else _ref(_v(state)), hi, wi,
-                                      flow_scale, _ref(f8), _ref(_v(i8)), fine_scale, _ref(_v(fx)), _ref(_v(l8)), h,
-                                      w, c, _stream_handle(stream)))
+         _lib().fhc_coarse_fine_input_n(_ref(o), _ref(_v(fv)), None if state is None else _ref(_v(state)), hi, wi,
+                                        flow_scale, _ref(f8), _ref(_v(i8)), fine_scale, _ref(_v(fx)), _ref(_v(l8)),
+                                        h, w, c, pairs, _stream_handle(stream)))
 
 
 def flow_vis_t_convex(wt, fv, dfilm, t, out, stream=None):
@@ -272,18 +280,25 @@ def flow_vis_t_convex(wt, fv, dfilm, t, out, stream=None):
                                                            n, h, w, _stream_handle(stream)))
 
 
-def refine_input(q, flow, vis, rx, flow_out_scale, stream=None):
-    flow = _v(flow)
-    _, h, w, _ = flow.shape
-    _run("refine_input", _lib().fhc_refine_input(_ref(_v(q)), _ref(flow), _ref(_v(vis)), _ref(_v(rx)), h, w,
-                                                 flow_out_scale, _stream_handle(stream)))
+def refine_input(q, flow, vis, rx, flow_out_scale, qmod=None, stream=None):
+    """refine_input over every image of flow (n of them): image i's pictures are pair i % qmod of q (default: q's
+    pairs, 2 images each)."""
+    flow, q = _v(flow), _v(q)
+    n, h, w, _ = flow.shape
+    qmod = q.shape[0] // 2 if qmod is None else qmod
+    _run("refine_input", _lib().fhc_refine_input_n(_ref(q), _ref(flow), _ref(_v(vis)), _ref(_v(rx)), h, w,
+                                                   flow_out_scale, n, qmod, _stream_handle(stream)))
 
 
 def pair_input(ab, q, i8, i16, l16, oh, ow, stream=None):
+    """The pictures' resize and pyramid for every pair of ab (pair k: images 2k, 2k + 1 of ab, q and i8, image k of
+    i16 and l16)."""
     ab = _v(ab)
-    _, ih, iw, _ = ab.shape
-    _run("pair_input", _lib().fhc_pair_input(_ref(ab), _ref(_v(q)), _ref(_v(i8)), _ref(_v(i16)), _ref(_v(l16)), ih,
-                                             iw, oh, ow, _stream_handle(stream)))
+    n2, ih, iw, _ = ab.shape
+    if n2 % 2:
+        raise FhcError(f"pair_input: {n2} pictures are no whole pairs")
+    _run("pair_input", _lib().fhc_pair_input_n(_ref(ab), _ref(_v(q)), _ref(_v(i8)), _ref(_v(i16)), _ref(_v(l16)),
+                                               ih, iw, oh, ow, n2 // 2, _stream_handle(stream)))
 
 
 def render(a, b, flow, vis, rt, cubic=True, flags=0, fsx=1.0, fsy=1.0, out=None, stream=None):
@@ -308,16 +323,18 @@ def fold_pair(x, out, also=None, stream=None, c=None):
 
 
 def fold_pair_sad(x, out, also, la, lb, sad_out, radius, stream=None, c=None):
-    """fold_pair(x, out, also, c=c) and sad(la, lb, radius, out=sad_out), which touch none of each other's tensors,
-    in one launch."""
+    """fold_pair(x, out, also, c=c) of every pair of x (pair k: images 2k, 2k + 1, folded into image k of out and
+    also) and sad(la, lb, radius, out=sad_out), which touch none of each other's tensors, in one launch."""
     x, la = _v(x), _v(la)
-    _, h, w, _ = x.shape
+    n2, h, w, _ = x.shape
     n, sh, sw, _ = la.shape
     c = x.channels if c is None else c
+    if n2 % 2:
+        raise FhcError(f"fold_pair_sad: {n2} maps are no whole pairs")
     _run("fold_pair_sad",
-         _lib().fhc_fold_pair_sad(_ref(x), _ref(_v(out)), None if also is None else _ref(_v(also)), h, w, c,
-                                  _ref(la), _ref(_v(lb)), _ref(_v(sad_out)), n, sh, sw, radius,
-                                  _stream_handle(stream)))
+         _lib().fhc_fold_pair_sad_n(_ref(x), _ref(_v(out)), None if also is None else _ref(_v(also)), h, w, c,
+                                    n2 // 2, _ref(la), _ref(_v(lb)), _ref(_v(sad_out)), n, sh, sw, radius,
+                                    _stream_handle(stream)))
 
 
 def coarse_up(o, out, state, oh, ow, flow_scale, stream=None):
@@ -396,10 +413,17 @@ def gmhs_params(h: int, w: int, full_w: int, level: int = 1) -> dict:
     return {n: getattr(p, n) for n, _ in GmhsPar._fields_}
 
 
-def gmhs_workspace(h: int, w: int, full_w: int, level: int = 1, device="cuda"):
-    """A workspace for fhc_gmhs (uint8, 256-byte aligned as torch's allocator aligns)."""
+def gmhs_workspace(h: int, w: int, full_w: int, level: int = 1, device="cuda", pairs: int = 1):
+    """A workspace for fhc_gmhs (uint8, 256-byte aligned as torch's allocator aligns), or for fhc_gmhs_n over
+    `pairs` pairs (pair k's at k * gmhs_ws_stride(...) bytes)."""
     import torch
-    return torch.empty(gmhs_params(h, w, full_w, level)["ws_bytes"], dtype=torch.uint8, device=device)
+    nb = gmhs_params(h, w, full_w, level)["ws_bytes"]
+    return torch.empty((pairs - 1) * ((nb + 255) // 256 * 256) + nb, dtype=torch.uint8, device=device)
+
+
+def gmhs_ws_stride(h: int, w: int, full_w: int, level: int = 1) -> int:
+    """The bytes between two pairs' workspaces in fhc_gmhs_n's."""
+    return (gmhs_params(h, w, full_w, level)["ws_bytes"] + 255) // 256 * 256
 
 
 def gmhs(a, b, flow, full_w: int, level: int = 1, ws=None, stream=None):
@@ -412,6 +436,23 @@ def gmhs(a, b, flow, full_w: int, level: int = 1, ws=None, stream=None):
         ws = gmhs_workspace(h, w, full_w, max(level, 1), a.t.device)
     _run("gmhs", _lib().fhc_gmhs(_ref(a), _ref(b), h, w, _ref(flow), h8, w8, full_w, level, ws.data_ptr(),
                                  ws.numel() * ws.element_size(), _stream_handle(stream)))
+    return ws
+
+
+def gmhs_n(ab, flow, full_w: int, level: int = 1, ws=None, stream=None):
+    """The repair of every pair at once (fhc_gmhs_n): pair k's pictures are images 2k, 2k + 1 of ab (BGR), its E8
+    flow image k of flow (channels c0 .. c0 + 3, repaired in place). Returns the workspace (pair k's at k *
+    gmhs_ws_stride(...) bytes)."""
+    ab, flow = _v(ab), _v(flow)
+    n2, h, w, _ = ab.shape
+    n, h8, w8, _ = flow.shape
+    if n2 != 2 * n:
+        raise FhcError(f"gmhs_n: {n2} pictures for {n} flows")
+    if ws is None:
+        ws = gmhs_workspace(h, w, full_w, max(level, 1), ab.t.device, n)
+    a, b = View(ab.t[0:1], ab.c0, ab.scale), View(ab.t[1:2], ab.c0, ab.scale)
+    _run("gmhs_n", _lib().fhc_gmhs_n(_ref(a), _ref(b), h, w, _ref(flow), h8, w8, full_w, level, n, ws.data_ptr(),
+                                     ws.numel() * ws.element_size(), _stream_handle(stream)))
     return ws
 
 

@@ -100,8 +100,13 @@ class ComposedChains:
     backend always runs them this way, the GPU backend when asked to (a check of the fused kernels)."""
 
     def pair_input(self, ab: V, q: V, i8: V, i16: V, l16: V, oh: int, ow: int):
+        """The resize of every picture, then each pair's pyramid (pair k: images 2k, 2k + 1 of ab, q and i8, image
+        k of i16 and l16)."""
         self.interp(ab, 3, q, oh, ow, True)
-        self.pair_pyramid(q, i8, i16, l16)
+        for k in range(q.buf.shape[0] // 2):
+            one = lambda x, i=k: V(sl(x.buf, i), x.c0, x.scale)  # noqa: E731
+            two = lambda x, i=k: V(sl(x.buf, 2 * i, 2), x.c0, x.scale)  # noqa: E731
+            self.pair_pyramid(two(q), two(i8), one(i16), one(l16))
 
     def coarse_up(self, o: V, out: V, state: Optional[V], oh: int, ow: int, flow_scale: float):
         if state is not None:
@@ -116,8 +121,11 @@ class ComposedChains:
             self.chcopy(V(self.image(x.buf, 1), x.c0), c, also)
 
     def fold_pair_sad(self, x: V, c: int, out: V, also: Optional[V], la: V, lb: V, sad_out: V, r: int):
-        """fold_pair and a sad that neither reads what the other writes (one launch on the GPU)."""
-        self.fold_pair(x, c, out, also)
+        """fold_pair of every pair of x (pair k: images 2k, 2k + 1 into image k of out and also) and a sad that
+        neither reads what the other writes (one launch on the GPU)."""
+        for k in range(x.buf.shape[0] // 2):
+            self.fold_pair(V(sl(x.buf, 2 * k, 2), x.c0), c, V(sl(out.buf, k), out.c0),
+                           None if also is None else V(sl(also.buf, k), also.c0))
         self.sad(la, lb, sad_out, r)
 
     def pair_affine_out(self, a, b, x: V, mid: V, y: V, out: V, c: int):
@@ -136,6 +144,12 @@ class ComposedChains:
         """The convs a (with its residual, if any) and b of the same input x (on the GPU one launch)."""
         self.conv(a, x, ya, res_a)
         self.conv(b, x, yb)
+
+    def gmhs_n(self, ab: V, flow: V, full_w: int, level: int):
+        """gmhs of every pair: pair k's pictures are images 2k, 2k + 1 of ab, its flow image k of flow."""
+        for k in range(flow.buf.shape[0]):
+            self.gmhs(V(sl(ab.buf, 2 * k), ab.c0), V(sl(ab.buf, 2 * k + 1), ab.c0), V(sl(flow.buf, k), flow.c0),
+                      full_w, level)
 
     def gmhs_film(self, a: V, b: V, flow: V, full_w: int, level: int, fa, fb, h: V, c: int, hm: V, mid: V, y: V,
                   fo, yo: V):
@@ -163,9 +177,14 @@ class ComposedChains:
 
     def coarse_fine_input(self, o: V, fv: V, state: Optional[V], flow_scale: float, f8: V, i8: V,
                           fine_scale: float, fx: V, l8: V, c: int):
+        """coarse_up then fine_input for every pair: pair k's image k of o, fv, state, fx and l8, its maps and
+        pictures images 2k, 2k + 1 of f8 and i8."""
         _, h, w, _ = f8.buf.shape
-        self.coarse_up(o, fv, state, h, w, flow_scale)
-        self.fine_input(f8, i8, V(fv.buf, fv.c0, fine_scale), fx, l8, c)
+        for k in range(o.buf.shape[0]):
+            one = lambda x, i=k: V(sl(x.buf, i), x.c0, x.scale)  # noqa: E731
+            two = lambda x, i=k: V(sl(x.buf, 2 * i, 2), x.c0, x.scale)  # noqa: E731
+            self.coarse_up(one(o), one(fv), None if state is None else one(state), h, w, flow_scale)
+            self.fine_input(two(f8), two(i8), V(sl(fv.buf, k), fv.c0, fine_scale), one(fx), one(l8), c)
 
     def flow_vis_t_convex(self, wt: V, fv: V, dfilm: V, t: float, out: V, ftvt: V, lin: V, dvis: V):
         """ftvt, lin, dvis: where the op-by-op chain keeps its intermediates (the fused launch stores none)."""
@@ -194,6 +213,13 @@ class ComposedChains:
         self.rgba_in(frames, V(full), hp, wp)
         self.render(V(self.image(full, 0)), V(self.image(full, 1)), flow, vis, rt, V(pic), cubic, flags, fsx, fsy)
         self.rgba_out(V(pic), out_frames)
+
+    def refine_input_n(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V, qmod: int):
+        """refine_input for every image k of flow (and vis, rx, blend), its pictures pair k % qmod of q"""
+        for k in range(flow.buf.shape[0]):
+            v = lambda x, i=k: V(sl(x.buf, i), x.c0, x.scale)  # noqa: E731
+            self.refine_input(V(sl(q.buf, 2 * (k % qmod), 2), q.c0, q.scale), v(flow), v(vis), v(rx), flow_out_scale,
+                              v(blend))
 
     def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
         for i in range(2):
@@ -530,6 +556,19 @@ class GpuBackend(ComposedChains):
         self._go("gmhs (fit x4, cost, texture window, decision window x2)",
                  lambda: self.fh.gmhs(va, vb, vf, full_w, level, ws=ws, stream=self.stream), nbytes, kernels=8)
 
+    def gmhs_n(self, ab: V, flow: V, full_w: int, level: int):
+        vab, vf = self._v(ab), self._v(flow)
+        _, h, w, _ = vab.shape
+        n, h8, w8, _ = vf.shape
+        key = ("gmhs", h, w, full_w, level, n)
+        if key not in self.plans:
+            self.plans[key] = self.fh.gmhs_workspace(h, w, full_w, level, self.dev, n)
+        ws = self.plans[key]
+        p = self.fh.gmhs_params(h, w, full_w, level)
+        nbytes = n * (5 * 4 * 2 * h8 * w8 + 2 * 3 * 2 * h * w + 4 * p["hc"] * p["wc"] * (5 + 5 + 5 + 3) + 4 * 2 * h8 * w8)
+        self._go("gmhs (fit x4, cost, texture window, decision window x2)",
+                 lambda: self.fh.gmhs_n(vab, vf, full_w, level, ws=ws, stream=self.stream), nbytes, kernels=8)
+
     # the fused chains (one launch each) unless asked for the ops one by one
     def coarse_up(self, o: V, out: V, state: Optional[V], oh: int, ow: int, flow_scale: float):
         if not self.chains:
@@ -611,6 +650,13 @@ class GpuBackend(ComposedChains):
             return super().refine_input(q, flow, vis, rx, flow_out_scale, blend)
         vs = [self._v(x) for x in (q, flow, vis, rx)]
         self._go("refine_input", lambda: self.fh.refine_input(*vs, flow_out_scale, stream=self.stream),
+                 2 * self._px(flow) * (6 + 4 + 3 + 14))
+
+    def refine_input_n(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V, qmod: int):
+        if not self.chains:
+            return super().refine_input_n(q, flow, vis, rx, flow_out_scale, blend, qmod)
+        vs = [self._v(x) for x in (q, flow, vis, rx)]
+        self._go("refine_input", lambda: self.fh.refine_input(*vs, flow_out_scale, qmod=qmod, stream=self.stream),
                  2 * self._px(flow) * (6 + 4 + 3 + 14))
 
 
@@ -716,17 +762,13 @@ class FlyHighFG:
                 be.frame_input(self.frames, self.full, V(self.AB), self.hp, self.wp, nh, nw)
             else:
                 be.rgba_in(self.frames, V(self.AB), nh, nw)
-        for p in range(P):                                                                    # 0-1, 14-24
-            be.pair_input(V(sl(self.AB, 2 * p, 2)), V(sl(self.aq, 2 * p, 2)), V(sl(self.i8, 2 * p, 2)),
-                          V(sl(self.cin, p), 144), V(sl(self.l16, p)), qh, qw)
+        be.pair_input(V(self.AB), V(self.aq), V(self.i8), V(self.cin, 144), V(self.l16), qh, qw)  # 0-1, 14-24
         be.pair("enc.e1", "enc.e2", V(self.aq), V(self.e1), V(self.f8), True)                 # 2-4, 8-10
         be.pair("enc.e3", "enc.e4", V(self.f8), V(self.e3), V(self.f16), True)                # 5-7, 11-13
         # 26, 43: f16a f16b into the concat and the state, beside the 1/16 lumas' cost volume (25, 26; 19-20 zeros),
         # which reads and writes nothing the encoders touch
-        for p in range(P):
-            cin, l16 = sl(self.cin, p), sl(self.l16, p)
-            be.fold_pair_sad(V(sl(self.f16, 2 * p, 2)), 72, V(cin, 0), V(sl(self.state_out, p), 0), V(l16, 0),
-                             V(l16, 1), V(cin, 230), 3)
+        be.fold_pair_sad(V(self.f16), 72, V(self.cin, 0), V(self.state_out, 0), V(self.l16, 0), V(self.l16, 1),
+                         V(self.cin, 230), 3)
         be.conv("coarse.c1", V(self.cin), V(self.ch1))                                        # 27
         be.conv("coarse.c2", V(self.ch1), V(self.ch2))                                        # 28
         be.conv("coarse.c3", V(self.ch2), V(self.ch3r), V(self.ch1))                          # 29, 30
@@ -734,10 +776,8 @@ class FlyHighFG:
         be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
         # 33-40 (43: flow16), then the fine loop's input, K = 1 (op 42: wa .. flow8); h enters as zeros (op 41: the
         # fx slice is never written)
-        for p in range(P):
-            be.coarse_fine_input(V(sl(self.o, p)), V(sl(self.fv, p)), V(sl(self.state_out, p), 72), 16.0,
-                                 V(sl(self.f8, 2 * p, 2)), V(sl(self.i8, 2 * p, 2)), 0.125, V(sl(self.fx, p)),
-                                 V(sl(self.l8, p)), 36)
+        be.coarse_fine_input(V(self.o), V(self.fv), V(self.state_out, 72), 16.0, V(self.f8), V(self.i8), 0.125,
+                             V(self.fx), V(self.l8), 36)
         be.sad(V(self.l8, 0), V(self.l8, 1), V(self.fx, 130), 2)                              # fcv
         be.conv("fine.r1", V(self.fx), V(self.fr1))
         be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
@@ -752,9 +792,7 @@ class FlyHighFG:
                          V(self.dfilm))
             return True
         if self.repair:  # the periodic-structure repair of each pair's flow, in place (gmhs.rs:149-206)
-            for p in range(P):
-                be.gmhs(V(sl(self.AB, 2 * p)), V(sl(self.AB, 2 * p + 1)), V(sl(self.fv, p)), self.full_w,
-                        self.repair)
+            be.gmhs_n(V(self.AB), V(self.fv), self.full_w, self.repair)
         return False
 
     def pair_mid(self, t: float, W: Optional[dict] = None):
@@ -815,10 +853,8 @@ class FlyHighFG:
             be.conv("film.out", V(m(self.fh2)), V(m(self.dfilm)))                             # 53
         be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(m(self.dfilm)), t, V(m(self.up7)), V(m(self.ftvt)),
                              V(m(self.lin)), V(m(self.dvis)))                                 # 44-48, 54-62
-        for p in range(P):                                                                    # 63-76
-            i = j * P + p
-            be.refine_input(V(sl(self.aq, 2 * p, 2)), V(sl(self.up7, i), 0, 0.25), V(sl(self.up7, i), 4),
-                            V(sl(self.rx, i)), 0.05, V(sl(self.blend, i)))
+        be.refine_input_n(V(self.aq), V(m(self.up7), 0, 0.25), V(m(self.up7), 4), V(m(self.rx)), 0.05,
+                          V(m(self.blend)), P)                                                # 63-76
 
     def _mid_tail(self):
         """ops 77-82 for all M * P images: the refine head at once, then each image's render."""

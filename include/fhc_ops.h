@@ -169,6 +169,12 @@ int fhc_pair_pyramid(const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor
 int fhc_pair_input(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16,
                    const fhc_tensor* l16, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow, void* stream);
 
+/* fhc_pair_input for `pairs` pairs in one launch: pair k's pictures are images 2k, 2k + 1 of ab, q and i8, its
+ * i16 and l16 image k. Bit-identical to one call per pair. */
+int fhc_pair_input_n(const fhc_tensor* ab, const fhc_tensor* q, const fhc_tensor* i8, const fhc_tensor* i16,
+                     const fhc_tensor* l16, uint32_t ih, uint32_t iw, uint32_t oh, uint32_t ow, uint32_t pairs,
+                     void* stream);
+
 /* graph.json ops 7, 13 (the encoders' outputs f16a, f16b), their places in the concat of op 26 and f16b's in the
  * streaming state of op 43: x (2, h, w, c) holds both pictures' features as a batch; image i is copied to channels
  * c0 + i * c of out (batch 1) and image 1 also to `also` when not NULL. Lets the encoders run as one batch. */
@@ -200,6 +206,11 @@ int fhc_flow_vis_t(const fhc_tensor* fv, const fhc_tensor* dfilm, const fhc_tens
  * c0 rwa, +3 rwb, +6 vis (copied), +9 the raw flow times flow_out_scale, +13 the gradient. */
 int fhc_refine_input(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rx,
                      uint32_t h, uint32_t w, float flow_out_scale, void* stream);
+/* fhc_refine_input over n images in one launch: image i of flow, vis and rx (each view's tensor holding n images of
+ * h x w) takes its two pictures from pair i % qmod of q (images 2p and 2p + 1 of a tensor of 2 qmod images), as a
+ * batch of frame pairs and their phases lays them out. Bit-identical to n calls. 1 <= qmod <= n. */
+int fhc_refine_input_n(const fhc_tensor* q, const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rx,
+                       uint32_t h, uint32_t w, float flow_out_scale, uint32_t n, uint32_t qmod, void* stream);
 
 
 /* coarse_up then the fine block's input in one launch (graph ops 33-40 with 43's flow16, then op 42's input): the
@@ -211,6 +222,13 @@ int fhc_coarse_fine_input(const fhc_tensor* o, const fhc_tensor* fv, const fhc_t
                           float flow_scale, const fhc_tensor* f8, const fhc_tensor* i8, float fine_scale,
                           const fhc_tensor* fx, const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c,
                           void* stream);
+
+/* fhc_coarse_fine_input for `pairs` pairs in one launch: pair k's maps and pictures are images 2k, 2k + 1 of f8 and
+ * i8, its image k of o, fv, state, fx and l8. Bit-identical to one call per pair. */
+int fhc_coarse_fine_input_n(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state, uint32_t hi,
+                            uint32_t wi, float flow_scale, const fhc_tensor* f8, const fhc_tensor* i8,
+                            float fine_scale, const fhc_tensor* fx, const fhc_tensor* l8, uint32_t h, uint32_t w,
+                            uint32_t c, uint32_t pairs, void* stream);
 
 /* fhc_flow_vis_t then fhc_convex_upsample of its output in one launch (graph ops 44-48, 54-62): the convex
  * upsample's 7-channel input (flow_t | vis_t) computed from fv and dfilm at phase t while it is staged, never
@@ -225,6 +243,13 @@ int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_
 int fhc_fold_pair_sad(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h, uint32_t w,
                       uint32_t c, const fhc_tensor* la, const fhc_tensor* lb, const fhc_tensor* sad_out, uint32_t sn,
                       uint32_t sh, uint32_t sw, uint32_t radius, void* stream);
+
+/* fhc_fold_pair_sad with the fold over `pairs` pairs: pair k's two maps are images 2k, 2k + 1 of x, its fold
+ * image k of out (and of also). Bit-identical to one call per pair. */
+int fhc_fold_pair_sad_n(const fhc_tensor* x, const fhc_tensor* out, const fhc_tensor* also, uint32_t h, uint32_t w,
+                        uint32_t c, uint32_t pairs, const fhc_tensor* la, const fhc_tensor* lb,
+                        const fhc_tensor* sad_out, uint32_t sn, uint32_t sh, uint32_t sw, uint32_t radius,
+                        void* stream);
 
 /* GMHS, the periodic-structure repair of the pair's E8 flow (crates/flyhigh-engine/src/gmhs.rs:149-206, run at the
  * end of the pair stage when the repair level is above 0, net/build.rs:640-660; the reference's default level is 1,
@@ -260,6 +285,14 @@ int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc
  * Eight launches on `stream`. Replaces gmhs::gm_steps and its 14 dispatches. */
 int fhc_gmhs(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
              uint32_t w8, uint32_t full_w, uint32_t level, void* ws, size_t ws_bytes, void* stream);
+
+/* fhc_gmhs for `pairs` independent pairs in the same eight launches: pair k's pictures are the images 2k past a and
+ * b (a and b: images 0 and 1 of a buffer holding the pairs' pictures A0 B0 A1 B1 ...), its flow image k of flow,
+ * its workspace at k * S bytes past ws, S = ws_bytes of fhc_gmhs_params rounded up to 256 (ws_bytes given >=
+ * (pairs - 1) * S + that ws_bytes). Bit-identical to fhc_gmhs on each pair. The reference repairs one pair a
+ * session (gmhs::gm_steps, gmhs.rs:149-206); this is the batched sessions' form. */
+int fhc_gmhs_n(const fhc_tensor* a, const fhc_tensor* b, uint32_t h, uint32_t w, const fhc_tensor* flow, uint32_t h8,
+               uint32_t w8, uint32_t full_w, uint32_t level, uint32_t pairs, void* ws, size_t ws_bytes, void* stream);
 
 /* fhc_gmhs and the FiLM head: a FiLM pair plan (fhc_conv_pair_plan_create with FHC_PAIR_FILM_IN, fhc_conv.h) run
  * as fhc_conv_pair_run_film(pair, pair_x, pair_film, pair_y) runs it, with its workgroups inside the repair's first

@@ -75,6 +75,37 @@ def test_coarse_fine_input_equals_coarse_up_then_fine_input(hi, wi, h, w, c, cs,
         same(outs[0][k], outs[1][k], k)
 
 
+@pytest.mark.parametrize("P,hi,wi,h,w,c,cs,state", [(3, 5, 9, 13, 21, 36, 40, True), (2, 7, 6, 20, 11, 6, 9, False)])
+def test_coarse_fine_input_batched_equals_one_pair_at_a_time(P, hi, wi, h, w, c, cs, state):
+    """P pairs in one launch (pair k: image k of o, fv, state, fx, l8; images 2k, 2k + 1 of f8 and i8) against one
+    fused launch per pair and against the ops one by one."""
+    say("coarse_fine_input batched", P, hi, wi, h, w, c, cs, state)
+    outs = []
+    fused, composed = backends()
+    for be, batched in ((fused, True), (composed, True), (fused, False)):
+        rng = np.random.default_rng(P * 100 + h)
+        o = fill(be, rng, P, hi, wi, 16, -3.0, 3.0)
+        f8 = fill(be, rng, 2 * P, h, w, cs)
+        i8 = fill(be, rng, 2 * P, h, w, 4, 0.0, 1.0)
+        fv = fill(be, rng, P, h, w, 8)
+        fx = fill(be, rng, P, h, w, 2 * c + 12)
+        l8 = fill(be, rng, P, h, w, 4)
+        st = fill(be, rng, P, hi, wi, 80) if state else None
+        if batched:
+            be.coarse_fine_input(V(o), V(fv), None if st is None else V(st, 72), 16.0, V(f8, cs - c), V(i8), 0.125,
+                                 V(fx, 1), V(l8, 1), c)
+        else:
+            for k in range(P):
+                one, two = (lambda t: net.sl(t, k)), (lambda t: net.sl(t, 2 * k, 2))
+                be.coarse_fine_input(V(one(o)), V(one(fv)), None if st is None else V(one(st), 72), 16.0,
+                                     V(two(f8), cs - c), V(two(i8)), 0.125, V(one(fx), 1), V(one(l8), 1), c)
+        outs.append({k: be.host(t).copy() for k, t in (("fv", fv), ("fx", fx), ("l8", l8), ("state", st))
+                     if t is not None})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k + " (batched vs op by op)")
+        same(outs[0][k], outs[2][k], k + " (batched vs one launch per pair)")
+
+
 @pytest.mark.parametrize("n,h,w,t", [(2, 9, 13, 0.3), (1, 60, 108, 0.5), (1, 5, 4, 1.0)])
 def test_flow_vis_t_convex_equals_flow_vis_t_then_convex(n, h, w, t):
     say("flow_vis_t_convex", n, h, w, t)
@@ -109,6 +140,33 @@ def test_pair_input_equals_resize_then_pyramid(H, W, oh, ow):
         same(outs[0][k], outs[1][k], k)
 
 
+# the one-launch form, and a downscale too steep for it (the resize, then each pair's pyramid)
+@pytest.mark.parametrize("P,H,W,oh,ow", [(3, 100, 150, 24, 36), (2, 400, 300, 20, 16)])
+def test_pair_input_batched_equals_one_pair_at_a_time(P, H, W, oh, ow):
+    """P pairs in one call (pair k: images 2k, 2k + 1 of ab, q and i8, image k of i16 and l16) against one call per
+    pair and against the ops one by one."""
+    say("pair_input batched", P, H, W, oh, ow)
+    outs = []
+    fused, composed = backends()
+    for be, batched in ((fused, True), (composed, True), (fused, False)):
+        rng = np.random.default_rng(P + H + ow)
+        ab = fill(be, rng, 2 * P, H, W, 4, 0.0, 1.0)
+        q = fill(be, rng, 2 * P, oh, ow, 8)
+        i8 = fill(be, rng, 2 * P, oh // 2, ow // 2, 8)
+        i16 = fill(be, rng, P, oh // 4, ow // 4, 16)
+        l16 = fill(be, rng, P, oh // 4, ow // 4, 4)
+        if batched:
+            be.pair_input(V(ab), V(q), V(i8), V(i16, 6), V(l16, 1), oh, ow)
+        else:
+            for k in range(P):
+                one, two = (lambda t: net.sl(t, k)), (lambda t: net.sl(t, 2 * k, 2))
+                be.pair_input(V(two(ab)), V(two(q)), V(two(i8)), V(one(i16), 6), V(one(l16), 1), oh, ow)
+        outs.append({k: be.host(t).copy() for k, t in (("q", q), ("i8", i8), ("i16", i16), ("l16", l16))})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k + " (batched vs op by op)")
+        same(outs[0][k], outs[2][k], k + " (batched vs one call per pair)")
+
+
 @pytest.mark.parametrize("h,w", [(13, 21), (120, 216), (7, 9)])
 def test_refine_input_equals_its_ops(h, w):
     say("refine_input", h, w)
@@ -122,6 +180,30 @@ def test_refine_input_equals_its_ops(h, w):
         be.refine_input(V(q), V(up7, 0, 0.25), V(up7, 4), V(rx), 0.05, V(blend))
         outs.append(be.host(rx)[..., :14].copy())
     same(outs[0], outs[1], "rx")
+
+
+@pytest.mark.parametrize("n,qmod,h,w", [(6, 3, 13, 21), (4, 4, 7, 9), (3, 1, 120, 216)])
+def test_refine_input_batched_equals_one_image_at_a_time(n, qmod, h, w):
+    """The batched launch (image k's pictures pair k % qmod of q) against one fused launch per image and against the
+    op-by-op chain of each image."""
+    say("refine_input_n", n, qmod, h, w)
+    outs = []
+    fused, composed = backends()
+    for be, batched in ((fused, True), (composed, False), (fused, False)):
+        rng = np.random.default_rng(n * h + w)
+        q = fill(be, rng, 2 * qmod, h, w, 8, 0.0, 1.0)
+        up7 = fill(be, rng, n, h, w, 8, -6.0, 6.0)
+        rx = fill(be, rng, n, h, w, 16)
+        blend = be.zeros(n, h, w, 8)
+        if batched:
+            be.refine_input_n(V(q), V(up7, 0, 0.25), V(up7, 4), V(rx, 1), 0.05, V(blend), qmod)
+        else:
+            for k in range(n):
+                be.refine_input(V(net.sl(q, 2 * (k % qmod), 2)), V(net.sl(up7, k), 0, 0.25), V(net.sl(up7, k), 4),
+                                V(net.sl(rx, k), 1), 0.05, V(net.sl(blend, k)))
+        outs.append(be.host(rx).copy())
+    same(outs[0], outs[1], "rx (batched vs op by op)")
+    same(outs[0], outs[2], "rx (batched vs one launch per image)")
 
 
 @pytest.mark.parametrize("h,w,c,also,sh,sw,r", [(30, 54, 72, True, 30, 54, 3), (9, 13, 6, False, 5, 7, 2),
@@ -144,6 +226,33 @@ def test_fold_pair_sad_equals_fold_pair_and_sad(h, w, c, also, sh, sw, r):
                      if t is not None})
     for k in outs[0]:
         same(outs[0][k], outs[1][k], k)
+
+
+@pytest.mark.parametrize("P,h,w,c,also", [(3, 30, 54, 72, True), (2, 9, 13, 6, False)])
+def test_fold_pair_sad_batched_equals_one_pair_at_a_time(P, h, w, c, also):
+    """P pairs' folds in one launch (pair k: maps 2k, 2k + 1 into image k) beside a cost volume over P images,
+    against one fused launch per pair and against the ops one by one."""
+    say("fold_pair_sad batched", P, h, w, c, also)
+    outs = []
+    fused, composed = backends()
+    for be, batched in ((fused, True), (composed, True), (fused, False)):
+        rng = np.random.default_rng(P * h + c)
+        x = fill(be, rng, 2 * P, h, w, c + 4)
+        out = fill(be, rng, P, h, w, 2 * c + 8)
+        st = fill(be, rng, P, h, w, c + 4) if also else None
+        l = fill(be, rng, P, h // 2, w // 2, 4, 0.0, 1.0)
+        so = fill(be, rng, P, h // 2, w // 2, 53)
+        if batched:
+            be.fold_pair_sad(V(x, 2), c, V(out, 4), None if st is None else V(st, 1), V(l, 0), V(l, 2), V(so, 3), 3)
+        else:
+            for k in range(P):
+                sk = lambda t: net.sl(t, k)  # noqa: E731
+                be.fold_pair_sad(V(net.sl(x, 2 * k, 2), 2), c, V(sk(out), 4), None if st is None else V(sk(st), 1),
+                                 V(sk(l), 0), V(sk(l), 2), V(sk(so), 3), 3)
+        outs.append({k: be.host(t).copy() for k, t in (("out", out), ("also", st), ("sad", so)) if t is not None})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k + " (batched vs op by op)")
+        same(outs[0][k], outs[2][k], k + " (batched vs one launch per pair)")
 
 
 @pytest.mark.parametrize("h,w", [(120, 216), (13, 30), (5, 7)])

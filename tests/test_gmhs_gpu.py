@@ -126,3 +126,50 @@ def test_gmhs_level_0_and_errors():
         fh.gmhs(a, a, flow, 16, 1)
     with pytest.raises(fh.FhcError, match="repair level"):
         fh.gmhs_params(32, 32, 64, 3)
+
+
+@pytest.mark.parametrize("h,w,full_w,cs,level,striped", [(100, 150, 160, 8, 1, False), (256, 384, 768, 8, 1, True),
+                                                         (70, 90, 128, 6, 2, False)])
+def test_gmhs_n_repairs_each_pair_as_the_oracle(h, w, full_w, cs, level, striped):
+    """Three pairs in one fhc_gmhs_n (pictures A0 B0 A1 B1 A2 B2 in one buffer, the flows in another, the workspaces
+    NaN-poisoned): each pair's coefficients, maps, decision values and flow equal the oracle's stage on that pair."""
+    import torch
+    say("gmhs_n", h, w, full_w, cs, level, striped)
+    fh = fhops()
+    rng = np.random.default_rng(h + w)
+    pics, flows = [], []
+    for k in range(3):
+        if striped and k == 1:
+            a, b = striped_scene(h, w, 6)
+            f = [np.full((h // 8, w // 8), v) for v in (-3.0, 0.0, 3.0, 0.0)]
+            f[0][8:16, 10:22], f[2][8:16, 10:22] = 5.0, -5.0
+            fl = np.zeros((1, h // 8, w // 8, cs), np.uint16)
+            fl[0, ..., :4] = f16(np.stack(f, -1))
+        else:
+            a = f16(rng.uniform(0, 1, (1, h, w, 4)))
+            b = np.roll(a, (k + 1, -2 * k - 1), axis=(1, 2)).copy()
+            fl = smooth_flow(rng, h // 8, w // 8, cs)
+        pics += [a, b]
+        flows.append(fl)
+    ab, fd = dev(np.concatenate(pics)), dev(np.concatenate(flows))
+    ws = fh.gmhs_workspace(h, w, full_w, level, "cuda", 3)
+    ws.view(torch.float32)[:ws.numel() // 4].fill_(float("nan"))
+    fh.gmhs_n(ab, fd, full_w, level, ws=ws)
+    got_flow = host(fd).view(np.uint16)
+    stride = fh.gmhs_ws_stride(h, w, full_w, level)
+    changed = 0
+    for k in range(3):
+        coef, maps, dec = (host(x) for x in fh.gmhs_results(ws[k * stride:], h, w, full_w, level, h // 8, w // 8))
+        want_flow, want_coef, want_maps, want_dec = oracle.gmhs_stages(pics[2 * k], pics[2 * k + 1], flows[k],
+                                                                       full_w, level)
+        assert np.array_equal(coef.view(np.uint32), want_coef.view(np.uint32)), f"pair {k}: coef"
+        for m in range(5):
+            assert np.array_equal(maps[m].view(np.uint32), want_maps[m].view(np.uint32)), f"pair {k}: map {m}"
+            assert np.array_equal(dec[m].view(np.uint32), want_dec[m].view(np.uint32)), f"pair {k}: decision {m}"
+        bad = np.argwhere(got_flow[k:k + 1] != want_flow)
+        assert bad.size == 0, f"pair {k}: flow: {len(bad)} elements differ, first at {bad[0].tolist()}"
+        changed += (want_flow != flows[k]).any(-1).sum()
+    if striped:
+        assert changed > 20  # the select fired on the striped pair
+    with pytest.raises(fh.FhcError, match="workspace"):
+        fh.gmhs_n(ab, fd, full_w, level, ws=ws[:2 * stride])
