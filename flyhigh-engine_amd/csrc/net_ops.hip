@@ -1511,12 +1511,13 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
 // 4-channel pixels (channel 3 written 0): rgba_in.wgsl then interp.wgsl:11-45 with antialias, as
 // interp_aa_lds_kernel computes it. A workgroup stages the union of its 16 x 16 outputs' windows, at most
 // EXT x EXT padded pixels (EXT <= 16 * R, the lanes' R x R load stripes covering it), each converted once; the
-// values are those of the f16 picture rgba_in writes. LAY: how a staged pixel is held in LDS, as a float4 (16 bytes,
-// no widening per tap), as f16 (8 bytes: three widenings per tap) or as an f32 pair plus an f32 (12 bytes, two reads
-// per tap, no widening). The LDS a workgroup holds sets how many share a CU, and the kernel runs at the rate its
-// waves in flight allow: at 1080p (a 39 x 38 window) 40 x 40 pixels held as f32 pair + f32 (21 KiB with the tables)
-// let seven workgroups share a CU and take 12.8 us, as f16 (15 KiB, eight) 13.1 us, as float4 (27 KiB, five)
-// 15.7 us, 48 x 48 as float4 (38 KiB, four) 16.0 us.
+// values are those of the f16 picture rgba_in writes. LAY: how a staged pixel is held in LDS, as a float4 (16 bytes),
+// as f16 (8 bytes, each tap's product one mixed-precision FMA that takes the f16 value as it is) or as an f32 pair
+// plus an f32 (12 bytes, two reads per tap). The LDS a workgroup holds sets how many share a CU: f16 cells, the
+// fewest bytes at the same VALU count per tap, serve every dispatch. Measured (warm, two 1080p frames, a 39 x 38
+// window, 40 x 40 cells): f16 12.9 us, f32 pair + f32 14.8 us (with the taps widened one by one, f16 was 13.1 us
+// where the f32 pair + f32 took 12.8 and float4 15.7); sixteen 2160p frames (10 taps, 80 x 80 cells) 334 us, 379
+// with the taps widened one by one.
 template <int KM, int R, int EXT, int LAY>
 __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* src, uint32_t w, uint32_t h,
                                                                uint32_t pitch, uint64_t fstride, uint32_t ih,
@@ -1600,8 +1601,10 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
             if constexpr (LAY == 0) vv[0] = q.x, vv[1] = q.y, vv[2] = q.z;
             else if constexpr (LAY == 1) vv[0] = h2f((uint16_t)q.x), vv[1] = h2f((uint16_t)(q.x >> 16)), vv[2] = h2f((uint16_t)q.y);
             else vv[0] = q.x, vv[1] = q.y, vv[2] = tileb[lrow + lc[jx]];
+            // f16 cells: each product as an FMA with +0, which takes the f16 tap as it is (one mixed-precision FMA,
+            // no widening) and rounds as the product does (taps and weights are >= 0, so no product is -0)
 #pragma unroll
-            for (int i = 0; i < 3; i++) acc[i] = acc[i] + vv[i] * wgt;
+            for (int i = 0; i < 3; i++) acc[i] = acc[i] + (LAY == 1 ? __builtin_fmaf(vv[i], wgt, 0.0f) : vv[i] * wgt);
             norm = norm + wgt;
         }
     }
@@ -2453,10 +2456,10 @@ extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_
         // the 40-pixel window covers the common downscales (1080p to 864 x 480: 39 x 38); 2160p to 864 x 480 takes
         // 10 taps and a 78 x 76 window (4096 x 2176: 81 columns); the 84 x 84 window of 8-byte cells keeps the
         // workgroup's LDS under 64 KiB
-        auto k = ext <= 40 && taps <= 5 ? rgba_resize_kernel<5, 3, 40, 2>
+        auto k = ext <= 40 && taps <= 5 ? rgba_resize_kernel<5, 3, 40, 1>
                  : ext <= 3 * kAaT
-                     ? (taps <= 5 ? rgba_resize_kernel<5, 3, 48, 2> : taps <= 6 ? rgba_resize_kernel<6, 3, 48, 2>
-                                                                    : rgba_resize_kernel<8, 3, 48, 2>)
+                     ? (taps <= 5 ? rgba_resize_kernel<5, 3, 48, 1> : taps <= 6 ? rgba_resize_kernel<6, 3, 48, 1>
+                                                                    : rgba_resize_kernel<8, 3, 48, 1>)
                  : ext <= 5 * kAaT
                      ? (taps <= 6 ? rgba_resize_kernel<6, 5, 80, 1> : taps <= 8 ? rgba_resize_kernel<8, 5, 80, 1>
                                                                     : rgba_resize_kernel<10, 5, 80, 1>)
