@@ -1317,26 +1317,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uin
 
 // sample_rgba's INNER case (every tap column inside the frame for the whole wave) through a buffer resource over
 // the frame: row y's taps at byte offset y * pitch4 + 4 (px - 1) (bicubic) or y * pitch4 + 4 px (bilinear); the same
-// taps, the same arithmetic.
-template <bool CUBIC, bool FMA>
+// taps, the same arithmetic. ROWS: every tap row inside the frame too for the whole wave, so no row is clamped and
+// row j's offset is the first row's plus the wave-uniform j * pitch4 (the load's scalar offset).
+template <bool CUBIC, bool FMA, bool ROWS = false>
 __device__ __forceinline__ void sample_rgba_inner(__amdgpu_buffer_rsrc_t rs, uint32_t pitch4, int hm1, int px, int py,
                                                   float tx, float ty, const float* tab, float (&o)[3]) {
     if constexpr (CUBIC) {
         const float cx[4] = {cub2m<FMA>(tx + 1.0f), cub1m<FMA>(tx), cub1m<FMA>(1.0f - tx), cub2m<FMA>(2.0f - tx)};
         const float cy[4] = {cub2m<FMA>(ty + 1.0f), cub1m<FMA>(ty), cub1m<FMA>(1.0f - ty), cub2m<FMA>(2.0f - ty)};
         const uint32_t col4 = (uint32_t)(px - 1) * 4u;
+        const uint32_t row0 = ROWS ? __umul24((uint32_t)(py - 1), pitch4) + col4 : 0u;
         uint32_t t[4][4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const uint32_t yy = (uint32_t)min(max(py - 1 + j, 0), hm1);
-            const uint4 q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, __umul24(yy, pitch4) + col4, 0, 0));
+            uint4 q;
+            if constexpr (ROWS) {
+                q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, row0, (uint32_t)j * pitch4, 0));
+            } else {
+                const uint32_t yy = (uint32_t)min(max(py - 1 + j, 0), hm1);
+                q = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, __umul24(yy, pitch4) + col4, 0, 0));
+            }
             t[j][0] = q.x, t[j][1] = q.y, t[j][2] = q.z, t[j][3] = q.w;
         }
 #pragma unroll
         for (int c = 0; c < 3; c++) o[c] = cubic_sum<FMA>(t, cx, cy, tab, c);
     } else {
         const uint32_t col4 = (uint32_t)px * 4u;
-        const uint32_t ya = (uint32_t)min(max(py, 0), hm1), yb = (uint32_t)min(max(py + 1, 0), hm1);
+        const uint32_t ya = ROWS ? (uint32_t)py : (uint32_t)min(max(py, 0), hm1);
+        const uint32_t yb = ROWS ? (uint32_t)py + 1u : (uint32_t)min(max(py + 1, 0), hm1);
         const uint2 q0 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, __umul24(ya, pitch4) + col4, 0, 0));
         const uint2 q1 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, __umul24(yb, pitch4) + col4, 0, 0));
 #pragma unroll
@@ -1367,10 +1375,14 @@ __device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const flo
     const float gxa = (float)x + f[0], gya = (float)y + f[1], gxb = (float)x + f[2], gyb = (float)y + f[3];
     const int pxa = (int)floorf(gxa), pya = (int)floorf(gya), pxb = (int)floorf(gxb), pyb = (int)floorf(gyb);
     const float txa = gxa - (float)pxa, tya = gya - (float)pya, txb = gxb - (float)pxb, tyb = gyb - (float)pyb;
-    const int lo = CUBIC ? 1 : 0, hi = (int)w - (CUBIC ? 3 : 2);
+    const int lo = CUBIC ? 1 : 0, hi = (int)w - (CUBIC ? 3 : 2), hir = (int)h - (CUBIC ? 3 : 2);
     const bool inner = pxa >= lo && pxa <= hi && pxb >= lo && pxb <= hi;
-    if (__all(inner)) {
-        const uint32_t fbytes = ((h - 1) * pitch + w) * 4u, pitch4 = pitch * 4u;
+    const bool rows = pya >= lo && pya <= hir && pyb >= lo && pyb <= hir;
+    const uint32_t fbytes = ((h - 1) * pitch + w) * 4u, pitch4 = pitch * 4u;
+    if (__all(inner && rows)) {
+        sample_rgba_inner<CUBIC, FMA, true>(buf_rsrc(fa, fbytes), pitch4, (int)h - 1, pxa, pya, txa, tya, tab, ca);
+        sample_rgba_inner<CUBIC, FMA, true>(buf_rsrc(fb, fbytes), pitch4, (int)h - 1, pxb, pyb, txb, tyb, tab, cb);
+    } else if (__all(inner)) {
         sample_rgba_inner<CUBIC, FMA>(buf_rsrc(fa, fbytes), pitch4, (int)h - 1, pxa, pya, txa, tya, tab, ca);
         sample_rgba_inner<CUBIC, FMA>(buf_rsrc(fb, fbytes), pitch4, (int)h - 1, pxb, pyb, txb, tyb, tab, cb);
     } else {
