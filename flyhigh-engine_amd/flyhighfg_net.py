@@ -857,11 +857,12 @@ class FlyHighFG:
                           V(m(self.blend)), P)                                                # 63-76
 
     def _mid_tail(self):
-        """ops 77-82 for all M * P images: the refine head at once, then each image's render."""
+        """ops 77-82 for all M * P images: the refine head at once, then each image's render, pair by pair (a pair's
+        M renders read the same two frames, which the last-level cache then still holds for all but the first)."""
         be, P = self.be, self.P
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
         be.pair_affine_out("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), V(self.Rt), 3)  # 79-81
-        for i in range(self.M * P):
+        for i in (j * P + p for p in range(P) for j in range(self.M)):
             p = i % P
             up7, rt = sl(self.up7, i), sl(self.Rt, i)
             if self.frame is not None and self.internal:  # the render at the frame size, to the RGBA8 frame
