@@ -1218,7 +1218,7 @@ def main():
     if dom["label"].startswith("frame_render"):
         # 1920 x 1088 lanes of bicubic sampling in the reference's f32 order: the SQ counters put it at ~900 VALU
         # instructions per wave over 32,400 waves, the VALU issue rate of the chip, far below the HBM roofline
-        roofline["note"] = "VALU issue-bound: ~526 VALU instructions per wave, 32,400 waves (SQ counter pass)"
+        roofline["note"] = "VALU issue-bound: ~509 VALU instructions per wave, 32,400 waves (SQ counter pass)"
     log("bench: dominant launch", json.dumps(roofline))
 
     cpu = None
