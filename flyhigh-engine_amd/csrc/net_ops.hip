@@ -886,13 +886,14 @@ __global__ __launch_bounds__(64) void refine_input_kernel(View q, View fl, View 
 // and image 1 also to `also` (the streaming state's f16b), when given. Bits are copied. One lane per (pixel,
 // image, 4 channels); VEC: 8-byte copies.
 template <bool VEC>
+// pair: pair k's two maps are images 2k, 2k + 1 of x, its fold image k of out and also
 __device__ __forceinline__ void fold_pair_at(const View& x, const OView& out, const OView& also, uint32_t hw,
-                                             uint32_t c, uint32_t groups, uint32_t t) {
-    // pix runs over the pairs' pixels: pair k's pictures are images 2k, 2k + 1 of x, its output image k
-    const uint32_t g = t % groups, r = t / groups, img = r % 2, pix = r / 2, ch = g * 4, pair = pix / hw;
-    const uint16_t* src = x.p + ((size_t)(pair + img) * hw + pix) * x.cs + x.c0 + ch;
-    uint16_t* dst = out.p + (size_t)pix * out.cs + out.c0 + img * c + ch;
-    uint16_t* dst2 = also.p ? also.p + (size_t)pix * also.cs + also.c0 + ch : nullptr;
+                                             uint32_t c, uint32_t groups, uint32_t t, uint32_t pair) {
+    const uint32_t g = t % groups, r = t / groups, img = r % 2, pix = r / 2, ch = g * 4;
+    const size_t opix = (size_t)pair * hw + pix;
+    const uint16_t* src = x.p + ((size_t)(2 * pair + img) * hw + pix) * x.cs + x.c0 + ch;
+    uint16_t* dst = out.p + opix * out.cs + out.c0 + img * c + ch;
+    uint16_t* dst2 = also.p ? also.p + opix * also.cs + also.c0 + ch : nullptr;
     if constexpr (VEC) {
         const uint2 v = *reinterpret_cast<const uint2*>(src);
         *reinterpret_cast<uint2*>(dst) = v;
@@ -908,12 +909,12 @@ template <bool VEC>
 __global__ __launch_bounds__(kThreads) void fold_pair_kernel(View x, OView out, OView also, uint32_t hw, uint32_t c,
                                                              uint32_t groups, uint32_t items) {
     const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-    if (t < items) fold_pair_at<VEC>(x, out, also, hw, c, groups, t);
+    if (t < items) fold_pair_at<VEC>(x, out, also, hw, c, groups, t, 0);
 }
 
 // fold_pair and a sad_volume that neither reads what the other writes, side by side in one launch: blocks below
-// fold_blocks run the fold, the rest the cost volume (pair() folds the second encoder pair's output while the 1/16
-// lumas' cost volume, ready since the pyramid, is computed)
+// fold_blocks run the fold of pair blockIdx.y, the rest (of row 0) the cost volume (pair() folds the second encoder
+// pair's output while the 1/16 lumas' cost volume, ready since the pyramid, is computed)
 struct SadArgs {
     View la, lb;
     OView out;
@@ -925,8 +926,8 @@ __global__ __launch_bounds__(kThreads) void fold_pair_sad_kernel(View x, OView o
                                                                  uint32_t fold_blocks, SadArgs sa) {
     if (blockIdx.x < fold_blocks) {
         const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-        if (t < items) fold_pair_at<VEC>(x, out, also, hw, c, groups, t);
-    } else {
+        if (t < items) fold_pair_at<VEC>(x, out, also, hw, c, groups, t, blockIdx.y);
+    } else if (blockIdx.y == 0) {
         const uint32_t t = (blockIdx.x - fold_blocks) * kThreads + threadIdx.x;
         if (t < sa.items) sad_at(sa.la, sa.lb, sa.out, sa.h, sa.w, sa.r, sa.span2, t);
     }
@@ -2702,8 +2703,9 @@ extern "C" int fhc_fold_pair_sad_n(const fhc_tensor* x, const fhc_tensor* out, c
                                    void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
-        const uint64_t fold_items = (uint64_t)pairs * h * w * 2 * ((c + 3) / 4);
+        const uint64_t fold_items = (uint64_t)pairs * h * w * 2 * ((c + 3) / 4);  // all pairs'
         if (radius > 7) return fail(-1, "fold_pair_sad: radius %u above 7", radius);
+        if (pairs > 65535) return fail(-1, "fold_pair_sad: %u pairs exceed the launch limit", pairs);
         const uint32_t span2 = (2 * radius + 1) * (2 * radius + 1);
         const uint64_t sad_items = (uint64_t)sn * sh * sw * span2;
         if (fold_items == 0 && sad_items == 0) return 0;
@@ -2717,7 +2719,8 @@ extern "C" int fhc_fold_pair_sad_n(const fhc_tensor* x, const fhc_tensor* out, c
             FHC_TRY(check(lb, "fold_pair_sad lb", 1, false));
             FHC_TRY(check(sad_out, "fold_pair_sad sad out", span2, false, true));
         }
-        const uint64_t fb = (fold_items + kThreads - 1) / kThreads, sb = (sad_items + kThreads - 1) / kThreads;
+        const uint64_t fold1 = fold_items ? fold_items / pairs : 0;  // one pair's
+        const uint64_t fb = (fold1 + kThreads - 1) / kThreads, sb = (sad_items + kThreads - 1) / kThreads;
         if (fold_items >= kMaxItems || sad_items >= kMaxItems || fb + sb >= (1u << 31))
             return fail(-1, "fold_pair_sad: too many work items");
         bool v = false;
@@ -2735,8 +2738,8 @@ extern "C" int fhc_fold_pair_sad_n(const fhc_tensor* x, const fhc_tensor* out, c
         const SadArgs sa{sad_items ? in(la) : none, sad_items ? in(lb) : none,
                          sad_items ? outv(sad_out) : OView{nullptr, 0, 0}, sh, sw, radius, span2, (uint32_t)sad_items};
         auto k = v ? fold_pair_sad_kernel<true> : fold_pair_sad_kernel<false>;
-        hipLaunchKernelGGL(k, dim3((uint32_t)(fb + sb)), dim3(kThreads), 0, (hipStream_t)stream, xv, ov, a2, h * w, c,
-                           (c + 3) / 4, (uint32_t)fold_items, (uint32_t)fb, sa);
+        hipLaunchKernelGGL(k, dim3((uint32_t)(fb + sb), fold_items ? pairs : 1u), dim3(kThreads), 0,
+                           (hipStream_t)stream, xv, ov, a2, h * w, c, (c + 3) / 4, (uint32_t)fold1, (uint32_t)fb, sa);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "fold_pair_sad: launch failed: %s", hipGetErrorString(e));
     });
