@@ -1524,22 +1524,23 @@ __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* f
 // 4-channel pixels (channel 3 written 0): rgba_in.wgsl then interp.wgsl:11-45 with antialias, as
 // interp_aa_lds_kernel computes it. A workgroup stages the union of its 16 x 16 outputs' windows, at most
 // EXT x EXT padded pixels (EXT <= 16 * R, the lanes' R x R load stripes covering it), each converted once; the
-// values are those of the f16 picture rgba_in writes. LAY: how a staged pixel is held in LDS, as a float4 (16 bytes),
-// as f16 (8 bytes, each tap's product one mixed-precision FMA that takes the f16 value as it is) or as an f32 pair
-// plus an f32 (12 bytes, two reads per tap). The LDS a workgroup holds sets how many share a CU: f16 cells, the
-// fewest bytes at the same VALU count per tap, serve every dispatch. Measured (warm, two 1080p frames, a 39 x 38
-// window, 40 x 40 cells): f16 12.9 us, f32 pair + f32 14.8 us (with the taps widened one by one, f16 was 13.1 us
-// where the f32 pair + f32 took 12.8 and float4 15.7); sixteen 2160p frames (10 taps, 80 x 80 cells) 334 us, 379
-// with the taps widened one by one.
-template <int KM, int R, int EXT, int LAY>
+// values are those of the f16 picture rgba_in writes, held in LDS as f16: each tap's product is one mixed-precision
+// FMA that takes the f16 value as it is. SPLIT: a staged pixel's B, G in a 4-byte cell and its R in a 2-byte cell of
+// a second array (6 bytes, two reads a tap) rather than one 8-byte cell (one read). The LDS a workgroup holds sets
+// how many share a CU: the 6-byte cells let four 78 x 78 windows share one where three 80 x 80 8-byte windows do
+// not fit. Measured warm: sixteen 2160p frames (10 taps, a 78-pixel window) 334 us in 8-byte cells, 310 us split;
+// two 1080p frames (40 x 40 cells, occupancy bound by waves either way) 12.9 us in 8-byte cells against 14.8 us
+// for an f32 pair plus an f32 (12 bytes, all-f32 arithmetic); with each tap widened one instruction at a time the
+// 8-byte cells were the slower layout (13.1 against 12.8 us, and 379 us at 2160p).
+template <int KM, int R, int EXT, bool SPLIT>
 __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* src, uint32_t w, uint32_t h,
                                                                uint32_t pitch, uint64_t fstride, uint32_t ih,
                                                                uint32_t iw, OView out, uint32_t oh, uint32_t ow,
                                                                uint32_t tiles_x, uint32_t tiles_y, float sh, float sw) {
-    static_assert(EXT <= kAaT * R && LAY >= 0 && LAY <= 2, "the load stripes cover the window");
-    using Cell = typename std::conditional<LAY == 0, float4, typename std::conditional<LAY == 1, uint2, float2>::type>::type;
+    static_assert(EXT <= kAaT * R, "the load stripes cover the window");
+    using Cell = typename std::conditional<SPLIT, uint32_t, uint2>::type;
     __shared__ Cell tile[EXT * EXT];
-    __shared__ float tileb[LAY == 2 ? EXT * EXT : 1];
+    __shared__ uint16_t tileb[SPLIT ? EXT * EXT : 1];
     __shared__ float tab[256], wxs[kAaT * KM], wys[kAaT * KM];
     __shared__ int lcs[kAaT * KM], lrs[kAaT * KM];
     const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
@@ -1581,15 +1582,11 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
             const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(
                 rf, __umul24((uint32_t)min(ylo + row, (int)h - 1), pitch4) + (uint32_t)min(xlo + col, (int)w - 1) * 4u,
                 0, 0);
-            if constexpr (LAY == 0)
-                tile[row * EXT + col] = float4{unit_tab(tab, v, 0), unit_tab(tab, v, 1), unit_tab(tab, v, 2), 0.0f};
-            else if constexpr (LAY == 1)
-                tile[row * EXT + col] = uint2{(uint32_t)f2h(unit_tab(tab, v, 0)) |
-                                                  ((uint32_t)f2h(unit_tab(tab, v, 1)) << 16),
-                                              (uint32_t)f2h(unit_tab(tab, v, 2))};
+            const uint32_t c01 = (uint32_t)f2h(unit_tab(tab, v, 0)) | ((uint32_t)f2h(unit_tab(tab, v, 1)) << 16);
+            if constexpr (SPLIT)
+                tile[row * EXT + col] = c01, tileb[row * EXT + col] = f2h(unit_tab(tab, v, 2));
             else
-                tile[row * EXT + col] = float2{unit_tab(tab, v, 0), unit_tab(tab, v, 1)},
-                tileb[row * EXT + col] = unit_tab(tab, v, 2);
+                tile[row * EXT + col] = uint2{c01, (uint32_t)f2h(unit_tab(tab, v, 2))};
         }
     __syncthreads();
     const uint32_t ox = ox0 + tx, oy = oy0 + ty;
@@ -1611,13 +1608,12 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
             const float wgt = wx[jx] * wy;
             const Cell q = tile[lrow + lc[jx]];
             float vv[3];
-            if constexpr (LAY == 0) vv[0] = q.x, vv[1] = q.y, vv[2] = q.z;
-            else if constexpr (LAY == 1) vv[0] = h2f((uint16_t)q.x), vv[1] = h2f((uint16_t)(q.x >> 16)), vv[2] = h2f((uint16_t)q.y);
-            else vv[0] = q.x, vv[1] = q.y, vv[2] = tileb[lrow + lc[jx]];
-            // f16 cells: each product as an FMA with +0, which takes the f16 tap as it is (one mixed-precision FMA,
-            // no widening) and rounds as the product does (taps and weights are >= 0, so no product is -0)
+            if constexpr (SPLIT) vv[0] = h2f((uint16_t)q), vv[1] = h2f((uint16_t)(q >> 16)), vv[2] = h2f(tileb[lrow + lc[jx]]);
+            else vv[0] = h2f((uint16_t)q.x), vv[1] = h2f((uint16_t)(q.x >> 16)), vv[2] = h2f((uint16_t)q.y);
+            // each product as an FMA with +0, which takes the f16 tap as it is (one mixed-precision FMA, no
+            // widening) and rounds as the product does (taps and weights are >= 0, so no product is -0)
 #pragma unroll
-            for (int i = 0; i < 3; i++) acc[i] = acc[i] + (LAY == 1 ? __builtin_fmaf(vv[i], wgt, 0.0f) : vv[i] * wgt);
+            for (int i = 0; i < 3; i++) acc[i] = acc[i] + __builtin_fmaf(vv[i], wgt, 0.0f);
             norm = norm + wgt;
         }
     }
@@ -2467,16 +2463,15 @@ extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_
                         wp, hp, ow, oh, taps, ext);
         const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
         // the 40-pixel window covers the common downscales (1080p to 864 x 480: 39 x 38); 2160p to 864 x 480 takes
-        // 10 taps and a 78 x 76 window (4096 x 2176: 81 columns); the 84 x 84 window of 8-byte cells keeps the
-        // workgroup's LDS under 64 KiB
-        auto k = ext <= 40 && taps <= 5 ? rgba_resize_kernel<5, 3, 40, 1>
+        // 10 taps and a 78 x 76 window (4096 x 2176: 81 columns); the windows above 48 pixels hold 6-byte cells
+        // (78 x 78: 40,096 bytes of LDS with the tables, four workgroups a CU)
+        auto k = ext <= 40 && taps <= 5 ? rgba_resize_kernel<5, 3, 40, false>
                  : ext <= 3 * kAaT
-                     ? (taps <= 5 ? rgba_resize_kernel<5, 3, 48, 1> : taps <= 6 ? rgba_resize_kernel<6, 3, 48, 1>
-                                                                    : rgba_resize_kernel<8, 3, 48, 1>)
-                 : ext <= 5 * kAaT
-                     ? (taps <= 6 ? rgba_resize_kernel<6, 5, 80, 1> : taps <= 8 ? rgba_resize_kernel<8, 5, 80, 1>
-                                                                    : rgba_resize_kernel<10, 5, 80, 1>)
-                     : rgba_resize_kernel<10, 6, 84, 1>;
+                     ? (taps <= 5 ? rgba_resize_kernel<5, 3, 48, false> : taps <= 6 ? rgba_resize_kernel<6, 3, 48, false>
+                                                                        : rgba_resize_kernel<8, 3, 48, false>)
+                 : ext <= 5 * kAaT && taps <= 8
+                     ? (taps <= 6 ? rgba_resize_kernel<6, 5, 80, true> : rgba_resize_kernel<8, 5, 80, true>)
+                 : ext <= 78 ? rgba_resize_kernel<10, 5, 78, true> : rgba_resize_kernel<10, 6, 84, true>;
         if ((uint64_t)pitch * 4 >= (1u << 24) || (uint64_t)h * pitch * 4 >= (1u << 31))
             return fail(-1, "rgba_resize: frames of pitch %u and %u rows are too large", pitch, h);
         hipLaunchKernelGGL(k, dim3(n * tx * ty), dim3(kThreads), 0, (hipStream_t)stream,

@@ -321,7 +321,8 @@ def test_rgba_in_and_out_match_oracle(n, h, w, hp, wp, cs, c0):
 
 
 # the shapes reach each kernel instantiation (taps, window): (5, 40) at 1080p, (5, 48), (8, 80), (8, 48), (6, 48),
-# (6, 80), (10, 80) at 2160p (10 taps, a 78-pixel window), (10, 84) at 4096 x 2160 (an 81-pixel window)
+# (6, 80), (10, 78) at 2160p (10 taps, a 78-pixel window), (10, 84) at 4096 x 2160 (an 81-pixel window); the 80-,
+# 78- and 84-pixel windows hold split 6-byte cells, the others 8-byte cells
 @pytest.mark.parametrize("h,w,oh,ow", [(1080, 1920, 480, 864), (150, 300, 64, 128), (61, 97, 30, 40),
                                        (60, 30, 40, 8), (60, 30, 40, 11), (60, 90, 40, 32), (2160, 3840, 480, 864),
                                        (2160, 4096, 480, 864)])
