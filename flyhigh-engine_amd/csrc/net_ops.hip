@@ -1541,7 +1541,8 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
     using Cell = typename std::conditional<SPLIT, uint32_t, uint2>::type;
     __shared__ Cell tile[EXT * EXT];
     __shared__ uint16_t tileb[SPLIT ? EXT * EXT : 1];
-    __shared__ float tab[256], wxs[kAaT * KM], wys[kAaT * KM];
+    __shared__ uint16_t tab[256];  // entry b: the f16 bits rgba_in stores for byte b
+    __shared__ float wxs[kAaT * KM], wys[kAaT * KM];
     __shared__ int lcs[kAaT * KM], lrs[kAaT * KM];
     const uint32_t tid = threadIdx.x, tx = tid % kAaT, ty = tid / kAaT;
     const uint32_t bt = blockIdx.x, txi = bt % tiles_x, rr = bt / tiles_x, tyi = rr % tiles_y, img = rr / tiles_y;
@@ -1555,7 +1556,7 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
     const int ny = max(1, min(yhi - ylo, (int)EXT)), nx = max(1, min(xhi - xlo, (int)EXT));
     // the tap weights and window indices of the block's 16 columns (entries 0 .. kAaT KM - 1) and 16 rows (the next
     // kAaT KM): interp_aa.wgsl's per-tap weight, which depends on the output column (row) alone, once per block
-    tab[tid] = unit_f32(tid << 16, 0);
+    tab[tid] = unit_f16(tid << 16, 0);
     for (uint32_t e = tid; e < 2 * kAaT * KM; e += kThreads) {
         const bool rows = e >= kAaT * KM;
         const uint32_t k = rows ? e - kAaT * KM : e;
@@ -1582,11 +1583,11 @@ __global__ __launch_bounds__(kThreads) void rgba_resize_kernel(const uint32_t* s
             const uint32_t v = __builtin_amdgcn_raw_buffer_load_b32(
                 rf, __umul24((uint32_t)min(ylo + row, (int)h - 1), pitch4) + (uint32_t)min(xlo + col, (int)w - 1) * 4u,
                 0, 0);
-            const uint32_t c01 = (uint32_t)f2h(unit_tab(tab, v, 0)) | ((uint32_t)f2h(unit_tab(tab, v, 1)) << 16);
+            const uint32_t c01 = (uint32_t)tab[(v >> 16) & 0xffu] | ((uint32_t)tab[(v >> 8) & 0xffu] << 16);
             if constexpr (SPLIT)
-                tile[row * EXT + col] = c01, tileb[row * EXT + col] = f2h(unit_tab(tab, v, 2));
+                tile[row * EXT + col] = c01, tileb[row * EXT + col] = tab[v & 0xffu];
             else
-                tile[row * EXT + col] = uint2{c01, (uint32_t)f2h(unit_tab(tab, v, 2))};
+                tile[row * EXT + col] = uint2{c01, (uint32_t)tab[v & 0xffu]};
         }
     __syncthreads();
     const uint32_t ox = ox0 + tx, oy = oy0 + ty;
