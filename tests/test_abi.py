@@ -222,6 +222,23 @@ def test_network_ops_reject_bad_views_before_any_launch():
                              ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, None), "render_rgba flow"),
         ("fhc_render_rgba", (0x1000, None, 64, 32, 64, 32, 64, _tv(cs=8), _tv(cs=8, c0=4), _tv(), 8, 16,
                              ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, None), "null frame"),
+        # the batched forms: their pair counts and the repair's workspace for all pairs
+        ("fhc_refine_input_n", (_tv(cs=8), _tv(cs=8), _tv(cs=8), _tv(cs=16), 8, 8, ctypes.c_float(0.05), 4, 0, None),
+         "picture pairs"),
+        ("fhc_refine_input_n", (_tv(cs=8), _tv(cs=8), _tv(cs=8), _tv(cs=16), 8, 8, ctypes.c_float(0.05), 4, 5, None),
+         "picture pairs"),
+        ("fhc_refine_input_n", (_tv(cs=8), _tv(cs=8), _tv(cs=8), _tv(cs=16), 8, 8, ctypes.c_float(0.05), 70000, 1,
+                                None), "launch limit"),
+        ("fhc_gmhs_n", (_tv(), _tv(), 480, 864, _tv(), 60, 108, 1920, 1, 2, 0x1000,
+                        fh.gmhs_params(480, 864, 1920, 1)["ws_bytes"], None), "workspace of"),
+        ("fhc_gmhs_n", (_tv(), _tv(), 480, 864, _tv(), 60, 108, 1920, 1, 70000, 0x1000, 1 << 40, None),
+         "launch limit"),
+        ("fhc_fold_pair_sad_n", (_tv(cs=8), _tv(cs=16), None, 4, 4, 8, 70000, _tv(), _tv(), _tv(cs=32), 1, 4, 4, 2,
+                                 None), "launch limit"),
+        ("fhc_coarse_fine_input_n", (_tv(cs=8), _tv(cs=8), None, 2, 2, ctypes.c_float(16.0), _tv(cs=8), _tv(),
+                                     ctypes.c_float(0.125), _tv(cs=24), _tv(), 4, 4, 4, 70000, None), "launch limit"),
+        ("fhc_pair_input_n", (_tv(), _tv(), _tv(), _tv(cs=8), _tv(), 64, 64, 16, 16, 5_000_000, None),
+         "too many tiles"),
     ]
     for name, args, msg in cases:
         rc = getattr(L, name)(*args)
