@@ -677,8 +677,9 @@ class FlyHighFG:
     pair each, side by side. The pictures of pair p are images 2p (A) and 2p + 1 (B) of the A/B buffers, so each
     pair's A and B are one contiguous batch of 2, as every op chain of one pair takes them; the pair stage's one-image
     tensors hold pair p at image p, and the mid stage's hold phase j of pair p at image j * P + p (each phase's P
-    images contiguous). Every conv runs once per layer over the whole batch (2P, P or M * P images); the op chains
-    of one pair run per pair, those of one phase per phase. P = M = 1 is the reference's single session."""
+    images contiguous). Every conv and every op chain runs once over the whole batch (2P, P or M * P images), but
+    the FiLM head, film.out, flow_t / vis_t and the refine input once per phase (over its P images) and the frame-size
+    render once per generated frame. P = M = 1 is the reference's single session."""
 
     def __init__(self, be, net_w: int = 864, net_h: int = 480, cubic: bool = True, render_flags: int = 0,
                  frame: Optional[tuple] = None, repair: int = 1, pairs: int = 1, mids: int = 1):
