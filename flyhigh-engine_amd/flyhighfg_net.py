@@ -821,17 +821,28 @@ class FlyHighFG:
         self._mid_tail()
 
     def mids(self, ts, W: Optional[dict] = None):
-        """mid(t) for each of the M phases ts of every pair: each phase's FiLM head, flow_t / vis_t and refine input
-        with that phase's FiLM vectors (slot j of the backend's vectors: be.set_g(self.film_vectors(W, t), j), set
-        here when W is given), then the refine head over all M * P images at once and the renders."""
+        """mid(t) for each of the M phases ts of every pair: each phase's FiLM pair with that phase's FiLM vectors
+        (slot j of the backend's vectors: be.set_g(self.film_vectors(W, t), j), set here when W is given), film.out
+        over all M * P images at once, each phase's flow_t / vis_t, the refine input and the refine head over all
+        M * P images at once, then the renders."""
         ts = tuple(ts)
         if len(ts) != self.M:
             raise ValueError(f"{len(ts)} phases for a program of {self.M}")
+        be, P = self.be, self.P
         if W is not None:
             for j, t in enumerate(ts):
-                self.be.set_g(self.film_vectors(W, t), j)
-        for j, t in enumerate(ts):
-            self._mid_phase(j, t, False)
+                be.set_g(self.film_vectors(W, t), j)
+        for j in range(self.M):                                                               # 50-52
+            m = lambda b: sl(b, j * P, P)  # noqa: E731  phase j's images
+            be.use_g(j)
+            be.film_pair("film.h1", "film.h2", V(self.h), 48, V(m(self.hm)), V(m(self.fh1)), V(m(self.fh2)))
+        be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
+        for j, t in enumerate(ts):                                                            # 44-48, 54-62
+            m = lambda b: sl(b, j * P, P)  # noqa: E731
+            be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(m(self.dfilm)), t, V(m(self.up7)), V(m(self.ftvt)),
+                                 V(m(self.lin)), V(m(self.dvis)))
+        be.refine_input_n(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend),
+                          P)                                                                  # 63-76
         self._mid_tail()
 
     def run(self, ts, W: Optional[dict] = None):
