@@ -175,28 +175,37 @@ constexpr uint32_t kCvIn = 4, kCvHalo = kCvIn + 2, kCvThreads = 4 * kCvIn * kCvI
 // FVT: x is mid()'s flow_t | vis_t (7 channels), computed while staging from fv (flow 0-3, vis 4-6) and the FiLM
 // head's output df (d_flow 0-3, d_mask 4) with flow_vis_t_kernel's arithmetic, so that x is never stored: the same
 // f16 values the two launches produce
-__device__ __forceinline__ void flow_vis_t_at(const View& fv, const View& df, size_t pix, float af, float ab,
-                                              uint16_t (&o)[7]) {
+// (fpix: the pixel's index in fv, dpix: in df)
+__device__ __forceinline__ void flow_vis_t_at(const View& fv, const View& df, size_t fpix, size_t dpix, float af,
+                                              float ab, uint16_t (&o)[7]) {
 #pragma unroll
     for (uint32_t i = 0; i < 4; i++) {
-        const float lin = h2f(f2h(ld(fv, pix, i) * fv.scale * (i < 2 ? af : ab)));
-        o[i] = f2h(lin + ld(df, pix, i) * df.scale);
+        const float lin = h2f(f2h(ld(fv, fpix, i) * fv.scale * (i < 2 ? af : ab)));
+        o[i] = f2h(lin + ld(df, dpix, i) * df.scale);
     }
-    const uint16_t dm = df.p[pix * df.cs + df.c0 + 4];
+    const uint16_t dm = df.p[dpix * df.cs + df.c0 + 4];
     const float dv[3] = {h2f(dm), h2f(f2h(h2f(dm) * -1.0f)), 0.0f};
 #pragma unroll
-    for (uint32_t j = 0; j < 3; j++) o[4 + j] = f2h(ld(fv, pix, 4 + j) * fv.scale + dv[j]);
+    for (uint32_t j = 0; j < 3; j++) o[4 + j] = f2h(ld(fv, fpix, 4 + j) * fv.scale + dv[j]);
 }
 
+// FVT with several phases: image i of df and out is phase i / per of pair i % per, whose wt and fv are image i % per
+// and whose mul_t factors are ph.af[i / per], ph.ab[i / per]
+constexpr uint32_t kMaxPhases = 8;
+struct PhaseT {
+    float af[kMaxPhases], ab[kMaxPhases];
+};
 template <bool FVT>
 __global__ __launch_bounds__(kCvThreads) void convex_tile_kernel(View wt, View x, OView out, uint32_t h, uint32_t w,
                                                                uint32_t c, uint32_t tiles_x, uint32_t tiles_y,
-                                                               View fv, View df, float af, float ab) {
+                                                               View fv, View df, PhaseT ph, uint32_t per) {
     extern __shared__ __align__(16) uint16_t lds[];
     uint16_t* lw = lds;                       // [kCvIn * kCvIn][36]
     uint16_t* lx = lds + kCvIn * kCvIn * 36;  // [kCvHalo * kCvHalo][c]
     const uint32_t tid = threadIdx.x, tx = tid % (2 * kCvIn), ty = tid / (2 * kCvIn);
     const uint32_t bt = blockIdx.x, txi = bt % tiles_x, r = bt / tiles_x, tyi = r % tiles_y, img = r / tiles_y;
+    const uint32_t pimg = img % per;  // the image of wt and fv
+    const float af = ph.af[img / per], ab = ph.ab[img / per];
     const int ix0 = (int)(txi * kCvIn), iy0 = (int)(tyi * kCvIn);
     // staging with every load unconditional (clamped to the image / the view) and unrolled, so they issue together
 #pragma unroll
@@ -204,7 +213,7 @@ __global__ __launch_bounds__(kCvThreads) void convex_tile_kernel(View wt, View x
         const uint32_t e = min(tid + k * kCvThreads, kCvIn * kCvIn * 9 - 1);
         const uint32_t p = e / 9, q = e - p * 9, py = p / kCvIn, px = p % kCvIn;
         const int gy = min(iy0 + (int)py, (int)h - 1), gx = min(ix0 + (int)px, (int)w - 1);
-        const uint16_t* src = wt.p + (((size_t)img * h + gy) * w + gx) * wt.cs + wt.c0 + q * 4;
+        const uint16_t* src = wt.p + (((size_t)pimg * h + gy) * w + gx) * wt.cs + wt.c0 + q * 4;
         // lanes past the last quad rewrite that quad with its own value (a conditional store would pull the load
         // into the branch and serialise the loads again)
 #pragma unroll
@@ -215,8 +224,8 @@ __global__ __launch_bounds__(kCvThreads) void convex_tile_kernel(View wt, View x
         const int gy = iy0 - 1 + (int)py, gx = ix0 - 1 + (int)px;
         const bool in = gy >= 0 && gy < (int)h && gx >= 0 && gx < (int)w;
         uint16_t v[7];
-        flow_vis_t_at(fv, df, ((size_t)img * h + clampi(gy, 0, (int)h - 1)) * w + clampi(gx, 0, (int)w - 1), af, ab,
-                      v);
+        const size_t pix = (size_t)clampi(gy, 0, (int)h - 1) * w + clampi(gx, 0, (int)w - 1);
+        flow_vis_t_at(fv, df, (size_t)pimg * h * w + pix, (size_t)img * h * w + pix, af, ab, v);
 #pragma unroll
         for (uint32_t cc = 0; cc < 7; cc++) lx[tid * 7 + cc] = in ? v[cc] : (uint16_t)0;
     } else if (!FVT && tid < kCvHalo * kCvHalo) {  // one lane per halo pixel, channels 8 at a time
@@ -2032,7 +2041,7 @@ extern "C" int fhc_convex_upsample(const fhc_tensor* wt, const fhc_tensor* x, co
         const size_t lds = (kCvIn * kCvIn * 36 + kCvHalo * kCvHalo * c) * 2;
         const View none{nullptr, 0, 0, 1.0f};
         hipLaunchKernelGGL(convex_tile_kernel<false>, dim3(n * tx * ty), dim3(kCvThreads), lds, (hipStream_t)stream,
-                           in(wt), in(x), outv(out), h, w, c, tx, ty, none, none, 0.0f, 0.0f);
+                           in(wt), in(x), outv(out), h, w, c, tx, ty, none, none, PhaseT{}, n);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "convex_upsample: launch failed: %s", hipGetErrorString(e));
     });
@@ -2667,20 +2676,30 @@ extern "C" int fhc_coarse_fine_input_n(const fhc_tensor* o, const fhc_tensor* fv
 
 extern "C" int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, float t,
                                      const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, void* stream) {
+    return fhc_flow_vis_t_convex_n(wt, fv, dfilm, &t, 1, out, n, h, w, stream);
+}
+
+extern "C" int fhc_flow_vis_t_convex_n(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm,
+                                       const float* ts, uint32_t phases, const fhc_tensor* out, uint32_t n, uint32_t h,
+                                       uint32_t w, void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
-        if ((uint64_t)n * h * w == 0) return 0;
+        if ((uint64_t)n * h * w * phases == 0) return 0;
+        if (!ts) return fail(-1, "flow_vis_t_convex: null phases");
+        if (phases > kMaxPhases) return fail(-1, "flow_vis_t_convex: %u phases (at most %u)", phases, kMaxPhases);
+        PhaseT ph{};
+        for (uint32_t j = 0; j < phases; j++)  // the mul_t factors (net/build.rs:293)
+            ph.af[j] = 2.0f * ts[j], ph.ab[j] = 2.0f * (1.0f - ts[j]);
         FHC_TRY(check(wt, "flow_vis_t_convex wt", 36, false));
         FHC_TRY(check(fv, "flow_vis_t_convex fv", 7, true));
         FHC_TRY(check(dfilm, "flow_vis_t_convex dfilm", 5, true));
         FHC_TRY(check(out, "flow_vis_t_convex out", 7, false, true));
         const uint32_t tx = (w + kCvIn - 1) / kCvIn, ty = (h + kCvIn - 1) / kCvIn;
-        if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "flow_vis_t_convex: too many tiles");
+        if ((uint64_t)phases * n * tx * ty >= kMaxItems) return fail(-1, "flow_vis_t_convex: too many tiles");
         const size_t lds = (kCvIn * kCvIn * 36 + kCvHalo * kCvHalo * 7) * 2;
-        const float af = 2.0f * t, ab = 2.0f * (1.0f - t);  // the mul_t factors (net/build.rs:293)
         const View none{nullptr, 0, 0, 1.0f};
-        hipLaunchKernelGGL(convex_tile_kernel<true>, dim3(n * tx * ty), dim3(kCvThreads), lds, (hipStream_t)stream,
-                           in(wt), none, outv(out), h, w, 7u, tx, ty, in(fv), in(dfilm), af, ab);
+        hipLaunchKernelGGL(convex_tile_kernel<true>, dim3(phases * n * tx * ty), dim3(kCvThreads), lds,
+                           (hipStream_t)stream, in(wt), none, outv(out), h, w, 7u, tx, ty, in(fv), in(dfilm), ph, n);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "flow_vis_t_convex: launch failed: %s", hipGetErrorString(e));
     });

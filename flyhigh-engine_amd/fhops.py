@@ -94,6 +94,7 @@ def _lib():
             "fhc_render_rgba": [P, P, U, U, U, U, U, T, T, T, U, U, ctypes.c_float, ctypes.c_float, I, U, P, U,
                                 P],
             "fhc_gmhs_params": [U, U, U, U, ctypes.POINTER(GmhsPar)],
+            "fhc_flow_vis_t_convex_n": [T, T, T, P, U, T, U, U, U, P],
             "fhc_gmhs": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P],
             "fhc_gmhs_n": [T, T, U, U, T, U, U, U, U, U, P, ctypes.c_size_t, P],
             "fhc_gmhs_film": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P, P, P, P, P, P, P, P],
@@ -273,11 +274,14 @@ def coarse_fine_input(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c, s
 
 
 def flow_vis_t_convex(wt, fv, dfilm, t, out, stream=None):
-    """flow_vis_t(fv, dfilm, ., t) then convex(wt, ., 7, out), the intermediate never stored: one launch."""
+    """flow_vis_t(fv, dfilm, ., t) then convex(wt, ., 7, out), the intermediate never stored: one launch. t: one
+    phase, or a sequence of phases (dfilm and out then hold phase j of pair p at image j * n + p, n = fv's images)."""
     fv = _v(fv)
     n, h, w, _ = fv.shape
-    _run("flow_vis_t_convex", _lib().fhc_flow_vis_t_convex(_ref(_v(wt)), _ref(fv), _ref(_v(dfilm)), t, _ref(_v(out)),
-                                                           n, h, w, _stream_handle(stream)))
+    ts = [float(t)] if isinstance(t, (int, float)) else [float(x) for x in t]
+    arr = (ctypes.c_float * len(ts))(*ts)
+    _run("flow_vis_t_convex", _lib().fhc_flow_vis_t_convex_n(_ref(_v(wt)), _ref(fv), _ref(_v(dfilm)), arr, len(ts),
+                                                             _ref(_v(out)), n, h, w, _stream_handle(stream)))
 
 
 def refine_input(q, flow, vis, rx, flow_out_scale, qmod=None, stream=None):

@@ -191,6 +191,14 @@ class ComposedChains:
         self.flow_vis_t(fv, dfilm, ftvt, t, lin, dvis)
         self.convex(wt, ftvt, 7, out)
 
+    def flow_vis_t_convex_n(self, wt: V, fv: V, dfilm: V, ts, out: V, ftvt: V, lin: V, dvis: V):
+        """flow_vis_t_convex for each phase j of ts over fv's P pairs: dfilm, out and the intermediates hold phase j
+        of pair p at image j * P + p."""
+        P = fv.buf.shape[0]
+        for j, t in enumerate(ts):
+            m = lambda x, i=j: V(sl(x.buf, i * P, P), x.c0, x.scale)  # noqa: E731
+            self.flow_vis_t_convex(wt, fv, m(dfilm), t, m(out), m(ftvt), m(lin), m(dvis))
+
     def flow_vis_t(self, fv: V, dfilm: V, out: V, t: float, lin: V, dvis: V):
         self.unary(V(fv.buf, fv.c0), 2, V(lin.buf, lin.c0), 0, 2.0 * t)
         self.unary(V(fv.buf, fv.c0 + 2), 2, V(lin.buf, lin.c0 + 2), 0, 2.0 * (1.0 - t))
@@ -645,6 +653,15 @@ class GpuBackend(ComposedChains):
                  lambda: self.fh.flow_vis_t_convex(vw, vfv, vd, t, vo, stream=self.stream),
                  2 * (36 + 7 + 5 + 4 * 7) * px)
 
+    def flow_vis_t_convex_n(self, wt: V, fv: V, dfilm: V, ts, out: V, ftvt: V, lin: V, dvis: V):
+        if not self.chains:
+            return super().flow_vis_t_convex_n(wt, fv, dfilm, ts, out, ftvt, lin, dvis)
+        vw, vfv, vd, vo = (self._v(x) for x in (wt, fv, dfilm, out))
+        ts = tuple(float(t) for t in ts)
+        self._go("flow_vis_t_convex (flow_vis_t + convex_upsample)",
+                 lambda: self.fh.flow_vis_t_convex(vw, vfv, vd, ts, vo, stream=self.stream),
+                 2 * (36 + 7 + 5 + 4 * 7) * self._px(fv) * len(ts))
+
     def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
         if not self.chains:
             return super().refine_input(q, flow, vis, rx, flow_out_scale, blend)
@@ -678,8 +695,7 @@ class FlyHighFG:
     pair's A and B are one contiguous batch of 2, as every op chain of one pair takes them; the pair stage's one-image
     tensors hold pair p at image p, and the mid stage's hold phase j of pair p at image j * P + p (each phase's P
     images contiguous). Every conv and every op chain runs once over the whole batch (2P, P or M * P images), but
-    the FiLM head, film.out, flow_t / vis_t and the refine input once per phase (over its P images) and the frame-size
-    render once per generated frame. P = M = 1 is the reference's single session."""
+    the FiLM pair once per phase (over its P images) and the frame-size render once per generated frame. P = M = 1 is the reference's single session."""
 
     def __init__(self, be, net_w: int = 864, net_h: int = 480, cubic: bool = True, render_flags: int = 0,
                  frame: Optional[tuple] = None, repair: int = 1, pairs: int = 1, mids: int = 1):
@@ -822,9 +838,9 @@ class FlyHighFG:
 
     def mids(self, ts, W: Optional[dict] = None):
         """mid(t) for each of the M phases ts of every pair: each phase's FiLM pair with that phase's FiLM vectors
-        (slot j of the backend's vectors: be.set_g(self.film_vectors(W, t), j), set here when W is given), film.out
-        over all M * P images at once, each phase's flow_t / vis_t, the refine input and the refine head over all
-        M * P images at once, then the renders."""
+        (slot j of the backend's vectors: be.set_g(self.film_vectors(W, t), j), set here when W is given), then
+        film.out, flow_t / vis_t with the convex upsample (each phase its t), the refine input and the refine head
+        over all M * P images at once, then the renders."""
         ts = tuple(ts)
         if len(ts) != self.M:
             raise ValueError(f"{len(ts)} phases for a program of {self.M}")
@@ -837,10 +853,8 @@ class FlyHighFG:
             be.use_g(j)
             be.film_pair("film.h1", "film.h2", V(self.h), 48, V(m(self.hm)), V(m(self.fh1)), V(m(self.fh2)))
         be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
-        for j, t in enumerate(ts):                                                            # 44-48, 54-62
-            m = lambda b: sl(b, j * P, P)  # noqa: E731
-            be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(m(self.dfilm)), t, V(m(self.up7)), V(m(self.ftvt)),
-                                 V(m(self.lin)), V(m(self.dvis)))
+        be.flow_vis_t_convex_n(V(self.wt36), V(self.fv), V(self.dfilm), ts, V(self.up7), V(self.ftvt), V(self.lin),
+                               V(self.dvis))                                                  # 44-48, 54-62
         be.refine_input_n(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend),
                           P)                                                                  # 63-76
         self._mid_tail()

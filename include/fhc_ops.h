@@ -236,6 +236,12 @@ int fhc_coarse_fine_input_n(const fhc_tensor* o, const fhc_tensor* fv, const fhc
 int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, float t,
                           const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, void* stream);
 
+/* fhc_flow_vis_t_convex for `phases` phases ts[0 .. phases - 1] (at most 8) of n pairs in one launch: image j * n + p
+ * of dfilm and out is phase j of pair p, whose wt and fv are image p. Bit-identical to one call per phase. The
+ * reference runs one phase a mid(t) (model/graph.rs:182); this is the batched program's form. */
+int fhc_flow_vis_t_convex_n(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, const float* ts,
+                            uint32_t phases, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, void* stream);
+
 /* fhc_fold_pair and fhc_sad_volume in one launch, for a sad_volume that reads nothing the fold writes and writes
  * nothing it reads (pair(): the second encoder pair's fold, op 26 and 43's f16b, beside the 1/16 lumas' cost volume,
  * ops 25-26, ready since the pyramid). The fold's arguments as fhc_fold_pair's (h x w, c channels); the cost

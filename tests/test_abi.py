@@ -239,6 +239,10 @@ def test_network_ops_reject_bad_views_before_any_launch():
                                      ctypes.c_float(0.125), _tv(cs=24), _tv(), 4, 4, 4, 70000, None), "launch limit"),
         ("fhc_pair_input_n", (_tv(), _tv(), _tv(), _tv(cs=8), _tv(), 64, 64, 16, 16, 5_000_000, None),
          "too many tiles"),
+        ("fhc_flow_vis_t_convex_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 9)(*[0.5] * 9), 9,
+                                     _tv(cs=8), 1, 4, 4, None), "phases"),
+        ("fhc_flow_vis_t_convex_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), None, 2, _tv(cs=8), 1, 4, 4, None),
+         "null phases"),
     ]
     for name, args, msg in cases:
         rc = getattr(L, name)(*args)

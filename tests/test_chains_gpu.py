@@ -123,6 +123,32 @@ def test_flow_vis_t_convex_equals_flow_vis_t_then_convex(n, h, w, t):
     same(outs[0], outs[1], "out")
 
 
+@pytest.mark.parametrize("P,ts,h,w", [(2, (0.25, 0.5, 0.75), 9, 13), (3, (0.3, 1.0), 60, 108)])
+def test_flow_vis_t_convex_phases_in_one_launch(P, ts, h, w):
+    """Every phase of ts in one launch (phase j of pair p at image j * P + p, each phase its own mul_t factors)
+    against one fused launch per phase and against the ops one by one."""
+    say("flow_vis_t_convex phases", P, ts, h, w)
+    outs = []
+    fused, composed = backends()
+    M = len(ts)
+    for be, batched in ((fused, True), (composed, True), (fused, False)):
+        rng = np.random.default_rng(P * 10 + h)
+        wt = fill(be, rng, P, h, w, 40, -4.0, 4.0)
+        fv = fill(be, rng, P, h, w, 8, -2.0, 2.0)
+        df = fill(be, rng, M * P, h, w, 8)
+        scratch = [be.zeros(M * P, h, w, 8) for _ in range(3)]
+        out = fill(be, rng, M * P, 2 * h, 2 * w, 8)
+        if batched:
+            be.flow_vis_t_convex_n(V(wt, 2), V(fv), V(df, 1), ts, V(out), *(V(x) for x in scratch))
+        else:
+            for j, t in enumerate(ts):
+                m = lambda x: net.sl(x, j * P, P)  # noqa: E731
+                be.flow_vis_t_convex(V(wt, 2), V(fv), V(m(df), 1), t, V(m(out)), *(V(m(x)) for x in scratch))
+        outs.append(be.host(out).copy())
+    same(outs[0], outs[1], "out (one launch vs op by op)")
+    same(outs[0], outs[2], "out (one launch vs one per phase)")
+
+
 @pytest.mark.parametrize("H,W,oh,ow", [(100, 150, 24, 36), (200, 328, 48, 80), (64, 64, 16, 16)])
 def test_pair_input_equals_resize_then_pyramid(H, W, oh, ow):
     say("pair_input", H, W, oh, ow)
