@@ -189,6 +189,24 @@ __device__ __forceinline__ void flow_vis_t_at(const View& fv, const View& df, si
     for (uint32_t j = 0; j < 3; j++) o[4 + j] = f2h(ld(fv, fpix, 4 + j) * fv.scale + dv[j]);
 }
 
+// the softmax of an output pixel's 9 mask weights pw[4 k] (k: its 3 x 3 neighbourhood, row-major)
+__device__ __forceinline__ void convex_weights(const uint16_t* pw, float (&ws)[9]) {
+    float m = -3.0e38f;
+#pragma unroll
+    for (uint32_t k = 0; k < 9; k++) {
+        ws[k] = h2f(pw[k * 4]);
+        m = fmaxf(m, ws[k]);
+    }
+    float denom = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < 9; k++) {
+        ws[k] = expf(ws[k] - m);
+        denom = denom + ws[k];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < 9; k++) ws[k] = ws[k] / denom;
+}
+
 // FVT with several phases: image i of df and out is phase i / per of pair i % per, whose wt and fv are image i % per
 // and whose mul_t factors are ph.af[i / per], ph.ab[i / per]
 constexpr uint32_t kMaxPhases = 8;
@@ -248,21 +266,8 @@ __global__ __launch_bounds__(kCvThreads) void convex_tile_kernel(View wt, View x
     const uint32_t ox = txi * 2 * kCvIn + tx, oy = tyi * 2 * kCvIn + ty;
     if (ox >= 2 * w || oy >= 2 * h) return;
     const uint32_t lix = tx / 2, liy = ty / 2, sub = (ty % 2) * 2 + tx % 2;
-    const uint16_t* pw = lw + (liy * kCvIn + lix) * 36 + sub;
-    float m = -3.0e38f, ws[9];
-#pragma unroll
-    for (uint32_t k = 0; k < 9; k++) {
-        ws[k] = h2f(pw[k * 4]);
-        m = fmaxf(m, ws[k]);
-    }
-    float denom = 0.0f;
-#pragma unroll
-    for (uint32_t k = 0; k < 9; k++) {
-        ws[k] = expf(ws[k] - m);
-        denom = denom + ws[k];
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < 9; k++) ws[k] = ws[k] / denom;
+    float ws[9];
+    convex_weights(lw + (liy * kCvIn + lix) * 36 + sub, ws);
     const size_t opix = ((size_t)img * 2 * h + oy) * 2 * w + ox;
     for (uint32_t co = 0; co < c; co++) {
         float acc = 0.0f;
@@ -292,11 +297,13 @@ __global__ __launch_bounds__(kThreads) void film_kernel(View hv, const uint16_t*
 }
 
 // ---- blend_weights and blendmix: shaders/blend.wgsl:11-20, blendmix.wgsl:14-27 ------------------------------------
-__device__ __forceinline__ void soft3(const View& vis, size_t pix, float& ea, float& eb, float& ec, float& s) {
-    const float a = ld(vis, pix, 0) * vis.scale, b = ld(vis, pix, 1) * vis.scale, c = ld(vis, pix, 2) * vis.scale;
+__device__ __forceinline__ void soft3v(float a, float b, float c, float& ea, float& eb, float& ec, float& s) {
     const float m = fmaxf(a, fmaxf(b, c));
     ea = expf(a - m), eb = expf(b - m), ec = expf(c - m);
     s = ea + eb + ec;
+}
+__device__ __forceinline__ void soft3(const View& vis, size_t pix, float& ea, float& eb, float& ec, float& s) {
+    soft3v(ld(vis, pix, 0) * vis.scale, ld(vis, pix, 1) * vis.scale, ld(vis, pix, 2) * vis.scale, ea, eb, ec, s);
 }
 __global__ __launch_bounds__(kThreads) void blend_kernel(View vis, OView out, uint32_t items) {
     const uint32_t pix = blockIdx.x * kThreads + threadIdx.x;
@@ -831,14 +838,15 @@ __global__ __launch_bounds__(kThreads) void flow_vis_t_kernel(View fv, View df, 
 // (blendmix), and the blend's luma gradient, written as the concat rx: c0 rwa, +3 rwb, +6 vis_tq, +9 flow_tq * fs,
 // +13 the gradient. The gradient reads the blend at the right and lower neighbours: a lane recomputes those blends
 // (from the same warps and weights, so the same values) instead of a second launch.
-__device__ __forceinline__ void blend_at(const View& q, const View& fl, const View& vis, uint32_t x, uint32_t y,
-                                         uint32_t h, uint32_t w, float (&ra)[3], float (&rb)[3], float (&bl)[3]) {
-    const size_t pix = (size_t)y * w + x;
+// f: the flow at pixel (x, y) (A's x, y, then B's), v: its visibility logits, both at their read scales
+__device__ __forceinline__ void blend_vals(const View& q, uint32_t x, uint32_t y, uint32_t h, uint32_t w,
+                                           const float (&f)[4], const float (&v)[3], float (&ra)[3], float (&rb)[3],
+                                           float (&bl)[3]) {
     float oa[4], ob[4];
-    warp4<false>(q, 0, x, y, h, w, ld(fl, pix, 0) * fl.scale, ld(fl, pix, 1) * fl.scale, 0, 3, oa);
-    warp4<false>(q, h, x, y, h, w, ld(fl, pix, 2) * fl.scale, ld(fl, pix, 3) * fl.scale, 0, 3, ob);
+    warp4<false>(q, 0, x, y, h, w, f[0], f[1], 0, 3, oa);
+    warp4<false>(q, h, x, y, h, w, f[2], f[3], 0, 3, ob);
     float ea, eb, ec, s;
-    soft3(vis, pix, ea, eb, ec, s);
+    soft3v(v[0], v[1], v[2], ea, eb, ec, s);
     const float pa = h2f(f2h((ea + 0.5f * ec) / s)), pb = h2f(f2h((eb + 0.5f * ec) / s));
 #pragma unroll
     for (uint32_t ch = 0; ch < 3; ch++) {
@@ -846,6 +854,14 @@ __device__ __forceinline__ void blend_at(const View& q, const View& fl, const Vi
         rb[ch] = h2f(f2h(ob[ch]));
         bl[ch] = h2f(f2h(h2f(f2h(ra[ch] * pa)) + h2f(f2h(rb[ch] * pb))));
     }
+}
+__device__ __forceinline__ void blend_at(const View& q, const View& fl, const View& vis, uint32_t x, uint32_t y,
+                                         uint32_t h, uint32_t w, float (&ra)[3], float (&rb)[3], float (&bl)[3]) {
+    const size_t pix = (size_t)y * w + x;
+    const float f[4] = {ld(fl, pix, 0) * fl.scale, ld(fl, pix, 1) * fl.scale, ld(fl, pix, 2) * fl.scale,
+                        ld(fl, pix, 3) * fl.scale};
+    const float v[3] = {ld(vis, pix, 0) * vis.scale, ld(vis, pix, 1) * vis.scale, ld(vis, pix, 2) * vis.scale};
+    blend_vals(q, x, y, h, w, f, v, ra, rb, bl);
 }
 
 // One wave per 7 x 7 output pixels: each lane computes the blend of one pixel of the 8 x 8 block around them (the
@@ -887,6 +903,97 @@ __global__ __launch_bounds__(64) void refine_input_kernel(View q, View fl, View 
     const float cl = lum3(bl[0], bl[1], bl[2]);
     const float gx = x + 1 < w ? lum3(br[0], br[1], br[2]) - cl : 0.0f;
     const float gy = y + 1 < h ? lum3(bd[0], bd[1], bd[2]) - cl : 0.0f;
+    o[13] = f2h(fabsf(gx) + fabsf(gy));
+}
+
+// ---- mid()'s upsampled flow and the refine head's input in one launch -------------------------------------------
+// flow_t / vis_t and the convex upsample (convex_tile_kernel<true>'s arithmetic) computed at every pixel of the
+// refine input's 8 x 8 blend block (a 7 x 7 output tile and its right and lower neighbours, clamped to the picture),
+// so that refine_input_kernel's warps and blend take the upsampled flow and visibility from the lane's registers as
+// they would read them back (rounded to f16): the lanes of the 7 x 7 outputs also store them (the render reads them).
+// An 8-pixel span covers at most kMiC input cells; they and their ring of neighbours make the flow_t | vis_t halo.
+constexpr uint32_t kMiC = 5, kMiHalo = kMiC + 2;
+// h x w: the input grid (the output 2h x 2w). blockIdx.y: image i, phase i / per of pair i % per: image i of df, up
+// and rx, image i % per of wt and fv, pair i % per of q. fls: the scale the refine input reads the flow at (the
+// visibility: 1); fs: flow_out_scale.
+__global__ __launch_bounds__(64) void mid_input_kernel(View wt, View fv, View df, PhaseT ph, uint32_t per, View q,
+                                                       OView up, OView rx, uint32_t h, uint32_t w, float fls, float fs,
+                                                       uint32_t tiles_x) {
+    __shared__ uint16_t lw[kMiC * kMiC * 36];
+    __shared__ uint16_t lx[kMiHalo * kMiHalo * 7];
+    __shared__ float bt[8 * 8 * 3];
+    const uint32_t img = blockIdx.y, pimg = img % per;
+    const float af = ph.af[img / per], ab = ph.ab[img / per];
+    const uint32_t oh = 2 * h, ow = 2 * w;
+    q.p += (size_t)pimg * 2 * oh * ow * q.cs;
+    const uint32_t tid = threadIdx.x, tx = tid % 8, ty = tid / 8;
+    const uint32_t x0 = (blockIdx.x % tiles_x) * kRiT, y0 = (blockIdx.x / tiles_x) * kRiT;
+    const uint32_t x = min(x0 + tx, ow - 1), y = min(y0 + ty, oh - 1);
+    const int cx0 = (int)(x0 / 2), cy0 = (int)(y0 / 2);
+    // the cells' mask weights (9 quads of 4 channels a cell), coordinates clamped to the grid; every load
+    // unconditional, lanes past the last quad rewriting it
+#pragma unroll
+    for (uint32_t k = 0; k < (kMiC * kMiC * 9 + 63) / 64; k++) {
+        const uint32_t e = min(tid + k * 64, kMiC * kMiC * 9 - 1);
+        const uint32_t p = e / 9, qd = e - p * 9, py = p / kMiC, px = p % kMiC;
+        const int gy = min(cy0 + (int)py, (int)h - 1), gx = min(cx0 + (int)px, (int)w - 1);
+        const uint16_t* src = wt.p + (((size_t)pimg * h + gy) * w + gx) * wt.cs + wt.c0 + qd * 4;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) lw[p * 36 + qd * 4 + i] = src[i];
+    }
+    if (tid < kMiHalo * kMiHalo) {  // one lane per halo cell: flow_t | vis_t, zero outside the grid
+        const uint32_t py = tid / kMiHalo, px = tid % kMiHalo;
+        const int gy = cy0 - 1 + (int)py, gx = cx0 - 1 + (int)px;
+        const bool in = gy >= 0 && gy < (int)h && gx >= 0 && gx < (int)w;
+        uint16_t v[7];
+        const size_t pix = (size_t)clampi(gy, 0, (int)h - 1) * w + clampi(gx, 0, (int)w - 1);
+        flow_vis_t_at(fv, df, (size_t)pimg * h * w + pix, (size_t)img * h * w + pix, af, ab, v);
+#pragma unroll
+        for (uint32_t cc = 0; cc < 7; cc++) lx[tid * 7 + cc] = in ? v[cc] : (uint16_t)0;
+    }
+    __syncthreads();
+    // the lane's pixel: cell (lcx, lcy) of the staged ones, sub-pixel sub
+    const uint32_t lcx = x / 2 - (uint32_t)cx0, lcy = y / 2 - (uint32_t)cy0, sub = (y % 2) * 2 + x % 2;
+    float ws[9];
+    convex_weights(lw + (lcy * kMiC + lcx) * 36 + sub, ws);
+    uint16_t u[7];
+#pragma unroll
+    for (uint32_t co = 0; co < 7; co++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < 9; k++) acc = acc + ws[k] * h2f(lx[((lcy + k / 3) * kMiHalo + lcx + k % 3) * 7 + co]);
+        u[co] = f2h(acc);
+    }
+    const bool own = tx < kRiT && ty < kRiT && x0 + tx < ow && y0 + ty < oh;
+    const size_t pix = ((size_t)img * oh + y) * ow + x;
+    if (own) {
+        uint16_t* o = up.p + pix * up.cs + up.c0;
+#pragma unroll
+        for (uint32_t co = 0; co < 7; co++) o[co] = u[co];
+    }
+    // refine_input_kernel from here, on these values
+    const float f[4] = {h2f(u[0]) * fls, h2f(u[1]) * fls, h2f(u[2]) * fls, h2f(u[3]) * fls};
+    const float v[3] = {h2f(u[4]), h2f(u[5]), h2f(u[6])};
+    float ra[3], rb[3], bl[3];
+    blend_vals(q, x, y, oh, ow, f, v, ra, rb, bl);
+#pragma unroll
+    for (uint32_t ch = 0; ch < 3; ch++) bt[(ty * 8 + tx) * 3 + ch] = bl[ch];
+    __syncthreads();
+    if (!own) return;
+    const float* br = bt + (ty * 8 + tx + 1) * 3;
+    const float* bd = bt + ((ty + 1) * 8 + tx) * 3;
+    uint16_t* o = rx.p + pix * rx.cs + rx.c0;
+#pragma unroll
+    for (uint32_t ch = 0; ch < 3; ch++) {
+        o[ch] = f2h(ra[ch]);
+        o[3 + ch] = f2h(rb[ch]);
+        o[6 + ch] = u[4 + ch];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) o[9 + i] = f2h(h2f(u[i]) * fs);
+    const float cl = lum3(bl[0], bl[1], bl[2]);
+    const float gx = x + 1 < ow ? lum3(br[0], br[1], br[2]) - cl : 0.0f;
+    const float gy = y + 1 < oh ? lum3(bd[0], bd[1], bd[2]) - cl : 0.0f;
     o[13] = f2h(fabsf(gx) + fabsf(gy));
 }
 
@@ -2702,6 +2809,35 @@ extern "C" int fhc_flow_vis_t_convex_n(const fhc_tensor* wt, const fhc_tensor* f
                            (hipStream_t)stream, in(wt), none, outv(out), h, w, 7u, tx, ty, in(fv), in(dfilm), ph, n);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "flow_vis_t_convex: launch failed: %s", hipGetErrorString(e));
+    });
+}
+
+extern "C" int fhc_mid_input_n(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, const float* ts,
+                               uint32_t phases, const fhc_tensor* up, const fhc_tensor* q, const fhc_tensor* rx,
+                               uint32_t n, uint32_t h, uint32_t w, float flow_scale, float flow_out_scale,
+                               void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)n * h * w * phases == 0) return 0;
+        if (!ts) return fail(-1, "mid_input: null phases");
+        if (phases > kMaxPhases) return fail(-1, "mid_input: %u phases (at most %u)", phases, kMaxPhases);
+        if ((uint64_t)phases * n > 65535) return fail(-1, "mid_input: %u images exceed the launch limit", phases * n);
+        if (!std::isfinite(flow_scale)) return fail(-1, "mid_input: the flow's read scale is not finite");
+        PhaseT ph{};
+        for (uint32_t j = 0; j < phases; j++)  // the mul_t factors (net/build.rs:293)
+            ph.af[j] = 2.0f * ts[j], ph.ab[j] = 2.0f * (1.0f - ts[j]);
+        FHC_TRY(check(wt, "mid_input wt", 36, false));
+        FHC_TRY(check(fv, "mid_input fv", 7, true));
+        FHC_TRY(check(dfilm, "mid_input dfilm", 5, true));
+        FHC_TRY(check(up, "mid_input up", 7, false, true));
+        FHC_TRY(check(q, "mid_input q", 3, true));
+        FHC_TRY(check(rx, "mid_input rx", 14, false, true));
+        const uint32_t tx = (2 * w + kRiT - 1) / kRiT, ty = (2 * h + kRiT - 1) / kRiT;
+        if ((uint64_t)tx * ty >= kMaxItems / 64) return fail(-1, "mid_input: %u x %u is too large", w, h);
+        hipLaunchKernelGGL(mid_input_kernel, dim3(tx * ty, phases * n), dim3(64), 0, (hipStream_t)stream, in(wt),
+                           in(fv), in(dfilm), ph, n, in(q), outv(up), outv(rx), h, w, flow_scale, flow_out_scale, tx);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "mid_input: launch failed: %s", hipGetErrorString(e));
     });
 }
 

@@ -95,6 +95,7 @@ def _lib():
                                 P],
             "fhc_gmhs_params": [U, U, U, U, ctypes.POINTER(GmhsPar)],
             "fhc_flow_vis_t_convex_n": [T, T, T, P, U, T, U, U, U, P],
+            "fhc_mid_input_n": [T, T, T, P, U, T, T, T, U, U, U, ctypes.c_float, ctypes.c_float, P],
             "fhc_gmhs": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P],
             "fhc_gmhs_n": [T, T, U, U, T, U, U, U, U, U, P, ctypes.c_size_t, P],
             "fhc_gmhs_film": [T, T, U, U, T, U, U, U, U, P, ctypes.c_size_t, P, P, P, P, P, P, P, P],
@@ -282,6 +283,19 @@ def flow_vis_t_convex(wt, fv, dfilm, t, out, stream=None):
     arr = (ctypes.c_float * len(ts))(*ts)
     _run("flow_vis_t_convex", _lib().fhc_flow_vis_t_convex_n(_ref(_v(wt)), _ref(fv), _ref(_v(dfilm)), arr, len(ts),
                                                              _ref(_v(out)), n, h, w, _stream_handle(stream)))
+
+
+def mid_input(wt, fv, dfilm, t, up, q, rx, flow_scale, flow_out_scale, stream=None):
+    """flow_vis_t_convex(wt, fv, dfilm, t, up) then refine_input(q, (up, flow_scale), (up + 4), rx, flow_out_scale,
+    qmod=n) in one launch (n = fv's images; t one phase or a sequence, up and rx holding phase j of pair p at image
+    j * n + p)."""
+    fv = _v(fv)
+    n, h, w, _ = fv.shape
+    ts = [float(t)] if isinstance(t, (int, float)) else [float(x) for x in t]
+    arr = (ctypes.c_float * len(ts))(*ts)
+    _run("mid_input", _lib().fhc_mid_input_n(_ref(_v(wt)), _ref(fv), _ref(_v(dfilm)), arr, len(ts), _ref(_v(up)),
+                                             _ref(_v(q)), _ref(_v(rx)), n, h, w, flow_scale, flow_out_scale,
+                                             _stream_handle(stream)))
 
 
 def refine_input(q, flow, vis, rx, flow_out_scale, qmod=None, stream=None):

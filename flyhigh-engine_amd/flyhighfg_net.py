@@ -229,6 +229,15 @@ class ComposedChains:
             self.refine_input(V(sl(q.buf, 2 * (k % qmod), 2), q.c0, q.scale), v(flow), v(vis), v(rx), flow_out_scale,
                               v(blend))
 
+    def mid_input_n(self, wt: V, fv: V, dfilm: V, ts, up: V, ftvt: V, lin: V, dvis: V, q: V, rx: V,
+                    flow_scale: float, flow_out_scale: float, blend: V):
+        """flow_vis_t_convex_n into up, then refine_input_n on up (its flow read at flow_scale, its visibility
+        unscaled) into rx, image j * P + p taking pair p's pictures from q (on the GPU one launch, which stores
+        neither the convex upsample's input nor the blend)."""
+        self.flow_vis_t_convex_n(wt, fv, dfilm, ts, up, ftvt, lin, dvis)
+        self.refine_input_n(q, V(up.buf, up.c0, flow_scale), V(up.buf, up.c0 + 4), rx, flow_out_scale, blend,
+                            fv.buf.shape[0])
+
     def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
         for i in range(2):
             self.warp(V(self.image(q.buf, i), q.c0), 3, V(flow.buf, flow.c0 + 2 * i, flow.scale),
@@ -662,6 +671,20 @@ class GpuBackend(ComposedChains):
                  lambda: self.fh.flow_vis_t_convex(vw, vfv, vd, ts, vo, stream=self.stream),
                  2 * (36 + 7 + 5 + 4 * 7) * self._px(fv) * len(ts))
 
+    def mid_input_n(self, wt: V, fv: V, dfilm: V, ts, up: V, ftvt: V, lin: V, dvis: V, q: V, rx: V,
+                    flow_scale: float, flow_out_scale: float, blend: V):
+        if not self.chains:
+            return super().mid_input_n(wt, fv, dfilm, ts, up, ftvt, lin, dvis, q, rx, flow_scale, flow_out_scale,
+                                       blend)
+        vw, vfv, vd, vu, vq, vr = (self._v(x) for x in (wt, fv, dfilm, up, q, rx))
+        ts = tuple(float(t) for t in ts)
+        # the convex upsample's reads (wt, fv at the input grid, dfilm every phase) and up written; the refine
+        # input's two warps of the pictures and rx written
+        self._go("mid_input (flow_vis_t + convex_upsample + refine_input)",
+                 lambda: self.fh.mid_input(vw, vfv, vd, ts, vu, vq, vr, flow_scale, flow_out_scale,
+                                           stream=self.stream),
+                 2 * (36 + 7) * self._px(fv) + 2 * 5 * self._px(dfilm) + 2 * self._px(up) * (7 + 6 + 14))
+
     def refine_input(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V):
         if not self.chains:
             return super().refine_input(q, flow, vis, rx, flow_out_scale, blend)
@@ -853,10 +876,8 @@ class FlyHighFG:
             be.use_g(j)
             be.film_pair("film.h1", "film.h2", V(self.h), 48, V(m(self.hm)), V(m(self.fh1)), V(m(self.fh2)))
         be.conv("film.out", V(self.fh2), V(self.dfilm))                                       # 53
-        be.flow_vis_t_convex_n(V(self.wt36), V(self.fv), V(self.dfilm), ts, V(self.up7), V(self.ftvt), V(self.lin),
-                               V(self.dvis))                                                  # 44-48, 54-62
-        be.refine_input_n(V(self.aq), V(self.up7, 0, 0.25), V(self.up7, 4), V(self.rx), 0.05, V(self.blend),
-                          P)                                                                  # 63-76
+        be.mid_input_n(V(self.wt36), V(self.fv), V(self.dfilm), ts, V(self.up7), V(self.ftvt), V(self.lin),
+                       V(self.dvis), V(self.aq), V(self.rx), 0.25, 0.05, V(self.blend))       # 44-48, 54-76
         self._mid_tail()
 
     def run(self, ts, W: Optional[dict] = None):
@@ -877,10 +898,9 @@ class FlyHighFG:
         if not film_done:
             be.film_pair("film.h1", "film.h2", V(self.h), 48, V(m(self.hm)), V(m(self.fh1)), V(m(self.fh2)))  # 50-52
             be.conv("film.out", V(m(self.fh2)), V(m(self.dfilm)))                             # 53
-        be.flow_vis_t_convex(V(self.wt36), V(self.fv), V(m(self.dfilm)), t, V(m(self.up7)), V(m(self.ftvt)),
-                             V(m(self.lin)), V(m(self.dvis)))                                 # 44-48, 54-62
-        be.refine_input_n(V(self.aq), V(m(self.up7), 0, 0.25), V(m(self.up7), 4), V(m(self.rx)), 0.05,
-                          V(m(self.blend)), P)                                                # 63-76
+        be.mid_input_n(V(self.wt36), V(self.fv), V(m(self.dfilm)), (t,), V(m(self.up7)), V(m(self.ftvt)),
+                       V(m(self.lin)), V(m(self.dvis)), V(self.aq), V(m(self.rx)), 0.25, 0.05,
+                       V(m(self.blend)))                                                      # 44-48, 54-76
 
     def _mid_tail(self):
         """ops 77-82 for all M * P images: the refine head at once, then each image's render, pair by pair (a pair's

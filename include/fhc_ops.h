@@ -242,6 +242,16 @@ int fhc_flow_vis_t_convex(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_
 int fhc_flow_vis_t_convex_n(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, const float* ts,
                             uint32_t phases, const fhc_tensor* out, uint32_t n, uint32_t h, uint32_t w, void* stream);
 
+/* fhc_flow_vis_t_convex_n into up (2h x 2w, 7 channels), then fhc_refine_input_n on it, in one launch (graph ops
+ * 44-48, 54-76): image i = j * n + p of up and rx is phase j of pair p, its pictures pair p of q (images 2p, 2p + 1
+ * of 2n), and the refine input reads up's flow (channels 0-3) at flow_scale and its visibility (4-6) unscaled, as
+ * fhc_refine_input_n(q, (up, flow_scale), (up + 4, 1), rx, 2h, 2w, flow_out_scale, phases * n, n) would. Each
+ * refine tile computes the upsampled values it reads itself (those at its right and lower edge twice, as the
+ * neighbouring tile does), so no launch boundary sits between the two. Bit-identical to the two calls. */
+int fhc_mid_input_n(const fhc_tensor* wt, const fhc_tensor* fv, const fhc_tensor* dfilm, const float* ts,
+                    uint32_t phases, const fhc_tensor* up, const fhc_tensor* q, const fhc_tensor* rx, uint32_t n,
+                    uint32_t h, uint32_t w, float flow_scale, float flow_out_scale, void* stream);
+
 /* fhc_fold_pair and fhc_sad_volume in one launch, for a sad_volume that reads nothing the fold writes and writes
  * nothing it reads (pair(): the second encoder pair's fold, op 26 and 43's f16b, beside the 1/16 lumas' cost volume,
  * ops 25-26, ready since the pyramid). The fold's arguments as fhc_fold_pair's (h x w, c channels); the cost

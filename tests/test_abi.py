@@ -243,6 +243,22 @@ def test_network_ops_reject_bad_views_before_any_launch():
                                      _tv(cs=8), 1, 4, 4, None), "phases"),
         ("fhc_flow_vis_t_convex_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), None, 2, _tv(cs=8), 1, 4, 4, None),
          "null phases"),
+        # the convex upsample with the refine input: its phases, image count and every view before any launch
+        ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 9)(*[0.5] * 9), 9, _tv(cs=8),
+                             _tv(cs=8), _tv(cs=16), 1, 4, 4, ctypes.c_float(0.25), ctypes.c_float(0.05), None),
+         "phases"),
+        ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), None, 2, _tv(cs=8), _tv(cs=8), _tv(cs=16), 1, 4, 4,
+                             ctypes.c_float(0.25), ctypes.c_float(0.05), None), "null phases"),
+        ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 8)(*[0.5] * 8), 8, _tv(cs=8),
+                             _tv(cs=8), _tv(cs=16), 9000, 4, 4, ctypes.c_float(0.25), ctypes.c_float(0.05), None),
+         "launch limit"),
+        ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 1)(0.5), 1, _tv(cs=8), _tv(cs=8),
+                             _tv(cs=12), 1, 4, 4, ctypes.c_float(0.25), ctypes.c_float(0.05), None), "mid_input rx"),
+        ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 1)(0.5), 1, _tv(cs=8), None,
+                             _tv(cs=16), 1, 4, 4, ctypes.c_float(0.25), ctypes.c_float(0.05), None), "mid_input q"),
+        ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 1)(0.5), 1, _tv(cs=8), _tv(cs=8),
+                             _tv(cs=16), 1, 4, 4, ctypes.c_float(float("inf")), ctypes.c_float(0.05), None),
+         "not finite"),
     ]
     for name, args, msg in cases:
         rc = getattr(L, name)(*args)

@@ -232,6 +232,40 @@ def test_refine_input_batched_equals_one_image_at_a_time(n, qmod, h, w):
     same(outs[0], outs[2], "rx (batched vs one launch per image)")
 
 
+@pytest.mark.parametrize("P,ts,h,w,fls", [(2, (0.25, 0.5, 0.75), 9, 13, 0.25), (1, (0.5,), 60, 108, 0.25),
+                                          (3, (0.3, 1.0), 5, 4, 1.0), (1, (0.7,), 4, 3, 0.25)])
+def test_mid_input_equals_convex_then_refine_input(P, ts, h, w, fls):
+    """flow_vis_t + the convex upsample + the refine input in one launch (each refine tile computing the upsampled
+    values it reads, its right and lower neighbours' too) against the two fused launches (flow_vis_t_convex_n, then
+    refine_input_n on its output) and against the ops one by one: the upsampled flow and visibility up, and rx.
+    Ragged grids whose 7-pixel refine tiles start on odd pixels, grids smaller than one tile, views into wider
+    buffers, a flow read scale of 1."""
+    say("mid_input", P, ts, h, w, fls)
+    outs = []
+    fused, composed = backends()
+    M = len(ts)
+    for be, one in ((fused, True), (composed, True), (fused, False)):
+        rng = np.random.default_rng(P * 1000 + h * 10 + w)
+        wt = fill(be, rng, P, h, w, 40, -4.0, 4.0)
+        fv = fill(be, rng, P, h, w, 8, -2.0, 2.0)
+        df = fill(be, rng, M * P, h, w, 8)
+        q = fill(be, rng, 2 * P, 2 * h, 2 * w, 8, 0.0, 1.0)
+        scratch = [be.zeros(M * P, h, w, 8) for _ in range(3)]
+        up = fill(be, rng, M * P, 2 * h, 2 * w, 8)
+        rx = fill(be, rng, M * P, 2 * h, 2 * w, 16)
+        blend = be.zeros(M * P, 2 * h, 2 * w, 8)
+        if one:
+            be.mid_input_n(V(wt, 2), V(fv), V(df, 1), ts, V(up), *(V(x) for x in scratch), V(q), V(rx, 1), fls, 0.05,
+                           V(blend))
+        else:
+            be.flow_vis_t_convex_n(V(wt, 2), V(fv), V(df, 1), ts, V(up), *(V(x) for x in scratch))
+            be.refine_input_n(V(q), V(up, 0, fls), V(up, 4), V(rx, 1), 0.05, V(blend), P)
+        outs.append({"up": be.host(up).copy(), "rx": be.host(rx).copy()})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k + " (one launch vs op by op)")
+        same(outs[0][k], outs[2][k], k + " (one launch vs two)")
+
+
 @pytest.mark.parametrize("h,w,c,also,sh,sw,r", [(30, 54, 72, True, 30, 54, 3), (9, 13, 6, False, 5, 7, 2),
                                                  (4, 4, 8, True, 17, 3, 1)])
 def test_fold_pair_sad_equals_fold_pair_and_sad(h, w, c, also, sh, sw, r):
