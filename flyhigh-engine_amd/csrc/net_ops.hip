@@ -748,15 +748,11 @@ __device__ __forceinline__ uint16_t coarse_up_at(const View& o, uint32_t hi, uin
 // csw = wi / w come from the host. blockIdx.y: the pair (its maps and pictures images 2k, 2k + 1 of f8 and i8, its
 // image k of every other view).
 template <bool VEC, bool UP>
-__global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, View fl, OView fx, OView l8,
-                                                              uint32_t h, uint32_t w, uint32_t c, uint32_t groups,
-                                                              uint32_t items, View o, OView fv, OView state,
-                                                              uint32_t hi, uint32_t wi, float fs, float csh,
-                                                              float csw) {
-    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
-    if (t >= items) return;
-    if (blockIdx.y) {
-        const size_t z = blockIdx.y, hw = (size_t)h * w;
+__device__ __forceinline__ void fine_input_at(View f8, View i8, View fl, OView fx, OView l8, uint32_t h, uint32_t w,
+                                              uint32_t c, uint32_t groups, View o, OView fv, OView state, uint32_t hi,
+                                              uint32_t wi, float fs, float csh, float csw, uint32_t t, uint32_t pair) {
+    if (pair) {
+        const size_t z = pair, hw = (size_t)h * w;
         f8.p += z * 2 * hw * f8.cs, i8.p += z * 2 * hw * i8.cs, fl.p += z * hw * fl.cs;
         fx.p += z * hw * fx.cs, l8.p += z * hw * l8.cs;
         if constexpr (UP) {
@@ -812,6 +808,98 @@ __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, 
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++)
             fx.p[(size_t)pix * fx.cs + fx.c0 + 2 * c + 6 + i] = fl.scale == 1.0f ? v[i] : f2h(h2f(v[i]) * fl.scale);
+    }
+}
+template <bool VEC, bool UP>
+__global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, View fl, OView fx, OView l8,
+                                                              uint32_t h, uint32_t w, uint32_t c, uint32_t groups,
+                                                              uint32_t items, View o, OView fv, OView state,
+                                                              uint32_t hi, uint32_t wi, float fs, float csh,
+                                                              float csw) {
+    const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+    if (t < items) fine_input_at<VEC, UP>(f8, i8, fl, fx, l8, h, w, c, groups, o, fv, state, hi, wi, fs, csh, csw, t,
+                                          blockIdx.y);
+}
+
+// The fine block's cost volume (sad_volume of the two lumas fine_input stores, radius R <= kSadRmax) beside
+// fine_input in the same launch: a workgroup takes a kSadT x kSadT tile of the cost volume and computes the lumas it
+// reads itself, A's on the tile and a ring of 1, B's on a ring of 1 + R, at the clamped pixels sad_at reads (so each
+// LDS cell holds what sad_at would load for that unclamped position), with fine_input's arithmetic (the flow from
+// coarse_up_at at the view's read scale, the picture's warp rounded to f16, its luma rounded to f16). Then sad_at's
+// sums from LDS, in its order, one lane per (pixel, displacement). Small tiles (the frame's 60 x 108 grid makes 112
+// of them a pair), loops unrolled so that each lane's luma loads issue together: the volume's workgroups then finish
+// within the fine input's.
+constexpr uint32_t kSadT = 8, kSadRmax = 3, kSadA = kSadT + 2;
+__device__ __forceinline__ float fine_luma_at(const View& i8, const View& o, float fl_scale, uint32_t h, uint32_t w,
+                                              uint32_t hi, uint32_t wi, float fs, float csh, float csw, uint32_t img,
+                                              uint32_t x, uint32_t y) {
+    const float fxv = h2f(coarse_up_at(o, hi, wi, csh, csw, fs, x, y, 2 * img)) * fl_scale;
+    const float fyv = h2f(coarse_up_at(o, hi, wi, csh, csw, fs, x, y, 2 * img + 1)) * fl_scale;
+    float v[4];
+    warp4<false>(i8, img * h, x, y, h, w, fxv, fyv, 0, 3, v);
+    return h2f(f2h(lum3(h2f(f2h(v[0])), h2f(f2h(v[1])), h2f(f2h(v[2])))));
+}
+// tile `tile` (tiles_x per row) of pair `pair`'s cost volume into out (image pair)
+template <int R>
+__device__ __forceinline__ void fine_sad_tile(View i8, View o, float fl_scale, OView out, uint32_t h, uint32_t w,
+                                              uint32_t hi, uint32_t wi, float fs, float csh, float csw, uint32_t tile,
+                                              uint32_t tiles_x, uint32_t pair) {
+    constexpr uint32_t BW = kSadT + 2 + 2 * R, NA = kSadA * kSadA, NB = BW * BW, SPAN = 2 * R + 1, S2 = SPAN * SPAN;
+    __shared__ float la[NA], lb[NB];
+    const size_t hw = (size_t)h * w;
+    i8.p += (size_t)pair * 2 * hw * i8.cs, o.p += (size_t)pair * hi * wi * o.cs, out.p += (size_t)pair * hw * out.cs;
+    const int x0 = (int)((tile % tiles_x) * kSadT), y0 = (int)((tile / tiles_x) * kSadT);
+    // lanes past the last cell recompute it (unconditional loads)
+#pragma unroll
+    for (uint32_t k = 0; k < (NA + NB + kThreads - 1) / kThreads; k++) {
+        const uint32_t e = min(threadIdx.x + k * kThreads, NA + NB - 1);
+        const bool a = e < NA;
+        const uint32_t c = a ? e : e - NA, rw = a ? kSadA : BW, ring = a ? 1 : 1 + R;
+        const int yy = y0 - (int)ring + (int)(c / rw), xx = x0 - (int)ring + (int)(c % rw);
+        const float v = fine_luma_at(i8, o, fl_scale, h, w, hi, wi, fs, csh, csw, a ? 0 : 1,
+                                     (uint32_t)clampi(xx, 0, (int)w - 1), (uint32_t)clampi(yy, 0, (int)h - 1));
+        if (a) la[c] = v;
+        else lb[c] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < (kSadT * kSadT * S2 + kThreads - 1) / kThreads; k++) {
+        const uint32_t e = threadIdx.x + k * kThreads;
+        const uint32_t p = e / S2, d = e - p * S2, lx = p % kSadT, ly = p / kSadT;
+        const int x = x0 + (int)lx, y = y0 + (int)ly;
+        if (e >= kSadT * kSadT * S2 || x >= (int)w || y >= (int)h) continue;
+        const int dy = (int)(d / SPAN) - R, dx = (int)(d % SPAN) - R;
+        float acc = 0.0f;
+#pragma unroll
+        for (int wy = -1; wy <= 1; wy++)
+#pragma unroll
+            for (int wx = -1; wx <= 1; wx++) {
+                const int yy = y + wy, xx = x + wx;
+                const bool in = yy >= 0 && yy < (int)h && xx >= 0 && xx < (int)w;
+                const float lav = la[((int)ly + 1 + wy) * (int)kSadA + (int)lx + 1 + wx];
+                const float lbv = lb[((int)ly + 1 + R + wy + dy) * (int)BW + (int)lx + 1 + R + wx + dx];
+                const float dd = fabsf(lav - lbv);
+                acc = acc + (in ? dd : 0.0f);
+            }
+        st(out, (size_t)y * w + x, d, acc / 9.0f);
+    }
+}
+// blocks [0, fine_blocks): fine_input_kernel<VEC, true>; the rest: the cost volume's tiles. blockIdx.y: the pair.
+template <bool VEC, int R>
+__global__ __launch_bounds__(kThreads) void fine_input_sad_kernel(View f8, View i8, View fl, OView fx, OView l8,
+                                                                  uint32_t h, uint32_t w, uint32_t c, uint32_t groups,
+                                                                  uint32_t items, View o, OView fv, OView state,
+                                                                  uint32_t hi, uint32_t wi, float fs, float csh,
+                                                                  float csw, uint32_t fine_blocks, OView sad,
+                                                                  uint32_t tiles_x) {
+    if (blockIdx.x < fine_blocks) {
+        const uint32_t t = blockIdx.x * kThreads + threadIdx.x;
+        if (t < items)
+            fine_input_at<VEC, true>(f8, i8, fl, fx, l8, h, w, c, groups, o, fv, state, hi, wi, fs, csh, csw, t,
+                                     blockIdx.y);
+    } else {
+        fine_sad_tile<R>(i8, o, fl.scale, sad, h, w, hi, wi, fs, csh, csw, blockIdx.x - fine_blocks, tiles_x,
+                         blockIdx.y);
     }
 }
 
@@ -2778,6 +2866,54 @@ extern "C" int fhc_coarse_fine_input_n(const fhc_tensor* o, const fhc_tensor* fv
                                outv(fx), outv(l8), h, w, c, groups, n, in(o), outv(fv), sv, hi, wi, flow_scale,
                                (float)hi / (float)h, (float)wi / (float)w);
         });
+    });
+}
+
+extern "C" int fhc_coarse_fine_input_sad_n(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state,
+                                           uint32_t hi, uint32_t wi, float flow_scale, const fhc_tensor* f8,
+                                           const fhc_tensor* i8, float fine_scale, const fhc_tensor* fx,
+                                           const fhc_tensor* l8, uint32_t h, uint32_t w, uint32_t c, uint32_t pairs,
+                                           const fhc_tensor* sad_out, uint32_t radius, void* stream) {
+    return guard(-3, [&]() -> int {
+        clear_error();
+        if ((uint64_t)h * w * c * pairs == 0) return 0;
+        if (pairs > 65535) return fail(-1, "coarse_fine_input_sad: %u pairs exceed the launch limit", pairs);
+        if (hi == 0 || wi == 0) return fail(-1, "coarse_fine_input_sad: empty coarse output (%u x %u)", hi, wi);
+        if (state && (hi > h || wi > w))
+            return fail(-1, "coarse_fine_input_sad: the state is larger than the fine grid");
+        if (radius > kSadRmax) return fail(-1, "coarse_fine_input_sad: radius %u above %u", radius, kSadRmax);
+        const uint32_t span2 = (2 * radius + 1) * (2 * radius + 1);
+        FHC_TRY(check(o, "coarse_fine_input_sad o", 7, false));
+        FHC_TRY(check(fv, "coarse_fine_input_sad fv", 7, false, true));
+        if (state) FHC_TRY(check(state, "coarse_fine_input_sad state", 4, false, true));
+        FHC_TRY(check(f8, "coarse_fine_input_sad f8", c, true));
+        FHC_TRY(check(i8, "coarse_fine_input_sad i8", 3, true));
+        FHC_TRY(check(fx, "coarse_fine_input_sad fx", 2 * c + 10, false, true));
+        FHC_TRY(check(l8, "coarse_fine_input_sad l8", 2, false, true));
+        FHC_TRY(check(sad_out, "coarse_fine_input_sad sad out", span2, false, true));
+        if (!std::isfinite(fine_scale)) return fail(-1, "coarse_fine_input_sad: the flow's read scale is not finite");
+        const uint32_t groups = (c + 3) / 4;
+        const uint64_t items = (uint64_t)h * w * (2 * groups + 3);
+        const uint32_t tiles_x = (w + kSadT - 1) / kSadT, tiles = tiles_x * ((h + kSadT - 1) / kSadT);
+        if (items + (uint64_t)tiles * kThreads >= kMaxItems)
+            return fail(-1, "coarse_fine_input_sad: %u x %u is too large", w, h);
+        fhc_tensor fxb = *fx;
+        fxb.c0 += c;
+        const bool v = vec4(c, {f8, fx, &fxb});
+        const View fl{static_cast<const uint16_t*>(fv->p), fv->cstride, fv->c0, fine_scale};
+        const OView sv = state ? outv(state) : OView{nullptr, 0, 0};
+        const uint32_t fine_blocks = (uint32_t)((items + kThreads - 1) / kThreads);
+        decltype(&fine_input_sad_kernel<true, 1>) k;
+        if (radius == 0) k = v ? fine_input_sad_kernel<true, 0> : fine_input_sad_kernel<false, 0>;
+        else if (radius == 1) k = v ? fine_input_sad_kernel<true, 1> : fine_input_sad_kernel<false, 1>;
+        else if (radius == 2) k = v ? fine_input_sad_kernel<true, 2> : fine_input_sad_kernel<false, 2>;
+        else k = v ? fine_input_sad_kernel<true, 3> : fine_input_sad_kernel<false, 3>;
+        hipLaunchKernelGGL(k, dim3(fine_blocks + tiles, pairs), dim3(kThreads), 0, (hipStream_t)stream, in(f8), in(i8),
+                           fl, outv(fx), outv(l8), h, w, c, groups, (uint32_t)items, in(o), outv(fv), sv, hi, wi,
+                           flow_scale, (float)hi / (float)h, (float)wi / (float)w, fine_blocks, outv(sad_out),
+                           tiles_x);
+        const hipError_t e = hipGetLastError();
+        return e == hipSuccess ? 0 : fail(-2, "coarse_fine_input_sad: launch failed: %s", hipGetErrorString(e));
     });
 }
 

@@ -85,6 +85,8 @@ def _lib():
             "fhc_flow_vis_t": [T, T, T, U, U, U, ctypes.c_float, P],
             "fhc_coarse_fine_input": [T, T, T, U, U, ctypes.c_float, T, T, ctypes.c_float, T, T, U, U, U, P],
             "fhc_coarse_fine_input_n": [T, T, T, U, U, ctypes.c_float, T, T, ctypes.c_float, T, T, U, U, U, U, P],
+            "fhc_coarse_fine_input_sad_n": [T, T, T, U, U, ctypes.c_float, T, T, ctypes.c_float, T, T, U, U, U, U, T,
+                                            U, P],
             "fhc_flow_vis_t_convex": [T, T, T, ctypes.c_float, T, U, U, U, P],
             "fhc_refine_input": [T, T, T, T, U, U, ctypes.c_float, P],
             "fhc_refine_input_n": [T, T, T, T, U, U, ctypes.c_float, U, U, P],
@@ -272,6 +274,21 @@ def coarse_fine_input(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c, s
          _lib().fhc_coarse_fine_input_n(_ref(o), _ref(_v(fv)), None if state is None else _ref(_v(state)), hi, wi,
                                         flow_scale, _ref(f8), _ref(_v(i8)), fine_scale, _ref(_v(fx)), _ref(_v(l8)),
                                         h, w, c, pairs, _stream_handle(stream)))
+
+
+def coarse_fine_input_sad(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c, sad_out, radius, stream=None):
+    """coarse_fine_input(...), then sad_volume(l8 channel 0, l8 channel 1, sad_out, radius) for every pair, in one
+    launch (pair k's volume: image k of sad_out)."""
+    o, f8 = _v(o), _v(f8)
+    pairs, hi, wi, _ = o.shape
+    n2, h, w, _ = f8.shape
+    if n2 != 2 * pairs:
+        raise FhcError(f"coarse_fine_input_sad: {n2} feature maps for {pairs} pairs")
+    _run("coarse_fine_input_sad",
+         _lib().fhc_coarse_fine_input_sad_n(_ref(o), _ref(_v(fv)), None if state is None else _ref(_v(state)), hi, wi,
+                                            flow_scale, _ref(f8), _ref(_v(i8)), fine_scale, _ref(_v(fx)),
+                                            _ref(_v(l8)), h, w, c, pairs, _ref(_v(sad_out)), radius,
+                                            _stream_handle(stream)))
 
 
 def flow_vis_t_convex(wt, fv, dfilm, t, out, stream=None):

@@ -186,6 +186,13 @@ class ComposedChains:
             self.coarse_up(one(o), one(fv), None if state is None else one(state), h, w, flow_scale)
             self.fine_input(two(f8), two(i8), V(sl(fv.buf, k), fv.c0, fine_scale), one(fx), one(l8), c)
 
+    def coarse_fine_input_sad(self, o: V, fv: V, state: Optional[V], flow_scale: float, f8: V, i8: V,
+                              fine_scale: float, fx: V, l8: V, c: int, sad_out: V, r: int):
+        """coarse_fine_input, then the sad of its two lumas (l8's channels 0 and 1) into sad_out (on the GPU one
+        launch, whose cost volume computes the lumas it reads)."""
+        self.coarse_fine_input(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c)
+        self.sad(V(l8.buf, l8.c0), V(l8.buf, l8.c0 + 1), sad_out, r)
+
     def flow_vis_t_convex(self, wt: V, fv: V, dfilm: V, t: float, out: V, ftvt: V, lin: V, dvis: V):
         """ftvt, lin, dvis: where the op-by-op chain keeps its intermediates (the fused launch stores none)."""
         self.flow_vis_t(fv, dfilm, ftvt, t, lin, dvis)
@@ -653,6 +660,21 @@ class GpuBackend(ComposedChains):
                                                    stream=self.stream),
                  2 * (7 + (0 if state is None else 8)) * po + 2 * 7 * p1 + 2 * p1 * (2 * c + 6 + (2 * c + 6 + 4) + 2))
 
+    def coarse_fine_input_sad(self, o: V, fv: V, state: Optional[V], flow_scale: float, f8: V, i8: V,
+                              fine_scale: float, fx: V, l8: V, c: int, sad_out: V, r: int):
+        if not self.chains:
+            return super().coarse_fine_input_sad(o, fv, state, flow_scale, f8, i8, fine_scale, fx, l8, c, sad_out, r)
+        vo, vfv, vs = self._v(o), self._v(fv), None if state is None else self._v(state)
+        vf8, vi8, vfx, vl8, vsd = (self._v(x) for x in (f8, i8, fx, l8, sad_out))
+        p1, po = self._px(f8) // 2, self._px(o)
+        span2 = (2 * r + 1) ** 2
+        # coarse_fine_input's traffic, then the cost volume written (its lumas are recomputed, not read)
+        self._go("coarse_fine_input_sad (coarse_up + fine_input + sad_volume)",
+                 lambda: self.fh.coarse_fine_input_sad(vo, vfv, vs, flow_scale, vf8, vi8, fine_scale, vfx, vl8, c,
+                                                       vsd, r, stream=self.stream),
+                 2 * (7 + (0 if state is None else 8)) * po + 2 * 7 * p1 + 2 * p1 * (2 * c + 6 + (2 * c + 6 + 4) + 2)
+                 + 2 * p1 * span2)
+
     def flow_vis_t_convex(self, wt: V, fv: V, dfilm: V, t: float, out: V, ftvt: V, lin: V, dvis: V):
         if not self.chains:
             return super().flow_vis_t_convex(wt, fv, dfilm, t, out, ftvt, lin, dvis)
@@ -816,9 +838,9 @@ class FlyHighFG:
         be.conv("coarse.head", V(self.hc), V(self.o))                                         # 32
         # 33-40 (43: flow16), then the fine loop's input, K = 1 (op 42: wa .. flow8); h enters as zeros (op 41: the
         # fx slice is never written)
-        be.coarse_fine_input(V(self.o), V(self.fv), V(self.state_out, 72), 16.0, V(self.f8), V(self.i8), 0.125,
-                             V(self.fx), V(self.l8), 36)
-        be.sad(V(self.l8, 0), V(self.l8, 1), V(self.fx, 130), 2)                              # fcv
+        # and the fine block's cost volume (fcv) of the warped pictures' lumas into its slice of fx
+        be.coarse_fine_input_sad(V(self.o), V(self.fv), V(self.state_out, 72), 16.0, V(self.f8), V(self.i8), 0.125,
+                                 V(self.fx), V(self.l8), 36, V(self.fx, 130), 2)
         be.conv("fine.r1", V(self.fx), V(self.fr1))
         be.pair("fine.r2", "fine.r3", V(self.fr1), V(self.fr2), V(self.h), False)             # h = fr3
         # flow, vis += d: the add of fine.out's output as the conv's residual, written in place (the planner's

@@ -230,6 +230,17 @@ int fhc_coarse_fine_input_n(const fhc_tensor* o, const fhc_tensor* fv, const fhc
                             float fine_scale, const fhc_tensor* fx, const fhc_tensor* l8, uint32_t h, uint32_t w,
                             uint32_t c, uint32_t pairs, void* stream);
 
+/* fhc_coarse_fine_input_n, then fhc_sad_volume(l8 channel 0, l8 channel 1, sad_out, pairs, h, w, radius) on its
+ * lumas, in one launch (pair(): ops 33-42 with the fine block's cost volume): the cost volume's workgroups compute
+ * the lumas they read themselves (the tile's and a ring of 1 + radius), with fine_input's arithmetic, beside the
+ * fine input's. radius <= 3; sad_out (image k: pair k's volume) must not overlap what the fine input writes (fx's
+ * first 2c + 10 channels, l8, fv, state). Bit-identical to the two calls. */
+int fhc_coarse_fine_input_sad_n(const fhc_tensor* o, const fhc_tensor* fv, const fhc_tensor* state, uint32_t hi,
+                                uint32_t wi, float flow_scale, const fhc_tensor* f8, const fhc_tensor* i8,
+                                float fine_scale, const fhc_tensor* fx, const fhc_tensor* l8, uint32_t h, uint32_t w,
+                                uint32_t c, uint32_t pairs, const fhc_tensor* sad_out, uint32_t radius,
+                                void* stream);
+
 /* fhc_flow_vis_t then fhc_convex_upsample of its output in one launch (graph ops 44-48, 54-62): the convex
  * upsample's 7-channel input (flow_t | vis_t) computed from fv and dfilm at phase t while it is staged, never
  * stored. Bit-identical to the two calls. */

@@ -243,6 +243,16 @@ def test_network_ops_reject_bad_views_before_any_launch():
                                      _tv(cs=8), 1, 4, 4, None), "phases"),
         ("fhc_flow_vis_t_convex_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), None, 2, _tv(cs=8), 1, 4, 4, None),
          "null phases"),
+        # the fine input with its cost volume: the radius its tiles hold, the volume's channels, the pair count
+        ("fhc_coarse_fine_input_sad_n", (_tv(cs=8), _tv(cs=8), None, 2, 2, ctypes.c_float(16.0), _tv(cs=8), _tv(),
+                                         ctypes.c_float(0.125), _tv(cs=24), _tv(), 4, 4, 4, 1, _tv(cs=64), 4, None),
+         "radius 4 above 3"),
+        ("fhc_coarse_fine_input_sad_n", (_tv(cs=8), _tv(cs=8), None, 2, 2, ctypes.c_float(16.0), _tv(cs=8), _tv(),
+                                         ctypes.c_float(0.125), _tv(cs=24), _tv(), 4, 4, 4, 1, _tv(cs=24), 2, None),
+         "sad out"),
+        ("fhc_coarse_fine_input_sad_n", (_tv(cs=8), _tv(cs=8), None, 2, 2, ctypes.c_float(16.0), _tv(cs=8), _tv(),
+                                         ctypes.c_float(0.125), _tv(cs=24), _tv(), 4, 4, 4, 70000, _tv(cs=32), 2,
+                                         None), "launch limit"),
         # the convex upsample with the refine input: its phases, image count and every view before any launch
         ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 9)(*[0.5] * 9), 9, _tv(cs=8),
                              _tv(cs=8), _tv(cs=16), 1, 4, 4, ctypes.c_float(0.25), ctypes.c_float(0.05), None),

@@ -106,6 +106,43 @@ def test_coarse_fine_input_batched_equals_one_pair_at_a_time(P, hi, wi, h, w, c,
         same(outs[0][k], outs[2][k], k + " (batched vs one launch per pair)")
 
 
+@pytest.mark.parametrize("P,hi,wi,h,w,c,cs,state,fine_scale,r", [
+    (1, 30, 54, 60, 108, 36, 40, True, 0.125, 2),   # the frame's grids
+    (3, 5, 9, 13, 21, 36, 40, True, 0.125, 2),      # ragged ratio, three pairs
+    (2, 7, 6, 20, 11, 6, 9, False, 1.0, 3),         # 2-byte path, no state, the largest radius
+    (1, 3, 2, 5, 3, 8, 8, False, 0.125, 1),         # a grid smaller than one cost-volume tile
+])
+def test_coarse_fine_input_sad_equals_coarse_fine_input_then_sad(P, hi, wi, h, w, c, cs, state, fine_scale, r):
+    """The fine input with the cost volume of its lumas in one launch (the volume's tiles computing the lumas they
+    read) against coarse_fine_input then sad_volume as two launches and against the ops one by one: fv, fx (the
+    volume written into its slice past the fine input's channels), l8, the state."""
+    say("coarse_fine_input_sad", P, hi, wi, h, w, c, cs, state, fine_scale, r)
+    outs = []
+    fused, composed = backends()
+    span2 = (2 * r + 1) ** 2
+    for be, one in ((fused, True), (composed, True), (fused, False)):
+        rng = np.random.default_rng(P * 1000 + hi * 10 + w)
+        o = fill(be, rng, P, hi, wi, 16, -3.0, 3.0)
+        f8 = fill(be, rng, 2 * P, h, w, cs)
+        i8 = fill(be, rng, 2 * P, h, w, 4, 0.0, 1.0)
+        fv = fill(be, rng, P, h, w, 8)
+        fx = fill(be, rng, P, h, w, 2 * c + 12 + span2)
+        l8 = fill(be, rng, P, h, w, 4)
+        st = fill(be, rng, P, hi, wi, 80) if state else None
+        args = (V(o), V(fv), None if st is None else V(st, 72), 16.0, V(f8, cs - c), V(i8), fine_scale, V(fx, 1),
+                V(l8, 1), c)
+        if one:
+            be.coarse_fine_input_sad(*args, V(fx, 2 * c + 12), r)
+        else:
+            be.coarse_fine_input(*args)
+            be.sad(V(l8, 1), V(l8, 2), V(fx, 2 * c + 12), r)
+        outs.append({k: be.host(t).copy() for k, t in (("fv", fv), ("fx", fx), ("l8", l8), ("state", st))
+                     if t is not None})
+    for k in outs[0]:
+        same(outs[0][k], outs[1][k], k + " (one launch vs op by op)")
+        same(outs[0][k], outs[2][k], k + " (one launch vs two)")
+
+
 @pytest.mark.parametrize("n,h,w,t", [(2, 9, 13, 0.3), (1, 60, 108, 0.5), (1, 5, 4, 1.0)])
 def test_flow_vis_t_convex_equals_flow_vis_t_then_convex(n, h, w, t):
     say("flow_vis_t_convex", n, h, w, t)
