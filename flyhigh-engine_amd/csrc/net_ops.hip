@@ -492,13 +492,21 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
     const int xlo = max(0, (int)floorf(((float)ox0 + 0.5f) * sw - fsw + 0.5f));
     const int xhi = min((int)iw, (int)floorf(((float)ox_last + 0.5f) * sw + fsw + 0.5f));
     const int ny = max(1, min(yhi - ylo, (int)kAaExt)), nx = max(1, min(xhi - xlo, (int)kAaExt));
-    const size_t rowbase = (size_t)img * ih + ylo;
+    // the window's first pixel (uniform), then 32-bit byte offsets of the lane's rows and columns (the window is at
+    // most kAaExt pixels square, so row * iw * cs stays far below 2^32 for any frame)
+    const char* wbase = reinterpret_cast<const char*>(x.p + (((size_t)img * ih + ylo) * iw + xlo) * x.cs + x.c0);
+    uint32_t roff[kAaR], coff[kAaR];
+#pragma unroll
+    for (uint32_t i = 0; i < kAaR; i++) {
+        roff[i] = (uint32_t)min((int)(ty + kAaT * i), ny - 1) * iw * x.cs * 2u;
+        coff[i] = (uint32_t)min((int)(tx + kAaT * i), nx - 1) * x.cs * 2u;
+    }
 #pragma unroll
     for (uint32_t i = 0; i < kAaR; i++)
 #pragma unroll
         for (uint32_t j = 0; j < kAaR; j++) {
             const int row = min((int)(ty + kAaT * i), ny - 1), col = min((int)(tx + kAaT * j), nx - 1);
-            const uint16_t* src = x.p + ((rowbase + row) * iw + xlo + col) * x.cs + x.c0;
+            const uint16_t* src = reinterpret_cast<const uint16_t*>(wbase + (roff[i] + coff[j]));
             if constexpr (V4) {  // channels past c are never read from the tile
                 tile[row * S + col] = *reinterpret_cast<const uint2*>(src);
             } else {
@@ -511,37 +519,52 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
         }
     if (tid < kAaExt) tile[tid * S + kAaExt] = uint2{0u, 0u};  // the zero column
     if (tid < S) tile[kAaExt * S + tid] = uint2{0u, 0u};       // the zero row
+    // The tap weights and LDS offsets of the tile's columns (threads 0 .. 16 KM - 1: column t / KM, tap t % KM) and
+    // rows (threads 128 ..), computed once for the tile: an invalid column or row (past the output) takes the
+    // clamped pixel's, whose lanes store nothing. A tap outside its pixel's window gets weight 0 and the zero cell.
+    __shared__ float wxs[kAaT * KM], wys[kAaT * KM];
+    __shared__ int lcs[kAaT * KM], lrs[kAaT * KM];
+    if (tid < kAaT * KM) {
+        const uint32_t k = tid / KM, j = tid % KM;
+        const float cx = ((float)min(ox0 + k, ow - 1) + 0.5f) * sw;
+        const int xmin = max(0, (int)floorf(cx - fsw + 0.5f)), xmax = min((int)iw, (int)floorf(cx + fsw + 0.5f));
+        const int xx = xmin + (int)j;
+        wxs[tid] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
+        lcs[tid] = xx < xmax ? xx - xlo : (int)kAaExt;
+    } else if (tid >= 128 && tid < 128 + kAaT * KM) {
+        const uint32_t k = (tid - 128) / KM, j = (tid - 128) % KM;
+        const float cy = ((float)min(oy0 + k, oh - 1) + 0.5f) * sh;
+        const int ymin = max(0, (int)floorf(cy - fsh + 0.5f)), ymax = min((int)ih, (int)floorf(cy + fsh + 0.5f));
+        const int y = ymin + (int)j;
+        wys[tid - 128] = y < ymax ? fmaxf(0.0f, 1.0f - fabsf(((float)y + 0.5f - cy) / fsh)) : 0.0f;
+        lrs[tid - 128] = y < ymax ? (y - ylo) * (int)S : (int)(kAaExt * S);
+    }
     __syncthreads();
     const uint32_t ox = ox0 + tx, oy = oy0 + ty;
     const bool valid = ox < ow && oy < oh;
     if (!PYR && !valid) return;
     // an invalid lane (PYR only: it must reach the barriers) computes a clamped pixel and stores nothing
-    const float cy = ((float)min(oy, oh - 1) + 0.5f) * sh, cx = ((float)min(ox, ow - 1) + 0.5f) * sw;
-    const int ymin = max(0, (int)floorf(cy - fsh + 0.5f)), ymax = min((int)ih, (int)floorf(cy + fsh + 0.5f));
-    const int xmin = max(0, (int)floorf(cx - fsw + 0.5f)), xmax = min((int)iw, (int)floorf(cx + fsw + 0.5f));
     float wx[KM];
     int lc[KM];
 #pragma unroll
-    for (int j = 0; j < KM; j++) {
-        const int xx = xmin + j;
-        wx[j] = xx < xmax ? fmaxf(0.0f, 1.0f - fabsf(((float)xx + 0.5f - cx) / fsw)) : 0.0f;
-        lc[j] = xx < xmax ? xx - xlo : (int)kAaExt;
-    }
+    for (int j = 0; j < KM; j++) wx[j] = wxs[tx * KM + j], lc[j] = lcs[tx * KM + j];
     constexpr int NC = PYR ? 3 : 4;  // the channels summed: the pyramid's pictures have 3
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f}, norm = 0.0f;
 #pragma unroll
     for (int jy = 0; jy < KM; jy++) {
-        const int y = ymin + jy;
-        const float wy = y < ymax ? fmaxf(0.0f, 1.0f - fabsf(((float)y + 0.5f - cy) / fsh)) : 0.0f;
-        const uint2* lrow = tile + (y < ymax ? (y - ylo) * (int)S : (int)(kAaExt * S));
+        const float wy = wys[ty * KM + jy];
+        const uint2* lrow = tile + lrs[ty * KM + jy];
 #pragma unroll
         for (int jx = 0; jx < KM; jx++) {
             const float wgt = wx[jx] * wy;
             const uint2 q = lrow[lc[jx]];
             const float v[4] = {h2f((uint16_t)q.x), h2f((uint16_t)(q.x >> 16)), h2f((uint16_t)q.y),
                                 h2f((uint16_t)(q.y >> 16))};
+            // each product as an FMA with +0, which takes the f16 tap as it is (one mixed-precision FMA): the
+            // product's value, or +0 for a product of -0, which the sum cannot tell apart (it starts at +0 and a
+            // sum of f32 values is -0 only when both are)
 #pragma unroll
-            for (int i = 0; i < NC; i++) acc[i] = acc[i] + v[i] * wgt;
+            for (int i = 0; i < NC; i++) acc[i] = acc[i] + __builtin_fmaf(v[i], wgt, 0.0f);
             norm = norm + wgt;
         }
     }
@@ -587,6 +610,9 @@ __global__ __launch_bounds__(kThreads) void interp_aa_lds_kernel(View x, OView o
         }
     }
 }
+
+// Whether interp_aa_lds_kernel's 32-bit byte offsets within a staged window (kAaExt rows of iw pixels) hold.
+bool aa_window_offsets_fit(uint32_t iw, uint32_t cs) { return (uint64_t)kAaExt * iw * cs * 2 < (1ull << 32); }
 
 // The largest input extent (rows or columns) of any kAaT-output tile's windows, from the kernel's f32 formulas.
 uint32_t aa_tile_extent(uint32_t in, uint32_t outn) {
@@ -2320,7 +2346,8 @@ extern "C" int fhc_interpolate(const fhc_tensor* x, const fhc_tensor* out, uint3
         const uint32_t groups = (c + 3) / 4;
         if (antialias) {
             const uint32_t taps = std::max(aa_taps(ih, oh), aa_taps(iw, ow));
-            if (c <= 4 && taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt) {
+            if (c <= 4 && taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt &&
+                aa_window_offsets_fit(iw, x->cstride)) {
                 const uint32_t tx = (ow + kAaT - 1) / kAaT, ty = (oh + kAaT - 1) / kAaT;
                 if ((uint64_t)n * tx * ty >= kMaxItems) return fail(-1, "interpolate: too many tiles");
                 const bool v4 = vec4(4, {x});
@@ -2510,7 +2537,8 @@ extern "C" int fhc_pair_input_n(const fhc_tensor* ab, const fhc_tensor* q, const
         FHC_TRY(check(i16, "pair_input i16", 6, false, true));
         FHC_TRY(check(l16, "pair_input l16", 2, false, true));
         const uint32_t taps = std::max(aa_taps(ih, oh), aa_taps(iw, ow));
-        if (!(taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt)) {
+        if (!(taps <= 8 && aa_tile_extent(ih, oh) <= kAaExt && aa_tile_extent(iw, ow) <= kAaExt &&
+              aa_window_offsets_fit(iw, ab->cstride))) {
             // no one-launch form for this scale: the resize of every picture, then each pair's pyramid
             FHC_TRY(fhc_interpolate(ab, q, 2 * pairs, 3, ih, iw, oh, ow, 1, stream));
             for (uint32_t k = 0; k < pairs; k++) {
