@@ -6,8 +6,8 @@ oracle's (oracle/fh_ops_oracle.c, gmhs.rs and its shaders restated) bit for bit:
 workgroups of 256 strided lanes and their pairwise lane tree, every other value is the same f32 operations in the
 same order, and the square roots and quotients are correctly rounded on both sides. Cases: the 1080p network (864 x 480 of
 1920-wide frames), a network as wide as its frame (the largest windows), ragged sizes whose cost grid is no multiple
-of the 16-cell tiles, the E8 flow as a view of a wider buffer, level 2, a striped scene where the select fires, and
-a workspace full of NaN (nothing in it is read before it is written).
+of the 16-cell tiles, the E8 flow as a view of a wider buffer, a flow grid coarser than E8, level 2, a striped scene
+where the select fires, and a workspace full of NaN (nothing in it is read before it is written).
 """
 import numpy as np
 import pytest
@@ -97,6 +97,17 @@ def test_gmhs_matches_the_oracle(h, w, full_w, cs, level):
     b = np.roll(a, (2, -3), axis=(1, 2)).copy()
     flow = smooth_flow(rng, h // 8, w // 8, cs)
     check(a, b, flow, full_w, level, f"random {h}x{w}")
+
+
+def test_gmhs_with_a_coarser_flow_matches_the_oracle():
+    """A flow grid of 1/16 the network (the select's cells 8 cost cells apart, where the reference's E8 grid puts
+    them 4 apart), at the largest decision window: the select's sampled rows and columns follow the flow's grid."""
+    say("gmhs coarse flow")
+    h, w = 192, 256
+    rng = np.random.default_rng(7)
+    a = f16(rng.uniform(0, 1, (1, h, w, 4)))
+    b = np.roll(a, (3, 2), axis=(1, 2)).copy()
+    check(a, b, smooth_flow(rng, h // 16, w // 16, 4), w, 1, "coarse flow")
 
 
 def test_gmhs_repairs_the_striped_scene_as_the_oracle():
