@@ -31,11 +31,6 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "flyhigh-engine_amd"))
 
-# HIP graph replay without the runtime's recorded-packet path (ROCm's DEBUG_CLR_GRAPH_PACKET_CAPTURE, read once
-# when the runtime starts, so before torch is imported): each node is then dispatched as an ordinary kernel launch,
-# which measured 174.4-175.0 us per 1080p frame against 178.3-178.9 us with recorded packets (200 timed frames,
-# alternating in one call). An explicit setting in the environment is kept; the bench line reports the one used.
-os.environ.setdefault("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0")
 
 METRIC = "1080p frames/s (pair+mid); per-conv-layer % of MFMA or HBM roofline"
 # the reference's published time for the same workload (1080p frames, network 856x480, k = 1, repair 1): pair 1.61 ms +
@@ -1314,8 +1309,7 @@ def emit(args, frame, conv_step, roofline, cpu, batched, detail):
         scaling="weak", vs_baseline=round(frame["frames_per_s"] * PUBLISHED_MS_PER_FRAME / 1e3, 3), dtype="f16",
         data="synthetic",
         config=dict(workload=frame["workload"], frame="1920x1080", network=frame["network"],
-                    launches=frame.get("launches"), parallelism="single GPU",
-                    hip_graph_packet_capture=os.environ.get("DEBUG_CLR_GRAPH_PACKET_CAPTURE")),
+                    launches=frame.get("launches"), parallelism="single GPU"),
         frame_without_repair_us=frame.get("no_repair", {}).get("us_per_frame"),
         frame_rotating_us=frame.get("rotating_us_per_frame"),
         roofline=None if roofline is None else {k: roofline[k] for k in keep_roof if k in roofline},
