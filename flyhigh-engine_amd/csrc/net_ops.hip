@@ -1675,12 +1675,22 @@ __device__ __forceinline__ void render_rgba_px(uint32_t x, uint32_t y, const flo
 // and rk = 1, so r * rk is r and mixed * (1 - stillw) + own * stillw is mixed (or +0 for a mixed of -0, which the
 // clamp and the byte conversion turn into the same byte 0): that variant leaves those terms out.
 template <bool CUBIC, bool QV, bool FL, bool FMA>
+// blockIdx.z: generated frame z of `phases` per pair, pair-major (pair p = z / phases, phase j): its frames at
+// p * pstride words past fa and fb, its maps image j * per + p of fl, vis and rt, its output frame j * per + p,
+// ostride words apart (one frame: z = 0)
 __global__ __launch_bounds__(kThreads) void render_rgba_kernel(const uint32_t* fa, const uint32_t* fb, uint32_t w,
                                                                uint32_t h, uint32_t pitch, float sh, float sw,
                                                                View fl, View vis, View rt, uint32_t hq, uint32_t wq,
                                                                float fsx, float fsy, uint32_t flags, uint32_t* dst,
-                                                               uint32_t opitch) {
+                                                               uint32_t opitch, uint64_t pstride, uint32_t per,
+                                                               uint32_t phases, uint64_t ostride) {
     __shared__ float tab[256];
+    if (blockIdx.z) {
+        const uint32_t p = blockIdx.z / phases, img = (blockIdx.z - p * phases) * per + p;
+        fa += p * pstride, fb += p * pstride, dst += img * ostride;
+        const size_t q = (size_t)img * hq * wq;
+        fl.p += q * fl.cs, vis.p += q * vis.cs, rt.p += q * rt.cs;
+    }
     fill_unit_table(tab);
     const uint32_t x = blockIdx.x * 64 + (threadIdx.x & 63u), y = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (x >= w || y >= h) return;
@@ -2715,20 +2725,25 @@ extern "C" int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_
     });
 }
 
-extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_t h, uint32_t pitch, uint32_t hp,
-                               uint32_t wp, const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rt,
-                               uint32_t hq, uint32_t wq, float fsx, float fsy, int cubic, uint32_t flags, void* out,
-                               uint32_t opitch, void* stream) {
+namespace {
+// fhc_render_rgba over pairs x phases generated frames (the pair's frames at p * pstride words past a and b)
+int render_rgba_run(const void* a, const void* b, uint64_t pstride, uint32_t pairs, uint32_t phases, uint32_t w,
+                    uint32_t h, uint32_t pitch, uint32_t hp, uint32_t wp, const fhc_tensor* flow, const fhc_tensor* vis,
+                    const fhc_tensor* rt, uint32_t hq, uint32_t wq, float fsx, float fsy, int cubic, uint32_t flags,
+                    void* out, uint32_t opitch, uint64_t ostride, void* stream) {
     return guard(-3, [&]() -> int {
         clear_error();
-        if ((uint64_t)h * w == 0) return 0;
+        if ((uint64_t)h * w * pairs * phases == 0) return 0;
+        if ((uint64_t)pairs * phases > 65535)
+            return fail(-1, "render_rgba: %u generated frames exceed the launch limit", pairs * phases);
         if (hq == 0 || wq == 0) return fail(-1, "render_rgba: empty quarter maps (%u x %u)", hq, wq);
         if (flags > 7)
             return fail(-1, "render_rgba: flags %u (bit 0 decisive, bit 1 still, bit 2 exact f32 order)", flags);
         if (w < 4) return fail(-1, "render_rgba: frames narrower than 4 pixels");
+        if (pairs > 1 && pstride < (uint64_t)pitch * h) return fail(-1, "render_rgba: pair stride below pitch * h");
         FHC_TRY(check_frames("render_rgba a", a, 1, w, h, pitch, 0, hp, wp));
         FHC_TRY(check_frames("render_rgba b", b, 1, w, h, pitch, 0, hp, wp));
-        FHC_TRY(check_frames("render_rgba out", out, 1, w, h, opitch, 0, hp, wp));
+        FHC_TRY(check_frames("render_rgba out", out, pairs * phases, w, h, opitch, ostride, hp, wp));
         FHC_TRY(check(flow, "render_rgba flow", 4, false));
         FHC_TRY(check(vis, "render_rgba vis", 3, true));
         FHC_TRY(check(rt, "render_rgba rt", 3, false));
@@ -2753,13 +2768,36 @@ extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_
               {render_rgba_kernel<true, true, false, false>, render_rgba_kernel<true, true, true, false>}}}};
         const uint32_t modes = flags & 3u;
         hipLaunchKernelGGL(ks[(flags >> 2) & 1u][cubic ? 1 : 0][qv ? 1 : 0][modes ? 1 : 0],
-                           dim3((w + 63) / 64, (h + 3) / 4), dim3(kThreads), 0, (hipStream_t)stream,
+                           dim3((w + 63) / 64, (h + 3) / 4, pairs * phases), dim3(kThreads), 0, (hipStream_t)stream,
                            static_cast<const uint32_t*>(a), static_cast<const uint32_t*>(b), w, h, pitch,
                            (float)hq / (float)hp, (float)wq / (float)wp, in(flow), in(vis), in(rt), hq, wq, fsx, fsy,
-                           modes, static_cast<uint32_t*>(out), opitch);
+                           modes, static_cast<uint32_t*>(out), opitch, pstride, pairs, phases, ostride);
         const hipError_t e = hipGetLastError();
         return e == hipSuccess ? 0 : fail(-2, "render_rgba: launch failed: %s", hipGetErrorString(e));
     });
+}
+}  // namespace
+
+extern "C" int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_t h, uint32_t pitch, uint32_t hp,
+                               uint32_t wp, const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rt,
+                               uint32_t hq, uint32_t wq, float fsx, float fsy, int cubic, uint32_t flags, void* out,
+                               uint32_t opitch, void* stream) {
+    return render_rgba_run(a, b, 0, 1, 1, w, h, pitch, hp, wp, flow, vis, rt, hq, wq, fsx, fsy, cubic, flags, out,
+                           opitch, 0, stream);
+}
+
+extern "C" int fhc_render_rgba_n(const void* frames, uint32_t pairs, uint32_t phases, uint32_t w, uint32_t h,
+                                 uint32_t pitch, uint64_t fstride, uint32_t hp, uint32_t wp, const fhc_tensor* flow,
+                                 const fhc_tensor* vis, const fhc_tensor* rt, uint32_t hq, uint32_t wq, float fsx,
+                                 float fsy, int cubic, uint32_t flags, void* out, uint32_t opitch, uint64_t ostride,
+                                 void* stream) {
+    if (pairs && fstride < (uint64_t)pitch * h) {
+        clear_error();
+        return fail(-1, "render_rgba: frame stride below pitch * h");
+    }
+    const void* b = frames ? static_cast<const uint32_t*>(frames) + fstride : nullptr;
+    return render_rgba_run(frames, b, 2 * fstride, pairs, phases, w, h, pitch, hp, wp, flow, vis, rt, hq, wq, fsx, fsy,
+                           cubic, flags, out, opitch, ostride, stream);
 }
 
 extern "C" int fhc_gmhs_params(uint32_t h, uint32_t w, uint32_t full_w, uint32_t level, fhc_gmhs_par* out) {

@@ -95,6 +95,8 @@ def _lib():
             "fhc_rgba_resize": [P, U, U, U, U, ctypes.c_uint64, U, U, T, U, U, P],
             "fhc_render_rgba": [P, P, U, U, U, U, U, T, T, T, U, U, ctypes.c_float, ctypes.c_float, I, U, P, U,
                                 P],
+            "fhc_render_rgba_n": [P, U, U, U, U, U, ctypes.c_uint64, U, U, T, T, T, U, U, ctypes.c_float,
+                                  ctypes.c_float, I, U, P, U, ctypes.c_uint64, P],
             "fhc_gmhs_params": [U, U, U, U, ctypes.POINTER(GmhsPar)],
             "fhc_flow_vis_t_convex_n": [T, T, T, P, U, T, U, U, U, P],
             "fhc_mid_input_n": [T, T, T, P, U, T, T, T, U, U, U, ctypes.c_float, ctypes.c_float, P],
@@ -437,6 +439,24 @@ def render_rgba(fa, fb, flow, vis, rt, hp: int, wp: int, cubic=True, flags=0, fs
     _run("render_rgba", _lib().fhc_render_rgba(fa.data_ptr(), fb.data_ptr(), w, h, w, hp, wp, _ref(flow), _ref(vis),
                                                _ref(rt), hq, wq, fsx, fsy, int(cubic), flags, o.data_ptr(), w,
                                                _stream_handle(stream)))
+    return o
+
+
+def render_rgba_n(frames, flow, vis, rt, hp: int, wp: int, phases: int, cubic=True, flags=0, fsx=1.0, fsy=1.0,
+                  out=None, stream=None):
+    """render_rgba of every pair of frames ((2P, h, w): A, B of pair p at 2p, 2p + 1) at `phases` phases, pair-major,
+    in one launch: phase j of pair p from maps image j * P + p, into frame j * P + p of out ((phases * P, h, w))."""
+    import torch
+    n2, h, w = _frames(frames)
+    if n2 % 2:
+        raise FhcError(f"render_rgba_n: {n2} frames are no whole pairs")
+    flow, vis, rt = _v(flow), _v(vis), _v(rt)
+    _, hq, wq, _ = flow.shape
+    P = n2 // 2
+    o = torch.empty((phases * P, h, w), dtype=torch.int32, device=frames.device) if out is None else out
+    _run("render_rgba", _lib().fhc_render_rgba_n(frames.data_ptr(), P, phases, w, h, w, h * w, hp, wp, _ref(flow),
+                                                 _ref(vis), _ref(rt), hq, wq, fsx, fsy, int(cubic), flags,
+                                                 o.data_ptr(), w, h * w, _stream_handle(stream)))
     return o
 
 

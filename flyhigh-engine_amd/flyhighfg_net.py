@@ -229,6 +229,18 @@ class ComposedChains:
         self.render(V(self.image(full, 0)), V(self.image(full, 1)), flow, vis, rt, V(pic), cubic, flags, fsx, fsy)
         self.rgba_out(V(pic), out_frames)
 
+    def frame_render_n(self, frames, full, pic, flow: V, vis: V, rt: V, out_frames, hp: int, wp: int, fsx: float,
+                       fsy: float, cubic: bool, flags: int, phases: int):
+        """frame_render of every generated frame, pair by pair (a pair's phases read the same two frames): phase j of
+        pair p (frames 2p, 2p + 1) from maps image j * P + p into frame j * P + p of out_frames (on the GPU one
+        launch, in the same order)."""
+        P = frames.shape[0] // 2
+        for i in (j * P + p for p in range(P) for j in range(phases)):
+            p = i % P
+            one = lambda x, k=i: V(sl(x.buf, k), x.c0, x.scale)  # noqa: E731
+            self.frame_render(sl(frames, 2 * p, 2), None if full is None else sl(full, 2 * p, 2), pic, one(flow),
+                              one(vis), one(rt), sl(out_frames, i), hp, wp, fsx, fsy, cubic, flags)
+
     def refine_input_n(self, q: V, flow: V, vis: V, rx: V, flow_out_scale: float, blend: V, qmod: int):
         """refine_input for every image k of flow (and vis, rx, blend), its pictures pair k % qmod of q"""
         for k in range(flow.buf.shape[0]):
@@ -563,6 +575,18 @@ class GpuBackend(ComposedChains):
                  lambda: self.fh.render_rgba(fa, fb, vf, vv, vr, hp, wp, cubic, fl, fsx, fsy, out=out_frames,
                                              stream=self.stream),
                  4 * (frames.numel() + out_frames.numel()) + 2 * 10 * self._px(flow))
+
+    def frame_render_n(self, frames, full, pic, flow: V, vis: V, rt: V, out_frames, hp: int, wp: int, fsx: float,
+                       fsy: float, cubic: bool, flags: int, phases: int):
+        if not self.chains or frames.shape[0] * phases == 2:
+            return super().frame_render_n(frames, full, pic, flow, vis, rt, out_frames, hp, wp, fsx, fsy, cubic,
+                                          flags, phases)
+        vf, vv, vr = self._v(flow), self._v(vis), self._v(rt)
+        fl = flags | (4 if self.exact_render else 0)  # bit 2: the reference's f32 order
+        self._go("frame_render (render_pix + rgba_out, every generated frame)",
+                 lambda: self.fh.render_rgba_n(frames, vf, vv, vr, hp, wp, phases, cubic, fl, fsx, fsy,
+                                               out=out_frames, stream=self.stream),
+                 4 * (frames.numel() * phases + out_frames.numel()) + 2 * 10 * self._px(flow))
 
     def gmhs(self, a: V, b: V, flow: V, full_w: int, level: int):
         va, vb, vf = self._v(a), self._v(b), self._v(flow)
@@ -930,14 +954,13 @@ class FlyHighFG:
         be, P = self.be, self.P
         be.pair("refine.q1", "refine.q2", V(self.rx), V(self.rq1), V(self.rq2), False)        # 77, 78
         be.pair_affine_out("refine.q3", "refine.q4", V(self.rq2), V(self.rq3), V(self.rr), V(self.Rt), 3)  # 79-81
+        if self.frame is not None and self.internal:  # the render at the frame size, to the RGBA8 frames
+            be.frame_render_n(self.frames, self.full, self.pic, V(self.up7, 0), V(self.up7, 4), V(self.Rt), self.rgba,
+                              self.hp, self.wp, self.fsx, self.fsy, self.cubic, self.render_flags, self.M)
+            return
         for i in (j * P + p for p in range(P) for j in range(self.M)):
             p = i % P
             up7, rt = sl(self.up7, i), sl(self.Rt, i)
-            if self.frame is not None and self.internal:  # the render at the frame size, to the RGBA8 frame
-                be.frame_render(sl(self.frames, 2 * p, 2), None if self.full is None else sl(self.full, 2 * p, 2),
-                                self.pic, V(up7, 0), V(up7, 4), V(rt), sl(self.rgba, i), self.hp, self.wp, self.fsx,
-                                self.fsy, self.cubic, self.render_flags)
-                continue
             out = sl(self.out, i)
             be.render(V(sl(self.AB, 2 * p)), V(sl(self.AB, 2 * p + 1)), V(up7, 0), V(up7, 4), V(rt), V(out),
                       self.cubic, self.render_flags)                                          # 82: render_pix

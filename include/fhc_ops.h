@@ -152,6 +152,14 @@ int fhc_rgba_resize(const void* rgba, uint32_t n, uint32_t w, uint32_t h, uint32
 int fhc_render_rgba(const void* a, const void* b, uint32_t w, uint32_t h, uint32_t pitch, uint32_t hp, uint32_t wp,
                     const fhc_tensor* flow, const fhc_tensor* vis, const fhc_tensor* rt, uint32_t hq, uint32_t wq,
                     float fsx, float fsy, int cubic, uint32_t flags, void* out, uint32_t opitch, void* stream);
+/* fhc_render_rgba of pairs x phases generated frames in one launch, pair-major: pair p's frames A, B are frames
+ * 2p, 2p + 1 (fstride words apart), phase j's maps image j * pairs + p of flow, vis and rt (each view's tensor holds
+ * phases * pairs images of hq x wq), its output frame j * pairs + p (ostride words apart). Bit-identical to one call
+ * per generated frame. pairs * phases <= 65535. The batched program's form; the reference renders one frame a mid(t). */
+int fhc_render_rgba_n(const void* frames, uint32_t pairs, uint32_t phases, uint32_t w, uint32_t h, uint32_t pitch,
+                      uint64_t fstride, uint32_t hp, uint32_t wp, const fhc_tensor* flow, const fhc_tensor* vis,
+                      const fhc_tensor* rt, uint32_t hq, uint32_t wq, float fsx, float fsy, int cubic, uint32_t flags,
+                      void* out, uint32_t opitch, uint64_t ostride, void* stream);
 
 /* ---- The graph's op chains, fused. Each computes what its ops compute one after another (the same f32 operations
  * and f16 roundings at the tensors the ops store); no reference counterpart as one call: each replaces the listed

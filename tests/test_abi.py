@@ -253,6 +253,16 @@ def test_network_ops_reject_bad_views_before_any_launch():
         ("fhc_coarse_fine_input_sad_n", (_tv(cs=8), _tv(cs=8), None, 2, 2, ctypes.c_float(16.0), _tv(cs=8), _tv(),
                                          ctypes.c_float(0.125), _tv(cs=24), _tv(), 4, 4, 4, 70000, _tv(cs=32), 2,
                                          None), "launch limit"),
+        # the batched frame render: its frame count and strides before any launch
+        ("fhc_render_rgba_n", (0x1000, 300, 300, 64, 32, 64, 64 * 32, 32, 64, _tv(cs=8), _tv(cs=8, c0=4), _tv(), 8, 16,
+                               ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, 64 * 32, None),
+         "launch limit"),
+        ("fhc_render_rgba_n", (0x1000, 2, 3, 64, 32, 64, 100, 32, 64, _tv(cs=8), _tv(cs=8, c0=4), _tv(), 8, 16,
+                               ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, 64 * 32, None),
+         "frame stride"),
+        ("fhc_render_rgba_n", (0x1000, 2, 3, 64, 32, 64, 64 * 32, 32, 64, _tv(cs=8), _tv(cs=8, c0=4), _tv(), 8, 16,
+                               ctypes.c_float(1.0), ctypes.c_float(1.0), 1, 0, 0x3000, 64, 100, None),
+         "frame stride"),
         # the convex upsample with the refine input: its phases, image count and every view before any launch
         ("fhc_mid_input_n", (_tv(cs=40), _tv(cs=8), _tv(cs=8), (ctypes.c_float * 9)(*[0.5] * 9), 9, _tv(cs=8),
                              _tv(cs=8), _tv(cs=16), 1, 4, 4, ctypes.c_float(0.25), ctypes.c_float(0.05), None),

@@ -364,6 +364,33 @@ def _bytes_diff(a, b):
     return diff
 
 
+@pytest.mark.parametrize("P,M,flags,size", [(3, 2, 0, (97, 130)), (2, 3, 4, (150, 300)), (1, 2, 3, (64, 80))])
+def test_render_rgba_n_equals_one_call_per_frame(P, M, flags, size):
+    """The batched frame render (pair p's frames 2p, 2p + 1; phase j's maps and output image j * P + p) against
+    one fhc_render_rgba call per generated frame: bit-identical, in the fused and the exact order."""
+    import torch
+    say("render_rgba_n", P, M, flags, size)
+    fh = fhops()
+    rng = np.random.default_rng(P * 10 + M)
+    h, w = size
+    hp, wp = (h + 31) // 32 * 32, (w + 31) // 32 * 32
+    hq, wq = hp // 8, wp // 8
+    fsx, fsy = float(np.float32(wp) / np.float32(4 * wq)), float(np.float32(hp) / np.float32(4 * hq))
+    dfr = dev32(_frames(rng, 2 * P, h, w))
+    up = np.zeros((M * P, hq, wq, 8), np.float32)
+    up[..., :4] = rng.uniform(-6, 6, (M * P, hq, wq, 4))
+    up[..., 4:7] = rng.normal(0, 2, (M * P, hq, wq, 3))
+    dup, drt = dev(f16_bits(up)), dev(rand(rng, (M * P, hq, wq, 4), -0.1, 0.1))
+    got = host32(fh.render_rgba_n(dfr, dup, fh.View(dup, 4), drt, hp, wp, M, flags=flags, fsx=fsx, fsy=fsy))
+    for p in range(P):
+        for j in range(M):
+            i = j * P + p
+            one = host32(fh.render_rgba(dfr[2 * p:2 * p + 1], dfr[2 * p + 1:2 * p + 2], dup[i:i + 1],
+                                        fh.View(dup[i:i + 1], 4), drt[i:i + 1], hp, wp, flags=flags, fsx=fsx, fsy=fsy))
+            exact(got[i:i + 1], one, f"render_rgba_n frame {i} (pair {p}, phase {j})")
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("cubic,flags,amp,size,qdiv", [(True, 0, 6, (1080, 1920), 9), (False, 0, 6, (1080, 1920), 9),
                                                        (True, 2, 3, (150, 300), 9), (True, 3, 6, (150, 300), 9),
                                                        (False, 3, 2, (97, 130), 9), (True, 0, 40, (97, 130), 9),
