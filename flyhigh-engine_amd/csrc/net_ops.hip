@@ -269,11 +269,14 @@ __global__ __launch_bounds__(kCvThreads) void convex_tile_kernel(View wt, View x
     float ws[9];
     convex_weights(lw + (liy * kCvIn + lix) * 36 + sub, ws);
     const size_t opix = ((size_t)img * 2 * h + oy) * 2 * w + ox;
+    // each product as an FMA with +0, which takes the f16 value as it is (one mixed-precision FMA): the product's
+    // value, or +0 for a product of -0, which the sum cannot tell apart (it starts at +0, and a sum of f32 values is
+    // -0 only when both are)
     for (uint32_t co = 0; co < c; co++) {
         float acc = 0.0f;
 #pragma unroll
         for (uint32_t k = 0; k < 9; k++)
-            acc = acc + ws[k] * h2f(lx[((liy + k / 3) * kCvHalo + lix + k % 3) * c + co]);
+            acc = acc + __builtin_fmaf(h2f(lx[((liy + k / 3) * kCvHalo + lix + k % 3) * c + co]), ws[k], 0.0f);
         st(out, opix, co, acc);
     }
 }
@@ -1075,7 +1078,8 @@ __global__ __launch_bounds__(64) void mid_input_kernel(View wt, View fv, View df
     for (uint32_t co = 0; co < 7; co++) {
         float acc = 0.0f;
 #pragma unroll
-        for (uint32_t k = 0; k < 9; k++) acc = acc + ws[k] * h2f(lx[((lcy + k / 3) * kMiHalo + lcx + k % 3) * 7 + co]);
+        for (uint32_t k = 0; k < 9; k++)
+            acc = acc + __builtin_fmaf(h2f(lx[((lcy + k / 3) * kMiHalo + lcx + k % 3) * 7 + co]), ws[k], 0.0f);
         u[co] = f2h(acc);
     }
     const bool own = tx < kRiT && ty < kRiT && x0 + tx < ow && y0 + ty < oh;
