@@ -851,14 +851,14 @@ __global__ __launch_bounds__(kThreads) void fine_input_kernel(View f8, View i8, 
 }
 
 // The fine block's cost volume (sad_volume of the two lumas fine_input stores, radius R <= kSadRmax) beside
-// fine_input in the same launch: a workgroup takes a kSadT x kSadT tile of the cost volume and computes the lumas it
+// fine_input in the same launch: a workgroup takes a kSadTX x kSadTY tile of the cost volume and computes the lumas it
 // reads itself, A's on the tile and a ring of 1, B's on a ring of 1 + R, at the clamped pixels sad_at reads (so each
 // LDS cell holds what sad_at would load for that unclamped position), with fine_input's arithmetic (the flow from
 // coarse_up_at at the view's read scale, the picture's warp rounded to f16, its luma rounded to f16). Then sad_at's
-// sums from LDS, in its order, one lane per (pixel, displacement). Small tiles (the frame's 60 x 108 grid makes 112
-// of them a pair), loops unrolled so that each lane's luma loads issue together: the volume's workgroups then finish
-// within the fine input's.
-constexpr uint32_t kSadT = 8, kSadRmax = 3, kSadA = kSadT + 2;
+// sums from LDS, in its order, one lane per (pixel, displacement). Small tiles (the frame's 60 x 108 grid makes 210
+// of them a pair; at radius 2 one luma a lane), loops unrolled so that each lane's luma loads issue together: the
+// volume's workgroups then finish within the fine input's.
+constexpr uint32_t kSadTX = 8, kSadTY = 4, kSadRmax = 3;
 __device__ __forceinline__ float fine_luma_at(const View& i8, const View& o, float fl_scale, uint32_t h, uint32_t w,
                                               uint32_t hi, uint32_t wi, float fs, float csh, float csw, uint32_t img,
                                               uint32_t x, uint32_t y) {
@@ -873,17 +873,18 @@ template <int R>
 __device__ __forceinline__ void fine_sad_tile(View i8, View o, float fl_scale, OView out, uint32_t h, uint32_t w,
                                               uint32_t hi, uint32_t wi, float fs, float csh, float csw, uint32_t tile,
                                               uint32_t tiles_x, uint32_t pair) {
-    constexpr uint32_t BW = kSadT + 2 + 2 * R, NA = kSadA * kSadA, NB = BW * BW, SPAN = 2 * R + 1, S2 = SPAN * SPAN;
+    constexpr uint32_t AW = kSadTX + 2, BW = kSadTX + 2 + 2 * R, NA = AW * (kSadTY + 2),
+                       NB = BW * (kSadTY + 2 + 2 * R), SPAN = 2 * R + 1, S2 = SPAN * SPAN;
     __shared__ float la[NA], lb[NB];
     const size_t hw = (size_t)h * w;
     i8.p += (size_t)pair * 2 * hw * i8.cs, o.p += (size_t)pair * hi * wi * o.cs, out.p += (size_t)pair * hw * out.cs;
-    const int x0 = (int)((tile % tiles_x) * kSadT), y0 = (int)((tile / tiles_x) * kSadT);
+    const int x0 = (int)((tile % tiles_x) * kSadTX), y0 = (int)((tile / tiles_x) * kSadTY);
     // lanes past the last cell recompute it (unconditional loads)
 #pragma unroll
     for (uint32_t k = 0; k < (NA + NB + kThreads - 1) / kThreads; k++) {
         const uint32_t e = min(threadIdx.x + k * kThreads, NA + NB - 1);
         const bool a = e < NA;
-        const uint32_t c = a ? e : e - NA, rw = a ? kSadA : BW, ring = a ? 1 : 1 + R;
+        const uint32_t c = a ? e : e - NA, rw = a ? AW : BW, ring = a ? 1 : 1 + R;
         const int yy = y0 - (int)ring + (int)(c / rw), xx = x0 - (int)ring + (int)(c % rw);
         const float v = fine_luma_at(i8, o, fl_scale, h, w, hi, wi, fs, csh, csw, a ? 0 : 1,
                                      (uint32_t)clampi(xx, 0, (int)w - 1), (uint32_t)clampi(yy, 0, (int)h - 1));
@@ -892,11 +893,11 @@ __device__ __forceinline__ void fine_sad_tile(View i8, View o, float fl_scale, O
     }
     __syncthreads();
 #pragma unroll
-    for (uint32_t k = 0; k < (kSadT * kSadT * S2 + kThreads - 1) / kThreads; k++) {
+    for (uint32_t k = 0; k < (kSadTX * kSadTY * S2 + kThreads - 1) / kThreads; k++) {
         const uint32_t e = threadIdx.x + k * kThreads;
-        const uint32_t p = e / S2, d = e - p * S2, lx = p % kSadT, ly = p / kSadT;
+        const uint32_t p = e / S2, d = e - p * S2, lx = p % kSadTX, ly = p / kSadTX;
         const int x = x0 + (int)lx, y = y0 + (int)ly;
-        if (e >= kSadT * kSadT * S2 || x >= (int)w || y >= (int)h) continue;
+        if (e >= kSadTX * kSadTY * S2 || x >= (int)w || y >= (int)h) continue;
         const int dy = (int)(d / SPAN) - R, dx = (int)(d % SPAN) - R;
         float acc = 0.0f;
 #pragma unroll
@@ -905,7 +906,7 @@ __device__ __forceinline__ void fine_sad_tile(View i8, View o, float fl_scale, O
             for (int wx = -1; wx <= 1; wx++) {
                 const int yy = y + wy, xx = x + wx;
                 const bool in = yy >= 0 && yy < (int)h && xx >= 0 && xx < (int)w;
-                const float lav = la[((int)ly + 1 + wy) * (int)kSadA + (int)lx + 1 + wx];
+                const float lav = la[((int)ly + 1 + wy) * (int)AW + (int)lx + 1 + wx];
                 const float lbv = lb[((int)ly + 1 + R + wy + dy) * (int)BW + (int)lx + 1 + R + wx + dx];
                 const float dd = fabsf(lav - lbv);
                 acc = acc + (in ? dd : 0.0f);
@@ -2964,7 +2965,7 @@ extern "C" int fhc_coarse_fine_input_sad_n(const fhc_tensor* o, const fhc_tensor
         if (!std::isfinite(fine_scale)) return fail(-1, "coarse_fine_input_sad: the flow's read scale is not finite");
         const uint32_t groups = (c + 3) / 4;
         const uint64_t items = (uint64_t)h * w * (2 * groups + 3);
-        const uint32_t tiles_x = (w + kSadT - 1) / kSadT, tiles = tiles_x * ((h + kSadT - 1) / kSadT);
+        const uint32_t tiles_x = (w + kSadTX - 1) / kSadTX, tiles = tiles_x * ((h + kSadTY - 1) / kSadTY);
         if (items + (uint64_t)tiles * kThreads >= kMaxItems)
             return fail(-1, "coarse_fine_input_sad: %u x %u is too large", w, h);
         fhc_tensor fxb = *fx;
